@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X log-linear attention hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step = one log-linear Mamba-2 chunkwise forward (``hattention_kernel``,
+HStruct.MAMBA2, the fused HIP kernel) over one batch of synthetic inputs at
+the BASELINE north-star shape B=4, T=16384, H=16, dk=dv=64, L=15, bf16
+q/k/v/lambda, fp32 g, inputs resident in HBM.  Prints one JSON line with the
+throughput (tokens/s), the roofline of the kernel (HBM-bound: algorithmic
+bytes / average launch time measured with HIP events on the launch stream)
+and a host-CPU baseline (this repo's fp32 torch restatement of the
+reference's chunkwise algorithm, timed on a bounded sample on rank 0).
+
+Only one GPU is used: ``--gpus`` above 1 exits with a message.
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "log-linear-attention_amd"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+# north-star workload (BASELINE.json north_star / SURVEY 8(d))
+NS = dict(B=4, T=16384, H=16, K=64, V=64, L=15)
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_BF16_PEAK = 2.5e15    # FLOP/s dense bf16
+
+
+def make_mamba2_inputs(B, T, H, K, V, L, G=None, seed=1000, dtype=torch.bfloat16,
+                       ldtype=None, device="cpu", with_do=False):
+    """Seeded synthetic inputs of the BASELINE configs (drawn fp32 on CPU in the
+    order q, k, v, A_log, dt-noise, lambda-noise, (dO), then cast / moved).
+
+    A = exp(A_log), A_log ~ U[log 1, log 16] per head; dt = clamp(softplus(N(0,1)
+    + b_h), 1e-3, 1e-1) with b_h = softplus^-1(dt0_h), dt0_h = exp(U[log 1e-3,
+    log 1e-1]); g = -A * dt (fp32); lambda = softplus(N(0,1)).
+    """
+    G = G or H
+    ldtype = ldtype or dtype
+    gen = torch.Generator("cpu").manual_seed(seed)
+    q = torch.randn(B, T, G, K, generator=gen)
+    k = torch.randn(B, T, G, K, generator=gen)
+    v = torch.randn(B, T, H, V, generator=gen)
+    A_log = torch.empty(H).uniform_(math.log(1.0), math.log(16.0), generator=gen)
+    dt0 = torch.exp(torch.empty(H).uniform_(math.log(1e-3), math.log(1e-1), generator=gen))
+    bias = dt0 + torch.log(-torch.expm1(-dt0))                  # softplus^-1
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, generator=gen) + bias)
+    dt = dt.clamp(1e-3, 1e-1)
+    g = (-torch.exp(A_log) * dt).float()
+    lam = torch.nn.functional.softplus(torch.randn(B, T, H, L, generator=gen))
+    out = [q.to(dtype), k.to(dtype), v.to(dtype), g, lam.to(ldtype)]
+    if with_do:
+        out.append(torch.randn(B, T, H, V, generator=gen).to(dtype))
+    return [t.to(device) for t in out]
+
+
+def fwd_bytes(B, T, H, K, V, L, es=2, es_l=2, G=None):
+    """Algorithmic HBM bytes of one forward: read q, k, v, g, lambda, write o."""
+    G = G or H
+    return B * T * (2 * G * K * es + H * V * es + H * V * es + H * 4 + H * L * es_l)
+
+
+def fwd_flops(B, T, H, K, V):
+    nlev = math.ceil(math.log2(T // 64)) if T > 64 else 0
+    return B * H * (2 * T * 64 * (K + V) + 2 * T * K * V + T * K * V * nlev)
+
+
+def cpu_baseline(seconds_budget=30.0):
+    """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
+    chunkwise algorithm) on the host cores, on the north-star workload (median
+    of up to 3 runs within the time budget)."""
+    from oracle.mamba2 import chunked_scan_fwd
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    B, T, H, K, V, L = NS["B"], NS["T"], NS["H"], NS["K"], NS["V"], NS["L"]
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=1000, dtype=torch.float32)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and (time.perf_counter() - t_start) < seconds_budget:
+        t0 = time.perf_counter()
+        chunked_scan_fwd(q, k, v, g, l, chunk_size=64)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    tokens_equiv = B * T
+    return {
+        "value": tokens_equiv / t,
+        "unit": "tokens/s",
+        "cores": n,
+        "kind": "port",
+        "sample": (f"fp32 torch chunked level-scan restatement (oracle/mamba2.py "
+                   f"chunked_scan_fwd) on the full north-star workload B={B} T={T} H={H} "
+                   f"dk=dv={K} L={L}, median of {len(times)} runs ({t:.2f}s each), "
+                   f"{n} threads; cpu={platform.processor() or platform.machine()}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every (batch, head) row is independent; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_kernel
+
+    dev = torch.device("cuda:0")
+    B, T, H, K, V, L = (NS[x] for x in ("B", "T", "H", "K", "V", "L"))
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=1000, device=dev)
+    torch.cuda.synchronize()
+
+    def step():
+        with torch.no_grad():
+            return hattention_kernel(q, k, v, None, g, l, None, False, 2, HType.WEAK,
+                                     HStruct.MAMBA2)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [a.elapsed_time(b) for a, b in ev]
+    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    ms_per_step = wall / args.steps * 1e3
+    tokens = B * T
+    value = tokens / (wall / args.steps)
+
+    nbytes = fwd_bytes(B, T, H, K, V, L)
+    flops = fwd_flops(B, T, H, K, V)
+    achieved = nbytes / avg_launch_s
+    out = {
+        "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, softplus lambda, Mamba-2 dt/A decay)",
+        "config": {"workload": "log-linear Mamba-2 chunkwise forward (hattention_kernel, "
+                               "MAMBA2, WEAK, base 2, chunk 64)",
+                   "batch": B, "seq_len": T, "heads": H, "dk": K, "dv": V, "levels": L,
+                   "dtype_qkv_lambda": "bf16", "dtype_g": "fp32"},
+        "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+                     "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,
+                     "mfma_frac": flops / avg_launch_s / MFMA_BF16_PEAK},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,84 @@
+/*
+ * hattn.h -- C-ABI of libhattn_hip.so, the MI355X (gfx950) chunkwise path of
+ * log-linear (Fenwick-tree hierarchical) attention.
+ *
+ * Every entry point takes plain device pointers, sizes and dtype codes, runs
+ * stream-ordered on the caller's HIP stream, never allocates, frees or
+ * synchronises, and returns an hattn_status.  Tensors are time-first and
+ * contiguous (the reference's head_first=False layout):
+ *
+ *   q, k   [B, T, G, K]        G divides H (head h reads group h / (H / G))
+ *   v, o   [B, T, H, V]
+ *   g      [B, T, H]   fp32    per-step log-decay
+ *   l      [B, T, H, L]        level weights lambda (linear)
+ *   ht     [B, H, K, V, L] fp32 final per-level states
+ *
+ * The caller (the Python host layer, or any FFI binding) allocates every
+ * output.  A failed call leaves a message retrievable with hattn_last_error()
+ * (thread-local) and returns the status the reference's Python would have
+ * raised as an exception (see hattn_status).
+ */
+#ifndef HATTN_H_
+#define HATTN_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The Python layer maps them to the exception types the
+ * reference raises for the same condition. */
+typedef enum {
+  HATTN_OK = 0,
+  HATTN_ERR_VALUE = 1,           /* ValueError (chunkwise.py:1140-1153, 1211-1214) */
+  HATTN_ERR_NOT_IMPLEMENTED = 2, /* NotImplementedError (kernel.py:55-123) */
+  HATTN_ERR_HIP = 3              /* HIP runtime error (launch / attribute) */
+} hattn_status;
+
+/* Element types of the tensors crossing the boundary. */
+typedef enum { HATTN_BF16 = 0, HATTN_FP16 = 1, HATTN_FP32 = 2 } hattn_dtype;
+
+/* HType / HStruct of hattention/base.py:12-19. */
+enum { HATTN_HTYPE_WEAK = 0, HATTN_HTYPE_STRONG = 1 };
+
+/* Library version string, e.g. "hattn-mi355x 0.1.0 gfx950". */
+const char* hattn_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* hattn_last_error(void);
+
+/*
+ * Log-linear Mamba-2 chunkwise forward.
+ *
+ * Replaces hattention/chunkwise.py:1118-1275 `chunkwise_fwd(q, k, v, g, l,
+ * head_first, level_base, htype, chunk_size, output_final_state)
+ * -> (o, g_cumsum, ht)`, the function HAttentionFunction.forward calls for
+ * HStruct.MAMBA2 with chunkwise=True (kernel.py:77-98).
+ *
+ *   o         [B, T, H, V] in dtype_o (the reference allocates it in v.dtype)
+ *   g_cumsum  [B, T, H] fp32 chunk-local inclusive cumsum of g, or NULL
+ *             (the reference returns it and saves it for backward)
+ *   ht        [B, H, K, V, L] fp32 final inter-chunk level states (levels
+ *             7 .. 6 + ceil(log2(T / 64))), or NULL for output_final_state=False.
+ *             Levels not written by the kernel are left untouched (the
+ *             reference zero-initialises ht, chunkwise.py:1179).
+ *
+ * Constraints (status on violation):
+ *   T % 64 == 0, T >= 64, H % G == 0, L >= 7 + ceil(log2(T / 64)),
+ *   V % 16 == 0                                    -> HATTN_ERR_VALUE
+ *   chunk_size == 64, level_base == 2, htype == WEAK, K == 64,
+ *   dtype_qk == BF16, dtype_v / dtype_l / dtype_o in {BF16, FP32}
+ *                                                  -> HATTN_ERR_NOT_IMPLEMENTED
+ */
+int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
+                               const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
+                               int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
+                               int dtype_l, int dtype_o, int level_base, int htype,
+                               int chunk_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HATTN_H_ */

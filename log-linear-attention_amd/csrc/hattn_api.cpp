@@ -1,0 +1,93 @@
+// C-ABI entry points of libhattn_hip.so (declared in include/hattn.h).
+//
+// Host-side validation mirrors the checks of the reference host drivers
+// (chunkwise.py:1140-1153, 1211-1214; kernel.py:55-123) and reports them as
+// status codes plus a thread-local message; the kernels themselves assume
+// validated shapes.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/hattn.h"
+
+hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, const float* g,
+                                   const void* l, void* o, float* gcum, float* ht, int B, int T,
+                                   int G, int H, int V, int L, int nlev, int dt_v, int dt_l,
+                                   int dt_o, hipStream_t stream, int* unsupported);
+
+namespace {
+
+thread_local char g_err[512] = {0};
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = 0;
+  return HATTN_OK;
+}
+
+// ceil(log2(n)) for n >= 1 (ceil_log(NT, 2), base.py:29-30; exact for integers)
+int ceil_log2(int n) {
+  int e = 0;
+  while ((1 << e) < n) ++e;
+  return e;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(HATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hattn_version(void) { return "hattn-mi355x 0.1.0 gfx950"; }
+
+const char* hattn_last_error(void) { return g_err; }
+
+int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
+                               const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
+                               int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
+                               int dtype_l, int dtype_o, int level_base, int htype,
+                               int chunk_size, void* stream) {
+  if (chunk_size != 64)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
+  if (level_base != 2)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
+  if (htype != HATTN_HTYPE_WEAK)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (B <= 0 || H <= 0 || G <= 0 || K <= 0 || V <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
+  if (H % G != 0) return fail(HATTN_ERR_VALUE, "H=%d is not a multiple of G=%d", H, G);
+  if (V % 16 != 0) return fail(HATTN_ERR_VALUE, "V=%d and BV could be 16", V);
+  if (K != 64) return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d (the MI355X kernel supports 64)", K);
+  const int NT = T / 64;
+  const int nlev = ceil_log2(NT);
+  if (7 + nlev > L)
+    return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (nlev > 17) return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^17", T);
+  if (7 + nlev > 24) return fail(HATTN_ERR_NOT_IMPLEMENTED, "too many levels");
+  if (dtype_qk != HATTN_BF16)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 required)", dtype_qk);
+  if (!q || !k || !v || !g || !l || !o) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  int unsupported = 0;
+  hipError_t e = hattn_mamba2_fwd_launch(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, V, L, nlev,
+                                         dtype_v, dtype_l, dtype_o, (hipStream_t)stream,
+                                         &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d o=%d", dtype_v, dtype_l,
+                dtype_o);
+  return check_hip(e, "hattn_mamba2_chunkwise_fwd launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+"""ctypes binding of libhattn_hip.so (declarations: include/hattn.h).
+
+There is no fallback: if the library is missing or a tensor is not on a HIP
+device the call raises.  Build the library with
+``python log-linear-attention_amd/build_lib.py``.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_native", "libhattn_hip.so")
+
+HATTN_OK, HATTN_ERR_VALUE, HATTN_ERR_NOT_IMPLEMENTED, HATTN_ERR_HIP = 0, 1, 2, 3
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+# (name, restype, argtypes) of every exported entry point, in header order.
+_P, _I, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p
+SIGNATURES = [
+    ("hattn_version", ctypes.c_char_p, []),
+    ("hattn_last_error", ctypes.c_char_p, []),
+    ("hattn_mamba2_chunkwise_fwd", _I,
+     [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P]),
+]
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the shared library once (raises ImportError if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise ImportError(
+                    f"libhattn_hip.so not found at {LIB_PATH}; build it with "
+                    "`python log-linear-attention_amd/build_lib.py`")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, res, args in SIGNATURES:
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Map an hattn_status to the exception type the reference raises."""
+    if status == HATTN_OK:
+        return
+    msg = load().hattn_last_error().decode(errors="replace")
+    if status == HATTN_ERR_VALUE:
+        raise ValueError(msg)
+    if status == HATTN_ERR_NOT_IMPLEMENTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(f"hattn HIP error: {msg}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise NotImplementedError(f"unsupported dtype {t.dtype}") from None
+
+
+def require_device(*tensors) -> torch.device:
+    """All tensors must live on one HIP device; the path has no CPU fallback."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "hattention (MI355X) runs only on HIP device tensors; got a tensor on "
+                f"{t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("tensors on different devices")
+    return dev
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,125 @@
+"""Host drivers of the log-linear Mamba-2 chunkwise path (MI355X).
+
+Same names, arguments and return tuples as hattention/chunkwise.py:
+* ``chunkwise_fwd(q, k, v, g, l, head_first, level_base, htype, chunk_size,
+  output_final_state) -> (o, g_cumsum, ht)``      -- chunkwise.py:1118-1275
+* ``chunkwise_bwd(...)``                            -- chunkwise.py:1286-1597
+
+Both validate like the reference (``ValueError`` for non-contiguous tensors,
+T % 64, K/V multiples, too few levels; ``NotImplementedError`` for modes
+outside the weak base-2 hierarchy), allocate the outputs with torch on the
+inputs' device and launch the fused HIP kernels of libhattn_hip.so on the
+current stream.  There is no CPU path.
+"""
+from typing import Optional, Tuple
+
+import torch
+
+from hattention import _lib
+from hattention.base import HType, get_num_levels, ceil_log
+
+CHUNK = 64
+
+
+def _assert_contiguous(**tensors):
+    """chunkwise.py:21-31 (assert_contiguous raises ValueError)."""
+    for name, t in tensors.items():
+        if isinstance(t, torch.Tensor) and not t.is_contiguous():
+            raise ValueError(f"Tensor argument {name} must be contiguous")
+
+
+def _shapes(q, k, v, l, head_first):
+    if head_first:
+        raise NotImplementedError("head_first=True is not supported (time-first layout only)")
+    if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or l.dim() != 4:
+        raise ValueError("expected q, k [B,T,G,K], v [B,T,H,V], l [B,T,H,L]")
+    B, T, G, K = k.shape
+    _, _, H, V = v.shape
+    L = l.shape[-1]
+    if v.shape[:2] != (B, T) or l.shape[:3] != (B, T, H):
+        raise ValueError("batch / length / head mismatch")
+    return B, T, G, H, K, V, L
+
+
+def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
+    """chunkwise.py:1140-1153 and :1211-1214."""
+    if htype != HType.WEAK:
+        raise NotImplementedError("HType.STRONG is outside the MI355X path")
+    if level_base != 2:
+        raise NotImplementedError("level_base must be 2")
+    if chunk_size != CHUNK:
+        raise NotImplementedError(f"chunk_size={chunk_size} (only {CHUNK})")
+    if H % G != 0:
+        raise ValueError(f"H={H} is not a multiple of G={G}")
+    if T % CHUNK != 0 or T < CHUNK:
+        raise ValueError(f"T={T} and BT={CHUNK}")
+    for bs in (32, 64):
+        if K % bs != 0:
+            raise ValueError(f"K={K} and BK could be {bs}")
+        if V % bs != 0:
+            raise ValueError(f"V={V} and BV could be {bs}")
+    NT = T // CHUNK
+    if get_num_levels(CHUNK, level_base) + ceil_log(NT, level_base) > L:
+        raise ValueError(f"L={L} levels are too few for T={T}")
+
+
+def chunkwise_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    l: torch.Tensor,
+    head_first: bool,
+    level_base: int,
+    htype: HType,
+    chunk_size: int,
+    output_final_state: bool,
+) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Log-linear Mamba-2 forward (chunkwise.py:1118-1275).
+
+    Returns ``o`` [B,T,H,V] in v.dtype, the chunk-local inclusive cumsum of g
+    [B,T,H] fp32 and, if ``output_final_state``, ``ht`` [B,H,K,V,L] fp32 holding
+    the inter-chunk level states at levels 7 .. 6 + ceil(log2(T/64)) (other
+    levels zero), like the reference.
+    """
+    _assert_contiguous(q=q, k=k, v=v, g=g, l=l)
+    B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
+    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size)
+    if g.shape != (B, T, H):
+        raise ValueError("g must be [B, T, H]")
+    if g.dtype != torch.float32:
+        raise ValueError("g (log-decay) must be float32")
+    dev = _lib.require_device(q, k, v, g, l)
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must share a dtype")
+    o = torch.empty(v.shape, dtype=v.dtype, device=dev)
+    g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
+    ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
+    lib = _lib.load()
+    st = lib.hattn_mamba2_chunkwise_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o),
+        _lib.ptr(g_cumsum), _lib.ptr(ht), B, T, G, H, K, V, L,
+        _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
+        level_base, htype.value, chunk_size, _lib.stream_handle(dev))
+    _lib.check(st)
+    return o, g_cumsum, ht
+
+
+def chunkwise_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    l: torch.Tensor,
+    do: torch.Tensor,
+    head_first: bool,
+    level_base: int,
+    htype: HType,
+    chunk_size: int,
+):
+    """Log-linear Mamba-2 backward (chunkwise.py:1286-1597).
+
+    ``g`` is the chunk-local cumsum returned by :func:`chunkwise_fwd`.
+    Returns (dq, dk, dv, dg, dl) with dg w.r.t. the raw per-step g.
+    """
+    raise NotImplementedError("the MI355X Mamba-2 backward kernel is not built yet")

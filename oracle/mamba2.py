@@ -1,0 +1,341 @@
+"""Log-linear Mamba-2 (HStruct.MAMBA2, HType.WEAK, level base 2): CPU oracle.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+All functions take time-first tensors (``head_first=False``, the only layout
+the reference APIs use):
+
+    q, k : [B, T, G, K]   (G divides H; group of head h is h // (H // G))
+    v    : [B, T, H, V]
+    g    : [B, T, H]      per-step log-decay (fp32 in the reference)
+    l    : [B, T, H, L]   level weights lambda (linear, not log)
+
+and return ``o : [B, T, H, V]`` computed in the dtype of the inputs (pass
+float64 for the parity checks).  The math they all implement is
+
+    o_t = sum_{s <= t} l[t, level(t, s)] * exp(G_t - G_s) * (q_t . k_s) * v_s
+
+with ``G`` the inclusive cumulative sum of ``g`` and ``level`` the weak Fenwick
+level (``oracle.levels``).
+
+Restatements (reference file:line):
+* ``materialized_fwd``  -- make_masked_H_matrix + hattention_materialized,
+  hattention/base.py:75-98, 334-349 (O(T^2), explicit H matrix).
+* ``recurrent_fwd``     -- HState.cascade_weak / insert / dot, step_state,
+  step_output, hattention_recurrent, hattention/recurrent.py:9-216
+  (Fenwick-tree state machine, one token at a time).
+* ``chunked_fwd``       -- hssd_minimal_discrete, hattention/hssd_minimal.py:108-220
+  (intra-chunk blocks + masked chunk-level decay matrix per level).
+* ``chunked_scan_fwd``  -- the host loop of chunkwise_fwd with its kernels,
+  hattention/chunkwise.py:1118-1275 (chunk_fwd_kernel_h :94-280 and
+  chunk_fwd_kernel_o :473-647): intra-chunk tile, then per inter-chunk level a
+  sequential scan over chunks with the skip_kv / skip_g / skip_q schedule.
+  Also returns the chunk-local cumsum of g (chunkwise.py:1175) and the final
+  per-level states ``ht`` [B, H, K, V, L] (chunkwise.py:1179, 229-279).
+* ``ssd_scan_fwd``      -- plain (non-hierarchical) gated linear attention /
+  Mamba-2 SSD recurrence h_t = exp(g_t) h_{t-1} + k_t v_t^T, o_t = q_t h_t:
+  the textbook form that log-linear Mamba-2 reduces to when lambda == 1
+  (the intent of the reference's check, hattention/mamba_apis.py:569-729).
+* ``autograd_bwd``      -- gradients (dq, dk, dv, dg, dl) of any of the above
+  through torch.autograd; dg is w.r.t. the raw per-step g, which is what the
+  reference returns after its reverse chunk-local cumsum (chunkwise.py:1596).
+
+Pinning: the four forward forms are structurally different algorithms and are
+checked against each other; ``ssd_scan_fwd`` (textbook) pins the lambda == 1
+case; lambda one-hot on one level is checked against a brute-force pair loop
+using the recursive level function; autograd is pinned by
+torch.autograd.gradcheck (finite differences) in float64.
+"""
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from oracle.levels import get_num_levels, levels_matrix, level_weak_recursive
+
+
+def _expand_groups(x: torch.Tensor, H: int) -> torch.Tensor:
+    """[B, T, G, D] -> [B, T, H, D] (chunkwise.py:1169-1171 repeat)."""
+    G = x.shape[2]
+    if G == H:
+        return x
+    return x.repeat_interleave(H // G, dim=2)
+
+
+def _check(q, k, v, g, l):
+    B, T, G, K = q.shape
+    H = v.shape[2]
+    if k.shape != q.shape or v.shape[:2] != (B, T) or g.shape != (B, T, H) \
+            or l.shape[:3] != (B, T, H) or H % G != 0:
+        raise ValueError("shape mismatch")
+    return B, T, G, H, K, v.shape[3], l.shape[3]
+
+
+# --------------------------------------------------------------------------
+# 1. materialised H matrix (base.py:75-98, 334-349)
+# --------------------------------------------------------------------------
+def materialized_H(g: torch.Tensor, l: torch.Tensor) -> torch.Tensor:
+    """H[b, h, t, s] = l[b, t, h, level(t, s)] * prod_{u=s+1..t} exp(g[b, u, h]).
+
+    base.py:87-96 builds the product of A = exp(g) over (s, t]; here the product
+    is formed as exp of the difference of inclusive cumsums (identical math).
+    """
+    B, T, H = g.shape
+    lev = torch.from_numpy(levels_matrix(T, default=0, clamp_min=0))
+    G = torch.cumsum(g, dim=1)                               # [B, T, H]
+    seg = G[:, :, None, :] - G[:, None, :, :]                # [B, t, s, H]
+    mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    seg = seg.masked_fill(~mask[None, :, :, None], float("-inf"))
+    tt = torch.arange(T)[:, None].expand(T, T)
+    lam = l.permute(0, 2, 1, 3)[:, :, tt, lev]               # [B, H, t, s]
+    return torch.exp(seg).permute(0, 3, 1, 2) * lam          # [B, H, t, s]
+
+
+def materialized_fwd(q, k, v, g, l) -> torch.Tensor:
+    """hattention_materialized (base.py:334-349): O = (H o Q K^T) V."""
+    B, T, G, H, K, V, L = _check(q, k, v, g, l)
+    q = _expand_groups(q, H)
+    k = _expand_groups(k, H)
+    Hm = materialized_H(g, l)
+    qkt = torch.einsum("bthd,bshd->bhts", q, k)
+    return torch.einsum("bhts,bshd->bthd", Hm * qkt, v)
+
+
+# --------------------------------------------------------------------------
+# 2. Fenwick recurrent form (recurrent.py:9-216)
+# --------------------------------------------------------------------------
+class FenwickState:
+    """HState for HStruct.MAMBA2 / HType.WEAK (recurrent.py:9-54, 76-100).
+
+    ``states`` [B, H, K, V, L]; ``counts`` [L] tokens merged into each level.
+    """
+
+    def __init__(self, B, H, K, V, L, dtype):
+        self.L = L
+        self.states = torch.zeros(B, H, K, V, L, dtype=dtype)
+        self.counts = [0] * L
+
+    def cascade_weak(self):
+        """recurrent.py:42-54: a full level (count == 2^level) is merged into
+        the next level and emptied; stop at the first non-full level."""
+        for level in range(self.L):
+            capacity = 2 ** level
+            if self.counts[level] == capacity:
+                nxt = level + 1
+                self.states[..., nxt] = self.states[..., nxt] + self.states[..., level]
+                self.counts[nxt] += self.counts[level]
+                self.states[..., level] = 0.0
+                self.counts[level] = 0
+            elif self.counts[level] < capacity:
+                break
+            else:
+                raise ValueError("level over capacity")
+
+    def insert(self, gate: torch.Tensor, value: torch.Tensor):
+        """recurrent.py:76-94 (MAMBA2 branch): cascade, decay every level by the
+        scalar gate, then the new token's k v^T becomes level 0."""
+        self.cascade_weak()
+        self.states = gate[:, :, None, None, None] * self.states
+        self.states[..., 0] = value
+        self.counts[0] += 1
+
+    def dot(self, lam: torch.Tensor) -> torch.Tensor:
+        """recurrent.py:96-100 with step_output :159-166 weights: sum_l lam_l S_l."""
+        return torch.einsum("bhkvl,bhl->bhkv", self.states, lam)
+
+
+def recurrent_fwd(q, k, v, g, l, return_state: bool = False):
+    """hattention_recurrent (recurrent.py:169-216) for HStruct.MAMBA2."""
+    B, T, G, H, K, V, L = _check(q, k, v, g, l)
+    q = _expand_groups(q, H)
+    k = _expand_groups(k, H)
+    S = FenwickState(B, H, K, V, L, q.dtype)
+    ys = []
+    for t in range(T):
+        value = torch.einsum("bhk,bhv->bhkv", k[:, t], v[:, t])      # step_state :145
+        S.insert(torch.exp(g[:, t]), value)                          # a = exp(g)
+        Sl = S.dot(l[:, t])
+        ys.append(torch.einsum("bhk,bhkv->bhv", q[:, t], Sl))       # step_output :166
+    o = torch.stack(ys, dim=1)
+    return (o, S) if return_state else o
+
+
+# --------------------------------------------------------------------------
+# 3. plain SSD scan (lambda == 1 special case)
+# --------------------------------------------------------------------------
+def ssd_scan_fwd(q, k, v, g) -> torch.Tensor:
+    """h_t = exp(g_t) h_{t-1} + k_t v_t^T ; o_t = q_t . h_t (no hierarchy)."""
+    B, T, G, K = q.shape
+    H, V = v.shape[2], v.shape[3]
+    q = _expand_groups(q, H)
+    k = _expand_groups(k, H)
+    h = torch.zeros(B, H, K, V, dtype=q.dtype)
+    ys = []
+    for t in range(T):
+        h = torch.exp(g[:, t])[:, :, None, None] * h + \
+            torch.einsum("bhk,bhv->bhkv", k[:, t], v[:, t])
+        ys.append(torch.einsum("bhk,bhkv->bhv", q[:, t], h))
+    return torch.stack(ys, dim=1)
+
+
+# --------------------------------------------------------------------------
+# 4. chunked forms
+# --------------------------------------------------------------------------
+def _intra_level_table(C: int) -> torch.Tensor:
+    return torch.from_numpy(levels_matrix(C, default=0, clamp_min=0))
+
+
+def _chunk_views(q, k, v, g, l, C):
+    B, T, G, H, K, V, L = _check(q, k, v, g, l)
+    if T % C != 0:
+        raise ValueError(f"T={T} must be a multiple of the chunk {C}")
+    NT = T // C
+    q = _expand_groups(q, H).reshape(B, NT, C, H, K)
+    k = _expand_groups(k, H).reshape(B, NT, C, H, K)
+    v = v.reshape(B, NT, C, H, V)
+    g = g.reshape(B, NT, C, H)
+    l = l.reshape(B, NT, C, H, L)
+    return q, k, v, g, l, (B, T, H, K, V, L, NT)
+
+
+def _intra_chunk(q, k, v, Gc, l, C):
+    """Diagonal blocks (hssd_minimal.py:170-172; chunk_fwd_kernel_o USE_A,
+    chunkwise.py:590-623): A = (Q K^T) o exp(Gc_t - Gc_s) o lambda[t, lev], causal."""
+    lev = _intra_level_table(C)                                       # [t, s]
+    mask = torch.tril(torch.ones(C, C, dtype=torch.bool))
+    seg = Gc[:, :, :, None, :] - Gc[:, :, None, :, :]                 # [B,NT,t,s,H]
+    seg = seg.masked_fill(~mask[None, None, :, :, None], float("-inf"))
+    tt = torch.arange(C)[:, None].expand(C, C)
+    lam = l.permute(0, 1, 3, 2, 4)[:, :, :, tt, lev]                  # [B,NT,H,t,s]
+    lam = lam.permute(0, 1, 3, 4, 2)                                  # [B,NT,t,s,H]
+    S = torch.einsum("bnthk,bnshk->bntsh", q, k)
+    A = S * torch.exp(seg) * lam
+    return torch.einsum("bntsh,bnshv->bnthv", A, v)
+
+
+def _chunk_states(k, v, Gc):
+    """hssd_minimal.py:176-178: kv_j = sum_s exp(Gc_last - Gc_s) k_s v_s^T."""
+    decay = torch.exp(Gc[:, :, -1:, :] - Gc)                         # [B,NT,C,H]
+    return torch.einsum("bnshk,bnsh,bnshv->bnhkv", k, decay, v)
+
+
+def chunked_fwd(q, k, v, g, l, chunk_size: int = 64) -> torch.Tensor:
+    """hssd_minimal_discrete (hssd_minimal.py:108-220), HType.WEAK.
+
+    Inter-chunk part: for each inter-chunk level ell the chunk-level decay matrix
+    exp(Cend[i-1] - Cend[j]) (hssd_minimal.py:184-188) is masked to the chunk
+    pairs whose level is ell (:199-206) and applied to the chunk states; the
+    reading chunk's output gets lambda[t, ell_h0 + ell] * exp(Gc_t) q_t . state
+    (:210-212).  Levels come from the closed form instead of the T x T table.
+    """
+    C = chunk_size
+    q, k, v, g, l, (B, T, H, K, V, L, NT) = _chunk_views(q, k, v, g, l, C)
+    ell_h0 = get_num_levels(C, 2)
+    nlev = math.ceil(math.log2(NT)) if NT > 1 else 0
+    if ell_h0 + nlev > L:
+        raise ValueError("too few levels")
+    Gc = torch.cumsum(g, dim=2)                                      # chunk-local
+    y = _intra_chunk(q, k, v, Gc, l, C)
+    if NT > 1:
+        kv = _chunk_states(k, v, Gc)                                 # [B,NT,H,K,V]
+        Cend = torch.cumsum(Gc[:, :, -1, :], dim=1)                  # [B,NT,H]
+        Cprev = torch.cat([torch.zeros_like(Cend[:, :1]), Cend[:, :-1]], dim=1)
+        seg = Cprev[:, :, None, :] - Cend[:, None, :, :]             # [B,i,j,H]
+        ii = torch.arange(NT)[:, None]
+        jj = torch.arange(NT)[None, :]
+        below = jj < ii
+        seg = seg.masked_fill(~below[None, :, :, None], float("-inf"))
+        dchunk = torch.exp(seg)
+        clev = torch.from_numpy(levels_matrix(NT, default=0, clamp_min=0)) - 1
+        out_decay = torch.exp(Gc)                                    # [B,NT,C,H]
+        for ell in range(nlev):
+            m = (clev == ell) & below
+            d = dchunk * m[None, :, :, None].to(dchunk.dtype)
+            st = torch.einsum("bijh,bjhkv->bihkv", d, kv)
+            qs = torch.einsum("bnthk,bnhkv->bnthv", q, st)
+            y = y + qs * (out_decay * l[..., ell_h0 + ell])[..., None]
+    return y.reshape(B, T, H, V)
+
+
+def chunked_scan_fwd(q, k, v, g, l, chunk_size: int = 64,
+                     output_final_state: bool = False
+                     ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """chunkwise_fwd (chunkwise.py:1118-1275): returns (o, g_cumsum, ht).
+
+    Per inter-chunk level ell (chunkwise.py:1219), scan the chunks in order
+    (chunk_fwd_kernel_h, :179-266): the reading chunks (bit ell set, :523-527)
+    first add lambda[t, ell_h0+ell] exp(Gc_t) q_t h (:576-606); then the state
+    is reset after the last chunk of each aligned 2^(ell+1) block or decayed by
+    exp(Gc_last) (:235-239), and the writing chunks (bit ell clear) add their
+    decayed k^T v (:256-266).  With ``output_final_state`` the last chunk decays
+    instead of resetting and the state is stored at level ell_h0+ell (:229-279).
+    """
+    C = chunk_size
+    B0, T0 = q.shape[0], q.shape[1]
+    q, k, v, g, l, (B, T, H, K, V, L, NT) = _chunk_views(q, k, v, g, l, C)
+    ell_h0 = get_num_levels(C, 2)
+    nlev = math.ceil(math.log2(NT)) if NT > 1 else 0
+    if ell_h0 + nlev > L:
+        raise ValueError("too few levels")
+    Gc = torch.cumsum(g, dim=2)
+    y = _intra_chunk(q, k, v, Gc, l, C)
+    ht = torch.zeros(B, H, K, V, L, dtype=q.dtype) if output_final_state else None
+    if NT > 1 or output_final_state:
+        kv = _chunk_states(k, v, Gc)                                 # [B,NT,H,K,V]
+        last = torch.exp(Gc[:, :, -1, :])                            # [B,NT,H]
+        out_decay = torch.exp(Gc)
+        ys = [y[:, i] for i in range(NT)]
+        for ell in range(nlev):
+            h = torch.zeros(B, H, K, V, dtype=q.dtype)
+            period = 1 << (ell + 1)
+            scale = out_decay * l[..., ell_h0 + ell]                 # [B,NT,C,H]
+            for i in range(NT):
+                if (i >> ell) & 1:                                   # reading chunk
+                    qs = torch.einsum("bthk,bhkv->bthv", q[:, i], h)
+                    ys[i] = ys[i] + qs * scale[:, i][..., None]
+                reset = (i % period == period - 1)
+                if output_final_state and i == NT - 1:
+                    reset = False
+                h = torch.zeros_like(h) if reset else h * last[:, i][:, :, None, None]
+                if not (i >> ell) & 1:                               # writing chunk
+                    h = h + kv[:, i]
+            if output_final_state:
+                ht[..., ell_h0 + ell] = h
+        y = torch.stack(ys, dim=1)
+    g_cumsum = Gc.reshape(B0, T0, H)
+    return y.reshape(B, T, H, V), g_cumsum, ht
+
+
+# --------------------------------------------------------------------------
+# 5. backward through autograd
+# --------------------------------------------------------------------------
+def autograd_bwd(fwd, q, k, v, g, l, do, **kw):
+    """(dq, dk, dv, dg, dl) of sum(o * do) for any forward form above.
+
+    Matches the reference's return contract (kernel.py:230-236): dq/dk have the
+    grouped shape of q/k, dg is w.r.t. the raw per-step g.
+    """
+    leaves = [x.detach().clone().requires_grad_(True) for x in (q, k, v, g, l)]
+    o = fwd(*leaves, **kw)
+    if isinstance(o, tuple):
+        o = o[0]
+    grads = torch.autograd.grad((o * do).sum(), leaves)
+    return tuple(grads)
+
+
+def brute_force_fwd(q, k, v, g, l) -> torch.Tensor:
+    """Pair-by-pair loop over (t, s) using the reference's own recursive level
+    function (base.py:41-46) and the product of exp(g) over (s, t] exactly as
+    base.py:87-96 writes it (tiny T only)."""
+    B, T, G, H, K, V, L = _check(q, k, v, g, l)
+    q = _expand_groups(q, H)
+    k = _expand_groups(k, H)
+    A = torch.exp(g)
+    o = torch.zeros(B, T, H, V, dtype=q.dtype)
+    for t in range(T):
+        for s in range(t + 1):
+            lev = 0 if s == t else level_weak_recursive(t, s)
+            w = l[:, t, :, lev] * torch.prod(A[:, s + 1:t + 1], dim=1) * \
+                (q[:, t] * k[:, s]).sum(-1)
+            o[:, t] += w[..., None] * v[:, s]
+    return o

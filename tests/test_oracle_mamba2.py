@@ -1,0 +1,139 @@
+"""Pin the log-linear Mamba-2 oracle (oracle/mamba2.py).
+
+Checks (all float64 on CPU):
+* materialised H form == Fenwick recurrent form == chunked form == chunked
+  level-scan form (four structurally different algorithms);
+* brute-force pair loop with the reference's recursive level function and
+  the product of exp(g) over (s, t] equals the materialised form;
+* lambda == 1 reduces to the textbook SSD recurrence (no hierarchy);
+* g == 0 (no decay) and lambda one-hot on a single level select exactly the
+  pairs of that level;
+* the final per-level states of the level scan equal the recurrent form's
+  Fenwick states decayed to the sequence end (levels >= ell_h0);
+* torch.autograd.gradcheck (finite differences) on the chunked form, and the
+  identity dG_t = q_t.dq_t - k_t.dk_t used by the HIP backward.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import mamba2 as M
+from oracle.levels import levels_matrix
+
+
+def make_inputs(B, T, H, K, V, L, G=None, seed=0, dtype=torch.float64):
+    gen = torch.Generator().manual_seed(seed)
+    G = G or H
+    q = torch.randn(B, T, G, K, generator=gen, dtype=dtype)
+    k = torch.randn(B, T, G, K, generator=gen, dtype=dtype)
+    v = torch.randn(B, T, H, V, generator=gen, dtype=dtype)
+    A = torch.exp(torch.empty(H, dtype=dtype).uniform_(0.0, math.log(16.0), generator=gen))
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, generator=gen, dtype=dtype) - 3.0)
+    g = -A * dt
+    l = torch.nn.functional.softplus(torch.randn(B, T, H, L, generator=gen, dtype=dtype))
+    return q, k, v, g, l
+
+
+def rel(a, b):
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+@pytest.mark.parametrize("T,C", [(16, 4), (32, 8), (64, 8)])
+def test_four_forms_agree(T, C):
+    L = int(math.log2(T)) + 1
+    q, k, v, g, l = make_inputs(2, T, 3, 5, 4, L)
+    o_mat = M.materialized_fwd(q, k, v, g, l)
+    o_rec = M.recurrent_fwd(q, k, v, g, l)
+    o_chk = M.chunked_fwd(q, k, v, g, l, chunk_size=C)
+    o_scn, gc, _ = M.chunked_scan_fwd(q, k, v, g, l, chunk_size=C)
+    assert rel(o_rec, o_mat) < 1e-12
+    assert rel(o_chk, o_mat) < 1e-12
+    assert rel(o_scn, o_mat) < 1e-12
+    # chunk-local inclusive cumsum of g (chunkwise.py:1175)
+    ref_gc = torch.cumsum(g.reshape(2, T // C, C, 3), dim=2).reshape(2, T, 3)
+    assert torch.allclose(gc, ref_gc)
+
+
+def test_brute_force_matches_materialized():
+    T = 24
+    q, k, v, g, l = make_inputs(1, T, 2, 3, 3, 6)
+    assert rel(M.brute_force_fwd(q, k, v, g, l), M.materialized_fwd(q, k, v, g, l)) < 1e-12
+
+
+def test_groups():
+    T, H, G = 32, 4, 2
+    q, k, v, g, l = make_inputs(1, T, H, 4, 3, 6, G=G)
+    o = M.chunked_fwd(q, k, v, g, l, chunk_size=8)
+    q2 = q.repeat_interleave(H // G, dim=2)
+    k2 = k.repeat_interleave(H // G, dim=2)
+    assert rel(o, M.materialized_fwd(q2, k2, v, g, l)) < 1e-12
+
+
+def test_lambda_one_is_plain_ssd():
+    T = 64
+    q, k, v, g, l = make_inputs(2, T, 2, 4, 3, 7)
+    l = torch.ones_like(l)
+    ref = M.ssd_scan_fwd(q, k, v, g)
+    assert rel(M.chunked_fwd(q, k, v, g, l, chunk_size=8), ref) < 1e-12
+    assert rel(M.recurrent_fwd(q, k, v, g, l), ref) < 1e-12
+
+
+@pytest.mark.parametrize("level", [0, 1, 3, 5, 6])
+def test_one_hot_level_selects_pairs(level):
+    T = 64
+    q, k, v, _, l = make_inputs(1, T, 1, 3, 2, 7, seed=level)
+    g = torch.zeros(1, T, 1, dtype=torch.float64)          # no decay
+    l = torch.zeros_like(l)
+    l[..., level] = 1.0
+    o = M.chunked_fwd(q, k, v, g, l, chunk_size=8)
+    lev = torch.from_numpy(levels_matrix(T, default=-1))
+    mask = (lev == level).to(torch.float64)
+    ref = torch.einsum("ts,ts,sv->tv", torch.einsum("tk,sk->ts", q[0, :, 0], k[0, :, 0]),
+                       mask, v[0, :, 0])
+    assert rel(o[0, :, 0], ref) < 1e-12
+
+
+def test_final_state_matches_recurrent():
+    T, C = 64, 8
+    L = 7
+    q, k, v, g, l = make_inputs(1, T, 2, 3, 4, L)
+    o, _, ht = M.chunked_scan_fwd(q, k, v, g, l, chunk_size=C, output_final_state=True)
+    o_rec, S = M.recurrent_fwd(q, k, v, g, l, return_state=True)
+    # The level scan holds, per inter-chunk level, the decayed sum of the
+    # chunks in that level's open block; with T a power of two the recurrent
+    # state after T tokens has every token merged into its top levels.  Their
+    # sum over levels >= ell_h0 plus the recurrent state's levels < ell_h0 is
+    # the full decayed sum of k v^T over all tokens.
+    ell_h0 = 4
+    total_scan = ht[..., ell_h0:].sum(-1) + S.states[..., :ell_h0].sum(-1)
+    Gt = torch.cumsum(g, 1)
+    full = torch.einsum("bthk,bthv,bth->bhkv", k, v, torch.exp(Gt[:, -1:] - Gt))
+    assert rel(total_scan, full) < 1e-12
+    assert rel(o, o_rec) < 1e-12
+
+
+def test_gradcheck_chunked():
+    T = 16
+    q, k, v, g, l = make_inputs(1, T, 1, 3, 2, 5)
+    for x in (q, k, v, g, l):
+        x.requires_grad_(True)
+    fn = lambda *a: M.chunked_fwd(*a, chunk_size=4)
+    assert torch.autograd.gradcheck(fn, (q, k, v, g, l), eps=1e-6, atol=1e-7)
+
+
+def test_backward_forms_agree_and_dg_identity():
+    T, C = 32, 8
+    q, k, v, g, l = make_inputs(2, T, 2, 4, 3, 6)
+    do = torch.randn(2, T, 2, 3, dtype=torch.float64)
+    gm = M.autograd_bwd(M.materialized_fwd, q, k, v, g, l, do)
+    gc = M.autograd_bwd(M.chunked_fwd, q, k, v, g, l, do, chunk_size=C)
+    gs = M.autograd_bwd(lambda *a: M.chunked_scan_fwd(*a, chunk_size=C)[0], q, k, v, g, l, do)
+    for a, b, c in zip(gm, gc, gs):
+        assert rel(b, a) < 1e-11 and rel(c, a) < 1e-11
+    dq, dk, dv, dg, dl = gm
+    dG = (q * dq).sum(-1) - (k * dk).sum(-1)                 # [B, T, H]
+    dg_from_identity = torch.flip(torch.cumsum(torch.flip(dG, [1]), 1), [1])
+    assert rel(dg_from_identity, dg) < 1e-10
+    # and the lambda form of the row sums: sum_l lambda dlambda = q . dq
+    assert rel((l * dl).sum(-1), (q * dq).sum(-1)) < 1e-10

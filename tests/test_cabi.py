@@ -1,0 +1,91 @@
+"""The C-ABI library loads and exports every entry point include/hattn.h declares.
+
+CPU-only: no compute call is made.  The argument checks of the entry points
+run on the host before any HIP call, so invalid shapes are exercised here and
+must come back as the status codes that the Python layer maps to the
+reference's exception types (chunkwise.py:1140-1153, 1211-1214).
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from hattention import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hattn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hattn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "hattn_mamba2_chunkwise_fwd" in syms
+    assert "hattn_version" in syms and "hattn_last_error" in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(hattn_[a-z0-9_]+)\b", out))
+    for s in declared_symbols():
+        assert s in exported, s
+        assert getattr(lib, s) is not None
+
+
+def test_binding_table_covers_header():
+    bound = {name for name, _, _ in _lib.SIGNATURES}
+    assert set(declared_symbols()) <= bound
+
+
+def test_version_string():
+    v = _lib.load().hattn_version().decode()
+    assert v.startswith("hattn-mi355x") and "gfx950" in v
+
+
+def _fwd(**kw):
+    a = dict(B=1, T=128, G=1, H=1, K=64, V=64, L=8, dq=0, dv=0, dl=0, do=0, base=2, htype=0,
+             chunk=64)
+    a.update(kw)
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: every case fails validation first
+    return lib.hattn_mamba2_chunkwise_fwd(p, p, p, p, p, p, None, None, a["B"], a["T"], a["G"],
+                                          a["H"], a["K"], a["V"], a["L"], a["dq"], a["dv"],
+                                          a["dl"], a["do"], a["base"], a["htype"], a["chunk"],
+                                          None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(T=100), _lib.HATTN_ERR_VALUE),            # T % 64
+    (dict(T=0), _lib.HATTN_ERR_VALUE),
+    (dict(H=3, G=2), _lib.HATTN_ERR_VALUE),         # G does not divide H
+    (dict(L=7), _lib.HATTN_ERR_VALUE),              # L < 7 + ceil(log2(T/64))
+    (dict(V=40), _lib.HATTN_ERR_VALUE),
+    (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(base=3), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(K=128), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(dq=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp32 q/k is the bf16x3 entry point's
+])
+def test_fwd_argument_checks(kw, code):
+    assert _fwd(**kw) == code
+    msg = _lib.load().hattn_last_error().decode()
+    assert msg
+
+
+def test_status_maps_to_reference_exceptions():
+    lib = _lib.load()
+    assert _fwd(T=100) == _lib.HATTN_ERR_VALUE
+    with pytest.raises(ValueError):
+        _lib.check(_lib.HATTN_ERR_VALUE)
+    assert _fwd(chunk=32) == _lib.HATTN_ERR_NOT_IMPLEMENTED
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.HATTN_ERR_NOT_IMPLEMENTED)
+    assert lib.hattn_last_error() is not None

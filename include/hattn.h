@@ -63,10 +63,13 @@ const char* hattn_last_error(void);
  *             7 .. 6 + ceil(log2(T / 64))), or NULL for output_final_state=False.
  *             Levels not written by the kernel are left untouched (the
  *             reference zero-initialises ht, chunkwise.py:1179).
+ *   workspace device scratch of at least
+ *             hattn_mamba2_chunkwise_fwd_workspace(...) bytes (may be NULL
+ *             when that is 0); contents on entry are ignored.
  *
  * Constraints (status on violation):
  *   T % 64 == 0, T >= 64, H % G == 0, L >= 7 + ceil(log2(T / 64)),
- *   V % 16 == 0                                    -> HATTN_ERR_VALUE
+ *   V % 64 == 0, workspace large enough               -> HATTN_ERR_VALUE
  *   chunk_size == 64, level_base == 2, htype == WEAK, K == 64,
  *   dtype_qk == BF16, dtype_v / dtype_l / dtype_o in {BF16, FP32}
  *                                                  -> HATTN_ERR_NOT_IMPLEMENTED
@@ -75,7 +78,14 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
                                const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
                                int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
                                int dtype_l, int dtype_o, int level_base, int htype,
-                               int chunk_size, void* stream);
+                               int chunk_size, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* Workspace bytes hattn_mamba2_chunkwise_fwd needs for these sizes (the
+ * per-segment K x V summaries of the segment-parallel scan).  No counterpart
+ * in the reference, which allocates its intermediates with torch inside
+ * chunkwise_fwd (chunkwise.py:1176-1179). */
+size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, int V, int L);
 
 #ifdef __cplusplus
 }

@@ -62,3 +62,87 @@ __device__ __forceinline__ XcdMap xcd_map(int wg, int nslices) {
 }
 
 }  // namespace hattn
+
+namespace hattn {
+
+// Transposed MFMA fragment from a row-major bf16 tile in LDS (gfx950
+// ds_read_b64_tr_b16).  Lane layout of the instruction, within each group of
+// 16 lanes: lane i receives element (i & 3) of the 8-byte rows addressed by
+// lanes 4j + (i >> 2), j = 0..3.  Lane (lq, ln) therefore addresses row
+// r0 + 8lq + (ln >> 2), columns c0 + 4(ln & 3) .. +3, and receives
+//     X[r0 + 8lq + j][c0 + ln],  j = 0..7   (two reads, rows +0..3 / +4..7),
+// which is the A operand of a contraction over the row index (A[m][k] = X[k][m])
+// or the B operand B[k][n] = X[k][n].  ld, r0, c0 must keep 8-byte alignment.
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+__device__ __forceinline__ bf16x4 ds_read_tr(const __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+}
+
+__device__ __forceinline__ bf16x8 tr_frag(const __bf16* X, int ld, int r0, int c0) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  const __bf16* p = X + (r0 + 8 * lq + (ln >> 2)) * ld + c0 + 4 * (ln & 3);
+  const bf16x4 lo = ds_read_tr(p);
+  const bf16x4 hi = ds_read_tr(p + 4 * ld);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Same read with the row order of a D-layout fragment pair: lane (lq, ln)
+// receives X[r0 + 4lq + j][c0 + ln] (j = 0..3) and X[r0 + 16 + 4lq + j][c0 + ln],
+// the k order {4lq + i, 16 + 4lq + i} in which two stacked 16x16 MFMA D tiles
+// hold rows (see the forward kernel's state fragments).
+__device__ __forceinline__ bf16x8 tr_frag_d(const __bf16* X, int ld, int r0, int c0) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  const __bf16* p = X + (r0 + 4 * lq + (ln >> 2)) * ld + c0 + 4 * (ln & 3);
+  const bf16x4 lo = ds_read_tr(p);
+  const bf16x4 hi = ds_read_tr(p + 16 * ld);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ bf16x4 cvt4(floatx4 x) {
+  return bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
+}
+
+__device__ __forceinline__ bf16x8 cat8(floatx4 a, floatx4 b) {
+  return bf16x8{(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
+}
+
+}  // namespace hattn
+
+namespace hattn {
+
+// Raw buffer access: a 128-bit descriptor in SGPRs holds the (uniform) base
+// address and byte range, so a load or store needs one 32-bit VGPR offset plus
+// an SGPR offset instead of a 64-bit per-lane address.  Accesses beyond the
+// range read zero / are dropped by the hardware.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, size_t bytes) {
+  const unsigned int n = bytes > 0xffffffffull ? 0xffffffffu : (unsigned int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, unsigned int voff, unsigned int soff) {
+  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return uint4{x[0], x[1], x[2], x[3]};
+}
+
+template <typename T> __device__ __forceinline__ T buf_load(rsrc_t r, unsigned int voff, unsigned int soff);
+template <> __device__ __forceinline__ float buf_load<float>(rsrc_t r, unsigned int voff, unsigned int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+template <> __device__ __forceinline__ __bf16 buf_load<__bf16>(rsrc_t r, unsigned int voff, unsigned int soff) {
+  return __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+}
+
+template <typename T> __device__ __forceinline__ void buf_store(T x, rsrc_t r, unsigned int voff, unsigned int soff);
+template <> __device__ __forceinline__ void buf_store<float>(float x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, x), r, voff, soff, 0);
+}
+template <> __device__ __forceinline__ void buf_store<__bf16>(__bf16 x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, x), r, voff, soff, 0);
+}
+
+}  // namespace hattn

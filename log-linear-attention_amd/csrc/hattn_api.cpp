@@ -13,9 +13,11 @@
 #include "../../include/hattn.h"
 
 hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, const float* g,
-                                   const void* l, void* o, float* gcum, float* ht, int B, int T,
-                                   int G, int H, int V, int L, int nlev, int dt_v, int dt_l,
-                                   int dt_o, hipStream_t stream, int* unsupported);
+                                   const void* l, void* o, float* gcum, float* ht, void* ws,
+                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_v,
+                                   int dt_l, int dt_o, hipStream_t stream, int* unsupported);
+size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V);
+int hattn_mamba2_fwd_max_levels();
 
 namespace {
 
@@ -54,11 +56,20 @@ const char* hattn_version(void) { return "hattn-mi355x 0.1.0 gfx950"; }
 
 const char* hattn_last_error(void) { return g_err; }
 
+size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, int V, int L) {
+  (void)G;
+  (void)K;
+  (void)L;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0) return 0;
+  return hattn_mamba2_fwd_ws_bytes(B, T, H, V);
+}
+
 int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
                                const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
                                int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
                                int dtype_l, int dtype_o, int level_base, int htype,
-                               int chunk_size, void* stream) {
+                               int chunk_size, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
@@ -69,21 +80,26 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
     return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
   if (H % G != 0) return fail(HATTN_ERR_VALUE, "H=%d is not a multiple of G=%d", H, G);
-  if (V % 16 != 0) return fail(HATTN_ERR_VALUE, "V=%d and BV could be 16", V);
+  if (V % 64 != 0) return fail(HATTN_ERR_VALUE, "V=%d and BV could be 64", V);
   if (K != 64) return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d (the MI355X kernel supports 64)", K);
   const int NT = T / 64;
   const int nlev = ceil_log2(NT);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
-  if (nlev > 17) return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^17", T);
-  if (7 + nlev > 24) return fail(HATTN_ERR_NOT_IMPLEMENTED, "too many levels");
+  if (nlev > hattn_mamba2_fwd_max_levels())
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
+                hattn_mamba2_fwd_max_levels());
   if (dtype_qk != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 required)", dtype_qk);
   if (!q || !k || !v || !g || !l || !o) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, V);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+    return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
   int unsupported = 0;
-  hipError_t e = hattn_mamba2_fwd_launch(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, V, L, nlev,
-                                         dtype_v, dtype_l, dtype_o, (hipStream_t)stream,
-                                         &unsupported);
+  hipError_t e = hattn_mamba2_fwd_launch(q, k, v, g, l, o, g_cumsum, ht, workspace, B, T, G, H,
+                                         V, L, nlev, dtype_v, dtype_l, dtype_o,
+                                         (hipStream_t)stream, &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d o=%d", dtype_v, dtype_l,
                 dtype_o);

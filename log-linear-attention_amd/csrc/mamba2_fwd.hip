@@ -1,366 +1,622 @@
-// Log-linear Mamba-2 chunkwise forward, fused into one pass over the sequence.
+// Log-linear Mamba-2 chunkwise forward for gfx950, segment-parallel.
 //
 // Replaces the reference's 1 + 2 * nlev Triton launches (chunkwise.py:1118-1275:
 // chunk_fwd_kernel_o with USE_A, then per inter-chunk level chunk_fwd_kernel_h
-// and chunk_fwd_kernel_o) with a single launch that reads q, k, v, g, lambda
-// once and writes o once.
+// and chunk_fwd_kernel_o) with two launches; the main one reads q, k, v, g and
+// lambda once and writes o once.
 //
-// One workgroup (4 wavefronts) owns one (batch, head) row and one 16-wide slice
-// of V and walks the 64-token chunks in order:
-//   * intra-chunk tile: S^T = K Q^T on MFMA, masked by the causal mask, scaled
-//     by exp(Gc_t - Gc_s) and lambda[t, bit_length(t ^ s)] in registers, then
-//     A V on MFMA (the D fragment of S^T is the A operand of A V);
-//   * inter-chunk Fenwick levels: the per-level K x V states live in fp32
-//     registers (wave w owns state rows 16w..16w+15) and are mirrored in LDS as
-//     bf16 for the levels the next chunk reads; each chunk's decayed K^T V is
-//     computed once and added to every level whose bit is clear (the reference
-//     recomputes it once per level, chunkwise.py:256-266);
-//   * reading levels (bits set in the chunk index) add
-//     lambda[t, 7 + ell] * exp(Gc_t) * q_t h_ell to the same fp32 accumulator,
-//     so o is stored once.
-// Loads for chunk i+1 are issued before chunk i is computed (register
-// prefetch); LDS holds two input stages and two state buffers, so one barrier
-// per chunk suffices.
+// The sequence of NT 64-token chunks is cut into aligned segments of S = 2^s
+// chunks, so a Fenwick block of 2^(e+1) <= S chunks never straddles a segment.
+// Inter-chunk level e (absolute level 7 + e) is
+//   * local (e < s): its blocks live inside one segment; the main kernel keeps
+//     the state in fp32 registers while it walks the segment's chunks;
+//   * top (e >= s): every chunk of segment p reads the same block of whole
+//     earlier segments (bit e - s of p set), decayed to the chunk.  With scalar
+//     per-token decay that state is exp(E_i) * Htop_e(p), where E_i is the
+//     log-decay from the segment start to chunk i and
+//         Htop_e(p) = sum_{q in block} exp(sum_{r=q+1}^{p-1} D_r) Sum(q),
+//         Sum(q)    = sum_{t in q} exp(G_end(q) - G_t) k_t v_t^T,
+//     with D_r the total log-decay of segment r.
+//
+// Kernel 1 (seg_sum) streams K, V, g and writes Sum(q) (fp32 [K, V]) and D_q
+// per segment.  Kernel 2 (main) builds Htop for its segment from those
+// summaries, then walks the segment's chunks.  One workgroup (4 waves) owns
+// one (batch, head) row, one segment and one 64-wide block of V:
+//   phase 1  the ten causal 16x16 tiles of S^T = K Q^T (three per wave, balanced)
+//            on MFMA, scaled by exp(Gc_t - Gc_s) and lambda[t, bit_length(t ^ s)]
+//            in registers, written as A = (S o M) in bf16 to LDS;
+//   phase 2  wave w owns V columns 16w..16w+15 for all 64 tokens: o = A V plus,
+//            for every level the chunk reads, lambda[t, 7 + e] exp(Gc_t) q_t h_e;
+//   phase 3  wave w updates the local-level states for its V columns with the
+//            chunk's decayed K^T V, computed once for all levels (the reference
+//            recomputes it once per level, chunkwise.py:256-266).
+// The level states stay in registers in the MFMA D layout; read as B operands
+// they pair row k = 32c + 4lq + i / 32c + 16 + 4lq + i with the same k order in
+// the Q fragments (any bijection of the contraction index works if both
+// operands use it).  K^T and V fragments of the contractions over t come from
+// row-major LDS tiles through the transposing LDS read.
+#include <cstddef>
+
 #include "common.h"
 
 namespace hattn {
 
 constexpr int kBT = 64;       // chunk length (the reference's only chunk size)
 constexpr int kKD = 64;       // head dim of q / k
-constexpr int kBV = 16;       // V columns per workgroup
-constexpr int kMaxLev = 17;   // inter-chunk levels supported (T <= 64 * 2^17)
-constexpr int kRow = 72;      // LDS row stride (bf16) of 64-wide tiles
-constexpr int kLamPerLane = 6;  // lambda elements per lane per chunk (16 rows x <= 24 cols)
+constexpr int kMaxLoc = 4;    // local levels held in registers (S <= 16 chunks)
+constexpr int kMaxTop = 8;    // top levels (LDS-resident, T <= 64 * 2^12)
+constexpr int kMaxLU = 7 + kMaxLoc + kMaxTop;  // lambda columns read (levels 0 .. 6 + nlev)
+constexpr int kLd = 72;       // LDS row stride (bf16) of 64-wide tiles
 
-struct FwdSmem {
-  int stage_bytes;
-  int off_k, off_kt, off_vt, off_gc, off_lam;
-  int off_h;      // state mirror: [2][nlev][kBV][kRow] bf16
-  int total;
-  int lam_stride;
-};
-
-__host__ __device__ inline FwdSmem fwd_smem_layout(int nlev) {
-  FwdSmem s;
-  const int lu = 7 + nlev;
-  s.lam_stride = lu | 1;
-  s.off_k = 0;
-  s.off_kt = s.off_k + kBT * kRow * 2;
-  s.off_vt = s.off_kt + kKD * kRow * 2;
-  s.off_gc = s.off_vt + kBV * kRow * 2;
-  s.off_lam = s.off_gc + kBT * 4;
-  int end = s.off_lam + kBT * s.lam_stride * 4;
-  s.stage_bytes = (end + 15) & ~15;
-  s.off_h = 2 * s.stage_bytes;
-  s.total = s.off_h + 2 * (nlev > 0 ? nlev : 1) * kBV * kRow * 2;
-  return s;
+// Chunks per segment: 16 (2^kMaxLoc), or the whole sequence when shorter.
+__host__ __device__ inline int seg_log2(int NT) {
+  int nlev = 0;
+  while ((1 << nlev) < NT) ++nlev;
+  return nlev < kMaxLoc ? nlev : kMaxLoc;
 }
 
-// Registers holding one chunk's global loads until they are written to LDS.
-template <typename TV, typename TL>
-struct ChunkRegs {
-  bf16x8 q[2];   // own rows of Q in the MFMA fragment layout
-  uint4 k[2];    // two 16-byte units of K (row = u / 8, cols 8 * (u % 8) ..)
-  uint4 v;       // one 16-byte unit of the V slice
-  float g;       // g[t] for t = lane (wave 0 only)
-  TL lam[kLamPerLane];
+// ---------------------------------------------------------------------------
+// chunk staging shared by both kernels
+// ---------------------------------------------------------------------------
+// Row-major 64 x 64 bf16 tile of a [.., T, heads, 64-block] tensor: 512 units
+// of 16 bytes, two per thread.
+__device__ __forceinline__ void load_tile_bf16(uint4 (&r)[2], const __bf16* __restrict__ base,
+                                               int row_stride) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int u = tid + 256 * rr;
+    r[rr] = *(const uint4*)(base + (u >> 3) * row_stride + 8 * (u & 7));
+  }
+}
+
+__device__ __forceinline__ void store_tile_bf16(const uint4 (&r)[2], __bf16* s) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int u = tid + 256 * rr;
+    *(uint4*)(s + (u >> 3) * kLd + 8 * (u & 7)) = r[rr];
+  }
+}
+
+template <typename TV>
+struct VTile {
+  static constexpr int N = sizeof(TV) == 2 ? 2 : 4;
+  uint4 r[N];
 };
 
-template <typename TV, typename TL>
-__device__ __forceinline__ void load_chunk(ChunkRegs<TV, TL>& r, const __bf16* __restrict__ q,
-                                           const __bf16* __restrict__ k, const TV* __restrict__ v,
-                                           const float* __restrict__ g, const TL* __restrict__ l,
-                                           int b, int h, int gq, int vb, int t0, int T, int G,
-                                           int H, int V, int L, int lu) {
+template <typename TV>
+__device__ __forceinline__ void load_vtile(VTile<TV>& t, const TV* __restrict__ base,
+                                           int row_stride) {
+  const int tid = threadIdx.x;
+  if constexpr (sizeof(TV) == 2) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int u = tid + 256 * rr;
+      t.r[rr] = *(const uint4*)(base + (u >> 3) * row_stride + 8 * (u & 7));
+    }
+  } else {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int u = tid + 256 * rr;
+      t.r[rr] = *(const uint4*)(base + (u >> 4) * row_stride + 4 * (u & 15));
+    }
+  }
+}
+
+template <typename TV>
+__device__ __forceinline__ void store_vtile(const VTile<TV>& t, __bf16* s) {
+  const int tid = threadIdx.x;
+  if constexpr (sizeof(TV) == 2) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int u = tid + 256 * rr;
+      *(uint4*)(s + (u >> 3) * kLd + 8 * (u & 7)) = t.r[rr];
+    }
+  } else {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int u = tid + 256 * rr;
+      const float* e = (const float*)&t.r[rr];
+      *(bf16x4*)(s + (u >> 4) * kLd + 4 * (u & 15)) = bf16x4{(__bf16)e[0], (__bf16)e[1],
+                                                             (__bf16)e[2], (__bf16)e[3]};
+    }
+  }
+}
+
+// Inclusive cumsum of g over the 64 tokens of a chunk (fla chunk_local_cumsum,
+// chunkwise.py:1175); lane l holds g[t = l] on entry and Gc[l] on exit.
+__device__ __forceinline__ float chunk_cumsum(float x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1: per-segment summaries Sum(q) and total log-decay D_q
+// ---------------------------------------------------------------------------
+// One workgroup per (row, segment, 64-column block of V).  Wave w owns summary
+// rows k = 16w .. 16w + 15, all 64 columns (4 MFMA tiles).
+struct SumSmem {
+  __bf16 k[2][kBT * kLd];
+  __bf16 v[2][kBT * kLd];
+  float wt[2][kBT];   // exp(Gc_last - Gc_t)
+  float cl[2];        // chunk total Gc_last
+};
+
+template <typename TV>
+__global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
+    const __bf16* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
+    float* __restrict__ sums, float* __restrict__ segd, int T, int G, int H, int V, int NT,
+    int S, int NSEG, int nvb64) {
+  __shared__ __attribute__((aligned(16))) SumSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const size_t rowq = (size_t)b * T + t0;
-  // Q: lane (lq, ln) -> row 16w + ln, cols 32c + 8lq .. +7
-  {
-    const __bf16* p = q + ((rowq + 16 * w + ln) * G + gq) * kKD + 8 * lq;
-    r.q[0] = *(const bf16x8*)(p);
-    r.q[1] = *(const bf16x8*)(p + 32);
-  }
-  // K: units u = tid, tid + 256 ; row u >> 3, col 8 * (u & 7)
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int u = tid + 256 * rr;
-    const __bf16* p = k + ((rowq + (u >> 3)) * G + gq) * kKD + 8 * (u & 7);
-    r.k[rr] = *(const uint4*)p;
-  }
-  // V slice: 64 rows x 16 columns
+  const int vblk = blockIdx.x % nvb64;
+  const int rest = blockIdx.x / nvb64;
+  const int h = rest % H, p = (rest / H) % NSEG, b = rest / (H * NSEG);
+  const int row = b * H + h, gq = h / (H / G);
+  const int c0 = p * S;
+  const int nch = min(S, NT - c0);
+  const int vcol0 = vblk * 64;
+  const int kstr = G * kKD, vstr = H * V;
+  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * kstr * 2);
+  const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
+  const rsrc_t rgg = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
+  const unsigned int vo_k = ((tid >> 3) * kstr + 8 * (tid & 7)) * 2;
+  unsigned int vo_v, so_v2;
   if constexpr (sizeof(TV) == 2) {
-    if (tid < 128) {
-      const TV* p = v + ((rowq + (tid >> 1)) * H + h) * V + vb * kBV + 8 * (tid & 1);
-      r.v = *(const uint4*)p;
-    }
+    vo_v = ((tid >> 3) * vstr + 8 * (tid & 7)) * 2;
+    so_v2 = 32 * vstr * 2;
   } else {
-    const TV* p = v + ((rowq + (tid >> 2)) * H + h) * V + vb * kBV + 4 * (tid & 3);
-    r.v = *(const uint4*)p;
+    vo_v = ((tid >> 4) * vstr + 4 * (tid & 15)) * 4;
+    so_v2 = 16 * vstr * 4;
   }
-  if (w == 0) r.g = g[(rowq + lane) * H + h];
-  // lambda: wave w loads its own 16 rows, lu columns
+  const unsigned int vo_g = lane * H * 4;
+
+  floatx4 acc[4];
 #pragma unroll
-  for (int rr = 0; rr < kLamPerLane; ++rr) {
-    const int e = lane + 64 * rr;
-    if (e < 16 * lu) {
-      const int row = 16 * w + e / lu, col = e % lu;
-      r.lam[rr] = l[((rowq + row) * H + h) * L + col];
-    }
+  for (int n = 0; n < 4; ++n) acc[n] = zero4();
+  float dsum = 0.f;
+
+  uint4 k0, k1;
+  VTile<TV> vr;
+  float gr = 0.f;
+#define SEG_LOAD(jj)                                                                   \
+  {                                                                                    \
+    const unsigned int row0 = (unsigned int)(c0 + (jj)) * kBT;                         \
+    k0 = buf_load16(rk, vo_k, row0 * kstr * 2);                                        \
+    k1 = buf_load16(rk, vo_k, (row0 + 32) * kstr * 2);                                 \
+    _Pragma("unroll") for (int rr = 0; rr < VTile<TV>::N; ++rr)                        \
+        vr.r[rr] = buf_load16(rv, vo_v, row0 * vstr * sizeof(TV) + rr * so_v2);        \
+    if (w == 0) gr = buf_load<float>(rgg, vo_g, row0 * H * 4);                         \
   }
+#define SEG_STORE(buf)                                                                 \
+  {                                                                                    \
+    *(uint4*)(sm.k[buf] + (tid >> 3) * kLd + 8 * (tid & 7)) = k0;                      \
+    *(uint4*)(sm.k[buf] + ((tid >> 3) + 32) * kLd + 8 * (tid & 7)) = k1;               \
+    store_vtile(vr, sm.v[buf]);                                                        \
+    if (w == 0) {                                                                      \
+      const float x = chunk_cumsum(gr);                                                \
+      const float last = __shfl(x, 63, 64);                                            \
+      sm.wt[buf][lane] = fexp(last - x);                                               \
+      if (lane == 0) sm.cl[buf] = last;                                                \
+    }                                                                                  \
+  }
+  SEG_LOAD(0);
+  SEG_STORE(0);
+  if (nch > 1) SEG_LOAD(1);
+  __syncthreads();
+  for (int j = 0; j < nch; ++j) {
+    const int buf = j & 1;
+    const float clast = sm.cl[buf];
+    const float dl = fexp(clast);
+    dsum += clast;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[n][i] *= dl;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const bf16x8 a = tr_frag(sm.k[buf], kLd, 32 * c, 16 * w);   // K^T[k][t]
+      const floatx4 w0 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq]);
+      const floatx4 w1 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq + 4]);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const bf16x8 vv = tr_frag(sm.v[buf], kLd, 32 * c, 16 * n);  // V[t][v]
+        bf16x8 bv;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          bv[jj] = (__bf16)((float)vv[jj] * w0[jj]);
+          bv[4 + jj] = (__bf16)((float)vv[4 + jj] * w1[jj]);
+        }
+        acc[n] = mfma16x16x32(a, bv, acc[n]);
+      }
+    }
+    if (j + 1 < nch) {
+      SEG_STORE(buf ^ 1);
+      if (j + 2 < nch) SEG_LOAD(j + 2);
+    }
+    __syncthreads();
+  }
+#undef SEG_LOAD
+#undef SEG_STORE
+  float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[(size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln] = acc[n][i];
+  if (tid == 0 && vblk == 0) segd[(size_t)row * NSEG + p] = dsum;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 2: main pass over one segment, one 64-wide block of V
+// ---------------------------------------------------------------------------
+// LDS: one chunk stage (single-buffered; the next chunk waits in registers),
+// the A tile, and the top-level states (bf16, [level][k][v]).
+struct Stage {
+  __bf16 q[kBT * kLd];
+  __bf16 k[kBT * kLd];
+  __bf16 v[kBT * kLd];
+  float gc[kBT];            // chunk-local inclusive cumsum of g
+  float wt[kBT];            // exp(Gc_last - Gc_t)
+  float lam[kMaxLU * kBT];  // lambda^T [level][t]; levels >= 7 pre-multiplied by exp(Gc_t)
+};
+
+struct MainSmem {
+  Stage st;
+  __bf16 a[kBT * kLd];      // A[t][s] = (S o M)[t][s] of the current chunk, bf16
+  __bf16 top[1];            // [ntop][kKD][kLd] top-level states (dynamic size)
+};
+
+inline int main_smem_bytes(int ntop) {
+  return (int)offsetof(MainSmem, top) + ntop * kKD * kLd * 2;
 }
 
 template <typename TV, typename TL>
-__device__ __forceinline__ void store_chunk(const ChunkRegs<TV, TL>& r, unsigned char* stage,
-                                            const FwdSmem& sm, int lu, float* __restrict__ gcum,
-                                            size_t gcum_base, int H, bool write_gcum) {
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  __bf16* kS = (__bf16*)(stage + sm.off_k);
-  __bf16* kT = (__bf16*)(stage + sm.off_kt);
-  __bf16* vT = (__bf16*)(stage + sm.off_vt);
-  float* gc = (float*)(stage + sm.off_gc);
-  float* lam = (float*)(stage + sm.off_lam);
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int u = tid + 256 * rr;
-    const int row = u >> 3, c0 = 8 * (u & 7);
-    *(uint4*)(kS + row * kRow + c0) = r.k[rr];
-    const __bf16* e = (const __bf16*)&r.k[rr];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) kT[(c0 + j) * kRow + row] = e[j];
-  }
-  if constexpr (sizeof(TV) == 2) {
-    if (tid < 128) {
-      const int row = tid >> 1, c0 = 8 * (tid & 1);
-      const TV* e = (const TV*)&r.v;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vT[(c0 + j) * kRow + row] = from_f32<__bf16>(to_f32<TV>(e[j]));
-    }
-  } else {
-    const int row = tid >> 2, c0 = 4 * (tid & 3);
-    const TV* e = (const TV*)&r.v;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vT[(c0 + j) * kRow + row] = from_f32<__bf16>(to_f32<TV>(e[j]));
-  }
-  if (w == 0) {
-    // inclusive chunk-local cumsum of g (fla chunk_local_cumsum, chunkwise.py:1175)
-    float x = r.g;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      float y = __shfl_up(x, d, 64);
-      if (lane >= d) x += y;
-    }
-    gc[lane] = x;
-    if (write_gcum) gcum[gcum_base + (size_t)lane * H] = x;
-  }
-#pragma unroll
-  for (int rr = 0; rr < kLamPerLane; ++rr) {
-    const int e = lane + 64 * rr;
-    if (e < 16 * lu) {
-      const int row = 16 * w + e / lu, col = e % lu;
-      lam[row * sm.lam_stride + col] = to_f32<TL>(r.lam[rr]);
-    }
-  }
+struct MainRegs {
+  uint4 q[2], k[2];
+  VTile<TV> v;
+  float g;
+  TL lam[kMaxLU / 4 + 1];
+};
+
+// Phase-1 tile schedule: the 10 causal 16x16 tiles (t-tile mt, s-tile j <= mt)
+// and the two zero tiles the 32-wide s steps of A V read above the diagonal
+// ((0,1), (2,3)), three per wave: code = mt * 4 + j, +16 marks a zero tile.
+__device__ __forceinline__ int p1_tile(int w, int n) {
+  constexpr int tab[4][3] = {{0, 10, 14}, {5, 12, 16 + 1}, {4, 8, 15}, {9, 13, 16 + 11}};
+  return tab[w][n];
 }
 
 template <typename TV, typename TL, typename TO>
-__global__ __launch_bounds__(256, 1) void mamba2_fwd_kernel(
+__global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
-    float* __restrict__ gcum, float* __restrict__ ht, int B, int T, int G, int H, int V, int L,
-    int nlev, int nvb, int final_state) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
+    const float* __restrict__ segd, int B, int T, int G, int H, int V, int L, int nlev,
+    int nvb64, int slog, int NSEG, int final_state) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  MainSmem& sm = *(MainSmem*)smem_raw;
+  Stage& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const XcdMap m = xcd_map(blockIdx.x, nvb);
-  const int BH = B * H;
-  if (m.row >= BH) return;
-  const int b = m.row / H, h = m.row % H, vb = m.slice;
+  const XcdMap xm = xcd_map(blockIdx.x, nvb64);
+  if (xm.row >= B * H * NSEG) return;
+  // heads fastest: the workgroups reading the same rows of q / k / v run together
+  const int h = xm.row % H, p = (xm.row / H) % NSEG, b = xm.row / (H * NSEG);
+  const int row = b * H + h, vblk = xm.slice;
   const int gq = h / (H / G);
   const int NT = T / kBT;
+  const int c0 = p << slog;
+  const int cend = min(c0 + (1 << slog), NT);
   const int lu = 7 + nlev;
-  const FwdSmem sm = fwd_smem_layout(nlev);
-  __bf16* hT = (__bf16*)(smem + sm.off_h);
-  const int hbuf_elems = nlev * kBV * kRow;
+  const int nloc = min(slog, nlev);
+  const int ntop = nlev - nloc;
+  const int vcol0 = vblk * 64;
+  const int vc = vcol0 + 16 * w + ln;   // this lane's V column in phases 2 and 3
+  const bool is_final_seg = final_state && ht != nullptr && p == NSEG - 1;
+  float* htb = ht ? ht + ((size_t)b * H + h) * kKD * V * L : nullptr;
 
-  floatx4 st[kMaxLev];
+  // ---- top levels: Htop_e(p) from the segment summaries -> LDS (bf16) ----------
+  if (ntop > 0) {
+    const float* sp = sums + (size_t)row * NSEG * kKD * V + vc;
+    const float* dp = segd + (size_t)row * NSEG;
+    const size_t qstride = (size_t)kKD * V;
+    for (int e2 = 0; e2 < ntop; ++e2) {
+      const bool reads = (p >> e2) & 1;
+      if (!reads && !is_final_seg) continue;
+      // reads: block [lo, lo + 2^e2) decayed to the start of p;
+      // final state of a level the last chunk writes: segments [lo, p] decayed to the end
+      const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
+      const int hi = reads ? lo + (1 << e2) : p + 1;
+      float dlog = 0.f;
+      for (int r = hi; r < p; ++r) dlog += dp[r];
+      floatx4 hacc[4];
 #pragma unroll
-  for (int e = 0; e < kMaxLev; ++e) st[e] = zero4();
-
-  ChunkRegs<TV, TL> cur, nxt;
-  load_chunk(cur, q, k, v, g, l, b, h, gq, vb, 0, T, G, H, V, L, lu);
-  const bool write_gcum = (gcum != nullptr) && vb == 0;
-  store_chunk(cur, smem, sm, lu, gcum, ((size_t)b * T) * H + h, H, write_gcum);
-  if (NT > 1) load_chunk(nxt, q, k, v, g, l, b, h, gq, vb, kBT, T, G, H, V, L, lu);
-  __syncthreads();
-
-  for (int ic = 0; ic < NT; ++ic) {
-    const unsigned char* stage = smem + (ic & 1) * sm.stage_bytes;
-    const __bf16* kS = (const __bf16*)(stage + sm.off_k);
-    const __bf16* kT = (const __bf16*)(stage + sm.off_kt);
-    const __bf16* vT = (const __bf16*)(stage + sm.off_vt);
-    const float* gc = (const float*)(stage + sm.off_gc);
-    const float* lam = (const float*)(stage + sm.off_lam);
-    const int LS = sm.lam_stride;
-
-    // ---- intra-chunk: S^T tiles (s-tile j, t-tile w), j <= w -----------------
-    const int t = 16 * w + ln;
-    const float gct = gc[t];
-    floatx4 sT[4];
+      for (int m = 0; m < 4; ++m) hacc[m] = zero4();
+      for (int qs = hi - 1; qs >= lo; --qs) {
+        const float sc = fexp(dlog);
+        const float* src = sp + qs * qstride;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sT[j] = zero4();
-      if (j <= w) {
+        for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const bf16x8 a = *(const bf16x8*)(kS + (16 * j + ln) * kRow + 32 * c + 8 * lq);
-          sT[j] = mfma16x16x32(a, cur.q[c], sT[j]);
-        }
-        const floatx4 gs = *(const floatx4*)(gc + 16 * j + 4 * lq);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int s = 16 * j + 4 * lq + i;
-          float val = 0.f;
-          if (s <= t) val = sT[j][i] * fexp(gct - gs[i]) * lam[t * LS + intra_level(t, s)];
-          sT[j][i] = val;
-        }
+          for (int i = 0; i < 4; ++i) hacc[m][i] += sc * src[(size_t)(16 * m + 4 * lq + i) * V];
+        dlog += dp[qs];
       }
-    }
-    // ---- A V: contraction over s, pairs of s-tiles (2p, 2p + 1) ----------------
-    floatx4 acc = zero4();
+      if (reads) {
+        __bf16* tp = sm.top + e2 * kKD * kLd + 16 * w + ln;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      if (2 * p <= w) {
-        bf16x8 a, bv;
+        for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          a[i] = (__bf16)sT[2 * p][i];
-          a[4 + i] = (__bf16)sT[2 * p + 1][i];
-        }
-        const bf16x4 v0 = *(const bf16x4*)(vT + ln * kRow + 32 * p + 4 * lq);
-        const bf16x4 v1 = *(const bf16x4*)(vT + ln * kRow + 32 * p + 16 + 4 * lq);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bv[i] = v0[i];
-          bv[4 + i] = v1[i];
-        }
-        acc = mfma16x16x32(a, bv, acc);
+          for (int i = 0; i < 4; ++i) tp[(16 * m + 4 * lq + i) * kLd] = (__bf16)hacc[m][i];
       }
-    }
-    // ---- inter-chunk levels read by this chunk (bits set in ic) ----------------
-    if (ic > 0) {
-      const __bf16* hR = hT + (ic & 1) * hbuf_elems;
-      float eg[4];
-      const floatx4 g4 = *(const floatx4*)(gc + 16 * w + 4 * lq);
+      if (is_final_seg) {
+        // final state (chunkwise.py:229-279): a level the last chunk reads holds
+        // its block decayed over segment p; one it writes holds [lo, p]
+        const float sc = reads ? fexp(dp[p]) : 1.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) eg[i] = fexp(g4[i]);
-#pragma unroll
-      for (int e = 0; e < kMaxLev; ++e) {
-        if (e < nlev && ((ic >> e) & 1)) {
-          floatx4 tmp = zero4();
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const bf16x8 bh = *(const bf16x8*)(hR + (e * kBV + ln) * kRow + 32 * c + 8 * lq);
-            tmp = mfma16x16x32(cur.q[c], bh, tmp);
-          }
+        for (int m = 0; m < 4; ++m)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            acc[i] += tmp[i] * eg[i] * lam[(16 * w + 4 * lq + i) * LS + 7 + e];
-        }
+            htb[((size_t)(16 * m + 4 * lq + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i] * sc;
       }
     }
-    // ---- store o ---------------------------------------------------------------
-    {
-      const size_t base = (((size_t)b * T + ic * kBT + 16 * w + 4 * lq) * H + h) * V + vb * kBV + ln;
+  }
+
+  // ---- per-row buffer descriptors and per-lane offsets ---------------------------
+  // Chunk j of the segment starts (c0 + j) * 64 rows into the row's span; that
+  // offset is uniform (SGPR), the lane's part of each access pattern is fixed.
+  const int qstr = G * kKD, vstr = H * V, lstr = H * L;
+  const rsrc_t rq = make_rsrc(q + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
+  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
+  const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
+  const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
+  const rsrc_t rl = make_rsrc(l + ((size_t)b * T * H + h) * L, (size_t)T * lstr * sizeof(TL));
+  const rsrc_t ro = make_rsrc(o + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TO));
+  const bool write_gcum = gcum != nullptr && vblk == 0;
+  const rsrc_t rgc = make_rsrc(write_gcum ? (const void*)(gcum + (size_t)b * T * H + h) : (const void*)g,
+                               write_gcum ? (size_t)T * H * 4 : 0);
+  // 16-byte units of a 64 x 64 tile: u = tid (+256): row u >> 3, col 8 (u & 7)
+  const unsigned int vo_qk = ((tid >> 3) * qstr + 8 * (tid & 7)) * 2;
+  const unsigned int so_qk2 = 32 * qstr * 2;                     // second unit: +32 rows
+  unsigned int vo_v, so_v2;
+  if constexpr (sizeof(TV) == 2) {
+    vo_v = ((tid >> 3) * vstr + 8 * (tid & 7)) * 2;
+    so_v2 = 32 * vstr * 2;
+  } else {
+    vo_v = ((tid >> 4) * vstr + 4 * (tid & 15)) * 4;                // 4 units, +16 rows each
+    so_v2 = 16 * vstr * 4;
+  }
+  const unsigned int vo_g = lane * H * 4;
+  // lambda tile: thread -> row tid >> 2, columns (tid & 3) + 4r
+  const int lrow = tid >> 2, lcol = tid & 3;
+  const unsigned int vo_l = (lrow * lstr + lcol) * sizeof(TL);
+  const unsigned int vo_o = (4 * lq * vstr + 16 * w + ln) * sizeof(TO);
+  constexpr int kLR = kMaxLU / 4 + 1;
+
+  MainRegs<TV, TL> rg;
+  auto load = [&](int j) {  // j: chunk index within the segment
+    const unsigned int row0 = (unsigned int)(c0 + j) * kBT;
+    const unsigned int so_qk = row0 * qstr * 2;
+    rg.q[0] = buf_load16(rq, vo_qk, so_qk);
+    rg.q[1] = buf_load16(rq, vo_qk, so_qk + so_qk2);
+    rg.k[0] = buf_load16(rk, vo_qk, so_qk);
+    rg.k[1] = buf_load16(rk, vo_qk, so_qk + so_qk2);
+    const unsigned int so_v = row0 * vstr * sizeof(TV);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[base + (size_t)i * H * V] = from_f32<TO>(acc[i]);
+    for (int rr = 0; rr < VTile<TV>::N; ++rr) rg.v.r[rr] = buf_load16(rv, vo_v, so_v + rr * so_v2);
+    rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+    const unsigned int so_l = row0 * lstr * sizeof(TL);
+#pragma unroll
+    for (int r = 0; r < kLR; ++r)
+      if (lcol + 4 * r < lu) rg.lam[r] = buf_load<TL>(rl, vo_l, so_l + 4 * r * sizeof(TL));
+  };
+  auto store = [&](int j) {
+    store_tile_bf16(rg.q, s.q);
+    store_tile_bf16(rg.k, s.k);
+    store_vtile(rg.v, s.v);
+    const float x = chunk_cumsum(rg.g);   // every wave scans the chunk's g
+    const float last = __shfl(x, 63, 64);
+    if (w == 0) {
+      s.gc[lane] = x;
+      s.wt[lane] = fexp(last - x);
+      if (write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
     }
-    // ---- state update: wave w owns state rows k = 16w .. 16w + 15 --------------
-    {
-      const float glr = gc[kBT - 1];
-      floatx4 kv = zero4();
+    const float eg = fexp(__shfl(x, lrow, 64));
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const bf16x8 a = *(const bf16x8*)(kT + (16 * w + ln) * kRow + 32 * c + 8 * lq);
-        const bf16x8 vv = *(const bf16x8*)(vT + ln * kRow + 32 * c + 8 * lq);
-        const floatx4 gA = *(const floatx4*)(gc + 32 * c + 8 * lq);
-        const floatx4 gB = *(const floatx4*)(gc + 32 * c + 8 * lq + 4);
-        bf16x8 bv;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bv[j] = (__bf16)((float)vv[j] * fexp(glr - gA[j]));
-          bv[4 + j] = (__bf16)((float)vv[4 + j] * fexp(glr - gB[j]));
-        }
-        kv = mfma16x16x32(a, bv, kv);
+    for (int r = 0; r < kLR; ++r) {
+      const int col = lcol + 4 * r;
+      if (col < lu) {
+        float val = to_f32<TL>(rg.lam[r]);
+        if (col >= 7) val *= eg;
+        s.lam[col * kBT + lrow] = val;
       }
-      const float gl = fexp(glr);
-      __bf16* hW = hT + ((ic + 1) & 1) * hbuf_elems;
-      const bool last = (ic == NT - 1);
+    }
+  };
+
+  floatx4 st[kMaxLoc][4];
 #pragma unroll
-      for (int e = 0; e < kMaxLev; ++e) {
-        if (e < nlev) {
-          const int per = 2 << e;
-          const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
-          const bool write_kv = !((ic >> e) & 1);
+  for (int e = 0; e < kMaxLoc; ++e)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) st[e][m] = zero4();
+
+  const int nch = cend - c0;
+  load(0);
+  float Eseg = 0.f;  // log-decay from the segment start to the current chunk start
+  for (int j = 0; j < nch; ++j) {
+    const int ic = c0 + j;
+    store(j);
+    if (j + 1 < nch) load(j + 1);
+    __syncthreads();
+
+    // ---- phase 1: three tiles of A[t][s] per wave ------------------------------
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      const int code = p1_tile(w, n);
+      const int mt = (code & 15) >> 2, jt = code & 3;
+      const int t = 16 * mt + ln;
+      bf16x4 out = bf16x4{};
+      if (code < 16) {
+        floatx4 acc = zero4();
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const bf16x8 a = *(const bf16x8*)(s.k + (16 * jt + ln) * kLd + 32 * c + 8 * lq);
+          const bf16x8 bq = *(const bf16x8*)(s.q + t * kLd + 32 * c + 8 * lq);
+          acc = mfma16x16x32(a, bq, acc);  // S^T[s = 16jt + 4lq + i][t]
+        }
+        const float gct = s.gc[t];
+        const floatx4 gs = *(const floatx4*)(s.gc + 16 * jt + 4 * lq);
+        if (jt < mt) {
+          // off-diagonal tile: level 4 + bit_length(mt ^ jt) for every pair
+          const float lam = s.lam[(4 + intra_level(mt, jt)) * kBT + t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[i] = (__bf16)(acc[i] * fexp(gct - gs[i]) * lam);
+        } else {
+          // diagonal tile: level bit_length(ln ^ (4lq + i)), causal s <= t
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float x = reset ? 0.f : st[e][i] * gl;
-            if (write_kv) x += kv[i];
-            st[e][i] = x;
-          }
-          if (!last && (((ic + 1) >> e) & 1)) {
-            bf16x4 hb;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) hb[i] = (__bf16)st[e][i];
-            *(bf16x4*)(hW + (e * kBV + ln) * kRow + 16 * w + 4 * lq) = hb;
+            const int sl = 4 * lq + i;
+            const float val = acc[i] * fexp(gct - gs[i]) * s.lam[intra_level(ln, sl) * kBT + t];
+            out[i] = (__bf16)(sl <= ln ? val : 0.f);
           }
         }
       }
-      if (last && ht != nullptr) {
-        // ht[b, h, k, v, 7 + e] (chunkwise.py:1179, 277-279)
+      *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+    }
+    __syncthreads();
+
+    // ---- phase 2: o[all t][V columns 16w..] ------------------------------------
+    floatx4 acc[4];
+    {
+      const bf16x8 vf0 = tr_frag(s.v, kLd, 0, 16 * w);    // V[s][v], s = 0..31
+      const bf16x8 vf1 = tr_frag(s.v, kLd, 32, 16 * w);   // s = 32..63
 #pragma unroll
-        for (int e = 0; e < kMaxLev; ++e) {
-          if (e < nlev) {
+      for (int mt = 0; mt < 4; ++mt) {
+        const __bf16* ar = sm.a + (16 * mt + ln) * kLd + 8 * lq;
+        acc[mt] = mfma16x16x32(*(const bf16x8*)ar, vf0, zero4());
+        if (mt >= 2) acc[mt] = mfma16x16x32(*(const bf16x8*)(ar + 32), vf1, acc[mt]);
+      }
+    }
+    const bool any_loc = nloc > 0 && j > 0;
+    const bool any_top = ntop > 0 && p > 0;
+    if (any_loc || any_top) {
+      const float ee = fexp(Eseg);
+      // Q fragments in the states' row order: k = 32c + 4lq + i, 32c + 16 + 4lq + i
+      bf16x8 qa[4][2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int kk = 16 * w + 4 * lq + i, vv = vb * kBV + ln;
-              ht[((((size_t)b * H + h) * kKD + kk) * V + vv) * L + 7 + e] = st[e][i];
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const __bf16* qp = s.q + (16 * mt + ln) * kLd + 32 * c + 4 * lq;
+          const bf16x4 lo = *(const bf16x4*)qp;
+          const bf16x4 hi = *(const bf16x4*)(qp + 16);
+          qa[mt][c] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      const float* lamt = s.lam + 4 * lq;
+      // local levels without branches (a level the chunk does not read gets a
+      // zero B operand), so the MFMA chains of all levels interleave
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        const bool rd = any_loc && e < nloc && ((ic >> e) & 1);
+        const float z = rd ? 1.f : 0.f;
+        const bf16x8 b0 = cat8(st[e][0] * z, st[e][1] * z), b1 = cat8(st[e][2] * z, st[e][3] * z);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          floatx4 tmp = mfma16x16x32(qa[mt][0], b0, zero4());
+          tmp = mfma16x16x32(qa[mt][1], b1, tmp);
+          const floatx4 lam = *(const floatx4*)(lamt + (7 + e) * kBT + 16 * mt);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * lam[i];
+        }
+      }
+      if (any_top) {
+        for (int e2 = 0; e2 < ntop; ++e2) {
+          if ((p >> e2) & 1) {
+            const __bf16* tp = sm.top + e2 * kKD * kLd;
+            const bf16x8 b0 = tr_frag_d(tp, kLd, 0, 16 * w), b1 = tr_frag_d(tp, kLd, 32, 16 * w);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+              floatx4 tmp = mfma16x16x32(qa[mt][0], b0, zero4());
+              tmp = mfma16x16x32(qa[mt][1], b1, tmp);
+              const floatx4 lam = *(const floatx4*)(lamt + (7 + nloc + e2) * kBT + 16 * mt);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * (lam[i] * ee);
             }
           }
         }
       }
     }
-    // ---- stage the next chunk --------------------------------------------------
-    if (ic + 1 < NT) {
-      cur = nxt;
-      store_chunk(cur, smem + ((ic + 1) & 1) * sm.stage_bytes, sm, lu, gcum,
-                  ((size_t)b * T + (ic + 1) * kBT) * H + h, H, write_gcum);
-      if (ic + 2 < NT)
-        load_chunk(nxt, q, k, v, g, l, b, h, gq, vb, (ic + 2) * kBT, T, G, H, V, L, lu);
-    }
-    __syncthreads();
-  }
-}
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        buf_store<TO>(from_f32<TO>(acc[mt][i]), ro, vo_o,
+                      ((unsigned int)ic * kBT + 16 * mt + i) * vstr * sizeof(TO));
 
-// ---------------------------------------------------------------------------
-// host launcher
-// ---------------------------------------------------------------------------
-template <typename TV, typename TL, typename TO>
-static hipError_t launch_t(const void* q, const void* k, const void* v, const float* g,
-                           const void* l, void* o, float* gcum, float* ht, int B, int T, int G,
-                           int H, int V, int L, int nlev, hipStream_t stream) {
-  const FwdSmem sm = fwd_smem_layout(nlev);
-  const int nvb = V / kBV;
-  const int rows8 = (B * H + 7) / 8;
-  const int grid = rows8 * 8 * nvb;
-  auto kern = mamba2_fwd_kernel<TV, TL, TO>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, sm.total);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), sm.total, stream, (const __bf16*)q,
-                     (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, B, T, G,
-                     H, V, L, nlev, nvb, ht != nullptr ? 1 : 0);
-  return hipGetLastError();
+    // ---- phase 3: local state update for V columns 16w.. -----------------------
+    const float glr = s.gc[kBT - 1];
+    if (nloc > 0) {
+      const floatx4 w0a = *(const floatx4*)(s.wt + 8 * lq);
+      const floatx4 w0b = *(const floatx4*)(s.wt + 8 * lq + 4);
+      const floatx4 w1a = *(const floatx4*)(s.wt + 32 + 8 * lq);
+      const floatx4 w1b = *(const floatx4*)(s.wt + 32 + 8 * lq + 4);
+      const bf16x8 vf0 = tr_frag(s.v, kLd, 0, 16 * w), vf1 = tr_frag(s.v, kLd, 32, 16 * w);
+      bf16x8 wv0, wv1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wv0[i] = (__bf16)((float)vf0[i] * w0a[i]);
+        wv0[4 + i] = (__bf16)((float)vf0[4 + i] * w0b[i]);
+        wv1[i] = (__bf16)((float)vf1[i] * w1a[i]);
+        wv1[4 + i] = (__bf16)((float)vf1[4 + i] * w1b[i]);
+      }
+      floatx4 kv[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        kv[m] = mfma16x16x32(tr_frag(s.k, kLd, 0, 16 * m), wv0, zero4());
+        kv[m] = mfma16x16x32(tr_frag(s.k, kLd, 32, 16 * m), wv1, kv[m]);
+      }
+      const float gl = fexp(glr);
+      const bool last = (ic == NT - 1);
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        if (e < nloc) {
+          const int per = 2 << e;
+          const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
+          const bool write_kv = !((ic >> e) & 1);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            if (reset) {
+              st[e][m] = write_kv ? kv[m] : zero4();
+            } else if (write_kv) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) st[e][m][i] = st[e][m][i] * gl + kv[m][i];
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) st[e][m][i] *= gl;
+            }
+          }
+        }
+      }
+      if (last && is_final_seg) {
+        // ht[b, h, k, v, 7 + e] (chunkwise.py:1179, 277-279)
+#pragma unroll
+        for (int e = 0; e < kMaxLoc; ++e)
+          if (e < nloc)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                htb[((size_t)(16 * m + 4 * lq + i) * V + vc) * L + 7 + e] = st[e][m][i];
+      }
+    }
+    Eseg += glr;
+    __syncthreads();   // every wave is done with the stage before it is refilled
+  }
 }
 
 }  // namespace hattn
@@ -368,17 +624,75 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
 // dtype codes shared with the C-ABI (include/hattn.h)
 enum { DT_BF16 = 0, DT_FP16 = 1, DT_FP32 = 2 };
 
+namespace {
+size_t segd_bytes(size_t rows, int NSEG) {
+  return (rows * NSEG * sizeof(float) + 255) & ~(size_t)255;
+}
+}  // namespace
+
+size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V) {
+  const int NT = T / hattn::kBT;
+  const int slog = hattn::seg_log2(NT);
+  const int NSEG = (NT + (1 << slog) - 1) >> slog;
+  if (NSEG <= 1) return 0;
+  const size_t rows = (size_t)B * H;
+  return segd_bytes(rows, NSEG) + rows * NSEG * hattn::kKD * V * sizeof(float);
+}
+
+// Largest inter-chunk level count the register-resident states support.
+int hattn_mamba2_fwd_max_levels() { return hattn::kMaxLoc + hattn::kMaxTop; }
+
+namespace hattn {
+
+template <typename TV, typename TL, typename TO>
+static hipError_t launch_t(const void* q, const void* k, const void* v, const float* g,
+                           const void* l, void* o, float* gcum, float* ht, void* ws, int B,
+                           int T, int G, int H, int V, int L, int nlev, hipStream_t stream) {
+  const int NT = T / kBT;
+  const int slog = seg_log2(NT);
+  const int S = 1 << slog;
+  const int NSEG = (NT + S - 1) / S;
+  const int rows = B * H;
+  const int nvb64 = V / 64;
+  float* segd = nullptr;
+  float* sums = nullptr;
+  if (NSEG > 1) {
+    segd = (float*)ws;
+    sums = (float*)((char*)ws + segd_bytes(rows, NSEG));
+    hipLaunchKernelGGL(mamba2_seg_sum_kernel<TV>, dim3(rows * NSEG * nvb64), dim3(256), 0,
+                       stream, (const __bf16*)k, (const TV*)v, g, sums, segd, T, G, H, V, NT, S,
+                       NSEG, nvb64);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int smem = main_smem_bytes(nlev - min(slog, nlev));
+  const int rows8 = (rows * NSEG + 7) / 8;
+  const int grid = rows8 * 8 * nvb64;
+  auto kern = mamba2_fwd_main_kernel<TV, TL, TO>;
+  hipError_t e =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const __bf16*)q,
+                     (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, sums,
+                     segd, B, T, G, H, V, L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
+  return hipGetLastError();
+}
+
+}  // namespace hattn
+
 hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, const float* g,
-                                   const void* l, void* o, float* gcum, float* ht, int B, int T,
-                                   int G, int H, int V, int L, int nlev, int dt_v, int dt_l,
-                                   int dt_o, hipStream_t stream, int* unsupported) {
+                                   const void* l, void* o, float* gcum, float* ht, void* ws,
+                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_v,
+                                   int dt_l, int dt_o, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
 #define HATTN_DISPATCH_O(TV_, TL_)                                                             \
   if (dt_o == DT_BF16)                                                                       \
-    return launch_t<TV_, TL_, __bf16>(q, k, v, g, l, o, gcum, ht, B, T, G, H, V, L, nlev, stream); \
+    return launch_t<TV_, TL_, __bf16>(q, k, v, g, l, o, gcum, ht, ws, B, T, G, H, V, L, nlev, \
+                                      stream);                                                \
   if (dt_o == DT_FP32)                                                                       \
-    return launch_t<TV_, TL_, float>(q, k, v, g, l, o, gcum, ht, B, T, G, H, V, L, nlev, stream);
+    return launch_t<TV_, TL_, float>(q, k, v, g, l, o, gcum, ht, ws, B, T, G, H, V, L, nlev,  \
+                                     stream);
   if (dt_v == DT_BF16 && dt_l == DT_BF16) { HATTN_DISPATCH_O(__bf16, __bf16) }
   if (dt_v == DT_BF16 && dt_l == DT_FP32) { HATTN_DISPATCH_O(__bf16, float) }
   if (dt_v == DT_FP32 && dt_l == DT_BF16) { HATTN_DISPATCH_O(float, __bf16) }

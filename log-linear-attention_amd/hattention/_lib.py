@@ -17,12 +17,13 @@ HATTN_OK, HATTN_ERR_VALUE, HATTN_ERR_NOT_IMPLEMENTED, HATTN_ERR_HIP = 0, 1, 2, 3
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 # (name, restype, argtypes) of every exported entry point, in header order.
-_P, _I, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p
+_P, _I, _F, _S = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
 SIGNATURES = [
     ("hattn_version", ctypes.c_char_p, []),
     ("hattn_last_error", ctypes.c_char_p, []),
     ("hattn_mamba2_chunkwise_fwd", _I,
-     [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P]),
+     [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P, _S, _P]),
+    ("hattn_mamba2_chunkwise_fwd_workspace", _S, [_I] * 7),
 ]
 
 _lock = threading.Lock()
@@ -91,3 +92,12 @@ def ptr(t) -> int:
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device):
+    """Device scratch of ``nbytes`` bytes from torch's caching allocator (None
+    when no scratch is needed); returns (tensor, pointer, size)."""
+    if nbytes <= 0:
+        return None, 0, 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return ws, ws.data_ptr(), nbytes

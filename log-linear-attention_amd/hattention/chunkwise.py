@@ -96,11 +96,13 @@ def chunkwise_fwd(
     g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
     ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
     lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, K, V, L), dev)
     st = lib.hattn_mamba2_chunkwise_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o),
         _lib.ptr(g_cumsum), _lib.ptr(ht), B, T, G, H, K, V, L,
         _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
-        level_base, htype.value, chunk_size, _lib.stream_handle(dev))
+        level_base, htype.value, chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
     _lib.check(st)
     return o, g_cumsum, ht
 

@@ -45,6 +45,20 @@ def test_binding_table_covers_header():
     assert set(declared_symbols()) <= bound
 
 
+def test_workspace_query():
+    lib = _lib.load()
+    # one segment (T <= 31 chunks): no scratch; otherwise rows * segments * K * V fp32 + decays
+    assert lib.hattn_mamba2_chunkwise_fwd_workspace(1, 64 * 16, 1, 1, 64, 64, 11) == 0
+    n = lib.hattn_mamba2_chunkwise_fwd_workspace(4, 16384, 16, 16, 64, 64, 15)
+    assert n >= 4 * 16 * 16 * 64 * 64 * 4
+    assert lib.hattn_mamba2_chunkwise_fwd_workspace(1, 100, 1, 1, 64, 64, 8) == 0
+
+
+def test_workspace_too_small_is_value_error():
+    assert _fwd(T=64 * 64, L=13) == _lib.HATTN_ERR_VALUE
+    assert b"workspace" in _lib.load().hattn_last_error()
+
+
 def test_version_string():
     v = _lib.load().hattn_version().decode()
     assert v.startswith("hattn-mi355x") and "gfx950" in v
@@ -59,7 +73,7 @@ def _fwd(**kw):
     return lib.hattn_mamba2_chunkwise_fwd(p, p, p, p, p, p, None, None, a["B"], a["T"], a["G"],
                                           a["H"], a["K"], a["V"], a["L"], a["dq"], a["dv"],
                                           a["dl"], a["do"], a["base"], a["htype"], a["chunk"],
-                                          None)
+                                          None, 0, None)
 
 
 @pytest.mark.parametrize("kw,code", [

@@ -11,6 +11,8 @@ throughput (tokens/s), the roofline of the kernel (HBM-bound: algorithmic
 bytes / average launch time measured with HIP events on the launch stream)
 and a host-CPU baseline (this repo's fp32 torch restatement of the
 reference's chunkwise algorithm, timed on a bounded sample on rank 0).
+A second figure, ``fwd_bwd``, times forward + backward through the autograd
+boundary (the HIP backward kernels) at the same shape.
 
 Only one GPU is used: ``--gpus`` above 1 exits with a message.
 """
@@ -73,6 +75,18 @@ def fwd_flops(B, T, H, K, V):
     return B * H * (2 * T * 64 * (K + V) + 2 * T * K * V + T * K * V * nlev)
 
 
+def bwd_bytes(B, T, H, K, V, L, es=2, es_l=2):
+    """Algorithmic HBM bytes of one backward: read q, k, v, g, lambda, dO,
+    write dq, dk, dv (input dtypes), dg and dlambda (fp32)."""
+    return B * T * H * (2 * K * es + V * es + 4 + L * es_l + V * es      # inputs + dO
+                        + 2 * K * es + V * es + 4 + L * 4)              # gradients
+
+
+def bwd_flops(B, T, H, K, V):
+    nlev = math.ceil(math.log2(T // 64)) if T > 64 else 0
+    return B * H * (2 * T * 64 * (3 * K + 2 * V) + 6 * T * K * V + 2 * T * K * V * nlev)
+
+
 def cpu_baseline(seconds_budget=30.0):
     """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
     chunkwise algorithm) on the host cores, on the north-star workload (median
@@ -108,6 +122,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fwd-only", action="store_true", help="skip the forward+backward timing")
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain 256 MiB copy kernel (elementwise mul by 1) so a "
                          "counter run can scale FETCH_SIZE / WRITE_SIZE by a known traffic")
@@ -165,6 +180,44 @@ def main():
     nbytes = fwd_bytes(B, T, H, K, V, L)
     flops = fwd_flops(B, T, H, K, V)
     achieved = nbytes / avg_launch_s
+
+    # forward + backward through the autograd boundary (HAttentionFunction):
+    # the HIP forward, then the HIP backward for dq, dk, dv, dg, dlambda
+    fb = None
+    if not args.fwd_only:
+        _, _, _, _, _, do = make_mamba2_inputs(B, T, H, K, V, L, seed=1000, device=dev,
+                                               with_do=True)
+        leaves = [x.detach().clone().requires_grad_(True) for x in (q, k, v, g, l)]
+
+        def fwd_bwd():
+            for x in leaves:
+                x.grad = None
+            o = hattention_kernel(leaves[0], leaves[1], leaves[2], None, leaves[3], leaves[4],
+                                  None, False, 2, HType.WEAK, HStruct.MAMBA2)
+            o.backward(do)
+
+        for _ in range(max(1, args.warmup)):
+            fwd_bwd()
+        torch.cuda.synchronize()
+        nfb = max(1, args.steps // 2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(nfb):
+            fwd_bwd()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall_fb = (time.perf_counter() - t0) / nfb
+        ev_fb = e0.elapsed_time(e1) / 1e3 / nfb
+        fb_bytes = nbytes + bwd_bytes(B, T, H, K, V, L)
+        fb = {"value": tokens / wall_fb, "unit": "tokens/s", "ms_per_step": wall_fb * 1e3,
+              "steps": nfb,
+              "roofline": {"bound": "hbm", "achieved": fb_bytes / ev_fb / 1e9,
+                           "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                           "frac": fb_bytes / ev_fb / HBM_PEAK, "algorithmic_bytes": fb_bytes,
+                           "avg_step_us": ev_fb * 1e6,
+                           "mfma_frac": (flops + bwd_flops(B, T, H, K, V)) / ev_fb
+                           / MFMA_BF16_PEAK}}
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
         "value": value,
@@ -182,6 +235,7 @@ def main():
                                "MAMBA2, WEAK, base 2, chunk 64)",
                    "batch": B, "seq_len": T, "heads": H, "dk": K, "dv": V, "levels": L,
                    "dtype_qkv_lambda": "bf16", "dtype_g": "fp32"},
+        "fwd_bwd": fb,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,

@@ -87,6 +87,42 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
  * chunkwise_fwd (chunkwise.py:1176-1179). */
 size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, int V, int L);
 
+/*
+ * Log-linear Mamba-2 chunkwise backward.
+ *
+ * Replaces hattention/chunkwise.py:1286-1597 `chunkwise_bwd(q, k, v, g, l, do,
+ * head_first, level_base, htype, chunk_size) -> (dq, dk, dv, dg, dl)`, called
+ * by HAttentionFunction.backward for HStruct.MAMBA2 (kernel.py:180-199).
+ * Inputs are per head (the reference expands grouped q / k before its
+ * kernels, chunkwise.py:1360-1362; the host layer does the same and sums the
+ * group's dq / dk afterwards):
+ *
+ *   q, k, dq, dk [B, T, H, K] bf16      v, dv [B, T, H, V] in dtype_v
+ *   g_cumsum     [B, T, H] fp32 chunk-local inclusive cumsum (the forward's output)
+ *   l            [B, T, H, L] in dtype_l   do [B, T, H, V] bf16
+ *   dg           [B, T, H] fp32: gradient w.r.t. the per-step g (what the
+ *                reference returns after its reverse chunk-local cumsum)
+ *   dl           [B, T, H, L] fp32 (every element written; levels no pair
+ *                uses are 0)
+ *   workspace    >= hattn_mamba2_chunkwise_bwd_workspace(...) bytes
+ *
+ * Constraints: as the forward (T % 64, L >= 7 + ceil(log2(T/64)), K and V
+ * multiples of 64 -> HATTN_ERR_VALUE); K == V == 64, q/k/do bf16, v and l in
+ * {BF16, FP32} -> HATTN_ERR_NOT_IMPLEMENTED.
+ */
+int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
+                               const void* l, const void* do_, void* dq, void* dk, void* dv,
+                               float* dg, float* dl, int B, int T, int H, int K, int V, int L,
+                               int dtype_qk, int dtype_v, int dtype_l, int dtype_do,
+                               int level_base, int htype, int chunk_size, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of hattn_mamba2_chunkwise_bwd (segment summaries of both
+ * scan directions and the q . dq row sums).  No counterpart in the reference,
+ * which allocates fp32 h / dh per level inside chunkwise_bwd
+ * (chunkwise.py:1371-1384). */
+size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
+
 #ifdef __cplusplus
 }
 #endif

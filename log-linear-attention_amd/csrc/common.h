@@ -146,3 +146,34 @@ template <> __device__ __forceinline__ void buf_store<__bf16>(__bf16 x, rsrc_t r
 }
 
 }  // namespace hattn
+
+namespace hattn {
+
+__device__ __forceinline__ void buf_store8(uint2 x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{x.x, x.y}, r, voff, soff, 0);
+}
+
+__device__ __forceinline__ void buf_store16(uint4 x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{x.x, x.y, x.z, x.w}, r, voff, soff, 0);
+}
+
+// Four fp32 values stored as T (bf16: one 8-byte store, fp32: one 16-byte store).
+template <typename T>
+__device__ __forceinline__ void buf_store4(floatx4 x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 b = cvt4(x);
+    buf_store8(__builtin_bit_cast(uint2, b), r, voff, soff);
+  } else {
+    buf_store16(__builtin_bit_cast(uint4, x), r, voff, soff);
+  }
+}
+
+// Sum over the four lanes ln, ln + 16, ln + 32, ln + 48 (the lq groups).
+__device__ __forceinline__ float sum_lq(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+}  // namespace hattn

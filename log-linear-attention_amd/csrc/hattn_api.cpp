@@ -18,6 +18,12 @@ hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, 
                                    int dt_l, int dt_o, hipStream_t stream, int* unsupported);
 size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V);
 int hattn_mamba2_fwd_max_levels();
+size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
+hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
+                                   const void* l, const void* dO, void* dq, void* dk, void* dv,
+                                   float* dg, float* dl, void* ws, int B, int T, int H, int V,
+                                   int L, int nlev, int dt_v, int dt_l, hipStream_t stream,
+                                   int* unsupported);
 
 namespace {
 
@@ -104,6 +110,56 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d o=%d", dtype_v, dtype_l,
                 dtype_o);
   return check_hip(e, "hattn_mamba2_chunkwise_fwd launch");
+}
+
+size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L) {
+  (void)K;
+  (void)L;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0) return 0;
+  return hattn_mamba2_bwd_ws_bytes(B, T, H, V, ceil_log2(T / 64));
+}
+
+int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
+                               const void* l, const void* do_, void* dq, void* dk, void* dv,
+                               float* dg, float* dl, int B, int T, int H, int K, int V, int L,
+                               int dtype_qk, int dtype_v, int dtype_l, int dtype_do,
+                               int level_base, int htype, int chunk_size, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (chunk_size != 64)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
+  if (level_base != 2)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
+  if (htype != HATTN_HTYPE_WEAK)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
+  if (K % 64 != 0 || V % 64 != 0)
+    return fail(HATTN_ERR_VALUE, "K=%d, V=%d and BK, BV could be 64", K, V);
+  if (K != 64 || V != 64)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (the MI355X backward supports 64)", K, V);
+  const int nlev = ceil_log2(T / 64);
+  if (7 + nlev > L)
+    return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (nlev > hattn_mamba2_fwd_max_levels())
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
+                hattn_mamba2_fwd_max_levels());
+  if (dtype_qk != HATTN_BF16 || dtype_do != HATTN_BF16)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 required)", dtype_qk,
+                dtype_do);
+  if (!q || !k || !v || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !dg || !dl)
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_mamba2_bwd_ws_bytes(B, T, H, V, nlev);
+  if (workspace_bytes < need || workspace == nullptr)
+    return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  int unsupported = 0;
+  hipError_t e = hattn_mamba2_bwd_launch(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl, workspace,
+                                         B, T, H, V, L, nlev, dtype_v, dtype_l,
+                                         (hipStream_t)stream, &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d", dtype_v, dtype_l);
+  return check_hip(e, "hattn_mamba2_chunkwise_bwd launch");
 }
 
 }  // extern "C"

@@ -1,0 +1,933 @@
+// Log-linear Mamba-2 chunkwise backward for gfx950, segment-parallel.
+//
+// Replaces chunkwise_bwd (chunkwise.py:1286-1597): the reference launches
+// chunk_bwd_kernel_dqkwg and chunk_bwd_kernel_dv for the intra-chunk part and,
+// per inter-chunk level, a forward state recompute (chunk_fwd_kernel_h), a
+// reverse state scan (chunk_bwd_kernel_dh) and the dqkwg / dv kernels again,
+// with dlambda scattered by atomics and fp32 h / dh round-tripping HBM.
+//
+// With o_t = sum_{s<=t} M[t,s] (q_t . k_s) v_s and M[t,s] = lambda[t, lev(t,s)]
+// exp(G_t - G_s):
+//   dq_t = sum_s M[t,s] (do_t . v_s) k_s           (past tokens: forward scan)
+//   dk_s = sum_t M[t,s] (do_t . v_s) q_t           (future tokens: reverse scan)
+//   dv_s = sum_t M[t,s] (q_t . k_s) do_t           (future tokens: reverse scan)
+//   dlambda[t, l] = sum_{s: lev(t,s) = l} exp(G_t - G_s) (q_t . k_s)(do_t . v_s)
+//   dG_t = q_t . dq_t - k_t . dk_t,  dg_u = sum_{t >= u} dG_t
+// (the last identity is what the reference's reverse chunk-local cumsum of its
+// dg accumulator computes, chunkwise.py:1596).
+//
+// Segments of S = 16 chunks as in the forward.  Inter-chunk level e is a
+// source for chunk j when bit e of j is clear and is read when it is set.
+//   * mamba2_seg_sum_kernel<GCUM>: forward summaries Sum(q), D_q (shared with
+//     the forward).
+//   * mamba2_bwd_rsum_kernel: reverse summaries of the top levels,
+//     R_e(q) = sum_{t in q} lambda[t, 7 + e] exp(G_t - G_start(q)) q_t do_t^T.
+//   * mamba2_bwd_dq_kernel: walks a segment forwards; forward level states
+//     h_e (local in registers, top built from Sum) give dq and the inter-chunk
+//     dlambda; the intra-chunk tile gives dq and dlambda[.., 0..6].
+//   * mamba2_bwd_dkv_kernel: walks a segment backwards with the reverse level
+//     states DH_e (local, registers) plus one combined top-level state built
+//     from R_e; waves 0-3 produce dk, waves 4-7 dv (each role keeps the states
+//     in the MFMA layout its contraction needs).  It also forms dG and its
+//     within-segment reverse cumsum.
+//   * mamba2_bwd_dg_kernel: adds the later segments' totals to dg.
+#include "mamba2_common.h"
+
+namespace hattn {
+
+// ---------------------------------------------------------------------------
+// staging
+// ---------------------------------------------------------------------------
+struct BwdStage {
+  __bf16 q[kBT * kLd];
+  __bf16 k[kBT * kLd];
+  __bf16 v[kBT * kLd];
+  __bf16 d[kBT * kLd];      // dO
+  float gc[kBT];            // chunk-local cumsum Gc (the input g)
+  float wt[kBT];            // exp(Gc_last - Gc_t)
+  float eg[kBT];            // exp(Gc_t)
+  float lam[kMaxLU * kBT];  // lambda^T [level][t]; levels >= 7 pre-multiplied by exp(Gc_t)
+};
+
+// Registers of one chunk in flight (NTHR threads share a 64 x 64 tile).
+template <int NTHR, typename TV, typename TL>
+struct BwdRegs {
+  static constexpr int NU = 512 / NTHR;  // 16-byte units of a bf16 tile per thread
+  static constexpr int NV = sizeof(TV) == 2 ? NU : 2 * NU;
+  static constexpr int NL = (kMaxLU + NTHR / 64 - 1) / (NTHR / 64);
+  uint4 q[NU], k[NU], d[NU], v[NV];
+  float g;
+  TL lam[NL];
+};
+
+// Per-row descriptors and per-lane offsets of the chunk loads.
+template <int NTHR, typename TV, typename TL>
+struct BwdLoader {
+  rsrc_t rq, rk, rv, rd, rg, rl;
+  unsigned int vo_qk, vo_v, vo_d, vo_g, vo_l;
+  unsigned int qrow, vrow, drow, lrowb;  // bytes per token row
+  int lrow, lcol, lu;
+
+  __device__ void init(const __bf16* q, const __bf16* k, const TV* v, const __bf16* dO,
+                       const float* g, const TL* l, int b, int h, int T, int H, int V, int L,
+                       int lu_) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const size_t rq0 = ((size_t)b * T * H + h);
+    qrow = H * kKD * 2;
+    vrow = H * V * sizeof(TV);
+    drow = H * V * 2;
+    lrowb = H * L * sizeof(TL);
+    rq = make_rsrc(q + rq0 * kKD, (size_t)T * qrow);
+    rk = make_rsrc(k + rq0 * kKD, (size_t)T * qrow);
+    rv = make_rsrc(v + rq0 * V, (size_t)T * vrow);
+    rd = make_rsrc(dO + rq0 * V, (size_t)T * drow);
+    rg = make_rsrc(g + rq0, (size_t)T * H * 4);
+    rl = make_rsrc(l + rq0 * L, (size_t)T * lrowb);
+    vo_qk = (tid >> 3) * qrow + 16 * (tid & 7);
+    vo_d = (tid >> 3) * drow + 16 * (tid & 7);
+    if constexpr (sizeof(TV) == 2) vo_v = (tid >> 3) * vrow + 16 * (tid & 7);
+    else vo_v = (tid >> 4) * vrow + 16 * (tid & 15);
+    vo_g = lane * H * 4;
+    constexpr int TPR = NTHR / 64;          // threads per lambda row
+    lrow = tid / TPR;
+    lcol = tid % TPR;
+    vo_l = lrow * lrowb + lcol * sizeof(TL);
+    lu = lu_;
+  }
+
+  __device__ void load(BwdRegs<NTHR, TV, TL>& r, int chunk) const {
+    using R = BwdRegs<NTHR, TV, TL>;
+    const unsigned int t0 = (unsigned int)chunk * kBT;
+#pragma unroll
+    for (int u = 0; u < R::NU; ++u) {
+      const unsigned int row = t0 + u * (NTHR / 8);
+      r.q[u] = buf_load16(rq, vo_qk, row * qrow);
+      r.k[u] = buf_load16(rk, vo_qk, row * qrow);
+      r.d[u] = buf_load16(rd, vo_d, row * drow);
+    }
+#pragma unroll
+    for (int u = 0; u < R::NV; ++u) {
+      const unsigned int row = t0 + u * (sizeof(TV) == 2 ? NTHR / 8 : NTHR / 16);
+      r.v[u] = buf_load16(rv, vo_v, row * vrow);
+    }
+    r.g = buf_load<float>(rg, vo_g, t0 * (qrow / (kKD * 2)) * 4);
+#pragma unroll
+    for (int c = 0; c < R::NL; ++c)
+      if (lcol + c * (NTHR / 64) < lu)
+        r.lam[c] = buf_load<TL>(rl, vo_l, t0 * lrowb + c * (NTHR / 64) * sizeof(TL));
+  }
+
+  __device__ void store(const BwdRegs<NTHR, TV, TL>& r, BwdStage& s) const {
+    using R = BwdRegs<NTHR, TV, TL>;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int u = 0; u < R::NU; ++u) {
+      const int off = ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7);
+      *(uint4*)(s.q + off) = r.q[u];
+      *(uint4*)(s.k + off) = r.k[u];
+      *(uint4*)(s.d + off) = r.d[u];
+    }
+#pragma unroll
+    for (int u = 0; u < R::NV; ++u) {
+      if constexpr (sizeof(TV) == 2) {
+        *(uint4*)(s.v + ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)) = r.v[u];
+      } else {
+        const float* e = (const float*)&r.v[u];
+        *(bf16x4*)(s.v + ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15)) =
+            bf16x4{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3]};
+      }
+    }
+    const float x = r.g;                       // already the chunk-local cumsum
+    const float last = __shfl(x, 63, 64);
+    if (w == 0) {
+      s.gc[lane] = x;
+      s.wt[lane] = fexp(last - x);
+      s.eg[lane] = fexp(x);
+    }
+    const float eg = fexp(__shfl(x, lrow, 64));
+#pragma unroll
+    for (int c = 0; c < R::NL; ++c) {
+      const int col = lcol + c * (NTHR / 64);
+      if (col < lu) {
+        float val = to_f32<TL>(r.lam[c]);
+        if (col >= 7) val *= eg;
+        s.lam[col * kBT + lrow] = val;
+      }
+    }
+  }
+};
+
+// Phase-1 tiles (t-tile mt, s-tile jt) of the 64 x 64 intra-chunk matrices:
+// the 10 causal tiles plus the zero tiles (0,1) and (2,3) that the 32-wide
+// contraction steps read.  code = mt * 4 + jt, +16 marks a zero tile, -1 none.
+__device__ __forceinline__ int p1_tile4(int w, int n) {   // 4 waves, 3 each
+  constexpr int tab[4][3] = {{0, 10, 14}, {5, 12, 16 + 1}, {4, 8, 15}, {9, 13, 16 + 11}};
+  return tab[w][n];
+}
+__device__ __forceinline__ int p1_tile8(int w, int n) {   // 8 waves, 2 each
+  constexpr int tab[8][2] = {{0, 15}, {5, 14}, {10, 13}, {4, 12}, {8, 9}, {16 + 1, -1},
+                             {16 + 11, -1}, {-1, -1}};
+  return tab[w][n];
+}
+
+// S^T and dP^T tile (s rows 16jt.., t columns 16mt..): D[m = s][n = t].
+__device__ __forceinline__ void st_dpt_tile(const BwdStage& s, int mt, int jt, floatx4& S,
+                                            floatx4& P) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  S = zero4();
+  P = zero4();
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int ra = (16 * jt + ln) * kLd + 32 * c + 8 * lq;
+    const int rb = (16 * mt + ln) * kLd + 32 * c + 8 * lq;
+    S = mfma16x16x32(*(const bf16x8*)(s.k + ra), *(const bf16x8*)(s.q + rb), S);
+    P = mfma16x16x32(*(const bf16x8*)(s.v + ra), *(const bf16x8*)(s.d + rb), P);
+  }
+}
+
+// exp(Gc_t - Gc_s) * [s <= t] and the level of each element of a phase-1 tile.
+struct TileMask {
+  float dec[4];
+  int lev[4];    // level of the pair (0..6)
+};
+__device__ __forceinline__ TileMask tile_mask(const BwdStage& s, int mt, int jt) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  TileMask m;
+  const int t = 16 * mt + ln;
+  const float gct = s.gc[t];
+  const floatx4 gs = *(const floatx4*)(s.gc + 16 * jt + 4 * lq);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sl = 4 * lq + i;
+    if (jt < mt) {
+      m.lev[i] = 4 + intra_level(mt, jt);
+      m.dec[i] = fexp(gct - gs[i]);
+    } else {
+      m.lev[i] = intra_level(ln, sl);
+      m.dec[i] = sl <= ln ? fexp(gct - gs[i]) : 0.f;
+    }
+  }
+  return m;
+}
+
+// 8-byte LDS read pair in the D-fragment row order: X[row][c0 + 4lq + i] and
+// X[row][c0 + 16 + 4lq + i], i = 0..3.
+__device__ __forceinline__ bf16x8 row_pair(const __bf16* X, int row, int c0) {
+  const int lq = (threadIdx.x & 63) >> 4;
+  const __bf16* p = X + row * kLd + c0 + 4 * lq;
+  const bf16x4 lo = *(const bf16x4*)p;
+  const bf16x4 hi = *(const bf16x4*)(p + 16);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ bf16x8 scale8(bf16x8 x, floatx4 a, floatx4 b) {
+  bf16x8 y;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[i] = (__bf16)((float)x[i] * a[i]);
+    y[4 + i] = (__bf16)((float)x[4 + i] * b[i]);
+  }
+  return y;
+}
+
+// ---------------------------------------------------------------------------
+// Reverse summaries of the top levels
+// ---------------------------------------------------------------------------
+// One workgroup per (row, segment, group of 4 top levels); wave w owns rows
+// k = 16w.. of R_e.  sig[e][t] = lambda[t, 7 + e] exp(E_i + Gc_t).
+struct RsumSmem {
+  __bf16 q[kBT * kLd];
+  __bf16 d[kBT * kLd];
+  float sig[4][kBT];
+};
+
+template <typename TL>
+__global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ dO, const float* __restrict__ gcin,
+    const TL* __restrict__ l, float* __restrict__ rsum, int T, int H, int L, int NT, int slog,
+    int NSEG, int nloc, int ntop, int ngrp) {
+  __shared__ __attribute__((aligned(16))) RsumSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int grp = blockIdx.x % ngrp;
+  const int rest = blockIdx.x / ngrp;
+  const int h = rest % H, p = (rest / H) % NSEG, b = rest / (H * NSEG);
+  const int row = b * H + h;
+  const int c0 = p << slog, cend = min(c0 + (1 << slog), NT);
+  const int e0 = 4 * grp;
+  const int ne = min(4, ntop - e0);
+  const size_t rq0 = (size_t)b * T * H + h;
+  const unsigned int qrow = H * kKD * 2, lrowb = H * L * sizeof(TL);
+  const rsrc_t rq = make_rsrc(q + rq0 * kKD, (size_t)T * qrow);
+  const rsrc_t rd = make_rsrc(dO + rq0 * kKD, (size_t)T * qrow);
+  const rsrc_t rg = make_rsrc(gcin + rq0, (size_t)T * H * 4);
+  const rsrc_t rl = make_rsrc(l + rq0 * L, (size_t)T * lrowb);
+  const unsigned int vo = (tid >> 3) * qrow + 16 * (tid & 7);
+  const int lt = tid >> 2, le = tid & 3;   // sigma entry of this thread
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[a][n] = zero4();
+  float E = 0.f;
+  for (int ic = c0; ic < cend; ++ic) {
+    const unsigned int t0 = (unsigned int)ic * kBT;
+    const uint4 q0 = buf_load16(rq, vo, t0 * qrow), q1 = buf_load16(rq, vo, (t0 + 32) * qrow);
+    const uint4 d0 = buf_load16(rd, vo, t0 * qrow), d1 = buf_load16(rd, vo, (t0 + 32) * qrow);
+    const float gct = buf_load<float>(rg, lt * H * 4, t0 * H * 4);
+    const float glast = buf_load<float>(rg, 63 * H * 4, t0 * H * 4);
+    float lv = 0.f;
+    if (le < ne) lv = to_f32<TL>(buf_load<TL>(rl, (lt * H * L + 7 + nloc + e0 + le) * sizeof(TL),
+                                             t0 * lrowb));
+    __syncthreads();   // previous chunk's reads of sm are done
+    const int off = (tid >> 3) * kLd + 8 * (tid & 7);
+    *(uint4*)(sm.q + off) = q0;
+    *(uint4*)(sm.q + off + 32 * kLd) = q1;
+    *(uint4*)(sm.d + off) = d0;
+    *(uint4*)(sm.d + off + 32 * kLd) = d1;
+    sm.sig[le][lt] = lv * fexp(E + gct);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const bf16x8 qa = tr_frag(sm.q, kLd, 32 * c, 16 * w);   // Q[t][k = 16w + ln]
+      bf16x8 db[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) db[n] = tr_frag(sm.d, kLd, 32 * c, 16 * n);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        if (a < ne) {
+          const float* sg = sm.sig[a] + 32 * c + 8 * lq;
+          const bf16x8 qs = scale8(qa, *(const floatx4*)sg, *(const floatx4*)(sg + 4));
+#pragma unroll
+          for (int n = 0; n < 4; ++n) acc[a][n] = mfma16x16x32(qs, db[n], acc[a][n]);
+        }
+      }
+    }
+    E += glast;
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    if (a < ne) {
+      float* out = rsum + (((size_t)row * NSEG + p) * ntop + e0 + a) * kKD * kKD;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[(16 * w + 4 * lq + i) * kKD + 16 * n + ln] = acc[a][n][i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq and dlambda: forward walk over one segment
+// ---------------------------------------------------------------------------
+struct DqSmem {
+  BwdStage st;
+  __bf16 a[kBT * kLd];                      // (M o dP)[t][s], bf16
+  float dl_off[kBT][4][4];                  // off-diagonal tile partials [t][jt][lq]
+  float dl_diag[kBT][5][4];                 // diagonal tile partials [t][level][lq]
+  float dl_int[kBT][kMaxLoc + kMaxTop][4];  // inter-level partials [t][e][wave]
+  __bf16 top[1];                            // [ntop][k][v] top-level states (dynamic)
+};
+
+inline int dq_smem_bytes(int ntop) { return (int)offsetof(DqSmem, top) + ntop * kKD * kLd * 2; }
+
+template <typename TV, typename TL>
+__global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
+    const float* __restrict__ sums, const float* __restrict__ segd, __bf16* __restrict__ dq,
+    float* __restrict__ dl, float* __restrict__ dgq, int B, int T, int H, int V, int L, int nlev,
+    int slog, int NSEG) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  DqSmem& sm = *(DqSmem*)smem_raw;
+  BwdStage& s = sm.st;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int I = blockIdx.x;
+  const int h = I % H, p = (I / H) % NSEG, b = I / (H * NSEG);
+  const int row = b * H + h;
+  const int NT = T / kBT;
+  const int c0 = p << slog, cend = min(c0 + (1 << slog), NT);
+  const int lu = 7 + nlev;
+  const int nloc = min(slog, nlev), ntop = nlev - nloc;
+
+  // ---- top-level states Htop_e(p) -> LDS, bf16 [k][v] ----------------------------
+  if (ntop > 0) {
+    const float* sp = sums + (size_t)row * NSEG * kKD * kKD;
+    const float* dp = segd + (size_t)row * NSEG;
+    const int kk = tid >> 2, v0 = 16 * (tid & 3);
+    for (int e2 = 0; e2 < ntop; ++e2) {
+      if (!((p >> e2) & 1)) continue;
+      const int lo = (p >> (e2 + 1)) << (e2 + 1), hi = lo + (1 << e2);
+      float dlog = 0.f;
+      for (int r = hi; r < p; ++r) dlog += dp[r];
+      float hacc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) hacc[i] = 0.f;
+      for (int qs = hi - 1; qs >= lo; --qs) {
+        const float sc = fexp(dlog);
+        const float* src = sp + ((size_t)qs * kKD + kk) * kKD + v0;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          const floatx4 x = *(const floatx4*)(src + i);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) hacc[i + u] += sc * x[u];
+        }
+        dlog += dp[qs];
+      }
+      __bf16* tp = sm.top + e2 * kKD * kLd + kk * kLd + v0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tp[i] = (__bf16)hacc[i];
+    }
+  }
+
+  BwdLoader<256, TV, TL> ld;
+  ld.init(q, k, v, dO, gcin, l, b, h, T, H, V, L, lu);
+  const size_t rq0 = (size_t)b * T * H + h;
+  const rsrc_t rdq = make_rsrc(dq + rq0 * kKD, (size_t)T * H * kKD * 2);
+  const rsrc_t rdl = make_rsrc(dl + rq0 * L, (size_t)T * H * L * 4);
+  const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
+  const unsigned int vo_dq = (ln * H * kKD + 16 * w + 4 * lq) * 2;
+
+  // forward states h_e^T [v][k]: lane holds v = 16m + 4lq + i, k = 16w + ln
+  floatx4 hT[kMaxLoc][4];
+#pragma unroll
+  for (int e = 0; e < kMaxLoc; ++e)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) hT[e][m] = zero4();
+
+  BwdRegs<256, TV, TL> rg;
+  ld.load(rg, c0);
+  float Eseg = 0.f;
+  for (int ic = c0; ic < cend; ++ic) {
+    ld.store(rg, s);
+    if (ic + 1 < cend) ld.load(rg, ic + 1);
+    __syncthreads();
+
+    // ---- phase 1: (M o dP) tiles and the intra-chunk dlambda partials ----------
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      const int code = p1_tile4(w, n);
+      const int mt = (code & 15) >> 2, jt = code & 3;
+      const int t = 16 * mt + ln;
+      bf16x4 out = bf16x4{};
+      if (code < 16) {
+        floatx4 S, P;
+        st_dpt_tile(s, mt, jt, S, P);
+        const TileMask mk = tile_mask(s, mt, jt);
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pd = mk.dec[i] * P[i];
+          out[i] = (__bf16)(pd * s.lam[mk.lev[i] * kBT + t]);
+          x[i] = pd * S[i];
+        }
+        if (jt < mt) {
+          sm.dl_off[t][jt][lq] = x[0] + x[1] + x[2] + x[3];
+        } else {
+#pragma unroll
+          for (int lv = 0; lv < 5; ++lv) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a += mk.lev[i] == lv ? x[i] : 0.f;
+            sm.dl_diag[t][lv][lq] = a;
+          }
+        }
+      }
+      *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+    }
+    __syncthreads();
+
+    // ---- phase 2: dq^T[k-tile w][t] ----------------------------------------------
+    floatx4 dqT[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const __bf16* ar = sm.a + (16 * mt + ln) * kLd + 8 * lq;
+      dqT[mt] = mfma16x16x32(tr_frag(s.k, kLd, 0, 16 * w), *(const bf16x8*)ar, zero4());
+      if (mt >= 2)
+        dqT[mt] = mfma16x16x32(tr_frag(s.k, kLd, 32, 16 * w), *(const bf16x8*)(ar + 32), dqT[mt]);
+    }
+    // q[t][k] for this lane's (t = 16mt + ln, k = 16w + 4lq + i)
+    floatx4 qk[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const bf16x4 x = *(const bf16x4*)(s.q + (16 * mt + ln) * kLd + 16 * w + 4 * lq);
+      qk[mt] = floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+    }
+    if (nlev > 0) {
+      bf16x8 da[4][2];   // dO[t][v] in the states' v order
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) da[mt][c] = row_pair(s.d, 16 * mt + ln, 32 * c);
+      auto level = [&](const bf16x8& a0, const bf16x8& a1, int e, int col, float scale) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          floatx4 y = mfma16x16x32(a0, da[mt][0], zero4());
+          y = mfma16x16x32(a1, da[mt][1], y);     // Y^T[k][t] = sum_v h[k][v] dO[t][v]
+          const int t = 16 * mt + ln;
+          const float sg = s.lam[col * kBT + t] * scale;
+          float r = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dqT[mt][i] += y[i] * sg;
+            r += qk[mt][i] * y[i];
+          }
+          r = sum_lq(r);
+          if (lq == 0) sm.dl_int[t][e][w] = r * scale;   // dlambda / exp(Gc_t)
+        }
+      };
+      if (nloc > 0) {
+#pragma unroll
+        for (int e = 0; e < kMaxLoc; ++e) {
+          if (e < nloc) {
+            const float z = (ic > c0 && ((ic >> e) & 1)) ? 1.f : 0.f;
+            level(cat8(hT[e][0] * z, hT[e][1] * z), cat8(hT[e][2] * z, hT[e][3] * z), e, 7 + e,
+                  1.f);
+          }
+        }
+      }
+      const float ee = fexp(Eseg);
+      for (int e2 = 0; e2 < ntop; ++e2) {
+        if ((p >> e2) & 1) {
+          const __bf16* tp = sm.top + e2 * kKD * kLd;
+          level(row_pair(tp, 16 * w + ln, 0), row_pair(tp, 16 * w + ln, 32), nloc + e2,
+                7 + nloc + e2, ee);
+        } else if (lq == 0) {
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][nloc + e2][w] = 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      buf_store4<__bf16>(dqT[mt], rdq, vo_dq, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * 2);
+
+    // ---- phase 3: forward state update h^T_e[v][k] += (w o V)^T K ---------------
+    const float glr = s.gc[kBT - 1];
+    if (nloc > 0) {
+      floatx4 kv[4];
+      {
+        const bf16x8 kb0 = scale8(tr_frag(s.k, kLd, 0, 16 * w), *(const floatx4*)(s.wt + 8 * lq),
+                                  *(const floatx4*)(s.wt + 8 * lq + 4));
+        const bf16x8 kb1 =
+            scale8(tr_frag(s.k, kLd, 32, 16 * w), *(const floatx4*)(s.wt + 32 + 8 * lq),
+                   *(const floatx4*)(s.wt + 36 + 8 * lq));
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          kv[m] = mfma16x16x32(tr_frag(s.v, kLd, 0, 16 * m), kb0, zero4());
+          kv[m] = mfma16x16x32(tr_frag(s.v, kLd, 32, 16 * m), kb1, kv[m]);
+        }
+      }
+      const float gl = fexp(glr);
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        if (e < nloc) {
+          const int per = 2 << e;
+          const bool reset = (ic & (per - 1)) == per - 1;
+          const bool wr = !((ic >> e) & 1);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            if (reset) {
+              hT[e][m] = wr ? kv[m] : zero4();
+            } else if (wr) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) hT[e][m][i] = hT[e][m][i] * gl + kv[m][i];
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) hT[e][m][i] *= gl;
+            }
+          }
+        }
+      }
+    }
+    Eseg += glr;
+    __syncthreads();
+
+    // ---- dlambda row of every token, and q . dq = sum_l lambda_l dlambda_l ----------
+    // (the identity holds term by term: row t of (M o S o dP) summed by level; it
+    // uses the fp32 tile products instead of the bf16-rounded (M o dP) behind dq)
+    {
+      const int t = tid >> 2, part = tid & 3;
+      const int mt = t >> 4;
+      const unsigned int so = ((unsigned int)ic * kBT + t) * H * L * 4;
+      float qdq = 0.f;
+      for (int col = part; col < L; col += 4) {
+        float val = 0.f;
+        if (col <= 4) {
+          val = sm.dl_diag[t][col][0] + sm.dl_diag[t][col][1] + sm.dl_diag[t][col][2] +
+                sm.dl_diag[t][col][3];
+        } else if (col <= 6) {
+          for (int jt = 0; jt < mt; ++jt)
+            if (4 + intra_level(mt, jt) == col)
+              val += sm.dl_off[t][jt][0] + sm.dl_off[t][jt][1] + sm.dl_off[t][jt][2] +
+                     sm.dl_off[t][jt][3];
+        } else if (col < lu) {
+          const int e = col - 7;
+          const float raw =
+              sm.dl_int[t][e][0] + sm.dl_int[t][e][1] + sm.dl_int[t][e][2] + sm.dl_int[t][e][3];
+          qdq += raw * s.lam[col * kBT + t];   // lambda exp(Gc_t) * dlambda / exp(Gc_t)
+          val = raw * s.eg[t];
+        }
+        if (col <= 6) qdq += val * s.lam[col * kBT + t];
+        buf_store<float>(val, rdl, col * 4, so);
+      }
+      qdq += __shfl_xor(qdq, 1, 64);
+      qdq += __shfl_xor(qdq, 2, 64);
+      if (part == 0) buf_store<float>(qdq, rgq, 0, ((unsigned int)ic * kBT + t) * H * 4);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dk, dv and dG: reverse walk over one segment, 8 waves
+// ---------------------------------------------------------------------------
+struct DkvSmem {
+  BwdStage st;
+  __bf16 as[kBT * kLd];     // (M o S)[t][s]
+  __bf16 ap[kBT * kLd];     // (M o dP)[t][s]
+  float dgk[kBT][4];        // k . dk inter-chunk partials [s][wave]
+  float kdk[kBT][4];        // k . dk intra-chunk column sums [s][t-tile]
+};
+
+template <typename TV, typename TL>
+__global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
+    const float* __restrict__ rsum, const float* __restrict__ segd,
+    const float* __restrict__ dgq, __bf16* __restrict__ dk, TV* __restrict__ dv,
+    float* __restrict__ dg, float* __restrict__ segtot, int B, int T, int H, int V, int L,
+    int nlev, int slog, int NSEG) {
+  __shared__ __attribute__((aligned(16))) DkvSmem sm;
+  BwdStage& s = sm.st;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int role = w >> 2, wr = w & 3;     // role 0: dk (k-tile wr), role 1: dv (v-tile wr)
+  const int I = blockIdx.x;
+  const int h = I % H, p = (I / H) % NSEG, b = I / (H * NSEG);
+  const int row = b * H + h;
+  const int NT = T / kBT;
+  const int c0 = p << slog, cend = min(c0 + (1 << slog), NT);
+  const int lu = 7 + nlev;
+  const int nloc = min(slog, nlev), ntop = nlev - nloc;
+
+  // Reverse states in the role's layout, lane (lq, ln), m = 0..3, i = 0..3:
+  //   role 0: DH^T[v = 16m + 4lq + i][k = 16wr + ln]
+  //   role 1: DH  [k = 16m + 4lq + i][v = 16wr + ln]
+  floatx4 dh[kMaxLoc][4];
+#pragma unroll
+  for (int e = 0; e < kMaxLoc; ++e)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) dh[e][m] = zero4();
+  // combined top-level state: sum over top levels whose bit in p is clear of
+  // the reading block's summaries decayed to the end of segment p
+  floatx4 tp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) tp[m] = zero4();
+  if (ntop > 0) {
+    const float* dp = segd + (size_t)row * NSEG;
+    for (int e2 = 0; e2 < ntop; ++e2) {
+      if ((p >> e2) & 1) continue;
+      const int lo = ((p >> e2) | 1) << e2;
+      const int hi = min(lo + (1 << e2), NSEG);
+      float dlog = 0.f;
+      for (int r = p + 1; r < lo; ++r) dlog += dp[r];
+      for (int qs = lo; qs < hi; ++qs) {
+        const float sc = fexp(dlog);
+        const float* src = rsum + (((size_t)row * NSEG + qs) * ntop + e2) * kKD * kKD;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int a = 16 * m + 4 * lq + i, c = 16 * wr + ln;
+            tp[m][i] += sc * (role == 0 ? src[c * kKD + a] : src[a * kKD + c]);
+          }
+        dlog += dp[qs];
+      }
+    }
+  }
+
+  BwdLoader<512, TV, TL> ld;
+  ld.init(q, k, v, dO, gcin, l, b, h, T, H, V, L, lu);
+  const size_t rq0 = (size_t)b * T * H + h;
+  const rsrc_t rdk = make_rsrc(dk + rq0 * kKD, (size_t)T * H * kKD * 2);
+  const rsrc_t rdv = make_rsrc(dv + rq0 * V, (size_t)T * H * V * sizeof(TV));
+  const rsrc_t rdg = make_rsrc(dg + rq0, (size_t)T * H * 4);
+  const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
+  const unsigned int vo_dk = (ln * H * kKD + 16 * wr + 4 * lq) * 2;
+  const unsigned int vo_dv = (ln * H * V + 16 * wr + 4 * lq) * sizeof(TV);
+
+  BwdRegs<512, TV, TL> rg;
+  ld.load(rg, cend - 1);
+  float carry = 0.f;   // sum of dG over the later chunks of this segment
+  for (int ic = cend - 1; ic >= c0; --ic) {
+    ld.store(rg, s);
+    if (ic - 1 >= c0) ld.load(rg, ic - 1);
+    __syncthreads();
+
+    // ---- phase 1: (M o S) and (M o dP) tiles ---------------------------------------
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int code = p1_tile8(w, n);
+      if (code >= 0) {
+        const int mt = (code & 15) >> 2, jt = code & 3;
+        const int t = 16 * mt + ln;
+        bf16x4 os = bf16x4{}, op = bf16x4{};
+        if (code < 16) {
+          floatx4 S, P;
+          st_dpt_tile(s, mt, jt, S, P);
+          const TileMask mk = tile_mask(s, mt, jt);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float m = mk.dec[i] * s.lam[mk.lev[i] * kBT + t];
+            os[i] = (__bf16)(m * S[i]);
+            op[i] = (__bf16)(m * P[i]);
+            // k_s . dk_s (intra part) = column sum over t of (M o S o dP), in fp32
+            float c = m * S[i] * P[i];
+            c += __shfl_xor(c, 1, 64);
+            c += __shfl_xor(c, 2, 64);
+            c += __shfl_xor(c, 4, 64);
+            c += __shfl_xor(c, 8, 64);
+            if (ln == 0) sm.kdk[16 * jt + 4 * lq + i][mt] = c;
+          }
+        }
+        *(bf16x4*)(sm.as + t * kLd + 16 * jt + 4 * lq) = os;
+        *(bf16x4*)(sm.ap + t * kLd + 16 * jt + 4 * lq) = op;
+      }
+    }
+    __syncthreads();
+
+    // ---- phase 2: dk^T (role 0) / dv^T (role 1) for the chunk's tokens s -------------
+    const __bf16* xa = role == 0 ? s.q : s.d;      // A of the intra product: Q^T / dO^T
+    const __bf16* xb = role == 0 ? sm.ap : sm.as;  // B: (M o dP) / (M o S)
+    const __bf16* xs = role == 0 ? s.v : s.k;      // B of the inter product: V / K rows s
+    floatx4 out[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      // t-steps covering t >= s: both for s-tiles 0, 1; the second for 2, 3
+      out[mt] = mfma16x16x32(tr_frag(xa, kLd, 32, 16 * wr), tr_frag(xb, kLd, 32, 16 * mt),
+                             zero4());
+      if (mt < 2)
+        out[mt] = mfma16x16x32(tr_frag(xa, kLd, 0, 16 * wr), tr_frag(xb, kLd, 0, 16 * mt),
+                               out[mt]);
+    }
+    {
+      // DHsum = sum of the local levels this chunk is a source of, plus the top part
+      floatx4 dsum[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) dsum[m] = tp[m];
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        if (e < nloc && !((ic >> e) & 1)) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) dsum[m] += dh[e][m];
+        }
+      }
+      const bf16x8 a0 = cat8(dsum[0], dsum[1]), a1 = cat8(dsum[2], dsum[3]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        floatx4 y = mfma16x16x32(a0, row_pair(xs, 16 * mt + ln, 0), zero4());
+        y = mfma16x16x32(a1, row_pair(xs, 16 * mt + ln, 32), y);
+        const float ws = s.wt[16 * mt + ln];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[mt][i] += y[i] * ws;
+        if (role == 0) {
+          // k_s . dk_s, inter-chunk part
+          const bf16x4 kx = *(const bf16x4*)(s.k + (16 * mt + ln) * kLd + 16 * wr + 4 * lq);
+          float r = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) r += (float)kx[i] * y[i];
+          r = sum_lq(r) * ws;
+          if (lq == 0) sm.dgk[16 * mt + ln][wr] = r;
+        }
+      }
+    }
+    if (role == 0) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        buf_store4<__bf16>(out[mt], rdk, vo_dk, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * 2);
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        buf_store4<TV>(out[mt], rdv, vo_dv, ((unsigned int)ic * kBT + 16 * mt) * H * V * sizeof(TV));
+    }
+
+    // ---- phase 3: reverse states to the boundary before this chunk ----------------------
+    const float cl = s.gc[kBT - 1];
+    const float gl = fexp(cl);
+    if (nloc > 0) {
+      const __bf16* ya = role == 0 ? s.d : s.q;   // A: dO^T / Q^T (rows of the state)
+      const __bf16* yb = role == 0 ? s.q : s.d;   // B: sigma o Q / sigma o dO
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        if (e < nloc) {
+          const int per = 2 << e;
+          const bool reset = (ic & (per - 1)) == 0;
+          const bool rd = (ic >> e) & 1;
+          if (reset) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) dh[e][m] = zero4();
+          } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) dh[e][m] *= gl;
+            if (rd) {
+              const float* sg = s.lam + (7 + e) * kBT;
+              const bf16x8 b0 = scale8(tr_frag(yb, kLd, 0, 16 * wr), *(const floatx4*)(sg + 8 * lq),
+                                       *(const floatx4*)(sg + 8 * lq + 4));
+              const bf16x8 b1 = scale8(tr_frag(yb, kLd, 32, 16 * wr),
+                                       *(const floatx4*)(sg + 32 + 8 * lq),
+                                       *(const floatx4*)(sg + 36 + 8 * lq));
+#pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                dh[e][m] = mfma16x16x32(tr_frag(ya, kLd, 0, 16 * m), b0, dh[e][m]);
+                dh[e][m] = mfma16x16x32(tr_frag(ya, kLd, 32, 16 * m), b1, dh[e][m]);
+              }
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) tp[m] *= gl;
+    __syncthreads();
+
+    // ---- dG = q . dq - k . dk and its reverse cumsum inside the segment --------------
+    if (w == 0) {
+      const unsigned int so = ((unsigned int)ic * kBT + lane) * H * 4;
+      // column sums over the t-tiles at or after this s-tile (the others are zero)
+      float kdk = sm.dgk[lane][0] + sm.dgk[lane][1] + sm.dgk[lane][2] + sm.dgk[lane][3];
+      for (int mt = lane >> 4; mt < 4; ++mt) kdk += sm.kdk[lane][mt];
+      const float dG = buf_load<float>(rgq, 0, so) - kdk;
+      float x = dG;   // inclusive suffix sum over the chunk
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_down(x, d, 64);
+        if (lane + d < 64) x += y;
+      }
+      buf_store<float>(x + carry, rdg, 0, so);
+      carry += __shfl(x, 0, 64);
+    }
+  }
+  if (tid == 0) segtot[(size_t)row * NSEG + p] = carry;
+}
+
+// dg of segment p += sum of the totals of the segments after p.
+__global__ __launch_bounds__(256) void mamba2_bwd_dg_kernel(float* __restrict__ dg,
+                                                            const float* __restrict__ segtot,
+                                                            int T, int H, int slog, int NSEG) {
+  const int I = blockIdx.x;
+  const int h = I % H, p = (I / H) % NSEG, b = I / (H * NSEG);
+  const int row = b * H + h;
+  float off = 0.f;
+  for (int r = p + 1; r < NSEG; ++r) off += segtot[(size_t)row * NSEG + r];
+  const int t0 = (p << slog) * kBT, t1 = min(((p + 1) << slog) * kBT, T);
+  float* d = dg + (size_t)b * T * H + h;
+  for (int t = t0 + (int)threadIdx.x; t < t1; t += 256) d[(size_t)t * H] += off;
+}
+
+// ---------------------------------------------------------------------------
+// host launcher
+// ---------------------------------------------------------------------------
+struct BwdWs {
+  float *segd, *sums, *rsum, *dgq, *segtot;
+  size_t bytes;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline BwdWs bwd_ws_layout(void* base, int B, int T, int H, int V, int nlev) {
+  const int NT = T / kBT;
+  const int slog = seg_log2(NT);
+  const int NSEG = (NT + (1 << slog) - 1) >> slog;
+  const int ntop = nlev - min(slog, nlev);
+  const size_t rows = (size_t)B * H;
+  BwdWs w;
+  size_t off = 0;
+  char* p = (char*)base;
+  w.segd = (float*)(p + off);   off += align256(rows * NSEG * 4);
+  w.segtot = (float*)(p + off); off += align256(rows * NSEG * 4);
+  w.dgq = (float*)(p + off);    off += align256((size_t)B * T * H * 4);
+  w.sums = (float*)(p + off);   off += align256(NSEG > 1 ? rows * NSEG * kKD * V * 4 : 0);
+  w.rsum = (float*)(p + off);   off += align256(rows * NSEG * ntop * kKD * kKD * 4);
+  w.bytes = off;
+  return w;
+}
+
+template <typename TV, typename TL>
+static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, const float* gc,
+                               const void* l, const void* dO, void* dq, void* dk, void* dv,
+                               float* dg, float* dl, void* ws, int B, int T, int H, int V,
+                               int L, int nlev, hipStream_t stream) {
+  const int NT = T / kBT;
+  const int slog = seg_log2(NT);
+  const int NSEG = (NT + (1 << slog) - 1) >> slog;
+  const int nloc = min(slog, nlev), ntop = nlev - nloc;
+  const int rows = B * H;
+  const BwdWs w = bwd_ws_layout(ws, B, T, H, V, nlev);
+  hipError_t e;
+  if (NSEG > 1) {
+    auto sk = mamba2_seg_sum_kernel<TV, true>;
+    hipLaunchKernelGGL(sk, dim3(rows * NSEG), dim3(256), 0, stream, (const __bf16*)k,
+                       (const TV*)v, gc, w.sums, w.segd, T, H, H, V, NT, 1 << slog, NSEG, 1);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (ntop > 0) {
+    const int ngrp = (ntop + 3) / 4;
+    auto rk = mamba2_bwd_rsum_kernel<TL>;
+    hipLaunchKernelGGL(rk, dim3(rows * NSEG * ngrp), dim3(256), 0, stream, (const __bf16*)q,
+                       (const __bf16*)dO, gc, (const TL*)l, w.rsum, T, H, L, NT, slog, NSEG,
+                       nloc, ntop, ngrp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  {
+    auto kq = mamba2_bwd_dq_kernel<TV, TL>;
+    const int smem = dq_smem_bytes(ntop);
+    if ((e = hipFuncSetAttribute((const void*)kq, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 smem)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(kq, dim3(rows * NSEG), dim3(256), smem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc, (const TL*)l,
+                       w.sums, w.segd, (__bf16*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog, NSEG);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  {
+    auto kk = mamba2_bwd_dkv_kernel<TV, TL>;
+    hipLaunchKernelGGL(kk, dim3(rows * NSEG), dim3(512), 0, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc, (const TL*)l,
+                       w.rsum, w.segd, w.dgq, (__bf16*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
+                       nlev, slog, NSEG);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (NSEG > 1) {
+    hipLaunchKernelGGL(mamba2_bwd_dg_kernel, dim3(rows * NSEG), dim3(256), 0, stream, dg,
+                       w.segtot, T, H, slog, NSEG);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace hattn
+
+size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev) {
+  return hattn::bwd_ws_layout(nullptr, B, T, H, V, nlev).bytes;
+}
+
+hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
+                                   const void* l, const void* dO, void* dq, void* dk, void* dv,
+                                   float* dg, float* dl, void* ws, int B, int T, int H, int V,
+                                   int L, int nlev, int dt_v, int dt_l, hipStream_t stream,
+                                   int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  if (dt_v == 0 && dt_l == 0)
+    return bwd_launch_t<__bf16, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+  if (dt_v == 0 && dt_l == 2)
+    return bwd_launch_t<__bf16, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+  if (dt_v == 2 && dt_l == 0)
+    return bwd_launch_t<float, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+  if (dt_v == 2 && dt_l == 2)
+    return bwd_launch_t<float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+  *unsupported = 1;
+  return hipSuccess;
+}

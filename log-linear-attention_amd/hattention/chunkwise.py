@@ -122,6 +122,39 @@ def chunkwise_bwd(
     """Log-linear Mamba-2 backward (chunkwise.py:1286-1597).
 
     ``g`` is the chunk-local cumsum returned by :func:`chunkwise_fwd`.
-    Returns (dq, dk, dv, dg, dl) with dg w.r.t. the raw per-step g.
+    Returns (dq, dk, dv, dg, dl): dq / dk / dv in the dtypes of q / k / v,
+    dg (w.r.t. the raw per-step g) and dl in fp32, like the reference.  Grouped
+    q / k are expanded per head before the kernels and their gradients summed
+    over the group afterwards (chunkwise.py:1360-1362, 1583-1594).
     """
-    raise NotImplementedError("the MI355X Mamba-2 backward kernel is not built yet")
+    _assert_contiguous(q=q, k=k, v=v, g=g, l=l, do=do)
+    B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
+    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size)
+    if g.shape != (B, T, H) or g.dtype != torch.float32:
+        raise ValueError("g must be the fp32 chunk-local cumsum [B, T, H]")
+    if do.shape != v.shape:
+        raise ValueError("do must have the shape of v")
+    dev = _lib.require_device(q, k, v, g, l, do)
+    if G != H:
+        q = q.repeat_interleave(H // G, dim=2).contiguous()
+        k = k.repeat_interleave(H // G, dim=2).contiguous()
+    do = do.to(q.dtype).contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, K, V, L), dev)
+    st = lib.hattn_mamba2_chunkwise_bwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
+        _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
+        B, T, H, K, V, L, _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l),
+        _lib.dtype_code(do), level_base, htype.value, chunk_size, ws_ptr, ws_bytes,
+        _lib.stream_handle(dev))
+    _lib.check(st)
+    if G != H:
+        dq = dq.view(B, T, G, H // G, K).sum(3)
+        dk = dk.view(B, T, G, H // G, K).sum(3)
+    return dq, dk, dv, dg, dl

@@ -15,8 +15,9 @@ Contents (each function cites the reference file:line it restates):
   Fenwick recurrent form, chunked form (masked chunk-level combination) and
   chunked level-scan form; plain (non-hierarchical) SSD scan for the
   lambda == 1 special case; backward through autograd.
-* ``gdn``     -- log-linear Gated DeltaNet: recurrent form, materialised form
-  and chunked (UT / WY) form.
+* ``gdn``     -- log-linear Gated DeltaNet: recurrent form (matrix gates),
+  materialised pair sum, chunked UT / WY form with per-level delta-rule scans,
+  the plain gated delta rule (lambda == 1) and the l2norm / scale boundary.
 
 Pinning (what checks each function against something other than itself) is
 listed in each module docstring; the tests that perform the checks live in

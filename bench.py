@@ -64,6 +64,27 @@ def make_mamba2_inputs(B, T, H, K, V, L, G=None, seed=1000, dtype=torch.bfloat16
     return [t.to(device) for t in out]
 
 
+def make_gdn_inputs(B, T, H, K, V, L, seed=1003, dtype=torch.bfloat16, device="cpu"):
+    """Seeded GDN inputs of BASELINE config 3 (drawn fp32 on CPU in the order q, k,
+    v, A_log, dt-noise, lambda-noise, beta-noise): q, k l2-normalised N(0,1);
+    v ~ N(0,1); beta = sigmoid(N(0,1)); g = -A * dt as in the Mamba-2 configs;
+    lambda = softplus(N(0,1))."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=gen), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=gen), dim=-1)
+    v = torch.randn(B, T, H, V, generator=gen)
+    A_log = torch.empty(H).uniform_(math.log(1.0), math.log(16.0), generator=gen)
+    dt0 = torch.exp(torch.empty(H).uniform_(math.log(1e-3), math.log(1e-1), generator=gen))
+    bias = dt0 + torch.log(-torch.expm1(-dt0))
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, generator=gen) + bias)
+    dt = dt.clamp(1e-3, 1e-1)
+    g = (-torch.exp(A_log) * dt).float()
+    lam = torch.nn.functional.softplus(torch.randn(B, T, H, L, generator=gen))
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    out = [q.to(dtype), k.to(dtype), v.to(dtype), beta.to(dtype), g, lam.to(dtype)]
+    return [t.to(device) for t in out]
+
+
 def fwd_bytes(B, T, H, K, V, L, es=2, es_l=2, G=None):
     """Algorithmic HBM bytes of one forward: read q, k, v, g, lambda, write o."""
     G = G or H

@@ -123,6 +123,39 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
  * (chunkwise.py:1371-1384). */
 size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
 
+/*
+ * Log-linear Gated DeltaNet chunkwise forward.
+ *
+ * Replaces hattention/chunkwise_hgdn.py:566-788 `chunkwise_fwd(q, k, v, b, g, l,
+ * head_first, level_base, htype, chunk_size, output_final_state)
+ * -> (g_cumsum, o, Aw, Au, ht)`, called by HAttentionFunction.forward for
+ * HStruct.GDELTA (kernel.py:100-123) with q = l2norm(q) * scale, k = l2norm(k).
+ * Per head (the reference expands grouped q / k first, chunkwise_hgdn.py:614-623):
+ *
+ *   q, k [B, T, H, K] bf16   v, o [B, T, H, V] bf16   beta [B, T, H] in dtype_beta
+ *   g [B, T, H] fp32 per-step log-decay     l [B, T, H, L] in dtype_l
+ *   g_cumsum [B, T, H] fp32 (output, chunk-local inclusive cumsum)
+ *   Aw, Au [B, T, H, 64] bf16 (outputs): per chunk (I + A)^-1 and (I + A)^-1 o gamma,
+ *          A = strict-tril(diag(beta) K K^T), gamma[t,s] = exp(Gc_t - Gc_s)
+ *   ht [B, H, K, V, L] fp32 final level states or NULL
+ *   workspace >= hattn_gdn_chunkwise_fwd_workspace(...) bytes
+ *
+ * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64
+ * -> HATTN_ERR_VALUE; (K, V) in {(64, 64), (128, 128)}, T <= 64 * 2^7, q/k/v
+ * bf16, beta / l in {BF16, FP32}, o bf16 -> HATTN_ERR_NOT_IMPLEMENTED.
+ */
+int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const void* beta,
+                            const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
+                            void* Au, float* ht, int B, int T, int H, int K, int V, int L,
+                            int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
+                            int level_base, int htype, int chunk_size, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of hattn_gdn_chunkwise_fwd (q_new, k_new, w_new, u in bf16
+ * and the fp32 intra-chunk output).  No counterpart in the reference, which
+ * allocates these with torch inside chunkwise_fwd (chunkwise_hgdn.py:636-642). */
+size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int L);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,574 @@
+// Log-linear Gated DeltaNet chunkwise forward for gfx950.
+//
+// Replaces chunkwise_hgdn.chunkwise_fwd (chunkwise_hgdn.py:566-788): the
+// reference materialises gamma = exp(segsum(g)) in torch, then launches
+// chunk_scaled_dot_kkt, two solve_tril passes, recompute_w_u, preprocess_qkw,
+// a torch einsum for q_new, the intra-chunk output kernel and, per inter-chunk
+// level, torch masked copies of u / w / g plus the delta-rule state kernel and
+// the output kernel.
+//
+// Per (b, h) row, chunk of C = 64 tokens, chunk-local cumsum Gc, with
+// A = strict-tril(diag(beta) K K^T), Aw = (I + A)^-1, gamma[t,s] =
+// exp(Gc_t - Gc_s) (s <= t), Au = Aw o gamma:
+//   W = Aw (beta K),  U = Au (beta V),  K_new = exp(Gc_last - Gc) K,
+//   W_new = exp(Gc) W,  q_new = exp(Gc) (Q - tril(Q K^T) W),
+//   o_intra = ((tril(Q K^T) Aw) o gamma o beta_s o lambda[t, lev(t, s)]) V
+// and every inter-chunk level e runs the delta-rule recurrence over chunks
+//   h_e <- (reset ? 0 : exp(Gc_last) h_e) + K_new^T ((write ? U : 0) - (reset ? 0 : W_new h_e))
+// (write: bit e of the chunk index clear; reset after the last chunk of an
+// aligned 2^(e+1) block), read by the chunks with bit e set:
+//   o += lambda[t, 7 + e] q_new h_e.
+//
+// Kernel 1 (gdn_prep_kernel): one workgroup per chunk computes everything
+// that is local to the chunk: the two 64 x 64 products K K^T and Q K^T on
+// MFMA, the fp32 unit-lower-triangular inverse (16 x 16 diagonal blocks by
+// substitution, off-diagonal blocks by block substitution), W, U, q_new,
+// K_new, W_new and o_intra, plus the Aw / Au the reference returns.
+// Kernel 2 (gdn_scan_kernel): one workgroup per (row, 32 columns of V) walks
+// the chunks in order with every level's [K x 32] state in fp32 registers
+// (wave w owns K / 4 state rows); per chunk it stages the states in LDS
+// as bf16, forms W_new h_e and q_new h_e for all levels, then
+// h_e += K_new^T V_new_e, and writes o = o_intra + sum of the level reads.
+#include "common.h"
+
+namespace hattn {
+
+constexpr int kGC = 64;       // chunk length
+constexpr int kLd64 = 72;     // LDS row stride of 64-wide bf16 tiles
+constexpr int kGMaxLev = 7;   // inter-chunk levels held by the scan (T <= 64 * 2^7)
+constexpr int kBVs = 32;      // V columns per scan workgroup
+
+template <int KD, int VD>
+struct GdnPrepSmem {
+  static constexpr int LK = KD + 8, LV = VD + 8, LF = (KD > VD ? KD : VD) + 4;
+  static constexpr int NF = kGC * LF > 2 * kGC * 65 ? kGC * LF : 2 * kGC * 65;
+  __bf16 k[kGC * LK];
+  __bf16 q[kGC * LK];
+  __bf16 v[kGC * LV];
+  float f[NF];                    // A / X (two 64 x 65 fp32 blocks), later fp32 staging
+  float t1[4][16 * 17];           // per-wave block-substitution scratch
+  __bf16 aw[kGC * kLd64];         // Aw (bf16)
+  __bf16 au[kGC * kLd64];         // Au = Aw o gamma (bf16)
+  __bf16 qk[kGC * kLd64];         // tril(Q K^T) (bf16)
+  __bf16 pm[kGC * kLd64];         // (tril(Q K^T) Aw) o gamma o beta o lambda (bf16)
+  __bf16 w[kGC * LK];             // W (bf16)
+  float gc[kGC];
+  float beta[kGC];
+  float lam[7][kGC];              // intra-chunk lambda columns 0..6
+};
+
+// 16-byte units of a row-major [64][N] bf16 tile, NTHR = 256 threads.
+template <int N>
+__device__ __forceinline__ void g2s_tile(const __bf16* __restrict__ src, size_t row_stride,
+                                         __bf16* dst, int ld) {
+  constexpr int UPR = N / 8;  // units per row
+  for (int u = threadIdx.x; u < kGC * UPR; u += 256) {
+    const int r = u / UPR, c = 8 * (u % UPR);
+    *(uint4*)(dst + r * ld + c) = *(const uint4*)(src + r * row_stride + c);
+  }
+}
+
+template <int KD, int VD, typename TB, typename TL>
+__global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
+    float* __restrict__ gcum, __bf16* __restrict__ aw_out, __bf16* __restrict__ au_out,
+    __bf16* __restrict__ qn, __bf16* __restrict__ kn, __bf16* __restrict__ wn,
+    __bf16* __restrict__ un, float* __restrict__ oi, int T, int H, int L) {
+  using Sm = GdnPrepSmem<KD, VD>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Sm& s = *(Sm*)smem_raw;
+  constexpr int LK = Sm::LK, LV = Sm::LV, LF = Sm::LF;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int NT = T / kGC;
+  const int ic = blockIdx.x % NT;
+  const int row = blockIdx.x / NT;
+  const int b = row / H, h = row % H;
+  const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;   // first token of the chunk
+  const size_t hk = (size_t)H * KD, hv = (size_t)H * VD;
+  float* A = s.f;                 // [64][65]
+  float* X = s.f + kGC * 65;      // [64][65]
+
+  // ---- load the chunk ---------------------------------------------------------
+  g2s_tile<KD>(k + tok0 * hk + (size_t)h * KD, hk, s.k, LK);
+  g2s_tile<KD>(q + tok0 * hk + (size_t)h * KD, hk, s.q, LK);
+  g2s_tile<VD>(v + tok0 * hv + (size_t)h * VD, hv, s.v, LV);
+  if (w == 0) {
+    float x = g[(tok0 + lane) * H + h];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    s.gc[lane] = x;
+    gcum[(tok0 + lane) * H + h] = x;
+    s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
+  }
+  for (int e = tid; e < 7 * kGC; e += 256) {
+    const int t = e / 7, c = e % 7;
+    s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + c]);
+  }
+  __syncthreads();
+
+  // ---- K K^T (-> A, fp32) and Q K^T (-> tril, bf16): wave w owns rows t-tile w -----
+  {
+    floatx4 kk[4], qk[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) kk[nt] = qk[nt] = zero4();
+#pragma unroll
+    for (int c = 0; c < KD / 32; ++c) {
+      const bf16x8 ak = *(const bf16x8*)(s.k + (16 * w + ln) * LK + 32 * c + 8 * lq);
+      const bf16x8 aq = *(const bf16x8*)(s.q + (16 * w + ln) * LK + 32 * c + 8 * lq);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
+        kk[nt] = mfma16x16x32(ak, bk, kk[nt]);
+        qk[nt] = mfma16x16x32(aq, bk, qk[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * lq + i, sc = 16 * nt + ln;
+        A[t * 65 + sc] = sc < t ? s.beta[t] * kk[nt][i] : 0.f;
+        s.qk[t * kLd64 + sc] = (__bf16)(sc <= t ? qk[nt][i] : 0.f);
+      }
+  }
+  __syncthreads();
+
+  // ---- X = (I + A)^-1, fp32 ----------------------------------------------------
+  // diagonal 16 x 16 blocks: forward substitution, lane ln owns column ln
+  if (lq == 0) {
+    const int o = 16 * w;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = (i == ln) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc -= A[(o + i) * 65 + o + j] * x[j];
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) X[(o + i) * 65 + o + ln] = x[i];
+  }
+  __syncthreads();
+  // off-diagonal blocks by distance d: X_ij = -X_ii sum_{m=j}^{i-1} A_im X_mj
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    const int bj = w, bi = w + d;
+    if (bi < 4) {
+      float* t1 = s.t1[w];
+      // T1 = sum_m A[bi][m] X[m][bj]; lane: rows 4lq + ii, column ln
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int r = 4 * lq + ii;
+        float acc = 0.f;
+        for (int m = bj; m < bi; ++m)
+#pragma unroll
+          for (int x = 0; x < 16; ++x)
+            acc += A[(16 * bi + r) * 65 + 16 * m + x] * X[(16 * m + x) * 65 + 16 * bj + ln];
+        t1[r * 17 + ln] = acc;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int r = 4 * lq + ii;
+        float acc = 0.f;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) acc += X[(16 * bi + r) * 65 + 16 * bi + x] * t1[x * 17 + ln];
+        X[(16 * bi + r) * 65 + 16 * bj + ln] = -acc;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- Aw, Au (bf16) to LDS and to the outputs ----------------------------------------
+  for (int u = tid; u < kGC * 8; u += 256) {
+    const int t = u >> 3, s0 = 8 * (u & 7);
+    bf16x8 a, au;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int sc = s0 + j;
+      const float x = sc <= t ? X[t * 65 + sc] : 0.f;
+      a[j] = (__bf16)x;
+      au[j] = (__bf16)(sc <= t ? x * fexp(s.gc[t] - s.gc[sc]) : 0.f);
+    }
+    *(bf16x8*)(s.aw + t * kLd64 + s0) = a;
+    *(bf16x8*)(s.au + t * kLd64 + s0) = au;
+    *(bf16x8*)(aw_out + ((tok0 + t) * H + h) * kGC + s0) = a;
+    *(bf16x8*)(au_out + ((tok0 + t) * H + h) * kGC + s0) = au;
+  }
+  __syncthreads();
+
+  // X[t][s] (bf16 LDS) times (beta o Y)[s][n] (bf16 LDS, row-major [s][n]):
+  // wave w computes output rows t-tile w, N/16 column tiles, into the fp32 staging.
+  auto gemm_rows = [&](const __bf16* xa, const __bf16* yb, int ldb, int ntile, bool scale_beta) {
+    const bf16x8 a0 = *(const bf16x8*)(xa + (16 * w + ln) * kLd64 + 8 * lq);
+    const bf16x8 a1 = *(const bf16x8*)(xa + (16 * w + ln) * kLd64 + 32 + 8 * lq);
+    const floatx4 b0a = *(const floatx4*)(s.beta + 8 * lq), b0b = *(const floatx4*)(s.beta + 8 * lq + 4);
+    const floatx4 b1a = *(const floatx4*)(s.beta + 32 + 8 * lq),
+                  b1b = *(const floatx4*)(s.beta + 36 + 8 * lq);
+    for (int nt = 0; nt < ntile; ++nt) {
+      bf16x8 y0 = tr_frag(yb, ldb, 0, 16 * nt), y1 = tr_frag(yb, ldb, 32, 16 * nt);
+      if (scale_beta) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y0[j] = (__bf16)((float)y0[j] * b0a[j]);
+          y0[4 + j] = (__bf16)((float)y0[4 + j] * b0b[j]);
+          y1[j] = (__bf16)((float)y1[j] * b1a[j]);
+          y1[4 + j] = (__bf16)((float)y1[4 + j] * b1b[j]);
+        }
+      }
+      floatx4 acc = mfma16x16x32(a0, y0, zero4());
+      acc = mfma16x16x32(a1, y1, acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s.f[(16 * w + 4 * lq + i) * LF + 16 * nt + ln] = acc[i];
+    }
+  };
+
+  // ---- W = Aw (beta K) -> W (bf16 LDS), W_new = exp(Gc) W (output) ---------------
+  gemm_rows(s.aw, s.k, LK, KD / 16, true);
+  __syncthreads();
+  for (int u = tid; u < kGC * KD / 8; u += 256) {
+    const int t = u / (KD / 8), c0 = 8 * (u % (KD / 8));
+    const float eg = fexp(s.gc[t]);
+    bf16x8 wb, wnb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = s.f[t * LF + c0 + j];
+      wb[j] = (__bf16)x;
+      wnb[j] = (__bf16)(x * eg);
+    }
+    *(bf16x8*)(s.w + t * LK + c0) = wb;
+    *(bf16x8*)(wn + (tok0 + t) * hk + (size_t)h * KD + c0) = wnb;
+    // K_new = exp(Gc_last - Gc_t) K
+    const float ek = fexp(s.gc[kGC - 1] - s.gc[t]);
+    const bf16x8 kx = *(const bf16x8*)(s.k + t * LK + c0);
+    bf16x8 knb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) knb[j] = (__bf16)((float)kx[j] * ek);
+    *(bf16x8*)(kn + (tok0 + t) * hk + (size_t)h * KD + c0) = knb;
+  }
+  __syncthreads();
+
+  // ---- U = Au (beta V) (output) ------------------------------------------------------
+  gemm_rows(s.au, s.v, LV, VD / 16, true);
+  __syncthreads();
+  for (int u = tid; u < kGC * VD / 8; u += 256) {
+    const int t = u / (VD / 8), c0 = 8 * (u % (VD / 8));
+    bf16x8 ub;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ub[j] = (__bf16)s.f[t * LF + c0 + j];
+    *(bf16x8*)(un + (tok0 + t) * hv + (size_t)h * VD + c0) = ub;
+  }
+  __syncthreads();
+
+  // ---- q_new = exp(Gc) (Q - tril(Q K^T) W) (output) ---------------------------------
+  gemm_rows(s.qk, s.w, LK, KD / 16, false);
+  __syncthreads();
+  for (int u = tid; u < kGC * KD / 8; u += 256) {
+    const int t = u / (KD / 8), c0 = 8 * (u % (KD / 8));
+    const float eg = fexp(s.gc[t]);
+    const bf16x8 qx = *(const bf16x8*)(s.q + t * LK + c0);
+    bf16x8 qb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qb[j] = (__bf16)(eg * ((float)qx[j] - s.f[t * LF + c0 + j]));
+    *(bf16x8*)(qn + (tok0 + t) * hk + (size_t)h * KD + c0) = qb;
+  }
+  __syncthreads();
+
+  // ---- P = (tril(Q K^T) Aw) o gamma o beta_s o lambda[t, lev] (bf16 LDS) -----------
+  gemm_rows(s.qk, s.aw, kLd64, 4, false);
+  __syncthreads();
+  for (int u = tid; u < kGC * 8; u += 256) {
+    const int t = u >> 3, s0 = 8 * (u & 7);
+    bf16x8 pb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int sc = s0 + j;
+      float x = 0.f;
+      if (sc <= t)
+        x = s.f[t * LF + sc] * fexp(s.gc[t] - s.gc[sc]) * s.beta[sc] *
+            s.lam[intra_level(t, sc)][t];
+      pb[j] = (__bf16)x;
+    }
+    *(bf16x8*)(s.pm + t * kLd64 + s0) = pb;
+  }
+  __syncthreads();
+
+  // ---- o_intra = P V (fp32 output) ---------------------------------------------------
+  gemm_rows(s.pm, s.v, LV, VD / 16, false);
+  __syncthreads();
+  for (int u = tid; u < kGC * VD / 4; u += 256) {
+    const int t = u / (VD / 4), c0 = 4 * (u % (VD / 4));
+    *(floatx4*)(oi + (tok0 + t) * hv + (size_t)h * VD + c0) = *(const floatx4*)(s.f + t * LF + c0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// level scan
+// ---------------------------------------------------------------------------
+template <int KD>
+struct GdnScanSmem {
+  static constexpr int LK = KD + 8;
+  __bf16 qn[kGC * LK];
+  __bf16 wn[kGC * LK];
+  __bf16 kn[kGC * LK];
+  __bf16 u[kGC * (kBVs + 8)];                 // U[t][v] slice
+  float lam[kGMaxLev][kGC];                   // lambda[t, 7 + e]
+  __bf16 hs[kGMaxLev][kBVs * LK];             // states, bf16 [v][k]
+  __bf16 vn[kGMaxLev][kBVs * kLd64];          // V_new, bf16 [v][t]
+};
+
+template <int KD, typename TL, typename TO>
+__global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
+    const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
+    const __bf16* __restrict__ un, const float* __restrict__ oi, const float* __restrict__ gcum,
+    const TL* __restrict__ l, TO* __restrict__ o, float* __restrict__ ht, int T, int H, int V,
+    int L, int nlev, int final_state) {
+  using Sm = GdnScanSmem<KD>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Sm& s = *(Sm*)smem_raw;
+  constexpr int LK = Sm::LK;
+  constexpr int LU = kBVs + 8;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int nvb = V / kBVs;
+  const int vb = blockIdx.x % nvb;
+  const int row = blockIdx.x / nvb;
+  const int b = row / H, h = row % H;
+  const int NT = T / kGC;
+  const size_t hk = (size_t)H * KD, hv = (size_t)H * V;
+  const int v0 = vb * kBVs;
+
+  // states: wave w owns rows k = RW w + 16m + 4lq + i (RW = K / 4 rows, MT = RW / 16
+  // tiles), columns v = 16n + ln
+  constexpr int MT = KD / 64, RW = KD / 4;
+  floatx4 st[kGMaxLev][MT][2];
+#pragma unroll
+  for (int e = 0; e < kGMaxLev; ++e)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) st[e][m][n] = zero4();
+
+  for (int ic = 0; ic < NT; ++ic) {
+    const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
+    g2s_tile<KD>(qn + tok0 * hk + (size_t)h * KD, hk, s.qn, LK);
+    g2s_tile<KD>(wn + tok0 * hk + (size_t)h * KD, hk, s.wn, LK);
+    g2s_tile<KD>(kn + tok0 * hk + (size_t)h * KD, hk, s.kn, LK);
+    g2s_tile<kBVs>(un + tok0 * hv + (size_t)h * V + v0, hv, s.u, LU);
+    for (int e2 = tid; e2 < nlev * kGC; e2 += 256) {
+      const int t = e2 / nlev, c = e2 % nlev;
+      s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + 7 + c]);
+    }
+    const float glast = gcum[(tok0 + kGC - 1) * H + h];
+    // states -> LDS, bf16 [v][k] (4 consecutive k per lane)
+#pragma unroll
+    for (int e = 0; e < kGMaxLev; ++e) {
+      if (e < nlev) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int n = 0; n < 2; ++n)
+            *(bf16x4*)(s.hs[e] + (16 * n + ln) * LK + RW * w + 16 * m + 4 * lq) = cvt4(st[e][m][n]);
+      }
+    }
+    __syncthreads();
+
+    // ---- reads (q_new h_e) and V_new_e = (write ? U : 0) - (reset ? 0 : W_new h_e) ----
+    const bool last = ic == NT - 1;
+    floatx4 acc[2] = {zero4(), zero4()};
+    {
+      bf16x8 aw[KD / 32], aq[KD / 32];
+#pragma unroll
+      for (int c = 0; c < KD / 32; ++c) {
+        aw[c] = *(const bf16x8*)(s.wn + (16 * w + ln) * LK + 32 * c + 8 * lq);
+        aq[c] = *(const bf16x8*)(s.qn + (16 * w + ln) * LK + 32 * c + 8 * lq);
+      }
+#pragma unroll
+      for (int e = 0; e < kGMaxLev; ++e) {
+        if (e < nlev) {
+          const int per = 2 << e;
+          const bool rd = (ic >> e) & 1;
+          const bool wr = !rd;
+          const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
+#pragma unroll
+          for (int n = 0; n < 2; ++n) {
+            floatx4 y = zero4(), z = zero4();
+#pragma unroll
+            for (int c = 0; c < KD / 32; ++c) {
+              const bf16x8 bh = *(const bf16x8*)(s.hs[e] + (16 * n + ln) * LK + 32 * c + 8 * lq);
+              if (!reset) y = mfma16x16x32(aw[c], bh, y);
+              if (rd) z = mfma16x16x32(aq[c], bh, z);
+            }
+            bf16x4 vb4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int t = 16 * w + 4 * lq + i;
+              if (rd) acc[n][i] += s.lam[e][t] * z[i];
+              const float uu = wr ? (float)s.u[t * LU + 16 * n + ln] : 0.f;
+              vb4[i] = (__bf16)(uu - y[i]);
+            }
+            *(bf16x4*)(s.vn[e] + (16 * n + ln) * kLd64 + 16 * w + 4 * lq) = vb4;
+          }
+        }
+      }
+    }
+    // ---- o = o_intra + reads ----------------------------------------------------------
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t idx = (tok0 + 16 * w + 4 * lq + i) * hv + (size_t)h * V + v0 + 16 * n + ln;
+        o[idx] = from_f32<TO>(oi[idx] + acc[n][i]);
+      }
+    __syncthreads();
+
+    // ---- h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new_e -----------------------
+    {
+      bf16x8 ak[MT][2];
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) ak[m][c] = tr_frag(s.kn, LK, 32 * c, RW * w + 16 * m);
+      const float gl = fexp(glast);
+#pragma unroll
+      for (int e = 0; e < kGMaxLev; ++e) {
+        if (e < nlev) {
+          const int per = 2 << e;
+          const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
+#pragma unroll
+          for (int n = 0; n < 2; ++n) {
+            const bf16x8 b0 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 8 * lq);
+            const bf16x8 b1 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 32 + 8 * lq);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+              floatx4 x = st[e][m][n];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x[i] = reset ? 0.f : x[i] * gl;
+              x = mfma16x16x32(ak[m][0], b0, x);
+              x = mfma16x16x32(ak[m][1], b1, x);
+              st[e][m][n] = x;
+            }
+          }
+        }
+      }
+    }
+    if (last && final_state && ht != nullptr) {
+      // ht[b, h, k, v, 7 + e] (chunkwise_hgdn.py:786-787)
+#pragma unroll
+      for (int e = 0; e < kGMaxLev; ++e)
+        if (e < nlev)
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int kk = RW * w + 16 * m + 4 * lq + i, vv = v0 + 16 * n + ln;
+                ht[((((size_t)b * H + h) * KD + kk) * V + vv) * L + 7 + e] = st[e][m][n][i];
+              }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launcher
+// ---------------------------------------------------------------------------
+struct GdnWs {
+  __bf16 *qn, *kn, *wn, *un;
+  float* oi;
+  size_t bytes;
+};
+
+inline size_t galign(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline GdnWs gdn_ws_layout(void* base, int B, int T, int H, int K, int V) {
+  GdnWs w;
+  char* p = (char*)base;
+  size_t off = 0;
+  const size_t n = (size_t)B * T * H;
+  w.qn = (__bf16*)(p + off); off += galign(n * K * 2);
+  w.kn = (__bf16*)(p + off); off += galign(n * K * 2);
+  w.wn = (__bf16*)(p + off); off += galign(n * K * 2);
+  w.un = (__bf16*)(p + off); off += galign(n * V * 2);
+  w.oi = (float*)(p + off);  off += galign(n * V * 4);
+  w.bytes = off;
+  return w;
+}
+
+template <int KD, int VD, typename TB, typename TL, typename TO>
+static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, const void* beta,
+                               const float* g, const void* l, void* o, float* gcum, void* aw,
+                               void* au, float* ht, void* ws, int B, int T, int H, int L,
+                               int nlev, hipStream_t stream) {
+  const GdnWs w = gdn_ws_layout(ws, B, T, H, KD, VD);
+  const int NT = T / kGC;
+  hipError_t e;
+  {
+    auto kp = gdn_prep_kernel<KD, VD, TB, TL>;
+    const int smem = (int)sizeof(GdnPrepSmem<KD, VD>);
+    if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 smem)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, (const TB*)beta, g, (const TL*)l, gcum,
+                       (__bf16*)aw, (__bf16*)au, w.qn, w.kn, w.wn, w.un, w.oi, T, H, L);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  {
+    auto ks = gdn_scan_kernel<KD, TL, TO>;
+    const int smem = (int)sizeof(GdnScanSmem<KD>);
+    if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 smem)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(256), smem, stream, w.qn, w.wn, w.kn,
+                       w.un, w.oi, gcum, (const TL*)l, (TO*)o, ht, T, H, VD, L, nlev,
+                       ht != nullptr ? 1 : 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace hattn
+
+size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V) {
+  return hattn::gdn_ws_layout(nullptr, B, T, H, K, V).bytes;
+}
+
+int hattn_gdn_fwd_max_levels() { return hattn::kGMaxLev; }
+
+hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, const void* beta,
+                                const float* g, const void* l, void* o, float* gcum, void* aw,
+                                void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
+                                int L, int nlev, int dt_b, int dt_l, int dt_o,
+                                hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+#define HATTN_GDN(KD_, VD_)                                                                     \
+  if (K == KD_ && V == VD_) {                                                                   \
+    if (dt_b == 0 && dt_l == 0 && dt_o == 0)                                                    \
+      return gdn_launch_t<KD_, VD_, __bf16, __bf16, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
+                                                            ht, ws, B, T, H, L, nlev, stream);  \
+    if (dt_b == 2 && dt_l == 2 && dt_o == 0)                                                    \
+      return gdn_launch_t<KD_, VD_, float, float, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
+                                                          ht, ws, B, T, H, L, nlev, stream);    \
+    if (dt_b == 0 && dt_l == 2 && dt_o == 0)                                                    \
+      return gdn_launch_t<KD_, VD_, __bf16, float, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
+                                                           ht, ws, B, T, H, L, nlev, stream);   \
+    if (dt_b == 2 && dt_l == 0 && dt_o == 0)                                                    \
+      return gdn_launch_t<KD_, VD_, float, __bf16, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
+                                                           ht, ws, B, T, H, L, nlev, stream);   \
+  }
+  HATTN_GDN(128, 128)
+  HATTN_GDN(64, 64)
+#undef HATTN_GDN
+  *unsupported = 1;
+  return hipSuccess;
+}

@@ -38,7 +38,8 @@ def input_guard(fn):
 
 
 def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """x / ||x||_2 over the last dim (fla.modules.l2norm.l2norm_fwd)."""
+    """x / sqrt(||x||^2 + eps) over the last dim in fp32, cast back to x.dtype
+    (fla.modules.l2norm.l2norm_fwd, used at kernel.py:20-23, 110-111)."""
     xf = x.float()
     return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)).to(x.dtype)
 

@@ -108,6 +108,16 @@ def bwd_flops(B, T, H, K, V):
     return B * H * (2 * T * 64 * (3 * K + 2 * V) + 6 * T * K * V + 2 * T * K * V * nlev)
 
 
+def gdn_fwd_flops(B, T, H, K, V):
+    """Algorithmic FLOPs of the GDN forward per (b, h) (KK^T, w, intra QK^T, the
+    two q_new products, u, A V, A Aw, the triangular solve, and nlev delta-rule
+    recurrences plus level reads)."""
+    BT = 64
+    nlev = math.ceil(math.log2(T // BT)) if T > BT else 0
+    return B * H * (2 * T * BT * (5 * K + 2 * V + BT) + (2 / 3) * BT * BT * T
+                    + 5 * T * K * V * nlev)
+
+
 def cpu_baseline(seconds_budget=30.0):
     """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
     chunkwise algorithm) on the host cores, on the north-star workload (median
@@ -239,6 +249,42 @@ def main():
                            "avg_step_us": ev_fb * 1e6,
                            "mfma_frac": (flops + bwd_flops(B, T, H, K, V)) / ev_fb
                            / MFMA_BF16_PEAK}}
+    # log-linear Gated DeltaNet forward at BASELINE config 3 (MFMA-bound path)
+    gdn = None
+    if not args.fwd_only:
+        from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd
+        GB, GT, GH, GK, GL = 4, 8192, 16, 128, 14
+        gq, gk, gv, gbeta, gg, gl = make_gdn_inputs(GB, GT, GH, GK, GK, GL, device=dev)
+
+        def gdn_step():
+            return gdn_fwd(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64, False)
+
+        for _ in range(max(1, args.warmup)):
+            gdn_step()
+        torch.cuda.synchronize()
+        ng = max(1, args.steps // 2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(ng):
+            gdn_step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall_g = (time.perf_counter() - t0) / ng
+        ev_g = e0.elapsed_time(e1) / 1e3 / ng
+        gfl = gdn_fwd_flops(GB, GT, GH, GK, GK)
+        gdn = {"value": GB * GT / wall_g, "unit": "tokens/s", "ms_per_step": wall_g * 1e3,
+               "steps": ng,
+               "config": {"workload": "log-linear Gated DeltaNet chunkwise forward "
+                                      "(chunkwise_hgdn.chunkwise_fwd, BASELINE config 3)",
+                          "batch": GB, "seq_len": GT, "heads": GH, "dk": GK, "dv": GK,
+                          "levels": GL},
+               "roofline": {"bound": "mfma", "achieved": gfl / ev_g / 1e12,
+                            "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                            "frac": gfl / ev_g / MFMA_BF16_PEAK, "algorithmic_flops": gfl,
+                            "avg_step_us": ev_g * 1e6}}
+        del gq, gk, gv, gbeta, gg, gl
+
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
         "value": value,
@@ -257,6 +303,7 @@ def main():
                    "batch": B, "seq_len": T, "heads": H, "dk": K, "dv": V, "levels": L,
                    "dtype_qkv_lambda": "bf16", "dtype_g": "fp32"},
         "fwd_bwd": fb,
+        "gdn_fwd": gdn,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,

@@ -177,3 +177,43 @@ __device__ __forceinline__ float sum_lq(float x) {
 }
 
 }  // namespace hattn
+
+namespace hattn {
+
+// bf16x3 products (Henry, Tang & Heinecke 2019, "Leveraging the bfloat16
+// artificial intelligence datatype for higher-precision computations"):
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi) carries about 16 mantissa
+// bits, and a.b = hi_a.hi_b + hi_a.lo_b + lo_a.hi_b up to the lo_a.lo_b term
+// (relative 2^-16), accumulated in fp32 by the MFMA.
+__device__ __forceinline__ __bf16 bf16_lo(float x, __bf16 hi) { return (__bf16)(x - (float)hi); }
+
+// Product of fragment planes: NP = 1 (plain bf16) or 2 (hi, lo); the small
+// terms are accumulated first.
+template <int NP>
+__device__ __forceinline__ floatx4 mma(const bf16x8* a, const bf16x8* b, floatx4 c) {
+  if constexpr (NP == 2) {
+    c = mfma16x16x32(a[1], b[0], c);
+    c = mfma16x16x32(a[0], b[1], c);
+  }
+  return mfma16x16x32(a[0], b[0], c);
+}
+
+// fp32 fragment (8 values) -> hi / lo planes.
+template <int NP>
+__device__ __forceinline__ void split8(const float* x, bf16x8* out) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const __bf16 h = (__bf16)x[j];
+    out[0][j] = h;
+    if constexpr (NP == 2) out[1][j] = bf16_lo(x[j], h);
+  }
+}
+
+// Two D-layout quads -> one B fragment (as cat8), split into NP planes.
+template <int NP>
+__device__ __forceinline__ void cat8s(floatx4 a, floatx4 b, bf16x8* out) {
+  const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  split8<NP>(x, out);
+}
+
+}  // namespace hattn

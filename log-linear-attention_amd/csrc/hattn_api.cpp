@@ -14,10 +14,11 @@
 
 hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, const float* g,
                                    const void* l, void* o, float* gcum, float* ht, void* ws,
-                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_v,
-                                   int dt_l, int dt_o, hipStream_t stream, int* unsupported);
-size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V);
-int hattn_mamba2_fwd_max_levels();
+                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_qk,
+                                   int dt_v, int dt_l, int dt_o, hipStream_t stream,
+                                   int* unsupported);
+size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3);
+int hattn_mamba2_fwd_max_levels(int x3);
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V);
 int hattn_gdn_fwd_max_levels();
 hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, const void* beta,
@@ -74,7 +75,11 @@ size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, i
   (void)K;
   (void)L;
   if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0) return 0;
-  return hattn_mamba2_fwd_ws_bytes(B, T, H, V);
+  // the bf16 kernels cut the sequence into the most segments: their workspace
+  // also covers the fp32 (bf16x3) kernels
+  const size_t a = hattn_mamba2_fwd_ws_bytes(B, T, H, V, 0);
+  const size_t b = hattn_mamba2_fwd_ws_bytes(B, T, H, V, 1);
+  return a > b ? a : b;
 }
 
 int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
@@ -99,23 +104,25 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
   const int nlev = ceil_log2(NT);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
-  if (nlev > hattn_mamba2_fwd_max_levels())
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
-                hattn_mamba2_fwd_max_levels());
-  if (dtype_qk != HATTN_BF16)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 required)", dtype_qk);
+  if (dtype_qk != HATTN_BF16 && dtype_qk != HATTN_FP32)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 or fp32 required)", dtype_qk);
+  // fp32 q / k select the bf16x3 kernels (fp32-accurate products)
+  const int x3 = dtype_qk == HATTN_FP32;
+  if (nlev > hattn_mamba2_fwd_max_levels(x3))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d%s", T,
+                hattn_mamba2_fwd_max_levels(x3), x3 ? " in fp32" : "");
   if (!q || !k || !v || !g || !l || !o) return fail(HATTN_ERR_VALUE, "null tensor pointer");
-  const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, V);
+  const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, V, x3);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
   int unsupported = 0;
   hipError_t e = hattn_mamba2_fwd_launch(q, k, v, g, l, o, g_cumsum, ht, workspace, B, T, G, H,
-                                         V, L, nlev, dtype_v, dtype_l, dtype_o,
+                                         V, L, nlev, dtype_qk, dtype_v, dtype_l, dtype_o,
                                          (hipStream_t)stream, &unsupported);
   if (unsupported)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d o=%d", dtype_v, dtype_l,
-                dtype_o);
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k=%d v=%d l=%d o=%d%s", dtype_qk,
+                dtype_v, dtype_l, dtype_o, x3 ? " (fp32 q/k need fp32 v, lambda and o)" : "");
   return check_hip(e, "hattn_mamba2_chunkwise_fwd launch");
 }
 
@@ -148,9 +155,9 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
   const int nlev = ceil_log2(T / 64);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
-  if (nlev > hattn_mamba2_fwd_max_levels())
+  if (nlev > hattn_mamba2_fwd_max_levels(0))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
-                hattn_mamba2_fwd_max_levels());
+                hattn_mamba2_fwd_max_levels(0));
   if (dtype_qk != HATTN_BF16 || dtype_do != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 required)", dtype_qk,
                 dtype_do);

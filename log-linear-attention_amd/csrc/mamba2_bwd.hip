@@ -18,7 +18,7 @@
 //
 // Segments of S = 16 chunks as in the forward.  Inter-chunk level e is a
 // source for chunk j when bit e of j is clear and is read when it is set.
-//   * mamba2_seg_sum_kernel<GCUM>: forward summaries Sum(q), D_q (shared with
+//   * mamba2_seg_sum_kernel<.., GCUM, ..>: forward summaries Sum(q), D_q (shared with
 //     the forward).
 //   * mamba2_bwd_rsum_kernel: reverse summaries of the top levels,
 //     R_e(q) = sum_{t in q} lambda[t, 7 + e] exp(G_t - G_start(q)) q_t do_t^T.
@@ -867,7 +867,7 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   const BwdWs w = bwd_ws_layout(ws, B, T, H, V, nlev);
   hipError_t e;
   if (NSEG > 1) {
-    auto sk = mamba2_seg_sum_kernel<TV, true>;
+    auto sk = mamba2_seg_sum_kernel<__bf16, TV, true, 1>;
     hipLaunchKernelGGL(sk, dim3(rows * NSEG), dim3(256), 0, stream, (const __bf16*)k,
                        (const TV*)v, gc, w.sums, w.segd, T, H, H, V, NT, 1 << slog, NSEG, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;

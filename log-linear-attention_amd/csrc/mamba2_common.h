@@ -11,83 +11,67 @@ namespace hattn {
 
 constexpr int kBT = 64;       // chunk length (the reference's only chunk size)
 constexpr int kKD = 64;       // head dim of q / k
-constexpr int kMaxLoc = 4;    // local levels held in registers (S <= 16 chunks)
-constexpr int kMaxTop = 8;    // top levels (LDS-resident, T <= 64 * 2^12)
-constexpr int kMaxLU = 7 + kMaxLoc + kMaxTop;  // lambda columns read (levels 0 .. 6 + nlev)
+constexpr int kMaxLoc = 4;    // local levels held in registers, bf16 kernels (S <= 16 chunks)
+constexpr int kMaxLocX3 = 6;  // same, bf16x3 kernels (S <= 64 chunks: fewer LDS-resident top levels)
+constexpr int kMaxTop = 8;    // top levels (LDS-resident, T <= 64 * 2^12 in bf16 mode)
+constexpr int kMaxLU = 7 + kMaxLoc + kMaxTop;  // lambda columns read by the bf16 kernels
 constexpr int kLd = 72;       // LDS row stride (bf16) of 64-wide tiles
 
-// Chunks per segment: 16 (2^kMaxLoc), or the whole sequence when shorter.
-__host__ __device__ inline int seg_log2(int NT) {
+// Chunks per segment: 2^maxloc, or the whole sequence when shorter.
+__host__ __device__ inline int seg_log2(int NT, int maxloc = kMaxLoc) {
   int nlev = 0;
   while ((1 << nlev) < NT) ++nlev;
-  return nlev < kMaxLoc ? nlev : kMaxLoc;
+  return nlev < maxloc ? nlev : maxloc;
 }
 
 // ---------------------------------------------------------------------------
-// chunk staging shared by both kernels
+// chunk staging shared by the kernels
 // ---------------------------------------------------------------------------
-// Row-major 64 x 64 bf16 tile of a [.., T, heads, 64-block] tensor: 512 units
-// of 16 bytes, two per thread.
-__device__ __forceinline__ void load_tile_bf16(uint4 (&r)[2], const __bf16* __restrict__ base,
-                                               int row_stride) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int u = tid + 256 * rr;
-    r[rr] = *(const uint4*)(base + (u >> 3) * row_stride + 8 * (u & 7));
-  }
-}
-
-__device__ __forceinline__ void store_tile_bf16(const uint4 (&r)[2], __bf16* s) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int u = tid + 256 * rr;
-    *(uint4*)(s + (u >> 3) * kLd + 8 * (u & 7)) = r[rr];
-  }
-}
-
-template <typename TV>
-struct VTile {
-  static constexpr int N = sizeof(TV) == 2 ? 2 : 4;
+// Row-major 64 x 64 tile of a [.., T, heads, 64-block] tensor in 16-byte units,
+// 256 threads: bf16 512 units (row u >> 3, col 8 (u & 7)), fp32 1024 units
+// (row u >> 4, col 4 (u & 15)), unit u = tid + 256 r.
+template <typename T>
+struct Tile64 {
+  static constexpr int N = sizeof(T) == 2 ? 2 : 4;
+  static constexpr int RSTEP = sizeof(T) == 2 ? 32 : 16;   // rows between a thread's units
   uint4 r[N];
 };
 
-template <typename TV>
-__device__ __forceinline__ void load_vtile(VTile<TV>& t, const TV* __restrict__ base,
-                                           int row_stride) {
+template <typename T>
+__device__ __forceinline__ unsigned int tile64_voff(int row_stride_elems) {
   const int tid = threadIdx.x;
-  if constexpr (sizeof(TV) == 2) {
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int u = tid + 256 * rr;
-      t.r[rr] = *(const uint4*)(base + (u >> 3) * row_stride + 8 * (u & 7));
-    }
-  } else {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int u = tid + 256 * rr;
-      t.r[rr] = *(const uint4*)(base + (u >> 4) * row_stride + 4 * (u & 15));
-    }
-  }
+  if constexpr (sizeof(T) == 2) return ((tid >> 3) * row_stride_elems + 8 * (tid & 7)) * 2;
+  else return ((tid >> 4) * row_stride_elems + 4 * (tid & 15)) * 4;
 }
 
-template <typename TV>
-__device__ __forceinline__ void store_vtile(const VTile<TV>& t, __bf16* s) {
+template <typename T>
+__device__ __forceinline__ void load_tile64(Tile64<T>& t, rsrc_t rs, unsigned int voff,
+                                            unsigned int soff, int row_stride_elems) {
+#pragma unroll
+  for (int rr = 0; rr < Tile64<T>::N; ++rr)
+    t.r[rr] = buf_load16(rs, voff, soff + rr * Tile64<T>::RSTEP * row_stride_elems * sizeof(T));
+}
+
+// Store a staged tile as NP bf16 planes (plane 1: the bf16x3 low part of fp32 data).
+template <int NP, typename T>
+__device__ __forceinline__ void store_tile64(const Tile64<T>& t, __bf16* p0, __bf16* p1) {
   const int tid = threadIdx.x;
-  if constexpr (sizeof(TV) == 2) {
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int u = tid + 256 * rr;
-      *(uint4*)(s + (u >> 3) * kLd + 8 * (u & 7)) = t.r[rr];
-    }
-  } else {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int u = tid + 256 * rr;
+  for (int rr = 0; rr < Tile64<T>::N; ++rr) {
+    if constexpr (sizeof(T) == 2) {
+      const int off = ((tid >> 3) + 32 * rr) * kLd + 8 * (tid & 7);
+      *(uint4*)(p0 + off) = t.r[rr];
+    } else {
+      const int off = ((tid >> 4) + 16 * rr) * kLd + 4 * (tid & 15);
       const float* e = (const float*)&t.r[rr];
-      *(bf16x4*)(s + (u >> 4) * kLd + 4 * (u & 15)) = bf16x4{(__bf16)e[0], (__bf16)e[1],
-                                                             (__bf16)e[2], (__bf16)e[3]};
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hi[j] = (__bf16)e[j];
+        lo[j] = bf16_lo(e[j], hi[j]);
+      }
+      *(bf16x4*)(p0 + off) = hi;
+      if constexpr (NP == 2) *(bf16x4*)(p1 + off) = lo;
     }
   }
 }
@@ -108,22 +92,24 @@ __device__ __forceinline__ float chunk_cumsum(float x) {
 // Per-segment summaries Sum(q) and total log-decay D_q
 // ---------------------------------------------------------------------------
 // One workgroup per (row, segment, 64-column block of V).  Wave w owns summary
-// rows k = 16w .. 16w + 15, all 64 columns (4 MFMA tiles).
+// rows k = 16w .. 16w + 15, all 64 columns (4 MFMA tiles).  NP = 2 keeps the
+// bf16x3 low planes of fp32 k and v and multiplies with three MFMAs.
+template <int NP>
 struct SumSmem {
-  __bf16 k[2][kBT * kLd];
-  __bf16 v[2][kBT * kLd];
+  __bf16 k[2][NP][kBT * kLd];
+  __bf16 v[2][NP][kBT * kLd];
   float wt[2][kBT];   // exp(Gc_last - Gc_t)
   float cl[2];        // chunk total Gc_last
 };
 
 // GCUM: g already holds the chunk-local inclusive cumsum (the backward's input,
 // chunkwise.py:1286-1299) instead of per-step log-decays.
-template <typename TV, bool GCUM>
+template <typename TK, typename TV, bool GCUM, int NP>
 __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
-    const __bf16* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
+    const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
     float* __restrict__ sums, float* __restrict__ segd, int T, int G, int H, int V, int NT,
     int S, int NSEG, int nvb64) {
-  __shared__ __attribute__((aligned(16))) SumSmem sm;
+  __shared__ __attribute__((aligned(16))) SumSmem<NP> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int vblk = blockIdx.x % nvb64;
@@ -134,18 +120,10 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   const int nch = min(S, NT - c0);
   const int vcol0 = vblk * 64;
   const int kstr = G * kKD, vstr = H * V;
-  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * kstr * 2);
+  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * kstr * sizeof(TK));
   const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
   const rsrc_t rgg = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
-  const unsigned int vo_k = ((tid >> 3) * kstr + 8 * (tid & 7)) * 2;
-  unsigned int vo_v, so_v2;
-  if constexpr (sizeof(TV) == 2) {
-    vo_v = ((tid >> 3) * vstr + 8 * (tid & 7)) * 2;
-    so_v2 = 32 * vstr * 2;
-  } else {
-    vo_v = ((tid >> 4) * vstr + 4 * (tid & 15)) * 4;
-    so_v2 = 16 * vstr * 4;
-  }
+  const unsigned int vo_k = tile64_voff<TK>(kstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
 
   floatx4 acc[4];
@@ -153,23 +131,20 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   for (int n = 0; n < 4; ++n) acc[n] = zero4();
   float dsum = 0.f;
 
-  uint4 k0, k1;
-  VTile<TV> vr;
+  Tile64<TK> kr;
+  Tile64<TV> vr;
   float gr = 0.f;
 #define SEG_LOAD(jj)                                                                   \
   {                                                                                    \
     const unsigned int row0 = (unsigned int)(c0 + (jj)) * kBT;                         \
-    k0 = buf_load16(rk, vo_k, row0 * kstr * 2);                                        \
-    k1 = buf_load16(rk, vo_k, (row0 + 32) * kstr * 2);                                 \
-    _Pragma("unroll") for (int rr = 0; rr < VTile<TV>::N; ++rr)                        \
-        vr.r[rr] = buf_load16(rv, vo_v, row0 * vstr * sizeof(TV) + rr * so_v2);        \
+    load_tile64(kr, rk, vo_k, row0 * kstr * sizeof(TK), kstr);                         \
+    load_tile64(vr, rv, vo_v, row0 * vstr * sizeof(TV), vstr);                        \
     if (w == 0) gr = buf_load<float>(rgg, vo_g, row0 * H * 4);                         \
   }
 #define SEG_STORE(buf)                                                                 \
   {                                                                                    \
-    *(uint4*)(sm.k[buf] + (tid >> 3) * kLd + 8 * (tid & 7)) = k0;                      \
-    *(uint4*)(sm.k[buf] + ((tid >> 3) + 32) * kLd + 8 * (tid & 7)) = k1;               \
-    store_vtile(vr, sm.v[buf]);                                                        \
+    store_tile64<NP>(kr, sm.k[buf][0], sm.k[buf][NP - 1]);                             \
+    store_tile64<NP>(vr, sm.v[buf][0], sm.v[buf][NP - 1]);                             \
     if (w == 0) {                                                                      \
       const float x = GCUM ? gr : chunk_cumsum(gr);                                    \
       const float last = __shfl(x, 63, 64);                                            \
@@ -192,19 +167,27 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
       for (int i = 0; i < 4; ++i) acc[n][i] *= dl;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const bf16x8 a = tr_frag(sm.k[buf], kLd, 32 * c, 16 * w);   // K^T[k][t]
+      bf16x8 a[NP];   // K^T[k][t]
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl) a[pl] = tr_frag(sm.k[buf][pl], kLd, 32 * c, 16 * w);
       const floatx4 w0 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq]);
       const floatx4 w1 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq + 4]);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const bf16x8 vv = tr_frag(sm.v[buf], kLd, 32 * c, 16 * n);  // V[t][v]
-        bf16x8 bv;
+        float wv[8];   // w o V[t][v], fp32
+        {
+          const bf16x8 vh = tr_frag(sm.v[buf][0], kLd, 32 * c, 16 * n);
+          bf16x8 vl{};
+          if constexpr (NP == 2) vl = tr_frag(sm.v[buf][1], kLd, 32 * c, 16 * n);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          bv[jj] = (__bf16)((float)vv[jj] * w0[jj]);
-          bv[4 + jj] = (__bf16)((float)vv[4 + jj] * w1[jj]);
+          for (int jj = 0; jj < 8; ++jj) {
+            const float x = NP == 2 ? (float)vh[jj] + (float)vl[jj] : (float)vh[jj];
+            wv[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
+          }
         }
-        acc[n] = mfma16x16x32(a, bv, acc[n]);
+        bf16x8 bv[NP];
+        split8<NP>(wv, bv);
+        acc[n] = mma<NP>(a, bv, acc[n]);
       }
     }
     if (j + 1 < nch) {

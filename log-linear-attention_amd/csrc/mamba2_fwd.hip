@@ -42,33 +42,40 @@ namespace hattn {
 // ---------------------------------------------------------------------------
 // Kernel 2: main pass over one segment, one 64-wide block of V
 // ---------------------------------------------------------------------------
-// LDS: one chunk stage (single-buffered; the next chunk waits in registers),
-// the A tile, and the top-level states (bf16, [level][k][v]).
+// NP bf16 planes per operand: 1 (bf16 inputs, bf16 MFMA) or 2 (fp32 inputs as
+// bf16x3 hi / lo planes, three MFMAs per product).  MAXLOC local levels live in
+// registers.  LDS: one chunk stage (single-buffered; the next chunk waits in
+// registers), the A tile, and the top-level states ([level][plane][k][v]).
+template <int NP, int MAXLOC>
 struct Stage {
-  __bf16 q[kBT * kLd];
-  __bf16 k[kBT * kLd];
-  __bf16 v[kBT * kLd];
+  static constexpr int LU = 7 + MAXLOC + kMaxTop;  // lambda columns (levels 0 .. 6 + nlev)
+  __bf16 q[NP][kBT * kLd];
+  __bf16 k[NP][kBT * kLd];
+  __bf16 v[NP][kBT * kLd];
   float gc[kBT];            // chunk-local inclusive cumsum of g
   float wt[kBT];            // exp(Gc_last - Gc_t)
-  float lam[kMaxLU * kBT];  // lambda^T [level][t]; levels >= 7 pre-multiplied by exp(Gc_t)
+  float lam[LU * kBT];      // lambda^T [level][t]; levels >= 7 pre-multiplied by exp(Gc_t)
 };
 
+template <int NP, int MAXLOC>
 struct MainSmem {
-  Stage st;
-  __bf16 a[kBT * kLd];      // A[t][s] = (S o M)[t][s] of the current chunk, bf16
-  __bf16 top[1];            // [ntop][kKD][kLd] top-level states (dynamic size)
+  Stage<NP, MAXLOC> st;
+  __bf16 a[NP][kBT * kLd];  // A[t][s] = (S o M)[t][s] of the current chunk
+  __bf16 top[1];            // [ntop][NP][kKD][kLd] top-level states (dynamic size)
 };
 
+template <int NP, int MAXLOC>
 inline int main_smem_bytes(int ntop) {
-  return (int)offsetof(MainSmem, top) + ntop * kKD * kLd * 2;
+  using Smem = MainSmem<NP, MAXLOC>;
+  return (int)offsetof(Smem, top) + ntop * NP * kKD * kLd * 2;
 }
 
-template <typename TV, typename TL>
+template <typename TK, typename TV, typename TL, int LR>
 struct MainRegs {
-  uint4 q[2], k[2];
-  VTile<TV> v;
+  Tile64<TK> q, k;
+  Tile64<TV> v;
   float g;
-  TL lam[kMaxLU / 4 + 1];
+  TL lam[LR];
 };
 
 // Phase-1 tile schedule: the 10 causal 16x16 tiles (t-tile mt, s-tile j <= mt)
@@ -79,16 +86,19 @@ __device__ __forceinline__ int p1_tile(int w, int n) {
   return tab[w][n];
 }
 
-template <typename TV, typename TL, typename TO>
-__global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
+template <typename TK, typename TV, typename TL, typename TO, int NP, int MAXLOC>
+__global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
+    const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
     const float* __restrict__ segd, int B, int T, int G, int H, int V, int L, int nlev,
     int nvb64, int slog, int NSEG, int final_state) {
+  using Smem = MainSmem<NP, MAXLOC>;
+  constexpr int kPl = kKD * kLd;                         // one bf16 plane of a 64 x 64 tile
+  constexpr int kLR = (Stage<NP, MAXLOC>::LU + 3) / 4;   // lambda registers per thread
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-  MainSmem& sm = *(MainSmem*)smem_raw;
-  Stage& s = sm.st;
+  Smem& sm = *(Smem*)smem_raw;
+  Stage<NP, MAXLOC>& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const XcdMap xm = xcd_map(blockIdx.x, nvb64);
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
   const bool is_final_seg = final_state && ht != nullptr && p == NSEG - 1;
   float* htb = ht ? ht + ((size_t)b * H + h) * kKD * V * L : nullptr;
 
-  // ---- top levels: Htop_e(p) from the segment summaries -> LDS (bf16) ----------
+  // ---- top levels: Htop_e(p) from the segment summaries -> LDS -----------------
   if (ntop > 0) {
     const float* sp = sums + (size_t)row * NSEG * kKD * V + vc;
     const float* dp = segd + (size_t)row * NSEG;
@@ -135,11 +145,15 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
         dlog += dp[qs];
       }
       if (reads) {
-        __bf16* tp = sm.top + e2 * kKD * kLd + 16 * w + ln;
+        __bf16* tp = sm.top + e2 * NP * kPl + 16 * w + ln;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) tp[(16 * m + 4 * lq + i) * kLd] = (__bf16)hacc[m][i];
+          for (int i = 0; i < 4; ++i) {
+            const __bf16 hv = (__bf16)hacc[m][i];
+            tp[(16 * m + 4 * lq + i) * kLd] = hv;
+            if constexpr (NP == 2) tp[kPl + (16 * m + 4 * lq + i) * kLd] = bf16_lo(hacc[m][i], hv);
+          }
       }
       if (is_final_seg) {
         // final state (chunkwise.py:229-279): a level the last chunk reads holds
@@ -158,8 +172,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
   // Chunk j of the segment starts (c0 + j) * 64 rows into the row's span; that
   // offset is uniform (SGPR), the lane's part of each access pattern is fixed.
   const int qstr = G * kKD, vstr = H * V, lstr = H * L;
-  const rsrc_t rq = make_rsrc(q + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
-  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
+  const rsrc_t rq = make_rsrc(q + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * sizeof(TK));
+  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * sizeof(TK));
   const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
   const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
   const rsrc_t rl = make_rsrc(l + ((size_t)b * T * H + h) * L, (size_t)T * lstr * sizeof(TL));
@@ -167,35 +181,19 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
   const bool write_gcum = gcum != nullptr && vblk == 0;
   const rsrc_t rgc = make_rsrc(write_gcum ? (const void*)(gcum + (size_t)b * T * H + h) : (const void*)g,
                                write_gcum ? (size_t)T * H * 4 : 0);
-  // 16-byte units of a 64 x 64 tile: u = tid (+256): row u >> 3, col 8 (u & 7)
-  const unsigned int vo_qk = ((tid >> 3) * qstr + 8 * (tid & 7)) * 2;
-  const unsigned int so_qk2 = 32 * qstr * 2;                     // second unit: +32 rows
-  unsigned int vo_v, so_v2;
-  if constexpr (sizeof(TV) == 2) {
-    vo_v = ((tid >> 3) * vstr + 8 * (tid & 7)) * 2;
-    so_v2 = 32 * vstr * 2;
-  } else {
-    vo_v = ((tid >> 4) * vstr + 4 * (tid & 15)) * 4;                // 4 units, +16 rows each
-    so_v2 = 16 * vstr * 4;
-  }
+  const unsigned int vo_qk = tile64_voff<TK>(qstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
   // lambda tile: thread -> row tid >> 2, columns (tid & 3) + 4r
   const int lrow = tid >> 2, lcol = tid & 3;
   const unsigned int vo_l = (lrow * lstr + lcol) * sizeof(TL);
   const unsigned int vo_o = (4 * lq * vstr + 16 * w + ln) * sizeof(TO);
-  constexpr int kLR = kMaxLU / 4 + 1;
 
-  MainRegs<TV, TL> rg;
+  MainRegs<TK, TV, TL, kLR> rg;
   auto load = [&](int j) {  // j: chunk index within the segment
     const unsigned int row0 = (unsigned int)(c0 + j) * kBT;
-    const unsigned int so_qk = row0 * qstr * 2;
-    rg.q[0] = buf_load16(rq, vo_qk, so_qk);
-    rg.q[1] = buf_load16(rq, vo_qk, so_qk + so_qk2);
-    rg.k[0] = buf_load16(rk, vo_qk, so_qk);
-    rg.k[1] = buf_load16(rk, vo_qk, so_qk + so_qk2);
-    const unsigned int so_v = row0 * vstr * sizeof(TV);
-#pragma unroll
-    for (int rr = 0; rr < VTile<TV>::N; ++rr) rg.v.r[rr] = buf_load16(rv, vo_v, so_v + rr * so_v2);
+    load_tile64(rg.q, rq, vo_qk, row0 * qstr * sizeof(TK), qstr);
+    load_tile64(rg.k, rk, vo_qk, row0 * qstr * sizeof(TK), qstr);
+    load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
     rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
     const unsigned int so_l = row0 * lstr * sizeof(TL);
 #pragma unroll
@@ -203,9 +201,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
       if (lcol + 4 * r < lu) rg.lam[r] = buf_load<TL>(rl, vo_l, so_l + 4 * r * sizeof(TL));
   };
   auto store = [&](int j) {
-    store_tile_bf16(rg.q, s.q);
-    store_tile_bf16(rg.k, s.k);
-    store_vtile(rg.v, s.v);
+    store_tile64<NP>(rg.q, s.q[0], s.q[NP - 1]);
+    store_tile64<NP>(rg.k, s.k[0], s.k[NP - 1]);
+    store_tile64<NP>(rg.v, s.v[0], s.v[NP - 1]);
     const float x = chunk_cumsum(rg.g);   // every wave scans the chunk's g
     const float last = __shfl(x, 63, 64);
     if (w == 0) {
@@ -225,9 +223,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
     }
   };
 
-  floatx4 st[kMaxLoc][4];
+  floatx4 st[MAXLOC][4];
 #pragma unroll
-  for (int e = 0; e < kMaxLoc; ++e)
+  for (int e = 0; e < MAXLOC; ++e)
 #pragma unroll
     for (int m = 0; m < 4; ++m) st[e][m] = zero4();
 
@@ -246,14 +244,18 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
       const int code = p1_tile(w, n);
       const int mt = (code & 15) >> 2, jt = code & 3;
       const int t = 16 * mt + ln;
-      bf16x4 out = bf16x4{};
+      float out[4] = {0.f, 0.f, 0.f, 0.f};
       if (code < 16) {
         floatx4 acc = zero4();
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const bf16x8 a = *(const bf16x8*)(s.k + (16 * jt + ln) * kLd + 32 * c + 8 * lq);
-          const bf16x8 bq = *(const bf16x8*)(s.q + t * kLd + 32 * c + 8 * lq);
-          acc = mfma16x16x32(a, bq, acc);  // S^T[s = 16jt + 4lq + i][t]
+          bf16x8 a[NP], bq[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            a[pl] = *(const bf16x8*)(s.k[pl] + (16 * jt + ln) * kLd + 32 * c + 8 * lq);
+            bq[pl] = *(const bf16x8*)(s.q[pl] + t * kLd + 32 * c + 8 * lq);
+          }
+          acc = mma<NP>(a, bq, acc);  // S^T[s = 16jt + 4lq + i][t]
         }
         const float gct = s.gc[t];
         const floatx4 gs = *(const floatx4*)(s.gc + 16 * jt + 4 * lq);
@@ -261,31 +263,49 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
           // off-diagonal tile: level 4 + bit_length(mt ^ jt) for every pair
           const float lam = s.lam[(4 + intra_level(mt, jt)) * kBT + t];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) out[i] = (__bf16)(acc[i] * fexp(gct - gs[i]) * lam);
+          for (int i = 0; i < 4; ++i) out[i] = acc[i] * fexp(gct - gs[i]) * lam;
         } else {
           // diagonal tile: level bit_length(ln ^ (4lq + i)), causal s <= t
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int sl = 4 * lq + i;
             const float val = acc[i] * fexp(gct - gs[i]) * s.lam[intra_level(ln, sl) * kBT + t];
-            out[i] = (__bf16)(sl <= ln ? val : 0.f);
+            out[i] = sl <= ln ? val : 0.f;
           }
         }
       }
-      *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+      bf16x4 ohi, olo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ohi[i] = (__bf16)out[i];
+        if constexpr (NP == 2) olo[i] = bf16_lo(out[i], ohi[i]);
+      }
+      *(bf16x4*)(sm.a[0] + t * kLd + 16 * jt + 4 * lq) = ohi;
+      if constexpr (NP == 2) *(bf16x4*)(sm.a[1] + t * kLd + 16 * jt + 4 * lq) = olo;
     }
     __syncthreads();
 
     // ---- phase 2: o[all t][V columns 16w..] ------------------------------------
     floatx4 acc[4];
     {
-      const bf16x8 vf0 = tr_frag(s.v, kLd, 0, 16 * w);    // V[s][v], s = 0..31
-      const bf16x8 vf1 = tr_frag(s.v, kLd, 32, 16 * w);   // s = 32..63
+      bf16x8 vf0[NP], vf1[NP];   // V[s][v], s = 0..31 / 32..63
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl) {
+        vf0[pl] = tr_frag(s.v[pl], kLd, 0, 16 * w);
+        vf1[pl] = tr_frag(s.v[pl], kLd, 32, 16 * w);
+      }
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const __bf16* ar = sm.a + (16 * mt + ln) * kLd + 8 * lq;
-        acc[mt] = mfma16x16x32(*(const bf16x8*)ar, vf0, zero4());
-        if (mt >= 2) acc[mt] = mfma16x16x32(*(const bf16x8*)(ar + 32), vf1, acc[mt]);
+        bf16x8 af[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) af[pl] = *(const bf16x8*)(sm.a[pl] + (16 * mt + ln) * kLd + 8 * lq);
+        acc[mt] = mma<NP>(af, vf0, zero4());
+        if (mt >= 2) {
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl)
+            af[pl] = *(const bf16x8*)(sm.a[pl] + (16 * mt + ln) * kLd + 32 + 8 * lq);
+          acc[mt] = mma<NP>(af, vf1, acc[mt]);
+        }
       }
     }
     const bool any_loc = nloc > 0 && j > 0;
@@ -293,28 +313,32 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
     if (any_loc || any_top) {
       const float ee = fexp(Eseg);
       // Q fragments in the states' row order: k = 32c + 4lq + i, 32c + 16 + 4lq + i
-      bf16x8 qa[4][2];
+      bf16x8 qa[4][2][NP];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const __bf16* qp = s.q + (16 * mt + ln) * kLd + 32 * c + 4 * lq;
-          const bf16x4 lo = *(const bf16x4*)qp;
-          const bf16x4 hi = *(const bf16x4*)(qp + 16);
-          qa[mt][c] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            const __bf16* qp = s.q[pl] + (16 * mt + ln) * kLd + 32 * c + 4 * lq;
+            const bf16x4 lo = *(const bf16x4*)qp;
+            const bf16x4 hi = *(const bf16x4*)(qp + 16);
+            qa[mt][c][pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          }
       const float* lamt = s.lam + 4 * lq;
       // local levels without branches (a level the chunk does not read gets a
       // zero B operand), so the MFMA chains of all levels interleave
 #pragma unroll
-      for (int e = 0; e < kMaxLoc; ++e) {
+      for (int e = 0; e < MAXLOC; ++e) {
         const bool rd = any_loc && e < nloc && ((ic >> e) & 1);
         const float z = rd ? 1.f : 0.f;
-        const bf16x8 b0 = cat8(st[e][0] * z, st[e][1] * z), b1 = cat8(st[e][2] * z, st[e][3] * z);
+        bf16x8 b0[NP], b1[NP];
+        cat8s<NP>(st[e][0] * z, st[e][1] * z, b0);
+        cat8s<NP>(st[e][2] * z, st[e][3] * z, b1);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          floatx4 tmp = mfma16x16x32(qa[mt][0], b0, zero4());
-          tmp = mfma16x16x32(qa[mt][1], b1, tmp);
+          floatx4 tmp = mma<NP>(qa[mt][0], b0, zero4());
+          tmp = mma<NP>(qa[mt][1], b1, tmp);
           const floatx4 lam = *(const floatx4*)(lamt + (7 + e) * kBT + 16 * mt);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * lam[i];
@@ -323,12 +347,17 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
       if (any_top) {
         for (int e2 = 0; e2 < ntop; ++e2) {
           if ((p >> e2) & 1) {
-            const __bf16* tp = sm.top + e2 * kKD * kLd;
-            const bf16x8 b0 = tr_frag_d(tp, kLd, 0, 16 * w), b1 = tr_frag_d(tp, kLd, 32, 16 * w);
+            const __bf16* tp = sm.top + e2 * NP * kPl;
+            bf16x8 b0[NP], b1[NP];
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl) {
+              b0[pl] = tr_frag_d(tp + pl * kPl, kLd, 0, 16 * w);
+              b1[pl] = tr_frag_d(tp + pl * kPl, kLd, 32, 16 * w);
+            }
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
-              floatx4 tmp = mfma16x16x32(qa[mt][0], b0, zero4());
-              tmp = mfma16x16x32(qa[mt][1], b1, tmp);
+              floatx4 tmp = mma<NP>(qa[mt][0], b0, zero4());
+              tmp = mma<NP>(qa[mt][1], b1, tmp);
               const floatx4 lam = *(const floatx4*)(lamt + (7 + nloc + e2) * kBT + 16 * mt);
 #pragma unroll
               for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * (lam[i] * ee);
@@ -351,25 +380,39 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
       const floatx4 w0b = *(const floatx4*)(s.wt + 8 * lq + 4);
       const floatx4 w1a = *(const floatx4*)(s.wt + 32 + 8 * lq);
       const floatx4 w1b = *(const floatx4*)(s.wt + 32 + 8 * lq + 4);
-      const bf16x8 vf0 = tr_frag(s.v, kLd, 0, 16 * w), vf1 = tr_frag(s.v, kLd, 32, 16 * w);
-      bf16x8 wv0, wv1;
+      // (w o V)[s][v] for s = 0..31 / 32..63
+      const bf16x8 vh0 = tr_frag(s.v[0], kLd, 0, 16 * w), vh1 = tr_frag(s.v[0], kLd, 32, 16 * w);
+      bf16x8 vl0{}, vl1{};
+      if constexpr (NP == 2) {
+        vl0 = tr_frag(s.v[1], kLd, 0, 16 * w);
+        vl1 = tr_frag(s.v[1], kLd, 32, 16 * w);
+      }
+      float x0[8], x1[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        wv0[i] = (__bf16)((float)vf0[i] * w0a[i]);
-        wv0[4 + i] = (__bf16)((float)vf0[4 + i] * w0b[i]);
-        wv1[i] = (__bf16)((float)vf1[i] * w1a[i]);
-        wv1[4 + i] = (__bf16)((float)vf1[4 + i] * w1b[i]);
+        x0[i] = ((float)vh0[i] + (float)vl0[i]) * w0a[i];
+        x0[4 + i] = ((float)vh0[4 + i] + (float)vl0[4 + i]) * w0b[i];
+        x1[i] = ((float)vh1[i] + (float)vl1[i]) * w1a[i];
+        x1[4 + i] = ((float)vh1[4 + i] + (float)vl1[4 + i]) * w1b[i];
       }
+      bf16x8 wv0[NP], wv1[NP];
+      split8<NP>(x0, wv0);
+      split8<NP>(x1, wv1);
       floatx4 kv[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        kv[m] = mfma16x16x32(tr_frag(s.k, kLd, 0, 16 * m), wv0, zero4());
-        kv[m] = mfma16x16x32(tr_frag(s.k, kLd, 32, 16 * m), wv1, kv[m]);
+        bf16x8 kf[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) kf[pl] = tr_frag(s.k[pl], kLd, 0, 16 * m);
+        kv[m] = mma<NP>(kf, wv0, zero4());
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) kf[pl] = tr_frag(s.k[pl], kLd, 32, 16 * m);
+        kv[m] = mma<NP>(kf, wv1, kv[m]);
       }
       const float gl = fexp(glr);
       const bool last = (ic == NT - 1);
 #pragma unroll
-      for (int e = 0; e < kMaxLoc; ++e) {
+      for (int e = 0; e < MAXLOC; ++e) {
         if (e < nloc) {
           const int per = 2 << e;
           const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
@@ -391,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_main_kernel(
       if (last && is_final_seg) {
         // ht[b, h, k, v, 7 + e] (chunkwise.py:1179, 277-279)
 #pragma unroll
-        for (int e = 0; e < kMaxLoc; ++e)
+        for (int e = 0; e < MAXLOC; ++e)
           if (e < nloc)
 #pragma unroll
             for (int m = 0; m < 4; ++m)
@@ -414,28 +457,38 @@ namespace {
 size_t segd_bytes(size_t rows, int NSEG) {
   return (rows * NSEG * sizeof(float) + 255) & ~(size_t)255;
 }
+int max_loc(int x3) { return x3 ? hattn::kMaxLocX3 : hattn::kMaxLoc; }
 }  // namespace
 
-size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V) {
+// x3: fp32 q / k / v / lambda computed as bf16x3 (more local levels per segment).
+size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3) {
   const int NT = T / hattn::kBT;
-  const int slog = hattn::seg_log2(NT);
+  const int slog = hattn::seg_log2(NT, max_loc(x3));
   const int NSEG = (NT + (1 << slog) - 1) >> slog;
   if (NSEG <= 1) return 0;
   const size_t rows = (size_t)B * H;
   return segd_bytes(rows, NSEG) + rows * NSEG * hattn::kKD * V * sizeof(float);
 }
 
-// Largest inter-chunk level count the register-resident states support.
-int hattn_mamba2_fwd_max_levels() { return hattn::kMaxLoc + hattn::kMaxTop; }
+// Largest inter-chunk level count: register-resident local levels plus the
+// top levels whose states fit in LDS.
+int hattn_mamba2_fwd_max_levels(int x3) {
+  using namespace hattn;
+  if (!x3) return kMaxLoc + kMaxTop;
+  constexpr int kLdsBytes = 160 * 1024;
+  const int base = main_smem_bytes<2, kMaxLocX3>(0), per = main_smem_bytes<2, kMaxLocX3>(1) - base;
+  const int ntop = (kLdsBytes - base) / per;
+  return kMaxLocX3 + (ntop < kMaxTop ? ntop : kMaxTop);
+}
 
 namespace hattn {
 
-template <typename TV, typename TL, typename TO>
+template <typename TK, typename TV, typename TL, typename TO, int NP, int MAXLOC>
 static hipError_t launch_t(const void* q, const void* k, const void* v, const float* g,
                            const void* l, void* o, float* gcum, float* ht, void* ws, int B,
                            int T, int G, int H, int V, int L, int nlev, hipStream_t stream) {
   const int NT = T / kBT;
-  const int slog = seg_log2(NT);
+  const int slog = seg_log2(NT, MAXLOC);
   const int S = 1 << slog;
   const int NSEG = (NT + S - 1) / S;
   const int rows = B * H;
@@ -445,40 +498,54 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
   if (NSEG > 1) {
     segd = (float*)ws;
     sums = (float*)((char*)ws + segd_bytes(rows, NSEG));
-    auto sk = mamba2_seg_sum_kernel<TV, false>;
-    hipLaunchKernelGGL(sk, dim3(rows * NSEG * nvb64), dim3(256), 0, stream, (const __bf16*)k, (const TV*)v, g, sums, segd, T, G, H, V, NT, S,
-                       NSEG, nvb64);
+    auto sk = mamba2_seg_sum_kernel<TK, TV, false, NP>;
+    hipLaunchKernelGGL(sk, dim3(rows * NSEG * nvb64), dim3(256), 0, stream, (const TK*)k,
+                       (const TV*)v, g, sums, segd, T, G, H, V, NT, S, NSEG, nvb64);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const int smem = main_smem_bytes(nlev - min(slog, nlev));
+  const int smem = main_smem_bytes<NP, MAXLOC>(nlev - min(slog, nlev));
   const int rows8 = (rows * NSEG + 7) / 8;
   const int grid = rows8 * 8 * nvb64;
-  auto kern = mamba2_fwd_main_kernel<TV, TL, TO>;
+  auto kern = mamba2_fwd_main_kernel<TK, TV, TL, TO, NP, MAXLOC>;
   hipError_t e =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const __bf16*)q,
-                     (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, sums,
-                     segd, B, T, G, H, V, L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const TK*)q, (const TK*)k,
+                     (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, sums, segd, B, T, G, H, V,
+                     L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
   return hipGetLastError();
 }
 
 }  // namespace hattn
 
+// dt_qk == DT_FP32 selects the bf16x3 kernels, which take fp32 q, k, v, lambda
+// and write fp32 o.
 hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, const float* g,
                                    const void* l, void* o, float* gcum, float* ht, void* ws,
-                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_v,
-                                   int dt_l, int dt_o, hipStream_t stream, int* unsupported) {
+                                   int B, int T, int G, int H, int V, int L, int nlev, int dt_qk,
+                                   int dt_v, int dt_l, int dt_o, hipStream_t stream,
+                                   int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
+  if (dt_qk == DT_FP32) {
+    if (dt_v == DT_FP32 && dt_l == DT_FP32 && dt_o == DT_FP32)
+      return launch_t<float, float, float, float, 2, kMaxLocX3>(q, k, v, g, l, o, gcum, ht, ws,
+                                                                B, T, G, H, V, L, nlev, stream);
+    *unsupported = 1;
+    return hipSuccess;
+  }
+  if (dt_qk != DT_BF16) {
+    *unsupported = 1;
+    return hipSuccess;
+  }
 #define HATTN_DISPATCH_O(TV_, TL_)                                                             \
   if (dt_o == DT_BF16)                                                                       \
-    return launch_t<TV_, TL_, __bf16>(q, k, v, g, l, o, gcum, ht, ws, B, T, G, H, V, L, nlev, \
-                                      stream);                                                \
+    return launch_t<__bf16, TV_, TL_, __bf16, 1, kMaxLoc>(q, k, v, g, l, o, gcum, ht, ws, B, T, \
+                                                          G, H, V, L, nlev, stream);           \
   if (dt_o == DT_FP32)                                                                       \
-    return launch_t<TV_, TL_, float>(q, k, v, g, l, o, gcum, ht, ws, B, T, G, H, V, L, nlev,  \
-                                     stream);
+    return launch_t<__bf16, TV_, TL_, float, 1, kMaxLoc>(q, k, v, g, l, o, gcum, ht, ws, B, T,  \
+                                                         G, H, V, L, nlev, stream);
   if (dt_v == DT_BF16 && dt_l == DT_BF16) { HATTN_DISPATCH_O(__bf16, __bf16) }
   if (dt_v == DT_BF16 && dt_l == DT_FP32) { HATTN_DISPATCH_O(__bf16, float) }
   if (dt_v == DT_FP32 && dt_l == DT_BF16) { HATTN_DISPATCH_O(float, __bf16) }

@@ -77,6 +77,10 @@ def chunkwise_fwd(
 ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """Log-linear Mamba-2 forward (chunkwise.py:1118-1275).
 
+    bf16 q / k multiply on bf16 MFMA; fp32 q / k select the bf16x3 kernels
+    (each product as three bf16 MFMAs over hi / lo splits, fp32-accurate), the
+    counterpart of the reference's fp32 dots.
+
     Returns ``o`` [B,T,H,V] in v.dtype, the chunk-local inclusive cumsum of g
     [B,T,H] fp32 and, if ``output_final_state``, ``ht`` [B,H,K,V,L] fp32 holding
     the inter-chunk level states at levels 7 .. 6 + ceil(log2(T/64)) (other
@@ -92,6 +96,11 @@ def chunkwise_fwd(
     dev = _lib.require_device(q, k, v, g, l)
     if q.dtype != k.dtype:
         raise ValueError("q and k must share a dtype")
+    out_dtype = v.dtype
+    if q.dtype == torch.float32:
+        # fp32 q / k run the bf16x3 (fp32-accurate) kernels, which read fp32 v
+        # and lambda and write fp32 o
+        v, l = v.float().contiguous(), l.float().contiguous()
     o = torch.empty(v.shape, dtype=v.dtype, device=dev)
     g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
     ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
@@ -104,6 +113,8 @@ def chunkwise_fwd(
         _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
         level_base, htype.value, chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
     _lib.check(st)
+    if o.dtype != out_dtype:
+        o = o.to(out_dtype)
     return o, g_cumsum, ht
 
 

@@ -86,7 +86,9 @@ def _fwd(**kw):
     (dict(base=3), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(K=128), _lib.HATTN_ERR_NOT_IMPLEMENTED),
-    (dict(dq=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp32 q/k is the bf16x3 entry point's
+    (dict(dq=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp16 q/k
+    (dict(dq=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp32 q/k (bf16x3) with bf16 v, lambda, o
+    (dict(dq=2, dv=2, dl=2, do=2, T=64 << 11, L=20), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > fp32 levels
 ])
 def test_fwd_argument_checks(kw, code):
     assert _fwd(**kw) == code

@@ -156,6 +156,40 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
  * allocates these with torch inside chunkwise_fwd (chunkwise_hgdn.py:636-642). */
 size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int L);
 
+/*
+ * Log-linear Gated DeltaNet chunkwise backward.
+ *
+ * Replaces hattention/chunkwise_hgdn.py:791-1222 `chunkwise_bwd(q, k, v, b, g, l,
+ * Aw, Au, do, head_first, level_base, htype, chunk_size) -> (dq, dk, dv, db, dg, dl)`,
+ * called by HAttentionFunction.backward for HStruct.GDELTA (kernel.py:201-225)
+ * with the same normalised q, k as the forward.  Per head:
+ *
+ *   q, k [B, T, H, K] bf16   v, do [B, T, H, V] bf16   beta [B, T, H] in dtype_beta
+ *   g_cumsum [B, T, H] fp32 (the forward's chunk-local cumsum)   l [B, T, H, L] in dtype_l
+ *   Aw, Au: the forward's outputs; accepted for the reference's signature and not
+ *           read (the kernels recompute (I + A)^-1 in fp32)
+ *   dq, dk [B, T, H, K] bf16   dv [B, T, H, V] bf16   db [B, T, H] in dtype_beta
+ *   dg [B, T, H] fp32 (w.r.t. the per-step g: reverse chunk-local cumsum applied,
+ *   chunkwise_hgdn.py:1219)   dl [B, T, H, L] fp32
+ *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
+ *
+ * Constraints as hattn_gdn_chunkwise_fwd; do bf16 -> else HATTN_ERR_NOT_IMPLEMENTED.
+ */
+int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,
+                            const float* g_cumsum, const void* l, const void* Aw, const void* Au,
+                            const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
+                            float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
+                            int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
+                            int chunk_size, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* Workspace bytes of hattn_gdn_chunkwise_bwd: the recomputed q_new, k_new, w_new,
+ * u (bf16), every level's state at every chunk start (bf16), and the fp32
+ * per-V-slice partial gradients of the level scan.  No counterpart in the
+ * reference, which allocates h / dh and its temporaries with torch inside
+ * chunkwise_bwd (chunkwise_hgdn.py:894-913). */
+size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,967 @@
+// Log-linear Gated DeltaNet chunkwise backward for gfx950.
+//
+// Replaces chunkwise_hgdn.chunkwise_bwd (chunkwise_hgdn.py:791-1222): the
+// reference runs two intra-chunk kernels, then per inter-chunk level a state
+// recompute, the delta-rule dh scan, torch products and three gradient kernels,
+// then the WY / UT-transform backward (fla_future/wy_fast.py:15-132).
+//
+// Forward quantities of one chunk (C = 64 tokens, chunk-local cumsum Gc,
+// e = exp(Gc), r = exp(Gc_last - Gc), Gamma[t,s] = exp(Gc_t - Gc_s) for s <= t):
+//   A = strict-tril(diag(beta) K K^T), Aw = (I + A)^-1, M = tril(Q K^T),
+//   P = M Aw, W = Aw diag(beta) K, U = (Aw o Gamma) diag(beta) V,
+//   q_new = e o (Q - M W), W_new = e o W, K_new = r o K,
+//   o_intra = (P o Gamma o Lambda o beta_s) V,
+// and per level e, over the chunks c:
+//   o_c += lambda_e o (q_new_c h_c),
+//   V_new_c = wr U_c - nr W_new_c h_c,
+//   h_{c+1} = nr exp(Gc_last) h_c + K_new_c^T V_new_c
+// (rd / wr: bit e of c set / clear; nr: c is not the last chunk of an aligned
+// 2^(e+1) block).
+//
+// Four launches:
+//   1. prep recompute (gdn_fwd.hip, from g_cumsum): q_new, K_new, W_new, U;
+//   2. forward scan recompute: every level's state at every chunk start, bf16;
+//   3. gdn_bwd_scan_kernel, one workgroup per (row, 32 columns of V), walks the
+//      chunks backwards with every level's dh [K x 32] in fp32 registers:
+//        dV_new = K_new dh_{c+1},   dU += wr dV_new,
+//        dq_new += rd lambda_e o (dO h_c^T),  dlambda_e = rd rowsum(dO o q_new h_c),
+//        dW_new -= nr dV_new h_c^T,  dK_new += V_new dh_{c+1}^T,
+//        d exp(Gc_last) += nr <h_c, dh_{c+1}>,
+//        dh_c = nr (exp(Gc_last) dh_{c+1} - W_new^T dV_new) + rd q_new^T (lambda_e o dO);
+//      the contractions over V give per-slice partials, summed by kernel 4;
+//   4. gdn_bwd_chunk_kernel, one workgroup per chunk, backpropagates through
+//      the chunk-local algebra.  With X = e o dq_new and E = dP - (X K^T) o beta_s,
+//        dM = tril(E Aw^T),  dAw = M^T E + ((e o dW_new) K^T + (dU V^T) o Gamma) o beta_s,
+//        dA = -strict-tril(Aw^T dAw Aw^T),
+//        dQ = X + dM K,
+//        dK = dM^T Q + dA^T (beta o K) + beta o (-P^T X + Aw^T (e o dW_new) + dA K) + r o dK_new,
+//        dV = beta o (Au^T dU + (P o Gamma o Lambda)^T dO),
+//      dbeta from the same row products, dGc from every e / r / Gamma factor, then
+//      dg = reverse chunk-local cumsum of dGc (chunkwise_hgdn.py:1219).  The
+//      64 x 64 products with fp32 operands run as bf16x3 (three MFMAs); the
+//      inverse is recomputed in fp32, so the Aw / Au of the forward are not read.
+#include "gdn_common.h"
+
+hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* v,
+                                      const void* beta, const float* gcum, const void* l,
+                                      __bf16* qn, __bf16* kn, __bf16* wn, __bf16* un,
+                                      __bf16* hsave, int B, int T, int H, int K, int V, int L,
+                                      int nlev, int dt_b, int dt_l, hipStream_t stream,
+                                      int* unsupported);
+
+namespace hattn {
+
+__device__ __forceinline__ float rsum16(float x) {
+  x += __shfl_xor(x, 1, 64);
+  x += __shfl_xor(x, 2, 64);
+  x += __shfl_xor(x, 4, 64);
+  x += __shfl_xor(x, 8, 64);
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 3: reverse level scan
+// ---------------------------------------------------------------------------
+template <int KD>
+struct GdnBscanSmem {
+  static constexpr int LK = KD + 8, LVS = kBVs + 8;
+  __bf16 qn[kGC * LK];
+  __bf16 wn[kGC * LK];
+  __bf16 kn[kGC * LK];
+  __bf16 u[kGC * LVS];       // U[t][v] slice
+  __bf16 dO[kGC * LVS];      // dO[t][v] slice
+  __bf16 hs[kBVs * LK];      // h_e at the chunk start, [v][k]
+  __bf16 dhs[kBVs * LK];     // dh_e after the chunk, [v][k]
+  __bf16 dvn[kBVs * kLd64];  // dV_new_e, [v][t]
+  __bf16 vn[kBVs * kLd64];   // V_new_e, [v][t]
+  float lam[kGMaxLev][kGC];  // lambda[t, 7 + e]
+  float dlr[2][kGC];         // dlambda row sums of the two 16-column halves
+  float red[8];
+};
+
+// 8 waves.  Wave w owns: dh tiles (k-tile, v-tile) = ((w TPW + j) >> 1, (w TPW + j) & 1),
+// TPW = K / 64; the [64 x 32] products of step (i) at (t-tile w & 3, v-tile w >> 2);
+// the [64 x K] accumulators at t-tile w & 3, k-tiles (w >> 2) APW + j, APW = K / 32.
+template <int KD, typename TL>
+__global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
+    const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
+    const __bf16* __restrict__ un, const __bf16* __restrict__ dO, const float* __restrict__ gcum,
+    const TL* __restrict__ l, const __bf16* __restrict__ hsave, float* __restrict__ dq_p,
+    float* __restrict__ dw_p, float* __restrict__ dk_p, float* __restrict__ du,
+    float* __restrict__ dl_p, float* __restrict__ del_p, int B, int T, int H, int V, int L,
+    int nlev) {
+  using Sm = GdnBscanSmem<KD>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Sm& s = *(Sm*)smem_raw;
+  constexpr int LK = Sm::LK, LVS = Sm::LVS, TPW = KD / 64, APW = KD / 32;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int tt = w & 3, vt = w >> 2;       // step (i) tile; tt is also the accumulators' t-tile
+  const int nvb = V / kBVs;
+  const int vb = blockIdx.x % nvb;
+  const int row = blockIdx.x / nvb;
+  const int b = row / H, h = row % H;
+  const int NT = T / kGC;
+  const size_t hk = (size_t)H * KD, hv = (size_t)H * V;
+  const size_t BTH = (size_t)B * T * H;
+  const int v0 = vb * kBVs;
+
+  floatx4 dh[kGMaxLev][TPW];
+#pragma unroll
+  for (int e = 0; e < kGMaxLev; ++e)
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) dh[e][j] = zero4();
+
+  for (int ic = NT - 1; ic >= 0; --ic) {
+    const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
+    // 512 threads: two 256-thread halves stage the tiles
+    if (w < 4) {
+      g2s_tile<KD>(qn + tok0 * hk + (size_t)h * KD, hk, s.qn, LK);
+      g2s_tile<KD>(wn + tok0 * hk + (size_t)h * KD, hk, s.wn, LK);
+      g2s_tile<kBVs>(un + tok0 * hv + (size_t)h * V + v0, hv, s.u, LVS);
+    } else {
+      g2s_tile<KD, kGC, 256>(kn + tok0 * hk + (size_t)h * KD, hk, s.kn, LK);
+      g2s_tile<kBVs, kGC, 256>(dO + tok0 * hv + (size_t)h * V + v0, hv, s.dO, LVS);
+    }
+    for (int e2 = tid; e2 < nlev * kGC; e2 += 512) {
+      const int t = e2 / nlev, c = e2 % nlev;
+      s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + 7 + c]);
+    }
+    const float eL = fexp(gcum[(tok0 + kGC - 1) * H + h]);
+
+    floatx4 adq[APW], adw[APW], adk[APW], adu = zero4();
+#pragma unroll
+    for (int j = 0; j < APW; ++j) adq[j] = adw[j] = adk[j] = zero4();
+    float del = 0.f;
+
+    // the level loop stays rolled (an unrolled one holds every level's fragments
+    // at once); the level's dh tiles move to and from a working set through a
+    // uniform switch, so the register array is only indexed by constants
+#pragma unroll 1
+    for (int e = 0; e < nlev; ++e) {
+      {
+        floatx4 cur[TPW];
+        switch (e) {
+#define HATTN_DH_GET(E) \
+  case E:               \
+    for (int j = 0; j < TPW; ++j) cur[j] = dh[E][j]; \
+    break;
+          HATTN_DH_GET(0) HATTN_DH_GET(1) HATTN_DH_GET(2) HATTN_DH_GET(3) HATTN_DH_GET(4)
+          HATTN_DH_GET(5) HATTN_DH_GET(6)
+#undef HATTN_DH_GET
+        }
+        const int per = 2 << e;
+        const bool rd = (ic >> e) & 1;
+        const bool wr = !rd;
+        const bool nr = (ic & (per - 1)) != per - 1;
+        if (w < 4)
+          g2s_tile<KD, kBVs>(hsave + (((size_t)row * NT + ic) * nlev + e) * (size_t)V * KD +
+                                 (size_t)v0 * KD,
+                             KD, s.hs, LK);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+          const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
+          *(bf16x4*)(s.dhs + (16 * vv + ln) * LK + 16 * kt + 4 * lq) = cvt4(cur[j]);
+        }
+        __syncthreads();
+
+        // (i) dV_new = K_new dh, V_new = wr U - nr W_new h, q_new h (for dlambda)
+        {
+          floatx4 dv = zero4(), y = zero4(), z = zero4();
+#pragma unroll
+          for (int c = 0; c < KD / 32; ++c) {
+            const bf16x8 bd = *(const bf16x8*)(s.dhs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
+            const bf16x8 bh = *(const bf16x8*)(s.hs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
+            dv = mfma16x16x32(*(const bf16x8*)(s.kn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bd, dv);
+            if (nr) y = mfma16x16x32(*(const bf16x8*)(s.wn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, y);
+            if (rd) z = mfma16x16x32(*(const bf16x8*)(s.qn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, z);
+          }
+          bf16x4 dvb, vnb;
+          float dlr[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 16 * tt + 4 * lq + i;
+            const float uu = wr ? (float)s.u[t * LVS + 16 * vt + ln] : 0.f;
+            vnb[i] = (__bf16)(uu - y[i]);
+            dvb[i] = (__bf16)dv[i];
+            if (wr) adu[i] += dv[i];
+            dlr[i] = rd ? (float)s.dO[t * LVS + 16 * vt + ln] * z[i] : 0.f;
+          }
+          *(bf16x4*)(s.dvn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = dvb;
+          *(bf16x4*)(s.vn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = vnb;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x = rsum16(dlr[i]);
+            if (ln == 0) s.dlr[vt][16 * tt + 4 * lq + i] = x;
+          }
+        }
+        __syncthreads();
+        if (tid < kGC)
+          dl_p[((size_t)vb * BTH + (tok0 + tid) * H + h) * nlev + e] = s.dlr[0][tid] + s.dlr[1][tid];
+
+        // (ii) contractions over this slice's 32 columns of V
+        {
+          const bf16x8 adO = *(const bf16x8*)(s.dO + (16 * tt + ln) * LVS + 8 * lq);
+          const bf16x8 advn = tr_frag(s.dvn, kLd64, 0, 16 * tt);   // dV_new[t][v]
+          const bf16x8 avn = tr_frag(s.vn, kLd64, 0, 16 * tt);     // V_new[t][v]
+          const floatx4 lam = *(const floatx4*)(s.lam[e] + 16 * tt + 4 * lq);
+#pragma unroll
+          for (int j = 0; j < APW; ++j) {
+            const int kt = vt * APW + j;
+            const bf16x8 bh = tr_frag(s.hs, LK, 0, 16 * kt);    // h^T[v][k]
+            const bf16x8 bd = tr_frag(s.dhs, LK, 0, 16 * kt);   // dh^T[v][k]
+            if (rd) {
+              const floatx4 tq = mfma16x16x32(adO, bh, zero4());
+#pragma unroll
+              for (int i = 0; i < 4; ++i) adq[j][i] += lam[i] * tq[i];
+            }
+            if (nr) adw[j] = mfma16x16x32(advn, bh, adw[j]);
+            adk[j] = mfma16x16x32(avn, bd, adk[j]);
+          }
+          if (nr) {
+#pragma unroll
+            for (int j = 0; j < TPW; ++j) {
+              const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
+              const bf16x4 hv4 = *(const bf16x4*)(s.hs + (16 * vv + ln) * LK + 16 * kt + 4 * lq);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) del += (float)hv4[i] * cur[j][i];
+            }
+          }
+        }
+
+        // (iii) dh_e <- nr (eL dh_e - W_new^T dV_new) + rd q_new^T (lambda_e o dO)
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+          const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
+          floatx4 tw = zero4(), tq = zero4();
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            if (nr) {
+              const bf16x8 bdv = *(const bf16x8*)(s.dvn + (16 * vv + ln) * kLd64 + 32 * c + 8 * lq);
+              tw = mfma16x16x32(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
+            }
+            if (rd) {
+              bf16x8 x = tr_frag(s.dO, LVS, 32 * c, 16 * vv);   // dO[t][v]
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj)
+                x[jj] = (__bf16)((float)x[jj] * s.lam[e][32 * c + 8 * lq + jj]);
+              tq = mfma16x16x32(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cur[j][i] = (nr ? eL * cur[j][i] - tw[i] : 0.f) + tq[i];
+        }
+        switch (e) {
+#define HATTN_DH_PUT(E) \
+  case E:               \
+    for (int j = 0; j < TPW; ++j) dh[E][j] = cur[j]; \
+    break;
+          HATTN_DH_PUT(0) HATTN_DH_PUT(1) HATTN_DH_PUT(2) HATTN_DH_PUT(3) HATTN_DH_PUT(4)
+          HATTN_DH_PUT(5) HATTN_DH_PUT(6)
+#undef HATTN_DH_PUT
+        }
+        __syncthreads();
+      }
+    }
+
+    // ---- the chunk's outputs -----------------------------------------------------
+#pragma unroll
+    for (int j = 0; j < APW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t o = ((size_t)vb * BTH + (tok0 + 16 * tt + 4 * lq + i) * H + h) * KD +
+                         16 * (vt * APW + j) + ln;
+        dq_p[o] = adq[j][i];
+        dw_p[o] = -adw[j][i];
+        dk_p[o] = adk[j][i];
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      du[((tok0 + 16 * tt + 4 * lq + i) * H + h) * V + v0 + 16 * vt + ln] = adu[i];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) del += __shfl_xor(del, off, 64);
+    if (lane == 0) s.red[w] = del;
+    __syncthreads();
+    if (tid == 0) {
+      float x = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 8; ++w2) x += s.red[w2];
+      del_p[(size_t)vb * B * H * NT + (size_t)row * NT + ic] = x;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 4: chunk-local backward
+// ---------------------------------------------------------------------------
+template <int KD, int VD>
+struct GdnBchunkSmem {
+  static constexpr int LK = KD + 8, LV = VD + 8;
+  static constexpr int LS = (KD > VD ? KD : VD) + 4;   // fp32 staging row stride
+  static constexpr int NR = kGC * LS > 2 * kGC * kLM ? kGC * LS : 2 * kGC * kLM;
+  __bf16 q[kGC * LK];
+  __bf16 k[kGC * LK];
+  __bf16 dO[kGC * LV];
+  float m[4][kGC * kLM];   // S0 .. S3: 64 x 64 fp32 matrices
+  float rg[NR];            // S4 | S5, or the fp32 staging tile, or the inverse scratch
+  float gc[kGC], e[kGC], r[kGC], beta[kGC];
+  float lam[7][kGC];       // lambda[t, 0..6]
+  float dlam[7][kGC];      // intra-chunk dlambda
+  float dgr[kGC];          // dGc: contributions of each row's owner
+  float dgcol[4][kGC];     // dGc: column-sum contributions, per wave
+  float dbr[kGC];          // dbeta
+  float lastc[kGC];        // contributions to dGc_last
+};
+
+// fp32 fragments of a 16 x 32 MFMA operand held in a row-major fp32 matrix:
+// element j of lane (lq, ln) is the operand's (non-contracted ln, contracted
+// 8lq + j) entry.  frn: stored [non-contracted][contracted]; frt: stored
+// [contracted][non-contracted].
+template <int LD>
+__device__ __forceinline__ void frn(const float* X, int r0, int c0, float* f) {
+  const int lane = threadIdx.x & 63;
+  const float* p = X + (r0 + (lane & 15)) * LD + c0 + 8 * (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = p[j];
+}
+template <int LD>
+__device__ __forceinline__ void frt(const float* X, int r0, int c0, float* f) {
+  const int lane = threadIdx.x & 63;
+  const float* p = X + (c0 + 8 * (lane >> 4)) * LD + r0 + (lane & 15);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = p[j * LD];
+}
+// Same from global rows of stride rs: sc * sum over np partials pstride apart.
+__device__ __forceinline__ void frg(const float* X, size_t rs, size_t pstride, int np, int r0,
+                                    int c0, float sc, float* f) {
+  const int lane = threadIdx.x & 63;
+  const float* p = X + (size_t)(r0 + (lane & 15)) * rs + c0 + 8 * (lane >> 4);
+  floatx4 a = *(const floatx4*)p, b = *(const floatx4*)(p + 4);
+  for (int pp = 1; pp < np; ++pp) {
+    a += *(const floatx4*)(p + pp * pstride);
+    b += *(const floatx4*)(p + pp * pstride + 4);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = sc * a[j];
+    f[4 + j] = sc * b[j];
+  }
+}
+// bf16x3 products: both operands fp32 (three MFMAs), or fp32 x bf16 (two).
+__device__ __forceinline__ floatx4 mma_ff(const float* a, const float* b, floatx4 c) {
+  bf16x8 A[2], Bf[2];
+  split8<2>(a, A);
+  split8<2>(b, Bf);
+  return mma<2>(A, Bf, c);
+}
+__device__ __forceinline__ floatx4 mma_fb(const float* a, bf16x8 b, floatx4 c) {
+  bf16x8 A[2];
+  split8<2>(a, A);
+  c = mfma16x16x32(A[1], b, c);
+  return mfma16x16x32(A[0], b, c);
+}
+// ST[t][c] = (scale ? scale[t] : 1) * sum over np partials of X[t][c], 64 rows of N.
+template <int N, int LS>
+__device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs, size_t pstride,
+                                           int np, const float* scale) {
+  for (int u = threadIdx.x; u < kGC * N / 4; u += 256) {
+    const int t = u / (N / 4), c = 4 * (u % (N / 4));
+    const float* p = X + (size_t)t * rs + c;
+    floatx4 a = *(const floatx4*)p;
+    for (int pp = 1; pp < np; ++pp) a += *(const floatx4*)(p + pp * pstride);
+    if (scale) a *= scale[t];
+    *(floatx4*)(ST + t * LS + c) = a;
+  }
+}
+
+template <int KD, int VD, typename TB, typename TL>
+__global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const TB* __restrict__ beta, const float* __restrict__ gcum, const TL* __restrict__ l,
+    const __bf16* __restrict__ dO, const float* __restrict__ dq_p, const float* __restrict__ dw_p,
+    const float* __restrict__ dk_p, const float* __restrict__ du, const float* __restrict__ dl_p,
+    const float* __restrict__ del_p, int nvs, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
+    __bf16* __restrict__ dv, TB* __restrict__ db, float* __restrict__ dg, float* __restrict__ dl,
+    int B, int T, int H, int L, int nlev) {
+  using Sm = GdnBchunkSmem<KD, VD>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Sm& s = *(Sm*)smem_raw;
+  constexpr int LK = Sm::LK, LV = Sm::LV, LS = Sm::LS, NKT = KD / 16, NVT = VD / 16;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int NT = T / kGC;
+  const int ic = blockIdx.x % NT, row = blockIdx.x / NT;
+  const int b = row / H, h = row % H;
+  const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
+  const size_t hk = (size_t)H * KD, hv = (size_t)H * VD;
+  const size_t BTH = (size_t)B * T * H;
+  const size_t rowk = (tok0 * H + h) * KD, rowv = (tok0 * H + h) * VD;
+  float* S0 = s.m[0];
+  float* S1 = s.m[1];
+  float* S2 = s.m[2];
+  float* S3 = s.m[3];
+  float* S4 = s.rg;
+  float* S5 = s.rg + kGC * kLM;
+  float* ST = s.rg;
+  const int t16 = 16 * w;   // this wave's 16-row tile
+
+  // ---- load ------------------------------------------------------------------
+  g2s_tile<KD>(k + rowk, hk, s.k, LK);
+  g2s_tile<KD>(q + rowk, hk, s.q, LK);
+  g2s_tile<VD>(dO + rowv, hv, s.dO, LV);
+  if (w == 0) {
+    const float x = gcum[(tok0 + lane) * H + h];
+    const float gl = __shfl(x, kGC - 1, 64);
+    s.gc[lane] = x;
+    s.e[lane] = fexp(x);
+    s.r[lane] = fexp(gl - x);
+    s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
+  }
+  for (int u = tid; u < 7 * kGC; u += 256) {
+    const int t = u / 7, c = u % 7;
+    s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + c]);
+    s.dlam[c][t] = 0.f;
+  }
+  if (tid < kGC) {
+    s.dgr[tid] = s.dbr[tid] = s.lastc[tid] = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) s.dgcol[w2][tid] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- 1: A = strict-tril(beta_t K K^T) -> S0, M = tril(Q K^T) -> S1 ---------------
+  {
+    floatx4 kk[4], qk[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) kk[nt] = qk[nt] = zero4();
+#pragma unroll
+    for (int c = 0; c < KD / 32; ++c) {
+      const bf16x8 ak = *(const bf16x8*)(s.k + (t16 + ln) * LK + 32 * c + 8 * lq);
+      const bf16x8 aq = *(const bf16x8*)(s.q + (t16 + ln) * LK + 32 * c + 8 * lq);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
+        kk[nt] = mfma16x16x32(ak, bk, kk[nt]);
+        qk[nt] = mfma16x16x32(aq, bk, qk[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
+        S0[t * kLM + sc] = sc < t ? s.beta[t] * kk[nt][i] : 0.f;
+        S1[t * kLM + sc] = sc <= t ? qk[nt][i] : 0.f;
+      }
+  }
+  __syncthreads();
+
+  // ---- 2: Aw = (I + A)^-1 -> S2 ---------------------------------------------------
+  tri_inv64(S0, S2, (float(*)[16 * 17])S5);
+
+  // ---- 3: P = M Aw -> S3 ------------------------------------------------------------
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    floatx4 acc = zero4();
+    if (nt <= w) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float a[8], bb[8];
+        frn<kLM>(S1, t16, 32 * c, a);
+        frt<kLM>(S2, 16 * nt, 32 * c, bb);
+        acc = mma_ff(a, bb, acc);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S3[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] = acc[i];
+  }
+  __syncthreads();
+
+  // ---- 4: Z = dO V^T; Z o P o Gamma -> S0, dP = Z o Gamma o Lambda o beta_s -> S4 -----
+  {
+    bf16x8 ad[VD / 32];
+#pragma unroll
+    for (int c = 0; c < VD / 32; ++c) ad[c] = *(const bf16x8*)(s.dO + (t16 + ln) * LV + 32 * c + 8 * lq);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      floatx4 z = zero4();
+      if (nt <= w) {
+#pragma unroll
+        for (int c = 0; c < VD / 32; ++c)
+          z = mfma16x16x32(ad[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), z);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
+        float zp = 0.f, dp = 0.f;
+        if (sc <= t) {
+          const float gam = fexp(s.gc[t] - s.gc[sc]);
+          zp = z[i] * S3[t * kLM + sc] * gam;
+          dp = z[i] * gam * s.lam[intra_level(t, sc)][t] * s.beta[sc];
+        }
+        S0[t * kLM + sc] = zp;
+        S4[t * kLM + sc] = dp;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 4b: intra-chunk dlambda; Gamma term of o_intra in dGc --------------------------
+  if (tid < kGC) {
+    const int t = tid;
+    float rs = 0.f;
+    for (int sc = 0; sc <= t; ++sc) {
+      const int lv = intra_level(t, sc);
+      const float val = S0[t * kLM + sc] * s.beta[sc];
+      s.dlam[lv][t] += val;
+      rs += val * s.lam[lv][t];
+    }
+    s.dgr[t] += rs;
+  } else if (tid < 2 * kGC) {
+    const int sc = tid - kGC;
+    float cs = 0.f;
+    for (int t = sc; t < kGC; ++t) cs += S0[t * kLM + sc] * s.lam[intra_level(t, sc)][t];
+    s.dgcol[1][sc] -= cs * s.beta[sc];
+  }
+  __syncthreads();
+
+  // ---- 5: F1 = X K^T (X = e o dq_new); E = dP - F1 o beta_s -> S4; F1 o beta_s -> S0 ---
+  {
+    float ax[KD / 32][8];
+#pragma unroll
+    for (int c = 0; c < KD / 32; ++c)
+      frg(dq_p + rowk, hk, BTH * KD, nvs, t16, 32 * c, s.e[t16 + ln], ax[c]);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      floatx4 f = zero4();
+#pragma unroll
+      for (int c = 0; c < KD / 32; ++c)
+        f = mma_fb(ax[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
+        const float fb = f[i] * s.beta[sc];
+        S4[t * kLM + sc] -= fb;
+        S0[t * kLM + sc] = fb;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 6: H = (F1 beta) Aw^T, D = E Aw^T; dGc_t -= rowsum(M o H); dM = tril(D) -> S0 --
+  {
+    floatx4 hacc[4], dacc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) hacc[nt] = dacc[nt] = zero4();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float ah[8], ae[8];
+      frn<kLM>(S0, t16, 32 * c, ah);
+      frn<kLM>(S4, t16, 32 * c, ae);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        float bw[8];
+        frn<kLM>(S2, 16 * nt, 32 * c, bw);
+        hacc[nt] = mma_ff(ah, bw, hacc[nt]);
+        dacc[nt] = mma_ff(ae, bw, dacc[nt]);
+      }
+    }
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rs[i] += S1[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] * hacc[nt][i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = rsum16(rs[i]);
+      if (ln == 0) s.dgr[t16 + 4 * lq + i] -= x;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
+        S0[t * kLM + sc] = sc <= t ? dacc[nt][i] : 0.f;
+      }
+  }
+  __syncthreads();
+
+  // ---- 7: F2 = (e o dW_new) K^T, F3 = dU V^T; (F2 + F3 o Gamma) o beta_s -> S5;
+  //         dGc from the W_new factor e and the Gamma of Au --------------------------
+  {
+    float a2[KD / 32][8], a3[VD / 32][8];
+#pragma unroll
+    for (int c = 0; c < KD / 32; ++c)
+      frg(dw_p + rowk, hk, BTH * KD, nvs, t16, 32 * c, s.e[t16 + ln], a2[c]);
+#pragma unroll
+    for (int c = 0; c < VD / 32; ++c) frg(du + rowv, hv, 0, 1, t16, 32 * c, 1.f, a3[c]);
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      floatx4 f2 = zero4(), f3 = zero4();
+#pragma unroll
+      for (int c = 0; c < KD / 32; ++c)
+        f2 = mma_fb(a2[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f2);
+#pragma unroll
+      for (int c = 0; c < VD / 32; ++c)
+        f3 = mma_fb(a3[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), f3);
+      float cs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
+        const float aw = S2[t * kLM + sc], bs = s.beta[sc];
+        const float gam = sc <= t ? fexp(s.gc[t] - s.gc[sc]) : 0.f;
+        const float t2 = f3[i] * bs * aw * gam;
+        rs[i] += aw * f2[i] * bs + t2;
+        cs += t2;
+        S5[t * kLM + sc] = (f2[i] + f3[i] * gam) * bs;
+      }
+      cs = sum_lq(cs);
+      if (lq == 0) s.dgcol[w][16 * nt + ln] -= cs;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = rsum16(rs[i]);
+      if (ln == 0) s.dgr[t16 + 4 * lq + i] += x;
+    }
+  }
+  __syncthreads();
+
+  // ---- 8: dAw = S5 + M^T E -> S5 ------------------------------------------------------
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    floatx4 acc = zero4();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float a[8], bb[8];
+      frt<kLM>(S1, t16, 32 * c, a);
+      frt<kLM>(S4, 16 * nt, 32 * c, bb);
+      acc = mma_ff(a, bb, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S5[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] += acc[i];
+  }
+  __syncthreads();
+
+  // ---- 9: Y = dAw Aw^T -> S1; dA = -strict-tril(Aw^T Y) -> S1 --------------------------
+  {
+    floatx4 acc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      acc[nt] = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float a[8], bb[8];
+        frn<kLM>(S5, t16, 32 * c, a);
+        frn<kLM>(S2, 16 * nt, 32 * c, bb);
+        acc[nt] = mma_ff(a, bb, acc[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S1[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] = acc[nt][i];
+  }
+  __syncthreads();
+  {
+    floatx4 acc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      acc[nt] = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float a[8], bb[8];
+        frt<kLM>(S2, t16, 32 * c, a);
+        frt<kLM>(S1, 16 * nt, 32 * c, bb);
+        acc[nt] = mma_ff(a, bb, acc[nt]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ii = t16 + 4 * lq + i, jj = 16 * nt + ln;
+        S1[ii * kLM + jj] = jj < ii ? -acc[nt][i] : 0.f;
+      }
+  }
+  __syncthreads();
+
+  // live: S0 = dM, S1 = dA, S2 = Aw, S3 = P; the staging region is free
+  // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ------------------
+  stage_rows<KD, LS>(ST, dq_p + rowk, hk, BTH * KD, nvs, s.e);
+  __syncthreads();
+  floatx4 u2[NKT];
+#pragma unroll
+  for (int nt = 0; nt < NKT; ++nt) {
+    floatx4 acc = zero4(), a2 = zero4();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float am[8], ap[8], bx[8];
+      frn<kLM>(S0, t16, 32 * c, am);
+      acc = mma_fb(am, tr_frag(s.k, LK, 32 * c, 16 * nt), acc);
+      frt<kLM>(S3, t16, 32 * c, ap);
+      frt<LS>(ST, 16 * nt, 32 * c, bx);
+      a2 = mma_ff(ap, bx, a2);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t16 + 4 * lq + i, kk = 16 * nt + ln;
+      dq[rowk + t * hk + kk] = (__bf16)(ST[t * LS + kk] + acc[i]);
+    }
+    u2[nt] = -a2;
+  }
+  {
+    const int t = tid >> 2, part = tid & 3;
+    float x = 0.f;
+    for (int kk = part * (KD / 4); kk < (part + 1) * (KD / 4); ++kk)
+      x += ST[t * LS + kk] * (float)s.q[t * LK + kk];
+    x += __shfl_xor(x, 1, 64);
+    x += __shfl_xor(x, 2, 64);
+    if (part == 0) s.dgr[t] += x;
+  }
+  __syncthreads();
+
+  // ---- 11: e o dW_new -> ST; U2 += Aw^T ST ---------------------------------------------
+  stage_rows<KD, LS>(ST, dw_p + rowk, hk, BTH * KD, nvs, s.e);
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float a[8], bb[8];
+      frt<kLM>(S2, t16, 32 * c, a);
+      frt<LS>(ST, 16 * nt, 32 * c, bb);
+      u2[nt] = mma_ff(a, bb, u2[nt]);
+    }
+  __syncthreads();
+
+  // ---- 12: U2 += dA K; U1 = dM^T Q + dA^T (beta o K) ----------------------------------
+  floatx4 u1[NKT];
+#pragma unroll
+  for (int nt = 0; nt < NKT; ++nt) {
+    floatx4 a1 = zero4();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const bf16x8 bk = tr_frag(s.k, LK, 32 * c, 16 * nt), bq = tr_frag(s.q, LK, 32 * c, 16 * nt);
+      float ad[8], am[8], at[8];
+      frn<kLM>(S1, t16, 32 * c, ad);
+      u2[nt] = mma_fb(ad, bk, u2[nt]);
+      frt<kLM>(S0, t16, 32 * c, am);
+      a1 = mma_fb(am, bq, a1);
+      frt<kLM>(S1, t16, 32 * c, at);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) at[j] *= s.beta[32 * c + 8 * lq + j];
+      a1 = mma_fb(at, bk, a1);
+    }
+    u1[nt] = a1;
+  }
+
+  // ---- 13: dK_new -> ST; dK = U1 + beta o U2 + r o dK_new; dbeta, dGc of K_new -------
+  stage_rows<KD, LS>(ST, dk_p + rowk, hk, BTH * KD, nvs, nullptr);
+  __syncthreads();
+  {
+    float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sr = t16 + 4 * lq + i, kk = 16 * nt + ln;
+        const float kv = (float)s.k[sr * LK + kk], dkn = ST[sr * LS + kk];
+        dk[rowk + sr * hk + kk] = (__bf16)(u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn);
+        rb[i] += kv * u2[nt][i];
+        kd[i] += dkn * kv;
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = rsum16(rb[i]), y = rsum16(kd[i]);
+      if (ln == 0) {
+        const int sr = t16 + 4 * lq + i;
+        s.dbr[sr] += x;
+        s.dgr[sr] -= s.r[sr] * y;
+        s.lastc[sr] = s.r[sr] * y;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 14: dU -> ST; GV = Au^T dU + (P o Gamma o Lambda)^T dO; dV = beta o GV --------
+  stage_rows<VD, LS>(ST, du + rowv, hv, 0, 1, nullptr);
+  __syncthreads();
+  {
+    float au[2][8], ar[2][8];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      frt<kLM>(S2, t16, 32 * c, au[c]);
+      frt<kLM>(S3, t16, 32 * c, ar[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = 32 * c + 8 * lq + j, sc = t16 + ln;
+        const float gam = t >= sc ? fexp(s.gc[t] - s.gc[sc]) : 0.f;
+        au[c][j] *= gam;
+        ar[c][j] *= gam * s.lam[intra_level(t, sc)][t];
+      }
+    }
+    float rb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nt = 0; nt < NVT; ++nt) {
+      floatx4 acc = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float bu[8];
+        frt<LS>(ST, 16 * nt, 32 * c, bu);
+        acc = mma_ff(au[c], bu, acc);
+        acc = mma_fb(ar[c], tr_frag(s.dO, LV, 32 * c, 16 * nt), acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sr = t16 + 4 * lq + i, vv = 16 * nt + ln;
+        dv[rowv + sr * hv + vv] = (__bf16)(s.beta[sr] * acc[i]);
+        rb[i] += (float)v[rowv + sr * hv + vv] * acc[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = rsum16(rb[i]);
+      if (ln == 0) s.dbr[t16 + 4 * lq + i] += x;
+    }
+  }
+  __syncthreads();
+
+  // ---- 15: per token: dg = reverse chunk-local cumsum of dGc, dbeta, dlambda ---------
+  if (w == 0) {
+    const int t = lane;
+    float x = s.dgr[t] + s.dgcol[0][t] + s.dgcol[1][t] + s.dgcol[2][t] + s.dgcol[3][t];
+    if (t == kGC - 1) {
+      float lc = 0.f, de = 0.f;
+      for (int u = 0; u < kGC; ++u) lc += s.lastc[u];
+      for (int p = 0; p < nvs; ++p) de += del_p[(size_t)p * B * H * NT + (size_t)row * NT + ic];
+      x += lc + s.e[kGC - 1] * de;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_down(x, d, 64);
+      if (t + d < 64) x += y;
+    }
+    dg[(tok0 + t) * H + h] = x;
+    db[(tok0 + t) * H + h] = from_f32<TB>(s.dbr[t]);
+  }
+  for (int u = tid; u < kGC * L; u += 256) {
+    const int t = u / L, c = u % L;
+    float x = 0.f;
+    if (c < 7) {
+      x = s.dlam[c][t];
+    } else if (c < 7 + nlev) {
+      for (int p = 0; p < nvs; ++p) x += dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + c - 7];
+    }
+    dl[((tok0 + t) * H + h) * L + c] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launcher
+// ---------------------------------------------------------------------------
+struct GdnBwdWs {
+  __bf16 *qn, *kn, *wn, *un, *hs;
+  float *dq_p, *dw_p, *dk_p, *du, *dl_p, *del_p;
+  size_t bytes;
+};
+
+inline size_t balign(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V, int nlev) {
+  GdnBwdWs w;
+  char* p = (char*)base;
+  size_t off = 0;
+  const size_t n = (size_t)B * T * H;
+  const size_t NT = (size_t)T / kGC, nvs = (size_t)V / kBVs;
+  const size_t nl = nlev > 0 ? (size_t)nlev : 1;
+  w.qn = (__bf16*)(p + off); off += balign(n * K * 2);
+  w.kn = (__bf16*)(p + off); off += balign(n * K * 2);
+  w.wn = (__bf16*)(p + off); off += balign(n * K * 2);
+  w.un = (__bf16*)(p + off); off += balign(n * V * 2);
+  w.hs = (__bf16*)(p + off); off += balign((size_t)B * H * NT * nl * V * K * 2);
+  w.dq_p = (float*)(p + off); off += balign(nvs * n * K * 4);
+  w.dw_p = (float*)(p + off); off += balign(nvs * n * K * 4);
+  w.dk_p = (float*)(p + off); off += balign(nvs * n * K * 4);
+  w.du = (float*)(p + off); off += balign(n * V * 4);
+  w.dl_p = (float*)(p + off); off += balign(nvs * n * nl * 4);
+  w.del_p = (float*)(p + off); off += balign(nvs * B * H * NT * 4);
+  w.bytes = off;
+  return w;
+}
+
+template <int KD, int VD, typename TB, typename TL>
+static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const void* beta,
+                            const float* gcum, const void* l, const void* dO, void* dq, void* dk,
+                            void* dv, void* db, float* dg, float* dl, const GdnBwdWs& w, int B,
+                            int T, int H, int L, int nlev, hipStream_t stream) {
+  const int NT = T / kGC;
+  hipError_t e;
+  {
+    auto ks = gdn_bwd_scan_kernel<KD, TL>;
+    const int smem = (int)sizeof(GdnBscanSmem<KD>);
+    if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 smem)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(512), smem, stream, w.qn, w.wn, w.kn,
+                       w.un, (const __bf16*)dO, gcum, (const TL*)l, w.hs, w.dq_p, w.dw_p, w.dk_p,
+                       w.du, w.dl_p, w.del_p, B, T, H, VD, L, nlev);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  {
+    auto kc = gdn_bwd_chunk_kernel<KD, VD, TB, TL>;
+    const int smem = (int)sizeof(GdnBchunkSmem<KD, VD>);
+    if ((e = hipFuncSetAttribute((const void*)kc, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 smem)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(kc, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, (const TB*)beta, gcum, (const TL*)l,
+                       (const __bf16*)dO, w.dq_p, w.dw_p, w.dk_p, w.du, w.dl_p, w.del_p,
+                       VD / kBVs, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, (TB*)db, dg, dl, B, T,
+                       H, L, nlev);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace hattn
+
+size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
+  return hattn::gdn_bwd_ws_layout(nullptr, B, T, H, K, V, nlev).bytes;
+}
+
+hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
+                                const float* gcum, const void* l, const void* dO, void* dq,
+                                void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
+                                int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
+                                int dt_l, hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
+  hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.wn, w.un, w.hs,
+                                            B, T, H, K, V, L, nlev, dt_b, dt_l, stream,
+                                            unsupported);
+  if (e != hipSuccess || *unsupported) return e;
+#define HATTN_GDN_B(KD_, VD_)                                                                   \
+  if (K == KD_ && V == VD_) {                                                                   \
+    if (dt_b == 0 && dt_l == 0)                                                                 \
+      return gdn_bwd_t<KD_, VD_, __bf16, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, \
+                                                 dl, w, B, T, H, L, nlev, stream);              \
+    if (dt_b == 2 && dt_l == 2)                                                                 \
+      return gdn_bwd_t<KD_, VD_, float, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,   \
+                                               dl, w, B, T, H, L, nlev, stream);                \
+    if (dt_b == 0 && dt_l == 2)                                                                 \
+      return gdn_bwd_t<KD_, VD_, __bf16, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
+                                                dl, w, B, T, H, L, nlev, stream);               \
+    if (dt_b == 2 && dt_l == 0)                                                                 \
+      return gdn_bwd_t<KD_, VD_, float, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
+                                                dl, w, B, T, H, L, nlev, stream);               \
+  }
+  HATTN_GDN_B(128, 128)
+  HATTN_GDN_B(64, 64)
+#undef HATTN_GDN_B
+  *unsupported = 1;
+  return hipSuccess;
+}

@@ -29,14 +29,9 @@
 // (wave w owns K / 4 state rows); per chunk it stages the states in LDS
 // as bf16, forms W_new h_e and q_new h_e for all levels, then
 // h_e += K_new^T V_new_e, and writes o = o_intra + sum of the level reads.
-#include "common.h"
+#include "gdn_common.h"
 
 namespace hattn {
-
-constexpr int kGC = 64;       // chunk length
-constexpr int kLd64 = 72;     // LDS row stride of 64-wide bf16 tiles
-constexpr int kGMaxLev = 7;   // inter-chunk levels held by the scan (T <= 64 * 2^7)
-constexpr int kBVs = 32;      // V columns per scan workgroup
 
 template <int KD, int VD>
 struct GdnPrepSmem {
@@ -57,18 +52,10 @@ struct GdnPrepSmem {
   float lam[7][kGC];              // intra-chunk lambda columns 0..6
 };
 
-// 16-byte units of a row-major [64][N] bf16 tile, NTHR = 256 threads.
-template <int N>
-__device__ __forceinline__ void g2s_tile(const __bf16* __restrict__ src, size_t row_stride,
-                                         __bf16* dst, int ld) {
-  constexpr int UPR = N / 8;  // units per row
-  for (int u = threadIdx.x; u < kGC * UPR; u += 256) {
-    const int r = u / UPR, c = 8 * (u % UPR);
-    *(uint4*)(dst + r * ld + c) = *(const uint4*)(src + r * row_stride + c);
-  }
-}
-
-template <int KD, int VD, typename TB, typename TL>
+// GCUM: g already holds the chunk-local cumsum (the backward's input,
+// chunkwise_hgdn.py:799-817) and gcum is not written.  aw_out, au_out and oi
+// may be null (the backward recomputes only q_new, K_new, W_new and U).
+template <int KD, int VD, typename TB, typename TL, bool GCUM = false>
 __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
@@ -87,8 +74,8 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   const int b = row / H, h = row % H;
   const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;   // first token of the chunk
   const size_t hk = (size_t)H * KD, hv = (size_t)H * VD;
-  float* A = s.f;                 // [64][65]
-  float* X = s.f + kGC * 65;      // [64][65]
+  float* A = s.f;                 // [64][kLM]
+  float* X = s.f + kGC * kLM;     // [64][65]
 
   // ---- load the chunk ---------------------------------------------------------
   g2s_tile<KD>(k + tok0 * hk + (size_t)h * KD, hk, s.k, LK);
@@ -96,13 +83,15 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   g2s_tile<VD>(v + tok0 * hv + (size_t)h * VD, hv, s.v, LV);
   if (w == 0) {
     float x = g[(tok0 + lane) * H + h];
+    if constexpr (!GCUM) {
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_up(x, d, 64);
-      if (lane >= d) x += y;
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      gcum[(tok0 + lane) * H + h] = x;
     }
     s.gc[lane] = x;
-    gcum[(tok0 + lane) * H + h] = x;
     s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
   }
   for (int e = tid; e < 7 * kGC; e += 256) {
@@ -132,59 +121,14 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * lq + i, sc = 16 * nt + ln;
-        A[t * 65 + sc] = sc < t ? s.beta[t] * kk[nt][i] : 0.f;
+        A[t * kLM + sc] = sc < t ? s.beta[t] * kk[nt][i] : 0.f;
         s.qk[t * kLd64 + sc] = (__bf16)(sc <= t ? qk[nt][i] : 0.f);
       }
   }
   __syncthreads();
 
   // ---- X = (I + A)^-1, fp32 ----------------------------------------------------
-  // diagonal 16 x 16 blocks: forward substitution, lane ln owns column ln
-  if (lq == 0) {
-    const int o = 16 * w;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = (i == ln) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) acc -= A[(o + i) * 65 + o + j] * x[j];
-      x[i] = acc;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) X[(o + i) * 65 + o + ln] = x[i];
-  }
-  __syncthreads();
-  // off-diagonal blocks by distance d: X_ij = -X_ii sum_{m=j}^{i-1} A_im X_mj
-#pragma unroll
-  for (int d = 1; d < 4; ++d) {
-    const int bj = w, bi = w + d;
-    if (bi < 4) {
-      float* t1 = s.t1[w];
-      // T1 = sum_m A[bi][m] X[m][bj]; lane: rows 4lq + ii, column ln
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int r = 4 * lq + ii;
-        float acc = 0.f;
-        for (int m = bj; m < bi; ++m)
-#pragma unroll
-          for (int x = 0; x < 16; ++x)
-            acc += A[(16 * bi + r) * 65 + 16 * m + x] * X[(16 * m + x) * 65 + 16 * bj + ln];
-        t1[r * 17 + ln] = acc;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int r = 4 * lq + ii;
-        float acc = 0.f;
-#pragma unroll
-        for (int x = 0; x < 16; ++x) acc += X[(16 * bi + r) * 65 + 16 * bi + x] * t1[x * 17 + ln];
-        X[(16 * bi + r) * 65 + 16 * bj + ln] = -acc;
-      }
-    }
-    __syncthreads();
-  }
+  tri_inv64(A, X, s.t1);
 
   // ---- Aw, Au (bf16) to LDS and to the outputs ----------------------------------------
   for (int u = tid; u < kGC * 8; u += 256) {
@@ -193,14 +137,14 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int sc = s0 + j;
-      const float x = sc <= t ? X[t * 65 + sc] : 0.f;
+      const float x = sc <= t ? X[t * kLM + sc] : 0.f;
       a[j] = (__bf16)x;
       au[j] = (__bf16)(sc <= t ? x * fexp(s.gc[t] - s.gc[sc]) : 0.f);
     }
     *(bf16x8*)(s.aw + t * kLd64 + s0) = a;
     *(bf16x8*)(s.au + t * kLd64 + s0) = au;
-    *(bf16x8*)(aw_out + ((tok0 + t) * H + h) * kGC + s0) = a;
-    *(bf16x8*)(au_out + ((tok0 + t) * H + h) * kGC + s0) = au;
+    if (aw_out) *(bf16x8*)(aw_out + ((tok0 + t) * H + h) * kGC + s0) = a;
+    if (au_out) *(bf16x8*)(au_out + ((tok0 + t) * H + h) * kGC + s0) = au;
   }
   __syncthreads();
 
@@ -281,6 +225,8 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   }
   __syncthreads();
 
+  if (oi == nullptr) return;
+
   // ---- P = (tril(Q K^T) Aw) o gamma o beta_s o lambda[t, lev] (bf16 LDS) -----------
   gemm_rows(s.qk, s.aw, kLd64, 4, false);
   __syncthreads();
@@ -328,8 +274,8 @@ template <int KD, typename TL, typename TO>
 __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
     const __bf16* __restrict__ un, const float* __restrict__ oi, const float* __restrict__ gcum,
-    const TL* __restrict__ l, TO* __restrict__ o, float* __restrict__ ht, int T, int H, int V,
-    int L, int nlev, int final_state) {
+    const TL* __restrict__ l, TO* __restrict__ o, float* __restrict__ ht,
+    __bf16* __restrict__ hsave, int T, int H, int V, int L, int nlev, int final_state) {
   using Sm = GdnScanSmem<KD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
@@ -367,15 +313,23 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
       s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + 7 + c]);
     }
     const float glast = gcum[(tok0 + kGC - 1) * H + h];
-    // states -> LDS, bf16 [v][k] (4 consecutive k per lane)
+    // states -> LDS, bf16 [v][k] (4 consecutive k per lane); with hsave also to
+    // hsave[row][chunk][level][v][k] (the state each chunk starts from)
 #pragma unroll
     for (int e = 0; e < kGMaxLev; ++e) {
       if (e < nlev) {
+        __bf16* hg = hsave ? hsave + (((size_t)row * NT + ic) * nlev + e) * (size_t)V * KD +
+                                 (size_t)v0 * KD
+                           : nullptr;
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-          for (int n = 0; n < 2; ++n)
-            *(bf16x4*)(s.hs[e] + (16 * n + ln) * LK + RW * w + 16 * m + 4 * lq) = cvt4(st[e][m][n]);
+          for (int n = 0; n < 2; ++n) {
+            const bf16x4 hv4 = cvt4(st[e][m][n]);
+            const int kk = RW * w + 16 * m + 4 * lq;
+            *(bf16x4*)(s.hs[e] + (16 * n + ln) * LK + kk) = hv4;
+            if (hg) *(bf16x4*)(hg + (size_t)(16 * n + ln) * KD + kk) = hv4;
+          }
       }
     }
     __syncthreads();
@@ -404,7 +358,7 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
             for (int c = 0; c < KD / 32; ++c) {
               const bf16x8 bh = *(const bf16x8*)(s.hs[e] + (16 * n + ln) * LK + 32 * c + 8 * lq);
               if (!reset) y = mfma16x16x32(aw[c], bh, y);
-              if (rd) z = mfma16x16x32(aq[c], bh, z);
+              if (rd && o) z = mfma16x16x32(aq[c], bh, z);
             }
             bf16x4 vb4;
 #pragma unroll
@@ -420,13 +374,15 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
       }
     }
     // ---- o = o_intra + reads ----------------------------------------------------------
+    if (o) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+      for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const size_t idx = (tok0 + 16 * w + 4 * lq + i) * hv + (size_t)h * V + v0 + 16 * n + ln;
-        o[idx] = from_f32<TO>(oi[idx] + acc[n][i]);
-      }
+        for (int i = 0; i < 4; ++i) {
+          const size_t idx = (tok0 + 16 * w + 4 * lq + i) * hv + (size_t)h * V + v0 + 16 * n + ln;
+          o[idx] = from_f32<TO>(oi[idx] + acc[n][i]);
+        }
+    }
     __syncthreads();
 
     // ---- h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new_e -----------------------
@@ -529,8 +485,8 @@ static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, cons
                                  smem)) != hipSuccess)
       return e;
     hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(256), smem, stream, w.qn, w.wn, w.kn,
-                       w.un, w.oi, gcum, (const TL*)l, (TO*)o, ht, T, H, VD, L, nlev,
-                       ht != nullptr ? 1 : 0);
+                       w.un, w.oi, gcum, (const TL*)l, (TO*)o, ht, (__bf16*)nullptr, T, H, VD, L,
+                       nlev, ht != nullptr ? 1 : 0);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
@@ -569,6 +525,56 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
   HATTN_GDN(128, 128)
   HATTN_GDN(64, 64)
 #undef HATTN_GDN
+  *unsupported = 1;
+  return hipSuccess;
+}
+
+// Forward recompute for the backward: q_new, K_new, W_new, U from the
+// chunk-local cumsum (prep kernel) and every level's per-chunk starting state,
+// bf16 [row][chunk][level][v][k] (scan kernel, no output).
+hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* v,
+                                      const void* beta, const float* gcum, const void* l,
+                                      __bf16* qn, __bf16* kn, __bf16* wn, __bf16* un,
+                                      __bf16* hsave, int B, int T, int H, int K, int V, int L,
+                                      int nlev, int dt_b, int dt_l, hipStream_t stream,
+                                      int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  const int NT = T / kGC;
+  hipError_t e;
+#define HATTN_GDN_RC(KD_, VD_, TB_, TL_)                                                           \
+  {                                                                                              \
+    auto kp = gdn_prep_kernel<KD_, VD_, TB_, TL_, true>;                                         \
+    const int smem = (int)sizeof(GdnPrepSmem<KD_, VD_>);                                         \
+    if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                                 smem)) != hipSuccess)                                           \
+      return e;                                                                                  \
+    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,          \
+                       (const __bf16*)k, (const __bf16*)v, (const TB_*)beta, gcum,               \
+                       (const TL_*)l, (float*)nullptr, (__bf16*)nullptr, (__bf16*)nullptr, qn,   \
+                       kn, wn, un, (float*)nullptr, T, H, L);                                    \
+    if ((e = hipGetLastError()) != hipSuccess) return e;                                         \
+    auto ks = gdn_scan_kernel<KD_, TL_, __bf16>;                                                 \
+    const int smem2 = (int)sizeof(GdnScanSmem<KD_>);                                             \
+    if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                                 smem2)) != hipSuccess)                                          \
+      return e;                                                                                  \
+    hipLaunchKernelGGL(ks, dim3(B * H * (VD_ / kBVs)), dim3(256), smem2, stream, qn, wn, kn, un, \
+                       (const float*)nullptr, gcum, (const TL_*)l, (__bf16*)nullptr,             \
+                       (float*)nullptr, hsave, T, H, VD_, L, nlev, 0);                           \
+    return hipGetLastError();                                                                    \
+  }
+#define HATTN_GDN_RC_D(KD_, VD_)                                                                 \
+  if (K == KD_ && V == VD_) {                                                                    \
+    if (dt_b == 0 && dt_l == 0) HATTN_GDN_RC(KD_, VD_, __bf16, __bf16)                           \
+    if (dt_b == 2 && dt_l == 2) HATTN_GDN_RC(KD_, VD_, float, float)                             \
+    if (dt_b == 0 && dt_l == 2) HATTN_GDN_RC(KD_, VD_, __bf16, float)                            \
+    if (dt_b == 2 && dt_l == 0) HATTN_GDN_RC(KD_, VD_, float, __bf16)                            \
+  }
+  HATTN_GDN_RC_D(128, 128)
+  HATTN_GDN_RC_D(64, 64)
+#undef HATTN_GDN_RC_D
+#undef HATTN_GDN_RC
   *unsupported = 1;
   return hipSuccess;
 }

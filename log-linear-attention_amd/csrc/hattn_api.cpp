@@ -26,6 +26,12 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o,
                                 hipStream_t stream, int* unsupported);
+size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev);
+hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
+                                const float* gcum, const void* l, const void* dO, void* dq,
+                                void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
+                                int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
+                                int dt_l, hipStream_t stream, int* unsupported);
 size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
@@ -224,6 +230,60 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d o=%d", dtype_beta,
                 dtype_l, dtype_o);
   return check_hip(e, "hattn_gdn_chunkwise_fwd launch");
+}
+
+size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L) {
+  (void)L;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+  return hattn_gdn_bwd_ws_bytes(B, T, H, K, V, ceil_log2(T / 64));
+}
+
+int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,
+                            const float* g_cumsum, const void* l, const void* Aw, const void* Au,
+                            const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
+                            float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
+                            int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
+                            int chunk_size, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  (void)Aw;
+  (void)Au;
+  // chunkwise_hgdn.py:818-858
+  if (chunk_size != 64)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
+  if (level_base != 2)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
+  if (htype != HATTN_HTYPE_WEAK)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
+  if (K > 256) return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d > 256", K);
+  if (K % 64 != 0 || V % 64 != 0)
+    return fail(HATTN_ERR_VALUE, "K=%d, V=%d and BK, BV could be 64", K, V);
+  if (!((K == 128 && V == 128) || (K == 64 && V == 64)))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (the MI355X GDN kernels support 64/64, 128/128)",
+                K, V);
+  const int nlev = ceil_log2(T / 64);
+  if (7 + nlev > L)
+    return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (nlev > hattn_gdn_fwd_max_levels())
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_fwd_max_levels());
+  if (dtype_qkv != HATTN_BF16 || dtype_do != HATTN_BF16)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v/do dtype codes %d/%d (bf16 required)", dtype_qkv,
+                dtype_do);
+  if (!q || !k || !v || !beta || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !db || !dg || !dl)
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_gdn_bwd_ws_bytes(B, T, H, K, V, nlev);
+  if (workspace_bytes < need || workspace == nullptr)
+    return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  int unsupported = 0;
+  hipError_t e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl,
+                                      workspace, B, T, H, K, V, L, nlev, dtype_beta, dtype_l,
+                                      (hipStream_t)stream, &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);
+  return check_hip(e, "hattn_gdn_chunkwise_bwd launch");
 }
 
 }  // extern "C"

@@ -32,6 +32,10 @@ SIGNATURES = [
      [_P, _P, _P, _P, _F, _P, _P, _F, _P, _P, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
      + [_P, _S, _P]),
     ("hattn_gdn_chunkwise_fwd_workspace", _S, [_I] * 6),
+    ("hattn_gdn_chunkwise_bwd", _I,
+     [_P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4
+     + [_I] * 3 + [_P, _S, _P]),
+    ("hattn_gdn_chunkwise_bwd_workspace", _S, [_I] * 6),
 ]
 
 _lock = threading.Lock()

@@ -1,15 +1,17 @@
 """Host driver of the log-linear Gated DeltaNet chunkwise path (MI355X).
 
-Same name, arguments and return tuple as hattention/chunkwise_hgdn.py:
+Same names, arguments and return tuples as hattention/chunkwise_hgdn.py:
 * ``chunkwise_fwd(q, k, v, b, g, l, head_first, level_base, htype, chunk_size,
   output_final_state) -> (g_cumsum, o, Aw, Au, ht)``   -- chunkwise_hgdn.py:566-788
+* ``chunkwise_bwd(q, k, v, b, g, l, Aw, Au, do, head_first, level_base, htype,
+  chunk_size) -> (dq, dk, dv, db, dg, dl)``            -- chunkwise_hgdn.py:791-1222
 
 Validation follows the reference (``ValueError`` for T % 64 and K / V not
 multiples of the block options, ``NotImplementedError`` for K > 256 and modes
 outside the weak base-2 hierarchy).  Grouped q / k are expanded per head
-before the kernels like the reference (chunkwise_hgdn.py:614-623).  There is
-no CPU path.  The GDN backward (chunkwise_hgdn.py:791-1222) is not part of
-this build yet.
+before the kernels like the reference (chunkwise_hgdn.py:614-623) and their
+gradients summed over the group (chunkwise_hgdn.py:1208-1215).  There is no
+CPU path.
 """
 from typing import Optional, Tuple
 
@@ -21,23 +23,11 @@ from hattention.base import HType, get_num_levels, ceil_log
 CHUNK = 64
 
 
-def chunkwise_fwd(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    b: torch.Tensor,
-    g: torch.Tensor,
-    l: torch.Tensor,
-    head_first: bool,
-    level_base: int,
-    htype: HType,
-    chunk_size: int,
-    output_final_state: bool,
-) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """Log-linear GDN forward; returns (g_cumsum, o, Aw, Au, ht) like the reference."""
+def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
+    """chunkwise_hgdn.py:589-612 and :818-858: returns (B, T, G, H, K, V, L)."""
     if head_first:
         raise NotImplementedError("head_first=True is not supported (time-first layout only)")
-    for name, t in dict(q=q, k=k, v=v, b=b, g=g, l=l).items():
+    for name, t in dict(q=q, k=k, v=v, l=l, **tensors).items():
         if not t.is_contiguous():
             raise ValueError(f"Tensor argument {name} must be contiguous")
     B, T, G, K = k.shape
@@ -60,6 +50,25 @@ def chunkwise_fwd(
             raise ValueError(f"V={V} and BV could be {bs}")
     if get_num_levels(CHUNK, level_base) + ceil_log(T // CHUNK, level_base) > L:
         raise ValueError(f"L={L} levels are too few for T={T}")
+    return B, T, G, H, K, V, L
+
+
+def chunkwise_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    b: torch.Tensor,
+    g: torch.Tensor,
+    l: torch.Tensor,
+    head_first: bool,
+    level_base: int,
+    htype: HType,
+    chunk_size: int,
+    output_final_state: bool,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Log-linear GDN forward; returns (g_cumsum, o, Aw, Au, ht) like the reference."""
+    B, T, G, H, K, V, L = _validate(q, k, v, l, head_first, level_base, htype, chunk_size,
+                                    b=b, g=g)
     if g.dtype != torch.float32:
         raise ValueError("g (log-decay) must be float32")
     dev = _lib.require_device(q, k, v, b, g, l)
@@ -84,6 +93,56 @@ def chunkwise_fwd(
     return g_cumsum, o, Aw, Au, ht
 
 
-def hgdn_backward(*args, **kwargs):
-    """chunkwise_hgdn.chunkwise_bwd (chunkwise_hgdn.py:791-1222): not built yet."""
-    raise NotImplementedError("the MI355X log-linear GDN backward is not built yet")
+def chunkwise_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    b: torch.Tensor,
+    g: torch.Tensor,
+    l: torch.Tensor,
+    Aw: torch.Tensor,
+    Au: torch.Tensor,
+    do: torch.Tensor,
+    head_first: bool,
+    level_base: int,
+    htype: HType,
+    chunk_size: int,
+):
+    """Log-linear GDN backward (chunkwise_hgdn.py:791-1222).
+
+    ``g`` is the forward's chunk-local cumsum.  Returns (dq, dk, dv, db, dg, dl):
+    dq / dk / dv / db in the dtypes of q / k / v / b, dg (w.r.t. the per-step g)
+    and dl in fp32, like the reference.  ``Aw`` / ``Au`` are accepted for the
+    reference's signature; the kernels recompute (I + A)^-1 in fp32.
+    """
+    B, T, G, H, K, V, L = _validate(q, k, v, l, head_first, level_base, htype, chunk_size,
+                                    b=b, g=g, do=do)
+    if g.dtype != torch.float32 or g.shape != (B, T, H):
+        raise ValueError("g must be the fp32 chunk-local cumsum [B, T, H]")
+    if do.shape != v.shape:
+        raise ValueError("do must have the shape of v")
+    dev = _lib.require_device(q, k, v, b, g, l, do)
+    if G != H:
+        q = q.repeat_interleave(H // G, dim=2).contiguous()
+        k = k.repeat_interleave(H // G, dim=2).contiguous()
+    do = do.to(v.dtype).contiguous()
+    dq = torch.empty(B, T, H, K, dtype=q.dtype, device=dev)
+    dk = torch.empty(B, T, H, K, dtype=k.dtype, device=dev)
+    dv = torch.empty_like(v)
+    db = torch.empty_like(b)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_gdn_chunkwise_bwd_workspace(B, T, H, K, V, L), dev)
+    st = lib.hattn_gdn_chunkwise_bwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
+        _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+        _lib.ptr(db), _lib.ptr(dg), _lib.ptr(dl), B, T, H, K, V, L, _lib.dtype_code(q),
+        _lib.dtype_code(b), _lib.dtype_code(l), _lib.dtype_code(do), level_base, htype.value,
+        chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
+    _lib.check(st)
+    if G != H:
+        dq = dq.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(q.dtype)
+        dk = dk.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(k.dtype)
+    return dq, dk, dv, db, dg, dl

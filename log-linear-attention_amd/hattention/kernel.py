@@ -49,6 +49,21 @@ def l2norm_and_scale_fwd(x: torch.Tensor, scale: float) -> torch.Tensor:
     return l2norm_fwd(x) * scale
 
 
+def l2norm_bwd(x: torch.Tensor, dy: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Gradient of y = x / sqrt(||x||^2 + eps): dx = r (dy - y (y . dy)), r =
+    (||x||^2 + eps)^-1/2, in fp32, cast to x.dtype (fla.modules.l2norm.l2norm_bwd,
+    used at kernel.py:24-29, 224-225)."""
+    xf, dyf = x.float(), dy.float()
+    r = torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)
+    y = xf * r
+    return (r * (dyf - y * (y * dyf).sum(-1, keepdim=True))).to(x.dtype)
+
+
+def l2norm_and_scale_bwd(x: torch.Tensor, dy: torch.Tensor, scale: float) -> torch.Tensor:
+    """kernel.py:24-29: gradient of l2norm(x) * scale."""
+    return l2norm_bwd(x, dy.float() * scale)
+
+
 class HAttentionFunction(torch.autograd.Function):
     """kernel.py:32-244."""
 
@@ -114,11 +129,19 @@ class HAttentionFunction(torch.autograd.Function):
         elif ctx.hstruct == HStruct.GDELTA and ctx.chunkwise:
             if b is None or Aw is None or Au is None:
                 raise ValueError
+            if ctx.chunk_sizes[0] != ctx.chunk_sizes[1]:
+                raise NotImplementedError
+            if not ctx.use_qk_l2norm_in_kernel:
+                raise NotImplementedError
+            if ctx.scale is None:
+                raise NotImplementedError
             from hattention import chunkwise_hgdn as _hg
-            dq, dk, dv, db, dg, dl = _hg.hgdn_backward(
-                q=q, k=k, v=v, b=b, g=g, l=l, Aw=Aw, Au=Au, do=do, scale=ctx.scale,
-                head_first=ctx.head_first, level_base=ctx.level_base, htype=ctx.htype,
-                chunk_size=ctx.chunk_sizes[0])
+            dq, dk, dv, db, dg, dl = _hg.chunkwise_bwd(
+                q=l2norm_and_scale_fwd(q, scale=ctx.scale), k=l2norm_fwd(k), v=v, b=b, g=g, l=l,
+                Aw=Aw, Au=Au, do=do, head_first=ctx.head_first, level_base=ctx.level_base,
+                htype=ctx.htype, chunk_size=ctx.chunk_sizes[0])
+            dq = l2norm_and_scale_bwd(q, dq, scale=ctx.scale)
+            dk = l2norm_bwd(k, dk)
         else:
             raise NotImplementedError
         return (dq.to(q), dk.to(k), dv.to(v), db.to(b) if b is not None else None,

@@ -105,3 +105,40 @@ def test_status_maps_to_reference_exceptions():
     with pytest.raises(NotImplementedError):
         _lib.check(_lib.HATTN_ERR_NOT_IMPLEMENTED)
     assert lib.hattn_last_error() is not None
+
+
+def _gdn_bwd(**kw):
+    a = dict(B=1, T=128, H=1, K=64, V=64, L=8, dq=0, db=0, dl=0, do=0, base=2, htype=0,
+             chunk=64, ws=1 << 30)
+    a.update(kw)
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: every case fails validation first
+    return lib.hattn_gdn_chunkwise_bwd(p, p, p, p, p, p, None, None, p, p, p, p, p, p, p,
+                                       a["B"], a["T"], a["H"], a["K"], a["V"], a["L"], a["dq"],
+                                       a["db"], a["dl"], a["do"], a["base"], a["htype"],
+                                       a["chunk"], p, a["ws"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(T=100), _lib.HATTN_ERR_VALUE),            # T % 64
+    (dict(L=7), _lib.HATTN_ERR_VALUE),              # L < 7 + ceil(log2(T/64))
+    (dict(K=96, V=96), _lib.HATTN_ERR_VALUE),       # K, V multiples of 64
+    (dict(K=320, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # K > 256
+    (dict(K=128, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # do must be bf16
+    (dict(T=64 << 8, L=16), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > 7 inter-chunk levels
+    (dict(ws=16), _lib.HATTN_ERR_VALUE),            # workspace too small
+])
+def test_gdn_bwd_argument_checks(kw, code):
+    assert _gdn_bwd(**kw) == code
+    assert _lib.load().hattn_last_error().decode()
+
+
+def test_gdn_bwd_workspace_query():
+    lib = _lib.load()
+    assert lib.hattn_gdn_chunkwise_bwd_workspace(1, 100, 1, 64, 64, 8) == 0
+    small = lib.hattn_gdn_chunkwise_bwd_workspace(1, 1024, 2, 64, 64, 11)
+    big = lib.hattn_gdn_chunkwise_bwd_workspace(1, 2048, 2, 64, 64, 12)
+    assert 0 < small < big

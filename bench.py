@@ -118,6 +118,20 @@ def gdn_fwd_flops(B, T, H, K, V):
                     + 5 * T * K * V * nlev)
 
 
+def _time_region(fn, n, stream):
+    """Run fn n times; return (wall seconds per call, HIP-event seconds per call on
+    the launch stream)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(n):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / n, e0.elapsed_time(e1) / 1e3 / n
+
+
 def cpu_baseline(seconds_budget=30.0):
     """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
     chunkwise algorithm) on the host cores, on the north-star workload (median
@@ -249,41 +263,44 @@ def main():
                            "avg_step_us": ev_fb * 1e6,
                            "mfma_frac": (flops + bwd_flops(B, T, H, K, V)) / ev_fb
                            / MFMA_BF16_PEAK}}
-    # log-linear Gated DeltaNet forward at BASELINE config 3 (MFMA-bound path)
-    gdn = None
+    # log-linear Gated DeltaNet at BASELINE config 3 (MFMA-bound path): forward,
+    # and forward + backward (chunkwise_hgdn.chunkwise_fwd / chunkwise_bwd)
+    gdn = gdn_fb = None
     if not args.fwd_only:
-        from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd
+        from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd, chunkwise_bwd as gdn_bwd
         GB, GT, GH, GK, GL = 4, 8192, 16, 128, 14
         gq, gk, gv, gbeta, gg, gl = make_gdn_inputs(GB, GT, GH, GK, GK, GL, device=dev)
+        gdo = torch.randn(GB, GT, GH, GK, device=dev, dtype=torch.bfloat16)
+        gcfg = {"workload": "log-linear Gated DeltaNet chunkwise path (chunkwise_hgdn, "
+                            "BASELINE config 3)",
+                "batch": GB, "seq_len": GT, "heads": GH, "dk": GK, "dv": GK, "levels": GL}
 
         def gdn_step():
             return gdn_fwd(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64, False)
 
-        for _ in range(max(1, args.warmup)):
-            gdn_step()
-        torch.cuda.synchronize()
-        ng = max(1, args.steps // 2)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(ng):
-            gdn_step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        wall_g = (time.perf_counter() - t0) / ng
-        ev_g = e0.elapsed_time(e1) / 1e3 / ng
+        def gdn_fb_step():
+            gc, _, Aw, Au, _ = gdn_step()
+            return gdn_bwd(gq, gk, gv, gbeta, gc, gl, Aw, Au, gdo, False, 2, HType.WEAK, 64)
+
         gfl = gdn_fwd_flops(GB, GT, GH, GK, GK)
-        gdn = {"value": GB * GT / wall_g, "unit": "tokens/s", "ms_per_step": wall_g * 1e3,
-               "steps": ng,
-               "config": {"workload": "log-linear Gated DeltaNet chunkwise forward "
-                                      "(chunkwise_hgdn.chunkwise_fwd, BASELINE config 3)",
-                          "batch": GB, "seq_len": GT, "heads": GH, "dk": GK, "dv": GK,
-                          "levels": GL},
-               "roofline": {"bound": "mfma", "achieved": gfl / ev_g / 1e12,
-                            "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                            "frac": gfl / ev_g / MFMA_BF16_PEAK, "algorithmic_flops": gfl,
-                            "avg_step_us": ev_g * 1e6}}
-        del gq, gk, gv, gbeta, gg, gl
+        for fn, key in ((gdn_step, "fwd"), (gdn_fb_step, "fwd_bwd")):
+            for _ in range(max(1, args.warmup)):
+                fn()
+            n = max(1, args.steps // 2)
+            wall_g, ev_g = _time_region(fn, n, stream)
+            # backward counted as twice the forward (the usual convention)
+            fl = gfl if key == "fwd" else 3 * gfl
+            rec = {"value": GB * GT / wall_g, "unit": "tokens/s", "ms_per_step": wall_g * 1e3,
+                   "steps": n, "config": gcfg,
+                   "roofline": {"bound": "mfma", "achieved": fl / ev_g / 1e12,
+                                "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                                "frac": fl / ev_g / MFMA_BF16_PEAK, "algorithmic_flops": fl,
+                                "avg_step_us": ev_g * 1e6}}
+            if key == "fwd":
+                gdn = rec
+            else:
+                gdn_fb = rec
+        del gq, gk, gv, gbeta, gg, gl, gdo
 
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
@@ -304,6 +321,7 @@ def main():
                    "dtype_qkv_lambda": "bf16", "dtype_g": "fp32"},
         "fwd_bwd": fb,
         "gdn_fwd": gdn,
+        "gdn_fwd_bwd": gdn_fb,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,

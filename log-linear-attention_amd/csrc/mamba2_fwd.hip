@@ -40,6 +40,79 @@
 namespace hattn {
 
 // ---------------------------------------------------------------------------
+// Kernel 1b: the top-level states every segment reads
+// ---------------------------------------------------------------------------
+// A scan over the segments of one row: per top level e2 (inter-chunk level
+// s + e2, blocks of 2^(e2 + 1) segments) the state
+//   h <- (p ends its aligned block ? 0 : exp(D_p) h) + (bit e2 of p clear ? Sum(p) : 0)
+// is read (before the update) by the segments with bit e2 set, which is
+// Htop_e2(p).  One workgroup per (row, 64-column block of V, quarter of the
+// 64 x 64 tile); each thread owns 4 consecutive elements and streams the
+// row's summaries.  Output: NP bf16 planes [row][p][e2][vblk][plane][64][64],
+// written only where segment p reads level e2.
+template <int NP>
+__global__ __launch_bounds__(256) void mamba2_htop_kernel(const float* __restrict__ sums,
+                                                          const float* __restrict__ segd,
+                                                          __bf16* __restrict__ htop, int V,
+                                                          int NSEG, int ntop, int nvb64) {
+  const int quarter = blockIdx.x & 3;
+  const int vblk = (blockIdx.x >> 2) % nvb64;
+  const int row = (blockIdx.x >> 2) / nvb64;
+  const int el = quarter * 1024 + 4 * threadIdx.x;
+  const int kk = el >> 6, c = el & 63;
+  const float* src = sums + ((size_t)row * NSEG * kKD + kk) * V + vblk * 64 + c;
+  const size_t sstride = (size_t)kKD * V;
+  __bf16* dst = htop + (size_t)row * NSEG * ntop * nvb64 * NP * (kKD * 64) + (size_t)vblk * NP * (kKD * 64) + el;
+  const size_t pstride = (size_t)ntop * nvb64 * NP * (kKD * 64), estride = (size_t)nvb64 * NP * (kKD * 64);
+  const float* dp = segd + (size_t)row * NSEG;
+  floatx4 h[kMaxTop];
+#pragma unroll
+  for (int e2 = 0; e2 < kMaxTop; ++e2) h[e2] = zero4();
+  constexpr int kBatch = 8;   // summaries loaded per round, all in flight together
+  for (int p0 = 0; p0 < NSEG; p0 += kBatch) {
+    floatx4 xs[kBatch];
+    float ds[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int pj = p0 + j < NSEG ? p0 + j : NSEG - 1;
+      xs[j] = *(const floatx4*)(src + (size_t)pj * sstride);
+      ds[j] = dp[pj];
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+    const int p = p0 + j;
+    if (p >= NSEG) break;
+    const floatx4 x = xs[j];
+    const float dec = fexp(ds[j]);
+#pragma unroll
+    for (int e2 = 0; e2 < kMaxTop; ++e2) {
+      if (e2 < ntop) {
+        const bool rd = (p >> e2) & 1;
+        if (rd) {
+          bf16x4 hi, lo;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            hi[jj] = (__bf16)h[e2][jj];
+            lo[jj] = bf16_lo(h[e2][jj], hi[jj]);
+          }
+          __bf16* o = dst + (size_t)p * pstride + (size_t)e2 * estride;
+          *(bf16x4*)o = hi;
+          if constexpr (NP == 2) *(bf16x4*)(o + kKD * 64) = lo;
+        }
+        const int per = 2 << e2;
+        if ((p & (per - 1)) == per - 1) {
+          h[e2] = zero4();
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) h[e2][jj] = h[e2][jj] * dec + (rd ? 0.f : x[jj]);
+        }
+      }
+    }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Kernel 2: main pass over one segment, one 64-wide block of V
 // ---------------------------------------------------------------------------
 // NP bf16 planes per operand: 1 (bf16 inputs, bf16 MFMA) or 2 (fp32 inputs as
@@ -91,8 +164,8 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
     const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
-    const float* __restrict__ segd, int B, int T, int G, int H, int V, int L, int nlev,
-    int nvb64, int slog, int NSEG, int final_state) {
+    const float* __restrict__ segd, const __bf16* __restrict__ htop, int B, int T, int G, int H,
+    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state) {
   using Smem = MainSmem<NP, MAXLOC>;
   constexpr int kPl = kKD * kLd;                         // one bf16 plane of a 64 x 64 tile
   constexpr int kLR = (Stage<NP, MAXLOC>::LU + 3) / 4;   // lambda registers per thread
@@ -118,53 +191,67 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
   const bool is_final_seg = final_state && ht != nullptr && p == NSEG - 1;
   float* htb = ht ? ht + ((size_t)b * H + h) * kKD * V * L : nullptr;
 
-  // ---- top levels: Htop_e(p) from the segment summaries -> LDS -----------------
+  // ---- top levels: Htop_e(p) (from the scan kernel) -> LDS ---------------------
   if (ntop > 0) {
-    const float* sp = sums + (size_t)row * NSEG * kKD * V + vc;
+    const __bf16* hsrc = htop + (((size_t)row * NSEG + p) * ntop * nvb64 + vblk) * NP * (kKD * 64);
+    for (int e2 = 0; e2 < ntop; ++e2) {
+      if (!((p >> e2) & 1)) continue;
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* src = hsrc + ((size_t)e2 * nvb64 * NP + pl) * (kKD * 64);
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int u = tid + 256 * rr, r = u >> 3, c = 8 * (u & 7);
+          *(uint4*)(sm.top + (e2 * NP + pl) * kPl + r * kLd + c) = *(const uint4*)(src + r * 64 + c);
+        }
+      }
+    }
+  }
+  if (ntop > 0 && is_final_seg) {
+    // final states of the top levels (chunkwise.py:229-279): a level the last
+    // chunk reads holds its block decayed over segment p; one it writes holds
+    // segments [lo, p] decayed to the end of p.  P[q] = sum_{r < q} D_r in LDS
+    // (the A tile is free until the first chunk).
+    float* pre = (float*)sm.a[0];
     const float* dp = segd + (size_t)row * NSEG;
+    if (w == 0) {
+      float carry = 0.f;
+      for (int base = 0; base <= p + 1; base += 64) {
+        const int q = base + lane;
+        const float x = q <= p ? dp[q] : 0.f;
+        float y = x;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float z = __shfl_up(y, d, 64);
+          if (lane >= d) y += z;
+        }
+        if (q <= p + 1) pre[q] = carry + y - x;
+        carry += __shfl(y, 63, 64);
+      }
+    }
+    __syncthreads();
+    const float* sp = sums + (size_t)row * NSEG * kKD * V + vc;
     const size_t qstride = (size_t)kKD * V;
     for (int e2 = 0; e2 < ntop; ++e2) {
       const bool reads = (p >> e2) & 1;
-      if (!reads && !is_final_seg) continue;
-      // reads: block [lo, lo + 2^e2) decayed to the start of p;
-      // final state of a level the last chunk writes: segments [lo, p] decayed to the end
       const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
       const int hi = reads ? lo + (1 << e2) : p + 1;
-      float dlog = 0.f;
-      for (int r = hi; r < p; ++r) dlog += dp[r];
       floatx4 hacc[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) hacc[m] = zero4();
-      for (int qs = hi - 1; qs >= lo; --qs) {
-        const float sc = fexp(dlog);
+      for (int qs = lo; qs < hi; ++qs) {
+        const float sc = fexp(pre[p + 1] - pre[qs + 1]);
         const float* src = sp + qs * qstride;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
           for (int i = 0; i < 4; ++i) hacc[m][i] += sc * src[(size_t)(16 * m + 4 * lq + i) * V];
-        dlog += dp[qs];
       }
-      if (reads) {
-        __bf16* tp = sm.top + e2 * NP * kPl + 16 * w + ln;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+      for (int m = 0; m < 4; ++m)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const __bf16 hv = (__bf16)hacc[m][i];
-            tp[(16 * m + 4 * lq + i) * kLd] = hv;
-            if constexpr (NP == 2) tp[kPl + (16 * m + 4 * lq + i) * kLd] = bf16_lo(hacc[m][i], hv);
-          }
-      }
-      if (is_final_seg) {
-        // final state (chunkwise.py:229-279): a level the last chunk reads holds
-        // its block decayed over segment p; one it writes holds [lo, p]
-        const float sc = reads ? fexp(dp[p]) : 1.f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            htb[((size_t)(16 * m + 4 * lq + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i] * sc;
-      }
+        for (int i = 0; i < 4; ++i)
+          htb[((size_t)(16 * m + 4 * lq + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i];
     }
   }
 
@@ -458,16 +545,41 @@ size_t segd_bytes(size_t rows, int NSEG) {
   return (rows * NSEG * sizeof(float) + 255) & ~(size_t)255;
 }
 int max_loc(int x3) { return x3 ? hattn::kMaxLocX3 : hattn::kMaxLoc; }
-}  // namespace
 
 // x3: fp32 q / k / v / lambda computed as bf16x3 (more local levels per segment).
-size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3) {
+// Workspace: segment log-decays, segment summaries (fp32 [row][seg][K][V]) and
+// the top-level states (bf16 planes [row][seg][level][vblk][plane][64][64]).
+struct FwdWs {
+  float* segd;
+  float* sums;
+  __bf16* htop;
+  size_t bytes;
+};
+
+FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   const int NT = T / hattn::kBT;
   const int slog = hattn::seg_log2(NT, max_loc(x3));
   const int NSEG = (NT + (1 << slog) - 1) >> slog;
-  if (NSEG <= 1) return 0;
+  int nlev = 0;
+  while ((1 << nlev) < NT) ++nlev;
+  const int ntop = nlev - (slog < nlev ? slog : nlev);
+  FwdWs w{nullptr, nullptr, nullptr, 0};
+  if (NSEG <= 1) return w;
   const size_t rows = (size_t)B * H;
-  return segd_bytes(rows, NSEG) + rows * NSEG * hattn::kKD * V * sizeof(float);
+  char* p = (char*)base;
+  const size_t a = segd_bytes(rows, NSEG);
+  const size_t b = (rows * NSEG * hattn::kKD * V * sizeof(float) + 255) & ~(size_t)255;
+  const size_t c = rows * NSEG * ntop * (size_t)(V / 64) * (x3 ? 2 : 1) * hattn::kKD * 64 * 2;
+  w.segd = (float*)p;
+  w.sums = (float*)(p + a);
+  w.htop = (__bf16*)(p + a + b);
+  w.bytes = a + b + c;
+  return w;
+}
+}  // namespace
+
+size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3) {
+  return fwd_ws_layout(nullptr, B, T, H, V, x3).bytes;
 }
 
 // Largest inter-chunk level count: register-resident local levels plus the
@@ -493,16 +605,20 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
   const int NSEG = (NT + S - 1) / S;
   const int rows = B * H;
   const int nvb64 = V / 64;
-  float* segd = nullptr;
-  float* sums = nullptr;
+  const FwdWs w = fwd_ws_layout(ws, B, T, H, V, NP == 2);
+  const int ntop = nlev - min(slog, nlev);
   if (NSEG > 1) {
-    segd = (float*)ws;
-    sums = (float*)((char*)ws + segd_bytes(rows, NSEG));
     auto sk = mamba2_seg_sum_kernel<TK, TV, false, NP>;
     hipLaunchKernelGGL(sk, dim3(rows * NSEG * nvb64), dim3(256), 0, stream, (const TK*)k,
-                       (const TV*)v, g, sums, segd, T, G, H, V, NT, S, NSEG, nvb64);
+                       (const TV*)v, g, w.sums, w.segd, T, G, H, V, NT, S, NSEG, nvb64);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (ntop > 0) {
+      auto hk = mamba2_htop_kernel<NP>;
+      hipLaunchKernelGGL(hk, dim3(rows * nvb64 * 4), dim3(256), 0, stream, w.sums, w.segd,
+                         w.htop, V, NSEG, ntop, nvb64);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
   }
   const int smem = main_smem_bytes<NP, MAXLOC>(nlev - min(slog, nlev));
   const int rows8 = (rows * NSEG + 7) / 8;
@@ -512,8 +628,9 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const TK*)q, (const TK*)k,
-                     (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, sums, segd, B, T, G, H, V,
-                     L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
+                     (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, w.sums, w.segd,
+                     (const __bf16*)w.htop, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
+                     ht != nullptr ? 1 : 0);
   return hipGetLastError();
 }
 

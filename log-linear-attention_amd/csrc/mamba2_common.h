@@ -76,15 +76,27 @@ __device__ __forceinline__ void store_tile64(const Tile64<T>& t, __bf16* p0, __b
   }
 }
 
+// DPP move of a float: lanes whose source is outside the row read 0, rows
+// outside row_mask keep `old`.
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ float dpp_f32(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, src), CTRL,
+                                                               ROW_MASK, 0xf, BOUND_ZERO));
+}
+
 // Inclusive cumsum of g over the 64 tokens of a chunk (fla chunk_local_cumsum,
 // chunkwise.py:1175); lane l holds g[t = l] on entry and Gc[l] on exit.
+// Hillis-Steele within each 16-lane row (DPP row_shr 1, 2, 4, 8), then the row
+// totals are carried with row_bcast:15 (into rows 1, 3) and row_bcast:31 (into
+// rows 2, 3): six VALU ops, no LDS round trips.
 __device__ __forceinline__ float chunk_cumsum(float x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+  x += dpp_f32<0x111, 0xf, true>(0.f, x);   // row_shr:1
+  x += dpp_f32<0x112, 0xf, true>(0.f, x);   // row_shr:2
+  x += dpp_f32<0x114, 0xf, true>(0.f, x);   // row_shr:4
+  x += dpp_f32<0x118, 0xf, true>(0.f, x);   // row_shr:8
+  x += dpp_f32<0x142, 0xa, false>(0.f, x);  // row_bcast:15
+  x += dpp_f32<0x143, 0xc, false>(0.f, x);  // row_bcast:31
   return x;
 }
 
@@ -104,6 +116,11 @@ struct SumSmem {
 
 // GCUM: g already holds the chunk-local inclusive cumsum (the backward's input,
 // chunkwise.py:1286-1299) instead of per-step log-decays.
+//
+// The decay weights w_s = exp(G_end - G_s) are applied to the wave's own K^T
+// fragment (16 k rows), so the V fragments enter the MFMA as staged.  Two
+// chunks wait in registers while one is multiplied from LDS, so every load has
+// two chunk iterations to land.
 template <typename TK, typename TV, bool GCUM, int NP>
 __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
     const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
@@ -131,33 +148,42 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   for (int n = 0; n < 4; ++n) acc[n] = zero4();
   float dsum = 0.f;
 
-  Tile64<TK> kr;
-  Tile64<TV> vr;
-  float gr = 0.f;
-#define SEG_LOAD(jj)                                                                   \
-  {                                                                                    \
-    const unsigned int row0 = (unsigned int)(c0 + (jj)) * kBT;                         \
-    load_tile64(kr, rk, vo_k, row0 * kstr * sizeof(TK), kstr);                         \
-    load_tile64(vr, rv, vo_v, row0 * vstr * sizeof(TV), vstr);                        \
-    if (w == 0) gr = buf_load<float>(rgg, vo_g, row0 * H * 4);                         \
-  }
-#define SEG_STORE(buf)                                                                 \
-  {                                                                                    \
-    store_tile64<NP>(kr, sm.k[buf][0], sm.k[buf][NP - 1]);                             \
-    store_tile64<NP>(vr, sm.v[buf][0], sm.v[buf][NP - 1]);                             \
-    if (w == 0) {                                                                      \
-      const float x = GCUM ? gr : chunk_cumsum(gr);                                    \
-      const float last = __shfl(x, 63, 64);                                            \
-      sm.wt[buf][lane] = fexp(last - x);                                               \
-      if (lane == 0) sm.cl[buf] = last;                                                \
-    }                                                                                  \
-  }
-  SEG_LOAD(0);
-  SEG_STORE(0);
-  if (nch > 1) SEG_LOAD(1);
+  Tile64<TK> kr[2];
+  Tile64<TV> vr[2];
+  float gr[2] = {0.f, 0.f};
+  auto seg_load = [&](int jj, int slot) {   // chunk jj of the segment -> register slot
+    if (jj >= nch) return;
+    const unsigned int row0 = (unsigned int)(c0 + jj) * kBT;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      if (s == slot) {
+        load_tile64(kr[s], rk, vo_k, row0 * kstr * sizeof(TK), kstr);
+        load_tile64(vr[s], rv, vo_v, row0 * vstr * sizeof(TV), vstr);
+        if (w == 0) gr[s] = buf_load<float>(rgg, vo_g, row0 * H * 4);
+      }
+  };
+  auto seg_store = [&](int slot, int buf) {   // register slot -> LDS buffer
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      if (s == slot) {
+        store_tile64<NP>(kr[s], sm.k[buf][0], sm.k[buf][NP - 1]);
+        store_tile64<NP>(vr[s], sm.v[buf][0], sm.v[buf][NP - 1]);
+        if (w == 0) {
+          const float x = GCUM ? gr[s] : chunk_cumsum(gr[s]);
+          const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+          sm.wt[buf][lane] = fexp(last - x);
+          if (lane == 0) sm.cl[buf] = last;
+        }
+      }
+  };
+  // chunk j is multiplied from LDS buffer j & 1; chunks j + 1, j + 2 wait in
+  // register slots (j + 1) & 1, j & 1
+  seg_load(0, 0);
+  seg_load(1, 1);
+  seg_store(0, 0);
+  seg_load(2, 0);
   __syncthreads();
-  for (int j = 0; j < nch; ++j) {
-    const int buf = j & 1;
+  auto step = [&](int j, int buf, int slot_next) {
     const float clast = sm.cl[buf];
     const float dl = fexp(clast);
     dsum += clast;
@@ -167,37 +193,40 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
       for (int i = 0; i < 4; ++i) acc[n][i] *= dl;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      bf16x8 a[NP];   // K^T[k][t]
-#pragma unroll
-      for (int pl = 0; pl < NP; ++pl) a[pl] = tr_frag(sm.k[buf][pl], kLd, 32 * c, 16 * w);
+      // A: (K^T diag(w))[k = 16w + ln][s = 32c + 8lq + jj], NP planes
       const floatx4 w0 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq]);
       const floatx4 w1 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq + 4]);
+      float ka[8];
+      {
+        const bf16x8 kh = tr_frag(sm.k[buf][0], kLd, 32 * c, 16 * w);
+        bf16x8 kl{};
+        if constexpr (NP == 2) kl = tr_frag(sm.k[buf][1], kLd, 32 * c, 16 * w);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float x = NP == 2 ? (float)kh[jj] + (float)kl[jj] : (float)kh[jj];
+          ka[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
+        }
+      }
+      bf16x8 a[NP];
+      split8<NP>(ka, a);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        float wv[8];   // w o V[t][v], fp32
-        {
-          const bf16x8 vh = tr_frag(sm.v[buf][0], kLd, 32 * c, 16 * n);
-          bf16x8 vl{};
-          if constexpr (NP == 2) vl = tr_frag(sm.v[buf][1], kLd, 32 * c, 16 * n);
+        bf16x8 bv[NP];   // V[s][v = 16n + ln]
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            const float x = NP == 2 ? (float)vh[jj] + (float)vl[jj] : (float)vh[jj];
-            wv[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
-          }
-        }
-        bf16x8 bv[NP];
-        split8<NP>(wv, bv);
+        for (int pl = 0; pl < NP; ++pl) bv[pl] = tr_frag(sm.v[buf][pl], kLd, 32 * c, 16 * n);
         acc[n] = mma<NP>(a, bv, acc[n]);
       }
     }
     if (j + 1 < nch) {
-      SEG_STORE(buf ^ 1);
-      if (j + 2 < nch) SEG_LOAD(j + 2);
+      seg_store(slot_next, buf ^ 1);
+      seg_load(j + 3, slot_next);
     }
     __syncthreads();
+  };
+  for (int j = 0; j < nch; j += 2) {
+    step(j, 0, 1);
+    if (j + 1 < nch) step(j + 1, 1, 0);
   }
-#undef SEG_LOAD
-#undef SEG_STORE
   float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
 #pragma unroll
   for (int n = 0; n < 4; ++n)

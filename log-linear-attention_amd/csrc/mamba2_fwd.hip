@@ -535,6 +535,525 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Kernel 2 (bf16 inputs): main pass, output computed transposed
+// ---------------------------------------------------------------------------
+// Same segment walk and the same three phases as mamba2_fwd_main_kernel, laid
+// out so that a wave issues as few instructions per chunk as possible:
+//   * every product of phase 2 is computed as o^T (rows v, columns t), so the
+//     lambda weight of a level is one scalar per lane and tile, and a lane
+//     stores 4 consecutive v of one token (one 8-byte store per t-tile);
+//   * the Q fragments are read from LDS once per chunk and serve both as the
+//     B operand of S^T = K Q^T (phase 1) and of o^T += h^T Q^T (phase 2);
+//   * the level states are produced by phase 3 with the contraction index in
+//     natural order (k = 32c + 8lq + j), by pointing the transposing LDS reads
+//     of K^T at column blocks 32c + 8(lane & 3) + 4h; so states, Q and the
+//     top-level states (stored [v][k]) all pair by plain 16-byte fragments;
+//   * only the levels a chunk reads are computed (uniform branches);
+//   * a local state carries a pending log-decay instead of being rescaled
+//     every chunk: h_e = st_e * 2^dl_e, rescaled only when it is written.
+// LDS holds the chunk stage (single-buffered; the next chunk waits in
+// registers), the A tile, lambda and decay vectors and the top-level states.
+struct Bf16Smem {
+  __bf16 q[kBT * kLd];        // Q[t][k]
+  __bf16 k[kBT * kLd];        // K[s][k]
+  __bf16 v[kBT * kLd];        // V[s][v] (this workgroup's 64 columns)
+  __bf16 a[kBT * kLd];        // A[t][s] = (S o M)[t][s]
+  float gc[kBT];              // log2(e) * chunk-local inclusive cumsum of g
+  float wt[kBT];              // exp(Gc_last - Gc_s)
+  float li[7 * kBT];          // lambda[t][lev] at [lev][t], intra levels 0..6
+  float lp[(kMaxLoc + kMaxTop) * kBT];  // exp(Gc_t) lambda[t][7 + e] at [e][ln][nt]
+  __bf16 top[1];              // [ntop][v][kLd] top-level states, transposed
+};
+
+inline int bf16_smem_bytes(int ntop) {
+  return (int)offsetof(Bf16Smem, top) + ntop * kKD * kLd * 2;
+}
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// K^T fragment with the contraction over s: lane (lq, ln) receives
+// K[s = r0 + 8lq + j][k = 32c + 8(ln >> 2) + 4h + (ln & 3)], j = 0..7, so the D
+// rows 4lq + i of the product are k = 32c + 8lq + 4h + i.
+__device__ __forceinline__ bf16x8 ktr_frag(const __bf16* X, int r0, int c, int h, int lq, int ln) {
+  const __bf16* p = X + (r0 + 8 * lq + (ln >> 2)) * kLd + 32 * c + 8 * (ln & 3) + 4 * h;
+  const bf16x4 lo = ds_read_tr(p);
+  const bf16x4 hi = ds_read_tr(p + 4 * kLd);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Phase-1 schedule: the 10 causal tiles plus the two zero tiles the 32-wide s
+// steps of A V read above the diagonal ((0,1), (2,3)), three per wave; tile n
+// of wave W is (P1T<W>::mt[n], P1T<W>::jt[n]).
+template <int W> struct P1T;
+template <> struct P1T<0> { static constexpr int mt[3] = {0, 2, 3}, jt[3] = {0, 2, 2}; };
+template <> struct P1T<1> { static constexpr int mt[3] = {1, 3, 0}, jt[3] = {1, 0, 1}; };
+template <> struct P1T<2> { static constexpr int mt[3] = {1, 2, 3}, jt[3] = {0, 0, 3}; };
+template <> struct P1T<3> { static constexpr int mt[3] = {2, 3, 2}, jt[3] = {1, 1, 3}; };
+
+// Phase 1 of one wave plus the chunk's K^T diag(w) V for its V columns (which
+// needs no level state, so it is computed here, where its LDS reads and MFMAs
+// interleave with the tile work): every LDS read is issued first, then the
+// MFMAs, then the scaling of the A tiles.
+//   A tile (mt, jt): S^T[s = 16jt + 4lq + i][t = 16mt + ln] o exp(Gc_t - Gc_s)
+//                    o lambda[t, level(t, s)] (causal) -> bf16 A[t][s] in LDS.
+//   kv[2c + h]: D rows k = 32c + 8lq + 4h + i, column v = 16w + ln.
+template <int W>
+__device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const bf16x8 (&qa)[4][2], const bf16x8& vt0,
+                                        const bf16x8& vt1, floatx4 (&kv)[4], int lq, int ln) {
+  using S = P1T<W>;
+  // ---- LDS reads ----
+  bf16x8 kf[3][2];
+  float gt[3];
+  floatx4 gs[3];
+  float lam[3][4];
+#pragma unroll
+  for (int n = 0; n < 3; ++n) {
+    const int mt = S::mt[n], jt = S::jt[n];
+    if (jt > mt) continue;
+    const int t = 16 * mt + ln;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) kf[n][c] = *(const bf16x8*)(sm.k + (16 * jt + ln) * kLd + 32 * c + 8 * lq);
+    gt[n] = sm.gc[t];
+    gs[n] = *(const floatx4*)(sm.gc + 16 * jt + 4 * lq);
+    if (jt < mt) {
+      const int lev = 4 + (32 - __builtin_clz(mt ^ jt));
+      lam[n][0] = sm.li[lev * kBT + t];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lam[n][i] = sm.li[intra_level(ln, 4 * lq + i) * kBT + t];
+    }
+  }
+  bf16x8 kt[2][2];   // [h][s-half], first for k-half c = 0
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    kt[hh][0] = ktr_frag(sm.k, 0, 0, hh, lq, ln);
+    kt[hh][1] = ktr_frag(sm.k, 32, 0, hh, lq, ln);
+  }
+  const floatx4 w0a = *(const floatx4*)(sm.wt + 8 * lq);
+  const floatx4 w0b = *(const floatx4*)(sm.wt + 8 * lq + 4);
+  const floatx4 w1a = *(const floatx4*)(sm.wt + 32 + 8 * lq);
+  const floatx4 w1b = *(const floatx4*)(sm.wt + 32 + 8 * lq + 4);
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- MFMAs ----
+  floatx4 acc[3];
+#pragma unroll
+  for (int n = 0; n < 3; ++n) {
+    const int mt = S::mt[n], jt = S::jt[n];
+    if (jt > mt) continue;
+    acc[n] = mfma16x16x32(kf[n][0], qa[mt][0], zero4());
+    acc[n] = mfma16x16x32(kf[n][1], qa[mt][1], acc[n]);
+  }
+  bf16x8 wv0, wv1;   // (w o V)[s][v = 16w + ln], s = 8lq + j / 32 + 8lq + j
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wv0[i] = (__bf16)((float)vt0[i] * w0a[i]);
+    wv0[4 + i] = (__bf16)((float)vt0[4 + i] * w0b[i]);
+    wv1[i] = (__bf16)((float)vt1[i] * w1a[i]);
+    wv1[4 + i] = (__bf16)((float)vt1[4 + i] * w1b[i]);
+  }
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    kv[hh] = mfma16x16x32(kt[hh][0], wv0, zero4());
+    kv[hh] = mfma16x16x32(kt[hh][1], wv1, kv[hh]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    kt[hh][0] = ktr_frag(sm.k, 0, 1, hh, lq, ln);
+    kt[hh][1] = ktr_frag(sm.k, 32, 1, hh, lq, ln);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    kv[2 + hh] = mfma16x16x32(kt[hh][0], wv0, zero4());
+    kv[2 + hh] = mfma16x16x32(kt[hh][1], wv1, kv[2 + hh]);
+  }
+  // ---- scaling, A tiles -> LDS ----
+#pragma unroll
+  for (int n = 0; n < 3; ++n) {
+    const int mt = S::mt[n], jt = S::jt[n];
+    if (jt > mt) continue;   // the zero tiles are written once, before the walk
+    const int t = 16 * mt + ln;
+    bf16x4 out;
+    if (jt < mt) {
+      float val[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = acc[n][i] * fexp2(gt[n] - gs[n][i]) * lam[n][0];
+      out = bf16x4{(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
+    } else {
+      float val[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = acc[n][i] * fexp2(gt[n] - gs[n][i]) * lam[n][i];
+        val[i] = 4 * lq + i <= ln ? x : 0.f;
+      }
+      out = bf16x4{(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
+    }
+    *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+  }
+}
+
+template <typename TV, typename TL, typename TO>
+__global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
+    const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
+    float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
+    const float* __restrict__ segd, int B, int T, int G, int H,
+    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state) {
+  constexpr int kPl = kKD * kLd;
+  constexpr int kLR = (7 + kMaxLoc + kMaxTop + 3) / 4;   // lambda registers per thread
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Bf16Smem& sm = *(Bf16Smem*)smem_raw;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq0 = lane >> 4, ln0 = lane & 15;
+  const XcdMap xm = xcd_map(blockIdx.x, nvb64);
+  if (xm.row >= B * H * NSEG) return;
+  const int h = xm.row % H, p = (xm.row / H) % NSEG, b = xm.row / (H * NSEG);
+  const int row = b * H + h, vblk = xm.slice;
+  const int gq = h / (H / G);
+  const int NT = T / kBT;
+  const int c0 = p << slog;
+  const int nch = min(c0 + (1 << slog), NT) - c0;
+  const int lu = 7 + nlev;
+  const int nloc = min(slog, nlev);
+  const int ntop = nlev - nloc;
+  const int vcol0 = vblk * 64;
+  const bool is_final_seg = final_state && ht != nullptr && p == NSEG - 1;
+  float* htb = ht ? ht + ((size_t)b * H + h) * kKD * V * L : nullptr;
+
+  // ---- top levels: Htop_e(p) for the levels segment p reads -> LDS (bf16, [v][k]) ----
+  // Htop_e(p) = sum_{q in block} exp(P[p] - P[q + 1]) Sum(q), block = the 2^e
+  // segments before p's half of its aligned 2^(e+1) block, P[x] = sum_{r < x} D_r
+  // (the top-level scan of chunkwise.py:199-247 over whole segments; the blocks
+  // of the levels p reads partition [0, p)).  The summaries were just written
+  // by the segment-summary kernel and are read from L2 / MALL.
+  if (ntop > 0 && (p > 0 || is_final_seg)) {
+    float* pre = (float*)sm.a;   // P[0 .. p + 1]; the A tile is free until the first chunk
+    const float* dp = segd + (size_t)row * NSEG;
+    if (w == 0) {
+      float carry = 0.f;
+      for (int base = 0; base <= p + 1; base += 64) {
+        const int qq = base + lane;
+        const float x = qq <= p ? dp[qq] : 0.f;
+        const float y = chunk_cumsum(x);
+        if (qq <= p + 1) pre[qq] = carry + y - x;
+        carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 63));
+      }
+    }
+    __syncthreads();
+    // thread: V columns 4 (tid & 15) .. + 3, k rows (tid >> 4) + 16 i
+    const int v4 = 4 * (tid & 15), kr = tid >> 4;
+    const float* sp = sums + (size_t)row * NSEG * kKD * V + (size_t)kr * V + vcol0 + v4;
+    const size_t qstride = (size_t)kKD * V;
+    const float pp = pre[p];
+    for (int e2 = 0; e2 < ntop && p > 0; ++e2) {
+      if (!((p >> e2) & 1)) continue;
+      const int lo = (p >> (e2 + 1)) << (e2 + 1);
+      floatx4 hacc[4] = {zero4(), zero4(), zero4(), zero4()};
+      for (int q0 = lo; q0 < lo + (1 << e2); q0 += 4) {
+        floatx4 xs[4][4];
+        float sc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int qs = min(q0 + u, lo + (1 << e2) - 1);
+          sc[u] = q0 + u < lo + (1 << e2) ? fexp(pp - pre[qs + 1]) : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[u][i] = *(const floatx4*)(sp + qs * qstride + (size_t)16 * i * V);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) hacc[i][c] += sc[u] * xs[u][i][c];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + (v4 + c) * kLd + kr + 16 * i] = (__bf16)hacc[i][c];
+    }
+    if (is_final_seg) {
+      // final states of the top levels (chunkwise.py:229-279): a level the last
+      // chunk reads holds its block decayed over segment p; one it writes holds
+      // segments [lo, p] decayed to the end of p
+      const int vc = vcol0 + 16 * w + ln0;
+      const float* spf = sums + (size_t)row * NSEG * kKD * V + vc;
+      for (int e2 = 0; e2 < ntop; ++e2) {
+        const bool reads = (p >> e2) & 1;
+        const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
+        const int hi = reads ? lo + (1 << e2) : p + 1;
+        floatx4 hacc[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) hacc[m] = zero4();
+        for (int qs = lo; qs < hi; ++qs) {
+          const float sc = fexp(pre[p + 1] - pre[qs + 1]);
+          const float* src = spf + qs * qstride;
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hacc[m][i] += sc * src[(size_t)(16 * m + 4 * lq0 + i) * V];
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            htb[((size_t)(16 * m + 4 * lq0 + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i];
+      }
+    }
+  }
+
+  // ---- per-row buffer descriptors and per-lane offsets ---------------------------
+  const int qstr = G * kKD, vstr = H * V, lstr = H * L;
+  const rsrc_t rq = make_rsrc(q + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
+  const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
+  const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
+  const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
+  const rsrc_t ro = make_rsrc(o + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TO));
+  const bool write_gcum = gcum != nullptr && vblk == 0;
+  const rsrc_t rgc = make_rsrc(write_gcum ? (const void*)(gcum + (size_t)b * T * H + h) : (const void*)g,
+                               write_gcum ? (size_t)T * H * 4 : 0);
+  const unsigned int vo_qk = tile64_voff<__bf16>(qstr), vo_v = tile64_voff<TV>(vstr);
+  const unsigned int vo_g = lane * H * 4;
+  const unsigned int vo_o = (ln0 * vstr + 16 * w + 4 * lq0) * sizeof(TO);
+  // lambda: lane = token row t of the chunk.  bf16 rows (L * 2 bytes, 2-byte
+  // aligned) are read as the aligned dwords covering columns 0 .. lu - 1, wave w
+  // taking dwords w, w + 4, ..; dword d of row t holds columns 2d - m, 2d + 1 - m
+  // with m the row's misalignment in elements.  fp32 rows: column w + 4r.
+  constexpr bool kL16 = sizeof(TL) == 2;
+  const char* lbase = (const char*)(l + (size_t)b * T * H * L);
+  const unsigned int lbmis = (unsigned int)((uintptr_t)lbase & 3);   // descriptor base aligned down
+  const rsrc_t rlb = make_rsrc(lbase - lbmis, (size_t)T * H * L * sizeof(TL) + lbmis);
+  const unsigned int lrow_b = lbmis + (unsigned int)((lane * H + h) * L) * sizeof(TL);
+  const int lmis = kL16 ? (int)((lrow_b >> 1) & 1) : 0;
+  const unsigned int vo_l = kL16 ? (lrow_b & ~3u) + 4 * w : lrow_b + 4 * w;
+  const int ldw = kL16 ? (2 * lu + 2 + 3) / 4 : lu;   // dwords (bf16) / columns (fp32) per row
+  constexpr int kLR2 = kL16 ? 3 : 5;                  // per-wave loads: ceil(max dwords / 4)
+
+  MainRegs<__bf16, TV, TL, 1> rg;
+  unsigned int lamr[kLR2];
+  auto load = [&](int j) {
+    const unsigned int row0 = (unsigned int)(c0 + j) * kBT;
+    load_tile64(rg.q, rq, vo_qk, row0 * qstr * 2, qstr);
+    load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
+    load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
+    rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+    const unsigned int so_l = row0 * lstr * sizeof(TL);
+#pragma unroll
+    for (int r = 0; r < kLR2; ++r)
+      if (w + 4 * r < ldw)
+        lamr[r] = __builtin_amdgcn_raw_buffer_load_b32(rlb, vo_l, so_l + 16 * r, 0);
+  };
+  auto store = [&](int j) {
+    store_tile64<1>(rg.q, sm.q, sm.q);
+    store_tile64<1>(rg.k, sm.k, sm.k);
+    store_tile64<1>(rg.v, sm.v, sm.v);
+    const float x = chunk_cumsum(rg.g);   // every wave scans the chunk's g: lane t holds Gc_t
+    const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+    if ((lane >> 4) == w) {   // each wave writes a quarter of the decay vectors
+      sm.gc[lane] = x * kLog2e;
+      sm.wt[lane] = fexp(last - x);
+    }
+    if (w == 3 && write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
+    const float eg = fexp(x);
+    auto put = [&](int col, float val) {
+      if (col < 7) sm.li[col * kBT + lane] = val;
+      else sm.lp[(col - 7) * kBT + 4 * (lane & 15) + (lane >> 4)] = val * eg;
+    };
+#pragma unroll
+    for (int r = 0; r < kLR2; ++r) {
+      const int d = w + 4 * r;
+      if (d < ldw) {
+        if constexpr (kL16) {
+          const int c = 2 * d - lmis;
+          const float lo = __builtin_bit_cast(float, lamr[r] << 16);
+          const float hi = __builtin_bit_cast(float, lamr[r] & 0xffff0000u);
+          if (c >= 0 && c < lu) put(c, lo);
+          if (c + 1 < lu) put(c + 1, hi);
+        } else {
+          put(d, __builtin_bit_cast(float, lamr[r]));
+        }
+      }
+    }
+  };
+
+  floatx4 st[kMaxLoc][4];     // local states: tile 2c + h holds k = 32c + 8lq + 4h + i, v = ln
+  float dl[kMaxLoc];          // pending log2-decay of each local state
+#pragma unroll
+  for (int e = 0; e < kMaxLoc; ++e) {
+    dl[e] = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) st[e][m] = zero4();
+  }
+
+  // the two A tiles above the diagonal that the 32-wide s steps of A V read
+  // ((t-tile 0, s-tile 1) and (2, 3)) stay zero for the whole walk
+  __syncthreads();   // the A tile may have served as scratch for the final states
+  {
+    const int r = tid >> 3, c = 4 * (tid & 3), tile = (tid >> 2) & 1;
+    *(bf16x4*)(sm.a + (32 * tile + (r & 15)) * kLd + 16 + 32 * tile + c) = bf16x4{};
+  }
+  load(0);
+  float Eseg = 0.f;   // log2-decay from the segment start to the current chunk start
+  const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
+  for (int j = 0; j < nch; ++j) {
+    const int ic = c0 + j;
+    store(j);
+    __syncthreads();
+    // Lane indices made opaque per chunk, so the compiler recomputes the LDS
+    // addresses of the phases (a few VALU ops) instead of keeping dozens of
+    // loop-invariant addresses in VGPRs across the whole walk.
+    int lq, ln;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lq) : "v"(lq0));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(ln0));
+
+    // Q fragments Q[t = 16mt + ln][k = 32c + 8lq + j]; V fragments
+    // V[s = 32c + 8lq + j][v = 16w + ln] (A operand of o^T = V^T A^T, and with
+    // the decay weights the B operand of K^T diag(w) V)
+    bf16x8 qa[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) qa[mt][c] = *(const bf16x8*)(sm.q + (16 * mt + ln) * kLd + 32 * c + 8 * lq);
+    const bf16x8 vt0 = tr_frag(sm.v, kLd, 0, 16 * w);
+    const bf16x8 vt1 = tr_frag(sm.v, kLd, 32, 16 * w);
+
+    // ---- phase 1: A = S o M, and the chunk's K^T diag(w) V -------------------------
+    floatx4 kv[4];
+    switch (w) {
+      case 0: bf16_p1<0>(sm, qa, vt0, vt1, kv, lq, ln); break;
+      case 1: bf16_p1<1>(sm, qa, vt0, vt1, kv, lq, ln); break;
+      case 2: bf16_p1<2>(sm, qa, vt0, vt1, kv, lq, ln); break;
+      default: bf16_p1<3>(sm, qa, vt0, vt1, kv, lq, ln); break;
+    }
+    const float glr = sm.gc[kBT - 1];   // chunk log2-decay
+    __syncthreads();
+    // the next chunk's loads land during phase 2 (issued after phase 1, whose
+    // register peak they would otherwise add to)
+    if (j + 1 < nch) load(j + 1);
+
+    // ---- phase 2: o^T[v = 16w + 4lq + i][t = 16nt + ln] ------------------------------
+    floatx4 acc[4];
+    {
+      bf16x8 af[6];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) af[nt] = *(const bf16x8*)(sm.a + (16 * nt + ln) * kLd + 8 * lq);
+      af[4] = *(const bf16x8*)(sm.a + (32 + ln) * kLd + 32 + 8 * lq);
+      af[5] = *(const bf16x8*)(sm.a + (48 + ln) * kLd + 32 + 8 * lq);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16x16x32(vt0, af[nt], zero4());
+      acc[2] = mfma16x16x32(vt1, af[4], acc[2]);
+      acc[3] = mfma16x16x32(vt1, af[5], acc[3]);
+    }
+    // local levels the chunk reads (bit e of the chunk index): all eight MFMAs of
+    // a level are issued before its lambda-weighted accumulation
+#pragma unroll
+    for (int e = 0; e < kMaxLoc; ++e) {
+      if (e < nloc && ((ic >> e) & 1)) {
+        const floatx4 lam = *(const floatx4*)(sm.lp + e * kBT + 4 * ln);
+        const bf16x8 h0 = cat8(st[e][0], st[e][1]);
+        const bf16x8 h1 = cat8(st[e][2], st[e][3]);
+        floatx4 tmp[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h0, qa[nt][0], zero4());
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h1, qa[nt][1], tmp[nt]);
+        const float sc = fexp2(dl[e]);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const float cf = lam[nt] * sc;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nt][i] += tmp[nt][i] * cf;
+        }
+      }
+    }
+    // top levels (bits of the segment index), the next level's fragments
+    // prefetched while the current one multiplies
+    if (topmask && j >= 0) {
+      const float ee = fexp2(Eseg);
+      int m = topmask;
+      int e2 = __builtin_ctz(m);
+      const __bf16* tb = sm.top + (16 * w + ln) * kLd + 8 * lq;
+      bf16x8 h0 = *(const bf16x8*)(tb + e2 * kPl);
+      bf16x8 h1 = *(const bf16x8*)(tb + e2 * kPl + 32);
+      floatx4 lam = *(const floatx4*)(sm.lp + (nloc + e2) * kBT + 4 * ln);
+      while (true) {
+        m &= m - 1;
+        bf16x8 n0 = h0, n1 = h1;
+        floatx4 nl = lam;
+        if (m) {
+          const int e2n = __builtin_ctz(m);
+          n0 = *(const bf16x8*)(tb + e2n * kPl);
+          n1 = *(const bf16x8*)(tb + e2n * kPl + 32);
+          nl = *(const floatx4*)(sm.lp + (nloc + e2n) * kBT + 4 * ln);
+        }
+        floatx4 tmp[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h0, qa[nt][0], zero4());
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h1, qa[nt][1], tmp[nt]);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const float cf = lam[nt] * ee;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nt][i] += tmp[nt][i] * cf;
+        }
+        if (!m) break;
+        h0 = n0;
+        h1 = n1;
+        lam = nl;
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      buf_store4<TO>(acc[nt], ro, vo_o, ((unsigned int)ic * kBT + 16 * nt) * vstr * sizeof(TO));
+
+    // ---- local state update with the chunk's K^T diag(w) V ---------------------------
+    if (nloc > 0) {
+      const bool keep_last = (ic == NT - 1) && final_state;
+#pragma unroll
+      for (int e = 0; e < kMaxLoc; ++e) {
+        if (e < nloc) {
+          const int per = 2 << e;
+          if (((ic & (per - 1)) == per - 1) && !keep_last) {
+            dl[e] = 0.f;   // block ends: the next chunk starts a fresh state
+#pragma unroll
+            for (int m = 0; m < 4; ++m) st[e][m] = zero4();
+          } else if (!((ic >> e) & 1)) {
+            const float s = fexp2(dl[e] + glr);
+            dl[e] = 0.f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) st[e][m][i] = st[e][m][i] * s + kv[m][i];
+          } else {
+            dl[e] += glr;
+          }
+        }
+      }
+      if (keep_last && is_final_seg) {
+        // ht[b, h, k, v, 7 + e] (chunkwise.py:1179, 277-279)
+        const int vc = vcol0 + 16 * w + ln;
+#pragma unroll
+        for (int e = 0; e < kMaxLoc; ++e)
+          if (e < nloc) {
+            const float s = fexp2(dl[e]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                htb[((size_t)(32 * (m >> 1) + 8 * lq + 4 * (m & 1) + i) * V + vc) * L + 7 + e] =
+                    st[e][m][i] * s;
+          }
+      }
+    }
+    Eseg += glr;
+    __syncthreads();   // every wave is done with the stage before it is refilled
+  }
+}
+
 }  // namespace hattn
 
 // dtype codes shared with the C-ABI (include/hattn.h)
@@ -569,7 +1088,9 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   char* p = (char*)base;
   const size_t a = segd_bytes(rows, NSEG);
   const size_t b = (rows * NSEG * hattn::kKD * V * sizeof(float) + 255) & ~(size_t)255;
-  const size_t c = rows * NSEG * ntop * (size_t)(V / 64) * (x3 ? 2 : 1) * hattn::kKD * 64 * 2;
+  // top-level states are staged by the scan kernel only for the bf16x3 kernels;
+  // the bf16 main kernel builds them from the summaries itself
+  const size_t c = x3 ? rows * NSEG * ntop * (size_t)(V / 64) * 2 * hattn::kKD * 64 * 2 : 0;
   w.segd = (float*)p;
   w.sums = (float*)(p + a);
   w.htop = (__bf16*)(p + a + b);
@@ -613,16 +1134,27 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
                        (const TV*)v, g, w.sums, w.segd, T, G, H, V, NT, S, NSEG, nvb64);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (ntop > 0) {
+    if (ntop > 0 && NP == 2) {
       auto hk = mamba2_htop_kernel<NP>;
       hipLaunchKernelGGL(hk, dim3(rows * nvb64 * 4), dim3(256), 0, stream, w.sums, w.segd,
                          w.htop, V, NSEG, ntop, nvb64);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
-  const int smem = main_smem_bytes<NP, MAXLOC>(nlev - min(slog, nlev));
   const int rows8 = (rows * NSEG + 7) / 8;
   const int grid = rows8 * 8 * nvb64;
+  if constexpr (NP == 1) {
+    const int smem = bf16_smem_bytes(ntop);
+    auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO>;
+    hipError_t e =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, w.sums,
+                       w.segd, B, T, G, H, V, L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
+    return hipGetLastError();
+  }
+  const int smem = main_smem_bytes<NP, MAXLOC>(ntop);
   auto kern = mamba2_fwd_main_kernel<TK, TV, TL, TO, NP, MAXLOC>;
   hipError_t e =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);

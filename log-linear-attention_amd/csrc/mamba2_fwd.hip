@@ -426,9 +426,11 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
         for (int mt = 0; mt < 4; ++mt) {
           floatx4 tmp = mma<NP>(qa[mt][0], b0, zero4());
           tmp = mma<NP>(qa[mt][1], b1, tmp);
+          // a level past nloc has no staged lambda column (stale LDS, possibly
+          // NaN bits): select, never multiply, its weight away
           const floatx4 lam = *(const floatx4*)(lamt + (7 + e) * kBT + 16 * mt);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * lam[i];
+          for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * (rd ? lam[i] : 0.f);
         }
       }
       if (any_top) {
@@ -562,12 +564,22 @@ struct Bf16Smem {
   float gc[kBT];              // log2(e) * chunk-local inclusive cumsum of g
   float wt[kBT];              // exp(Gc_last - Gc_s)
   float li[7 * kBT];          // lambda[t][lev] at [lev][t], intra levels 0..6
-  float lp[(kMaxLoc + kMaxTop) * kBT];  // exp(Gc_t) lambda[t][7 + e] at [e][ln][nt]
-  __bf16 top[1];              // [ntop][v][kLd] top-level states, transposed
+  // lambda[t][7 + e] at [e][ln][nt] and exp(Gc_t) at [ln][nt], double-buffered:
+  // chunk j + 1's are staged while phase 2 of chunk j reads chunk j's
+  float lp[2][(kMaxLoc + kMaxTop) * kBT];
+  float eg[2][kBT];
+  __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
 };
 
 inline int bf16_smem_bytes(int ntop) {
-  return (int)offsetof(Bf16Smem, top) + ntop * kKD * kLd * 2;
+  return (int)offsetof(Bf16Smem, top) + ntop * kKD * 64 * 2;
+}
+
+// Top-level state element (v, k) in a 64 x 64 bf16 tile without padding: the
+// 16-byte unit k >> 3 of row v is stored at unit (k >> 3) ^ (v & 7), so the
+// 16-byte fragment reads of eight consecutive rows hit eight different units.
+__device__ __forceinline__ int top_idx(int v, int k) {
+  return v * 64 + ((((k >> 3) ^ v) & 7) << 3) + (k & 7);
 }
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -703,8 +715,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
     const float* __restrict__ segd, int B, int T, int G, int H,
     int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state) {
-  constexpr int kPl = kKD * kLd;
-  constexpr int kLR = (7 + kMaxLoc + kMaxTop + 3) / 4;   // lambda registers per thread
+  constexpr int kPl = kKD * 64;                           // one top-level state tile
+  constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Bf16Smem& sm = *(Bf16Smem*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -773,7 +785,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + (v4 + c) * kLd + kr + 16 * i] = (__bf16)hacc[i][c];
+        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + top_idx(v4 + c, kr + 16 * i)] = (__bf16)hacc[i][c];
     }
     if (is_final_seg) {
       // final states of the top levels (chunkwise.py:229-279): a level the last
@@ -818,62 +830,72 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const unsigned int vo_qk = tile64_voff<__bf16>(qstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
   const unsigned int vo_o = (ln0 * vstr + 16 * w + 4 * lq0) * sizeof(TO);
-  // lambda: lane = token row t of the chunk.  bf16 rows (L * 2 bytes, 2-byte
-  // aligned) are read as the aligned dwords covering columns 0 .. lu - 1, wave w
-  // taking dwords w, w + 4, ..; dword d of row t holds columns 2d - m, 2d + 1 - m
-  // with m the row's misalignment in elements.  fp32 rows: column w + 4r.
+  // g and lambda are read with one lane per token row (lane = t) and as few
+  // instructions as possible: each of their rows is a separate cache line, so
+  // the cost is per instruction and row, not per byte.  Wave 0 reads g (4 B per
+  // row) and owns the chunk's decay vectors; waves 1 .. 3 read lambda in 16-byte
+  // pieces of the row, aligned down to 4 bytes: piece r of a bf16 row holds
+  // columns 8r - m .. 8r - m + 7 (m = the row's misalignment in elements), of an
+  // fp32 row columns 4r .. 4r + 3.  Wave w reads pieces w - 1 and w + 2.
   constexpr bool kL16 = sizeof(TL) == 2;
+  constexpr int kPE = kL16 ? 8 : 4;   // lambda columns per 16-byte piece
   const char* lbase = (const char*)(l + (size_t)b * T * H * L);
   const unsigned int lbmis = (unsigned int)((uintptr_t)lbase & 3);   // descriptor base aligned down
   const rsrc_t rlb = make_rsrc(lbase - lbmis, (size_t)T * H * L * sizeof(TL) + lbmis);
   const unsigned int lrow_b = lbmis + (unsigned int)((lane * H + h) * L) * sizeof(TL);
   const int lmis = kL16 ? (int)((lrow_b >> 1) & 1) : 0;
-  const unsigned int vo_l = kL16 ? (lrow_b & ~3u) + 4 * w : lrow_b + 4 * w;
-  const int ldw = kL16 ? (2 * lu + 2 + 3) / 4 : lu;   // dwords (bf16) / columns (fp32) per row
-  constexpr int kLR2 = kL16 ? 3 : 5;                  // per-wave loads: ceil(max dwords / 4)
+  const unsigned int vo_l = lrow_b & ~3u;
+  const int npc = (lu + lmis + kPE - 1) / kPE;   // pieces per row (<= 5)
 
   MainRegs<__bf16, TV, TL, 1> rg;
-  unsigned int lamr[kLR2];
-  auto load = [&](int j) {
+  constexpr int kLP = kL16 ? 1 : 2;   // pieces per wave (bf16 rows: lu <= 19 needs <= 3 pieces)
+  uint4 lamr[kLP];
+  // part < 0: everything; parts 0, 1, 2: q / k / v, g and lambda (the loads of
+  // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
+  auto load = [&](int j, int part) {
     const unsigned int row0 = (unsigned int)(c0 + j) * kBT;
-    load_tile64(rg.q, rq, vo_qk, row0 * qstr * 2, qstr);
-    load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
+    if (part <= 0) load_tile64(rg.q, rq, vo_qk, row0 * qstr * 2, qstr);
+    if (part < 0 || part == 1) load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
+    if (part == 0 || part == 1) return;
     load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
-    rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
-    const unsigned int so_l = row0 * lstr * sizeof(TL);
+    if (w == 0) {
+      rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+    } else {
+      const unsigned int so_l = row0 * lstr * sizeof(TL);
 #pragma unroll
-    for (int r = 0; r < kLR2; ++r)
-      if (w + 4 * r < ldw)
-        lamr[r] = __builtin_amdgcn_raw_buffer_load_b32(rlb, vo_l, so_l + 16 * r, 0);
+      for (int r = 0; r < kLP; ++r)
+        if (w - 1 + 3 * r < npc) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (w - 1 + 3 * r));
+    }
   };
   auto store = [&](int j) {
     store_tile64<1>(rg.q, sm.q, sm.q);
     store_tile64<1>(rg.k, sm.k, sm.k);
     store_tile64<1>(rg.v, sm.v, sm.v);
-    const float x = chunk_cumsum(rg.g);   // every wave scans the chunk's g: lane t holds Gc_t
-    const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-    if ((lane >> 4) == w) {   // each wave writes a quarter of the decay vectors
+    if (w == 0) {
+      const float x = chunk_cumsum(rg.g);   // lane t holds Gc_t
+      const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
       sm.gc[lane] = x * kLog2e;
       sm.wt[lane] = fexp(last - x);
-    }
-    if (w == 3 && write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
-    const float eg = fexp(x);
-    auto put = [&](int col, float val) {
-      if (col < 7) sm.li[col * kBT + lane] = val;
-      else sm.lp[(col - 7) * kBT + 4 * (lane & 15) + (lane >> 4)] = val * eg;
-    };
+      sm.eg[j & 1][4 * ln0 + lq0] = fexp(x);
+      if (write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
+    } else {
+      float* lpw = sm.lp[j & 1];
 #pragma unroll
-    for (int r = 0; r < kLR2; ++r) {
-      const int d = w + 4 * r;
-      if (d < ldw) {
-        if constexpr (kL16) {
-          const int c = 2 * d - lmis;
-          const float lo = __builtin_bit_cast(float, lamr[r] << 16);
-          const float hi = __builtin_bit_cast(float, lamr[r] & 0xffff0000u);
-          if (c >= 0 && c < lu) put(c, lo);
-          if (c + 1 < lu) put(c + 1, hi);
-        } else {
-          put(d, __builtin_bit_cast(float, lamr[r]));
+      for (int r = 0; r < kLP; ++r) {
+        const int pc = w - 1 + 3 * r;
+        if (pc < npc) {
+          const unsigned int* u = (const unsigned int*)&lamr[r];
+#pragma unroll
+          for (int i = 0; i < kPE; ++i) {
+            const int col = kPE * pc + i - lmis;
+            float val;
+            if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
+            else val = __builtin_bit_cast(float, u[i]);
+            if (col >= 0 && col < lu) {
+              if (col < 7) sm.li[col * kBT + lane] = val;
+              else lpw[(col - 7) * kBT + 4 * (lane & 15) + (lane >> 4)] = val;
+            }
+          }
         }
       }
     }
@@ -895,13 +917,18 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const int r = tid >> 3, c = 4 * (tid & 3), tile = (tid >> 2) & 1;
     *(bf16x4*)(sm.a + (32 * tile + (r & 15)) * kLd + 16 + 32 * tile + c) = bf16x4{};
   }
-  load(0);
+  // Pipeline: chunk j + 1 is staged in LDS right after phase 1 of chunk j (from
+  // then on chunk j's stage is dead except lambda', which is double-buffered),
+  // and chunk j + 2's loads are issued at the same point, so they have a whole
+  // chunk period to land and a chunk needs two barriers instead of three.
+  load(0, -1);
+  store(0);
+  if (nch > 1) load(1, -1);
   float Eseg = 0.f;   // log2-decay from the segment start to the current chunk start
   const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
   for (int j = 0; j < nch; ++j) {
     const int ic = c0 + j;
-    store(j);
-    __syncthreads();
+    __syncthreads();   // chunk j staged; every wave is done with chunk j - 1
     // Lane indices made opaque per chunk, so the compiler recomputes the LDS
     // addresses of the phases (a few VALU ops) instead of keeping dozens of
     // loop-invariant addresses in VGPRs across the whole walk.
@@ -929,10 +956,12 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       default: bf16_p1<3>(sm, qa, vt0, vt1, kv, lq, ln); break;
     }
     const float glr = sm.gc[kBT - 1];   // chunk log2-decay
-    __syncthreads();
-    // the next chunk's loads land during phase 2 (issued after phase 1, whose
-    // register peak they would otherwise add to)
-    if (j + 1 < nch) load(j + 1);
+    __syncthreads();   // A visible; chunk j's stage (but lambda') no longer read
+    if (j + 1 < nch) store(j + 1);
+    const bool more = j + 2 < nch;
+    if (more) load(j + 2, 0);
+    const float* lpr = sm.lp[j & 1];
+    const floatx4 egr = *(const floatx4*)(sm.eg[j & 1] + 4 * ln);   // exp(Gc_t), t = 16nt + ln
 
     // ---- phase 2: o^T[v = 16w + 4lq + i][t = 16nt + ln] ------------------------------
     floatx4 acc[4];
@@ -947,12 +976,13 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       acc[2] = mfma16x16x32(vt1, af[4], acc[2]);
       acc[3] = mfma16x16x32(vt1, af[5], acc[3]);
     }
+    if (more) load(j + 2, 1);
     // local levels the chunk reads (bit e of the chunk index): all eight MFMAs of
     // a level are issued before its lambda-weighted accumulation
 #pragma unroll
     for (int e = 0; e < kMaxLoc; ++e) {
       if (e < nloc && ((ic >> e) & 1)) {
-        const floatx4 lam = *(const floatx4*)(sm.lp + e * kBT + 4 * ln);
+        const floatx4 lam = *(const floatx4*)(lpr + e * kBT + 4 * ln);
         const bf16x8 h0 = cat8(st[e][0], st[e][1]);
         const bf16x8 h1 = cat8(st[e][2], st[e][3]);
         floatx4 tmp[4];
@@ -963,31 +993,35 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         const float sc = fexp2(dl[e]);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
-          const float cf = lam[nt] * sc;
+          const float cf = lam[nt] * egr[nt] * sc;
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[nt][i] += tmp[nt][i] * cf;
         }
       }
     }
+    if (more) load(j + 2, 2);
     // top levels (bits of the segment index), the next level's fragments
     // prefetched while the current one multiplies
     if (topmask && j >= 0) {
       const float ee = fexp2(Eseg);
       int m = topmask;
       int e2 = __builtin_ctz(m);
-      const __bf16* tb = sm.top + (16 * w + ln) * kLd + 8 * lq;
-      bf16x8 h0 = *(const bf16x8*)(tb + e2 * kPl);
-      bf16x8 h1 = *(const bf16x8*)(tb + e2 * kPl + 32);
-      floatx4 lam = *(const floatx4*)(sm.lp + (nloc + e2) * kBT + 4 * ln);
+      // A operand h^T[v = 16w + ln][k = 32c + 8lq + j]: 16-byte units lq, 4 + lq of row v
+      const int vrow = 16 * w + ln;
+      const __bf16* tb = sm.top + vrow * 64;
+      const int u0 = ((lq ^ vrow) & 7) << 3, u1 = (((4 + lq) ^ vrow) & 7) << 3;
+      bf16x8 h0 = *(const bf16x8*)(tb + e2 * kPl + u0);
+      bf16x8 h1 = *(const bf16x8*)(tb + e2 * kPl + u1);
+      floatx4 lam = *(const floatx4*)(lpr + (nloc + e2) * kBT + 4 * ln);
       while (true) {
         m &= m - 1;
         bf16x8 n0 = h0, n1 = h1;
         floatx4 nl = lam;
         if (m) {
           const int e2n = __builtin_ctz(m);
-          n0 = *(const bf16x8*)(tb + e2n * kPl);
-          n1 = *(const bf16x8*)(tb + e2n * kPl + 32);
-          nl = *(const floatx4*)(sm.lp + (nloc + e2n) * kBT + 4 * ln);
+          n0 = *(const bf16x8*)(tb + e2n * kPl + u0);
+          n1 = *(const bf16x8*)(tb + e2n * kPl + u1);
+          nl = *(const floatx4*)(lpr + (nloc + e2n) * kBT + 4 * ln);
         }
         floatx4 tmp[4];
 #pragma unroll
@@ -996,7 +1030,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h1, qa[nt][1], tmp[nt]);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
-          const float cf = lam[nt] * ee;
+          const float cf = lam[nt] * egr[nt] * ee;
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[nt][i] += tmp[nt][i] * cf;
         }
@@ -1050,7 +1084,6 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       }
     }
     Eseg += glr;
-    __syncthreads();   // every wave is done with the stage before it is refilled
   }
 }
 

@@ -118,6 +118,18 @@ def gdn_fwd_flops(B, T, H, K, V):
                     + 5 * T * K * V * nlev)
 
 
+def measured_traffic(path=os.path.join(ROOT, "profiles", "mamba2_fwd_ns_traffic.txt")):
+    """HBM bytes per forward launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (line 'traffic_bytes: N'), or None."""
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _time_region(fn, n, stream):
     """Run fn n times; return (wall seconds per call, HIP-event seconds per call on
     the launch stream)."""
@@ -169,8 +181,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fwd-only", action="store_true", help="skip the forward+backward timing")
     ap.add_argument("--calib", action="store_true",
-                    help="also run a plain 256 MiB copy kernel (elementwise mul by 1) so a "
-                         "counter run can scale FETCH_SIZE / WRITE_SIZE by a known traffic")
+                    help="also run a 2 GiB read-only kernel (sum) and a 2 GiB write-only kernel "
+                         "(fill), larger than the 256 MB MALL, so a counter run can scale "
+                         "FETCH_SIZE / WRITE_SIZE by a known traffic")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -198,10 +211,12 @@ def main():
         step()
     torch.cuda.synchronize()
     if args.calib:
-        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)   # 256 MiB
+        src = torch.ones(512 * 1024 * 1024, dtype=torch.float32, device=dev)   # 2 GiB
         dst = torch.empty_like(src)
+        torch.cuda.synchronize()
         for _ in range(3):
-            torch.mul(src, 1.0, out=dst)
+            dst.fill_(0.5)        # writes 2 GiB
+            src.sum()             # reads 2 GiB (src last written long before, evicted by dst)
         torch.cuda.synchronize()
         del src, dst
 
@@ -323,7 +338,7 @@ def main():
         "gdn_fwd": gdn,
         "gdn_fwd_bwd": gdn_fb,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,
                      "mfma_frac": flops / avg_launch_s / MFMA_BF16_PEAK},
     }

@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 
 import torch  # noqa: E402
 
-# north-star workload (BASELINE.json north_star / SURVEY 8(d))
+# north-star workload
 NS = dict(B=4, T=16384, H=16, K=64, V=64, L=15)
 HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
 MFMA_BF16_PEAK = 2.5e15    # FLOP/s dense bf16
@@ -144,6 +144,50 @@ def _time_region(fn, n, stream):
     return (time.perf_counter() - t0) / n, e0.elapsed_time(e1) / 1e3 / n
 
 
+def decode_bench(dev, stream, n_steps, warmup):
+    """Decode steps (hattention_step: cascade, gate, insert and output in one
+    launch) from an empty HState: Mamba-2 at the north-star state shape and
+    GDN at the config-3 state shape, per-token inputs contiguous [B, H, D].
+    The HBM bytes per step are the state's read and write (the per-token
+    operands are < 0.1 percent)."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_step
+    from hattention.recurrent import HState
+    res = {}
+    for name, hs, (B, H, K, V, L) in (("mamba2", HStruct.MAMBA2, (4, 16, 64, 64, 16)),
+                                      ("gdn", HStruct.GDELTA, (4, 16, 128, 128, 14))):
+        T = n_steps + warmup
+        if hs == HStruct.MAMBA2:
+            q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=1004, device=dev)
+            b, scale, norm = None, None, False
+        else:
+            q, k, v, b, g, l = make_gdn_inputs(B, T, H, K, V, L, seed=1005, device=dev)
+            scale, norm = K ** -0.5, True
+        tm = lambda x: x.transpose(0, 1).contiguous() if x is not None else None
+        q, k, v, b, g, l = (tm(x) for x in (q, k, v, b, g, l))
+        S = HState(2, HType.WEAK, hs, (B, H, K, V, L), torch.float32, dev)
+        it = iter(range(T))
+
+        def step():
+            t = next(it)
+            return hattention_step(S, q[t], k[t], v[t], b[t] if b is not None else None, g[t],
+                                   l[t], scale, 2, HType.WEAK, hs, use_qk_l2norm_in_kernel=norm)
+
+        for _ in range(warmup):
+            step()
+        wall, ev = _time_region(step, n_steps, stream)
+        nbytes = 2 * B * H * K * V * L * 4
+        res[name] = {"state": {"batch": B, "heads": H, "dk": K, "dv": V, "levels": L,
+                               "dtype_state": "fp32", "dtype_qkv": "bf16"},
+                     "us_per_step": wall * 1e6, "steps": n_steps,
+                     "roofline": {"bound": "hbm", "achieved": nbytes / ev / 1e9,
+                                  "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                                  "frac": nbytes / ev / HBM_PEAK, "algorithmic_bytes": nbytes,
+                                  "avg_step_us": ev * 1e6}}
+        del q, k, v, b, g, l, S
+    return res
+
+
 def cpu_baseline(seconds_budget=30.0):
     """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
     chunkwise algorithm) on the host cores, on the north-star workload (median
@@ -187,7 +231,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(every (batch, head) row is independent; see DESIGN.md for how it would shard)",
+              "(every (batch, head) row is independent, so rows would shard over GPUs "
+              "without communication)",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
@@ -317,6 +362,8 @@ def main():
                 gdn_fb = rec
         del gq, gk, gv, gbeta, gg, gl, gdo
 
+    dec = decode_bench(dev, stream, 128, 8) if not args.fwd_only else None
+
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
         "value": value,
@@ -337,6 +384,7 @@ def main():
         "fwd_bwd": fb,
         "gdn_fwd": gdn,
         "gdn_fwd_bwd": gdn_fb,
+        "decode": dec,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,

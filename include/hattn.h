@@ -41,6 +41,7 @@ typedef enum { HATTN_BF16 = 0, HATTN_FP16 = 1, HATTN_FP32 = 2 } hattn_dtype;
 
 /* HType / HStruct of hattention/base.py:12-19. */
 enum { HATTN_HTYPE_WEAK = 0, HATTN_HTYPE_STRONG = 1 };
+enum { HATTN_HSTRUCT_MAMBA2 = 0, HATTN_HSTRUCT_GDELTA = 1 };
 
 /* Library version string, e.g. "hattn-mi355x 0.1.0 gfx950". */
 const char* hattn_version(void);
@@ -189,6 +190,56 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
  * reference, which allocates h / dh and its temporaries with torch inside
  * chunkwise_bwd (chunkwise_hgdn.py:894-913). */
 size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
+
+/*
+ * One decode step of the Fenwick level state (HState) for every (b, h).
+ *
+ * Replaces hattention/kernel.py:577-633 `hattention_step(hstate, q, k, v, b, g, l,
+ * scale, level_base, htype, hstruct, use_qk_l2norm_in_kernel) -> (o, hstate)`
+ * with its step_state / step_output (hattention/recurrent.py:134-166), called by
+ * hattention_prefill (kernel.py:555-570) and hselective_state_update
+ * (mamba_apis.py:407-566).  HType.WEAK, level base 2.
+ *
+ *   states [B, H, K, V, L] fp32 (read and written)   counts [L] int32 or NULL
+ *   q, k [B, G, K] in dtype_qk   v, o [B, H, V] in dtype_v   l [B, H, L] in dtype_l
+ *   g [B, H] fp32 log-decay (gate exp(g))   beta [B, H] in dtype_beta (GDELTA) or NULL
+ *   hstruct HATTN_HSTRUCT_MAMBA2 or HATTN_HSTRUCT_GDELTA
+ *   cascade: number of full levels that cascade upwards before the insert
+ *            (HState.cascade_weak, recurrent.py:42-54), planned by the caller
+ *            from its copy of counts; 0 <= cascade < L
+ *   update / output: 1 to advance the state (step_state) / write o (step_output);
+ *            k, v, g, beta are read only with update, q, l, o only with output
+ *            (the others may be NULL)
+ *   l2norm_qk: 1 to use q / |q| * scale and k / |k| (|x| = sqrt(sum x^2 + 1e-6),
+ *            kernel.py:20-23, 626-629); scale is ignored otherwise
+ *
+ * Constraints: K <= 256, V a multiple of 16, L <= 32, dtype codes BF16 or FP32
+ * -> else HATTN_ERR_NOT_IMPLEMENTED.
+ */
+int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, const void* v,
+                      const void* beta, const float* g, const void* l, void* o, int B, int G,
+                      int H, int K, int V, int L, int hstruct, int cascade, int update,
+                      int output, int l2norm_qk, float scale, int dtype_qk, int dtype_v,
+                      int dtype_l, int dtype_beta, void* stream);
+
+/*
+ * Levels 0 .. nlo - 1 of the HState after a chunkwise prefill of T tokens
+ * (T % 64 == 0), MAMBA2.
+ *
+ * Replaces the MAMBA2 fast path of hattention/kernel.py:378-465
+ * `postprocess_prefill_hstate_` (the torch einsums of :420-436): level 0 is
+ * k_{T-1} v_{T-1}^T, level e >= 1 the 2^(e-1) tokens before the tokens of the
+ * lower levels, each weighted by exp(sum of g after it).  The levels >= nlo come
+ * from the chunkwise forward's final states.
+ *
+ *   states [B, H, K, V, L] fp32 (levels < nlo written)   k [B, T, G, K] in dtype_k
+ *   v [B, T, H, V] in dtype_v   g [B, T, H] fp32 per-step log-decay
+ *
+ * Constraints: K <= 256, V a multiple of 16, 1 <= nlo <= min(7, L).
+ */
+int hattn_mamba2_prefill_levels(float* states, const void* k, const void* v, const float* g,
+                                int B, int T, int G, int H, int K, int V, int L, int nlo,
+                                int dtype_k, int dtype_v, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,17 @@ hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, 
                                    int L, int nlev, int dt_v, int dt_l, hipStream_t stream,
                                    int* unsupported);
 
+hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
+                                    const void* v, const void* beta, const float* g,
+                                    const void* l, void* o, int B, int G, int H, int K, int V,
+                                    int L, int gdn, int cascade, int update, int output,
+                                    int norm_qk, float scale, int dt_qk, int dt_v, int dt_l,
+                                    int dt_b, hipStream_t stream, int* unsupported);
+hipError_t hattn_mamba2_prefill_levels_launch(float* states, const void* k, const void* v,
+                                              const float* g, int B, int T, int G, int H, int K,
+                                              int V, int L, int nlo, int dt_k, int dt_v,
+                                              hipStream_t stream, int* unsupported);
+
 namespace {
 
 thread_local char g_err[512] = {0};
@@ -284,6 +295,56 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);
   return check_hip(e, "hattn_gdn_chunkwise_bwd launch");
+}
+
+int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, const void* v,
+                      const void* beta, const float* g, const void* l, void* o, int B, int G,
+                      int H, int K, int V, int L, int hstruct, int cascade, int update,
+                      int output, int l2norm_qk, float scale, int dtype_qk, int dtype_v,
+                      int dtype_l, int dtype_beta, void* stream) {
+  if (B <= 0 || G <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (H % G != 0) return fail(HATTN_ERR_VALUE, "G=%d does not divide H=%d", G, H);
+  if (hstruct != HATTN_HSTRUCT_MAMBA2 && hstruct != HATTN_HSTRUCT_GDELTA)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "hstruct=%d", hstruct);
+  if (K > 256 || V % 16 != 0 || L > 32)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "K=%d V=%d L=%d (K <= 256, V a multiple of 16, L <= 32)", K, V, L);
+  if (cascade < 0 || cascade >= L)
+    return fail(HATTN_ERR_VALUE, "cascade depth %d with %d levels (level overflow)", cascade, L);
+  if (!states || (output && (!q || !l || !o)) ||
+      (update && (!k || !v || !g || (hstruct == HATTN_HSTRUCT_GDELTA && !beta))))
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  int unsupported = 0;
+  hipError_t e = hattn_hstate_step_launch(
+      states, counts, q, k, v, beta, g, l, o, B, G, H, K, V, L,
+      hstruct == HATTN_HSTRUCT_GDELTA ? 1 : 0, cascade, update ? 1 : 0, output ? 1 : 0,
+      l2norm_qk ? 1 : 0, scale, dtype_qk, dtype_v, dtype_l, dtype_beta, (hipStream_t)stream,
+      &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype codes qk=%d v=%d l=%d beta=%d", dtype_qk,
+                dtype_v, dtype_l, dtype_beta);
+  return check_hip(e, "hattn_hstate_step launch");
+}
+
+int hattn_mamba2_prefill_levels(float* states, const void* k, const void* v, const float* g,
+                                int B, int T, int G, int H, int K, int V, int L, int nlo,
+                                int dtype_k, int dtype_v, void* stream) {
+  if (B <= 0 || G <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (H % G != 0) return fail(HATTN_ERR_VALUE, "G=%d does not divide H=%d", G, H);
+  if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d is not a positive multiple of 64", T);
+  if (nlo < 1 || nlo > 7 || nlo > L) return fail(HATTN_ERR_VALUE, "nlo=%d with L=%d", nlo, L);
+  if (K > 256 || V % 16 != 0)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (K <= 256, V a multiple of 16)", K, V);
+  if (!states || !k || !v || !g) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  int unsupported = 0;
+  hipError_t e = hattn_mamba2_prefill_levels_launch(states, k, v, g, B, T, G, H, K, V, L, nlo,
+                                                    dtype_k, dtype_v, (hipStream_t)stream,
+                                                    &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype codes k=%d v=%d", dtype_k, dtype_v);
+  return check_hip(e, "hattn_mamba2_prefill_levels launch");
 }
 
 }  // extern "C"

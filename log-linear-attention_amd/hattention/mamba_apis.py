@@ -4,7 +4,10 @@ Mirrors hattention/mamba_apis.py:
 * ``compute_lambda``             -- :70-85  (lambda modes positive / bounded / None)
 * ``compute_lambda_maybe_fixed`` -- :88-113 (fixed per-level lambdas only)
 * ``hmamba_chunk_scan_combined`` -- :263-404 (dt / A / lambda pre-processing,
-  then ``hattention_kernel`` with q=C, k=B, v=x*dt, g=A*dt, plus the D residual)
+  then ``hattention_kernel`` with q=C, k=B, v=x*dt, g=A*dt, plus the D residual;
+  with ``return_final_states`` the prefill ``hattention_prefill`` and its HState)
+* ``hselective_state_update``    -- :407-566 (the same pre-processing for one
+  token, then one decode step of the HState)
 
 The pre-processing is elementwise torch on the device; the scan itself is the
 HIP kernel.  Options the reference rejects with NotImplementedError are
@@ -15,7 +18,7 @@ from typing import Optional, Tuple
 import torch
 
 from hattention.base import HType, HStruct
-from hattention.kernel import hattention_kernel
+from hattention.kernel import hattention_kernel, hattention_prefill
 
 
 def compute_lambda(L: torch.Tensor, dl: torch.Tensor, lambda_mode: Optional[str]) -> torch.Tensor:
@@ -94,8 +97,6 @@ def hmamba_chunk_scan_combined(
                 lambda_level_fixed):
         if arg is None:
             raise ValueError
-    if return_final_states:
-        raise NotImplementedError("prefill (return_final_states=True) is not built yet")
 
     if D is not None:
         if D.dim() != 1:
@@ -110,9 +111,104 @@ def hmamba_chunk_scan_combined(
                                      lambda_level_max=lambda_level_max,
                                      lambda_level_fixed=lambda_level_fixed,
                                      lambda_level_module=lambda_level_module)
-    y = hattention_kernel(q=C, k=B, v=x, b=None, g=g.float(), l=lam, scale=None,
-                          head_first=False, level_base=lambda_level_base, htype=lambda_htype,
-                          hstruct=lambda_hstruct)
+    if not return_final_states:
+        state = None
+        y = hattention_kernel(q=C, k=B, v=x, b=None, g=g.float(), l=lam, scale=None,
+                              head_first=False, level_base=lambda_level_base,
+                              htype=lambda_htype, hstruct=lambda_hstruct)
+    else:
+        # :386-403: prefill with the final HState; x and lambda take C's / dl's dtype
+        if x.dtype != C.dtype:
+            x = x.to(dtype=C.dtype)
+        if lam.dtype != dl.dtype:
+            lam = lam.to(dtype=dl.dtype)
+        y, state = hattention_prefill(q=C, k=B, v=x, b=None, g=g.float(), l=lam, scale=None,
+                                      head_first=False, level_base=lambda_level_base,
+                                      htype=lambda_htype, hstruct=lambda_hstruct)
     if D is not None:
         y = y + D_residual
-    return y, None
+    return y, state
+
+
+def hselective_state_update(
+    state,
+    x: torch.Tensor,
+    dt: torch.Tensor,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    dl: torch.Tensor,
+    L: torch.Tensor,
+    D: Optional[torch.Tensor] = None,
+    z: Optional[torch.Tensor] = None,
+    dt_bias: Optional[torch.Tensor] = None,
+    dt_softplus: bool = False,
+    state_batch_indices: Optional[torch.Tensor] = None,
+    lambda_mode: Optional[str] = None,
+    lambda_level_max: Optional[int] = None,
+    lambda_level_base: Optional[int] = None,
+    lambda_htype: Optional[HType] = None,
+    lambda_hstruct: Optional[HStruct] = None,
+    lambda_level_fixed: Optional[bool] = None,
+    lambda_level_module=None,
+):
+    """mamba_apis.py:407-566: one decode step of the log-linear Mamba-2 layer.
+
+    x [B,H,P], dt [B,H], A [H], B/C [B,G,N], dl [B,H,L], L [H,L], D [H].
+    Returns (out [B,H,P], state advanced in place).  The dt / A / lambda
+    pre-processing is elementwise torch on the device; the state step is one
+    ``hattn_hstate_step`` launch (q = C, k = B, v = x * dt, g = A * dt).
+    """
+    from hattention.recurrent import launch_step
+    if state_batch_indices is not None:
+        raise NotImplementedError
+    if z is not None:
+        raise NotImplementedError
+    dims = [(x, 3), (dt, 2), (A, 1), (B, 3), (C, 3), (dl, 3), (L, 2)]
+    if any(t.dim() != n for t, n in dims):
+        raise ValueError
+    if D is not None and D.dim() != 1:
+        raise ValueError
+    if dt_bias is not None and dt_bias.dim() != 1:
+        raise ValueError
+    batch, nheads, headdim = x.shape
+    _, ngroups, dstate = B.shape
+    dlambda = L.shape[-1]
+    if dt.shape != x.shape[:2] or A.shape != (nheads,) or nheads % ngroups != 0:
+        raise ValueError
+    if B.shape != (batch, ngroups, dstate) or C.shape != B.shape:
+        raise ValueError
+    if dl.shape != (batch, nheads, dlambda) or L.shape != (nheads, dlambda):
+        raise ValueError
+    if D is not None and D.shape != (nheads,):
+        raise ValueError
+    for arg in (lambda_level_max, lambda_level_base, lambda_htype, lambda_hstruct,
+                lambda_level_fixed):
+        if arg is None:
+            raise ValueError
+
+    if D is not None:
+        D_residual = x * D.view(1, -1, 1)
+    if dt_bias is not None:
+        dt = dt + dt_bias.view(1, -1)
+    if dt_softplus:
+        dt = torch.nn.functional.softplus(dt)
+    x = x * dt.unsqueeze(-1)
+    A = A.view(1, -1) * dt
+    lam = compute_lambda_maybe_fixed(L=L.view(1, *L.shape), dl=dl, lambda_mode=lambda_mode,
+                                     lambda_level_max=lambda_level_max,
+                                     lambda_level_fixed=lambda_level_fixed,
+                                     lambda_level_module=lambda_level_module)
+    if not all([A.dtype == state.dtype, C.dtype == B.dtype,
+                C.dtype == x.dtype or x.dtype == state.dtype,
+                C.dtype == lam.dtype or lam.dtype == state.dtype,
+                state.base == lambda_level_base, state.htype == lambda_htype,
+                state.hstruct == lambda_hstruct]):
+        raise TypeError
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    launch_step(state, q=C.contiguous(), k=B.contiguous(), v=x, g=A.contiguous(),
+                l=lam.contiguous(), o=out, update=True, output=True)
+    if D is not None:
+        out = out + D_residual
+    return out, state

@@ -479,12 +479,17 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
         }
       };
       if (nloc > 0) {
+        // only the levels the chunk reads (bit e of the chunk index, uniform) are
+        // multiplied; the others contribute zero to dq and dlambda
 #pragma unroll
         for (int e = 0; e < kMaxLoc; ++e) {
           if (e < nloc) {
-            const float z = (ic > c0 && ((ic >> e) & 1)) ? 1.f : 0.f;
-            level(cat8(hT[e][0] * z, hT[e][1] * z), cat8(hT[e][2] * z, hT[e][3] * z), e, 7 + e,
-                  1.f);
+            if (ic > c0 && ((ic >> e) & 1)) {
+              level(cat8(hT[e][0], hT[e][1]), cat8(hT[e][2], hT[e][3]), e, 7 + e, 1.f);
+            } else if (lq == 0) {
+#pragma unroll
+              for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][e][w] = 0.f;
+            }
           }
         }
       }

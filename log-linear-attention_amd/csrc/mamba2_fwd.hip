@@ -849,6 +849,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
 
   MainRegs<__bf16, TV, TL, 1> rg;
   constexpr int kLP = kL16 ? 1 : 2;   // pieces per wave (bf16 rows: lu <= 19 needs <= 3 pieces)
+  const int lpw0 = w > 0 ? w - 1 : 0;   // first lambda piece of this wave
   uint4 lamr[kLP];
   // part < 0: everything; parts 0, 1, 2: q / k / v, g and lambda (the loads of
   // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
@@ -858,14 +859,15 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     if (part < 0 || part == 1) load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
     if (part == 0 || part == 1) return;
     load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
-    if (w == 0) {
-      rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
-    } else {
-      const unsigned int so_l = row0 * lstr * sizeof(TL);
+    // every wave issues the same loads (wave 0 uses only g, waves 1 .. 3 only
+    // their lambda pieces; a piece past the row reads bytes of the next row, or
+    // zeros past the buffer end, and is not used): a load assigned on some waves
+    // only makes the compiler merge registers after the branch with copies that
+    // wait for the load, i.e. a full memory round trip per chunk
+    rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+    const unsigned int so_l = row0 * lstr * sizeof(TL);
 #pragma unroll
-      for (int r = 0; r < kLP; ++r)
-        if (w - 1 + 3 * r < npc) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (w - 1 + 3 * r));
-    }
+    for (int r = 0; r < kLP; ++r) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (lpw0 + 3 * r));
   };
   auto store = [&](int j) {
     store_tile64<1>(rg.q, sm.q, sm.q);

@@ -188,6 +188,68 @@ def decode_bench(dev, stream, n_steps, warmup):
     return res
 
 
+def layer_bench(dev, stream, n_steps, warmup):
+    """The Mamba-2 layer scan of hmamba_chunk_scan_combined at the north-star
+    shape (x [4, 16384, 16, 64] bf16, B = C [4, 16384, 16, 64] bf16, dl bf16 with
+    15 levels, positive lambda, D and dt_bias): the fused HIP pre- / post-
+    processing around the scan, against the same scan kernels wrapped in the
+    reference's torch expressions (mamba_apis.py:346-403), forward and
+    forward + backward.  HBM bytes of the fused forward: x, B, C, dt, dl read
+    and y written once by the kernels plus the v / g / lambda round trip."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_kernel
+    from hattention.mamba_apis import hmamba_chunk_scan_combined
+    B, T, H, P, N, L = NS["B"], NS["T"], NS["H"], NS["V"], NS["K"], NS["L"]
+    gen = torch.Generator("cpu").manual_seed(1006)
+    x = torch.randn(B, T, H, P, generator=gen).bfloat16().to(dev)
+    dt = (torch.randn(B, T, H, generator=gen) * 0.5 - 2.5).to(dev)
+    A = -torch.exp(torch.rand(H, generator=gen)).to(dev)
+    Bm = torch.randn(B, T, H, N, generator=gen).bfloat16().to(dev)
+    Cm = torch.randn(B, T, H, N, generator=gen).bfloat16().to(dev)
+    dl = torch.randn(B, T, H, L, generator=gen).bfloat16().to(dev)
+    Lp = (torch.randn(H, L, generator=gen) * 0.5).to(dev)
+    D = torch.randn(H, generator=gen).to(dev)
+    bias = (torch.randn(H, generator=gen) * 0.1).to(dev)
+    kw = dict(lambda_mode="positive", lambda_level_max=L, lambda_level_base=2,
+              lambda_htype=HType.WEAK, lambda_hstruct=HStruct.MAMBA2, lambda_level_fixed=True)
+
+    def fused(*a):
+        return hmamba_chunk_scan_combined(*a[:7], 64, D=a[7], dt_bias=a[8], dt_softplus=True,
+                                          **kw)[0]
+
+    def chain(*a):
+        d = torch.nn.functional.softplus(a[1] + a[8][None, None])
+        lam = torch.nn.functional.softplus(a[6][None, None] * a[5])
+        y = hattention_kernel(a[4], a[3], a[0] * d[..., None], None, a[2][None, None] * d, lam,
+                              None, False, 2, HType.WEAK, HStruct.MAMBA2)
+        return y + a[0] * a[7][None, None, :, None]
+
+    base = (x, dt, A, Bm, Cm, dl, Lp, D, bias)
+    dy = torch.randn(B, T, H, P, device=dev)
+    res = {}
+    for name, fn in (("fused", fused), ("torch_chain", chain)):
+        with torch.no_grad():
+            for _ in range(warmup):
+                fn(*base)
+            wall_f, _ = _time_region(lambda: fn(*base), n_steps, stream)
+        leaves = [t.detach().clone().requires_grad_(True) for t in base]
+
+        def fb():
+            for t in leaves:
+                t.grad = None
+            fn(*leaves).backward(dy)
+
+        for _ in range(max(1, warmup)):
+            fb()
+        wall_fb, _ = _time_region(fb, max(1, n_steps // 2), stream)
+        res[name] = {"fwd_tokens_per_s": B * T / wall_f, "fwd_ms": wall_f * 1e3,
+                     "fwd_bwd_tokens_per_s": B * T / wall_fb, "fwd_bwd_ms": wall_fb * 1e3}
+        del leaves
+    res["shape"] = {"batch": B, "seq_len": T, "heads": H, "headdim": P, "dstate": N,
+                    "levels": L, "lambda_mode": "positive", "dtype_x_bc_dl": "bf16"}
+    return res
+
+
 def cpu_baseline(seconds_budget=30.0):
     """fp32 torch restatement (oracle.mamba2.chunked_scan_fwd, the reference's
     chunkwise algorithm) on the host cores, on the north-star workload (median
@@ -363,6 +425,7 @@ def main():
         del gq, gk, gv, gbeta, gg, gl, gdo
 
     dec = decode_bench(dev, stream, 128, 8) if not args.fwd_only else None
+    layer = layer_bench(dev, stream, max(2, args.steps // 5), 2) if not args.fwd_only else None
 
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",
@@ -385,6 +448,7 @@ def main():
         "gdn_fwd": gdn,
         "gdn_fwd_bwd": gdn_fb,
         "decode": dec,
+        "mamba2_layer": layer,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,

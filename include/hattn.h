@@ -241,6 +241,53 @@ int hattn_mamba2_prefill_levels(float* states, const void* k, const void* v, con
                                 int B, int T, int G, int H, int K, int V, int L, int nlo,
                                 int dtype_k, int dtype_v, void* stream);
 
+/*
+ * Layer pre-processing of hmamba_chunk_scan_combined, one pass
+ * (hattention/mamba_apis.py:346-366, compute_lambda :70-85):
+ *   d = dt + dt_bias (dt_bias may be NULL), softplus(d) if dt_softplus;
+ *   v = x * d;  g = A[h] * d (fp32);  lam = compute_lambda(Lp[h], dl, lambda_mode).
+ * x, v [B, T, H, P]; dt [B, T, H]; dl, lam [B, T, H, L]; A [H] fp32; Lp [H, L].
+ * lambda_mode: HATTN_LAMBDA_LINEAR (None), _POSITIVE, _BOUNDED.  P a multiple of
+ * 4 with P / 4 a power of two <= 64, L <= 32; every tensor 16-byte aligned.
+ * Element types (BF16 / FP32) per tensor: dtype_x, dtype_dt, dtype_dl, dtype_lp,
+ * dtype_v, dtype_lam.
+ */
+enum { HATTN_LAMBDA_LINEAR = 0, HATTN_LAMBDA_POSITIVE = 1, HATTN_LAMBDA_BOUNDED = 2 };
+int hattn_mamba2_layer_prologue(const void* x, const void* dt, const float* A,
+                                const float* dt_bias, const void* dl, const void* Lp, void* v,
+                                float* g, void* lam, int B, int T, int H, int P, int L,
+                                int dt_softplus, int lambda_mode, int dtype_x, int dtype_dt,
+                                int dtype_dl, int dtype_lp, int dtype_v, int dtype_lam,
+                                void* stream);
+
+/*
+ * Layer post-processing, out = y + x * D[h] (mamba_apis.py:346-349, :402-403).
+ * y, x, out [B, T, H, P] in dtype_y, dtype_x, dtype_out; D [H] fp32.
+ */
+int hattn_mamba2_layer_epilogue(const void* y, const void* x, const float* D, void* out, int B,
+                                int T, int H, int P, int dtype_y, int dtype_x, int dtype_out,
+                                void* stream);
+
+/*
+ * Backward of the layer pre- and post-processing: what torch autograd computes
+ * through mamba_apis.py:346-366 and :402-403 given the scan's gradients dv,
+ * dg (fp32), dlam and the layer output gradient dy (read only when D != NULL):
+ *   dx = dv d + dy D,  ddt = (sum_p dv x + dg A) softplus'(dt + dt_bias),
+ *   ddl from dlam per lambda mode; per-head sums dA, ddt_bias, dD [H] and
+ *   dLp [H, L] in fp32 (any of them may be NULL), reduced in a fixed order.
+ * Workspace: hattn_mamba2_layer_bwd_workspace(B, T, H, L) bytes.
+ */
+size_t hattn_mamba2_layer_bwd_workspace(int B, int T, int H, int L);
+int hattn_mamba2_layer_bwd(const void* x, const void* dt, const float* A, const float* dt_bias,
+                           const void* dl, const void* Lp, const float* D, const void* dy,
+                           const void* dv, const float* dg, const void* dlam, void* dx,
+                           void* ddt, void* ddl, float* dA, float* ddt_bias, float* dD,
+                           float* dLp, int B, int T, int H, int P, int L, int dt_softplus,
+                           int lambda_mode, int dtype_x, int dtype_dt, int dtype_dl,
+                           int dtype_lp, int dtype_dy, int dtype_dv, int dtype_dlam,
+                           int dtype_dx, int dtype_ddt, int dtype_ddl, void* ws,
+                           size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

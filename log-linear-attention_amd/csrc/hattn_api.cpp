@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 
@@ -49,6 +50,24 @@ hipError_t hattn_mamba2_prefill_levels_launch(float* states, const void* k, cons
                                               const float* g, int B, int T, int G, int H, int K,
                                               int V, int L, int nlo, int dt_k, int dt_v,
                                               hipStream_t stream, int* unsupported);
+
+size_t hattn_mamba2_layer_bwd_ws_bytes(int B, int T, int H, int L);
+hipError_t hattn_mamba2_layer_prologue_launch(const void* x, const void* dt, const float* A,
+                                              const float* dt_bias, const void* dl,
+                                              const void* Lp, void* v, float* g, void* lam,
+                                              int B, int T, int H, int P, int L, int softplus,
+                                              int mode, const int* bf, hipStream_t stream);
+hipError_t hattn_mamba2_layer_epilogue_launch(const void* y, const void* x, const float* D,
+                                              void* out, int B, int T, int H, int P, int ybf,
+                                              int xbf, int obf, hipStream_t stream);
+hipError_t hattn_mamba2_layer_bwd_launch(const void* x, const void* dt, const float* A,
+                                         const float* dt_bias, const void* dl, const void* Lp,
+                                         const float* D, const void* dy, const void* dv,
+                                         const float* dg, const void* dlam, void* dx, void* ddt,
+                                         void* ddl, float* dA, float* ddt_bias, float* dD,
+                                         float* dLp, float* ws, int B, int T, int H, int P, int L,
+                                         int softplus, int mode, const int* bf,
+                                         hipStream_t stream);
 
 namespace {
 
@@ -345,6 +364,92 @@ int hattn_mamba2_prefill_levels(float* states, const void* k, const void* v, con
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype codes k=%d v=%d", dtype_k, dtype_v);
   return check_hip(e, "hattn_mamba2_prefill_levels launch");
+}
+
+namespace {
+// dtype code -> 1 for bf16, 0 for fp32, -1 otherwise
+int bf_flag(int code) { return code == HATTN_BF16 ? 1 : code == HATTN_FP32 ? 0 : -1; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+int layer_dims_check(int B, int T, int H, int P, int L) {
+  if (B <= 0 || T <= 0 || H <= 0 || P <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (P % 4 != 0 || (P / 4) > 64 || ((P / 4) & (P / 4 - 1)) != 0)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "P=%d (a multiple of 4 with P/4 a power of two <= 64)", P);
+  if (L > 32) return fail(HATTN_ERR_NOT_IMPLEMENTED, "L=%d above 32", L);
+  return HATTN_OK;
+}
+}  // namespace
+
+int hattn_mamba2_layer_prologue(const void* x, const void* dt, const float* A,
+                                const float* dt_bias, const void* dl, const void* Lp, void* v,
+                                float* g, void* lam, int B, int T, int H, int P, int L,
+                                int dt_softplus, int lambda_mode, int dtype_x, int dtype_dt,
+                                int dtype_dl, int dtype_lp, int dtype_v, int dtype_lam,
+                                void* stream) {
+  if (int st = layer_dims_check(B, T, H, P, L)) return st;
+  if (lambda_mode < 0 || lambda_mode > 2) return fail(HATTN_ERR_VALUE, "lambda_mode=%d", lambda_mode);
+  if (!x || !dt || !A || !dl || !Lp || !v || !g || !lam) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  if (!aligned16(x) || !aligned16(v)) return fail(HATTN_ERR_VALUE, "x / v not 16-byte aligned");
+  const int bf[6] = {bf_flag(dtype_x), bf_flag(dtype_dt), bf_flag(dtype_dl), bf_flag(dtype_lp),
+                     bf_flag(dtype_v), bf_flag(dtype_lam)};
+  for (int i = 0; i < 6; ++i)
+    if (bf[i] < 0) return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype code (bf16 or fp32 only)");
+  return check_hip(hattn_mamba2_layer_prologue_launch(x, dt, A, dt_bias, dl, Lp, v, g, lam, B, T,
+                                                      H, P, L, dt_softplus ? 1 : 0, lambda_mode,
+                                                      bf, (hipStream_t)stream),
+                   "hattn_mamba2_layer_prologue launch");
+}
+
+int hattn_mamba2_layer_epilogue(const void* y, const void* x, const float* D, void* out, int B,
+                                int T, int H, int P, int dtype_y, int dtype_x, int dtype_out,
+                                void* stream) {
+  if (int st = layer_dims_check(B, T, H, P, 1)) return st;
+  if (!y || !x || !D || !out) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  if (!aligned16(y) || !aligned16(x) || !aligned16(out))
+    return fail(HATTN_ERR_VALUE, "y / x / out not 16-byte aligned");
+  const int yb = bf_flag(dtype_y), xb = bf_flag(dtype_x), ob = bf_flag(dtype_out);
+  if (yb < 0 || xb < 0 || ob < 0) return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype code (bf16 or fp32 only)");
+  return check_hip(hattn_mamba2_layer_epilogue_launch(y, x, D, out, B, T, H, P, yb, xb, ob,
+                                                      (hipStream_t)stream),
+                   "hattn_mamba2_layer_epilogue launch");
+}
+
+size_t hattn_mamba2_layer_bwd_workspace(int B, int T, int H, int L) {
+  if (B <= 0 || T <= 0 || H <= 0 || L <= 0 || L > 32) return 0;
+  return hattn_mamba2_layer_bwd_ws_bytes(B, T, H, L);
+}
+
+int hattn_mamba2_layer_bwd(const void* x, const void* dt, const float* A, const float* dt_bias,
+                           const void* dl, const void* Lp, const float* D, const void* dy,
+                           const void* dv, const float* dg, const void* dlam, void* dx,
+                           void* ddt, void* ddl, float* dA, float* ddt_bias, float* dD,
+                           float* dLp, int B, int T, int H, int P, int L, int dt_softplus,
+                           int lambda_mode, int dtype_x, int dtype_dt, int dtype_dl,
+                           int dtype_lp, int dtype_dy, int dtype_dv, int dtype_dlam,
+                           int dtype_dx, int dtype_ddt, int dtype_ddl, void* ws,
+                           size_t ws_bytes, void* stream) {
+  if (int st = layer_dims_check(B, T, H, P, L)) return st;
+  if (lambda_mode < 0 || lambda_mode > 2) return fail(HATTN_ERR_VALUE, "lambda_mode=%d", lambda_mode);
+  if (!x || !dt || !A || !dl || !Lp || !dv || !dg || !dlam || !dx || !ddt || !ddl ||
+      (D && !dy))
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  if (!aligned16(x) || !aligned16(dv) || !aligned16(dx) || (D && !aligned16(dy)))
+    return fail(HATTN_ERR_VALUE, "x / dv / dx / dy not 16-byte aligned");
+  const size_t need = hattn_mamba2_layer_bwd_ws_bytes(B, T, H, L);
+  if (!ws || ws_bytes < need)
+    return fail(HATTN_ERR_VALUE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
+  const int bf[10] = {bf_flag(dtype_x), bf_flag(dtype_dt), bf_flag(dtype_dl), bf_flag(dtype_lp),
+                      bf_flag(dtype_dy), bf_flag(dtype_dv), bf_flag(dtype_dlam), bf_flag(dtype_dx),
+                      bf_flag(dtype_ddt), bf_flag(dtype_ddl)};
+  for (int i = 0; i < 10; ++i)
+    if (bf[i] < 0 && !(i == 4 && !D)) return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype code (bf16 or fp32 only)");
+  int bfx[10];
+  for (int i = 0; i < 10; ++i) bfx[i] = bf[i] < 0 ? 0 : bf[i];
+  return check_hip(hattn_mamba2_layer_bwd_launch(x, dt, A, dt_bias, dl, Lp, D, dy, dv, dg, dlam, dx,
+                                                 ddt, ddl, dA, ddt_bias, dD, dLp, (float*)ws, B,
+                                                 T, H, P, L, dt_softplus ? 1 : 0, lambda_mode, bfx,
+                                                 (hipStream_t)stream),
+                   "hattn_mamba2_layer_bwd launch");
 }
 
 }  // extern "C"

@@ -39,6 +39,10 @@ SIGNATURES = [
     ("hattn_hstate_step", _I,
      [_P] * 9 + [_I] * 11 + [ctypes.c_float] + [_I] * 4 + [_P]),
     ("hattn_mamba2_prefill_levels", _I, [_P] * 4 + [_I] * 10 + [_P]),
+    ("hattn_mamba2_layer_prologue", _I, [_P] * 9 + [_I] * 13 + [_P]),
+    ("hattn_mamba2_layer_epilogue", _I, [_P] * 4 + [_I] * 7 + [_P]),
+    ("hattn_mamba2_layer_bwd_workspace", _S, [_I] * 4),
+    ("hattn_mamba2_layer_bwd", _I, [_P] * 18 + [_I] * 17 + [_P, _S, _P]),
 ]
 
 _lock = threading.Lock()

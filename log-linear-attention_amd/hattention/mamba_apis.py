@@ -9,8 +9,9 @@ Mirrors hattention/mamba_apis.py:
 * ``hselective_state_update``    -- :407-566 (the same pre-processing for one
   token, then one decode step of the HState)
 
-The pre-processing is elementwise torch on the device; the scan itself is the
-HIP kernel.  Options the reference rejects with NotImplementedError are
+The pre- and post-processing (dt softplus, x dt, A dt, lambda, D x) run as
+fused HIP kernels around the scan (hattention/mamba_layer.py), with their
+backward.  Options the reference rejects with NotImplementedError are
 rejected the same way; the per-call warnings of the reference are not emitted.
 """
 from typing import Optional, Tuple
@@ -19,6 +20,8 @@ import torch
 
 from hattention.base import HType, HStruct
 from hattention.kernel import hattention_kernel, hattention_prefill
+from hattention.mamba_layer import (HMambaScanFunction, lambda_mode_code, layer_epilogue,
+                                     layer_prologue)
 
 
 def compute_lambda(L: torch.Tensor, dl: torch.Tensor, lambda_mode: Optional[str]) -> torch.Tensor:
@@ -98,35 +101,39 @@ def hmamba_chunk_scan_combined(
         if arg is None:
             raise ValueError
 
-    if D is not None:
-        if D.dim() != 1:
-            raise ValueError
-        D_residual = x * D.view(1, 1, -1, 1)
-    if dt_bias is not None:
-        dt = dt + dt_bias.view(1, 1, -1)
-    dt = torch.nn.functional.softplus(dt)
-    x = x * dt.unsqueeze(-1)
-    g = A.view(1, 1, -1) * dt
-    lam = compute_lambda_maybe_fixed(L=L.view(1, 1, *L.shape), dl=dl, lambda_mode=lambda_mode,
-                                     lambda_level_max=lambda_level_max,
-                                     lambda_level_fixed=lambda_level_fixed,
-                                     lambda_level_module=lambda_level_module)
+    if D is not None and D.dim() != 1:
+        raise ValueError
+    if dt_bias is not None and dt_bias.dim() != 1:
+        raise ValueError
+    # compute_lambda_maybe_fixed's checks (mamba_apis.py:96-102) on L [1, 1, H, Lv]
+    if not lambda_level_fixed:
+        raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+    if not all([L.dim() + 2 in (3, 4), dl.dim() in (3, 4), L.shape[-1] == lambda_level_max,
+                dl.shape[-1] == lambda_level_max]):
+        raise ValueError
+    lambda_mode_code(lambda_mode)
+    if lambda_hstruct != HStruct.MAMBA2:
+        # the reference calls hattention_kernel with b=None, which GDELTA rejects
+        raise ValueError
+
     if not return_final_states:
-        state = None
-        y = hattention_kernel(q=C, k=B, v=x, b=None, g=g.float(), l=lam, scale=None,
-                              head_first=False, level_base=lambda_level_base,
-                              htype=lambda_htype, hstruct=lambda_hstruct)
-    else:
-        # :386-403: prefill with the final HState; x and lambda take C's / dl's dtype
-        if x.dtype != C.dtype:
-            x = x.to(dtype=C.dtype)
+        # prologue -> chunkwise scan (q = C, k = B) -> epilogue, one autograd node
+        y = HMambaScanFunction.apply(x, dt, A, B, C, dl, L, D, dt_bias, dt_softplus,
+                                     lambda_mode, lambda_level_base, lambda_htype)
+        return y, None
+    with torch.no_grad():
+        # :386-403: prefill with the final HState; v and lambda take C's / dl's dtype
+        v, g, lam = layer_prologue(x, dt, A, dt_bias, dl, L, dt_softplus, lambda_mode,
+                                   v_dtype=C.dtype)
+        if v.dtype != C.dtype:
+            v = v.to(dtype=C.dtype)
         if lam.dtype != dl.dtype:
             lam = lam.to(dtype=dl.dtype)
-        y, state = hattention_prefill(q=C, k=B, v=x, b=None, g=g.float(), l=lam, scale=None,
+        y, state = hattention_prefill(q=C, k=B, v=v, b=None, g=g, l=lam, scale=None,
                                       head_first=False, level_base=lambda_level_base,
                                       htype=lambda_htype, hstruct=lambda_hstruct)
-    if D is not None:
-        y = y + D_residual
+        if D is not None:
+            y = layer_epilogue(y, x, D)
     return y, state
 
 
@@ -187,28 +194,29 @@ def hselective_state_update(
         if arg is None:
             raise ValueError
 
-    if D is not None:
-        D_residual = x * D.view(1, -1, 1)
-    if dt_bias is not None:
-        dt = dt + dt_bias.view(1, -1)
-    if dt_softplus:
-        dt = torch.nn.functional.softplus(dt)
-    x = x * dt.unsqueeze(-1)
-    A = A.view(1, -1) * dt
-    lam = compute_lambda_maybe_fixed(L=L.view(1, *L.shape), dl=dl, lambda_mode=lambda_mode,
-                                     lambda_level_max=lambda_level_max,
-                                     lambda_level_fixed=lambda_level_fixed,
-                                     lambda_level_module=lambda_level_module)
-    if not all([A.dtype == state.dtype, C.dtype == B.dtype,
-                C.dtype == x.dtype or x.dtype == state.dtype,
-                C.dtype == lam.dtype or lam.dtype == state.dtype,
+    if not lambda_level_fixed:
+        raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+    if not all([L.dim() + 1 in (3, 4), dl.dim() in (3, 4), L.shape[-1] == lambda_level_max,
+                dl.shape[-1] == lambda_level_max]):
+        raise ValueError
+    # dtypes of the reference's intermediates (:493-509), for its checks (:517-525)
+    dtp = torch.promote_types(dt.dtype, dt_bias.dtype) if dt_bias is not None else dt.dtype
+    x_dtype = torch.promote_types(x.dtype, dtp)
+    a_dtype = torch.promote_types(A.dtype, dtp)
+    lam_dtype = torch.promote_types(L.dtype, dl.dtype)
+    if not all([a_dtype == state.dtype, C.dtype == B.dtype,
+                C.dtype == x_dtype or x_dtype == state.dtype,
+                C.dtype == lam_dtype or lam_dtype == state.dtype,
                 state.base == lambda_level_base, state.htype == lambda_htype,
                 state.hstruct == lambda_hstruct]):
         raise TypeError
-    x = x.contiguous()
-    out = torch.empty_like(x)
-    launch_step(state, q=C.contiguous(), k=B.contiguous(), v=x, g=A.contiguous(),
-                l=lam.contiguous(), o=out, update=True, output=True)
+    # one token: the layer prologue on [B, 1, H, .] views, one step launch, the epilogue
+    v, g, lam = layer_prologue(x.unsqueeze(1), dt.unsqueeze(1), A, dt_bias, dl.unsqueeze(1), L,
+                               dt_softplus, lambda_mode)
+    v, g, lam = v.squeeze(1), g.squeeze(1), lam.squeeze(1)
+    out = torch.empty_like(v)
+    launch_step(state, q=C.contiguous(), k=B.contiguous(), v=v, g=g, l=lam, o=out, update=True,
+                output=True)
     if D is not None:
-        out = out + D_residual
+        out = layer_epilogue(out.unsqueeze(1), x.unsqueeze(1), D).squeeze(1)
     return out, state

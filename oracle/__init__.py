@@ -14,7 +14,9 @@ Contents (each function cites the reference file:line it restates):
 * ``mamba2``  -- log-linear Mamba-2: materialised O(T^2) H-matrix form,
   Fenwick recurrent form, chunked form (masked chunk-level combination) and
   chunked level-scan form; plain (non-hierarchical) SSD scan for the
-  lambda == 1 special case; backward through autograd.
+  lambda == 1 special case; backward through autograd; the Mamba-2 layer
+  scan with its pre- and post-processing (dt softplus, x dt, A dt, lambda
+  modes, D residual) on top of the chunked level-scan form.
 * ``gdn``     -- log-linear Gated DeltaNet: recurrent form (matrix gates),
   materialised pair sum, chunked UT / WY form with per-level delta-rule scans,
   the plain gated delta rule (lambda == 1) and the l2norm / scale boundary.

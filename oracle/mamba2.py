@@ -339,3 +339,47 @@ def brute_force_fwd(q, k, v, g, l) -> torch.Tensor:
                 (q[:, t] * k[:, s]).sum(-1)
             o[:, t] += w[..., None] * v[:, s]
     return o
+
+
+# --------------------------------------------------------------------------
+# 6. the Mamba-2 layer scan with its pre- and post-processing
+# --------------------------------------------------------------------------
+def layer_lambda(L, dl, lambda_mode):
+    """compute_lambda (hattention/mamba_apis.py:70-85) with L [H, Lv] broadcast
+    over [B, T, H, Lv] (the rearrange of :360-366)."""
+    Lb = L[None, None]
+    if lambda_mode == "positive":
+        return torch.nn.functional.softplus(Lb * dl)
+    if lambda_mode == "bounded":
+        return torch.exp(-torch.exp(Lb) * torch.nn.functional.softplus(dl))
+    if lambda_mode is None:
+        return Lb * dl
+    raise ValueError
+
+
+def layer_fwd(x, dt, A, B, C, dl, L, D=None, dt_bias=None, lambda_mode="positive",
+              dt_softplus=True, scan=None, return_intermediates=False):
+    """hmamba_chunk_scan_combined (hattention/mamba_apis.py:346-403) for
+    HStruct.MAMBA2: dt' = softplus(dt + dt_bias), q = C, k = B, v = x dt',
+    g = A dt', lambda = compute_lambda(L, dl), y = scan(...) + x D.
+
+    x [B,T,H,P], dt [B,T,H], A [H], B / C [B,T,G,N], dl [B,T,H,Lv], L [H,Lv],
+    D [H].  ``scan`` defaults to chunked_scan_fwd (the level-scan form).  The
+    pre- and post-processing are torch's own functions (softplus, exp), so the
+    restatement is pinned by them and by the scan's pinning; its gradients come
+    from torch.autograd.  ``return_intermediates`` also returns (dt', v, g,
+    lambda), the scan's inputs, as nodes of the same graph."""
+    if dt_bias is not None:
+        dt = dt + dt_bias[None, None]
+    if dt_softplus:
+        dt = torch.nn.functional.softplus(dt)
+    v = x * dt[..., None]
+    g = A[None, None] * dt
+    lam = layer_lambda(L, dl, lambda_mode)
+    if scan is None:
+        y = chunked_scan_fwd(C, B, v, g, lam, chunk_size=64)[0]
+    else:
+        y = scan(C, B, v, g, lam)
+    if D is not None:
+        y = y + x * D[None, None, :, None]
+    return (y, (dt, v, g, lam)) if return_intermediates else y

@@ -1,0 +1,190 @@
+"""GPU parity of the fused Mamba-2 layer scan (hmamba_chunk_scan_combined).
+
+The HIP path: hattn_mamba2_layer_prologue -> chunkwise forward -> layer
+epilogue, and in the backward the chunkwise backward -> hattn_mamba2_layer_bwd
+(hattention.mamba_layer.HMambaScanFunction through
+hattention.mamba_apis.hmamba_chunk_scan_combined).  The checker is
+oracle.mamba2.layer_fwd in float64 on the CPU (the reference's expressions of
+mamba_apis.py:346-403 around the pinned chunked level scan), its gradients by
+torch.autograd, fed the identical inputs.
+
+Tolerances: bf16 scan inputs (B, C, x) -> max|y - y_ref| / max|y_ref| < 2e-2
+and relative Frobenius < 1e-2; every per-element
+gradient (dx, ddt, dB, dC, ddl) to 2e-2 of its own max (max-abs / max-ref).
+The per-head sums (dA, ddt_bias, dD, dL) add up many terms of both signs, so
+their error is bounded relative to the sum of the absolute values of their
+terms (2e-2 of it), taken from the oracle: dA = sum dg dt', ddt_bias = sum ddt,
+dD = sum dy x, dL = sum dlam dlam/dL.  fp32 inputs run the bf16x3 forward scan:
+1e-4 (the Mamba-2 backward kernels take bf16, dv = 64, so the fp32 and the
+dv = 128 cases check the forward).  The full-size case compares the fused
+layer with the reference's torch expressions on the GPU around the same scan
+kernels, which checks the layer backward exactly given the scan gradients.
+"""
+import pytest
+import torch
+
+from oracle import mamba2 as M
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _errs(out, ref):
+    out = out.double().cpu()
+    ref = ref.double().cpu()
+    mx = ((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+    fro = ((out - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+    return mx, fro
+
+
+def _inputs(B, T, H, G, P, N, Lv, seed, dtype):
+    gen = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(B, T, H, P, generator=gen).to(dtype)
+    dt = (torch.randn(B, T, H, generator=gen) * 0.5 - 2.5)
+    A = -torch.exp(torch.rand(H, generator=gen))
+    Bm = torch.randn(B, T, G, N, generator=gen).to(dtype)
+    Cm = torch.randn(B, T, G, N, generator=gen).to(dtype)
+    dl = torch.randn(B, T, H, Lv, generator=gen).to(dtype)
+    L = torch.randn(H, Lv, generator=gen) * 0.5
+    D = torch.randn(H, generator=gen)
+    bias = torch.randn(H, generator=gen) * 0.1
+    return x, dt, A, Bm, Cm, dl, L, D, bias
+
+
+def _kw(Lv, mode):
+    from hattention.base import HType, HStruct
+    return dict(lambda_mode=mode, lambda_level_max=Lv, lambda_level_base=2,
+                lambda_htype=HType.WEAK, lambda_hstruct=HStruct.MAMBA2, lambda_level_fixed=True)
+
+
+def _run(B, T, H, G, P, N, Lv, mode, seed, dtype=torch.bfloat16, use_D=True, use_bias=True,
+         tol=(2e-2, 1e-2, 2e-2), backward=True):
+    from hattention.mamba_apis import hmamba_chunk_scan_combined
+    x, dt, A, Bm, Cm, dl, L, D, bias = _inputs(B, T, H, G, P, N, Lv, seed, dtype)
+    D = D if use_D else None
+    bias = bias if use_bias else None
+    print(f"[layer] B={B} T={T} H={H} G={G} P={P} N={N} L={Lv} mode={mode} {dtype} "
+          f"D={use_D} bias={use_bias}", flush=True)
+    leaves = [t.to(DEV).requires_grad_(backward) if t is not None else None
+              for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
+    y, st = hmamba_chunk_scan_combined(leaves[0], leaves[1], leaves[2], leaves[3], leaves[4],
+                                       leaves[5], leaves[6], 64, D=leaves[7],
+                                       dt_bias=leaves[8], dt_softplus=True, **_kw(Lv, mode))
+    assert st is None
+    gen = torch.Generator("cpu").manual_seed(seed + 1)
+    dy = torch.randn(y.shape, generator=gen).to(y.dtype)
+    if backward:
+        y.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    # fp64 oracle and its autograd gradients (also w.r.t. the scan's inputs)
+    ref_leaves = [t.double().requires_grad_(True) if t is not None else None
+                  for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
+    y_ref, (dtp, v, g, lam) = M.layer_fwd(*ref_leaves[:7], D=ref_leaves[7],
+                                          dt_bias=ref_leaves[8], lambda_mode=mode,
+                                          return_intermediates=True)
+    tmax, tfro, tg = tol
+    mx, fro = _errs(y, y_ref)
+    print(f"  y: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+    assert mx < tmax and fro < tfro, (mx, fro)
+    if not backward:
+        return
+    used = [t for t in ref_leaves if t is not None]
+    grads = torch.autograd.grad((y_ref * dy.double()).sum(), used + [g, lam])
+    dg_ref, dlam_ref = grads[-2], grads[-1]
+    ref = dict(zip([n for n, t in zip(["x", "dt", "A", "B", "C", "dl", "L", "D", "dt_bias"],
+                                      ref_leaves) if t is not None], grads))
+    # per-head sums: bound relative to the sum of absolute terms
+    Lb = ref_leaves[6].detach()[None, None].expand_as(dl).clone().requires_grad_(True)
+    dlam_dL = torch.autograd.grad(_lam_elem(Lb, dl.double(), mode).sum(), Lb)[0]
+    scale = {"A": (dg_ref * dtp).abs().sum((0, 1)).detach(),
+             "dt_bias": ref["dt"].abs().sum((0, 1)),
+             "D": (dy.double() * x.double()).abs().sum((0, 1, 3)),
+             "L": (dlam_ref * dlam_dL).abs().sum((0, 1)).detach()}
+    for name, leaf in zip(["x", "dt", "A", "B", "C", "dl", "L", "D", "dt_bias"], leaves):
+        if leaf is None:
+            continue
+        assert leaf.grad is not None, name
+        assert leaf.grad.dtype == leaf.dtype and leaf.grad.shape == leaf.shape, name
+        if name in scale:
+            e = ((leaf.grad.double().cpu() - ref[name]).abs() / scale[name].clamp_min(1e-30)).max().item()
+            print(f"  d{name}: err / sum|terms| {e:.2e}", flush=True)
+        else:
+            e, _ = _errs(leaf.grad, ref[name])
+            print(f"  d{name}: max-rel {e:.2e}", flush=True)
+        assert e < tg, (name, e)
+
+
+def _lam_elem(Lb, dl, mode):
+    """compute_lambda (mamba_apis.py:70-85) with L already broadcast to dl's shape."""
+    if mode == "positive":
+        return torch.nn.functional.softplus(Lb * dl)
+    if mode == "bounded":
+        return torch.exp(-torch.exp(Lb) * torch.nn.functional.softplus(dl))
+    return Lb * dl
+
+
+@pytest.mark.parametrize("mode", ["positive", "bounded", None])
+def test_layer_modes(mode):
+    _run(1, 256, 4, 2, 64, 64, 9, mode, seed=401)
+
+
+def test_layer_no_D_no_bias():
+    _run(2, 128, 2, 2, 64, 64, 8, "positive", seed=402, use_D=False, use_bias=False)
+
+
+def test_layer_headdim_128_ragged_levels():
+    _run(1, 192, 2, 1, 128, 64, 10, "positive", seed=403, backward=False)
+
+
+def test_layer_fp32_bf16x3():
+    _run(1, 128, 2, 2, 64, 64, 8, "positive", seed=404, dtype=torch.float32,
+         tol=(1e-4, 1e-4, 1e-4), backward=False)
+
+
+def test_layer_bwd_deterministic():
+    """Two backward passes give bit-identical gradients (fixed-order per-head sums)."""
+    from hattention.mamba_apis import hmamba_chunk_scan_combined
+    x, dt, A, Bm, Cm, dl, L, D, bias = _inputs(1, 256, 4, 4, 64, 64, 9, 405, torch.bfloat16)
+    outs = []
+    for _ in range(2):
+        leaves = [t.to(DEV).requires_grad_(True) for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
+        y, _ = hmamba_chunk_scan_combined(*leaves[:7], 64, D=leaves[7], dt_bias=leaves[8],
+                                          dt_softplus=True, **_kw(9, "positive"))
+        y.backward(torch.ones_like(y))
+        outs.append([t.grad.clone() for t in leaves])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_layer_full_size_matches_torch_chain():
+    """North-star shape (B=4 T=16384 H=16 P=N=64, L=15): the fused layer against
+    the reference's torch expressions on the GPU around the same scan
+    (hattention_kernel), forward and gradients."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_kernel
+    from hattention.mamba_apis import hmamba_chunk_scan_combined
+    B, T, H, G, P, N, Lv = 4, 16384, 16, 16, 64, 64, 15
+    x, dt, A, Bm, Cm, dl, L, D, bias = (t.to(DEV) for t in
+                                        _inputs(B, T, H, G, P, N, Lv, 406, torch.bfloat16))
+    print("[layer] full size", flush=True)
+    a = [t.clone().requires_grad_(True) for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
+    y1, _ = hmamba_chunk_scan_combined(*a[:7], 64, D=a[7], dt_bias=a[8], dt_softplus=True,
+                                       **_kw(Lv, "positive"))
+    b = [t.clone().requires_grad_(True) for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
+    d = torch.nn.functional.softplus(b[1] + b[8][None, None])
+    lam = torch.nn.functional.softplus(b[6][None, None] * b[5])
+    y2 = hattention_kernel(b[4], b[3], b[0] * d[..., None], None, b[2][None, None] * d, lam,
+                           None, False, 2, HType.WEAK, HStruct.MAMBA2)
+    y2 = y2 + b[0] * b[7][None, None, :, None]
+    dy = torch.randn_like(y1)
+    y1.backward(dy)
+    y2.backward(dy.to(y2.dtype))
+    torch.cuda.synchronize()
+    mx, fro = _errs(y1, y2)
+    assert mx < 1e-2 and fro < 5e-3, (mx, fro)
+    for name, g1, g2 in zip(["x", "dt", "A", "B", "C", "dl", "L", "D", "dt_bias"], a, b):
+        e, _ = _errs(g1.grad, g2.grad)
+        print(f"  d{name}: max-rel {e:.2e}", flush=True)
+        assert e < 2e-2, (name, e)

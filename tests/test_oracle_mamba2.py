@@ -137,3 +137,42 @@ def test_backward_forms_agree_and_dg_identity():
     assert rel(dg_from_identity, dg) < 1e-10
     # and the lambda form of the row sums: sum_l lambda dlambda = q . dq
     assert rel((l * dl).sum(-1), (q * dq).sum(-1)) < 1e-10
+
+
+def test_layer_fwd_scan_forms_agree_and_lambda_special_values():
+    """layer_fwd (mamba_apis.py:346-403) with the chunked level scan equals it
+    with the materialised form; lambda modes hit their closed-form values."""
+    torch.manual_seed(21)
+    B, T, H, G, P, N, Lv = 1, 128, 2, 1, 3, 4, 8
+    x = torch.randn(B, T, H, P, dtype=torch.float64)
+    dt = torch.randn(B, T, H, dtype=torch.float64) - 2
+    A = -torch.rand(H, dtype=torch.float64) - 0.5
+    Bm = torch.randn(B, T, G, N, dtype=torch.float64)
+    Cm = torch.randn(B, T, G, N, dtype=torch.float64)
+    dl = torch.randn(B, T, H, Lv, dtype=torch.float64)
+    L = torch.randn(H, Lv, dtype=torch.float64)
+    D = torch.randn(H, dtype=torch.float64)
+    bias = torch.randn(H, dtype=torch.float64) * 0.1
+    for mode in ("positive", "bounded", None):
+        y1 = M.layer_fwd(x, dt, A, Bm, Cm, dl, L, D, bias, mode)
+        y2 = M.layer_fwd(x, dt, A, Bm, Cm, dl, L, D, bias, mode,
+                         scan=lambda q, k, v, g, l: M.materialized_fwd(q, k, v, g, l))
+        assert rel(y1, y2) < 1e-12, mode
+    zeros = torch.zeros(1, 1, 1, 1, dtype=torch.float64)
+    one = torch.ones(1, 1, dtype=torch.float64)
+    assert abs(M.layer_lambda(one, zeros, "positive").item() - math.log(2.0)) < 1e-15
+    assert abs(M.layer_lambda(-1e3 * one, zeros + 1, "bounded").item() - 1.0) < 1e-15
+    assert M.layer_lambda(2 * one, zeros + 3, None).item() == 6.0
+
+
+def test_layer_fwd_gradcheck():
+    torch.manual_seed(22)
+    B, T, H, G, P, N, Lv = 1, 8, 2, 1, 2, 3, 4
+    args = [torch.randn(B, T, H, P), torch.randn(B, T, H) - 1, -torch.rand(H) - 0.5,
+            torch.randn(B, T, G, N), torch.randn(B, T, G, N), torch.randn(B, T, H, Lv),
+            torch.randn(H, Lv), torch.randn(H), torch.randn(H) * 0.1]
+    args = [a.double().requires_grad_(True) for a in args]
+    for mode in ("positive", "bounded", None):
+        fn = lambda *a: M.layer_fwd(*a, lambda_mode=mode,
+                                    scan=lambda q, k, v, g, l: M.materialized_fwd(q, k, v, g, l))
+        assert torch.autograd.gradcheck(fn, args, eps=1e-6, atol=1e-7), mode

@@ -247,6 +247,78 @@ def layer_bench(dev, stream, n_steps, warmup):
         del leaves
     res["shape"] = {"batch": B, "seq_len": T, "heads": H, "headdim": P, "dstate": N,
                     "levels": L, "lambda_mode": "positive", "dtype_x_bc_dl": "bf16"}
+    del base, dy, x, dt, Bm, Cm, dl
+    res["split_conv1d"] = split_layer_bench(dev, stream, n_steps, warmup)
+    return res
+
+
+def split_layer_bench(dev, stream, n_steps, warmup):
+    """hmamba_split_conv1d_scan_combined at the north-star scan shape (ngroups 1,
+    conv width 4, out-projection 1024 -> 1024, zxbcdtdl bf16, fp32 parameters):
+    the HIP conv1d + SiLU and gated RMSNorm kernels around the fused scan,
+    against torch's grouped conv1d and the RMSNorm expressions around the same
+    scan.  Forward and forward + backward."""
+    from hattention.base import HType, HStruct
+    from hattention.mamba_apis import hmamba_chunk_scan_combined, hmamba_split_conv1d_scan_combined
+    B, T, H, P, N, L, G, W = NS["B"], NS["T"], NS["H"], NS["V"], NS["K"], NS["L"], 1, 4
+    dim = H * P
+    width = 2 * dim + 2 * G * N + H + H * L
+    gen = torch.Generator("cpu").manual_seed(1007)
+    zx = torch.randn(B, T, width, generator=gen)
+    zx[..., 2 * dim + 2 * G * N:2 * dim + 2 * G * N + H] -= 2.5
+    zx = zx.bfloat16().to(dev)
+    prm = [t.to(dev) for t in (torch.randn(dim + 2 * G * N, W, generator=gen) * 0.5,
+                               torch.randn(dim + 2 * G * N, generator=gen) * 0.1,
+                               torch.randn(H, generator=gen) * 0.1,
+                               -torch.exp(torch.rand(H, generator=gen)),
+                               torch.randn(H, L, generator=gen) * 0.5, torch.randn(H, generator=gen),
+                               1 + 0.1 * torch.randn(dim, generator=gen),
+                               torch.randn(dim, dim, generator=gen) / dim ** 0.5,
+                               torch.randn(dim, generator=gen) * 0.1)]
+    kw = dict(lambda_mode="positive", lambda_level_max=L, lambda_level_base=2,
+              lambda_htype=HType.WEAK, lambda_hstruct=HStruct.MAMBA2, lambda_level_fixed=True)
+
+    def fused(z, cw, cb, db, A, Lp, D, rw, ow, ob):
+        return hmamba_split_conv1d_scan_combined(
+            z, cw, cb, db, A, Lp, D, 64, rmsnorm_weight=rw, rmsnorm_eps=1e-6, outproj_weight=ow,
+            outproj_bias=ob, headdim=P, ngroups=G, norm_before_gate=False, **kw)
+
+    def chain(z, cw, cb, db, A, Lp, D, rw, ow, ob):
+        zz, xBC, dt, dl = torch.split(z, [dim, dim + 2 * G * N, H, H * L], dim=-1)
+        xBC = torch.nn.functional.conv1d(torch.nn.functional.pad(xBC.transpose(1, 2), (W - 1, 0)),
+                                         cw[:, None, :].to(z.dtype), cb.to(z.dtype),
+                                         groups=dim + 2 * G * N)
+        xBC = torch.nn.functional.silu(xBC).transpose(1, 2)
+        x, Bm, Cm = torch.split(xBC, [dim, G * N, G * N], dim=-1)
+        y, _ = hmamba_chunk_scan_combined(x.reshape(B, T, H, P), dt, A, Bm.reshape(B, T, G, N),
+                                          Cm.reshape(B, T, G, N), dl.reshape(B, T, H, L), Lp, 64,
+                                          D=D, dt_bias=db, dt_softplus=True, **kw)
+        u = y.reshape(B, T, dim) * torch.nn.functional.silu(zz)
+        u = u * torch.rsqrt((u * u).mean(-1, keepdim=True) + 1e-6) * rw
+        return torch.nn.functional.linear(u, ow, ob)
+
+    res = {}
+    for name, fn in (("fused", fused), ("torch_conv_norm", chain)):
+        with torch.no_grad():
+            for _ in range(warmup):
+                fn(zx, *prm)
+            wall_f, _ = _time_region(lambda: fn(zx, *prm), n_steps, stream)
+        leaves = [zx.detach().clone().requires_grad_(True)] + \
+            [t.detach().clone().requires_grad_(True) for t in prm]
+
+        def fb():
+            for t in leaves:
+                t.grad = None
+            fn(*leaves).sum().backward()
+
+        for _ in range(max(1, warmup)):
+            fb()
+        wall_fb, _ = _time_region(fb, max(1, n_steps // 2), stream)
+        res[name] = {"fwd_tokens_per_s": B * T / wall_f, "fwd_ms": wall_f * 1e3,
+                     "fwd_bwd_tokens_per_s": B * T / wall_fb, "fwd_bwd_ms": wall_fb * 1e3}
+        del leaves
+    res["shape"] = {"batch": B, "seq_len": T, "d_inner": dim, "heads": H, "headdim": P,
+                    "dstate": N, "ngroups": G, "conv_width": W, "levels": L, "d_out": dim}
     return res
 
 

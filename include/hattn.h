@@ -288,6 +288,60 @@ int hattn_mamba2_layer_bwd(const void* x, const void* dt, const float* A, const 
                            int dtype_dx, int dtype_ddt, int dtype_ddl, void* ws,
                            size_t ws_bytes, void* stream);
 
+/*
+ * Depthwise causal conv1d + SiLU of hmamba_split_conv1d_scan_combined
+ * (hattention/mamba_apis.py:206-213, causal_conv1d_fn with activation "silu"):
+ *   pre[b,s,d] = bias[d] + sum_{w<W} weight[d,w] in[b, s-(W-1)+w, d],  out = silu(pre)
+ * The input is the column window [col0, col0 + Dc) of rows of stride ld
+ * (elements) of a [B, S, ld] tensor (the xBC channels of zxbcdtdl); the output
+ * channels [0, d1), [d1, d2), [d2, Dc) go to the contiguous tensors out0
+ * [B,S,d1], out1 [B,S,d2-d1], out2 [B,S,Dc-d2] (x, B, C).  weight [Dc, W],
+ * bias [Dc] or NULL; W <= 8.
+ */
+int hattn_causal_conv1d_silu_fwd(const void* in, long long ld, long long col0, const void* weight,
+                                 const void* bias, void* out0, void* out1, void* out2, int B,
+                                 int S, int Dc, int d1, int d2, int W, int dtype_in,
+                                 int dtype_w, int dtype_out, void* stream);
+
+/*
+ * Backward of the conv + SiLU given the gradients g0, g1, g2 of out0 / out1 /
+ * out2: din is written into the column window [colo, colo + Dc) of rows of
+ * stride ldo (the xBC slice of the zxbcdtdl gradient); dweight [Dc, W] and
+ * dbias [Dc] (fp32, either may be NULL) are reduced in a fixed order.
+ * Workspace: hattn_causal_conv1d_silu_bwd_workspace(B, S, Dc, W) bytes.
+ */
+size_t hattn_causal_conv1d_silu_bwd_workspace(int B, int S, int Dc, int W);
+int hattn_causal_conv1d_silu_bwd(const void* in, long long ld, long long col0,
+                                 const void* weight, const void* bias, const void* g0,
+                                 const void* g1, const void* g2, void* din, long long ldo,
+                                 long long colo, float* dweight, float* dbias, int B, int S,
+                                 int Dc, int d1, int d2, int W, int dtype_in, int dtype_w,
+                                 int dtype_g0, int dtype_g1, int dtype_g2, int dtype_din,
+                                 void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Gated RMSNorm of hmamba_split_conv1d_scan_combined (mamba_apis.py:247-255,
+ * rmsnorm_fn with z, no bias, norm_before_gate=False, one group):
+ *   u = y * silu(z),  r = (mean_j u_j^2 + eps)^-1/2,  out = u * r * weight
+ * y, out [rows, n] contiguous; z rows of stride ldz (the z slice of zxbcdtdl);
+ * weight [n]; rstd [rows] fp32 receives r for the backward.
+ */
+int hattn_gated_rmsnorm_fwd(const void* y, const void* z, long long ldz, const void* weight,
+                            void* out, float* rstd, long long rows, int n, float eps,
+                            int dtype_y, int dtype_z, int dtype_w, int dtype_out, void* stream);
+
+/*
+ * Backward of the gated RMSNorm: dy [rows, n]; dz into rows of stride lddz;
+ * dweight [n] fp32 reduced in a fixed order.  Workspace:
+ * hattn_gated_rmsnorm_bwd_workspace(rows, n) bytes.
+ */
+size_t hattn_gated_rmsnorm_bwd_workspace(long long rows, int n);
+int hattn_gated_rmsnorm_bwd(const void* y, const void* z, long long ldz, const void* weight,
+                            const float* rstd, const void* dout, void* dy, void* dz,
+                            long long lddz, float* dweight, long long rows, int n, int dtype_y,
+                            int dtype_z, int dtype_w, int dtype_dout, int dtype_dy,
+                            int dtype_dz, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

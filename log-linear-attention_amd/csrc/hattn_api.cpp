@@ -69,6 +69,27 @@ hipError_t hattn_mamba2_layer_bwd_launch(const void* x, const void* dt, const fl
                                          int softplus, int mode, const int* bf,
                                          hipStream_t stream);
 
+size_t hattn_conv1d_bwd_ws_bytes(int B, int S, int Dc, int W);
+size_t hattn_rmsnorm_bwd_ws_bytes(long rows, int n);
+hipError_t hattn_conv1d_silu_fwd_launch(const void* in, long ld, long col0, const void* wt,
+                                        const void* bias, void* o0, void* o1, void* o2, int B,
+                                        int S, int Dc, int d1, int d2, int W, int fin, int fw,
+                                        int fo, hipStream_t stream);
+hipError_t hattn_conv1d_silu_bwd_launch(const void* in, long ld, long col0, const void* wt,
+                                        const void* bias, const void* g0, const void* g1,
+                                        const void* g2, void* din, long ldo, long colo,
+                                        float* dw, float* db, float* ws, int B, int S, int Dc,
+                                        int d1, int d2, int W, int fin, int fw, int fg0, int fg1,
+                                        int fg2, int fdi, hipStream_t stream);
+hipError_t hattn_gated_rmsnorm_fwd_launch(const void* y, const void* z, long ldz, const void* w,
+                                          void* out, float* rstd, long rows, int n, float eps,
+                                          int fy, int fz, int fw, int fo, hipStream_t stream);
+hipError_t hattn_gated_rmsnorm_bwd_launch(const void* y, const void* z, long ldz, const void* w,
+                                          const float* rstd, const void* dout, void* dy, void* dz,
+                                          long lddz, float* dw, float* ws, long rows, int n,
+                                          int fy, int fz, int fw, int fdo, int fdy, int fdz,
+                                          hipStream_t stream);
+
 namespace {
 
 thread_local char g_err[512] = {0};
@@ -450,6 +471,109 @@ int hattn_mamba2_layer_bwd(const void* x, const void* dt, const float* A, const 
                                                  T, H, P, L, dt_softplus ? 1 : 0, lambda_mode, bfx,
                                                  (hipStream_t)stream),
                    "hattn_mamba2_layer_bwd launch");
+}
+
+namespace {
+int flags(const int* codes, int* out, int n) {
+  for (int i = 0; i < n; ++i) {
+    out[i] = bf_flag(codes[i]);
+    if (out[i] < 0) return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype code %d (bf16 or fp32 only)", codes[i]);
+  }
+  return HATTN_OK;
+}
+int conv_check(int B, int S, int Dc, int d1, int d2, int W, long long ld, long long col0) {
+  if (B <= 0 || S <= 0 || Dc <= 0 || W <= 0) return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (W > 8) return fail(HATTN_ERR_NOT_IMPLEMENTED, "conv width %d above 8", W);
+  if (!(0 <= d1 && d1 <= d2 && d2 <= Dc)) return fail(HATTN_ERR_VALUE, "channel split %d %d of %d", d1, d2, Dc);
+  if (col0 < 0 || ld < col0 + Dc) return fail(HATTN_ERR_VALUE, "row stride %lld too small", ld);
+  return HATTN_OK;
+}
+}  // namespace
+
+int hattn_causal_conv1d_silu_fwd(const void* in, long long ld, long long col0, const void* weight,
+                                 const void* bias, void* out0, void* out1, void* out2, int B,
+                                 int S, int Dc, int d1, int d2, int W, int dtype_in,
+                                 int dtype_w, int dtype_out, void* stream) {
+  if (int st = conv_check(B, S, Dc, d1, d2, W, ld, col0)) return st;
+  if (!in || !weight || (d1 > 0 && !out0) || (d2 > d1 && !out1) || (Dc > d2 && !out2))
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const int codes[3] = {dtype_in, dtype_w, dtype_out};
+  int f[3];
+  if (int st = flags(codes, f, 3)) return st;
+  return check_hip(hattn_conv1d_silu_fwd_launch(in, (long)ld, (long)col0, weight, bias, out0, out1,
+                                                out2, B, S, Dc, d1, d2, W, f[0], f[1], f[2],
+                                                (hipStream_t)stream),
+                   "hattn_causal_conv1d_silu_fwd launch");
+}
+
+size_t hattn_causal_conv1d_silu_bwd_workspace(int B, int S, int Dc, int W) {
+  if (B <= 0 || S <= 0 || Dc <= 0 || W <= 0 || W > 8) return 0;
+  return hattn_conv1d_bwd_ws_bytes(B, S, Dc, W);
+}
+
+int hattn_causal_conv1d_silu_bwd(const void* in, long long ld, long long col0,
+                                 const void* weight, const void* bias, const void* g0,
+                                 const void* g1, const void* g2, void* din, long long ldo,
+                                 long long colo, float* dweight, float* dbias, int B, int S,
+                                 int Dc, int d1, int d2, int W, int dtype_in, int dtype_w,
+                                 int dtype_g0, int dtype_g1, int dtype_g2, int dtype_din,
+                                 void* ws, size_t ws_bytes, void* stream) {
+  if (int st = conv_check(B, S, Dc, d1, d2, W, ld, col0)) return st;
+  if (colo < 0 || ldo < colo + Dc) return fail(HATTN_ERR_VALUE, "gradient row stride %lld too small", ldo);
+  if (!in || !weight || !din || (d1 > 0 && !g0) || (d2 > d1 && !g1) || (Dc > d2 && !g2))
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_conv1d_bwd_ws_bytes(B, S, Dc, W);
+  if (!ws || ws_bytes < need) return fail(HATTN_ERR_VALUE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
+  const int codes[6] = {dtype_in, dtype_w, d1 > 0 ? dtype_g0 : HATTN_FP32,
+                        d2 > d1 ? dtype_g1 : HATTN_FP32, Dc > d2 ? dtype_g2 : HATTN_FP32, dtype_din};
+  int f[6];
+  if (int st = flags(codes, f, 6)) return st;
+  return check_hip(hattn_conv1d_silu_bwd_launch(in, (long)ld, (long)col0, weight, bias, g0, g1, g2, din,
+                                                (long)ldo, (long)colo, dweight, dbias, (float*)ws, B, S,
+                                                Dc, d1, d2, W, f[0], f[1], f[2], f[3], f[4], f[5],
+                                                (hipStream_t)stream),
+                   "hattn_causal_conv1d_silu_bwd launch");
+}
+
+int hattn_gated_rmsnorm_fwd(const void* y, const void* z, long long ldz, const void* weight,
+                            void* out, float* rstd, long long rows, int n, float eps,
+                            int dtype_y, int dtype_z, int dtype_w, int dtype_out, void* stream) {
+  if (rows <= 0 || n <= 0) return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (ldz < n) return fail(HATTN_ERR_VALUE, "z row stride %lld below n=%d", ldz, n);
+  if (!y || !z || !weight || !out || !rstd) return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const int codes[4] = {dtype_y, dtype_z, dtype_w, dtype_out};
+  int f[4];
+  if (int st = flags(codes, f, 4)) return st;
+  return check_hip(hattn_gated_rmsnorm_fwd_launch(y, z, (long)ldz, weight, out, rstd, (long)rows, n,
+                                                  eps, f[0], f[1], f[2], f[3], (hipStream_t)stream),
+                   "hattn_gated_rmsnorm_fwd launch");
+}
+
+size_t hattn_gated_rmsnorm_bwd_workspace(long long rows, int n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return hattn_rmsnorm_bwd_ws_bytes((long)rows, n);
+}
+
+int hattn_gated_rmsnorm_bwd(const void* y, const void* z, long long ldz, const void* weight,
+                            const float* rstd, const void* dout, void* dy, void* dz,
+                            long long lddz, float* dweight, long long rows, int n, int dtype_y,
+                            int dtype_z, int dtype_w, int dtype_dout, int dtype_dy,
+                            int dtype_dz, void* ws, size_t ws_bytes, void* stream) {
+  if (rows <= 0 || n <= 0) return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (ldz < n || lddz < n) return fail(HATTN_ERR_VALUE, "row stride below n=%d", n);
+  if (n > 8192) return fail(HATTN_ERR_NOT_IMPLEMENTED, "n=%d above 8192", n);
+  if (!y || !z || !weight || !rstd || !dout || !dy || !dz || !dweight)
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_rmsnorm_bwd_ws_bytes((long)rows, n);
+  if (!ws || ws_bytes < need) return fail(HATTN_ERR_VALUE, "workspace of %zu bytes, %zu needed", ws_bytes, need);
+  const int codes[6] = {dtype_y, dtype_z, dtype_w, dtype_dout, dtype_dy, dtype_dz};
+  int f[6];
+  if (int st = flags(codes, f, 6)) return st;
+  return check_hip(hattn_gated_rmsnorm_bwd_launch(y, z, (long)ldz, weight, rstd, dout, dy, dz,
+                                                  (long)lddz, dweight, (float*)ws, (long)rows, n,
+                                                  f[0], f[1], f[2], f[3], f[4], f[5],
+                                                  (hipStream_t)stream),
+                   "hattn_gated_rmsnorm_bwd launch");
 }
 
 }  // extern "C"

@@ -855,19 +855,23 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
   auto load = [&](int j, int part) {
     const unsigned int row0 = (unsigned int)(c0 + j) * kBT;
-    if (part <= 0) load_tile64(rg.q, rq, vo_qk, row0 * qstr * 2, qstr);
+    if (part <= 0) {
+      // g and lambda first: they are one cache line per token row each, so they
+      // take the longest to arrive, and their staging work is the first to use them.
+      // Every wave issues the same loads (wave 0 uses only g, waves 1 .. 3 only
+      // their lambda pieces; a piece past the row reads bytes of the next row, or
+      // zeros past the buffer end, and is not used): a load assigned on some waves
+      // only makes the compiler merge registers after the branch with copies that
+      // wait for the load, i.e. a full memory round trip per chunk
+      rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+      const unsigned int so_l = row0 * lstr * sizeof(TL);
+#pragma unroll
+      for (int r = 0; r < kLP; ++r) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (lpw0 + 3 * r));
+      load_tile64(rg.q, rq, vo_qk, row0 * qstr * 2, qstr);
+    }
     if (part < 0 || part == 1) load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
     if (part == 0 || part == 1) return;
     load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
-    // every wave issues the same loads (wave 0 uses only g, waves 1 .. 3 only
-    // their lambda pieces; a piece past the row reads bytes of the next row, or
-    // zeros past the buffer end, and is not used): a load assigned on some waves
-    // only makes the compiler merge registers after the branch with copies that
-    // wait for the load, i.e. a full memory round trip per chunk
-    rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
-    const unsigned int so_l = row0 * lstr * sizeof(TL);
-#pragma unroll
-    for (int r = 0; r < kLP; ++r) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (lpw0 + 3 * r));
   };
   auto store = [&](int j) {
     store_tile64<1>(rg.q, sm.q, sm.q);

@@ -18,6 +18,7 @@ DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 # (name, restype, argtypes) of every exported entry point, in header order.
 _P, _I, _F, _S = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+_LL = ctypes.c_longlong
 SIGNATURES = [
     ("hattn_version", ctypes.c_char_p, []),
     ("hattn_last_error", ctypes.c_char_p, []),
@@ -43,6 +44,15 @@ SIGNATURES = [
     ("hattn_mamba2_layer_epilogue", _I, [_P] * 4 + [_I] * 7 + [_P]),
     ("hattn_mamba2_layer_bwd_workspace", _S, [_I] * 4),
     ("hattn_mamba2_layer_bwd", _I, [_P] * 18 + [_I] * 17 + [_P, _S, _P]),
+    ("hattn_causal_conv1d_silu_fwd", _I, [_P, _LL, _LL, _P, _P, _P, _P, _P] + [_I] * 9 + [_P]),
+    ("hattn_causal_conv1d_silu_bwd_workspace", _S, [_I] * 4),
+    ("hattn_causal_conv1d_silu_bwd", _I,
+     [_P, _LL, _LL, _P, _P, _P, _P, _P, _P, _LL, _LL, _P, _P] + [_I] * 12 + [_P, _S, _P]),
+    ("hattn_gated_rmsnorm_fwd", _I, [_P, _P, _LL, _P, _P, _P, _LL, _I, ctypes.c_float] + [_I] * 4
+     + [_P]),
+    ("hattn_gated_rmsnorm_bwd_workspace", _S, [_LL, _I]),
+    ("hattn_gated_rmsnorm_bwd", _I, [_P, _P, _LL, _P, _P, _P, _P, _P, _LL, _P, _LL, _I] + [_I] * 6
+     + [_P, _S, _P]),
 ]
 
 _lock = threading.Lock()

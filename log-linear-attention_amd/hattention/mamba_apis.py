@@ -6,6 +6,8 @@ Mirrors hattention/mamba_apis.py:
 * ``hmamba_chunk_scan_combined`` -- :263-404 (dt / A / lambda pre-processing,
   then ``hattention_kernel`` with q=C, k=B, v=x*dt, g=A*dt, plus the D residual;
   with ``return_final_states`` the prefill ``hattention_prefill`` and its HState)
+* ``hmamba_split_conv1d_scan_combined`` -- :116-260 (causal conv1d + SiLU,
+  the layer scan, gated RMSNorm, out-projection)
 * ``hselective_state_update``    -- :407-566 (the same pre-processing for one
   token, then one decode step of the HState)
 
@@ -20,8 +22,8 @@ import torch
 
 from hattention.base import HType, HStruct
 from hattention.kernel import hattention_kernel, hattention_prefill
-from hattention.mamba_layer import (HMambaScanFunction, lambda_mode_code, layer_epilogue,
-                                     layer_prologue)
+from hattention.mamba_layer import (CausalConv1dSilu, GatedRMSNorm, HMambaScanFunction,
+                                     lambda_mode_code, layer_epilogue, layer_prologue)
 
 
 def compute_lambda(L: torch.Tensor, dl: torch.Tensor, lambda_mode: Optional[str]) -> torch.Tensor:
@@ -45,6 +47,93 @@ def compute_lambda_maybe_fixed(L, dl, lambda_mode, lambda_level_max, lambda_leve
             raise ValueError
         return compute_lambda(L=L, dl=dl, lambda_mode=lambda_mode)
     raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+
+
+def hmamba_split_conv1d_scan_combined(
+    zxbcdtdl: torch.Tensor,
+    conv1d_weight: torch.Tensor,
+    conv1d_bias: torch.Tensor,
+    dt_bias: torch.Tensor,
+    A: torch.Tensor,
+    L: torch.Tensor,
+    D: torch.Tensor,
+    chunk_size: int,
+    initial_states: Optional[torch.Tensor] = None,
+    seq_idx: Optional[torch.Tensor] = None,
+    dt_limit: Tuple[float, float] = (0.0, float("inf")),
+    return_final_states: bool = False,
+    activation: str = "silu",
+    rmsnorm_weight: Optional[torch.Tensor] = None,
+    rmsnorm_eps: float = 1e-6,
+    outproj_weight: Optional[torch.Tensor] = None,
+    outproj_bias: Optional[torch.Tensor] = None,
+    headdim: Optional[int] = None,
+    ngroups: int = 1,
+    norm_before_gate: bool = True,
+    lambda_mode: Optional[str] = None,
+    lambda_level_max: Optional[int] = None,
+    lambda_level_base: Optional[int] = None,
+    lambda_htype: Optional[HType] = None,
+    lambda_hstruct: Optional[HStruct] = None,
+    lambda_level_fixed: Optional[bool] = None,
+    lambda_level_module=None,
+) -> torch.Tensor:
+    """mamba_apis.py:116-260: split the packed zxbcdtdl [B, S, 2 dim + 2 G N + H +
+    H Lv] into z, xBC, dt, dl; xBC -> causal conv1d + SiLU (HIP kernel) -> x, B,
+    C; the fused layer scan (hmamba_chunk_scan_combined); gated RMSNorm of the
+    result with z (HIP kernel); the out-projection (torch linear, a library GEMM)."""
+    if initial_states is not None:
+        raise NotImplementedError
+    if seq_idx is not None:
+        raise NotImplementedError
+    if tuple(dt_limit) != (0.0, float("inf")):
+        raise NotImplementedError
+    if return_final_states is not False:
+        raise NotImplementedError
+    if norm_before_gate is not False:
+        raise NotImplementedError
+    if rmsnorm_weight is None:
+        raise NotImplementedError
+    if activation not in ["silu", "swish"]:
+        raise NotImplementedError
+
+    batch, seqlen, _ = zxbcdtdl.shape
+    dlambda = L.shape[-1]
+    nheads, = D.shape
+    dim = nheads * headdim
+    dstate = (zxbcdtdl.shape[-1] - 2 * dim - nheads - nheads * dlambda) // ngroups // 2
+    if D.dim() != 1:
+        raise ValueError
+    if headdim is None:
+        raise ValueError
+    if nheads % ngroups != 0:
+        raise ValueError
+    if zxbcdtdl.shape != (batch, seqlen, 2 * dim + 2 * ngroups * dstate + nheads + nheads * dlambda):
+        raise ValueError
+    if dt_bias.shape != (nheads,) or A.shape != (nheads,) or L.shape != (nheads, dlambda) or \
+            D.shape != (nheads,):
+        raise ValueError
+
+    gn = ngroups * dstate
+    Dc = dim + 2 * gn
+    x, Bm, Cm = CausalConv1dSilu.apply(zxbcdtdl, dim, Dc, dim, dim + gn, conv1d_weight,
+                                       conv1d_bias)
+    c_dt = dim + Dc
+    dt = zxbcdtdl[..., c_dt:c_dt + nheads]
+    dl = zxbcdtdl[..., c_dt + nheads:].reshape(batch, seqlen, nheads, dlambda)
+    y, _ = hmamba_chunk_scan_combined(
+        x=x.view(batch, seqlen, nheads, headdim), dt=dt, A=A,
+        B=Bm.view(batch, seqlen, ngroups, dstate), C=Cm.view(batch, seqlen, ngroups, dstate),
+        dl=dl, L=L, chunk_size=chunk_size, D=D, z=None, dt_bias=dt_bias, dt_softplus=True,
+        seq_idx=seq_idx, cu_seqlens=None, dt_limit=dt_limit,
+        return_final_states=return_final_states, return_varlen_states=False,
+        lambda_mode=lambda_mode, lambda_level_max=lambda_level_max,
+        lambda_level_base=lambda_level_base, lambda_htype=lambda_htype,
+        lambda_hstruct=lambda_hstruct, lambda_level_fixed=lambda_level_fixed,
+        lambda_level_module=lambda_level_module)
+    y = GatedRMSNorm.apply(y.reshape(batch, seqlen, dim), zxbcdtdl, 0, rmsnorm_weight,
+                           rmsnorm_eps)
+    return torch.nn.functional.linear(y, outproj_weight, outproj_bias)
 
 
 def hmamba_chunk_scan_combined(

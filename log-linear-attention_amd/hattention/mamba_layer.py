@@ -164,3 +164,101 @@ class HMambaScanFunction(torch.autograd.Function):
                 dD.to(D.dtype) if D is not None else None,
                 dbias.to(dt_bias.dtype) if dt_bias is not None else None,
                 None, None, None, None)
+
+
+# --------------------------------------------------------------------------
+# hmamba_split_conv1d_scan_combined (mamba_apis.py:116-260): conv1d + SiLU of
+# the xBC channels and the gated RMSNorm of the scan output
+# --------------------------------------------------------------------------
+class CausalConv1dSilu(torch.autograd.Function):
+    """causal_conv1d_fn(xBC, weight, bias, activation="silu") of
+    mamba_apis.py:206-213 on the column window [col0, col0 + Dc) of the packed
+    rows of ``zx`` [B, S, width]; returns the contiguous x, B, C parts
+    (channels [0, d1), [d1, d2), [d2, Dc)).  Backward: the window of the
+    zx gradient (zeros elsewhere), dweight, dbias."""
+
+    @staticmethod
+    def forward(ctx, zx, col0, Dc, d1, d2, weight, bias):
+        B_, S, width = zx.shape
+        W = weight.shape[-1]
+        dev = _lib.require_device(zx, weight, bias)
+        zx = zx.contiguous()
+        wt = weight.reshape(Dc, W).contiguous()
+        bs = bias.contiguous() if bias is not None else None
+        outs = [torch.empty(B_, S, n, dtype=zx.dtype, device=dev) for n in (d1, d2 - d1, Dc - d2)]
+        _lib.check(_lib.load().hattn_causal_conv1d_silu_fwd(
+            _lib.ptr(zx), width, col0, _lib.ptr(wt), _lib.ptr(bs), *(_lib.ptr(o) for o in outs),
+            B_, S, Dc, d1, d2, W, _code(zx.dtype), _code(wt.dtype), _code(zx.dtype),
+            _lib.stream_handle(dev)))
+        ctx.save_for_backward(zx, wt, bs)
+        ctx.cfg = (col0, Dc, d1, d2, weight.shape, bias is not None)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, g0, g1, g2):
+        zx, wt, bs = ctx.saved_tensors
+        col0, Dc, d1, d2, wshape, has_bias = ctx.cfg
+        B_, S, width = zx.shape
+        W = wt.shape[-1]
+        dev = zx.device
+        gs = []
+        for g, n in ((g0, d1), (g1, d2 - d1), (g2, Dc - d2)):
+            gs.append(g.contiguous() if g is not None else torch.zeros(B_, S, n, dtype=zx.dtype,
+                                                                       device=dev))
+        dzx = torch.zeros_like(zx)
+        dw = torch.empty(Dc, W, dtype=torch.float32, device=dev)
+        db = torch.empty(Dc, dtype=torch.float32, device=dev) if has_bias else None
+        lib = _lib.load()
+        ws, ws_ptr, ws_bytes = _lib.workspace(
+            lib.hattn_causal_conv1d_silu_bwd_workspace(B_, S, Dc, W), dev)
+        _lib.check(lib.hattn_causal_conv1d_silu_bwd(
+            _lib.ptr(zx), width, col0, _lib.ptr(wt), _lib.ptr(bs), *(_lib.ptr(g) for g in gs),
+            _lib.ptr(dzx), width, col0, _lib.ptr(dw), _lib.ptr(db), B_, S, Dc, d1, d2, W,
+            _code(zx.dtype), _code(wt.dtype), *(_code(g.dtype) for g in gs), _code(dzx.dtype),
+            ws_ptr, ws_bytes, _lib.stream_handle(dev)))
+        return (dzx, None, None, None, None, dw.to(wt.dtype).reshape(wshape),
+                db.to(bs.dtype) if db is not None else None)
+
+
+class GatedRMSNorm(torch.autograd.Function):
+    """rmsnorm_fn(y, weight, bias=None, z, eps, norm_before_gate=False) of
+    mamba_apis.py:247-255 with z the column window [zcol0, zcol0 + n) of the
+    packed rows of ``zx``: out = u / sqrt(mean(u^2) + eps) * weight, u = y silu(z),
+    in y's dtype.  Backward: dy, the z window of the zx gradient, dweight."""
+
+    @staticmethod
+    def forward(ctx, y, zx, zcol0, weight, eps):
+        B_, S, n = y.shape
+        width = zx.shape[-1]
+        dev = _lib.require_device(y, zx, weight)
+        y, zx, w = y.contiguous(), zx.contiguous(), weight.contiguous()
+        zv = zx.view(-1)[zcol0:]   # z row r starts at r * width
+        out = torch.empty_like(y)
+        rstd = torch.empty(B_ * S, dtype=torch.float32, device=dev)
+        _lib.check(_lib.load().hattn_gated_rmsnorm_fwd(
+            _lib.ptr(y), _lib.ptr(zv), width, _lib.ptr(w), _lib.ptr(out), _lib.ptr(rstd),
+            B_ * S, n, float(eps), _code(y.dtype), _code(zx.dtype), _code(w.dtype),
+            _code(out.dtype), _lib.stream_handle(dev)))
+        ctx.save_for_backward(y, zx, w, rstd)
+        ctx.zcol0 = zcol0
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, zx, w, rstd = ctx.saved_tensors
+        zcol0 = ctx.zcol0
+        B_, S, n = y.shape
+        width = zx.shape[-1]
+        dev = y.device
+        dout = dout.contiguous()
+        dy = torch.empty_like(y)
+        dzx = torch.zeros_like(zx)
+        dw = torch.empty(n, dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        ws, ws_ptr, ws_bytes = _lib.workspace(lib.hattn_gated_rmsnorm_bwd_workspace(B_ * S, n), dev)
+        _lib.check(lib.hattn_gated_rmsnorm_bwd(
+            _lib.ptr(y), _lib.ptr(zx.view(-1)[zcol0:]), width, _lib.ptr(w), _lib.ptr(rstd),
+            _lib.ptr(dout), _lib.ptr(dy), _lib.ptr(dzx.view(-1)[zcol0:]), width, _lib.ptr(dw),
+            B_ * S, n, _code(y.dtype), _code(zx.dtype), _code(w.dtype), _code(dout.dtype),
+            _code(dy.dtype), _code(dzx.dtype), ws_ptr, ws_bytes, _lib.stream_handle(dev)))
+        return dy, dzx, None, dw.to(w.dtype), None

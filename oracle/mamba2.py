@@ -383,3 +383,44 @@ def layer_fwd(x, dt, A, B, C, dl, L, D=None, dt_bias=None, lambda_mode="positive
     if D is not None:
         y = y + x * D[None, None, :, None]
     return (y, (dt, v, g, lam)) if return_intermediates else y
+
+
+def causal_conv1d_silu(x, weight, bias):
+    """causal_conv1d_fn(x, weight, bias, activation="silu") as called at
+    hattention/mamba_apis.py:206-213 (the causal_conv1d package, absent here; its
+    published algorithm): x [B, D, S], weight [D, W], bias [D] ->
+    silu(bias[d] + sum_w weight[d, w] x[b, d, s - (W - 1) + w]), zero left padding;
+    torch's grouped conv1d with W - 1 zeros on the left."""
+    D, W = weight.shape
+    y = torch.nn.functional.conv1d(torch.nn.functional.pad(x, (W - 1, 0)), weight[:, None, :],
+                                   bias, groups=D)
+    return torch.nn.functional.silu(y)
+
+
+def gated_rmsnorm(x, weight, z, eps):
+    """rmsnorm_fn(x, weight, bias=None, z=z, eps, group_size=None,
+    norm_before_gate=False) as called at mamba_apis.py:247-255 (mamba_ssm's
+    gated RMSNorm, absent here; its published algorithm):
+    u = x silu(z), u / sqrt(mean(u^2) + eps) * weight."""
+    u = x * torch.nn.functional.silu(z)
+    return u * torch.rsqrt((u * u).mean(-1, keepdim=True) + eps) * weight
+
+
+def split_conv1d_layer_fwd(zxbcdtdl, conv_w, conv_b, dt_bias, A, L, D, rms_w, eps, out_w, out_b,
+                           headdim, ngroups, lambda_mode="positive", scan=None):
+    """hmamba_split_conv1d_scan_combined (mamba_apis.py:116-260): split z, xBC, dt,
+    dl; causal conv1d + SiLU of xBC; layer_fwd with D and dt_bias; gated RMSNorm
+    with z; out-projection."""
+    Bsz, S, _ = zxbcdtdl.shape
+    H = D.shape[0]
+    Lv = L.shape[-1]
+    dim = H * headdim
+    dstate = (zxbcdtdl.shape[-1] - 2 * dim - H - H * Lv) // ngroups // 2
+    z, xBC, dt, dl = torch.split(zxbcdtdl, [dim, dim + 2 * ngroups * dstate, H, H * Lv], dim=-1)
+    xBC = causal_conv1d_silu(xBC.transpose(1, 2), conv_w, conv_b).transpose(1, 2)
+    x, Bm, Cm = torch.split(xBC, [dim, ngroups * dstate, ngroups * dstate], dim=-1)
+    y = layer_fwd(x.reshape(Bsz, S, H, headdim), dt, A, Bm.reshape(Bsz, S, ngroups, dstate),
+                  Cm.reshape(Bsz, S, ngroups, dstate), dl.reshape(Bsz, S, H, Lv), L, D=D,
+                  dt_bias=dt_bias, lambda_mode=lambda_mode, scan=scan)
+    y = gated_rmsnorm(y.reshape(Bsz, S, dim), rms_w, z, eps)
+    return torch.nn.functional.linear(y, out_w, out_b)

@@ -188,3 +188,82 @@ def test_layer_full_size_matches_torch_chain():
         e, _ = _errs(g1.grad, g2.grad)
         print(f"  d{name}: max-rel {e:.2e}", flush=True)
         assert e < 2e-2, (name, e)
+
+
+# ---------------------------------------------------------------------------
+# hmamba_split_conv1d_scan_combined
+# ---------------------------------------------------------------------------
+def _split_inputs(Bsz, S, H, P, G, N, Lv, W, out_dim, seed, dtype):
+    gen = torch.Generator("cpu").manual_seed(seed)
+    dim = H * P
+    width = 2 * dim + 2 * G * N + H + H * Lv
+    zx = torch.randn(Bsz, S, width, generator=gen)
+    zx[..., 2 * dim + 2 * G * N:2 * dim + 2 * G * N + H] = \
+        zx[..., 2 * dim + 2 * G * N:2 * dim + 2 * G * N + H] * 0.5 - 2.5   # dt
+    p = dict(conv_w=torch.randn(dim + 2 * G * N, W, generator=gen) * 0.5,
+             conv_b=torch.randn(dim + 2 * G * N, generator=gen) * 0.1,
+             dt_bias=torch.randn(H, generator=gen) * 0.1,
+             A=-torch.exp(torch.rand(H, generator=gen)),
+             L=torch.randn(H, Lv, generator=gen) * 0.5,
+             D=torch.randn(H, generator=gen),
+             rms_w=1 + 0.1 * torch.randn(dim, generator=gen),
+             out_w=torch.randn(out_dim, dim, generator=gen) / dim ** 0.5,
+             out_b=torch.randn(out_dim, generator=gen) * 0.1)
+    return zx.to(dtype), p
+
+
+def _split_api(zx, p, P, G, Lv, mode="positive"):
+    from hattention.mamba_apis import hmamba_split_conv1d_scan_combined
+    return hmamba_split_conv1d_scan_combined(
+        zx, p["conv_w"], p["conv_b"], p["dt_bias"], p["A"], p["L"], p["D"], 64,
+        rmsnorm_weight=p["rms_w"], rmsnorm_eps=1e-6, outproj_weight=p["out_w"],
+        outproj_bias=p["out_b"], headdim=P, ngroups=G, norm_before_gate=False, **_kw(Lv, mode))
+
+
+def test_split_conv1d_layer_matches_oracle():
+    """Output and every gradient (zxbcdtdl, conv weight / bias, dt_bias, A, L,
+    D, RMSNorm weight, out-projection) against autograd through the fp64
+    oracle (oracle.mamba2.split_conv1d_layer_fwd); the parameters are fp32 as
+    in an fp32-master layer, the activations bf16."""
+    Bsz, S, H, P, G, N, Lv, W, od = 1, 256, 4, 64, 1, 64, 9, 4, 96
+    zx, p = _split_inputs(Bsz, S, H, P, G, N, Lv, W, od, 410, torch.bfloat16)
+    print(f"[split] B={Bsz} S={S} H={H} P={P} G={G} N={N} L={Lv} W={W}", flush=True)
+    dz = zx.to(DEV).requires_grad_(True)
+    dp = {k: v.to(DEV).requires_grad_(True) for k, v in p.items()}
+    # the layer output comes from the fp32 RMSNorm (y is fp32 with D fp32), so
+    # the out-projection runs in fp32
+    out = _split_api(dz, dp, P, G, Lv)
+    gen = torch.Generator("cpu").manual_seed(411)
+    dy = torch.randn(out.shape, generator=gen)
+    out.backward(dy.to(DEV).to(out.dtype))
+    torch.cuda.synchronize()
+    rz = zx.double().requires_grad_(True)
+    rp = {k: v.double().requires_grad_(True) for k, v in p.items()}
+    ref = M.split_conv1d_layer_fwd(rz, rp["conv_w"], rp["conv_b"], rp["dt_bias"], rp["A"],
+                                   rp["L"], rp["D"], rp["rms_w"], 1e-6, rp["out_w"],
+                                   rp["out_b"], P, G)
+    names = list(p.keys())
+    grads = torch.autograd.grad((ref * dy.double()).sum(), [rz] + [rp[k] for k in names])
+    mx, fro = _errs(out, ref)
+    print(f"  out: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+    assert mx < 2e-2 and fro < 1e-2, (mx, fro)
+    for name, got, want in zip(["zxbcdtdl"] + names, [dz.grad] + [dp[k].grad for k in names],
+                               grads):
+        e, f = _errs(got, want)
+        print(f"  d{name}: max-rel {e:.2e} fro {f:.2e}", flush=True)
+        # per-parameter sums over tokens: bound by the relative Frobenius error
+        assert (e < 2e-2) or (name in ("A", "dt_bias", "L", "D") and f < 2e-2), (name, e, f)
+
+
+def test_split_conv1d_layer_bwd_deterministic():
+    Bsz, S, H, P, G, N, Lv, W, od = 1, 128, 2, 64, 1, 64, 8, 4, 32
+    zx, p = _split_inputs(Bsz, S, H, P, G, N, Lv, W, od, 412, torch.bfloat16)
+    outs = []
+    for _ in range(2):
+        dz = zx.to(DEV).requires_grad_(True)
+        dp = {k: v.to(DEV).requires_grad_(True) for k, v in p.items()}
+        _split_api(dz, dp, P, G, Lv).sum().backward()
+        outs.append([dz.grad.clone()] + [dp[k].grad.clone() for k in p])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

@@ -176,3 +176,44 @@ def test_layer_fwd_gradcheck():
         fn = lambda *a: M.layer_fwd(*a, lambda_mode=mode,
                                     scan=lambda q, k, v, g, l: M.materialized_fwd(q, k, v, g, l))
         assert torch.autograd.gradcheck(fn, args, eps=1e-6, atol=1e-7), mode
+
+
+def test_causal_conv1d_and_gated_rmsnorm_closed_forms():
+    """The conv restatement against a direct loop over taps; the gated RMSNorm
+    against its definition on a hand-picked row; the split layer's forms agree."""
+    torch.manual_seed(23)
+    Bsz, Dch, S, W = 2, 5, 9, 4
+    x = torch.randn(Bsz, Dch, S, dtype=torch.float64)
+    w = torch.randn(Dch, W, dtype=torch.float64)
+    b = torch.randn(Dch, dtype=torch.float64)
+    ref = torch.zeros_like(x)
+    for s in range(S):
+        acc = b[None, :].clone().expand(Bsz, Dch).clone()
+        for k in range(W):
+            sp = s - (W - 1) + k
+            if sp >= 0:
+                acc = acc + w[None, :, k] * x[:, :, sp]
+        ref[:, :, s] = acc * torch.sigmoid(acc)
+    assert rel(M.causal_conv1d_silu(x, w, b), ref) < 1e-14
+    # gated rmsnorm: u = [3, 4] * silu(z) with z large -> silu(z) ~ z ... use z = 0 -> u = 0
+    xx = torch.tensor([[3.0, 4.0]], dtype=torch.float64)
+    zz = torch.full((1, 2), 50.0, dtype=torch.float64)     # silu(50) = 50 (to 1e-20)
+    u = xx * 50.0
+    expect = u / math.sqrt((u * u).mean().item() + 1e-6) * torch.tensor([2.0, -1.0], dtype=torch.float64)
+    assert rel(M.gated_rmsnorm(xx, torch.tensor([2.0, -1.0], dtype=torch.float64), zz, 1e-6), expect) < 1e-14
+    # the split layer with the chunked and the materialised scans
+    H, P, G, N, Lv, S2 = 2, 4, 1, 3, 8, 128
+    dim = H * P
+    width = 2 * dim + 2 * G * N + H + H * Lv
+    zx = torch.randn(1, S2, width, dtype=torch.float64)
+    args = dict(conv_w=torch.randn(dim + 2 * G * N, 4, dtype=torch.float64) * 0.5,
+                conv_b=torch.randn(dim + 2 * G * N, dtype=torch.float64) * 0.1,
+                dt_bias=torch.randn(H, dtype=torch.float64) * 0.1 - 2,
+                A=-torch.rand(H, dtype=torch.float64) - 0.5, L=torch.randn(H, Lv, dtype=torch.float64),
+                D=torch.randn(H, dtype=torch.float64), rms_w=torch.randn(dim, dtype=torch.float64),
+                eps=1e-6, out_w=torch.randn(6, dim, dtype=torch.float64),
+                out_b=torch.randn(6, dtype=torch.float64), headdim=P, ngroups=G)
+    y1 = M.split_conv1d_layer_fwd(zx, **args)
+    y2 = M.split_conv1d_layer_fwd(zx, **args,
+                                  scan=lambda q, k, v, g, l: M.materialized_fwd(q, k, v, g, l))
+    assert rel(y1, y2) < 1e-12

@@ -171,3 +171,24 @@ def test_hattention_kernel_api_matches_chunkwise():
     ref = chunked_scan_fwd(*(x.double().cpu() for x in (q, k, v, g, l)))[0]
     mx, fro = _errs(o, ref)
     assert o.dtype == q.dtype and mx < TOL_MAX and fro < TOL_FRO
+
+
+def test_config0_fp32_against_recurrent():
+    """BASELINE config 0 (the reference's CPU-runnable case): B=2 T=1024 H=4
+    dk=dv=64 L=11, fp32 inputs (bf16x3 kernels), checked to 1e-4 against the
+    Fenwick recurrent restatement (recurrent.py) on two rows and the chunked
+    level-scan restatement on all rows."""
+    from hattention.chunkwise import chunkwise_fwd
+    from hattention.base import HType
+    from oracle.mamba2 import recurrent_fwd
+    B, T, H, K, V, L = 2, 1024, 4, 64, 64, 11
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=1010, dtype=torch.float32)
+    o, _, _ = chunkwise_fwd(*(x.cuda() for x in (q, k, v, g, l)), False, 2, HType.WEAK, 64, False)
+    torch.cuda.synchronize()
+    for (b, h) in [(0, 0), (1, 3)]:
+        sl = lambda x, i: x[b:b + 1, :, i:i + 1].double()
+        ref = recurrent_fwd(sl(q, h), sl(k, h), sl(v, h), sl(g, h), sl(l, h))
+        mx, fro = _errs(o[b:b + 1, :, h:h + 1], ref)
+        print(f"  recurrent row ({b},{h}): max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < TOL_X3 and fro < TOL_X3, (b, h, mx, fro)
+    _run(B, T, H, K, V, L, seed=1010, dtype=torch.float32)

@@ -397,6 +397,10 @@ int layer_dims_check(int B, int T, int H, int P, int L) {
   if (P % 4 != 0 || (P / 4) > 64 || ((P / 4) & (P / 4 - 1)) != 0)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "P=%d (a multiple of 4 with P/4 a power of two <= 64)", P);
   if (L > 32) return fail(HATTN_ERR_NOT_IMPLEMENTED, "L=%d above 32", L);
+  // the elementwise kernels index elements in 32 bits
+  if ((long long)B * T * H * (P > L ? P : L) >= (1LL << 31))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "B*T*H*max(P, L) = %lld elements (below 2^31)",
+                (long long)B * T * H * (P > L ? P : L));
   return HATTN_OK;
 }
 }  // namespace
@@ -484,6 +488,7 @@ int flags(const int* codes, int* out, int n) {
 int conv_check(int B, int S, int Dc, int d1, int d2, int W, long long ld, long long col0) {
   if (B <= 0 || S <= 0 || Dc <= 0 || W <= 0) return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (W > 8) return fail(HATTN_ERR_NOT_IMPLEMENTED, "conv width %d above 8", W);
+  if ((long long)B * S >= (1LL << 31)) return fail(HATTN_ERR_NOT_IMPLEMENTED, "B*S above 2^31 - 1");
   if (!(0 <= d1 && d1 <= d2 && d2 <= Dc)) return fail(HATTN_ERR_VALUE, "channel split %d %d of %d", d1, d2, Dc);
   if (col0 < 0 || ld < col0 + Dc) return fail(HATTN_ERR_VALUE, "row stride %lld too small", ld);
   return HATTN_OK;

@@ -21,6 +21,9 @@
 // kernels are bound by HBM, and a uniform branch per load costs nothing there.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
+#include <initializer_list>
+
 #include "common.h"
 
 namespace hattn {
@@ -61,6 +64,32 @@ __device__ __forceinline__ float lambda_of(float Lv, float dlv, int mode) {
   return Lv * dlv;
 }
 
+// Ordered column sums of partial rows: out column c (of ncol) = sum over
+// b < nblk of ws[b * stride + c].  Grid ceil(ncol / 64) workgroups of 16
+// waves; wave g adds rows g, g + 16, ... in order, then the 16 wave sums are
+// added in order, so the result does not depend on timing.
+__device__ __forceinline__ float ordered_colsum(const float* __restrict__ ws, long stride,
+                                                int nblk, int ncol, int c) {
+  __shared__ float part[16][64];
+  const int g = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float s0 = 0.f, s1 = 0.f;   // two interleaved chains, added at the end
+  if (c < ncol) {
+    int b = g;
+    for (; b + 16 < nblk; b += 32) {
+      s0 += ws[(size_t)b * stride + c];
+      s1 += ws[(size_t)(b + 16) * stride + c];
+    }
+    if (b < nblk) s0 += ws[(size_t)b * stride + c];
+  }
+  part[g][lane] = s0 + s1;
+  __syncthreads();
+  float sum = 0.f;
+  if (g == 0)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum += part[i][lane];
+  return sum;
+}
+
 }  // namespace
 
 struct LayerDt {
@@ -74,23 +103,25 @@ __global__ __launch_bounds__(256) void mamba2_layer_prologue_kernel(
     const float* __restrict__ dt_bias, const void* __restrict__ dl, const void* __restrict__ Lp,
     void* __restrict__ v, float* __restrict__ g, void* __restrict__ lam, long rows, int H,
     int P, int L, int softplus, int mode, LayerDt f, int nbx) {
+  // 32-bit index arithmetic (the host keeps rows * max(P, L) below 2^31); P is a
+  // power of two
+  const unsigned int lp = 31 - __builtin_clz((unsigned int)P);
   if ((int)blockIdx.x < nbx) {
-    const long q4 = (long)blockIdx.x * 256 + threadIdx.x;
-    const long e0 = 4 * q4;
-    if (e0 >= rows * P) return;
-    const long r = e0 / P;
-    const int h = (int)(r % H);
+    const unsigned int e0 = 4u * (blockIdx.x * 256u + threadIdx.x);
+    if (e0 >= (unsigned int)(rows * P)) return;
+    const unsigned int r = e0 >> lp;
+    const int h = (int)(r % (unsigned int)H);
     float d = ld1(dt, r, f.dt) + (dt_bias ? dt_bias[h] : 0.f);
     if (softplus) d = softplus20(d);
     const floatx4 xv = ld4(x, e0, f.x);
     st4(v, e0, floatx4{xv[0] * d, xv[1] * d, xv[2] * d, xv[3] * d}, f.v);
     if (e0 == r * P) g[r] = A[h] * d;
   } else {
-    const long e = (long)(blockIdx.x - nbx) * 256 + threadIdx.x;
-    if (e >= rows * L) return;
-    const long r = e / L;
+    const unsigned int e = (blockIdx.x - nbx) * 256u + threadIdx.x;
+    if (e >= (unsigned int)(rows * L)) return;
+    const unsigned int r = e / (unsigned int)L;
     const int l = (int)(e - r * L);
-    const int h = (int)(r % H);
+    const int h = (int)(r % (unsigned int)H);
     st1(lam, e, lambda_of(ld1(Lp, (size_t)h * L + l, f.lp), ld1(dl, e, f.dl), mode), f.lam);
   }
 }
@@ -99,9 +130,9 @@ __global__ __launch_bounds__(256) void mamba2_layer_prologue_kernel(
 __global__ __launch_bounds__(256) void mamba2_layer_epilogue_kernel(
     const void* __restrict__ y, const void* __restrict__ x, const float* __restrict__ D,
     void* __restrict__ out, long rows, int H, int P, int ybf, int xbf, int obf) {
-  const long e0 = 4 * ((long)blockIdx.x * 256 + threadIdx.x);
-  if (e0 >= rows * P) return;
-  const int h = (int)((e0 / P) % H);
+  const unsigned int e0 = 4u * (blockIdx.x * 256u + threadIdx.x);
+  if (e0 >= (unsigned int)(rows * P)) return;
+  const int h = (int)((e0 >> (31 - __builtin_clz((unsigned int)P))) % (unsigned int)H);
   const float d = D[h];
   const floatx4 a = ld4(y, e0, ybf), b = ld4(x, e0, xbf);
   st4(out, e0, floatx4{a[0] + b[0] * d, a[1] + b[1] * d, a[2] + b[2] * d, a[3] + b[3] * d}, obf);
@@ -111,13 +142,12 @@ struct LayerBwdDt {
   int x, dt, dl, lp, dy, dv, dlam, dx, ddt, ddl;   // 1 = bf16, 0 = fp32
 };
 
-constexpr int kLayerMaxL = 32;   // lambda levels
-constexpr int kLayerNQ = 3 + kLayerMaxL;
-
 // Backward: grid (nblk, H); workgroup (blk, h) owns the rows bt*H + h for bt in
 // its contiguous share of [0, B*T).  A row is handled by tpr = P / 4 threads
-// (four elements each, P / 4 a power of two <= 64).  Per-head partials
-// [dA, ddt_bias, dD, dL[0..L)] go to ws[h][blk][3 + L].
+// (four elements each, P / 4 a power of two <= 64); lambda entry l of a row is
+// handled by its thread l % tpr (NI >= ceil(L / tpr) entries per thread).
+// Per-head partials [dA, ddt_bias, dD, dL[0..L)] go to ws[h][blk][3 + L].
+template <int NI>
 __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
     const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ A,
     const float* __restrict__ dt_bias, const void* __restrict__ dl, const void* __restrict__ Lp,
@@ -125,16 +155,17 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
     const float* __restrict__ dg, const void* __restrict__ dlam, void* __restrict__ dx,
     void* __restrict__ ddt, void* __restrict__ ddl, float* __restrict__ ws, long BT, int H,
     int P, int L, int softplus, int mode, LayerBwdDt f) {
-  __shared__ float red[kLayerNQ][256];
+  __shared__ float red[3][256];
+  __shared__ float redL[NI * 256];   // [l][ri]: L * rpi <= NI * tpr * rpi = NI * 256
   const int tid = threadIdx.x, h = blockIdx.y, blk = blockIdx.x, nblk = gridDim.x;
   const int tpr = P / 4, rpi = 256 / tpr;
   const int j = tid % tpr, ri = tid / tpr;
   const long per = (BT + nblk - 1) / nblk;
   const long bt0 = (long)blk * per, bt1 = min(BT, bt0 + per);
   const float Ah = A[h], bias = dt_bias ? dt_bias[h] : 0.f, Dh = D ? D[h] : 0.f;
-  float accA = 0.f, accB = 0.f, accD = 0.f, accL[kLayerMaxL];
+  float accA = 0.f, accB = 0.f, accD = 0.f, accL[NI];   // lambda entries j + i tpr, i < NI
 #pragma unroll
-  for (int i = 0; i < kLayerMaxL; ++i) accL[i] = 0.f;
+  for (int i = 0; i < NI; ++i) accL[i] = 0.f;
   for (long bt = bt0 + ri; bt < bt1; bt += rpi) {
     const long r = bt * H + h;
     const size_t e0 = (size_t)r * P + 4 * j;
@@ -158,7 +189,7 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
       accB += dd;
     }
 #pragma unroll
-    for (int i = 0; i < kLayerMaxL; ++i) {
+    for (int i = 0; i < NI; ++i) {
       const int l = j + i * tpr;
       if (l < L) {
         const size_t el = (size_t)r * L + l;
@@ -188,28 +219,28 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
   red[1][tid] = accB;
   red[2][tid] = accD;
 #pragma unroll
-  for (int i = 0; i < kLayerMaxL; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int l = j + i * tpr;
-    if (l < L) red[3 + l][ri] = accL[i];   // slot ri of level l (rpi slots per level)
+    if (l < L) redL[l * rpi + ri] = accL[i];   // slot ri of level l (rpi slots per level)
   }
   __syncthreads();
   const int nq = 3 + L;
   if (tid < nq) {
+    const float* src = tid < 3 ? red[tid] : redL + (tid - 3) * rpi;
     const int n = tid < 3 ? 256 : rpi;
     float sum = 0.f;
-    for (int i = 0; i < n; ++i) sum += red[tid][i];
+    for (int i = 0; i < n; ++i) sum += src[i];
     ws[((size_t)h * nblk + blk) * nq + tid] = sum;
   }
 }
 
-// Per-head sums over the workgroups, in order.
-__global__ __launch_bounds__(64) void mamba2_layer_bwd_reduce_kernel(
+// Per-head sums over the workgroups, in a fixed order; grid H.
+__global__ __launch_bounds__(1024) void mamba2_layer_bwd_reduce_kernel(
     const float* __restrict__ ws, float* __restrict__ dA, float* __restrict__ ddt_bias,
     float* __restrict__ dD, float* __restrict__ dLp, int nblk, int L) {
-  const int h = blockIdx.x, q = threadIdx.x, nq = 3 + L;
-  if (q >= nq) return;
-  float sum = 0.f;
-  for (int b = 0; b < nblk; ++b) sum += ws[((size_t)h * nblk + b) * nq + q];
+  const int h = blockIdx.x, q = threadIdx.x & 63, nq = 3 + L;
+  const float sum = ordered_colsum(ws + (size_t)h * nblk * nq, nq, nblk, nq, q);
+  if (threadIdx.x >= 64 || q >= nq) return;
   if (q == 0) { if (dA) dA[h] = sum; }
   else if (q == 1) { if (ddt_bias) ddt_bias[h] = sum; }
   else if (q == 2) { if (dD) dD[h] = sum; }
@@ -272,12 +303,20 @@ hipError_t hattn_mamba2_layer_bwd_launch(const void* x, const void* dt, const fl
   const long BT = (long)B * T;
   const int nblk = layer_bwd_nblk(BT, H);
   const LayerBwdDt f{bf[0], bf[1], bf[2], bf[3], bf[4], bf[5], bf[6], bf[7], bf[8], bf[9]};
-  hipLaunchKernelGGL(mamba2_layer_bwd_kernel, dim3(nblk, H), dim3(256), 0, stream, x, dt, A,
-                     dt_bias, dl, Lp, D, dy, dv, dg, dlam, dx, ddt, ddl, ws, BT, H, P, L, softplus,
-                     mode, f);
+  const int tpr = P / 4, ni = (L + tpr - 1) / tpr;   // lambda entries per thread
+#define LAYER_BWD(NI_)                                                                         \
+  hipLaunchKernelGGL((mamba2_layer_bwd_kernel<NI_>), dim3(nblk, H), dim3(256), 0, stream, x,   \
+                     dt, A, dt_bias, dl, Lp, D, dy, dv, dg, dlam, dx, ddt, ddl, ws, BT, H, P, L, \
+                     softplus, mode, f)
+  if (ni <= 1) LAYER_BWD(1);
+  else if (ni <= 2) LAYER_BWD(2);
+  else if (ni <= 4) LAYER_BWD(4);
+  else if (ni <= 8) LAYER_BWD(8);
+  else LAYER_BWD(32);
+#undef LAYER_BWD
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(mamba2_layer_bwd_reduce_kernel, dim3(H), dim3(64), 0, stream, ws, dA,
+  hipLaunchKernelGGL(mamba2_layer_bwd_reduce_kernel, dim3(H), dim3(1024), 0, stream, ws, dA,
                      ddt_bias, dD, dLp, nblk, L);
   return hipGetLastError();
 }
@@ -301,24 +340,27 @@ __device__ __forceinline__ float dsilu_f(float x) {
   return s * (1.f + x * (1.f - s));
 }
 
-constexpr int kConvMaxW = 8;
-
-// one thread per (b, s, d); d fastest
+// grid (B * S, ceil(Dc / 256)): one thread per (b, s, d), d fastest; the
+// kernel width W (1..8) is a template argument
+template <int W>
 __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(
     const void* __restrict__ in, long ld, long col0, const void* __restrict__ wt,
     const void* __restrict__ bias, void* __restrict__ o0, void* __restrict__ o1,
-    void* __restrict__ o2, long BS, int S, int Dc, int d1, int d2, int W, int fin, int fw,
-    int fo) {
-  const long e = (long)blockIdx.x * 256 + threadIdx.x;
-  if (e >= BS * Dc) return;
-  const long bs = e / Dc;
-  const int d = (int)(e - bs * Dc);
-  const int s = (int)(bs % S);
-  float acc = bias ? ld1(bias, d, fw) : 0.f;
+    void* __restrict__ o2, long BS, int S, int Dc, int d1, int d2, int fin, int fw, int fo) {
+  const long bs = blockIdx.x;
+  const int d = blockIdx.y * 256 + threadIdx.x;
+  if (d >= Dc) return;
+  const int s = (int)(blockIdx.x % (unsigned int)S);
+  float xv[W], wv[W];
+#pragma unroll
   for (int w = 0; w < W; ++w) {
     const int sp = s - (W - 1) + w;
-    if (sp >= 0) acc += ld1(wt, (size_t)d * W + w, fw) * ld1(in, (size_t)(bs - s + sp) * ld + col0 + d, fin);
+    wv[w] = ld1(wt, (size_t)d * W + w, fw);
+    xv[w] = sp >= 0 ? ld1(in, (size_t)(bs - s + sp) * ld + col0 + d, fin) : 0.f;
   }
+  float acc = bias ? ld1(bias, d, fw) : 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) acc += wv[w] * xv[w];
   const float y = silu_f(acc);
   if (d < d1) st1(o0, (size_t)bs * d1 + d, y, fo);
   else if (d < d2) st1(o1, (size_t)bs * (d2 - d1) + (d - d1), y, fo);
@@ -333,93 +375,96 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(
 // ws[blk][64 cg + c][W + 1] and are summed in order afterwards.
 constexpr int kConvTile = 64;
 
+template <int W>
 __global__ __launch_bounds__(256) void conv1d_silu_bwd_kernel(
     const void* __restrict__ in, long ld, long col0, const void* __restrict__ wt,
     const void* __restrict__ bias, const void* __restrict__ g0, const void* __restrict__ g1,
     const void* __restrict__ g2, void* __restrict__ din, long ldo, long colo,
-    float* __restrict__ ws, int B, int S, int Dc, int d1, int d2, int W, int fin, int fw,
+    float* __restrict__ ws, int B, int S, int Dc, int d1, int d2, int fin, int fw,
     int fg0, int fg1, int fg2, int fdi) {
-  __shared__ float xs[kConvTile + 2 * kConvMaxW][64];   // input rows s0-(W-1) .. s0+63+(W-1)
-  __shared__ float dp[kConvTile + kConvMaxW][64];       // dpre rows s0 .. s0+63+(W-1)
-  __shared__ float red[4][64][kConvMaxW + 1];
+  constexpr int NX = kConvTile + 2 * (W - 1);   // staged input rows s0-(W-1) .. s0+63+(W-1)
+  constexpr int NP = kConvTile + W - 1;         // dpre rows s0 .. s0+63+(W-1)
+  __shared__ float xs[NX][64];
+  __shared__ float dp[NP][64];
+  __shared__ float red[4][64][W + 1];
   const int tid = threadIdx.x, c = tid & 63, sr = tid >> 6;
   const int cg = blockIdx.x, blk = blockIdx.y, nblk = gridDim.y;
   const int d = 64 * cg + c;
   const bool dok = d < Dc;
   const int ntile_s = (S + kConvTile - 1) / kConvTile;
   const long ntiles = (long)B * ntile_s;
-  float wv[kConvMaxW];
+  float wv[W];
 #pragma unroll
-  for (int w = 0; w < kConvMaxW; ++w) wv[w] = (dok && w < W) ? ld1(wt, (size_t)d * W + w, fw) : 0.f;
+  for (int w = 0; w < W; ++w) wv[w] = dok ? ld1(wt, (size_t)d * W + w, fw) : 0.f;
   const float bv = (dok && bias) ? ld1(bias, d, fw) : 0.f;
-  float accw[kConvMaxW], accb = 0.f;
+  float accw[W], accb = 0.f;
 #pragma unroll
-  for (int w = 0; w < kConvMaxW; ++w) accw[w] = 0.f;
+  for (int w = 0; w < W; ++w) accw[w] = 0.f;
   auto gout = [&](long bs) -> float {
     if (d < d1) return ld1(g0, (size_t)bs * d1 + d, fg0);
     if (d < d2) return ld1(g1, (size_t)bs * (d2 - d1) + (d - d1), fg1);
     return ld1(g2, (size_t)bs * (Dc - d2) + (d - d2), fg2);
   };
+  // fixed trip counts (row sr + 4 i) so that each phase's loads issue together
   for (long tile = blk; tile < ntiles; tile += nblk) {
     const int b = (int)(tile / ntile_s), s0 = (int)(tile % ntile_s) * kConvTile;
     const long base = (long)b * S;
-    // input rows s0 - (W-1) .. s0 + 63 + (W-1)
-    const int nx = kConvTile + 2 * (W - 1);
-    for (int r = sr; r < nx; r += 4) {
-      const int sp = s0 - (W - 1) + r;
-      xs[r][c] = (dok && sp >= 0 && sp < S) ? ld1(in, (size_t)(base + sp) * ld + col0 + d, fin) : 0.f;
+    float xr[(NX + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (NX + 3) / 4; ++i) {
+      const int r = sr + 4 * i, sp = s0 - (W - 1) + r;
+      xr[i] = (r < NX && dok && sp >= 0 && sp < S) ? ld1(in, (size_t)(base + sp) * ld + col0 + d, fin) : 0.f;
     }
+    float gr[(NP + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (NP + 3) / 4; ++i) {
+      const int r = sr + 4 * i, sp = s0 + r;
+      gr[i] = (r < NP && dok && sp < S) ? gout(base + sp) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < (NX + 3) / 4; ++i)
+      if (sr + 4 * i < NX) xs[sr + 4 * i][c] = xr[i];
     __syncthreads();
-    // dpre rows s0 .. s0 + 63 + (W-1)
-    const int np = kConvTile + W - 1;
-    for (int r = sr; r < np; r += 4) {
-      const int sp = s0 + r;
-      float v = 0.f;
-      if (dok && sp < S) {
+    // dpre = dout * silu'(pre) (zero beyond the sequence: gr is zero there)
+#pragma unroll
+    for (int i = 0; i < (NP + 3) / 4; ++i) {
+      const int r = sr + 4 * i;
+      if (r < NP) {
         float pre = bv;
+#pragma unroll
         for (int w = 0; w < W; ++w) pre += wv[w] * xs[r + w][c];   // xs row r + w is s0 + r - (W-1) + w
-        v = gout(base + sp) * dsilu_f(pre);
+        dp[r][c] = s0 + r < S ? gr[i] * dsilu_f(pre) : 0.f;
       }
-      dp[r][c] = v;
     }
     __syncthreads();
     // din and the weight / bias partials for rows s0 .. s0 + 63
-    for (int r = sr; r < kConvTile; r += 4) {
-      const int sp = s0 + r;
-      if (!dok || sp >= S) continue;
-      float gi = 0.f;
-      for (int w = 0; w < W; ++w) gi += wv[w] * dp[r + (W - 1) - w][c];   // out row sp + W-1-w
-      st1(din, (size_t)(base + sp) * ldo + colo + d, gi, fdi);
-      const float dpr = dp[r][c];
-      accb += dpr;
-      for (int w = 0; w < W; ++w) accw[w] += dpr * xs[r + w][c];        // input row sp-(W-1)+w
+#pragma unroll
+    for (int i = 0; i < kConvTile / 4; ++i) {
+      const int r = sr + 4 * i, sp = s0 + r;
+      if (dok && sp < S) {
+        float gi = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) gi += wv[w] * dp[r + (W - 1) - w][c];   // out row sp + W-1-w
+        st1(din, (size_t)(base + sp) * ldo + colo + d, gi, fdi);
+        const float dpr = dp[r][c];
+        accb += dpr;
+#pragma unroll
+        for (int w = 0; w < W; ++w) accw[w] += dpr * xs[r + w][c];        // input row sp-(W-1)+w
+      }
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int w = 0; w < kConvMaxW; ++w) red[sr][c][w] = accw[w];
-  red[sr][c][kConvMaxW] = accb;
+  for (int w = 0; w < W; ++w) red[sr][c][w] = accw[w];
+  red[sr][c][W] = accb;
   __syncthreads();
   if (sr == 0 && dok) {
     float* out = ws + ((size_t)blk * Dc + d) * (W + 1);
-    for (int w = 0; w < W; ++w) out[w] = red[0][c][w] + red[1][c][w] + red[2][c][w] + red[3][c][w];
-    out[W] = red[0][c][kConvMaxW] + red[1][c][kConvMaxW] + red[2][c][kConvMaxW] + red[3][c][kConvMaxW];
+#pragma unroll
+    for (int w = 0; w <= W; ++w) out[w] = red[0][c][w] + red[1][c][w] + red[2][c][w] + red[3][c][w];
   }
 }
 
-// dweight[d][w], dbias[d] = ordered sums over the workgroups' partials
-__global__ __launch_bounds__(256) void conv1d_bwd_reduce_kernel(const float* __restrict__ ws,
-                                                                float* __restrict__ dw,
-                                                                float* __restrict__ db,
-                                                                int nblk, int Dc, int W) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= Dc * (W + 1)) return;
-  const int d = e / (W + 1), q = e % (W + 1);
-  float sum = 0.f;
-  for (int b = 0; b < nblk; ++b) sum += ws[((size_t)b * Dc + d) * (W + 1) + q];
-  if (q < W) { if (dw) dw[(size_t)d * W + q] = sum; }
-  else if (db) db[d] = sum;
-}
 
 // Gated RMSNorm, one wave per row of n features: u = y silu(z), r = rsqrt(mean
 // u^2 + eps), out = u r w; r is saved for the backward.
@@ -482,13 +527,162 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_bwd_kernel(
     ws[(size_t)blk * n + j] = wacc[j] + wacc[n + j] + wacc[2 * n + j] + wacc[3 * n + j];
 }
 
-__global__ __launch_bounds__(256) void rows_sum_kernel(const float* __restrict__ ws,
-                                                       float* __restrict__ out, int nblk, int n) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= n) return;
-  float sum = 0.f;
-  for (int b = 0; b < nblk; ++b) sum += ws[(size_t)b * n + j];
-  out[j] = sum;
+// Vector forms of the gated RMSNorm for n % 8 == 0, n <= 512 NC, 16-byte aligned
+// rows: lane l of a row's wave owns elements 512 c + 8 l .. + 7 (c < NC) and
+// keeps them in registers between the sum and the output.
+__device__ __forceinline__ void ld8(const void* p, size_t i, int bf, float* o) {
+  if (bf) {
+    const bf16x8 a = *(const bf16x8*)((const __bf16*)p + i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = (float)a[k];
+  } else {
+    const floatx4 a = *(const floatx4*)((const float*)p + i);
+    const floatx4 b = *(const floatx4*)((const float*)p + i + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { o[k] = a[k]; o[4 + k] = b[k]; }
+  }
+}
+__device__ __forceinline__ void st8(void* p, size_t i, const float* x, int bf) {
+  if (bf) {
+    bf16x8 a;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = (__bf16)x[k];
+    *(bf16x8*)((__bf16*)p + i) = a;
+  } else {
+    *(floatx4*)((float*)p + i) = floatx4{x[0], x[1], x[2], x[3]};
+    *(floatx4*)((float*)p + i + 4) = floatx4{x[4], x[5], x[6], x[7]};
+  }
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) void gated_rmsnorm_fwd_vec_kernel(
+    const void* __restrict__ y, const void* __restrict__ z, long ldz, const void* __restrict__ w,
+    void* __restrict__ out, float* __restrict__ rstd, long rows, int n, float eps, int fy,
+    int fz, int fw, int fo) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float u[NC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = 512 * c + 8 * lane;
+    if (j < n) {
+      float yy[8], zz[8];
+      ld8(y, (size_t)row * n + j, fy, yy);
+      ld8(z, (size_t)row * ldz + j, fz, zz);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        u[c][k] = yy[k] * silu_f(zz[k]);
+        ss += u[c][k] * u[c][k];
+      }
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  const float r = rsqrtf(ss / n + eps);
+  if (lane == 0) rstd[row] = r;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = 512 * c + 8 * lane;
+    if (j < n) {
+      float wv[8], o[8];
+      ld8(w, j, fw, wv);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = u[c][k] * r * wv[k];
+      st8(out, (size_t)row * n + j, o, fo);
+    }
+  }
+}
+
+// Backward, vector form: as gated_rmsnorm_bwd_kernel, with each wave's dw
+// partial kept in registers over its rows.
+template <int NC>
+__global__ __launch_bounds__(256) void gated_rmsnorm_bwd_vec_kernel(
+    const void* __restrict__ y, const void* __restrict__ z, long ldz, const void* __restrict__ w,
+    const float* __restrict__ rstd, const void* __restrict__ dout, void* __restrict__ dy,
+    void* __restrict__ dz, long lddz, float* __restrict__ ws, long rows, int n, int fy, int fz,
+    int fw, int fdo, int fdy, int fdz) {
+  extern __shared__ float wacc[];   // [4][n] per-wave dw partials
+  const int q = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int blk = blockIdx.x, nblk = gridDim.x;
+  float wv[NC][8], acc[NC][8];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = 512 * c + 8 * lane;
+    if (j < n) ld8(w, j, fw, wv[c]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (j >= n) wv[c][k] = 0.f;
+      acc[c][k] = 0.f;
+    }
+  }
+  for (long row = (long)blk * 4 + q; row < rows; row += 4L * nblk) {
+    const float r = rstd[row];
+    float yy[NC][8], zz[NC][8], go[NC][8];
+    float sgu = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int j = 512 * c + 8 * lane;
+      if (j < n) {
+        ld8(y, (size_t)row * n + j, fy, yy[c]);
+        ld8(z, (size_t)row * ldz + j, fz, zz[c]);
+        ld8(dout, (size_t)row * n + j, fdo, go[c]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sgu += go[c][k] * wv[c][k] * (yy[c][k] * silu_f(zz[c][k]));
+      }
+    }
+    for (int m = 32; m >= 1; m >>= 1) sgu += __shfl_xor(sgu, m, 64);
+    const float mgu = sgu / n;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int j = 512 * c + 8 * lane;
+      if (j < n) {
+        float oy[8], oz[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float sz = silu_f(zz[c][k]), u = yy[c][k] * sz;
+          const float du = r * (go[c][k] * wv[c][k] - u * r * r * mgu);
+          oy[k] = du * sz;
+          oz[k] = du * yy[c][k] * dsilu_f(zz[c][k]);
+          acc[c][k] += go[c][k] * u * r;
+        }
+        st8(dy, (size_t)row * n + j, oy, fdy);
+        st8(dz, (size_t)row * lddz + j, oz, fdz);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = 512 * c + 8 * lane;
+    if (j < n) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) wacc[q * n + j + k] = acc[c][k];
+    }
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += 256)
+    ws[(size_t)blk * n + j] = wacc[j] + wacc[n + j] + wacc[2 * n + j] + wacc[3 * n + j];
+}
+
+// dweight[d][w], dbias[d] = ordered sums over the workgroups' partials
+// ws[blk][d][W + 1]
+__global__ __launch_bounds__(1024) void conv1d_bwd_reduce_kernel(const float* __restrict__ ws,
+                                                                 float* __restrict__ dw,
+                                                                 float* __restrict__ db,
+                                                                 int nblk, int Dc, int W) {
+  const int ncol = Dc * (W + 1), e = blockIdx.x * 64 + (threadIdx.x & 63);
+  const float sum = ordered_colsum(ws, ncol, nblk, ncol, e);
+  if (threadIdx.x >= 64 || e >= ncol) return;
+  const int d = e / (W + 1), q = e % (W + 1);
+  if (q < W) { if (dw) dw[(size_t)d * W + q] = sum; }
+  else if (db) db[d] = sum;
+}
+
+__global__ __launch_bounds__(1024) void rows_sum_kernel(const float* __restrict__ ws,
+                                                        float* __restrict__ out, int nblk, int n) {
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  const float sum = ordered_colsum(ws, n, nblk, n, c);
+  if (threadIdx.x < 64 && c < n) out[c] = sum;
 }
 
 }  // namespace hattn
@@ -498,6 +692,14 @@ int conv_bwd_nblk(long tiles, int ncg) {
   long n = 2048 / (ncg > 0 ? ncg : 1);
   if (n > tiles) n = tiles;
   return (int)(n < 1 ? 1 : n);
+}
+// 512-element chunks per row for the vector RMSNorm kernels (1..4), or 0 for the
+// scalar kernels: needs n % 8 == 0, row strides % 8 == 0 and 16-byte aligned bases
+int norm_vec_chunks(int n, long ld1, long ld2, std::initializer_list<const void*> ptrs) {
+  if (n % 8 != 0 || ld1 % 8 != 0 || ld2 % 8 != 0 || n > 2048) return 0;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return 0;
+  return (n + 511) / 512;
 }
 int norm_bwd_nblk(long rows) {
   long n = (rows + 3) / 4;
@@ -520,9 +722,19 @@ hipError_t hattn_conv1d_silu_fwd_launch(const void* in, long ld, long col0, cons
                                         int fo, hipStream_t stream) {
   using namespace hattn;
   const long BS = (long)B * S;
-  const long n = (BS * Dc + 255) / 256;
-  hipLaunchKernelGGL(conv1d_silu_fwd_kernel, dim3((unsigned)n), dim3(256), 0, stream, in, ld,
-                     col0, wt, bias, o0, o1, o2, BS, S, Dc, d1, d2, W, fin, fw, fo);
+  const dim3 grid((unsigned)BS, (unsigned)((Dc + 255) / 256));
+  switch (W) {
+#define CONV_FWD(W_)                                                                          \
+  case W_:                                                                                    \
+    hipLaunchKernelGGL((conv1d_silu_fwd_kernel<W_>), grid, dim3(256), 0, stream, in, ld, col0, \
+                       wt, bias, o0, o1, o2, BS, S, Dc, d1, d2, fin, fw, fo);                  \
+    break;
+    CONV_FWD(1) CONV_FWD(2) CONV_FWD(3) CONV_FWD(4) CONV_FWD(5) CONV_FWD(6) CONV_FWD(7)
+    CONV_FWD(8)
+#undef CONV_FWD
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -536,12 +748,22 @@ hipError_t hattn_conv1d_silu_bwd_launch(const void* in, long ld, long col0, cons
   const int ncg = (Dc + 63) / 64;
   const long tiles = (long)B * ((S + kConvTile - 1) / kConvTile);
   const int nblk = conv_bwd_nblk(tiles, ncg);
-  hipLaunchKernelGGL(conv1d_silu_bwd_kernel, dim3(ncg, nblk), dim3(256), 0, stream, in, ld, col0,
-                     wt, bias, g0, g1, g2, din, ldo, colo, ws, B, S, Dc, d1, d2, W, fin, fw, fg0,
-                     fg1, fg2, fdi);
+  switch (W) {
+#define CONV_BWD(W_)                                                                            \
+  case W_:                                                                                      \
+    hipLaunchKernelGGL((conv1d_silu_bwd_kernel<W_>), dim3(ncg, nblk), dim3(256), 0, stream, in, \
+                       ld, col0, wt, bias, g0, g1, g2, din, ldo, colo, ws, B, S, Dc, d1, d2,    \
+                       fin, fw, fg0, fg1, fg2, fdi);                                             \
+    break;
+    CONV_BWD(1) CONV_BWD(2) CONV_BWD(3) CONV_BWD(4) CONV_BWD(5) CONV_BWD(6) CONV_BWD(7)
+    CONV_BWD(8)
+#undef CONV_BWD
+    default:
+      return hipErrorInvalidValue;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(conv1d_bwd_reduce_kernel, dim3((Dc * (W + 1) + 255) / 256), dim3(256), 0,
+  hipLaunchKernelGGL(conv1d_bwd_reduce_kernel, dim3((Dc * (W + 1) + 63) / 64), dim3(1024), 0,
                      stream, ws, dw, db, nblk, Dc, W);
   return hipGetLastError();
 }
@@ -550,8 +772,19 @@ hipError_t hattn_gated_rmsnorm_fwd_launch(const void* y, const void* z, long ldz
                                           void* out, float* rstd, long rows, int n, float eps,
                                           int fy, int fz, int fw, int fo, hipStream_t stream) {
   using namespace hattn;
-  hipLaunchKernelGGL(gated_rmsnorm_fwd_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     stream, y, z, ldz, w, out, rstd, rows, n, eps, fy, fz, fw, fo);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  switch (norm_vec_chunks(n, ldz, ldz, {y, z, w, out})) {
+#define NORM_FWD(NC_)                                                                       \
+  case NC_:                                                                                 \
+    hipLaunchKernelGGL((gated_rmsnorm_fwd_vec_kernel<NC_>), grid, dim3(256), 0, stream, y, z, \
+                       ldz, w, out, rstd, rows, n, eps, fy, fz, fw, fo);                    \
+    break;
+    NORM_FWD(1) NORM_FWD(2) NORM_FWD(3) NORM_FWD(4)
+#undef NORM_FWD
+    default:
+      hipLaunchKernelGGL(gated_rmsnorm_fwd_kernel, grid, dim3(256), 0, stream, y, z, ldz, w, out,
+                         rstd, rows, n, eps, fy, fz, fw, fo);
+  }
   return hipGetLastError();
 }
 
@@ -563,12 +796,28 @@ hipError_t hattn_gated_rmsnorm_bwd_launch(const void* y, const void* z, long ldz
   using namespace hattn;
   const int nblk = norm_bwd_nblk(rows);
   const size_t smem = (size_t)4 * n * sizeof(float);
-  hipError_t e = hipFuncSetAttribute((const void*)gated_rmsnorm_bwd_kernel,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int nc = norm_vec_chunks(n, ldz, lddz, {y, z, w, dout, dy, dz});
+  const void* fn = (const void*)gated_rmsnorm_bwd_kernel;
+  if (nc == 1) fn = (const void*)gated_rmsnorm_bwd_vec_kernel<1>;
+  else if (nc == 2) fn = (const void*)gated_rmsnorm_bwd_vec_kernel<2>;
+  else if (nc == 3) fn = (const void*)gated_rmsnorm_bwd_vec_kernel<3>;
+  else if (nc == 4) fn = (const void*)gated_rmsnorm_bwd_vec_kernel<4>;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(gated_rmsnorm_bwd_kernel, dim3(nblk), dim3(256), smem, stream, y, z, ldz, w,
-                     rstd, dout, dy, dz, lddz, ws, rows, n, fy, fz, fw, fdo, fdy, fdz);
+  switch (nc) {
+#define NORM_BWD(NC_)                                                                        \
+  case NC_:                                                                                  \
+    hipLaunchKernelGGL((gated_rmsnorm_bwd_vec_kernel<NC_>), dim3(nblk), dim3(256), smem,     \
+                       stream, y, z, ldz, w, rstd, dout, dy, dz, lddz, ws, rows, n, fy, fz, fw, \
+                       fdo, fdy, fdz);                                                        \
+    break;
+    NORM_BWD(1) NORM_BWD(2) NORM_BWD(3) NORM_BWD(4)
+#undef NORM_BWD
+    default:
+      hipLaunchKernelGGL(gated_rmsnorm_bwd_kernel, dim3(nblk), dim3(256), smem, stream, y, z, ldz,
+                         w, rstd, dout, dy, dz, lddz, ws, rows, n, fy, fz, fw, fdo, fdy, fdz);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(rows_sum_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ws, dw, nblk, n);
+  hipLaunchKernelGGL(rows_sum_kernel, dim3((n + 63) / 64), dim3(1024), 0, stream, ws, dw, nblk, n);
   return hipGetLastError();
 }

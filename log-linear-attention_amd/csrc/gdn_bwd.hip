@@ -112,22 +112,68 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
 #pragma unroll
     for (int j = 0; j < TPW; ++j) dh[e][j] = zero4();
 
+  // Register prefetch: the saved state of the next (chunk, level) pair is
+  // loaded while the current level computes (thread tid owns 16-byte unit tid
+  // of the [32 x K] slice), and the next chunk's q_new / W_new / K_new / U / dO
+  // tiles, lambda columns and last decay while the current chunk computes
+  // (K = 64 only: with K = 128 those registers would spill, and the tiles are
+  // loaded at the chunk start).  Every load is issued unconditionally, clamped
+  // to a valid address where its value is not used: a load under a condition
+  // makes the compiler merge its registers after the branch, which waits for
+  // the load right away.
+  constexpr bool kPrefTiles = KD <= 64;
+  constexpr int UPR = KD / 8, QU = kGC * UPR / 512;   // units per row / per thread
+  static_assert(kBVs * UPR <= 512 && kGC * kBVs / 8 <= 512, "one unit per thread");
+  const __bf16* hsrow = hsave + (size_t)row * NT * nlev * V * KD + (size_t)v0 * KD;
+  u32x4 ph;
+  auto fetch_h = [&](int jc, int e) __attribute__((always_inline)) {
+    const int u = tid % (kBVs * UPR);
+    ph = *(const u32x4*)(hsrow + ((size_t)jc * nlev + e) * V * KD + (size_t)(u / UPR) * KD +
+                         8 * (u % UPR));
+  };
+  u32x4 pq[QU], pw[QU], pk[QU], pu, pdo;
+  float plam, peL;
+  auto fetch_tiles = [&](int jc) __attribute__((always_inline)) {
+    const size_t t0 = (size_t)b * T + (size_t)jc * kGC;
+#pragma unroll
+    for (int i = 0; i < QU; ++i) {
+      const int u = tid + 512 * i, r = u / UPR, c = 8 * (u % UPR);
+      const size_t off = (t0 + r) * hk + (size_t)h * KD + c;
+      pq[i] = *(const u32x4*)(qn + off);
+      pw[i] = *(const u32x4*)(wn + off);
+      pk[i] = *(const u32x4*)(kn + off);
+    }
+    {
+      const int u = tid % (kGC * kBVs / 8);
+      const size_t off = (t0 + (u >> 2)) * hv + (size_t)h * V + v0 + 8 * (u & 3);
+      pu = *(const u32x4*)(un + off);
+      pdo = *(const u32x4*)(dO + off);
+    }
+    const int le = min(tid, nlev * kGC - 1);
+    plam = to_f32<TL>(l[((t0 + le / nlev) * H + h) * L + 7 + le % nlev]);
+    peL = gcum[(t0 + kGC - 1) * H + h];
+  };
+  if (kPrefTiles) fetch_tiles(NT - 1);
+  fetch_h(NT - 1, 0);
+
   for (int ic = NT - 1; ic >= 0; --ic) {
     const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
-    // 512 threads: two 256-thread halves stage the tiles
-    if (w < 4) {
-      g2s_tile<KD>(qn + tok0 * hk + (size_t)h * KD, hk, s.qn, LK);
-      g2s_tile<KD>(wn + tok0 * hk + (size_t)h * KD, hk, s.wn, LK);
-      g2s_tile<kBVs>(un + tok0 * hv + (size_t)h * V + v0, hv, s.u, LVS);
-    } else {
-      g2s_tile<KD, kGC, 256>(kn + tok0 * hk + (size_t)h * KD, hk, s.kn, LK);
-      g2s_tile<kBVs, kGC, 256>(dO + tok0 * hv + (size_t)h * V + v0, hv, s.dO, LVS);
+    if (!kPrefTiles) fetch_tiles(ic);
+#pragma unroll
+    for (int i = 0; i < QU; ++i) {
+      const int u = tid + 512 * i, r = u / UPR, c = 8 * (u % UPR);
+      *(u32x4*)(s.qn + r * LK + c) = pq[i];
+      *(u32x4*)(s.wn + r * LK + c) = pw[i];
+      *(u32x4*)(s.kn + r * LK + c) = pk[i];
     }
-    for (int e2 = tid; e2 < nlev * kGC; e2 += 512) {
-      const int t = e2 / nlev, c = e2 % nlev;
-      s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + 7 + c]);
+    if (tid < kGC * kBVs / 8) {
+      *(u32x4*)(s.u + (tid >> 2) * LVS + 8 * (tid & 3)) = pu;
+      *(u32x4*)(s.dO + (tid >> 2) * LVS + 8 * (tid & 3)) = pdo;
     }
-    const float eL = fexp(gcum[(tok0 + kGC - 1) * H + h]);
+    if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = plam;
+    const float eL = fexp(peL);
+    // the first level's barrier publishes the tiles; the prefetch registers are
+    // reloaded after it
 
     floatx4 adq[APW], adw[APW], adk[APW], adu = zero4();
 #pragma unroll
@@ -136,7 +182,9 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
 
     // the level loop stays rolled (an unrolled one holds every level's fragments
     // at once); the level's dh tiles move to and from a working set through a
-    // uniform switch, so the register array is only indexed by constants
+    // uniform switch, so the register array is only indexed by constants.  The
+    // level's read / write / no-reset flags enter the products as 0 / 1 factors,
+    // so that its LDS reads and MFMAs issue without a branch per product.
 #pragma unroll 1
     for (int e = 0; e < nlev; ++e) {
       {
@@ -152,18 +200,20 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
         }
         const int per = 2 << e;
         const bool rd = (ic >> e) & 1;
-        const bool wr = !rd;
         const bool nr = (ic & (per - 1)) != per - 1;
-        if (w < 4)
-          g2s_tile<KD, kBVs>(hsave + (((size_t)row * NT + ic) * nlev + e) * (size_t)V * KD +
-                                 (size_t)v0 * KD,
-                             KD, s.hs, LK);
+        const float frd = rd ? 1.f : 0.f, fwr = 1.f - frd, fnr = nr ? 1.f : 0.f;
+        if (tid < kBVs * UPR) *(u32x4*)(s.hs + (tid / UPR) * LK + 8 * (tid % UPR)) = ph;
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
           const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
           *(bf16x4*)(s.dhs + (16 * vv + ln) * LK + 16 * kt + 4 * lq) = cvt4(cur[j]);
         }
         __syncthreads();
+        {
+          const bool nxt = e + 1 < nlev;
+          fetch_h(nxt ? ic : max(ic - 1, 0), nxt ? e + 1 : 0);
+        }
+        if (kPrefTiles && e == 0) fetch_tiles(max(ic - 1, 0));
 
         // (i) dV_new = K_new dh, V_new = wr U - nr W_new h, q_new h (for dlambda)
         {
@@ -173,19 +223,18 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
             const bf16x8 bd = *(const bf16x8*)(s.dhs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
             const bf16x8 bh = *(const bf16x8*)(s.hs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
             dv = mfma16x16x32(*(const bf16x8*)(s.kn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bd, dv);
-            if (nr) y = mfma16x16x32(*(const bf16x8*)(s.wn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, y);
-            if (rd) z = mfma16x16x32(*(const bf16x8*)(s.qn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, z);
+            y = mfma16x16x32(*(const bf16x8*)(s.wn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, y);
+            z = mfma16x16x32(*(const bf16x8*)(s.qn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, z);
           }
           bf16x4 dvb, vnb;
           float dlr[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int t = 16 * tt + 4 * lq + i;
-            const float uu = wr ? (float)s.u[t * LVS + 16 * vt + ln] : 0.f;
-            vnb[i] = (__bf16)(uu - y[i]);
+            vnb[i] = (__bf16)(fwr * (float)s.u[t * LVS + 16 * vt + ln] - fnr * y[i]);
             dvb[i] = (__bf16)dv[i];
-            if (wr) adu[i] += dv[i];
-            dlr[i] = rd ? (float)s.dO[t * LVS + 16 * vt + ln] * z[i] : 0.f;
+            adu[i] += fwr * dv[i];
+            dlr[i] = frd * (float)s.dO[t * LVS + 16 * vt + ln] * z[i];
           }
           *(bf16x4*)(s.dvn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = dvb;
           *(bf16x4*)(s.vn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = vnb;
@@ -210,23 +259,24 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
             const int kt = vt * APW + j;
             const bf16x8 bh = tr_frag(s.hs, LK, 0, 16 * kt);    // h^T[v][k]
             const bf16x8 bd = tr_frag(s.dhs, LK, 0, 16 * kt);   // dh^T[v][k]
-            if (rd) {
-              const floatx4 tq = mfma16x16x32(adO, bh, zero4());
+            const floatx4 tq = mfma16x16x32(adO, bh, zero4());
+            const floatx4 tw = mfma16x16x32(advn, bh, zero4());
 #pragma unroll
-              for (int i = 0; i < 4; ++i) adq[j][i] += lam[i] * tq[i];
+            for (int i = 0; i < 4; ++i) {
+              adq[j][i] += frd * lam[i] * tq[i];
+              adw[j][i] += fnr * tw[i];
             }
-            if (nr) adw[j] = mfma16x16x32(advn, bh, adw[j]);
             adk[j] = mfma16x16x32(avn, bd, adk[j]);
           }
-          if (nr) {
+          float dd = 0.f;
 #pragma unroll
-            for (int j = 0; j < TPW; ++j) {
-              const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
-              const bf16x4 hv4 = *(const bf16x4*)(s.hs + (16 * vv + ln) * LK + 16 * kt + 4 * lq);
+          for (int j = 0; j < TPW; ++j) {
+            const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
+            const bf16x4 hv4 = *(const bf16x4*)(s.hs + (16 * vv + ln) * LK + 16 * kt + 4 * lq);
 #pragma unroll
-              for (int i = 0; i < 4; ++i) del += (float)hv4[i] * cur[j][i];
-            }
+            for (int i = 0; i < 4; ++i) dd += (float)hv4[i] * cur[j][i];
           }
+          del += fnr * dd;
         }
 
         // (iii) dh_e <- nr (eL dh_e - W_new^T dV_new) + rd q_new^T (lambda_e o dO)
@@ -236,20 +286,20 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
           floatx4 tw = zero4(), tq = zero4();
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            if (nr) {
-              const bf16x8 bdv = *(const bf16x8*)(s.dvn + (16 * vv + ln) * kLd64 + 32 * c + 8 * lq);
-              tw = mfma16x16x32(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
-            }
-            if (rd) {
-              bf16x8 x = tr_frag(s.dO, LVS, 32 * c, 16 * vv);   // dO[t][v]
+            const bf16x8 bdv = *(const bf16x8*)(s.dvn + (16 * vv + ln) * kLd64 + 32 * c + 8 * lq);
+            tw = mfma16x16x32(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
+            bf16x8 x = tr_frag(s.dO, LVS, 32 * c, 16 * vv);   // dO[t][v]
+            const floatx4 la = *(const floatx4*)(s.lam[e] + 32 * c + 8 * lq);
+            const floatx4 lb = *(const floatx4*)(s.lam[e] + 32 * c + 8 * lq + 4);
 #pragma unroll
-              for (int jj = 0; jj < 8; ++jj)
-                x[jj] = (__bf16)((float)x[jj] * s.lam[e][32 * c + 8 * lq + jj]);
-              tq = mfma16x16x32(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
+            for (int jj = 0; jj < 4; ++jj) {
+              x[jj] = (__bf16)((float)x[jj] * la[jj]);
+              x[4 + jj] = (__bf16)((float)x[4 + jj] * lb[jj]);
             }
+            tq = mfma16x16x32(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) cur[j][i] = (nr ? eL * cur[j][i] - tw[i] : 0.f) + tq[i];
+          for (int i = 0; i < 4; ++i) cur[j][i] = fnr * (eL * cur[j][i] - tw[i]) + frd * tq[i];
         }
         switch (e) {
 #define HATTN_DH_PUT(E) \

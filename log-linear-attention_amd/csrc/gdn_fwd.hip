@@ -302,17 +302,65 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
 #pragma unroll
       for (int n = 0; n < 2; ++n) st[e][m][n] = zero4();
 
+  // Chunk ic + 1's q_new / W_new / K_new / U tiles, lambda columns and last
+  // decay are loaded into registers while chunk ic computes, and chunk ic + 1's
+  // o_intra after chunk ic's output is written; each chunk starts by moving them
+  // to LDS.  Thread tid owns 16-byte units tid + 256 i of each tile.  Every
+  // load is issued unconditionally (clamped to a valid address where its value
+  // is not used): a load under a condition would make the compiler merge its
+  // registers after the branch, which waits for the load right away.
+  constexpr int UPR = KD / 8, QU = kGC * UPR / 256;   // units per row / per thread
+  static_assert(kGC * kBVs / 8 == 256, "one U unit per thread");
+  u32x4 pq[QU], pw[QU], pk[QU], pu;
+  float plam[2], pgl = 0.f, poi[2][4];
+  auto fetch_tiles = [&](int jc) __attribute__((always_inline)) {
+    const size_t t0 = (size_t)b * T + (size_t)jc * kGC;
+#pragma unroll
+    for (int i = 0; i < QU; ++i) {
+      const int u = tid + 256 * i, r = u / UPR, c = 8 * (u % UPR);
+      const size_t off = (t0 + r) * hk + (size_t)h * KD + c;
+      pq[i] = *(const u32x4*)(qn + off);
+      pw[i] = *(const u32x4*)(wn + off);
+      pk[i] = *(const u32x4*)(kn + off);
+    }
+    pu = *(const u32x4*)(un + (t0 + (tid >> 2)) * hv + (size_t)h * V + v0 + 8 * (tid & 3));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e2 = min(tid + 256 * i, nlev * kGC - 1);
+      plam[i] = to_f32<TL>(l[((t0 + e2 / nlev) * H + h) * L + 7 + e2 % nlev]);
+    }
+    pgl = gcum[(t0 + kGC - 1) * H + h];
+  };
+  // without an output (the backward's recompute) the o_intra loads read gcum
+  // row 0 instead, and their values are not used
+  const float* oisrc = o ? oi : gcum;
+  auto fetch_oi = [&](int jc) __attribute__((always_inline)) {
+    const size_t t0 = (size_t)b * T + (size_t)jc * kGC;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        poi[n][i] = oisrc[o ? (t0 + 16 * w + 4 * lq + i) * hv + (size_t)h * V + v0 + 16 * n + ln : 0];
+  };
+  fetch_tiles(0);
+  fetch_oi(0);
+
   for (int ic = 0; ic < NT; ++ic) {
     const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
-    g2s_tile<KD>(qn + tok0 * hk + (size_t)h * KD, hk, s.qn, LK);
-    g2s_tile<KD>(wn + tok0 * hk + (size_t)h * KD, hk, s.wn, LK);
-    g2s_tile<KD>(kn + tok0 * hk + (size_t)h * KD, hk, s.kn, LK);
-    g2s_tile<kBVs>(un + tok0 * hv + (size_t)h * V + v0, hv, s.u, LU);
-    for (int e2 = tid; e2 < nlev * kGC; e2 += 256) {
-      const int t = e2 / nlev, c = e2 % nlev;
-      s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + 7 + c]);
+#pragma unroll
+    for (int i = 0; i < QU; ++i) {
+      const int u = tid + 256 * i, r = u / UPR, c = 8 * (u % UPR);
+      *(u32x4*)(s.qn + r * LK + c) = pq[i];
+      *(u32x4*)(s.wn + r * LK + c) = pw[i];
+      *(u32x4*)(s.kn + r * LK + c) = pk[i];
     }
-    const float glast = gcum[(tok0 + kGC - 1) * H + h];
+    *(u32x4*)(s.u + (tid >> 2) * LU + 8 * (tid & 3)) = pu;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e2 = tid + 256 * i;
+      if (e2 < nlev * kGC) s.lam[e2 % nlev][e2 / nlev] = plam[i];
+    }
+    const float glast = pgl;
     // states -> LDS, bf16 [v][k] (4 consecutive k per lane); with hsave also to
     // hsave[row][chunk][level][v][k] (the state each chunk starts from)
 #pragma unroll
@@ -333,8 +381,12 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
       }
     }
     __syncthreads();
+    fetch_tiles(min(ic + 1, NT - 1));
 
     // ---- reads (q_new h_e) and V_new_e = (write ? U : 0) - (reset ? 0 : W_new h_e) ----
+    // Branch-free per level: both products are always formed and the level's
+    // read / write / reset flags enter as 0 / 1 factors, so the LDS reads and
+    // MFMAs of a level issue back to back instead of one wait per product.
     const bool last = ic == NT - 1;
     floatx4 acc[2] = {zero4(), zero4()};
     {
@@ -344,29 +396,37 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
         aw[c] = *(const bf16x8*)(s.wn + (16 * w + ln) * LK + 32 * c + 8 * lq);
         aq[c] = *(const bf16x8*)(s.qn + (16 * w + ln) * LK + 32 * c + 8 * lq);
       }
+      float uv[2][4];   // U[t = 16w + 4lq + i][16n + ln]
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) uv[n][i] = (float)s.u[(16 * w + 4 * lq + i) * LU + 16 * n + ln];
 #pragma unroll
       for (int e = 0; e < kGMaxLev; ++e) {
         if (e < nlev) {
           const int per = 2 << e;
-          const bool rd = (ic >> e) & 1;
-          const bool wr = !rd;
-          const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
+          const float frd = ((ic >> e) & 1) ? 1.f : 0.f;
+          const float fkeep = (((ic & (per - 1)) == per - 1) && !(last && final_state)) ? 0.f : 1.f;
+          const floatx4 lam4 = *(const floatx4*)(&s.lam[e][16 * w + 4 * lq]);
+          bf16x8 bh[2][KD / 32];
+#pragma unroll
+          for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int c = 0; c < KD / 32; ++c)
+              bh[n][c] = *(const bf16x8*)(s.hs[e] + (16 * n + ln) * LK + 32 * c + 8 * lq);
 #pragma unroll
           for (int n = 0; n < 2; ++n) {
             floatx4 y = zero4(), z = zero4();
 #pragma unroll
             for (int c = 0; c < KD / 32; ++c) {
-              const bf16x8 bh = *(const bf16x8*)(s.hs[e] + (16 * n + ln) * LK + 32 * c + 8 * lq);
-              if (!reset) y = mfma16x16x32(aw[c], bh, y);
-              if (rd && o) z = mfma16x16x32(aq[c], bh, z);
+              y = mfma16x16x32(aw[c], bh[n][c], y);
+              z = mfma16x16x32(aq[c], bh[n][c], z);
             }
             bf16x4 vb4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int t = 16 * w + 4 * lq + i;
-              if (rd) acc[n][i] += s.lam[e][t] * z[i];
-              const float uu = wr ? (float)s.u[t * LU + 16 * n + ln] : 0.f;
-              vb4[i] = (__bf16)(uu - y[i]);
+              acc[n][i] += frd * lam4[i] * z[i];
+              vb4[i] = (__bf16)((1.f - frd) * uv[n][i] - fkeep * y[i]);
             }
             *(bf16x4*)(s.vn[e] + (16 * n + ln) * kLd64 + 16 * w + 4 * lq) = vb4;
           }
@@ -380,9 +440,10 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const size_t idx = (tok0 + 16 * w + 4 * lq + i) * hv + (size_t)h * V + v0 + 16 * n + ln;
-          o[idx] = from_f32<TO>(oi[idx] + acc[n][i]);
+          o[idx] = from_f32<TO>(poi[n][i] + acc[n][i]);
         }
     }
+    fetch_oi(min(ic + 1, NT - 1));
     __syncthreads();
 
     // ---- h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new_e -----------------------
@@ -398,17 +459,22 @@ __global__ __launch_bounds__(256, 1) void gdn_scan_kernel(
         if (e < nlev) {
           const int per = 2 << e;
           const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
+          const float gk = reset ? 0.f : gl;
+          bf16x8 b0[2], b1[2];
 #pragma unroll
           for (int n = 0; n < 2; ++n) {
-            const bf16x8 b0 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 8 * lq);
-            const bf16x8 b1 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 32 + 8 * lq);
+            b0[n] = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 8 * lq);
+            b1[n] = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 32 + 8 * lq);
+          }
+#pragma unroll
+          for (int n = 0; n < 2; ++n) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
               floatx4 x = st[e][m][n];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) x[i] = reset ? 0.f : x[i] * gl;
-              x = mfma16x16x32(ak[m][0], b0, x);
-              x = mfma16x16x32(ak[m][1], b1, x);
+              for (int i = 0; i < 4; ++i) x[i] *= gk;
+              x = mfma16x16x32(ak[m][0], b0[n], x);
+              x = mfma16x16x32(ak[m][1], b1[n], x);
               st[e][m][n] = x;
             }
           }

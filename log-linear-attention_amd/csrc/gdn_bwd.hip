@@ -382,14 +382,22 @@ __device__ __forceinline__ void frt(const float* X, int r0, int c0, float* f) {
   for (int j = 0; j < 8; ++j) f[j] = p[j * LD];
 }
 // Same from global rows of stride rs: sc * sum over np partials pstride apart.
-__device__ __forceinline__ void frg(const float* X, size_t rs, size_t pstride, int np, int r0,
-                                    int c0, float sc, float* f) {
+template <int NP>
+__device__ __forceinline__ void frg(const float* X, size_t rs, size_t pstride, int r0, int c0,
+                                    float sc, float* f) {
   const int lane = threadIdx.x & 63;
   const float* p = X + (size_t)(r0 + (lane & 15)) * rs + c0 + 8 * (lane >> 4);
-  floatx4 a = *(const floatx4*)p, b = *(const floatx4*)(p + 4);
-  for (int pp = 1; pp < np; ++pp) {
-    a += *(const floatx4*)(p + pp * pstride);
-    b += *(const floatx4*)(p + pp * pstride + 4);
+  floatx4 pa[NP], pb[NP];   // every partial's loads first, then the sums in order
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+    pa[pp] = *(const floatx4*)(p + pp * pstride);
+    pb[pp] = *(const floatx4*)(p + pp * pstride + 4);
+  }
+  floatx4 a = pa[0], b = pb[0];
+#pragma unroll
+  for (int pp = 1; pp < NP; ++pp) {
+    a += pa[pp];
+    b += pb[pp];
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -410,17 +418,33 @@ __device__ __forceinline__ floatx4 mma_fb(const float* a, bf16x8 b, floatx4 c) {
   c = mfma16x16x32(A[1], b, c);
   return mfma16x16x32(A[0], b, c);
 }
-// ST[t][c] = (scale ? scale[t] : 1) * sum over np partials of X[t][c], 64 rows of N.
-template <int N, int LS>
+// ST[t][c] = (scale ? scale[t] : 1) * sum over NP partials of X[t][c], 64 rows of N.
+// Two units per step with all their partial loads issued together.
+template <int N, int LS, int NP>
 __device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs, size_t pstride,
-                                           int np, const float* scale) {
-  for (int u = threadIdx.x; u < kGC * N / 4; u += 256) {
-    const int t = u / (N / 4), c = 4 * (u % (N / 4));
-    const float* p = X + (size_t)t * rs + c;
-    floatx4 a = *(const floatx4*)p;
-    for (int pp = 1; pp < np; ++pp) a += *(const floatx4*)(p + pp * pstride);
-    if (scale) a *= scale[t];
-    *(floatx4*)(ST + t * LS + c) = a;
+                                           const float* scale) {
+  constexpr int IT = kGC * N / 4 / 256;
+  static_assert(IT % 2 == 0, "units per thread");
+#pragma unroll 1
+  for (int i0 = 0; i0 < IT; i0 += 2) {
+    floatx4 pv[2][NP];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int u = threadIdx.x + 256 * (i0 + d);
+      const int t = u / (N / 4), c = 4 * (u % (N / 4));
+#pragma unroll
+      for (int pp = 0; pp < NP; ++pp) pv[d][pp] = *(const floatx4*)(X + (size_t)t * rs + c + pp * pstride);
+    }
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int u = threadIdx.x + 256 * (i0 + d);
+      const int t = u / (N / 4), c = 4 * (u % (N / 4));
+      floatx4 a = pv[d][0];
+#pragma unroll
+      for (int pp = 1; pp < NP; ++pp) a += pv[d][pp];
+      if (scale) a *= scale[t];
+      *(floatx4*)(ST + t * LS + c) = a;
+    }
   }
 }
 
@@ -430,13 +454,14 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const TB* __restrict__ beta, const float* __restrict__ gcum, const TL* __restrict__ l,
     const __bf16* __restrict__ dO, const float* __restrict__ dq_p, const float* __restrict__ dw_p,
     const float* __restrict__ dk_p, const float* __restrict__ du, const float* __restrict__ dl_p,
-    const float* __restrict__ del_p, int nvs, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
+    const float* __restrict__ del_p, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
     __bf16* __restrict__ dv, TB* __restrict__ db, float* __restrict__ dg, float* __restrict__ dl,
     int B, int T, int H, int L, int nlev) {
   using Sm = GdnBchunkSmem<KD, VD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
   constexpr int LK = Sm::LK, LV = Sm::LV, LS = Sm::LS, NKT = KD / 16, NVT = VD / 16;
+  constexpr int NPV = VD / kBVs;   // V slices of the level scan = partials per entry
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int NT = T / kGC;
@@ -467,10 +492,21 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     s.r[lane] = fexp(gl - x);
     s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
   }
-  for (int u = tid; u < 7 * kGC; u += 256) {
-    const int t = u / 7, c = u % 7;
-    s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + c]);
-    s.dlam[c][t] = 0.f;
+  {
+    float lv[2];   // both loads issued before either store
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = min(tid + 256 * i, 7 * kGC - 1);
+      lv[i] = to_f32<TL>(l[((tok0 + u / 7) * H + h) * L + u % 7]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = tid + 256 * i;
+      if (u < 7 * kGC) {
+        s.lam[u % 7][u / 7] = lv[i];
+        s.dlam[u % 7][u / 7] = 0.f;
+      }
+    }
   }
   if (tid < kGC) {
     s.dgr[tid] = s.dbr[tid] = s.lastc[tid] = 0.f;
@@ -580,7 +616,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     float ax[KD / 32][8];
 #pragma unroll
     for (int c = 0; c < KD / 32; ++c)
-      frg(dq_p + rowk, hk, BTH * KD, nvs, t16, 32 * c, s.e[t16 + ln], ax[c]);
+      frg<NPV>(dq_p + rowk, hk, BTH * KD, t16, 32 * c, s.e[t16 + ln], ax[c]);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       floatx4 f = zero4();
@@ -643,9 +679,9 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     float a2[KD / 32][8], a3[VD / 32][8];
 #pragma unroll
     for (int c = 0; c < KD / 32; ++c)
-      frg(dw_p + rowk, hk, BTH * KD, nvs, t16, 32 * c, s.e[t16 + ln], a2[c]);
+      frg<NPV>(dw_p + rowk, hk, BTH * KD, t16, 32 * c, s.e[t16 + ln], a2[c]);
 #pragma unroll
-    for (int c = 0; c < VD / 32; ++c) frg(du + rowv, hv, 0, 1, t16, 32 * c, 1.f, a3[c]);
+    for (int c = 0; c < VD / 32; ++c) frg<1>(du + rowv, hv, 0, t16, 32 * c, 1.f, a3[c]);
     float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -740,7 +776,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 
   // live: S0 = dM, S1 = dA, S2 = Aw, S3 = P; the staging region is free
   // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ------------------
-  stage_rows<KD, LS>(ST, dq_p + rowk, hk, BTH * KD, nvs, s.e);
+  stage_rows<KD, LS, NPV>(ST, dq_p + rowk, hk, BTH * KD, s.e);
   __syncthreads();
   floatx4 u2[NKT];
 #pragma unroll
@@ -774,7 +810,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   __syncthreads();
 
   // ---- 11: e o dW_new -> ST; U2 += Aw^T ST ---------------------------------------------
-  stage_rows<KD, LS>(ST, dw_p + rowk, hk, BTH * KD, nvs, s.e);
+  stage_rows<KD, LS, NPV>(ST, dw_p + rowk, hk, BTH * KD, s.e);
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < NKT; ++nt)
@@ -809,7 +845,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
 
   // ---- 13: dK_new -> ST; dK = U1 + beta o U2 + r o dK_new; dbeta, dGc of K_new -------
-  stage_rows<KD, LS>(ST, dk_p + rowk, hk, BTH * KD, nvs, nullptr);
+  stage_rows<KD, LS, NPV>(ST, dk_p + rowk, hk, BTH * KD, nullptr);
   __syncthreads();
   {
     float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
@@ -837,7 +873,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   __syncthreads();
 
   // ---- 14: dU -> ST; GV = Au^T dU + (P o Gamma o Lambda)^T dO; dV = beta o GV --------
-  stage_rows<VD, LS>(ST, du + rowv, hv, 0, 1, nullptr);
+  stage_rows<VD, LS, 1>(ST, du + rowv, hv, 0, nullptr);
   __syncthreads();
   {
     float au[2][8], ar[2][8];
@@ -886,7 +922,8 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     if (t == kGC - 1) {
       float lc = 0.f, de = 0.f;
       for (int u = 0; u < kGC; ++u) lc += s.lastc[u];
-      for (int p = 0; p < nvs; ++p) de += del_p[(size_t)p * B * H * NT + (size_t)row * NT + ic];
+#pragma unroll
+      for (int p = 0; p < NPV; ++p) de += del_p[(size_t)p * B * H * NT + (size_t)row * NT + ic];
       x += lc + s.e[kGC - 1] * de;
     }
 #pragma unroll
@@ -899,11 +936,18 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   for (int u = tid; u < kGC * L; u += 256) {
     const int t = u / L, c = u % L;
+    // inter-chunk columns: the partial loads of every slice issue together
+    // (clamped to column 7 elsewhere, and not used there)
+    const int ce = min(max(c, 7), 6 + nlev) - 7;
+    float pl[NPV];
+#pragma unroll
+    for (int p = 0; p < NPV; ++p) pl[p] = dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + ce];
     float x = 0.f;
     if (c < 7) {
       x = s.dlam[c][t];
     } else if (c < 7 + nlev) {
-      for (int p = 0; p < nvs; ++p) x += dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + c - 7];
+#pragma unroll
+      for (int p = 0; p < NPV; ++p) x += pl[p];
     }
     dl[((tok0 + t) * H + h) * L + c] = x;
   }
@@ -969,7 +1013,7 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
     hipLaunchKernelGGL(kc, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const TB*)beta, gcum, (const TL*)l,
                        (const __bf16*)dO, w.dq_p, w.dw_p, w.dk_p, w.du, w.dl_p, w.del_p,
-                       VD / kBVs, (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, (TB*)db, dg, dl, B, T,
+                       (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, (TB*)db, dg, dl, B, T,
                        H, L, nlev);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

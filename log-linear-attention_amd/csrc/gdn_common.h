@@ -11,14 +11,24 @@ constexpr int kBVs = 32;      // V columns per scan workgroup
 constexpr int kLM = 65;       // row stride of 64 x 64 fp32 LDS matrices
 
 // 16-byte units of a row-major [NR][N] bf16 tile, 256 threads (threads
-// T0 .. T0 + 255 of the workgroup).
+// T0 .. T0 + 255 of the workgroup).  The unit loop has a compile-time trip
+// count and every load is issued before the first LDS store, so the tile costs
+// one memory round trip instead of one per unit.
 template <int N, int NR = kGC, int T0 = 0>
 __device__ __forceinline__ void g2s_tile(const __bf16* __restrict__ src, size_t row_stride,
                                          __bf16* dst, int ld) {
-  constexpr int UPR = N / 8;  // units per row
-  for (int u = (int)threadIdx.x - T0; u < NR * UPR; u += 256) {
-    const int r = u / UPR, c = 8 * (u % UPR);
-    *(uint4*)(dst + r * ld + c) = *(const uint4*)(src + r * row_stride + c);
+  constexpr int UPR = N / 8, NU = NR * UPR, IT = (NU + 255) / 256;   // units per row / in all / per thread
+  const int t = (int)threadIdx.x - T0;
+  u32x4 r[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int u = (NU % 256 == 0) ? t + 256 * i : min(t + 256 * i, NU - 1);
+    r[i] = *(const u32x4*)(src + (size_t)(u / UPR) * row_stride + 8 * (u % UPR));
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int u = t + 256 * i;
+    if (NU % 256 == 0 || u < NU) *(u32x4*)(dst + (u / UPR) * ld + 8 * (u % UPR)) = r[i];
   }
 }
 

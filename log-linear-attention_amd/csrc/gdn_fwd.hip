@@ -94,9 +94,18 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
     s.gc[lane] = x;
     s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
   }
-  for (int e = tid; e < 7 * kGC; e += 256) {
-    const int t = e / 7, c = e % 7;
-    s.lam[c][t] = to_f32<TL>(l[((tok0 + t) * H + h) * L + c]);
+  {
+    float lv[2];   // both loads issued before either store
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = min(tid + 256 * i, 7 * kGC - 1);
+      lv[i] = to_f32<TL>(l[((tok0 + e / 7) * H + h) * L + e % 7]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i;
+      if (e < 7 * kGC) s.lam[e % 7][e / 7] = lv[i];
+    }
   }
   __syncthreads();
 

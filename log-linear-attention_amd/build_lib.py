@@ -6,6 +6,7 @@ Compiles every ``csrc/*.hip`` / ``csrc/*.cpp`` into
 ``hattention/_native/libhattn_hip.so``.  No torch extension machinery: the
 library is a plain C-ABI shared object loaded with ctypes.
 """
+import concurrent.futures
 import glob
 import os
 import shutil
@@ -30,26 +31,32 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
+def _compile_cmd(src: str, obj: str) -> list:
+    inc = ["-I", os.path.join(HERE, "..", "include")]
+    if src.endswith(".cpp"):
+        return [hipcc(), "-c", "-fPIC", "-O2", "-std=c++17", *inc, src, "-o", obj]
+    return [hipcc(), "-c", "-fPIC", "-O3", "-std=c++17", f"--offload-arch={ARCH}", *inc,
+            *DEVICE_FLAGS, src, "-o", obj]
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every source (in parallel, one hipcc process per file) and link."""
     os.makedirs(OUT_DIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
-    objs = []
     tmp = tempfile.mkdtemp(prefix="hattn_build_")
     try:
-        for src in srcs:
-            obj = os.path.join(tmp, os.path.basename(src) + ".o")
-            cmd = [hipcc(), "-c", "-fPIC", "-O3", "-std=c++17", f"--offload-arch={ARCH}",
-                   "-I", os.path.join(HERE, "..", "include"), *DEVICE_FLAGS, src, "-o", obj]
-            if src.endswith(".cpp"):
-                cmd = [hipcc(), "-c", "-fPIC", "-O2", "-std=c++17",
-                       "-I", os.path.join(HERE, "..", "include"), src, "-o", obj]
-            if verbose:
+        objs = [os.path.join(tmp, os.path.basename(src) + ".o") for src in srcs]
+        cmds = [_compile_cmd(src, obj) for src, obj in zip(srcs, objs)]
+        if verbose:
+            for cmd in cmds:
                 print(" ".join(cmd), flush=True)
-            r = subprocess.run(cmd, capture_output=True, text=True)
+        jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 1) // 2), 8)
+        with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+            results = list(ex.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds))
+        for src, r in zip(srcs, results):
             if r.returncode != 0:
                 sys.stderr.write(r.stdout + r.stderr)
                 raise RuntimeError(f"compile failed: {src}")
-            objs.append(obj)
         tmp_out = OUT + ".tmp"
         cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp_out]
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -61,6 +61,25 @@ __device__ __forceinline__ XcdMap xcd_map(int wg, int nslices) {
   return XcdMap{(r / nslices) * 8 + xcd, r % nslices};
 }
 
+// Workgroup -> (group, head, slice) map for kernels over [group][head] work
+// items: all H heads (and their slices) of one group run consecutively on one
+// XCD, so the cache lines that interleave the heads of a token row (lambda
+// [.., H, L], g [.., H]) are fetched into a single L2 and shared by the heads.
+// Groups grp, grp + 8, .. go to XCD grp & 7; the grid has ceil(ngroups / 8) *
+// 8 * H * nslices workgroups and a workgroup with grp >= ngroups has no work.
+struct XcdHeadMap {
+  int grp, h, slice;
+};
+__device__ __forceinline__ XcdHeadMap xcd_head_map(int wg, int H, int nslices) {
+  const int xcd = wg & 7;
+  const int r = wg >> 3;
+  const int u = r / nslices;
+  return XcdHeadMap{(u / H) * 8 + xcd, u % H, r % nslices};
+}
+__host__ __device__ inline int xcd_head_grid(int ngroups, int H, int nslices) {
+  return (ngroups + 7) / 8 * 8 * H * nslices;
+}
+
 }  // namespace hattn
 
 namespace hattn {

@@ -873,8 +873,9 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   hipError_t e;
   if (NSEG > 1) {
     auto sk = mamba2_seg_sum_kernel<__bf16, TV, true, 1>;
-    hipLaunchKernelGGL(sk, dim3(rows * NSEG), dim3(256), 0, stream, (const __bf16*)k,
-                       (const TV*)v, gc, w.sums, w.segd, T, H, H, V, NT, 1 << slog, NSEG, 1);
+    hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
+                       (const __bf16*)k, (const TV*)v, gc, w.sums, w.segd, B, T, H, H, V, NT,
+                       1 << slog, NSEG, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ntop > 0) {

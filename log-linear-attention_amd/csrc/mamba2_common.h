@@ -124,14 +124,15 @@ struct SumSmem {
 template <typename TK, typename TV, bool GCUM, int NP>
 __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
     const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
-    float* __restrict__ sums, float* __restrict__ segd, int T, int G, int H, int V, int NT,
-    int S, int NSEG, int nvb64) {
+    float* __restrict__ sums, float* __restrict__ segd, int B, int T, int G, int H, int V,
+    int NT, int S, int NSEG, int nvb64) {
   __shared__ __attribute__((aligned(16))) SumSmem<NP> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const int vblk = blockIdx.x % nvb64;
-  const int rest = blockIdx.x / nvb64;
-  const int h = rest % H, p = (rest / H) % NSEG, b = rest / (H * NSEG);
+  // grid: xcd_head_grid(B * NSEG, H, nvb64); the heads of one (batch, segment) share an XCD
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
+  if (xm.grp >= B * NSEG) return;
+  const int vblk = xm.slice, h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h, gq = h / (H / G);
   const int c0 = p * S;
   const int nch = min(S, NT - c0);

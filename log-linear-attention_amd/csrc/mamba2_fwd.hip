@@ -174,10 +174,11 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
   Stage<NP, MAXLOC>& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const XcdMap xm = xcd_map(blockIdx.x, nvb64);
-  if (xm.row >= B * H * NSEG) return;
-  // heads fastest: the workgroups reading the same rows of q / k / v run together
-  const int h = xm.row % H, p = (xm.row / H) % NSEG, b = xm.row / (H * NSEG);
+  // grid: xcd_head_grid(B * NSEG, H, nvb64): the heads (and V slices) of one
+  // (batch, segment) run together on one XCD and share its L2
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
+  if (xm.grp >= B * NSEG) return;
+  const int h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h, vblk = xm.slice;
   const int gq = h / (H / G);
   const int NT = T / kBT;
@@ -556,18 +557,31 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
 //     every chunk: h_e = st_e * 2^dl_e, rescaled only when it is written.
 // LDS holds the chunk stage (single-buffered; the next chunk waits in
 // registers), the A tile, lambda and decay vectors and the top-level states.
+//
+// The four 64 x 64 bf16 tiles have unpadded 128-byte rows whose 16-byte units
+// are permuted per row: element (r, c) sits in unit (c >> 3) ^ f(r), with one
+// XOR map f per tile chosen for that tile's accesses (gfx950 LDS: 64 banks for
+// reads, serving 16-byte reads 16 lanes (two 8-lane row groups) at a time and
+// 8-byte transposing reads 32 lanes at a time; 32 banks for writes):
+//   Q, K  f = bits 1, 2 of r, and bit 3 onto unit bit 2: row-fragment reads
+//         (16 rows x 2 units per 16 lanes) and the transposing K^T reads (rows
+//         r0 + 8lq + (ln >> 2)) each take the minimum number of LDS cycles;
+//   V     f = bit 1 of r, and bit 3 onto unit bit 2: conflict-free transposing reads;
+//   A     f = bits 1, 2 of r, and bit 3 onto unit bit 0: conflict-free
+//         row-fragment reads; the 8-byte writes of the MFMA D layout two-way.
+// Staging writes (one row of 8 units per 8 lanes) are conflict-free for all.
 struct Bf16Smem {
-  __bf16 q[kBT * kLd];        // Q[t][k]
-  __bf16 k[kBT * kLd];        // K[s][k]
-  __bf16 v[kBT * kLd];        // V[s][v] (this workgroup's 64 columns)
-  __bf16 a[kBT * kLd];        // A[t][s] = (S o M)[t][s]
+  __bf16 q[kBT * 64];         // Q[t][k]
+  __bf16 k[kBT * 64];         // K[s][k]
+  __bf16 v[kBT * 64];         // V[s][v] (this workgroup's 64 columns)
+  __bf16 a[kBT * 64];         // A[t][s] = (S o M)[t][s]
   float gc[kBT];              // log2(e) * chunk-local inclusive cumsum of g
   float wt[kBT];              // exp(Gc_last - Gc_s)
-  float li[7 * kBT];          // lambda[t][lev] at [lev][t], intra levels 0..6
-  // lambda[t][7 + e] at [e][ln][nt] and exp(Gc_t) at [ln][nt], double-buffered:
-  // chunk j + 1's are staged while phase 2 of chunk j reads chunk j's
-  float lp[2][(kMaxLoc + kMaxTop) * kBT];
+  // lambda[t = 16nt + ln][lev] at [lev][4ln + nt] and exp(Gc_t) at [4ln + nt],
+  // double-buffered: chunk j + 1's are staged while chunk j's are read
+  float lam[2][kMaxLU * kBT];
   float eg[2][kBT];
+  float junk[kBT];            // per-lane sink of the lambda columns past the row's levels
   __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
 };
 
@@ -584,15 +598,85 @@ __device__ __forceinline__ int top_idx(int v, int k) {
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+__device__ __forceinline__ int swz_qk(int r) { return (r & 6) ^ ((r >> 1) & 4); }
+__device__ __forceinline__ int swz_v(int r) { return (r & 2) ^ ((r >> 1) & 4); }
+__device__ __forceinline__ int swz_a(int r) { return (r & 6) ^ ((r >> 3) & 1); }
+// element offset of (r, c) in a swizzled tile
+template <int (*F)(int)>
+__device__ __forceinline__ int sidx(int r, int c) {
+  return r * 64 + ((((c >> 3) ^ F(r)) & 7) << 3) + (c & 7);
+}
+
+// Stage a 64 x 64 tile held in registers (Tile64 layout) into a swizzled
+// bf16 tile: bf16 data as 16-byte units, fp32 data converted to 8-byte halves.
+template <int (*F)(int), typename T>
+__device__ __forceinline__ void store_tile_swz(const Tile64<T>& t, __bf16* dst) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int rr = 0; rr < Tile64<T>::N; ++rr) {
+    if constexpr (sizeof(T) == 2) {
+      const int r = (tid >> 3) + 32 * rr;
+      *(uint4*)(dst + sidx<F>(r, 8 * (tid & 7))) = t.r[rr];
+    } else {
+      const int r = (tid >> 4) + 16 * rr;
+      const float* e = (const float*)&t.r[rr];
+      *(bf16x4*)(dst + sidx<F>(r, 4 * (tid & 15))) =
+          bf16x4{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3]};
+    }
+  }
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // K^T fragment with the contraction over s: lane (lq, ln) receives
 // K[s = r0 + 8lq + j][k = 32c + 8(ln >> 2) + 4h + (ln & 3)], j = 0..7, so the D
 // rows 4lq + i of the product are k = 32c + 8lq + 4h + i.
-__device__ __forceinline__ bf16x8 ktr_frag(const __bf16* X, int r0, int c, int h, int lq, int ln) {
-  const __bf16* p = X + (r0 + 8 * lq + (ln >> 2)) * kLd + 32 * c + 8 * (ln & 3) + 4 * h;
-  const bf16x4 lo = ds_read_tr(p);
-  const bf16x4 hi = ds_read_tr(p + 4 * kLd);
+// Per-lane element offsets of one chunk's swizzled LDS accesses.  The XOR term
+// of every pattern depends on the lane only (tile and row-block steps change
+// row bits that no swizzle map reads), so each pattern needs one or two
+// per-lane bases and its steps become immediate offsets.
+struct LdsBase {
+  int rq0, rq1;   // Q / K rows 16m + ln, columns 8lq (+0 / +32); +1024 per 16-row tile
+  int ra0, ra1;   // A rows 16m + ln, columns 8lq (+0 / +32)
+  int aw, awu;    // A writes: row ln, half lq & 1; unit (2jt + (lq >> 1)) ^ f = awu ^ 2jt
+  int kt0, kt1;   // K^T reads (rows 8lq + (ln >> 2)): k-half 0 / 1; rows + 4 swap the bases
+  int vt;         // V reads (rows 8lq + (ln >> 2)), this wave's 16 columns
+};
+
+__device__ __forceinline__ LdsBase lds_base(int lq, int ln, int w) {
+  LdsBase b;
+  const int uq = lq ^ swz_qk(ln);
+  b.rq0 = ln * 64 + (uq << 3);
+  b.rq1 = ln * 64 + ((uq ^ 4) << 3);
+  const int fa = swz_a(ln);
+  const int ua = lq ^ fa;
+  b.ra0 = ln * 64 + (ua << 3);
+  b.ra1 = ln * 64 + ((ua ^ 4) << 3);
+  b.awu = (lq >> 1) ^ fa;
+  b.aw = ln * 64 + 4 * (lq & 1);
+  const int rk = 8 * lq + (ln >> 2);
+  const int uk = (ln & 3) ^ swz_qk(rk);
+  b.kt0 = rk * 64 + (uk << 3);
+  b.kt1 = rk * 64 + ((uk ^ 4) << 3);
+  b.vt = rk * 64 + (((((ln & 3) >> 1) ^ swz_v(rk)) ^ (2 * w)) << 3) + 4 * (ln & 1);
+  return b;
+}
+
+// K^T fragment: lane (lq, ln) receives K[s = r0 + 8lq + j][k = 32c + 8(ln >> 2) + 4h + (ln & 3)]
+// (row r + 4 flips unit bit 2 under swz_qk, which swaps the two k-half bases).
+__device__ __forceinline__ bf16x8 ktr_frag(const __bf16* X, const LdsBase& b, int r0, int c, int h) {
+  const int lo_off = (c ? b.kt1 : b.kt0) + r0 * 64 + 4 * h;
+  const int hi_off = (c ? b.kt0 : b.kt1) + (r0 + 4) * 64 + 4 * h;
+  const bf16x4 lo = ds_read_tr(X + lo_off);
+  const bf16x4 hi = ds_read_tr(X + hi_off);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// V fragment with the contraction over s: lane (lq, ln) receives
+// V[s = r0 + 8lq + j][v = 16w + ln], j = 0..7.
+__device__ __forceinline__ bf16x8 vtr_frag(const __bf16* X, const LdsBase& b, int r0) {
+  const bf16x4 lo = ds_read_tr(X + b.vt + r0 * 64);
+  const bf16x4 hi = ds_read_tr(X + b.vt + (r0 + 4) * 64);
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -613,7 +697,8 @@ template <> struct P1T<3> { static constexpr int mt[3] = {2, 3, 2}, jt[3] = {1, 
 //                    o lambda[t, level(t, s)] (causal) -> bf16 A[t][s] in LDS.
 //   kv[2c + h]: D rows k = 32c + 8lq + 4h + i, column v = 16w + ln.
 template <int W>
-__device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const bf16x8 (&qa)[4][2], const bf16x8& vt0,
+__device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const float* li,
+                                        const bf16x8 (&qa)[4][2], const bf16x8& vt0,
                                         const bf16x8& vt1, floatx4 (&kv)[4], int lq, int ln) {
   using S = P1T<W>;
   // ---- LDS reads ----
@@ -627,22 +712,22 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const bf16x8 (&qa)[4][2], 
     if (jt > mt) continue;
     const int t = 16 * mt + ln;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) kf[n][c] = *(const bf16x8*)(sm.k + (16 * jt + ln) * kLd + 32 * c + 8 * lq);
+    for (int c = 0; c < 2; ++c) kf[n][c] = *(const bf16x8*)(sm.k + (c ? lb.rq1 : lb.rq0) + 1024 * jt);
     gt[n] = sm.gc[t];
     gs[n] = *(const floatx4*)(sm.gc + 16 * jt + 4 * lq);
     if (jt < mt) {
       const int lev = 4 + (32 - __builtin_clz(mt ^ jt));
-      lam[n][0] = sm.li[lev * kBT + t];
+      lam[n][0] = li[lev * kBT + 4 * ln + mt];
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lam[n][i] = sm.li[intra_level(ln, 4 * lq + i) * kBT + t];
+      for (int i = 0; i < 4; ++i) lam[n][i] = li[intra_level(ln, 4 * lq + i) * kBT + 4 * ln + mt];
     }
   }
   bf16x8 kt[2][2];   // [h][s-half], first for k-half c = 0
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    kt[hh][0] = ktr_frag(sm.k, 0, 0, hh, lq, ln);
-    kt[hh][1] = ktr_frag(sm.k, 32, 0, hh, lq, ln);
+    kt[hh][0] = ktr_frag(sm.k, lb, 0, 0, hh);
+    kt[hh][1] = ktr_frag(sm.k, lb, 32, 0, hh);
   }
   const floatx4 w0a = *(const floatx4*)(sm.wt + 8 * lq);
   const floatx4 w0b = *(const floatx4*)(sm.wt + 8 * lq + 4);
@@ -674,8 +759,8 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const bf16x8 (&qa)[4][2], 
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    kt[hh][0] = ktr_frag(sm.k, 0, 1, hh, lq, ln);
-    kt[hh][1] = ktr_frag(sm.k, 32, 1, hh, lq, ln);
+    kt[hh][0] = ktr_frag(sm.k, lb, 0, 1, hh);
+    kt[hh][1] = ktr_frag(sm.k, lb, 32, 1, hh);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -704,7 +789,7 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const bf16x8 (&qa)[4][2], 
       }
       out = bf16x4{(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
     }
-    *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+    *(bf16x4*)(sm.a + lb.aw + 1024 * mt + ((lb.awu ^ (2 * jt)) << 3)) = out;
   }
 }
 
@@ -721,9 +806,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   Bf16Smem& sm = *(Bf16Smem*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq0 = lane >> 4, ln0 = lane & 15;
-  const XcdMap xm = xcd_map(blockIdx.x, nvb64);
-  if (xm.row >= B * H * NSEG) return;
-  const int h = xm.row % H, p = (xm.row / H) % NSEG, b = xm.row / (H * NSEG);
+  // grid: xcd_head_grid(B * NSEG, H, nvb64)
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
+  if (xm.grp >= B * NSEG) return;
+  const int h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h, vblk = xm.slice;
   const int gq = h / (H / G);
   const int NT = T / kBT;
@@ -845,12 +931,14 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const unsigned int lrow_b = lbmis + (unsigned int)((lane * H + h) * L) * sizeof(TL);
   const int lmis = kL16 ? (int)((lrow_b >> 1) & 1) : 0;
   const unsigned int vo_l = lrow_b & ~3u;
-  const int npc = (lu + lmis + kPE - 1) / kPE;   // pieces per row (<= 5)
 
   MainRegs<__bf16, TV, TL, 1> rg;
   constexpr int kLP = kL16 ? 1 : 2;   // pieces per wave (bf16 rows: lu <= 19 needs <= 3 pieces)
   const int lpw0 = w > 0 ? w - 1 : 0;   // first lambda piece of this wave
   uint4 lamr[kLP];
+  constexpr int kLamBuf = kMaxLU * kBT;           // floats between the two lambda buffers
+  const int lslot = 4 * (lane & 15) + (lane >> 4);   // this lane's token row t, permuted
+  const int junk_rel = (int)(sm.junk - sm.lam[0]) + lane - lslot;
   // part < 0: everything; parts 0, 1, 2: q / k / v, g and lambda (the loads of
   // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
   auto load = [&](int j, int part) {
@@ -874,9 +962,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
   };
   auto store = [&](int j) {
-    store_tile64<1>(rg.q, sm.q, sm.q);
-    store_tile64<1>(rg.k, sm.k, sm.k);
-    store_tile64<1>(rg.v, sm.v, sm.v);
+    store_tile_swz<swz_qk>(rg.q, sm.q);
+    store_tile_swz<swz_qk>(rg.k, sm.k);
+    store_tile_swz<swz_v>(rg.v, sm.v);
     if (w == 0) {
       const float x = chunk_cumsum(rg.g);   // lane t holds Gc_t
       const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
@@ -885,23 +973,22 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       sm.eg[j & 1][4 * ln0 + lq0] = fexp(x);
       if (write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
     } else {
-      float* lpw = sm.lp[j & 1];
+      // value i of piece pc is column kPE * pc + i - lmis; columns outside
+      // [0, lu) go to the lane's junk slot, so every lane stores unconditionally
+      // through one LDS base (no divergent branches, no generic pointers)
+      float* lamw = sm.lam[j & 1] + lslot;
 #pragma unroll
       for (int r = 0; r < kLP; ++r) {
-        const int pc = w - 1 + 3 * r;
-        if (pc < npc) {
-          const unsigned int* u = (const unsigned int*)&lamr[r];
+        const int col0 = kPE * (w - 1 + 3 * r) - lmis;
+        const unsigned int* u = (const unsigned int*)&lamr[r];
 #pragma unroll
-          for (int i = 0; i < kPE; ++i) {
-            const int col = kPE * pc + i - lmis;
-            float val;
-            if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
-            else val = __builtin_bit_cast(float, u[i]);
-            if (col >= 0 && col < lu) {
-              if (col < 7) sm.li[col * kBT + lane] = val;
-              else lpw[(col - 7) * kBT + 4 * (lane & 15) + (lane >> 4)] = val;
-            }
-          }
+        for (int i = 0; i < kPE; ++i) {
+          float val;
+          if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
+          else val = __builtin_bit_cast(float, u[i]);
+          const int col = col0 + i;
+          const int idx = (unsigned int)col < (unsigned int)lu ? col * kBT : junk_rel - (int)(j & 1) * kLamBuf;
+          lamw[idx] = val;
         }
       }
     }
@@ -921,7 +1008,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   __syncthreads();   // the A tile may have served as scratch for the final states
   {
     const int r = tid >> 3, c = 4 * (tid & 3), tile = (tid >> 2) & 1;
-    *(bf16x4*)(sm.a + (32 * tile + (r & 15)) * kLd + 16 + 32 * tile + c) = bf16x4{};
+    *(bf16x4*)(sm.a + sidx<swz_a>(32 * tile + (r & 15), 16 + 32 * tile + c)) = bf16x4{};
   }
   // Pipeline: chunk j + 1 is staged in LDS right after phase 1 of chunk j (from
   // then on chunk j's stage is dead except lambda', which is double-buffered),
@@ -941,6 +1028,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     int lq, ln;
     asm volatile("v_mov_b32 %0, %1" : "=v"(lq) : "v"(lq0));
     asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(ln0));
+    const LdsBase lb = lds_base(lq, ln, w);
 
     // Q fragments Q[t = 16mt + ln][k = 32c + 8lq + j]; V fragments
     // V[s = 32c + 8lq + j][v = 16w + ln] (A operand of o^T = V^T A^T, and with
@@ -949,24 +1037,24 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) qa[mt][c] = *(const bf16x8*)(sm.q + (16 * mt + ln) * kLd + 32 * c + 8 * lq);
-    const bf16x8 vt0 = tr_frag(sm.v, kLd, 0, 16 * w);
-    const bf16x8 vt1 = tr_frag(sm.v, kLd, 32, 16 * w);
+      for (int c = 0; c < 2; ++c) qa[mt][c] = *(const bf16x8*)(sm.q + (c ? lb.rq1 : lb.rq0) + 1024 * mt);
+    const bf16x8 vt0 = vtr_frag(sm.v, lb, 0);
+    const bf16x8 vt1 = vtr_frag(sm.v, lb, 32);
 
     // ---- phase 1: A = S o M, and the chunk's K^T diag(w) V -------------------------
     floatx4 kv[4];
     switch (w) {
-      case 0: bf16_p1<0>(sm, qa, vt0, vt1, kv, lq, ln); break;
-      case 1: bf16_p1<1>(sm, qa, vt0, vt1, kv, lq, ln); break;
-      case 2: bf16_p1<2>(sm, qa, vt0, vt1, kv, lq, ln); break;
-      default: bf16_p1<3>(sm, qa, vt0, vt1, kv, lq, ln); break;
+      case 0: bf16_p1<0>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
+      case 1: bf16_p1<1>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
+      case 2: bf16_p1<2>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
+      default: bf16_p1<3>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
     }
     const float glr = sm.gc[kBT - 1];   // chunk log2-decay
     __syncthreads();   // A visible; chunk j's stage (but lambda') no longer read
     if (j + 1 < nch) store(j + 1);
     const bool more = j + 2 < nch;
     if (more) load(j + 2, 0);
-    const float* lpr = sm.lp[j & 1];
+    const float* lpr = sm.lam[j & 1] + 7 * kBT;
     const floatx4 egr = *(const floatx4*)(sm.eg[j & 1] + 4 * ln);   // exp(Gc_t), t = 16nt + ln
 
     // ---- phase 2: o^T[v = 16w + 4lq + i][t = 16nt + ln] ------------------------------
@@ -974,9 +1062,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     {
       bf16x8 af[6];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) af[nt] = *(const bf16x8*)(sm.a + (16 * nt + ln) * kLd + 8 * lq);
-      af[4] = *(const bf16x8*)(sm.a + (32 + ln) * kLd + 32 + 8 * lq);
-      af[5] = *(const bf16x8*)(sm.a + (48 + ln) * kLd + 32 + 8 * lq);
+      for (int nt = 0; nt < 4; ++nt) af[nt] = *(const bf16x8*)(sm.a + lb.ra0 + 1024 * nt);
+      af[4] = *(const bf16x8*)(sm.a + lb.ra1 + 1024 * 2);
+      af[5] = *(const bf16x8*)(sm.a + lb.ra1 + 1024 * 3);
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16x16x32(vt0, af[nt], zero4());
       acc[2] = mfma16x16x32(vt1, af[4], acc[2]);
@@ -1169,8 +1257,9 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
   const int ntop = nlev - min(slog, nlev);
   if (NSEG > 1) {
     auto sk = mamba2_seg_sum_kernel<TK, TV, false, NP>;
-    hipLaunchKernelGGL(sk, dim3(rows * NSEG * nvb64), dim3(256), 0, stream, (const TK*)k,
-                       (const TV*)v, g, w.sums, w.segd, T, G, H, V, NT, S, NSEG, nvb64);
+    hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), 0, stream,
+                       (const TK*)k, (const TV*)v, g, w.sums, w.segd, B, T, G, H, V, NT, S, NSEG,
+                       nvb64);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ntop > 0 && NP == 2) {
@@ -1180,8 +1269,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
-  const int rows8 = (rows * NSEG + 7) / 8;
-  const int grid = rows8 * 8 * nvb64;
+  const int grid = xcd_head_grid(B * NSEG, H, nvb64);
   if constexpr (NP == 1) {
     const int smem = bf16_smem_bytes(ntop);
     auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO>;

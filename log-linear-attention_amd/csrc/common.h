@@ -168,6 +168,12 @@ template <> __device__ __forceinline__ void buf_store<__bf16>(__bf16 x, rsrc_t r
 
 namespace hattn {
 
+__device__ __forceinline__ uint2 buf_load8(rsrc_t r, unsigned int voff, unsigned int soff) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return uint2{x[0], x[1]};
+}
+
 __device__ __forceinline__ void buf_store8(uint2 x, rsrc_t r, unsigned int voff, unsigned int soff) {
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
   __builtin_amdgcn_raw_buffer_store_b64(u32x2{x.x, x.y}, r, voff, soff, 0);

@@ -321,65 +321,58 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
 // ---------------------------------------------------------------------------
 // dq and dlambda: forward walk over one segment
 // ---------------------------------------------------------------------------
+// LDS of the dq kernel (about 73 KB, so two workgroups share a CU); the
+// top-level states stay in HBM / L2 (see htop below).
 struct DqSmem {
   BwdStage st;
   __bf16 a[kBT * kLd];                      // (M o dP)[t][s], bf16
   float dl_off[kBT][4][4];                  // off-diagonal tile partials [t][jt][lq]
   float dl_diag[kBT][5][4];                 // diagonal tile partials [t][level][lq]
   float dl_int[kBT][kMaxLoc + kMaxTop][4];  // inter-level partials [t][e][wave]
-  __bf16 top[1];                            // [ntop][k][v] top-level states (dynamic)
 };
 
-inline int dq_smem_bytes(int ntop) { return (int)offsetof(DqSmem, top) + ntop * kKD * kLd * 2; }
-
+// htop: the top-level states Htop_e2(p) of every (row, segment) in bf16 [k][v]
+// tiles, written by mamba2_htop_kernel<1> from the segment summaries (layout
+// [row][p][e2][64][64]).  Every chunk of a segment reads the same tiles, so
+// after the first chunk their MFMA fragments come from L2; the fragments of
+// the segment's first top level are loaded once, before the walk, the others
+// one level ahead of their use.
 template <typename TV, typename TL>
-__global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
+__global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
-    const float* __restrict__ sums, const float* __restrict__ segd, __bf16* __restrict__ dq,
-    float* __restrict__ dl, float* __restrict__ dgq, int B, int T, int H, int V, int L, int nlev,
-    int slog, int NSEG) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-  DqSmem& sm = *(DqSmem*)smem_raw;
+    const __bf16* __restrict__ htop, __bf16* __restrict__ dq, float* __restrict__ dl,
+    float* __restrict__ dgq, int B, int T, int H, int V, int L, int nlev, int slog, int NSEG) {
+  __shared__ __attribute__((aligned(16))) DqSmem sm;
   BwdStage& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lq = lane >> 4, ln = lane & 15;
-  const int I = blockIdx.x;
-  const int h = I % H, p = (I / H) % NSEG, b = I / (H * NSEG);
+  const int lq0 = lane >> 4, ln0 = lane & 15;
+  // grid: xcd_head_grid(B * NSEG, H, 1): the heads of one (batch, segment) share an XCD
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, 1);
+  if (xm.grp >= B * NSEG) return;
+  const int h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h;
   const int NT = T / kBT;
   const int c0 = p << slog, cend = min(c0 + (1 << slog), NT);
   const int lu = 7 + nlev;
   const int nloc = min(slog, nlev), ntop = nlev - nloc;
+  const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
 
-  // ---- top-level states Htop_e(p) -> LDS, bf16 [k][v] ----------------------------
-  if (ntop > 0) {
-    const float* sp = sums + (size_t)row * NSEG * kKD * kKD;
-    const float* dp = segd + (size_t)row * NSEG;
-    const int kk = tid >> 2, v0 = 16 * (tid & 3);
-    for (int e2 = 0; e2 < ntop; ++e2) {
-      if (!((p >> e2) & 1)) continue;
-      const int lo = (p >> (e2 + 1)) << (e2 + 1), hi = lo + (1 << e2);
-      float dlog = 0.f;
-      for (int r = hi; r < p; ++r) dlog += dp[r];
-      float hacc[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) hacc[i] = 0.f;
-      for (int qs = hi - 1; qs >= lo; --qs) {
-        const float sc = fexp(dlog);
-        const float* src = sp + ((size_t)qs * kKD + kk) * kKD + v0;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-          const floatx4 x = *(const floatx4*)(src + i);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) hacc[i + u] += sc * x[u];
-        }
-        dlog += dp[qs];
-      }
-      __bf16* tp = sm.top + e2 * kKD * kLd + kk * kLd + v0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) tp[i] = (__bf16)hacc[i];
-    }
+  // A operand of a top level: h[k = 16w + ln][v = c0 + 4lq + i, c0 + 16 + 4lq + i]
+  const rsrc_t rt = make_rsrc(ntop > 0 ? (const void*)(htop + ((size_t)row * NSEG + p) * ntop * kKD * kKD)
+                                       : (const void*)htop,
+                              ntop > 0 ? (size_t)ntop * kKD * kKD * 2 : 0);
+  const unsigned int vo_t = ((16 * w + ln0) * kKD + 4 * lq0) * 2;
+  auto top_frag = [&](int e2, int cc) {
+    const unsigned int so = (unsigned int)(e2 * kKD * kKD + cc) * 2;
+    const uint2 lo = buf_load8(rt, vo_t, so), hi = buf_load8(rt, vo_t, so + 32);
+    return __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+  };
+  bf16x8 tf0{}, tf1{};   // the segment's first top level (loaded once)
+  if (topmask) {
+    const int e0 = __builtin_ctz(topmask);
+    tf0 = top_frag(e0, 0);
+    tf1 = top_frag(e0, 32);
   }
 
   BwdLoader<256, TV, TL> ld;
@@ -388,7 +381,7 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
   const rsrc_t rdq = make_rsrc(dq + rq0 * kKD, (size_t)T * H * kKD * 2);
   const rsrc_t rdl = make_rsrc(dl + rq0 * L, (size_t)T * H * L * 4);
   const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
-  const unsigned int vo_dq = (ln * H * kKD + 16 * w + 4 * lq) * 2;
+  const unsigned int vo_dq = (ln0 * H * kKD + 16 * w + 4 * lq0) * 2;
 
   // forward states h_e^T [v][k]: lane holds v = 16m + 4lq + i, k = 16w + ln
   floatx4 hT[kMaxLoc][4];
@@ -404,6 +397,11 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
     ld.store(rg, s);
     if (ic + 1 < cend) ld.load(rg, ic + 1);
     __syncthreads();
+    // lane indices made opaque per chunk, so the LDS addresses of the phases are
+    // recomputed (a few VALU ops) instead of held in VGPRs across the walk
+    int lq, ln;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lq) : "v"(lq0));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(ln0));
 
     // ---- phase 1: (M o dP) tiles and the intra-chunk dlambda partials ----------
 #pragma unroll
@@ -493,17 +491,29 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_dq_kernel(
           }
         }
       }
-      const float ee = fexp(Eseg);
-      for (int e2 = 0; e2 < ntop; ++e2) {
-        if ((p >> e2) & 1) {
-          const __bf16* tp = sm.top + e2 * kKD * kLd;
-          level(row_pair(tp, 16 * w + ln, 0), row_pair(tp, 16 * w + ln, 32), nloc + e2,
-                7 + nloc + e2, ee);
-        } else if (lq == 0) {
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][nloc + e2][w] = 0.f;
+      if (topmask) {
+        const float ee = fexp(Eseg);
+        int m = topmask, e2 = __builtin_ctz(topmask);
+        bf16x8 a0 = tf0, a1 = tf1;
+        while (true) {
+          m &= m - 1;
+          bf16x8 n0 = a0, n1 = a1;
+          if (m) {   // the next read level's fragments, in flight during this level
+            n0 = top_frag(__builtin_ctz(m), 0);
+            n1 = top_frag(__builtin_ctz(m), 32);
+          }
+          level(a0, a1, nloc + e2, 7 + nloc + e2, ee);
+          if (!m) break;
+          e2 = __builtin_ctz(m);
+          a0 = n0;
+          a1 = n1;
         }
       }
+      if (lq == 0)
+        for (int e2 = 0; e2 < ntop; ++e2)
+          if (!((p >> e2) & 1))
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][nloc + e2][w] = 0.f;
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -836,6 +846,7 @@ __global__ __launch_bounds__(256) void mamba2_bwd_dg_kernel(float* __restrict__ 
 // ---------------------------------------------------------------------------
 struct BwdWs {
   float *segd, *sums, *rsum, *dgq, *segtot;
+  __bf16* htop;
   size_t bytes;
 };
 
@@ -855,6 +866,7 @@ inline BwdWs bwd_ws_layout(void* base, int B, int T, int H, int V, int nlev) {
   w.dgq = (float*)(p + off);    off += align256((size_t)B * T * H * 4);
   w.sums = (float*)(p + off);   off += align256(NSEG > 1 ? rows * NSEG * kKD * V * 4 : 0);
   w.rsum = (float*)(p + off);   off += align256(rows * NSEG * ntop * kKD * kKD * 4);
+  w.htop = (__bf16*)(p + off);  off += align256(rows * NSEG * ntop * kKD * kKD * 2);
   w.bytes = off;
   return w;
 }
@@ -879,6 +891,10 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ntop > 0) {
+    // top-level states of every segment for the dq kernel
+    hipLaunchKernelGGL(mamba2_htop_kernel<1>, dim3(rows * 4), dim3(256), 0, stream, w.sums,
+                       w.segd, w.htop, V, NSEG, ntop, 1);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ngrp = (ntop + 3) / 4;
     auto rk = mamba2_bwd_rsum_kernel<TL>;
     hipLaunchKernelGGL(rk, dim3(rows * NSEG * ngrp), dim3(256), 0, stream, (const __bf16*)q,
@@ -888,13 +904,10 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   }
   {
     auto kq = mamba2_bwd_dq_kernel<TV, TL>;
-    const int smem = dq_smem_bytes(ntop);
-    if ((e = hipFuncSetAttribute((const void*)kq, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 smem)) != hipSuccess)
-      return e;
-    hipLaunchKernelGGL(kq, dim3(rows * NSEG), dim3(256), smem, stream, (const __bf16*)q,
-                       (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc, (const TL*)l,
-                       w.sums, w.segd, (__bf16*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog, NSEG);
+    hipLaunchKernelGGL(kq, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
+                       (const __bf16*)q, (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc,
+                       (const TL*)l, w.htop, (__bf16*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog,
+                       NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {

@@ -236,4 +236,77 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   if (tid == 0 && vblk == 0) segd[(size_t)row * NSEG + p] = dsum;
 }
 
+// ---------------------------------------------------------------------------
+// Top-level states every segment reads (from the segment summaries)
+// ---------------------------------------------------------------------------
+// A scan over the segments of one row: per top level e2 (inter-chunk level
+// s + e2, blocks of 2^(e2 + 1) segments) the state
+//   h <- (p ends its aligned block ? 0 : exp(D_p) h) + (bit e2 of p clear ? Sum(p) : 0)
+// is read (before the update) by the segments with bit e2 set, which is
+// Htop_e2(p).  One workgroup per (row, 64-column block of V, quarter of the
+// 64 x 64 tile); each thread owns 4 consecutive elements and streams the
+// row's summaries.  Output: NP bf16 planes [row][p][e2][vblk][plane][64][64],
+// written only where segment p reads level e2.
+template <int NP>
+__global__ __launch_bounds__(256) void mamba2_htop_kernel(const float* __restrict__ sums,
+                                                          const float* __restrict__ segd,
+                                                          __bf16* __restrict__ htop, int V,
+                                                          int NSEG, int ntop, int nvb64) {
+  const int quarter = blockIdx.x & 3;
+  const int vblk = (blockIdx.x >> 2) % nvb64;
+  const int row = (blockIdx.x >> 2) / nvb64;
+  const int el = quarter * 1024 + 4 * threadIdx.x;
+  const int kk = el >> 6, c = el & 63;
+  const float* src = sums + ((size_t)row * NSEG * kKD + kk) * V + vblk * 64 + c;
+  const size_t sstride = (size_t)kKD * V;
+  __bf16* dst = htop + (size_t)row * NSEG * ntop * nvb64 * NP * (kKD * 64) + (size_t)vblk * NP * (kKD * 64) + el;
+  const size_t pstride = (size_t)ntop * nvb64 * NP * (kKD * 64), estride = (size_t)nvb64 * NP * (kKD * 64);
+  const float* dp = segd + (size_t)row * NSEG;
+  floatx4 h[kMaxTop];
+#pragma unroll
+  for (int e2 = 0; e2 < kMaxTop; ++e2) h[e2] = zero4();
+  constexpr int kBatch = 8;   // summaries loaded per round, all in flight together
+  for (int p0 = 0; p0 < NSEG; p0 += kBatch) {
+    floatx4 xs[kBatch];
+    float ds[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int pj = p0 + j < NSEG ? p0 + j : NSEG - 1;
+      xs[j] = *(const floatx4*)(src + (size_t)pj * sstride);
+      ds[j] = dp[pj];
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+    const int p = p0 + j;
+    if (p >= NSEG) break;
+    const floatx4 x = xs[j];
+    const float dec = fexp(ds[j]);
+#pragma unroll
+    for (int e2 = 0; e2 < kMaxTop; ++e2) {
+      if (e2 < ntop) {
+        const bool rd = (p >> e2) & 1;
+        if (rd) {
+          bf16x4 hi, lo;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            hi[jj] = (__bf16)h[e2][jj];
+            lo[jj] = bf16_lo(h[e2][jj], hi[jj]);
+          }
+          __bf16* o = dst + (size_t)p * pstride + (size_t)e2 * estride;
+          *(bf16x4*)o = hi;
+          if constexpr (NP == 2) *(bf16x4*)(o + kKD * 64) = lo;
+        }
+        const int per = 2 << e2;
+        if ((p & (per - 1)) == per - 1) {
+          h[e2] = zero4();
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) h[e2][jj] = h[e2][jj] * dec + (rd ? 0.f : x[jj]);
+        }
+      }
+    }
+    }
+  }
+}
+
 }  // namespace hattn

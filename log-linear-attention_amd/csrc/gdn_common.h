@@ -39,16 +39,19 @@ __device__ __forceinline__ void g2s_tile(const __bf16* __restrict__ src, size_t 
 // with a per-wave 16 x 17 scratch t1all[w].  The upper blocks of X are set to
 // zero.  256 threads; starts and ends with the caller's data in LDS and ends
 // with a barrier.
+// NTHR threads call it together; waves 0..3 do the block work (the others only
+// take part in the zero fill and the barriers).
+template <int NTHR = 256>
 __device__ inline void tri_inv64(const float* A, float* X, float (*t1all)[16 * 17]) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  for (int u = tid; u < 6 * 256; u += 256) {   // the six upper 16 x 16 blocks
+  for (int u = tid; u < 6 * 256; u += NTHR) {   // the six upper 16 x 16 blocks
     const int blk = u >> 8, e = u & 255;
     const int bi = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
     const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
     X[(16 * bi + (e >> 4)) * kLM + 16 * bj + (e & 15)] = 0.f;
   }
-  if (lq == 0) {
+  if (w < 4 && lq == 0) {
     const int o = 16 * w;
     float x[16];
 #pragma unroll

@@ -23,7 +23,9 @@
 // that is local to the chunk: the two 64 x 64 products K K^T and Q K^T on
 // MFMA, the fp32 unit-lower-triangular inverse (16 x 16 diagonal blocks by
 // substitution, off-diagonal blocks by block substitution), W, U, q_new,
-// K_new, W_new and o_intra, plus the Aw / Au the reference returns.
+// K_new, W_new and o_intra, plus the Aw / Au the reference returns.  Its LDS
+// holds one workgroup per CU, so it runs eight waves (two per SIMD): wave w
+// owns output rows t-tile w & 3 and half w >> 2 of the column tiles.
 // Kernel 2 (gdn_scan_kernel): one workgroup per (row, 32 columns of V) walks
 // the chunks in order with every level's [K x 32] state in fp32 registers
 // (wave w owns K / 4 state rows); per chunk it stages the states in LDS
@@ -55,8 +57,10 @@ struct GdnPrepSmem {
 // GCUM: g already holds the chunk-local cumsum (the backward's input,
 // chunkwise_hgdn.py:799-817) and gcum is not written.  aw_out, au_out and oi
 // may be null (the backward recomputes only q_new, K_new, W_new and U).
+constexpr int kPrepThreads = 512;
+
 template <int KD, int VD, typename TB, typename TL, bool GCUM = false>
-__global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
+__global__ __launch_bounds__(kPrepThreads, 1) void gdn_prep_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
     float* __restrict__ gcum, __bf16* __restrict__ aw_out, __bf16* __restrict__ au_out,
@@ -66,8 +70,10 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
   constexpr int LK = Sm::LK, LV = Sm::LV, LF = Sm::LF;
+  constexpr int NTH = kPrepThreads;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
+  const int wt = w & 3, wh = w >> 2;   // output row tile, column-tile half
   const int NT = T / kGC;
   const int ic = blockIdx.x % NT;
   const int row = blockIdx.x / NT;
@@ -78,9 +84,15 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   float* X = s.f + kGC * kLM;     // [64][65]
 
   // ---- load the chunk ---------------------------------------------------------
-  g2s_tile<KD>(k + tok0 * hk + (size_t)h * KD, hk, s.k, LK);
-  g2s_tile<KD>(q + tok0 * hk + (size_t)h * KD, hk, s.q, LK);
-  g2s_tile<VD>(v + tok0 * hv + (size_t)h * VD, hv, s.v, LV);
+  // threads 0..255 stage K and V rows 0..31, threads 256..511 Q and V rows 32..63
+  if (tid < 256) {
+    g2s_tile<KD>(k + tok0 * hk + (size_t)h * KD, hk, s.k, LK);
+    g2s_tile<VD, kGC / 2>(v + tok0 * hv + (size_t)h * VD, hv, s.v, LV);
+  } else {
+    g2s_tile<KD, kGC, 256>(q + tok0 * hk + (size_t)h * KD, hk, s.q, LK);
+    g2s_tile<VD, kGC / 2, 256>(v + (tok0 + kGC / 2) * hv + (size_t)h * VD, hv,
+                               s.v + (kGC / 2) * LV, LV);
+  }
   if (w == 0) {
     float x = g[(tok0 + lane) * H + h];
     if constexpr (!GCUM) {
@@ -95,52 +107,47 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
     s.beta[lane] = to_f32<TB>(beta[(tok0 + lane) * H + h]);
   }
   {
-    float lv[2];   // both loads issued before either store
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = min(tid + 256 * i, 7 * kGC - 1);
-      lv[i] = to_f32<TL>(l[((tok0 + e / 7) * H + h) * L + e % 7]);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 256 * i;
-      if (e < 7 * kGC) s.lam[e % 7][e / 7] = lv[i];
-    }
+    static_assert(NTH >= 7 * kGC, "one lambda entry per thread");
+    const int e = min(tid, 7 * kGC - 1);
+    const float lv = to_f32<TL>(l[((tok0 + e / 7) * H + h) * L + e % 7]);
+    if (tid < 7 * kGC) s.lam[e % 7][e / 7] = lv;
   }
   __syncthreads();
 
-  // ---- K K^T (-> A, fp32) and Q K^T (-> tril, bf16): wave w owns rows t-tile w -----
+  // ---- K K^T (-> A, fp32) and Q K^T (-> tril, bf16): wave w owns rows t-tile wt,
+  // column tiles 2wh, 2wh + 1 ------------------------------------------------------
   {
-    floatx4 kk[4], qk[4];
+    floatx4 kk[2], qk[2];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) kk[nt] = qk[nt] = zero4();
+    for (int n = 0; n < 2; ++n) kk[n] = qk[n] = zero4();
 #pragma unroll
     for (int c = 0; c < KD / 32; ++c) {
-      const bf16x8 ak = *(const bf16x8*)(s.k + (16 * w + ln) * LK + 32 * c + 8 * lq);
-      const bf16x8 aq = *(const bf16x8*)(s.q + (16 * w + ln) * LK + 32 * c + 8 * lq);
+      const bf16x8 ak = *(const bf16x8*)(s.k + (16 * wt + ln) * LK + 32 * c + 8 * lq);
+      const bf16x8 aq = *(const bf16x8*)(s.q + (16 * wt + ln) * LK + 32 * c + 8 * lq);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int n = 0; n < 2; ++n) {
+        const int nt = 2 * wh + n;
         const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
-        kk[nt] = mfma16x16x32(ak, bk, kk[nt]);
-        qk[nt] = mfma16x16x32(aq, bk, qk[nt]);
+        kk[n] = mfma16x16x32(ak, bk, kk[n]);
+        qk[n] = mfma16x16x32(aq, bk, qk[n]);
       }
     }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * w + 4 * lq + i, sc = 16 * nt + ln;
-        A[t * kLM + sc] = sc < t ? s.beta[t] * kk[nt][i] : 0.f;
-        s.qk[t * kLd64 + sc] = (__bf16)(sc <= t ? qk[nt][i] : 0.f);
+        const int t = 16 * wt + 4 * lq + i, sc = 16 * (2 * wh + n) + ln;
+        A[t * kLM + sc] = sc < t ? s.beta[t] * kk[n][i] : 0.f;
+        s.qk[t * kLd64 + sc] = (__bf16)(sc <= t ? qk[n][i] : 0.f);
       }
   }
   __syncthreads();
 
   // ---- X = (I + A)^-1, fp32 ----------------------------------------------------
-  tri_inv64(A, X, s.t1);
+  tri_inv64<NTH>(A, X, s.t1);
 
   // ---- Aw, Au (bf16) to LDS and to the outputs ----------------------------------------
-  for (int u = tid; u < kGC * 8; u += 256) {
+  for (int u = tid; u < kGC * 8; u += NTH) {
     const int t = u >> 3, s0 = 8 * (u & 7);
     bf16x8 a, au;
 #pragma unroll
@@ -158,14 +165,16 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   __syncthreads();
 
   // X[t][s] (bf16 LDS) times (beta o Y)[s][n] (bf16 LDS, row-major [s][n]):
-  // wave w computes output rows t-tile w, N/16 column tiles, into the fp32 staging.
+  // wave w computes output rows t-tile wt, its half of the N/16 column tiles,
+  // into the fp32 staging.
   auto gemm_rows = [&](const __bf16* xa, const __bf16* yb, int ldb, int ntile, bool scale_beta) {
-    const bf16x8 a0 = *(const bf16x8*)(xa + (16 * w + ln) * kLd64 + 8 * lq);
-    const bf16x8 a1 = *(const bf16x8*)(xa + (16 * w + ln) * kLd64 + 32 + 8 * lq);
+    const bf16x8 a0 = *(const bf16x8*)(xa + (16 * wt + ln) * kLd64 + 8 * lq);
+    const bf16x8 a1 = *(const bf16x8*)(xa + (16 * wt + ln) * kLd64 + 32 + 8 * lq);
     const floatx4 b0a = *(const floatx4*)(s.beta + 8 * lq), b0b = *(const floatx4*)(s.beta + 8 * lq + 4);
     const floatx4 b1a = *(const floatx4*)(s.beta + 32 + 8 * lq),
                   b1b = *(const floatx4*)(s.beta + 36 + 8 * lq);
-    for (int nt = 0; nt < ntile; ++nt) {
+    const int nh = ntile / 2;
+    for (int nt = wh * nh; nt < (wh + 1) * nh; ++nt) {
       bf16x8 y0 = tr_frag(yb, ldb, 0, 16 * nt), y1 = tr_frag(yb, ldb, 32, 16 * nt);
       if (scale_beta) {
 #pragma unroll
@@ -179,14 +188,14 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
       floatx4 acc = mfma16x16x32(a0, y0, zero4());
       acc = mfma16x16x32(a1, y1, acc);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s.f[(16 * w + 4 * lq + i) * LF + 16 * nt + ln] = acc[i];
+      for (int i = 0; i < 4; ++i) s.f[(16 * wt + 4 * lq + i) * LF + 16 * nt + ln] = acc[i];
     }
   };
 
   // ---- W = Aw (beta K) -> W (bf16 LDS), W_new = exp(Gc) W (output) ---------------
   gemm_rows(s.aw, s.k, LK, KD / 16, true);
   __syncthreads();
-  for (int u = tid; u < kGC * KD / 8; u += 256) {
+  for (int u = tid; u < kGC * KD / 8; u += NTH) {
     const int t = u / (KD / 8), c0 = 8 * (u % (KD / 8));
     const float eg = fexp(s.gc[t]);
     bf16x8 wb, wnb;
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   // ---- U = Au (beta V) (output) ------------------------------------------------------
   gemm_rows(s.au, s.v, LV, VD / 16, true);
   __syncthreads();
-  for (int u = tid; u < kGC * VD / 8; u += 256) {
+  for (int u = tid; u < kGC * VD / 8; u += NTH) {
     const int t = u / (VD / 8), c0 = 8 * (u % (VD / 8));
     bf16x8 ub;
 #pragma unroll
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   // ---- q_new = exp(Gc) (Q - tril(Q K^T) W) (output) ---------------------------------
   gemm_rows(s.qk, s.w, LK, KD / 16, false);
   __syncthreads();
-  for (int u = tid; u < kGC * KD / 8; u += 256) {
+  for (int u = tid; u < kGC * KD / 8; u += NTH) {
     const int t = u / (KD / 8), c0 = 8 * (u % (KD / 8));
     const float eg = fexp(s.gc[t]);
     const bf16x8 qx = *(const bf16x8*)(s.q + t * LK + c0);
@@ -239,7 +248,7 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   // ---- P = (tril(Q K^T) Aw) o gamma o beta_s o lambda[t, lev] (bf16 LDS) -----------
   gemm_rows(s.qk, s.aw, kLd64, 4, false);
   __syncthreads();
-  for (int u = tid; u < kGC * 8; u += 256) {
+  for (int u = tid; u < kGC * 8; u += NTH) {
     const int t = u >> 3, s0 = 8 * (u & 7);
     bf16x8 pb;
 #pragma unroll
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(256, 1) void gdn_prep_kernel(
   // ---- o_intra = P V (fp32 output) ---------------------------------------------------
   gemm_rows(s.pm, s.v, LV, VD / 16, false);
   __syncthreads();
-  for (int u = tid; u < kGC * VD / 4; u += 256) {
+  for (int u = tid; u < kGC * VD / 4; u += NTH) {
     const int t = u / (VD / 4), c0 = 4 * (u % (VD / 4));
     *(floatx4*)(oi + (tok0 + t) * hv + (size_t)h * VD + c0) = *(const floatx4*)(s.f + t * LF + c0);
   }
@@ -548,7 +557,7 @@ static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, cons
     if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  smem)) != hipSuccess)
       return e;
-    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,
+    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(kPrepThreads), smem, stream, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const TB*)beta, g, (const TL*)l, gcum,
                        (__bf16*)aw, (__bf16*)au, w.qn, w.kn, w.wn, w.un, w.oi, T, H, L);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -624,7 +633,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
     if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,   \
                                  smem)) != hipSuccess)                                           \
       return e;                                                                                  \
-    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(256), smem, stream, (const __bf16*)q,          \
+    hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(kPrepThreads), smem, stream, (const __bf16*)q, \
                        (const __bf16*)k, (const __bf16*)v, (const TB_*)beta, gcum,               \
                        (const TL_*)l, (float*)nullptr, (__bf16*)nullptr, (__bf16*)nullptr, qn,   \
                        kn, wn, un, (float*)nullptr, T, H, L);                                    \

@@ -642,23 +642,39 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
   for (int m = 0; m < 4; ++m) tp[m] = zero4();
   if (ntop > 0) {
     const float* dp = segd + (size_t)row * NSEG;
+    // element (a, c) of this lane's part of a summary: role 0 reads R[c][a], role 1 R[a][c]
+    const int c = 16 * wr + ln;
     for (int e2 = 0; e2 < ntop; ++e2) {
       if ((p >> e2) & 1) continue;
       const int lo = ((p >> e2) | 1) << e2;
       const int hi = min(lo + (1 << e2), NSEG);
       float dlog = 0.f;
       for (int r = p + 1; r < lo; ++r) dlog += dp[r];
-      for (int qs = lo; qs < hi; ++qs) {
-        const float sc = fexp(dlog);
-        const float* src = rsum + (((size_t)row * NSEG + qs) * ntop + e2) * kKD * kKD;
+      // two summaries per step, all their loads issued before the sums
+      for (int q0 = lo; q0 < hi; q0 += 2) {
+        float x[2][16], sc[2];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int u = 0; u < 2; ++u) {
+          const int qs = min(q0 + u, hi - 1);
+          const float* src = rsum + (((size_t)row * NSEG + qs) * ntop + e2) * kKD * kKD;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int a = 16 * m + 4 * lq + i, c = 16 * wr + ln;
-            tp[m][i] += sc * (role == 0 ? src[c * kKD + a] : src[a * kKD + c]);
-          }
-        dlog += dp[qs];
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int a = 16 * m + 4 * lq + i;
+              x[u][4 * m + i] = role == 0 ? src[c * kKD + a] : src[a * kKD + c];
+            }
+        }
+        sc[0] = fexp(dlog);
+        dlog += dp[q0];
+        sc[1] = q0 + 1 < hi ? fexp(dlog) : 0.f;
+        if (q0 + 1 < hi) dlog += dp[q0 + 1];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tp[m][i] += sc[u] * x[u][4 * m + i];
       }
     }
   }
@@ -679,6 +695,10 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
   for (int ic = cend - 1; ic >= c0; --ic) {
     ld.store(rg, s);
     if (ic - 1 >= c0) ld.load(rg, ic - 1);
+    // q . dq of this chunk's tokens (written by the dq kernel), needed by wave 0 at
+    // the end of the chunk: loaded now so the load has the whole chunk to land
+    const unsigned int so_g = ((unsigned int)ic * kBT + lane) * H * 4;
+    const float qdq = w == 0 ? buf_load<float>(rgq, 0, so_g) : 0.f;
     __syncthreads();
 
     // ---- phase 1: (M o S) and (M o dP) tiles ---------------------------------------
@@ -809,11 +829,11 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
 
     // ---- dG = q . dq - k . dk and its reverse cumsum inside the segment --------------
     if (w == 0) {
-      const unsigned int so = ((unsigned int)ic * kBT + lane) * H * 4;
+      const unsigned int so = so_g;
       // column sums over the t-tiles at or after this s-tile (the others are zero)
       float kdk = sm.dgk[lane][0] + sm.dgk[lane][1] + sm.dgk[lane][2] + sm.dgk[lane][3];
       for (int mt = lane >> 4; mt < 4; ++mt) kdk += sm.kdk[lane][mt];
-      const float dG = buf_load<float>(rgq, 0, so) - kdk;
+      const float dG = qdq - kdk;
       float x = dG;   // inclusive suffix sum over the chunk
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {

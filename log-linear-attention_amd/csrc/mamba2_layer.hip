@@ -367,6 +367,98 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(
   else st1(o2, (size_t)bs * (Dc - d2) + (d - d2), y, fo);
 }
 
+// Vector form for bf16 input rows: each thread owns 8 consecutive channels
+// (16-byte loads and stores, consecutive lanes on consecutive channel groups)
+// and a run of kConvRun tokens of one sequence; the W - 1 input rows before the
+// current one stay in registers, so every input element is loaded once per
+// run (plus W - 1 halo rows).  Requires Dc, d1, d2, ld, col0 multiples of 8
+// and 16-byte aligned bases (checked by the host).
+constexpr int kConvRun = 32;
+
+template <int W>
+__global__ __launch_bounds__(256) void conv1d_silu_fwd_vec_kernel(
+    const __bf16* __restrict__ in, long ld, long col0, const void* __restrict__ wt,
+    const void* __restrict__ bias, void* __restrict__ o0, void* __restrict__ o1,
+    void* __restrict__ o2, int B, int S, int Dc, int d1, int d2, int fw, int fo) {
+  const int ng = Dc / 8;
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  const int cgp = (int)(gid % ng);
+  const long run = gid / ng;
+  const int nrun = (S + kConvRun - 1) / kConvRun;
+  if (run >= (long)B * nrun) return;
+  const int b = (int)(run / nrun), s0 = (int)(run % nrun) * kConvRun;
+  const int s1 = min(s0 + kConvRun, S);
+  const int d = 8 * cgp;
+  float wv[8][W], bv[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    bv[c] = bias ? ld1(bias, d + c, fw) : 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) wv[c][w] = ld1(wt, (size_t)(d + c) * W + w, fw);
+  }
+  // output tensor and row stride of this channel group
+  void* ob = d < d1 ? o0 : (d < d2 ? o1 : o2);
+  const int on = d < d1 ? d1 : (d < d2 ? d2 - d1 : Dc - d2);
+  const int oc = d < d1 ? d : (d < d2 ? d - d1 : d - d2);
+  const __bf16* src = in + (size_t)b * S * ld + col0 + d;
+  auto cvt = [](const bf16x8& u, float (&x)[8]) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[c] = (float)u[c];
+  };
+  float win[W][8];   // rows s - (W - 1) .. s
+#pragma unroll
+  for (int w = 0; w < W - 1; ++w) {
+    const int sp = s0 - (W - 1) + w;
+    const bf16x8 u = sp >= 0 ? *(const bf16x8*)(src + (size_t)sp * ld) : bf16x8{};
+    cvt(u, win[w]);
+  }
+  // rows in blocks of kConvBlk: the next block's loads are issued before the
+  // current block is computed, so each has a block's work to land
+  constexpr int kConvBlk = 8;
+  bf16x8 nxt[kConvBlk];
+  auto issue = [&](int sb) {
+#pragma unroll
+    for (int r = 0; r < kConvBlk; ++r)
+      nxt[r] = sb + r < s1 ? *(const bf16x8*)(src + (size_t)(sb + r) * ld) : bf16x8{};
+  };
+  issue(s0);
+  for (int sb = s0; sb < s1; sb += kConvBlk) {
+    bf16x8 cur[kConvBlk];
+#pragma unroll
+    for (int r = 0; r < kConvBlk; ++r) cur[r] = nxt[r];
+    if (sb + kConvBlk < s1) issue(sb + kConvBlk);
+#pragma unroll
+    for (int r = 0; r < kConvBlk; ++r) {
+      const int s = sb + r;
+      if (s < s1) {
+        cvt(cur[r], win[W - 1]);
+        float y[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          float acc = bv[c];
+#pragma unroll
+          for (int w = 0; w < W; ++w) acc += wv[c][w] * win[w][c];
+          y[c] = silu_f(acc);
+        }
+        const size_t oi = ((size_t)b * S + s) * on + oc;
+        if (fo) {
+          bf16x8 o;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) o[c] = (__bf16)y[c];
+          *(bf16x8*)((__bf16*)ob + oi) = o;
+        } else {
+          *(floatx4*)((float*)ob + oi) = floatx4{y[0], y[1], y[2], y[3]};
+          *(floatx4*)((float*)ob + oi + 4) = floatx4{y[4], y[5], y[6], y[7]};
+        }
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) win[w][c] = win[w + 1][c];
+      }
+    }
+  }
+}
+
 // Backward of the conv + SiLU.  Grid (Dc / 64, nblk): workgroup (cg, blk)
 // owns channels 64 cg .. + 63 and the 64-token tiles blk, blk + nblk, ... of
 // the flattened (b, s-tile) index.  Per tile it stages the input rows the
@@ -722,6 +814,24 @@ hipError_t hattn_conv1d_silu_fwd_launch(const void* in, long ld, long col0, cons
                                         int fo, hipStream_t stream) {
   using namespace hattn;
   const long BS = (long)B * S;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (fin == 1 && Dc % 8 == 0 && d1 % 8 == 0 && d2 % 8 == 0 && ld % 8 == 0 && col0 % 8 == 0 &&
+      a16(in) && a16(o0) && a16(o1) && a16(o2) && W >= 1 && W <= 8) {
+    const long threads = (long)B * ((S + kConvRun - 1) / kConvRun) * (Dc / 8);
+    const dim3 vgrid((unsigned)((threads + 255) / 256));
+    switch (W) {
+#define CONV_FWD_VEC(W_)                                                                        \
+  case W_:                                                                                      \
+    hipLaunchKernelGGL((conv1d_silu_fwd_vec_kernel<W_>), vgrid, dim3(256), 0, stream,            \
+                       (const __bf16*)in, ld, col0, wt, bias, o0, o1, o2, B, S, Dc, d1, d2, fw,  \
+                       fo);                                                                      \
+    break;
+      CONV_FWD_VEC(1) CONV_FWD_VEC(2) CONV_FWD_VEC(3) CONV_FWD_VEC(4) CONV_FWD_VEC(5)
+      CONV_FWD_VEC(6) CONV_FWD_VEC(7) CONV_FWD_VEC(8)
+#undef CONV_FWD_VEC
+    }
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)BS, (unsigned)((Dc + 255) / 256));
   switch (W) {
 #define CONV_FWD(W_)                                                                          \

@@ -129,14 +129,10 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   __shared__ __attribute__((aligned(16))) SumSmem<NP> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  // grid: xcd_head_grid(B * NSEG, H, nvb64); the heads of one (batch, segment) share an XCD.
-  // Groups run in reverse order: the consumer kernels walk them forwards, so
-  // they start on the k / v lines this kernel read last (the ones still held
-  // by the memory-side cache) instead of chasing the oldest ones out.
+  // grid: xcd_head_grid(B * NSEG, H, nvb64); the heads of one (batch, segment) share an XCD
   const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
-  const int grp = (B * NSEG + 7) / 8 * 8 - 1 - xm.grp;
-  if (grp >= B * NSEG) return;
-  const int vblk = xm.slice, h = xm.h, p = grp % NSEG, b = grp / NSEG;
+  if (xm.grp >= B * NSEG) return;
+  const int vblk = xm.slice, h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h, gq = h / (H / G);
   const int c0 = p * S;
   const int nch = min(S, NT - c0);

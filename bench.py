@@ -358,6 +358,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fwd-only", action="store_true", help="skip the forward+backward timing")
+    ap.add_argument("--cold-cache", action="store_true",
+                    help="also time each forward after evicting the memory-side cache")
     ap.add_argument("--calib", action="store_true",
                     help="also run a 2 GiB read-only kernel (sum) and a 2 GiB write-only kernel "
                          "(fill), larger than the 256 MB MALL, so a counter run can scale "
@@ -419,6 +421,24 @@ def main():
     nbytes = fwd_bytes(B, T, H, K, V, L)
     flops = fwd_flops(B, T, H, K, V)
     achieved = nbytes / avg_launch_s
+
+    # the same launches with the memory-side cache (256 MB) evicted before each
+    # one by a 1 GiB fill outside the events: no reuse of the previous step's
+    # lines, only what one forward call reuses within itself
+    cold_launch_s = None
+    if args.cold_cache:
+        evict = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+        cold_ms = []
+        for i in range(args.steps):
+            evict.fill_(float(i))
+            a, b_ = ev[i]
+            a.record(stream)
+            step()
+            b_.record(stream)
+            torch.cuda.synchronize()
+            cold_ms.append(a.elapsed_time(b_))
+        del evict
+        cold_launch_s = sum(cold_ms) / len(cold_ms) / 1e3
 
     # forward + backward through the autograd boundary (HAttentionFunction):
     # the HIP forward, then the HIP backward for dq, dk, dv, dg, dlambda
@@ -524,7 +544,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes, "avg_launch_us": avg_launch_s * 1e6,
-                     "mfma_frac": flops / avg_launch_s / MFMA_BF16_PEAK},
+                     "mfma_frac": flops / avg_launch_s / MFMA_BF16_PEAK,
+                     **({"cold_cache_avg_launch_us": cold_launch_s * 1e6,
+                         "cold_cache_frac": nbytes / cold_launch_s / HBM_PEAK}
+                        if cold_launch_s else {})},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

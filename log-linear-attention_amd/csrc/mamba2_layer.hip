@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <algorithm>
 #include <initializer_list>
 
 #include "common.h"
@@ -558,6 +559,150 @@ __global__ __launch_bounds__(256) void conv1d_silu_bwd_kernel(
 }
 
 
+// Vector form of the backward for bf16 rows (input, output gradients and din):
+// each thread owns 8 consecutive channels and a run of kConvRun tokens; the
+// W - 1 input rows and dpre values before the current row stay in registers,
+// so one pass over rows s0 .. s0 + kConvRun + W - 2 yields dpre, din for the
+// run and the weight / bias partials.  Workgroup (cb, rb): channel groups
+// 16 cb + (tid & 15) and runs 16 rb + (tid >> 4) of the flattened (b, run)
+// index; the partials of its 16 runs are summed in a fixed order (lane
+// shuffles, then the four waves) into ws[rb][d][W + 1].
+constexpr int kConvBwdRuns = 16;
+
+template <int W>
+__global__ __launch_bounds__(256) void conv1d_silu_bwd_vec_kernel(
+    const __bf16* __restrict__ in, long ld, long col0, const void* __restrict__ wt,
+    const void* __restrict__ bias, const __bf16* __restrict__ g0,
+    const __bf16* __restrict__ g1, const __bf16* __restrict__ g2, __bf16* __restrict__ din,
+    long ldo, long colo, float* __restrict__ ws, int B, int S, int Dc, int d1, int d2,
+    int fw) {
+  __shared__ float red[4][16][8][W + 1];
+  const int tid = threadIdx.x, cl = tid & 15, rl = tid >> 4;
+  const int ng = Dc / 8, nrun = (S + kConvRun - 1) / kConvRun;
+  const int cg = blockIdx.x * 16 + cl;
+  const long run = (long)blockIdx.y * kConvBwdRuns + rl;
+  const bool ok = cg < ng && run < (long)B * nrun;
+  const int d = 8 * min(cg, ng - 1);
+  float wv[8][W], bv[8], accw[8][W], accb[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    bv[c] = bias ? ld1(bias, d + c, fw) : 0.f;
+    accb[c] = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      wv[c][w] = ld1(wt, (size_t)(d + c) * W + w, fw);
+      accw[c][w] = 0.f;
+    }
+  }
+  if (ok) {
+    const int b = (int)(run / nrun), s0 = (int)(run % nrun) * kConvRun;
+    const int s1 = min(s0 + kConvRun, S);
+    const int tend = min(s1 + W - 1, S);   // rows with a dpre value (zero past S)
+    const __bf16* gb = d < d1 ? g0 : (d < d2 ? g1 : g2);
+    const int gn = d < d1 ? d1 : (d < d2 ? d2 - d1 : Dc - d2);
+    const int gc = d < d1 ? d : (d < d2 ? d - d1 : d - d2);
+    const __bf16* src = in + (size_t)b * S * ld + col0 + d;
+    const __bf16* gsrc = gb + (size_t)b * S * gn + gc;
+    __bf16* dst = din + (size_t)b * S * ldo + colo + d;
+    float xw[W][8], dw[W][8];   // x rows t-(W-1)..t, dpre rows t-(W-1)..t
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+      const int sp = s0 - (W - 1) + w;
+      const bf16x8 u = sp >= 0 ? *(const bf16x8*)(src + (size_t)sp * ld) : bf16x8{};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        xw[w][c] = (float)u[c];
+        dw[w][c] = 0.f;
+      }
+    }
+    constexpr int kBlk = 4;
+    bf16x8 nx[kBlk], ngr[kBlk];
+    auto issue = [&](int tb) {
+#pragma unroll
+      for (int r = 0; r < kBlk; ++r) {
+        const bool in_s = tb + r < tend;
+        nx[r] = in_s ? *(const bf16x8*)(src + (size_t)(tb + r) * ld) : bf16x8{};
+        ngr[r] = in_s ? *(const bf16x8*)(gsrc + (size_t)(tb + r) * gn) : bf16x8{};
+      }
+    };
+    const int tlast = s1 + W - 1;   // rows s0 .. tlast - 1 are walked
+    issue(s0);
+    for (int tb = s0; tb < tlast; tb += kBlk) {
+      bf16x8 cx[kBlk], cgr[kBlk];
+#pragma unroll
+      for (int r = 0; r < kBlk; ++r) {
+        cx[r] = nx[r];
+        cgr[r] = ngr[r];
+      }
+      if (tb + kBlk < tlast) issue(tb + kBlk);
+#pragma unroll
+      for (int r = 0; r < kBlk; ++r) {
+        const int t = tb + r;
+        if (t < tlast) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            xw[W - 1][c] = (float)cx[r][c];
+            float pre = bv[c];
+#pragma unroll
+            for (int w = 0; w < W; ++w) pre += wv[c][w] * xw[w][c];
+            // rows past S load as zero gradients, so dpre is zero there
+            dw[W - 1][c] = (float)cgr[r][c] * dsilu_f(pre);
+          }
+          if (t < s1) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              accb[c] += dw[W - 1][c];
+#pragma unroll
+              for (int w = 0; w < W; ++w) accw[c][w] += dw[W - 1][c] * xw[w][c];
+            }
+          }
+          const int so = t - (W - 1);   // din row completed by this dpre
+          if (so >= s0 && so < s1) {
+            bf16x8 o;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              float gi = 0.f;
+#pragma unroll
+              for (int w = 0; w < W; ++w) gi += wv[c][w] * dw[W - 1 - w][c];
+              o[c] = (__bf16)gi;
+            }
+            *(bf16x8*)(dst + (size_t)so * ldo) = o;
+          }
+#pragma unroll
+          for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              xw[w][c] = xw[w + 1][c];
+              dw[w][c] = dw[w + 1][c];
+            }
+        }
+      }
+    }
+  }
+  // the wave's four runs (lanes 16 apart), then the four waves, in fixed order
+  const int wv_id = tid >> 6;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int w = 0; w <= W; ++w) {
+      float a = w < W ? accw[c][w] : accb[c];
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      if ((tid & 63) < 16) red[wv_id][cl][c][w] = a;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < 16 * 8 * (W + 1); e += 256) {
+    const int l = e / (8 * (W + 1)), rem = e % (8 * (W + 1));
+    const int c = rem / (W + 1), w = rem % (W + 1);
+    const int cgo = blockIdx.x * 16 + l;
+    if (cgo < ng) {
+      const float sum = red[0][l][c][w] + red[1][l][c][w] + red[2][l][c][w] + red[3][l][c][w];
+      ws[((size_t)blockIdx.y * Dc + 8 * cgo + c) * (W + 1) + w] = sum;
+    }
+  }
+}
+
 // Gated RMSNorm, one wave per row of n features: u = y silu(z), r = rsqrt(mean
 // u^2 + eps), out = u r w; r is saved for the backward.
 __global__ __launch_bounds__(256) void gated_rmsnorm_fwd_kernel(
@@ -800,9 +945,15 @@ int norm_bwd_nblk(long rows) {
 }
 }  // namespace
 
+// run blocks of the vector backward (one partial row of ws each)
+long conv_bwd_vec_nblk(int B, int S) {
+  const long runs = (long)B * ((S + hattn::kConvRun - 1) / hattn::kConvRun);
+  return (runs + hattn::kConvBwdRuns - 1) / hattn::kConvBwdRuns;
+}
 size_t hattn_conv1d_bwd_ws_bytes(int B, int S, int Dc, int W) {
   const long tiles = (long)B * ((S + hattn::kConvTile - 1) / hattn::kConvTile);
-  return (size_t)conv_bwd_nblk(tiles, (Dc + 63) / 64) * Dc * (W + 1) * sizeof(float);
+  const long nblk = std::max<long>(conv_bwd_nblk(tiles, (Dc + 63) / 64), conv_bwd_vec_nblk(B, S));
+  return (size_t)nblk * Dc * (W + 1) * sizeof(float);
 }
 size_t hattn_rmsnorm_bwd_ws_bytes(long rows, int n) {
   return (size_t)norm_bwd_nblk(rows) * n * sizeof(float);
@@ -855,6 +1006,30 @@ hipError_t hattn_conv1d_silu_bwd_launch(const void* in, long ld, long col0, cons
                                         int d1, int d2, int W, int fin, int fw, int fg0, int fg1,
                                         int fg2, int fdi, hipStream_t stream) {
   using namespace hattn;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (fin == 1 && fg0 == 1 && fg1 == 1 && fg2 == 1 && fdi == 1 && Dc % 8 == 0 && d1 % 8 == 0 &&
+      d2 % 8 == 0 && ld % 8 == 0 && col0 % 8 == 0 && ldo % 8 == 0 && colo % 8 == 0 &&
+      a16(in) && a16(g0) && a16(g1) && a16(g2) && a16(din) && W >= 1 && W <= 8) {
+    const long vblk = conv_bwd_vec_nblk(B, S);
+    const dim3 vgrid((unsigned)((Dc / 8 + 15) / 16), (unsigned)vblk);
+    switch (W) {
+#define CONV_BWD_VEC(W_)                                                                       \
+  case W_:                                                                                     \
+    hipLaunchKernelGGL((conv1d_silu_bwd_vec_kernel<W_>), vgrid, dim3(256), 0, stream,           \
+                       (const __bf16*)in, ld, col0, wt, bias, (const __bf16*)g0,                \
+                       (const __bf16*)g1, (const __bf16*)g2, (__bf16*)din, ldo, colo, ws, B, S, \
+                       Dc, d1, d2, fw);                                                         \
+    break;
+      CONV_BWD_VEC(1) CONV_BWD_VEC(2) CONV_BWD_VEC(3) CONV_BWD_VEC(4) CONV_BWD_VEC(5)
+      CONV_BWD_VEC(6) CONV_BWD_VEC(7) CONV_BWD_VEC(8)
+#undef CONV_BWD_VEC
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(conv1d_bwd_reduce_kernel, dim3((Dc * (W + 1) + 63) / 64), dim3(1024), 0,
+                       stream, ws, dw, db, (int)vblk, Dc, W);
+    return hipGetLastError();
+  }
   const int ncg = (Dc + 63) / 64;
   const long tiles = (long)B * ((S + kConvTile - 1) / kConvTile);
   const int nblk = conv_bwd_nblk(tiles, ncg);

@@ -267,3 +267,51 @@ def test_split_conv1d_layer_bwd_deterministic():
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# causal conv1d + SiLU alone (hattention.mamba_layer.CausalConv1dSilu)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,W,S", [(torch.bfloat16, 4, 256), (torch.bfloat16, 2, 100),
+                                       (torch.bfloat16, 7, 45), (torch.bfloat16, 1, 64),
+                                       (torch.float32, 4, 100), (torch.float32, 3, 33)])
+def test_causal_conv1d_silu_matches_oracle(dtype, W, S):
+    """Output windows x, B, C and the gradients (zx window, weight, bias)
+    against autograd through oracle.mamba2.causal_conv1d_silu in float64.
+    bf16 rows with 8-aligned windows take the vector kernels (8 channels x
+    32-token runs per thread, sequence lengths ragged against the run), fp32
+    rows the scalar kernels.  Tolerance: 2e-2 of each tensor's max for bf16
+    (outputs and din are rounded to bf16), 1e-4 for fp32."""
+    from hattention.mamba_layer import CausalConv1dSilu
+    Bsz, col0, d1, d2, Dc = 2, 16, 64, 96, 136
+    width = col0 + Dc + 24
+    gen = torch.Generator("cpu").manual_seed(500 + W * 7 + S)
+    zx = torch.randn(Bsz, S, width, generator=gen).to(dtype)
+    w = torch.randn(Dc, W, generator=gen) * 0.5
+    b = torch.randn(Dc, generator=gen) * 0.1
+    gs = [torch.randn(Bsz, S, n, generator=gen) for n in (d1, d2 - d1, Dc - d2)]
+    print(f"[conv] dtype={dtype} W={W} S={S}", flush=True)
+    dz = zx.to(DEV).requires_grad_(True)
+    dw, db = w.to(DEV).requires_grad_(True), b.to(DEV).requires_grad_(True)
+    outs = CausalConv1dSilu.apply(dz, col0, Dc, d1, d2, dw, db)
+    torch.autograd.backward(outs, [g.to(DEV).to(dtype) for g in gs])
+    torch.cuda.synchronize()
+    rz = zx.double().requires_grad_(True)
+    rw, rb = w.double().requires_grad_(True), b.double().requires_grad_(True)
+    y = M.causal_conv1d_silu(rz[..., col0:col0 + Dc].transpose(1, 2), rw, rb).transpose(1, 2)
+    refs = torch.split(y, [d1, d2 - d1, Dc - d2], dim=-1)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    for o, r in zip(outs, refs):
+        assert o.dtype == dtype
+        mx, _ = _errs(o, r)
+        assert mx < tol, mx
+    # gradients of the bf16-rounded gradient inputs, as the kernels see them
+    rg = torch.cat([g.to(dtype).double() for g in gs], dim=-1)
+    gz, gw, gb = torch.autograd.grad((y * rg).sum(), [rz, rw, rb])
+    for name, got, want in (("zx", dz.grad, gz), ("weight", dw.grad, gw), ("bias", db.grad, gb)):
+        mx, fro = _errs(got, want)
+        print(f"  d{name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < tol, (name, mx)
+    # columns outside the conv window get no gradient from this op
+    assert torch.count_nonzero(dz.grad[..., :col0]) == 0
+    assert torch.count_nonzero(dz.grad[..., col0 + Dc:]) == 0

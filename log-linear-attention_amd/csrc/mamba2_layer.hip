@@ -51,6 +51,31 @@ __device__ __forceinline__ void st4(void* p, size_t i, floatx4 x, int bf) {
   else *(floatx4*)((float*)p + i) = x;
 }
 
+// eight consecutive elements starting at a multiple of 8 (16-byte aligned base)
+__device__ __forceinline__ void ld8(const void* p, size_t i, int bf, float* o) {
+  if (bf) {
+    const bf16x8 a = *(const bf16x8*)((const __bf16*)p + i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = (float)a[k];
+  } else {
+    const floatx4 a = *(const floatx4*)((const float*)p + i);
+    const floatx4 b = *(const floatx4*)((const float*)p + i + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { o[k] = a[k]; o[4 + k] = b[k]; }
+  }
+}
+__device__ __forceinline__ void st8(void* p, size_t i, const float* x, int bf) {
+  if (bf) {
+    bf16x8 a;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = (__bf16)x[k];
+    *(bf16x8*)((__bf16*)p + i) = a;
+  } else {
+    *(floatx4*)((float*)p + i) = floatx4{x[0], x[1], x[2], x[3]};
+    *(floatx4*)((float*)p + i + 4) = floatx4{x[4], x[5], x[6], x[7]};
+  }
+}
+
 // torch.nn.functional.softplus (beta 1, threshold 20) and its derivative
 __device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float dsoftplus20(float x) {
@@ -124,6 +149,60 @@ __global__ __launch_bounds__(256) void mamba2_layer_prologue_kernel(
     const int l = (int)(e - r * L);
     const int h = (int)(r % (unsigned int)H);
     st1(lam, e, lambda_of(ld1(Lp, (size_t)h * L + l, f.lp), ld1(dl, e, f.dl), mode), f.lam);
+  }
+}
+
+// Vector form (P % 8 == 0, 16-byte aligned x, v, dl, lam): eight x elements
+// per thread in blocks [0, nbx), eight consecutive lambda elements per thread
+// after them (the row / level of the first one divided out once, then
+// stepped).
+__global__ __launch_bounds__(256) void mamba2_layer_prologue_vec_kernel(
+    const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ A,
+    const float* __restrict__ dt_bias, const void* __restrict__ dl, const void* __restrict__ Lp,
+    void* __restrict__ v, float* __restrict__ g, void* __restrict__ lam, long rows, int H,
+    int P, int L, int softplus, int mode, LayerDt f, int nbx) {
+  const unsigned int lp = 31 - __builtin_clz((unsigned int)P);
+  if ((int)blockIdx.x < nbx) {
+    const unsigned int e0 = 8u * (blockIdx.x * 256u + threadIdx.x);
+    if (e0 >= (unsigned int)(rows * P)) return;
+    const unsigned int r = e0 >> lp;
+    const int h = (int)(r % (unsigned int)H);
+    float d = ld1(dt, r, f.dt) + (dt_bias ? dt_bias[h] : 0.f);
+    if (softplus) d = softplus20(d);
+    float xv[8];
+    ld8(x, e0, f.x, xv);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) xv[c] *= d;
+    st8(v, e0, xv, f.v);
+    if (e0 == r * P) g[r] = A[h] * d;
+  } else {
+    const unsigned int n = (unsigned int)(rows * L);
+    const unsigned int e0 = 8u * ((blockIdx.x - nbx) * 256u + threadIdx.x);
+    if (e0 >= n) return;
+    unsigned int r = e0 / (unsigned int)L;
+    int l = (int)(e0 - r * L);
+    int h = (int)(r % (unsigned int)H);
+    if (e0 + 8 <= n) {
+      float dv[8];
+      ld8(dl, e0, f.dl, dv);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        dv[c] = lambda_of(ld1(Lp, (size_t)h * L + l, f.lp), dv[c], mode);
+        if (++l == L) {
+          l = 0;
+          h = h + 1 == H ? 0 : h + 1;
+        }
+      }
+      st8(lam, e0, dv, f.lam);
+    } else {
+      for (unsigned int e = e0; e < n; ++e) {
+        st1(lam, e, lambda_of(ld1(Lp, (size_t)h * L + l, f.lp), ld1(dl, e, f.dl), mode), f.lam);
+        if (++l == L) {
+          l = 0;
+          h = h + 1 == H ? 0 : h + 1;
+        }
+      }
+    }
   }
 }
 
@@ -274,6 +353,14 @@ hipError_t hattn_mamba2_layer_prologue_launch(const void* x, const void* dt, con
   using namespace hattn;
   const long rows = (long)B * T * H;
   const LayerDt f{bf[0], bf[1], bf[2], bf[3], bf[4], bf[5]};
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (P % 8 == 0 && a16(x) && a16(v) && a16(dl) && a16(lam)) {
+    const long nx = (rows * P / 8 + 255) / 256, nl = ((rows * L + 7) / 8 + 255) / 256;
+    hipLaunchKernelGGL(mamba2_layer_prologue_vec_kernel, dim3((unsigned)(nx + nl)), dim3(256), 0,
+                       stream, x, dt, A, dt_bias, dl, Lp, v, g, lam, rows, H, P, L, softplus,
+                       mode, f, (int)nx);
+    return hipGetLastError();
+  }
   const long nx = (rows * P / 4 + 255) / 256, nl = (rows * L + 255) / 256;
   hipLaunchKernelGGL(mamba2_layer_prologue_kernel, dim3((unsigned)(nx + nl)), dim3(256), 0, stream,
                      x, dt, A, dt_bias, dl, Lp, v, g, lam, rows, H, P, L, softplus, mode, f,
@@ -767,30 +854,6 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_bwd_kernel(
 // Vector forms of the gated RMSNorm for n % 8 == 0, n <= 512 NC, 16-byte aligned
 // rows: lane l of a row's wave owns elements 512 c + 8 l .. + 7 (c < NC) and
 // keeps them in registers between the sum and the output.
-__device__ __forceinline__ void ld8(const void* p, size_t i, int bf, float* o) {
-  if (bf) {
-    const bf16x8 a = *(const bf16x8*)((const __bf16*)p + i);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) o[k] = (float)a[k];
-  } else {
-    const floatx4 a = *(const floatx4*)((const float*)p + i);
-    const floatx4 b = *(const floatx4*)((const float*)p + i + 4);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) { o[k] = a[k]; o[4 + k] = b[k]; }
-  }
-}
-__device__ __forceinline__ void st8(void* p, size_t i, const float* x, int bf) {
-  if (bf) {
-    bf16x8 a;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) a[k] = (__bf16)x[k];
-    *(bf16x8*)((__bf16*)p + i) = a;
-  } else {
-    *(floatx4*)((float*)p + i) = floatx4{x[0], x[1], x[2], x[3]};
-    *(floatx4*)((float*)p + i + 4) = floatx4{x[4], x[5], x[6], x[7]};
-  }
-}
-
 template <int NC>
 __global__ __launch_bounds__(256) void gated_rmsnorm_fwd_vec_kernel(
     const void* __restrict__ y, const void* __restrict__ z, long ldz, const void* __restrict__ w,

@@ -315,6 +315,122 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
 }
 
 // Per-head sums over the workgroups, in a fixed order; grid H.
+// Vector form of the backward (P % 8 == 0, H P / 8 dividing 256, 3 H <= 256, H L <= 1024,
+// 16-byte aligned x, dv, dy, dx): workgroup blk owns a contiguous share of the
+// B T token rows, all heads.  x part: thread tid handles the eight elements
+// 8 (tid % tpb) .. + 7 of rows bt = slot, slot + rpi, ... (tpb = H P / 8
+// threads per row, rpi = 256 / tpb rows at a time), so its head is fixed; a
+// (row, head) is summed over its P / 8 consecutive lanes.  lambda part:
+// thread tid handles offsets tid + 256 k of every row's H L entries, so each
+// (head, level) has one owner and dL needs no reduction in the workgroup.
+// Partials go to ws[h][blk][3 + L] like the per-head kernel's.
+template <int NL>
+__global__ __launch_bounds__(256) void mamba2_layer_bwd_vec_kernel(
+    const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ A,
+    const float* __restrict__ dt_bias, const void* __restrict__ dl, const void* __restrict__ Lp,
+    const float* __restrict__ D, const void* __restrict__ dy, const void* __restrict__ dv,
+    const float* __restrict__ dg, const void* __restrict__ dlam, void* __restrict__ dx,
+    void* __restrict__ ddt, void* __restrict__ ddl, float* __restrict__ ws, long BT, int H,
+    int P, int L, int softplus, int mode, LayerBwdDt f) {
+  __shared__ float red[3][256];
+  const int tid = threadIdx.x, blk = blockIdx.x, nblk = gridDim.x;
+  const int HP = H * P, tpb = HP / 8, rpi = 256 / tpb, gl = P / 8;
+  const int slot = tid / tpb, col = (tid % tpb) * 8, h = col / P, j = (col % P) / 8;
+  const long per = (BT + nblk - 1) / nblk;
+  const long bt0 = (long)blk * per, bt1 = min(BT, bt0 + per);
+  const float Ah = A[h], bias = dt_bias ? dt_bias[h] : 0.f, Dh = D ? D[h] : 0.f;
+  float accA = 0.f, accB = 0.f, accD = 0.f;
+  for (long bt = bt0 + slot; bt < bt1; bt += rpi) {
+    const long r = bt * H + h;
+    const size_t e0 = (size_t)bt * HP + col;
+    const float pre = ld1(dt, r, f.dt) + bias;
+    const float d = softplus ? softplus20(pre) : pre;
+    float xv[8], gv[8], yv[8], o[8];
+    ld8(x, e0, f.x, xv);
+    ld8(dv, e0, f.dv, gv);
+    if (D) ld8(dy, e0, f.dy, yv);
+    else
+#pragma unroll
+      for (int c = 0; c < 8; ++c) yv[c] = 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      o[c] = gv[c] * d + yv[c] * Dh;
+      s += gv[c] * xv[c];
+      accD += yv[c] * xv[c];
+    }
+    st8(dx, e0, o, f.dx);
+    for (int m = 1; m < gl; m <<= 1) s += __shfl_xor(s, m, 64);
+    if (j == 0) {
+      const float dgr = dg[r];
+      const float ddtv = s + dgr * Ah;
+      const float dd = softplus ? ddtv * dsoftplus20(pre) : ddtv;
+      st1(ddt, r, dd, f.ddt);
+      accA += dgr * d;
+      accB += dd;
+    }
+  }
+  // lambda entries: fixed (head, level) per thread and k
+  const int HL = H * L;
+  float accL[NL], Lv[NL];
+  int lk[NL];
+#pragma unroll
+  for (int k = 0; k < NL; ++k) {
+    const int oq = tid + 256 * k;
+    accL[k] = 0.f;
+    lk[k] = oq < HL ? oq % L : 0;
+    Lv[k] = oq < HL ? ld1(Lp, oq, f.lp) : 0.f;   // Lp [H, L] row-major: offset oq
+  }
+#pragma unroll 4
+  for (long bt = bt0; bt < bt1; ++bt) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int oq = tid + 256 * k;
+      if (oq < HL) {
+        const size_t el = (size_t)bt * HL + oq;
+        const float dlv = ld1(dl, el, f.dl), gq = ld1(dlam, el, f.dlam);
+        float gdl, gL;
+        if (mode == kLamPositive) {
+          const float u = gq * dsoftplus20(Lv[k] * dlv);
+          gdl = u * Lv[k];
+          gL = u * dlv;
+        } else if (mode == kLamBounded) {
+          const float eL = expf(Lv[k]), sp = softplus20(dlv);
+          const float lamv = expf(-eL * sp);
+          gL = gq * lamv * (-eL * sp);
+          gdl = gq * lamv * (-eL) * dsoftplus20(dlv);
+        } else {
+          gdl = gq * Lv[k];
+          gL = gq * dlv;
+        }
+        st1(ddl, el, gdl, f.ddl);
+        accL[k] += gL;
+      }
+    }
+  }
+  // dD: sum over the (row, head) group's lanes, then everything per head over
+  // the rpi row slots in order
+  for (int m = 1; m < gl; m <<= 1) accD += __shfl_xor(accD, m, 64);
+  if (j == 0) {
+    red[0][slot * H + h] = accA;
+    red[1][slot * H + h] = accB;
+    red[2][slot * H + h] = accD;
+  }
+  __syncthreads();
+  const int nq = 3 + L;
+  if (tid < 3 * H) {
+    const int q = tid / H, hh = tid % H;
+    float sum = 0.f;
+    for (int sl = 0; sl < rpi; ++sl) sum += red[q][sl * H + hh];
+    ws[((size_t)hh * nblk + blk) * nq + q] = sum;
+  }
+#pragma unroll
+  for (int k = 0; k < NL; ++k) {
+    const int oq = tid + 256 * k;
+    if (oq < HL) ws[((size_t)(oq / L) * nblk + blk) * nq + 3 + lk[k]] = accL[k];
+  }
+}
+
 __global__ __launch_bounds__(1024) void mamba2_layer_bwd_reduce_kernel(
     const float* __restrict__ ws, float* __restrict__ dA, float* __restrict__ ddt_bias,
     float* __restrict__ dD, float* __restrict__ dLp, int nblk, int L) {
@@ -340,9 +456,16 @@ int layer_bwd_nblk(long BT, int H) {
 }
 }  // namespace
 
+// workgroups of the vector backward: about 1024, at least 16 rows each
+int layer_bwd_vec_nblk(long BT) {
+  long n = (BT + 15) / 16;
+  if (n > 1024) n = 1024;
+  return (int)(n < 1 ? 1 : n);
+}
 size_t hattn_mamba2_layer_bwd_ws_bytes(int B, int T, int H, int L) {
   const long BT = (long)B * T;
-  return (size_t)H * layer_bwd_nblk(BT, H) * (3 + L) * sizeof(float);
+  const long nblk = std::max<long>(layer_bwd_nblk(BT, H), layer_bwd_vec_nblk(BT));
+  return (size_t)H * nblk * (3 + L) * sizeof(float);
 }
 
 hipError_t hattn_mamba2_layer_prologue_launch(const void* x, const void* dt, const float* A,
@@ -389,8 +512,27 @@ hipError_t hattn_mamba2_layer_bwd_launch(const void* x, const void* dt, const fl
                                          hipStream_t stream) {
   using namespace hattn;
   const long BT = (long)B * T;
-  const int nblk = layer_bwd_nblk(BT, H);
   const LayerBwdDt f{bf[0], bf[1], bf[2], bf[3], bf[4], bf[5], bf[6], bf[7], bf[8], bf[9]};
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int tpb = H * P / 8;
+  if (P % 8 == 0 && tpb <= 256 && 256 % tpb == 0 && 3 * H <= 256 && H * L <= 4 * 256 && a16(x) &&
+      a16(dv) && (D == nullptr || a16(dy)) && a16(dx)) {
+    const int vblk = layer_bwd_vec_nblk(BT), nl = (H * L + 255) / 256;
+#define LAYER_BWD_VEC(NL_)                                                                      \
+  hipLaunchKernelGGL((mamba2_layer_bwd_vec_kernel<NL_>), dim3(vblk), dim3(256), 0, stream, x,   \
+                     dt, A, dt_bias, dl, Lp, D, dy, dv, dg, dlam, dx, ddt, ddl, ws, BT, H, P, L, \
+                     softplus, mode, f)
+    if (nl <= 1) LAYER_BWD_VEC(1);
+    else if (nl <= 2) LAYER_BWD_VEC(2);
+    else LAYER_BWD_VEC(4);
+#undef LAYER_BWD_VEC
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mamba2_layer_bwd_reduce_kernel, dim3(H), dim3(1024), 0, stream, ws, dA,
+                       ddt_bias, dD, dLp, vblk, L);
+    return hipGetLastError();
+  }
+  const int nblk = layer_bwd_nblk(BT, H);
   const int tpr = P / 4, ni = (L + tpr - 1) / tpr;   // lambda entries per thread
 #define LAYER_BWD(NI_)                                                                         \
   hipLaunchKernelGGL((mamba2_layer_bwd_kernel<NI_>), dim3(nblk, H), dim3(256), 0, stream, x,   \

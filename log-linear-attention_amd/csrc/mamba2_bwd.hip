@@ -270,23 +270,48 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[a][n] = zero4();
-  float E = 0.f;
-  for (int ic = c0; ic < cend; ++ic) {
+  // chunk ic + 2 is loaded into the register slot that chunk ic leaves when it
+  // is stored to LDS, so two chunks' loads are in flight behind each chunk's
+  // MFMAs (the loop is unrolled by two so the slots are static registers).
+  // Every lane issues the same loads: the lambda column is clamped to a valid
+  // one and zeroed at the store, so no load sits behind a divergent branch.
+  struct ChunkRegs {
+    uint4 q0, q1, d0, d1;
+    float gct, glast, lv;
+  };
+  const unsigned int lcol = (unsigned int)(7 + nloc + e0 + min(le, ne - 1));
+  ChunkRegs rr[2];
+  auto load = [&](int ic, int slot) {
+    if (ic >= cend) return;
     const unsigned int t0 = (unsigned int)ic * kBT;
-    const uint4 q0 = buf_load16(rq, vo, t0 * qrow), q1 = buf_load16(rq, vo, (t0 + 32) * qrow);
-    const uint4 d0 = buf_load16(rd, vo, t0 * qrow), d1 = buf_load16(rd, vo, (t0 + 32) * qrow);
-    const float gct = buf_load<float>(rg, lt * H * 4, t0 * H * 4);
-    const float glast = buf_load<float>(rg, 63 * H * 4, t0 * H * 4);
-    float lv = 0.f;
-    if (le < ne) lv = to_f32<TL>(buf_load<TL>(rl, (lt * H * L + 7 + nloc + e0 + le) * sizeof(TL),
-                                             t0 * lrowb));
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+      if (sl == slot) {
+        rr[sl].q0 = buf_load16(rq, vo, t0 * qrow);
+        rr[sl].q1 = buf_load16(rq, vo, (t0 + 32) * qrow);
+        rr[sl].d0 = buf_load16(rd, vo, t0 * qrow);
+        rr[sl].d1 = buf_load16(rd, vo, (t0 + 32) * qrow);
+        rr[sl].gct = buf_load<float>(rg, lt * H * 4, t0 * H * 4);
+        rr[sl].glast = buf_load<float>(rg, 63 * H * 4, t0 * H * 4);
+        rr[sl].lv = to_f32<TL>(buf_load<TL>(rl, (lt * H * L + lcol) * sizeof(TL), t0 * lrowb));
+      }
+  };
+  float E = 0.f;
+  auto step = [&](int ic, int slot) {
     __syncthreads();   // previous chunk's reads of sm are done
     const int off = (tid >> 3) * kLd + 8 * (tid & 7);
-    *(uint4*)(sm.q + off) = q0;
-    *(uint4*)(sm.q + off + 32 * kLd) = q1;
-    *(uint4*)(sm.d + off) = d0;
-    *(uint4*)(sm.d + off + 32 * kLd) = d1;
-    sm.sig[le][lt] = lv * fexp(E + gct);
+    float glast = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+      if (sl == slot) {
+        *(uint4*)(sm.q + off) = rr[sl].q0;
+        *(uint4*)(sm.q + off + 32 * kLd) = rr[sl].q1;
+        *(uint4*)(sm.d + off) = rr[sl].d0;
+        *(uint4*)(sm.d + off + 32 * kLd) = rr[sl].d1;
+        sm.sig[le][lt] = le < ne ? rr[sl].lv * fexp(E + rr[sl].gct) : 0.f;
+        glast = rr[sl].glast;
+      }
+    load(ic + 2, slot);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -305,6 +330,12 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
       }
     }
     E += glast;
+  };
+  load(c0, 0);
+  load(c0 + 1, 1);
+  for (int ic = c0; ic < cend; ic += 2) {
+    step(ic, 0);
+    if (ic + 1 < cend) step(ic + 1, 1);
   }
 #pragma unroll
   for (int a = 0; a < 4; ++a) {

@@ -937,11 +937,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   for (int u = tid; u < kGC * L; u += 256) {
     const int t = u / L, c = u % L;
     // inter-chunk columns: the partial loads of every slice issue together
-    // (clamped to column 7 elsewhere, and not used there)
+    // (clamped to column 7 elsewhere, and not used there); with no inter-chunk
+    // level (T = 64) the partial buffer is empty and nothing is loaded
     const int ce = min(max(c, 7), 6 + nlev) - 7;
     float pl[NPV];
 #pragma unroll
-    for (int p = 0; p < NPV; ++p) pl[p] = dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + ce];
+    for (int p = 0; p < NPV; ++p)
+      pl[p] = nlev > 0 ? dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + ce] : 0.f;
     float x = 0.f;
     if (c < 7) {
       x = s.dlam[c][t];

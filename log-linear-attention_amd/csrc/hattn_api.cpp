@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 
 #include "../../include/hattn.h"
 
@@ -119,6 +120,26 @@ int check_hip(hipError_t e, const char* what) {
   return ok();
 }
 
+size_t elem_bytes(int code) { return code == HATTN_FP32 ? 4 : 2; }
+
+// The Mamba-2 kernels address one batch's [T, heads, D] slice of each tensor
+// through a buffer descriptor whose byte range and offsets are 32-bit, so
+// every slice must stay below 4 GiB.  row_bytes: the largest per-token row
+// (all heads) of any tensor the call reads or writes.
+int check_span(int T, size_t row_bytes) {
+  if ((unsigned long long)T * row_bytes >= (1ull << 32))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "one batch's slice of T=%d rows of %zu bytes reaches 4 GiB (32-bit buffer range)",
+                T, row_bytes);
+  return HATTN_OK;
+}
+
+size_t max_of(std::initializer_list<size_t> xs) {
+  size_t m = 0;
+  for (size_t x : xs) m = x > m ? x : m;
+  return m;
+}
+
 }  // namespace
 
 extern "C" {
@@ -168,6 +189,18 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
   if (nlev > hattn_mamba2_fwd_max_levels(x3))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d%s", T,
                 hattn_mamba2_fwd_max_levels(x3), x3 ? " in fp32" : "");
+  // dtype combinations the kernels are instantiated for (checked again at dispatch)
+  const bool bf_or_f32 = (dtype_v == HATTN_BF16 || dtype_v == HATTN_FP32) &&
+                         (dtype_l == HATTN_BF16 || dtype_l == HATTN_FP32) &&
+                         (dtype_o == HATTN_BF16 || dtype_o == HATTN_FP32);
+  if (x3 ? !(dtype_v == HATTN_FP32 && dtype_l == HATTN_FP32 && dtype_o == HATTN_FP32) : !bf_or_f32)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k=%d v=%d l=%d o=%d%s", dtype_qk,
+                dtype_v, dtype_l, dtype_o, x3 ? " (fp32 q/k need fp32 v, lambda and o)" : "");
+  if (int st = check_span(T, max_of({(size_t)G * K * elem_bytes(dtype_qk),
+                                      (size_t)H * V * elem_bytes(dtype_v),
+                                      (size_t)H * V * elem_bytes(dtype_o),
+                                      (size_t)H * L * elem_bytes(dtype_l), (size_t)H * 4})))
+    return st;
   if (!q || !k || !v || !g || !l || !o) return fail(HATTN_ERR_VALUE, "null tensor pointer");
   const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, V, x3);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
@@ -218,6 +251,11 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
   if (dtype_qk != HATTN_BF16 || dtype_do != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 required)", dtype_qk,
                 dtype_do);
+  if (int st = check_span(T, max_of({(size_t)H * K * elem_bytes(dtype_qk),
+                                      (size_t)H * V * elem_bytes(dtype_v),
+                                      (size_t)H * V * elem_bytes(dtype_do),
+                                      (size_t)H * L * 4, (size_t)H * 4})))
+    return st;
   if (!q || !k || !v || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !dg || !dl)
     return fail(HATTN_ERR_VALUE, "null tensor pointer");
   const size_t need = hattn_mamba2_bwd_ws_bytes(B, T, H, V, nlev);

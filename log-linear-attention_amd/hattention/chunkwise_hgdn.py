@@ -33,6 +33,9 @@ def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
     B, T, G, K = k.shape
     _, _, H, V = v.shape
     L = l.shape[-1]
+    # the kernels read q, k and v with one element type (dtype_qkv)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k and v must share one dtype (got {q.dtype}, {k.dtype}, {v.dtype})")
     if H % G != 0:
         raise ValueError(f"H={H} is not a multiple of G={G}")
     if chunk_size != CHUNK:

@@ -89,6 +89,23 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
 size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, int V, int L);
 
 /*
+ * Log-linear Mamba-2 chunkwise forward that allocates nothing and takes no
+ * workspace.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and status codes
+ * as hattn_mamba2_chunkwise_fwd without the workspace pair; its scratch is a
+ * file-scope static device array of 64 MiB per GPU (held until the process
+ * ends), so sizes whose hattn_mamba2_chunkwise_fwd_workspace(...) exceeds
+ * 64 MiB return HATTN_ERR_VALUE.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (concurrent streams or threads) race.
+ */
+int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void* v,
+                                       const float* g, const void* l, void* o, float* g_cumsum,
+                                       float* ht, int B, int T, int G, int H, int K, int V, int L,
+                                       int dtype_qk, int dtype_v, int dtype_l, int dtype_o,
+                                       int level_base, int htype, int chunk_size, void* stream);
+
+/*
  * Log-linear Mamba-2 chunkwise backward.
  *
  * Replaces hattention/chunkwise.py:1286-1597 `chunkwise_bwd(q, k, v, g, l, do,

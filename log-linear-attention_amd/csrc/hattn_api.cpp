@@ -20,6 +20,8 @@ hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, 
                                    int dt_v, int dt_l, int dt_o, hipStream_t stream,
                                    int* unsupported);
 size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3);
+size_t hattn_mamba2_fwd_static_scratch_bytes();
+hipError_t hattn_mamba2_fwd_static_scratch(void** ptr);
 int hattn_mamba2_fwd_max_levels(int x3);
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V);
 int hattn_gdn_fwd_max_levels();
@@ -214,6 +216,30 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k=%d v=%d l=%d o=%d%s", dtype_qk,
                 dtype_v, dtype_l, dtype_o, x3 ? " (fp32 q/k need fp32 v, lambda and o)" : "");
   return check_hip(e, "hattn_mamba2_chunkwise_fwd launch");
+}
+
+int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void* v,
+                                       const float* g, const void* l, void* o, float* g_cumsum,
+                                       float* ht, int B, int T, int G, int H, int K, int V, int L,
+                                       int dtype_qk, int dtype_v, int dtype_l, int dtype_o,
+                                       int level_base, int htype, int chunk_size, void* stream) {
+  // the shape checks of the allocating entry point come first, so a bad shape
+  // reports the same status; then the workspace must fit the static scratch
+  const size_t need = hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, K, V, L);
+  const size_t cap = hattn_mamba2_fwd_static_scratch_bytes();
+  if (B > 0 && T >= 64 && T % 64 == 0 && H > 0 && V > 0 && need > cap)
+    return fail(HATTN_ERR_VALUE,
+                "these sizes need %zu bytes of scratch, above the %zu-byte static scratch of "
+                "hattn_mamba2_chunkwise_fwd_noalloc (use hattn_mamba2_chunkwise_fwd)",
+                need, cap);
+  void* ws = nullptr;
+  if (need > 0) {
+    const hipError_t e = hattn_mamba2_fwd_static_scratch(&ws);
+    if (e != hipSuccess) return check_hip(e, "static scratch address (hipGetSymbolAddress)");
+  }
+  return hattn_mamba2_chunkwise_fwd(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, K, V, L, dtype_qk,
+                                    dtype_v, dtype_l, dtype_o, level_base, htype, chunk_size, ws,
+                                    need > 0 ? cap : 0, stream);
 }
 
 size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L) {

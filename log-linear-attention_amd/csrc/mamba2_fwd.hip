@@ -35,6 +35,8 @@
 // the Q fragments (any bijection of the contraction index works if both
 // operands use it).  K^T and V fragments of the contractions over t come from
 // row-major LDS tiles through the transposing LDS read.
+#include <mutex>
+
 #include "mamba2_common.h"
 
 namespace hattn {
@@ -1155,6 +1157,42 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
 
 size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3) {
   return fwd_ws_layout(nullptr, B, T, H, V, x3).bytes;
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of the no-allocation forward entry point
+// ---------------------------------------------------------------------------
+// A file-scope device array that replaces the caller's workspace for callers
+// that cannot allocate.  Each GPU holds its own copy (at its own address) until
+// the process ends; every call on a GPU shares it, so calls that overlap on one
+// GPU race.  Host code never uses the array's name as an address: the device
+// address comes from hipGetSymbolAddress, looked up once per device.
+namespace {
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+size_t hattn_mamba2_fwd_static_scratch_bytes() { return kStaticScratchBytes; }
+
+// Device address of the current device's static scratch (looked up on the
+// first call on that device, with the device current).
+hipError_t hattn_mamba2_fwd_static_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 // Largest inter-chunk level count: register-resident local levels plus the

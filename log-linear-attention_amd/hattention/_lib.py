@@ -25,6 +25,8 @@ SIGNATURES = [
     ("hattn_mamba2_chunkwise_fwd", _I,
      [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P, _S, _P]),
     ("hattn_mamba2_chunkwise_fwd_workspace", _S, [_I] * 7),
+    ("hattn_mamba2_chunkwise_fwd_noalloc", _I,
+     [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P]),
     ("hattn_mamba2_chunkwise_bwd", _I,
      [_P, _P, _P, _F, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
      + [_P, _S, _P]),

@@ -7,7 +7,7 @@ One step = one log-linear Mamba-2 chunkwise forward (``hattention_kernel``,
 HStruct.MAMBA2, the fused HIP kernels) over one batch of synthetic inputs at
 the BASELINE north-star shape B=4, T=16384, H=16, dk=dv=64, L=15, bf16
 q/k/v/lambda, fp32 g, inputs resident in HBM.  Each step first evicts the
-256 MB memory-side cache (a 1 GiB fill, outside the timed events), then runs
+256 MB memory-side cache (a 1 GiB read, outside the timed events), then runs
 the forward between HIP events on the launch stream; ``value`` and the
 roofline use the median step, the back-to-back (warm)
 figures are kept under ``timing``.  Prints one JSON line with the throughput
@@ -141,16 +141,18 @@ def _median(xs):
 
 
 class Evictor:
-    """A 1 GiB buffer written before each timed rep: four times the 256 MB
-    memory-side cache (MALL), so no line of the previous rep survives."""
+    """A 1 GiB buffer read before each timed rep: four times the 256 MB
+    memory-side cache (MALL), so no line of the previous rep survives.  A read
+    (a reduction into one value) leaves only clean lines behind; a write fill
+    would leave 256 MB of dirty lines whose write-back then lands inside the
+    timed rep."""
 
     def __init__(self, dev):
-        self.buf = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)
-        self.n = 0
+        self.buf = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+        self.out = torch.empty((), dtype=torch.float32, device=dev)
 
     def __call__(self):
-        self.n += 1
-        self.buf.fill_(float(self.n))
+        torch.sum(self.buf, (0,), out=self.out)
 
 
 def time_cold(fn, reps, stream, evict):
@@ -606,9 +608,10 @@ def main():
                                "MAMBA2, WEAK, base 2, chunk 64)",
                    "batch": B, "seq_len": T, "heads": H, "dk": K, "dv": V, "levels": L,
                    "dtype_qkv_lambda": "bf16", "dtype_g": "fp32"},
-        "timing": {"protocol": "per step: 1 GiB fill evicts the 256 MB memory-side cache "
-                               "(outside the events), then one forward between HIP events on "
-                               "the launch stream; value and ms_per_step use the median",
+        "timing": {"protocol": "per step: a 1 GiB read (a reduction) evicts the 256 MB "
+                               "memory-side cache (outside the events), then one forward "
+                               "between HIP events on the launch stream; value and "
+                               "ms_per_step use the median",
                    "cold_median_us": t_med * 1e6, "cold_min_us": min(cold) * 1e6,
                    "cold_max_us": max(cold) * 1e6,
                    "wall_ms_per_step_incl_evict": wall / args.steps * 1e3,

@@ -121,19 +121,26 @@ struct SumSmem {
 // fragment (16 k rows), so the V fragments enter the MFMA as staged.  Two
 // chunks wait in registers while one is multiplied from LDS, so every load has
 // two chunk iterations to land.
-template <typename TK, typename TV, bool GCUM, int NP>
-__global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
-    const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
-    float* __restrict__ sums, float* __restrict__ segd, int B, int T, int G, int H, int V,
-    int NT, int S, int NSEG, int nvb64) {
-  __shared__ __attribute__((aligned(16))) SumSmem<NP> sm;
+// Cache-policy bits of the buffer accesses that other workgroups of the same
+// launch read or write (the fused forward's segment summaries and flags):
+// sc1 makes the access coherent across the XCDs' L2 caches, sc0 also skips
+// the CU's L1.  Every such access carries them, so no cache write-back or
+// invalidate is needed.
+constexpr int kCohLoad = 17;   // sc0 | sc1
+constexpr int kCohStore = 16;  // sc1
+
+// Body of the summary pass over segment p of one (row, 64-column block of V):
+// writes Sum(p) into out (row-major [K][V] with row stride V, this block's 64
+// columns) and returns D_p (on every thread).  COH: the stores carry kCohStore.
+template <typename TK, typename TV, bool GCUM, int NP, bool COH>
+__device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restrict__ k,
+                                              const TV* __restrict__ v,
+                                              const float* __restrict__ g, float* __restrict__ out,
+                                              int b, int h, int p, int vblk, int T, int G, int H,
+                                              int V, int NT, int S) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  // grid: xcd_head_grid(B * NSEG, H, nvb64); the heads of one (batch, segment) share an XCD
-  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
-  if (xm.grp >= B * NSEG) return;
-  const int vblk = xm.slice, h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
-  const int row = b * H + h, gq = h / (H / G);
+  const int gq = h / (H / G);
   const int c0 = p * S;
   const int nch = min(S, NT - c0);
   const int vcol0 = vblk * 64;
@@ -228,12 +235,40 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
     step(j, 0, 1);
     if (j + 1 < nch) step(j + 1, 1, 0);
   }
-  float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
+  if constexpr (COH) {
+    // relaxed device-scope atomic stores: plain stores with the sc1 bit.  (The
+    // raw-buffer-store builtin fed acc[n][i] here compiled to four stores of
+    // acc[n][0] with hipcc 7.2 inside the fused forward kernel.)
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[(size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln] = acc[n][i];
-  if (tid == 0 && vblk == 0) segd[(size_t)row * NSEG + p] = dsum;
+      for (int i = 0; i < 4; ++i)
+        __hip_atomic_store(out + (size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln, acc[n][i],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[(size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln] = acc[n][i];
+  }
+  return dsum;
+}
+
+template <typename TK, typename TV, bool GCUM, int NP>
+__global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
+    const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
+    float* __restrict__ sums, float* __restrict__ segd, int B, int T, int G, int H, int V,
+    int NT, int S, int NSEG, int nvb64) {
+  __shared__ __attribute__((aligned(16))) SumSmem<NP> sm;
+  // grid: xcd_head_grid(B * NSEG, H, nvb64); the heads of one (batch, segment) share an XCD
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
+  if (xm.grp >= B * NSEG) return;
+  const int vblk = xm.slice, h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
+  const int row = b * H + h;
+  float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vblk * 64;
+  const float dsum = seg_sum_body<TK, TV, GCUM, NP, false>(sm, k, v, g, out, b, h, p, vblk, T, G,
+                                                          H, V, NT, S);
+  if (threadIdx.x == 0 && vblk == 0) segd[(size_t)row * NSEG + p] = dsum;
 }
 
 // ---------------------------------------------------------------------------

@@ -722,12 +722,30 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const f
   }
 }
 
-template <typename TV, typename TL, typename TO>
+// FUSED: one launch computes everything (single pass).  Work items (batch,
+// segment, head, V block) are handed out in that order by a ticket counter, so
+// a workgroup only ever waits for work that a running workgroup has already
+// claimed.  Phase A streams the segment's K, V, g and publishes Sum(p) and D_p
+// (coherent stores, then a flag); the workgroup then waits for the flags of
+// the earlier segments of its row and builds its top-level states from their
+// summaries (coherent loads).  The walk re-reads K and V shortly after phase A,
+// from the L2 / memory-side cache.  Not FUSED: the summaries come from
+// mamba2_seg_sum_kernel (or there is a single segment and none are needed).
+// sync: [0] ticket counter, [1 ..] one flag per (row, V block, segment); zeroed
+// by mamba2_fwd_sync_init_kernel before the launch.
+constexpr int kSpinLimit = 1 << 24;   // ~1 s of polling: a lost flag ends the wait, never hangs
+
+__global__ void mamba2_fwd_sync_init_kernel(unsigned int* __restrict__ sync, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) sync[i] = 0u;
+}
+
+template <typename TV, typename TL, typename TO, bool FUSED>
 __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
-    float* __restrict__ gcum, float* __restrict__ ht, const float* __restrict__ sums,
-    const float* __restrict__ segd, int B, int T, int G, int H,
+    float* __restrict__ gcum, float* __restrict__ ht, float* __restrict__ sums,
+    float* __restrict__ segd, unsigned int* __restrict__ sync, int B, int T, int G, int H,
     int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state) {
   constexpr int kPl = kKD * 64;                           // one top-level state tile
   constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
@@ -735,11 +753,29 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   Bf16Smem& sm = *(Bf16Smem*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq0 = lane >> 4, ln0 = lane & 15;
-  // grid: xcd_head_grid(B * NSEG, H, nvb64)
-  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
-  if (xm.grp >= B * NSEG) return;
-  const int h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
-  const int row = b * H + h, vblk = xm.slice;
+  int h, p, b, vblk;
+  if constexpr (FUSED) {
+    __shared__ int ticket;
+    if (tid == 0)
+      ticket = (int)__hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    int r = ticket;   // (batch, segment, head, V block), V block fastest
+    vblk = r % nvb64;
+    r /= nvb64;
+    h = r % H;
+    r /= H;
+    p = r % NSEG;
+    b = r / NSEG;
+  } else {
+    // grid: xcd_head_grid(B * NSEG, H, nvb64)
+    const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
+    if (xm.grp >= B * NSEG) return;
+    h = xm.h;
+    p = xm.grp % NSEG;
+    b = xm.grp / NSEG;
+    vblk = xm.slice;
+  }
+  const int row = b * H + h;
   const int gq = h / (H / G);
   const int NT = T / kBT;
   const int c0 = p << slog;
@@ -750,6 +786,59 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const int vcol0 = vblk * 64;
   const bool is_final_seg = final_state && ht != nullptr && p == NSEG - 1;
   float* htb = ht ? ht + ((size_t)b * H + h) * kKD * V * L : nullptr;
+  // this row's summaries ([segment][K][V], fp32) and segment log-decays
+  const float* srow = sums + (size_t)row * NSEG * kKD * V;
+  const float* drow = FUSED ? segd + ((size_t)row * nvb64 + vblk) * NSEG : segd + (size_t)row * NSEG;
+  const rsrc_t rsum = make_rsrc(srow, (size_t)NSEG * kKD * V * 4);
+  const rsrc_t rsd = make_rsrc(drow, (size_t)NSEG * 4);
+  // summary reads: coherent when another workgroup of this launch wrote them
+  auto sum4 = [&](size_t el) -> floatx4 {
+    if constexpr (FUSED)
+      return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsum, (unsigned int)(el * 4), 0, kCohLoad));
+    else
+      return *(const floatx4*)(srow + el);
+  };
+  auto sum1 = [&](size_t el) -> float {
+    if constexpr (FUSED)
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsum, (unsigned int)(el * 4), 0, kCohLoad));
+    else
+      return srow[el];
+  };
+  auto segd1 = [&](int qq) -> float {
+    if constexpr (FUSED)
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsd, (unsigned int)qq * 4, 0, kCohLoad));
+    else
+      return drow[qq];
+  };
+
+  if constexpr (FUSED) {
+    // ---- phase A: Sum(p), D_p for the later segments (and this one's final states) ----
+    if (p < NSEG - 1 || is_final_seg) {
+      SumSmem<1>& ss = *(SumSmem<1>*)smem_raw;
+      float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
+      const float dsum = seg_sum_body<__bf16, TV, false, 1, true>(ss, k, v, g, out, b, h, p, vblk,
+                                                                  T, G, H, V, NT, 1 << slog);
+      if (tid == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, dsum), rsd,
+                                              (unsigned int)p * 4, 0, kCohStore);
+      __builtin_amdgcn_s_waitcnt(0);   // this thread's summary stores are complete
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + p, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // ---- look-back: the earlier segments of this row have published ----
+    if (p > 0) {
+      if (tid < p) {
+        const unsigned int* f = sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + tid;
+        int spins = 0;
+        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
+               ++spins < kSpinLimit)
+          __builtin_amdgcn_s_sleep(2);
+      }
+      __syncthreads();
+    }
+  }
 
   // ---- top levels: Htop_e(p) for the levels segment p reads -> LDS (bf16, [v][k]) ----
   // Htop_e(p) = sum_{q in block} exp(P[p] - P[q + 1]) Sum(q), block = the 2^e
@@ -759,12 +848,11 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   // by the segment-summary kernel and are read from L2 / MALL.
   if (ntop > 0 && (p > 0 || is_final_seg)) {
     float* pre = (float*)sm.a;   // P[0 .. p + 1]; the A tile is free until the first chunk
-    const float* dp = segd + (size_t)row * NSEG;
     if (w == 0) {
       float carry = 0.f;
       for (int base = 0; base <= p + 1; base += 64) {
         const int qq = base + lane;
-        const float x = qq <= p ? dp[qq] : 0.f;
+        const float x = qq <= p ? segd1(qq) : 0.f;
         const float y = chunk_cumsum(x);
         if (qq <= p + 1) pre[qq] = carry + y - x;
         carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 63));
@@ -773,7 +861,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     __syncthreads();
     // thread: V columns 4 (tid & 15) .. + 3, k rows (tid >> 4) + 16 i
     const int v4 = 4 * (tid & 15), kr = tid >> 4;
-    const float* sp = sums + (size_t)row * NSEG * kKD * V + (size_t)kr * V + vcol0 + v4;
+    const size_t sp = (size_t)kr * V + vcol0 + v4;   // element offset in the row's summaries
     const size_t qstride = (size_t)kKD * V;
     const float pp = pre[p];
     for (int e2 = 0; e2 < ntop && p > 0; ++e2) {
@@ -788,7 +876,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           const int qs = min(q0 + u, lo + (1 << e2) - 1);
           sc[u] = q0 + u < lo + (1 << e2) ? fexp(pp - pre[qs + 1]) : 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) xs[u][i] = *(const floatx4*)(sp + qs * qstride + (size_t)16 * i * V);
+          for (int i = 0; i < 4; ++i) xs[u][i] = sum4(sp + qs * qstride + (size_t)16 * i * V);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
@@ -807,7 +895,6 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       // chunk reads holds its block decayed over segment p; one it writes holds
       // segments [lo, p] decayed to the end of p
       const int vc = vcol0 + 16 * w + ln0;
-      const float* spf = sums + (size_t)row * NSEG * kKD * V + vc;
       for (int e2 = 0; e2 < ntop; ++e2) {
         const bool reads = (p >> e2) & 1;
         const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
@@ -817,11 +904,11 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         for (int m = 0; m < 4; ++m) hacc[m] = zero4();
         for (int qs = lo; qs < hi; ++qs) {
           const float sc = fexp(pre[p + 1] - pre[qs + 1]);
-          const float* src = spf + qs * qstride;
+          const size_t src = qs * qstride + vc;
 #pragma unroll
           for (int m = 0; m < 4; ++m)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) hacc[m][i] += sc * src[(size_t)(16 * m + 4 * lq0 + i) * V];
+            for (int i = 0; i < 4; ++i) hacc[m][i] += sc * sum1(src + (size_t)(16 * m + 4 * lq0 + i) * V);
         }
 #pragma unroll
         for (int m = 0; m < 4; ++m)
@@ -1128,9 +1215,14 @@ struct FwdWs {
   float* segd;
   float* sums;
   __bf16* htop;
+  unsigned int* sync;   // fused bf16 forward: ticket counter + one flag per (row, V block, segment)
+  int nsync;
   size_t bytes;
 };
 
+// x3 (bf16x3 kernels): segment log-decays per row, summaries, staged top-level
+// states.  bf16 (fused single pass): log-decays per (row, V block), summaries,
+// the ticket counter and flags.
 FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   const int NT = T / hattn::kBT;
   const int slog = hattn::seg_log2(NT, max_loc(x3));
@@ -1138,11 +1230,12 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   int nlev = 0;
   while ((1 << nlev) < NT) ++nlev;
   const int ntop = nlev - (slog < nlev ? slog : nlev);
-  FwdWs w{nullptr, nullptr, nullptr, 0};
+  FwdWs w{nullptr, nullptr, nullptr, nullptr, 0, 0};
   if (NSEG <= 1) return w;
   const size_t rows = (size_t)B * H;
+  const int nvb = V / 64;
   char* p = (char*)base;
-  const size_t a = segd_bytes(rows, NSEG);
+  const size_t a = segd_bytes(x3 ? rows : rows * nvb, NSEG);
   const size_t b = (rows * NSEG * hattn::kKD * V * sizeof(float) + 255) & ~(size_t)255;
   // top-level states are staged by the scan kernel only for the bf16x3 kernels;
   // the bf16 main kernel builds them from the summaries itself
@@ -1151,6 +1244,11 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   w.sums = (float*)(p + a);
   w.htop = (__bf16*)(p + a + b);
   w.bytes = a + b + c;
+  if (!x3) {
+    w.nsync = 1 + (int)(rows * nvb * NSEG);
+    w.sync = (unsigned int*)(p + a + b);
+    w.bytes = a + b + (((size_t)w.nsync * 4 + 255) & ~(size_t)255);
+  }
   return w;
 }
 }  // namespace
@@ -1220,6 +1318,33 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
   const int nvb64 = V / 64;
   const FwdWs w = fwd_ws_layout(ws, B, T, H, V, NP == 2);
   const int ntop = nlev - min(slog, nlev);
+  if constexpr (NP == 1) {
+    // bf16: one fused single-pass launch (plus the flag reset) when there is
+    // more than one segment, else the plain walk
+    const int smem = bf16_smem_bytes(ntop);
+    hipError_t e;
+    if (NSEG > 1) {
+      hipLaunchKernelGGL(mamba2_fwd_sync_init_kernel, dim3((w.nsync + 255) / 256), dim3(256), 0,
+                         stream, w.sync, w.nsync);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true>;
+      e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3(B * NSEG * H * nvb64), dim3(256), smem, stream,
+                         (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
+                         gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog,
+                         NSEG, ht != nullptr ? 1 : 0);
+      return hipGetLastError();
+    }
+    auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, false>;
+    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
+                       (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
+                       gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
+                       ht != nullptr ? 1 : 0);
+    return hipGetLastError();
+  }
   if (NSEG > 1) {
     auto sk = mamba2_seg_sum_kernel<TK, TV, false, NP>;
     hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), 0, stream,
@@ -1235,17 +1360,6 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
     }
   }
   const int grid = xcd_head_grid(B * NSEG, H, nvb64);
-  if constexpr (NP == 1) {
-    const int smem = bf16_smem_bytes(ntop);
-    auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO>;
-    hipError_t e =
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, (const __bf16*)q,
-                       (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, w.sums,
-                       w.segd, B, T, G, H, V, L, nlev, nvb64, slog, NSEG, ht != nullptr ? 1 : 0);
-    return hipGetLastError();
-  }
   const int smem = main_smem_bytes<NP, MAXLOC>(ntop);
   auto kern = mamba2_fwd_main_kernel<TK, TV, TL, TO, NP, MAXLOC>;
   hipError_t e =

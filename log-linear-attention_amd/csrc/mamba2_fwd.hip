@@ -924,7 +924,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const rsrc_t rq = make_rsrc(q + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
   const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * qstr * 2);
   const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
-  const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
+  // g is read by wave 0 only: the other waves issue the same load through an
+  // empty range, which returns zeros without a memory request
+  const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, w == 0 ? (size_t)T * H * 4 : 0);
   const rsrc_t ro = make_rsrc(o + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TO));
   const bool write_gcum = gcum != nullptr && vblk == 0;
   const rsrc_t rgc = make_rsrc(write_gcum ? (const void*)(gcum + (size_t)b * T * H + h) : (const void*)g,
@@ -943,7 +945,11 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   constexpr int kPE = kL16 ? 8 : 4;   // lambda columns per 16-byte piece
   const char* lbase = (const char*)(l + (size_t)b * T * H * L);
   const unsigned int lbmis = (unsigned int)((uintptr_t)lbase & 3);   // descriptor base aligned down
-  const rsrc_t rlb = make_rsrc(lbase - lbmis, (size_t)T * H * L * sizeof(TL) + lbmis);
+  // lambda is read by waves 1 .. 3 only (wave 0's range is empty, as for g);
+  // bf16 rows of at most 15 used columns fit in pieces 0 and 1 whatever their
+  // misalignment, so then wave 3 (piece 2) reads nothing either
+  const bool lam_reader = w > 0 && !(kL16 && w == 3 && lu + 1 <= 2 * kPE);
+  const rsrc_t rlb = make_rsrc(lbase - lbmis, lam_reader ? (size_t)T * H * L * sizeof(TL) + lbmis : 0);
   const unsigned int lrow_b = lbmis + (unsigned int)((lane * H + h) * L) * sizeof(TL);
   const int lmis = kL16 ? (int)((lrow_b >> 1) & 1) : 0;
   const unsigned int vo_l = lrow_b & ~3u;
@@ -966,7 +972,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       // their lambda pieces; a piece past the row reads bytes of the next row, or
       // zeros past the buffer end, and is not used): a load assigned on some waves
       // only makes the compiler merge registers after the branch with copies that
-      // wait for the load, i.e. a full memory round trip per chunk
+      // wait for the load, i.e. a full memory round trip per chunk.  The unused
+      // load of a wave goes through an empty range, so it makes no request.
       rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
       const unsigned int so_l = row0 * lstr * sizeof(TL);
 #pragma unroll

@@ -19,6 +19,7 @@ from hattention import _lib
 from hattention.base import HType, get_num_levels, ceil_log
 
 CHUNK = 64
+KB = 64   # key / value dimensions per kernel launch
 
 
 def _assert_contiguous(**tensors):
@@ -63,6 +64,23 @@ def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
         raise ValueError(f"L={L} levels are too few for T={T}")
 
 
+def _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht, o_dtype):
+    """One launch of hattn_mamba2_chunkwise_fwd (K = 64): returns (o, g_cumsum)."""
+    dev = q.device
+    o = torch.empty(v.shape, dtype=o_dtype, device=dev)
+    g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, KB, V, L), dev)
+    st = lib.hattn_mamba2_chunkwise_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o),
+        _lib.ptr(g_cumsum), _lib.ptr(ht), B, T, G, H, KB, V, L,
+        _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
+        level_base, htype.value, chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
+    _lib.check(st)
+    return o, g_cumsum
+
+
 def chunkwise_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -85,6 +103,11 @@ def chunkwise_fwd(
     [B,T,H] fp32 and, if ``output_final_state``, ``ht`` [B,H,K,V,L] fp32 holding
     the inter-chunk level states at levels 7 .. 6 + ceil(log2(T/64)) (other
     levels zero), like the reference.
+
+    The kernels contract over 64 key dimensions.  A larger K (a multiple of 64)
+    runs one launch per 64-wide block of q and k: the output is linear in that
+    split (o = sum over blocks of the blocks' outputs, accumulated in fp32), and
+    block i of the final states is the states' rows 64 i .. 64 i + 63.
     """
     _assert_contiguous(q=q, k=k, v=v, g=g, l=l)
     B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
@@ -101,21 +124,45 @@ def chunkwise_fwd(
         # fp32 q / k run the bf16x3 (fp32-accurate) kernels, which read fp32 v
         # and lambda and write fp32 o
         v, l = v.float().contiguous(), l.float().contiguous()
-    o = torch.empty(v.shape, dtype=v.dtype, device=dev)
-    g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
     ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
-    lib = _lib.load()
-    ws, ws_ptr, ws_bytes = _lib.workspace(
-        lib.hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, K, V, L), dev)
-    st = lib.hattn_mamba2_chunkwise_fwd(
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o),
-        _lib.ptr(g_cumsum), _lib.ptr(ht), B, T, G, H, K, V, L,
-        _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
-        level_base, htype.value, chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
-    _lib.check(st)
+    if K == KB:
+        o, g_cumsum = _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht,
+                                v.dtype)
+    else:
+        o = None
+        for i in range(K // KB):
+            blk = slice(KB * i, KB * (i + 1))
+            hti = torch.zeros(B, H, KB, V, L, dtype=torch.float32, device=dev) if ht is not None else None
+            oi, g_cumsum = _fwd_call(q[..., blk].contiguous(), k[..., blk].contiguous(), v, g, l,
+                                     B, T, G, H, V, L, level_base, htype, chunk_size, hti,
+                                     torch.float32)
+            o = oi if o is None else o.add_(oi)
+            if ht is not None:
+                ht[:, :, blk] = hti
     if o.dtype != out_dtype:
         o = o.to(out_dtype)
     return o, g_cumsum, ht
+
+
+def _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype, chunk_size):
+    """One launch of hattn_mamba2_chunkwise_bwd (K = V = 64, per-head q / k)."""
+    dev = q.device
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, KB, V, L), dev)
+    st = lib.hattn_mamba2_chunkwise_bwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
+        _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
+        B, T, H, KB, V, L, _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l),
+        _lib.dtype_code(do), level_base, htype.value, chunk_size, ws_ptr, ws_bytes,
+        _lib.stream_handle(dev))
+    _lib.check(st)
+    return dq, dk, dv, dg, dl
 
 
 def chunkwise_bwd(
@@ -137,6 +184,12 @@ def chunkwise_bwd(
     dg (w.r.t. the raw per-step g) and dl in fp32, like the reference.  Grouped
     q / k are expanded per head before the kernels and their gradients summed
     over the group afterwards (chunkwise.py:1360-1362, 1583-1594).
+
+    The kernels take 64 key and 64 value dimensions.  Larger K and V (multiples
+    of 64) run one launch per (key block, value block): with
+    o_t = sum_s M[t,s] (q_t . k_s) v_s every gradient is a sum over those
+    blocks (dq and dk of a key block sum over the value blocks, dv of a value
+    block over the key blocks, dg and dlambda over all), accumulated in fp32.
     """
     _assert_contiguous(q=q, k=k, v=v, g=g, l=l, do=do)
     B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
@@ -145,26 +198,35 @@ def chunkwise_bwd(
         raise ValueError("g must be the fp32 chunk-local cumsum [B, T, H]")
     if do.shape != v.shape:
         raise ValueError("do must have the shape of v")
-    dev = _lib.require_device(q, k, v, g, l, do)
+    _lib.require_device(q, k, v, g, l, do)
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
     do = do.to(q.dtype).contiguous()
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
-    dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
-    lib = _lib.load()
-    ws, ws_ptr, ws_bytes = _lib.workspace(
-        lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, K, V, L), dev)
-    st = lib.hattn_mamba2_chunkwise_bwd(
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
-        _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
-        B, T, H, K, V, L, _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l),
-        _lib.dtype_code(do), level_base, htype.value, chunk_size, ws_ptr, ws_bytes,
-        _lib.stream_handle(dev))
-    _lib.check(st)
+    if K == KB and V == KB:
+        dq, dk, dv, dg, dl = _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype,
+                                       chunk_size)
+    else:
+        f32 = dict(dtype=torch.float32, device=q.device)
+        dq = torch.zeros(B, T, H, K, **f32)
+        dk = torch.zeros(B, T, H, K, **f32)
+        dv = torch.zeros(B, T, H, V, **f32)
+        dg = torch.zeros(B, T, H, **f32)
+        dl = torch.zeros(B, T, H, L, **f32)
+        kblocks = [slice(KB * i, KB * (i + 1)) for i in range(K // KB)]
+        vblocks = [slice(KB * i, KB * (i + 1)) for i in range(V // KB)]
+        vb = [(v[..., c].contiguous(), do[..., c].contiguous()) for c in vblocks]
+        for kc in kblocks:
+            qk = (q[..., kc].contiguous(), k[..., kc].contiguous())
+            for c, (vc, doc) in zip(vblocks, vb):
+                r = _bwd_call(qk[0], qk[1], vc, g, l, doc, B, T, H, KB, L, level_base, htype,
+                              chunk_size)
+                dq[..., kc] += r[0].float()
+                dk[..., kc] += r[1].float()
+                dv[..., c] += r[2].float()
+                dg += r[3]
+                dl += r[4]
+        dq, dk, dv = dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3)
         dk = dk.view(B, T, G, H // G, K).sum(3)

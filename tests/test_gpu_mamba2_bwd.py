@@ -91,6 +91,13 @@ def test_segments_and_top_levels(T):
     _run(1, T, 2, 64, 64, L, seed=T + 1)
 
 
+@pytest.mark.parametrize("K,V", [(128, 64), (64, 128), (128, 128)])
+def test_head_dims_above_64(K, V):
+    # one launch per (64-wide key block, 64-wide value block); every gradient
+    # is a sum over the blocks
+    _run(1, 2112, 2, K, V, 13, seed=K * 3 + V)
+
+
 def test_fp32_v_and_lambda():
     _run(1, 2048, 2, 64, 64, 12, seed=3, vdtype=torch.float32, ldtype=torch.float32)
 

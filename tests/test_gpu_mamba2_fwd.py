@@ -37,7 +37,15 @@ def _errs(out, ref):
 
 
 def _oracle_rows(q, k, v, g, l, rows, H, G, **kw):
-    """Run the fp64 oracle on selected (b, h) rows at full length."""
+    """Run the fp64 oracle on selected (b, h) rows at full length (rows=None:
+    once on the whole tensor, returned as one entry per row)."""
+    if rows is None:
+        B = q.shape[0]
+        o, gc, ht = chunked_scan_fwd(*(x.double().cpu() for x in (q, k, v, g, l)), chunk_size=64,
+                                     **kw)
+        return [(o[b:b + 1, :, h:h + 1], gc[b:b + 1, :, h:h + 1],
+                 ht[b:b + 1, h:h + 1] if ht is not None else None)
+                for b in range(B) for h in range(H)]
     outs = []
     for (b, h) in rows:
         gq = h // (H // G)
@@ -66,12 +74,13 @@ def _run(B, T, H, K, V, L, G=None, seed=0, dtype=torch.bfloat16, vdtype=None, ld
     assert o.dtype == v.dtype
     x3 = q.dtype == torch.float32
     tmax, tfro = (TOL_X3, TOL_X3) if x3 else (TOL_MAX, TOL_FRO)
+    refs = _oracle_rows(q, k, v, g, l, rows, H, G, output_final_state=final_state)
     if rows is None:
         rows = [(b, h) for b in range(B) for h in range(H)]
-    refs = _oracle_rows(q, k, v, g, l, rows, H, G, output_final_state=final_state)
     for (b, h), (o_ref, gc_ref, ht_ref) in zip(rows, refs):
         mx, fro = _errs(o[b:b + 1, :, h:h + 1], o_ref)
-        print(f"  row ({b},{h}): max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        if len(rows) <= 8:
+            print(f"  row ({b},{h}): max-rel {mx:.2e} fro {fro:.2e}", flush=True)
         assert mx < tmax and fro < tfro, (b, h, mx, fro)
         assert torch.allclose(gc[b:b + 1, :, h:h + 1].cpu().double(), gc_ref, rtol=1e-5,
                               atol=1e-4), (b, h)
@@ -117,13 +126,24 @@ def test_final_state(T):
 
 
 def test_config1_full_size():
-    # B=8 T=4096 H=16 dk=dv=64 L=13 bf16
-    _run(8, 4096, 16, 64, 64, 13, seed=1001, rows=[(0, 0), (3, 7), (7, 15)])
+    # B=8 T=4096 H=16 dk=dv=64 L=13 bf16, every (batch, head) row
+    _run(8, 4096, 16, 64, 64, 13, seed=1001)
 
 
 def test_north_star_full_size():
-    # B=4 T=16384 H=16 dk=dv=64 L=15 bf16
-    _run(4, 16384, 16, 64, 64, 15, seed=1000, rows=[(0, 0), (2, 9), (3, 15)])
+    # B=4 T=16384 H=16 dk=dv=64 L=15 bf16, every (batch, head) row
+    _run(4, 16384, 16, 64, 64, 15, seed=1000)
+
+
+@pytest.mark.parametrize("K,V", [(128, 64), (128, 128), (192, 64)])
+def test_head_dims_above_64(K, V):
+    # K > 64 runs one launch per 64-wide key block (the output is linear in the
+    # split); several segments, top levels and the final states
+    _run(1, 2112, 2, K, V, 13, seed=K + V, final_state=True)
+
+
+def test_head_dim_128_bf16x3():
+    _run(1, 1024, 2, 128, 64, 11, seed=5, dtype=torch.float32, final_state=True)
 
 
 def test_config2_long_context():

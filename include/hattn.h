@@ -115,9 +115,9 @@ int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void*
  * kernels, chunkwise.py:1360-1362; the host layer does the same and sums the
  * group's dq / dk afterwards):
  *
- *   q, k, dq, dk [B, T, H, K] bf16      v, dv [B, T, H, V] in dtype_v
+ *   q, k, dq, dk [B, T, H, K] in dtype_qk  v, dv [B, T, H, V] in dtype_v
  *   g_cumsum     [B, T, H] fp32 chunk-local inclusive cumsum (the forward's output)
- *   l            [B, T, H, L] in dtype_l   do [B, T, H, V] bf16
+ *   l            [B, T, H, L] in dtype_l   do [B, T, H, V] in dtype_do (= dtype_qk)
  *   dg           [B, T, H] fp32: gradient w.r.t. the per-step g (what the
  *                reference returns after its reverse chunk-local cumsum)
  *   dl           [B, T, H, L] fp32 (every element written; levels no pair
@@ -125,8 +125,11 @@ int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void*
  *   workspace    >= hattn_mamba2_chunkwise_bwd_workspace(...) bytes
  *
  * Constraints: as the forward (T % 64, L >= 7 + ceil(log2(T/64)), K and V
- * multiples of 64 -> HATTN_ERR_VALUE); K == V == 64, q/k/do bf16, v and l in
- * {BF16, FP32} -> HATTN_ERR_NOT_IMPLEMENTED.
+ * multiples of 64 -> HATTN_ERR_VALUE); K == V == 64 (the Python host layer
+ * runs larger K and V as one call per 64-wide block), q/k/do either all BF16
+ * (bf16 MFMA; v and l in {BF16, FP32}) or all FP32 (bf16x3 kernels,
+ * fp32-accurate; v and l FP32, dq / dk / dv written in fp32)
+ *                                                  -> HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
                                const void* l, const void* do_, void* dq, void* dk, void* dv,

@@ -40,8 +40,8 @@ size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
                                    float* dg, float* dl, void* ws, int B, int T, int H, int V,
-                                   int L, int nlev, int dt_v, int dt_l, hipStream_t stream,
-                                   int* unsupported);
+                                   int L, int nlev, int dt_qk, int dt_v, int dt_l,
+                                   hipStream_t stream, int* unsupported);
 
 hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
                                     const void* v, const void* beta, const float* g,
@@ -274,9 +274,14 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
   if (nlev > hattn_mamba2_fwd_max_levels(0))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
                 hattn_mamba2_fwd_max_levels(0));
-  if (dtype_qk != HATTN_BF16 || dtype_do != HATTN_BF16)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 required)", dtype_qk,
-                dtype_do);
+  // bf16 q / k / dO: bf16 kernels; fp32 q / k / dO: bf16x3 kernels (fp32 v and lambda)
+  if (!((dtype_qk == HATTN_BF16 && dtype_do == HATTN_BF16) ||
+        (dtype_qk == HATTN_FP32 && dtype_do == HATTN_FP32)))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 or fp32, both alike)",
+                dtype_qk, dtype_do);
+  if (dtype_qk == HATTN_FP32 && !(dtype_v == HATTN_FP32 && dtype_l == HATTN_FP32))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "fp32 q/k need fp32 v and lambda (v=%d l=%d)", dtype_v,
+                dtype_l);
   if (int st = check_span(T, max_of({(size_t)H * K * elem_bytes(dtype_qk),
                                       (size_t)H * V * elem_bytes(dtype_v),
                                       (size_t)H * V * elem_bytes(dtype_do),
@@ -290,7 +295,7 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
                 workspace_bytes, need);
   int unsupported = 0;
   hipError_t e = hattn_mamba2_bwd_launch(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl, workspace,
-                                         B, T, H, V, L, nlev, dtype_v, dtype_l,
+                                         B, T, H, V, L, nlev, dtype_qk, dtype_v, dtype_l,
                                          (hipStream_t)stream, &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d", dtype_v, dtype_l);

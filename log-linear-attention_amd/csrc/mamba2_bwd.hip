@@ -38,44 +38,68 @@ namespace hattn {
 // ---------------------------------------------------------------------------
 // staging
 // ---------------------------------------------------------------------------
+// NP bf16 planes per tile: 1 (bf16 q, k, dO: plain bf16 MFMA) or 2 (fp32 q, k,
+// v, dO as bf16x3 hi / lo planes, three MFMAs per product; every intermediate
+// that feeds another product is split the same way).
+template <int NP>
 struct BwdStage {
-  __bf16 q[kBT * kLd];
-  __bf16 k[kBT * kLd];
-  __bf16 v[kBT * kLd];
-  __bf16 d[kBT * kLd];      // dO
+  __bf16 q[NP][kBT * kLd];
+  __bf16 k[NP][kBT * kLd];
+  __bf16 v[NP][kBT * kLd];
+  __bf16 d[NP][kBT * kLd];  // dO
   float gc[kBT];            // chunk-local cumsum Gc (the input g)
   float wt[kBT];            // exp(Gc_last - Gc_t)
   float eg[kBT];            // exp(Gc_t)
   float lam[kMaxLU * kBT];  // lambda^T [level][t]; levels >= 7 pre-multiplied by exp(Gc_t)
 };
 
-// Registers of one chunk in flight (NTHR threads share a 64 x 64 tile).
-template <int NTHR, typename TV, typename TL>
+// Registers of one chunk in flight (NTHR threads share a 64 x 64 tile).  TK:
+// element type of q, k and dO; TV of v.
+template <int NTHR, typename TK, typename TV, typename TL>
 struct BwdRegs {
   static constexpr int NU = 512 / NTHR;  // 16-byte units of a bf16 tile per thread
+  static constexpr int NK = sizeof(TK) == 2 ? NU : 2 * NU;
   static constexpr int NV = sizeof(TV) == 2 ? NU : 2 * NU;
   static constexpr int NL = (kMaxLU + NTHR / 64 - 1) / (NTHR / 64);
-  uint4 q[NU], k[NU], d[NU], v[NV];
+  uint4 q[NK], k[NK], d[NK], v[NV];
   float g;
   TL lam[NL];
 };
 
+// One 16-byte unit of a staged tile: bf16 data as is, fp32 data as NP bf16
+// planes of four elements (row r, column c of a kLd-strided tile).
+template <int NP, typename T>
+__device__ __forceinline__ void stage_unit(const uint4& u, __bf16 (*dst)[kBT * kLd], int off) {
+  if constexpr (sizeof(T) == 2) {
+    *(uint4*)(dst[0] + off) = u;
+  } else {
+    const float* e = (const float*)&u;
+    bf16x4 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hi[j] = (__bf16)e[j];
+      lo[j] = bf16_lo(e[j], hi[j]);
+    }
+    *(bf16x4*)(dst[0] + off) = hi;
+    if constexpr (NP == 2) *(bf16x4*)(dst[NP - 1] + off) = lo;
+  }
+}
+
 // Per-row descriptors and per-lane offsets of the chunk loads.
-template <int NTHR, typename TV, typename TL>
+template <int NTHR, typename TK, typename TV, typename TL>
 struct BwdLoader {
   rsrc_t rq, rk, rv, rd, rg, rl;
   unsigned int vo_qk, vo_v, vo_d, vo_g, vo_l;
   unsigned int qrow, vrow, drow, lrowb;  // bytes per token row
   int lrow, lcol, lu;
 
-  __device__ void init(const __bf16* q, const __bf16* k, const TV* v, const __bf16* dO,
-                       const float* g, const TL* l, int b, int h, int T, int H, int V, int L,
-                       int lu_) {
+  __device__ void init(const TK* q, const TK* k, const TV* v, const TK* dO, const float* g,
+                       const TL* l, int b, int h, int T, int H, int V, int L, int lu_) {
     const int tid = threadIdx.x, lane = tid & 63;
     const size_t rq0 = ((size_t)b * T * H + h);
-    qrow = H * kKD * 2;
+    qrow = H * kKD * sizeof(TK);
     vrow = H * V * sizeof(TV);
-    drow = H * V * 2;
+    drow = H * V * sizeof(TK);
     lrowb = H * L * sizeof(TL);
     rq = make_rsrc(q + rq0 * kKD, (size_t)T * qrow);
     rk = make_rsrc(k + rq0 * kKD, (size_t)T * qrow);
@@ -83,8 +107,13 @@ struct BwdLoader {
     rd = make_rsrc(dO + rq0 * V, (size_t)T * drow);
     rg = make_rsrc(g + rq0, (size_t)T * H * 4);
     rl = make_rsrc(l + rq0 * L, (size_t)T * lrowb);
-    vo_qk = (tid >> 3) * qrow + 16 * (tid & 7);
-    vo_d = (tid >> 3) * drow + 16 * (tid & 7);
+    if constexpr (sizeof(TK) == 2) {
+      vo_qk = (tid >> 3) * qrow + 16 * (tid & 7);
+      vo_d = (tid >> 3) * drow + 16 * (tid & 7);
+    } else {
+      vo_qk = (tid >> 4) * qrow + 16 * (tid & 15);
+      vo_d = (tid >> 4) * drow + 16 * (tid & 15);
+    }
     if constexpr (sizeof(TV) == 2) vo_v = (tid >> 3) * vrow + 16 * (tid & 7);
     else vo_v = (tid >> 4) * vrow + 16 * (tid & 15);
     vo_g = lane * H * 4;
@@ -95,12 +124,13 @@ struct BwdLoader {
     lu = lu_;
   }
 
-  __device__ void load(BwdRegs<NTHR, TV, TL>& r, int chunk) const {
-    using R = BwdRegs<NTHR, TV, TL>;
+  __device__ void load(BwdRegs<NTHR, TK, TV, TL>& r, int chunk) const {
+    using R = BwdRegs<NTHR, TK, TV, TL>;
     const unsigned int t0 = (unsigned int)chunk * kBT;
+    constexpr int RK = sizeof(TK) == 2 ? NTHR / 8 : NTHR / 16;   // rows per q / k / dO load
 #pragma unroll
-    for (int u = 0; u < R::NU; ++u) {
-      const unsigned int row = t0 + u * (NTHR / 8);
+    for (int u = 0; u < R::NK; ++u) {
+      const unsigned int row = t0 + u * RK;
       r.q[u] = buf_load16(rq, vo_qk, row * qrow);
       r.k[u] = buf_load16(rk, vo_qk, row * qrow);
       r.d[u] = buf_load16(rd, vo_d, row * drow);
@@ -110,32 +140,35 @@ struct BwdLoader {
       const unsigned int row = t0 + u * (sizeof(TV) == 2 ? NTHR / 8 : NTHR / 16);
       r.v[u] = buf_load16(rv, vo_v, row * vrow);
     }
-    r.g = buf_load<float>(rg, vo_g, t0 * (qrow / (kKD * 2)) * 4);
+    r.g = buf_load<float>(rg, vo_g, t0 * H_of(qrow) * 4);
 #pragma unroll
     for (int c = 0; c < R::NL; ++c)
       if (lcol + c * (NTHR / 64) < lu)
         r.lam[c] = buf_load<TL>(rl, vo_l, t0 * lrowb + c * (NTHR / 64) * sizeof(TL));
   }
 
-  __device__ void store(const BwdRegs<NTHR, TV, TL>& r, BwdStage& s) const {
-    using R = BwdRegs<NTHR, TV, TL>;
+  // heads per token row, from the q row bytes
+  __device__ static unsigned int H_of(unsigned int qrow_bytes) {
+    return qrow_bytes / (kKD * sizeof(TK));
+  }
+
+  template <int NP>
+  __device__ void store(const BwdRegs<NTHR, TK, TV, TL>& r, BwdStage<NP>& s) const {
+    using R = BwdRegs<NTHR, TK, TV, TL>;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 #pragma unroll
-    for (int u = 0; u < R::NU; ++u) {
-      const int off = ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7);
-      *(uint4*)(s.q + off) = r.q[u];
-      *(uint4*)(s.k + off) = r.k[u];
-      *(uint4*)(s.d + off) = r.d[u];
+    for (int u = 0; u < R::NK; ++u) {
+      const int off = sizeof(TK) == 2 ? ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)
+                                      : ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15);
+      stage_unit<NP, TK>(r.q[u], s.q, off);
+      stage_unit<NP, TK>(r.k[u], s.k, off);
+      stage_unit<NP, TK>(r.d[u], s.d, off);
     }
 #pragma unroll
     for (int u = 0; u < R::NV; ++u) {
-      if constexpr (sizeof(TV) == 2) {
-        *(uint4*)(s.v + ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)) = r.v[u];
-      } else {
-        const float* e = (const float*)&r.v[u];
-        *(bf16x4*)(s.v + ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15)) =
-            bf16x4{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3]};
-      }
+      const int off = sizeof(TV) == 2 ? ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)
+                                      : ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15);
+      stage_unit<NP, TV>(r.v[u], s.v, off);
     }
     const float x = r.g;                       // already the chunk-local cumsum
     const float last = __shfl(x, 63, 64);
@@ -170,8 +203,21 @@ __device__ __forceinline__ int p1_tile8(int w, int n) {   // 8 waves, 2 each
   return tab[w][n];
 }
 
+// Fragment planes of a staged tile at one element offset.
+template <int NP>
+__device__ __forceinline__ void frag8(const __bf16 (*X)[kBT * kLd], int off, bf16x8* f) {
+#pragma unroll
+  for (int pl = 0; pl < NP; ++pl) f[pl] = *(const bf16x8*)(X[pl] + off);
+}
+template <int NP>
+__device__ __forceinline__ void trfrag(const __bf16 (*X)[kBT * kLd], int r0, int c0, bf16x8* f) {
+#pragma unroll
+  for (int pl = 0; pl < NP; ++pl) f[pl] = tr_frag(X[pl], kLd, r0, c0);
+}
+
 // S^T and dP^T tile (s rows 16jt.., t columns 16mt..): D[m = s][n = t].
-__device__ __forceinline__ void st_dpt_tile(const BwdStage& s, int mt, int jt, floatx4& S,
+template <int NP>
+__device__ __forceinline__ void st_dpt_tile(const BwdStage<NP>& s, int mt, int jt, floatx4& S,
                                             floatx4& P) {
   const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
   S = zero4();
@@ -180,9 +226,33 @@ __device__ __forceinline__ void st_dpt_tile(const BwdStage& s, int mt, int jt, f
   for (int c = 0; c < 2; ++c) {
     const int ra = (16 * jt + ln) * kLd + 32 * c + 8 * lq;
     const int rb = (16 * mt + ln) * kLd + 32 * c + 8 * lq;
-    S = mfma16x16x32(*(const bf16x8*)(s.k + ra), *(const bf16x8*)(s.q + rb), S);
-    P = mfma16x16x32(*(const bf16x8*)(s.v + ra), *(const bf16x8*)(s.d + rb), P);
+    bf16x8 a[NP], bq[NP];
+    frag8<NP>(s.k, ra, a);
+    frag8<NP>(s.q, rb, bq);
+    S = mma<NP>(a, bq, S);
+    frag8<NP>(s.v, ra, a);
+    frag8<NP>(s.d, rb, bq);
+    P = mma<NP>(a, bq, P);
   }
+}
+
+// fp32 value of staged element planes
+template <int NP>
+__device__ __forceinline__ float plane_val(const __bf16 (*X)[kBT * kLd], int off) {
+  return NP == 2 ? (float)X[0][off] + (float)X[NP - 1][off] : (float)X[0][off];
+}
+
+// Four fp32 values stored as NP bf16 planes of an intermediate tile.
+template <int NP>
+__device__ __forceinline__ void store_planes4(__bf16 (*X)[kBT * kLd], int off, const float* x) {
+  bf16x4 hi, lo;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = (__bf16)x[i];
+    lo[i] = bf16_lo(x[i], hi[i]);
+  }
+  *(bf16x4*)(X[0] + off) = hi;
+  if constexpr (NP == 2) *(bf16x4*)(X[NP - 1] + off) = lo;
 }
 
 // exp(Gc_t - Gc_s) * [s <= t] and the level of each element of a phase-1 tile.
@@ -190,7 +260,8 @@ struct TileMask {
   float dec[4];
   int lev[4];    // level of the pair (0..6)
 };
-__device__ __forceinline__ TileMask tile_mask(const BwdStage& s, int mt, int jt) {
+template <int NP>
+__device__ __forceinline__ TileMask tile_mask(const BwdStage<NP>& s, int mt, int jt) {
   const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
   TileMask m;
   const int t = 16 * mt + ln;
@@ -219,6 +290,12 @@ __device__ __forceinline__ bf16x8 row_pair(const __bf16* X, int row, int c0) {
   const bf16x4 hi = *(const bf16x4*)(p + 16);
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
+template <int NP>
+__device__ __forceinline__ void row_pairs(const __bf16 (*X)[kBT * kLd], int row, int c0,
+                                          bf16x8* f) {
+#pragma unroll
+  for (int pl = 0; pl < NP; ++pl) f[pl] = row_pair(X[pl], row, c0);
+}
 
 __device__ __forceinline__ bf16x8 scale8(bf16x8 x, floatx4 a, floatx4 b) {
   bf16x8 y;
@@ -229,24 +306,40 @@ __device__ __forceinline__ bf16x8 scale8(bf16x8 x, floatx4 a, floatx4 b) {
   }
   return y;
 }
+// planes x (value hi + lo) scaled elementwise by (a, b), re-split into planes
+template <int NP>
+__device__ __forceinline__ void scale8s(const bf16x8* x, floatx4 a, floatx4 b, bf16x8* y) {
+  if constexpr (NP == 1) {
+    y[0] = scale8(x[0], a, b);
+  } else {
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[i] = ((float)x[0][i] + (float)x[1][i]) * a[i];
+      f[4 + i] = ((float)x[0][4 + i] + (float)x[1][4 + i]) * b[i];
+    }
+    split8<NP>(f, y);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Reverse summaries of the top levels
 // ---------------------------------------------------------------------------
 // One workgroup per (row, segment, group of 4 top levels); wave w owns rows
 // k = 16w.. of R_e.  sig[e][t] = lambda[t, 7 + e] exp(E_i + Gc_t).
+template <int NP>
 struct RsumSmem {
-  __bf16 q[kBT * kLd];
-  __bf16 d[kBT * kLd];
+  __bf16 q[NP][kBT * kLd];
+  __bf16 d[NP][kBT * kLd];
   float sig[4][kBT];
 };
 
-template <typename TL>
+template <int NP, typename TK, typename TL>
 __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ dO, const float* __restrict__ gcin,
+    const TK* __restrict__ q, const TK* __restrict__ dO, const float* __restrict__ gcin,
     const TL* __restrict__ l, float* __restrict__ rsum, int T, int H, int L, int NT, int slog,
     int NSEG, int nloc, int ntop, int ngrp) {
-  __shared__ __attribute__((aligned(16))) RsumSmem sm;
+  __shared__ __attribute__((aligned(16))) RsumSmem<NP> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int grp = blockIdx.x % ngrp;
@@ -257,12 +350,17 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
   const int e0 = 4 * grp;
   const int ne = min(4, ntop - e0);
   const size_t rq0 = (size_t)b * T * H + h;
-  const unsigned int qrow = H * kKD * 2, lrowb = H * L * sizeof(TL);
+  const unsigned int qrow = H * kKD * sizeof(TK), lrowb = H * L * sizeof(TL);
   const rsrc_t rq = make_rsrc(q + rq0 * kKD, (size_t)T * qrow);
   const rsrc_t rd = make_rsrc(dO + rq0 * kKD, (size_t)T * qrow);
   const rsrc_t rg = make_rsrc(gcin + rq0, (size_t)T * H * 4);
   const rsrc_t rl = make_rsrc(l + rq0 * L, (size_t)T * lrowb);
-  const unsigned int vo = (tid >> 3) * qrow + 16 * (tid & 7);
+  constexpr int NK = sizeof(TK) == 2 ? 2 : 4;   // 16-byte units of a tile per thread
+  constexpr int RK = 64 / NK;                    // rows between them
+  const unsigned int vo = sizeof(TK) == 2 ? (tid >> 3) * qrow + 16 * (tid & 7)
+                                          : (tid >> 4) * qrow + 16 * (tid & 15);
+  const int soff = sizeof(TK) == 2 ? (tid >> 3) * kLd + 8 * (tid & 7)
+                                   : (tid >> 4) * kLd + 4 * (tid & 15);
   const int lt = tid >> 2, le = tid & 3;   // sigma entry of this thread
 
   floatx4 acc[4][4];
@@ -276,7 +374,7 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
   // Every lane issues the same loads: the lambda column is clamped to a valid
   // one and zeroed at the store, so no load sits behind a divergent branch.
   struct ChunkRegs {
-    uint4 q0, q1, d0, d1;
+    uint4 q[NK], d[NK];
     float gct, glast, lv;
   };
   const unsigned int lcol = (unsigned int)(7 + nloc + e0 + min(le, ne - 1));
@@ -287,10 +385,11 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
       if (sl == slot) {
-        rr[sl].q0 = buf_load16(rq, vo, t0 * qrow);
-        rr[sl].q1 = buf_load16(rq, vo, (t0 + 32) * qrow);
-        rr[sl].d0 = buf_load16(rd, vo, t0 * qrow);
-        rr[sl].d1 = buf_load16(rd, vo, (t0 + 32) * qrow);
+#pragma unroll
+        for (int u = 0; u < NK; ++u) {
+          rr[sl].q[u] = buf_load16(rq, vo, (t0 + RK * u) * qrow);
+          rr[sl].d[u] = buf_load16(rd, vo, (t0 + RK * u) * qrow);
+        }
         rr[sl].gct = buf_load<float>(rg, lt * H * 4, t0 * H * 4);
         rr[sl].glast = buf_load<float>(rg, 63 * H * 4, t0 * H * 4);
         rr[sl].lv = to_f32<TL>(buf_load<TL>(rl, (lt * H * L + lcol) * sizeof(TL), t0 * lrowb));
@@ -299,15 +398,15 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
   float E = 0.f;
   auto step = [&](int ic, int slot) {
     __syncthreads();   // previous chunk's reads of sm are done
-    const int off = (tid >> 3) * kLd + 8 * (tid & 7);
     float glast = 0.f;
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
       if (sl == slot) {
-        *(uint4*)(sm.q + off) = rr[sl].q0;
-        *(uint4*)(sm.q + off + 32 * kLd) = rr[sl].q1;
-        *(uint4*)(sm.d + off) = rr[sl].d0;
-        *(uint4*)(sm.d + off + 32 * kLd) = rr[sl].d1;
+#pragma unroll
+        for (int u = 0; u < NK; ++u) {
+          stage_unit<NP, TK>(rr[sl].q[u], sm.q, soff + RK * u * kLd);
+          stage_unit<NP, TK>(rr[sl].d[u], sm.d, soff + RK * u * kLd);
+        }
         sm.sig[le][lt] = le < ne ? rr[sl].lv * fexp(E + rr[sl].gct) : 0.f;
         glast = rr[sl].glast;
       }
@@ -315,17 +414,19 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const bf16x8 qa = tr_frag(sm.q, kLd, 32 * c, 16 * w);   // Q[t][k = 16w + ln]
-      bf16x8 db[4];
+      bf16x8 qa[NP];   // Q[t][k = 16w + ln]
+      trfrag<NP>(sm.q, 32 * c, 16 * w, qa);
+      bf16x8 db[4][NP];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) db[n] = tr_frag(sm.d, kLd, 32 * c, 16 * n);
+      for (int n = 0; n < 4; ++n) trfrag<NP>(sm.d, 32 * c, 16 * n, db[n]);
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         if (a < ne) {
           const float* sg = sm.sig[a] + 32 * c + 8 * lq;
-          const bf16x8 qs = scale8(qa, *(const floatx4*)sg, *(const floatx4*)(sg + 4));
+          bf16x8 qs[NP];
+          scale8s<NP>(qa, *(const floatx4*)sg, *(const floatx4*)(sg + 4), qs);
 #pragma unroll
-          for (int n = 0; n < 4; ++n) acc[a][n] = mfma16x16x32(qs, db[n], acc[a][n]);
+          for (int n = 0; n < 4; ++n) acc[a][n] = mma<NP>(qs, db[n], acc[a][n]);
         }
       }
     }
@@ -354,9 +455,10 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
 // ---------------------------------------------------------------------------
 // LDS of the dq kernel (about 73 KB, so two workgroups share a CU); the
 // top-level states stay in HBM / L2 (see htop below).
+template <int NP>
 struct DqSmem {
-  BwdStage st;
-  __bf16 a[kBT * kLd];                      // (M o dP)[t][s], bf16
+  BwdStage<NP> st;
+  __bf16 a[NP][kBT * kLd];                  // (M o dP)[t][s], NP bf16 planes
   float dl_off[kBT][4][4];                  // off-diagonal tile partials [t][jt][lq]
   float dl_diag[kBT][5][4];                 // diagonal tile partials [t][level][lq]
   float dl_int[kBT][kMaxLoc + kMaxTop][4];  // inter-level partials [t][e][wave]
@@ -368,14 +470,14 @@ struct DqSmem {
 // after the first chunk their MFMA fragments come from L2; the fragments of
 // the segment's first top level are loaded once, before the walk, the others
 // one level ahead of their use.
-template <typename TV, typename TL>
-__global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
-    const __bf16* __restrict__ htop, __bf16* __restrict__ dq, float* __restrict__ dl,
+template <int NP, typename TK, typename TV, typename TL>
+__global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
+    const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
+    const TK* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
+    const __bf16* __restrict__ htop, TK* __restrict__ dq, float* __restrict__ dl,
     float* __restrict__ dgq, int B, int T, int H, int V, int L, int nlev, int slog, int NSEG) {
-  __shared__ __attribute__((aligned(16))) DqSmem sm;
-  BwdStage& s = sm.st;
+  __shared__ __attribute__((aligned(16))) DqSmem<NP> sm;
+  BwdStage<NP>& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq0 = lane >> 4, ln0 = lane & 15;
   // grid: xcd_head_grid(B * NSEG, H, 1): the heads of one (batch, segment) share an XCD
@@ -390,29 +492,33 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
   const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
 
   // A operand of a top level: h[k = 16w + ln][v = c0 + 4lq + i, c0 + 16 + 4lq + i]
-  const rsrc_t rt = make_rsrc(ntop > 0 ? (const void*)(htop + ((size_t)row * NSEG + p) * ntop * kKD * kKD)
+  // (htop: [row][p][e2][plane][64][64])
+  const rsrc_t rt = make_rsrc(ntop > 0 ? (const void*)(htop + ((size_t)row * NSEG + p) * ntop * NP * kKD * kKD)
                                        : (const void*)htop,
-                              ntop > 0 ? (size_t)ntop * kKD * kKD * 2 : 0);
+                              ntop > 0 ? (size_t)ntop * NP * kKD * kKD * 2 : 0);
   const unsigned int vo_t = ((16 * w + ln0) * kKD + 4 * lq0) * 2;
-  auto top_frag = [&](int e2, int cc) {
-    const unsigned int so = (unsigned int)(e2 * kKD * kKD + cc) * 2;
-    const uint2 lo = buf_load8(rt, vo_t, so), hi = buf_load8(rt, vo_t, so + 32);
-    return __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+  auto top_frag = [&](int e2, int cc, bf16x8* f) {
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+      const unsigned int so = (unsigned int)((e2 * NP + pl) * kKD * kKD + cc) * 2;
+      const uint2 lo = buf_load8(rt, vo_t, so), hi = buf_load8(rt, vo_t, so + 32);
+      f[pl] = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+    }
   };
-  bf16x8 tf0{}, tf1{};   // the segment's first top level (loaded once)
+  bf16x8 tf0[NP] = {}, tf1[NP] = {};   // the segment's first top level (loaded once)
   if (topmask) {
     const int e0 = __builtin_ctz(topmask);
-    tf0 = top_frag(e0, 0);
-    tf1 = top_frag(e0, 32);
+    top_frag(e0, 0, tf0);
+    top_frag(e0, 32, tf1);
   }
 
-  BwdLoader<256, TV, TL> ld;
+  BwdLoader<256, TK, TV, TL> ld;
   ld.init(q, k, v, dO, gcin, l, b, h, T, H, V, L, lu);
   const size_t rq0 = (size_t)b * T * H + h;
-  const rsrc_t rdq = make_rsrc(dq + rq0 * kKD, (size_t)T * H * kKD * 2);
+  const rsrc_t rdq = make_rsrc(dq + rq0 * kKD, (size_t)T * H * kKD * sizeof(TK));
   const rsrc_t rdl = make_rsrc(dl + rq0 * L, (size_t)T * H * L * 4);
   const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
-  const unsigned int vo_dq = (ln0 * H * kKD + 16 * w + 4 * lq0) * 2;
+  const unsigned int vo_dq = (ln0 * H * kKD + 16 * w + 4 * lq0) * sizeof(TK);
 
   // forward states h_e^T [v][k]: lane holds v = 16m + 4lq + i, k = 16w + ln
   floatx4 hT[kMaxLoc][4];
@@ -421,7 +527,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
 #pragma unroll
     for (int m = 0; m < 4; ++m) hT[e][m] = zero4();
 
-  BwdRegs<256, TV, TL> rg;
+  BwdRegs<256, TK, TV, TL> rg;
   ld.load(rg, c0);
   float Eseg = 0.f;
   for (int ic = c0; ic < cend; ++ic) {
@@ -440,7 +546,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
       const int code = p1_tile4(w, n);
       const int mt = (code & 15) >> 2, jt = code & 3;
       const int t = 16 * mt + ln;
-      bf16x4 out = bf16x4{};
+      float out[4] = {0.f, 0.f, 0.f, 0.f};
       if (code < 16) {
         floatx4 S, P;
         st_dpt_tile(s, mt, jt, S, P);
@@ -449,7 +555,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float pd = mk.dec[i] * P[i];
-          out[i] = (__bf16)(pd * s.lam[mk.lev[i] * kBT + t]);
+          out[i] = pd * s.lam[mk.lev[i] * kBT + t];
           x[i] = pd * S[i];
         }
         if (jt < mt) {
@@ -464,37 +570,51 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
           }
         }
       }
-      *(bf16x4*)(sm.a + t * kLd + 16 * jt + 4 * lq) = out;
+      store_planes4<NP>(sm.a, t * kLd + 16 * jt + 4 * lq, out);
     }
     __syncthreads();
 
     // ---- phase 2: dq^T[k-tile w][t] ----------------------------------------------
     floatx4 dqT[4];
+    {
+      bf16x8 kt0[NP], kt1[NP];
+      trfrag<NP>(s.k, 0, 16 * w, kt0);
+      trfrag<NP>(s.k, 32, 16 * w, kt1);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const __bf16* ar = sm.a + (16 * mt + ln) * kLd + 8 * lq;
-      dqT[mt] = mfma16x16x32(tr_frag(s.k, kLd, 0, 16 * w), *(const bf16x8*)ar, zero4());
-      if (mt >= 2)
-        dqT[mt] = mfma16x16x32(tr_frag(s.k, kLd, 32, 16 * w), *(const bf16x8*)(ar + 32), dqT[mt]);
+      for (int mt = 0; mt < 4; ++mt) {
+        const int ar = (16 * mt + ln) * kLd + 8 * lq;
+        bf16x8 af[NP];
+        frag8<NP>(sm.a, ar, af);
+        dqT[mt] = mma<NP>(kt0, af, zero4());
+        if (mt >= 2) {
+          frag8<NP>(sm.a, ar + 32, af);
+          dqT[mt] = mma<NP>(kt1, af, dqT[mt]);
+        }
+      }
     }
     // q[t][k] for this lane's (t = 16mt + ln, k = 16w + 4lq + i)
     floatx4 qk[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const bf16x4 x = *(const bf16x4*)(s.q + (16 * mt + ln) * kLd + 16 * w + 4 * lq);
+      const int off = (16 * mt + ln) * kLd + 16 * w + 4 * lq;
+      const bf16x4 x = *(const bf16x4*)(s.q[0] + off);
       qk[mt] = floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+      if constexpr (NP == 2) {
+        const bf16x4 y = *(const bf16x4*)(s.q[1] + off);
+        qk[mt] += floatx4{(float)y[0], (float)y[1], (float)y[2], (float)y[3]};
+      }
     }
     if (nlev > 0) {
-      bf16x8 da[4][2];   // dO[t][v] in the states' v order
+      bf16x8 da[4][2][NP];   // dO[t][v] in the states' v order
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) da[mt][c] = row_pair(s.d, 16 * mt + ln, 32 * c);
-      auto level = [&](const bf16x8& a0, const bf16x8& a1, int e, int col, float scale) {
+        for (int c = 0; c < 2; ++c) row_pairs<NP>(s.d, 16 * mt + ln, 32 * c, da[mt][c]);
+      auto level = [&](const bf16x8* a0, const bf16x8* a1, int e, int col, float scale) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          floatx4 y = mfma16x16x32(a0, da[mt][0], zero4());
-          y = mfma16x16x32(a1, da[mt][1], y);     // Y^T[k][t] = sum_v h[k][v] dO[t][v]
+          floatx4 y = mma<NP>(a0, da[mt][0], zero4());
+          y = mma<NP>(a1, da[mt][1], y);     // Y^T[k][t] = sum_v h[k][v] dO[t][v]
           const int t = 16 * mt + ln;
           const float sg = s.lam[col * kBT + t] * scale;
           float r = 0.f;
@@ -514,7 +634,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
         for (int e = 0; e < kMaxLoc; ++e) {
           if (e < nloc) {
             if (ic > c0 && ((ic >> e) & 1)) {
-              level(cat8(hT[e][0], hT[e][1]), cat8(hT[e][2], hT[e][3]), e, 7 + e, 1.f);
+              bf16x8 h0[NP], h1[NP];
+              cat8s<NP>(hT[e][0], hT[e][1], h0);
+              cat8s<NP>(hT[e][2], hT[e][3], h1);
+              level(h0, h1, e, 7 + e, 1.f);
             } else if (lq == 0) {
 #pragma unroll
               for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][e][w] = 0.f;
@@ -525,19 +648,32 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
       if (topmask) {
         const float ee = fexp(Eseg);
         int m = topmask, e2 = __builtin_ctz(topmask);
-        bf16x8 a0 = tf0, a1 = tf1;
+        bf16x8 a0[NP], a1[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+          a0[pl] = tf0[pl];
+          a1[pl] = tf1[pl];
+        }
         while (true) {
           m &= m - 1;
-          bf16x8 n0 = a0, n1 = a1;
+          bf16x8 n0[NP], n1[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            n0[pl] = a0[pl];
+            n1[pl] = a1[pl];
+          }
           if (m) {   // the next read level's fragments, in flight during this level
-            n0 = top_frag(__builtin_ctz(m), 0);
-            n1 = top_frag(__builtin_ctz(m), 32);
+            top_frag(__builtin_ctz(m), 0, n0);
+            top_frag(__builtin_ctz(m), 32, n1);
           }
           level(a0, a1, nloc + e2, 7 + nloc + e2, ee);
           if (!m) break;
           e2 = __builtin_ctz(m);
-          a0 = n0;
-          a1 = n1;
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            a0[pl] = n0[pl];
+            a1[pl] = n1[pl];
+          }
         }
       }
       if (lq == 0)
@@ -548,22 +684,27 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
-      buf_store4<__bf16>(dqT[mt], rdq, vo_dq, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * 2);
+      buf_store4<TK>(dqT[mt], rdq, vo_dq, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * sizeof(TK));
 
     // ---- phase 3: forward state update h^T_e[v][k] += (w o V)^T K ---------------
     const float glr = s.gc[kBT - 1];
     if (nloc > 0) {
       floatx4 kv[4];
       {
-        const bf16x8 kb0 = scale8(tr_frag(s.k, kLd, 0, 16 * w), *(const floatx4*)(s.wt + 8 * lq),
-                                  *(const floatx4*)(s.wt + 8 * lq + 4));
-        const bf16x8 kb1 =
-            scale8(tr_frag(s.k, kLd, 32, 16 * w), *(const floatx4*)(s.wt + 32 + 8 * lq),
-                   *(const floatx4*)(s.wt + 36 + 8 * lq));
+        bf16x8 kt[NP], kb0[NP], kb1[NP];
+        trfrag<NP>(s.k, 0, 16 * w, kt);
+        scale8s<NP>(kt, *(const floatx4*)(s.wt + 8 * lq), *(const floatx4*)(s.wt + 8 * lq + 4),
+                    kb0);
+        trfrag<NP>(s.k, 32, 16 * w, kt);
+        scale8s<NP>(kt, *(const floatx4*)(s.wt + 32 + 8 * lq),
+                    *(const floatx4*)(s.wt + 36 + 8 * lq), kb1);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          kv[m] = mfma16x16x32(tr_frag(s.v, kLd, 0, 16 * m), kb0, zero4());
-          kv[m] = mfma16x16x32(tr_frag(s.v, kLd, 32, 16 * m), kb1, kv[m]);
+          bf16x8 vf[NP];
+          trfrag<NP>(s.v, 0, 16 * m, vf);
+          kv[m] = mma<NP>(vf, kb0, zero4());
+          trfrag<NP>(s.v, 32, 16 * m, vf);
+          kv[m] = mma<NP>(vf, kb1, kv[m]);
         }
       }
       const float gl = fexp(glr);
@@ -629,24 +770,25 @@ __global__ __launch_bounds__(256, 2) void mamba2_bwd_dq_kernel(
 // ---------------------------------------------------------------------------
 // dk, dv and dG: reverse walk over one segment, 8 waves
 // ---------------------------------------------------------------------------
+template <int NP>
 struct DkvSmem {
-  BwdStage st;
-  __bf16 as[kBT * kLd];     // (M o S)[t][s]
-  __bf16 ap[kBT * kLd];     // (M o dP)[t][s]
+  BwdStage<NP> st;
+  __bf16 as[NP][kBT * kLd];  // (M o S)[t][s]
+  __bf16 ap[NP][kBT * kLd];  // (M o dP)[t][s]
   float dgk[kBT][4];        // k . dk inter-chunk partials [s][wave]
   float kdk[kBT][4];        // k . dk intra-chunk column sums [s][t-tile]
 };
 
-template <typename TV, typename TL>
+template <int NP, typename TK, typename TV, typename TL>
 __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
+    const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
+    const TK* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
     const float* __restrict__ rsum, const float* __restrict__ segd,
-    const float* __restrict__ dgq, __bf16* __restrict__ dk, TV* __restrict__ dv,
+    const float* __restrict__ dgq, TK* __restrict__ dk, TV* __restrict__ dv,
     float* __restrict__ dg, float* __restrict__ segtot, int B, int T, int H, int V, int L,
     int nlev, int slog, int NSEG) {
-  __shared__ __attribute__((aligned(16))) DkvSmem sm;
-  BwdStage& s = sm.st;
+  __shared__ __attribute__((aligned(16))) DkvSmem<NP> sm;
+  BwdStage<NP>& s = sm.st;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int role = w >> 2, wr = w & 3;     // role 0: dk (k-tile wr), role 1: dv (v-tile wr)
@@ -710,17 +852,17 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     }
   }
 
-  BwdLoader<512, TV, TL> ld;
+  BwdLoader<512, TK, TV, TL> ld;
   ld.init(q, k, v, dO, gcin, l, b, h, T, H, V, L, lu);
   const size_t rq0 = (size_t)b * T * H + h;
-  const rsrc_t rdk = make_rsrc(dk + rq0 * kKD, (size_t)T * H * kKD * 2);
+  const rsrc_t rdk = make_rsrc(dk + rq0 * kKD, (size_t)T * H * kKD * sizeof(TK));
   const rsrc_t rdv = make_rsrc(dv + rq0 * V, (size_t)T * H * V * sizeof(TV));
   const rsrc_t rdg = make_rsrc(dg + rq0, (size_t)T * H * 4);
   const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
-  const unsigned int vo_dk = (ln * H * kKD + 16 * wr + 4 * lq) * 2;
+  const unsigned int vo_dk = (ln * H * kKD + 16 * wr + 4 * lq) * sizeof(TK);
   const unsigned int vo_dv = (ln * H * V + 16 * wr + 4 * lq) * sizeof(TV);
 
-  BwdRegs<512, TV, TL> rg;
+  BwdRegs<512, TK, TV, TL> rg;
   ld.load(rg, cend - 1);
   float carry = 0.f;   // sum of dG over the later chunks of this segment
   for (int ic = cend - 1; ic >= c0; --ic) {
@@ -739,7 +881,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
       if (code >= 0) {
         const int mt = (code & 15) >> 2, jt = code & 3;
         const int t = 16 * mt + ln;
-        bf16x4 os = bf16x4{}, op = bf16x4{};
+        float os[4] = {0.f, 0.f, 0.f, 0.f}, op[4] = {0.f, 0.f, 0.f, 0.f};
         if (code < 16) {
           floatx4 S, P;
           st_dpt_tile(s, mt, jt, S, P);
@@ -747,8 +889,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float m = mk.dec[i] * s.lam[mk.lev[i] * kBT + t];
-            os[i] = (__bf16)(m * S[i]);
-            op[i] = (__bf16)(m * P[i]);
+            os[i] = m * S[i];
+            op[i] = m * P[i];
             // k_s . dk_s (intra part) = column sum over t of (M o S o dP), in fp32
             float c = m * S[i] * P[i];
             c += __shfl_xor(c, 1, 64);
@@ -758,25 +900,33 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             if (ln == 0) sm.kdk[16 * jt + 4 * lq + i][mt] = c;
           }
         }
-        *(bf16x4*)(sm.as + t * kLd + 16 * jt + 4 * lq) = os;
-        *(bf16x4*)(sm.ap + t * kLd + 16 * jt + 4 * lq) = op;
+        store_planes4<NP>(sm.as, t * kLd + 16 * jt + 4 * lq, os);
+        store_planes4<NP>(sm.ap, t * kLd + 16 * jt + 4 * lq, op);
       }
     }
     __syncthreads();
 
     // ---- phase 2: dk^T (role 0) / dv^T (role 1) for the chunk's tokens s -------------
-    const __bf16* xa = role == 0 ? s.q : s.d;      // A of the intra product: Q^T / dO^T
-    const __bf16* xb = role == 0 ? sm.ap : sm.as;  // B: (M o dP) / (M o S)
-    const __bf16* xs = role == 0 ? s.v : s.k;      // B of the inter product: V / K rows s
+    typedef const __bf16 (*Planes)[kBT * kLd];
+    Planes xa = role == 0 ? s.q : s.d;      // A of the intra product: Q^T / dO^T
+    Planes xb = role == 0 ? sm.ap : sm.as;  // B: (M o dP) / (M o S)
+    Planes xs = role == 0 ? s.v : s.k;      // B of the inter product: V / K rows s
     floatx4 out[4];
+    {
+      bf16x8 a1[NP], a0[NP];
+      trfrag<NP>(xa, 32, 16 * wr, a1);
+      trfrag<NP>(xa, 0, 16 * wr, a0);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      // t-steps covering t >= s: both for s-tiles 0, 1; the second for 2, 3
-      out[mt] = mfma16x16x32(tr_frag(xa, kLd, 32, 16 * wr), tr_frag(xb, kLd, 32, 16 * mt),
-                             zero4());
-      if (mt < 2)
-        out[mt] = mfma16x16x32(tr_frag(xa, kLd, 0, 16 * wr), tr_frag(xb, kLd, 0, 16 * mt),
-                               out[mt]);
+      for (int mt = 0; mt < 4; ++mt) {
+        // t-steps covering t >= s: both for s-tiles 0, 1; the second for 2, 3
+        bf16x8 bx[NP];
+        trfrag<NP>(xb, 32, 16 * mt, bx);
+        out[mt] = mma<NP>(a1, bx, zero4());
+        if (mt < 2) {
+          trfrag<NP>(xb, 0, 16 * mt, bx);
+          out[mt] = mma<NP>(a0, bx, out[mt]);
+        }
+      }
     }
     {
       // DHsum = sum of the local levels this chunk is a source of, plus the top part
@@ -790,20 +940,31 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
           for (int m = 0; m < 4; ++m) dsum[m] += dh[e][m];
         }
       }
-      const bf16x8 a0 = cat8(dsum[0], dsum[1]), a1 = cat8(dsum[2], dsum[3]);
+      bf16x8 a0[NP], a1[NP];
+      cat8s<NP>(dsum[0], dsum[1], a0);
+      cat8s<NP>(dsum[2], dsum[3], a1);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        floatx4 y = mfma16x16x32(a0, row_pair(xs, 16 * mt + ln, 0), zero4());
-        y = mfma16x16x32(a1, row_pair(xs, 16 * mt + ln, 32), y);
+        bf16x8 rp[NP];
+        row_pairs<NP>(xs, 16 * mt + ln, 0, rp);
+        floatx4 y = mma<NP>(a0, rp, zero4());
+        row_pairs<NP>(xs, 16 * mt + ln, 32, rp);
+        y = mma<NP>(a1, rp, y);
         const float ws = s.wt[16 * mt + ln];
 #pragma unroll
         for (int i = 0; i < 4; ++i) out[mt][i] += y[i] * ws;
         if (role == 0) {
           // k_s . dk_s, inter-chunk part
-          const bf16x4 kx = *(const bf16x4*)(s.k + (16 * mt + ln) * kLd + 16 * wr + 4 * lq);
+          const int koff = (16 * mt + ln) * kLd + 16 * wr + 4 * lq;
+          const bf16x4 kx = *(const bf16x4*)(s.k[0] + koff);
           float r = 0.f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) r += (float)kx[i] * y[i];
+          if constexpr (NP == 2) {
+            const bf16x4 kl = *(const bf16x4*)(s.k[1] + koff);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r += (float)kl[i] * y[i];
+          }
           r = sum_lq(r) * ws;
           if (lq == 0) sm.dgk[16 * mt + ln][wr] = r;
         }
@@ -812,7 +973,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     if (role == 0) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
-        buf_store4<__bf16>(out[mt], rdk, vo_dk, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * 2);
+        buf_store4<TK>(out[mt], rdk, vo_dk, ((unsigned int)ic * kBT + 16 * mt) * H * kKD * sizeof(TK));
     } else {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -823,8 +984,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     const float cl = s.gc[kBT - 1];
     const float gl = fexp(cl);
     if (nloc > 0) {
-      const __bf16* ya = role == 0 ? s.d : s.q;   // A: dO^T / Q^T (rows of the state)
-      const __bf16* yb = role == 0 ? s.q : s.d;   // B: sigma o Q / sigma o dO
+      Planes ya = role == 0 ? s.d : s.q;   // A: dO^T / Q^T (rows of the state)
+      Planes yb = role == 0 ? s.q : s.d;   // B: sigma o Q / sigma o dO
 #pragma unroll
       for (int e = 0; e < kMaxLoc; ++e) {
         if (e < nloc) {
@@ -839,15 +1000,20 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             for (int m = 0; m < 4; ++m) dh[e][m] *= gl;
             if (rd) {
               const float* sg = s.lam + (7 + e) * kBT;
-              const bf16x8 b0 = scale8(tr_frag(yb, kLd, 0, 16 * wr), *(const floatx4*)(sg + 8 * lq),
-                                       *(const floatx4*)(sg + 8 * lq + 4));
-              const bf16x8 b1 = scale8(tr_frag(yb, kLd, 32, 16 * wr),
-                                       *(const floatx4*)(sg + 32 + 8 * lq),
-                                       *(const floatx4*)(sg + 36 + 8 * lq));
+              bf16x8 yt[NP], b0[NP], b1[NP];
+              trfrag<NP>(yb, 0, 16 * wr, yt);
+              scale8s<NP>(yt, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
+                          b0);
+              trfrag<NP>(yb, 32, 16 * wr, yt);
+              scale8s<NP>(yt, *(const floatx4*)(sg + 32 + 8 * lq),
+                          *(const floatx4*)(sg + 36 + 8 * lq), b1);
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
-                dh[e][m] = mfma16x16x32(tr_frag(ya, kLd, 0, 16 * m), b0, dh[e][m]);
-                dh[e][m] = mfma16x16x32(tr_frag(ya, kLd, 32, 16 * m), b1, dh[e][m]);
+                bf16x8 af[NP];
+                trfrag<NP>(ya, 0, 16 * m, af);
+                dh[e][m] = mma<NP>(af, b0, dh[e][m]);
+                trfrag<NP>(ya, 32, 16 * m, af);
+                dh[e][m] = mma<NP>(af, b1, dh[e][m]);
               }
             }
           }
@@ -917,12 +1083,13 @@ inline BwdWs bwd_ws_layout(void* base, int B, int T, int H, int V, int nlev) {
   w.dgq = (float*)(p + off);    off += align256((size_t)B * T * H * 4);
   w.sums = (float*)(p + off);   off += align256(NSEG > 1 ? rows * NSEG * kKD * V * 4 : 0);
   w.rsum = (float*)(p + off);   off += align256(rows * NSEG * ntop * kKD * kKD * 4);
-  w.htop = (__bf16*)(p + off);  off += align256(rows * NSEG * ntop * kKD * kKD * 2);
+  // room for two bf16 planes (the bf16x3 backward)
+  w.htop = (__bf16*)(p + off);  off += align256(rows * NSEG * ntop * kKD * kKD * 2 * 2);
   w.bytes = off;
   return w;
 }
 
-template <typename TV, typename TL>
+template <int NP, typename TK, typename TV, typename TL>
 static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, const float* gc,
                                const void* l, const void* dO, void* dq, void* dk, void* dv,
                                float* dg, float* dl, void* ws, int B, int T, int H, int V,
@@ -935,37 +1102,37 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   const BwdWs w = bwd_ws_layout(ws, B, T, H, V, nlev);
   hipError_t e;
   if (NSEG > 1) {
-    auto sk = mamba2_seg_sum_kernel<__bf16, TV, true, 1>;
+    auto sk = mamba2_seg_sum_kernel<TK, TV, true, NP>;
     hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
-                       (const __bf16*)k, (const TV*)v, gc, w.sums, w.segd, B, T, H, H, V, NT,
+                       (const TK*)k, (const TV*)v, gc, w.sums, w.segd, B, T, H, H, V, NT,
                        1 << slog, NSEG, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ntop > 0) {
     // top-level states of every segment for the dq kernel
-    hipLaunchKernelGGL(mamba2_htop_kernel<1>, dim3(rows * 4), dim3(256), 0, stream, w.sums,
+    hipLaunchKernelGGL(mamba2_htop_kernel<NP>, dim3(rows * 4), dim3(256), 0, stream, w.sums,
                        w.segd, w.htop, V, NSEG, ntop, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ngrp = (ntop + 3) / 4;
-    auto rk = mamba2_bwd_rsum_kernel<TL>;
-    hipLaunchKernelGGL(rk, dim3(rows * NSEG * ngrp), dim3(256), 0, stream, (const __bf16*)q,
-                       (const __bf16*)dO, gc, (const TL*)l, w.rsum, T, H, L, NT, slog, NSEG,
+    auto rk = mamba2_bwd_rsum_kernel<NP, TK, TL>;
+    hipLaunchKernelGGL(rk, dim3(rows * NSEG * ngrp), dim3(256), 0, stream, (const TK*)q,
+                       (const TK*)dO, gc, (const TL*)l, w.rsum, T, H, L, NT, slog, NSEG,
                        nloc, ntop, ngrp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kq = mamba2_bwd_dq_kernel<TV, TL>;
+    auto kq = mamba2_bwd_dq_kernel<NP, TK, TV, TL>;
     hipLaunchKernelGGL(kq, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
-                       (const __bf16*)q, (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc,
-                       (const TL*)l, w.htop, (__bf16*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog,
+                       (const TK*)q, (const TK*)k, (const TV*)v, (const TK*)dO, gc,
+                       (const TL*)l, w.htop, (TK*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog,
                        NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kk = mamba2_bwd_dkv_kernel<TV, TL>;
-    hipLaunchKernelGGL(kk, dim3(rows * NSEG), dim3(512), 0, stream, (const __bf16*)q,
-                       (const __bf16*)k, (const TV*)v, (const __bf16*)dO, gc, (const TL*)l,
-                       w.rsum, w.segd, w.dgq, (__bf16*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
+    auto kk = mamba2_bwd_dkv_kernel<NP, TK, TV, TL>;
+    hipLaunchKernelGGL(kk, dim3(rows * NSEG), dim3(512), 0, stream, (const TK*)q,
+                       (const TK*)k, (const TV*)v, (const TK*)dO, gc, (const TL*)l,
+                       w.rsum, w.segd, w.dgq, (TK*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
                        nlev, slog, NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -983,21 +1150,35 @@ size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev) {
   return hattn::bwd_ws_layout(nullptr, B, T, H, V, nlev).bytes;
 }
 
+// dt_qk (= the dtype of dO): bf16 selects the bf16 kernels (v and lambda bf16 or
+// fp32); fp32 the bf16x3 kernels, which take fp32 v and lambda and write fp32
+// dq, dk, dv.
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
                                    float* dg, float* dl, void* ws, int B, int T, int H, int V,
-                                   int L, int nlev, int dt_v, int dt_l, hipStream_t stream,
-                                   int* unsupported) {
+                                   int L, int nlev, int dt_qk, int dt_v, int dt_l,
+                                   hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
+  if (dt_qk == 2) {
+    if (dt_v == 2 && dt_l == 2)
+      return bwd_launch_t<2, float, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B,
+                                                  T, H, V, L, nlev, stream);
+    *unsupported = 1;
+    return hipSuccess;
+  }
+  if (dt_qk != 0) {
+    *unsupported = 1;
+    return hipSuccess;
+  }
   if (dt_v == 0 && dt_l == 0)
-    return bwd_launch_t<__bf16, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, __bf16, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
   if (dt_v == 0 && dt_l == 2)
-    return bwd_launch_t<__bf16, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, __bf16, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
   if (dt_v == 2 && dt_l == 0)
-    return bwd_launch_t<float, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, float, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
   if (dt_v == 2 && dt_l == 2)
-    return bwd_launch_t<float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
   *unsupported = 1;
   return hipSuccess;
 }

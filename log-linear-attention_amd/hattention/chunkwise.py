@@ -179,6 +179,10 @@ def chunkwise_bwd(
 ):
     """Log-linear Mamba-2 backward (chunkwise.py:1286-1597).
 
+    bf16 q / k run the bf16 MFMA kernels; fp32 q / k the bf16x3 kernels (every
+    product and every intermediate that feeds one as hi / lo bf16 planes,
+    fp32-accurate), the counterpart of the reference's fp32 backward.
+
     ``g`` is the chunk-local cumsum returned by :func:`chunkwise_fwd`.
     Returns (dq, dk, dv, dg, dl): dq / dk / dv in the dtypes of q / k / v,
     dg (w.r.t. the raw per-step g) and dl in fp32, like the reference.  Grouped
@@ -203,6 +207,11 @@ def chunkwise_bwd(
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
     do = do.to(q.dtype).contiguous()
+    v_dtype = v.dtype
+    if q.dtype == torch.float32:
+        # fp32 q / k run the bf16x3 (fp32-accurate) backward, which reads fp32 v,
+        # lambda and dO and writes fp32 dq, dk, dv
+        v, l = v.float().contiguous(), l.float().contiguous()
     if K == KB and V == KB:
         dq, dk, dv, dg, dl = _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype,
                                        chunk_size)
@@ -227,6 +236,7 @@ def chunkwise_bwd(
                 dg += r[3]
                 dl += r[4]
         dq, dk, dv = dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
+    dv = dv.to(v_dtype)
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3)
         dk = dk.view(B, T, G, H // G, K).sum(3)

@@ -151,3 +151,62 @@ def test_config4_full_size():
 def test_north_star_full_size_bwd():
     # north-star shape B=4 T=16384 H=16 dk=dv=64 L=15 (fwd + bwd throughput metric)
     _run(4, 16384, 16, 64, 64, 15, seed=1000, rows=[(3, 15)])
+
+
+# ---------------------------------------------------------------------------
+# fp32 inputs: the bf16x3 backward (north_star tolerance 1e-4 in fp32 mode)
+# ---------------------------------------------------------------------------
+TOL_X3 = 1e-4
+
+
+def _run_x3(B, T, H, K, V, L, seed):
+    from hattention.chunkwise import chunkwise_fwd, chunkwise_bwd
+    from hattention.base import HType
+    q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, seed=seed, dtype=torch.float32,
+                                           with_do=True)
+    dev = torch.device("cuda:0")
+    print(f"[mamba2_bwd x3] B={B} T={T} H={H} K={K} V={V} L={L}", flush=True)
+    qd, kd, vd, gd, ld, dod = (x.to(dev) for x in (q, k, v, g, l, do))
+    _, gc, _ = chunkwise_fwd(qd, kd, vd, gd, ld, False, 2, HType.WEAK, 64, False)
+    grads = chunkwise_bwd(qd, kd, vd, gc, ld, dod, False, 2, HType.WEAK, 64)
+    torch.cuda.synchronize()
+    assert all(x.dtype == torch.float32 for x in grads)
+    ref = autograd_bwd(chunked_fwd, *(x.double() for x in (q, k, v, g, l, do)), chunk_size=64)
+    for name, a, r in zip(NAMES, grads, ref):
+        mx, fro = _errs(a, r)
+        print(f"  {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < TOL_X3 and fro < TOL_X3, (name, mx, fro)
+
+
+def test_fp32_bf16x3_config0():
+    # B=2 T=1024 H=4 dk=dv=64 L=11, fp32
+    _run_x3(2, 1024, 4, 64, 64, 11, seed=1000)
+
+
+def test_fp32_bf16x3_segments_and_top_levels():
+    # several 16-chunk segments and top levels (T >= 4096)
+    _run_x3(1, 4096, 2, 64, 64, 13, seed=4097)
+
+
+def test_fp32_bf16x3_head_dim_128():
+    _run_x3(1, 1024, 2, 128, 128, 11, seed=129)
+
+
+def test_fp32_autograd_function():
+    """hattention_kernel(fp32 ...).backward() runs the bf16x3 HIP backward and
+    returns gradients in the input dtypes (kernel.py:230-244), within 1e-4."""
+    from hattention.kernel import hattention_kernel
+    from hattention.base import HType, HStruct
+    q, k, v, g, l, do = make_mamba2_inputs(1, 2048, 2, 64, 64, 12, seed=23, dtype=torch.float32,
+                                           with_do=True)
+    dev = torch.device("cuda:0")
+    leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, g, l)]
+    o = hattention_kernel(*leaves[:3], None, leaves[3], leaves[4], None, False, 2, HType.WEAK,
+                          HStruct.MAMBA2)
+    (o * do.to(dev)).sum().backward()
+    ref = autograd_bwd(chunked_fwd, *(x.double() for x in (q, k, v, g, l, do)), chunk_size=64)
+    for name, x, r in zip(NAMES, leaves, ref):
+        assert x.grad is not None and x.grad.dtype == torch.float32, name
+        mx, fro = _errs(x.grad, r)
+        print(f"  {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < TOL_X3 and fro < TOL_X3, (name, mx, fro)

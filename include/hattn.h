@@ -159,6 +159,11 @@ size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, i
  *   Aw, Au [B, T, H, 64] bf16 (outputs): per chunk (I + A)^-1 and (I + A)^-1 o gamma,
  *          A = strict-tril(diag(beta) K K^T), gamma[t,s] = exp(Gc_t - Gc_s)
  *   ht [B, H, K, V, L] fp32 final level states or NULL
+ *   l2norm_qk, qk_scale: nonzero l2norm_qk normalises inside the kernels,
+ *          q <- q * qk_scale / ||q||, k <- k / ||k|| (||x|| = sqrt(sum x^2 +
+ *          1e-6)), which is what HAttentionFunction does before the call
+ *          (kernel.py:110-111, use_qk_l2norm_in_kernel); 0 takes q and k as
+ *          given, as the reference's chunkwise_fwd does
  *   workspace >= hattn_gdn_chunkwise_fwd_workspace(...) bytes
  *
  * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64
@@ -169,8 +174,9 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
                             const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
                             void* Au, float* ht, int B, int T, int H, int K, int V, int L,
                             int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
-                            int level_base, int htype, int chunk_size, void* workspace,
-                            size_t workspace_bytes, void* stream);
+                            int level_base, int htype, int chunk_size, int l2norm_qk,
+                            float qk_scale, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* Workspace bytes of hattn_gdn_chunkwise_fwd (q_new, k_new, w_new, u in bf16
  * and the fp32 intra-chunk output).  No counterpart in the reference, which
@@ -192,6 +198,9 @@ size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int 
  *   dq, dk [B, T, H, K] bf16   dv [B, T, H, V] bf16   db [B, T, H] in dtype_beta
  *   dg [B, T, H] fp32 (w.r.t. the per-step g: reverse chunk-local cumsum applied,
  *   chunkwise_hgdn.py:1219)   dl [B, T, H, L] fp32
+ *   l2norm_qk, qk_scale: as the forward; with l2norm_qk nonzero, q and k are the
+ *   raw inputs and dq, dk are w.r.t. them (the l2norm chain rule of
+ *   kernel.py:24-29, 224-225 applied inside the kernel)
  *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
  *
  * Constraints as hattn_gdn_chunkwise_fwd; do bf16 -> else HATTN_ERR_NOT_IMPLEMENTED.
@@ -201,8 +210,8 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
                             const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
                             float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
                             int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
-                            int chunk_size, void* workspace, size_t workspace_bytes,
-                            void* stream);
+                            int chunk_size, int l2norm_qk, float qk_scale, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of hattn_gdn_chunkwise_bwd: the recomputed q_new, k_new, w_new,
  * u (bf16), every level's state at every chunk start (bf16), and the fp32

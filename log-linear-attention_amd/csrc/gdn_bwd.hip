@@ -46,8 +46,8 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
                                       const void* beta, const float* gcum, const void* l,
                                       __bf16* qn, __bf16* kn, __bf16* wn, __bf16* un,
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
-                                      int nlev, int dt_b, int dt_l, hipStream_t stream,
-                                      int* unsupported);
+                                      int nlev, int dt_b, int dt_l, int norm_qk, float scale,
+                                      hipStream_t stream, int* unsupported);
 
 namespace hattn {
 
@@ -361,6 +361,7 @@ struct GdnBchunkSmem {
   float dgcol[4][kGC];     // dGc: column-sum contributions, per wave
   float dbr[kGC];          // dbeta
   float lastc[kGC];        // contributions to dGc_last
+  float rq[kGC], rk[kGC];  // 1 / ||q_t||, 1 / ||k_t|| (in-kernel l2 normalisation)
 };
 
 // fp32 fragments of a 16 x 32 MFMA operand held in a row-major fp32 matrix:
@@ -448,6 +449,34 @@ __device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs,
   }
 }
 
+// Store a 64 x (16 NKT) gradient held in the MFMA D layout (x[nt][i] is row
+// t16 + 4lq + i, column 16 nt + ln) as bf16 rows of stride ld.  With norm set,
+// the rows are the gradient w.r.t. y = x r s (r = 1 / ||x||, staged y in Y)
+// and the stored gradient is w.r.t. x: r s (x - y' (y' . x)), y' = y / s.
+template <int NKT>
+__device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], const __bf16* Y,
+                                                  const float* rinv, float inv_s, float s,
+                                                  int norm, __bf16* out, size_t ld, int t16) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  constexpr int LY = NKT * 16 + 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = t16 + 4 * lq + i;
+    float f = 1.f, dot = 0.f;
+    if (norm) {
+#pragma unroll
+      for (int nt = 0; nt < NKT; ++nt) dot += (float)Y[t * LY + 16 * nt + ln] * inv_s * x[nt][i];
+      dot = rsum16(dot);
+      f = rinv[t] * s;
+    }
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt) {
+      const float y = norm ? (float)Y[t * LY + 16 * nt + ln] * inv_s : 0.f;
+      out[t * ld + 16 * nt + ln] = (__bf16)(f * (x[nt][i] - y * dot));
+    }
+  }
+}
+
 template <int KD, int VD, typename TB, typename TL>
 __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
@@ -456,7 +485,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const float* __restrict__ dk_p, const float* __restrict__ du, const float* __restrict__ dl_p,
     const float* __restrict__ del_p, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
     __bf16* __restrict__ dv, TB* __restrict__ db, float* __restrict__ dg, float* __restrict__ dl,
-    int B, int T, int H, int L, int nlev) {
+    int B, int T, int H, int L, int nlev, int norm_qk, float qk_scale) {
   using Sm = GdnBchunkSmem<KD, VD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
@@ -484,6 +513,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   g2s_tile<KD>(k + rowk, hk, s.k, LK);
   g2s_tile<KD>(q + rowk, hk, s.q, LK);
   g2s_tile<VD>(dO + rowv, hv, s.dO, LV);
+  if (norm_qk) {
+    // use_qk_l2norm_in_kernel: the gradients below are w.r.t. q scale / ||q|| and
+    // k / ||k||; the chain rule back to q and k is applied where dq, dk are stored
+    __syncthreads();
+    l2norm_rows<KD, LK>(s.q, qk_scale, s.rq);
+    l2norm_rows<KD, LK>(s.k, 1.f, s.rk);
+  }
   if (w == 0) {
     const float x = gcum[(tok0 + lane) * H + h];
     const float gl = __shfl(x, kGC - 1, 64);
@@ -779,6 +815,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   stage_rows<KD, LS, NPV>(ST, dq_p + rowk, hk, BTH * KD, s.e);
   __syncthreads();
   floatx4 u2[NKT];
+  float dqh[NKT][4];
 #pragma unroll
   for (int nt = 0; nt < NKT; ++nt) {
     floatx4 acc = zero4(), a2 = zero4();
@@ -792,12 +829,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       a2 = mma_ff(ap, bx, a2);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t16 + 4 * lq + i, kk = 16 * nt + ln;
-      dq[rowk + t * hk + kk] = (__bf16)(ST[t * LS + kk] + acc[i]);
-    }
+    for (int i = 0; i < 4; ++i) dqh[nt][i] = ST[(t16 + 4 * lq + i) * LS + 16 * nt + ln] + acc[i];
     u2[nt] = -a2;
   }
+  // dq = dq_hat, or with the in-kernel normalisation x -> y = x r (r = 1 / ||x||)
+  // scaled by s: dq = r s (dq_hat - y (y . dq_hat)) (fla l2norm_bwd, kernel.py:24-29)
+  store_l2norm_grad<NKT>(dqh, s.q, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
+                         dq + rowk, hk, t16);
   {
     const int t = tid >> 2, part = tid & 3;
     float x = 0.f;
@@ -849,16 +887,18 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   __syncthreads();
   {
     float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
+    float dkh[NKT][4];
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int sr = t16 + 4 * lq + i, kk = 16 * nt + ln;
         const float kv = (float)s.k[sr * LK + kk], dkn = ST[sr * LS + kk];
-        dk[rowk + sr * hk + kk] = (__bf16)(u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn);
+        dkh[nt][i] = u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn;
         rb[i] += kv * u2[nt][i];
         kd[i] += dkn * kv;
       }
+    store_l2norm_grad<NKT>(dkh, s.k, s.rk, 1.f, 1.f, norm_qk, dk + rowk, hk, t16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = rsum16(rb[i]), y = rsum16(kd[i]);
@@ -992,7 +1032,8 @@ template <int KD, int VD, typename TB, typename TL>
 static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const void* beta,
                             const float* gcum, const void* l, const void* dO, void* dq, void* dk,
                             void* dv, void* db, float* dg, float* dl, const GdnBwdWs& w, int B,
-                            int T, int H, int L, int nlev, hipStream_t stream) {
+                            int T, int H, int L, int nlev, int norm_qk, float scale,
+                            hipStream_t stream) {
   const int NT = T / kGC;
   hipError_t e;
   {
@@ -1016,7 +1057,7 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
                        (const __bf16*)k, (const __bf16*)v, (const TB*)beta, gcum, (const TL*)l,
                        (const __bf16*)dO, w.dq_p, w.dw_p, w.dk_p, w.du, w.dl_p, w.del_p,
                        (__bf16*)dq, (__bf16*)dk, (__bf16*)dv, (TB*)db, dg, dl, B, T,
-                       H, L, nlev);
+                       H, L, nlev, norm_qk, scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
@@ -1032,28 +1073,29 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, hipStream_t stream, int* unsupported) {
+                                int dt_l, int norm_qk, float scale, hipStream_t stream,
+                                int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
   hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.wn, w.un, w.hs,
-                                            B, T, H, K, V, L, nlev, dt_b, dt_l, stream,
-                                            unsupported);
+                                            B, T, H, K, V, L, nlev, dt_b, dt_l, norm_qk, scale,
+                                            stream, unsupported);
   if (e != hipSuccess || *unsupported) return e;
 #define HATTN_GDN_B(KD_, VD_)                                                                   \
   if (K == KD_ && V == VD_) {                                                                   \
     if (dt_b == 0 && dt_l == 0)                                                                 \
       return gdn_bwd_t<KD_, VD_, __bf16, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, \
-                                                 dl, w, B, T, H, L, nlev, stream);              \
+                                                 dl, w, B, T, H, L, nlev, norm_qk, scale, stream);              \
     if (dt_b == 2 && dt_l == 2)                                                                 \
       return gdn_bwd_t<KD_, VD_, float, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,   \
-                                               dl, w, B, T, H, L, nlev, stream);                \
+                                               dl, w, B, T, H, L, nlev, norm_qk, scale, stream);                \
     if (dt_b == 0 && dt_l == 2)                                                                 \
       return gdn_bwd_t<KD_, VD_, __bf16, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
-                                                dl, w, B, T, H, L, nlev, stream);               \
+                                                dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
     if (dt_b == 2 && dt_l == 0)                                                                 \
       return gdn_bwd_t<KD_, VD_, float, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
-                                                dl, w, B, T, H, L, nlev, stream);               \
+                                                dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
   }
   HATTN_GDN_B(128, 128)
   HATTN_GDN_B(64, 64)

@@ -97,4 +97,36 @@ __device__ inline void tri_inv64(const float* A, float* X, float (*t1all)[16 * 1
   }
 }
 
+// In-place l2 normalisation of the 64 rows of a staged bf16 tile [64][LD] with
+// N columns: x <- x * scale / sqrt(||x||^2 + eps), eps = 1e-6 (fla's l2norm,
+// used at kernel.py:20-23, 110-111), over fp32 sums.  Threads T0 .. T0 + 255
+// take part, four per row (consecutive lanes); rinv (if not null) receives
+// 1 / sqrt(||x||^2 + eps) of each row, for the backward's chain rule.
+template <int N, int LD, int T0 = 0>
+__device__ __forceinline__ void l2norm_rows(__bf16* X, float scale, float* rinv) {
+  constexpr int PER = N / 4, NU = PER / 8;   // columns per thread, 16-byte units
+  const int t = (int)threadIdx.x - T0, r = t >> 2, part = t & 3;
+  __bf16* row = X + r * LD + part * PER;
+  float ss = 0.f;
+  bf16x8 u[NU];
+#pragma unroll
+  for (int j = 0; j < NU; ++j) {
+    u[j] = *(const bf16x8*)(row + 8 * j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (float)u[j][i] * (float)u[j][i];
+  }
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  const float ri = __builtin_amdgcn_rsqf(ss + 1e-6f);
+  const float f = ri * scale;
+#pragma unroll
+  for (int j = 0; j < NU; ++j) {
+    bf16x8 y;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = (__bf16)((float)u[j][i] * f);
+    *(bf16x8*)(row + 8 * j) = y;
+  }
+  if (rinv != nullptr && part == 0) rinv[r] = ri;
+}
+
 }  // namespace hattn

@@ -65,7 +65,8 @@ __global__ __launch_bounds__(kPrepThreads, 1) void gdn_prep_kernel(
     const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
     float* __restrict__ gcum, __bf16* __restrict__ aw_out, __bf16* __restrict__ au_out,
     __bf16* __restrict__ qn, __bf16* __restrict__ kn, __bf16* __restrict__ wn,
-    __bf16* __restrict__ un, float* __restrict__ oi, int T, int H, int L) {
+    __bf16* __restrict__ un, float* __restrict__ oi, int T, int H, int L, int norm_qk,
+    float qk_scale) {
   using Sm = GdnPrepSmem<KD, VD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
@@ -113,6 +114,12 @@ __global__ __launch_bounds__(kPrepThreads, 1) void gdn_prep_kernel(
     if (tid < 7 * kGC) s.lam[e % 7][e / 7] = lv;
   }
   __syncthreads();
+  if (norm_qk) {
+    // use_qk_l2norm_in_kernel (kernel.py:110-111): k / ||k|| and q scale / ||q||
+    if (tid < 256) l2norm_rows<KD, LK>(s.k, 1.f, nullptr);
+    else l2norm_rows<KD, LK, 256>(s.q, qk_scale, nullptr);
+    __syncthreads();
+  }
 
   // ---- K K^T (-> A, fp32) and Q K^T (-> tril, bf16): wave w owns rows t-tile wt,
   // column tiles 2wh, 2wh + 1 ------------------------------------------------------
@@ -547,7 +554,7 @@ template <int KD, int VD, typename TB, typename TL, typename TO>
 static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, const void* beta,
                                const float* g, const void* l, void* o, float* gcum, void* aw,
                                void* au, float* ht, void* ws, int B, int T, int H, int L,
-                               int nlev, hipStream_t stream) {
+                               int nlev, int norm_qk, float scale, hipStream_t stream) {
   const GdnWs w = gdn_ws_layout(ws, B, T, H, KD, VD);
   const int NT = T / kGC;
   hipError_t e;
@@ -559,7 +566,8 @@ static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, cons
       return e;
     hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(kPrepThreads), smem, stream, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const TB*)beta, g, (const TL*)l, gcum,
-                       (__bf16*)aw, (__bf16*)au, w.qn, w.kn, w.wn, w.un, w.oi, T, H, L);
+                       (__bf16*)aw, (__bf16*)au, w.qn, w.kn, w.wn, w.un, w.oi, T, H, L, norm_qk,
+                       scale);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
@@ -587,24 +595,24 @@ int hattn_gdn_fwd_max_levels() { return hattn::kGMaxLev; }
 hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
-                                int L, int nlev, int dt_b, int dt_l, int dt_o,
-                                hipStream_t stream, int* unsupported) {
+                                int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
+                                float scale, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
 #define HATTN_GDN(KD_, VD_)                                                                     \
   if (K == KD_ && V == VD_) {                                                                   \
     if (dt_b == 0 && dt_l == 0 && dt_o == 0)                                                    \
       return gdn_launch_t<KD_, VD_, __bf16, __bf16, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
-                                                            ht, ws, B, T, H, L, nlev, stream);  \
+                                                            ht, ws, B, T, H, L, nlev, norm_qk, scale, stream);  \
     if (dt_b == 2 && dt_l == 2 && dt_o == 0)                                                    \
       return gdn_launch_t<KD_, VD_, float, float, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
-                                                          ht, ws, B, T, H, L, nlev, stream);    \
+                                                          ht, ws, B, T, H, L, nlev, norm_qk, scale, stream);    \
     if (dt_b == 0 && dt_l == 2 && dt_o == 0)                                                    \
       return gdn_launch_t<KD_, VD_, __bf16, float, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
-                                                           ht, ws, B, T, H, L, nlev, stream);   \
+                                                           ht, ws, B, T, H, L, nlev, norm_qk, scale, stream);   \
     if (dt_b == 2 && dt_l == 0 && dt_o == 0)                                                    \
       return gdn_launch_t<KD_, VD_, float, __bf16, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, \
-                                                           ht, ws, B, T, H, L, nlev, stream);   \
+                                                           ht, ws, B, T, H, L, nlev, norm_qk, scale, stream);   \
   }
   HATTN_GDN(128, 128)
   HATTN_GDN(64, 64)
@@ -620,8 +628,8 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
                                       const void* beta, const float* gcum, const void* l,
                                       __bf16* qn, __bf16* kn, __bf16* wn, __bf16* un,
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
-                                      int nlev, int dt_b, int dt_l, hipStream_t stream,
-                                      int* unsupported) {
+                                      int nlev, int dt_b, int dt_l, int norm_qk, float scale,
+                                      hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   const int NT = T / kGC;
@@ -636,7 +644,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
     hipLaunchKernelGGL(kp, dim3(B * H * NT), dim3(kPrepThreads), smem, stream, (const __bf16*)q, \
                        (const __bf16*)k, (const __bf16*)v, (const TB_*)beta, gcum,               \
                        (const TL_*)l, (float*)nullptr, (__bf16*)nullptr, (__bf16*)nullptr, qn,   \
-                       kn, wn, un, (float*)nullptr, T, H, L);                                    \
+                       kn, wn, un, (float*)nullptr, T, H, L, norm_qk, scale);                    \
     if ((e = hipGetLastError()) != hipSuccess) return e;                                         \
     auto ks = gdn_scan_kernel<KD_, TL_, __bf16>;                                                 \
     const int smem2 = (int)sizeof(GdnScanSmem<KD_>);                                             \

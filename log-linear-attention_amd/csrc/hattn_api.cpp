@@ -28,14 +28,15 @@ int hattn_gdn_fwd_max_levels();
 hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
-                                int L, int nlev, int dt_b, int dt_l, int dt_o,
-                                hipStream_t stream, int* unsupported);
+                                int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
+                                float scale, hipStream_t stream, int* unsupported);
 size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, hipStream_t stream, int* unsupported);
+                                int dt_l, int norm_qk, float scale, hipStream_t stream,
+                                int* unsupported);
 size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
@@ -312,8 +313,9 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
                             const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
                             void* Au, float* ht, int B, int T, int H, int K, int V, int L,
                             int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
-                            int level_base, int htype, int chunk_size, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            int level_base, int htype, int chunk_size, int l2norm_qk,
+                            float qk_scale, void* workspace, size_t workspace_bytes,
+                            void* stream) {
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
@@ -345,7 +347,8 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
   int unsupported = 0;
   hipError_t e = hattn_gdn_fwd_launch(q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, workspace, B,
                                       T, H, K, V, L, nlev, dtype_beta, dtype_l, dtype_o,
-                                      (hipStream_t)stream, &unsupported);
+                                      l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
+                                      &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d o=%d", dtype_beta,
                 dtype_l, dtype_o);
@@ -363,8 +366,8 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
                             const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
                             float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
                             int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
-                            int chunk_size, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+                            int chunk_size, int l2norm_qk, float qk_scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   (void)Aw;
   (void)Au;
   // chunkwise_hgdn.py:818-858
@@ -400,7 +403,8 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
   int unsupported = 0;
   hipError_t e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl,
                                       workspace, B, T, H, K, V, L, nlev, dtype_beta, dtype_l,
-                                      (hipStream_t)stream, &unsupported);
+                                      l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
+                                      &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);
   return check_hip(e, "hattn_gdn_chunkwise_bwd launch");

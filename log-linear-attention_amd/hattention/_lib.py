@@ -33,11 +33,11 @@ SIGNATURES = [
     ("hattn_mamba2_chunkwise_bwd_workspace", _S, [_I] * 6),
     ("hattn_gdn_chunkwise_fwd", _I,
      [_P, _P, _P, _P, _F, _P, _P, _F, _P, _P, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
-     + [_P, _S, _P]),
+     + [_I, ctypes.c_float] + [_P, _S, _P]),
     ("hattn_gdn_chunkwise_fwd_workspace", _S, [_I] * 6),
     ("hattn_gdn_chunkwise_bwd", _I,
      [_P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4
-     + [_I] * 3 + [_P, _S, _P]),
+     + [_I] * 3 + [_I, ctypes.c_float] + [_P, _S, _P]),
     ("hattn_gdn_chunkwise_bwd_workspace", _S, [_I] * 6),
     ("hattn_hstate_step", _I,
      [_P] * 9 + [_I] * 11 + [ctypes.c_float] + [_I] * 4 + [_P]),

@@ -68,8 +68,15 @@ def chunkwise_fwd(
     htype: HType,
     chunk_size: int,
     output_final_state: bool,
+    *,
+    qk_l2norm_scale: Optional[float] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """Log-linear GDN forward; returns (g_cumsum, o, Aw, Au, ht) like the reference."""
+    """Log-linear GDN forward; returns (g_cumsum, o, Aw, Au, ht) like the reference.
+
+    ``qk_l2norm_scale`` (not in the reference's signature, default None = its
+    behaviour): the kernels take raw q, k and use q * scale / ||q|| and
+    k / ||k||, what HAttentionFunction computes before the reference's call
+    (kernel.py:110-111), without a separate pass over q and k."""
     B, T, G, H, K, V, L = _validate(q, k, v, l, head_first, level_base, htype, chunk_size,
                                     b=b, g=g)
     if g.dtype != torch.float32:
@@ -90,7 +97,9 @@ def chunkwise_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
         _lib.ptr(o), _lib.ptr(g_cumsum), _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(ht),
         B, T, H, K, V, L, _lib.dtype_code(q), _lib.dtype_code(b), _lib.dtype_code(l),
-        _lib.dtype_code(o), level_base, htype.value, chunk_size, ws_ptr, ws_bytes,
+        _lib.dtype_code(o), level_base, htype.value, chunk_size,
+        1 if qk_l2norm_scale is not None else 0,
+        float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
         _lib.stream_handle(dev))
     _lib.check(st)
     return g_cumsum, o, Aw, Au, ht
@@ -110,8 +119,14 @@ def chunkwise_bwd(
     level_base: int,
     htype: HType,
     chunk_size: int,
+    *,
+    qk_l2norm_scale: Optional[float] = None,
 ):
     """Log-linear GDN backward (chunkwise_hgdn.py:791-1222).
+
+    With ``qk_l2norm_scale`` (as in :func:`chunkwise_fwd`) q and k are the raw
+    inputs and dq, dk come back w.r.t. them: the kernels apply the l2norm
+    chain rule (kernel.py:24-29, 224-225) before storing them.
 
     ``g`` is the forward's chunk-local cumsum.  Returns (dq, dk, dv, db, dg, dl):
     dq / dk / dv / db in the dtypes of q / k / v / b, dg (w.r.t. the per-step g)
@@ -143,7 +158,9 @@ def chunkwise_bwd(
         _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
         _lib.ptr(db), _lib.ptr(dg), _lib.ptr(dl), B, T, H, K, V, L, _lib.dtype_code(q),
         _lib.dtype_code(b), _lib.dtype_code(l), _lib.dtype_code(do), level_base, htype.value,
-        chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
+        chunk_size, 1 if qk_l2norm_scale is not None else 0,
+        float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
+        _lib.stream_handle(dev))
     _lib.check(st)
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(q.dtype)

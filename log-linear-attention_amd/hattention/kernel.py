@@ -37,33 +37,6 @@ def input_guard(fn):
     return wrapper
 
 
-def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """x / sqrt(||x||^2 + eps) over the last dim in fp32, cast back to x.dtype
-    (fla.modules.l2norm.l2norm_fwd, used at kernel.py:20-23, 110-111)."""
-    xf = x.float()
-    return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)).to(x.dtype)
-
-
-def l2norm_and_scale_fwd(x: torch.Tensor, scale: float) -> torch.Tensor:
-    """kernel.py:20-23."""
-    return l2norm_fwd(x) * scale
-
-
-def l2norm_bwd(x: torch.Tensor, dy: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """Gradient of y = x / sqrt(||x||^2 + eps): dx = r (dy - y (y . dy)), r =
-    (||x||^2 + eps)^-1/2, in fp32, cast to x.dtype (fla.modules.l2norm.l2norm_bwd,
-    used at kernel.py:24-29, 224-225)."""
-    xf, dyf = x.float(), dy.float()
-    r = torch.rsqrt((xf * xf).sum(-1, keepdim=True) + eps)
-    y = xf * r
-    return (r * (dyf - y * (y * dyf).sum(-1, keepdim=True))).to(x.dtype)
-
-
-def l2norm_and_scale_bwd(x: torch.Tensor, dy: torch.Tensor, scale: float) -> torch.Tensor:
-    """kernel.py:24-29: gradient of l2norm(x) * scale."""
-    return l2norm_bwd(x, dy.float() * scale)
-
-
 class HAttentionFunction(torch.autograd.Function):
     """kernel.py:32-244."""
 
@@ -95,10 +68,11 @@ class HAttentionFunction(torch.autograd.Function):
             if scale is None:
                 raise NotImplementedError
             from hattention import chunkwise_hgdn as _hg
+            # q * scale / ||q|| and k / ||k|| are formed inside the kernels
             g, o, Aw, Au, _ = _hg.chunkwise_fwd(
-                q=l2norm_and_scale_fwd(q, scale=scale), k=l2norm_fwd(k), v=v, b=b, g=g, l=l,
-                head_first=head_first, level_base=level_base, htype=htype,
-                chunk_size=chunk_sizes[0], output_final_state=False)
+                q=q, k=k, v=v, b=b, g=g, l=l, head_first=head_first, level_base=level_base,
+                htype=htype, chunk_size=chunk_sizes[0], output_final_state=False,
+                qk_l2norm_scale=scale)
         else:
             # MAMBA2 with chunkwise=False is the reference's parallel.py path.
             raise NotImplementedError("only the chunkwise path is implemented on MI355X")
@@ -136,12 +110,11 @@ class HAttentionFunction(torch.autograd.Function):
             if ctx.scale is None:
                 raise NotImplementedError
             from hattention import chunkwise_hgdn as _hg
+            # the kernels normalise q, k and apply the l2norm chain rule to dq, dk
             dq, dk, dv, db, dg, dl = _hg.chunkwise_bwd(
-                q=l2norm_and_scale_fwd(q, scale=ctx.scale), k=l2norm_fwd(k), v=v, b=b, g=g, l=l,
-                Aw=Aw, Au=Au, do=do, head_first=ctx.head_first, level_base=ctx.level_base,
-                htype=ctx.htype, chunk_size=ctx.chunk_sizes[0])
-            dq = l2norm_and_scale_bwd(q, dq, scale=ctx.scale)
-            dk = l2norm_bwd(k, dk)
+                q=q, k=k, v=v, b=b, g=g, l=l, Aw=Aw, Au=Au, do=do, head_first=ctx.head_first,
+                level_base=ctx.level_base, htype=ctx.htype, chunk_size=ctx.chunk_sizes[0],
+                qk_l2norm_scale=ctx.scale)
         else:
             raise NotImplementedError
         return (dq.to(q), dk.to(k), dv.to(v), db.to(b) if b is not None else None,
@@ -201,9 +174,9 @@ class HAttentionPrefillFunction(torch.autograd.Function):
                 raise NotImplementedError
             from hattention import chunkwise_hgdn as _hg
             _, o, _, _, h = _hg.chunkwise_fwd(
-                q=l2norm_and_scale_fwd(q, scale=scale), k=l2norm_fwd(k), v=v, b=b, g=g, l=l,
-                head_first=head_first, level_base=level_base, htype=htype,
-                chunk_size=chunk_size, output_final_state=True)
+                q=q, k=k, v=v, b=b, g=g, l=l, head_first=head_first, level_base=level_base,
+                htype=htype, chunk_size=chunk_size, output_final_state=True,
+                qk_l2norm_scale=scale)
         else:
             raise NotImplementedError
         if h is None:

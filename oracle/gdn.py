@@ -224,6 +224,16 @@ def l2norm(x, eps: float = 1e-6):
     return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
 
 
+def l2norm_scale_bwd(x, dy, scale: float = 1.0, eps: float = 1e-6):
+    """Closed-form gradient of y = l2norm(x) * scale (fla l2norm_bwd as used at
+    kernel.py:24-29, 224-225): with r = (sum x^2 + eps)^-1/2 and u = x r,
+    dx = r scale (dy - u (u . dy)).  The GDN backward kernel applies this form
+    to dq (scale = the attention scale) and dk (scale = 1)."""
+    r = torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
+    u = x * r
+    return r * scale * (dy - u * (u * dy).sum(-1, keepdim=True))
+
+
 def hattention_gdn_fwd(q, k, v, beta, g, l, scale: Optional[float] = None, chunk_size: int = 64):
     """HAttentionFunction.forward, GDELTA branch (kernel.py:100-123): q <- l2norm(q) * scale,
     k <- l2norm(k), then chunkwise_hgdn.chunkwise_fwd; returns o."""

@@ -142,7 +142,7 @@ def _gdn_bwd(**kw):
     return lib.hattn_gdn_chunkwise_bwd(p, p, p, p, p, p, None, None, p, p, p, p, p, p, p,
                                        a["B"], a["T"], a["H"], a["K"], a["V"], a["L"], a["dq"],
                                        a["db"], a["dl"], a["do"], a["base"], a["htype"],
-                                       a["chunk"], p, a["ws"], None)
+                                       a["chunk"], 0, 1.0, p, a["ws"], None)
 
 
 @pytest.mark.parametrize("kw,code", [

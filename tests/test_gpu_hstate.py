@@ -317,15 +317,18 @@ def test_north_star_prefill_then_decode_matches_chunkwise():
 
 
 @pytest.mark.parametrize("hs", ["MAMBA2", "GDELTA"])
-def test_register_kernel_matches_lds_kernel(hs):
+@pytest.mark.parametrize("L", [7, 18])
+def test_register_kernel_matches_lds_kernel(hs, L):
     """A state whose storage is not 16-byte aligned runs the register kernel
-    (no LDS staging); both kernels give the same outputs and states, and the
-    GDELTA case is also checked against the oracle."""
+    (no LDS staging); both kernels give the same outputs and states, and both
+    are checked against the recurrent oracle.  L = 18 runs the kernels' 32-level
+    instances (16 < L <= 32, states of more than 32K tokens)."""
     from hattention.base import HType, HStruct
     from hattention.kernel import hattention_step
     from hattention.recurrent import HState
     hstruct = HStruct[hs]
-    B, T, H, K, V, L = 1, 40, 2, 128, 64, 7
+    B, T, H, K, V = 1, 40, 2, 128, 64
+    print(f"[hstate] register vs LDS kernel {hs} L={L}", flush=True)
     if hstruct == HStruct.MAMBA2:
         q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=360, dtype=torch.float32)
         beta, scale, norm = None, None, False
@@ -353,3 +356,7 @@ def test_register_kernel_matches_lds_kernel(hs):
         qn, kn = _gdn_normed(q, k, scale)
         o_ref = D.recurrent_fwd(qn, kn, v.double(), beta.double(), g.double(), l.double())
         _check_out(torch.stack(o1, 1), o_ref, torch.float32, "gdn K=128")
+    else:
+        o_ref = M.recurrent_fwd(*(x.double() for x in (q, k, v, g, l)))
+        _check_out(torch.stack(o1, 1), o_ref, torch.float32, "mamba2 K=128")
+    _check_out(torch.stack(o2, 1), o_ref, torch.float32, "register kernel")

@@ -473,6 +473,66 @@ def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, back
                          "algorithmic_flops": flops}}
 
 
+GDN_C3 = (4, 8192, 16, 128, 128, 14)
+
+
+def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3):
+    """Cold-cache medians of the log-linear Gated DeltaNet chunkwise forward and
+    forward + backward (chunkwise_hgdn.chunkwise_fwd / chunkwise_bwd) at BASELINE
+    config 3, MFMA roofline by the algorithmic FLOPs (backward counted as twice
+    the forward, the usual convention).  Returns one record per key (None for
+    keys not asked for)."""
+    from hattention.base import HType
+    from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd, chunkwise_bwd as gdn_bwd
+    GB, GT, GH, GK, GV, GL = shape
+    gq, gk, gv, gbeta, gg, gl = make_gdn_inputs(GB, GT, GH, GK, GV, GL, device=dev)
+    gdo = torch.randn(GB, GT, GH, GV, device=dev, dtype=torch.bfloat16)
+    gcfg = {"workload": "log-linear Gated DeltaNet chunkwise path (chunkwise_hgdn, "
+                        "BASELINE config 3)",
+            "batch": GB, "seq_len": GT, "heads": GH, "dk": GK, "dv": GV, "levels": GL}
+
+    def gdn_step():
+        return gdn_fwd(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64, False)
+
+    def gdn_fb_step():
+        gc, _, Aw, Au, _ = gdn_step()
+        return gdn_bwd(gq, gk, gv, gbeta, gc, gl, Aw, Au, gdo, False, 2, HType.WEAK, 64)
+
+    gfl = gdn_fwd_flops(GB, GT, GH, GK, GV)
+    out = {}
+    for fn, key in ((gdn_step, "fwd"), (gdn_fb_step, "fwd_bwd")):
+        if key not in keys:
+            out[key] = None
+            continue
+        for _ in range(2):
+            fn()
+        times = time_cold(fn, reps, stream, evict)
+        t_g = _median(times)
+        fl = gfl if key == "fwd" else 3 * gfl
+        out[key] = {"value": GB * GT / t_g, "unit": "tokens/s", "median_us": t_g * 1e6,
+                    "reps": reps, "config": gcfg,
+                    "roofline": {"bound": "mfma", "achieved": fl / t_g / 1e12,
+                                 "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                                 "frac": fl / t_g / MFMA_BF16_PEAK, "algorithmic_flops": fl}}
+    del gq, gk, gv, gbeta, gg, gl, gdo
+    return out["fwd"], out["fwd_bwd"]
+
+
+NS_SHAPE = (NS["B"], NS["T"], NS["H"], NS["K"], NS["V"], NS["L"])
+ONLY_CASES = {
+    "ns_fwd": None,      # the headline loop alone (--fwd-only --no-cpu-baseline)
+    "ns_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "north star fwd+bwd", NS_SHAPE, torch.bfloat16, dev, st, ev, n, w, backward=True),
+    "c2_fwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "C2", (1, 32768, 32, 64, 128, 16), torch.bfloat16, dev, st, ev, n, w),
+    "c4_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "C4 fwd+bwd", (8, 8192, 24, 64, 64, 14), torch.bfloat16, dev, st, ev, n, w,
+        backward=True),
+    "gdn_fwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd",))[0],
+    "gdn_fwd_bwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd_bwd",))[1],
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -485,6 +545,9 @@ def main():
                     help="also run a 2 GiB read-only kernel (sum) and a 2 GiB write-only kernel "
                          "(fill), larger than the 256 MB MALL, so a counter run can scale "
                          "FETCH_SIZE / WRITE_SIZE by a known traffic")
+    ap.add_argument("--only", choices=sorted(ONLY_CASES),
+                    help="time one case alone (cold-cache median over --steps reps) and print "
+                         "its record: the driver of the per-kernel profiles")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -501,6 +564,13 @@ def main():
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
+    if args.only and args.only != "ns_fwd":
+        evict = Evictor(dev)
+        rec = ONLY_CASES[args.only](dev, stream, evict, args.steps, args.warmup)
+        print(json.dumps({"case": args.only, "record": rec}), flush=True)
+        return
+    if args.only == "ns_fwd":
+        args.fwd_only, args.no_cpu_baseline = True, True
     B, T, H, K, V, L = (NS[x] for x in ("B", "T", "H", "K", "V", "L"))
     q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=1000, device=dev)
     evict = Evictor(dev)
@@ -552,41 +622,8 @@ def main():
                                              backward=bw))
             torch.cuda.empty_cache()
 
-        # log-linear Gated DeltaNet at BASELINE config 3 (MFMA-bound path): forward,
-        # and forward + backward (chunkwise_hgdn.chunkwise_fwd / chunkwise_bwd)
-        from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd, chunkwise_bwd as gdn_bwd
-        GB, GT, GH, GK, GL = 4, 8192, 16, 128, 14
-        gq, gk, gv, gbeta, gg, gl = make_gdn_inputs(GB, GT, GH, GK, GK, GL, device=dev)
-        gdo = torch.randn(GB, GT, GH, GK, device=dev, dtype=torch.bfloat16)
-        gcfg = {"workload": "log-linear Gated DeltaNet chunkwise path (chunkwise_hgdn, "
-                            "BASELINE config 3)",
-                "batch": GB, "seq_len": GT, "heads": GH, "dk": GK, "dv": GK, "levels": GL}
-
-        def gdn_step():
-            return gdn_fwd(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64, False)
-
-        def gdn_fb_step():
-            gc, _, Aw, Au, _ = gdn_step()
-            return gdn_bwd(gq, gk, gv, gbeta, gc, gl, Aw, Au, gdo, False, 2, HType.WEAK, 64)
-
-        gfl = gdn_fwd_flops(GB, GT, GH, GK, GK)
-        for fn, key in ((gdn_step, "fwd"), (gdn_fb_step, "fwd_bwd")):
-            for _ in range(2):
-                fn()
-            times = time_cold(fn, reps, stream, evict)
-            t_g = _median(times)
-            # backward counted as twice the forward (the usual convention)
-            fl = gfl if key == "fwd" else 3 * gfl
-            rec = {"value": GB * GT / t_g, "unit": "tokens/s", "median_us": t_g * 1e6,
-                   "reps": reps, "config": gcfg,
-                   "roofline": {"bound": "mfma", "achieved": fl / t_g / 1e12,
-                                "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                                "frac": fl / t_g / MFMA_BF16_PEAK, "algorithmic_flops": fl}}
-            if key == "fwd":
-                gdn = rec
-            else:
-                gdn_fb = rec
-        del gq, gk, gv, gbeta, gg, gl, gdo
+        # log-linear Gated DeltaNet at BASELINE config 3 (MFMA-bound path)
+        gdn, gdn_fb = gdn_records(dev, stream, evict, reps)
         torch.cuda.empty_cache()
         dec = decode_bench(dev, stream, 128, 8)
         layer = layer_bench(dev, stream, max(2, args.steps // 5), 2)

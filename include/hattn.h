@@ -166,9 +166,11 @@ size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, i
  *          given, as the reference's chunkwise_fwd does
  *   workspace >= hattn_gdn_chunkwise_fwd_workspace(...) bytes
  *
- * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64
- * -> HATTN_ERR_VALUE; (K, V) in {(64, 64), (128, 128)}, T <= 64 * 2^7, q/k/v
- * bf16, beta / l in {BF16, FP32}, o bf16 -> HATTN_ERR_NOT_IMPLEMENTED.
+ * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64,
+ * T * H * max(K, V) < 2^31 -> HATTN_ERR_VALUE; K in {64, 128, 192, 256} (the
+ * reference's limit is K <= 256, chunkwise_hgdn.py:600-601), any V multiple of
+ * 64, T <= 64 * 2^8 (16384), q/k/v bf16, beta / l in {BF16, FP32}, o bf16 ->
+ * HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const void* beta,
                             const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
@@ -178,9 +180,10 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
                             float qk_scale, void* workspace, size_t workspace_bytes,
                             void* stream);
 
-/* Workspace bytes of hattn_gdn_chunkwise_fwd (q_new, k_new, w_new, u in bf16
- * and the fp32 intra-chunk output).  No counterpart in the reference, which
- * allocates these with torch inside chunkwise_fwd (chunkwise_hgdn.py:636-642). */
+/* Workspace bytes of hattn_gdn_chunkwise_fwd (q_new, w_new, per-chunk transposed
+ * k_new, u and the intra-chunk matrix P, all bf16).  No counterpart in the
+ * reference, which allocates these with torch inside chunkwise_fwd
+ * (chunkwise_hgdn.py:636-642). */
 size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int L);
 
 /*
@@ -203,7 +206,9 @@ size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int 
  *   kernel.py:24-29, 224-225 applied inside the kernel)
  *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
  *
- * Constraints as hattn_gdn_chunkwise_fwd; do bf16 -> else HATTN_ERR_NOT_IMPLEMENTED.
+ * Constraints as hattn_gdn_chunkwise_fwd, except (K, V) in {(64, 64), (128, 128)}
+ * and T <= 64 * 2^7 (8192) -> HATTN_ERR_NOT_IMPLEMENTED; do bf16 -> else
+ * HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,
                             const float* g_cumsum, const void* l, const void* Aw, const void* Au,
@@ -213,8 +218,8 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
                             int chunk_size, int l2norm_qk, float qk_scale, void* workspace,
                             size_t workspace_bytes, void* stream);
 
-/* Workspace bytes of hattn_gdn_chunkwise_bwd: the recomputed q_new, k_new, w_new,
- * u (bf16), every level's state at every chunk start (bf16), and the fp32
+/* Workspace bytes of hattn_gdn_chunkwise_bwd: the recomputed q_new, k_new (token-major
+ * and per-chunk transposed), w_new, u (bf16), every level's state at every chunk start (bf16), and the fp32
  * per-V-slice partial gradients of the level scan.  No counterpart in the
  * reference, which allocates h / dh and its temporaries with torch inside
  * chunkwise_bwd (chunkwise_hgdn.py:894-913). */

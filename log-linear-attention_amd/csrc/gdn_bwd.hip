@@ -44,7 +44,7 @@
 
 hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* v,
                                       const void* beta, const float* gcum, const void* l,
-                                      __bf16* qn, __bf16* kn, __bf16* wn, __bf16* un,
+                                      __bf16* qn, __bf16* kn, __bf16* knT, __bf16* wn, __bf16* un,
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
                                       int nlev, int dt_b, int dt_l, int norm_qk, float scale,
                                       hipStream_t stream, int* unsupported);
@@ -74,7 +74,7 @@ struct GdnBscanSmem {
   __bf16 dhs[kBVs * LK];     // dh_e after the chunk, [v][k]
   __bf16 dvn[kBVs * kLd64];  // dV_new_e, [v][t]
   __bf16 vn[kBVs * kLd64];   // V_new_e, [v][t]
-  float lam[kGMaxLev][kGC];  // lambda[t, 7 + e]
+  float lam[kGBwdMaxLev][kGC];  // lambda[t, 7 + e]
   float dlr[2][kGC];         // dlambda row sums of the two 16-column halves
   float red[8];
 };
@@ -106,9 +106,9 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
   const size_t BTH = (size_t)B * T * H;
   const int v0 = vb * kBVs;
 
-  floatx4 dh[kGMaxLev][TPW];
+  floatx4 dh[kGBwdMaxLev][TPW];
 #pragma unroll
-  for (int e = 0; e < kGMaxLev; ++e)
+  for (int e = 0; e < kGBwdMaxLev; ++e)
 #pragma unroll
     for (int j = 0; j < TPW; ++j) dh[e][j] = zero4();
 
@@ -149,8 +149,9 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
       pu = *(const u32x4*)(un + off);
       pdo = *(const u32x4*)(dO + off);
     }
-    const int le = min(tid, nlev * kGC - 1);
-    plam = to_f32<TL>(l[((t0 + le / nlev) * H + h) * L + 7 + le % nlev]);
+    const int nl1 = nlev > 0 ? nlev : 1;   // T = 64 has no inter-chunk level
+    const int le = min(tid, nl1 * kGC - 1);
+    plam = to_f32<TL>(l[((t0 + le / nl1) * H + h) * L + min(7 + le % nl1, L - 1)]);
     peL = gcum[(t0 + kGC - 1) * H + h];
   };
   if (kPrefTiles) fetch_tiles(NT - 1);
@@ -999,7 +1000,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 // host launcher
 // ---------------------------------------------------------------------------
 struct GdnBwdWs {
-  __bf16 *qn, *kn, *wn, *un, *hs;
+  __bf16 *qn, *kn, *knT, *wn, *un, *hs;
   float *dq_p, *dw_p, *dk_p, *du, *dl_p, *del_p;
   size_t bytes;
 };
@@ -1015,6 +1016,7 @@ inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V,
   const size_t nl = nlev > 0 ? (size_t)nlev : 1;
   w.qn = (__bf16*)(p + off); off += balign(n * K * 2);
   w.kn = (__bf16*)(p + off); off += balign(n * K * 2);
+  w.knT = (__bf16*)(p + off); off += balign(n * K * 2);
   w.wn = (__bf16*)(p + off); off += balign(n * K * 2);
   w.un = (__bf16*)(p + off); off += balign(n * V * 2);
   w.hs = (__bf16*)(p + off); off += balign((size_t)B * H * NT * nl * V * K * 2);
@@ -1065,6 +1067,8 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
 
 }  // namespace hattn
 
+int hattn_gdn_bwd_max_levels() { return hattn::kGBwdMaxLev; }
+
 size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
   return hattn::gdn_bwd_ws_layout(nullptr, B, T, H, K, V, nlev).bytes;
 }
@@ -1078,7 +1082,7 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
   using namespace hattn;
   *unsupported = 0;
   const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
-  hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.wn, w.un, w.hs,
+  hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.knT, w.wn, w.un, w.hs,
                                             B, T, H, K, V, L, nlev, dt_b, dt_l, norm_qk, scale,
                                             stream, unsupported);
   if (e != hipSuccess || *unsupported) return e;

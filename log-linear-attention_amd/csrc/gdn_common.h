@@ -6,8 +6,9 @@ namespace hattn {
 
 constexpr int kGC = 64;       // chunk length
 constexpr int kLd64 = 72;     // LDS row stride of 64-wide bf16 tiles
-constexpr int kGMaxLev = 7;   // inter-chunk levels held by the scans (T <= 64 * 2^7)
-constexpr int kBVs = 32;      // V columns per scan workgroup
+constexpr int kGMaxLev = 8;   // inter-chunk levels of the forward scan (T <= 64 * 2^8)
+constexpr int kGBwdMaxLev = 7;   // inter-chunk levels of the backward scan (T <= 64 * 2^7)
+constexpr int kBVs = 32;      // V columns per backward-scan workgroup
 constexpr int kLM = 65;       // row stride of 64 x 64 fp32 LDS matrices
 
 // 16-byte units of a row-major [NR][N] bf16 tile, 256 threads (threads
@@ -42,7 +43,7 @@ __device__ __forceinline__ void g2s_tile(const __bf16* __restrict__ src, size_t 
 // NTHR threads call it together; waves 0..3 do the block work (the others only
 // take part in the zero fill and the barriers).
 template <int NTHR = 256>
-__device__ inline void tri_inv64(const float* A, float* X, float (*t1all)[16 * 17]) {
+__device__ __forceinline__ void tri_inv64(const float* A, float* X, float (*t1all)[16 * 17]) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   for (int u = tid; u < 6 * 256; u += NTHR) {   // the six upper 16 x 16 blocks
@@ -95,6 +96,116 @@ __device__ inline void tri_inv64(const float* A, float* X, float (*t1all)[16 * 1
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------
+// X = (I + A)^-1 on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32 products,
+// fp32 accumulation) for a strictly lower-triangular 64 x 64 fp32 A.
+//   Diagonal 16 x 16 blocks, N = A_ii nilpotent (N^16 = 0):
+//     (I + N)^-1 = sum_{k < 16} (-N)^k = (I - N)(I + N^2)(I + N^4)(I + N^8)
+//   (the factors commute), from N^2, N^4, N^8 and three more products.
+//   Off-diagonal blocks by block forward substitution down each block column:
+//     X_ij = -X_ii sum_{m=j}^{i-1} A_im X_mj,
+//   which only needs X_mj of the same column (wave j) and the diagonal blocks.
+// Wave w < 4 owns diagonal block w and block column w; every wave takes part
+// in the zero fill of the upper blocks and in the two barriers.  scratch holds
+// 3 x 16 x 17 floats per wave (waves 0..3).  Starts and ends with the
+// caller's data in LDS and ends with a barrier.
+// ---------------------------------------------------------------------------
+constexpr int kInvScratchFloats = 4 * 3 * 16 * 17;
+
+// C += L R for 16 x 16 fp32 blocks in LDS (row-major, strides ldl, ldr); C and
+// the result in the D layout (lane (lq, ln): rows 4 lq + i, column ln).
+__device__ __forceinline__ floatx4 mm16_f32(const float* L, int ldl, const float* R, int ldr,
+                                            floatx4 c) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  float a[4], b[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    a[s] = L[ln * ldl + 4 * s + lq];     // A_s[m = ln][k = lq] = L[ln][4s + lq]
+    b[s] = R[(4 * s + lq) * ldr + ln];   // B_s[k = lq][n = ln] = R[4s + lq][ln]
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+__device__ __forceinline__ void st16_f32(float* D, int ld, floatx4 d) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) D[(4 * lq + i) * ld + ln] = d[i];
+}
+
+// LDS writes of this wave visible to its later LDS reads (the wave's LDS
+// operations execute in order; the fences keep the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <int NTHR>
+__device__ __forceinline__ void tri_inv64_mfma(const float* A, float* X, float* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  for (int u = tid; u < 6 * 256; u += NTHR) {   // the six upper 16 x 16 blocks
+    const int blk = u >> 8, e = u & 255;
+    const int bi = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
+    const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
+    X[(16 * bi + (e >> 4)) * kLM + 16 * bj + (e & 15)] = 0.f;
+  }
+  if (w < 4) {
+    constexpr int LS = 17;
+    float* S0 = scratch + w * 3 * 16 * LS;
+    float* S1 = S0 + 16 * LS;
+    float* S2 = S1 + 16 * LS;
+    const float* N = A + 16 * w * kLM + 16 * w;
+    floatx4 p = mm16_f32(N, kLM, N, kLM, zero4());           // N^2
+    st16_f32(S0, LS, p);
+    wave_lds_sync();
+    p = mm16_f32(S0, LS, S0, LS, zero4());                    // N^4
+    st16_f32(S1, LS, p);
+    wave_lds_sync();
+    p = mm16_f32(S1, LS, S1, LS, zero4());                    // N^8
+    st16_f32(S2, LS, p);
+    wave_lds_sync();
+    // R1 = (I - N)(I + N^2) = I - N + N^2 - N N^2
+    floatx4 r = mm16_f32(N, kLM, S0, LS, zero4());
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * lq + i;
+      r[i] = (row == ln ? 1.f : 0.f) - N[row * kLM + ln] + S0[row * LS + ln] - r[i];
+    }
+    wave_lds_sync();
+    st16_f32(S0, LS, r);
+    wave_lds_sync();
+    r = mm16_f32(S0, LS, S1, LS, r);                          // R2 = R1 (I + N^4)
+    wave_lds_sync();
+    st16_f32(S1, LS, r);
+    wave_lds_sync();
+    r = mm16_f32(S1, LS, S2, LS, r);                          // R3 = R2 (I + N^8)
+    st16_f32(X + 16 * w * kLM + 16 * w, kLM, r);
+  }
+  __syncthreads();
+  if (w < 3) {
+    constexpr int LS = 17;
+    float* S0 = scratch + w * 3 * 16 * LS;
+    const int j = w;
+    for (int i = j + 1; i < 4; ++i) {
+      floatx4 t = zero4();
+      for (int m = j; m < i; ++m)
+        t = mm16_f32(A + 16 * i * kLM + 16 * m, kLM, X + 16 * m * kLM + 16 * j, kLM, t);
+      st16_f32(S0, LS, t);
+      wave_lds_sync();
+      floatx4 x = mm16_f32(X + 16 * i * kLM + 16 * i, kLM, S0, LS, zero4());
+#pragma unroll
+      for (int q = 0; q < 4; ++q) x[q] = -x[q];
+      wave_lds_sync();
+      st16_f32(X + 16 * i * kLM + 16 * j, kLM, x);
+      wave_lds_sync();
+    }
+  }
+  __syncthreads();
 }
 
 // In-place l2 normalisation of the 64 rows of a staged bf16 tile [64][LD] with

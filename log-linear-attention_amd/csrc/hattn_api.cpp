@@ -25,6 +25,8 @@ hipError_t hattn_mamba2_fwd_static_scratch(void** ptr);
 int hattn_mamba2_fwd_max_levels(int x3);
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V);
 int hattn_gdn_fwd_max_levels();
+int hattn_gdn_fwd_supports_k(int K);
+int hattn_gdn_bwd_max_levels();
 hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
@@ -328,14 +330,16 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
   if (K > 256) return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d > 256", K);
   if (K % 64 != 0 || V % 64 != 0)
     return fail(HATTN_ERR_VALUE, "K=%d, V=%d and BK, BV could be 64", K, V);
-  if (!((K == 128 && V == 128) || (K == 64 && V == 64)))
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (the MI355X GDN kernels support 64/64, 128/128)",
-                K, V);
+  if (!hattn_gdn_fwd_supports_k(K))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d (the MI355X GDN forward supports 64, 128, 192, 256)",
+                K);
   const int nlev = ceil_log2(T / 64);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
   if (nlev > hattn_gdn_fwd_max_levels())
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_fwd_max_levels());
+  if ((size_t)T * H * (K > V ? K : V) >= ((size_t)1 << 31))
+    return fail(HATTN_ERR_VALUE, "T * H * max(K, V) = %zu exceeds 2^31", (size_t)T * H * (K > V ? K : V));
   if (dtype_qkv != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v dtype code %d (bf16 required)", dtype_qkv);
   if (!q || !k || !v || !beta || !g || !l || !o || !g_cumsum || !Aw || !Au)
@@ -384,13 +388,13 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
   if (K % 64 != 0 || V % 64 != 0)
     return fail(HATTN_ERR_VALUE, "K=%d, V=%d and BK, BV could be 64", K, V);
   if (!((K == 128 && V == 128) || (K == 64 && V == 64)))
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (the MI355X GDN kernels support 64/64, 128/128)",
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d V=%d (the MI355X GDN backward supports 64/64, 128/128)",
                 K, V);
   const int nlev = ceil_log2(T / 64);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
-  if (nlev > hattn_gdn_fwd_max_levels())
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_fwd_max_levels());
+  if (nlev > hattn_gdn_bwd_max_levels())
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_bwd_max_levels());
   if (dtype_qkv != HATTN_BF16 || dtype_do != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v/do dtype codes %d/%d (bf16 required)", dtype_qkv,
                 dtype_do);

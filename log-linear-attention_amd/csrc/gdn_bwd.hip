@@ -196,7 +196,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     for (int j = 0; j < TPW; ++j) cur[j] = dh[E][j]; \
     break;
           HATTN_DH_GET(0) HATTN_DH_GET(1) HATTN_DH_GET(2) HATTN_DH_GET(3) HATTN_DH_GET(4)
-          HATTN_DH_GET(5) HATTN_DH_GET(6)
+          HATTN_DH_GET(5) HATTN_DH_GET(6) HATTN_DH_GET(7)
 #undef HATTN_DH_GET
         }
         const int per = 2 << e;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     for (int j = 0; j < TPW; ++j) dh[E][j] = cur[j]; \
     break;
           HATTN_DH_PUT(0) HATTN_DH_PUT(1) HATTN_DH_PUT(2) HATTN_DH_PUT(3) HATTN_DH_PUT(4)
-          HATTN_DH_PUT(5) HATTN_DH_PUT(6)
+          HATTN_DH_PUT(5) HATTN_DH_PUT(6) HATTN_DH_PUT(7)
 #undef HATTN_DH_PUT
         }
         __syncthreads();
@@ -1102,6 +1102,8 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
                                                 dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
   }
   HATTN_GDN_B(128, 128)
+  HATTN_GDN_B(128, 64)
+  HATTN_GDN_B(64, 128)
   HATTN_GDN_B(64, 64)
 #undef HATTN_GDN_B
   *unsupported = 1;

@@ -7,7 +7,7 @@ namespace hattn {
 constexpr int kGC = 64;       // chunk length
 constexpr int kLd64 = 72;     // LDS row stride of 64-wide bf16 tiles
 constexpr int kGMaxLev = 8;   // inter-chunk levels of the forward scan (T <= 64 * 2^8)
-constexpr int kGBwdMaxLev = 7;   // inter-chunk levels of the backward scan (T <= 64 * 2^7)
+constexpr int kGBwdMaxLev = 8;   // inter-chunk levels of the backward scan (T <= 64 * 2^8)
 constexpr int kBVs = 32;      // V columns per backward-scan workgroup
 constexpr int kLM = 65;       // row stride of 64 x 64 fp32 LDS matrices
 

@@ -8,7 +8,8 @@ Same names, arguments and return tuples as hattention/chunkwise_hgdn.py:
 
 Validation follows the reference (``ValueError`` for T % 64 and K / V not
 multiples of the block options, ``NotImplementedError`` for K > 256 and modes
-outside the weak base-2 hierarchy).  Grouped q / k are expanded per head
+outside the weak base-2 hierarchy).  The backward kernels take K in {64, 128}
+(``NotImplementedError`` from the C-ABI otherwise) and V in blocks of 128.  Grouped q / k are expanded per head
 before the kernels like the reference (chunkwise_hgdn.py:614-623) and their
 gradients summed over the group (chunkwise_hgdn.py:1208-1215).  There is no
 CPU path.
@@ -21,6 +22,7 @@ from hattention import _lib
 from hattention.base import HType, get_num_levels, ceil_log
 
 CHUNK = 64
+VB = 128   # V columns per backward launch
 
 
 def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
@@ -144,24 +146,44 @@ def chunkwise_bwd(
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
     do = do.to(v.dtype).contiguous()
-    dq = torch.empty(B, T, H, K, dtype=q.dtype, device=dev)
-    dk = torch.empty(B, T, H, K, dtype=k.dtype, device=dev)
-    dv = torch.empty_like(v)
-    db = torch.empty_like(b)
-    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
-    dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
     lib = _lib.load()
-    ws, ws_ptr, ws_bytes = _lib.workspace(
-        lib.hattn_gdn_chunkwise_bwd_workspace(B, T, H, K, V, L), dev)
-    st = lib.hattn_gdn_chunkwise_bwd(
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
-        _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
-        _lib.ptr(db), _lib.ptr(dg), _lib.ptr(dl), B, T, H, K, V, L, _lib.dtype_code(q),
-        _lib.dtype_code(b), _lib.dtype_code(l), _lib.dtype_code(do), level_base, htype.value,
-        chunk_size, 1 if qk_l2norm_scale is not None else 0,
-        float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
-        _lib.stream_handle(dev))
-    _lib.check(st)
+    # The gradients are sums over independent column blocks of V (each column of
+    # o depends on its column of v only): the kernels take V in {64, 128}, so a
+    # larger V runs block by block, dq / dk / db / dg / dl summed in fp32.
+    blocks = [(v0, min(v0 + VB, V)) for v0 in range(0, V, VB)]
+    dv = torch.empty_like(v)
+    acc = None
+    for v0, v1 in blocks:
+        vb = v if len(blocks) == 1 else v[..., v0:v1].contiguous()
+        dob = do if len(blocks) == 1 else do[..., v0:v1].contiguous()
+        Vb = v1 - v0
+        dq_b = torch.empty(B, T, H, K, dtype=q.dtype, device=dev)
+        dk_b = torch.empty(B, T, H, K, dtype=k.dtype, device=dev)
+        dv_b = dv if len(blocks) == 1 else torch.empty_like(vb)
+        db_b = torch.empty_like(b)
+        dg_b = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        dl_b = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
+        ws, ws_ptr, ws_bytes = _lib.workspace(
+            lib.hattn_gdn_chunkwise_bwd_workspace(B, T, H, K, Vb, L), dev)
+        st = lib.hattn_gdn_chunkwise_bwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(vb), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
+            _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(dob), _lib.ptr(dq_b), _lib.ptr(dk_b),
+            _lib.ptr(dv_b), _lib.ptr(db_b), _lib.ptr(dg_b), _lib.ptr(dl_b), B, T, H, K, Vb, L,
+            _lib.dtype_code(q), _lib.dtype_code(b), _lib.dtype_code(l), _lib.dtype_code(dob),
+            level_base, htype.value, chunk_size, 1 if qk_l2norm_scale is not None else 0,
+            float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
+            _lib.stream_handle(dev))
+        _lib.check(st)
+        del ws
+        if len(blocks) == 1:
+            dq, dk, db, dg, dl = dq_b, dk_b, db_b, dg_b, dl_b
+            break
+        dv[..., v0:v1] = dv_b
+        parts = (dq_b.float(), dk_b.float(), db_b.float(), dg_b, dl_b)
+        acc = parts if acc is None else tuple(a + p for a, p in zip(acc, parts))
+    if acc is not None:
+        dq, dk = acc[0].to(q.dtype), acc[1].to(k.dtype)
+        db, dg, dl = acc[2].to(b.dtype), acc[3], acc[4]
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(q.dtype)
         dk = dk.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(k.dtype)

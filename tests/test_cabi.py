@@ -150,11 +150,12 @@ def _gdn_bwd(**kw):
     (dict(L=7), _lib.HATTN_ERR_VALUE),              # L < 7 + ceil(log2(T/64))
     (dict(K=96, V=96), _lib.HATTN_ERR_VALUE),       # K, V multiples of 64
     (dict(K=320, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # K > 256
-    (dict(K=128, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(K=192, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # backward K in {64, 128}
+    (dict(K=64, V=192), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # V blocks of 64 / 128
     (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # do must be bf16
-    (dict(T=64 << 8, L=16), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > 7 inter-chunk levels
+    (dict(T=64 << 9, L=17), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > 8 inter-chunk levels
     (dict(ws=16), _lib.HATTN_ERR_VALUE),            # workspace too small
 ])
 def test_gdn_bwd_argument_checks(kw, code):

@@ -132,3 +132,29 @@ def test_autograd_function_l2norm_and_scale():
 def test_config3_full_size_bwd():
     # BASELINE config 3 shape: B=4 T=8192 H=16 dk=dv=128 L=14 bf16, fwd + custom bwd
     _run(4, 8192, 16, 128, 128, 14, seed=1003, rows=[(0, 0), (3, 15)])
+
+
+@pytest.mark.parametrize("K,V", [(128, 64), (64, 128), (128, 384), (64, 192)])
+def test_v_blocks(K, V):
+    """V in blocks of 128 / 64 through the host driver (chunkwise_hgdn.py:834-837
+    allows any V multiple of 64); the shared gradients are sums over the blocks."""
+    _run(1, 1024, 2, K, V, 11, seed=K + V)
+
+
+def test_eight_levels_bwd():
+    """T = 16384: eight inter-chunk levels (L = 15)."""
+    _run(1, 16384, 1, 64, 64, 15, seed=31)
+
+
+def test_head_dim_192_bwd_not_implemented():
+    """The backward kernels take K in {64, 128}; K = 192 raises instead of
+    returning wrong gradients."""
+    from hattention.chunkwise_hgdn import chunkwise_fwd, chunkwise_bwd
+    from hattention.base import HType
+    q, k, v, beta, g, l = make_gdn_inputs(1, 128, 1, 192, 64, 8, seed=3)
+    dev = torch.device("cuda:0")
+    xs = [x.to(dev) for x in (q, k, v, beta, g, l)]
+    gc, o, Aw, Au, _ = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, False)
+    with pytest.raises(NotImplementedError):
+        chunkwise_bwd(xs[0], xs[1], xs[2], xs[3], gc, xs[5], Aw, Au, torch.ones_like(o), False,
+                      2, HType.WEAK, 64)

@@ -1,4 +1,4 @@
-"""Log-linear Mamba-2 (HStruct.MAMBA2, HType.WEAK, level base 2): CPU oracle.
+"""Log-linear Mamba-2 (HStruct.MAMBA2, HType.WEAK and STRONG, level base 2): CPU oracle.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
@@ -40,6 +40,15 @@ Restatements (reference file:line):
   through torch.autograd; dg is w.r.t. the raw per-step g, which is what the
   reference returns after its reverse chunk-local cumsum (chunkwise.py:1596).
 
+Strong hierarchy (HType.STRONG): ``materialized_fwd(..., htype=STRONG)`` uses
+the strong level table (base.py:49-62 via oracle.levels), ``recurrent_fwd(...,
+htype=STRONG)`` the cascade of HState.cascade_strong (recurrent.py:56-74), and
+``chunked_strong_fwd`` the chunk decomposition the HIP strong kernel
+implements.  The first two restate the reference's two definitions of the
+strong hierarchy independently, and all three agree to 1e-12; a one-hot
+lambda with g == 0 is checked against a pair loop over the recursion and
+lambda == 1 against the plain SSD scan.
+
 Pinning: the four forward forms are structurally different algorithms and are
 checked against each other; ``ssd_scan_fwd`` (textbook) pins the lambda == 1
 case; lambda one-hot on one level is checked against a brute-force pair loop
@@ -51,7 +60,10 @@ from typing import Optional, Tuple
 
 import torch
 
-from oracle.levels import get_num_levels, levels_matrix, level_weak_recursive
+from oracle.levels import (get_num_levels, levels_matrix, level_weak_recursive,
+                           levels_matrix_strong, strong_intra_table, strong_subdiag_table)
+
+WEAK, STRONG = 0, 1   # HType values (hattention/base.py:12-14)
 
 
 def _expand_groups(x: torch.Tensor, H: int) -> torch.Tensor:
@@ -74,14 +86,16 @@ def _check(q, k, v, g, l):
 # --------------------------------------------------------------------------
 # 1. materialised H matrix (base.py:75-98, 334-349)
 # --------------------------------------------------------------------------
-def materialized_H(g: torch.Tensor, l: torch.Tensor) -> torch.Tensor:
+def materialized_H(g: torch.Tensor, l: torch.Tensor, htype: int = WEAK) -> torch.Tensor:
     """H[b, h, t, s] = l[b, t, h, level(t, s)] * prod_{u=s+1..t} exp(g[b, u, h]).
 
     base.py:87-96 builds the product of A = exp(g) over (s, t]; here the product
     is formed as exp of the difference of inclusive cumsums (identical math).
+    ``htype`` selects the weak or the strong level function (base.py:65-72).
     """
     B, T, H = g.shape
-    lev = torch.from_numpy(levels_matrix(T, default=0, clamp_min=0))
+    table = levels_matrix if htype == WEAK else levels_matrix_strong
+    lev = torch.from_numpy(table(T, default=0, clamp_min=0))
     G = torch.cumsum(g, dim=1)                               # [B, T, H]
     seg = G[:, :, None, :] - G[:, None, :, :]                # [B, t, s, H]
     mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
@@ -91,12 +105,12 @@ def materialized_H(g: torch.Tensor, l: torch.Tensor) -> torch.Tensor:
     return torch.exp(seg).permute(0, 3, 1, 2) * lam          # [B, H, t, s]
 
 
-def materialized_fwd(q, k, v, g, l) -> torch.Tensor:
+def materialized_fwd(q, k, v, g, l, htype: int = WEAK) -> torch.Tensor:
     """hattention_materialized (base.py:334-349): O = (H o Q K^T) V."""
     B, T, G, H, K, V, L = _check(q, k, v, g, l)
     q = _expand_groups(q, H)
     k = _expand_groups(k, H)
-    Hm = materialized_H(g, l)
+    Hm = materialized_H(g, l, htype)
     qkt = torch.einsum("bthd,bshd->bhts", q, k)
     return torch.einsum("bhts,bshd->bthd", Hm * qkt, v)
 
@@ -105,13 +119,15 @@ def materialized_fwd(q, k, v, g, l) -> torch.Tensor:
 # 2. Fenwick recurrent form (recurrent.py:9-216)
 # --------------------------------------------------------------------------
 class FenwickState:
-    """HState for HStruct.MAMBA2 / HType.WEAK (recurrent.py:9-54, 76-100).
+    """HState for HStruct.MAMBA2 (recurrent.py:9-54, 56-74, 76-100), weak or
+    strong cascade.
 
     ``states`` [B, H, K, V, L]; ``counts`` [L] tokens merged into each level.
     """
 
-    def __init__(self, B, H, K, V, L, dtype):
+    def __init__(self, B, H, K, V, L, dtype, htype: int = WEAK):
         self.L = L
+        self.htype = htype
         self.states = torch.zeros(B, H, K, V, L, dtype=dtype)
         self.counts = [0] * L
 
@@ -131,10 +147,37 @@ class FenwickState:
             else:
                 raise ValueError("level over capacity")
 
+    def cascade_strong(self):
+        """recurrent.py:56-74: a carry (state, count) walks up the levels; level
+        0, and a level whose count plus the carry's would exceed its capacity
+        2^max(level - 1, 0), hands its content on as the next carry and takes
+        the current one; otherwise the carry merges into the level and is
+        cleared.  A carry left after the top level is dropped."""
+        carry_s = torch.zeros_like(self.states[..., 0])
+        carry_c = 0
+        for level in range(self.L):
+            capacity = 2 ** max(level - 1, 0)
+            if self.counts[level] + carry_c > capacity or level == 0:
+                over_s, over_c = self.states[..., level].clone(), self.counts[level]
+                self.states[..., level] = carry_s
+                self.counts[level] = carry_c
+                carry_s, carry_c = over_s, over_c
+            else:
+                self.states[..., level] = self.states[..., level] + carry_s
+                self.counts[level] += carry_c
+                carry_s = torch.zeros_like(carry_s)
+                carry_c = 0
+
+    def cascade(self):
+        if self.htype == WEAK:
+            self.cascade_weak()
+        else:
+            self.cascade_strong()
+
     def insert(self, gate: torch.Tensor, value: torch.Tensor):
         """recurrent.py:76-94 (MAMBA2 branch): cascade, decay every level by the
         scalar gate, then the new token's k v^T becomes level 0."""
-        self.cascade_weak()
+        self.cascade()
         self.states = gate[:, :, None, None, None] * self.states
         self.states[..., 0] = value
         self.counts[0] += 1
@@ -144,12 +187,12 @@ class FenwickState:
         return torch.einsum("bhkvl,bhl->bhkv", self.states, lam)
 
 
-def recurrent_fwd(q, k, v, g, l, return_state: bool = False):
+def recurrent_fwd(q, k, v, g, l, return_state: bool = False, htype: int = WEAK):
     """hattention_recurrent (recurrent.py:169-216) for HStruct.MAMBA2."""
     B, T, G, H, K, V, L = _check(q, k, v, g, l)
     q = _expand_groups(q, H)
     k = _expand_groups(k, H)
-    S = FenwickState(B, H, K, V, L, q.dtype)
+    S = FenwickState(B, H, K, V, L, q.dtype, htype)
     ys = []
     for t in range(T):
         value = torch.einsum("bhk,bhv->bhkv", k[:, t], v[:, t])      # step_state :145
@@ -254,6 +297,67 @@ def chunked_fwd(q, k, v, g, l, chunk_size: int = 64) -> torch.Tensor:
             st = torch.einsum("bijh,bjhkv->bihkv", d, kv)
             qs = torch.einsum("bnthk,bnhkv->bnthv", q, st)
             y = y + qs * (out_decay * l[..., ell_h0 + ell])[..., None]
+    return y.reshape(B, T, H, V)
+
+
+def chunked_strong_fwd(q, k, v, g, l, chunk_size: int = 64) -> torch.Tensor:
+    """Chunked form of the strong hierarchy (HType.STRONG), the decomposition
+    the HIP strong kernel implements (checked against materialized_fwd and
+    recurrent_fwd with htype=STRONG, which restate base.py:49-62 and
+    recurrent.py:56-74):
+
+      o_t = sum_{s in chunk(t), s <= t} lam[t, intra(a, b)] e^{G_t - G_s} (q_t.k_s) v_s
+          + sum_{s in chunk(t) - 1}     lam[t, sub(a, b)]  e^{G_t - G_s} (q_t.k_s) v_s
+          + sum_{j >= 2} lam[t, log2(C) + j] e^{Gc_t} q_t . S_j(chunk(t)),
+
+    with a, b the positions inside the chunks, intra / sub the two C x C level
+    tables (oracle.levels.strong_intra_table / strong_subdiag_table), Gc the
+    chunk-local inclusive cumsum, and S_j(i) level j of a chunk-level strong
+    state (the cascade of recurrent.py:56-74 over whole chunks: each chunk is
+    one insertion with value sum_s e^{Gc_last - Gc_s} k_s v_s^T and gate
+    e^{Gc_last}), read for chunk i after the cascade and before the chunk's
+    own decay and insertion, so it holds the source chunks c <= i - 2 with
+    strong(i, c) = j, decayed to the start of chunk i.
+    """
+    C = chunk_size
+    q, k, v, g, l, (B, T, H, K, V, L, NT) = _chunk_views(q, k, v, g, l, C)
+    c = int(math.log2(C))
+    nlev = math.ceil(math.log2(NT)) if NT > 1 else 0
+    if c + 1 + nlev > L:
+        raise ValueError("too few levels")
+    Gc = torch.cumsum(g, dim=2)                                         # [B,NT,C,H]
+    tt = torch.arange(C)[:, None].expand(C, C)
+    # diagonal blocks
+    lev = torch.from_numpy(strong_intra_table(C))
+    mask = torch.tril(torch.ones(C, C, dtype=torch.bool))
+    seg = Gc[:, :, :, None, :] - Gc[:, :, None, :, :]
+    seg = seg.masked_fill(~mask[None, None, :, :, None], float("-inf"))
+    lam = l.permute(0, 1, 3, 2, 4)[:, :, :, tt, lev].permute(0, 1, 3, 4, 2)
+    A = torch.einsum("bnthk,bnshk->bntsh", q, k) * torch.exp(seg) * lam
+    y = torch.einsum("bntsh,bnshv->bnthv", A, v)
+    if NT > 1:
+        # sub-diagonal blocks: source chunk n - 1 of target chunk n
+        sub = torch.from_numpy(strong_subdiag_table(C))
+        gl = Gc[:, :-1, -1:, :]                                         # [B,NT-1,1,H]
+        seg = Gc[:, 1:, :, None, :] + (gl - Gc[:, :-1])[:, :, None, :, :]
+        lam = l[:, 1:].permute(0, 1, 3, 2, 4)[:, :, :, tt, sub].permute(0, 1, 3, 4, 2)
+        A = torch.einsum("bnthk,bnshk->bntsh", q[:, 1:], k[:, :-1]) * torch.exp(seg) * lam
+        y[:, 1:] = y[:, 1:] + torch.einsum("bntsh,bnshv->bnthv", A, v[:, :-1])
+        # far chunks: chunk-level strong state
+        kv = _chunk_states(k, v, Gc)                                    # [B,NT,H,K,V]
+        Lc = nlev + 2
+        S = FenwickState(B, H, K, V, Lc, q.dtype, STRONG)
+        for n in range(NT):
+            S.cascade_strong()
+            for j in range(2, Lc):
+                if c + j >= L:
+                    break
+                w = l[:, n, :, :, c + j] * torch.exp(Gc[:, n])          # [B,C,H]
+                y[:, n] = y[:, n] + torch.einsum("bthk,bhkv->bthv", q[:, n], S.states[..., j]) \
+                    * w[..., None]
+            S.states = torch.exp(Gc[:, n, -1])[:, :, None, None, None] * S.states
+            S.states[..., 0] = kv[:, n]
+            S.counts[0] += 1
     return y.reshape(B, T, H, V)
 
 

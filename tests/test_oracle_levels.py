@@ -5,10 +5,16 @@ recursion (base.py:41-46, restated with math.log exactly as written) by brute
 force, and the chunk-scan schedule (chunkwise.py:34-74) is checked against
 the closed form: every (reading chunk i, source chunk j<i) pair is served by
 exactly one inter-chunk level, and that level is bit_length(i ^ j) - 1.
+
+The strong level function (base.py:49-62): the vectorised table against the
+recursion by brute force, a few hand-derived rows, and the chunk
+decomposition a chunkwise strong kernel relies on (one table for the diagonal
+blocks, one for the sub-diagonal blocks, a single chunk-pair level elsewhere).
 """
 import random
 
 import numpy as np
+import pytest
 
 from oracle.levels import (level_weak_recursive, level_closed_form, levels_matrix,
                            skip_kv, skip_q, skip_g, get_num_levels, ceil_log)
@@ -66,3 +72,42 @@ def test_schedule_serves_each_pair_once_at_its_level():
                 state = set()
             if not skip_kv(i, ell):
                 state.add(i)
+
+
+# ---- strong hierarchy (base.py:49-62) ------------------------------------
+from oracle.levels import (level_strong_recursive, levels_matrix_strong, strong_far_level,  # noqa: E402
+                           strong_intra_table, strong_subdiag_table)
+
+
+def test_strong_matrix_matches_recursion_all_pairs_below_512():
+    M = levels_matrix_strong(512)
+    for t in range(512):
+        for s in range(t):
+            assert M[t, s] == level_strong_recursive(t, s), (t, s)
+        assert M[t, t] == 0
+        assert (M[t, t + 1:] == -1).all()
+
+
+def test_strong_known_values():
+    # a row of the strong table (every level boundary of the recursion's cases)
+    assert [level_strong_recursive(15, s) for s in range(15)] == \
+        [4] * 8 + [3] * 4 + [2, 2, 1]
+    assert [level_strong_recursive(12, s) for s in range(12)] == [4] * 8 + [3, 3, 2, 1]
+    # the strong hierarchy is finer than the weak one near the diagonal
+    assert level_strong_recursive(8, 7) == 1 and (8 ^ 7).bit_length() == 4
+
+
+@pytest.mark.parametrize("C", [16, 64])
+def test_strong_chunk_decomposition(C):
+    """Every diagonal block holds strong_intra_table, every sub-diagonal block
+    strong_subdiag_table, every farther block one level log2(C) + strong(i, j)."""
+    NT = 2048 // C
+    M = levels_matrix_strong(NT * C, default=0)
+    intra, sub = strong_intra_table(C), strong_subdiag_table(C)
+    for i in range(NT):
+        assert (M[i * C:(i + 1) * C, i * C:(i + 1) * C] == intra).all(), i
+        if i >= 1:
+            assert (M[i * C:(i + 1) * C, (i - 1) * C:i * C] == sub).all(), i
+        for j in range(i - 1):
+            blk = M[i * C:(i + 1) * C, j * C:(j + 1) * C]
+            assert (blk == strong_far_level(i, j, C)).all(), (i, j)

@@ -217,3 +217,46 @@ def test_causal_conv1d_and_gated_rmsnorm_closed_forms():
     y2 = M.split_conv1d_layer_fwd(zx, **args,
                                   scan=lambda q, k, v, g, l: M.materialized_fwd(q, k, v, g, l))
     assert rel(y1, y2) < 1e-12
+
+
+# ---- strong hierarchy (HType.STRONG) --------------------------------------
+@pytest.mark.parametrize("T,C", [(16, 4), (64, 8), (96, 16), (256, 64)])
+def test_strong_forms_agree(T, C):
+    """materialised strong table (base.py:49-62) == recurrent cascade_strong
+    (recurrent.py:56-74) == the chunked decomposition of chunked_strong_fwd."""
+    L = int(math.log2(T)) + 2
+    q, k, v, g, l = make_inputs(2, T, 2, 5, 4, L, seed=T + C)
+    o_mat = M.materialized_fwd(q, k, v, g, l, htype=M.STRONG)
+    o_rec = M.recurrent_fwd(q, k, v, g, l, htype=M.STRONG)
+    o_chk = M.chunked_strong_fwd(q, k, v, g, l, chunk_size=C)
+    assert rel(o_rec, o_mat) < 1e-12
+    assert rel(o_chk, o_mat) < 1e-12
+    # and it is a different hierarchy from the weak one
+    assert rel(M.materialized_fwd(q, k, v, g, l), o_mat) > 1e-3
+
+
+@pytest.mark.parametrize("level", [0, 1, 2, 4, 6, 7])
+def test_strong_one_hot_level_selects_pairs(level):
+    """g == 0, lambda one-hot: exactly the pairs whose strong level (the
+    reference's recursion, pair by pair) is `level`."""
+    from oracle.levels import level_strong_recursive
+    T = 192
+    q, k, v, _, l = make_inputs(1, T, 1, 3, 2, 9, seed=level)
+    g = torch.zeros(1, T, 1, dtype=torch.float64)
+    l = torch.zeros_like(l)
+    l[..., level] = 1.0
+    o = M.chunked_strong_fwd(q, k, v, g, l, chunk_size=16)
+    mask = torch.zeros(T, T, dtype=torch.float64)
+    for t in range(T):
+        for s in range(t + 1):
+            mask[t, s] = float((0 if s == t else level_strong_recursive(t, s)) == level)
+    ref = torch.einsum("ts,ts,sv->tv", torch.einsum("tk,sk->ts", q[0, :, 0], k[0, :, 0]),
+                       mask, v[0, :, 0])
+    assert rel(o[0, :, 0], ref) < 1e-12
+
+
+def test_strong_lambda_one_is_plain_ssd():
+    T = 128
+    q, k, v, g, l = make_inputs(1, T, 2, 4, 3, 9, seed=3)
+    o = M.chunked_strong_fwd(q, k, v, g, torch.ones_like(l), chunk_size=16)
+    assert rel(o, M.ssd_scan_fwd(q, k, v, g)) < 1e-12

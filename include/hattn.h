@@ -234,15 +234,21 @@ size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int 
  * scale, level_base, htype, hstruct, use_qk_l2norm_in_kernel) -> (o, hstate)`
  * with its step_state / step_output (hattention/recurrent.py:134-166), called by
  * hattention_prefill (kernel.py:555-570) and hselective_state_update
- * (mamba_apis.py:407-566).  HType.WEAK, level base 2.
+ * (mamba_apis.py:407-566).  HType.WEAK or HType.STRONG, level base 2.
  *
  *   states [B, H, K, V, L] fp32 (read and written)   counts [L] int32 or NULL
  *   q, k [B, G, K] in dtype_qk   v, o [B, H, V] in dtype_v   l [B, H, L] in dtype_l
  *   g [B, H] fp32 log-decay (gate exp(g))   beta [B, H] in dtype_beta (GDELTA) or NULL
  *   hstruct HATTN_HSTRUCT_MAMBA2 or HATTN_HSTRUCT_GDELTA
- *   cascade: number of full levels that cascade upwards before the insert
- *            (HState.cascade_weak, recurrent.py:42-54), planned by the caller
- *            from its copy of counts; 0 <= cascade < L
+ *   htype HATTN_HTYPE_WEAK or HATTN_HTYPE_STRONG
+ *   cascade, planned by the caller from its copy of counts (the cascade depends
+ *            only on the counts):
+ *            WEAK: number of full levels that merge upwards before the insert
+ *            (HState.cascade_weak, recurrent.py:42-54); 0 <= cascade < L.
+ *            STRONG: the level m where HState.cascade_strong's carry merges
+ *            (recurrent.py:56-74): levels 0 .. m-1 move up one level, level
+ *            m - 1 merging into level m; m = L when the carry leaves the top
+ *            level; 1 <= cascade <= L.
  *   update / output: 1 to advance the state (step_state) / write o (step_output);
  *            k, v, g, beta are read only with update, q, l, o only with output
  *            (the others may be NULL)
@@ -254,9 +260,9 @@ size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int 
  */
 int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, const void* v,
                       const void* beta, const float* g, const void* l, void* o, int B, int G,
-                      int H, int K, int V, int L, int hstruct, int cascade, int update,
-                      int output, int l2norm_qk, float scale, int dtype_qk, int dtype_v,
-                      int dtype_l, int dtype_beta, void* stream);
+                      int H, int K, int V, int L, int hstruct, int htype, int cascade,
+                      int update, int output, int l2norm_qk, float scale, int dtype_qk,
+                      int dtype_v, int dtype_l, int dtype_beta, void* stream);
 
 /*
  * Levels 0 .. nlo - 1 of the HState after a chunkwise prefill of T tokens

@@ -23,6 +23,11 @@ size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3);
 size_t hattn_mamba2_fwd_static_scratch_bytes();
 hipError_t hattn_mamba2_fwd_static_scratch(void** ptr);
 int hattn_mamba2_fwd_max_levels(int x3);
+int hattn_mamba2_strong_max_levels();
+hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const void* v,
+                                          const float* g, const void* l, void* o, float* gcum,
+                                          int B, int T, int G, int H, int V, int L, int dt_l,
+                                          int dt_o, hipStream_t stream, int* unsupported);
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V);
 int hattn_gdn_fwd_max_levels();
 int hattn_gdn_fwd_supports_k(int K);
@@ -49,7 +54,7 @@ hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, 
 hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
                                     const void* v, const void* beta, const float* g,
                                     const void* l, void* o, int B, int G, int H, int K, int V,
-                                    int L, int gdn, int cascade, int update, int output,
+                                    int L, int gdn, int cascade, int strong, int update, int output,
                                     int norm_qk, float scale, int dt_qk, int dt_v, int dt_l,
                                     int dt_b, hipStream_t stream, int* unsupported);
 hipError_t hattn_mamba2_prefill_levels_launch(float* states, const void* k, const void* v,
@@ -175,8 +180,8 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
-  if (htype != HATTN_HTYPE_WEAK)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (htype != HATTN_HTYPE_WEAK && htype != HATTN_HTYPE_STRONG)
+    return fail(HATTN_ERR_VALUE, "htype=%d", htype);
   if (B <= 0 || H <= 0 || G <= 0 || K <= 0 || V <= 0 || L <= 0)
     return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
@@ -187,6 +192,33 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
   const int nlev = ceil_log2(NT);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (htype == HATTN_HTYPE_STRONG) {
+    // chunkwise.py:1118-1275 with USE_A2 / USE_H2
+    if (nlev > hattn_mamba2_strong_max_levels())
+      return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d (HType.STRONG)", T,
+                  hattn_mamba2_strong_max_levels());
+    if (L > 32) return fail(HATTN_ERR_NOT_IMPLEMENTED, "L=%d > 32 (HType.STRONG)", L);
+    if (dtype_qk != HATTN_BF16 || dtype_v != HATTN_BF16)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: q/k/v dtype codes %d/%d (bf16 required)",
+                  dtype_qk, dtype_v);
+    if (ht != nullptr)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                  "HType.STRONG: output_final_state (the reference stores one of four phase states "
+                  "per level, chunkwise.py:275-279; use the recurrent HState for decoding)");
+    if (int st = check_span(T, max_of({(size_t)G * K * 2, (size_t)H * V * elem_bytes(dtype_o),
+                                        (size_t)H * L * elem_bytes(dtype_l), (size_t)H * 4})))
+      return st;
+    if (!q || !k || !v || !g || !l || !o || !g_cumsum)
+      return fail(HATTN_ERR_VALUE, "null tensor pointer");
+    int unsupported = 0;
+    hipError_t e = hattn_mamba2_strong_fwd_launch(q, k, v, g, l, o, g_cumsum, B, T, G, H, V, L,
+                                                  dtype_l, dtype_o, (hipStream_t)stream,
+                                                  &unsupported);
+    if (unsupported)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: dtype combination l=%d o=%d", dtype_l,
+                  dtype_o);
+    return check_hip(e, "hattn_mamba2_chunkwise_fwd (strong) launch");
+  }
   if (dtype_qk != HATTN_BF16 && dtype_qk != HATTN_FP32)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 or fp32 required)", dtype_qk);
   // fp32 q / k select the bf16x3 kernels (fp32-accurate products)
@@ -417,7 +449,7 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
 
 int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, const void* v,
                       const void* beta, const float* g, const void* l, void* o, int B, int G,
-                      int H, int K, int V, int L, int hstruct, int cascade, int update,
+                      int H, int K, int V, int L, int hstruct, int htype, int cascade, int update,
                       int output, int l2norm_qk, float scale, int dtype_qk, int dtype_v,
                       int dtype_l, int dtype_beta, void* stream) {
   if (B <= 0 || G <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
@@ -428,15 +460,21 @@ int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, 
   if (K > 256 || V % 16 != 0 || L > 32)
     return fail(HATTN_ERR_NOT_IMPLEMENTED,
                 "K=%d V=%d L=%d (K <= 256, V a multiple of 16, L <= 32)", K, V, L);
-  if (cascade < 0 || cascade >= L)
+  if (htype != HATTN_HTYPE_WEAK && htype != HATTN_HTYPE_STRONG)
+    return fail(HATTN_ERR_VALUE, "htype=%d", htype);
+  if (htype == HATTN_HTYPE_WEAK && (cascade < 0 || cascade >= L))
     return fail(HATTN_ERR_VALUE, "cascade depth %d with %d levels (level overflow)", cascade, L);
+  if (htype == HATTN_HTYPE_STRONG && update && (cascade < 1 || cascade > L))
+    return fail(HATTN_ERR_VALUE, "strong cascade merge level %d with %d levels", cascade, L);
   if (!states || (output && (!q || !l || !o)) ||
       (update && (!k || !v || !g || (hstruct == HATTN_HSTRUCT_GDELTA && !beta))))
     return fail(HATTN_ERR_VALUE, "null tensor pointer");
   int unsupported = 0;
   hipError_t e = hattn_hstate_step_launch(
       states, counts, q, k, v, beta, g, l, o, B, G, H, K, V, L,
-      hstruct == HATTN_HSTRUCT_GDELTA ? 1 : 0, cascade, update ? 1 : 0, output ? 1 : 0,
+      hstruct == HATTN_HSTRUCT_GDELTA ? 1 : 0, update ? cascade : 0,
+      (htype == HATTN_HTYPE_STRONG && update) ? 1 : 0,
+      update ? 1 : 0, output ? 1 : 0,
       l2norm_qk ? 1 : 0, scale, dtype_qk, dtype_v, dtype_l, dtype_beta, (hipStream_t)stream,
       &unsupported);
   if (unsupported)

@@ -46,12 +46,34 @@ __device__ __forceinline__ float block_sum256(float x, float* scratch4) {
   return scratch4[0] + scratch4[1] + scratch4[2] + scratch4[3];
 }
 
+// The level counts (shared by all rows) after the step: the cascade (weak: levels
+// 0 .. c-1 merge into level c; strong: levels 0 .. m-1 move up one level, m - 1
+// merging into m), then one more token at level 0.
+__device__ inline void cascade_counts(int* counts, int L, int cascade, int strong) {
+  if (strong) {
+    int prev = 0;
+    for (int e = 0; e < L; ++e) {
+      const int cur = counts[e];
+      counts[e] = e == 0 ? 0 : (e < cascade ? prev : (e == cascade ? cur + prev : cur));
+      prev = cur;
+    }
+  } else {
+    int moved = 0;
+    for (int e = 0; e < cascade; ++e) {
+      moved += counts[e];
+      counts[e] = 0;
+    }
+    if (cascade > 0) counts[cascade] += moved;
+  }
+  counts[0] += 1;
+}
+
 template <typename TQ, typename TV, typename TL, typename TB, bool GDN>
 __global__ __launch_bounds__(256) void hstate_step_kernel(
     float* __restrict__ states, int* __restrict__ counts, const TQ* __restrict__ q,
     const TQ* __restrict__ k, const TV* __restrict__ v, const TB* __restrict__ beta,
     const float* __restrict__ g, const TL* __restrict__ l, TV* __restrict__ o, int G, int H,
-    int K, int V, int L, int cascade, int update, int output, int norm_qk, float scale) {
+    int K, int V, int L, int cascade, int strong, int update, int output, int norm_qk, float scale) {
   __shared__ float sq[256], sk[256], sv[kHsCols], sl[kHsMaxL], snorm[8];
   __shared__ float red[256 * 4];   // [row group][column][4]: k^T S per level, then o
   const int tid = threadIdx.x;
@@ -88,7 +110,18 @@ __global__ __launch_bounds__(256) void hstate_step_kernel(
     const float* p = sbase + ((size_t)kk * V + v0 + vv) * L;
 #pragma unroll
     for (int e = 0; e < kHsMaxL; ++e) s[e] = e < L ? p[e] : 0.f;
-    if (cascade > 0) {
+    if (strong) {
+      // cascade_strong (recurrent.py:56-74) with merge level m = cascade: levels
+      // 0 .. m-1 move up one level, level m - 1 merging into level m (m = L: the
+      // top level's content leaves the state); level 0 ends empty
+      float prev = 0.f;
+#pragma unroll
+      for (int e = 0; e < kHsMaxL; ++e) {
+        const float cur = s[e];
+        s[e] = e == 0 ? 0.f : (e < cascade ? prev : (e == cascade ? cur + prev : cur));
+        prev = cur;
+      }
+    } else if (cascade > 0) {
       float acc = 0.f;
 #pragma unroll
       for (int e = 0; e < kHsMaxL; ++e)
@@ -171,15 +204,8 @@ __global__ __launch_bounds__(256) void hstate_step_kernel(
     }
   }
   // counts (shared by all rows): the same cascade, then one more token at level 0
-  if (update && counts != nullptr && blockIdx.y == 0 && bh == 0 && tid == 0) {
-    int moved = 0;
-    for (int e = 0; e < cascade; ++e) {
-      moved += counts[e];
-      counts[e] = 0;
-    }
-    if (cascade > 0) counts[cascade] += moved;
-    counts[0] += 1;
-  }
+  if (update && counts != nullptr && blockIdx.y == 0 && bh == 0 && tid == 0)
+    cascade_counts(counts, L, cascade, strong);
 }
 
 // Sum over the lanes of one wave that share lane % VB (VB a power of two <= 32):
@@ -204,7 +230,7 @@ __global__ __launch_bounds__(256) void hstate_step_lds_kernel(
     float* __restrict__ states, int* __restrict__ counts, const TQ* __restrict__ q,
     const TQ* __restrict__ k, const TV* __restrict__ v, const TB* __restrict__ beta,
     const float* __restrict__ g, const TL* __restrict__ l, TV* __restrict__ o, int G, int H,
-    int K, int V, int L, int VB, int cascade, int update, int output, int norm_qk,
+    int K, int V, int L, int VB, int cascade, int strong, int update, int output, int norm_qk,
     float scale) {
   extern __shared__ float slab[];
   __shared__ float sq[256], sk[256], sv[kHsCols], sl[NL], snorm[8];
@@ -292,7 +318,15 @@ __global__ __launch_bounds__(256) void hstate_step_lds_kernel(
     const float* p = slab + (kk * VB + vv) * Lp;
 #pragma unroll
     for (int e = 0; e < NL; ++e) s[e] = e < L ? p[e] : 0.f;
-    if (cascade > 0) {
+    if (strong) {
+      float prev = 0.f;   // cascade_strong, as in hstate_step_kernel
+#pragma unroll
+      for (int e = 0; e < NL; ++e) {
+        const float cur = s[e];
+        s[e] = e == 0 ? 0.f : (e < cascade ? prev : (e == cascade ? cur + prev : cur));
+        prev = cur;
+      }
+    } else if (cascade > 0) {
       float acc = 0.f;
 #pragma unroll
       for (int e = 0; e < NL; ++e)
@@ -381,15 +415,8 @@ __global__ __launch_bounds__(256) void hstate_step_lds_kernel(
       }
       advance(row, off);
     }
-    if (counts != nullptr && blockIdx.y == 0 && bh == 0 && tid == 0) {
-      int moved = 0;
-      for (int e = 0; e < cascade; ++e) {
-        moved += counts[e];
-        counts[e] = 0;
-      }
-      if (cascade > 0) counts[cascade] += moved;
-      counts[0] += 1;
-    }
+    if (counts != nullptr && blockIdx.y == 0 && bh == 0 && tid == 0)
+      cascade_counts(counts, L, cascade, strong);
   }
 }
 
@@ -473,9 +500,9 @@ bool with_type(int dt, F&& f) {
 hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
                                     const void* v, const void* beta, const float* g,
                                     const void* l, void* o, int B, int G, int H, int K, int V,
-                                    int L, int gdn, int cascade, int update, int output,
-                                    int norm_qk, float scale, int dt_qk, int dt_v, int dt_l,
-                                    int dt_b, hipStream_t stream, int* unsupported) {
+                                    int L, int gdn, int cascade, int strong, int update,
+                                    int output, int norm_qk, float scale, int dt_qk, int dt_v,
+                                    int dt_l, int dt_b, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   const bool known = (dt_qk == HS_BF16 || dt_qk == HS_FP32) &&
                      (dt_v == HS_BF16 || dt_v == HS_FP32) &&
@@ -507,12 +534,12 @@ hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, c
         return;
       hipLaunchKernelGGL(kern_lds, dim3(B * H, V / VB), dim3(256), smem, stream, states, counts,
                          (const TQ*)q, (const TQ*)k, (const TV*)v, (const TB*)beta, g,
-                         (const TL*)l, (TV*)o, G, H, K, V, L, VB, cascade, update, output,
+                         (const TL*)l, (TV*)o, G, H, K, V, L, VB, cascade, strong, update, output,
                          norm_qk, scale);
     } else {
       hipLaunchKernelGGL(kern_reg, dim3(B * H, V / kHsCols), dim3(256), 0, stream, states,
                          counts, (const TQ*)q, (const TQ*)k, (const TV*)v, (const TB*)beta, g,
-                         (const TL*)l, (TV*)o, G, H, K, V, L, cascade, update, output, norm_qk,
+                         (const TL*)l, (TV*)o, G, H, K, V, L, cascade, strong, update, output, norm_qk,
                          scale);
     }
   };

@@ -1,0 +1,301 @@
+// Log-linear Mamba-2 chunkwise forward for the strong hierarchy (HType.STRONG)
+// on gfx950.
+//
+// Replaces chunkwise.chunkwise_fwd with htype == STRONG (chunkwise.py:1118-1275):
+// the reference runs the intra-chunk kernel with USE_A2 (the sub-diagonal
+// tiles, chunkwise.py:587-641) and, per inter-chunk level from 1, the state
+// kernel with four phase states per level (USE_H2, chunkwise.py:199-276) and
+// the output kernel.
+//
+// The strong level function (base.py:49-62) at a chunk of 64 tokens: every
+// diagonal 64 x 64 block holds one level table (kStrong.intra), every
+// sub-diagonal block (source chunk = target chunk - 1) one other table
+// (kStrong.sub), and a pair of chunks further apart has the single level
+// 6 + strong(c_t, c_s) (the strong function of the chunk indices).  So
+//   o_t = sum_{s in chunk c}     lam[t, intra(a, b)] e^{G_t - G_s} (q_t.k_s) v_s
+//       + sum_{s in chunk c - 1} lam[t, sub(a, b)]   e^{G_t - G_s} (q_t.k_s) v_s
+//       + sum_{j >= 2} lam[t, 6 + j] e^{Gc_t} q_t . S_j(c),
+// where S_j(c) is level j of a chunk-level strong state: the cascade of
+// HState.cascade_strong (recurrent.py:56-74) with one insertion per chunk
+// (value sum_s e^{Gc_last - Gc_s} k_s v_s^T, gate e^{Gc_last}), read after
+// the cascade and before the chunk's own decay and insertion.
+//
+// One workgroup (four waves) per (batch, head, 16 columns of V) walks the
+// chunks in order.  Wave w owns the output rows t = 16 w .. +15 and the state
+// rows k = 16 w .. +15 of every chunk-level level (one 16 x 16 fp32 tile per
+// level in registers).  Per chunk: the cascade (uniform selects over the
+// levels), the levels >= 2 staged in LDS as bf16, then with transposed
+// products (lane: one token t, four consecutive v)
+//   o^T += V^T (P o W)^T over the chunk and its predecessor (P = Q K^T, W the
+//          decay and lambda weights, from the two level tables in LDS)
+//   o^T += sum_j S_j^T (lam_j e^{Gc} Q)^T
+// and finally S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay.
+#include "mamba2_common.h"
+
+namespace hattn {
+
+constexpr int kSC = 64;           // chunk
+constexpr int kSBV = 16;          // V columns per workgroup
+constexpr int kSMaxLev = 10;      // chunk-level levels 0 .. 9 (T <= 64 * 2^9)
+constexpr int kSLK = 64 + 8;      // row stride of the bf16 q / k tiles
+constexpr int kSLV = kSBV + 8;    // row stride of the bf16 v tiles
+
+// The strong level function of base.py:49-62 for t > s (t, s < 128), and its
+// two 64 x 64 chunk tables, built at compile time.
+constexpr int strong_level_ce(int t, int s) {
+  for (;;) {
+    int ell = 0;
+    while ((2 << ell) <= t) ++ell;          // floor(log2 t)
+    const int v = 1 << (ell > 0 ? ell - 1 : 0);
+    const int r = t - (1 << ell);
+    if (s < v) return ell + 1;
+    if (s < 2 * v && r >= v) return ell + 1;
+    if (s < 2 * v) {
+      t -= v;
+      s -= v;
+    } else {
+      t -= 2 * v;
+      s -= 2 * v;
+    }
+  }
+}
+struct StrongTables {
+  unsigned char intra[kSC * kSC];   // [a][b], a >= b: level of (a, b) inside a chunk
+  unsigned char sub[kSC * kSC];     // [a][b]: level of (64 + a, b)
+  constexpr StrongTables() : intra(), sub() {
+    for (int a = 0; a < kSC; ++a)
+      for (int b = 0; b < kSC; ++b) {
+        intra[a * kSC + b] = (unsigned char)(b < a ? strong_level_ce(a, b) : 0);
+        sub[a * kSC + b] = (unsigned char)strong_level_ce(kSC + a, b);
+      }
+  }
+};
+__device__ constexpr StrongTables kStrong{};
+
+struct StrongSmem {
+  __bf16 q[kSC * kSLK];
+  __bf16 k[2][kSC * kSLK];           // this chunk and the previous one (by parity)
+  __bf16 v[2][kSC * kSLV];
+  __bf16 hs[kSMaxLev][kSBV * kSLK];  // chunk-level states, bf16 [v][k]
+  float gc[2][kSC];                  // chunk-local inclusive cumsum of g
+  float lam[kSC][32];                // lambda[t, 0 .. L-1] of this chunk (L <= 32)
+  unsigned char tab[2][kSC * kSC];   // intra / sub level tables
+};
+
+template <typename TL, typename TO>
+__global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
+    float* __restrict__ gcum, int nrows, int T, int G, int H, int V, int L) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  StrongSmem& s = *(StrongSmem*)smem_raw;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int nvb = V / kSBV;
+  const XcdMap mp = xcd_map(blockIdx.x, nvb);
+  if (mp.row >= nrows) return;
+  const int row = mp.row, v0 = mp.slice * kSBV;
+  const int b = row / H, h = row % H, gq = h / (H / G);
+  const int NT = T / kSC;
+  const size_t hk = (size_t)G * 64, hv = (size_t)H * V;
+  const int t_me = 16 * w + ln;   // this lane's token in the transposed products
+
+  for (int i = tid; i < kSC * kSC; i += 256) {
+    s.tab[0][i] = kStrong.intra[i];
+    s.tab[1][i] = kStrong.sub[i];
+  }
+
+  floatx4 st[kSMaxLev];
+#pragma unroll
+  for (int j = 0; j < kSMaxLev; ++j) st[j] = zero4();
+  int cnt[kSMaxLev];
+#pragma unroll
+  for (int j = 0; j < kSMaxLev; ++j) cnt[j] = 0;
+
+  for (int ic = 0; ic < NT; ++ic) {
+    const int par = ic & 1;
+    const size_t tok0 = (size_t)b * T + (size_t)ic * kSC;
+    // ---- cascade (recurrent.py:56-74) over the chunk-level states ------------------
+    {
+      floatx4 carry = zero4();
+      int cc = 0;
+#pragma unroll
+      for (int j = 0; j < kSMaxLev; ++j) {
+        const int cap = 1 << (j > 0 ? j - 1 : 0);
+        const bool swap = j == 0 || cnt[j] + cc > cap;
+        const floatx4 old = st[j];
+        const int oc = cnt[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st[j][i] = swap ? carry[i] : old[i] + carry[i];
+          carry[i] = swap ? old[i] : 0.f;
+        }
+        cnt[j] = swap ? cc : oc + cc;
+        cc = swap ? oc : 0;
+      }
+    }
+    // ---- stage: q, k, v tiles, g cumsum, lambda, levels >= 2 -------------------------
+    {
+      const int r = tid >> 2, c16 = 16 * (tid & 3);
+      const size_t rq = (tok0 + r) * hk + (size_t)gq * 64 + c16;
+      const u32x4 q0 = *(const u32x4*)(q + rq), q1 = *(const u32x4*)(q + rq + 8);
+      const u32x4 k0 = *(const u32x4*)(k + rq), k1 = *(const u32x4*)(k + rq + 8);
+      *(u32x4*)(s.q + r * kSLK + c16) = q0;
+      *(u32x4*)(s.q + r * kSLK + c16 + 8) = q1;
+      *(u32x4*)(s.k[par] + r * kSLK + c16) = k0;
+      *(u32x4*)(s.k[par] + r * kSLK + c16 + 8) = k1;
+      if (tid < 128) {
+        const int rv = tid >> 1, cv = 8 * (tid & 1);
+        *(u32x4*)(s.v[par] + rv * kSLV + cv) =
+            *(const u32x4*)(v + (tok0 + rv) * hv + (size_t)h * V + v0 + cv);
+      }
+      if (w == 0) {
+        float x = g[(tok0 + lane) * H + h];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float y = __shfl_up(x, d, 64);
+          if (lane >= d) x += y;
+        }
+        s.gc[par][lane] = x;
+        if (v0 == 0) gcum[(tok0 + lane) * H + h] = x;
+      }
+      for (int i = tid; i < kSC * L; i += 256)
+        s.lam[i / L][i % L] = to_f32<TL>(l[((tok0 + i / L) * H + h) * L + i % L]);
+#pragma unroll
+      for (int j = 2; j < kSMaxLev; ++j)
+        *(bf16x4*)(s.hs[j] + ln * kSLK + 16 * w + 4 * lq) = cvt4(st[j]);
+    }
+    __syncthreads();
+
+    // ---- o^T[v][t] for t = 16 w + ln ----------------------------------------------------
+    floatx4 acc = zero4();   // o^T[v = 4 lq + i][t = t_me]
+    const float gct = s.gc[par][t_me];
+    // B operand of the q . k products: Q[t_me][32 c + 8 lq ..]
+    const bf16x8 bq0 = *(const bf16x8*)(s.q + t_me * kSLK + 8 * lq);
+    const bf16x8 bq1 = *(const bf16x8*)(s.q + t_me * kSLK + 32 + 8 * lq);
+    // diagonal (cur = 1) and sub-diagonal (cur = 0) blocks
+#pragma unroll
+    for (int cur = 1; cur >= 0; --cur) {
+      if (!cur && ic == 0) break;
+      const int pk = cur ? par : par ^ 1;
+      const unsigned char* tab = s.tab[cur ? 0 : 1];
+      const float* lrow = s.lam[t_me];
+      // the source tiles of the block: the diagonal stops at this wave's tile
+      const int npair = cur ? (w >> 1) + 1 : 2;
+      const float base = cur ? 0.f : s.gc[pk][kSC - 1];
+      for (int p = 0; p < npair; ++p) {
+        bf16x8 pb;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int n = 2 * p + half;   // source tile
+          floatx4 sc = zero4();
+          sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 8 * lq), bq0, sc);
+          sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 32 + 8 * lq), bq1, sc);
+          // sc[i] = q_t . k_s, s = 16 n + 4 lq + i, t = t_me
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int sp = 16 * n + 4 * lq + i;
+            float x = 0.f;
+            if (!cur || sp <= t_me) {
+              const int lev = tab[t_me * kSC + sp];
+              x = sc[i] * fexp(gct + base - s.gc[pk][sp]) * lrow[lev];
+            }
+            pb[4 * half + i] = (__bf16)x;
+          }
+        }
+        // o^T[v][t] += V[s][v] P^T[s][t] over the 32 sources of the pair
+        acc = mfma16x16x32(tr_frag_d(s.v[pk], kSLV, 32 * p, 0), pb, acc);
+      }
+    }
+    // far levels: o^T[v][t] += S_j^T[v][k] (lam[t, 6 + j] e^{Gc_t} q_t[k])
+    {
+      const float eg = fexp(gct);
+#pragma unroll
+      for (int j = 2; j < kSMaxLev; ++j) {
+        if (6 + j < L) {
+          const float f = s.lam[t_me][6 + j] * eg;
+          bf16x8 b0, b1;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            b0[jj] = (__bf16)((float)bq0[jj] * f);
+            b1[jj] = (__bf16)((float)bq1[jj] * f);
+          }
+          acc = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 8 * lq), b0, acc);
+          acc = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 32 + 8 * lq), b1, acc);
+        }
+      }
+    }
+    // store o[t_me][v0 + 4 lq .. +3]
+    {
+      TO* op = o + (tok0 + t_me) * hv + (size_t)h * V + v0 + 4 * lq;
+      if constexpr (sizeof(TO) == 2) {
+        *(bf16x4*)op = cvt4(acc);
+      } else {
+        *(floatx4*)op = acc;
+      }
+    }
+
+    // ---- decay the levels, insert S_0 = K^T diag(e^{Gc_last - Gc}) V ------------------
+    {
+      const float glast = s.gc[par][kSC - 1];
+      const float gd = fexp(glast);
+#pragma unroll
+      for (int j = 1; j < kSMaxLev; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[j][i] *= gd;
+      floatx4 sum = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bf16x8 a = tr_frag(s.k[par], kSLK, 32 * c, 16 * w);   // K[s][k = 16 w + ln]
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          a[jj] = (__bf16)((float)a[jj] * fexp(glast - s.gc[par][32 * c + 8 * lq + jj]));
+        sum = mfma16x16x32(a, tr_frag(s.v[par], kSLV, 32 * c, 0), sum);
+      }
+      st[0] = sum;
+      cnt[0] += 1;
+    }
+    __syncthreads();
+  }
+}
+
+template <typename TL, typename TO>
+static hipError_t strong_launch_t(const void* q, const void* k, const void* v, const float* g,
+                                  const void* l, void* o, float* gcum, int B, int T, int G,
+                                  int H, int V, int L, hipStream_t stream) {
+  auto kf = mamba2_strong_fwd_kernel<TL, TO>;
+  const int smem = (int)sizeof(StrongSmem);
+  hipError_t e;
+  if ((e = hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               smem)) != hipSuccess)
+    return e;
+  const int rows = B * H;
+  const int grid = (rows + 7) / 8 * 8 * (V / kSBV);
+  hipLaunchKernelGGL(kf, dim3(grid), dim3(256), smem, stream, (const __bf16*)q, (const __bf16*)k,
+                     (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum, rows, T, G, H, V, L);
+  return hipGetLastError();
+}
+
+}  // namespace hattn
+
+int hattn_mamba2_strong_max_levels() { return hattn::kSMaxLev - 1; }
+
+// bf16 q / k / v; lambda bf16 or fp32; o bf16 or fp32; K = 64; V a multiple of 16;
+// L <= 32.
+hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const void* v,
+                                          const float* g, const void* l, void* o, float* gcum,
+                                          int B, int T, int G, int H, int V, int L, int dt_l,
+                                          int dt_o, hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  if (dt_l == 0 && dt_o == 0)
+    return strong_launch_t<__bf16, __bf16>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+  if (dt_l == 2 && dt_o == 0)
+    return strong_launch_t<float, __bf16>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+  if (dt_l == 0 && dt_o == 2)
+    return strong_launch_t<__bf16, float>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+  if (dt_l == 2 && dt_o == 2)
+    return strong_launch_t<float, float>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+  *unsupported = 1;
+  return hipSuccess;
+}

@@ -40,7 +40,7 @@ SIGNATURES = [
      + [_I] * 3 + [_I, ctypes.c_float] + [_P, _S, _P]),
     ("hattn_gdn_chunkwise_bwd_workspace", _S, [_I] * 6),
     ("hattn_hstate_step", _I,
-     [_P] * 9 + [_I] * 11 + [ctypes.c_float] + [_I] * 4 + [_P]),
+     [_P] * 9 + [_I] * 12 + [ctypes.c_float] + [_I] * 4 + [_P]),
     ("hattn_mamba2_prefill_levels", _I, [_P] * 4 + [_I] * 10 + [_P]),
     ("hattn_mamba2_layer_prologue", _I, [_P] * 9 + [_I] * 13 + [_P]),
     ("hattn_mamba2_layer_epilogue", _I, [_P] * 4 + [_I] * 7 + [_P]),

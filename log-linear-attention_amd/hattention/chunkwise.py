@@ -42,10 +42,13 @@ def _shapes(q, k, v, l, head_first):
     return B, T, G, H, K, V, L
 
 
-def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
-    """chunkwise.py:1140-1153 and :1211-1214."""
-    if htype != HType.WEAK:
-        raise NotImplementedError("HType.STRONG is outside the MI355X path")
+def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size, strong_ok=False):
+    """chunkwise.py:1140-1153 and :1211-1214.  HType.STRONG has a forward
+    kernel (mamba2_strong.hip) and no backward kernel."""
+    if htype == HType.STRONG and not strong_ok:
+        raise NotImplementedError("HType.STRONG: the MI355X path has the forward only")
+    if htype not in (HType.WEAK, HType.STRONG):
+        raise ValueError(f"htype={htype}")
     if level_base != 2:
         raise NotImplementedError("level_base must be 2")
     if chunk_size != CHUNK:
@@ -104,6 +107,10 @@ def chunkwise_fwd(
     the inter-chunk level states at levels 7 .. 6 + ceil(log2(T/64)) (other
     levels zero), like the reference.
 
+    HType.STRONG (bf16 q / k / v, no final state) runs the strong kernel:
+    diagonal and sub-diagonal blocks from the strong level tables, farther
+    chunks from a chunk-level strong cascade (chunkwise.py:199-276, 587-641).
+
     The kernels contract over 64 key dimensions.  A larger K (a multiple of 64)
     runs one launch per 64-wide block of q and k: the output is linear in that
     split (o = sum over blocks of the blocks' outputs, accumulated in fp32), and
@@ -111,7 +118,7 @@ def chunkwise_fwd(
     """
     _assert_contiguous(q=q, k=k, v=v, g=g, l=l)
     B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
-    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size)
+    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size, strong_ok=True)
     if g.shape != (B, T, H):
         raise ValueError("g must be [B, T, H]")
     if g.dtype != torch.float32:

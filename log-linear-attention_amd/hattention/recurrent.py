@@ -70,6 +70,33 @@ class HState:
         self.host_counts = counts
         return depth
 
+    def plan_cascade_strong(self) -> int:
+        """recurrent.py:56-74 on the host copy of the counts, followed by the
+        insert's counts[0] += 1.  The carry (state, count) walks up: level 0,
+        and a level whose count plus the carry's exceeds its capacity
+        2^max(level - 1, 0), hands its content on and takes the carry; the
+        first other level merges the carry, and nothing above it changes.
+        Returns that merge level m (L when the carry leaves the top level, as
+        the reference drops it): levels 0 .. m-1 move up one level, level m - 1
+        merging into level m."""
+        counts = list(self.host_counts)
+        carry = 0
+        merge = self.max_num_levels
+        for level in range(self.max_num_levels):
+            capacity = self.base ** max(level - 1, 0)
+            if counts[level] + carry > capacity or level == 0:
+                counts[level], carry = carry, counts[level]
+            else:
+                counts[level] += carry
+                merge = level
+                break
+        counts[0] += 1
+        self.host_counts = counts
+        return merge
+
+    def plan_cascade(self) -> int:
+        return self.plan_cascade_weak() if self.htype == HType.WEAK else self.plan_cascade_strong()
+
     def set_counts(self, counts: List[int]) -> None:
         """Set the level counts on the host and the device."""
         if len(counts) != self.max_num_levels:
@@ -107,8 +134,8 @@ class HState:
 
 
 def _check_state(S: HState) -> None:
-    if S.htype != HType.WEAK or S.base != 2:
-        raise NotImplementedError("only HType.WEAK with level base 2 is built")
+    if S.htype not in (HType.WEAK, HType.STRONG) or S.base != 2:
+        raise NotImplementedError("only level base 2 (HType.WEAK or HType.STRONG) is built")
     if S.dtype != torch.float32:
         raise NotImplementedError(f"HState in {S.dtype}: the step kernels keep fp32 states")
     if not S.states.is_contiguous():
@@ -143,8 +170,7 @@ def launch_step(S: HState, *, q=None, k=None, v=None, beta=None, g=None, l=None,
     all contiguous on the state's device (g fp32).  Plans the cascade when
     ``update``.  Kept lean: it runs once per decoded token."""
     st = S.states
-    if S.htype is not HType.WEAK or S.base != 2 or st.dtype is not torch.float32 or \
-            not st.is_contiguous():
+    if S.base != 2 or st.dtype is not torch.float32 or not st.is_contiguous():
         _check_state(S)
         st = S.states
     if not st.is_cuda:
@@ -179,10 +205,10 @@ def launch_step(S: HState, *, q=None, k=None, v=None, beta=None, g=None, l=None,
         raise NotImplementedError(f"unsupported dtype {e}") from None
     fn = _step_fn()
     saved = S.host_counts
-    cascade = S.plan_cascade_weak() if update else 0
+    cascade = S.plan_cascade() if update else 0
     status = fn(st.data_ptr(), S.counts.data_ptr(), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
                 _lib.ptr(beta), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o), B, G, H, K, V, L,
-                S.hstruct.value, cascade, int(update), int(output), int(l2norm_qk),
+                S.hstruct.value, S.htype.value, cascade, int(update), int(output), int(l2norm_qk),
                 float(scale if scale is not None else 1.0), *codes,
                 torch.cuda.current_stream(dev).cuda_stream)
     if status:

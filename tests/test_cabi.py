@@ -108,7 +108,9 @@ def _fwd(ptr=None, **kw):
     (dict(V=40), _lib.HATTN_ERR_VALUE),
     (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(base=3), _lib.HATTN_ERR_NOT_IMPLEMENTED),
-    (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(htype=2), _lib.HATTN_ERR_VALUE),          # neither WEAK nor STRONG
+    (dict(htype=1, dq=2, dv=2, dl=2, do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # STRONG: bf16 q/k/v
+    (dict(htype=1, T=64 << 10, L=20), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # STRONG: > 9 chunk levels
     (dict(K=128), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(dq=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp16 q/k
     (dict(dq=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # fp32 q/k (bf16x3) with bf16 v, lambda, o

@@ -1,0 +1,162 @@
+"""GPU parity of the strong hierarchy (HType.STRONG).
+
+The HIP paths run through the C-ABI: the strong chunkwise forward
+(hattention.chunkwise.chunkwise_fwd with HType.STRONG -> hattn_mamba2_chunkwise_fwd
+-> mamba2_strong.hip) and the decode step with the strong cascade
+(hattention.kernel.hattention_step -> hattn_hstate_step).  The checkers are
+the oracle's strong forms in float64 on the CPU (oracle.mamba2.chunked_strong_fwd
+and recurrent_fwd(htype=STRONG), pinned against the materialised strong table
+of base.py:49-62 and against each other), fed the identical inputs.
+
+Tolerances as the weak tests: bf16 inputs max|o - o_ref| / max|o_ref| < 2e-2 and
+relative Frobenius error < 1e-2; level states of the decode 2e-2 per level.
+"""
+import math
+
+import pytest
+import torch
+
+from bench import make_mamba2_inputs
+from oracle import mamba2 as M
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL_MAX = 2e-2
+TOL_FRO = 1e-2
+
+
+def _errs(out, ref):
+    out = out.double().cpu()
+    ref = ref.double().cpu()
+    mx = ((out - ref).abs().max() / ref.abs().max()).item()
+    fro = ((out - ref).norm() / ref.norm()).item()
+    return mx, fro
+
+
+def _levels(T):
+    return 7 + (math.ceil(math.log2(T // 64)) if T > 64 else 0)
+
+
+def _run_fwd(B, T, G, H, K, V, L, seed, rows=None, ldtype=None):
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_fwd
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=seed, ldtype=ldtype)
+    print(f"[strong fwd] B={B} T={T} G={G} H={H} K={K} V={V} L={L} lambda={l.dtype}", flush=True)
+    o, gc, ht = chunkwise_fwd(*(x.to(DEV) for x in (q, k, v, g, l)), False, 2, HType.STRONG, 64,
+                              False)
+    torch.cuda.synchronize()
+    assert ht is None and o.dtype == v.dtype and o.shape == v.shape
+    rows = rows or [(b, h) for b in range(B) for h in range(H)]
+    for (b, h) in rows:
+        gi = h // (H // G)
+        qs, ks = (x[b:b + 1, :, gi:gi + 1].double() for x in (q, k))
+        vs, gs, ls = (x[b:b + 1, :, h:h + 1].double() for x in (v, g, l))
+        ref = M.chunked_strong_fwd(qs, ks, vs, gs, ls, chunk_size=64)
+        mx, fro = _errs(o[b:b + 1, :, h:h + 1], ref)
+        print(f"  row ({b},{h}) o: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < TOL_MAX and fro < TOL_FRO, (b, h, mx, fro)
+        ref_gc = torch.cumsum(gs.reshape(1, T // 64, 64, 1), dim=2).reshape(1, T, 1)
+        assert torch.allclose(gc[b:b + 1, :, h:h + 1].double().cpu(), ref_gc, rtol=1e-5,
+                              atol=1e-4)
+    return o, (q, k, v, g, l)
+
+
+@pytest.mark.parametrize("T", [64, 128, 192, 640, 1024])
+def test_strong_fwd_lengths(T):
+    _run_fwd(1, T, 2, 2, 64, 64, _levels(T), seed=T)
+
+
+def test_strong_fwd_groups_k128_fp32_lambda():
+    """grouped q / k, K = 128 (two 64-wide launches summed), fp32 lambda."""
+    _run_fwd(2, 512, 1, 4, 128, 128, 10, seed=5, ldtype=torch.float32)
+
+
+def test_strong_fwd_north_star_shape():
+    """The north-star shape (B=4 T=16384 H=16 d=64 L=15) with the strong hierarchy,
+    rows at both ends of the grid (and of the XCD map)."""
+    _run_fwd(4, 16384, 16, 16, 64, 64, 15, seed=1000, rows=[(0, 0), (1, 7), (3, 15)])
+
+
+def test_strong_differs_from_weak():
+    """The strong path is taken: its output differs from the weak one's on the
+    same inputs by far more than the tolerance."""
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_fwd
+    o_s, xs = _run_fwd(1, 1024, 1, 1, 64, 64, 11, seed=7)
+    o_w = chunkwise_fwd(*(x.to(DEV) for x in xs), False, 2, HType.WEAK, 64, False)[0]
+    mx, _ = _errs(o_s, o_w)
+    assert mx > 0.1, mx
+
+
+def test_strong_hattention_kernel_forward_and_backward_raises():
+    """HAttentionFunction with HType.STRONG: the forward runs the strong kernel;
+    the backward (no strong backward kernel) raises NotImplementedError."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_kernel
+    B, T, H, K, V, L = 1, 256, 2, 64, 64, 9
+    q, k, v, g, l = (x.to(DEV) for x in make_mamba2_inputs(B, T, H, K, V, L, seed=11))
+    with torch.no_grad():
+        o = hattention_kernel(q, k, v, None, g, l, None, False, 2, HType.STRONG, HStruct.MAMBA2)
+    ref = M.chunked_strong_fwd(*(x.double().cpu() for x in (q, k, v, g, l)), chunk_size=64)
+    mx, fro = _errs(o, ref)
+    assert mx < TOL_MAX and fro < TOL_FRO, (mx, fro)
+    leaves = [x.detach().clone().requires_grad_(True) for x in (q, k, v, g, l)]
+    out = hattention_kernel(leaves[0], leaves[1], leaves[2], None, leaves[3], leaves[4], None,
+                            False, 2, HType.STRONG, HStruct.MAMBA2)
+    with pytest.raises(NotImplementedError):
+        out.sum().backward()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_strong_decode_matches_recurrent(dtype):
+    """hattention_step with a strong HState from empty: every token's output and
+    the final level states and counts against the recurrent cascade_strong."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_step
+    from hattention.recurrent import HState
+    B, T, G, H, K, V, L = 2, 150, 1, 2, 64, 32, 9
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=401, dtype=dtype)
+    print(f"[strong decode] B={B} T={T} H={H} K={K} V={V} L={L} {dtype}", flush=True)
+    S = HState(2, HType.STRONG, HStruct.MAMBA2, (B, H, K, V, L), torch.float32, DEV)
+    qd, kd, vd, gd, ld = (x.to(DEV) for x in (q, k, v, g, l))
+    outs = []
+    for t in range(T):
+        o, S = hattention_step(S, qd[:, t], kd[:, t], vd[:, t], None, gd[:, t], ld[:, t], None,
+                               2, HType.STRONG, HStruct.MAMBA2)
+        outs.append(o)
+    torch.cuda.synchronize()
+    o = torch.stack(outs, 1)
+    o_ref, F = M.recurrent_fwd(*(x.double() for x in (q, k, v, g, l)), return_state=True,
+                               htype=M.STRONG)
+    tol = (1e-4, 1e-4) if dtype == torch.float32 else (TOL_MAX, TOL_FRO)
+    mx, fro = _errs(o, o_ref)
+    print(f"  o: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+    assert mx < tol[0] and fro < tol[1], (mx, fro)
+    assert [int(c) for c in S.counts.cpu()] == list(F.counts) == S.host_counts
+    got = S.states.double().cpu()
+    for e in range(L):
+        r = F.states[..., e]
+        if r.abs().max() == 0:
+            assert got[..., e].abs().max() == 0, e
+            continue
+        err = ((got[..., e] - r).norm() / r.norm()).item()
+        assert err < max(tol[0], 1e-4), (e, err)
+
+
+def test_strong_prefill_matches_recurrent():
+    """hattention_prefill with HType.STRONG (every token through the decode
+    step, as the reference's T0 = 0 for the strong hierarchy, kernel.py:495-499)."""
+    from hattention.base import HType, HStruct
+    from hattention.kernel import hattention_prefill
+    B, T, H, K, V, L = 1, 100, 2, 64, 32, 9
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=402, dtype=torch.float32)
+    o, S = hattention_prefill(*(x.to(DEV) for x in (q, k, v)), None,
+                              *(x.to(DEV) for x in (g, l)), None, False, 2, HType.STRONG,
+                              HStruct.MAMBA2)
+    torch.cuda.synchronize()
+    o_ref, F = M.recurrent_fwd(*(x.double() for x in (q, k, v, g, l)), return_state=True,
+                               htype=M.STRONG)
+    mx, fro = _errs(o, o_ref)
+    assert mx < 1e-4 and fro < 1e-4, (mx, fro)
+    assert S.host_counts == list(F.counts)

@@ -114,10 +114,46 @@ def test_step_argument_checks():
         hattention_step(S, q, q, v, g, g, l, None, 2, HType.WEAK, HStruct.GDELTA)
 
 
-def test_strong_hierarchy_not_built():
+def test_strong_step_needs_device_tensors():
+    """HType.STRONG runs the same step kernels (strong cascade); no CPU path."""
     from hattention.base import HType, HStruct
     from hattention.recurrent import HState, launch_step
     S = HState(2, HType.STRONG, HStruct.MAMBA2, (1, 1, 64, 16, 4), torch.float32, "cpu")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError):
         launch_step(S, k=torch.randn(1, 1, 64), v=torch.randn(1, 1, 16), g=torch.randn(1, 1),
                     update=True, output=False)
+    S3 = HState(3, HType.WEAK, HStruct.MAMBA2, (1, 1, 64, 16, 4), torch.float32, "cpu")
+    with pytest.raises(NotImplementedError):
+        launch_step(S3, k=torch.randn(1, 1, 64), v=torch.randn(1, 1, 16), g=torch.randn(1, 1),
+                    update=True, output=False)
+
+
+def test_strong_cascade_plan_matches_oracle():
+    """plan_cascade_strong against the oracle's cascade_strong (restatement of
+    recurrent.py:56-74): the counts after every insert, and the kernels' state
+    move for the planned merge level m (levels 0 .. m-1 up one level, m - 1
+    merging into m) applied to per-level values equals the oracle's states."""
+    import random
+    from hattention.base import HType, HStruct
+    from hattention.recurrent import HState
+    L = 9
+    S = HState(2, HType.STRONG, HStruct.MAMBA2, (1, 1, 1, 1, L), torch.float32, "cpu")
+    O = M.FenwickState(1, 1, 1, 1, L, torch.float64, htype=M.STRONG)
+    rng = random.Random(0)
+    shadow = [0.0] * L
+    for n in range(700):
+        gate, value = rng.uniform(0.5, 1.0), rng.uniform(-1.0, 1.0)
+        m = S.plan_cascade_strong()
+        assert 1 <= m <= L
+        prev, new = 0.0, []
+        for e in range(L):
+            cur = shadow[e]
+            new.append(0.0 if e == 0 else (prev if e < m else (cur + prev if e == m else cur)))
+            prev = cur
+        shadow = [x * gate for x in new]
+        shadow[0] = value
+        O.insert(torch.full((1, 1), gate, dtype=torch.float64),
+                 torch.full((1, 1, 1, 1), value, dtype=torch.float64))
+        assert S.host_counts == O.counts, n
+        ref = O.states[0, 0, 0, 0].tolist()
+        assert max(abs(a - b) for a, b in zip(shadow, ref)) < 1e-12, n

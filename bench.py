@@ -425,12 +425,15 @@ def cpu_baseline(seconds_budget=20.0):
     }
 
 
-def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, backward=False):
+def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, backward=False,
+                      strong=False):
     """Cold-cache median of one Mamba-2 chunkwise forward
     (or forward + backward through HAttentionFunction) at one BASELINE config,
-    with its roofline: HBM-bound by algorithmic bytes (SURVEY formulas)."""
+    with its roofline: HBM-bound by algorithmic bytes (SURVEY formulas).
+    ``strong``: the strong hierarchy (HType.STRONG) on the same inputs."""
     from hattention.base import HType, HStruct
     from hattention.kernel import hattention_kernel
+    ht = HType.STRONG if strong else HType.WEAK
     B, T, H, K, V, L = shape
     es = 4 if dtype == torch.float32 else 2
     q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, seed=1000, dtype=dtype, device=dev,
@@ -442,11 +445,11 @@ def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, back
             for x in leaves:
                 x.grad = None
             hattention_kernel(leaves[0], leaves[1], leaves[2], None, leaves[3], leaves[4], None,
-                              False, 2, HType.WEAK, HStruct.MAMBA2).backward(do)
+                              False, 2, ht, HStruct.MAMBA2).backward(do)
     else:
         def fn():
             with torch.no_grad():
-                hattention_kernel(q, k, v, None, g, l, None, False, 2, HType.WEAK, HStruct.MAMBA2)
+                hattention_kernel(q, k, v, None, g, l, None, False, 2, ht, HStruct.MAMBA2)
     for _ in range(warmup):
         fn()
     times = time_cold(fn, reps, stream, evict)
@@ -461,6 +464,7 @@ def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, back
     bound = "hbm" if nbytes / HBM_PEAK >= mfma_equiv / MFMA_BF16_PEAK else "mfma"
     del q, k, v, g, l, do
     return {"config": name, "batch": B, "seq_len": T, "heads": H, "dk": K, "dv": V, "levels": L,
+            "htype": ht.name,
             "dtype": "fp32 (bf16x3)" if dtype == torch.float32 else "bf16",
             "pass": "fwd+bwd" if backward else "fwd",
             "value": B * T / t, "unit": "tokens/s", "median_us": t * 1e6,
@@ -528,6 +532,11 @@ ONLY_CASES = {
     "c4_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
         "C4 fwd+bwd", (8, 8192, 24, 64, 64, 14), torch.bfloat16, dev, st, ev, n, w,
         backward=True),
+    "ns_strong_fwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "north star fwd, HType.STRONG", NS_SHAPE, torch.bfloat16, dev, st, ev, n, w, strong=True),
+    "ns_strong_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "north star fwd+bwd, HType.STRONG", NS_SHAPE, torch.bfloat16, dev, st, ev, n, w,
+        backward=True, strong=True),
     "gdn_fwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd",))[0],
     "gdn_fwd_bwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd_bwd",))[1],
 }
@@ -620,6 +629,13 @@ def main():
                 ("C4 fwd+bwd", (8, 8192, 24, 64, 64, 14), torch.bfloat16, True)):
             records.append(mamba2_fwd_record(name, shape, dt, dev, stream, evict, reps, 2,
                                              backward=bw))
+            torch.cuda.empty_cache()
+        # the strong hierarchy (HType.STRONG) at the north-star shape
+        for bw in (False, True):
+            records.append(mamba2_fwd_record(
+                "north star fwd+bwd, HType.STRONG" if bw else "north star fwd, HType.STRONG",
+                (B, T, H, K, V, L), torch.bfloat16, dev, stream, evict, reps, 2, backward=bw,
+                strong=True))
             torch.cuda.empty_cache()
 
         # log-linear Gated DeltaNet at BASELINE config 3 (MFMA-bound path)

@@ -130,6 +130,9 @@ int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void*
  * (bf16 MFMA; v and l in {BF16, FP32}) or all FP32 (bf16x3 kernels,
  * fp32-accurate; v and l FP32, dq / dk / dv written in fp32)
  *                                                  -> HATTN_ERR_NOT_IMPLEMENTED.
+ * htype HATTN_HTYPE_STRONG (the reference's USE_A2 / USE_H2 backward,
+ * chunkwise.py:1377-1580): BF16 q, k, v and do (l BF16 or FP32), T <= 64 *
+ * 2^9; else HATTN_ERR_NOT_IMPLEMENTED.  Any other htype -> HATTN_ERR_VALUE.
  */
 int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
                                const void* l, const void* do_, void* dq, void* dk, void* dv,
@@ -138,11 +141,13 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
                                int level_base, int htype, int chunk_size, void* workspace,
                                size_t workspace_bytes, void* stream);
 
-/* Workspace bytes of hattn_mamba2_chunkwise_bwd (segment summaries of both
- * scan directions and the q . dq row sums).  No counterpart in the reference,
- * which allocates fp32 h / dh per level inside chunkwise_bwd
+/* Workspace bytes of hattn_mamba2_chunkwise_bwd for the given htype (WEAK:
+ * segment summaries of both scan directions and the q . dq row sums; STRONG:
+ * the far dq / dlambda partials of the chunk walks and the adjoint of every
+ * chunk's state insertion).  No counterpart in the reference, which allocates
+ * fp32 h / dh (and hr / dhr for STRONG) per level inside chunkwise_bwd
  * (chunkwise.py:1371-1384). */
-size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
+size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L, int htype);
 
 /*
  * Log-linear Gated DeltaNet chunkwise forward.

@@ -28,6 +28,12 @@ hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const vo
                                           const float* g, const void* l, void* o, float* gcum,
                                           int B, int T, int G, int H, int V, int L, int dt_l,
                                           int dt_o, hipStream_t stream, int* unsupported);
+size_t hattn_mamba2_strong_bwd_ws_bytes(int B, int T, int H, int nlev);
+hipError_t hattn_mamba2_strong_bwd_launch(const void* q, const void* k, const void* v,
+                                          const float* gc, const void* l, const void* dO,
+                                          void* dq, void* dk, void* dv, float* dg, float* dl,
+                                          void* ws, int B, int T, int H, int L, int nlev,
+                                          int dt_l, hipStream_t stream, int* unsupported);
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V);
 int hattn_gdn_fwd_max_levels();
 int hattn_gdn_fwd_supports_k(int K);
@@ -277,10 +283,12 @@ int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void*
                                     need > 0 ? cap : 0, stream);
 }
 
-size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L) {
+size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L,
+                                             int htype) {
   (void)K;
   (void)L;
   if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0) return 0;
+  if (htype == HATTN_HTYPE_STRONG) return hattn_mamba2_strong_bwd_ws_bytes(B, T, H, ceil_log2(T / 64));
   return hattn_mamba2_bwd_ws_bytes(B, T, H, V, ceil_log2(T / 64));
 }
 
@@ -294,8 +302,8 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
-  if (htype != HATTN_HTYPE_WEAK)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (htype != HATTN_HTYPE_WEAK && htype != HATTN_HTYPE_STRONG)
+    return fail(HATTN_ERR_VALUE, "htype=%d", htype);
   if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
     return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
@@ -306,6 +314,32 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
   const int nlev = ceil_log2(T / 64);
   if (7 + nlev > L)
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (htype == HATTN_HTYPE_STRONG) {
+    // chunkwise.py:1286-1597 with USE_A2 / USE_H2 (MODE_H2 = 3)
+    if (nlev > hattn_mamba2_strong_max_levels())
+      return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d (HType.STRONG)", T,
+                  hattn_mamba2_strong_max_levels());
+    if (dtype_qk != HATTN_BF16 || dtype_v != HATTN_BF16 || dtype_do != HATTN_BF16)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                  "HType.STRONG: q/k, v, do dtype codes %d/%d/%d (bf16 required)", dtype_qk,
+                  dtype_v, dtype_do);
+    if (int st = check_span(T, max_of({(size_t)H * K * 2, (size_t)H * V * 2,
+                                        (size_t)H * L * elem_bytes(dtype_l), (size_t)H * 4})))
+      return st;
+    if (!q || !k || !v || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !dg || !dl)
+      return fail(HATTN_ERR_VALUE, "null tensor pointer");
+    const size_t need = hattn_mamba2_strong_bwd_ws_bytes(B, T, H, nlev);
+    if (workspace_bytes < need || workspace == nullptr)
+      return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
+                  workspace_bytes, need);
+    int unsupported = 0;
+    hipError_t e = hattn_mamba2_strong_bwd_launch(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl,
+                                                  workspace, B, T, H, L, nlev, dtype_l,
+                                                  (hipStream_t)stream, &unsupported);
+    if (unsupported)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: lambda dtype code %d", dtype_l);
+    return check_hip(e, "hattn_mamba2_chunkwise_bwd (strong) launch");
+  }
   if (nlev > hattn_mamba2_fwd_max_levels(0))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
                 hattn_mamba2_fwd_max_levels(0));

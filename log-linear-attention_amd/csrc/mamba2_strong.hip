@@ -30,46 +30,14 @@
 //          decay and lambda weights, from the two level tables in LDS)
 //   o^T += sum_j S_j^T (lam_j e^{Gc} Q)^T
 // and finally S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay.
-#include "mamba2_common.h"
+#include "mamba2_strong.h"
 
 namespace hattn {
 
-constexpr int kSC = 64;           // chunk
 constexpr int kSBV = 16;          // V columns per workgroup
-constexpr int kSMaxLev = 10;      // chunk-level levels 0 .. 9 (T <= 64 * 2^9)
 constexpr int kSLK = 64 + 8;      // row stride of the bf16 q / k tiles
 constexpr int kSLV = kSBV + 8;    // row stride of the bf16 v tiles
 
-// The strong level function of base.py:49-62 for t > s (t, s < 128), and its
-// two 64 x 64 chunk tables, built at compile time.
-constexpr int strong_level_ce(int t, int s) {
-  for (;;) {
-    int ell = 0;
-    while ((2 << ell) <= t) ++ell;          // floor(log2 t)
-    const int v = 1 << (ell > 0 ? ell - 1 : 0);
-    const int r = t - (1 << ell);
-    if (s < v) return ell + 1;
-    if (s < 2 * v && r >= v) return ell + 1;
-    if (s < 2 * v) {
-      t -= v;
-      s -= v;
-    } else {
-      t -= 2 * v;
-      s -= 2 * v;
-    }
-  }
-}
-struct StrongTables {
-  unsigned char intra[kSC * kSC];   // [a][b], a >= b: level of (a, b) inside a chunk
-  unsigned char sub[kSC * kSC];     // [a][b]: level of (64 + a, b)
-  constexpr StrongTables() : intra(), sub() {
-    for (int a = 0; a < kSC; ++a)
-      for (int b = 0; b < kSC; ++b) {
-        intra[a * kSC + b] = (unsigned char)(b < a ? strong_level_ce(a, b) : 0);
-        sub[a * kSC + b] = (unsigned char)strong_level_ce(kSC + a, b);
-      }
-  }
-};
 __device__ constexpr StrongTables kStrong{};
 
 struct StrongSmem {

@@ -7,7 +7,7 @@ Same names, arguments and return tuples as hattention/chunkwise.py:
 
 Both validate like the reference (``ValueError`` for non-contiguous tensors,
 T % 64, K/V multiples, too few levels; ``NotImplementedError`` for modes
-outside the weak base-2 hierarchy), allocate the outputs with torch on the
+outside the base-2 weak and strong hierarchies), allocate the outputs with torch on the
 inputs' device and launch the fused HIP kernels of libhattn_hip.so on the
 current stream.  There is no CPU path.
 """
@@ -42,11 +42,8 @@ def _shapes(q, k, v, l, head_first):
     return B, T, G, H, K, V, L
 
 
-def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size, strong_ok=False):
-    """chunkwise.py:1140-1153 and :1211-1214.  HType.STRONG has a forward
-    kernel (mamba2_strong.hip) and no backward kernel."""
-    if htype == HType.STRONG and not strong_ok:
-        raise NotImplementedError("HType.STRONG: the MI355X path has the forward only")
+def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
+    """chunkwise.py:1140-1153 and :1211-1214 (HType.WEAK and HType.STRONG)."""
     if htype not in (HType.WEAK, HType.STRONG):
         raise ValueError(f"htype={htype}")
     if level_base != 2:
@@ -118,7 +115,7 @@ def chunkwise_fwd(
     """
     _assert_contiguous(q=q, k=k, v=v, g=g, l=l)
     B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
-    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size, strong_ok=True)
+    _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size)
     if g.shape != (B, T, H):
         raise ValueError("g must be [B, T, H]")
     if g.dtype != torch.float32:
@@ -161,7 +158,7 @@ def _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype, chunk_size):
     dl = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
     lib = _lib.load()
     ws, ws_ptr, ws_bytes = _lib.workspace(
-        lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, KB, V, L), dev)
+        lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, KB, V, L, htype.value), dev)
     st = lib.hattn_mamba2_chunkwise_bwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
         _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
@@ -195,6 +192,11 @@ def chunkwise_bwd(
     dg (w.r.t. the raw per-step g) and dl in fp32, like the reference.  Grouped
     q / k are expanded per head before the kernels and their gradients summed
     over the group afterwards (chunkwise.py:1360-1362, 1583-1594).
+
+    HType.STRONG (bf16 q / k / v / do) runs the strong backward kernels: chunk
+    walks for the far levels (the forward's chunk-level strong cascade and its
+    transpose in reverse order) and chunk-parallel diagonal / sub-diagonal
+    blocks (chunkwise.py:1377-1580 with USE_A2 / USE_H2).
 
     The kernels take 64 key and 64 value dimensions.  Larger K and V (multiples
     of 64) run one launch per (key block, value block): with

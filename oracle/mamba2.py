@@ -44,7 +44,10 @@ Strong hierarchy (HType.STRONG): ``materialized_fwd(..., htype=STRONG)`` uses
 the strong level table (base.py:49-62 via oracle.levels), ``recurrent_fwd(...,
 htype=STRONG)`` the cascade of HState.cascade_strong (recurrent.py:56-74), and
 ``chunked_strong_fwd`` the chunk decomposition the HIP strong kernel
-implements.  The first two restate the reference's two definitions of the
+implements; ``chunked_strong_bwd`` restates the HIP strong backward's
+decomposition (chunk walks forward and, with the transposed cascade, in
+reverse; dense diagonal / sub-diagonal tiles) and is checked against autograd
+through ``chunked_strong_fwd``.  The first two restate the reference's two definitions of the
 strong hierarchy independently, and all three agree to 1e-12; a one-hot
 lambda with g == 0 is checked against a pair loop over the recursion and
 lambda == 1 against the plain SSD scan.
@@ -359,6 +362,141 @@ def chunked_strong_fwd(q, k, v, g, l, chunk_size: int = 64) -> torch.Tensor:
             S.states[..., 0] = kv[:, n]
             S.counts[0] += 1
     return y.reshape(B, T, H, V)
+
+
+def _strong_merge_levels(NT: int, LM: int):
+    """Merge level m of the chunk-level strong cascade at each step n (after n
+    insertions): levels 0 .. m-1 move up one level and m - 1 merges into m;
+    m == LM means the carry left the top level (recurrent.py:56-74)."""
+    cnt = [0] * LM
+    out = []
+    for _ in range(NT):
+        cc, m = 0, LM
+        for j in range(LM):
+            cap = 1 << max(j - 1, 0)
+            swap = j == 0 or cnt[j] + cc > cap
+            oc = cnt[j]
+            if swap:
+                cnt[j], cc = cc, oc
+            else:
+                cnt[j], cc = oc + cc, 0
+            if j >= 1 and m == LM and (not swap or oc == 0):
+                m = j
+        out.append(m)
+        cnt[0] += 1
+    return out
+
+
+def chunked_strong_bwd(q, k, v, g, l, do, chunk_size: int = 64, levels: int = 10):
+    """(dq, dk, dv, dg, dl) of sum(o * do) for the strong chunk decomposition of
+    ``chunked_strong_fwd``, by the decomposition the HIP strong backward
+    implements (the reference's strong backward is chunkwise.py:1377-1580 with
+    USE_A2 / USE_H2):
+
+    * far levels, forward in time: the chunk-level strong state S_j(n) (read
+      after the cascade of step n) gives dq_t += lam[t, 6 + j] e^{Gc_t} S_j do_t
+      and dlam[t, 6 + j] = e^{Gc_t} q_t . S_j do_t;
+    * far levels, backward in time: the adjoint A of the state runs the
+      transposed steps in reverse (A_0 is d kv_n, then A_0 = 0, A *= e^{Gc_last},
+      A_j += Q_n^T diag(lam[., 6 + j] e^{Gc}) dO_n, transposed cascade), and
+      kv_n = K_n^T diag(e^{Gc_last - Gc}) V_n gives dk, dv;
+    * diagonal / sub-diagonal blocks: dense 64 x 64 tiles with the two strong
+      level tables; dlam of levels 0 .. log2(C) + 1 binned by the tables;
+    * dG_t = q_t . dq_t - k_t . dk_t, dg_u = sum_{t >= u} dG_t.
+
+    ``levels``: chunk-level state levels (the kernels hold 10; the carry that
+    leaves the top is dropped, as in HState.cascade_strong).
+    """
+    C = chunk_size
+    G0 = q.shape[2]
+    q, k, v, g, l, (B, T, H, K, V, L, NT) = _chunk_views(q, k, v, g, l, C)
+    do_ = do.reshape(B, NT, C, H, V)
+    LM = levels
+    c = int(math.log2(C))
+    Gc = torch.cumsum(g, dim=2)                                       # [B,NT,C,H]
+    eg = torch.exp(Gc)
+    mlev = _strong_merge_levels(NT, LM)
+    far = [j for j in range(2, LM) if c + j < L]
+    # forward walk
+    S = torch.zeros(LM, B, H, K, V, dtype=q.dtype)
+    dq = torch.zeros_like(q)
+    dl = torch.zeros_like(l)
+    for n in range(NT):
+        m = mlev[n]
+        new = S.clone()
+        new[0] = 0
+        for e in range(1, LM):
+            if e < m:
+                new[e] = S[e - 1]
+            elif e == m:
+                new[e] = S[e] + S[e - 1]
+        S = new
+        for j in far:
+            Y = torch.einsum("bthv,bhkv->bthk", do_[:, n], S[j])
+            dq[:, n] += (l[:, n, :, :, c + j] * eg[:, n])[..., None] * Y
+            dl[:, n, :, :, c + j] += eg[:, n] * (q[:, n] * Y).sum(-1)
+        S = S * torch.exp(Gc[:, n, -1])[None, :, :, None, None]
+        w = torch.exp(Gc[:, n, -1:] - Gc[:, n])                       # [B,C,H]
+        S[0] = torch.einsum("bshk,bsh,bshv->bhkv", k[:, n], w, v[:, n])
+    # reverse walk
+    A = torch.zeros(LM, B, H, K, V, dtype=q.dtype)
+    adj = torch.zeros(B, NT, H, K, V, dtype=q.dtype)
+    for n in range(NT - 1, -1, -1):
+        adj[:, n] = A[0]
+        A[0] = 0
+        A = A * torch.exp(Gc[:, n, -1])[None, :, :, None, None]
+        for j in far:
+            f = l[:, n, :, :, c + j] * eg[:, n]                        # [B,C,H]
+            A[j] = A[j] + torch.einsum("bthk,bth,bthv->bhkv", q[:, n], f, do_[:, n])
+        m = mlev[n]
+        new = A.clone()
+        for e in range(min(m, LM)):
+            new[e] = A[e + 1] if e + 1 < LM else 0
+        A = new
+    # diagonal and sub-diagonal blocks
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    tt = torch.arange(C)[:, None].expand(C, C)
+    it = torch.from_numpy(strong_intra_table(C))
+    mask = torch.tril(torch.ones(C, C, dtype=torch.bool))
+    blocks = [(0, it, mask)]
+    if NT > 1:
+        blocks.append((1, torch.from_numpy(strong_subdiag_table(C)), None))
+    for back, tab, msk in blocks:
+        nt = slice(back, NT)
+        ns = slice(0, NT - back)
+        if back:
+            seg = Gc[:, nt, :, None, :] + (Gc[:, ns, -1:, :] - Gc[:, ns])[:, :, None, :, :]
+        else:
+            seg = Gc[:, :, :, None, :] - Gc[:, :, None, :, :]
+        E = torch.exp(seg)                                            # [B,n,t,s,H]
+        if msk is not None:
+            E = E * msk[None, None, :, :, None].to(E.dtype)
+        lam = l[:, nt].permute(0, 1, 3, 2, 4)[:, :, :, tt, tab].permute(0, 1, 3, 4, 2)
+        W = E * lam
+        Sc = torch.einsum("bnthk,bnshk->bntsh", q[:, nt], k[:, ns])
+        Dc = torch.einsum("bnthv,bnshv->bntsh", do_[:, nt], v[:, ns])
+        dq[:, nt] += torch.einsum("bntsh,bnshk->bnthk", W * Dc, k[:, ns])
+        dk[:, ns] += torch.einsum("bntsh,bnthk->bnshk", W * Dc, q[:, nt])
+        dv[:, ns] += torch.einsum("bntsh,bnthv->bnshv", W * Sc, do_[:, nt])
+        Mx = E * Sc * Dc
+        for lev in range(min(c + 2, L)):
+            sel = (tab == lev)
+            if msk is not None:
+                sel = sel & msk
+            dl[:, nt, :, :, lev] += (Mx * sel[None, None, :, :, None].to(Mx.dtype)).sum(3)
+    w = torch.exp(Gc[:, :, -1:] - Gc)                                  # [B,NT,C,H]
+    dk += w[..., None] * torch.einsum("bnshv,bnhkv->bnshk", v, adj)
+    dv += w[..., None] * torch.einsum("bnshk,bnhkv->bnshv", k, adj)
+    dG = (q * dq).sum(-1) - (k * dk).sum(-1)                          # [B,NT,C,H]
+    dG = dG.reshape(B, T, H)
+    dg = dG.flip(1).cumsum(1).flip(1)
+    dq = dq.reshape(B, T, H, K)
+    dk = dk.reshape(B, T, H, K)
+    if G0 != H:
+        dq = dq.view(B, T, G0, H // G0, K).sum(3)
+        dk = dk.view(B, T, G0, H // G0, K).sum(3)
+    return dq, dk, dv.reshape(B, T, H, V), dg, dl.reshape(B, T, H, L)
 
 
 def chunked_scan_fwd(q, k, v, g, l, chunk_size: int = 64,

@@ -133,6 +133,46 @@ def test_status_maps_to_reference_exceptions():
     assert lib.hattn_last_error() is not None
 
 
+def _bwd(**kw):
+    """Mamba-2 backward with NULL tensor pointers: every case fails in the
+    host-side validation, before any HIP call."""
+    a = dict(B=1, T=128, H=1, K=64, V=64, L=8, dq=0, dv=0, dl=0, do=0, base=2, htype=0,
+             chunk=64, ws=1 << 30)
+    a.update(kw)
+    lib = _lib.load()
+    p = ctypes.c_void_p(None)
+    return lib.hattn_mamba2_chunkwise_bwd(p, p, p, p, p, p, p, p, p, p, p, a["B"], a["T"], a["H"],
+                                          a["K"], a["V"], a["L"], a["dq"], a["dv"], a["dl"],
+                                          a["do"], a["base"], a["htype"], a["chunk"], p, a["ws"],
+                                          None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(T=100), _lib.HATTN_ERR_VALUE),            # T % 64
+    (dict(L=7), _lib.HATTN_ERR_VALUE),              # L < 7 + ceil(log2(T/64))
+    (dict(K=96), _lib.HATTN_ERR_VALUE),             # K, V multiples of 64
+    (dict(K=128), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # one 64-wide block per call
+    (dict(htype=2), _lib.HATTN_ERR_VALUE),          # neither WEAK nor STRONG
+    (dict(htype=1, dq=2, dv=2, dl=2, do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # STRONG: bf16
+    (dict(htype=1, T=64 << 10, L=20), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # STRONG: > 9 levels
+    (dict(htype=1), _lib.HATTN_ERR_VALUE),          # STRONG, valid: fails on the null pointers
+    (dict(), _lib.HATTN_ERR_VALUE),                 # WEAK, valid: fails on the null pointers
+])
+def test_bwd_argument_checks(kw, code):
+    assert _bwd(**kw) == code
+    assert _lib.load().hattn_last_error().decode()
+
+
+def test_bwd_workspace_query_per_htype():
+    lib = _lib.load()
+    assert lib.hattn_mamba2_chunkwise_bwd_workspace(1, 100, 1, 64, 64, 8, 0) == 0
+    weak = lib.hattn_mamba2_chunkwise_bwd_workspace(2, 4096, 4, 64, 64, 13, 0)
+    strong = lib.hattn_mamba2_chunkwise_bwd_workspace(2, 4096, 4, 64, 64, 13, 1)
+    assert weak > 0 and strong > 0 and weak != strong
+    # the strong workspace holds at least the fp32 far dq and the bf16 adjoint tiles
+    assert strong >= 2 * 4096 * 4 * 64 * (4 + 2)
+
+
 def _gdn_bwd(**kw):
     """NULL tensor pointers: every case fails in the host-side validation, before
     any HIP call (the workspace case on the null check or the size check)."""

@@ -2,14 +2,18 @@
 
 The HIP paths run through the C-ABI: the strong chunkwise forward
 (hattention.chunkwise.chunkwise_fwd with HType.STRONG -> hattn_mamba2_chunkwise_fwd
--> mamba2_strong.hip) and the decode step with the strong cascade
-(hattention.kernel.hattention_step -> hattn_hstate_step).  The checkers are
-the oracle's strong forms in float64 on the CPU (oracle.mamba2.chunked_strong_fwd
-and recurrent_fwd(htype=STRONG), pinned against the materialised strong table
-of base.py:49-62 and against each other), fed the identical inputs.
+-> mamba2_strong.hip), the strong backward (chunkwise_bwd ->
+hattn_mamba2_chunkwise_bwd -> mamba2_strong_bwd.hip) and the decode step with
+the strong cascade (hattention.kernel.hattention_step -> hattn_hstate_step).
+The checkers are the oracle's strong forms in float64 on the CPU
+(oracle.mamba2.chunked_strong_fwd and recurrent_fwd(htype=STRONG), pinned
+against the materialised strong table of base.py:49-62 and against each
+other; the gradients by torch.autograd through chunked_strong_fwd), fed the
+identical inputs.
 
 Tolerances as the weak tests: bf16 inputs max|o - o_ref| / max|o_ref| < 2e-2 and
-relative Frobenius error < 1e-2; level states of the decode 2e-2 per level.
+relative Frobenius error < 1e-2 (5e-2 for dg); level states of the decode 2e-2
+per level.
 """
 import math
 
@@ -89,23 +93,107 @@ def test_strong_differs_from_weak():
     assert mx > 0.1, mx
 
 
-def test_strong_hattention_kernel_forward_and_backward_raises():
-    """HAttentionFunction with HType.STRONG: the forward runs the strong kernel;
-    the backward (no strong backward kernel) raises NotImplementedError."""
+def test_strong_hattention_kernel_forward_and_backward():
+    """HAttentionFunction with HType.STRONG: the forward runs the strong kernel,
+    the backward the strong backward kernels; gradients in the input dtypes
+    against autograd through the oracle (kernel.py:230-244)."""
     from hattention.base import HType, HStruct
     from hattention.kernel import hattention_kernel
     B, T, H, K, V, L = 1, 256, 2, 64, 64, 9
-    q, k, v, g, l = (x.to(DEV) for x in make_mamba2_inputs(B, T, H, K, V, L, seed=11))
-    with torch.no_grad():
-        o = hattention_kernel(q, k, v, None, g, l, None, False, 2, HType.STRONG, HStruct.MAMBA2)
-    ref = M.chunked_strong_fwd(*(x.double().cpu() for x in (q, k, v, g, l)), chunk_size=64)
-    mx, fro = _errs(o, ref)
+    q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, seed=11, with_do=True)
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v, g, l)]
+    o = hattention_kernel(leaves[0], leaves[1], leaves[2], None, leaves[3], leaves[4], None,
+                          False, 2, HType.STRONG, HStruct.MAMBA2)
+    ref_o = M.chunked_strong_fwd(*(x.double() for x in (q, k, v, g, l)), chunk_size=64)
+    mx, fro = _errs(o.detach(), ref_o)
     assert mx < TOL_MAX and fro < TOL_FRO, (mx, fro)
-    leaves = [x.detach().clone().requires_grad_(True) for x in (q, k, v, g, l)]
-    out = hattention_kernel(leaves[0], leaves[1], leaves[2], None, leaves[3], leaves[4], None,
-                            False, 2, HType.STRONG, HStruct.MAMBA2)
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+    (o.float() * do.to(DEV).float()).sum().backward()
+    ref = M.autograd_bwd(M.chunked_strong_fwd, *(x.double() for x in (q, k, v, g, l, do)),
+                         chunk_size=64)
+    for name, x, r in zip(NAMES, leaves, ref):
+        assert x.grad is not None and x.grad.dtype == x.dtype, name
+        mx, fro = _errs(x.grad, r)
+        tf = TOL_FRO_DG if name == "dg" else TOL_FRO
+        assert mx < TOL_MAX and fro < tf, (name, mx, fro)
+
+
+# ---------------------------------------------------------------------------
+# backward (chunkwise_bwd with HType.STRONG)
+# ---------------------------------------------------------------------------
+NAMES = ("dq", "dk", "dv", "dg", "dl")
+# dg is the reverse cumsum of dG_t = q_t . dq_t - k_t . dk_t, which cancels
+# heavily (sum_t dG_t = 0): the weak backward's bound, 5e-2 relative Frobenius
+# on dg, with the max-abs/rel 2e-2 kept.
+TOL_FRO_DG = 5e-2
+
+
+def _run_bwd(B, T, G, H, K, V, L, seed, rows=None, ldtype=None, full=False):
+    """chunkwise_bwd(HType.STRONG) against autograd through
+    oracle.mamba2.chunked_strong_fwd in float64 on the identical inputs: every
+    row (full=True: one vectorised oracle call over the whole batch) or the
+    listed rows."""
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_bwd, chunkwise_fwd
+    q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=seed, ldtype=ldtype,
+                                           with_do=True)
+    print(f"[strong bwd] B={B} T={T} G={G} H={H} K={K} V={V} L={L} lambda={l.dtype}", flush=True)
+    qd, kd, vd, gd, ld, dod = (x.to(DEV) for x in (q, k, v, g, l, do))
+    _, gc, _ = chunkwise_fwd(qd, kd, vd, gd, ld, False, 2, HType.STRONG, 64, False)
+    grads = chunkwise_bwd(qd, kd, vd, gc, ld, dod, False, 2, HType.STRONG, 64)
+    torch.cuda.synchronize()
+    assert grads[0].dtype == q.dtype and grads[2].dtype == v.dtype
+    assert grads[3].dtype == torch.float32 and grads[4].dtype == torch.float32
+    if full:
+        ref = M.autograd_bwd(M.chunked_strong_fwd, *(x.double() for x in (q, k, v, g, l, do)),
+                             chunk_size=64)
+        for name, a_, r in zip(NAMES, grads, ref):
+            mx, fro = _errs(a_, r)
+            print(f"  all rows {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+            tf = TOL_FRO_DG if name == "dg" else TOL_FRO
+            assert mx < TOL_MAX and fro < tf, (name, mx, fro)
+        return grads
+    assert G == H, "row checks of grouped dq / dk need the whole group"
+    rows = rows or [(b, h) for b in range(B) for h in range(H)]
+    for (b, h) in rows:
+        sl = lambda x: x[b:b + 1, :, h:h + 1].double()
+        ref = M.autograd_bwd(M.chunked_strong_fwd, *(sl(x) for x in (q, k, v, g, l, do)),
+                             chunk_size=64)
+        for name, a_, r in zip(NAMES, grads, ref):
+            mx, fro = _errs(a_[b:b + 1, :, h:h + 1], r)
+            print(f"  row ({b},{h}) {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+            tf = TOL_FRO_DG if name == "dg" else TOL_FRO
+            assert mx < TOL_MAX and fro < tf, (b, h, name, mx, fro)
+    return grads
+
+
+@pytest.mark.parametrize("T", [64, 128, 192, 640, 1024])
+def test_strong_bwd_lengths(T):
+    """one chunk (no sub-diagonal block, no far level), two chunks (no far
+    level), ragged chunk counts and several far levels"""
+    _run_bwd(1, T, 2, 2, 64, 64, _levels(T), seed=100 + T, full=True)
+
+
+def test_strong_bwd_more_levels_than_needed():
+    """L above 7 + ceil(log2(T/64)): the unused dlambda columns are zero"""
+    g = _run_bwd(1, 1024, 1, 1, 64, 64, 14, seed=77, full=True)
+    assert g[4][..., 11:].abs().max().item() == 0.0
+
+
+def test_strong_bwd_groups_k128_v128_fp32_lambda():
+    """grouped q / k (dq, dk summed over the group), K = V = 128 (one launch per
+    64-wide key / value block, gradients summed in fp32), fp32 lambda"""
+    _run_bwd(2, 512, 1, 2, 128, 128, 10, seed=5, ldtype=torch.float32, full=True)
+
+
+def test_strong_bwd_many_rows():
+    """every (batch, head) row of a grid that spans several XCD groups"""
+    _run_bwd(3, 2048, 6, 6, 64, 64, 12, seed=9, full=True)
+
+
+def test_strong_bwd_north_star_shape():
+    """the north-star shape (B=4 T=16384 H=16 d=64 L=15) with the strong
+    hierarchy: rows at both ends of the grid"""
+    _run_bwd(4, 16384, 16, 16, 64, 64, 15, seed=1001, rows=[(0, 0), (3, 15)])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

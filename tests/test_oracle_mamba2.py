@@ -260,3 +260,19 @@ def test_strong_lambda_one_is_plain_ssd():
     q, k, v, g, l = make_inputs(1, T, 2, 4, 3, 9, seed=3)
     o = M.chunked_strong_fwd(q, k, v, g, torch.ones_like(l), chunk_size=16)
     assert rel(o, M.ssd_scan_fwd(q, k, v, g)) < 1e-12
+
+
+@pytest.mark.parametrize("T,C,G", [(64, 16, 2), (256, 16, 1), (320, 64, 2), (1024, 64, 1)])
+def test_strong_backward_decomposition_matches_autograd(T, C, G):
+    """chunked_strong_bwd (chunk walks forward and, through the transposed
+    cascade, in reverse; dense diagonal / sub-diagonal tiles; dG identity)
+    against torch.autograd through the materialised strong table of
+    base.py:49-62 (a structurally different form), grouped q / k included."""
+    L = int(math.log2(T)) + 3
+    q, k, v, g, l = make_inputs(1, T, 2, 5, 4, L, G=G, seed=T + C)
+    do = torch.randn(1, T, 2, 4, generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+    got = M.chunked_strong_bwd(q, k, v, g, l, do, chunk_size=C)
+    ref = M.autograd_bwd(lambda *a: M.materialized_fwd(*a, htype=M.STRONG), q, k, v, g, l, do)
+    for name, a, r in zip(("dq", "dk", "dv", "dg", "dl"), got, ref):
+        assert a.shape == r.shape, name
+        assert rel(a, r) < 1e-11, (name, rel(a, r))

@@ -37,6 +37,11 @@ namespace hattn {
 constexpr int kSBV = 16;          // V columns per workgroup
 constexpr int kSLK = 64 + 8;      // row stride of the bf16 q / k tiles
 constexpr int kSLV = kSBV + 8;    // row stride of the bf16 v tiles
+// Row strides of the per-token LDS rows that each lane of a 16-lane group reads
+// for a different token: 33 words (lambda) and 17 words (level tables) put
+// the 16 rows on 16 different banks.
+constexpr int kSLam = 33;
+constexpr int kSTab = 17;
 
 __device__ constexpr StrongTables kStrong{};
 
@@ -46,8 +51,8 @@ struct StrongSmem {
   __bf16 v[2][kSC * kSLV];
   __bf16 hs[kSMaxLev][kSBV * kSLK];  // chunk-level states, bf16 [v][k]
   float gc[2][kSC];                  // chunk-local inclusive cumsum of g
-  float lam[kSC][32];                // lambda[t, 0 .. L-1] of this chunk (L <= 32)
-  unsigned char tab[2][kSC * kSC];   // intra / sub level tables
+  float lam[kSC][kSLam];             // lambda[t, 0 .. L-1] of this chunk (L <= 32)
+  unsigned tab[2][kSC * kSTab];      // intra / sub level tables, four levels a word
 };
 
 template <typename TL, typename TO>
@@ -68,9 +73,9 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
   const size_t hk = (size_t)G * 64, hv = (size_t)H * V;
   const int t_me = 16 * w + ln;   // this lane's token in the transposed products
 
-  for (int i = tid; i < kSC * kSC; i += 256) {
-    s.tab[0][i] = kStrong.intra[i];
-    s.tab[1][i] = kStrong.sub[i];
+  for (int i = tid; i < kSC * kSC / 4; i += 256) {
+    s.tab[0][(i >> 4) * kSTab + (i & 15)] = ((const unsigned*)kStrong.intra)[i];
+    s.tab[1][(i >> 4) * kSTab + (i & 15)] = ((const unsigned*)kStrong.sub)[i];
   }
 
   floatx4 st[kSMaxLev];
@@ -79,6 +84,37 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
   int cnt[kSMaxLev];
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) cnt[j] = 0;
+
+  // Inputs of one chunk in registers, loaded one chunk ahead so their latency
+  // hides behind the previous chunk's products: q / k rows (16 columns per
+  // thread), a v unit, g (wave 0) and up to eight lambda entries per thread
+  // (64 x L <= 2048).
+  const int r_ld = tid >> 2, c_ld = 16 * (tid & 3);
+  const int rv_ld = tid >> 1, cv_ld = 8 * (tid & 1);
+  int lrel[8], llds[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int i = min(tid + 256 * u, kSC * L - 1);
+    lrel[u] = (i / L) * H * L + i % L;
+    llds[u] = (i / L) * kSLam + i % L;
+  }
+  u32x4 pq0, pq1, pk0, pk1, pv;
+  float pg;
+  TL pl[8];
+  auto prefetch = [&](int jc) __attribute__((always_inline)) {
+    const size_t t0 = (size_t)b * T + (size_t)jc * kSC;
+    const size_t rq = (t0 + r_ld) * hk + (size_t)gq * 64 + c_ld;
+    pq0 = *(const u32x4*)(q + rq);
+    pq1 = *(const u32x4*)(q + rq + 8);
+    pk0 = *(const u32x4*)(k + rq);
+    pk1 = *(const u32x4*)(k + rq + 8);
+    pv = *(const u32x4*)(v + (t0 + (tid < 128 ? rv_ld : 0)) * hv + (size_t)h * V + v0 + cv_ld);
+    pg = g[(t0 + lane) * H + h];
+    const TL* lb = l + (t0 * H + h) * L;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) pl[u] = lb[lrel[u]];
+  };
+  prefetch(0);
 
   for (int ic = 0; ic < NT; ++ic) {
     const int par = ic & 1;
@@ -104,21 +140,13 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
     }
     // ---- stage: q, k, v tiles, g cumsum, lambda, levels >= 2 -------------------------
     {
-      const int r = tid >> 2, c16 = 16 * (tid & 3);
-      const size_t rq = (tok0 + r) * hk + (size_t)gq * 64 + c16;
-      const u32x4 q0 = *(const u32x4*)(q + rq), q1 = *(const u32x4*)(q + rq + 8);
-      const u32x4 k0 = *(const u32x4*)(k + rq), k1 = *(const u32x4*)(k + rq + 8);
-      *(u32x4*)(s.q + r * kSLK + c16) = q0;
-      *(u32x4*)(s.q + r * kSLK + c16 + 8) = q1;
-      *(u32x4*)(s.k[par] + r * kSLK + c16) = k0;
-      *(u32x4*)(s.k[par] + r * kSLK + c16 + 8) = k1;
-      if (tid < 128) {
-        const int rv = tid >> 1, cv = 8 * (tid & 1);
-        *(u32x4*)(s.v[par] + rv * kSLV + cv) =
-            *(const u32x4*)(v + (tok0 + rv) * hv + (size_t)h * V + v0 + cv);
-      }
+      *(u32x4*)(s.q + r_ld * kSLK + c_ld) = pq0;
+      *(u32x4*)(s.q + r_ld * kSLK + c_ld + 8) = pq1;
+      *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld) = pk0;
+      *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld + 8) = pk1;
+      if (tid < 128) *(u32x4*)(s.v[par] + rv_ld * kSLV + cv_ld) = pv;
       if (w == 0) {
-        float x = g[(tok0 + lane) * H + h];
+        float x = pg;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
           const float y = __shfl_up(x, d, 64);
@@ -127,13 +155,15 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
         s.gc[par][lane] = x;
         if (v0 == 0) gcum[(tok0 + lane) * H + h] = x;
       }
-      for (int i = tid; i < kSC * L; i += 256)
-        s.lam[i / L][i % L] = to_f32<TL>(l[((tok0 + i / L) * H + h) * L + i % L]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (tid + 256 * u < kSC * L) (&s.lam[0][0])[llds[u]] = to_f32<TL>(pl[u]);
 #pragma unroll
       for (int j = 2; j < kSMaxLev; ++j)
         *(bf16x4*)(s.hs[j] + ln * kSLK + 16 * w + 4 * lq) = cvt4(st[j]);
     }
     __syncthreads();
+    if (ic + 1 < NT) prefetch(ic + 1);
 
     // ---- o^T[v][t] for t = 16 w + ln ----------------------------------------------------
     floatx4 acc = zero4();   // o^T[v = 4 lq + i][t = t_me]
@@ -146,7 +176,7 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
     for (int cur = 1; cur >= 0; --cur) {
       if (!cur && ic == 0) break;
       const int pk = cur ? par : par ^ 1;
-      const unsigned char* tab = s.tab[cur ? 0 : 1];
+      const unsigned* tab = s.tab[cur ? 0 : 1] + t_me * kSTab;
       const float* lrow = s.lam[t_me];
       // the source tiles of the block: the diagonal stops at this wave's tile
       const int npair = cur ? (w >> 1) + 1 : 2;
@@ -160,12 +190,13 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
           sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 8 * lq), bq0, sc);
           sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 32 + 8 * lq), bq1, sc);
           // sc[i] = q_t . k_s, s = 16 n + 4 lq + i, t = t_me
+          const unsigned lv4 = tab[4 * n + lq];   // levels of the lane's four sources
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int sp = 16 * n + 4 * lq + i;
             float x = 0.f;
             if (!cur || sp <= t_me) {
-              const int lev = tab[t_me * kSC + sp];
+              const int lev = (lv4 >> (8 * i)) & 0xff;
               x = sc[i] * fexp(gct + base - s.gc[pk][sp]) * lrow[lev];
             }
             pb[4 * half + i] = (__bf16)x;

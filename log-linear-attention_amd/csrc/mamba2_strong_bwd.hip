@@ -96,37 +96,72 @@ struct WalkArgs {
   int rows, T, H, L, nf;
 };
 
-// Stage the chunk's dO (and for the forward walk V), the 16-column q (and k)
-// slice, Gc and the far lambda weights.
+// The chunk's dO (and for the forward walk V), the 16-column q (and k) slice,
+// Gc and the far lambda weights, loaded into registers one chunk ahead
+// (walk_load) and written to LDS at the chunk start (walk_store).
+template <typename TL>
+struct WalkPre {
+  u32x4 d0, d1, v0, v1, q, k;
+  float g;
+  TL lf[2];
+  float gf[2];
+};
+
 template <typename TL, bool FWD>
-__device__ __forceinline__ void walk_stage(WalkSmem& s, const WalkArgs& a, size_t tok0, int h,
-                                           int k0) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__device__ __forceinline__ void walk_load(WalkPre<TL>& p, const WalkArgs& a, size_t tok0, int h,
+                                          int k0) {
+  const int tid = threadIdx.x, lane = tid & 63;
   const size_t hd = (size_t)a.H * 64;
   {
     const int r = tid >> 2, c16 = 16 * (tid & 3);
     const size_t off = (tok0 + r) * hd + (size_t)h * 64 + c16;
-    const u32x4 d0 = *(const u32x4*)(a.dO + off), d1 = *(const u32x4*)(a.dO + off + 8);
-    *(u32x4*)(s.d + r * kWLd + c16) = d0;
-    *(u32x4*)(s.d + r * kWLd + c16 + 8) = d1;
+    p.d0 = *(const u32x4*)(a.dO + off);
+    p.d1 = *(const u32x4*)(a.dO + off + 8);
     if constexpr (FWD) {
-      const u32x4 v0 = *(const u32x4*)(a.v + off), v1 = *(const u32x4*)(a.v + off + 8);
-      *(u32x4*)(s.v + r * kWLd + c16) = v0;
-      *(u32x4*)(s.v + r * kWLd + c16 + 8) = v1;
+      p.v0 = *(const u32x4*)(a.v + off);
+      p.v1 = *(const u32x4*)(a.v + off + 8);
+    }
+  }
+  {
+    const int r = (tid & 127) >> 1, c8 = 8 * (tid & 1);
+    const size_t off = (tok0 + r) * hd + (size_t)h * 64 + k0 + c8;
+    p.q = *(const u32x4*)(a.q + off);
+    if constexpr (FWD) p.k = *(const u32x4*)(a.k + off);
+  }
+  p.g = a.gc[(tok0 + lane) * a.H + h];
+  const TL* l = (const TL*)a.l;
+  const int nf1 = a.nf > 0 ? a.nf : 1;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = min(tid + 256 * u, nf1 * kSC - 1);
+    const size_t tk = (tok0 + i / nf1) * a.H + h;
+    p.lf[u] = l[tk * a.L + min(8 + i % nf1, a.L - 1)];   // column clamped for nf == 0
+    p.gf[u] = a.gc[tk];
+  }
+}
+
+template <typename TL, bool FWD>
+__device__ __forceinline__ void walk_store(WalkSmem& s, const WalkPre<TL>& p, const WalkArgs& a) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  {
+    const int r = tid >> 2, c16 = 16 * (tid & 3);
+    *(u32x4*)(s.d + r * kWLd + c16) = p.d0;
+    *(u32x4*)(s.d + r * kWLd + c16 + 8) = p.d1;
+    if constexpr (FWD) {
+      *(u32x4*)(s.v + r * kWLd + c16) = p.v0;
+      *(u32x4*)(s.v + r * kWLd + c16 + 8) = p.v1;
     }
   }
   if (tid < 128) {
     const int r = tid >> 1, c8 = 8 * (tid & 1);
-    const size_t off = (tok0 + r) * hd + (size_t)h * 64 + k0 + c8;
-    *(u32x4*)(s.q + r * kWLs + c8) = *(const u32x4*)(a.q + off);
-    if constexpr (FWD) *(u32x4*)(s.k + r * kWLs + c8) = *(const u32x4*)(a.k + off);
+    *(u32x4*)(s.q + r * kWLs + c8) = p.q;
+    if constexpr (FWD) *(u32x4*)(s.k + r * kWLs + c8) = p.k;
   }
-  if (w == 0) s.gc[lane] = a.gc[(tok0 + lane) * a.H + h];
-  const TL* l = (const TL*)a.l;
-  for (int i = tid; i < a.nf * kSC; i += 256) {
-    const int t = i / a.nf, jj = i % a.nf;
-    const size_t tk = (tok0 + t) * a.H + h;
-    s.f[jj][t] = to_f32<TL>(l[tk * a.L + 8 + jj]) * fexp(a.gc[tk]);
+  if (w == 0) s.gc[lane] = p.g;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = tid + 256 * u;
+    if (i < a.nf * kSC) s.f[i % a.nf][i / a.nf] = to_f32<TL>(p.lf[u]) * fexp(p.gf[u]);
   }
 }
 
@@ -144,8 +179,9 @@ __device__ __forceinline__ void strong_walk_fwd(WalkSmem& s, const WalkArgs& a, 
     st[j] = zero4();
     cnt[j] = 0;
   }
+  WalkPre<TL> pre;
+  walk_load<TL, true>(pre, a, (size_t)b * a.T, h, k0);
   for (int ic = 0; ic < NT; ++ic) {
-    const size_t tok0 = (size_t)b * a.T + (size_t)ic * kSC;
     // cascade (recurrent.py:56-74) over the chunk-level states
     {
       floatx4 carry = zero4();
@@ -165,13 +201,14 @@ __device__ __forceinline__ void strong_walk_fwd(WalkSmem& s, const WalkArgs& a, 
         cc = swap ? oc : 0;
       }
     }
-    walk_stage<TL, true>(s, a, tok0, h, k0);
+    walk_store<TL, true>(s, pre, a);
 #pragma unroll
     for (int j = 2; j < kSMaxLev; ++j)
       if (j - 2 < a.nf)
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.hs[j][(4 * lq + i) * kWLd + 16 * w + ln] = (__bf16)st[j][i];
     __syncthreads();
+    if (ic + 1 < NT) walk_load<TL, true>(pre, a, (size_t)b * a.T + (size_t)(ic + 1) * kSC, h, k0);
 
     // Y^T[k][t] = S_j[k][v] dO^T[v][t] for the lane's token t_me, k = k0 + 4 lq + i
     const bf16x8 bd0 = *(const bf16x8*)(s.d + t_me * kWLd + 8 * lq);
@@ -251,9 +288,10 @@ __device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, 
   floatx4 st[kSMaxLev];   // A_j[k = k0 + 4 lq + i][v = 16 w + ln]
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) st[j] = zero4();
+  WalkPre<TL> pre;
+  walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(NT - 1) * kSC, h, k0);
   for (int ic = NT - 1; ic >= 0; --ic) {
-    const size_t tok0 = (size_t)b * a.T + (size_t)ic * kSC;
-    walk_stage<TL, false>(s, a, tok0, h, k0);
+    walk_store<TL, false>(s, pre, a);
     {
       __bf16* ap = a.ws.adj + (((size_t)row * NT + ic) * 64 + k0 + 4 * lq) * 64 + 16 * w + ln;
 #pragma unroll
@@ -261,6 +299,7 @@ __device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, 
     }
     st[0] = zero4();
     __syncthreads();
+    if (ic > 0) walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(ic - 1) * kSC, h, k0);
     const float gd = fexp(s.gc[kSC - 1]);
 #pragma unroll
     for (int j = 1; j < kSMaxLev; ++j)
@@ -372,6 +411,34 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dq_kernel(
   const size_t rme = (tok0 + t_me) * hd + hoff;
   const bf16x8 bq0 = *(const bf16x8*)(q + rme + 8 * lq), bq1 = *(const bf16x8*)(q + rme + 32 + 8 * lq);
   const bf16x8 bd0 = *(const bf16x8*)(dO + rme + 8 * lq), bd1 = *(const bf16x8*)(dO + rme + 32 + 8 * lq);
+  // every later global read, issued now: the level-table words of the lane's
+  // source tiles, the far dq and q (q . dq), the far dlambda partials
+  unsigned lvw[2][4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    lvw[0][st] = *(const unsigned*)(kStrongB.sub + t_me * kSC + 16 * st + 4 * lq);
+    lvw[1][st] = *(const unsigned*)(kStrongB.intra + t_me * kSC + 16 * st + 4 * lq);
+  }
+  floatx4 fq[4];
+  bf16x4 qk4[4];
+  {
+    const float* fp = ws.dqf + ((size_t)row * T + (size_t)n * kSC + t_me) * 64 + 4 * lq;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      fq[kt] = *(const floatx4*)(fp + 16 * kt);
+      qk4[kt] = *(const bf16x4*)(q + rme + 16 * kt + 4 * lq);
+    }
+  }
+  const int t_dl = tid >> 2, l0 = tid & 3;
+  float dlp[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int jj = min(l0 + 4 * u, nf > 0 ? nf - 1 : 0);
+#pragma unroll
+    for (int kap = 0; kap < 4; ++kap)
+      dlp[u][kap] = nf > 0 ? ws.dlf[(((size_t)kap * rows + row) * T + (size_t)n * kSC + t_dl) * nf + jj]
+                           : 0.f;
+  }
   __syncthreads();
 
   const float gct = s.gc[1][t_me];
@@ -386,7 +453,6 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dq_kernel(
       for (int st = 0; st < 4; ++st) *(floatx4*)(mrow + 16 * st + 4 * lq) = zero4();
       continue;
     }
-    const unsigned char* tab = cur ? kStrongB.intra : kStrongB.sub;
     const float base = cur ? 0.f : s.gc[0][kSC - 1];
     const int npair = cur ? (w >> 1) + 1 : 2;
     for (int p = 0; p < npair; ++p) {
@@ -400,7 +466,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dq_kernel(
         sc = mfma16x16x32(*(const bf16x8*)(kr + 32), bq1, sc);
         floatx4 dd = mfma16x16x32(*(const bf16x8*)vr, bd0, zero4());
         dd = mfma16x16x32(*(const bf16x8*)(vr + 32), bd1, dd);
-        const unsigned lv4 = *(const unsigned*)(tab + t_me * kSC + 16 * st + 4 * lq);
+        const unsigned lv4 = lvw[cur][st];
         floatx4 mv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -423,16 +489,13 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dq_kernel(
 
   // dq: far part, q . dq, store
   {
-    const float* fq = ws.dqf + ((size_t)row * T + (size_t)n * kSC + t_me) * 64 + 4 * lq;
     float qd = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      const floatx4 f = *(const floatx4*)(fq + 16 * kt);
-      const bf16x4 q4 = *(const bf16x4*)(q + rme + 16 * kt + 4 * lq);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[kt][i] += f[i];
-        qd += (float)q4[i] * acc[kt][i];
+        acc[kt][i] += fq[kt][i];
+        qd += (float)qk4[kt][i] * acc[kt][i];
       }
       *(bf16x4*)(dq + rme + 16 * kt + 4 * lq) = cvt4(acc[kt]);
     }
@@ -445,23 +508,20 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dq_kernel(
   // dlambda row of every target: levels 0 .. 7 from their source ranges, far
   // levels from the four slice partials, zero above
   {
-    const int t = tid >> 2, l0 = tid & 3;
+    const int t = t_dl;
     float* dlrow = dl + ((tok0 + t) * H + h) * L;
     const float* mr = s.m + t * kMLd;
 #pragma unroll
     for (int l = l0; l < kSLocLev; l += 4) {
       const int lo = kStrongR.lo[t][l], hi = kStrongR.hi[t][l];
       float x = 0.f;
+#pragma unroll 8
       for (int i = lo; i < hi; ++i) x += mr[i];
       if (l < L) dlrow[l] = x;
     }
-    for (int jj = l0; jj < nf; jj += 4) {
-      float x = 0.f;
 #pragma unroll
-      for (int kap = 0; kap < 4; ++kap)
-        x += ws.dlf[(((size_t)kap * rows + row) * T + (size_t)n * kSC + t) * nf + jj];
-      dlrow[kSLocLev + jj] = x;
-    }
+    for (int u = 0; u < 2; ++u)
+      if (l0 + 4 * u < nf) dlrow[kSLocLev + l0 + 4 * u] = dlp[u][0] + dlp[u][1] + dlp[u][2] + dlp[u][3];
     for (int c = kSLocLev + nf + l0; c < L; c += 4) dlrow[c] = 0.f;
   }
 }
@@ -539,6 +599,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dkv_kernel(
   const size_t rme = (tok0 + s_me) * hd + hoff;
   const bf16x8 bk0 = *(const bf16x8*)(k + rme + 8 * lq), bk1 = *(const bf16x8*)(k + rme + 32 + 8 * lq);
   const bf16x8 bv0 = *(const bf16x8*)(v + rme + 8 * lq), bv1 = *(const bf16x8*)(v + rme + 32 + 8 * lq);
+  bf16x4 kk4[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) kk4[kt] = *(const bf16x4*)(k + rme + 16 * kt + 4 * lq);
+  const float qdq_me = ws.qdq[(size_t)row * T + (size_t)n * kSC + s_me];
   __syncthreads();
 
   const float gcs = s.gc[0][s_me];
@@ -602,15 +666,14 @@ __global__ __launch_bounds__(256, 2) void mamba2_strong_bwd_dkv_kernel(
     float kd = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      const bf16x4 k4 = *(const bf16x4*)(k + rme + 16 * kt + 4 * lq);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kd += (float)k4[i] * ak[kt][i];
+      for (int i = 0; i < 4; ++i) kd += (float)kk4[kt][i] * ak[kt][i];
       *(bf16x4*)(dk + rme + 16 * kt + 4 * lq) = cvt4(ak[kt]);
       *(bf16x4*)(dv + rme + 16 * kt + 4 * lq) = cvt4(av[kt]);
     }
     kd += __shfl_xor(kd, 16, 64);
     kd += __shfl_xor(kd, 32, 64);
-    if (lq == 0) s.dG[s_me] = ws.qdq[(size_t)row * T + (size_t)n * kSC + s_me] - kd;
+    if (lq == 0) s.dG[s_me] = qdq_me - kd;
   }
   __syncthreads();
   if (w == 0) {

@@ -79,11 +79,18 @@ struct GdnBscanSmem {
   float red[8];
 };
 
-// 8 waves.  Wave w owns: dh tiles (k-tile, v-tile) = ((w TPW + j) >> 1, (w TPW + j) & 1),
-// TPW = K / 64; the [64 x 32] products of step (i) at (t-tile w & 3, v-tile w >> 2);
-// the [64 x K] accumulators at t-tile w & 3, k-tiles (w >> 2) APW + j, APW = K / 32.
+// NW = 8 waves (the wave-count parameter keeps the tile map general).  With
+// VTW = 8 / NW, wave w owns: dh tiles (k-tile, v-tile) = ((w TPW + j) >> 1,
+// (w TPW + j) & 1), TPW = VTW K / 64; the [64 x 32] products of step (i) at
+// (t-tile w & 3, v-tile (w >> 2) VTW + x), x < VTW; the [64 x K] accumulators at
+// t-tile w & 3, k-tiles ((w >> 2) VTW + x) APW + j, APW = K / 32.  At K = 192
+// every level's dh (96 registers) and the three accumulators (72) leave too
+// few registers for the products and some values spill.
+template <int KD>
+constexpr int gdn_bscan_waves() { return 8; }
+
 template <int KD, typename TL>
-__global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
+__global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
     const __bf16* __restrict__ un, const __bf16* __restrict__ dO, const float* __restrict__ gcum,
     const TL* __restrict__ l, const __bf16* __restrict__ hsave, float* __restrict__ dq_p,
@@ -93,10 +100,11 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
   using Sm = GdnBscanSmem<KD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
-  constexpr int LK = Sm::LK, LVS = Sm::LVS, TPW = KD / 64, APW = KD / 32;
+  constexpr int NW = gdn_bscan_waves<KD>(), NTH = 64 * NW, VTW = 8 / NW;
+  constexpr int LK = Sm::LK, LVS = Sm::LVS, TPW = VTW * KD / 64, APW = KD / 32;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const int tt = w & 3, vt = w >> 2;       // step (i) tile; tt is also the accumulators' t-tile
+  const int tt = w & 3, vt0 = (w >> 2) * VTW;   // step (i) tiles; tt is also the accumulators' t-tile
   const int nvb = V / kBVs;
   const int vb = blockIdx.x % nvb;
   const int row = blockIdx.x / nvb;
@@ -122,14 +130,18 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
   // makes the compiler merge its registers after the branch, which waits for
   // the load right away.
   constexpr bool kPrefTiles = KD <= 64;
-  constexpr int UPR = KD / 8, QU = kGC * UPR / 512;   // units per row / per thread
-  static_assert(kBVs * UPR <= 512 && kGC * kBVs / 8 <= 512, "one unit per thread");
+  constexpr int UPR = KD / 8, QU = kGC * UPR / NTH;   // units per row / per thread
+  constexpr int HU = (kBVs * UPR + NTH - 1) / NTH;     // units of the saved state per thread
+  static_assert(kGC * UPR % NTH == 0 && kGC * kBVs / 8 <= NTH, "units per thread");
   const __bf16* hsrow = hsave + (size_t)row * NT * nlev * V * KD + (size_t)v0 * KD;
-  u32x4 ph;
+  u32x4 ph[HU];
   auto fetch_h = [&](int jc, int e) __attribute__((always_inline)) {
-    const int u = tid % (kBVs * UPR);
-    ph = *(const u32x4*)(hsrow + ((size_t)jc * nlev + e) * V * KD + (size_t)(u / UPR) * KD +
-                         8 * (u % UPR));
+#pragma unroll
+    for (int i = 0; i < HU; ++i) {
+      const int u = (tid + NTH * i) % (kBVs * UPR);
+      ph[i] = *(const u32x4*)(hsrow + ((size_t)jc * nlev + e) * V * KD + (size_t)(u / UPR) * KD +
+                              8 * (u % UPR));
+    }
   };
   u32x4 pq[QU], pw[QU], pk[QU], pu, pdo;
   float plam, peL;
@@ -137,7 +149,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     const size_t t0 = (size_t)b * T + (size_t)jc * kGC;
 #pragma unroll
     for (int i = 0; i < QU; ++i) {
-      const int u = tid + 512 * i, r = u / UPR, c = 8 * (u % UPR);
+      const int u = tid + NTH * i, r = u / UPR, c = 8 * (u % UPR);
       const size_t off = (t0 + r) * hk + (size_t)h * KD + c;
       pq[i] = *(const u32x4*)(qn + off);
       pw[i] = *(const u32x4*)(wn + off);
@@ -162,7 +174,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     if (!kPrefTiles) fetch_tiles(ic);
 #pragma unroll
     for (int i = 0; i < QU; ++i) {
-      const int u = tid + 512 * i, r = u / UPR, c = 8 * (u % UPR);
+      const int u = tid + NTH * i, r = u / UPR, c = 8 * (u % UPR);
       *(u32x4*)(s.qn + r * LK + c) = pq[i];
       *(u32x4*)(s.wn + r * LK + c) = pw[i];
       *(u32x4*)(s.kn + r * LK + c) = pk[i];
@@ -176,34 +188,34 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     // the first level's barrier publishes the tiles; the prefetch registers are
     // reloaded after it
 
-    floatx4 adq[APW], adw[APW], adk[APW], adu = zero4();
+    floatx4 adq[VTW * APW], adw[VTW * APW], adk[VTW * APW], adu[VTW];
 #pragma unroll
-    for (int j = 0; j < APW; ++j) adq[j] = adw[j] = adk[j] = zero4();
+    for (int j = 0; j < VTW * APW; ++j) adq[j] = adw[j] = adk[j] = zero4();
+#pragma unroll
+    for (int x = 0; x < VTW; ++x) adu[x] = zero4();
     float del = 0.f;
 
     // the level loop stays rolled (an unrolled one holds every level's fragments
-    // at once); the level's dh tiles move to and from a working set through a
-    // uniform switch, so the register array is only indexed by constants.  The
-    // level's read / write / no-reset flags enter the products as 0 / 1 factors,
-    // so that its LDS reads and MFMAs issue without a branch per product.
+    // at once); slot 0 of the dh array is the current level and the array
+    // rotates by one level per iteration (kGBwdMaxLev iterations, the levels
+    // >= nlev only rotating), so it is only indexed by constants.  The level's
+    // read / write / no-reset flags enter the products as 0 / 1 factors, so
+    // that its LDS reads and MFMAs issue without a branch per product.
 #pragma unroll 1
-    for (int e = 0; e < nlev; ++e) {
-      {
-        floatx4 cur[TPW];
-        switch (e) {
-#define HATTN_DH_GET(E) \
-  case E:               \
-    for (int j = 0; j < TPW; ++j) cur[j] = dh[E][j]; \
-    break;
-          HATTN_DH_GET(0) HATTN_DH_GET(1) HATTN_DH_GET(2) HATTN_DH_GET(3) HATTN_DH_GET(4)
-          HATTN_DH_GET(5) HATTN_DH_GET(6) HATTN_DH_GET(7)
-#undef HATTN_DH_GET
-        }
+    for (int e = 0; e < kGBwdMaxLev; ++e) {
+      floatx4 cur[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) cur[j] = dh[0][j];
+      if (e < nlev) {
         const int per = 2 << e;
         const bool rd = (ic >> e) & 1;
         const bool nr = (ic & (per - 1)) != per - 1;
         const float frd = rd ? 1.f : 0.f, fwr = 1.f - frd, fnr = nr ? 1.f : 0.f;
-        if (tid < kBVs * UPR) *(u32x4*)(s.hs + (tid / UPR) * LK + 8 * (tid % UPR)) = ph;
+#pragma unroll
+        for (int i = 0; i < HU; ++i) {
+          const int u = tid + NTH * i;
+          if (u < kBVs * UPR) *(u32x4*)(s.hs + (u / UPR) * LK + 8 * (u % UPR)) = ph[i];
+        }
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
           const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
@@ -217,10 +229,14 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
         if (kPrefTiles && e == 0) fetch_tiles(max(ic - 1, 0));
 
         // (i) dV_new = K_new dh, V_new = wr U - nr W_new h, q_new h (for dlambda)
-        {
+#pragma unroll
+        for (int x = 0; x < VTW; ++x) {
+          const int vt = vt0 + x;
           floatx4 dv = zero4(), y = zero4(), z = zero4();
 #pragma unroll
           for (int c = 0; c < KD / 32; ++c) {
+            // bound the operand loads in flight (registers) for the wide K
+            if (KD > 128) __builtin_amdgcn_sched_barrier(0);
             const bf16x8 bd = *(const bf16x8*)(s.dhs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
             const bf16x8 bh = *(const bf16x8*)(s.hs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
             dv = mfma16x16x32(*(const bf16x8*)(s.kn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bd, dv);
@@ -234,15 +250,15 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
             const int t = 16 * tt + 4 * lq + i;
             vnb[i] = (__bf16)(fwr * (float)s.u[t * LVS + 16 * vt + ln] - fnr * y[i]);
             dvb[i] = (__bf16)dv[i];
-            adu[i] += fwr * dv[i];
+            adu[x][i] += fwr * dv[i];
             dlr[i] = frd * (float)s.dO[t * LVS + 16 * vt + ln] * z[i];
           }
           *(bf16x4*)(s.dvn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = dvb;
           *(bf16x4*)(s.vn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = vnb;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float x = rsum16(dlr[i]);
-            if (ln == 0) s.dlr[vt][16 * tt + 4 * lq + i] = x;
+            const float xs = rsum16(dlr[i]);
+            if (ln == 0) s.dlr[vt][16 * tt + 4 * lq + i] = xs;
           }
         }
         __syncthreads();
@@ -251,22 +267,25 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
 
         // (ii) contractions over this slice's 32 columns of V
         {
-          const bf16x8 adO = *(const bf16x8*)(s.dO + (16 * tt + ln) * LVS + 8 * lq);
-          const bf16x8 advn = tr_frag(s.dvn, kLd64, 0, 16 * tt);   // dV_new[t][v]
+          // A operands with the level's factors folded into their rows (t = 16 tt + ln),
+          // so the three accumulators take plain MFMA accumulation
+          bf16x8 adO = *(const bf16x8*)(s.dO + (16 * tt + ln) * LVS + 8 * lq);
+          bf16x8 advn = tr_frag(s.dvn, kLd64, 0, 16 * tt);   // dV_new[t][v]
           const bf16x8 avn = tr_frag(s.vn, kLd64, 0, 16 * tt);     // V_new[t][v]
-          const floatx4 lam = *(const floatx4*)(s.lam[e] + 16 * tt + 4 * lq);
+          const float fq = frd * s.lam[e][16 * tt + ln];
 #pragma unroll
-          for (int j = 0; j < APW; ++j) {
-            const int kt = vt * APW + j;
+          for (int jj = 0; jj < 8; ++jj) {
+            adO[jj] = (__bf16)((float)adO[jj] * fq);
+            advn[jj] = (__bf16)((float)advn[jj] * fnr);
+          }
+#pragma unroll
+          for (int j = 0; j < VTW * APW; ++j) {
+            if (KD > 128 && (j & 1) == 0) __builtin_amdgcn_sched_barrier(0);
+            const int kt = vt0 * APW + j;
             const bf16x8 bh = tr_frag(s.hs, LK, 0, 16 * kt);    // h^T[v][k]
             const bf16x8 bd = tr_frag(s.dhs, LK, 0, 16 * kt);   // dh^T[v][k]
-            const floatx4 tq = mfma16x16x32(adO, bh, zero4());
-            const floatx4 tw = mfma16x16x32(advn, bh, zero4());
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              adq[j][i] += frd * lam[i] * tq[i];
-              adw[j][i] += fnr * tw[i];
-            }
+            adq[j] = mfma16x16x32(adO, bh, adq[j]);
+            adw[j] = mfma16x16x32(advn, bh, adw[j]);
             adk[j] = mfma16x16x32(avn, bd, adk[j]);
           }
           float dd = 0.f;
@@ -283,6 +302,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
         // (iii) dh_e <- nr (eL dh_e - W_new^T dV_new) + rd q_new^T (lambda_e o dO)
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
+          if (KD > 128) __builtin_amdgcn_sched_barrier(0);
           const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
           floatx4 tw = zero4(), tq = zero4();
 #pragma unroll
@@ -302,33 +322,34 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) cur[j][i] = fnr * (eL * cur[j][i] - tw[i]) + frd * tq[i];
         }
-        switch (e) {
-#define HATTN_DH_PUT(E) \
-  case E:               \
-    for (int j = 0; j < TPW; ++j) dh[E][j] = cur[j]; \
-    break;
-          HATTN_DH_PUT(0) HATTN_DH_PUT(1) HATTN_DH_PUT(2) HATTN_DH_PUT(3) HATTN_DH_PUT(4)
-          HATTN_DH_PUT(5) HATTN_DH_PUT(6) HATTN_DH_PUT(7)
-#undef HATTN_DH_PUT
-        }
         __syncthreads();
       }
+      // rotate: level e + 1 moves to slot 0; after all kGBwdMaxLev steps every
+      // level is back in its own slot
+#pragma unroll
+      for (int l = 0; l + 1 < kGBwdMaxLev; ++l)
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) dh[l][j] = dh[l + 1][j];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) dh[kGBwdMaxLev - 1][j] = cur[j];
     }
 
     // ---- the chunk's outputs -----------------------------------------------------
 #pragma unroll
-    for (int j = 0; j < APW; ++j)
+    for (int j = 0; j < VTW * APW; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const size_t o = ((size_t)vb * BTH + (tok0 + 16 * tt + 4 * lq + i) * H + h) * KD +
-                         16 * (vt * APW + j) + ln;
+                         16 * (vt0 * APW + j) + ln;
         dq_p[o] = adq[j][i];
         dw_p[o] = -adw[j][i];
         dk_p[o] = adk[j][i];
       }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      du[((tok0 + 16 * tt + 4 * lq + i) * H + h) * V + v0 + 16 * vt + ln] = adu[i];
+    for (int x = 0; x < VTW; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        du[((tok0 + 16 * tt + 4 * lq + i) * H + h) * V + v0 + 16 * (vt0 + x) + ln] = adu[x][i];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) del += __shfl_xor(del, off, 64);
     if (lane == 0) s.red[w] = del;
@@ -336,7 +357,7 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
     if (tid == 0) {
       float x = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < 8; ++w2) x += s.red[w2];
+      for (int w2 = 0; w2 < NW; ++w2) x += s.red[w2];
       del_p[(size_t)vb * B * H * NT + (size_t)row * NT + ic] = x;
     }
   }
@@ -347,14 +368,15 @@ __global__ __launch_bounds__(512, 1) void gdn_bwd_scan_kernel(
 // ---------------------------------------------------------------------------
 template <int KD, int VD>
 struct GdnBchunkSmem {
-  static constexpr int LK = KD + 8, LV = VD + 8;
-  static constexpr int LS = (KD > VD ? KD : VD) + 4;   // fp32 staging row stride
-  static constexpr int NR = kGC * LS > 2 * kGC * kLM ? kGC * LS : 2 * kGC * kLM;
+  static constexpr int LK = KD + 8;
+  static constexpr int LS = 64 + 4;     // fp32 staging row stride (64-column blocks)
+  static constexpr int LDB = 64 + 8;    // bf16 staging row stride
+  static constexpr int NR = 2 * kGC * kLM;
+  static_assert(kGC * LS + kGC * LDB / 2 <= NR, "step 14 staging fits the S4 | S5 region");
   __bf16 q[kGC * LK];
   __bf16 k[kGC * LK];
-  __bf16 dO[kGC * LV];
   float m[4][kGC * kLM];   // S0 .. S3: 64 x 64 fp32 matrices
-  float rg[NR];            // S4 | S5, or the fp32 staging tile, or the inverse scratch
+  float rg[NR];            // S4 | S5, or the fp32 (and bf16) staging tiles, or the inverse scratch
   float gc[kGC], e[kGC], r[kGC], beta[kGC];
   float lam[7][kGC];       // lambda[t, 0..6]
   float dlam[7][kGC];      // intra-chunk dlambda
@@ -490,7 +512,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   using Sm = GdnBchunkSmem<KD, VD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
-  constexpr int LK = Sm::LK, LV = Sm::LV, LS = Sm::LS, NKT = KD / 16, NVT = VD / 16;
+  constexpr int LK = Sm::LK, LS = Sm::LS, LDB = Sm::LDB, NKT = KD / 16;
   constexpr int NPV = VD / kBVs;   // V slices of the level scan = partials per entry
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
@@ -513,7 +535,6 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   // ---- load ------------------------------------------------------------------
   g2s_tile<KD>(k + rowk, hk, s.k, LK);
   g2s_tile<KD>(q + rowk, hk, s.q, LK);
-  g2s_tile<VD>(dO + rowv, hv, s.dO, LV);
   if (norm_qk) {
     // use_qk_l2norm_in_kernel: the gradients below are w.r.t. q scale / ||q|| and
     // k / ||k||; the chain rule back to q and k is applied where dq, dk are stored
@@ -604,7 +625,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   {
     bf16x8 ad[VD / 32];
 #pragma unroll
-    for (int c = 0; c < VD / 32; ++c) ad[c] = *(const bf16x8*)(s.dO + (t16 + ln) * LV + 32 * c + 8 * lq);
+    for (int c = 0; c < VD / 32; ++c) ad[c] = *(const bf16x8*)(dO + rowv + (size_t)(t16 + ln) * hv + 32 * c + 8 * lq);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       floatx4 z = zero4();
@@ -811,112 +832,122 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   __syncthreads();
 
-  // live: S0 = dM, S1 = dA, S2 = Aw, S3 = P; the staging region is free
-  // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ------------------
-  stage_rows<KD, LS, NPV>(ST, dq_p + rowk, hk, BTH * KD, s.e);
-  __syncthreads();
-  floatx4 u2[NKT];
-  float dqh[NKT][4];
+  // live: S0 = dM, S1 = dA, S2 = Aw, S3 = P; the staging region is free.
+  // Steps 10 - 13 run per 64-column block kb of K (the staged blocks of X,
+  // e o dW_new and dK_new fit the staging region for every K); dq and dk stay
+  // in registers until the l2norm chain rule, which needs whole rows.
+  float dqh[NKT][4], dkh[NKT][4];
+  float qx = 0.f;                                   // rowdot(X, Q), thread (t = tid >> 2, part)
+  float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int nt = 0; nt < NKT; ++nt) {
-    floatx4 acc = zero4(), a2 = zero4();
+  for (int kb = 0; kb < KD / 64; ++kb) {
+    const int k0 = 64 * kb;
+    // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ----------------
+    stage_rows<64, LS, NPV>(ST, dq_p + rowk + k0, hk, BTH * KD, s.e);
+    __syncthreads();
+    floatx4 u2[4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float am[8], ap[8], bx[8];
-      frn<kLM>(S0, t16, 32 * c, am);
-      acc = mma_fb(am, tr_frag(s.k, LK, 32 * c, 16 * nt), acc);
-      frt<kLM>(S3, t16, 32 * c, ap);
-      frt<LS>(ST, 16 * nt, 32 * c, bx);
-      a2 = mma_ff(ap, bx, a2);
+    for (int nt = 0; nt < 4; ++nt) {
+      floatx4 acc = zero4(), a2 = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float am[8], ap[8], bx[8];
+        frn<kLM>(S0, t16, 32 * c, am);
+        acc = mma_fb(am, tr_frag(s.k, LK, 32 * c, k0 + 16 * nt), acc);
+        frt<kLM>(S3, t16, 32 * c, ap);
+        frt<LS>(ST, 16 * nt, 32 * c, bx);
+        a2 = mma_ff(ap, bx, a2);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dqh[4 * kb + nt][i] = ST[(t16 + 4 * lq + i) * LS + 16 * nt + ln] + acc[i];
+      u2[nt] = -a2;
     }
+    {
+      const int t = tid >> 2, part = tid & 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dqh[nt][i] = ST[(t16 + 4 * lq + i) * LS + 16 * nt + ln] + acc[i];
-    u2[nt] = -a2;
+      for (int kk = 16 * part; kk < 16 * part + 16; ++kk)
+        qx += ST[t * LS + kk] * (float)s.q[t * LK + k0 + kk];
+    }
+    __syncthreads();
+
+    // ---- 11: e o dW_new -> ST; U2 += Aw^T ST ---------------------------------------------
+    stage_rows<64, LS, NPV>(ST, dw_p + rowk + k0, hk, BTH * KD, s.e);
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float a[8], bb[8];
+        frt<kLM>(S2, t16, 32 * c, a);
+        frt<LS>(ST, 16 * nt, 32 * c, bb);
+        u2[nt] = mma_ff(a, bb, u2[nt]);
+      }
+    __syncthreads();
+
+    // ---- 12: U2 += dA K; U1 = dM^T Q + dA^T (beta o K) ----------------------------------
+    floatx4 u1[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      floatx4 a1 = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 bk = tr_frag(s.k, LK, 32 * c, k0 + 16 * nt);
+        const bf16x8 bq = tr_frag(s.q, LK, 32 * c, k0 + 16 * nt);
+        float ad[8], am[8], at[8];
+        frn<kLM>(S1, t16, 32 * c, ad);
+        u2[nt] = mma_fb(ad, bk, u2[nt]);
+        frt<kLM>(S0, t16, 32 * c, am);
+        a1 = mma_fb(am, bq, a1);
+        frt<kLM>(S1, t16, 32 * c, at);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) at[j] *= s.beta[32 * c + 8 * lq + j];
+        a1 = mma_fb(at, bk, a1);
+      }
+      u1[nt] = a1;
+    }
+
+    // ---- 13: dK_new -> ST; dK = U1 + beta o U2 + r o dK_new; dbeta, dGc of K_new -------
+    stage_rows<64, LS, NPV>(ST, dk_p + rowk + k0, hk, BTH * KD, nullptr);
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sr = t16 + 4 * lq + i, kk = 16 * nt + ln;
+        const float kv = (float)s.k[sr * LK + k0 + kk], dkn = ST[sr * LS + kk];
+        dkh[4 * kb + nt][i] = u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn;
+        rb[i] += kv * u2[nt][i];
+        kd[i] += dkn * kv;
+      }
+    __syncthreads();
   }
   // dq = dq_hat, or with the in-kernel normalisation x -> y = x r (r = 1 / ||x||)
   // scaled by s: dq = r s (dq_hat - y (y . dq_hat)) (fla l2norm_bwd, kernel.py:24-29)
   store_l2norm_grad<NKT>(dqh, s.q, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
                          dq + rowk, hk, t16);
+  store_l2norm_grad<NKT>(dkh, s.k, s.rk, 1.f, 1.f, norm_qk, dk + rowk, hk, t16);
   {
-    const int t = tid >> 2, part = tid & 3;
-    float x = 0.f;
-    for (int kk = part * (KD / 4); kk < (part + 1) * (KD / 4); ++kk)
-      x += ST[t * LS + kk] * (float)s.q[t * LK + kk];
-    x += __shfl_xor(x, 1, 64);
-    x += __shfl_xor(x, 2, 64);
-    if (part == 0) s.dgr[t] += x;
+    qx += __shfl_xor(qx, 1, 64);
+    qx += __shfl_xor(qx, 2, 64);
+    if ((tid & 3) == 0) s.dgr[tid >> 2] += qx;
   }
-  __syncthreads();
-
-  // ---- 11: e o dW_new -> ST; U2 += Aw^T ST ---------------------------------------------
-  stage_rows<KD, LS, NPV>(ST, dw_p + rowk, hk, BTH * KD, s.e);
-  __syncthreads();
+  __syncthreads();   // the next updates of dGc come from other threads
 #pragma unroll
-  for (int nt = 0; nt < NKT; ++nt)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float a[8], bb[8];
-      frt<kLM>(S2, t16, 32 * c, a);
-      frt<LS>(ST, 16 * nt, 32 * c, bb);
-      u2[nt] = mma_ff(a, bb, u2[nt]);
-    }
-  __syncthreads();
-
-  // ---- 12: U2 += dA K; U1 = dM^T Q + dA^T (beta o K) ----------------------------------
-  floatx4 u1[NKT];
-#pragma unroll
-  for (int nt = 0; nt < NKT; ++nt) {
-    floatx4 a1 = zero4();
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const bf16x8 bk = tr_frag(s.k, LK, 32 * c, 16 * nt), bq = tr_frag(s.q, LK, 32 * c, 16 * nt);
-      float ad[8], am[8], at[8];
-      frn<kLM>(S1, t16, 32 * c, ad);
-      u2[nt] = mma_fb(ad, bk, u2[nt]);
-      frt<kLM>(S0, t16, 32 * c, am);
-      a1 = mma_fb(am, bq, a1);
-      frt<kLM>(S1, t16, 32 * c, at);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) at[j] *= s.beta[32 * c + 8 * lq + j];
-      a1 = mma_fb(at, bk, a1);
-    }
-    u1[nt] = a1;
-  }
-
-  // ---- 13: dK_new -> ST; dK = U1 + beta o U2 + r o dK_new; dbeta, dGc of K_new -------
-  stage_rows<KD, LS, NPV>(ST, dk_p + rowk, hk, BTH * KD, nullptr);
-  __syncthreads();
-  {
-    float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
-    float dkh[NKT][4];
-#pragma unroll
-    for (int nt = 0; nt < NKT; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int sr = t16 + 4 * lq + i, kk = 16 * nt + ln;
-        const float kv = (float)s.k[sr * LK + kk], dkn = ST[sr * LS + kk];
-        dkh[nt][i] = u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn;
-        rb[i] += kv * u2[nt][i];
-        kd[i] += dkn * kv;
-      }
-    store_l2norm_grad<NKT>(dkh, s.k, s.rk, 1.f, 1.f, norm_qk, dk + rowk, hk, t16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = rsum16(rb[i]), y = rsum16(kd[i]);
-      if (ln == 0) {
-        const int sr = t16 + 4 * lq + i;
-        s.dbr[sr] += x;
-        s.dgr[sr] -= s.r[sr] * y;
-        s.lastc[sr] = s.r[sr] * y;
-      }
+  for (int i = 0; i < 4; ++i) {
+    const float x = rsum16(rb[i]), y = rsum16(kd[i]);
+    if (ln == 0) {
+      const int sr = t16 + 4 * lq + i;
+      s.dbr[sr] += x;
+      s.dgr[sr] -= s.r[sr] * y;
+      s.lastc[sr] = s.r[sr] * y;
     }
   }
   __syncthreads();
 
-  // ---- 14: dU -> ST; GV = Au^T dU + (P o Gamma o Lambda)^T dO; dV = beta o GV --------
-  stage_rows<VD, LS, 1>(ST, du + rowv, hv, 0, nullptr);
-  __syncthreads();
+  // ---- 14: per 64-column block of V: dU, dO -> staging; GV = Au^T dU +
+  //          (P o Gamma o Lambda)^T dO; dV = beta o GV -------------------------------------
   {
+    __bf16* SD = (__bf16*)(s.rg + kGC * LS);   // dO block [t][v]
     float au[2][8], ar[2][8];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -930,27 +961,35 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
         ar[c][j] *= gam * s.lam[intra_level(t, sc)][t];
       }
     }
-    float rb[4] = {0.f, 0.f, 0.f, 0.f};
+    float rbv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < NVT; ++nt) {
-      floatx4 acc = zero4();
+    for (int vb = 0; vb < VD / 64; ++vb) {
+      const int v0 = 64 * vb;
+      stage_rows<64, LS, 1>(ST, du + rowv + v0, hv, 0, nullptr);
+      g2s_tile<64>(dO + rowv + v0, hv, SD, LDB);
+      __syncthreads();
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        float bu[8];
-        frt<LS>(ST, 16 * nt, 32 * c, bu);
-        acc = mma_ff(au[c], bu, acc);
-        acc = mma_fb(ar[c], tr_frag(s.dO, LV, 32 * c, 16 * nt), acc);
+      for (int nt = 0; nt < 4; ++nt) {
+        floatx4 acc = zero4();
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          float bu[8];
+          frt<LS>(ST, 16 * nt, 32 * c, bu);
+          acc = mma_ff(au[c], bu, acc);
+          acc = mma_fb(ar[c], tr_frag(SD, LDB, 32 * c, 16 * nt), acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int sr = t16 + 4 * lq + i, vv = v0 + 16 * nt + ln;
+          dv[rowv + sr * hv + vv] = (__bf16)(s.beta[sr] * acc[i]);
+          rbv[i] += (float)v[rowv + sr * hv + vv] * acc[i];
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int sr = t16 + 4 * lq + i, vv = 16 * nt + ln;
-        dv[rowv + sr * hv + vv] = (__bf16)(s.beta[sr] * acc[i]);
-        rb[i] += (float)v[rowv + sr * hv + vv] * acc[i];
-      }
+      __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = rsum16(rb[i]);
+      const float x = rsum16(rbv[i]);
       if (ln == 0) s.dbr[t16 + 4 * lq + i] += x;
     }
   }
@@ -1044,7 +1083,8 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
     if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  smem)) != hipSuccess)
       return e;
-    hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(512), smem, stream, w.qn, w.wn, w.kn,
+    hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(64 * gdn_bscan_waves<KD>()), smem,
+                       stream, w.qn, w.wn, w.kn,
                        w.un, (const __bf16*)dO, gcum, (const TL*)l, w.hs, w.dq_p, w.dw_p, w.dk_p,
                        w.du, w.dl_p, w.del_p, B, T, H, VD, L, nlev);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1101,6 +1141,8 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
       return gdn_bwd_t<KD_, VD_, float, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
                                                 dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
   }
+  HATTN_GDN_B(192, 128)
+  HATTN_GDN_B(192, 64)
   HATTN_GDN_B(128, 128)
   HATTN_GDN_B(128, 64)
   HATTN_GDN_B(64, 128)

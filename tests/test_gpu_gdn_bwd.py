@@ -104,13 +104,14 @@ def test_groups():
         _check(name, a, r, "groups")
 
 
-def test_autograd_function_l2norm_and_scale():
+@pytest.mark.parametrize("K", [128, 192])
+def test_autograd_function_l2norm_and_scale(K):
     """hattention_kernel(GDELTA).backward(): the HIP backward plus the l2norm /
     scale chain rule of kernel.py:201-225, against autograd through the oracle's
     hattention_gdn_fwd (l2norm, scale, chunked form)."""
     from hattention.kernel import hattention_kernel
     from hattention.base import HType, HStruct
-    B, T, H, K, L = 1, 512, 2, 128, 10
+    B, T, H, L = 1, 512, 2, 10
     gen = torch.Generator().manual_seed(51)
     q = torch.randn(B, T, H, K, generator=gen).bfloat16()
     k = torch.randn(B, T, H, K, generator=gen).bfloat16()
@@ -146,12 +147,27 @@ def test_eight_levels_bwd():
     _run(1, 16384, 1, 64, 64, 15, seed=31)
 
 
-def test_head_dim_192_bwd_not_implemented():
-    """The backward kernels take K in {64, 128}; K = 192 raises instead of
+@pytest.mark.parametrize("T,V", [(128, 64), (640, 128), (1024, 384)])
+def test_head_dim_192_bwd(T, V):
+    """K = 192 (the reference GDN model's head_dim, configs/flame/h_gated_deltanet_mid.json):
+    the chunk kernel's K-sized steps run per 64-column block of K."""
+    L = 7 + math.ceil(math.log2(T // 64)) + 1
+    _run(1, T, 2, 192, V, L, seed=T + V)
+
+
+def test_reference_model_shape_bwd():
+    """the reference GDN model's training shape: B=1 T=16384 H=6 head_dim 192,
+    expand_v 2 (V = 384), L = 15 (modeling_h_gated_deltanet.py:47-52,
+    scripts/train_flame.sh:52,74); rows at both ends of the grid."""
+    _run(1, 16384, 6, 192, 384, 15, seed=1192, rows=[(0, 0), (0, 5)])
+
+
+def test_head_dim_256_bwd_not_implemented():
+    """The backward kernels take K in {64, 128, 192}; K = 256 raises instead of
     returning wrong gradients."""
     from hattention.chunkwise_hgdn import chunkwise_fwd, chunkwise_bwd
     from hattention.base import HType
-    q, k, v, beta, g, l = make_gdn_inputs(1, 128, 1, 192, 64, 8, seed=3)
+    q, k, v, beta, g, l = make_gdn_inputs(1, 128, 1, 256, 64, 8, seed=3)
     dev = torch.device("cuda:0")
     xs = [x.to(dev) for x in (q, k, v, beta, g, l)]
     gc, o, Aw, Au, _ = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, False)

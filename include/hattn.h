@@ -316,6 +316,32 @@ int hattn_mamba2_layer_epilogue(const void* y, const void* x, const float* D, vo
                                 void* stream);
 
 /*
+ * The layer scan of hmamba_chunk_scan_combined with its pre- and
+ * post-processing folded into the scan's loads and stores (replaces
+ * mamba_apis.py:263-404 without final states: layer prologue ->
+ * HAttentionFunction (q = C, k = B, v = x dt', g = A dt', lambda) -> y = o + x D):
+ * the forward scan reads x, dt and dl in place of v, g and lambda and writes
+ *   y = bf16(o) + x D[h]   (D != NULL; y in dtype_y), or y = o (D == NULL).
+ * v and lambda are computed with the prologue's formulas (v rounded to bf16,
+ * lambda to dtype_lam), so y equals the separate prologue -> chunkwise forward
+ * -> epilogue chain.  g_cumsum [B, T, H] fp32 as the chunkwise forward's.
+ *   x [B, T, H, P] bf16, dt [B, T, H] dtype_dt, A [H] fp32, dt_bias [H] fp32 or
+ *   NULL, B / C [B, T, G, N] bf16, dl [B, T, H, L] dtype_dl, Lp [H, L] fp32,
+ *   D [H] fp32 or NULL.
+ * Constraints: N == 64, P % 64 == 0, L <= 32, HType.WEAK, chunk 64, base 2,
+ * x / B / C bf16 (-> HATTN_ERR_NOT_IMPLEMENTED); workspace as
+ * hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, N, P, L).
+ */
+int hattn_mamba2_layer_scan_fwd(const void* x, const void* dt, const float* A,
+                                const float* dt_bias, const void* Bm, const void* Cm,
+                                const void* dl, const float* Lp, const float* D, void* y,
+                                float* g_cumsum, int B, int T, int G, int H, int P, int N, int L,
+                                int dtype_x, int dtype_dt, int dtype_bc, int dtype_dl,
+                                int dtype_lam, int dtype_y, int dt_softplus, int lambda_mode,
+                                int level_base, int htype, int chunk_size, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * Backward of the layer pre- and post-processing: what torch autograd computes
  * through mamba_apis.py:346-366 and :402-403 given the scan's gradients dv,
  * dg (fp32), dlam and the layer output gradient dy (read only when D != NULL):

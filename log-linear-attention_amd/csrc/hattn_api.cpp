@@ -29,6 +29,13 @@ hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const vo
                                           int B, int T, int G, int H, int V, int L, int dt_l,
                                           int dt_o, hipStream_t stream, int* unsupported);
 size_t hattn_mamba2_strong_bwd_ws_bytes(int B, int T, int H, int nlev);
+hipError_t hattn_mamba2_layer_fwd_launch(const void* q, const void* k, const void* x,
+                                         const void* dl, void* o, float* gcum, void* ws,
+                                         const void* dt, const float* A, const float* dt_bias,
+                                         const float* Lp, const float* D, int dt_f32,
+                                         int softplus, int mode, int lam_bf16, int B, int T,
+                                         int G, int H, int V, int L, int nlev, int dt_l,
+                                         int dt_o, hipStream_t stream, int* unsupported);
 hipError_t hattn_mamba2_strong_bwd_launch(const void* q, const void* k, const void* v,
                                           const float* gc, const void* l, const void* dO,
                                           void* dq, void* dk, void* dv, float* dg, float* dl,
@@ -587,6 +594,59 @@ int hattn_mamba2_layer_epilogue(const void* y, const void* x, const float* D, vo
   return check_hip(hattn_mamba2_layer_epilogue_launch(y, x, D, out, B, T, H, P, yb, xb, ob,
                                                       (hipStream_t)stream),
                    "hattn_mamba2_layer_epilogue launch");
+}
+
+int hattn_mamba2_layer_scan_fwd(const void* x, const void* dt, const float* A,
+                                const float* dt_bias, const void* Bm, const void* Cm,
+                                const void* dl, const float* Lp, const float* D, void* y,
+                                float* g_cumsum, int B, int T, int G, int H, int P, int N, int L,
+                                int dtype_x, int dtype_dt, int dtype_bc, int dtype_dl,
+                                int dtype_lam, int dtype_y, int dt_softplus, int lambda_mode,
+                                int level_base, int htype, int chunk_size, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  // mamba_apis.py:263-404 (the layer scan of hmamba_chunk_scan_combined, no final state)
+  if (chunk_size != 64)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
+  if (level_base != 2)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
+  if (htype != HATTN_HTYPE_WEAK)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "the folded layer scan runs HType.WEAK only");
+  if (B <= 0 || T <= 0 || G <= 0 || H <= 0 || P <= 0 || N <= 0 || L <= 0)
+    return fail(HATTN_ERR_VALUE, "non-positive dimension");
+  if (T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
+  if (H % G != 0) return fail(HATTN_ERR_VALUE, "H=%d is not a multiple of G=%d", H, G);
+  if (P % 64 != 0) return fail(HATTN_ERR_VALUE, "P=%d and BV could be 64", P);
+  if (N != 64) return fail(HATTN_ERR_NOT_IMPLEMENTED, "N=%d (the folded layer scan takes 64)", N);
+  if (lambda_mode < 0 || lambda_mode > 2) return fail(HATTN_ERR_VALUE, "lambda_mode=%d", lambda_mode);
+  const int nlev = ceil_log2(T / 64);
+  if (7 + nlev > L)
+    return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
+  if (nlev > hattn_mamba2_fwd_max_levels(0))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_mamba2_fwd_max_levels(0));
+  if (L > 32) return fail(HATTN_ERR_NOT_IMPLEMENTED, "L=%d > 32 (folded layer scan)", L);
+  if (dtype_x != HATTN_BF16 || dtype_bc != HATTN_BF16)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "x / B / C dtype codes %d / %d (bf16 required)",
+                dtype_x, dtype_bc);
+  const int dtb = bf_flag(dtype_dt), lb = bf_flag(dtype_lam);
+  if (dtb < 0 || lb < 0 || bf_flag(dtype_dl) < 0 || bf_flag(dtype_y) < 0)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype code (bf16 or fp32 only)");
+  if (int st = check_span(T, max_of({(size_t)G * N * 2, (size_t)H * P * elem_bytes(dtype_y),
+                                      (size_t)H * L * elem_bytes(dtype_dl), (size_t)H * 4})))
+    return st;
+  if (!x || !dt || !A || !Bm || !Cm || !dl || !Lp || !y || !g_cumsum)
+    return fail(HATTN_ERR_VALUE, "null tensor pointer");
+  const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, P, 0);
+  if (need > 0 && (workspace_bytes < need || workspace == nullptr))
+    return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, need);
+  int unsupported = 0;
+  hipError_t e = hattn_mamba2_layer_fwd_launch(
+      Cm, Bm, x, dl, y, g_cumsum, workspace, dt, A, dt_bias, Lp, D, dtb ? 0 : 1,
+      dt_softplus ? 1 : 0, lambda_mode, lb, B, T, G, H, P, L, nlev, dtype_dl, dtype_y,
+      (hipStream_t)stream, &unsupported);
+  if (unsupported)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination dl=%d y=%d", dtype_dl, dtype_y);
+  return check_hip(e, "hattn_mamba2_layer_scan_fwd launch");
 }
 
 size_t hattn_mamba2_layer_bwd_workspace(int B, int T, int H, int L) {

@@ -6,6 +6,7 @@
 #include <cstddef>
 
 #include "common.h"
+#include "layer_math.h"
 
 namespace hattn {
 
@@ -132,12 +133,16 @@ constexpr int kCohStore = 16;  // sc1
 // Body of the summary pass over segment p of one (row, 64-column block of V):
 // writes Sum(p) into out (row-major [K][V] with row stride V, this block's 64
 // columns) and returns D_p (on every thread).  COH: the stores carry kCohStore.
-template <typename TK, typename TV, bool GCUM, int NP, bool COH>
+// LAYER: v is the layer's x and g comes from dt (v = x dt', g = A dt', see
+// layer_math.h); bf16 x only.
+template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false>
 __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restrict__ k,
                                               const TV* __restrict__ v,
                                               const float* __restrict__ g, float* __restrict__ out,
                                               int b, int h, int p, int vblk, int T, int G, int H,
-                                              int V, int NT, int S) {
+                                              int V, int NT, int S,
+                                              const LayerArgs& la = LayerArgs{}) {
+  static_assert(!LAYER || (sizeof(TV) == 2 && NP == 1 && !GCUM), "layer mode: bf16 x");
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int gq = h / (H / G);
@@ -150,6 +155,13 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   const rsrc_t rgg = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
   const unsigned int vo_k = tile64_voff<TK>(kstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
+  // layer mode: dt words of the wave-0 lane's row (g) and of the thread's two
+  // V tile rows (tid >> 3, + 32)
+  const int desz = la.dt_f32 ? 4 : 2;
+  const rsrc_t rdt = make_rsrc(LAYER ? (const char*)la.dt + (size_t)b * T * H * desz : (const char*)g,
+                               LAYER ? (size_t)T * H * desz : 0);
+  const float Ah = LAYER ? la.A[h] : 0.f, bh = LAYER && la.bias ? la.bias[h] : 0.f;
+  const unsigned int el_g = (unsigned int)(lane * H + h), el_v = (unsigned int)((tid >> 3) * H + h);
 
   floatx4 acc[4];
 #pragma unroll
@@ -159,6 +171,7 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   Tile64<TK> kr[2];
   Tile64<TV> vr[2];
   float gr[2] = {0.f, 0.f};
+  unsigned int dw[2][2] = {{0u, 0u}, {0u, 0u}};   // layer: dt words of the V rows
   auto seg_load = [&](int jj, int slot) {   // chunk jj of the segment -> register slot
     if (jj >= nch) return;
     const unsigned int row0 = (unsigned int)(c0 + jj) * kBT;
@@ -167,7 +180,16 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
       if (s == slot) {
         load_tile64(kr[s], rk, vo_k, row0 * kstr * sizeof(TK), kstr);
         load_tile64(vr[s], rv, vo_v, row0 * vstr * sizeof(TV), vstr);
-        if (w == 0) gr[s] = buf_load<float>(rgg, vo_g, row0 * H * 4);
+        if constexpr (LAYER) {
+          const unsigned int e0 = row0 * H;   // even: the bf16 half of an element is its own parity
+          if (w == 0) gr[s] = buf_load<float>(rdt, ((e0 + el_g) * desz) & ~3u, 0);
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            dw[s][r] = __builtin_bit_cast(unsigned int, buf_load<float>(
+                rdt, ((e0 + el_v + 32u * r * H) * desz) & ~3u, 0));
+        } else if (w == 0) {
+          gr[s] = buf_load<float>(rgg, vo_g, row0 * H * 4);
+        }
       }
   };
   auto seg_store = [&](int slot, int buf) {   // register slot -> LDS buffer
@@ -175,9 +197,28 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
     for (int s = 0; s < 2; ++s)
       if (s == slot) {
         store_tile64<NP>(kr[s], sm.k[buf][0], sm.k[buf][NP - 1]);
-        store_tile64<NP>(vr[s], sm.v[buf][0], sm.v[buf][NP - 1]);
+        if constexpr (LAYER) {
+          // v = x dt' on the thread's two rows (tid >> 3 and + 32), rounded to bf16
+          Tile64<TV> vs = vr[s];
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const float d = layer_dtp(layer_dt_word(dw[s][r], el_v + 32u * r * H, la.dt_f32),
+                                      bh, la.softplus);
+            bf16x8 xv = __builtin_bit_cast(bf16x8, vs.r[r]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = (__bf16)((float)xv[i] * d);
+            vs.r[r] = __builtin_bit_cast(uint4, xv);
+          }
+          store_tile64<NP>(vs, sm.v[buf][0], sm.v[buf][NP - 1]);
+        } else {
+          store_tile64<NP>(vr[s], sm.v[buf][0], sm.v[buf][NP - 1]);
+        }
         if (w == 0) {
-          const float x = GCUM ? gr[s] : chunk_cumsum(gr[s]);
+          float gv = gr[s];
+          if constexpr (LAYER)
+            gv = layer_g(Ah, layer_dtp(layer_dt_word(__builtin_bit_cast(unsigned int, gr[s]), el_g,
+                                                   la.dt_f32), bh, la.softplus));
+          const float x = GCUM ? gv : chunk_cumsum(gv);
           const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
           sm.wt[buf][lane] = fexp(last - x);
           if (lane == 0) sm.cl[buf] = last;

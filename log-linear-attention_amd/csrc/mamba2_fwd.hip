@@ -511,6 +511,7 @@ struct Bf16Smem {
   float lam[2][kMaxLU * kBT];
   float eg[2][kBT];
   float junk[kBT];            // per-lane sink of the lambda columns past the row's levels
+  float lpar[32];             // layer mode: L[h, 0 .. L - 1] (lambda parameters of the head)
   __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
 };
 
@@ -740,13 +741,19 @@ __global__ void mamba2_fwd_sync_init_kernel(unsigned int* __restrict__ sync, int
   if (i < n) sync[i] = 0u;
 }
 
-template <typename TV, typename TL, typename TO, bool FUSED>
+// LAYER: the layer pre- / post-processing of hmamba_chunk_scan_combined
+// (mamba_apis.py:346-403) folded into the loads and stores: v is the layer's x
+// (v = x dt' as it is staged), l is dl (lambda = compute_lambda(L[h], dl) as it
+// is staged), g comes from dt (g = A dt'), and the output is bf16(o) + x D[h]
+// (see layer_math.h); bf16 x only.
+template <typename TV, typename TL, typename TO, bool FUSED, bool LAYER = false>
 __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, float* __restrict__ ht, float* __restrict__ sums,
     float* __restrict__ segd, unsigned int* __restrict__ sync, int B, int T, int G, int H,
-    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state) {
+    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state, LayerArgs la) {
+  static_assert(!LAYER || sizeof(TV) == 2, "layer mode: bf16 x");
   constexpr int kPl = kKD * 64;                           // one top-level state tile
   constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
@@ -816,8 +823,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     if (p < NSEG - 1 || is_final_seg) {
       SumSmem<1>& ss = *(SumSmem<1>*)smem_raw;
       float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
-      const float dsum = seg_sum_body<__bf16, TV, false, 1, true>(ss, k, v, g, out, b, h, p, vblk,
-                                                                  T, G, H, V, NT, 1 << slog);
+      const float dsum = seg_sum_body<__bf16, TV, false, 1, true, LAYER>(
+          ss, k, v, g, out, b, h, p, vblk, T, G, H, V, NT, 1 << slog, la);
       if (tid == 0)
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, dsum), rsd,
                                               (unsigned int)p * 4, 0, kCohStore);
@@ -957,6 +964,18 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   MainRegs<__bf16, TV, TL, 1> rg;
   constexpr int kLP = kL16 ? 1 : 2;   // pieces per wave (bf16 rows: lu <= 19 needs <= 3 pieces)
   const int lpw0 = w > 0 ? w - 1 : 0;   // first lambda piece of this wave
+  // layer mode: dt words (wave 0: the lane's token row, for g; every thread: its
+  // two V tile rows tid >> 3 and + 32, for v = x dt'), the head's A, bias, D and
+  // the L[h] entries of the lambda columns this lane stages
+  const int desz = la.dt_f32 ? 4 : 2;
+  const char* dtb = LAYER ? (const char*)la.dt + (size_t)b * T * H * desz : (const char*)g;
+  const rsrc_t rdt = make_rsrc(dtb, LAYER ? (size_t)T * H * desz : 0);
+  const rsrc_t rdt0 = make_rsrc(dtb, LAYER && w == 0 ? (size_t)T * H * desz : 0);
+  const float lay_A = LAYER ? la.A[h] : 0.f, lay_b = LAYER && la.bias ? la.bias[h] : 0.f;
+  const float lay_D = LAYER && la.D ? la.D[h] : 0.f;
+  const unsigned int el_g = (unsigned int)(lane * H + h), el_v = (unsigned int)((tid >> 3) * H + h);
+  unsigned int dwv[2] = {0u, 0u};
+  if (LAYER && tid < L) sm.lpar[tid] = la.Lp[h * L + tid];   // read after the first barrier
   uint4 lamr[kLP];
   constexpr int kLamBuf = kMaxLU * kBT;           // floats between the two lambda buffers
   const int lslot = 4 * (lane & 15) + (lane >> 4);   // this lane's token row t, permuted
@@ -974,7 +993,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       // only makes the compiler merge registers after the branch with copies that
       // wait for the load, i.e. a full memory round trip per chunk.  The unused
       // load of a wave goes through an empty range, so it makes no request.
-      rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
+      if constexpr (LAYER) rg.g = buf_load<float>(rdt0, ((row0 * H + el_g) * desz) & ~3u, 0);
+      else rg.g = buf_load<float>(rg_, vo_g, row0 * H * 4);
       const unsigned int so_l = row0 * lstr * sizeof(TL);
 #pragma unroll
       for (int r = 0; r < kLP; ++r) lamr[r] = buf_load16(rlb, vo_l, so_l + 16 * (lpw0 + 3 * r));
@@ -983,13 +1003,34 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     if (part < 0 || part == 1) load_tile64(rg.k, rk, vo_qk, row0 * qstr * 2, qstr);
     if (part == 0 || part == 1) return;
     load_tile64(rg.v, rv, vo_v, row0 * vstr * sizeof(TV), vstr);
+    if constexpr (LAYER) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        dwv[r] = __builtin_bit_cast(unsigned int, buf_load<float>(
+            rdt, ((row0 * H + el_v + 32u * r * H) * desz) & ~3u, 0));
+    }
   };
   auto store = [&](int j) {
     store_tile_swz<swz_qk>(rg.q, sm.q);
     store_tile_swz<swz_qk>(rg.k, sm.k);
-    store_tile_swz<swz_v>(rg.v, sm.v);
+    if constexpr (LAYER) {
+      // v = x dt' on the thread's two rows (dwv holds their dt', see dt_xform),
+      // rounded to bf16 as the layer's v
+      auto xs = rg.v;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float d = __builtin_bit_cast(float, dwv[r]);
+        bf16x8 xv = __builtin_bit_cast(bf16x8, xs.r[r]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = (__bf16)((float)xv[i] * d);
+        xs.r[r] = __builtin_bit_cast(uint4, xv);
+      }
+      store_tile_swz<swz_v>(xs, sm.v);
+    } else {
+      store_tile_swz<swz_v>(rg.v, sm.v);
+    }
     if (w == 0) {
-      const float x = chunk_cumsum(rg.g);   // lane t holds Gc_t
+      const float x = chunk_cumsum(rg.g);   // lane t holds Gc_t (layer mode: g from dt_xform)
       const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
       sm.gc[lane] = x * kLog2e;
       sm.wt[lane] = fexp(last - x);
@@ -1009,9 +1050,49 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           float val;
           if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
           else val = __builtin_bit_cast(float, u[i]);
+
           const int col = col0 + i;
           const int idx = (unsigned int)col < (unsigned int)lu ? col * kBT : junk_rel - (int)(j & 1) * kLamBuf;
           lamw[idx] = val;
+        }
+      }
+    }
+  };
+
+  // layer mode: the dt words of the chunk in the prefetch registers become dt'
+  // (V rows) and g = A dt' (wave 0) once they have landed, at the end of a
+  // chunk rather than in the register-heavy middle where store() runs
+  auto dt_xform = [&]() {
+    if constexpr (LAYER) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        dwv[r] = __builtin_bit_cast(unsigned int,
+                                    layer_dtp(layer_dt_word(dwv[r], el_v + 32u * r * H, la.dt_f32),
+                                              lay_b, la.softplus));
+      if (w == 0)
+        rg.g = layer_g(lay_A, layer_dtp(layer_dt_word(__builtin_bit_cast(unsigned int, rg.g), el_g,
+                                                      la.dt_f32), lay_b, la.softplus));
+    }
+  };
+  // layer mode: lambda = compute_lambda(L[h], dl) applied in place to the dl
+  // values this lane staged for chunk jj (its own entries only; the next
+  // barrier publishes them), away from the register-heavy middle of a chunk
+  auto lam_xform = [&](int jj) {
+    if constexpr (LAYER) {
+      if (w > 0) {
+        float* lamw = sm.lam[jj & 1] + lslot;
+#pragma unroll
+        for (int r = 0; r < kLP; ++r) {
+          const int col0 = kPE * (w - 1 + 3 * r) - lmis;
+#pragma unroll
+          for (int i = 0; i < kPE; ++i) {
+            const int col = col0 + i;
+            if ((unsigned int)col < (unsigned int)lu) {
+              float val = lambda_of(sm.lpar[col], lamw[col * kBT], la.mode);
+              if (la.lam_bf16) val = (float)(__bf16)val;
+              lamw[col * kBT] = val;
+            }
+          }
         }
       }
     }
@@ -1038,8 +1119,14 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   // and chunk j + 2's loads are issued at the same point, so they have a whole
   // chunk period to land and a chunk needs two barriers instead of three.
   load(0, -1);
+  if (LAYER) __syncthreads();   // L[h] staged in LDS
+  dt_xform();
   store(0);
-  if (nch > 1) load(1, -1);
+  lam_xform(0);
+  if (nch > 1) {
+    load(1, -1);
+    dt_xform();
+  }
   float Eseg = 0.f;   // log2-decay from the segment start to the current chunk start
   const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
   for (int j = 0; j < nch; ++j) {
@@ -1157,9 +1244,27 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         lam = nl;
       }
     }
+    if (LAYER && la.D != nullptr) {
+      // y = bf16(o) + x D[h]: x[t = 16 nt + ln][v = 16 w + 4 lq .. + 3]
+      // one x row group at a time, fenced so the loads are not hoisted into the
+      // register-heavy part of the chunk
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      buf_store4<TO>(acc[nt], ro, vo_o, ((unsigned int)ic * kBT + 16 * nt) * vstr * sizeof(TO));
+      for (int nt = 0; nt < 4; ++nt) {
+        __builtin_amdgcn_sched_barrier(0);
+        const bf16x4 x4 = __builtin_bit_cast(
+            bf16x4, buf_load8(rv, (ln0 * vstr + 16 * w + 4 * lq0) * 2,
+                              ((unsigned int)ic * kBT + 16 * nt) * vstr * 2));
+        floatx4 y;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = layer_out((float)(__bf16)acc[nt][i], (float)x4[i], lay_D);
+        buf_store4<TO>(y, ro, vo_o, ((unsigned int)ic * kBT + 16 * nt) * vstr * sizeof(TO));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        buf_store4<TO>(acc[nt], ro, vo_o, ((unsigned int)ic * kBT + 16 * nt) * vstr * sizeof(TO));
+    }
 
     // ---- local state update with the chunk's K^T diag(w) V ---------------------------
     if (nloc > 0) {
@@ -1200,6 +1305,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           }
       }
     }
+    if (j + 1 < nch) lam_xform(j + 1);
+    if (more) dt_xform();   // chunk j + 2's dt words
     Eseg += glr;
   }
 }
@@ -1340,7 +1447,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
       hipLaunchKernelGGL(kern, dim3(B * NSEG * H * nvb64), dim3(256), smem, stream,
                          (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
                          gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog,
-                         NSEG, ht != nullptr ? 1 : 0);
+                         NSEG, ht != nullptr ? 1 : 0, LayerArgs{});
       return hipGetLastError();
     }
     auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, false>;
@@ -1349,7 +1456,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
     hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
                        (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
                        gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
-                       ht != nullptr ? 1 : 0);
+                       ht != nullptr ? 1 : 0, LayerArgs{});
     return hipGetLastError();
   }
   if (NSEG > 1) {
@@ -1376,6 +1483,45 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
                      (const TV*)v, g, (const TL*)l, (TO*)o, gcum, ht, w.sums, w.segd,
                      (const __bf16*)w.htop, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
                      ht != nullptr ? 1 : 0);
+  return hipGetLastError();
+}
+
+// The layer scan of hmamba_chunk_scan_combined with its pre- and
+// post-processing folded into the fused bf16 forward: x and dl are read in
+// place of v and lambda, dt in place of g; o receives bf16(scan) + x D[h] (or
+// the scan output when D is null).
+template <typename TL, typename TO>
+static hipError_t layer_launch_t(const void* q, const void* k, const void* x, const void* dl,
+                                 void* o, float* gcum, void* ws, const LayerArgs& la, int B, int T,
+                                 int G, int H, int V, int L, int nlev, hipStream_t stream) {
+  const int NT = T / kBT;
+  const int slog = seg_log2(NT, kMaxLoc);
+  const int NSEG = (NT + (1 << slog) - 1) >> slog;
+  const int nvb64 = V / 64;
+  const FwdWs w = fwd_ws_layout(ws, B, T, H, V, 0);
+  const int ntop = nlev - min(slog, nlev);
+  const int smem = bf16_smem_bytes(ntop);
+  hipError_t e;
+  if (NSEG > 1) {
+    hipLaunchKernelGGL(mamba2_fwd_sync_init_kernel, dim3((w.nsync + 255) / 256), dim3(256), 0,
+                       stream, w.sync, w.nsync);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    auto kern = mamba2_fwd_bf16_kernel<__bf16, TL, TO, true, true>;
+    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(B * NSEG * H * nvb64), dim3(256), smem, stream,
+                       (const __bf16*)q, (const __bf16*)k, (const __bf16*)x, (const float*)nullptr,
+                       (const TL*)dl, (TO*)o, gcum, (float*)nullptr, w.sums, w.segd, w.sync, B, T,
+                       G, H, V, L, nlev, nvb64, slog, NSEG, 0, la);
+    return hipGetLastError();
+  }
+  auto kern = mamba2_fwd_bf16_kernel<__bf16, TL, TO, false, true>;
+  e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)x, (const float*)nullptr,
+                     (const TL*)dl, (TO*)o, gcum, (float*)nullptr, w.sums, w.segd, w.sync, B, T, G,
+                     H, V, L, nlev, nvb64, slog, NSEG, 0, la);
   return hipGetLastError();
 }
 
@@ -1413,6 +1559,30 @@ hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, 
   if (dt_v == DT_FP32 && dt_l == DT_BF16) { HATTN_DISPATCH_O(float, __bf16) }
   if (dt_v == DT_FP32 && dt_l == DT_FP32) { HATTN_DISPATCH_O(float, float) }
 #undef HATTN_DISPATCH_O
+  *unsupported = 1;
+  return hipSuccess;
+}
+
+// Layer scan with the pre- / post-processing folded in: bf16 q (= C), k (= B),
+// x; dl bf16 or fp32; o (y) bf16 or fp32; dt bf16 or fp32 (la.dt_f32).
+hipError_t hattn_mamba2_layer_fwd_launch(const void* q, const void* k, const void* x,
+                                         const void* dl, void* o, float* gcum, void* ws,
+                                         const void* dt, const float* A, const float* dt_bias,
+                                         const float* Lp, const float* D, int dt_f32,
+                                         int softplus, int mode, int lam_bf16, int B, int T,
+                                         int G, int H, int V, int L, int nlev, int dt_l,
+                                         int dt_o, hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  const LayerArgs la{dt, A, dt_bias, Lp, D, dt_f32, softplus, mode, lam_bf16};
+  if (dt_l == DT_BF16 && dt_o == DT_BF16)
+    return layer_launch_t<__bf16, __bf16>(q, k, x, dl, o, gcum, ws, la, B, T, G, H, V, L, nlev, stream);
+  if (dt_l == DT_BF16 && dt_o == DT_FP32)
+    return layer_launch_t<__bf16, float>(q, k, x, dl, o, gcum, ws, la, B, T, G, H, V, L, nlev, stream);
+  if (dt_l == DT_FP32 && dt_o == DT_BF16)
+    return layer_launch_t<float, __bf16>(q, k, x, dl, o, gcum, ws, la, B, T, G, H, V, L, nlev, stream);
+  if (dt_l == DT_FP32 && dt_o == DT_FP32)
+    return layer_launch_t<float, float>(q, k, x, dl, o, gcum, ws, la, B, T, G, H, V, L, nlev, stream);
   *unsupported = 1;
   return hipSuccess;
 }

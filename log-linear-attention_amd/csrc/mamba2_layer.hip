@@ -26,6 +26,7 @@
 #include <initializer_list>
 
 #include "common.h"
+#include "layer_math.h"
 
 namespace hattn {
 
@@ -76,20 +77,6 @@ __device__ __forceinline__ void st8(void* p, size_t i, const float* x, int bf) {
   }
 }
 
-// torch.nn.functional.softplus (beta 1, threshold 20) and its derivative
-__device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float dsoftplus20(float x) {
-  return x > 20.f ? 1.f : 1.f / (1.f + expf(-x));
-}
-
-enum { kLamLinear = 0, kLamPositive = 1, kLamBounded = 2 };
-
-__device__ __forceinline__ float lambda_of(float Lv, float dlv, int mode) {
-  if (mode == kLamPositive) return softplus20(Lv * dlv);
-  if (mode == kLamBounded) return expf(-expf(Lv) * softplus20(dlv));
-  return Lv * dlv;
-}
-
 // Ordered column sums of partial rows: out column c (of ncol) = sum over
 // b < nblk of ws[b * stride + c].  Grid ceil(ncol / 64) workgroups of 16
 // waves; wave g adds rows g, g + 16, ... in order, then the 16 wave sums are
@@ -137,11 +124,10 @@ __global__ __launch_bounds__(256) void mamba2_layer_prologue_kernel(
     if (e0 >= (unsigned int)(rows * P)) return;
     const unsigned int r = e0 >> lp;
     const int h = (int)(r % (unsigned int)H);
-    float d = ld1(dt, r, f.dt) + (dt_bias ? dt_bias[h] : 0.f);
-    if (softplus) d = softplus20(d);
+    const float d = layer_dtp(ld1(dt, r, f.dt), dt_bias ? dt_bias[h] : 0.f, softplus);
     const floatx4 xv = ld4(x, e0, f.x);
     st4(v, e0, floatx4{xv[0] * d, xv[1] * d, xv[2] * d, xv[3] * d}, f.v);
-    if (e0 == r * P) g[r] = A[h] * d;
+    if (e0 == r * P) g[r] = layer_g(A[h], d);
   } else {
     const unsigned int e = (blockIdx.x - nbx) * 256u + threadIdx.x;
     if (e >= (unsigned int)(rows * L)) return;
@@ -167,14 +153,13 @@ __global__ __launch_bounds__(256) void mamba2_layer_prologue_vec_kernel(
     if (e0 >= (unsigned int)(rows * P)) return;
     const unsigned int r = e0 >> lp;
     const int h = (int)(r % (unsigned int)H);
-    float d = ld1(dt, r, f.dt) + (dt_bias ? dt_bias[h] : 0.f);
-    if (softplus) d = softplus20(d);
+    const float d = layer_dtp(ld1(dt, r, f.dt), dt_bias ? dt_bias[h] : 0.f, softplus);
     float xv[8];
     ld8(x, e0, f.x, xv);
 #pragma unroll
     for (int c = 0; c < 8; ++c) xv[c] *= d;
     st8(v, e0, xv, f.v);
-    if (e0 == r * P) g[r] = A[h] * d;
+    if (e0 == r * P) g[r] = layer_g(A[h], d);
   } else {
     const unsigned int n = (unsigned int)(rows * L);
     const unsigned int e0 = 8u * ((blockIdx.x - nbx) * 256u + threadIdx.x);
@@ -215,7 +200,8 @@ __global__ __launch_bounds__(256) void mamba2_layer_epilogue_kernel(
   const int h = (int)((e0 >> (31 - __builtin_clz((unsigned int)P))) % (unsigned int)H);
   const float d = D[h];
   const floatx4 a = ld4(y, e0, ybf), b = ld4(x, e0, xbf);
-  st4(out, e0, floatx4{a[0] + b[0] * d, a[1] + b[1] * d, a[2] + b[2] * d, a[3] + b[3] * d}, obf);
+  st4(out, e0, floatx4{layer_out(a[0], b[0], d), layer_out(a[1], b[1], d), layer_out(a[2], b[2], d),
+                       layer_out(a[3], b[3], d)}, obf);
 }
 
 struct LayerBwdDt {
@@ -281,8 +267,8 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_kernel(
           gdl = u * Lv;
           gL = u * dlv;
         } else if (mode == kLamBounded) {
-          const float eL = expf(Lv), sp = softplus20(dlv);
-          const float lamv = expf(-eL * sp);
+          const float eL = __expf(Lv), sp = softplus20(dlv);
+          const float lamv = __expf(-eL * sp);
           gL = gl * lamv * (-eL * sp);
           gdl = gl * lamv * (-eL) * dsoftplus20(dlv);
         } else {
@@ -395,8 +381,8 @@ __global__ __launch_bounds__(256) void mamba2_layer_bwd_vec_kernel(
           gdl = u * Lv[k];
           gL = u * dlv;
         } else if (mode == kLamBounded) {
-          const float eL = expf(Lv[k]), sp = softplus20(dlv);
-          const float lamv = expf(-eL * sp);
+          const float eL = __expf(Lv[k]), sp = softplus20(dlv);
+          const float lamv = __expf(-eL * sp);
           gL = gq * lamv * (-eL * sp);
           gdl = gq * lamv * (-eL) * dsoftplus20(dlv);
         } else {

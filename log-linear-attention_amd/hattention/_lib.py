@@ -44,6 +44,7 @@ SIGNATURES = [
     ("hattn_mamba2_prefill_levels", _I, [_P] * 4 + [_I] * 10 + [_P]),
     ("hattn_mamba2_layer_prologue", _I, [_P] * 9 + [_I] * 13 + [_P]),
     ("hattn_mamba2_layer_epilogue", _I, [_P] * 4 + [_I] * 7 + [_P]),
+    ("hattn_mamba2_layer_scan_fwd", _I, [_P] * 11 + [_I] * 18 + [_P, _S, _P]),
     ("hattn_mamba2_layer_bwd_workspace", _S, [_I] * 4),
     ("hattn_mamba2_layer_bwd", _I, [_P] * 18 + [_I] * 17 + [_P, _S, _P]),
     ("hattn_causal_conv1d_silu_fwd", _I, [_P, _LL, _LL, _P, _P, _P, _P, _P] + [_I] * 9 + [_P]),

@@ -2,7 +2,9 @@
 
 hmamba_chunk_scan_combined (hattention/mamba_apis.py:263-404) wraps the scan in
 elementwise torch work: dt' = softplus(dt + dt_bias), v = x dt', g = A dt',
-lambda = compute_lambda(L, dl) and y = o + x D.  Here that work is three HIP
+lambda = compute_lambda(L, dl) and y = o + x D.  Here the forward is one launch
+of the bf16 forward scan with that work folded into its loads and stores
+(``hattn_mamba2_layer_scan_fwd``), or, outside its shapes and dtypes, three HIP
 launches (libhattn_hip.so): ``hattn_mamba2_layer_prologue`` (one pass over x,
 dt, dl writing v, g, lambda), the chunkwise kernels, and
 ``hattn_mamba2_layer_epilogue`` (y = o + x D); the backward is the chunkwise
@@ -125,29 +127,82 @@ def layer_backward(x, dt, A, dt_bias, dl, L, D, dy, dv, dg, dlam, dt_softplus, l
     return dx, ddt, ddl, dA, dbias, dD, dL
 
 
+def layer_scan_folded(x, dt, A, Bc, Cc, dl, L, D, dt_bias, dt_softplus, lambda_mode, level_base,
+                      htype):
+    """The layer scan with the pre- and post-processing folded into the forward
+    scan's loads and stores (``hattn_mamba2_layer_scan_fwd``): returns (y,
+    g_cumsum), or None where that kernel does not apply (then the prologue ->
+    chunkwise forward -> epilogue chain runs).  y has the dtype of that chain:
+    C's (bf16) without D, torch's promotion of (C, x, D) with it."""
+    from hattention.base import HType
+    Bsz, T, H, P = x.shape
+    G, N = Cc.shape[2], Cc.shape[3]
+    Lv = dl.shape[-1]
+    bf = torch.bfloat16
+    if not (x.dtype == bf and Cc.dtype == bf and Bc.dtype == bf and N == 64 and P % 64 == 0
+            and Lv <= 32 and htype == HType.WEAK and level_base == 2 and T % 64 == 0
+            and Bc.shape == Cc.shape and dt.dtype in (bf, torch.float32)
+            and dl.dtype in (bf, torch.float32)):
+        return None
+    if dt.shape != (Bsz, T, H) or dl.shape[:3] != (Bsz, T, H) or L.shape != (H, Lv) or \
+            A.shape != (H,) or (dt_bias is not None and dt_bias.shape != (H,)):
+        raise ValueError("shape mismatch in the layer pre-processing")
+    dev = _lib.require_device(x, dt, A, dt_bias, dl, L, Bc, Cc, D)
+    y_dtype = torch.promote_types(Cc.dtype, torch.promote_types(x.dtype, D.dtype)) \
+        if D is not None else Cc.dtype
+    lam_dtype = torch.promote_types(L.dtype, dl.dtype)
+    x, dt, dl = x.contiguous(), dt.contiguous(), dl.contiguous()
+    A32 = A.float().contiguous()
+    bias = dt_bias.float().contiguous() if dt_bias is not None else None
+    Lp = L.float().contiguous()
+    Df = D.float().contiguous() if D is not None else None
+    y = torch.empty(x.shape, dtype=y_dtype, device=dev)
+    gcum = torch.empty(Bsz, T, H, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws, ws_ptr, ws_bytes = _lib.workspace(
+        lib.hattn_mamba2_chunkwise_fwd_workspace(Bsz, T, G, H, N, P, Lv), dev)
+    _lib.check(lib.hattn_mamba2_layer_scan_fwd(
+        _lib.ptr(x), _lib.ptr(dt), _lib.ptr(A32), _lib.ptr(bias), _lib.ptr(Bc), _lib.ptr(Cc),
+        _lib.ptr(dl), _lib.ptr(Lp), _lib.ptr(Df), _lib.ptr(y), _lib.ptr(gcum), Bsz, T, G, H, P, N,
+        Lv, _code(x.dtype), _code(dt.dtype), _code(Cc.dtype), _code(dl.dtype), _code(lam_dtype),
+        _code(y_dtype), int(bool(dt_softplus)), lambda_mode_code(lambda_mode), level_base,
+        htype.value, 64, ws_ptr, ws_bytes, _lib.stream_handle(dev)))
+    return y, gcum
+
+
 class HMambaScanFunction(torch.autograd.Function):
     """The scan of hmamba_chunk_scan_combined (mamba_apis.py:346-403, MAMBA2,
-    chunkwise, no final state) with its pre- and post-processing fused:
-    prologue -> chunkwise forward (q = C, k = B) -> epilogue; backward: chunkwise
-    backward -> layer backward.  Same gradients as torch autograd through the
-    reference's expressions and HAttentionFunction."""
+    chunkwise, no final state) with its pre- and post-processing fused: one
+    forward launch that folds the prologue into the scan's loads and the
+    epilogue into its stores (``layer_scan_folded``), or prologue -> chunkwise
+    forward (q = C, k = B) -> epilogue where that launch does not apply;
+    backward: the prologue's v and lambda (recomputed when the folded forward
+    did not write them) -> chunkwise backward -> layer backward.  Same
+    gradients as torch autograd through the reference's expressions and
+    HAttentionFunction."""
 
     @staticmethod
     def forward(ctx, x, dt, A, B, C, dl, L, D, dt_bias, dt_softplus, lambda_mode, level_base,
                 htype):
         from hattention import chunkwise as _cw
+        Cc, Bc = C.contiguous(), B.contiguous()
+        ctx.cfg = (dt_softplus, lambda_mode, level_base, htype)
+        folded = layer_scan_folded(x, dt, A, Bc, Cc, dl, L, D, dt_bias, dt_softplus, lambda_mode,
+                                   level_base, htype)
+        if folded is not None:
+            y, gcum = folded
+            ctx.save_for_backward(x, dt, A, Bc, Cc, dl, L, D, dt_bias, None, gcum, None)
+            return y
         # v leaves the prologue in bf16 when the scan runs the bf16 kernels: they
         # round v to bf16 when they stage it for the MFMAs, so the forward values
         # are those of an fp32 v, at half its traffic (dv then comes back in bf16)
         v, g, lam = layer_prologue(x, dt, A, dt_bias, dl, L, dt_softplus, lambda_mode,
                                    v_dtype=torch.bfloat16 if C.dtype == torch.bfloat16 else None)
-        Cc, Bc = C.contiguous(), B.contiguous()
         o, gcum, _ = _cw.chunkwise_fwd(Cc, Bc, v, g, lam, False, level_base, htype, 64, False)
         y = o.to(C.dtype)
         if D is not None:
             y = layer_epilogue(y, x, D)
         ctx.save_for_backward(x, dt, A, Bc, Cc, dl, L, D, dt_bias, v, gcum, lam)
-        ctx.cfg = (dt_softplus, lambda_mode, level_base, htype)
         return y
 
     @staticmethod
@@ -155,6 +210,9 @@ class HMambaScanFunction(torch.autograd.Function):
         from hattention import chunkwise as _cw
         x, dt, A, Bc, Cc, dl, L, D, dt_bias, v, gcum, lam = ctx.saved_tensors
         dt_softplus, lambda_mode, level_base, htype = ctx.cfg
+        if v is None:
+            v, _, lam = layer_prologue(x, dt, A, dt_bias, dl, L, dt_softplus, lambda_mode,
+                                       v_dtype=torch.bfloat16)
         do = dy.to(Cc.dtype).contiguous()
         dq, dk, dv, dg, dlam = _cw.chunkwise_bwd(Cc, Bc, v, gcum, lam, do, False, level_base,
                                                  htype, 64)

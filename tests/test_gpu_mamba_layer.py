@@ -20,6 +20,8 @@ dv = 128 cases check the forward).  The full-size case compares the fused
 layer with the reference's torch expressions on the GPU around the same scan
 kernels, which checks the layer backward exactly given the scan gradients.
 """
+import math
+
 import pytest
 import torch
 
@@ -161,7 +163,10 @@ def test_layer_bwd_deterministic():
 def test_layer_full_size_matches_torch_chain():
     """North-star shape (B=4 T=16384 H=16 P=N=64, L=15): the fused layer against
     the reference's torch expressions on the GPU around the same scan
-    (hattention_kernel), forward and gradients."""
+    (hattention_kernel), forward and gradients.  Elementwise gradients: max-rel
+    < 2e-2.  The per-head sums dA, ddt_bias, dD, dL cancel heavily over the
+    65536 tokens of a head (|dA| is ~2% of the sum of its terms' magnitudes), so
+    their bound is relative to that sum (as in _run): < 2e-3."""
     from hattention.base import HType, HStruct
     from hattention.kernel import hattention_kernel
     from hattention.mamba_apis import hmamba_chunk_scan_combined
@@ -174,20 +179,80 @@ def test_layer_full_size_matches_torch_chain():
                                        **_kw(Lv, "positive"))
     b = [t.clone().requires_grad_(True) for t in (x, dt, A, Bm, Cm, dl, L, D, bias)]
     d = torch.nn.functional.softplus(b[1] + b[8][None, None])
-    lam = torch.nn.functional.softplus(b[6][None, None] * b[5])
-    y2 = hattention_kernel(b[4], b[3], b[0] * d[..., None], None, b[2][None, None] * d, lam,
+    Lb = b[6][None, None].expand_as(b[5])
+    lam = torch.nn.functional.softplus(Lb * b[5])
+    g2 = b[2][None, None] * d
+    for t in (d, lam, g2):
+        t.retain_grad()
+    y2 = hattention_kernel(b[4], b[3], b[0] * d[..., None], None, g2, lam,
                            None, False, 2, HType.WEAK, HStruct.MAMBA2)
     y2 = y2 + b[0] * b[7][None, None, :, None]
-    dy = torch.randn_like(y1)
+    gen = torch.Generator("cpu").manual_seed(4061)
+    dy = torch.randn(y1.shape, generator=gen).to(DEV)
     y1.backward(dy)
     y2.backward(dy.to(y2.dtype))
     torch.cuda.synchronize()
     mx, fro = _errs(y1, y2)
     assert mx < 1e-2 and fro < 5e-3, (mx, fro)
-    for name, g1, g2 in zip(["x", "dt", "A", "B", "C", "dl", "L", "D", "dt_bias"], a, b):
-        e, _ = _errs(g1.grad, g2.grad)
-        print(f"  d{name}: max-rel {e:.2e}", flush=True)
-        assert e < 2e-2, (name, e)
+    # sums of the per-token terms' magnitudes of each per-head gradient
+    with torch.no_grad():
+        dlam_dL = torch.sigmoid(Lb * b[5]) * b[5]
+        scale = {"A": (g2.grad * d).abs().sum((0, 1)),
+                 "dt_bias": b[1].grad.abs().sum((0, 1)),
+                 "D": (dy * b[0]).abs().sum((0, 1, 3)),
+                 "L": (lam.grad * dlam_dL).abs().sum((0, 1))}
+    for name, g1, g2_ in zip(["x", "dt", "A", "B", "C", "dl", "L", "D", "dt_bias"], a, b):
+        if name in scale:
+            e = ((g1.grad.double() - g2_.grad.double()).abs()
+                 / scale[name].double().clamp_min(1e-30)).max().item()
+            print(f"  d{name}: err / sum|terms| {e:.2e}", flush=True)
+            assert e < 2e-3, (name, e)
+        else:
+            e, _ = _errs(g1.grad, g2_.grad)
+            print(f"  d{name}: max-rel {e:.2e}", flush=True)
+            assert e < 2e-2, (name, e)
+
+
+@pytest.mark.parametrize("T,mode,use_D,dt_bf16,L_bf16", [
+    (640, "positive", True, False, False),      # one segment (single-segment kernel)
+    (2048, "positive", True, False, False),     # several segments (single-pass kernel)
+    (2048, "bounded", True, True, False),       # bf16 dt
+    (2048, None, False, False, True),           # no D (y in C's dtype), bf16 lambda
+    (4096, "positive", True, False, True),
+])
+def test_layer_folded_matches_separate_chain(T, mode, use_D, dt_bf16, L_bf16):
+    """The folded forward (one launch, hattn_mamba2_layer_scan_fwd) against the
+    separate prologue -> chunkwise forward -> epilogue launches on the same
+    inputs: the same v, g, lambda and y formulas (layer_math.h), so g_cumsum
+    agrees to fp32 rounding (softplus inlined in two kernels may differ in the
+    last bit) and y to that and one bf16 rounding of o."""
+    from hattention import chunkwise as _cw
+    from hattention.base import HType
+    from hattention.mamba_layer import layer_epilogue, layer_prologue, layer_scan_folded
+    B, H, G, P, N, Lv = 2, 4, 2, 128, 64, 7 + int(math.log2(T // 64)) + 1
+    x, dt, A, Bm, Cm, dl, L, D, bias = (t.to(DEV) for t in
+                                        _inputs(B, T, H, G, P, N, Lv, 407 + T, torch.bfloat16))
+    if dt_bf16:
+        dt = dt.bfloat16()
+    if L_bf16:
+        L = L.bfloat16()
+    D = D if use_D else None
+    print(f"[layer folded] T={T} mode={mode} D={use_D} dt={dt.dtype} L={L.dtype}", flush=True)
+    y1, g1 = layer_scan_folded(x, dt, A, Bm, Cm, dl, L, D, bias, True, mode, 2, HType.WEAK)
+    v, g, lam = layer_prologue(x, dt, A, bias, dl, L, True, mode, v_dtype=torch.bfloat16)
+    o, g2, _ = _cw.chunkwise_fwd(Cm, Bm, v, g, lam, False, 2, HType.WEAK, 64, False)
+    y2 = o.to(Cm.dtype)
+    if D is not None:
+        y2 = layer_epilogue(y2, x, D)
+    torch.cuda.synchronize()
+    assert y1.dtype == y2.dtype and y1.shape == y2.shape
+    gd = ((g1 - g2).abs() / g2.abs().clamp_min(1.0)).max().item()
+    diff = ((y1.float() - y2.float()).abs().max() / y2.float().abs().max()).item()
+    fro = ((y1.float() - y2.float()).norm() / y2.float().norm()).item()
+    print(f"  folded vs separate: g_cumsum {gd:.2e}, y max-rel {diff:.2e} fro {fro:.2e}",
+          flush=True)
+    assert gd < 1e-6, gd
+    assert diff < 1e-2 and fro < 1e-3, (diff, fro)
 
 
 # ---------------------------------------------------------------------------

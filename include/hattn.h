@@ -71,9 +71,16 @@ const char* hattn_last_error(void);
  * Constraints (status on violation):
  *   T % 64 == 0, T >= 64, H % G == 0, L >= 7 + ceil(log2(T / 64)),
  *   V % 64 == 0, workspace large enough               -> HATTN_ERR_VALUE
- *   chunk_size == 64, level_base == 2, htype == WEAK, K == 64,
- *   dtype_qk == BF16, dtype_v / dtype_l / dtype_o in {BF16, FP32}
- *                                                  -> HATTN_ERR_NOT_IMPLEMENTED
+ *   htype not HATTN_HTYPE_WEAK / HATTN_HTYPE_STRONG  -> HATTN_ERR_VALUE
+ *   chunk_size == 64, level_base == 2, K == 64 (the Python host layer runs a
+ *   larger K as one call per 64-wide block of q and k and sums the outputs),
+ *   dtype_qk BF16 (bf16 MFMA) or FP32 (bf16x3, fp32-accurate), dtype_v /
+ *   dtype_l / dtype_o in {BF16, FP32}                -> HATTN_ERR_NOT_IMPLEMENTED
+ * htype HATTN_HTYPE_STRONG (the reference's USE_A2 / USE_H2 forward,
+ * chunkwise.py:1118-1275 with the strong level function, base.py:49-62): BF16
+ * q, k, v, L <= 32, T <= 64 * 2^9 and ht NULL (the reference keeps one of
+ * four phase states per level, chunkwise.py:275-279, which is no HState; the
+ * decode step builds strong states itself); else HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
                                const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
@@ -211,8 +218,8 @@ size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int 
  *   kernel.py:24-29, 224-225 applied inside the kernel)
  *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
  *
- * Constraints as hattn_gdn_chunkwise_fwd, except K, V in {64, 128} ->
- * HATTN_ERR_NOT_IMPLEMENTED (the gradients are sums over independent column
+ * Constraints as hattn_gdn_chunkwise_fwd, except K in {64, 128, 192} and V in
+ * {64, 128} -> HATTN_ERR_NOT_IMPLEMENTED (the gradients are sums over independent column
  * blocks of V, so a caller splits a larger V into blocks of 128 / 64 and sums
  * dq, dk, db, dg, dl; hattention.chunkwise_hgdn.chunkwise_bwd does); do bf16 ->
  * else HATTN_ERR_NOT_IMPLEMENTED.

@@ -30,14 +30,14 @@
 // operand layout), U, and P (bf16, [row][chunk][t][s]); the backward's
 // recompute also writes K_new token-major.
 // Kernel 2 (gdn_scan_kernel): one workgroup per (row, BV columns of V), eight
-// waves.  Every level's [K x BV] state lives in fp32 registers, tile j of the
-// (K / 16) x (BV / 16) state tiles on wave j % 8.  Per chunk the states are
-// staged in LDS as bf16, waves 0-3 form W_new h_e (-> V_new_e, LDS) and
-// waves 4-7 q_new h_e (-> the level reads) for their 16-row t-tile with the
-// A operands read straight from global memory one chunk ahead, waves 4-7 add
-// o_intra = P V and write o, and every wave updates its state tiles with
-// K_new^T V_new_e.  The slices of one row run on one XCD, so the chunk tiles
-// they share are fetched into one L2.
+// waves in two level groups.  Every level's [K x BV] state lives in fp32
+// registers (a group's levels, the wave's k-quarter).  Per chunk the states
+// are staged in LDS as bf16, each wave forms W_new h_e (-> V_new_e, LDS) and
+// q_new h_e (-> the level reads) of its group's levels for its 16-row t-tile,
+// group 0 adds o_intra = P V and writes o, and every wave updates its state
+// tiles with K_new^T V_new_e.  The next chunk's operands are loaded while the
+// current one computes.  The slices of one row run on one XCD, so the chunk
+// tiles they share are fetched into one L2.
 #include "gdn_common.h"
 
 namespace hattn {
@@ -365,7 +365,8 @@ struct GdnScanCfg {
   static constexpr int NC = KD / 32;                  // MFMA steps of a contraction over K
   static constexpr int LPG = kGMaxLev / 2;            // levels per level group
   static constexpr int LK = KD + 8;                   // row stride of the staged states
-  static constexpr int LVS = BV + 8;                  // row stride of the staged V slice
+  static constexpr int LVS = BV + 8;                  // row stride of the staged V and U slices
+  static constexpr int KU = KD / 64;                  // 16-byte units of K_new^T per thread
 };
 
 template <int KD, int BV>
@@ -373,10 +374,18 @@ struct GdnScanSmem {
   using C = GdnScanCfg<KD, BV>;
   __bf16 hs[kGMaxLev][BV * C::LK];    // states, bf16 [v][k]
   __bf16 vn[kGMaxLev][BV * kLd64];    // V_new, bf16 [v][t]
+  __bf16 kb[KD * kGC];                // the chunk's K_new^T [k][t] (swz64)
+  __bf16 pm[kGC * kGC];               // the chunk's P [t][s] (swz64)
   __bf16 vs[kGC * C::LVS];            // the chunk's V slice [t][v] (o_intra)
+  __bf16 us[kGC * C::LVS];            // the chunk's U slice [t][v] (V_new)
   float lam[kGMaxLev][kGC];           // lambda[t, 7 + e], zero for e >= nlev
   floatx4 xacc[4][C::NVT][64];        // level group 1's reads, summed into group 0's
 };
+
+// Element offset of 16-byte unit u of row r in a [rows][64] bf16 tile whose
+// units are XOR-permuted by the row: the 16-byte row-fragment reads of the
+// MFMA operands (16 rows, one unit each) hit distinct banks.
+__device__ __forceinline__ int swz64(int r, int u) { return r * 64 + ((u ^ r) & 7) * 8; }
 
 // Eight waves in two level groups: wave w runs levels 4 (w >> 2) .. +3 with
 // q = w & 3 as its t-tile (the products W_new h_e and q_new h_e, which share
@@ -385,6 +394,12 @@ struct GdnScanSmem {
 // compiler interleaves their LDS reads and MFMA chains; a level e >= nlev
 // never writes (its V_new is zero, so its state stays zero) and is never read
 // (lambda is zero for it, bit e of the chunk index is clear).
+// Operand pipeline: the loads of chunk ic + 1 are issued right after the
+// level products of chunk ic, small operands first, and land in LDS at the
+// start of chunk ic + 1 (K_new^T, read only by the state update, right after
+// the first barrier), so no wave waits for memory inside a chunk.  The K_new^T,
+// P, V and U tiles are loaded once per workgroup (one 16-byte unit per thread
+// and tile) instead of once per wave.
 // HSAVE (the backward's recompute): every level's state at every chunk start
 // is written to hsave, bf16 [row][chunk][level][v][k]; then o may be null and
 // pm any valid pointer.  A separate instantiation, so the forward carries no
@@ -401,6 +416,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
   constexpr int LK = C::LK, LVS = C::LVS, NVT = C::NVT, MT = C::MT, NC = C::NC, LPG = C::LPG;
+  constexpr int KU = C::KU;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int nvb = V / BV;
@@ -409,7 +425,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   const int row = mp.row, v0 = mp.slice * BV;
   const int b = row / H, h = row % H;
   const int NT = T / kGC;
-  const size_t hv = (size_t)H * V;
   const size_t rowtok = (size_t)b * T * H + h;   // (token 0 of the row) * H + h
   const int lg = w >> 2, q = w & 3, e0 = LPG * lg;
 
@@ -423,27 +438,26 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       for (int n = 0; n < NVT; ++n) st[le][m][n] = zero4();
   for (int i = tid; i < kGMaxLev * kGC; i += 512) s.lam[i / kGC][i % kGC] = 0.f;
 
-  // Operand loads: a uniform per-row base (scalar registers) plus a 32-bit lane
-  // offset, advanced by a uniform per-chunk offset.  The A operands of the
-  // products of the level reads (q_new / W_new rows of t-tile q) are loaded for
-  // the next chunk right after their last use in this chunk, the A operands of
-  // the state update (K_new^T rows of k-quarter q) right after the reads, and
-  // the small operands one chunk ahead; none of them is held across the reads,
-  // where the register pressure peaks.  Every load is unconditional, so the
+  // Operand loads: a uniform per-row base plus a 32-bit lane offset, advanced
+  // by a uniform per-chunk offset.  Every load is unconditional, so the
   // compiler does not wait for it at a branch.
   const unsigned HV = (unsigned)H * V, HK = (unsigned)H * KD, HL = (unsigned)H * L;
   const __bf16* qrow = qn + rowtok * KD;
   const __bf16* wrow = wn + rowtok * KD;
   const unsigned a_off = (16 * q + ln) * HK + 8 * lq;
   const __bf16* knrow = knT + (size_t)row * NT * KD * kGC;
-  const unsigned k_off = (16 * MT * q + ln) * kGC + 8 * lq;
   const __bf16* pmrow = pm + (size_t)row * NT * kGC * kGC;
-  const unsigned p_off = (16 * q + ln) * kGC + 8 * lq;
-  const __bf16* unrow = un + rowtok * V + v0;
-  const unsigned u_off = (16 * q + 4 * lq) * HV + ln;
-  const int vu = min(tid, 8 * BV - 1);   // 16-byte unit of the [64 x BV] V slice
-  const __bf16* vrow = vin + rowtok * V + v0;
-  const unsigned v_off = (vu / (BV / 8)) * HV + 8 * (vu % (BV / 8));
+  const unsigned u_off = (16 * q + 4 * lq) * HV + ln;   // o[t = 16q + 4lq + i][v = 16n + ln]
+  // V slice (threads 0 .. 8 BV - 1) and U slice (8 BV .. 16 BV - 1): one
+  // 16-byte unit of the [64 x BV] tile each; threads past 16 BV repeat the
+  // last unit and do not store it
+  const bool s_store = tid < 16 * BV;
+  const int su = s_store ? tid : 16 * BV - 1;
+  const bool is_u = su >= 8 * BV;
+  const int vu = is_u ? su - 8 * BV : su;
+  const __bf16* sbase = (is_u ? un : vin) + rowtok * V + v0;
+  const unsigned s_off = (vu / (BV / 8)) * HV + 8 * (vu % (BV / 8));
+  __bf16* sdst = (is_u ? s.us : s.vs) + (vu / (BV / 8)) * LVS + 8 * (vu % (BV / 8));
   const int nl1 = nlev > 0 ? nlev : 1;   // T = 64 has no inter-chunk level
   const int e2 = min(tid, nl1 * kGC - 1);
   const TL* lrow = l + rowtok * L;
@@ -454,7 +468,9 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   __bf16* hrow = HSAVE ? hsave + (size_t)row * NT * nlev * V * KD + (size_t)v0 * KD : nullptr;
   const unsigned h_off = ln * KD + 16 * MT * q + 4 * lq;
 
-  u32x4 aq[NC], aw[NC], kf[MT][2];
+  u32x4 aq[NC], aw[NC], kfn[KU], pvu, pp1;
+  TL plr;
+  float pgl;
   auto load_a = [&](int jc) __attribute__((always_inline)) {
     const size_t off = (size_t)jc * kGC * HK;
 #pragma unroll
@@ -466,41 +482,22 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   auto load_k = [&](int jc) __attribute__((always_inline)) {
     const __bf16* base = knrow + (size_t)jc * KD * kGC;
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) kf[m][c] = *(const u32x4*)(base + k_off + 16 * m * kGC + 32 * c);
+    for (int r = 0; r < KU; ++r) kfn[r] = *(const u32x4*)(base + 8 * (tid + 512 * r));
   };
-  u32x4 pp[2], pv;
-  float pu[NVT][4], pl, pgl;
   auto fetch_small = [&](int jc) __attribute__((always_inline)) {
     const size_t tokoff = (size_t)jc * kGC * H;   // chunk jc's first token, times H
-    const __bf16* pb = pmrow + (size_t)jc * kGC * kGC;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) pp[c] = *(const u32x4*)(pb + p_off + 32 * c);
-    const __bf16* ub = unrow + tokoff * V;
-#pragma unroll
-    for (int n = 0; n < NVT; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pu[n][i] = (float)ub[u_off + i * HV + 16 * n];
-    pv = *(const u32x4*)(vrow + tokoff * V + v_off);
-    pl = to_f32<TL>(lrow[tokoff * L + l_off]);
+    pvu = *(const u32x4*)(sbase + tokoff * V + s_off);
+    if constexpr (!HSAVE) pp1 = *(const u32x4*)(pmrow + (size_t)jc * kGC * kGC + 8 * tid);
+    plr = lrow[tokoff * L + l_off];
     pgl = buf_load<float>(grs, 0, (unsigned)(tokoff * 4));
   };
-  load_a(0);
   fetch_small(0);
+  load_k(0);
+  load_a(0);
 
   for (int ic = 0; ic < NT; ++ic) {
     const int icn = min(ic + 1, NT - 1);
-    // this chunk's small operands, moved out of the prefetch registers
-    u32x4 pf[2] = {pp[0], pp[1]};
-    float uu[NVT][4];
-#pragma unroll
-    for (int n = 0; n < NVT; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) uu[n][i] = pu[n][i];
     const float glast = pgl;
-    if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = pl;
-    if (tid < 8 * BV) *(u32x4*)(s.vs + (tid / (BV / 8)) * LVS + 8 * (tid % (BV / 8))) = pv;
     // states -> LDS (bf16 [v][k]) and, with hsave, to hsave[row][chunk][level][v][k]
 #pragma unroll
     for (int le = 0; le < LPG; ++le)
@@ -514,12 +511,28 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           if (HSAVE && e0 + le < nlev)
             *(bf16x4*)(hrow + ((size_t)ic * nlev + e0 + le) * V * KD + h_off + (16 * n * KD + 16 * m)) = h4;
         }
+    // the chunk's lambda, V and U slices and P -> LDS
+    if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = to_f32<TL>(plr);
+    if (s_store) *(u32x4*)sdst = pvu;
+    if constexpr (!HSAVE) *(u32x4*)(s.pm + swz64(tid >> 3, tid & 7)) = pp1;
     __syncthreads();
+    // the chunk's K_new^T -> LDS: every wave is past the previous chunk's state
+    // update, and the second barrier orders these stores before this chunk's
+#pragma unroll
+    for (int r = 0; r < KU; ++r) {
+      const int u = tid + 512 * r;
+      *(u32x4*)(s.kb + swz64(u >> 3, u & 7)) = kfn[r];
+    }
 
     // ---- V_new_e = (write ? U : 0) - (reset ? 0 : W_new h_e) -> LDS, and the reads
     //      lambda_e o (q_new h_e) of the levels with bit e of ic set.  The level's
     //      flags enter as 0 / 1 factors.
     const bool last = ic == NT - 1;
+    float uu[NVT][4];
+#pragma unroll
+    for (int n = 0; n < NVT; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) uu[n][i] = (float)s.us[(16 * q + 4 * lq + i) * LVS + 16 * n + ln];
     floatx4 acc[NVT];
 #pragma unroll
     for (int n = 0; n < NVT; ++n) acc[n] = zero4();
@@ -553,21 +566,23 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       // pressure)
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_a(icn);
-    load_k(ic);
+    // chunk ic + 1's operands: the ones needed first are issued first (the
+    // wait counter is in order)
     fetch_small(icn);
+    load_k(icn);
+    load_a(icn);
     if (lg == 1) {
 #pragma unroll
       for (int n = 0; n < NVT; ++n) s.xacc[q][n][lane] = acc[n];
     } else if (o != nullptr) {
-      // o_intra = P V (the V slice is rewritten at the next chunk's start, so it
-      // is read before the barrier)
+      // o_intra = P V
 #pragma unroll
-      for (int n = 0; n < NVT; ++n)
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 pf = *(const bf16x8*)(s.pm + swz64(16 * q + ln, lq + 4 * c));
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-          acc[n] = mfma16x16x32(__builtin_bit_cast(bf16x8, pf[c]), tr_frag(s.vs, LVS, 32 * c, 16 * n),
-                                acc[n]);
+        for (int n = 0; n < NVT; ++n)
+          acc[n] = mfma16x16x32(pf, tr_frag(s.vs, LVS, 32 * c, 16 * n), acc[n]);
+      }
     }
     __syncthreads();
 
@@ -584,6 +599,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
 
     // ---- h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new_e -----------------------
     const float gl = fexp(glast);
+    bf16x8 kf[MT][2];   // K_new^T[k = 16 (MT q + m) + ln][t = 32 c + 8 lq ..]
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        kf[m][c] = *(const bf16x8*)(s.kb + swz64(16 * (MT * q + m) + ln, lq + 4 * c));
 #pragma unroll
     for (int le = 0; le < LPG; ++le) {
       const int e = e0 + le;
@@ -599,8 +620,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           floatx4 x = st[le][m][n];
 #pragma unroll
           for (int i = 0; i < 4; ++i) x[i] *= gk;
-          x = mfma16x16x32(__builtin_bit_cast(bf16x8, kf[m][0]), b0, x);
-          x = mfma16x16x32(__builtin_bit_cast(bf16x8, kf[m][1]), b1, x);
+          x = mfma16x16x32(kf[m][0], b0, x);
+          x = mfma16x16x32(kf[m][1], b1, x);
           st[le][m][n] = x;
         }
       }

@@ -134,8 +134,9 @@ constexpr int kCohStore = 16;  // sc1
 // writes Sum(p) into out (row-major [K][V] with row stride V, this block's 64
 // columns) and returns D_p (on every thread).  COH: the stores carry kCohStore.
 // LAYER: v is the layer's x and g comes from dt (v = x dt', g = A dt', see
-// layer_math.h); bf16 x only.
-template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false>
+// layer_math.h); bf16 x only.  NSLOT: chunks held in registers ahead of the
+// one being multiplied (the loads in flight per workgroup).
+template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false, int NSLOT = 2>
 __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restrict__ k,
                                               const TV* __restrict__ v,
                                               const float* __restrict__ g, float* __restrict__ out,
@@ -152,7 +153,11 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   const int kstr = G * kKD, vstr = H * V;
   const rsrc_t rk = make_rsrc(k + ((size_t)b * T * G + gq) * kKD, (size_t)T * kstr * sizeof(TK));
   const rsrc_t rv = make_rsrc(v + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TV));
-  const rsrc_t rgg = make_rsrc(g + (size_t)b * T * H + h, (size_t)T * H * 4);
+  // g (or, in layer mode, its dt words) is used by wave 0 only: the other waves
+  // issue the same load through an empty range, which returns zeros without a
+  // memory request.  Every load of the pass is unconditional, so the compiler
+  // can count the loads in flight and wait for one chunk's data only.
+  const rsrc_t rgg = make_rsrc(g + (size_t)b * T * H + h, w == 0 ? (size_t)T * H * 4 : 0);
   const unsigned int vo_k = tile64_voff<TK>(kstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
   // layer mode: dt words of the wave-0 lane's row (g) and of the thread's two
@@ -160,6 +165,8 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   const int desz = la.dt_f32 ? 4 : 2;
   const rsrc_t rdt = make_rsrc(LAYER ? (const char*)la.dt + (size_t)b * T * H * desz : (const char*)g,
                                LAYER ? (size_t)T * H * desz : 0);
+  const rsrc_t rdt0 = make_rsrc(LAYER ? (const char*)la.dt + (size_t)b * T * H * desz : (const char*)g,
+                                LAYER && w == 0 ? (size_t)T * H * desz : 0);
   const float Ah = LAYER ? la.A[h] : 0.f, bh = LAYER && la.bias ? la.bias[h] : 0.f;
   const unsigned int el_g = (unsigned int)(lane * H + h), el_v = (unsigned int)((tid >> 3) * H + h);
 
@@ -168,33 +175,36 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   for (int n = 0; n < 4; ++n) acc[n] = zero4();
   float dsum = 0.f;
 
-  Tile64<TK> kr[2];
-  Tile64<TV> vr[2];
-  float gr[2] = {0.f, 0.f};
-  unsigned int dw[2][2] = {{0u, 0u}, {0u, 0u}};   // layer: dt words of the V rows
-  auto seg_load = [&](int jj, int slot) {   // chunk jj of the segment -> register slot
-    if (jj >= nch) return;
-    const unsigned int row0 = (unsigned int)(c0 + jj) * kBT;
+  static_assert(NSLOT == 2 || NSLOT == 4, "register slots");
+  Tile64<TK> kr[NSLOT];
+  Tile64<TV> vr[NSLOT];
+  float gr[NSLOT];
+  unsigned int dw[NSLOT][2];   // layer: dt words of the V rows
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < NSLOT; ++s) gr[s] = 0.f, dw[s][0] = dw[s][1] = 0u;
+  auto seg_load = [&](int jj, int slot) {   // chunk jj of the segment -> register slot
+    // past the segment's end the last chunk is loaded again (unused)
+    const unsigned int row0 = (unsigned int)(c0 + min(jj, nch - 1)) * kBT;
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s)
       if (s == slot) {
         load_tile64(kr[s], rk, vo_k, row0 * kstr * sizeof(TK), kstr);
         load_tile64(vr[s], rv, vo_v, row0 * vstr * sizeof(TV), vstr);
         if constexpr (LAYER) {
           const unsigned int e0 = row0 * H;   // even: the bf16 half of an element is its own parity
-          if (w == 0) gr[s] = buf_load<float>(rdt, ((e0 + el_g) * desz) & ~3u, 0);
+          gr[s] = buf_load<float>(rdt0, ((e0 + el_g) * desz) & ~3u, 0);
 #pragma unroll
           for (int r = 0; r < 2; ++r)
             dw[s][r] = __builtin_bit_cast(unsigned int, buf_load<float>(
                 rdt, ((e0 + el_v + 32u * r * H) * desz) & ~3u, 0));
-        } else if (w == 0) {
+        } else {
           gr[s] = buf_load<float>(rgg, vo_g, row0 * H * 4);
         }
       }
   };
   auto seg_store = [&](int slot, int buf) {   // register slot -> LDS buffer
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < NSLOT; ++s)
       if (s == slot) {
         store_tile64<NP>(kr[s], sm.k[buf][0], sm.k[buf][NP - 1]);
         if constexpr (LAYER) {
@@ -225,56 +235,62 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
         }
       }
   };
-  // chunk j is multiplied from LDS buffer j & 1; chunks j + 1, j + 2 wait in
-  // register slots (j + 1) & 1, j & 1
-  seg_load(0, 0);
-  seg_load(1, 1);
+  // chunk j is multiplied from LDS buffer j & 1; chunks j + 1 .. j + NSLOT
+  // wait in register slot (chunk index) % NSLOT
+#pragma unroll
+  for (int s = 0; s < NSLOT; ++s) seg_load(s, s);
   seg_store(0, 0);
-  seg_load(2, 0);
+  seg_load(NSLOT, 0);
   __syncthreads();
   auto step = [&](int j, int buf, int slot_next) {
-    const float clast = sm.cl[buf];
-    const float dl = fexp(clast);
-    dsum += clast;
+    if (j < nch) {
+      const float clast = sm.cl[buf];
+      const float dl = fexp(clast);
+      dsum += clast;
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[n][i] *= dl;
+        for (int i = 0; i < 4; ++i) acc[n][i] *= dl;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      // A: (K^T diag(w))[k = 16w + ln][s = 32c + 8lq + jj], NP planes
-      const floatx4 w0 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq]);
-      const floatx4 w1 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq + 4]);
-      float ka[8];
-      {
-        const bf16x8 kh = tr_frag(sm.k[buf][0], kLd, 32 * c, 16 * w);
-        bf16x8 kl{};
-        if constexpr (NP == 2) kl = tr_frag(sm.k[buf][1], kLd, 32 * c, 16 * w);
+      for (int c = 0; c < 2; ++c) {
+        // A: (K^T diag(w))[k = 16w + ln][s = 32c + 8lq + jj], NP planes
+        const floatx4 w0 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq]);
+        const floatx4 w1 = *(const floatx4*)(&sm.wt[buf][32 * c + 8 * lq + 4]);
+        float ka[8];
+        {
+          const bf16x8 kh = tr_frag(sm.k[buf][0], kLd, 32 * c, 16 * w);
+          bf16x8 kl{};
+          if constexpr (NP == 2) kl = tr_frag(sm.k[buf][1], kLd, 32 * c, 16 * w);
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float x = NP == 2 ? (float)kh[jj] + (float)kl[jj] : (float)kh[jj];
-          ka[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
+          for (int jj = 0; jj < 8; ++jj) {
+            const float x = NP == 2 ? (float)kh[jj] + (float)kl[jj] : (float)kh[jj];
+            ka[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
+          }
+        }
+        bf16x8 a[NP];
+        split8<NP>(ka, a);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          bf16x8 bv[NP];   // V[s][v = 16n + ln]
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) bv[pl] = tr_frag(sm.v[buf][pl], kLd, 32 * c, 16 * n);
+          acc[n] = mma<NP>(a, bv, acc[n]);
         }
       }
-      bf16x8 a[NP];
-      split8<NP>(ka, a);
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        bf16x8 bv[NP];   // V[s][v = 16n + ln]
-#pragma unroll
-        for (int pl = 0; pl < NP; ++pl) bv[pl] = tr_frag(sm.v[buf][pl], kLd, 32 * c, 16 * n);
-        acc[n] = mma<NP>(a, bv, acc[n]);
-      }
     }
-    if (j + 1 < nch) {
-      seg_store(slot_next, buf ^ 1);
-      seg_load(j + 3, slot_next);
-    }
+    // the next chunk -> LDS and a later one -> registers, also past the
+    // segment's end (then unused), so the loads do not depend on a branch
+    seg_store(slot_next, buf ^ 1);
+    seg_load(j + 1 + NSLOT, slot_next);
     __syncthreads();
   };
-  for (int j = 0; j < nch; j += 2) {
+  for (int j = 0; j < nch; j += NSLOT) {
     step(j, 0, 1);
-    if (j + 1 < nch) step(j + 1, 1, 0);
+    step(j + 1, 1, 2 % NSLOT);
+    if (NSLOT == 4) {
+      step(j + 2, 0, 3);
+      step(j + 3, 1, 0);
+    }
   }
   if constexpr (COH) {
     // relaxed device-scope atomic stores: plain stores with the sc1 bit.  (The

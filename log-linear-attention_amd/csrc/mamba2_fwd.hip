@@ -823,7 +823,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     if (p < NSEG - 1 || is_final_seg) {
       SumSmem<1>& ss = *(SumSmem<1>*)smem_raw;
       float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
-      const float dsum = seg_sum_body<__bf16, TV, false, 1, true, LAYER>(
+      const float dsum = seg_sum_body<__bf16, TV, false, 1, true, LAYER, 4>(
           ss, k, v, g, out, b, h, p, vblk, T, G, H, V, NT, 1 << slog, la);
       if (tid == 0)
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, dsum), rsd,

@@ -29,15 +29,14 @@
 // major), K_new transposed per chunk ([row][chunk][k][t], the scan's MFMA
 // operand layout), U, and P (bf16, [row][chunk][t][s]); the backward's
 // recompute also writes K_new token-major.
-// Kernel 2 (gdn_scan_kernel): one workgroup per (row, BV columns of V), eight
-// waves in two level groups.  Every level's [K x BV] state lives in fp32
-// registers (a group's levels, the wave's k-quarter).  Per chunk the states
-// are staged in LDS as bf16, each wave forms W_new h_e (-> V_new_e, LDS) and
-// q_new h_e (-> the level reads) of its group's levels for its 16-row t-tile,
-// group 0 adds o_intra = P V and writes o, and every wave updates its state
-// tiles with K_new^T V_new_e.  The next chunk's operands are loaded while the
-// current one computes.  The slices of one row run on one XCD, so the chunk
-// tiles they share are fetched into one L2.
+// Kernel 2 (gdn_scan_kernel): one workgroup per (row, BV columns of V), one
+// wave per inter-chunk level.  Each wave keeps its level's [K x BV] state in
+// fp32 registers and runs the level's recurrence on its own (the products take
+// the state and V_new as B operands straight from the accumulators, with the
+// A operands' contraction index permuted to match), so the waves meet only to
+// share the chunk's operands (staged in LDS from registers loaded during the
+// previous chunk) and to sum the level reads into o.  The slices of one row
+// run on one XCD, so the chunk tiles they share are fetched into one L2.
 #include "gdn_common.h"
 
 namespace hattn {
@@ -360,50 +359,55 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
 // ---------------------------------------------------------------------------
 template <int KD, int BV>
 struct GdnScanCfg {
-  static constexpr int NVT = BV / 16;                 // 16-column v-tiles
-  static constexpr int MT = KD / 64;                  // 16-row k-tiles of one k-quarter
-  static constexpr int NC = KD / 32;                  // MFMA steps of a contraction over K
-  static constexpr int LPG = kGMaxLev / 2;            // levels per level group
-  static constexpr int LK = KD + 8;                   // row stride of the staged states
-  static constexpr int LVS = BV + 8;                  // row stride of the staged V and U slices
-  static constexpr int KU = KD / 64;                  // 16-byte units of K_new^T per thread
+  static constexpr int NVT = BV / 16;   // 16-column v-tiles
+  static constexpr int NKT = KD / 16;   // 16-row k-tiles of the state
+  static constexpr int NC = KD / 32;    // MFMA steps of a contraction over K
+  static constexpr int LK = KD + 8;     // row stride of the staged W_new / q_new tiles
+  static constexpr int LT = kGC + 8;    // row stride of the staged K_new^T, U^T and P tiles
+  static constexpr int LVS = BV + 8;    // row stride of the staged V slice
+  static constexpr int LP = kGC + 4;    // row stride (floats) of the level-read partials
+  static constexpr int KU = KD / 64;    // 16-byte units per thread of a [64 x KD] or [KD x 64] tile
 };
 
 template <int KD, int BV>
 struct GdnScanSmem {
   using C = GdnScanCfg<KD, BV>;
-  __bf16 hs[kGMaxLev][BV * C::LK];    // states, bf16 [v][k]
-  __bf16 vn[kGMaxLev][BV * kLd64];    // V_new, bf16 [v][t]
-  __bf16 kb[KD * kGC];                // the chunk's K_new^T [k][t] (swz64)
-  __bf16 pm[kGC * kGC];               // the chunk's P [t][s] (swz64)
-  __bf16 vs[kGC * C::LVS];            // the chunk's V slice [t][v] (o_intra)
-  __bf16 us[kGC * C::LVS];            // the chunk's U slice [t][v] (V_new)
-  float lam[kGMaxLev][kGC];           // lambda[t, 7 + e], zero for e >= nlev
-  floatx4 xacc[4][C::NVT][64];        // level group 1's reads, summed into group 0's
+  __bf16 wq[2][kGC * C::LK];             // the chunk's W_new, q_new [t][k]
+  __bf16 kt[KD * C::LT];                 // K_new^T [k][t]
+  __bf16 ut[BV * C::LT];                 // U slice, transposed [v][t]
+  __bf16 pm[kGC * C::LT];                // P [t][s]
+  __bf16 vs[kGC * C::LVS];               // V slice [t][v]
+  float lam[kGMaxLev][kGC];              // lambda[t, 7 + e]
+  float part[kGMaxLev + 1][BV * C::LP];  // lambda_e o (q_new h_e) per level, o_intra last; [v][t]
 };
 
-// Element offset of 16-byte unit u of row r in a [rows][64] bf16 tile whose
-// units are XOR-permuted by the row: the 16-byte row-fragment reads of the
-// MFMA operands (16 rows, one unit each) hit distinct banks.
-__device__ __forceinline__ int swz64(int r, int u) { return r * 64 + ((u ^ r) & 7) * 8; }
+// A-operand fragment whose contraction index runs in the row order of two
+// stacked D tiles: lane (lq, ln) receives row r's elements c .. c + 3 and
+// c + 16 .. c + 19 (c = 32 step + 4 lq).  Paired with a B fragment built from
+// two D-layout accumulator quads (cat8), so states and V_new feed the next
+// product straight from registers.
+__device__ __forceinline__ bf16x8 frag_k2(const __bf16* X, int ld, int r, int c) {
+  const bf16x4 lo = *(const bf16x4*)(X + r * ld + c);
+  const bf16x4 hi = *(const bf16x4*)(X + r * ld + c + 16);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
 
-// Eight waves in two level groups: wave w runs levels 4 (w >> 2) .. +3 with
-// q = w & 3 as its t-tile (the products W_new h_e and q_new h_e, which share
-// each B fragment) and as its k-quarter (the state rows it holds and updates).
-// All levels of a group run every chunk without a branch per level, so the
-// compiler interleaves their LDS reads and MFMA chains; a level e >= nlev
-// never writes (its V_new is zero, so its state stays zero) and is never read
-// (lambda is zero for it, bit e of the chunk index is clear).
-// Operand pipeline: the loads of chunk ic + 1 are issued right after the
-// level products of chunk ic, small operands first, and land in LDS at the
-// start of chunk ic + 1 (K_new^T, read only by the state update, right after
-// the first barrier), so no wave waits for memory inside a chunk.  The K_new^T,
-// P, V and U tiles are loaded once per workgroup (one 16-byte unit per thread
-// and tile) instead of once per wave.
+// One wave per inter-chunk level: wave e holds level e's whole [K x BV] state
+// in fp32 registers (tile (kt, nt) holds rows 16 kt + 4 lq + i, columns
+// 16 nt + ln) and runs its recurrence on its own,
+//   R   = q_new h_e                         (chunks with bit e set: the level read)
+//   V_new = (write ? U : 0) - W_new h_e     (not on the chunk that resets the level)
+//   h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new,
+// skipping the products of a zero state (the first chunk of a block) and of a
+// chunk whose result the reset discards; a level e >= nlev does nothing.
+// Wave 0 also forms o_intra = P V.  Per chunk the waves meet twice: the first
+// barrier publishes the chunk's operands (staged in LDS from registers loaded
+// during the previous chunk), the second the level reads, which every thread
+// then sums for four outputs and stores.
 // HSAVE (the backward's recompute): every level's state at every chunk start
-// is written to hsave, bf16 [row][chunk][level][v][k]; then o may be null and
-// pm any valid pointer.  A separate instantiation, so the forward carries no
-// registers for it.
+// is written to hsave, bf16 [row][chunk][level][v][k]; no output (o, q_new,
+// P and the V slice are not read).  A separate instantiation, so the forward
+// carries no registers for it.
 template <int KD, int BV, typename TL, typename TO, bool HSAVE>
 __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ knT,
@@ -415,8 +419,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   using Sm = GdnScanSmem<KD, BV>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
-  constexpr int LK = C::LK, LVS = C::LVS, NVT = C::NVT, MT = C::MT, NC = C::NC, LPG = C::LPG;
-  constexpr int KU = C::KU;
+  constexpr int NVT = C::NVT, NKT = C::NKT, NC = C::NC, LK = C::LK, LT = C::LT, LVS = C::LVS;
+  constexpr int LP = C::LP, KU = C::KU;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   const int nvb = V / BV;
@@ -426,38 +430,40 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   const int b = row / H, h = row % H;
   const int NT = T / kGC;
   const size_t rowtok = (size_t)b * T * H + h;   // (token 0 of the row) * H + h
-  const int lg = w >> 2, q = w & 3, e0 = LPG * lg;
+  const int e = w;                               // this wave's level
+  const bool act = e < nlev;
 
-  // states: level e0 + le, rows k = 16 (MT q + m) + 4 lq + i, columns v = 16 n + ln
-  floatx4 st[LPG][MT][NVT];
+  floatx4 st[NKT][NVT];
 #pragma unroll
-  for (int le = 0; le < LPG; ++le)
+  for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int n = 0; n < NVT; ++n) st[le][m][n] = zero4();
+    for (int nt = 0; nt < NVT; ++nt) st[kt][nt] = zero4();
   for (int i = tid; i < kGMaxLev * kGC; i += 512) s.lam[i / kGC][i % kGC] = 0.f;
 
-  // Operand loads: a uniform per-row base plus a 32-bit lane offset, advanced
-  // by a uniform per-chunk offset.  Every load is unconditional, so the
-  // compiler does not wait for it at a branch.
+  // ---- staging loads: one 16-byte unit per thread and tile row piece; every
+  //      load is unconditional (threads past a tile repeat its last unit and
+  //      do not store it), so the compiler can count the loads in flight
   const unsigned HV = (unsigned)H * V, HK = (unsigned)H * KD, HL = (unsigned)H * L;
-  const __bf16* qrow = qn + rowtok * KD;
   const __bf16* wrow = wn + rowtok * KD;
-  const unsigned a_off = (16 * q + ln) * HK + 8 * lq;
+  const __bf16* qrow = qn + rowtok * KD;
   const __bf16* knrow = knT + (size_t)row * NT * KD * kGC;
   const __bf16* pmrow = pm + (size_t)row * NT * kGC * kGC;
-  const unsigned u_off = (16 * q + 4 * lq) * HV + ln;   // o[t = 16q + 4lq + i][v = 16n + ln]
-  // V slice (threads 0 .. 8 BV - 1) and U slice (8 BV .. 16 BV - 1): one
-  // 16-byte unit of the [64 x BV] tile each; threads past 16 BV repeat the
-  // last unit and do not store it
+  unsigned wq_off[KU];   // element offset of unit tid + 512 r of a [64 x KD] token-major tile
+  int wq_lds[KU];
+#pragma unroll
+  for (int r = 0; r < KU; ++r) {
+    const int u = tid + 512 * r, t = u / (KD / 8), ku = u % (KD / 8);
+    wq_off[r] = t * HK + 8 * ku;
+    wq_lds[r] = t * LK + 8 * ku;
+  }
+  // V slice (threads 0 .. 8 BV - 1) and U slice (8 BV .. 16 BV - 1)
   const bool s_store = tid < 16 * BV;
   const int su = s_store ? tid : 16 * BV - 1;
   const bool is_u = su >= 8 * BV;
   const int vu = is_u ? su - 8 * BV : su;
+  const int s_t = vu / (BV / 8), s_v = 8 * (vu % (BV / 8));
   const __bf16* sbase = (is_u ? un : vin) + rowtok * V + v0;
-  const unsigned s_off = (vu / (BV / 8)) * HV + 8 * (vu % (BV / 8));
-  __bf16* sdst = (is_u ? s.us : s.vs) + (vu / (BV / 8)) * LVS + 8 * (vu % (BV / 8));
+  const unsigned s_off = s_t * HV + s_v;
   const int nl1 = nlev > 0 ? nlev : 1;   // T = 64 has no inter-chunk level
   const int e2 = min(tid, nl1 * kGC - 1);
   const TL* lrow = l + rowtok * L;
@@ -465,184 +471,225 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   // Gc_last through a buffer (vector-memory) load: a scalar load would share the
   // LDS wait counter and stall every LDS wait until it returns
   const rsrc_t grs = make_rsrc(gcum + rowtok + (size_t)(kGC - 1) * H, (size_t)T * H * 4);
-  __bf16* hrow = HSAVE ? hsave + (size_t)row * NT * nlev * V * KD + (size_t)v0 * KD : nullptr;
-  const unsigned h_off = ln * KD + 16 * MT * q + 4 * lq;
 
-  u32x4 aq[NC], aw[NC], kfn[KU], pvu, pp1;
-  TL plr;
-  float pgl;
-  auto load_a = [&](int jc) __attribute__((always_inline)) {
-    const size_t off = (size_t)jc * kGC * HK;
+  u32x4 rw[KU], rq[KU], rk[KU], rsv, rp;
+  TL rl;
+  float rg;
+  auto stage_load = [&](int jc) __attribute__((always_inline)) {
+    const size_t tokoff = (size_t)jc * kGC * H;   // chunk jc's first token, times H
+    rsv = *(const u32x4*)(sbase + tokoff * V + s_off);
+    rl = lrow[tokoff * L + l_off];
+    rg = buf_load<float>(grs, 0, (unsigned)(tokoff * 4));
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      aq[c] = *(const u32x4*)(qrow + off + a_off + 32 * c);
-      aw[c] = *(const u32x4*)(wrow + off + a_off + 32 * c);
+    for (int r = 0; r < KU; ++r)
+      rk[r] = *(const u32x4*)(knrow + (size_t)jc * KD * kGC + 8 * (tid + 512 * r));
+#pragma unroll
+    for (int r = 0; r < KU; ++r) rw[r] = *(const u32x4*)(wrow + tokoff * KD + wq_off[r]);
+    if constexpr (!HSAVE) {
+      rp = *(const u32x4*)(pmrow + (size_t)jc * kGC * kGC + 8 * tid);
+#pragma unroll
+      for (int r = 0; r < KU; ++r) rq[r] = *(const u32x4*)(qrow + tokoff * KD + wq_off[r]);
     }
   };
-  auto load_k = [&](int jc) __attribute__((always_inline)) {
-    const __bf16* base = knrow + (size_t)jc * KD * kGC;
+  auto stage_store = [&]() __attribute__((always_inline)) {
+    if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = to_f32<TL>(rl);
+    if (s_store) {
+      if (is_u) {
+        const bf16x8 x = __builtin_bit_cast(bf16x8, rsv);
 #pragma unroll
-    for (int r = 0; r < KU; ++r) kfn[r] = *(const u32x4*)(base + 8 * (tid + 512 * r));
-  };
-  auto fetch_small = [&](int jc) __attribute__((always_inline)) {
-    const size_t tokoff = (size_t)jc * kGC * H;   // chunk jc's first token, times H
-    pvu = *(const u32x4*)(sbase + tokoff * V + s_off);
-    if constexpr (!HSAVE) pp1 = *(const u32x4*)(pmrow + (size_t)jc * kGC * kGC + 8 * tid);
-    plr = lrow[tokoff * L + l_off];
-    pgl = buf_load<float>(grs, 0, (unsigned)(tokoff * 4));
-  };
-  fetch_small(0);
-  load_k(0);
-  load_a(0);
-
-  for (int ic = 0; ic < NT; ++ic) {
-    const int icn = min(ic + 1, NT - 1);
-    const float glast = pgl;
-    // states -> LDS (bf16 [v][k]) and, with hsave, to hsave[row][chunk][level][v][k]
-#pragma unroll
-    for (int le = 0; le < LPG; ++le)
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int n = 0; n < NVT; ++n) {
-          const bf16x4 h4 = cvt4(st[le][m][n]);
-          const int kk = 16 * (MT * q + m) + 4 * lq, vv = 16 * n + ln;
-          *(bf16x4*)(s.hs[e0 + le] + vv * LK + kk) = h4;
-          if (HSAVE && e0 + le < nlev)
-            *(bf16x4*)(hrow + ((size_t)ic * nlev + e0 + le) * V * KD + h_off + (16 * n * KD + 16 * m)) = h4;
-        }
-    // the chunk's lambda, V and U slices and P -> LDS
-    if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = to_f32<TL>(plr);
-    if (s_store) *(u32x4*)sdst = pvu;
-    if constexpr (!HSAVE) *(u32x4*)(s.pm + swz64(tid >> 3, tid & 7)) = pp1;
-    __syncthreads();
-    // the chunk's K_new^T -> LDS: every wave is past the previous chunk's state
-    // update, and the second barrier orders these stores before this chunk's
+        for (int j = 0; j < 8; ++j) s.ut[(s_v + j) * LT + s_t] = x[j];
+      } else {
+        *(u32x4*)(s.vs + s_t * LVS + s_v) = rsv;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < KU; ++r) {
       const int u = tid + 512 * r;
-      *(u32x4*)(s.kb + swz64(u >> 3, u & 7)) = kfn[r];
+      *(u32x4*)(s.kt + (u >> 3) * LT + 8 * (u & 7)) = rk[r];
+      *(u32x4*)(s.wq[0] + wq_lds[r]) = rw[r];
     }
+    if constexpr (!HSAVE) {
+      *(u32x4*)(s.pm + (tid >> 3) * LT + 8 * (tid & 7)) = rp;
+#pragma unroll
+      for (int r = 0; r < KU; ++r) *(u32x4*)(s.wq[1] + wq_lds[r]) = rq[r];
+    }
+  };
 
-    // ---- V_new_e = (write ? U : 0) - (reset ? 0 : W_new h_e) -> LDS, and the reads
-    //      lambda_e o (q_new h_e) of the levels with bit e of ic set.  The level's
-    //      flags enter as 0 / 1 factors.
+  // outputs: thread -> token row ot of the chunk and columns ov .. ov + 3 of the
+  // slice (threads past the 64 x BV tile store through an empty range)
+  constexpr int VG = BV / 4;
+  const int ot = tid / VG, ov = 4 * (tid % VG);
+  const bool o_ok = !HSAVE && o != nullptr && ot < kGC;
+  const rsrc_t ro = make_rsrc(o_ok ? (const void*)(o + rowtok * V + v0) : (const void*)gcum,
+                              o_ok ? (size_t)T * H * V * sizeof(TO) : 0);
+  const unsigned o_voff = ((o_ok ? ot : 0) * HV + ov) * sizeof(TO);
+  // hsave: this level's planes (an empty range for the waves without a level)
+  const rsrc_t rh = make_rsrc(HSAVE ? (const void*)(hsave + (size_t)row * NT * nlev * V * KD +
+                                                    (size_t)(act ? e : 0) * V * KD + (size_t)v0 * KD)
+                                    : (const void*)gcum,
+                              HSAVE && act ? (size_t)NT * nlev * V * KD * 2 : 0);
+
+  stage_load(0);
+  stage_store();
+  __syncthreads();
+
+  for (int ic = 0; ic < NT; ++ic) {
+    const float gl = fexp(rg);   // exp(Gc_last) of chunk ic
     const bool last = ic == NT - 1;
-    float uu[NVT][4];
+    // chunk ic + 1's operands, into registers while this chunk computes
+    stage_load(min(ic + 1, NT - 1));
+
+    const int per = 2 << e, pos = ic & (per - 1);
+    const bool rd = act && ((ic >> e) & 1);
+    const bool first = act && pos == 0;
+    const bool reset = act && pos == per - 1 && !(last && final_state);
+    const bool wr = act && !rd;
+    const bool needy = act && !first && !reset;
+
+    if constexpr (HSAVE) {
+      // level e's state at the chunk start -> hsave[row][ic][e][v][k]
 #pragma unroll
-    for (int n = 0; n < NVT; ++n)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) uu[n][i] = (float)s.us[(16 * q + 4 * lq + i) * LVS + 16 * n + ln];
-    floatx4 acc[NVT];
+        for (int nt = 0; nt < NVT; ++nt)
+          buf_store8(__builtin_bit_cast(uint2, cvt4(st[kt][nt])), rh,
+                     (unsigned)(((16 * nt + ln) * KD + 16 * kt + 4 * lq) * 2),
+                     (unsigned)((size_t)ic * nlev * V * KD * 2));
+    } else {
+      if (rd) {
+        // the level read lambda[t, 7 + e] (q_new h_e)[t][v] -> part[e]
+        floatx4 racc[4][NVT];
 #pragma unroll
-    for (int n = 0; n < NVT; ++n) acc[n] = zero4();
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-    for (int le = 0; le < LPG; ++le) {
-      const int e = e0 + le;
-      const int per = 2 << e;
-      const bool rd = (ic >> e) & 1;
-      const float frd = rd ? 1.f : 0.f;
-      const float fwr = (e < nlev && !rd) ? 1.f : 0.f;
-      const float fkeep = (((ic & (per - 1)) == per - 1) && !(last && final_state)) ? 0.f : 1.f;
-      const floatx4 lam4 = *(const floatx4*)(&s.lam[e][16 * q + 4 * lq]);
-#pragma unroll
-      for (int n = 0; n < NVT; ++n) {
-        floatx4 y = zero4(), z = zero4();
+          for (int nt = 0; nt < NVT; ++nt) racc[tt][nt] = zero4();
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const bf16x8 bh = *(const bf16x8*)(s.hs[e] + (16 * n + ln) * LK + 32 * c + 8 * lq);
-          y = mfma16x16x32(__builtin_bit_cast(bf16x8, aw[c]), bh, y);
-          z = mfma16x16x32(__builtin_bit_cast(bf16x8, aq[c]), bh, z);
-        }
-        bf16x4 vb4;
+          bf16x8 bh[NVT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vb4[i] = (__bf16)(fwr * uu[n][i] - fkeep * y[i]);
-          acc[n][i] += frd * lam4[i] * z[i];
+          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8(st[2 * c][nt], st[2 * c + 1][nt]);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const bf16x8 a = frag_k2(s.wq[1], LK, 16 * tt + ln, 32 * c + 4 * lq);
+#pragma unroll
+            for (int nt = 0; nt < NVT; ++nt) racc[tt][nt] = mfma16x16x32(a, bh[nt], racc[tt][nt]);
+          }
         }
-        *(bf16x4*)(s.vn[e] + (16 * n + ln) * kLd64 + 16 * q + 4 * lq) = vb4;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const floatx4 lam4 = *(const floatx4*)(&s.lam[e][16 * tt + 4 * lq]);
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt)
+            *(floatx4*)(&s.part[e][(16 * nt + ln) * LP + 16 * tt + 4 * lq]) = racc[tt][nt] * lam4;
+        }
       }
-      // bound the scheduler's hoisting of the next level's LDS reads (register
-      // pressure)
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // chunk ic + 1's operands: the ones needed first are issued first (the
-    // wait counter is in order)
-    fetch_small(icn);
-    load_k(icn);
-    load_a(icn);
-    if (lg == 1) {
+      if (w == 0) {
+        // o_intra = P V -> part[kGMaxLev]
 #pragma unroll
-      for (int n = 0; n < NVT; ++n) s.xacc[q][n][lane] = acc[n];
-    } else if (o != nullptr) {
-      // o_intra = P V
+        for (int tt = 0; tt < 4; ++tt) {
+          floatx4 x[NVT];
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt) x[nt] = zero4();
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const bf16x8 a = *(const bf16x8*)(s.pm + (16 * tt + ln) * LT + 32 * c + 8 * lq);
+#pragma unroll
+            for (int nt = 0; nt < NVT; ++nt)
+              x[nt] = mfma16x16x32(a, tr_frag(s.vs, LVS, 32 * c, 16 * nt), x[nt]);
+          }
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt)
+            *(floatx4*)(&s.part[kGMaxLev][(16 * nt + ln) * LP + 16 * tt + 4 * lq]) = x[nt];
+        }
+      }
+    }
+
+    if (reset) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < NVT; ++nt) st[kt][nt] = zero4();
+    } else if (act) {
+      // V_new[t = 16 tt + 4 lq + i][v = 16 nt + ln] = (write ? U : 0) - W_new h_e
+      floatx4 vn[4][NVT];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int nt = 0; nt < NVT; ++nt) vn[tt][nt] = zero4();
+      if (needy) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          bf16x8 bh[NVT];
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8(st[2 * c][nt], st[2 * c + 1][nt]);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const bf16x8 a = frag_k2(s.wq[0], LK, 16 * tt + ln, 32 * c + 4 * lq);
+#pragma unroll
+            for (int nt = 0; nt < NVT; ++nt) vn[tt][nt] = mfma16x16x32(a, bh[nt], vn[tt][nt]);
+          }
+        }
+      }
+      if (wr) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt) {
+            const bf16x4 u4 = *(const bf16x4*)(s.ut + (16 * nt + ln) * LT + 16 * tt + 4 * lq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vn[tt][nt][i] = (float)u4[i] - vn[tt][nt][i];
+          }
+      } else {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int nt = 0; nt < NVT; ++nt) vn[tt][nt] = -vn[tt][nt];
+      }
+      // h_e = exp(Gc_last) h_e + K_new^T V_new (the state is zero on a block's first chunk)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int nt = 0; nt < NVT; ++nt) st[kt][nt] *= gl;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const bf16x8 pf = *(const bf16x8*)(s.pm + swz64(16 * q + ln, lq + 4 * c));
+        bf16x8 bv[NVT];
 #pragma unroll
-        for (int n = 0; n < NVT; ++n)
-          acc[n] = mfma16x16x32(pf, tr_frag(s.vs, LVS, 32 * c, 16 * n), acc[n]);
-      }
-    }
-    __syncthreads();
-
-    // ---- group 0: o = o_intra + reads of both groups --------------------------------
-    if (lg == 0 && o != nullptr) {
-      TO* ob = o + (rowtok + (size_t)ic * kGC * H) * V + v0;
+        for (int nt = 0; nt < NVT; ++nt) bv[nt] = cat8(vn[2 * c][nt], vn[2 * c + 1][nt]);
 #pragma unroll
-      for (int n = 0; n < NVT; ++n) {
-        const floatx4 x = acc[n] + s.xacc[q][n][lane];
+        for (int kt = 0; kt < NKT; ++kt) {
+          const bf16x8 a = frag_k2(s.kt, LT, 16 * kt + ln, 32 * c + 4 * lq);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ob[u_off + i * HV + 16 * n] = from_f32<TO>(x[i]);
-      }
-    }
-
-    // ---- h_e = (reset ? 0 : exp(Gc_last) h_e) + K_new^T V_new_e -----------------------
-    const float gl = fexp(glast);
-    bf16x8 kf[MT][2];   // K_new^T[k = 16 (MT q + m) + ln][t = 32 c + 8 lq ..]
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-        kf[m][c] = *(const bf16x8*)(s.kb + swz64(16 * (MT * q + m) + ln, lq + 4 * c));
-#pragma unroll
-    for (int le = 0; le < LPG; ++le) {
-      const int e = e0 + le;
-      const int per = 2 << e;
-      const bool reset = ((ic & (per - 1)) == per - 1) && !(last && final_state);
-      const float gk = reset ? 0.f : gl;
-#pragma unroll
-      for (int n = 0; n < NVT; ++n) {
-        const bf16x8 b0 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 8 * lq);
-        const bf16x8 b1 = *(const bf16x8*)(s.vn[e] + (16 * n + ln) * kLd64 + 32 + 8 * lq);
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          floatx4 x = st[le][m][n];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] *= gk;
-          x = mfma16x16x32(kf[m][0], b0, x);
-          x = mfma16x16x32(kf[m][1], b1, x);
-          st[le][m][n] = x;
+          for (int nt = 0; nt < NVT; ++nt) st[kt][nt] = mfma16x16x32(a, bv[nt], st[kt][nt]);
         }
       }
-      if (le & 1) __builtin_amdgcn_sched_barrier(0);
     }
+    __syncthreads();   // the chunk's operands are consumed, its level reads written
+
+    stage_store();     // chunk ic + 1
+    if constexpr (!HSAVE) {
+      // o = o_intra + the reads of the levels with bit e of ic set
+      floatx4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = s.part[kGMaxLev][(ov + j) * LP + (ot & (kGC - 1))];
+      for (int le = 0; le < nlev; ++le)
+        if ((ic >> le) & 1)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[j] += s.part[le][(ov + j) * LP + (ot & (kGC - 1))];
+      buf_store4<TO>(x, ro, o_voff, (unsigned)((size_t)ic * kGC * HV * sizeof(TO)));
+    }
+    __syncthreads();   // chunk ic + 1 staged; the level reads are summed
   }
-  if (final_state && ht != nullptr) {
+  if (final_state && ht != nullptr && act) {
     // ht[b, h, k, v, 7 + e] (chunkwise_hgdn.py:786-787)
-    float* hb = ht + (size_t)row * KD * V * L + v0 * L + 7 + e0;
-    const unsigned VL = (unsigned)V * L;
-    const unsigned t_off = (16 * MT * q + 4 * lq) * VL + ln * L;
+    float* hb = ht + (size_t)row * KD * V * L + (size_t)v0 * L + 7 + e;
+    const size_t VL = (size_t)V * L;
 #pragma unroll
-    for (int le = 0; le < LPG; ++le)
-      if (e0 + le < nlev)
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+      for (int nt = 0; nt < NVT; ++nt)
 #pragma unroll
-          for (int n = 0; n < NVT; ++n)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              hb[t_off + (16 * m + i) * VL + 16 * n * L + le] = st[le][m][n][i];
+        for (int i = 0; i < 4; ++i)
+          hb[(size_t)(16 * kt + 4 * lq + i) * VL + (16 * nt + ln) * L] = st[kt][nt][i];
   }
 }
 

@@ -365,7 +365,9 @@ struct GdnScanCfg {
   static constexpr int LK = KD + 8;     // row stride of the staged W_new / q_new tiles
   static constexpr int LT = kGC + 8;    // row stride of the staged K_new^T, U^T and P tiles
   static constexpr int LVS = BV + 8;    // row stride of the staged V slice
-  static constexpr int LP = kGC + 4;    // row stride (floats) of the level-read partials
+  // row stride (floats) of the level-read partials (unpadded at K = 256, which
+  // needs the LDS for its operand tiles)
+  static constexpr int LP = KD >= 256 ? BV : BV + 4;
   static constexpr int KU = KD / 64;    // 16-byte units per thread of a [64 x KD] or [KD x 64] tile
 };
 
@@ -378,7 +380,7 @@ struct GdnScanSmem {
   __bf16 pm[kGC * C::LT];                // P [t][s]
   __bf16 vs[kGC * C::LVS];               // V slice [t][v]
   float lam[kGMaxLev][kGC];              // lambda[t, 7 + e]
-  float part[kGMaxLev + 1][BV * C::LP];  // lambda_e o (q_new h_e) per level, o_intra last; [v][t]
+  float part[kGMaxLev + 1][kGC * C::LP]; // lambda_e o (q_new h_e) per level, o_intra last; [t][v]
 };
 
 // A-operand fragment whose contraction index runs in the row order of two
@@ -536,8 +538,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   for (int ic = 0; ic < NT; ++ic) {
     const float gl = fexp(rg);   // exp(Gc_last) of chunk ic
     const bool last = ic == NT - 1;
-    // chunk ic + 1's operands, into registers while this chunk computes
-    stage_load(min(ic + 1, NT - 1));
 
     const int per = 2 << e, pos = ic & (per - 1);
     const bool rd = act && ((ic >> e) & 1);
@@ -580,7 +580,9 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           const floatx4 lam4 = *(const floatx4*)(&s.lam[e][16 * tt + 4 * lq]);
 #pragma unroll
           for (int nt = 0; nt < NVT; ++nt)
-            *(floatx4*)(&s.part[e][(16 * nt + ln) * LP + 16 * tt + 4 * lq]) = racc[tt][nt] * lam4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              s.part[e][(16 * tt + 4 * lq + i) * LP + 16 * nt + ln] = racc[tt][nt][i] * lam4[i];
         }
       }
       if (w == 0) {
@@ -599,10 +601,13 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           }
 #pragma unroll
           for (int nt = 0; nt < NVT; ++nt)
-            *(floatx4*)(&s.part[kGMaxLev][(16 * nt + ln) * LP + 16 * tt + 4 * lq]) = x[nt];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s.part[kGMaxLev][(16 * tt + 4 * lq + i) * LP + 16 * nt + ln] = x[nt][i];
         }
       }
     }
+    // chunk ic + 1's operands, into registers while this chunk's state update runs
+    stage_load(min(ic + 1, NT - 1));
 
     if (reset) {
 #pragma unroll
@@ -668,13 +673,10 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     stage_store();     // chunk ic + 1
     if constexpr (!HSAVE) {
       // o = o_intra + the reads of the levels with bit e of ic set
-      floatx4 x;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = s.part[kGMaxLev][(ov + j) * LP + (ot & (kGC - 1))];
+      const int po = (ot & (kGC - 1)) * LP + ov;
+      floatx4 x = *(const floatx4*)(&s.part[kGMaxLev][po]);
       for (int le = 0; le < nlev; ++le)
-        if ((ic >> le) & 1)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) x[j] += s.part[le][(ov + j) * LP + (ot & (kGC - 1))];
+        if ((ic >> le) & 1) x += *(const floatx4*)(&s.part[le][po]);
       buf_store4<TO>(x, ro, o_voff, (unsigned)((size_t)ic * kGC * HV * sizeof(TO)));
     }
     __syncthreads();   // chunk ic + 1 staged; the level reads are summed

@@ -738,7 +738,9 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     {
       const int t = tid >> 2, part = tid & 3;
       const int mt = t >> 4;
-      const unsigned int so = ((unsigned int)ic * kBT + t) * H * L * 4;
+      // per-lane part of the offsets in the VGPR operand, the chunk's in the SGPR
+      // one (a lane-dependent scalar offset makes the compiler loop over lanes)
+      const unsigned int vo = (unsigned int)t * H * L * 4, so = (unsigned int)ic * kBT * H * L * 4;
       float qdq = 0.f;
       for (int col = part; col < L; col += 4) {
         float val = 0.f;
@@ -758,11 +760,11 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           val = raw * s.eg[t];
         }
         if (col <= 6) qdq += val * s.lam[col * kBT + t];
-        buf_store<float>(val, rdl, col * 4, so);
+        buf_store<float>(val, rdl, vo + col * 4, so);
       }
       qdq += __shfl_xor(qdq, 1, 64);
       qdq += __shfl_xor(qdq, 2, 64);
-      if (part == 0) buf_store<float>(qdq, rgq, 0, ((unsigned int)ic * kBT + t) * H * 4);
+      if (part == 0) buf_store<float>(qdq, rgq, (unsigned int)t * H * 4, (unsigned int)ic * kBT * H * 4);
     }
   }
 }
@@ -870,8 +872,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     if (ic - 1 >= c0) ld.load(rg, ic - 1);
     // q . dq of this chunk's tokens (written by the dq kernel), needed by wave 0 at
     // the end of the chunk: loaded now so the load has the whole chunk to land
-    const unsigned int so_g = ((unsigned int)ic * kBT + lane) * H * 4;
-    const float qdq = w == 0 ? buf_load<float>(rgq, 0, so_g) : 0.f;
+    const unsigned int vo_g = (unsigned int)lane * H * 4, so_g = (unsigned int)ic * kBT * H * 4;
+    const float qdq = w == 0 ? buf_load<float>(rgq, vo_g, so_g) : 0.f;
     __syncthreads();
 
     // ---- phase 1: (M o S) and (M o dP) tiles ---------------------------------------
@@ -1026,7 +1028,6 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
 
     // ---- dG = q . dq - k . dk and its reverse cumsum inside the segment --------------
     if (w == 0) {
-      const unsigned int so = so_g;
       // column sums over the t-tiles at or after this s-tile (the others are zero)
       float kdk = sm.dgk[lane][0] + sm.dgk[lane][1] + sm.dgk[lane][2] + sm.dgk[lane][3];
       for (int mt = lane >> 4; mt < 4; ++mt) kdk += sm.kdk[lane][mt];
@@ -1037,7 +1038,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         const float y = __shfl_down(x, d, 64);
         if (lane + d < 64) x += y;
       }
-      buf_store<float>(x + carry, rdg, 0, so);
+      buf_store<float>(x + carry, rdg, vo_g, so_g);
       carry += __shfl(x, 0, 64);
     }
   }

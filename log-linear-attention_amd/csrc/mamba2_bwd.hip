@@ -171,7 +171,7 @@ struct BwdLoader {
       stage_unit<NP, TV>(r.v[u], s.v, off);
     }
     const float x = r.g;                       // already the chunk-local cumsum
-    const float last = __shfl(x, 63, 64);
+    const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
     if (w == 0) {
       s.gc[lane] = x;
       s.wt[lane] = fexp(last - x);
@@ -762,8 +762,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
         if (col <= 6) qdq += val * s.lam[col * kBT + t];
         buf_store<float>(val, rdl, vo + col * 4, so);
       }
-      qdq += __shfl_xor(qdq, 1, 64);
-      qdq += __shfl_xor(qdq, 2, 64);
+      qdq = quad_sum(qdq);
       if (part == 0) buf_store<float>(qdq, rgq, (unsigned int)t * H * 4, (unsigned int)ic * kBT * H * 4);
     }
   }
@@ -894,11 +893,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             os[i] = m * S[i];
             op[i] = m * P[i];
             // k_s . dk_s (intra part) = column sum over t of (M o S o dP), in fp32
-            float c = m * S[i] * P[i];
-            c += __shfl_xor(c, 1, 64);
-            c += __shfl_xor(c, 2, 64);
-            c += __shfl_xor(c, 4, 64);
-            c += __shfl_xor(c, 8, 64);
+            const float c = row_sum16(m * S[i] * P[i]);
             if (ln == 0) sm.kdk[16 * jt + 4 * lq + i][mt] = c;
           }
         }
@@ -1032,14 +1027,9 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
       float kdk = sm.dgk[lane][0] + sm.dgk[lane][1] + sm.dgk[lane][2] + sm.dgk[lane][3];
       for (int mt = lane >> 4; mt < 4; ++mt) kdk += sm.kdk[lane][mt];
       const float dG = qdq - kdk;
-      float x = dG;   // inclusive suffix sum over the chunk
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_down(x, d, 64);
-        if (lane + d < 64) x += y;
-      }
+      const float x = chunk_rsum(dG);   // inclusive suffix sum over the chunk
       buf_store<float>(x + carry, rdg, vo_g, so_g);
-      carry += __shfl(x, 0, 64);
+      carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
     }
   }
   if (tid == 0) segtot[(size_t)row * NSEG + p] = carry;

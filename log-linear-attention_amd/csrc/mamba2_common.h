@@ -101,6 +101,37 @@ __device__ __forceinline__ float chunk_cumsum(float x) {
   return x;
 }
 
+// Inclusive suffix sum over the 64 lanes (lane l: sum of lanes l .. 63): the
+// same Hillis-Steele steps toward lower lanes (row_shl), then each row adds the
+// totals of the rows after it (read from lanes 16, 32, 48).
+__device__ __forceinline__ float chunk_rsum(float x) {
+  x += dpp_f32<0x101, 0xf, true>(0.f, x);   // row_shl:1
+  x += dpp_f32<0x102, 0xf, true>(0.f, x);   // row_shl:2
+  x += dpp_f32<0x104, 0xf, true>(0.f, x);   // row_shl:4
+  x += dpp_f32<0x108, 0xf, true>(0.f, x);   // row_shl:8
+  const int xi = __builtin_bit_cast(int, x);
+  const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
+  const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
+  const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
+  const int r = (threadIdx.x & 63) >> 4;
+  return x + ((r < 3 ? t3 : 0.f) + (r < 2 ? t2 : 0.f) + (r < 1 ? t1 : 0.f));
+}
+
+// Sums over the lanes of a DPP quad (4 q .. 4 q + 3) and of a 16-lane row, in
+// every lane of the quad / row: quad permutations, then the mirrored half-row
+// and row.  VALU only, no LDS round trip.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp_f32<0xb1, 0xf, false>(0.f, x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_f32<0x4e, 0xf, false>(0.f, x);   // quad_perm [2, 3, 0, 1]
+  return x;
+}
+__device__ __forceinline__ float row_sum16(float x) {
+  x = quad_sum(x);
+  x += dpp_f32<0x141, 0xf, false>(0.f, x);  // row_half_mirror
+  x += dpp_f32<0x140, 0xf, false>(0.f, x);  // row_mirror
+  return x;
+}
+
 // ---------------------------------------------------------------------------
 // Per-segment summaries Sum(q) and total log-decay D_q
 // ---------------------------------------------------------------------------

@@ -131,43 +131,48 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
   fetch_qk(ci);
   fetch_v(ci, 0, pv[0]);
   fetch_v(ci, 1, pv[1]);
+  // the chunk-local cumsum of g is written by wave 0; the other waves store
+  // through an empty range, so the store (like every load) is unconditional and
+  // the compiler can count the memory operations in flight
+  const rsrc_t rgc = make_rsrc(gcum, MODE == kPrepFwd && w == 0 ? (size_t)nchunks * kGC * 4 : 0);
 
-  for (; ci < nchunks; ci += gridDim.x) {
-    const int row = ci / NT, ic = ci % NT;
-    const int h = row % H;
-    const size_t tok0 = tok_of(ci);
-    const int nxt = min(ci + (int)gridDim.x, nchunks - 1);
-
-    // ---- stage the chunk -------------------------------------------------------------
+  // ---- stage a chunk: Q, K (l2-normalised on request), the cumsum of g, beta,
+  //      lambda -> LDS, then the next chunk's Q, K loads.  Called before the
+  //      walk and at the end of each chunk, so every wait for those loads sees
+  //      the same memory operations in flight on every path.
+  auto stage = [&](int c) __attribute__((always_inline)) {
+    const int hs = (c / NT) % H;
+    const size_t t0 = tok_of(c);
 #pragma unroll
     for (int i = 0; i < QU; ++i) {
       const int u = tid + NTH * i, r = u / UPR, cc = 8 * (u % UPR);
       *(u32x4*)(s.q + r * LK + cc) = pq[i];
       *(u32x4*)(s.k + r * LK + cc) = pk[i];
     }
-    if (w == 0) {
-      float x = pg;
-      if constexpr (MODE == kPrepFwd) {
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const float y = __shfl_up(x, d, 64);
-          if (lane >= d) x += y;
-        }
-        gcum[(tok0 + lane) * H + h] = x;
-      }
-      s.gc[lane] = x;
-    } else if (w == 1) {
-      s.beta[lane] = pb;
+    float x = pg;
+    if constexpr (MODE == kPrepFwd) {
+      x = chunk_cumsum(x);
+      buf_store<float>(x, rgc, (unsigned int)(lane * H * 4), (unsigned int)((t0 * H + hs) * 4));
     }
+    if (w == 0) s.gc[lane] = x;
+    if (w == 1) s.beta[lane] = pb;
     if (tid < 7 * kGC) s.lam[tid % 7][tid / 7] = pl;
     __syncthreads();
-    fetch_qk(nxt);
+    fetch_qk(min(c + (int)gridDim.x, nchunks - 1));
     if (norm_qk) {
       // use_qk_l2norm_in_kernel (kernel.py:110-111): k / ||k|| and q scale / ||q||
       if (tid < 256) l2norm_rows<KD, LK>(s.k, 1.f, nullptr);
       else l2norm_rows<KD, LK, 256>(s.q, qk_scale, nullptr);
       __syncthreads();
     }
+  };
+  stage(ci);
+
+  for (;;) {
+    const int row = ci / NT, ic = ci % NT;
+    const int h = row % H;
+    const size_t tok0 = tok_of(ci);
+    const int nxt = min(ci + (int)gridDim.x, nchunks - 1);
 
     // ---- K K^T (-> A, fp32) and Q K^T (-> M, bf16): wave w owns rows t-tile tt,
     // column tiles 2wh, 2wh + 1 -------------------------------------------------------
@@ -256,7 +261,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const bf16x8 ba0 = rows_frag(s.aw, 0), ba1 = rows_frag(s.aw, 1);
     const bf16x8 bq0 = rows_frag(s.mq, 0), bq1 = rows_frag(s.mq, 1);
     const float egl = s.gc[kGC - 1];
-#pragma unroll 1
+#pragma unroll
     for (int cb = 0; cb < KD / 64; ++cb) {
       // W^T tile (column tile ct, t-tile tt): A[m = col][s] = beta_s K[s][col]
 #pragma unroll
@@ -319,17 +324,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     }
 
     // ---- per 64-column block of V: U = Au (beta V) ------------------------------------
+    // blocks 0 and 1 come from the prefetch registers (their next-chunk loads are
+    // issued unconditionally; with one block the second reloads block 0), later
+    // blocks are loaded here
     const bf16x8 bu0 = rows_frag(s.au, 0), bu1 = rows_frag(s.au, 1);
-#pragma unroll 1
-    for (int vb = 0; vb < NVB; ++vb) {
-      u32x4 x;
-      if (vb < 2) {
-        x = pv[vb & 1];
-      } else {
-        fetch_v(ci, vb, x);
-      }
+    auto u_block = [&](int vb, const u32x4& x) __attribute__((always_inline)) {
       *(u32x4*)(s.v + (tid >> 3) * kLd64 + 8 * (tid & 7)) = x;
-      if (vb < 2) fetch_v(nxt, vb, pv[vb & 1]);
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -350,7 +350,22 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         *(bf16x4*)(un + ((tok0 + t) * H + h) * V + 64 * vb + 16 * ct + 4 * lq) = cvt4(d);
       }
       __syncthreads();
+    };
+    {
+      const u32x4 x0 = pv[0], x1 = pv[1];
+      fetch_v(nxt, 0, pv[0]);
+      fetch_v(nxt, 1, pv[1]);
+      u_block(0, x0);
+      if (NVB > 1) u_block(1, x1);
     }
+    for (int vb = 2; vb < NVB; ++vb) {
+      u32x4 x;
+      fetch_v(ci, vb, x);
+      u_block(vb, x);
+    }
+    ci += gridDim.x;
+    if (ci >= nchunks) break;
+    stage(ci);
   }
 }
 

@@ -77,61 +77,6 @@ __device__ __forceinline__ void store_tile64(const Tile64<T>& t, __bf16* p0, __b
   }
 }
 
-// DPP move of a float: lanes whose source is outside the row read 0, rows
-// outside row_mask keep `old`.
-template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
-__device__ __forceinline__ float dpp_f32(float old, float src) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                               __builtin_bit_cast(int, src), CTRL,
-                                                               ROW_MASK, 0xf, BOUND_ZERO));
-}
-
-// Inclusive cumsum of g over the 64 tokens of a chunk (fla chunk_local_cumsum,
-// chunkwise.py:1175); lane l holds g[t = l] on entry and Gc[l] on exit.
-// Hillis-Steele within each 16-lane row (DPP row_shr 1, 2, 4, 8), then the row
-// totals are carried with row_bcast:15 (into rows 1, 3) and row_bcast:31 (into
-// rows 2, 3): six VALU ops, no LDS round trips.
-__device__ __forceinline__ float chunk_cumsum(float x) {
-  x += dpp_f32<0x111, 0xf, true>(0.f, x);   // row_shr:1
-  x += dpp_f32<0x112, 0xf, true>(0.f, x);   // row_shr:2
-  x += dpp_f32<0x114, 0xf, true>(0.f, x);   // row_shr:4
-  x += dpp_f32<0x118, 0xf, true>(0.f, x);   // row_shr:8
-  x += dpp_f32<0x142, 0xa, false>(0.f, x);  // row_bcast:15
-  x += dpp_f32<0x143, 0xc, false>(0.f, x);  // row_bcast:31
-  return x;
-}
-
-// Inclusive suffix sum over the 64 lanes (lane l: sum of lanes l .. 63): the
-// same Hillis-Steele steps toward lower lanes (row_shl), then each row adds the
-// totals of the rows after it (read from lanes 16, 32, 48).
-__device__ __forceinline__ float chunk_rsum(float x) {
-  x += dpp_f32<0x101, 0xf, true>(0.f, x);   // row_shl:1
-  x += dpp_f32<0x102, 0xf, true>(0.f, x);   // row_shl:2
-  x += dpp_f32<0x104, 0xf, true>(0.f, x);   // row_shl:4
-  x += dpp_f32<0x108, 0xf, true>(0.f, x);   // row_shl:8
-  const int xi = __builtin_bit_cast(int, x);
-  const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
-  const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
-  const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
-  const int r = (threadIdx.x & 63) >> 4;
-  return x + ((r < 3 ? t3 : 0.f) + (r < 2 ? t2 : 0.f) + (r < 1 ? t1 : 0.f));
-}
-
-// Sums over the lanes of a DPP quad (4 q .. 4 q + 3) and of a 16-lane row, in
-// every lane of the quad / row: quad permutations, then the mirrored half-row
-// and row.  VALU only, no LDS round trip.
-__device__ __forceinline__ float quad_sum(float x) {
-  x += dpp_f32<0xb1, 0xf, false>(0.f, x);   // quad_perm [1, 0, 3, 2]
-  x += dpp_f32<0x4e, 0xf, false>(0.f, x);   // quad_perm [2, 3, 0, 1]
-  return x;
-}
-__device__ __forceinline__ float row_sum16(float x) {
-  x = quad_sum(x);
-  x += dpp_f32<0x141, 0xf, false>(0.f, x);  // row_half_mirror
-  x += dpp_f32<0x140, 0xf, false>(0.f, x);  // row_mirror
-  return x;
-}
-
 // ---------------------------------------------------------------------------
 // Per-segment summaries Sum(q) and total log-decay D_q
 // ---------------------------------------------------------------------------

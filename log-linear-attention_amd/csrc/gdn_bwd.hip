@@ -51,14 +51,6 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
 
 namespace hattn {
 
-__device__ __forceinline__ float rsum16(float x) {
-  x += __shfl_xor(x, 1, 64);
-  x += __shfl_xor(x, 2, 64);
-  x += __shfl_xor(x, 4, 64);
-  x += __shfl_xor(x, 8, 64);
-  return x;
-}
-
 // ---------------------------------------------------------------------------
 // Kernel 3: reverse level scan
 // ---------------------------------------------------------------------------
@@ -168,6 +160,8 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
   };
   if (kPrefTiles) fetch_tiles(NT - 1);
   fetch_h(NT - 1, 0);
+  const rsrc_t rdl = make_rsrc(dl_p + ((size_t)vb * BTH + h) * nlev,
+                               w == 0 ? (size_t)B * T * H * nlev * 4 : 0);
 
   for (int ic = NT - 1; ic >= 0; --ic) {
     const size_t tok0 = (size_t)b * T + (size_t)ic * kGC;
@@ -257,13 +251,16 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
           *(bf16x4*)(s.vn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = vnb;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float xs = rsum16(dlr[i]);
+            const float xs = row_sum16(dlr[i]);
             if (ln == 0) s.dlr[vt][16 * tt + 4 * lq + i] = xs;
           }
         }
         __syncthreads();
-        if (tid < kGC)
-          dl_p[((size_t)vb * BTH + (tok0 + tid) * H + h) * nlev + e] = s.dlr[0][tid] + s.dlr[1][tid];
+        // wave 0's lanes store the level's dlambda row sums; the other waves store
+        // through an empty range, so the store is unconditional and the memory
+        // waits of the walk count exactly
+        buf_store<float>(s.dlr[0][lane] + s.dlr[1][lane], rdl,
+                         (unsigned int)((lane * H) * nlev + e) * 4, (unsigned int)(tok0 * H * nlev * 4));
 
         // (ii) contractions over this slice's 32 columns of V
         {
@@ -489,7 +486,7 @@ __device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], const __bf
     if (norm) {
 #pragma unroll
       for (int nt = 0; nt < NKT; ++nt) dot += (float)Y[t * LY + 16 * nt + ln] * inv_s * x[nt][i];
-      dot = rsum16(dot);
+      dot = row_sum16(dot);
       f = rinv[t] * s;
     }
 #pragma unroll
@@ -717,7 +714,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       for (int i = 0; i < 4; ++i) rs[i] += S1[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] * hacc[nt][i];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = rsum16(rs[i]);
+      const float x = row_sum16(rs[i]);
       if (ln == 0) s.dgr[t16 + 4 * lq + i] -= x;
     }
     __syncthreads();
@@ -766,7 +763,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = rsum16(rs[i]);
+      const float x = row_sum16(rs[i]);
       if (ln == 0) s.dgr[t16 + 4 * lq + i] += x;
     }
   }
@@ -934,7 +931,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   __syncthreads();   // the next updates of dGc come from other threads
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float x = rsum16(rb[i]), y = rsum16(kd[i]);
+    const float x = row_sum16(rb[i]), y = row_sum16(kd[i]);
     if (ln == 0) {
       const int sr = t16 + 4 * lq + i;
       s.dbr[sr] += x;
@@ -989,7 +986,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = rsum16(rbv[i]);
+      const float x = row_sum16(rbv[i]);
       if (ln == 0) s.dbr[t16 + 4 * lq + i] += x;
     }
   }

@@ -64,6 +64,21 @@ def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
         raise ValueError(f"L={L} levels are too few for T={T}")
 
 
+def _widen_half(q, k, v, l):
+    """fp16 inputs have no kernels of their own.  fp16 values are exact in
+    fp32, so fp16 q / k run the fp32-accurate (bf16x3) kernels, and fp16 v or
+    lambda next to bf16 q / k are read as fp32; the caller returns o and the
+    gradients in the inputs' dtypes."""
+    half = torch.float16
+    if q.dtype == half:
+        q, k = q.float().contiguous(), k.float().contiguous()
+    if v.dtype == half:
+        v = v.float().contiguous()
+    if l.dtype == half:
+        l = l.float().contiguous()
+    return q, k, v, l
+
+
 def _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht, o_dtype):
     """One launch of hattn_mamba2_chunkwise_fwd (K = 64): returns (o, g_cumsum)."""
     dev = q.device
@@ -124,6 +139,7 @@ def chunkwise_fwd(
     if q.dtype != k.dtype:
         raise ValueError("q and k must share a dtype")
     out_dtype = v.dtype
+    q, k, v, l = _widen_half(q, k, v, l)
     if q.dtype == torch.float32:
         # fp32 q / k run the bf16x3 (fp32-accurate) kernels, which read fp32 v
         # and lambda and write fp32 o
@@ -215,8 +231,9 @@ def chunkwise_bwd(
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
+    q_dtype, k_dtype, v_dtype = q.dtype, k.dtype, v.dtype
+    q, k, v, l = _widen_half(q, k, v, l)
     do = do.to(q.dtype).contiguous()
-    v_dtype = v.dtype
     if q.dtype == torch.float32:
         # fp32 q / k run the bf16x3 (fp32-accurate) backward, which reads fp32 v,
         # lambda and dO and writes fp32 dq, dk, dv
@@ -245,7 +262,7 @@ def chunkwise_bwd(
                 dg += r[3]
                 dl += r[4]
         dq, dk, dv = dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
-    dv = dv.to(v_dtype)
+    dq, dk, dv = dq.to(q_dtype), dk.to(k_dtype), dv.to(v_dtype)
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3)
         dk = dk.view(B, T, G, H // G, K).sum(3)

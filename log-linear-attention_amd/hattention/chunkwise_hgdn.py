@@ -58,6 +58,22 @@ def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
     return B, T, G, H, K, V, L
 
 
+def _narrow_half(q, k, v, b, l):
+    """fp16 inputs have no kernels of their own: fp16 q / k / v are rounded to
+    bf16 on the device (the GDN kernels read bf16; the reference's fp16 dots
+    keep three more mantissa bits of the inputs), fp16 beta and lambda are
+    read as fp32 (exact).  The caller returns the outputs and gradients in the
+    inputs' dtypes."""
+    half = torch.float16
+    if q.dtype == half:
+        q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
+    if b.dtype == half:
+        b = b.float().contiguous()
+    if l.dtype == half:
+        l = l.float().contiguous()
+    return q, k, v, b, l
+
+
 def chunkwise_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -84,6 +100,8 @@ def chunkwise_fwd(
     if g.dtype != torch.float32:
         raise ValueError("g (log-decay) must be float32")
     dev = _lib.require_device(q, k, v, b, g, l)
+    o_dtype, k_dtype = v.dtype, k.dtype
+    q, k, v, b, l = _narrow_half(q, k, v, b, l)
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
@@ -104,6 +122,8 @@ def chunkwise_fwd(
         float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
         _lib.stream_handle(dev))
     _lib.check(st)
+    if o_dtype != o.dtype:
+        o, Aw, Au = o.to(o_dtype), Aw.to(k_dtype), Au.to(k_dtype)
     return g_cumsum, o, Aw, Au, ht
 
 
@@ -142,6 +162,9 @@ def chunkwise_bwd(
     if do.shape != v.shape:
         raise ValueError("do must have the shape of v")
     dev = _lib.require_device(q, k, v, b, g, l, do)
+    dtypes = (q.dtype, k.dtype, v.dtype, b.dtype)
+    q, k, v, b, l = _narrow_half(q, k, v, b, l)
+    Aw, Au = Aw.to(k.dtype), Au.to(k.dtype)
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
@@ -187,4 +210,5 @@ def chunkwise_bwd(
     if G != H:
         dq = dq.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(q.dtype)
         dk = dk.view(B, T, G, H // G, K).sum(3, dtype=torch.float32).to(k.dtype)
+    dq, dk, dv, db = (x.to(d) for x, d in zip((dq, dk, dv, db), dtypes))
     return dq, dk, dv, db, dg, dl

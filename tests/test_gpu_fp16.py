@@ -1,0 +1,118 @@
+"""fp16 inputs (the reference's kernels take fp16 q / k / v / lambda).
+
+The library has no fp16 kernels.  The host layer widens fp16 exactly: fp16
+Mamba-2 q / k run the fp32-accurate (bf16x3) kernels, fp16 v / lambda next to
+bf16 q / k are read as fp32, and the output and gradients come back in the
+inputs' dtypes.  GDN rounds fp16 q / k / v to bf16 (its kernels read bf16) and
+reads fp16 beta / lambda as fp32.
+
+Checks:
+* Mamba-2 forward and backward with fp16 inputs against the fp64 oracle fed
+  the same fp16 values: the bf16x3 kernels are fp32-accurate, so the error is
+  the final fp16 rounding of o and the gradients (2^-11 relative): max-abs/rel
+  below 2e-3, relative Frobenius below 1e-3 (dg, a reverse cumsum with heavy
+  cancellation, below 1e-2);
+* GDN forward with fp16 inputs against the fp64 oracle on the same fp16
+  values, to the bf16 tolerances of the GDN tests (2e-2 / 1e-2);
+* GDN backward with fp16 inputs equals the backward on the bf16-rounded
+  inputs up to the fp16 rounding of the gradients (the kernels see identical
+  operands).
+"""
+import math
+
+import pytest
+import torch
+
+from bench import make_gdn_inputs, make_mamba2_inputs
+from oracle import gdn as D
+from oracle.mamba2 import autograd_bwd, chunked_fwd, chunked_scan_fwd
+
+pytestmark = pytest.mark.gpu
+
+HALF = torch.float16
+
+
+def _errs(out, ref):
+    out = out.double().cpu()
+    ref = ref.double().cpu()
+    mx = ((out - ref).abs().max() / ref.abs().max()).item()
+    fro = ((out - ref).norm() / ref.norm()).item()
+    return mx, fro
+
+
+@pytest.mark.parametrize("T,K,V", [(256, 64, 64), (1024, 128, 64)])
+def test_mamba2_forward_backward_fp16(T, K, V):
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_bwd, chunkwise_fwd
+    B, H = 1, 2
+    L = 7 + math.ceil(math.log2(T // 64))
+    q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, seed=T + K, dtype=HALF,
+                                           with_do=True)
+    do = do.to(HALF)
+    dev = torch.device("cuda:0")
+    print(f"[fp16 mamba2] T={T} K={K} V={V}", flush=True)
+    qd, kd, vd, gd, ld, dod = (x.to(dev) for x in (q, k, v, g, l, do))
+    o, gc, _ = chunkwise_fwd(qd, kd, vd, gd, ld, False, 2, HType.WEAK, 64, False)
+    grads = chunkwise_bwd(qd, kd, vd, gc, ld, dod, False, 2, HType.WEAK, 64)
+    torch.cuda.synchronize()
+    assert o.dtype == HALF and grads[0].dtype == HALF and grads[1].dtype == HALF
+    assert grads[2].dtype == HALF and grads[3].dtype == torch.float32
+    for h in range(H):
+        sl = lambda x: x[:, :, h:h + 1].double().cpu()
+        o_ref, _, _ = chunked_scan_fwd(sl(q), sl(k), sl(v), sl(g), sl(l), chunk_size=64)
+        mx, fro = _errs(o[:, :, h:h + 1], o_ref)
+        print(f"  head {h} o: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < 2e-3 and fro < 1e-3, (h, mx, fro)
+        ref = autograd_bwd(chunked_fwd, sl(q), sl(k), sl(v), sl(g), sl(l), sl(do), chunk_size=64)
+        for name, a, r in zip(("dq", "dk", "dv", "dg", "dl"), grads, ref):
+            mx, fro = _errs(a[:, :, h:h + 1], r)
+            print(f"  head {h} {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+            tol = 1e-2 if name == "dg" else 1e-3
+            assert mx < 2e-3 and fro < tol, (h, name, mx, fro)
+
+
+def test_gdn_forward_fp16():
+    from hattention.base import HType
+    from hattention.chunkwise_hgdn import chunkwise_fwd
+    B, T, H, K, V, L = 1, 512, 2, 64, 64, 10
+    q, k, v, beta, g, l = make_gdn_inputs(B, T, H, K, V, L, seed=11, dtype=HALF)
+    dev = torch.device("cuda:0")
+    print("[fp16 gdn fwd]", flush=True)
+    gc, o, Aw, Au, _ = chunkwise_fwd(*(x.to(dev) for x in (q, k, v, beta, g, l)), False, 2,
+                                     HType.WEAK, 64, False)
+    torch.cuda.synchronize()
+    assert o.dtype == HALF and Aw.dtype == HALF and Au.dtype == HALF
+    for h in range(H):
+        sl = lambda x: x[:, :, h:h + 1].double().cpu()
+        _, o_ref, aw_ref, _, _ = D.chunked_fwd(sl(q), sl(k), sl(v), sl(beta), sl(g), sl(l),
+                                               chunk_size=64)
+        mx, fro = _errs(o[:, :, h:h + 1], o_ref)
+        print(f"  head {h} o: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < 2e-2 and fro < 1e-2, (h, mx, fro)
+        assert _errs(Aw[:, :, h:h + 1], aw_ref)[0] < 1e-2
+
+
+def test_gdn_backward_fp16_matches_bf16_rounded_inputs():
+    from hattention.base import HType
+    from hattention.chunkwise_hgdn import chunkwise_bwd, chunkwise_fwd
+    B, T, H, K, V, L = 1, 512, 2, 128, 128, 10
+    q, k, v, beta, g, l = make_gdn_inputs(B, T, H, K, V, L, seed=12, dtype=HALF)
+    do = torch.randn(B, T, H, V, generator=torch.Generator().manual_seed(5)).to(HALF)
+    dev = torch.device("cuda:0")
+    print("[fp16 gdn bwd]", flush=True)
+
+    def run(dt_qkv, dt_bl):
+        xs = [q.to(dt_qkv), k.to(dt_qkv), v.to(dt_qkv), beta.to(dt_bl), g, l.to(dt_bl)]
+        xs = [x.to(dev).contiguous() for x in xs]
+        gc, o, Aw, Au, _ = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, False)
+        return chunkwise_bwd(xs[0], xs[1], xs[2], xs[3], gc, xs[5], Aw, Au,
+                             do.to(dt_qkv).to(dev), False, 2, HType.WEAK, 64)
+
+    g16 = run(HALF, HALF)
+    gref = run(torch.bfloat16, torch.float32)
+    torch.cuda.synchronize()
+    assert all(x.dtype == HALF for x in g16[:4])
+    for name, a, r in zip(("dq", "dk", "dv", "db", "dg", "dl"), g16, gref):
+        mx, fro = _errs(a, r.float())
+        print(f"  {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < 2e-3 and fro < 1e-3, (name, mx, fro)

@@ -148,6 +148,31 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
                                int level_base, int htype, int chunk_size, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/*
+ * hattn_mamba2_chunkwise_bwd that reuses the forward's segment summaries.
+ *
+ * No counterpart in the reference (its backward recomputes its states,
+ * chunkwise.py:1371-1384); for callers that keep the forward's workspace until
+ * the backward, as HAttentionFunction does between its forward and backward
+ * (kernel.py:125-244).  Same arguments, results and status codes as
+ * hattn_mamba2_chunkwise_bwd, plus fwd_workspace / fwd_workspace_bytes: the
+ * workspace of the hattn_mamba2_chunkwise_fwd call (bf16 q / k, WEAK) on the
+ * same q, k, v, g, l, with the same B, T, H, K = V = 64 and L, unchanged
+ * since.  Its segment summaries and log-decays replace the backward's summary
+ * pass (one read of K and V).  htype STRONG -> HATTN_ERR_NOT_IMPLEMENTED; q/k
+ * not BF16 -> HATTN_ERR_NOT_IMPLEMENTED; fwd_workspace null or
+ * fwd_workspace_bytes below hattn_mamba2_chunkwise_fwd_workspace(...) ->
+ * HATTN_ERR_VALUE.  A workspace of another call gives wrong gradients.
+ */
+int hattn_mamba2_chunkwise_bwd_fwd_ws(const void* q, const void* k, const void* v,
+                                      const float* g_cumsum, const void* l, const void* do_,
+                                      void* dq, void* dk, void* dv, float* dg, float* dl, int B,
+                                      int T, int H, int K, int V, int L, int dtype_qk,
+                                      int dtype_v, int dtype_l, int dtype_do, int level_base,
+                                      int htype, int chunk_size, void* workspace,
+                                      size_t workspace_bytes, const void* fwd_workspace,
+                                      size_t fwd_workspace_bytes, void* stream);
+
 /* Workspace bytes of hattn_mamba2_chunkwise_bwd for the given htype (WEAK:
  * segment summaries of both scan directions and the q . dq row sums; STRONG:
  * the far dq / dlambda partials of the chunk walks and the adjoint of every

@@ -60,9 +60,12 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
 size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
-                                   float* dg, float* dl, void* ws, int B, int T, int H, int V,
-                                   int L, int nlev, int dt_qk, int dt_v, int dt_l,
-                                   hipStream_t stream, int* unsupported);
+                                   float* dg, float* dl, void* ws, const float* fsums,
+                                   const float* fsegd, int B, int T, int H, int V, int L,
+                                   int nlev, int dt_qk, int dt_v, int dt_l, hipStream_t stream,
+                                   int* unsupported);
+void hattn_mamba2_fwd_ws_summaries(void* ws, int B, int T, int H, int V, const float** sums,
+                                   const float** segd);
 
 hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
                                     const void* v, const void* beta, const float* g,
@@ -299,12 +302,14 @@ size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, i
   return hattn_mamba2_bwd_ws_bytes(B, T, H, V, ceil_log2(T / 64));
 }
 
-int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
-                               const void* l, const void* do_, void* dq, void* dk, void* dv,
-                               float* dg, float* dl, int B, int T, int H, int K, int V, int L,
-                               int dtype_qk, int dtype_v, int dtype_l, int dtype_do,
-                               int level_base, int htype, int chunk_size, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+// fwd_ws (or null): the workspace of the bf16 WEAK forward of the same inputs,
+// whose segment summaries replace the backward's own summary pass
+static int mamba2_bwd_impl(const void* q, const void* k, const void* v, const float* g_cumsum,
+                           const void* l, const void* do_, void* dq, void* dk, void* dv,
+                           float* dg, float* dl, int B, int T, int H, int K, int V, int L,
+                           int dtype_qk, int dtype_v, int dtype_l, int dtype_do, int level_base,
+                           int htype, int chunk_size, void* workspace, size_t workspace_bytes,
+                           const void* fwd_ws, size_t fwd_ws_bytes, void* stream) {
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
@@ -369,13 +374,52 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
   if (workspace_bytes < need || workspace == nullptr)
     return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
+  const float* fsums = nullptr;
+  const float* fsegd = nullptr;
+  if (fwd_ws != nullptr) {
+    if (dtype_qk != HATTN_BF16)
+      return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                  "forward summaries: q/k dtype code %d (the bf16 forward keeps them)", dtype_qk);
+    const size_t fneed = hattn_mamba2_fwd_ws_bytes(B, T, H, V, 0);
+    if (fwd_ws_bytes < fneed)
+      return fail(HATTN_ERR_VALUE, "forward workspace of %zu bytes is smaller than the %zu its "
+                  "forward used", fwd_ws_bytes, fneed);
+    hattn_mamba2_fwd_ws_summaries(const_cast<void*>(fwd_ws), B, T, H, V, &fsums, &fsegd);
+  }
   int unsupported = 0;
   hipError_t e = hattn_mamba2_bwd_launch(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl, workspace,
-                                         B, T, H, V, L, nlev, dtype_qk, dtype_v, dtype_l,
-                                         (hipStream_t)stream, &unsupported);
+                                         fsums, fsegd, B, T, H, V, L, nlev, dtype_qk, dtype_v,
+                                         dtype_l, (hipStream_t)stream, &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination v=%d l=%d", dtype_v, dtype_l);
   return check_hip(e, "hattn_mamba2_chunkwise_bwd launch");
+}
+
+int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, const float* g_cumsum,
+                               const void* l, const void* do_, void* dq, void* dk, void* dv,
+                               float* dg, float* dl, int B, int T, int H, int K, int V, int L,
+                               int dtype_qk, int dtype_v, int dtype_l, int dtype_do,
+                               int level_base, int htype, int chunk_size, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return mamba2_bwd_impl(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl, B, T, H, K, V, L,
+                         dtype_qk, dtype_v, dtype_l, dtype_do, level_base, htype, chunk_size,
+                         workspace, workspace_bytes, nullptr, 0, stream);
+}
+
+int hattn_mamba2_chunkwise_bwd_fwd_ws(const void* q, const void* k, const void* v,
+                                      const float* g_cumsum, const void* l, const void* do_,
+                                      void* dq, void* dk, void* dv, float* dg, float* dl, int B,
+                                      int T, int H, int K, int V, int L, int dtype_qk,
+                                      int dtype_v, int dtype_l, int dtype_do, int level_base,
+                                      int htype, int chunk_size, void* workspace,
+                                      size_t workspace_bytes, const void* fwd_workspace,
+                                      size_t fwd_workspace_bytes, void* stream) {
+  if (fwd_workspace == nullptr) return fail(HATTN_ERR_VALUE, "null forward workspace");
+  if (htype != HATTN_HTYPE_WEAK)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "forward summaries: htype=%d (WEAK only)", htype);
+  return mamba2_bwd_impl(q, k, v, g_cumsum, l, do_, dq, dk, dv, dg, dl, B, T, H, K, V, L,
+                         dtype_qk, dtype_v, dtype_l, dtype_do, level_base, htype, chunk_size,
+                         workspace, workspace_bytes, fwd_workspace, fwd_workspace_bytes, stream);
 }
 
 size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int L) {

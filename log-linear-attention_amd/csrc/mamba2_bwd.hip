@@ -1080,19 +1080,26 @@ inline BwdWs bwd_ws_layout(void* base, int B, int T, int H, int V, int nlev) {
   return w;
 }
 
+// fsums / fsegd (or null): the forward's segment summaries and log-decays of
+// these inputs (its workspace, same segmentation and layout), which then
+// replace the summary pass.
 template <int NP, typename TK, typename TV, typename TL>
 static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, const float* gc,
                                const void* l, const void* dO, void* dq, void* dk, void* dv,
-                               float* dg, float* dl, void* ws, int B, int T, int H, int V,
-                               int L, int nlev, hipStream_t stream) {
+                               float* dg, float* dl, void* ws, const float* fsums,
+                               const float* fsegd, int B, int T, int H, int V, int L, int nlev,
+                               hipStream_t stream) {
   const int NT = T / kBT;
   const int slog = seg_log2(NT);
   const int NSEG = (NT + (1 << slog) - 1) >> slog;
   const int nloc = min(slog, nlev), ntop = nlev - nloc;
   const int rows = B * H;
   const BwdWs w = bwd_ws_layout(ws, B, T, H, V, nlev);
+  const bool reuse = fsums != nullptr && fsegd != nullptr;
+  const float* sums = reuse ? fsums : w.sums;
+  const float* segd = reuse ? fsegd : w.segd;
   hipError_t e;
-  if (NSEG > 1) {
+  if (NSEG > 1 && !reuse) {
     auto sk = mamba2_seg_sum_kernel<TK, TV, true, NP>;
     hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
                        (const TK*)k, (const TV*)v, gc, w.sums, w.segd, B, T, H, H, V, NT,
@@ -1101,8 +1108,8 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   }
   if (ntop > 0) {
     // top-level states of every segment for the dq kernel
-    hipLaunchKernelGGL(mamba2_htop_kernel<NP>, dim3(rows * 4), dim3(256), 0, stream, w.sums,
-                       w.segd, w.htop, V, NSEG, ntop, 1);
+    hipLaunchKernelGGL(mamba2_htop_kernel<NP>, dim3(rows * 4), dim3(256), 0, stream, sums,
+                       segd, w.htop, V, NSEG, ntop, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ngrp = (ntop + 3) / 4;
     auto rk = mamba2_bwd_rsum_kernel<NP, TK, TL>;
@@ -1123,7 +1130,7 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
     auto kk = mamba2_bwd_dkv_kernel<NP, TK, TV, TL>;
     hipLaunchKernelGGL(kk, dim3(rows * NSEG), dim3(512), 0, stream, (const TK*)q,
                        (const TK*)k, (const TV*)v, (const TK*)dO, gc, (const TL*)l,
-                       w.rsum, w.segd, w.dgq, (TK*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
+                       w.rsum, segd, w.dgq, (TK*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
                        nlev, slog, NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -1146,15 +1153,16 @@ size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev) {
 // dq, dk, dv.
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
-                                   float* dg, float* dl, void* ws, int B, int T, int H, int V,
-                                   int L, int nlev, int dt_qk, int dt_v, int dt_l,
-                                   hipStream_t stream, int* unsupported) {
+                                   float* dg, float* dl, void* ws, const float* fsums,
+                                   const float* fsegd, int B, int T, int H, int V, int L,
+                                   int nlev, int dt_qk, int dt_v, int dt_l, hipStream_t stream,
+                                   int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   if (dt_qk == 2) {
     if (dt_v == 2 && dt_l == 2)
-      return bwd_launch_t<2, float, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B,
-                                                  T, H, V, L, nlev, stream);
+      return bwd_launch_t<2, float, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums,
+                                                  fsegd, B, T, H, V, L, nlev, stream);
     *unsupported = 1;
     return hipSuccess;
   }
@@ -1163,13 +1171,13 @@ hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, 
     return hipSuccess;
   }
   if (dt_v == 0 && dt_l == 0)
-    return bwd_launch_t<1, __bf16, __bf16, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, __bf16, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
   if (dt_v == 0 && dt_l == 2)
-    return bwd_launch_t<1, __bf16, __bf16, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, __bf16, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
   if (dt_v == 2 && dt_l == 0)
-    return bwd_launch_t<1, __bf16, float, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, float, __bf16>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
   if (dt_v == 2 && dt_l == 2)
-    return bwd_launch_t<1, __bf16, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, B, T, H, V, L, nlev, stream);
+    return bwd_launch_t<1, __bf16, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
   *unsupported = 1;
   return hipSuccess;
 }

@@ -507,10 +507,11 @@ struct Bf16Smem {
   float gc[kBT];              // log2(e) * chunk-local inclusive cumsum of g
   float wt[kBT];              // exp(Gc_last - Gc_s)
   // lambda[t = 16nt + ln][lev] at [lev][4ln + nt] and exp(Gc_t) at [4ln + nt],
-  // double-buffered: chunk j + 1's are staged while chunk j's are read
-  float lam[2][kMaxLU * kBT];
+  // double-buffered: chunk j + 1's are staged while chunk j's are read.  Row
+  // kMaxLU of each buffer is a per-lane sink for the lambda columns past the
+  // row's levels, so a staged value's slot does not depend on the chunk
+  float lam[2][(kMaxLU + 1) * kBT];
   float eg[2][kBT];
-  float junk[kBT];            // per-lane sink of the lambda columns past the row's levels
   float lpar[32];             // layer mode: L[h, 0 .. L - 1] (lambda parameters of the head)
   __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
 };
@@ -833,6 +834,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       if (tid == 0)
         __hip_atomic_store(sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + p, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+    } else if (tid == 0) {
+      // no later segment reads the last one's summary; its log-decay slot is
+      // zeroed so the workspace (which the backward may reuse) holds no stale value
+      __builtin_amdgcn_raw_buffer_store_b32(0u, rsd, (unsigned int)p * 4, 0, kCohStore);
     }
     // ---- look-back: the earlier segments of this row have published ----
     if (p > 0) {
@@ -936,8 +941,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const rsrc_t rg_ = make_rsrc(g + (size_t)b * T * H + h, w == 0 ? (size_t)T * H * 4 : 0);
   const rsrc_t ro = make_rsrc(o + ((size_t)b * T * H + h) * V + vcol0, (size_t)T * vstr * sizeof(TO));
   const bool write_gcum = gcum != nullptr && vblk == 0;
+  // wave 0 computes Gc; the other waves issue the same store through an empty
+  // range, so every wave has the same memory-operation sequence per chunk
   const rsrc_t rgc = make_rsrc(write_gcum ? (const void*)(gcum + (size_t)b * T * H + h) : (const void*)g,
-                               write_gcum ? (size_t)T * H * 4 : 0);
+                               write_gcum && w == 0 ? (size_t)T * H * 4 : 0);
   const unsigned int vo_qk = tile64_voff<__bf16>(qstr), vo_v = tile64_voff<TV>(vstr);
   const unsigned int vo_g = lane * H * 4;
   const unsigned int vo_o = (ln0 * vstr + 16 * w + 4 * lq0) * sizeof(TO);
@@ -977,9 +984,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   unsigned int dwv[2] = {0u, 0u};
   if (LAYER && tid < L) sm.lpar[tid] = la.Lp[h * L + tid];   // read after the first barrier
   uint4 lamr[kLP];
-  constexpr int kLamBuf = kMaxLU * kBT;           // floats between the two lambda buffers
   const int lslot = 4 * (lane & 15) + (lane >> 4);   // this lane's token row t, permuted
-  const int junk_rel = (int)(sm.junk - sm.lam[0]) + lane - lslot;
+  const int junk_rel = kMaxLU * kBT + lane - lslot;  // the sink row, relative to lslot
   // part < 0: everything; parts 0, 1, 2: q / k / v, g and lambda (the loads of
   // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
   auto load = [&](int j, int part) {
@@ -1010,7 +1016,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
             rdt, ((row0 * H + el_v + 32u * r * H) * desz) & ~3u, 0));
     }
   };
-  auto store = [&](int j) {
+  // chunk j's registers -> LDS; par: the lambda / exp(Gc) buffer it goes to
+  auto store = [&](int j, int par) {
+    float gx = 0.f;
     store_tile_swz<swz_qk>(rg.q, sm.q);
     store_tile_swz<swz_qk>(rg.k, sm.k);
     if constexpr (LAYER) {
@@ -1034,13 +1042,13 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
       sm.gc[lane] = x * kLog2e;
       sm.wt[lane] = fexp(last - x);
-      sm.eg[j & 1][4 * ln0 + lq0] = fexp(x);
-      if (write_gcum) buf_store<float>(x, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
+      sm.eg[par][4 * ln0 + lq0] = fexp(x);
+      gx = x;
     } else {
       // value i of piece pc is column kPE * pc + i - lmis; columns outside
       // [0, lu) go to the lane's junk slot, so every lane stores unconditionally
       // through one LDS base (no divergent branches, no generic pointers)
-      float* lamw = sm.lam[j & 1] + lslot;
+      float* lamw = sm.lam[par] + lslot;
 #pragma unroll
       for (int r = 0; r < kLP; ++r) {
         const int col0 = kPE * (w - 1 + 3 * r) - lmis;
@@ -1052,11 +1060,12 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           else val = __builtin_bit_cast(float, u[i]);
 
           const int col = col0 + i;
-          const int idx = (unsigned int)col < (unsigned int)lu ? col * kBT : junk_rel - (int)(j & 1) * kLamBuf;
+          const int idx = (unsigned int)col < (unsigned int)lu ? col * kBT : junk_rel;
           lamw[idx] = val;
         }
       }
     }
+    buf_store<float>(gx, rgc, vo_g, (unsigned int)(c0 + j) * kBT * H * 4);
   };
 
   // layer mode: the dt words of the chunk in the prefetch registers become dt'
@@ -1121,15 +1130,32 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   load(0, -1);
   if (LAYER) __syncthreads();   // L[h] staged in LDS
   dt_xform();
-  store(0);
+  store(0, 0);
   lam_xform(0);
-  if (nch > 1) {
-    load(1, -1);
-    dt_xform();
+  // The loads and LDS staging of chunks 1, j + 1, j + 2 are unconditional (the
+  // chunk index clamped to the last chunk, the staging of a chunk past the end
+  // repeating the last one into buffers nothing reads): a memory operation
+  // behind a branch makes the compiler's wait counts ignore the operations
+  // after it, i.e. wait for more than the chunk being staged.
+  load(min(1, nch - 1), -1);
+  dt_xform();
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // Four o-shaped stores through an empty range (no request is made): on the
+    // back edge the loop's four o stores follow the next chunk's loads, so with
+    // these the loop header sees the same memory-operation order on both
+    // incoming paths, and the staging waits of chunk j + 1 leave the previous
+    // chunk's o stores in flight instead of waiting for every operation.
+    const rsrc_t rnone = make_rsrc(o, 0);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) buf_store4<TO>(zero4(), rnone, vo_o, 16u * nt * vstr * sizeof(TO));
   }
   float Eseg = 0.f;   // log2-decay from the segment start to the current chunk start
   const int topmask = ntop > 0 ? (p & ((1 << ntop) - 1)) : 0;   // top levels this segment reads
-  for (int j = 0; j < nch; ++j) {
+  // nch >= 1: a do-while, so the preheader runs straight into the body (a loop
+  // guard would let the compiler sink chunk 1's loads below the stores above)
+  int j = 0;
+  do {
     const int ic = c0 + j;
     __syncthreads();   // chunk j staged; every wave is done with chunk j - 1
     // Lane indices made opaque per chunk, so the compiler recomputes the LDS
@@ -1161,9 +1187,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     }
     const float glr = sm.gc[kBT - 1];   // chunk log2-decay
     __syncthreads();   // A visible; chunk j's stage (but lambda') no longer read
-    if (j + 1 < nch) store(j + 1);
-    const bool more = j + 2 < nch;
-    if (more) load(j + 2, 0);
+    store(min(j + 1, nch - 1), (j + 1) & 1);
+    const int jn = min(j + 2, nch - 1);
+    load(jn, 0);
     const float* lpr = sm.lam[j & 1] + 7 * kBT;
     const floatx4 egr = *(const floatx4*)(sm.eg[j & 1] + 4 * ln);   // exp(Gc_t), t = 16nt + ln
 
@@ -1180,7 +1206,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       acc[2] = mfma16x16x32(vt1, af[4], acc[2]);
       acc[3] = mfma16x16x32(vt1, af[5], acc[3]);
     }
-    if (more) load(j + 2, 1);
+    load(jn, 1);
     // local levels the chunk reads (bit e of the chunk index): all eight MFMAs of
     // a level are issued before its lambda-weighted accumulation
 #pragma unroll
@@ -1203,7 +1229,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         }
       }
     }
-    if (more) load(j + 2, 2);
+    load(jn, 2);
     // top levels (bits of the segment index), the next level's fragments
     // prefetched while the current one multiplies
     if (topmask && j >= 0) {
@@ -1306,9 +1332,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       }
     }
     if (j + 1 < nch) lam_xform(j + 1);
-    if (more) dt_xform();   // chunk j + 2's dt words
+    dt_xform();   // chunk j + 2's dt words (the last chunk's again past the end)
     Eseg += glr;
-  }
+  } while (++j < nch);
 }
 
 }  // namespace hattn
@@ -1369,6 +1395,16 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
 
 size_t hattn_mamba2_fwd_ws_bytes(int B, int T, int H, int V, int x3) {
   return fwd_ws_layout(nullptr, B, T, H, V, x3).bytes;
+}
+
+// Where a bf16 forward's workspace holds its segment summaries (fp32
+// [row][segment][K][V]) and segment log-decays ([row][V block][segment]); both
+// null when the sizes have a single segment (no summaries).
+void hattn_mamba2_fwd_ws_summaries(void* ws, int B, int T, int H, int V, const float** sums,
+                                   const float** segd) {
+  const FwdWs w = fwd_ws_layout(ws, B, T, H, V, 0);
+  *sums = w.sums;
+  *segd = w.segd;
 }
 
 // ---------------------------------------------------------------------------

@@ -30,6 +30,9 @@ SIGNATURES = [
     ("hattn_mamba2_chunkwise_bwd", _I,
      [_P, _P, _P, _F, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
      + [_P, _S, _P]),
+    ("hattn_mamba2_chunkwise_bwd_fwd_ws", _I,
+     [_P, _P, _P, _F, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
+     + [_P, _S, _P, _S, _P]),
     ("hattn_mamba2_chunkwise_bwd_workspace", _S, [_I] * 7),
     ("hattn_gdn_chunkwise_fwd", _I,
      [_P, _P, _P, _P, _F, _P, _P, _F, _P, _P, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3

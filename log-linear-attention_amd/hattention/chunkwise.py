@@ -80,7 +80,7 @@ def _widen_half(q, k, v, l):
 
 
 def _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht, o_dtype):
-    """One launch of hattn_mamba2_chunkwise_fwd (K = 64): returns (o, g_cumsum)."""
+    """One launch of hattn_mamba2_chunkwise_fwd (K = 64): returns (o, g_cumsum, workspace)."""
     dev = q.device
     o = torch.empty(v.shape, dtype=o_dtype, device=dev)
     g_cumsum = torch.empty(g.shape, dtype=torch.float32, device=dev)
@@ -93,7 +93,7 @@ def _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht
         _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l), _lib.dtype_code(o),
         level_base, htype.value, chunk_size, ws_ptr, ws_bytes, _lib.stream_handle(dev))
     _lib.check(st)
-    return o, g_cumsum
+    return o, g_cumsum, ws
 
 
 def chunkwise_fwd(
@@ -128,6 +128,16 @@ def chunkwise_fwd(
     split (o = sum over blocks of the blocks' outputs, accumulated in fp32), and
     block i of the final states is the states' rows 64 i .. 64 i + 63.
     """
+    return chunkwise_fwd_keep(q, k, v, g, l, head_first, level_base, htype, chunk_size,
+                              output_final_state)[:3]
+
+
+def chunkwise_fwd_keep(q, k, v, g, l, head_first, level_base, htype, chunk_size,
+                       output_final_state):
+    """:func:`chunkwise_fwd` that also returns the forward's workspace when the
+    backward can reuse its segment summaries (bf16 q / k, K = V = 64, WEAK;
+    else None): pass it to :func:`chunkwise_bwd` as ``fwd_ws`` with the same
+    inputs (HAttentionFunction keeps it between its forward and backward)."""
     _assert_contiguous(q=q, k=k, v=v, g=g, l=l)
     B, T, G, H, K, V, L = _shapes(q, k, v, l, head_first)
     _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size)
@@ -145,27 +155,31 @@ def chunkwise_fwd(
         # and lambda and write fp32 o
         v, l = v.float().contiguous(), l.float().contiguous()
     ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
+    keep = None
     if K == KB:
-        o, g_cumsum = _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size, ht,
-                                v.dtype)
+        o, g_cumsum, ws = _fwd_call(q, k, v, g, l, B, T, G, H, V, L, level_base, htype, chunk_size,
+                                    ht, v.dtype)
+        if V == KB and q.dtype == torch.bfloat16 and htype == HType.WEAK:
+            keep = ws
     else:
         o = None
         for i in range(K // KB):
             blk = slice(KB * i, KB * (i + 1))
             hti = torch.zeros(B, H, KB, V, L, dtype=torch.float32, device=dev) if ht is not None else None
-            oi, g_cumsum = _fwd_call(q[..., blk].contiguous(), k[..., blk].contiguous(), v, g, l,
-                                     B, T, G, H, V, L, level_base, htype, chunk_size, hti,
-                                     torch.float32)
+            oi, g_cumsum, _ = _fwd_call(q[..., blk].contiguous(), k[..., blk].contiguous(), v, g,
+                                        l, B, T, G, H, V, L, level_base, htype, chunk_size, hti,
+                                        torch.float32)
             o = oi if o is None else o.add_(oi)
             if ht is not None:
                 ht[:, :, blk] = hti
     if o.dtype != out_dtype:
         o = o.to(out_dtype)
-    return o, g_cumsum, ht
+    return o, g_cumsum, ht, keep
 
 
-def _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype, chunk_size):
-    """One launch of hattn_mamba2_chunkwise_bwd (K = V = 64, per-head q / k)."""
+def _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype, chunk_size, fwd_ws=None):
+    """One launch of hattn_mamba2_chunkwise_bwd (K = V = 64, per-head q / k), or of
+    hattn_mamba2_chunkwise_bwd_fwd_ws with the forward's workspace."""
     dev = q.device
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
@@ -175,12 +189,15 @@ def _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype, chunk_size):
     lib = _lib.load()
     ws, ws_ptr, ws_bytes = _lib.workspace(
         lib.hattn_mamba2_chunkwise_bwd_workspace(B, T, H, KB, V, L, htype.value), dev)
-    st = lib.hattn_mamba2_chunkwise_bwd(
-        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
-        _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
-        B, T, H, KB, V, L, _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l),
-        _lib.dtype_code(do), level_base, htype.value, chunk_size, ws_ptr, ws_bytes,
-        _lib.stream_handle(dev))
+    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(l), _lib.ptr(do),
+            _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dl),
+            B, T, H, KB, V, L, _lib.dtype_code(q), _lib.dtype_code(v), _lib.dtype_code(l),
+            _lib.dtype_code(do), level_base, htype.value, chunk_size, ws_ptr, ws_bytes)
+    if fwd_ws is None:
+        st = lib.hattn_mamba2_chunkwise_bwd(*args, _lib.stream_handle(dev))
+    else:
+        st = lib.hattn_mamba2_chunkwise_bwd_fwd_ws(*args, _lib.ptr(fwd_ws), fwd_ws.numel(),
+                                                   _lib.stream_handle(dev))
     _lib.check(st)
     return dq, dk, dv, dg, dl
 
@@ -196,6 +213,7 @@ def chunkwise_bwd(
     level_base: int,
     htype: HType,
     chunk_size: int,
+    fwd_ws: Optional[torch.Tensor] = None,
 ):
     """Log-linear Mamba-2 backward (chunkwise.py:1286-1597).
 
@@ -213,6 +231,10 @@ def chunkwise_bwd(
     walks for the far levels (the forward's chunk-level strong cascade and its
     transpose in reverse order) and chunk-parallel diagonal / sub-diagonal
     blocks (chunkwise.py:1377-1580 with USE_A2 / USE_H2).
+
+    ``fwd_ws`` (not in the reference): the workspace :func:`chunkwise_fwd_keep`
+    returned for these inputs; its segment summaries replace the backward's own
+    summary pass.  Used only where the forward kept it (bf16, K = V = 64, WEAK).
 
     The kernels take 64 key and 64 value dimensions.  Larger K and V (multiples
     of 64) run one launch per (key block, value block): with
@@ -239,8 +261,9 @@ def chunkwise_bwd(
         # lambda and dO and writes fp32 dq, dk, dv
         v, l = v.float().contiguous(), l.float().contiguous()
     if K == KB and V == KB:
+        reuse = fwd_ws is not None and q.dtype == torch.bfloat16 and htype == HType.WEAK
         dq, dk, dv, dg, dl = _bwd_call(q, k, v, g, l, do, B, T, H, V, L, level_base, htype,
-                                       chunk_size)
+                                       chunk_size, fwd_ws if reuse else None)
     else:
         f32 = dict(dtype=torch.float32, device=q.device)
         dq = torch.zeros(B, T, H, K, **f32)

@@ -53,9 +53,9 @@ class HAttentionFunction(torch.autograd.Function):
                 raise NotImplementedError
             if scale is not None:
                 raise NotImplementedError
-            o, g, _ = _cw.chunkwise_fwd(
-                q=q, k=k, v=v, g=g, l=l, head_first=head_first, level_base=level_base,
-                htype=htype, chunk_size=chunk_sizes[0], output_final_state=False)
+            # the forward's workspace (its segment summaries) is kept for the backward
+            o, g, _, ctx.fwd_ws = _cw.chunkwise_fwd_keep(
+                q, k, v, g, l, head_first, level_base, htype, chunk_sizes[0], False)
             Aw = None
             Au = None
         elif hstruct == HStruct.GDELTA and chunkwise:
@@ -98,7 +98,8 @@ class HAttentionFunction(torch.autograd.Function):
                 raise ValueError
             dq, dk, dv, dg, dl = _cw.chunkwise_bwd(
                 q=q, k=k, v=v, g=g, l=l, do=do, head_first=ctx.head_first,
-                level_base=ctx.level_base, htype=ctx.htype, chunk_size=ctx.chunk_sizes[0])
+                level_base=ctx.level_base, htype=ctx.htype, chunk_size=ctx.chunk_sizes[0],
+                fwd_ws=ctx.fwd_ws)
             db = None
         elif ctx.hstruct == HStruct.GDELTA and ctx.chunkwise:
             if b is None or Aw is None or Au is None:

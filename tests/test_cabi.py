@@ -122,6 +122,23 @@ def test_fwd_argument_checks(kw, code):
     assert msg
 
 
+def _bwd_fwd_ws(htype=0, dq=0):
+    """hattn_mamba2_chunkwise_bwd_fwd_ws with NULL tensors and a NULL forward
+    workspace: both fail on the host before any HIP call."""
+    lib = _lib.load()
+    nul = ctypes.c_void_p(None)
+    return lib.hattn_mamba2_chunkwise_bwd_fwd_ws(
+        *([nul] * 11), 1, 4096, 1, 64, 64, 13, dq, 0, 0, dq, 2, htype, 64, None, 0, None, 0,
+        None)
+
+
+def test_bwd_forward_workspace_checks():
+    # no forward workspace -> ValueError, checked before the htype and dtype rules
+    assert _bwd_fwd_ws() == _lib.HATTN_ERR_VALUE
+    assert b"forward workspace" in _lib.load().hattn_last_error()
+    assert _bwd_fwd_ws(htype=1) == _lib.HATTN_ERR_VALUE
+
+
 def test_status_maps_to_reference_exceptions():
     lib = _lib.load()
     assert _fwd(T=100) == _lib.HATTN_ERR_VALUE

@@ -40,8 +40,8 @@ def _errs(out, ref):
     return mx, fro
 
 
-def _run(B, T, H, K, V, L, G=None, seed=0, vdtype=None, ldtype=None, rows=None):
-    from hattention.chunkwise import chunkwise_fwd, chunkwise_bwd
+def _run(B, T, H, K, V, L, G=None, seed=0, vdtype=None, ldtype=None, rows=None, reuse=False):
+    from hattention.chunkwise import chunkwise_bwd, chunkwise_fwd_keep
     from hattention.base import HType
     G = G or H
     q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=seed, ldtype=ldtype,
@@ -49,13 +49,15 @@ def _run(B, T, H, K, V, L, G=None, seed=0, vdtype=None, ldtype=None, rows=None):
     if vdtype is not None:
         v = v.to(vdtype)
     dev = torch.device("cuda:0")
-    print(f"[mamba2_bwd] B={B} T={T} H={H} G={G} K={K} V={V} L={L} v={v.dtype} l={l.dtype}",
-          flush=True)
+    print(f"[mamba2_bwd] B={B} T={T} H={H} G={G} K={K} V={V} L={L} v={v.dtype} l={l.dtype}"
+          f" reuse={reuse}", flush=True)
     qd, kd, vd, gd, ld, dod = (x.to(dev) for x in (q, k, v, g, l, do))
-    _, gc, _ = chunkwise_fwd(qd, kd, vd, gd, ld, head_first=False, level_base=2,
-                             htype=HType.WEAK, chunk_size=64, output_final_state=False)
+    _, gc, _, fws = chunkwise_fwd_keep(qd, kd, vd, gd, ld, False, 2, HType.WEAK, 64, False)
+    if reuse:
+        # more than one segment: the forward kept its workspace (segment summaries)
+        assert fws is not None
     grads = chunkwise_bwd(qd, kd, vd, gc, ld, dod, head_first=False, level_base=2,
-                          htype=HType.WEAK, chunk_size=64)
+                          htype=HType.WEAK, chunk_size=64, fwd_ws=fws if reuse else None)
     torch.cuda.synchronize()
     assert grads[0].dtype == q.dtype and grads[2].dtype == v.dtype
     assert grads[3].dtype == torch.float32 and grads[4].dtype == torch.float32
@@ -89,6 +91,25 @@ def test_segments_and_top_levels(T):
     # 2112 has a ragged last segment
     L = 7 + math.ceil(math.log2(T // 64)) + 1
     _run(1, T, 2, 64, 64, L, seed=T + 1)
+
+
+@pytest.mark.parametrize("T", [2112, 4096])
+def test_forward_summaries_reused(T):
+    # hattn_mamba2_chunkwise_bwd_fwd_ws: the forward's segment summaries replace
+    # the backward's summary pass (2112: ragged last segment); the gradients
+    # match the oracle and the backward that computes its own summaries
+    L = 7 + math.ceil(math.log2(T // 64)) + 1
+    a = _run(1, T, 2, 64, 64, L, seed=T + 5, reuse=True)
+    b = _run(1, T, 2, 64, 64, L, seed=T + 5, reuse=False)
+    for name, x, y in zip(NAMES, a, b):
+        mx, fro = _errs(x, y)
+        print(f"  reuse vs own summaries {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < 1e-2 and fro < 2e-3, (name, mx, fro)
+
+
+def test_forward_summaries_grouped():
+    # G < H: the summaries are per head (v and g are), whatever the q / k groups
+    _run(1, 2048, 4, 64, 64, 12, G=2, seed=77, reuse=True)
 
 
 @pytest.mark.parametrize("K,V", [(128, 64), (64, 128), (128, 128)])
@@ -143,6 +164,26 @@ def test_autograd_function():
         assert mx < TOL_MAX and fro < tf, (name, mx, fro)
 
 
+def test_autograd_function_reuses_forward_summaries():
+    """HAttentionFunction keeps the forward's workspace and its backward takes
+    the segment summaries from it (several segments: T = 4096)."""
+    from hattention.kernel import hattention_kernel
+    from hattention.base import HType, HStruct
+    q, k, v, g, l, do = make_mamba2_inputs(1, 4096, 2, 64, 64, 13, seed=23, with_do=True)
+    dev = torch.device("cuda:0")
+    leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, g, l)]
+    o = hattention_kernel(*leaves[:3], None, leaves[3], leaves[4], None, False, 2, HType.WEAK,
+                          HStruct.MAMBA2)
+    assert o.grad_fn is not None and o.grad_fn.fwd_ws is not None
+    (o.float() * do.to(dev).float()).sum().backward()
+    ref = autograd_bwd(chunked_fwd, *(x.double() for x in (q, k, v, g, l, do)), chunk_size=64)
+    for name, x, r in zip(NAMES, leaves, ref):
+        mx, fro = _errs(x.grad, r)
+        print(f"  {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        tf = TOL_FRO_DG if name == "dg" else TOL_FRO
+        assert mx < TOL_MAX and fro < tf, (name, mx, fro)
+
+
 def test_config4_full_size():
     # BASELINE config 4: B=8 T=8192 H=24 dk=dv=64 L=14 bf16, fwd + custom bwd
     _run(8, 8192, 24, 64, 64, 14, seed=1004, rows=[(0, 0), (7, 23)])
@@ -151,6 +192,11 @@ def test_config4_full_size():
 def test_north_star_full_size_bwd():
     # north-star shape B=4 T=16384 H=16 dk=dv=64 L=15 (fwd + bwd throughput metric)
     _run(4, 16384, 16, 64, 64, 15, seed=1000, rows=[(3, 15)])
+
+
+def test_north_star_full_size_bwd_forward_summaries():
+    # the fwd + bwd benchmark's path: the backward reuses the forward's summaries
+    _run(4, 16384, 16, 64, 64, 15, seed=1001, rows=[(0, 0), (2, 9)], reuse=True)
 
 
 # ---------------------------------------------------------------------------

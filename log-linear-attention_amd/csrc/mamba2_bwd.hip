@@ -141,10 +141,19 @@ struct BwdLoader {
       r.v[u] = buf_load16(rv, vo_v, row * vrow);
     }
     r.g = buf_load<float>(rg, vo_g, t0 * H_of(qrow) * 4);
+    // every lane loads (columns past the row's levels repeat the last one and are
+    // not staged): a load behind a per-lane branch makes the compiler wait for
+    // every outstanding memory operation wherever it waits for this one
+    // (the column index is made opaque here, so the clamped offsets are
+    // recomputed per chunk rather than held in registers across the walk)
+    int lc;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lc) : "v"(lcol));
+    const unsigned int vo_row = vo_l - lcol * sizeof(TL);
 #pragma unroll
-    for (int c = 0; c < R::NL; ++c)
-      if (lcol + c * (NTHR / 64) < lu)
-        r.lam[c] = buf_load<TL>(rl, vo_l, t0 * lrowb + c * (NTHR / 64) * sizeof(TL));
+    for (int c = 0; c < R::NL; ++c) {
+      const int col = min(lc + c * (NTHR / 64), lu - 1);
+      r.lam[c] = buf_load<TL>(rl, vo_row + col * sizeof(TL), t0 * lrowb);
+    }
   }
 
   // heads per token row, from the q row bytes
@@ -152,8 +161,9 @@ struct BwdLoader {
     return qrow_bytes / (kKD * sizeof(TK));
   }
 
+  // Returns exp(Gc) of this thread's lambda row (token lrow of the chunk).
   template <int NP>
-  __device__ void store(const BwdRegs<NTHR, TK, TV, TL>& r, BwdStage<NP>& s) const {
+  __device__ float store(const BwdRegs<NTHR, TK, TV, TL>& r, BwdStage<NP>& s) const {
     using R = BwdRegs<NTHR, TK, TV, TL>;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 #pragma unroll
@@ -187,6 +197,7 @@ struct BwdLoader {
         s.lam[col * kBT + lrow] = val;
       }
     }
+    return eg;
   }
 };
 
@@ -462,6 +473,7 @@ struct DqSmem {
   float dl_off[kBT][4][4];                  // off-diagonal tile partials [t][jt][lq]
   float dl_diag[kBT][5][4];                 // diagonal tile partials [t][level][lq]
   float dl_int[kBT][kMaxLoc + kMaxTop][4];  // inter-level partials [t][e][wave]
+  float eg_own[256];                        // exp(Gc_t), t = tid >> 2, one slot per thread
 };
 
 // htop: the top-level states Htop_e2(p) of every (row, segment) in bf16 [k][v]
@@ -529,10 +541,28 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
 
   BwdRegs<256, TK, TV, TL> rg;
   ld.load(rg, c0);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // Four dq-shaped stores through an empty range (no request is made): on the
+    // back edge the chunk's four dq stores follow the next chunk's loads, so
+    // the loop header sees the same memory-operation order on both incoming
+    // paths and the staging wait leaves those stores in flight.
+    const rsrc_t rnone = make_rsrc(dq, 0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      buf_store4<TK>(zero4(), rnone, vo_dq, 16u * mt * H * kKD * sizeof(TK));
+  }
   float Eseg = 0.f;
-  for (int ic = c0; ic < cend; ++ic) {
-    ld.store(rg, s);
-    if (ic + 1 < cend) ld.load(rg, ic + 1);
+  // cend > c0: a do-while, so the preheader runs straight into the body; the
+  // next chunk's loads are unconditional (the last chunk reloaded at the end)
+  int ic = c0;
+  do {
+    // exp(Gc_t) of token t = tid >> 2 (the lambda row this thread stages) goes to
+    // the thread's own slot: the dlambda section reads it after the chunk's last
+    // barrier, and the next chunk's staging rewrites the shared stage before its
+    // first barrier
+    sm.eg_own[tid] = ld.store(rg, s);
+    ld.load(rg, min(ic + 1, cend - 1));
     __syncthreads();
     // lane indices made opaque per chunk, so the LDS addresses of the phases are
     // recomputed (a few VALU ops) instead of held in VGPRs across the walk
@@ -757,7 +787,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           const float raw =
               sm.dl_int[t][e][0] + sm.dl_int[t][e][1] + sm.dl_int[t][e][2] + sm.dl_int[t][e][3];
           qdq += raw * s.lam[col * kBT + t];   // lambda exp(Gc_t) * dlambda / exp(Gc_t)
-          val = raw * s.eg[t];
+          val = raw * sm.eg_own[tid];
         }
         if (col <= 6) qdq += val * s.lam[col * kBT + t];
         buf_store<float>(val, rdl, vo + col * 4, so);
@@ -765,7 +795,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       qdq = quad_sum(qdq);
       if (part == 0) buf_store<float>(qdq, rgq, (unsigned int)t * H * 4, (unsigned int)ic * kBT * H * 4);
     }
-  }
+  } while (++ic < cend);
 }
 
 // ---------------------------------------------------------------------------
@@ -858,21 +888,38 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
   const size_t rq0 = (size_t)b * T * H + h;
   const rsrc_t rdk = make_rsrc(dk + rq0 * kKD, (size_t)T * H * kKD * sizeof(TK));
   const rsrc_t rdv = make_rsrc(dv + rq0 * V, (size_t)T * H * V * sizeof(TV));
-  const rsrc_t rdg = make_rsrc(dg + rq0, (size_t)T * H * 4);
-  const rsrc_t rgq = make_rsrc(dgq + rq0, (size_t)T * H * 4);
+  // dg and q . dq are wave 0's: the other waves issue the same load and store
+  // through empty ranges, so every wave has one memory-operation sequence
+  const rsrc_t rdg = make_rsrc(dg + rq0, w == 0 ? (size_t)T * H * 4 : 0);
+  const rsrc_t rgq = make_rsrc(dgq + rq0, w == 0 ? (size_t)T * H * 4 : 0);
   const unsigned int vo_dk = (ln * H * kKD + 16 * wr + 4 * lq) * sizeof(TK);
   const unsigned int vo_dv = (ln * H * V + 16 * wr + 4 * lq) * sizeof(TV);
 
   BwdRegs<512, TK, TV, TL> rg;
   ld.load(rg, cend - 1);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    // As many stores through an empty range as the loop issues after the next
+    // chunk's loads (the q . dq load, four dk / dv stores and the dg store
+    // follow them on the back edge): the loop header then sees the same
+    // memory-operation order on both incoming paths, and the staging wait
+    // leaves those operations in flight.
+    const rsrc_t rnone = make_rsrc(dk, 0);
+#pragma unroll
+    for (int m = 0; m < 6; ++m)
+      buf_store4<TK>(zero4(), rnone, vo_dk, 16u * m * H * kKD * sizeof(TK));
+  }
   float carry = 0.f;   // sum of dG over the later chunks of this segment
-  for (int ic = cend - 1; ic >= c0; --ic) {
+  // cend > c0: a do-while, so the preheader runs straight into the body; the
+  // previous chunk's loads are unconditional (the first chunk reloaded at the end)
+  int ic = cend - 1;
+  do {
     ld.store(rg, s);
-    if (ic - 1 >= c0) ld.load(rg, ic - 1);
+    ld.load(rg, max(ic - 1, c0));
     // q . dq of this chunk's tokens (written by the dq kernel), needed by wave 0 at
     // the end of the chunk: loaded now so the load has the whole chunk to land
     const unsigned int vo_g = (unsigned int)lane * H * 4, so_g = (unsigned int)ic * kBT * H * 4;
-    const float qdq = w == 0 ? buf_load<float>(rgq, vo_g, so_g) : 0.f;
+    const float qdq = buf_load<float>(rgq, vo_g, so_g);
     __syncthreads();
 
     // ---- phase 1: (M o S) and (M o dP) tiles ---------------------------------------
@@ -1022,16 +1069,18 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     __syncthreads();
 
     // ---- dG = q . dq - k . dk and its reverse cumsum inside the segment --------------
+    float xg = 0.f;
     if (w == 0) {
       // column sums over the t-tiles at or after this s-tile (the others are zero)
       float kdk = sm.dgk[lane][0] + sm.dgk[lane][1] + sm.dgk[lane][2] + sm.dgk[lane][3];
       for (int mt = lane >> 4; mt < 4; ++mt) kdk += sm.kdk[lane][mt];
       const float dG = qdq - kdk;
       const float x = chunk_rsum(dG);   // inclusive suffix sum over the chunk
-      buf_store<float>(x + carry, rdg, vo_g, so_g);
+      xg = x + carry;
       carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
     }
-  }
+    buf_store<float>(xg, rdg, vo_g, so_g);
+  } while (--ic >= c0);
   if (tid == 0) segtot[(size_t)row * NSEG + p] = carry;
 }
 

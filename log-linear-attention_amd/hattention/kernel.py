@@ -37,11 +37,21 @@ def input_guard(fn):
     return wrapper
 
 
+# The reference decorates its autograd functions with fla.utils'
+# autocast_custom_fwd / autocast_custom_bwd (kernel.py:36, 139, 251, 317), which
+# are torch.amp.custom_fwd / custom_bwd for the GPU device without cast_inputs:
+# under torch.autocast the forward records the autocast state and the backward
+# runs in that same state; the inputs are not cast.
+autocast_custom_fwd = functools.partial(torch.amp.custom_fwd, device_type="cuda")
+autocast_custom_bwd = functools.partial(torch.amp.custom_bwd, device_type="cuda")
+
+
 class HAttentionFunction(torch.autograd.Function):
     """kernel.py:32-244."""
 
     @staticmethod
     @input_guard
+    @autocast_custom_fwd
     def forward(ctx, q, k, v, b, g, l, scale, head_first, level_base, htype, hstruct,
                 chunk_sizes, chunkwise, use_qk_l2norm_in_kernel):
         if hstruct == HStruct.MAMBA2 and chunkwise:
@@ -91,6 +101,7 @@ class HAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     @input_guard
+    @autocast_custom_bwd
     def backward(ctx, do):
         q, k, v, b, g, l, Aw, Au = ctx.saved_tensors
         if ctx.hstruct == HStruct.MAMBA2 and ctx.chunkwise:
@@ -154,6 +165,7 @@ class HAttentionPrefillFunction(torch.autograd.Function):
 
     @staticmethod
     @input_guard
+    @autocast_custom_fwd
     def forward(ctx, q, k, v, b, g, l, scale, head_first, level_base, htype, hstruct, chunk_size,
                 use_qk_l2norm_in_kernel):
         if hstruct == HStruct.MAMBA2:
@@ -185,6 +197,7 @@ class HAttentionPrefillFunction(torch.autograd.Function):
         return o.to(q.dtype), h
 
     @staticmethod
+    @autocast_custom_bwd
     def backward(ctx, do, dh):
         raise NotImplementedError
 

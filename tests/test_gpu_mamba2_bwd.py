@@ -164,6 +164,33 @@ def test_autograd_function():
         assert mx < TOL_MAX and fro < tf, (name, mx, fro)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_autograd_function_under_autocast(dtype):
+    """Like the reference (autocast_custom_fwd / _bwd, kernel.py:36, 139), the
+    inputs are not cast under torch.autocast and the backward runs in the
+    forward's autocast state: output and gradients equal those of the same call
+    outside autocast, bit for bit (fp32 inputs keep the bf16x3 kernels)."""
+    from hattention.kernel import hattention_kernel
+    from hattention.base import HType, HStruct
+    q, k, v, g, l, do = make_mamba2_inputs(1, 2048, 2, 64, 64, 12, seed=29, dtype=dtype,
+                                           with_do=True)
+    dev = torch.device("cuda:0")
+
+    def run(amp):
+        leaves = [x.to(dev).requires_grad_(True) for x in (q, k, v, g, l)]
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            o = hattention_kernel(*leaves[:3], None, leaves[3], leaves[4], None, False, 2,
+                                  HType.WEAK, HStruct.MAMBA2)
+            (o.float() * do.to(dev).float()).sum().backward()
+        return [o.detach()] + [x.grad for x in leaves]
+
+    plain, amp = run(False), run(True)
+    torch.cuda.synchronize()
+    assert plain[0].dtype == dtype and amp[0].dtype == dtype
+    for name, a, b in zip(("o",) + NAMES, amp, plain):
+        assert a.dtype == b.dtype and torch.equal(a, b), name
+
+
 def test_autograd_function_reuses_forward_summaries():
     """HAttentionFunction keeps the forward's workspace and its backward takes
     the segment summaries from it (several segments: T = 4096)."""

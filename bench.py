@@ -204,7 +204,9 @@ def decode_bench(dev, stream, n_steps, warmup):
         else:
             q, k, v, b, g, l = make_gdn_inputs(B, T, H, K, V, L, seed=1005, device=dev)
             scale, norm = K ** -0.5, True
-        tm = lambda x: x.transpose(0, 1).contiguous() if x is not None else None
+        # token-major copies split into per-token views up front, so a step's
+        # host time is hattention_step's own, not the harness's tensor indexing
+        tm = lambda x: list(x.transpose(0, 1).contiguous().unbind(0)) if x is not None else None
         q, k, v, b, g, l = (tm(x) for x in (q, k, v, b, g, l))
         S = HState(2, HType.WEAK, hs, (B, H, K, V, L), torch.float32, dev)
         it = iter(range(T))
@@ -537,6 +539,7 @@ ONLY_CASES = {
     "ns_strong_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
         "north star fwd+bwd, HType.STRONG", NS_SHAPE, torch.bfloat16, dev, st, ev, n, w,
         backward=True, strong=True),
+    "decode": lambda dev, st, ev, n, w: decode_bench(dev, st, max(n, 128), w),
     "gdn_fwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd",))[0],
     "gdn_fwd_bwd": lambda dev, st, ev, n, w: gdn_records(dev, st, ev, n, keys=("fwd_bwd",))[1],
 }

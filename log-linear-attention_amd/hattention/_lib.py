@@ -125,7 +125,17 @@ def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The current stream of ``device`` as a raw hipStream_t (what
+    torch.cuda.current_stream(device).cuda_stream returns, without building a
+    Stream object: about 0.1 us instead of 1.8 us per call, which matters on
+    the per-token decode path)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None
+                           else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

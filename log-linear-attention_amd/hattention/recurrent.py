@@ -177,16 +177,19 @@ def launch_step(S: HState, *, q=None, k=None, v=None, beta=None, g=None, l=None,
         raise RuntimeError("hattention (MI355X) runs only on HIP device tensors; the HState "
                            f"is on {st.device}")
     dev = st.device
+    didx = st.get_device()
     B, H, K, V, L = S.shape
     qk = q if q is not None else k
     if qk is None or (update and (k is None or v is None or g is None)) or \
             (output and (q is None or l is None or o is None)):
         raise ValueError("missing operand for the step")
     G = qk.shape[1]
+    # (the device compared by index: t.device builds a torch.device per call)
     for name, t, shape in (("q", q, (B, G, K)), ("k", k, (B, G, K)), ("v", v, (B, H, V)),
                            ("beta", beta, (B, H)), ("g", g, (B, H)), ("l", l, (B, H, L)),
                            ("o", o, (B, H, V))):
-        if t is not None and (t.shape != shape or not t.is_contiguous() or t.device != dev):
+        if t is not None and (t.shape != shape or not t.is_contiguous() or
+                              t.get_device() != didx):
             raise _operand_error(name, t, shape, dev)
     if G <= 0 or H % G != 0:
         raise ValueError(f"G={G} does not divide H={H}")
@@ -210,7 +213,7 @@ def launch_step(S: HState, *, q=None, k=None, v=None, beta=None, g=None, l=None,
                 _lib.ptr(beta), _lib.ptr(g), _lib.ptr(l), _lib.ptr(o), B, G, H, K, V, L,
                 S.hstruct.value, S.htype.value, cascade, int(update), int(output), int(l2norm_qk),
                 float(scale if scale is not None else 1.0), *codes,
-                torch.cuda.current_stream(dev).cuda_stream)
+                _lib.stream_handle(dev))
     if status:
         S.host_counts = saved
         _lib.check(status)

@@ -360,3 +360,17 @@ def test_register_kernel_matches_lds_kernel(hs, L):
         o_ref = M.recurrent_fwd(*(x.double() for x in (q, k, v, g, l)))
         _check_out(torch.stack(o1, 1), o_ref, torch.float32, "mamba2 K=128")
     _check_out(torch.stack(o2, 1), o_ref, torch.float32, "register kernel")
+
+
+def test_stream_handle_is_the_current_stream():
+    """The library's launches go to torch's current stream: the raw handle the
+    binding passes equals torch.cuda.current_stream(dev).cuda_stream, on the
+    default stream and inside a torch.cuda.stream context."""
+    from hattention import _lib
+    dev = torch.device("cuda:0")
+    assert _lib.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        assert _lib.stream_handle(dev) == s.cuda_stream
+        assert _lib.stream_handle(torch.device("cuda")) == s.cuda_stream
+    assert _lib.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream

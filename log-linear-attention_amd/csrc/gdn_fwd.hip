@@ -473,13 +473,14 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     wq_off[r] = t * HK + 8 * ku;
     wq_lds[r] = t * LK + 8 * ku;
   }
-  // V slice (threads 0 .. 8 BV - 1) and U slice (8 BV .. 16 BV - 1)
+  // V and U slices: thread tid < 16 BV stages 4 elements of each (token s_t,
+  // columns s_v .. s_v + 3), so the transposing U writes are spread over every
+  // wave (the others repeat the last unit and do not store it)
   const bool s_store = tid < 16 * BV;
   const int su = s_store ? tid : 16 * BV - 1;
-  const bool is_u = su >= 8 * BV;
-  const int vu = is_u ? su - 8 * BV : su;
-  const int s_t = vu / (BV / 8), s_v = 8 * (vu % (BV / 8));
-  const __bf16* sbase = (is_u ? un : vin) + rowtok * V + v0;
+  const int s_t = su / (BV / 4), s_v = 4 * (su % (BV / 4));
+  const __bf16* vbase = vin + rowtok * V + v0;
+  const __bf16* ubase = un + rowtok * V + v0;
   const unsigned s_off = s_t * HV + s_v;
   const int nl1 = nlev > 0 ? nlev : 1;   // T = 64 has no inter-chunk level
   const int e2 = min(tid, nl1 * kGC - 1);
@@ -489,12 +490,14 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   // LDS wait counter and stall every LDS wait until it returns
   const rsrc_t grs = make_rsrc(gcum + rowtok + (size_t)(kGC - 1) * H, (size_t)T * H * 4);
 
-  u32x4 rw[KU], rq[KU], rk[KU], rsv, rp;
+  u32x4 rw[KU], rq[KU], rk[KU], rp;
+  uint2 rsv, rsu;
   TL rl;
   float rg;
   auto stage_load = [&](int jc) __attribute__((always_inline)) {
     const size_t tokoff = (size_t)jc * kGC * H;   // chunk jc's first token, times H
-    rsv = *(const u32x4*)(sbase + tokoff * V + s_off);
+    rsv = *(const uint2*)(vbase + tokoff * V + s_off);
+    rsu = *(const uint2*)(ubase + tokoff * V + s_off);
     rl = lrow[tokoff * L + l_off];
     rg = buf_load<float>(grs, 0, (unsigned)(tokoff * 4));
 #pragma unroll
@@ -511,13 +514,10 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   auto stage_store = [&]() __attribute__((always_inline)) {
     if (tid < nlev * kGC) s.lam[tid % nlev][tid / nlev] = to_f32<TL>(rl);
     if (s_store) {
-      if (is_u) {
-        const bf16x8 x = __builtin_bit_cast(bf16x8, rsv);
+      *(uint2*)(s.vs + s_t * LVS + s_v) = rsv;
+      const bf16x4 x = __builtin_bit_cast(bf16x4, rsu);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s.ut[(s_v + j) * LT + s_t] = x[j];
-      } else {
-        *(u32x4*)(s.vs + s_t * LVS + s_v) = rsv;
-      }
+      for (int j = 0; j < 4; ++j) s.ut[(s_v + j) * LT + s_t] = x[j];
     }
 #pragma unroll
     for (int r = 0; r < KU; ++r) {
@@ -536,7 +536,9 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   // slice (threads past the 64 x BV tile store through an empty range)
   constexpr int VG = BV / 4;
   const int ot = tid / VG, ov = 4 * (tid % VG);
-  const bool o_ok = !HSAVE && o != nullptr && ot < kGC;
+  // ot < kGC <=> tid < 64 VG <=> w < VG: a wave-uniform test, so the output
+  // descriptor is scalar (a per-lane one makes the store a loop over lanes)
+  const bool o_ok = !HSAVE && o != nullptr && w < VG;
   const rsrc_t ro = make_rsrc(o_ok ? (const void*)(o + rowtok * V + v0) : (const void*)gcum,
                               o_ok ? (size_t)T * H * V * sizeof(TO) : 0);
   const unsigned o_voff = ((o_ok ? ot : 0) * HV + ov) * sizeof(TO);

@@ -348,14 +348,17 @@ struct RsumSmem {
 template <int NP, typename TK, typename TL>
 __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
     const TK* __restrict__ q, const TK* __restrict__ dO, const float* __restrict__ gcin,
-    const TL* __restrict__ l, float* __restrict__ rsum, int T, int H, int L, int NT, int slog,
-    int NSEG, int nloc, int ntop, int ngrp) {
+    const TL* __restrict__ l, float* __restrict__ rsum, int B, int T, int H, int L, int NT,
+    int slog, int NSEG, int nloc, int ntop, int ngrp) {
   __shared__ __attribute__((aligned(16))) RsumSmem<NP> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const int grp = blockIdx.x % ngrp;
-  const int rest = blockIdx.x / ngrp;
-  const int h = rest % H, p = (rest / H) % NSEG, b = rest / (H * NSEG);
+  // grid: xcd_head_grid(B * NSEG, H, ngrp): the heads of one (batch, segment)
+  // share an XCD, so the lambda and g lines that interleave them are fetched once
+  const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, ngrp);
+  if (xm.grp >= B * NSEG) return;
+  const int grp = xm.slice;
+  const int h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h;
   const int c0 = p << slog, cend = min(c0 + (1 << slog), NT);
   const int e0 = 4 * grp;
@@ -1162,9 +1165,9 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ngrp = (ntop + 3) / 4;
     auto rk = mamba2_bwd_rsum_kernel<NP, TK, TL>;
-    hipLaunchKernelGGL(rk, dim3(rows * NSEG * ngrp), dim3(256), 0, stream, (const TK*)q,
-                       (const TK*)dO, gc, (const TL*)l, w.rsum, T, H, L, NT, slog, NSEG,
-                       nloc, ntop, ngrp);
+    hipLaunchKernelGGL(rk, dim3(xcd_head_grid(B * NSEG, H, ngrp)), dim3(256), 0, stream,
+                       (const TK*)q, (const TK*)dO, gc, (const TL*)l, w.rsum, B, T, H, L, NT,
+                       slog, NSEG, nloc, ntop, ngrp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {

@@ -137,9 +137,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
   const rsrc_t rgc = make_rsrc(gcum, MODE == kPrepFwd && w == 0 ? (size_t)nchunks * kGC * 4 : 0);
 
   // ---- stage a chunk: Q, K (l2-normalised on request), the cumsum of g, beta,
-  //      lambda -> LDS, then the next chunk's Q, K loads.  Called before the
-  //      walk and at the end of each chunk, so every wait for those loads sees
-  //      the same memory operations in flight on every path.
+  //      lambda -> LDS.  Called before the walk and at the end of each chunk.
+  //      The next chunk's loads are issued after the K K^T barrier of the
+  //      current one: issued here, right behind the previous chunk's output
+  //      stores, they queue in the CU's memory pipeline until those drain.
   auto stage = [&](int c) __attribute__((always_inline)) {
     const int hs = (c / NT) % H;
     const size_t t0 = tok_of(c);
@@ -158,7 +159,6 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     if (w == 1) s.beta[lane] = pb;
     if (tid < 7 * kGC) s.lam[tid % 7][tid / 7] = pl;
     __syncthreads();
-    fetch_qk(min(c + (int)gridDim.x, nchunks - 1));
     if (norm_qk) {
       // use_qk_l2norm_in_kernel (kernel.py:110-111): k / ||k|| and q scale / ||q||
       if (tid < 256) l2norm_rows<KD, LK>(s.k, 1.f, nullptr);
@@ -202,6 +202,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         }
     }
     __syncthreads();
+    fetch_qk(nxt);   // the next chunk's Q, K, g, beta, lambda (staged at the end)
 
     // ---- X = (I + A)^-1, fp32 ------------------------------------------------------
     tri_inv64_mfma<NTH>(A, X, s.wt.inv);

@@ -565,7 +565,6 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     // barrier, and the next chunk's staging rewrites the shared stage before its
     // first barrier
     sm.eg_own[tid] = ld.store(rg, s);
-    ld.load(rg, min(ic + 1, cend - 1));
     __syncthreads();
     // lane indices made opaque per chunk, so the LDS addresses of the phases are
     // recomputed (a few VALU ops) instead of held in VGPRs across the walk
@@ -606,6 +605,10 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       store_planes4<NP>(sm.a, t * kLd + 16 * jt + 4 * lq, out);
     }
     __syncthreads();
+    // the next chunk's loads, issued after phase 1 rather than at the chunk start,
+    // right behind the previous chunk's dq / dlambda stores, where their issue
+    // waits for those stores to drain
+    ld.load(rg, min(ic + 1, cend - 1));
 
     // ---- phase 2: dq^T[k-tile w][t] ----------------------------------------------
     floatx4 dqT[4];
@@ -918,7 +921,6 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
   int ic = cend - 1;
   do {
     ld.store(rg, s);
-    ld.load(rg, max(ic - 1, c0));
     // q . dq of this chunk's tokens (written by the dq kernel), needed by wave 0 at
     // the end of the chunk: loaded now so the load has the whole chunk to land
     const unsigned int vo_g = (unsigned int)lane * H * 4, so_g = (unsigned int)ic * kBT * H * 4;
@@ -952,6 +954,9 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
       }
     }
     __syncthreads();
+    // the previous chunk's loads, issued after phase 1 rather than at the chunk
+    // start, right behind the dk / dv / dg stores of the chunk before
+    ld.load(rg, max(ic - 1, c0));
 
     // ---- phase 2: dk^T (role 0) / dv^T (role 1) for the chunk's tokens s -------------
     typedef const __bf16 (*Planes)[kBT * kLd];

@@ -9,7 +9,7 @@ the BASELINE north-star shape B=4, T=16384, H=16, dk=dv=64, L=15, bf16
 q/k/v/lambda, fp32 g, inputs resident in HBM.  Each step first evicts the
 256 MB memory-side cache (a 1 GiB read, outside the timed events), then runs
 the forward between HIP events on the launch stream; ``value`` and the
-roofline use the median step, the back-to-back (warm)
+roofline use the median step (cold memory-side cache, median of the reps), the back-to-back (warm)
 figures are kept under ``timing``.  Prints one JSON line with the throughput
 (tokens/s), the HBM roofline (algorithmic bytes / median forward time), the
 other BASELINE configs (C1, C2, C2 bf16x3, C4 forward + backward, the GDN
@@ -156,7 +156,7 @@ class Evictor:
 
 
 def time_cold(fn, reps, stream, evict):
-    """BASELINE.md section 3 protocol: before each rep the memory-side cache is
+    """Cold-cache protocol: before each rep the memory-side cache is
     evicted (outside the events); each rep is bracketed by HIP events on the
     launch stream.  Returns the per-rep event times in seconds."""
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -377,7 +377,7 @@ def cpu_model():
 
 
 def cpu_baseline(seconds_budget=20.0):
-    """Host-CPU baselines of BASELINE.md section 3, all fp32 torch restatements
+    """Host-CPU baselines (the chunkwise and recurrent forms on the host cores), all fp32 torch restatements
     of the reference (the reference itself cannot run on the box):
     * chunkwise: oracle.mamba2.chunked_scan_fwd (the reference's chunkwise
       level-scan algorithm, chunkwise.py:1118-1275) at the full north-star, C1
@@ -429,9 +429,9 @@ def cpu_baseline(seconds_budget=20.0):
 
 def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, backward=False,
                       strong=False):
-    """Cold-cache median of one Mamba-2 chunkwise forward
+    """Cold-cache median (memory-side cache evicted before each rep) of one Mamba-2 chunkwise forward
     (or forward + backward through HAttentionFunction) at one BASELINE config,
-    with its roofline: HBM-bound by algorithmic bytes (SURVEY formulas).
+    with its roofline: HBM-bound by algorithmic bytes (q, k, v, g, lambda read and o written once).
     ``strong``: the strong hierarchy (HType.STRONG) on the same inputs."""
     from hattention.base import HType, HStruct
     from hattention.kernel import hattention_kernel

@@ -107,6 +107,39 @@ def test_forward_summaries_reused(T):
         assert mx < 1e-2 and fro < 2e-3, (name, mx, fro)
 
 
+def test_forward_workspace_kept_only_where_reused():
+    """chunkwise_fwd_keep returns its workspace only for the backward that can
+    take the summaries (bf16 q / k, K = V = 64, WEAK, several segments); a
+    backward that cannot use a passed workspace ignores it."""
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_bwd, chunkwise_fwd_keep
+    dev = torch.device("cuda:0")
+    print("[fwd_ws eligibility]", flush=True)
+    cases = [((1, 2048, 2, 64, 64, 12), torch.bfloat16, HType.WEAK, True),
+             ((1, 1024, 2, 64, 64, 11), torch.bfloat16, HType.WEAK, False),   # one segment
+             ((1, 2048, 2, 128, 64, 12), torch.bfloat16, HType.WEAK, False),  # K = 128
+             ((1, 2048, 2, 64, 128, 12), torch.bfloat16, HType.WEAK, False),  # V = 128
+             ((1, 2048, 2, 64, 64, 12), torch.float32, HType.WEAK, False),    # bf16x3
+             ((1, 2048, 2, 64, 64, 12), torch.bfloat16, HType.STRONG, False)]
+    for (B, T, H, K, V, L), dt, ht, keep in cases:
+        q, k, v, g, l, do = make_mamba2_inputs(B, T, H, K, V, L, seed=T + K + V, dtype=dt,
+                                               with_do=True)
+        xs = [x.to(dev) for x in (q, k, v, g, l, do)]
+        _, gc, _, fws = chunkwise_fwd_keep(*xs[:5], False, 2, ht, 64, False)
+        assert (fws is not None) == keep, ((B, T, H, K, V, L), dt, ht)
+    # an fp32 backward handed a bf16 forward's workspace runs its own summaries
+    q, k, v, g, l, do = make_mamba2_inputs(1, 2048, 2, 64, 64, 12, seed=31, with_do=True)
+    xs = [x.to(dev) for x in (q, k, v, g, l, do)]
+    _, gc, _, fws = chunkwise_fwd_keep(*xs[:5], False, 2, HType.WEAK, 64, False)
+    xf = [x.float() for x in xs]
+    a = chunkwise_bwd(xf[0], xf[1], xf[2], gc, xf[4], xf[5], False, 2, HType.WEAK, 64,
+                      fwd_ws=fws)
+    b = chunkwise_bwd(xf[0], xf[1], xf[2], gc, xf[4], xf[5], False, 2, HType.WEAK, 64)
+    torch.cuda.synchronize()
+    for name, x, y in zip(NAMES, a, b):
+        assert torch.equal(x, y), name
+
+
 def test_forward_summaries_grouped():
     # G < H: the summaries are per head (v and g are), whatever the q / k groups
     _run(1, 2048, 4, 64, 64, 12, G=2, seed=77, reuse=True)

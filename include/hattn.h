@@ -154,7 +154,7 @@ int hattn_mamba2_chunkwise_bwd(const void* q, const void* k, const void* v, cons
  * No counterpart in the reference (its backward recomputes its states,
  * chunkwise.py:1371-1384); for callers that keep the forward's workspace until
  * the backward, as HAttentionFunction does between its forward and backward
- * (kernel.py:125-244).  Same arguments, results and status codes as
+ * (kernel.py:32-244).  Same arguments, results and status codes as
  * hattn_mamba2_chunkwise_bwd, plus fwd_workspace / fwd_workspace_bytes: the
  * workspace of the hattn_mamba2_chunkwise_fwd call (bf16 q / k, WEAK) on the
  * same q, k, v, g, l, with the same B, T, H, K = V = 64 and L, unchanged

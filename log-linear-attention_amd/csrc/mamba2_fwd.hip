@@ -839,96 +839,6 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       // zeroed so the workspace (which the backward may reuse) holds no stale value
       __builtin_amdgcn_raw_buffer_store_b32(0u, rsd, (unsigned int)p * 4, 0, kCohStore);
     }
-    // ---- look-back: the earlier segments of this row have published ----
-    if (p > 0) {
-      if (tid < p) {
-        const unsigned int* f = sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + tid;
-        int spins = 0;
-        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
-               ++spins < kSpinLimit)
-          __builtin_amdgcn_s_sleep(2);
-      }
-      __syncthreads();
-    }
-  }
-
-  // ---- top levels: Htop_e(p) for the levels segment p reads -> LDS (bf16, [v][k]) ----
-  // Htop_e(p) = sum_{q in block} exp(P[p] - P[q + 1]) Sum(q), block = the 2^e
-  // segments before p's half of its aligned 2^(e+1) block, P[x] = sum_{r < x} D_r
-  // (the top-level scan of chunkwise.py:199-247 over whole segments; the blocks
-  // of the levels p reads partition [0, p)).  The summaries were just written
-  // by the segment-summary kernel and are read from L2 / MALL.
-  if (ntop > 0 && (p > 0 || is_final_seg)) {
-    float* pre = (float*)sm.a;   // P[0 .. p + 1]; the A tile is free until the first chunk
-    if (w == 0) {
-      float carry = 0.f;
-      for (int base = 0; base <= p + 1; base += 64) {
-        const int qq = base + lane;
-        const float x = qq <= p ? segd1(qq) : 0.f;
-        const float y = chunk_cumsum(x);
-        if (qq <= p + 1) pre[qq] = carry + y - x;
-        carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 63));
-      }
-    }
-    __syncthreads();
-    // thread: V columns 4 (tid & 15) .. + 3, k rows (tid >> 4) + 16 i
-    const int v4 = 4 * (tid & 15), kr = tid >> 4;
-    const size_t sp = (size_t)kr * V + vcol0 + v4;   // element offset in the row's summaries
-    const size_t qstride = (size_t)kKD * V;
-    const float pp = pre[p];
-    for (int e2 = 0; e2 < ntop && p > 0; ++e2) {
-      if (!((p >> e2) & 1)) continue;
-      const int lo = (p >> (e2 + 1)) << (e2 + 1);
-      floatx4 hacc[4] = {zero4(), zero4(), zero4(), zero4()};
-      for (int q0 = lo; q0 < lo + (1 << e2); q0 += 4) {
-        floatx4 xs[4][4];
-        float sc[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int qs = min(q0 + u, lo + (1 << e2) - 1);
-          sc[u] = q0 + u < lo + (1 << e2) ? fexp(pp - pre[qs + 1]) : 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xs[u][i] = sum4(sp + qs * qstride + (size_t)16 * i * V);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) hacc[i][c] += sc[u] * xs[u][i][c];
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + top_idx(v4 + c, kr + 16 * i)] = (__bf16)hacc[i][c];
-    }
-    if (is_final_seg) {
-      // final states of the top levels (chunkwise.py:229-279): a level the last
-      // chunk reads holds its block decayed over segment p; one it writes holds
-      // segments [lo, p] decayed to the end of p
-      const int vc = vcol0 + 16 * w + ln0;
-      for (int e2 = 0; e2 < ntop; ++e2) {
-        const bool reads = (p >> e2) & 1;
-        const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
-        const int hi = reads ? lo + (1 << e2) : p + 1;
-        floatx4 hacc[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) hacc[m] = zero4();
-        for (int qs = lo; qs < hi; ++qs) {
-          const float sc = fexp(pre[p + 1] - pre[qs + 1]);
-          const size_t src = qs * qstride + vc;
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) hacc[m][i] += sc * sum1(src + (size_t)(16 * m + 4 * lq0 + i) * V);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            htb[((size_t)(16 * m + 4 * lq0 + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i];
-      }
-    }
   }
 
   // ---- per-row buffer descriptors and per-lane offsets ---------------------------
@@ -1116,20 +1026,115 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     for (int m = 0; m < 4; ++m) st[e][m] = zero4();
   }
 
-  // the two A tiles above the diagonal that the 32-wide s steps of A V read
-  // ((t-tile 0, s-tile 1) and (2, 3)) stay zero for the whole walk
-  __syncthreads();   // the A tile may have served as scratch for the final states
-  {
-    const int r = tid >> 3, c = 4 * (tid & 3), tile = (tid >> 2) & 1;
-    *(bf16x4*)(sm.a + sidx<swz_a>(32 * tile + (r & 15), 16 + 32 * tile + c)) = bf16x4{};
-  }
   // Pipeline: chunk j + 1 is staged in LDS right after phase 1 of chunk j (from
   // then on chunk j's stage is dead except lambda', which is double-buffered),
   // and chunk j + 2's loads are issued at the same point, so they have a whole
   // chunk period to land and a chunk needs two barriers instead of three.
+  // the first chunk's loads go out before the look-back and the top-level
+  // build, so their latency hides behind the wait for the earlier segments
   load(0, -1);
   if (LAYER) __syncthreads();   // L[h] staged in LDS
   dt_xform();
+  if constexpr (FUSED) {
+    // ---- look-back: the earlier segments of this row have published ----
+    if (p > 0) {
+      if (tid < p) {
+        const unsigned int* f = sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + tid;
+        int spins = 0;
+        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
+               ++spins < kSpinLimit)
+          __builtin_amdgcn_s_sleep(2);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- top levels: Htop_e(p) for the levels segment p reads -> LDS (bf16, [v][k]) ----
+  // Htop_e(p) = sum_{q in block} exp(P[p] - P[q + 1]) Sum(q), block = the 2^e
+  // segments before p's half of its aligned 2^(e+1) block, P[x] = sum_{r < x} D_r
+  // (the top-level scan of chunkwise.py:199-247 over whole segments; the blocks
+  // of the levels p reads partition [0, p)).  The summaries were just written
+  // by the segment-summary kernel and are read from L2 / MALL.
+  if (ntop > 0 && (p > 0 || is_final_seg)) {
+    float* pre = (float*)sm.a;   // P[0 .. p + 1]; the A tile is free until the first chunk
+    if (w == 0) {
+      float carry = 0.f;
+      for (int base = 0; base <= p + 1; base += 64) {
+        const int qq = base + lane;
+        const float x = qq <= p ? segd1(qq) : 0.f;
+        const float y = chunk_cumsum(x);
+        if (qq <= p + 1) pre[qq] = carry + y - x;
+        carry += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, y), 63));
+      }
+    }
+    __syncthreads();
+    // thread: V columns 4 (tid & 15) .. + 3, k rows (tid >> 4) + 16 i
+    const int v4 = 4 * (tid & 15), kr = tid >> 4;
+    const size_t sp = (size_t)kr * V + vcol0 + v4;   // element offset in the row's summaries
+    const size_t qstride = (size_t)kKD * V;
+    const float pp = pre[p];
+    for (int e2 = 0; e2 < ntop && p > 0; ++e2) {
+      if (!((p >> e2) & 1)) continue;
+      const int lo = (p >> (e2 + 1)) << (e2 + 1);
+      floatx4 hacc[4] = {zero4(), zero4(), zero4(), zero4()};
+      for (int q0 = lo; q0 < lo + (1 << e2); q0 += 4) {
+        floatx4 xs[4][4];
+        float sc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int qs = min(q0 + u, lo + (1 << e2) - 1);
+          sc[u] = q0 + u < lo + (1 << e2) ? fexp(pp - pre[qs + 1]) : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[u][i] = sum4(sp + qs * qstride + (size_t)16 * i * V);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) hacc[i][c] += sc[u] * xs[u][i][c];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + top_idx(v4 + c, kr + 16 * i)] = (__bf16)hacc[i][c];
+    }
+    if (is_final_seg) {
+      // final states of the top levels (chunkwise.py:229-279): a level the last
+      // chunk reads holds its block decayed over segment p; one it writes holds
+      // segments [lo, p] decayed to the end of p
+      const int vc = vcol0 + 16 * w + ln0;
+      for (int e2 = 0; e2 < ntop; ++e2) {
+        const bool reads = (p >> e2) & 1;
+        const int lo = reads ? (p >> (e2 + 1)) << (e2 + 1) : (p >> e2) << e2;
+        const int hi = reads ? lo + (1 << e2) : p + 1;
+        floatx4 hacc[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) hacc[m] = zero4();
+        for (int qs = lo; qs < hi; ++qs) {
+          const float sc = fexp(pre[p + 1] - pre[qs + 1]);
+          const size_t src = qs * qstride + vc;
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hacc[m][i] += sc * sum1(src + (size_t)(16 * m + 4 * lq0 + i) * V);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            htb[((size_t)(16 * m + 4 * lq0 + i) * V + vc) * L + 7 + nloc + e2] = hacc[m][i];
+      }
+    }
+  }
+
+  // the two A tiles above the diagonal that the 32-wide s steps of A V read
+  // ((t-tile 0, s-tile 1) and (2, 3)) stay zero for the whole walk
+  __syncthreads();   // the A tile may have served as scratch for the top-level build
+  {
+    const int r = tid >> 3, c = 4 * (tid & 3), tile = (tid >> 2) & 1;
+    *(bf16x4*)(sm.a + sidx<swz_a>(32 * tile + (r & 15), 16 + 32 * tile + c)) = bf16x4{};
+  }
   store(0, 0);
   lam_xform(0);
   // The loads and LDS staging of chunks 1, j + 1, j + 2 are unconditional (the

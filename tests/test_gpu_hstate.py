@@ -374,3 +374,38 @@ def test_stream_handle_is_the_current_stream():
         assert _lib.stream_handle(dev) == s.cuda_stream
         assert _lib.stream_handle(torch.device("cuda")) == s.cuda_stream
     assert _lib.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+
+
+def test_launches_follow_a_side_stream():
+    """A decode step and a chunkwise forward issued inside a torch.cuda.stream
+    context run on that stream (the binding passes the current stream) and
+    give bit-identical results to the same calls on the default stream."""
+    from hattention.base import HType, HStruct
+    from hattention.chunkwise import chunkwise_fwd
+    from hattention.kernel import hattention_step
+    from hattention.recurrent import HState
+    dev = torch.device("cuda:0")
+    B, T, H, K, V, L = 2, 2048, 2, 64, 64, 12
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=41, device=dev)
+
+    def run():
+        o, gc, _ = chunkwise_fwd(q, k, v, g, l, False, 2, HType.WEAK, 64, False)
+        S = HState(2, HType.WEAK, HStruct.MAMBA2, (B, H, K, V, L + 1), torch.float32, dev)
+        lx = torch.cat([l, l[..., :1]], dim=-1)
+        outs = []
+        for t in range(8):
+            ot, _ = hattention_step(S, q[:, t].contiguous(), k[:, t].contiguous(),
+                                    v[:, t].contiguous(), None, g[:, t].contiguous(),
+                                    lx[:, t].contiguous(), None, 2, HType.WEAK, HStruct.MAMBA2)
+            outs.append(ot)
+        return [o, gc, torch.stack(outs), S.states]
+
+    ref = run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        side = run()
+    s.synchronize()
+    for i, (a, b) in enumerate(zip(side, ref)):
+        assert torch.equal(a, b), i

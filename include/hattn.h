@@ -113,6 +113,32 @@ int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void*
                                        int level_base, int htype, int chunk_size, void* stream);
 
 /*
+ * Health word of the last bf16 hattn_mamba2_chunkwise_fwd on this workspace
+ * (no counterpart in the reference, whose forward is a sequence of launches
+ * with no cross-workgroup waits).  The single-pass forward waits for the
+ * segment summaries of earlier workgroups with a bounded poll; a wait that
+ * gives up sets bit 0 (1 = look-back timeout) and that workgroup writes NaN
+ * over its part of o, g_cumsum and ht.  A timeout means the results are
+ * invalid (a lost flag, or two calls overlapping on one workspace or on the
+ * no-allocation entry point's static scratch).  Copies the word to *status
+ * and synchronises `stream` (a diagnostic, not for the hot path); 0 when the
+ * sizes have one segment (no waits).  For hattn_mamba2_chunkwise_fwd_noalloc,
+ * whose workspace is not exported, the NaN outputs are the signal.
+ */
+int hattn_mamba2_chunkwise_fwd_status(const void* workspace, int B, int T, int H, int V,
+                                      unsigned int* status, void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: sets the look-back controls of
+ * the later forward launches of this process.  spin_limit: polls before a
+ * wait gives up (<= 0 restores the default, about 1 s); publish = 0 makes the
+ * summary phase skip its flags, so every look-back wait gives up.  With both
+ * the tests exercise the timeout path while every kernel still exits
+ * normally.  Not thread-safe with respect to concurrent forward calls.
+ */
+void hattn_debug_lookback(int spin_limit, int publish);
+
+/*
  * Log-linear Mamba-2 chunkwise backward.
  *
  * Replaces hattention/chunkwise.py:1286-1597 `chunkwise_bwd(q, k, v, g, l, do,

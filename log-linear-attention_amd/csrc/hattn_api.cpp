@@ -66,6 +66,8 @@ hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, 
                                    int* unsupported);
 void hattn_mamba2_fwd_ws_summaries(void* ws, int B, int T, int H, int V, const float** sums,
                                    const float** segd);
+void hattn_mamba2_fwd_set_lookback(int spin_limit, int publish);
+const unsigned int* hattn_mamba2_fwd_status_word(const void* ws, int B, int T, int H, int V);
 
 hipError_t hattn_hstate_step_launch(float* states, int* counts, const void* q, const void* k,
                                     const void* v, const void* beta, const float* g,
@@ -186,12 +188,17 @@ size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, i
   return a > b ? a : b;
 }
 
-int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
-                               const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
-                               int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
-                               int dtype_l, int dtype_o, int level_base, int htype,
-                               int chunk_size, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+}  // extern "C"
+
+// The forward behind both entry points.  noalloc: the workspace is the static
+// scratch of hattn_mamba2_chunkwise_fwd_noalloc, looked up (and its capacity
+// checked) after every other check, so a bad shape reports the same status
+// through either entry point.
+static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const float* g,
+                           const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
+                           int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
+                           int dtype_l, int dtype_o, int level_base, int htype, int chunk_size,
+                           void* workspace, size_t workspace_bytes, bool noalloc, void* stream) {
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
@@ -256,6 +263,17 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
     return st;
   if (!q || !k || !v || !g || !l || !o) return fail(HATTN_ERR_VALUE, "null tensor pointer");
   const size_t need = hattn_mamba2_fwd_ws_bytes(B, T, H, V, x3);
+  if (noalloc && need > 0) {
+    const size_t cap = hattn_mamba2_fwd_static_scratch_bytes();
+    if (need > cap)
+      return fail(HATTN_ERR_VALUE,
+                  "these sizes need %zu bytes of scratch, above the %zu-byte static scratch of "
+                  "hattn_mamba2_chunkwise_fwd_noalloc (use hattn_mamba2_chunkwise_fwd)",
+                  need, cap);
+    const hipError_t e = hattn_mamba2_fwd_static_scratch(&workspace);
+    if (e != hipSuccess) return check_hip(e, "static scratch address (hipGetSymbolAddress)");
+    workspace_bytes = cap;
+  }
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
@@ -269,28 +287,52 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
   return check_hip(e, "hattn_mamba2_chunkwise_fwd launch");
 }
 
+extern "C" {
+
+int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
+                               const void* l, void* o, float* g_cumsum, float* ht, int B, int T,
+                               int G, int H, int K, int V, int L, int dtype_qk, int dtype_v,
+                               int dtype_l, int dtype_o, int level_base, int htype,
+                               int chunk_size, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return mamba2_fwd_impl(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, K, V, L, dtype_qk, dtype_v,
+                         dtype_l, dtype_o, level_base, htype, chunk_size, workspace,
+                         workspace_bytes, false, stream);
+}
+
 int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void* v,
                                        const float* g, const void* l, void* o, float* g_cumsum,
                                        float* ht, int B, int T, int G, int H, int K, int V, int L,
                                        int dtype_qk, int dtype_v, int dtype_l, int dtype_o,
                                        int level_base, int htype, int chunk_size, void* stream) {
-  // the shape checks of the allocating entry point come first, so a bad shape
-  // reports the same status; then the workspace must fit the static scratch
-  const size_t need = hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, K, V, L);
-  const size_t cap = hattn_mamba2_fwd_static_scratch_bytes();
-  if (B > 0 && T >= 64 && T % 64 == 0 && H > 0 && V > 0 && need > cap)
-    return fail(HATTN_ERR_VALUE,
-                "these sizes need %zu bytes of scratch, above the %zu-byte static scratch of "
-                "hattn_mamba2_chunkwise_fwd_noalloc (use hattn_mamba2_chunkwise_fwd)",
-                need, cap);
-  void* ws = nullptr;
-  if (need > 0) {
-    const hipError_t e = hattn_mamba2_fwd_static_scratch(&ws);
-    if (e != hipSuccess) return check_hip(e, "static scratch address (hipGetSymbolAddress)");
+  // HType.STRONG takes no workspace; WEAK uses the static scratch, checked
+  // against its capacity after the shape and dtype checks
+  return mamba2_fwd_impl(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, K, V, L, dtype_qk, dtype_v,
+                         dtype_l, dtype_o, level_base, htype, chunk_size, nullptr, 0, true,
+                         stream);
+}
+
+int hattn_mamba2_chunkwise_fwd_status(const void* workspace, int B, int T, int H, int V,
+                                      unsigned int* status, void* stream) {
+  if (status == nullptr) return fail(HATTN_ERR_VALUE, "null status pointer");
+  *status = 0;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0 || V % 64 != 0)
+    return fail(HATTN_ERR_VALUE, "sizes B=%d T=%d H=%d V=%d", B, T, H, V);
+  if (workspace == nullptr) {
+    if (hattn_mamba2_fwd_ws_bytes(B, T, H, V, 0) > 0)
+      return fail(HATTN_ERR_VALUE, "null workspace for sizes that have one");
+    return ok();
   }
-  return hattn_mamba2_chunkwise_fwd(q, k, v, g, l, o, g_cumsum, ht, B, T, G, H, K, V, L, dtype_qk,
-                                    dtype_v, dtype_l, dtype_o, level_base, htype, chunk_size, ws,
-                                    need > 0 ? cap : 0, stream);
+  const unsigned int* word = hattn_mamba2_fwd_status_word(workspace, B, T, H, V);
+  if (word == nullptr) return ok();   // one segment: no look-back
+  hipError_t e = hipMemcpyAsync(status, word, sizeof(unsigned int), hipMemcpyDeviceToHost,
+                                (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  return check_hip(e, "hattn_mamba2_chunkwise_fwd_status");
+}
+
+void hattn_debug_lookback(int spin_limit, int publish) {
+  hattn_mamba2_fwd_set_lookback(spin_limit, publish);
 }
 
 size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L,

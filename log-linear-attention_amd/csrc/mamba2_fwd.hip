@@ -35,6 +35,7 @@
 // the Q fragments (any bijection of the contraction index works if both
 // operands use it).  K^T and V fragments of the contractions over t come from
 // row-major LDS tiles through the transposing LDS read.
+#include <atomic>
 #include <mutex>
 
 #include "mamba2_common.h"
@@ -499,6 +500,11 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
 //   A     f = bits 1, 2 of r, and bit 3 onto unit bit 0: conflict-free
 //         row-fragment reads; the 8-byte writes of the MFMA D layout two-way.
 // Staging writes (one row of 8 units per 8 lanes) are conflict-free for all.
+// lambda columns a staging wave may write per token row: three 16-byte bf16
+// pieces (or six fp32 pieces) cover 24 columns, plus one for a misaligned row
+constexpr int kLamCols = 25;
+static_assert(kMaxLU + 1 < kLamCols, "lambda pieces cover every level");
+
 struct Bf16Smem {
   __bf16 q[kBT * 64];         // Q[t][k]
   __bf16 k[kBT * 64];         // K[s][k]
@@ -506,11 +512,14 @@ struct Bf16Smem {
   __bf16 a[kBT * 64];         // A[t][s] = (S o M)[t][s]
   float gc[kBT];              // log2(e) * chunk-local inclusive cumsum of g
   float wt[kBT];              // exp(Gc_last - Gc_s)
-  // lambda[t = 16nt + ln][lev] at [lev][4ln + nt] and exp(Gc_t) at [4ln + nt],
-  // double-buffered: chunk j + 1's are staged while chunk j's are read.  Row
-  // kMaxLU of each buffer is a per-lane sink for the lambda columns past the
-  // row's levels, so a staged value's slot does not depend on the chunk
-  float lam[2][(kMaxLU + 1) * kBT];
+  // lambda[t = 16nt + ln][lev] at row lev + 1, column 4ln + nt, and exp(Gc_t)
+  // at [4ln + nt], double-buffered: chunk j + 1's are staged while chunk j's
+  // are read.  A staging lane writes all the values of its 16-byte lambda
+  // pieces, columns -1 .. kLamCols - 2 of its token row (the row's misalignment
+  // shifts them by one), to rows 0 .. kLamCols - 1: a value's row is a
+  // compile-time offset from a per-lane base, and the rows outside 1 .. lu hold
+  // values nobody reads (the neighbouring head's lambda or zeros)
+  float lam[2][kLamCols * kBT];
   float eg[2][kBT];
   float lpar[32];             // layer mode: L[h, 0 .. L - 1] (lambda parameters of the head)
   __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
@@ -725,17 +734,41 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const f
 }
 
 // FUSED: one launch computes everything (single pass).  Work items (batch,
-// segment, head, V block) are handed out in that order by a ticket counter, so
-// a workgroup only ever waits for work that a running workgroup has already
-// claimed.  Phase A streams the segment's K, V, g and publishes Sum(p) and D_p
+// segment, head, V block) are handed out by eight ticket counters, one per
+// XCD (workgroup blockIdx.x goes to XCD blockIdx.x % 8): the groups (batch,
+// segment) g = x, x + 8, x + 16, .. go to XCD x, in that order, each with all
+// its heads and V blocks, so the cache lines of lambda and g that interleave
+// the heads of a token row are fetched into one L2.  A workgroup only ever
+// waits for a smaller group; each XCD claims its groups in increasing order,
+// so the smallest unfinished group is always claimed by running workgroups
+// whose waits are all satisfied, and the launch cannot deadlock.
+// Phase A streams the segment's K, V, g and publishes Sum(p) and D_p
 // (coherent stores, then a flag); the workgroup then waits for the flags of
 // the earlier segments of its row and builds its top-level states from their
 // summaries (coherent loads).  The walk re-reads K and V shortly after phase A,
 // from the L2 / memory-side cache.  Not FUSED: the summaries come from
 // mamba2_seg_sum_kernel (or there is a single segment and none are needed).
-// sync: [0] ticket counter, [1 ..] one flag per (row, V block, segment); zeroed
-// by mamba2_fwd_sync_init_kernel before the launch.
-constexpr int kSpinLimit = 1 << 24;   // ~1 s of polling: a lost flag ends the wait, never hangs
+//
+// sync (zeroed by mamba2_fwd_sync_init_kernel before the launch): the ticket
+// counter of XCD x at [16 x], the status word at [kSyncStatus], one flag per
+// (row, V block, segment) from [kSyncHdr].  The look-back wait is bounded
+// (spin_limit polls, ~1 s by default): a wait that gives up sets bit 0 of the
+// status word and the workgroup writes NaN over its outputs (o, g_cumsum, its
+// part of ht) instead of computing them, so a lost flag (or a call that
+// overlaps another on the same workspace) shows as NaN, never as a hang or as
+// plausible wrong numbers.
+constexpr int kSpinLimit = 1 << 24;
+constexpr int kSyncStatus = 128;
+constexpr int kSyncHdr = 144;
+constexpr unsigned int kStatusLookbackTimeout = 1u;
+
+// Look-back controls: spin_limit polls before a wait gives up, and publish = 0
+// suppresses the flags of phase A (every later wait then gives up): the test
+// hook hattn_debug_lookback sets both to exercise the timeout path.
+struct LookbackCtl {
+  int spin_limit;
+  int publish;
+};
 
 __global__ void mamba2_fwd_sync_init_kernel(unsigned int* __restrict__ sync, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -753,7 +786,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, float* __restrict__ ht, float* __restrict__ sums,
     float* __restrict__ segd, unsigned int* __restrict__ sync, int B, int T, int G, int H,
-    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state, LayerArgs la) {
+    int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state, LayerArgs la,
+    LookbackCtl lbc) {
   static_assert(!LAYER || sizeof(TV) == 2, "layer mode: bf16 x");
   constexpr int kPl = kKD * 64;                           // one top-level state tile
   constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
@@ -762,18 +796,26 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq0 = lane >> 4, ln0 = lane & 15;
   int h, p, b, vblk;
+  __shared__ int lb_fail;   // a look-back wait of this workgroup gave up
   if constexpr (FUSED) {
     __shared__ int ticket;
-    if (tid == 0)
-      ticket = (int)__hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int xcd = blockIdx.x & 7;
+    if (tid == 0) {
+      ticket = (int)__hip_atomic_fetch_add(sync + 16 * xcd, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      lb_fail = 0;
+    }
     __syncthreads();
-    int r = ticket;   // (batch, segment, head, V block), V block fastest
+    // ticket -> (group xcd + 8 i, head, V block), V block fastest; the grid has
+    // as many workgroups per XCD as the XCD with the most groups has items
+    const int per = H * nvb64;
+    const int grp = xcd + 8 * (ticket / per);
+    if (grp >= B * NSEG) return;
+    const int r = ticket % per;
     vblk = r % nvb64;
-    r /= nvb64;
-    h = r % H;
-    r /= H;
-    p = r % NSEG;
-    b = r / NSEG;
+    h = r / nvb64;
+    p = grp % NSEG;
+    b = grp / NSEG;
   } else {
     // grid: xcd_head_grid(B * NSEG, H, nvb64)
     const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);
@@ -831,9 +873,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
                                               (unsigned int)p * 4, 0, kCohStore);
       __builtin_amdgcn_s_waitcnt(0);   // this thread's summary stores are complete
       __syncthreads();
-      if (tid == 0)
-        __hip_atomic_store(sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + p, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && lbc.publish)
+        __hip_atomic_store(sync + kSyncHdr + ((size_t)row * nvb64 + vblk) * NSEG + p, 1u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (tid == 0) {
       // no later segment reads the last one's summary; its log-decay slot is
       // zeroed so the workspace (which the backward may reuse) holds no stale value
@@ -895,7 +937,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   if (LAYER && tid < L) sm.lpar[tid] = la.Lp[h * L + tid];   // read after the first barrier
   uint4 lamr[kLP];
   const int lslot = 4 * (lane & 15) + (lane >> 4);   // this lane's token row t, permuted
-  const int junk_rel = kMaxLU * kBT + lane - lslot;  // the sink row, relative to lslot
+  // value i of piece r goes to column kPE (w - 1 + 3 r) + i - lmis, staged at
+  // row column + 1: element offset lam_lane + (3 kPE r + i) kBT of the buffer
+  const int lam_lane = lslot + (1 - lmis + kPE * (w - 1)) * kBT;
   // part < 0: everything; parts 0, 1, 2: q / k / v, g and lambda (the loads of
   // chunk j + 2 are spread over phase 2 of chunk j, between its MFMA groups)
   auto load = [&](int j, int part) {
@@ -955,23 +999,18 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       sm.eg[par][4 * ln0 + lq0] = fexp(x);
       gx = x;
     } else {
-      // value i of piece pc is column kPE * pc + i - lmis; columns outside
-      // [0, lu) go to the lane's junk slot, so every lane stores unconditionally
-      // through one LDS base (no divergent branches, no generic pointers)
-      float* lamw = sm.lam[par] + lslot;
+      // every value of the lane's pieces is stored, at a compile-time offset
+      // from one per-lane base (no compares, no divergent branches)
+      float* lamw = sm.lam[par] + lam_lane;
 #pragma unroll
       for (int r = 0; r < kLP; ++r) {
-        const int col0 = kPE * (w - 1 + 3 * r) - lmis;
         const unsigned int* u = (const unsigned int*)&lamr[r];
 #pragma unroll
         for (int i = 0; i < kPE; ++i) {
           float val;
           if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
           else val = __builtin_bit_cast(float, u[i]);
-
-          const int col = col0 + i;
-          const int idx = (unsigned int)col < (unsigned int)lu ? col * kBT : junk_rel;
-          lamw[idx] = val;
+          lamw[(3 * kPE * r + i) * kBT] = val;
         }
       }
     }
@@ -999,7 +1038,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   auto lam_xform = [&](int jj) {
     if constexpr (LAYER) {
       if (w > 0) {
-        float* lamw = sm.lam[jj & 1] + lslot;
+        float* lamw = sm.lam[jj & 1] + lam_lane;
 #pragma unroll
         for (int r = 0; r < kLP; ++r) {
           const int col0 = kPE * (w - 1 + 3 * r) - lmis;
@@ -1007,9 +1046,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           for (int i = 0; i < kPE; ++i) {
             const int col = col0 + i;
             if ((unsigned int)col < (unsigned int)lu) {
-              float val = lambda_of(sm.lpar[col], lamw[col * kBT], la.mode);
+              const int off = (3 * kPE * r + i) * kBT;
+              float val = lambda_of(sm.lpar[col], lamw[off], la.mode);
               if (la.lam_bf16) val = (float)(__bf16)val;
-              lamw[col * kBT] = val;
+              lamw[off] = val;
             }
           }
         }
@@ -1039,13 +1079,38 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     // ---- look-back: the earlier segments of this row have published ----
     if (p > 0) {
       if (tid < p) {
-        const unsigned int* f = sync + 1 + ((size_t)row * nvb64 + vblk) * NSEG + tid;
-        int spins = 0;
-        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
-               ++spins < kSpinLimit)
+        const unsigned int* f = sync + kSyncHdr + ((size_t)row * nvb64 + vblk) * NSEG + tid;
+        unsigned int fv = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int spins = 0; fv == 0u && spins < lbc.spin_limit; ++spins) {
           __builtin_amdgcn_s_sleep(2);
+          fv = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (fv == 0u) lb_fail = 1;
       }
       __syncthreads();
+      if (lb_fail) {
+        // the wait gave up: report it and poison this item's outputs
+        if (tid == 0)
+          __hip_atomic_fetch_or(sync + kSyncStatus, kStatusLookbackTimeout, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        const float qnan = __builtin_nanf("");
+        // o (layer mode: y): 64 rows x 64 columns per chunk, 8 columns per thread and row
+        for (int jj = 0; jj < nch; ++jj)
+          for (int u = tid; u < kBT * 8; u += 256) {
+            const unsigned int t = (unsigned int)(c0 + jj) * kBT + (u >> 3);
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+              buf_store<TO>(from_f32<TO>(qnan), ro,
+                            (t * vstr + 8 * (u & 7) + c) * (unsigned int)sizeof(TO), 0);
+          }
+        for (int t = lane; t < nch * kBT; t += 64)   // wave 0 (the others' range is empty)
+          buf_store<float>(qnan, rgc, 0, (((unsigned int)c0 * kBT + t) * H) * 4);
+        if (is_final_seg)
+          for (int u = tid; u < kKD * 64; u += 256)
+            for (int e = 0; e < nlev; ++e)
+              htb[((size_t)(u >> 6) * V + vcol0 + (u & 63)) * L + 7 + e] = qnan;
+        return;
+      }
     }
   }
 
@@ -1185,17 +1250,17 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     // ---- phase 1: A = S o M, and the chunk's K^T diag(w) V -------------------------
     floatx4 kv[4];
     switch (w) {
-      case 0: bf16_p1<0>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
-      case 1: bf16_p1<1>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
-      case 2: bf16_p1<2>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
-      default: bf16_p1<3>(sm, lb, sm.lam[j & 1], qa, vt0, vt1, kv, lq, ln); break;
+      case 0: bf16_p1<0>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      case 1: bf16_p1<1>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      case 2: bf16_p1<2>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      default: bf16_p1<3>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
     }
     const float glr = sm.gc[kBT - 1];   // chunk log2-decay
     __syncthreads();   // A visible; chunk j's stage (but lambda') no longer read
     store(min(j + 1, nch - 1), (j + 1) & 1);
     const int jn = min(j + 2, nch - 1);
     load(jn, 0);
-    const float* lpr = sm.lam[j & 1] + 7 * kBT;
+    const float* lpr = sm.lam[j & 1] + 8 * kBT;   // level 7 (row 8)
     const floatx4 egr = *(const floatx4*)(sm.eg[j & 1] + 4 * ln);   // exp(Gc_t), t = 16nt + ln
 
     // ---- phase 2: o^T[v = 16w + 4lq + i][t = 16nt + ln] ------------------------------
@@ -1360,7 +1425,7 @@ struct FwdWs {
   float* segd;
   float* sums;
   __bf16* htop;
-  unsigned int* sync;   // fused bf16 forward: ticket counter + one flag per (row, V block, segment)
+  unsigned int* sync;   // fused bf16 forward: ticket counters, status word, one flag per (row, V block, segment)
   int nsync;
   size_t bytes;
 };
@@ -1390,7 +1455,7 @@ FwdWs fwd_ws_layout(void* base, int B, int T, int H, int V, int x3) {
   w.htop = (__bf16*)(p + a + b);
   w.bytes = a + b + c;
   if (!x3) {
-    w.nsync = 1 + (int)(rows * nvb * NSEG);
+    w.nsync = hattn::kSyncHdr + (int)(rows * nvb * NSEG);
     w.sync = (unsigned int*)(p + a + b);
     w.bytes = a + b + (((size_t)w.nsync * 4 + 255) & ~(size_t)255);
   }
@@ -1459,7 +1524,28 @@ int hattn_mamba2_fwd_max_levels(int x3) {
   return kMaxLocX3 + (ntop < kMaxTop ? ntop : kMaxTop);
 }
 
+// Look-back controls of the fused forward launches (test hook; the defaults
+// are the production values).
+namespace {
+std::atomic<int> g_spin_limit{hattn::kSpinLimit};
+std::atomic<int> g_publish{1};
+}  // namespace
+
+void hattn_mamba2_fwd_set_lookback(int spin_limit, int publish) {
+  g_spin_limit.store(spin_limit > 0 ? spin_limit : hattn::kSpinLimit);
+  g_publish.store(publish ? 1 : 0);
+}
+
+// Where the fused forward's status word sits in its workspace (null when the
+// sizes have a single segment and the forward has no look-back).
+const unsigned int* hattn_mamba2_fwd_status_word(const void* ws, int B, int T, int H, int V) {
+  const FwdWs w = fwd_ws_layout(const_cast<void*>(ws), B, T, H, V, 0);
+  return w.sync ? w.sync + hattn::kSyncStatus : nullptr;
+}
+
 namespace hattn {
+
+inline LookbackCtl lookback_ctl() { return LookbackCtl{g_spin_limit.load(), g_publish.load()}; }
 
 template <typename TK, typename TV, typename TL, typename TO, int NP, int MAXLOC>
 static hipError_t launch_t(const void* q, const void* k, const void* v, const float* g,
@@ -1485,10 +1571,10 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
       auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true>;
       e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(kern, dim3(B * NSEG * H * nvb64), dim3(256), smem, stream,
+      hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
                          (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
                          gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog,
-                         NSEG, ht != nullptr ? 1 : 0, LayerArgs{});
+                         NSEG, ht != nullptr ? 1 : 0, LayerArgs{}, lookback_ctl());
       return hipGetLastError();
     }
     auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, false>;
@@ -1497,7 +1583,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
     hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
                        (const __bf16*)q, (const __bf16*)k, (const TV*)v, g, (const TL*)l, (TO*)o,
                        gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
-                       ht != nullptr ? 1 : 0, LayerArgs{});
+                       ht != nullptr ? 1 : 0, LayerArgs{}, lookback_ctl());
     return hipGetLastError();
   }
   if (NSEG > 1) {
@@ -1550,10 +1636,10 @@ static hipError_t layer_launch_t(const void* q, const void* k, const void* x, co
     auto kern = mamba2_fwd_bf16_kernel<__bf16, TL, TO, true, true>;
     e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(B * NSEG * H * nvb64), dim3(256), smem, stream,
+    hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
                        (const __bf16*)q, (const __bf16*)k, (const __bf16*)x, (const float*)nullptr,
                        (const TL*)dl, (TO*)o, gcum, (float*)nullptr, w.sums, w.segd, w.sync, B, T,
-                       G, H, V, L, nlev, nvb64, slog, NSEG, 0, la);
+                       G, H, V, L, nlev, nvb64, slog, NSEG, 0, la, lookback_ctl());
     return hipGetLastError();
   }
   auto kern = mamba2_fwd_bf16_kernel<__bf16, TL, TO, false, true>;
@@ -1562,7 +1648,7 @@ static hipError_t layer_launch_t(const void* q, const void* k, const void* x, co
   hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
                      (const __bf16*)q, (const __bf16*)k, (const __bf16*)x, (const float*)nullptr,
                      (const TL*)dl, (TO*)o, gcum, (float*)nullptr, w.sums, w.segd, w.sync, B, T, G,
-                     H, V, L, nlev, nvb64, slog, NSEG, 0, la);
+                     H, V, L, nlev, nvb64, slog, NSEG, 0, la, lookback_ctl());
   return hipGetLastError();
 }
 

@@ -27,6 +27,8 @@ SIGNATURES = [
     ("hattn_mamba2_chunkwise_fwd_workspace", _S, [_I] * 7),
     ("hattn_mamba2_chunkwise_fwd_noalloc", _I,
      [_P, _P, _P, _F, _P, _P, _F, _F] + [_I] * 7 + [_I] * 4 + [_I] * 3 + [_P]),
+    ("hattn_mamba2_chunkwise_fwd_status", _I, [_P, _I, _I, _I, _I, _P, _P]),
+    ("hattn_debug_lookback", None, [_I, _I]),
     ("hattn_mamba2_chunkwise_bwd", _I,
      [_P, _P, _P, _F, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
      + [_P, _S, _P]),
@@ -137,6 +139,17 @@ def stream_handle(device: torch.device) -> int:
         return _raw_stream(device.index if device.index is not None
                            else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def fwd_status(ws, B: int, T: int, H: int, V: int, device: torch.device) -> int:
+    """Health word of the last bf16 Mamba-2 forward on workspace ``ws`` (a
+    tensor from :func:`workspace`, or None): bit 0 set means a look-back wait
+    gave up and that call's outputs hold NaN.  Synchronises the stream."""
+    import ctypes as _ct
+    out = _ct.c_uint(0)
+    check(load().hattn_mamba2_chunkwise_fwd_status(ptr(ws), B, T, H, V, _ct.byref(out),
+                                                   stream_handle(device)))
+    return out.value
 
 
 def workspace(nbytes: int, device: torch.device):

@@ -60,12 +60,13 @@ def test_noalloc_matches_workspace_entry(dtype):
 @pytest.mark.gpu
 def test_noalloc_rejects_sizes_beyond_static_scratch():
     # B=32 T=65536 H=32 V=64 needs well over 64 MiB of segment summaries
+    # (placeholder tensor pointers: the capacity check fails before any HIP call)
     lib = _lib.load()
     dev = torch.device("cuda:0")
-    p = ctypes.c_void_p(None)
+    p = ctypes.c_void_p(0x1000)
     need = lib.hattn_mamba2_chunkwise_fwd_workspace(32, 65536, 32, 32, 64, 64, 17)
     assert need > (64 << 20)
-    st = lib.hattn_mamba2_chunkwise_fwd_noalloc(p, p, p, p, p, p, None, None, 32, 65536, 32, 32,
+    st = lib.hattn_mamba2_chunkwise_fwd_noalloc(p, p, p, p, p, p, p, None, 32, 65536, 32, 32,
                                                 64, 64, 17, 0, 0, 0, 0, 2, 0, 64,
                                                 _lib.stream_handle(dev))
     assert st == _lib.HATTN_ERR_VALUE

@@ -269,7 +269,7 @@ size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int 
  *   kernel.py:24-29, 224-225 applied inside the kernel)
  *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
  *
- * Constraints as hattn_gdn_chunkwise_fwd, except K in {64, 128, 192} and V in
+ * Constraints as hattn_gdn_chunkwise_fwd, except K in {64, 128, 192, 256} and V in
  * {64, 128} -> HATTN_ERR_NOT_IMPLEMENTED (the gradients are sums over independent column
  * blocks of V, so a caller splits a larger V into blocks of 128 / 64 and sums
  * dq, dk, db, dg, dl; hattention.chunkwise_hgdn.chunkwise_bwd does); do bf16 ->

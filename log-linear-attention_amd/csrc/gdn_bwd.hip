@@ -363,14 +363,18 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
 // ---------------------------------------------------------------------------
 // Kernel 4: chunk-local backward
 // ---------------------------------------------------------------------------
+// QG (K > 192): q is not staged in LDS (the tile would not fit next to the
+// fp32 matrices); its fragments come from global memory (L2) and each
+// 64-column block is staged beside the fp32 staging tile when a step needs it.
 template <int KD, int VD>
 struct GdnBchunkSmem {
+  static constexpr bool QG = KD > 192;
   static constexpr int LK = KD + 8;
   static constexpr int LS = 64 + 4;     // fp32 staging row stride (64-column blocks)
   static constexpr int LDB = 64 + 8;    // bf16 staging row stride
   static constexpr int NR = 2 * kGC * kLM;
   static_assert(kGC * LS + kGC * LDB / 2 <= NR, "step 14 staging fits the S4 | S5 region");
-  __bf16 q[kGC * LK];
+  __bf16 q[QG ? 8 : kGC * LK];
   __bf16 k[kGC * LK];
   float m[4][kGC * kLM];   // S0 .. S3: 64 x 64 fp32 matrices
   float rg[NR];            // S4 | S5, or the fp32 (and bf16) staging tiles, or the inverse scratch
@@ -473,25 +477,25 @@ __device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs,
 // t16 + 4lq + i, column 16 nt + ln) as bf16 rows of stride ld.  With norm set,
 // the rows are the gradient w.r.t. y = x r s (r = 1 / ||x||, staged y in Y)
 // and the stored gradient is w.r.t. x: r s (x - y' (y' . x)), y' = y / s.
-template <int NKT>
-__device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], const __bf16* Y,
+// yat(t, c): the staged (normalised, scaled) value of row t, column c.
+template <int NKT, typename YAt>
+__device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], YAt yat,
                                                   const float* rinv, float inv_s, float s,
                                                   int norm, __bf16* out, size_t ld, int t16) {
   const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
-  constexpr int LY = NKT * 16 + 8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = t16 + 4 * lq + i;
     float f = 1.f, dot = 0.f;
     if (norm) {
 #pragma unroll
-      for (int nt = 0; nt < NKT; ++nt) dot += (float)Y[t * LY + 16 * nt + ln] * inv_s * x[nt][i];
+      for (int nt = 0; nt < NKT; ++nt) dot += yat(t, 16 * nt + ln) * inv_s * x[nt][i];
       dot = row_sum16(dot);
       f = rinv[t] * s;
     }
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt) {
-      const float y = norm ? (float)Y[t * LY + 16 * nt + ln] * inv_s : 0.f;
+      const float y = norm ? yat(t, 16 * nt + ln) * inv_s : 0.f;
       out[t * ld + 16 * nt + ln] = (__bf16)(f * (x[nt][i] - y * dot));
     }
   }
@@ -530,15 +534,26 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   const int t16 = 16 * w;   // this wave's 16-row tile
 
   // ---- load ------------------------------------------------------------------
+  constexpr bool QG = Sm::QG;
   g2s_tile<KD>(k + rowk, hk, s.k, LK);
-  g2s_tile<KD>(q + rowk, hk, s.q, LK);
+  if constexpr (!QG) g2s_tile<KD>(q + rowk, hk, s.q, LK);
   if (norm_qk) {
     // use_qk_l2norm_in_kernel: the gradients below are w.r.t. q scale / ||q|| and
     // k / ||k||; the chain rule back to q and k is applied where dq, dk are stored
+    if constexpr (QG) l2norm_rinv_global<KD>(q + rowk, hk, s.rq);
     __syncthreads();
-    l2norm_rows<KD, LK>(s.q, qk_scale, s.rq);
+    if constexpr (!QG) l2norm_rows<KD, LK>(s.q, qk_scale, s.rq);
     l2norm_rows<KD, LK>(s.k, 1.f, s.rk);
   }
+  // the staged value of q[t][c] (QG: from global memory, normalised as staged)
+  auto q_at = [&](int t, int c) -> float {
+    if constexpr (QG) {
+      const float x = (float)q[rowk + (size_t)t * hk + c];
+      return norm_qk ? (float)(__bf16)((float)(__bf16)(x * s.rq[t]) * qk_scale) : x;
+    } else {
+      return (float)s.q[t * LK + c];
+    }
+  };
   if (w == 0) {
     const float x = gcum[(tok0 + lane) * H + h];
     const float gl = __shfl(x, kGC - 1, 64);
@@ -578,7 +593,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 #pragma unroll
     for (int c = 0; c < KD / 32; ++c) {
       const bf16x8 ak = *(const bf16x8*)(s.k + (t16 + ln) * LK + 32 * c + 8 * lq);
-      const bf16x8 aq = *(const bf16x8*)(s.q + (t16 + ln) * LK + 32 * c + 8 * lq);
+      bf16x8 aq;
+      if constexpr (QG) {
+        aq = *(const bf16x8*)(q + rowk + (size_t)(t16 + ln) * hk + 32 * c + 8 * lq);
+        if (norm_qk) aq = l2norm_scale8(aq, s.rq[t16 + ln], qk_scale);
+      } else {
+        aq = *(const bf16x8*)(s.q + (t16 + ln) * LK + 32 * c + 8 * lq);
+      }
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
@@ -836,9 +857,23 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   float dqh[NKT][4], dkh[NKT][4];
   float qx = 0.f;                                   // rowdot(X, Q), thread (t = tid >> 2, part)
   float rb[4] = {0.f, 0.f, 0.f, 0.f}, kd[4] = {0.f, 0.f, 0.f, 0.f};
+  // QG: the block of q the steps below read, [t][k] bf16 beside the staging tile
+  __bf16* SQ = (__bf16*)(s.rg + kGC * LS);
+  const __bf16* QB = QG ? SQ : s.q;    // Q block base and row stride for steps 10, 12
+  constexpr int LQB = QG ? LDB : LK;
 #pragma unroll
   for (int kb = 0; kb < KD / 64; ++kb) {
     const int k0 = 64 * kb;
+    const int kq = QG ? 0 : k0;        // column of the block in QB
+    if constexpr (QG) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int u = tid + 256 * rr, t = u >> 3, c = 8 * (u & 7);
+        bf16x8 x = *(const bf16x8*)(q + rowk + (size_t)t * hk + k0 + c);
+        if (norm_qk) x = l2norm_scale8(x, s.rq[t], qk_scale);
+        *(bf16x8*)(SQ + t * LDB + c) = x;
+      }
+    }
     // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ----------------
     stage_rows<64, LS, NPV>(ST, dq_p + rowk + k0, hk, BTH * KD, s.e);
     __syncthreads();
@@ -863,7 +898,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       const int t = tid >> 2, part = tid & 3;
 #pragma unroll
       for (int kk = 16 * part; kk < 16 * part + 16; ++kk)
-        qx += ST[t * LS + kk] * (float)s.q[t * LK + k0 + kk];
+        qx += ST[t * LS + kk] * (float)QB[t * LQB + kq + kk];
     }
     __syncthreads();
 
@@ -889,7 +924,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const bf16x8 bk = tr_frag(s.k, LK, 32 * c, k0 + 16 * nt);
-        const bf16x8 bq = tr_frag(s.q, LK, 32 * c, k0 + 16 * nt);
+        const bf16x8 bq = tr_frag(QB, LQB, 32 * c, kq + 16 * nt);
         float ad[8], am[8], at[8];
         frn<kLM>(S1, t16, 32 * c, ad);
         u2[nt] = mma_fb(ad, bk, u2[nt]);
@@ -920,9 +955,10 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   // dq = dq_hat, or with the in-kernel normalisation x -> y = x r (r = 1 / ||x||)
   // scaled by s: dq = r s (dq_hat - y (y . dq_hat)) (fla l2norm_bwd, kernel.py:24-29)
-  store_l2norm_grad<NKT>(dqh, s.q, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
+  store_l2norm_grad<NKT>(dqh, q_at, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
                          dq + rowk, hk, t16);
-  store_l2norm_grad<NKT>(dkh, s.k, s.rk, 1.f, 1.f, norm_qk, dk + rowk, hk, t16);
+  store_l2norm_grad<NKT>(dkh, [&](int t, int c) { return (float)s.k[t * LK + c]; }, s.rk, 1.f,
+                         1.f, norm_qk, dk + rowk, hk, t16);
   {
     qx += __shfl_xor(qx, 1, 64);
     qx += __shfl_xor(qx, 2, 64);
@@ -1138,6 +1174,8 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
       return gdn_bwd_t<KD_, VD_, float, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
                                                 dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
   }
+  HATTN_GDN_B(256, 128)
+  HATTN_GDN_B(256, 64)
   HATTN_GDN_B(192, 128)
   HATTN_GDN_B(192, 64)
   HATTN_GDN_B(128, 128)

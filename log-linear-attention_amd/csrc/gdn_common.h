@@ -209,10 +209,21 @@ __device__ __forceinline__ void tri_inv64_mfma(const float* A, float* X, float* 
 }
 
 // In-place l2 normalisation of the 64 rows of a staged bf16 tile [64][LD] with
-// N columns: x <- x * scale / sqrt(||x||^2 + eps), eps = 1e-6 (fla's l2norm,
-// used at kernel.py:20-23, 110-111), over fp32 sums.  Threads T0 .. T0 + 255
-// take part, four per row (consecutive lanes); rinv (if not null) receives
-// 1 / sqrt(||x||^2 + eps) of each row, for the backward's chain rule.
+// N columns: x <- bf16(bf16(x / sqrt(||x||^2 + eps)) * scale), eps = 1e-6,
+// over fp32 sums: fla's l2norm stores its output in the input dtype and the
+// scale multiplies that (l2norm_and_scale_fwd, kernel.py:20-23, 110-111), so
+// the value is rounded after the norm and again after the scale (the decode
+// step rounds the same way).  Threads T0 .. T0 + 255 take part, four per row
+// (consecutive lanes); rinv (if not null) receives 1 / sqrt(||x||^2 + eps) of
+// each row, for the backward's chain rule.
+// bf16(bf16(x * ri) * scale) of eight values (the stored l2norm output).
+__device__ __forceinline__ bf16x8 l2norm_scale8(bf16x8 x, float ri, float scale) {
+  bf16x8 y;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = (__bf16)((float)(__bf16)((float)x[i] * ri) * scale);
+  return y;
+}
+
 template <int N, int LD, int T0 = 0>
 __device__ __forceinline__ void l2norm_rows(__bf16* X, float scale, float* rinv) {
   constexpr int PER = N / 4, NU = PER / 8;   // columns per thread, 16-byte units
@@ -229,15 +240,30 @@ __device__ __forceinline__ void l2norm_rows(__bf16* X, float scale, float* rinv)
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   const float ri = __builtin_amdgcn_rsqf(ss + 1e-6f);
-  const float f = ri * scale;
 #pragma unroll
-  for (int j = 0; j < NU; ++j) {
-    bf16x8 y;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = (__bf16)((float)u[j][i] * f);
-    *(bf16x8*)(row + 8 * j) = y;
-  }
+  for (int j = 0; j < NU; ++j) *(bf16x8*)(row + 8 * j) = l2norm_scale8(u[j], ri, scale);
   if (rinv != nullptr && part == 0) rinv[r] = ri;
+}
+
+// 1 / sqrt(||x||^2 + eps) of the 64 rows of a global bf16 tile (row stride
+// ld elements, N columns), with the arithmetic of l2norm_rows (same column
+// split and sum order, so the same value): four threads per row, rinv[r].
+template <int N>
+__device__ __forceinline__ void l2norm_rinv_global(const __bf16* X, size_t ld, float* rinv) {
+  constexpr int PER = N / 4, NU = PER / 8;
+  const int t = (int)threadIdx.x, r = t >> 2, part = t & 3;
+  const __bf16* row = X + (size_t)r * ld + part * PER;
+  bf16x8 u[NU];
+#pragma unroll
+  for (int j = 0; j < NU; ++j) u[j] = *(const bf16x8*)(row + 8 * j);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NU; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (float)u[j][i] * (float)u[j][i];
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  if (part == 0) rinv[r] = __builtin_amdgcn_rsqf(ss + 1e-6f);
 }
 
 }  // namespace hattn

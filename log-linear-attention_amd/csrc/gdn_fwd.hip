@@ -885,6 +885,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
   HATTN_GDN_RC_D(64)
   HATTN_GDN_RC_D(128)
   HATTN_GDN_RC_D(192)
+  HATTN_GDN_RC_D(256)
 #undef HATTN_GDN_RC_D
 #undef HATTN_GDN_RC
   *unsupported = 1;

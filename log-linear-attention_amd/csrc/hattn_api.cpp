@@ -546,9 +546,9 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
   if (K > 256) return fail(HATTN_ERR_NOT_IMPLEMENTED, "K=%d > 256", K);
   if (K % 64 != 0 || V % 64 != 0)
     return fail(HATTN_ERR_VALUE, "K=%d, V=%d and BK, BV could be 64", K, V);
-  if (!((K == 64 || K == 128 || K == 192) && (V == 64 || V == 128)))
+  if (!((K == 64 || K == 128 || K == 192 || K == 256) && (V == 64 || V == 128)))
     return fail(HATTN_ERR_NOT_IMPLEMENTED,
-                "K=%d V=%d (the MI355X GDN backward supports K in {64, 128, 192} and V in "
+                "K=%d V=%d (the MI355X GDN backward supports K in {64, 128, 192, 256} and V in "
                 "{64, 128}; the host driver splits larger V into blocks)", K, V);
   const int nlev = ceil_log2(T / 64);
   if (7 + nlev > L)

@@ -733,13 +733,14 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const f
   }
 }
 
-// FUSED: one launch computes everything (single pass).  Work items (batch,
-// segment, head, V block) are handed out by eight ticket counters, one per
-// XCD (workgroup blockIdx.x goes to XCD blockIdx.x % 8): the groups (batch,
-// segment) g = x, x + 8, x + 16, .. go to XCD x, in that order, each with all
-// its heads and V blocks, so the cache lines of lambda and g that interleave
-// the heads of a token row are fetched into one L2.  A workgroup only ever
-// waits for a smaller group; each XCD claims its groups in increasing order,
+// FUSED: one launch computes everything (single pass).  Work items (segment,
+// batch, head, V block) are handed out by eight ticket counters, one per XCD
+// (workgroup blockIdx.x goes to XCD blockIdx.x % 8): the groups g = p B + b
+// (segment p of batch b) g = x, x + 8, x + 16, .. go to XCD x, in that order,
+// each with all its heads and V blocks, so the cache lines of lambda and g
+// that interleave the heads of a token row are fetched into one L2.  A
+// workgroup only ever waits for a smaller group (an earlier segment of its
+// batch); each XCD claims its groups in increasing order,
 // so the smallest unfinished group is always claimed by running workgroups
 // whose waits are all satisfied, and the launch cannot deadlock.
 // Phase A streams the segment's K, V, g and publishes Sum(p) and D_p
@@ -807,15 +808,19 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     }
     __syncthreads();
     // ticket -> (group xcd + 8 i, head, V block), V block fastest; the grid has
-    // as many workgroups per XCD as the XCD with the most groups has items
+    // as many workgroups per XCD as the XCD with the most groups has items.
+    // Groups are segment-major (g = p B + b): every batch's segment p is
+    // claimed before any segment p + 1, so the look-backs find their summaries
+    // early and the last items claimed are last segments, which have no
+    // summary pass (p = NSEG - 1 waits only for smaller groups either way).
     const int per = H * nvb64;
     const int grp = xcd + 8 * (ticket / per);
     if (grp >= B * NSEG) return;
     const int r = ticket % per;
     vblk = r % nvb64;
     h = r / nvb64;
-    p = grp % NSEG;
-    b = grp / NSEG;
+    p = grp / B;
+    b = grp % B;
   } else {
     // grid: xcd_head_grid(B * NSEG, H, nvb64)
     const XcdHeadMap xm = xcd_head_map(blockIdx.x, H, nvb64);

@@ -9,7 +9,8 @@ Same names, arguments and return tuples as hattention/chunkwise_hgdn.py:
 Validation follows the reference (``ValueError`` for T % 64 and K / V not
 multiples of the block options, ``NotImplementedError`` for K > 256 and modes
 outside the weak base-2 hierarchy).  The backward kernels take K in {64, 128,
-192} (``NotImplementedError`` from the C-ABI otherwise) and V in blocks of 128.  Grouped q / k are expanded per head
+192, 256} (``NotImplementedError`` from the C-ABI otherwise) and V in blocks of
+128.  Grouped q / k are expanded per head
 before the kernels like the reference (chunkwise_hgdn.py:614-623) and their
 gradients summed over the group (chunkwise_hgdn.py:1208-1215).  There is no
 CPU path.

@@ -209,7 +209,7 @@ def _gdn_bwd(**kw):
     (dict(L=7), _lib.HATTN_ERR_VALUE),              # L < 7 + ceil(log2(T/64))
     (dict(K=96, V=96), _lib.HATTN_ERR_VALUE),       # K, V multiples of 64
     (dict(K=320, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # K > 256
-    (dict(K=256, V=64), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # backward K in {64, 128, 192}
+    (dict(K=256, V=64), _lib.HATTN_ERR_VALUE),      # K = 256 valid: fails on the null pointers
     (dict(K=64, V=192), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # V blocks of 64 / 128
     (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
     (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),

@@ -104,7 +104,7 @@ def test_groups():
         _check(name, a, r, "groups")
 
 
-@pytest.mark.parametrize("K", [128, 192])
+@pytest.mark.parametrize("K", [128, 192, 256])
 def test_autograd_function_l2norm_and_scale(K):
     """hattention_kernel(GDELTA).backward(): the HIP backward plus the l2norm /
     scale chain rule of kernel.py:201-225, against autograd through the oracle's
@@ -162,15 +162,11 @@ def test_reference_model_shape_bwd():
     _run(1, 16384, 6, 192, 384, 15, seed=1192, rows=[(0, 0), (0, 5)])
 
 
-def test_head_dim_256_bwd_not_implemented():
-    """The backward kernels take K in {64, 128, 192}; K = 256 raises instead of
-    returning wrong gradients."""
-    from hattention.chunkwise_hgdn import chunkwise_fwd, chunkwise_bwd
-    from hattention.base import HType
-    q, k, v, beta, g, l = make_gdn_inputs(1, 128, 1, 256, 64, 8, seed=3)
-    dev = torch.device("cuda:0")
-    xs = [x.to(dev) for x in (q, k, v, beta, g, l)]
-    gc, o, Aw, Au, _ = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, False)
-    with pytest.raises(NotImplementedError):
-        chunkwise_bwd(xs[0], xs[1], xs[2], xs[3], gc, xs[5], Aw, Au, torch.ones_like(o), False,
-                      2, HType.WEAK, 64)
+@pytest.mark.parametrize("T,V", [(640, 64), (1024, 256)])
+def test_head_dim_256_bwd(T, V):
+    """K = 256, the largest head dimension the reference accepts
+    (chunkwise_hgdn.py:836): the chunk kernel reads q from global memory (the
+    q tile would not fit in LDS next to its fp32 matrices) and stages one
+    64-column block at a time; V = 256 runs as two 128-column blocks."""
+    L = 7 + math.ceil(math.log2(T // 64)) + 1
+    _run(1, T, 2, 256, V, L, seed=T + V + 256)

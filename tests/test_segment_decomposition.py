@@ -132,3 +132,4 @@ def test_segmented_matches_level_scan(NT, slog):
     o2, _ = segmented_fwd(q, k, v, g, l, C, slog, final_state=False)
     ref2 = M.chunked_scan_fwd(q, k, v, g, l, chunk_size=C)[0]
     assert ((o2 - ref2).abs().max() / ref2.abs().max()).item() < 1e-12
+

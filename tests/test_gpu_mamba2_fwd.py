@@ -6,8 +6,8 @@ on the CPU, fed the identical (bf16-rounded) inputs.  Tolerance for bf16 inputs
 max|o - o_ref| / max|o_ref| <= 2e-2; the relative
 Frobenius error of the reference's own checks (mamba_apis.py:666) is reported
 and must stay below 1e-2.  At full BASELINE sizes every (batch, head) row is
-independent, so the oracle runs on a few rows at the full length T and the
-GPU output of the full-size launch is compared on those rows.
+independent; the oracle runs on whole tensors (or on a few rows where noted)
+at the full length T and the full-size launch is compared row by row.
 
 fp32 q / k run the bf16x3 kernels; their tolerance (north_star, fp32/bf16x3
 mode) is 1e-4 on both the max-abs/rel and the relative Frobenius error, and
@@ -147,8 +147,8 @@ def test_head_dim_128_bf16x3():
 
 
 def test_config2_long_context():
-    # B=1 T=32768 H=32 dk=64 dv=128 L=16 bf16
-    _run(1, 32768, 32, 64, 128, 16, seed=1002, rows=[(0, 0), (0, 31)])
+    # B=1 T=32768 H=32 dk=64 dv=128 L=16 bf16, every row
+    _run(1, 32768, 32, 64, 128, 16, seed=1002)
 
 
 @pytest.mark.parametrize("T", [64, 256, 1024, 4096])
@@ -179,8 +179,7 @@ def test_fp32_bf16x3_groups_mixed_v():
 
 def test_config2_long_context_bf16x3():
     # BASELINE config 2 in bf16x3 (fp32-accurate) mode, checked to 1e-4
-    _run(1, 32768, 32, 64, 128, 16, seed=1002, dtype=torch.float32, rows=[(0, 0), (0, 17),
-                                                                         (0, 31)])
+    _run(1, 32768, 32, 64, 128, 16, seed=1002, dtype=torch.float32)
 
 
 def test_hattention_kernel_api_matches_chunkwise():

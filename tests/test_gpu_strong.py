@@ -82,6 +82,13 @@ def test_strong_fwd_north_star_shape():
     _run_fwd(4, 16384, 16, 16, 64, 64, 15, seed=1000, rows=[(0, 0), (1, 7), (3, 15)])
 
 
+def test_strong_fwd_nine_chunk_levels():
+    """T = 32768, the longest sequence the strong C-ABI accepts (nine chunk
+    levels: the last slot of the kernel's level arrays, lambda column 15 and
+    the cascade's carry into the top level)."""
+    _run_fwd(1, 32768, 2, 2, 64, 64, 16, seed=327)
+
+
 def test_strong_differs_from_weak():
     """The strong path is taken: its output differs from the weak one's on the
     same inputs by far more than the tolerance."""
@@ -194,6 +201,11 @@ def test_strong_bwd_north_star_shape():
     """the north-star shape (B=4 T=16384 H=16 d=64 L=15) with the strong
     hierarchy: rows at both ends of the grid"""
     _run_bwd(4, 16384, 16, 16, 64, 64, 15, seed=1001, rows=[(0, 0), (3, 15)])
+
+
+def test_strong_bwd_nine_chunk_levels():
+    """T = 32768 (nine chunk levels, the strong C-ABI's maximum): every row."""
+    _run_bwd(1, 32768, 2, 2, 64, 64, 16, seed=328, full=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

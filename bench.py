@@ -284,7 +284,7 @@ def layer_bench(dev, stream, n_steps, warmup):
 
         for _ in range(max(1, warmup)):
             fb()
-        wall_fb, _ = _time_region(fb, max(1, n_steps // 2), stream)
+        wall_fb, _ = _time_region(fb, n_steps, stream)
         res[name] = {"fwd_tokens_per_s": B * T / wall_f, "fwd_ms": wall_f * 1e3,
                      "fwd_bwd_tokens_per_s": B * T / wall_fb, "fwd_bwd_ms": wall_fb * 1e3}
         del leaves
@@ -356,7 +356,7 @@ def split_layer_bench(dev, stream, n_steps, warmup):
 
         for _ in range(max(1, warmup)):
             fb()
-        wall_fb, _ = _time_region(fb, max(1, n_steps // 2), stream)
+        wall_fb, _ = _time_region(fb, n_steps, stream)
         res[name] = {"fwd_tokens_per_s": B * T / wall_f, "fwd_ms": wall_f * 1e3,
                      "fwd_bwd_tokens_per_s": B * T / wall_fb, "fwd_bwd_ms": wall_fb * 1e3}
         del leaves
@@ -376,6 +376,11 @@ def cpu_model():
     return platform.processor() or platform.machine()
 
 
+def _progress(msg):
+    """One progress line on stderr (stdout carries only the JSON record)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def cpu_baseline(seconds_budget=20.0):
     """Host-CPU baselines (the chunkwise and recurrent forms on the host cores), all fp32 torch restatements
     of the reference (the reference itself cannot run on the box):
@@ -383,8 +388,9 @@ def cpu_baseline(seconds_budget=20.0):
       level-scan algorithm, chunkwise.py:1118-1275) at the full north-star, C1
       and C4 shapes, median of up to 3 runs within the budget each;
     * recurrent: oracle.mamba2.recurrent_fwd (the Fenwick state machine of
-      recurrent.py:9-216) on config 0 in full and on a 1024-token prefix of the
-      north-star shape (its cost per token does not depend on T at fixed L).
+      recurrent.py:9-216) on config 0 in full and on a 2048-token prefix of the
+      north-star shape (its cost per token does not depend on T at fixed L),
+      median of up to 3 runs within 100 s.
     ``value`` is the chunkwise north-star figure (the GPU headline's workload)."""
     from oracle.mamba2 import chunked_scan_fwd, recurrent_fwd
     n = len(os.sched_getaffinity(0))
@@ -400,6 +406,7 @@ def cpu_baseline(seconds_budget=20.0):
             fn(q, k, v, g, l)
             times.append(time.perf_counter() - t0)
         t = _median(times)
+        _progress(f"cpu {getattr(fn, '__name__', 'fn')} {shape}: {t:.2f} s x {len(times)}")
         return {"tokens_per_s": B * T / t, "seconds": t, "runs": len(times),
                 "shape": dict(zip(("batch", "seq_len", "heads", "dk", "dv", "levels"), shape))}
 
@@ -409,7 +416,8 @@ def cpu_baseline(seconds_budget=20.0):
         "chunkwise_c1": run(chunk, (8, 4096, 16, 64, 64, 13), 1001, seconds_budget / 2),
         "chunkwise_c4": run(chunk, (8, 8192, 24, 64, 64, 14), 1004, seconds_budget / 2),
         "recurrent_c0": run(recurrent_fwd, (2, 1024, 4, 64, 64, 11), 1000, 1.0),
-        "recurrent_ns_prefix1024": run(recurrent_fwd, (4, 1024, 16, 64, 64, 15), 1000, 1.0),
+        # median of up to 3 runs of a 2048-token prefix (one run takes ~40-60 s)
+        "recurrent_ns_prefix2048": run(recurrent_fwd, (4, 2048, 16, 64, 64, 15), 1000, 100.0),
     }
     t = res["chunkwise_ns"]
     return {
@@ -456,6 +464,7 @@ def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, back
         fn()
     times = time_cold(fn, reps, stream, evict)
     t = _median(times)
+    _progress(f"{name}{' strong' if strong else ''}: {t * 1e6:.1f} us")
     nbytes = fwd_bytes(B, T, H, K, V, L, es=es, es_l=es)
     flops = fwd_flops(B, T, H, K, V)
     if backward:
@@ -482,7 +491,7 @@ def mamba2_fwd_record(name, shape, dtype, dev, stream, evict, reps, warmup, back
 GDN_C3 = (4, 8192, 16, 128, 128, 14)
 
 
-def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3):
+def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3, warmup=5):
     """Cold-cache medians of the log-linear Gated DeltaNet chunkwise forward and
     forward + backward (chunkwise_hgdn.chunkwise_fwd / chunkwise_bwd) at BASELINE
     config 3, MFMA roofline by the algorithmic FLOPs (backward counted as twice
@@ -510,10 +519,11 @@ def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3)
         if key not in keys:
             out[key] = None
             continue
-        for _ in range(2):
+        for _ in range(warmup):
             fn()
         times = time_cold(fn, reps, stream, evict)
         t_g = _median(times)
+        _progress(f"gdn {key}: {t_g * 1e6:.1f} us")
         fl = gfl if key == "fwd" else 3 * gfl
         out[key] = {"value": GB * GT / t_g, "unit": "tokens/s", "median_us": t_g * 1e6,
                     "reps": reps, "config": gcfg,
@@ -621,31 +631,32 @@ def main():
     records = []
     fb = gdn = gdn_fb = dec = layer = None
     if not args.fwd_only:
-        reps = max(5, args.steps // 2)
+        # every secondary record: >= 20 cold reps after >= 5 warm-ups
+        reps, wu = max(20, args.steps), max(5, args.warmup)
         # north-star forward + backward, then the other BASELINE configs
         fb = mamba2_fwd_record("north star fwd+bwd", (B, T, H, K, V, L), torch.bfloat16, dev,
-                               stream, evict, reps, 2, backward=True)
+                               stream, evict, reps, wu, backward=True)
         for name, shape, dt, bw in (
                 ("C1", (8, 4096, 16, 64, 64, 13), torch.bfloat16, False),
                 ("C2", (1, 32768, 32, 64, 128, 16), torch.bfloat16, False),
                 ("C2 bf16x3", (1, 32768, 32, 64, 128, 16), torch.float32, False),
                 ("C4 fwd+bwd", (8, 8192, 24, 64, 64, 14), torch.bfloat16, True)):
-            records.append(mamba2_fwd_record(name, shape, dt, dev, stream, evict, reps, 2,
+            records.append(mamba2_fwd_record(name, shape, dt, dev, stream, evict, reps, wu,
                                              backward=bw))
             torch.cuda.empty_cache()
         # the strong hierarchy (HType.STRONG) at the north-star shape
         for bw in (False, True):
             records.append(mamba2_fwd_record(
                 "north star fwd+bwd, HType.STRONG" if bw else "north star fwd, HType.STRONG",
-                (B, T, H, K, V, L), torch.bfloat16, dev, stream, evict, reps, 2, backward=bw,
+                (B, T, H, K, V, L), torch.bfloat16, dev, stream, evict, reps, wu, backward=bw,
                 strong=True))
             torch.cuda.empty_cache()
 
         # log-linear Gated DeltaNet at BASELINE config 3 (MFMA-bound path)
-        gdn, gdn_fb = gdn_records(dev, stream, evict, reps)
+        gdn, gdn_fb = gdn_records(dev, stream, evict, reps, warmup=wu)
         torch.cuda.empty_cache()
         dec = decode_bench(dev, stream, 128, 8)
-        layer = layer_bench(dev, stream, max(2, args.steps // 5), 2)
+        layer = layer_bench(dev, stream, reps, wu)
 
     out = {
         "metric": "fwd tokens/s @B=4,T=16K,H=16,d=64 bf16; % MFMA/HBM roofline; fwd+bwd tok/s",

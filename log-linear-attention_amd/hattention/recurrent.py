@@ -8,13 +8,14 @@ Mirrors hattention/recurrent.py:9-216:
 
 The state lives in HBM in the reference's layout and is advanced in place by
 one ``hattn_hstate_step`` launch per token (libhattn_hip.so): cascade, gate,
-insert, and for ``hattention_step`` also the output.  The weak cascade
-(:42-54) depends only on the level counts, which depend only on the number of
-tokens inserted, so it is planned here on a host copy of the counts; the
-device ``counts`` tensor is advanced by the same launch.  No step reads
-anything back from the device.  Only HType.WEAK with level base 2 is built
-(the strong hierarchy, :56-74, raises NotImplementedError); states are fp32,
-the dtype the reference gives them (state dtype = g.dtype, :185, kernel.py:505).
+insert, and for ``hattention_step`` also the output.  The cascades (weak,
+:42-54, and strong, :56-74) depend only on the level counts, which depend only
+on the number of tokens inserted, so they are planned here on a host copy of
+the counts (``plan_cascade_weak`` / ``plan_cascade_strong``); the device
+``counts`` tensor is advanced by the same launch.  No step reads anything back
+from the device.  Level base 2 only (other bases raise NotImplementedError, as
+the reference's strong check does); states are fp32, the dtype the reference
+gives them (state dtype = g.dtype, :185, kernel.py:505).
 """
 from typing import List, Optional, Tuple
 

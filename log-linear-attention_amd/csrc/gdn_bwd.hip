@@ -28,7 +28,7 @@
 //        dW_new -= nr dV_new h_c^T,  dK_new += V_new dh_{c+1}^T,
 //        d exp(Gc_last) += nr <h_c, dh_{c+1}>,
 //        dh_c = nr (exp(Gc_last) dh_{c+1} - W_new^T dV_new) + rd q_new^T (lambda_e o dO);
-//      the contractions over V give per-slice partials, summed by kernel 4;
+//      the contractions over V give per-slice partials (bf16), summed in fp32 by kernel 4;
 //   4. gdn_bwd_chunk_kernel, one workgroup per chunk, backpropagates through
 //      the chunk-local algebra.  With X = e o dq_new and E = dP - (X K^T) o beta_s,
 //        dM = tril(E Aw^T),  dAw = M^T E + ((e o dW_new) K^T + (dU V^T) o Gamma) o beta_s,
@@ -85,8 +85,8 @@ template <int KD, typename TL>
 __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
     const __bf16* __restrict__ un, const __bf16* __restrict__ dO, const float* __restrict__ gcum,
-    const TL* __restrict__ l, const __bf16* __restrict__ hsave, float* __restrict__ dq_p,
-    float* __restrict__ dw_p, float* __restrict__ dk_p, float* __restrict__ du,
+    const TL* __restrict__ l, const __bf16* __restrict__ hsave, __bf16* __restrict__ dq_p,
+    __bf16* __restrict__ dw_p, __bf16* __restrict__ dk_p, float* __restrict__ du,
     float* __restrict__ dl_p, float* __restrict__ del_p, int B, int T, int H, int V, int L,
     int nlev) {
   using Sm = GdnBscanSmem<KD>;
@@ -338,9 +338,9 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
       for (int i = 0; i < 4; ++i) {
         const size_t o = ((size_t)vb * BTH + (tok0 + 16 * tt + 4 * lq + i) * H + h) * KD +
                          16 * (vt0 * APW + j) + ln;
-        dq_p[o] = adq[j][i];
-        dw_p[o] = -adw[j][i];
-        dk_p[o] = adk[j][i];
+        dq_p[o] = (__bf16)adq[j][i];
+        dw_p[o] = (__bf16)-adw[j][i];
+        dk_p[o] = (__bf16)adk[j][i];
       }
 #pragma unroll
     for (int x = 0; x < VTW; ++x)
@@ -407,16 +407,25 @@ __device__ __forceinline__ void frt(const float* X, int r0, int c0, float* f) {
   for (int j = 0; j < 8; ++j) f[j] = p[j * LD];
 }
 // Same from global rows of stride rs: sc * sum over np partials pstride apart.
-template <int NP>
-__device__ __forceinline__ void frg(const float* X, size_t rs, size_t pstride, int r0, int c0,
+template <typename T>
+__device__ __forceinline__ floatx4 ld4f(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *(const floatx4*)p;
+  } else {
+    const bf16x4 x = *(const bf16x4*)p;
+    return floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+  }
+}
+template <int NP, typename T>
+__device__ __forceinline__ void frg(const T* X, size_t rs, size_t pstride, int r0, int c0,
                                     float sc, float* f) {
   const int lane = threadIdx.x & 63;
-  const float* p = X + (size_t)(r0 + (lane & 15)) * rs + c0 + 8 * (lane >> 4);
+  const T* p = X + (size_t)(r0 + (lane & 15)) * rs + c0 + 8 * (lane >> 4);
   floatx4 pa[NP], pb[NP];   // every partial's loads first, then the sums in order
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp) {
-    pa[pp] = *(const floatx4*)(p + pp * pstride);
-    pb[pp] = *(const floatx4*)(p + pp * pstride + 4);
+    pa[pp] = ld4f(p + pp * pstride);
+    pb[pp] = ld4f(p + pp * pstride + 4);
   }
   floatx4 a = pa[0], b = pb[0];
 #pragma unroll
@@ -445,8 +454,8 @@ __device__ __forceinline__ floatx4 mma_fb(const float* a, bf16x8 b, floatx4 c) {
 }
 // ST[t][c] = (scale ? scale[t] : 1) * sum over NP partials of X[t][c], 64 rows of N.
 // Two units per step with all their partial loads issued together.
-template <int N, int LS, int NP>
-__device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs, size_t pstride,
+template <int N, int LS, int NP, typename T>
+__device__ __forceinline__ void stage_rows(float* ST, const T* X, size_t rs, size_t pstride,
                                            const float* scale) {
   constexpr int IT = kGC * N / 4 / 256;
   static_assert(IT % 2 == 0, "units per thread");
@@ -458,7 +467,7 @@ __device__ __forceinline__ void stage_rows(float* ST, const float* X, size_t rs,
       const int u = threadIdx.x + 256 * (i0 + d);
       const int t = u / (N / 4), c = 4 * (u % (N / 4));
 #pragma unroll
-      for (int pp = 0; pp < NP; ++pp) pv[d][pp] = *(const floatx4*)(X + (size_t)t * rs + c + pp * pstride);
+      for (int pp = 0; pp < NP; ++pp) pv[d][pp] = ld4f(X + (size_t)t * rs + c + pp * pstride);
     }
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
@@ -505,8 +514,8 @@ template <int KD, int VD, typename TB, typename TL>
 __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ gcum, const TL* __restrict__ l,
-    const __bf16* __restrict__ dO, const float* __restrict__ dq_p, const float* __restrict__ dw_p,
-    const float* __restrict__ dk_p, const float* __restrict__ du, const float* __restrict__ dl_p,
+    const __bf16* __restrict__ dO, const __bf16* __restrict__ dq_p, const __bf16* __restrict__ dw_p,
+    const __bf16* __restrict__ dk_p, const float* __restrict__ du, const float* __restrict__ dl_p,
     const float* __restrict__ del_p, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
     __bf16* __restrict__ dv, TB* __restrict__ db, float* __restrict__ dg, float* __restrict__ dl,
     int B, int T, int H, int L, int nlev, int norm_qk, float qk_scale) {
@@ -1073,7 +1082,8 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 // ---------------------------------------------------------------------------
 struct GdnBwdWs {
   __bf16 *qn, *kn, *knT, *wn, *un, *hs;
-  float *dq_p, *dw_p, *dk_p, *du, *dl_p, *del_p;
+  __bf16 *dq_p, *dw_p, *dk_p;   // per-V-slice partials, bf16 (summed in fp32 by the chunk kernel)
+  float *du, *dl_p, *del_p;
   size_t bytes;
 };
 
@@ -1092,9 +1102,9 @@ inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V,
   w.wn = (__bf16*)(p + off); off += balign(n * K * 2);
   w.un = (__bf16*)(p + off); off += balign(n * V * 2);
   w.hs = (__bf16*)(p + off); off += balign((size_t)B * H * NT * nl * V * K * 2);
-  w.dq_p = (float*)(p + off); off += balign(nvs * n * K * 4);
-  w.dw_p = (float*)(p + off); off += balign(nvs * n * K * 4);
-  w.dk_p = (float*)(p + off); off += balign(nvs * n * K * 4);
+  w.dq_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
+  w.dw_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
+  w.dk_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
   w.du = (float*)(p + off); off += balign(n * V * 4);
   w.dl_p = (float*)(p + off); off += balign(nvs * n * nl * 4);
   w.del_p = (float*)(p + off); off += balign(nvs * B * H * NT * 4);

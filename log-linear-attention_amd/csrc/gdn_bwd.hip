@@ -62,6 +62,7 @@ struct GdnBscanSmem {
   __bf16 kn[kGC * LK];
   __bf16 u[kGC * LVS];       // U[t][v] slice
   __bf16 dO[kGC * LVS];      // dO[t][v] slice
+  __bf16 ldo[kGC * LVS];     // lambda[t, 7 + e] dO[t][v] of the current level e
   __bf16 hs[kBVs * LK];      // h_e at the chunk start, [v][k]
   __bf16 dhs[kBVs * LK];     // dh_e after the chunk, [v][k]
   __bf16 dvn[kBVs * kLd64];  // dV_new_e, [v][t]
@@ -193,8 +194,9 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
     // at once); slot 0 of the dh array is the current level and the array
     // rotates by one level per iteration (kGBwdMaxLev iterations, the levels
     // >= nlev only rotating), so it is only indexed by constants.  The level's
-    // read / write / no-reset flags enter the products as 0 / 1 factors, so
-    // that its LDS reads and MFMAs issue without a branch per product.
+    // read / write / no-reset flags enter the products as 0 / 1 factors or
+    // operand selects, so that its LDS reads and MFMAs issue without a branch
+    // per product.
 #pragma unroll 1
     for (int e = 0; e < kGBwdMaxLev; ++e) {
       floatx4 cur[TPW];
@@ -221,6 +223,17 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
           fetch_h(nxt ? ic : max(ic - 1, 0), nxt ? e + 1 : 0);
         }
         if (kPrefTiles && e == 0) fetch_tiles(max(ic - 1, 0));
+        // lambda_e o dO, once per level for the products of steps (ii), (iii): written
+        // after the barrier that publishes the chunk's dO and lambda (and that
+        // orders it after the previous level's readers), read after the next one
+        for (int u = tid; u < kGC * kBVs / 4; u += NTH) {
+          const int t = u / (kBVs / 4), c = 4 * (u % (kBVs / 4));
+          const float la = s.lam[e][t];
+          const bf16x4 x = *(const bf16x4*)(s.dO + t * LVS + c);
+          *(bf16x4*)(s.ldo + t * LVS + c) =
+              bf16x4{(__bf16)((float)x[0] * la), (__bf16)((float)x[1] * la),
+                     (__bf16)((float)x[2] * la), (__bf16)((float)x[3] * la)};
+        }
 
         // (i) dV_new = K_new dh, V_new = wr U - nr W_new h, q_new h (for dlambda)
 #pragma unroll
@@ -264,17 +277,14 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
 
         // (ii) contractions over this slice's 32 columns of V
         {
-          // A operands with the level's factors folded into their rows (t = 16 tt + ln),
-          // so the three accumulators take plain MFMA accumulation
-          bf16x8 adO = *(const bf16x8*)(s.dO + (16 * tt + ln) * LVS + 8 * lq);
-          bf16x8 advn = tr_frag(s.dvn, kLd64, 0, 16 * tt);   // dV_new[t][v]
+          // A operands with the level's factors in their rows (t = 16 tt + ln): the
+          // staged lambda_e o dO, and the read / no-reset flags as selects, so the
+          // three accumulators take plain MFMA accumulation
+          const bf16x8 ldo8 = *(const bf16x8*)(s.ldo + (16 * tt + ln) * LVS + 8 * lq);
+          const bf16x8 dvn8 = tr_frag(s.dvn, kLd64, 0, 16 * tt);   // dV_new[t][v]
+          const bf16x8 adO = rd ? ldo8 : bf16x8{};
+          const bf16x8 advn = nr ? dvn8 : bf16x8{};
           const bf16x8 avn = tr_frag(s.vn, kLd64, 0, 16 * tt);     // V_new[t][v]
-          const float fq = frd * s.lam[e][16 * tt + ln];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            adO[jj] = (__bf16)((float)adO[jj] * fq);
-            advn[jj] = (__bf16)((float)advn[jj] * fnr);
-          }
 #pragma unroll
           for (int j = 0; j < VTW * APW; ++j) {
             if (KD > 128 && (j & 1) == 0) __builtin_amdgcn_sched_barrier(0);
@@ -306,14 +316,7 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
           for (int c = 0; c < 2; ++c) {
             const bf16x8 bdv = *(const bf16x8*)(s.dvn + (16 * vv + ln) * kLd64 + 32 * c + 8 * lq);
             tw = mfma16x16x32(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
-            bf16x8 x = tr_frag(s.dO, LVS, 32 * c, 16 * vv);   // dO[t][v]
-            const floatx4 la = *(const floatx4*)(s.lam[e] + 32 * c + 8 * lq);
-            const floatx4 lb = *(const floatx4*)(s.lam[e] + 32 * c + 8 * lq + 4);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              x[jj] = (__bf16)((float)x[jj] * la[jj]);
-              x[4 + jj] = (__bf16)((float)x[4 + jj] * lb[jj]);
-            }
+            const bf16x8 x = tr_frag(s.ldo, LVS, 32 * c, 16 * vv);   // (lambda_e o dO)[t][v]
             tq = mfma16x16x32(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
           }
 #pragma unroll

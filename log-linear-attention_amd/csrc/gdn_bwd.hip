@@ -630,8 +630,9 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   __syncthreads();
 
-  // ---- 2: Aw = (I + A)^-1 -> S2 ---------------------------------------------------
-  tri_inv64(S0, S2, (float(*)[16 * 17])S5);
+  // ---- 2: Aw = (I + A)^-1 -> S2 (fp32 MFMA, the forward's inverse) --------------------
+  static_assert(kGC * kLM >= kInvScratchFloats, "inverse scratch fits S5");
+  tri_inv64_mfma<256>(S0, S2, S5);
 
   // ---- 3: P = M Aw -> S3 ------------------------------------------------------------
 #pragma unroll
@@ -681,21 +682,44 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   __syncthreads();
 
   // ---- 4b: intra-chunk dlambda; Gamma term of o_intra in dGc --------------------------
-  if (tid < kGC) {
-    const int t = tid;
+  // four threads per row t (consecutive lanes), each over 16 columns s, then
+  // four per column s over 16 rows t; the partial sums meet by lane shuffles
+  {
+    const int r = tid >> 2, part = tid & 3, c0 = 16 * part;
+    float dlv[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float rs = 0.f;
-    for (int sc = 0; sc <= t; ++sc) {
-      const int lv = intra_level(t, sc);
-      const float val = S0[t * kLM + sc] * s.beta[sc];
-      s.dlam[lv][t] += val;
-      rs += val * s.lam[lv][t];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int sc = c0 + x;
+      if (sc <= r) {
+        const int lv = intra_level(r, sc);
+        const float val = S0[r * kLM + sc] * s.beta[sc];
+#pragma unroll
+        for (int l = 0; l < 7; ++l) dlv[l] += l == lv ? val : 0.f;
+        rs += val * s.lam[lv][r];
+      }
     }
-    s.dgr[t] += rs;
-  } else if (tid < 2 * kGC) {
-    const int sc = tid - kGC;
     float cs = 0.f;
-    for (int t = sc; t < kGC; ++t) cs += S0[t * kLM + sc] * s.lam[intra_level(t, sc)][t];
-    s.dgcol[1][sc] -= cs * s.beta[sc];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int t = c0 + x;
+      if (t >= r) cs += S0[t * kLM + r] * s.lam[intra_level(t, r)][t];
+    }
+#pragma unroll
+    for (int l = 0; l < 7; ++l) {
+      dlv[l] += __shfl_xor(dlv[l], 1, 64);
+      dlv[l] += __shfl_xor(dlv[l], 2, 64);
+    }
+    rs += __shfl_xor(rs, 1, 64);
+    rs += __shfl_xor(rs, 2, 64);
+    cs += __shfl_xor(cs, 1, 64);
+    cs += __shfl_xor(cs, 2, 64);
+    if (part == 0) {
+#pragma unroll
+      for (int l = 0; l < 7; ++l) s.dlam[l][r] += dlv[l];
+      s.dgr[r] += rs;
+      s.dgcol[1][r] -= cs * s.beta[r];
+    }
   }
   __syncthreads();
 
@@ -1059,24 +1083,37 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     dg[(tok0 + t) * H + h] = x;
     db[(tok0 + t) * H + h] = from_f32<TB>(s.dbr[t]);
   }
-  for (int u = tid; u < kGC * L; u += 256) {
-    const int t = u / L, c = u % L;
-    // inter-chunk columns: the partial loads of every slice issue together
-    // (clamped to column 7 elsewhere, and not used there); with no inter-chunk
-    // level (T = 64) the partial buffer is empty and nothing is loaded
-    const int ce = min(max(c, 7), 6 + nlev) - 7;
-    float pl[NPV];
+  // four elements per thread and round: the partial loads of every slice and
+  // element of a round issue together (inter-chunk columns; clamped to column
+  // 7 elsewhere and to the last element past the end, and not used there;
+  // with no inter-chunk level (T = 64) the partial buffer is empty and nothing
+  // is loaded)
+  for (int u0 = 0; u0 < kGC * L; u0 += 4 * 256) {
+    float pl[4][NPV];
 #pragma unroll
-    for (int p = 0; p < NPV; ++p)
-      pl[p] = nlev > 0 ? dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + ce] : 0.f;
-    float x = 0.f;
-    if (c < 7) {
-      x = s.dlam[c][t];
-    } else if (c < 7 + nlev) {
+    for (int q = 0; q < 4; ++q) {
+      const int u = min(u0 + tid + 256 * q, kGC * L - 1);
+      const int t = u / L, c = u % L;
+      const int ce = min(max(c, 7), 6 + nlev) - 7;
 #pragma unroll
-      for (int p = 0; p < NPV; ++p) x += pl[p];
+      for (int p = 0; p < NPV; ++p)
+        pl[q][p] = nlev > 0 ? dl_p[((size_t)p * BTH + (tok0 + t) * H + h) * nlev + ce] : 0.f;
     }
-    dl[((tok0 + t) * H + h) * L + c] = x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int u = u0 + tid + 256 * q;
+      if (u < kGC * L) {
+        const int t = u / L, c = u % L;
+        float x = 0.f;
+        if (c < 7) {
+          x = s.dlam[c][t];
+        } else if (c < 7 + nlev) {
+#pragma unroll
+          for (int p = 0; p < NPV; ++p) x += pl[q][p];
+        }
+        dl[((tok0 + t) * H + h) * L + c] = x;
+      }
+    }
   }
 }
 

@@ -409,7 +409,7 @@ __device__ __forceinline__ void frt(const float* X, int r0, int c0, float* f) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) f[j] = p[j * LD];
 }
-// Same from global rows of stride rs: sc * sum over np partials pstride apart.
+// Four consecutive elements of bf16 or fp32 memory as fp32.
 template <typename T>
 __device__ __forceinline__ floatx4 ld4f(const T* p) {
   if constexpr (sizeof(T) == 4) {
@@ -419,27 +419,42 @@ __device__ __forceinline__ floatx4 ld4f(const T* p) {
     return floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
   }
 }
+// An fp32 fragment of a 16 x 32 MFMA operand from global rows of stride rs,
+// sc * the sum over NP partials pstride apart (element j of lane (lq, ln): row
+// r0 + ln, column c0 + 8 lq + j), in two halves: frg_load issues the loads
+// (raw values in registers), frg_done sums and scales, so the loads can be
+// issued a step before the fragment is used.
 template <int NP, typename T>
-__device__ __forceinline__ void frg(const T* X, size_t rs, size_t pstride, int r0, int c0,
-                                    float sc, float* f) {
+struct FrgPf {
+  using V4 = typename std::conditional<sizeof(T) == 4, floatx4, bf16x4>::type;
+  V4 a[NP], b[NP];
+};
+template <int NP, typename T>
+__device__ __forceinline__ void frg_load(FrgPf<NP, T>& f, const T* X, size_t rs, size_t pstride,
+                                         int r0, int c0) {
   const int lane = threadIdx.x & 63;
   const T* p = X + (size_t)(r0 + (lane & 15)) * rs + c0 + 8 * (lane >> 4);
-  floatx4 pa[NP], pb[NP];   // every partial's loads first, then the sums in order
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp) {
-    pa[pp] = ld4f(p + pp * pstride);
-    pb[pp] = ld4f(p + pp * pstride + 4);
+    f.a[pp] = *(const typename FrgPf<NP, T>::V4*)(p + pp * pstride);
+    f.b[pp] = *(const typename FrgPf<NP, T>::V4*)(p + pp * pstride + 4);
   }
-  floatx4 a = pa[0], b = pb[0];
+}
+template <int NP, typename T>
+__device__ __forceinline__ void frg_done(const FrgPf<NP, T>& f, float sc, float* out) {
+  floatx4 a = zero4(), b = zero4();
 #pragma unroll
-  for (int pp = 1; pp < NP; ++pp) {
-    a += pa[pp];
-    b += pb[pp];
+  for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] += (float)f.a[pp][j];
+      b[j] += (float)f.b[pp][j];
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    f[j] = sc * a[j];
-    f[4 + j] = sc * b[j];
+    out[j] = sc * a[j];
+    out[4 + j] = sc * b[j];
   }
 }
 // bf16x3 products: both operands fp32 (three MFMAs), or fp32 x bf16 (two).
@@ -482,6 +497,39 @@ __device__ __forceinline__ void stage_rows(float* ST, const T* X, size_t rs, siz
       if (scale) a *= scale[t];
       *(floatx4*)(ST + t * LS + c) = a;
     }
+  }
+}
+
+// stage_rows of 64 bf16 partial rows of 64 columns in two halves: rows_load
+// issues every load of the block (4 units per thread, NP partials each) into
+// registers, rows_store sums, scales and writes them to ST later, so the loads
+// of a block fly while an earlier step computes.
+template <int NP>
+struct RowsPf {
+  bf16x4 x[4][NP];
+};
+template <int NP>
+__device__ __forceinline__ void rows_load(RowsPf<NP>& pf, const __bf16* X, size_t rs,
+                                          size_t pstride) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int u = threadIdx.x + 256 * d, t = u >> 4, c = 4 * (u & 15);
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) pf.x[d][pp] = *(const bf16x4*)(X + (size_t)t * rs + c + pp * pstride);
+  }
+}
+template <int LS, int NP>
+__device__ __forceinline__ void rows_store(float* ST, const RowsPf<NP>& pf, const float* scale) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int u = threadIdx.x + 256 * d, t = u >> 4, c = 4 * (u & 15);
+    floatx4 a = zero4();
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp)
+      a += floatx4{(float)pf.x[d][pp][0], (float)pf.x[d][pp][1], (float)pf.x[d][pp][2],
+                   (float)pf.x[d][pp][3]};
+    if (scale) a *= scale[t];
+    *(floatx4*)(ST + t * LS + c) = a;
   }
 }
 
@@ -652,6 +700,11 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   __syncthreads();
 
+  // step 5's fragments of X = e o dq_new (partials) are loaded while step 4 computes
+  FrgPf<NPV, __bf16> pfx[KD / 32];
+#pragma unroll
+  for (int c = 0; c < KD / 32; ++c) frg_load(pfx[c], dq_p + rowk, hk, BTH * KD, t16, 32 * c);
+
   // ---- 4: Z = dO V^T; Z o P o Gamma -> S0, dP = Z o Gamma o Lambda o beta_s -> S4 -----
   {
     bf16x8 ad[VD / 32];
@@ -727,8 +780,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   {
     float ax[KD / 32][8];
 #pragma unroll
-    for (int c = 0; c < KD / 32; ++c)
-      frg<NPV>(dq_p + rowk, hk, BTH * KD, t16, 32 * c, s.e[t16 + ln], ax[c]);
+    for (int c = 0; c < KD / 32; ++c) frg_done(pfx[c], s.e[t16 + ln], ax[c]);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       floatx4 f = zero4();
@@ -745,6 +797,14 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     }
   }
   __syncthreads();
+
+  // step 7's fragments of e o dW_new (partials) and dU are loaded while step 6 computes
+  FrgPf<NPV, __bf16> pfw[KD / 32];
+  FrgPf<1, float> pfu[VD / 32];
+#pragma unroll
+  for (int c = 0; c < KD / 32; ++c) frg_load(pfw[c], dw_p + rowk, hk, BTH * KD, t16, 32 * c);
+#pragma unroll
+  for (int c = 0; c < VD / 32; ++c) frg_load(pfu[c], du + rowv, hv, 0, t16, 32 * c);
 
   // ---- 6: H = (F1 beta) Aw^T, D = E Aw^T; dGc_t -= rowsum(M o H); dM = tril(D) -> S0 --
   {
@@ -790,10 +850,9 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   {
     float a2[KD / 32][8], a3[VD / 32][8];
 #pragma unroll
-    for (int c = 0; c < KD / 32; ++c)
-      frg<NPV>(dw_p + rowk, hk, BTH * KD, t16, 32 * c, s.e[t16 + ln], a2[c]);
+    for (int c = 0; c < KD / 32; ++c) frg_done(pfw[c], s.e[t16 + ln], a2[c]);
 #pragma unroll
-    for (int c = 0; c < VD / 32; ++c) frg<1>(du + rowv, hv, 0, t16, 32 * c, 1.f, a3[c]);
+    for (int c = 0; c < VD / 32; ++c) frg_done(pfu[c], 1.f, a3[c]);
     float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -841,6 +900,11 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     for (int i = 0; i < 4; ++i) S5[(t16 + 4 * lq + i) * kLM + 16 * nt + ln] += acc[i];
   }
   __syncthreads();
+
+  // the kb loop's first partial block (X) is loaded while steps 9 compute
+  constexpr bool PF = KD <= 128;   // partial blocks prefetched into registers
+  RowsPf<NPV> pf;
+  if constexpr (PF) rows_load<NPV>(pf, dq_p + rowk, hk, BTH * KD);
 
   // ---- 9: Y = dAw Aw^T -> S1; dA = -strict-tril(Aw^T Y) -> S1 --------------------------
   {
@@ -911,7 +975,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       }
     }
     // ---- 10: X -> ST; dQ = X + dM K; U2 = -P^T X; dGc += rowdot(X, Q) ----------------
-    stage_rows<64, LS, NPV>(ST, dq_p + rowk + k0, hk, BTH * KD, s.e);
+    // (PF: each block's partial loads are issued one step before it is staged)
+    if constexpr (PF) {
+      rows_store<LS, NPV>(ST, pf, s.e);
+      rows_load<NPV>(pf, dw_p + rowk + k0, hk, BTH * KD);
+    } else {
+      stage_rows<64, LS, NPV>(ST, dq_p + rowk + k0, hk, BTH * KD, s.e);
+    }
     __syncthreads();
     floatx4 u2[4];
 #pragma unroll
@@ -939,7 +1009,12 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     __syncthreads();
 
     // ---- 11: e o dW_new -> ST; U2 += Aw^T ST ---------------------------------------------
-    stage_rows<64, LS, NPV>(ST, dw_p + rowk + k0, hk, BTH * KD, s.e);
+    if constexpr (PF) {
+      rows_store<LS, NPV>(ST, pf, s.e);
+      rows_load<NPV>(pf, dk_p + rowk + k0, hk, BTH * KD);
+    } else {
+      stage_rows<64, LS, NPV>(ST, dw_p + rowk + k0, hk, BTH * KD, s.e);
+    }
     __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
@@ -975,7 +1050,12 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     }
 
     // ---- 13: dK_new -> ST; dK = U1 + beta o U2 + r o dK_new; dbeta, dGc of K_new -------
-    stage_rows<64, LS, NPV>(ST, dk_p + rowk + k0, hk, BTH * KD, nullptr);
+    if constexpr (PF) {
+      rows_store<LS, NPV>(ST, pf, nullptr);
+      if (kb + 1 < KD / 64) rows_load<NPV>(pf, dq_p + rowk + k0 + 64, hk, BTH * KD);
+    } else {
+      stage_rows<64, LS, NPV>(ST, dk_p + rowk + k0, hk, BTH * KD, nullptr);
+    }
     __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)

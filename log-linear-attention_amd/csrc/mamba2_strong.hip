@@ -20,16 +20,20 @@
 // (value sum_s e^{Gc_last - Gc_s} k_s v_s^T, gate e^{Gc_last}), read after
 // the cascade and before the chunk's own decay and insertion.
 //
-// One workgroup (four waves) per (batch, head, 16 columns of V) walks the
-// chunks in order.  Wave w owns the output rows t = 16 w .. +15 and the state
-// rows k = 16 w .. +15 of every chunk-level level (one 16 x 16 fp32 tile per
-// level in registers).  Per chunk: the cascade (uniform selects over the
-// levels), the levels >= 2 staged in LDS as bf16, then with transposed
-// products (lane: one token t, four consecutive v)
-//   o^T += V^T (P o W)^T over the chunk and its predecessor (P = Q K^T, W the
-//          decay and lambda weights, from the two level tables in LDS)
-//   o^T += sum_j S_j^T (lam_j e^{Gc} Q)^T
-// and finally S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay.
+// One workgroup (eight waves) per (batch, head, 16 columns of V) walks the
+// chunks in order; the walk is a chain of dependent steps, so the chunk's
+// work is split over two sets of waves that run side by side.  Near wave w
+// (0-3) owns the state rows k = 16 w .. +15 of every chunk-level level (one
+// 16 x 16 fp32 tile per level in registers); wave w and far wave w + 4 both
+// own the output rows t = 16 w .. +15.  Per chunk: the cascade (near, uniform
+// selects over the levels), the levels >= 2 staged in LDS as bf16, then with
+// transposed products (lane: one token t, four consecutive v)
+//   near: o^T  = V^T (P o W)^T over the chunk and its predecessor (P = Q K^T,
+//               W the decay and lambda weights, from the two level tables in
+//               LDS), handed to the far wave through LDS
+//   far:  o^T += sum_j S_j^T (lam_j e^{Gc} Q)^T, and the store of o
+// and, after the hand-over, S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay
+// (near).
 #include "mamba2_strong.h"
 
 namespace hattn {
@@ -53,10 +57,13 @@ struct StrongSmem {
   float gc[2][kSC];                  // chunk-local inclusive cumsum of g
   float lam[kSC][kSLam];             // lambda[t, 0 .. L-1] of this chunk (L <= 32)
   unsigned tab[2][kSC * kSTab];      // intra / sub level tables, four levels a word
+  floatx4 onear[kSC][kSBV / 4];      // o^T of the near blocks, [t][v / 4]
 };
 
+constexpr int kSThreads = 512;
+
 template <typename TL, typename TO>
-__global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
+__global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, int nrows, int T, int G, int H, int V, int L) {
@@ -64,6 +71,11 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
   StrongSmem& s = *(StrongSmem*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
+  // waves 0-3 (near): the cascade and the chunk-level states (rows k = 16 w ..),
+  // the diagonal and sub-diagonal blocks, the insertion; waves 4-7 (far): the
+  // levels >= 2 and the output stores.  Wave w & 3 owns the tokens 16 (w & 3) ..
+  const bool near = w < 4;
+  const int wq = w & 3;
   const int nvb = V / kSBV;
   const XcdMap mp = xcd_map(blockIdx.x, nvb);
   if (mp.row >= nrows) return;
@@ -71,13 +83,15 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
   const int b = row / H, h = row % H, gq = h / (H / G);
   const int NT = T / kSC;
   const size_t hk = (size_t)G * 64, hv = (size_t)H * V;
-  const int t_me = 16 * w + ln;   // this lane's token in the transposed products
+  const int t_me = 16 * wq + ln;   // this lane's token in the transposed products
 
-  for (int i = tid; i < kSC * kSC / 4; i += 256) {
+  for (int i = tid; i < kSC * kSC / 4; i += kSThreads) {
     s.tab[0][(i >> 4) * kSTab + (i & 15)] = ((const unsigned*)kStrong.intra)[i];
     s.tab[1][(i >> 4) * kSTab + (i & 15)] = ((const unsigned*)kStrong.sub)[i];
   }
 
+  // Level-j state (near waves): one 16 x 16 fp32 tile, rows k = 16 w + 4 lq + i,
+  // column v = ln (the MFMA D layout), and the number of chunks it holds.
   floatx4 st[kSMaxLev];
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) st[j] = zero4();
@@ -86,33 +100,31 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
   for (int j = 0; j < kSMaxLev; ++j) cnt[j] = 0;
 
   // Inputs of one chunk in registers, loaded one chunk ahead so their latency
-  // hides behind the previous chunk's products: q / k rows (16 columns per
-  // thread), a v unit, g (wave 0) and up to eight lambda entries per thread
-  // (64 x L <= 2048).
-  const int r_ld = tid >> 2, c_ld = 16 * (tid & 3);
+  // hides behind the previous chunk's products: one 16-byte unit of q and of
+  // k per thread, a v unit (threads < 128), g (wave 0) and up to four lambda
+  // entries per thread (64 x L <= 2048).
+  const int r_ld = tid >> 3, c_ld = 8 * (tid & 7);
   const int rv_ld = tid >> 1, cv_ld = 8 * (tid & 1);
-  int lrel[8], llds[8];
+  int lrel[4], llds[4];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int i = min(tid + 256 * u, kSC * L - 1);
+  for (int u = 0; u < 4; ++u) {
+    const int i = min(tid + kSThreads * u, kSC * L - 1);
     lrel[u] = (i / L) * H * L + i % L;
     llds[u] = (i / L) * kSLam + i % L;
   }
-  u32x4 pq0, pq1, pk0, pk1, pv;
+  u32x4 pq, pk, pv;
   float pg;
-  TL pl[8];
+  TL pl[4];
   auto prefetch = [&](int jc) __attribute__((always_inline)) {
     const size_t t0 = (size_t)b * T + (size_t)jc * kSC;
     const size_t rq = (t0 + r_ld) * hk + (size_t)gq * 64 + c_ld;
-    pq0 = *(const u32x4*)(q + rq);
-    pq1 = *(const u32x4*)(q + rq + 8);
-    pk0 = *(const u32x4*)(k + rq);
-    pk1 = *(const u32x4*)(k + rq + 8);
+    pq = *(const u32x4*)(q + rq);
+    pk = *(const u32x4*)(k + rq);
     pv = *(const u32x4*)(v + (t0 + (tid < 128 ? rv_ld : 0)) * hv + (size_t)h * V + v0 + cv_ld);
     pg = g[(t0 + lane) * H + h];
     const TL* lb = l + (t0 * H + h) * L;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) pl[u] = lb[lrel[u]];
+    for (int u = 0; u < 4; ++u) pl[u] = lb[lrel[u]];
   };
   prefetch(0);
 
@@ -120,7 +132,7 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
     const int par = ic & 1;
     const size_t tok0 = (size_t)b * T + (size_t)ic * kSC;
     // ---- cascade (recurrent.py:56-74) over the chunk-level states ------------------
-    {
+    if (near) {
       floatx4 carry = zero4();
       int cc = 0;
 #pragma unroll
@@ -140,10 +152,8 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
     }
     // ---- stage: q, k, v tiles, g cumsum, lambda, levels >= 2 -------------------------
     {
-      *(u32x4*)(s.q + r_ld * kSLK + c_ld) = pq0;
-      *(u32x4*)(s.q + r_ld * kSLK + c_ld + 8) = pq1;
-      *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld) = pk0;
-      *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld + 8) = pk1;
+      *(u32x4*)(s.q + r_ld * kSLK + c_ld) = pq;
+      *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld) = pk;
       if (tid < 128) *(u32x4*)(s.v[par] + rv_ld * kSLV + cv_ld) = pv;
       if (w == 0) {
         float x = pg;
@@ -156,58 +166,61 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
         if (v0 == 0) gcum[(tok0 + lane) * H + h] = x;
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (tid + 256 * u < kSC * L) (&s.lam[0][0])[llds[u]] = to_f32<TL>(pl[u]);
+      for (int u = 0; u < 4; ++u)
+        if (tid + kSThreads * u < kSC * L) (&s.lam[0][0])[llds[u]] = to_f32<TL>(pl[u]);
+      if (near) {
 #pragma unroll
-      for (int j = 2; j < kSMaxLev; ++j)
-        *(bf16x4*)(s.hs[j] + ln * kSLK + 16 * w + 4 * lq) = cvt4(st[j]);
+        for (int j = 2; j < kSMaxLev; ++j)
+          *(bf16x4*)(s.hs[j] + ln * kSLK + 16 * w + 4 * lq) = cvt4(st[j]);
+      }
     }
     __syncthreads();
     if (ic + 1 < NT) prefetch(ic + 1);
 
-    // ---- o^T[v][t] for t = 16 w + ln ----------------------------------------------------
     floatx4 acc = zero4();   // o^T[v = 4 lq + i][t = t_me]
     const float gct = s.gc[par][t_me];
     // B operand of the q . k products: Q[t_me][32 c + 8 lq ..]
     const bf16x8 bq0 = *(const bf16x8*)(s.q + t_me * kSLK + 8 * lq);
     const bf16x8 bq1 = *(const bf16x8*)(s.q + t_me * kSLK + 32 + 8 * lq);
-    // diagonal (cur = 1) and sub-diagonal (cur = 0) blocks
+    if (near) {
+      // ---- diagonal (cur = 1) and sub-diagonal (cur = 0) blocks -------------------------
 #pragma unroll
-    for (int cur = 1; cur >= 0; --cur) {
-      if (!cur && ic == 0) break;
-      const int pk = cur ? par : par ^ 1;
-      const unsigned* tab = s.tab[cur ? 0 : 1] + t_me * kSTab;
-      const float* lrow = s.lam[t_me];
-      // the source tiles of the block: the diagonal stops at this wave's tile
-      const int npair = cur ? (w >> 1) + 1 : 2;
-      const float base = cur ? 0.f : s.gc[pk][kSC - 1];
-      for (int p = 0; p < npair; ++p) {
-        bf16x8 pb;
+      for (int cur = 1; cur >= 0; --cur) {
+        if (!cur && ic == 0) break;
+        const int pk2 = cur ? par : par ^ 1;
+        const unsigned* tab = s.tab[cur ? 0 : 1] + t_me * kSTab;
+        const float* lrow = s.lam[t_me];
+        // the source tiles of the block: the diagonal stops at this wave's tile
+        const int npair = cur ? (w >> 1) + 1 : 2;
+        const float base = cur ? 0.f : s.gc[pk2][kSC - 1];
+        for (int pp = 0; pp < npair; ++pp) {
+          bf16x8 pb;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int n = 2 * p + half;   // source tile
-          floatx4 sc = zero4();
-          sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 8 * lq), bq0, sc);
-          sc = mfma16x16x32(*(const bf16x8*)(s.k[pk] + (16 * n + ln) * kSLK + 32 + 8 * lq), bq1, sc);
-          // sc[i] = q_t . k_s, s = 16 n + 4 lq + i, t = t_me
-          const unsigned lv4 = tab[4 * n + lq];   // levels of the lane's four sources
+          for (int half = 0; half < 2; ++half) {
+            const int n = 2 * pp + half;   // source tile
+            floatx4 sc = zero4();
+            sc = mfma16x16x32(*(const bf16x8*)(s.k[pk2] + (16 * n + ln) * kSLK + 8 * lq), bq0, sc);
+            sc = mfma16x16x32(*(const bf16x8*)(s.k[pk2] + (16 * n + ln) * kSLK + 32 + 8 * lq), bq1, sc);
+            // sc[i] = q_t . k_s, s = 16 n + 4 lq + i, t = t_me
+            const unsigned lv4 = tab[4 * n + lq];   // levels of the lane's four sources
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int sp = 16 * n + 4 * lq + i;
-            float x = 0.f;
-            if (!cur || sp <= t_me) {
-              const int lev = (lv4 >> (8 * i)) & 0xff;
-              x = sc[i] * fexp(gct + base - s.gc[pk][sp]) * lrow[lev];
+            for (int i = 0; i < 4; ++i) {
+              const int sp = 16 * n + 4 * lq + i;
+              float x = 0.f;
+              if (!cur || sp <= t_me) {
+                const int lev = (lv4 >> (8 * i)) & 0xff;
+                x = sc[i] * fexp(gct + base - s.gc[pk2][sp]) * lrow[lev];
+              }
+              pb[4 * half + i] = (__bf16)x;
             }
-            pb[4 * half + i] = (__bf16)x;
           }
+          // o^T[v][t] += V[s][v] P^T[s][t] over the 32 sources of the pair
+          acc = mfma16x16x32(tr_frag_d(s.v[pk2], kSLV, 32 * pp, 0), pb, acc);
         }
-        // o^T[v][t] += V[s][v] P^T[s][t] over the 32 sources of the pair
-        acc = mfma16x16x32(tr_frag_d(s.v[pk], kSLV, 32 * p, 0), pb, acc);
       }
-    }
-    // far levels: o^T[v][t] += S_j^T[v][k] (lam[t, 6 + j] e^{Gc_t} q_t[k])
-    {
+      s.onear[t_me][lq] = acc;
+    } else {
+      // ---- far levels: o^T[v][t] += S_j^T[v][k] (lam[t, 6 + j] e^{Gc_t} q_t[k]) ----------
       const float eg = fexp(gct);
 #pragma unroll
       for (int j = 2; j < kSMaxLev; ++j) {
@@ -224,18 +237,10 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
         }
       }
     }
-    // store o[t_me][v0 + 4 lq .. +3]
-    {
-      TO* op = o + (tok0 + t_me) * hv + (size_t)h * V + v0 + 4 * lq;
-      if constexpr (sizeof(TO) == 2) {
-        *(bf16x4*)op = cvt4(acc);
-      } else {
-        *(floatx4*)op = acc;
-      }
-    }
+    __syncthreads();   // the near blocks' o^T in LDS
 
-    // ---- decay the levels, insert S_0 = K^T diag(e^{Gc_last - Gc}) V ------------------
-    {
+    if (near) {
+      // ---- decay the levels, insert S_0 = K^T diag(e^{Gc_last - Gc}) V ----------------
       const float glast = s.gc[par][kSC - 1];
       const float gd = fexp(glast);
 #pragma unroll
@@ -253,8 +258,22 @@ __global__ __launch_bounds__(256) void mamba2_strong_fwd_kernel(
       }
       st[0] = sum;
       cnt[0] += 1;
+    } else {
+      // ---- o[t_me][v0 + 4 lq .. +3] = far + near ------------------------------------
+      const floatx4 an = s.onear[t_me][lq];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += an[i];
+      TO* op = o + (tok0 + t_me) * hv + (size_t)h * V + v0 + 4 * lq;
+      if constexpr (sizeof(TO) == 2) {
+        *(bf16x4*)op = cvt4(acc);
+      } else {
+        *(floatx4*)op = acc;
+      }
     }
-    __syncthreads();
+    // No barrier here: the next chunk's staging writes q, lambda, the level
+    // states and the other parity's k / v / g cumsum, which this chunk read
+    // before the barrier above; the insertion reads this parity's, and the
+    // near waves stage the level states after it (program order).
   }
 }
 
@@ -270,7 +289,7 @@ static hipError_t strong_launch_t(const void* q, const void* k, const void* v, c
     return e;
   const int rows = B * H;
   const int grid = (rows + 7) / 8 * 8 * (V / kSBV);
-  hipLaunchKernelGGL(kf, dim3(grid), dim3(256), smem, stream, (const __bf16*)q, (const __bf16*)k,
+  hipLaunchKernelGGL(kf, dim3(grid), dim3(kSThreads), smem, stream, (const __bf16*)q, (const __bf16*)k,
                      (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum, rows, T, G, H, V, L);
   return hipGetLastError();
 }

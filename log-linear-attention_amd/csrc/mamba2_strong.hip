@@ -221,19 +221,17 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
       s.onear[t_me][lq] = acc;
     } else {
       // ---- far levels: o^T[v][t] += S_j^T[v][k] (lam[t, 6 + j] e^{Gc_t} q_t[k]) ----------
+      // a lane's four values share its token t_me: the level weight is one
+      // scalar per lane, applied to the product (q stays the exact bf16 input)
       const float eg = fexp(gct);
 #pragma unroll
       for (int j = 2; j < kSMaxLev; ++j) {
         if (6 + j < L) {
           const float f = s.lam[t_me][6 + j] * eg;
-          bf16x8 b0, b1;
+          floatx4 y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 8 * lq), bq0, zero4());
+          y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 32 + 8 * lq), bq1, y);
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            b0[jj] = (__bf16)((float)bq0[jj] * f);
-            b1[jj] = (__bf16)((float)bq1[jj] * f);
-          }
-          acc = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 8 * lq), b0, acc);
-          acc = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 32 + 8 * lq), b1, acc);
+          for (int i = 0; i < 4; ++i) acc[i] += f * y[i];
         }
       }
     }

@@ -77,10 +77,13 @@ inline StrongBwdWs strong_bwd_ws_layout(void* base, int B, int T, int H, int nf)
 // ---------------------------------------------------------------------------
 // chunk walks (far levels)
 // ---------------------------------------------------------------------------
+constexpr int kWThreads = 512;   // eight waves per walk workgroup
+
 struct WalkSmem {
   __bf16 d[kSC * kWLd];               // dO [t][v]
   __bf16 v[kSC * kWLd];               // V [t][v] (forward walk)
-  __bf16 q[kSC * kWLs];               // q [t][16-row K slice]
+  __bf16 q[2][kSC * kWLs];            // q [t][16-row K slice]: the forward walk's slice
+                                      // (first), or the reverse walk's two slices
   __bf16 k[kSC * kWLs];               // k [t][16-row K slice] (forward walk)
   __bf16 hs[kSMaxLev][16 * kWLd];     // forward walk: levels >= 2 as bf16 [k][v]
   float gc[kSC];
@@ -96,83 +99,86 @@ struct WalkArgs {
   int rows, T, H, L, nf;
 };
 
-// The chunk's dO (and for the forward walk V), the 16-column q (and k) slice,
-// Gc and the far lambda weights, loaded into registers one chunk ahead
-// (walk_load) and written to LDS at the chunk start (walk_store).
+// The chunk's dO (and for the forward walk V), the q (and k) columns of the
+// workgroup's K slices, Gc and the far lambda weights, loaded into registers
+// one chunk ahead (walk_load) and written to LDS at the chunk start
+// (walk_store).  One 16-byte unit of each per thread.
 template <typename TL>
 struct WalkPre {
-  u32x4 d0, d1, v0, v1, q, k;
+  u32x4 d, v, q, k;
   float g;
-  TL lf[2];
-  float gf[2];
+  TL lf;
+  float gf;
 };
 
+// k0: the first K column of the workgroup's slices (16 forward, 32 reverse)
 template <typename TL, bool FWD>
 __device__ __forceinline__ void walk_load(WalkPre<TL>& p, const WalkArgs& a, size_t tok0, int h,
                                           int k0) {
   const int tid = threadIdx.x, lane = tid & 63;
   const size_t hd = (size_t)a.H * 64;
   {
-    const int r = tid >> 2, c16 = 16 * (tid & 3);
-    const size_t off = (tok0 + r) * hd + (size_t)h * 64 + c16;
-    p.d0 = *(const u32x4*)(a.dO + off);
-    p.d1 = *(const u32x4*)(a.dO + off + 8);
-    if constexpr (FWD) {
-      p.v0 = *(const u32x4*)(a.v + off);
-      p.v1 = *(const u32x4*)(a.v + off + 8);
-    }
+    const int r = tid >> 3, c8 = 8 * (tid & 7);
+    const size_t off = (tok0 + r) * hd + (size_t)h * 64 + c8;
+    p.d = *(const u32x4*)(a.dO + off);
+    if constexpr (FWD) p.v = *(const u32x4*)(a.v + off);
   }
-  {
+  if constexpr (FWD) {
     const int r = (tid & 127) >> 1, c8 = 8 * (tid & 1);
     const size_t off = (tok0 + r) * hd + (size_t)h * 64 + k0 + c8;
     p.q = *(const u32x4*)(a.q + off);
-    if constexpr (FWD) p.k = *(const u32x4*)(a.k + off);
+    p.k = *(const u32x4*)(a.k + off);
+  } else {
+    const int r = (tid & 255) >> 2, c8 = 8 * (tid & 3);
+    p.q = *(const u32x4*)(a.q + (tok0 + r) * hd + (size_t)h * 64 + k0 + c8);
   }
   p.g = a.gc[(tok0 + lane) * a.H + h];
   const TL* l = (const TL*)a.l;
   const int nf1 = a.nf > 0 ? a.nf : 1;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = min(tid + 256 * u, nf1 * kSC - 1);
-    const size_t tk = (tok0 + i / nf1) * a.H + h;
-    p.lf[u] = l[tk * a.L + min(8 + i % nf1, a.L - 1)];   // column clamped for nf == 0
-    p.gf[u] = a.gc[tk];
-  }
+  const int i = min(tid, nf1 * kSC - 1);
+  const size_t tk = (tok0 + i / nf1) * a.H + h;
+  p.lf = l[tk * a.L + min(8 + i % nf1, a.L - 1)];   // column clamped for nf == 0
+  p.gf = a.gc[tk];
 }
 
 template <typename TL, bool FWD>
 __device__ __forceinline__ void walk_store(WalkSmem& s, const WalkPre<TL>& p, const WalkArgs& a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   {
-    const int r = tid >> 2, c16 = 16 * (tid & 3);
-    *(u32x4*)(s.d + r * kWLd + c16) = p.d0;
-    *(u32x4*)(s.d + r * kWLd + c16 + 8) = p.d1;
-    if constexpr (FWD) {
-      *(u32x4*)(s.v + r * kWLd + c16) = p.v0;
-      *(u32x4*)(s.v + r * kWLd + c16 + 8) = p.v1;
+    const int r = tid >> 3, c8 = 8 * (tid & 7);
+    *(u32x4*)(s.d + r * kWLd + c8) = p.d;
+    if constexpr (FWD) *(u32x4*)(s.v + r * kWLd + c8) = p.v;
+  }
+  if constexpr (FWD) {
+    if (tid < 128) {
+      const int r = tid >> 1, c8 = 8 * (tid & 1);
+      *(u32x4*)(s.q[0] + r * kWLs + c8) = p.q;
+      *(u32x4*)(s.k + r * kWLs + c8) = p.k;
+    }
+  } else {
+    if (tid < 256) {
+      const int r = tid >> 2, c8 = 8 * (tid & 3);
+      *(u32x4*)(s.q[c8 >> 4] + r * kWLs + (c8 & 15)) = p.q;
     }
   }
-  if (tid < 128) {
-    const int r = tid >> 1, c8 = 8 * (tid & 1);
-    *(u32x4*)(s.q + r * kWLs + c8) = p.q;
-    if constexpr (FWD) *(u32x4*)(s.k + r * kWLs + c8) = p.k;
-  }
   if (w == 0) s.gc[lane] = p.g;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = tid + 256 * u;
-    if (i < a.nf * kSC) s.f[i % a.nf][i / a.nf] = to_f32<TL>(p.lf[u]) * fexp(p.gf[u]);
-  }
+  if (tid < a.nf * kSC) s.f[tid % a.nf][tid / a.nf] = to_f32<TL>(p.lf) * fexp(p.gf);
 }
 
-// Forward walk: far dq of the slice (complete) and the slice's partial far dlambda.
+// Forward walk: far dq of the slice (complete) and the slice's partial far
+// dlambda.  Near waves 0-3 own the strong state (S_j[k = k0 + 4 lq + i][v =
+// 16 w + ln]): the cascade, the bf16 staging of the levels >= 2 and, after the
+// far products are issued, the decay and insertion of the chunk; far waves
+// 4-7 run the products of the levels >= 2 for the tokens 16 (w - 4) .. + 15.
 template <typename TL>
 __device__ __forceinline__ void strong_walk_fwd(WalkSmem& s, const WalkArgs& a, int row, int kap) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
+  const bool near = w < 4;
+  const int wq = w & 3;
   const int b = row / a.H, h = row % a.H, NT = a.T / kSC, k0 = 16 * kap;
-  const int t_me = 16 * w + ln;
-  floatx4 st[kSMaxLev];   // S_j[k = k0 + 4 lq + i][v = 16 w + ln]
+  const int t_me = 16 * wq + ln;
+  floatx4 st[kSMaxLev];   // near: S_j[k = k0 + 4 lq + i][v = 16 w + ln]
   int cnt[kSMaxLev];
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) {
@@ -183,7 +189,7 @@ __device__ __forceinline__ void strong_walk_fwd(WalkSmem& s, const WalkArgs& a, 
   walk_load<TL, true>(pre, a, (size_t)b * a.T, h, k0);
   for (int ic = 0; ic < NT; ++ic) {
     // cascade (recurrent.py:56-74) over the chunk-level states
-    {
+    if (near) {
       floatx4 carry = zero4();
       int cc = 0;
 #pragma unroll
@@ -202,68 +208,75 @@ __device__ __forceinline__ void strong_walk_fwd(WalkSmem& s, const WalkArgs& a, 
       }
     }
     walk_store<TL, true>(s, pre, a);
+    if (near) {
 #pragma unroll
-    for (int j = 2; j < kSMaxLev; ++j)
-      if (j - 2 < a.nf)
+      for (int j = 2; j < kSMaxLev; ++j)
+        if (j - 2 < a.nf)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s.hs[j][(4 * lq + i) * kWLd + 16 * w + ln] = (__bf16)st[j][i];
+          for (int i = 0; i < 4; ++i) s.hs[j][(4 * lq + i) * kWLd + 16 * w + ln] = (__bf16)st[j][i];
+    }
     __syncthreads();
     if (ic + 1 < NT) walk_load<TL, true>(pre, a, (size_t)b * a.T + (size_t)(ic + 1) * kSC, h, k0);
 
-    // Y^T[k][t] = S_j[k][v] dO^T[v][t] for the lane's token t_me, k = k0 + 4 lq + i
-    const bf16x8 bd0 = *(const bf16x8*)(s.d + t_me * kWLd + 8 * lq);
-    const bf16x8 bd1 = *(const bf16x8*)(s.d + t_me * kWLd + 32 + 8 * lq);
-    const bf16x4 q4 = *(const bf16x4*)(s.q + t_me * kWLs + 4 * lq);
-    const float eg = fexp(s.gc[t_me]);
-    floatx4 dq = zero4();
-    float* dlrow = a.ws.dlf + (((size_t)kap * a.rows + row) * a.T + (size_t)ic * kSC + t_me) * a.nf;
+    if (!near) {
+      // Y^T[k][t] = S_j[k][v] dO^T[v][t] for the lane's token t_me, k = k0 + 4 lq + i
+      const bf16x8 bd0 = *(const bf16x8*)(s.d + t_me * kWLd + 8 * lq);
+      const bf16x8 bd1 = *(const bf16x8*)(s.d + t_me * kWLd + 32 + 8 * lq);
+      const bf16x4 q4 = *(const bf16x4*)(s.q[0] + t_me * kWLs + 4 * lq);
+      const float eg = fexp(s.gc[t_me]);
+      floatx4 dq = zero4();
+      float* dlrow = a.ws.dlf + (((size_t)kap * a.rows + row) * a.T + (size_t)ic * kSC + t_me) * a.nf;
 #pragma unroll
-    for (int j = 2; j < kSMaxLev; ++j) {
-      if (j - 2 < a.nf) {
-        floatx4 y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kWLd + 8 * lq), bd0, zero4());
-        y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kWLd + 32 + 8 * lq), bd1, y);
-        const float f = s.f[j - 2][t_me];
-        float p = 0.f;
+      for (int j = 2; j < kSMaxLev; ++j) {
+        if (j - 2 < a.nf) {
+          floatx4 y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kWLd + 8 * lq), bd0, zero4());
+          y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kWLd + 32 + 8 * lq), bd1, y);
+          const float f = s.f[j - 2][t_me];
+          float p = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dq[i] += f * y[i];
-          p += (float)q4[i] * y[i];
+          for (int i = 0; i < 4; ++i) {
+            dq[i] += f * y[i];
+            p += (float)q4[i] * y[i];
+          }
+          p += __shfl_xor(p, 16, 64);
+          p += __shfl_xor(p, 32, 64);
+          if (lq == ((j - 2) & 3)) dlrow[j - 2] = p * eg;
         }
-        p += __shfl_xor(p, 16, 64);
-        p += __shfl_xor(p, 32, 64);
-        if (lq == ((j - 2) & 3)) dlrow[j - 2] = p * eg;
       }
+      *(floatx4*)(a.ws.dqf + ((size_t)row * a.T + (size_t)ic * kSC + t_me) * 64 + k0 + 4 * lq) = dq;
+    } else {
+      // decay, then S_0 = K^T diag(e^{Gc_last - Gc}) V
+      const float glast = s.gc[kSC - 1];
+      const float gd = fexp(glast);
+#pragma unroll
+      for (int j = 1; j < kSMaxLev; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[j][i] *= gd;
+      floatx4 sum = zero4();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bf16x8 ka = tr_frag(s.k, kWLs, 32 * c, 0);   // K[t = 32 c + 8 lq + jj][k0 + ln]
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          ka[jj] = (__bf16)((float)ka[jj] * fexp(glast - s.gc[32 * c + 8 * lq + jj]));
+        sum = mfma16x16x32(ka, tr_frag(s.v, kWLd, 32 * c, 16 * w), sum);
+      }
+      st[0] = sum;
+      cnt[0] += 1;
     }
-    *(floatx4*)(a.ws.dqf + ((size_t)row * a.T + (size_t)ic * kSC + t_me) * 64 + k0 + 4 * lq) = dq;
-
-    // decay, then S_0 = K^T diag(e^{Gc_last - Gc}) V
-    const float glast = s.gc[kSC - 1];
-    const float gd = fexp(glast);
-#pragma unroll
-    for (int j = 1; j < kSMaxLev; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st[j][i] *= gd;
-    floatx4 sum = zero4();
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      bf16x8 ka = tr_frag(s.k, kWLs, 32 * c, 0);   // K[t = 32 c + 8 lq + jj][k0 + ln]
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj)
-        ka[jj] = (__bf16)((float)ka[jj] * fexp(glast - s.gc[32 * c + 8 * lq + jj]));
-      sum = mfma16x16x32(ka, tr_frag(s.v, kWLd, 32 * c, 16 * w), sum);
-    }
-    st[0] = sum;
-    cnt[0] += 1;
     __syncthreads();
   }
 }
 
-// Reverse walk: the adjoint of every chunk's insertion, d kv_n, for the slice's 16 rows of K.
+// Reverse walk: the adjoint of every chunk's insertion, d kv_n, for two 16-row
+// slices of K (slices 2 kp and 2 kp + 1): waves 4 sl .. 4 sl + 3 run slice
+// 2 kp + sl, wave w & 3 owning the columns v = 16 (w & 3) .. + 15.
 template <typename TL>
-__device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, int row, int kap) {
+__device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, int row, int kp) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
-  const int b = row / a.H, h = row % a.H, NT = a.T / kSC, k0 = 16 * kap;
+  const int wv = w & 3, sl = w >> 2;
+  const int b = row / a.H, h = row % a.H, NT = a.T / kSC, k0 = 16 * (2 * kp + sl);
   // merge level of the forward cascade at each step: the first level >= 1
   // that keeps (or takes into an empty slot) the carry; kSMaxLev = dropped
   if (tid == 0) {
@@ -285,29 +298,29 @@ __device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, 
       cnt[0] += 1;
     }
   }
-  floatx4 st[kSMaxLev];   // A_j[k = k0 + 4 lq + i][v = 16 w + ln]
+  floatx4 st[kSMaxLev];   // A_j[k = k0 + 4 lq + i][v = 16 wv + ln]
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) st[j] = zero4();
   WalkPre<TL> pre;
-  walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(NT - 1) * kSC, h, k0);
+  walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(NT - 1) * kSC, h, 32 * kp);
   for (int ic = NT - 1; ic >= 0; --ic) {
     walk_store<TL, false>(s, pre, a);
     {
-      __bf16* ap = a.ws.adj + (((size_t)row * NT + ic) * 64 + k0 + 4 * lq) * 64 + 16 * w + ln;
+      __bf16* ap = a.ws.adj + (((size_t)row * NT + ic) * 64 + k0 + 4 * lq) * 64 + 16 * wv + ln;
 #pragma unroll
       for (int i = 0; i < 4; ++i) ap[i * 64] = (__bf16)st[0][i];
     }
     st[0] = zero4();
     __syncthreads();
-    if (ic > 0) walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(ic - 1) * kSC, h, k0);
+    if (ic > 0) walk_load<TL, false>(pre, a, (size_t)b * a.T + (size_t)(ic - 1) * kSC, h, 32 * kp);
     const float gd = fexp(s.gc[kSC - 1]);
 #pragma unroll
     for (int j = 1; j < kSMaxLev; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) st[j][i] *= gd;
     // A_j[k][v] += sum_t Q[t][k] f_j[t] dO[t][v], t = 32 c + 8 lq + jj
-    const bf16x8 bd0 = tr_frag(s.d, kWLd, 0, 16 * w), bd1 = tr_frag(s.d, kWLd, 32, 16 * w);
-    const bf16x8 qa0 = tr_frag(s.q, kWLs, 0, 0), qa1 = tr_frag(s.q, kWLs, 32, 0);
+    const bf16x8 bd0 = tr_frag(s.d, kWLd, 0, 16 * wv), bd1 = tr_frag(s.d, kWLd, 32, 16 * wv);
+    const bf16x8 qa0 = tr_frag(s.q[sl], kWLs, 0, 0), qa1 = tr_frag(s.q[sl], kWLs, 32, 0);
 #pragma unroll
     for (int j = 2; j < kSMaxLev; ++j) {
       if (j - 2 < a.nf) {
@@ -338,14 +351,16 @@ __device__ __forceinline__ void strong_walk_rev(WalkSmem& s, const WalkArgs& a, 
   }
 }
 
+// Blocks [0, half): forward walks, one per (row, 16-row K slice); blocks
+// [half, ..): reverse walks, one per (row, pair of K slices).
 template <typename TL>
-__global__ __launch_bounds__(256) void mamba2_strong_bwd_walk_kernel(WalkArgs a, int half) {
+__global__ __launch_bounds__(kWThreads) void mamba2_strong_bwd_walk_kernel(WalkArgs a, int half) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   WalkSmem& s = *(WalkSmem*)smem_raw;
   int wg = blockIdx.x;
   const bool rev = wg >= half;
   if (rev) wg -= half;
-  const XcdMap mp = xcd_map(wg, 4);
+  const XcdMap mp = xcd_map(wg, rev ? 2 : 4);
   if (mp.row >= a.rows) return;
   if (rev) strong_walk_rev<TL>(s, a, mp.row, mp.slice);
   else strong_walk_fwd<TL>(s, a, mp.row, mp.slice);
@@ -723,8 +738,8 @@ static hipError_t strong_bwd_launch_t(const void* q, const void* k, const void* 
       return e;
     WalkArgs a{(const __bf16*)q, (const __bf16*)k, (const __bf16*)v, (const __bf16*)dO, gc, l,
                ws, rows, T, H, L, nf};
-    const int half = rpad * 4;
-    hipLaunchKernelGGL(kf, dim3(2 * half), dim3(256), smem, stream, a, half);
+    const int half = rpad * 4;   // forward walks; then rpad * 2 reverse walks
+    hipLaunchKernelGGL(kf, dim3(half + rpad * 2), dim3(kWThreads), smem, stream, a, half);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {

@@ -492,13 +492,15 @@ GDN_C3 = (4, 8192, 16, 128, 128, 14)
 
 
 def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3, warmup=5):
-    """Cold-cache medians of the log-linear Gated DeltaNet chunkwise forward and
-    forward + backward (chunkwise_hgdn.chunkwise_fwd / chunkwise_bwd) at BASELINE
-    config 3, MFMA roofline by the algorithmic FLOPs (backward counted as twice
-    the forward, the usual convention).  Returns one record per key (None for
-    keys not asked for)."""
+    """Cold-cache medians of the log-linear Gated DeltaNet chunkwise forward
+    (chunkwise_hgdn.chunkwise_fwd) and forward + backward (chunkwise_fwd_keep /
+    chunkwise_bwd with the kept workspace, the HAttentionFunction path) at
+    BASELINE config 3, MFMA roofline by the algorithmic FLOPs (backward counted
+    as twice the forward, the usual convention).  Returns one record per key
+    (None for keys not asked for)."""
     from hattention.base import HType
-    from hattention.chunkwise_hgdn import chunkwise_fwd as gdn_fwd, chunkwise_bwd as gdn_bwd
+    from hattention.chunkwise_hgdn import (chunkwise_fwd as gdn_fwd, chunkwise_bwd as gdn_bwd,
+                                           chunkwise_fwd_keep as gdn_fwd_keep)
     GB, GT, GH, GK, GV, GL = shape
     gq, gk, gv, gbeta, gg, gl = make_gdn_inputs(GB, GT, GH, GK, GV, GL, device=dev)
     gdo = torch.randn(GB, GT, GH, GV, device=dev, dtype=torch.bfloat16)
@@ -510,8 +512,11 @@ def gdn_records(dev, stream, evict, reps, keys=("fwd", "fwd_bwd"), shape=GDN_C3,
         return gdn_fwd(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64, False)
 
     def gdn_fb_step():
-        gc, _, Aw, Au, _ = gdn_step()
-        return gdn_bwd(gq, gk, gv, gbeta, gc, gl, Aw, Au, gdo, False, 2, HType.WEAK, 64)
+        # as HAttentionFunction: the forward keeps what the backward would recompute
+        gc, _, Aw, Au, _, fws = gdn_fwd_keep(gq, gk, gv, gbeta, gg, gl, False, 2, HType.WEAK, 64,
+                                             False)
+        return gdn_bwd(gq, gk, gv, gbeta, gc, gl, Aw, Au, gdo, False, 2, HType.WEAK, 64,
+                       fwd_ws=fws)
 
     gfl = gdn_fwd_flops(GB, GT, GH, GK, GV)
     out = {}

@@ -250,6 +250,31 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
 size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int L);
 
 /*
+ * hattn_gdn_chunkwise_fwd that also leaves, in its workspace, what the
+ * backward's recompute would produce: q_new, W_new, K_new, U and every level's
+ * state at every chunk start (bf16), the same values bit for bit.  No
+ * counterpart in the reference (its backward recomputes them,
+ * chunkwise_hgdn.py:860-893); for callers that keep the forward's workspace
+ * until the backward, as HAttentionFunction does between its forward and
+ * backward (kernel.py:32-244).  Same arguments, outputs and status codes as
+ * hattn_gdn_chunkwise_fwd with workspace >= hattn_gdn_chunkwise_fwd_keep_workspace(...)
+ * bytes; additionally V in {64, 128} and T <= 64 * 2^8 (the backward's
+ * limits) -> else HATTN_ERR_NOT_IMPLEMENTED.
+ */
+int hattn_gdn_chunkwise_fwd_keep(const void* q, const void* k, const void* v, const void* beta,
+                                 const float* g, const void* l, void* o, float* g_cumsum,
+                                 void* Aw, void* Au, float* ht, int B, int T, int H, int K, int V,
+                                 int L, int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
+                                 int level_base, int htype, int chunk_size, int l2norm_qk,
+                                 float qk_scale, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/* Workspace bytes of hattn_gdn_chunkwise_fwd_keep (the forward's, plus the
+ * token-major k_new and the per-chunk level states).  No counterpart in the
+ * reference. */
+size_t hattn_gdn_chunkwise_fwd_keep_workspace(int B, int T, int H, int K, int V, int L);
+
+/*
  * Log-linear Gated DeltaNet chunkwise backward.
  *
  * Replaces hattention/chunkwise_hgdn.py:791-1222 `chunkwise_bwd(q, k, v, b, g, l,
@@ -284,11 +309,38 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
                             size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of hattn_gdn_chunkwise_bwd: the recomputed q_new, k_new (token-major
- * and per-chunk transposed), w_new, u (bf16), every level's state at every chunk start (bf16), and the fp32
+ * and per-chunk transposed), w_new, u (bf16), every level's state at every chunk start (bf16), and the
  * per-V-slice partial gradients of the level scan.  No counterpart in the
  * reference, which allocates h / dh and its temporaries with torch inside
  * chunkwise_bwd (chunkwise_hgdn.py:894-913). */
 size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L);
+
+/*
+ * hattn_gdn_chunkwise_bwd without the recompute: q_new, W_new, K_new, U and
+ * the level states come from fwd_workspace, the workspace of the
+ * hattn_gdn_chunkwise_fwd_keep call on the same q, k, v, beta, g, l, B, T, H,
+ * K, V, L, l2norm_qk and qk_scale, unchanged since.  No counterpart in the
+ * reference (see hattn_gdn_chunkwise_fwd_keep).  Same arguments, results and
+ * status codes as hattn_gdn_chunkwise_bwd, with workspace >=
+ * hattn_gdn_chunkwise_bwd_fwd_ws_workspace(...) bytes (the level scan's
+ * partial gradients only), plus fwd_workspace null or fwd_workspace_bytes
+ * below hattn_gdn_chunkwise_fwd_keep_workspace(...) -> HATTN_ERR_VALUE.  The
+ * results equal hattn_gdn_chunkwise_bwd's bit for bit; a workspace of another
+ * call gives wrong gradients.
+ */
+int hattn_gdn_chunkwise_bwd_fwd_ws(const void* q, const void* k, const void* v, const void* beta,
+                                   const float* g_cumsum, const void* l, const void* Aw,
+                                   const void* Au, const void* do_, void* dq, void* dk, void* dv,
+                                   void* db, float* dg, float* dl, int B, int T, int H, int K,
+                                   int V, int L, int dtype_qkv, int dtype_beta, int dtype_l,
+                                   int dtype_do, int level_base, int htype, int chunk_size,
+                                   int l2norm_qk, float qk_scale, void* workspace,
+                                   size_t workspace_bytes, const void* fwd_workspace,
+                                   size_t fwd_workspace_bytes, void* stream);
+
+/* Workspace bytes of hattn_gdn_chunkwise_bwd_fwd_ws: the level scan's partial
+ * gradients (no recompute regions).  No counterpart in the reference. */
+size_t hattn_gdn_chunkwise_bwd_fwd_ws_workspace(int B, int T, int H, int K, int V, int L);
 
 /*
  * One decode step of the Fenwick level state (HState) for every (b, h).

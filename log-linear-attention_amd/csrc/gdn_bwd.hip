@@ -1209,19 +1209,25 @@ struct GdnBwdWs {
 
 inline size_t balign(size_t x) { return (x + 255) & ~(size_t)255; }
 
-inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V, int nlev) {
+// recompute = false: no recompute regions (the caller brings q_new, K_new,
+// W_new, U and the level states from a forward that kept them).
+inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V, int nlev,
+                                  bool recompute = true) {
   GdnBwdWs w;
   char* p = (char*)base;
   size_t off = 0;
   const size_t n = (size_t)B * T * H;
   const size_t NT = (size_t)T / kGC, nvs = (size_t)V / kBVs;
   const size_t nl = nlev > 0 ? (size_t)nlev : 1;
-  w.qn = (__bf16*)(p + off); off += balign(n * K * 2);
-  w.kn = (__bf16*)(p + off); off += balign(n * K * 2);
-  w.knT = (__bf16*)(p + off); off += balign(n * K * 2);
-  w.wn = (__bf16*)(p + off); off += balign(n * K * 2);
-  w.un = (__bf16*)(p + off); off += balign(n * V * 2);
-  w.hs = (__bf16*)(p + off); off += balign((size_t)B * H * NT * nl * V * K * 2);
+  w.qn = w.kn = w.knT = w.wn = w.un = w.hs = nullptr;
+  if (recompute) {
+    w.qn = (__bf16*)(p + off); off += balign(n * K * 2);
+    w.kn = (__bf16*)(p + off); off += balign(n * K * 2);
+    w.knT = (__bf16*)(p + off); off += balign(n * K * 2);
+    w.wn = (__bf16*)(p + off); off += balign(n * K * 2);
+    w.un = (__bf16*)(p + off); off += balign(n * V * 2);
+    w.hs = (__bf16*)(p + off); off += balign((size_t)B * H * NT * nl * V * K * 2);
+  }
   w.dq_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
   w.dw_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
   w.dk_p = (__bf16*)(p + off); off += balign(nvs * n * K * 2);
@@ -1276,19 +1282,14 @@ size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
   return hattn::gdn_bwd_ws_layout(nullptr, B, T, H, K, V, nlev).bytes;
 }
 
-hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
-                                const float* gcum, const void* l, const void* dO, void* dq,
-                                void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
-                                int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, int norm_qk, float scale, hipStream_t stream,
-                                int* unsupported) {
+namespace {
+// The level scan and the chunk kernel on the recompute results in w.
+hipError_t gdn_bwd_dispatch(const void* q, const void* k, const void* v, const void* beta,
+                            const float* gcum, const void* l, const void* dO, void* dq, void* dk,
+                            void* dv, void* db, float* dg, float* dl, const hattn::GdnBwdWs& w,
+                            int B, int T, int H, int K, int V, int L, int nlev, int dt_b, int dt_l,
+                            int norm_qk, float scale, hipStream_t stream, int* unsupported) {
   using namespace hattn;
-  *unsupported = 0;
-  const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
-  hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.knT, w.wn, w.un, w.hs,
-                                            B, T, H, K, V, L, nlev, dt_b, dt_l, norm_qk, scale,
-                                            stream, unsupported);
-  if (e != hipSuccess || *unsupported) return e;
 #define HATTN_GDN_B(KD_, VD_)                                                                   \
   if (K == KD_ && V == VD_) {                                                                   \
     if (dt_b == 0 && dt_l == 0)                                                                 \
@@ -1315,4 +1316,48 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
 #undef HATTN_GDN_B
   *unsupported = 1;
   return hipSuccess;
+}
+}  // namespace
+
+hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
+                                const float* gcum, const void* l, const void* dO, void* dq,
+                                void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
+                                int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
+                                int dt_l, int norm_qk, float scale, hipStream_t stream,
+                                int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
+  hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.knT, w.wn, w.un, w.hs,
+                                            B, T, H, K, V, L, nlev, dt_b, dt_l, norm_qk, scale,
+                                            stream, unsupported);
+  if (e != hipSuccess || *unsupported) return e;
+  return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
+                          L, nlev, dt_b, dt_l, norm_qk, scale, stream, unsupported);
+}
+
+size_t hattn_gdn_bwd_kept_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
+  return hattn::gdn_bwd_ws_layout(nullptr, B, T, H, K, V, nlev, false).bytes;
+}
+
+// The backward with q_new, W_new, K_new, U and the level states from a forward
+// that kept them (hattn_gdn_fwd_keep_launch): no recompute.
+hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v,
+                                     const void* beta, const float* gcum, const void* l,
+                                     const void* dO, void* dq, void* dk, void* dv, void* db,
+                                     float* dg, float* dl, const __bf16* qn, const __bf16* wn,
+                                     const __bf16* kn, const __bf16* un, const __bf16* hs,
+                                     void* ws, int B, int T, int H, int K, int V, int L, int nlev,
+                                     int dt_b, int dt_l, int norm_qk, float scale,
+                                     hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+  GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev, false);
+  w.qn = const_cast<__bf16*>(qn);
+  w.wn = const_cast<__bf16*>(wn);
+  w.kn = const_cast<__bf16*>(kn);
+  w.un = const_cast<__bf16*>(un);
+  w.hs = const_cast<__bf16*>(hs);
+  return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
+                          L, nlev, dt_b, dt_l, norm_qk, scale, stream, unsupported);
 }

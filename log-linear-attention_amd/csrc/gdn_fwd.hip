@@ -66,10 +66,12 @@ struct GdnPrepSmem {
 constexpr int kPrepThreads = 512;
 // MODE kPrepFwd: g is the per-step log decay (its chunk-local cumsum is
 // written to gcum); outputs Aw, Au, q_new, W_new, K_new^T, U, P.
+// MODE kPrepFwdKeep: the same, plus the token-major K_new, so that the
+// backward can take q_new, W_new, K_new and U from the forward.
 // MODE kPrepRecompute (the backward): g already holds the chunk-local cumsum
 // (chunkwise_hgdn.py:799-817); outputs q_new, W_new, K_new (token-major and
 // transposed) and U.
-enum { kPrepFwd = 0, kPrepRecompute = 1 };
+enum { kPrepFwd = 0, kPrepRecompute = 1, kPrepFwdKeep = 2 };
 
 template <int KD, typename TB, typename TL, int MODE>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
   // the chunk-local cumsum of g is written by wave 0; the other waves store
   // through an empty range, so the store (like every load) is unconditional and
   // the compiler can count the memory operations in flight
-  const rsrc_t rgc = make_rsrc(gcum, MODE == kPrepFwd && w == 0 ? (size_t)nchunks * kGC * 4 : 0);
+  constexpr bool kFwd = MODE != kPrepRecompute;
+  const rsrc_t rgc = make_rsrc(gcum, kFwd && w == 0 ? (size_t)nchunks * kGC * 4 : 0);
 
   // ---- stage a chunk: Q, K (l2-normalised on request), the cumsum of g, beta,
   //      lambda -> LDS.  Called before the walk and at the end of each chunk.
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
       *(u32x4*)(s.k + r * LK + cc) = pk[i];
     }
     float x = pg;
-    if constexpr (MODE == kPrepFwd) {
+    if constexpr (kFwd) {
       x = chunk_cumsum(x);
       buf_store<float>(x, rgc, (unsigned int)(lane * H * 4), (unsigned int)((t0 * H + hs) * 4));
     }
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
       }
       *(bf16x8*)(s.aw + t * kLd64 + s0) = a;
       *(bf16x8*)(s.au + t * kLd64 + s0) = au;
-      if constexpr (MODE == kPrepFwd) {
+      if constexpr (kFwd) {
         *(bf16x8*)(aw_out + ((tok0 + t) * H + h) * kGC + s0) = a;
         *(bf16x8*)(au_out + ((tok0 + t) * H + h) * kGC + s0) = au;
       }
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const float egt = fexp(s.gc[t]);
 
     // ---- P = (M Aw) o gamma o beta_s o lambda[t, lev(t, s)] (bf16 output) -------------
-    if constexpr (MODE == kPrepFwd) {
+    if constexpr (kFwd) {
       const bf16x8 bm0 = rows_frag(s.mq, 0), bm1 = rows_frag(s.mq, 1);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -297,7 +300,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         for (int j = 0; j < 8; ++j)
           x[j] = (__bf16)((float)s.k[(t8 + j) * LK + 64 * cb + col] * fexp(egl - s.gc[t8 + j]));
         *(bf16x8*)(knT + (((size_t)row * NT + ic) * KD + 64 * cb + col) * kGC + t8) = x;
-        if constexpr (MODE == kPrepRecompute) {
+        if constexpr (MODE != kPrepFwd) {
           const int tr = tid >> 3, c8 = 8 * (tid & 7);
           const float ek = fexp(egl - s.gc[tr]);
           const bf16x8 kx = *(const bf16x8*)(s.k + tr * LK + 64 * cb + c8);
@@ -422,11 +425,14 @@ __device__ __forceinline__ bf16x8 frag_k2(const __bf16* X, int ld, int r, int c)
 // barrier publishes the chunk's operands (staged in LDS from registers loaded
 // during the previous chunk), the second the level reads, which every thread
 // then sums for four outputs and stores.
-// HSAVE (the backward's recompute): every level's state at every chunk start
-// is written to hsave, bf16 [row][chunk][level][v][k]; no output (o, q_new,
-// P and the V slice are not read).  A separate instantiation, so the forward
-// carries no registers for it.
-template <int KD, int BV, typename TL, typename TO, bool HSAVE>
+// SMODE kScanOut: the forward (o).  kScanSave (the backward's recompute): every
+// level's state at every chunk start is written to hsave, bf16
+// [row][chunk][level][v][k]; no output (o, q_new, P and the V slice are not
+// read).  kScanOutSave: both, for a forward whose backward takes the states
+// from it.  Separate instantiations, so the plain forward carries no
+// registers for the states' stores.
+enum { kScanOut = 0, kScanSave = 1, kScanOutSave = 2 };
+template <int KD, int BV, typename TL, typename TO, int SMODE>
 __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ knT,
     const __bf16* __restrict__ un, const __bf16* __restrict__ pm, const __bf16* __restrict__ vin,
@@ -435,6 +441,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     int nlev, int final_state) {
   using C = GdnScanCfg<KD, BV>;
   using Sm = GdnScanSmem<KD, BV>;
+  constexpr bool kSave = SMODE != kScanOut, kOut = SMODE != kScanSave;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
   constexpr int NVT = C::NVT, NKT = C::NKT, NC = C::NC, LK = C::LK, LT = C::LT, LVS = C::LVS;
@@ -506,7 +513,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       rk[r] = *(const u32x4*)(knrow + (size_t)jc * KD * kGC + 8 * (tid + 512 * r));
 #pragma unroll
     for (int r = 0; r < KU; ++r) rw[r] = *(const u32x4*)(wrow + tokoff * KD + wq_off[r]);
-    if constexpr (!HSAVE) {
+    if constexpr (kOut) {
       rp = *(const u32x4*)(pmrow + (size_t)jc * kGC * kGC + 8 * tid);
 #pragma unroll
       for (int r = 0; r < KU; ++r) rq[r] = *(const u32x4*)(qrow + tokoff * KD + wq_off[r]);
@@ -526,7 +533,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       *(u32x4*)(s.kt + (u >> 3) * LT + 8 * (u & 7)) = rk[r];
       *(u32x4*)(s.wq[0] + wq_lds[r]) = rw[r];
     }
-    if constexpr (!HSAVE) {
+    if constexpr (kOut) {
       *(u32x4*)(s.pm + (tid >> 3) * LT + 8 * (tid & 7)) = rp;
 #pragma unroll
       for (int r = 0; r < KU; ++r) *(u32x4*)(s.wq[1] + wq_lds[r]) = rq[r];
@@ -539,15 +546,15 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
   const int ot = tid / VG, ov = 4 * (tid % VG);
   // ot < kGC <=> tid < 64 VG <=> w < VG: a wave-uniform test, so the output
   // descriptor is scalar (a per-lane one makes the store a loop over lanes)
-  const bool o_ok = !HSAVE && o != nullptr && w < VG;
+  const bool o_ok = kOut && o != nullptr && w < VG;
   const rsrc_t ro = make_rsrc(o_ok ? (const void*)(o + rowtok * V + v0) : (const void*)gcum,
                               o_ok ? (size_t)T * H * V * sizeof(TO) : 0);
   const unsigned o_voff = ((o_ok ? ot : 0) * HV + ov) * sizeof(TO);
   // hsave: this level's planes (an empty range for the waves without a level)
-  const rsrc_t rh = make_rsrc(HSAVE ? (const void*)(hsave + (size_t)row * NT * nlev * V * KD +
+  const rsrc_t rh = make_rsrc(kSave ? (const void*)(hsave + (size_t)row * NT * nlev * V * KD +
                                                     (size_t)(act ? e : 0) * V * KD + (size_t)v0 * KD)
                                     : (const void*)gcum,
-                              HSAVE && act ? (size_t)NT * nlev * V * KD * 2 : 0);
+                              kSave && act ? (size_t)NT * nlev * V * KD * 2 : 0);
 
   stage_load(0);
   stage_store();
@@ -564,7 +571,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const bool wr = act && !rd;
     const bool needy = act && !first && !reset;
 
-    if constexpr (HSAVE) {
+    if constexpr (kSave) {
       // level e's state at the chunk start -> hsave[row][ic][e][v][k]
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
@@ -573,7 +580,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           buf_store8(__builtin_bit_cast(uint2, cvt4(st[kt][nt])), rh,
                      (unsigned)(((16 * nt + ln) * KD + 16 * kt + 4 * lq) * 2),
                      (unsigned)((size_t)ic * nlev * V * KD * 2));
-    } else {
+    }
+    if constexpr (kOut) {
       if (rd) {
         // the level read lambda[t, 7 + e] (q_new h_e)[t][v] -> part[e]
         floatx4 racc[4][NVT];
@@ -689,7 +697,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     __syncthreads();   // the chunk's operands are consumed, its level reads written
 
     stage_store();     // chunk ic + 1
-    if constexpr (!HSAVE) {
+    if constexpr (kOut) {
       // o = o_intra + the reads of the levels with bit e of ic set
       const int po = (ot & (kGC - 1)) * LP + ov;
       floatx4 x = *(const floatx4*)(&s.part[kGMaxLev][po]);
@@ -733,6 +741,27 @@ inline GdnWs gdn_ws_layout(void* base, int B, int T, int H, int K, int V) {
   w.knT = (__bf16*)(p + off); off += galign(n * K * 2);
   w.un = (__bf16*)(p + off); off += galign(n * V * 2);
   w.pm = (__bf16*)(p + off); off += galign(n * kGC * 2);
+  w.bytes = off;
+  return w;
+}
+
+// The forward that keeps, for the backward, what its recompute would produce:
+// the forward's buffers, then the token-major K_new and every level's state at
+// every chunk start (bf16 [row][chunk][level][v][k], the backward's layout).
+struct GdnKeepWs {
+  GdnWs f;
+  __bf16 *kn, *hs;
+  size_t bytes;
+};
+
+inline GdnKeepWs gdn_keep_ws_layout(void* base, int B, int T, int H, int K, int V, int nlev) {
+  GdnKeepWs w;
+  w.f = gdn_ws_layout(base, B, T, H, K, V);
+  char* p = (char*)base;
+  size_t off = w.f.bytes;
+  const size_t n = (size_t)B * T * H, NT = (size_t)T / kGC, nl = nlev > 0 ? (size_t)nlev : 1;
+  w.kn = (__bf16*)(p + off); off += galign(n * K * 2);
+  w.hs = (__bf16*)(p + off); off += galign((size_t)B * H * NT * nl * V * K * 2);
   w.bytes = off;
   return w;
 }
@@ -782,7 +811,10 @@ static hipError_t gdn_scan_launch_t(const GdnWs& w, const void* v, const float* 
                                     int T, int H, int V, int L, int nlev, int final_state,
                                     hipStream_t stream) {
   constexpr int BV = ScanBV<KD>::value;
-  auto ks = hsave ? gdn_scan_kernel<KD, BV, TL, TO, true> : gdn_scan_kernel<KD, BV, TL, TO, false>;
+  // hsave without o: the recompute; both: a forward that keeps the states
+  auto ks = !hsave ? gdn_scan_kernel<KD, BV, TL, TO, kScanOut>
+            : o ? gdn_scan_kernel<KD, BV, TL, TO, kScanOutSave>
+                : gdn_scan_kernel<KD, BV, TL, TO, kScanSave>;
   const int smem = (int)sizeof(GdnScanSmem<KD, BV>);
   hipError_t e;
   if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -810,7 +842,66 @@ static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, cons
                                        ht != nullptr ? 1 : 0, stream);
 }
 
+template <int KD, typename TB, typename TL, typename TO>
+static hipError_t gdn_launch_keep_t(const void* q, const void* k, const void* v, const void* beta,
+                                    const float* g, const void* l, void* o, float* gcum, void* aw,
+                                    void* au, float* ht, void* ws, int B, int T, int H, int V,
+                                    int L, int nlev, int norm_qk, float scale, hipStream_t stream) {
+  const GdnKeepWs w = gdn_keep_ws_layout(ws, B, T, H, KD, V, nlev);
+  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwdKeep>(
+      q, k, v, beta, g, l, gcum, aw, au, w.f.qn, w.f.wn, w.kn, w.f.knT, w.f.un, w.f.pm, B, T, H,
+      V, L, norm_qk, scale, stream);
+  if (e != hipSuccess) return e;
+  return gdn_scan_launch_t<KD, TL, TO>(w.f, v, gcum, l, o, ht, w.hs, B, T, H, V, L, nlev,
+                                       ht != nullptr ? 1 : 0, stream);
+}
+
 }  // namespace hattn
+
+size_t hattn_gdn_fwd_keep_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
+  return hattn::gdn_keep_ws_layout(nullptr, B, T, H, K, V, nlev).bytes;
+}
+
+void hattn_gdn_fwd_keep_buffers(const void* ws, int B, int T, int H, int K, int V, int nlev,
+                                const __bf16** qn, const __bf16** wn, const __bf16** kn,
+                                const __bf16** un, const __bf16** hs) {
+  const hattn::GdnKeepWs w = hattn::gdn_keep_ws_layout(const_cast<void*>(ws), B, T, H, K, V, nlev);
+  *qn = w.f.qn;
+  *wn = w.f.wn;
+  *kn = w.kn;
+  *un = w.f.un;
+  *hs = w.hs;
+}
+
+// The forward plus, in the workspace, the backward's recompute results
+// (q_new, W_new, K_new, U, every level's state at every chunk start).
+hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v,
+                                     const void* beta, const float* g, const void* l, void* o,
+                                     float* gcum, void* aw, void* au, float* ht, void* ws, int B,
+                                     int T, int H, int K, int V, int L, int nlev, int dt_b,
+                                     int dt_l, int dt_o, int norm_qk, float scale,
+                                     hipStream_t stream, int* unsupported) {
+  using namespace hattn;
+  *unsupported = 0;
+#define HATTN_GDN_KDT(KD_, TB_, TL_)                                                            \
+  return gdn_launch_keep_t<KD_, TB_, TL_, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, \
+                                                  T, H, V, L, nlev, norm_qk, scale, stream);
+#define HATTN_GDN_K(KD_)                                                                        \
+  if (K == KD_ && dt_o == 0) {                                                                  \
+    if (dt_b == 0 && dt_l == 0) HATTN_GDN_KDT(KD_, __bf16, __bf16)                              \
+    if (dt_b == 2 && dt_l == 2) HATTN_GDN_KDT(KD_, float, float)                                \
+    if (dt_b == 0 && dt_l == 2) HATTN_GDN_KDT(KD_, __bf16, float)                               \
+    if (dt_b == 2 && dt_l == 0) HATTN_GDN_KDT(KD_, float, __bf16)                               \
+  }
+  HATTN_GDN_K(64)
+  HATTN_GDN_K(128)
+  HATTN_GDN_K(192)
+  HATTN_GDN_K(256)
+#undef HATTN_GDN_K
+#undef HATTN_GDN_KDT
+  *unsupported = 1;
+  return hipSuccess;
+}
 
 size_t hattn_gdn_fwd_ws_bytes(int B, int T, int H, int K, int V) {
   return hattn::gdn_ws_layout(nullptr, B, T, H, K, V).bytes;

@@ -50,6 +50,25 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
                                 float scale, hipStream_t stream, int* unsupported);
+size_t hattn_gdn_fwd_keep_ws_bytes(int B, int T, int H, int K, int V, int nlev);
+hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v,
+                                     const void* beta, const float* g, const void* l, void* o,
+                                     float* gcum, void* aw, void* au, float* ht, void* ws, int B,
+                                     int T, int H, int K, int V, int L, int nlev, int dt_b,
+                                     int dt_l, int dt_o, int norm_qk, float scale,
+                                     hipStream_t stream, int* unsupported);
+void hattn_gdn_fwd_keep_buffers(const void* ws, int B, int T, int H, int K, int V, int nlev,
+                                const __bf16** qn, const __bf16** wn, const __bf16** kn,
+                                const __bf16** un, const __bf16** hs);
+size_t hattn_gdn_bwd_kept_ws_bytes(int B, int T, int H, int K, int V, int nlev);
+hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v,
+                                     const void* beta, const float* gcum, const void* l,
+                                     const void* dO, void* dq, void* dk, void* dv, void* db,
+                                     float* dg, float* dl, const __bf16* qn, const __bf16* wn,
+                                     const __bf16* kn, const __bf16* un, const __bf16* hs,
+                                     void* ws, int B, int T, int H, int K, int V, int L, int nlev,
+                                     int dt_b, int dt_l, int norm_qk, float scale,
+                                     hipStream_t stream, int* unsupported);
 size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* gcum, const void* l, const void* dO, void* dq,
@@ -470,13 +489,14 @@ size_t hattn_gdn_chunkwise_fwd_workspace(int B, int T, int H, int K, int V, int 
   return hattn_gdn_fwd_ws_bytes(B, T, H, K, V);
 }
 
-int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const void* beta,
-                            const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
-                            void* Au, float* ht, int B, int T, int H, int K, int V, int L,
-                            int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
-                            int level_base, int htype, int chunk_size, int l2norm_qk,
-                            float qk_scale, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+// keep: also leave, in the workspace, what the backward's recompute would
+// produce (hattn_gdn_chunkwise_fwd_keep)
+static int gdn_fwd_impl(const void* q, const void* k, const void* v, const void* beta,
+                        const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
+                        void* Au, float* ht, int B, int T, int H, int K, int V, int L,
+                        int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o, int level_base,
+                        int htype, int chunk_size, int l2norm_qk, float qk_scale,
+                        void* workspace, size_t workspace_bytes, bool keep, void* stream) {
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
@@ -501,21 +521,59 @@ int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const v
     return fail(HATTN_ERR_VALUE, "T * H * max(K, V) = %zu exceeds 2^31", (size_t)T * H * (K > V ? K : V));
   if (dtype_qkv != HATTN_BF16)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v dtype code %d (bf16 required)", dtype_qkv);
+  if (keep && !(V == 64 || V == 128))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "V=%d: the kept buffers serve a backward in one V block (V in {64, 128})", V);
+  if (keep && nlev > hattn_gdn_bwd_max_levels())
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d (the backward's limit)", T,
+                hattn_gdn_bwd_max_levels());
   if (!q || !k || !v || !beta || !g || !l || !o || !g_cumsum || !Aw || !Au)
     return fail(HATTN_ERR_VALUE, "null tensor pointer");
-  const size_t need = hattn_gdn_fwd_ws_bytes(B, T, H, K, V);
+  const size_t need = keep ? hattn_gdn_fwd_keep_ws_bytes(B, T, H, K, V, nlev)
+                           : hattn_gdn_fwd_ws_bytes(B, T, H, K, V);
   if (workspace_bytes < need || workspace == nullptr)
     return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
   int unsupported = 0;
-  hipError_t e = hattn_gdn_fwd_launch(q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, workspace, B,
-                                      T, H, K, V, L, nlev, dtype_beta, dtype_l, dtype_o,
-                                      l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
-                                      &unsupported);
+  hipError_t e =
+      (keep ? hattn_gdn_fwd_keep_launch : hattn_gdn_fwd_launch)(
+          q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, workspace, B, T, H, K, V, L, nlev,
+          dtype_beta, dtype_l, dtype_o, l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
+          &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d o=%d", dtype_beta,
                 dtype_l, dtype_o);
-  return check_hip(e, "hattn_gdn_chunkwise_fwd launch");
+  return check_hip(e, keep ? "hattn_gdn_chunkwise_fwd_keep launch" : "hattn_gdn_chunkwise_fwd launch");
+}
+
+int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const void* beta,
+                            const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
+                            void* Au, float* ht, int B, int T, int H, int K, int V, int L,
+                            int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
+                            int level_base, int htype, int chunk_size, int l2norm_qk,
+                            float qk_scale, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return gdn_fwd_impl(q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, B, T, H, K, V, L, dtype_qkv,
+                      dtype_beta, dtype_l, dtype_o, level_base, htype, chunk_size, l2norm_qk,
+                      qk_scale, workspace, workspace_bytes, false, stream);
+}
+
+size_t hattn_gdn_chunkwise_fwd_keep_workspace(int B, int T, int H, int K, int V, int L) {
+  (void)L;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+  return hattn_gdn_fwd_keep_ws_bytes(B, T, H, K, V, ceil_log2(T / 64));
+}
+
+int hattn_gdn_chunkwise_fwd_keep(const void* q, const void* k, const void* v, const void* beta,
+                                 const float* g, const void* l, void* o, float* g_cumsum,
+                                 void* Aw, void* Au, float* ht, int B, int T, int H, int K, int V,
+                                 int L, int dtype_qkv, int dtype_beta, int dtype_l, int dtype_o,
+                                 int level_base, int htype, int chunk_size, int l2norm_qk,
+                                 float qk_scale, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return gdn_fwd_impl(q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, B, T, H, K, V, L, dtype_qkv,
+                      dtype_beta, dtype_l, dtype_o, level_base, htype, chunk_size, l2norm_qk,
+                      qk_scale, workspace, workspace_bytes, true, stream);
 }
 
 size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int L) {
@@ -524,15 +582,15 @@ size_t hattn_gdn_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, int 
   return hattn_gdn_bwd_ws_bytes(B, T, H, K, V, ceil_log2(T / 64));
 }
 
-int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,
-                            const float* g_cumsum, const void* l, const void* Aw, const void* Au,
-                            const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
-                            float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
-                            int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
-                            int chunk_size, int l2norm_qk, float qk_scale, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  (void)Aw;
-  (void)Au;
+// fwd_ws != nullptr: q_new, W_new, K_new, U and the level states come from the
+// workspace of hattn_gdn_chunkwise_fwd_keep (hattn_gdn_chunkwise_bwd_fwd_ws)
+static int gdn_bwd_impl(const void* q, const void* k, const void* v, const void* beta,
+                        const float* g_cumsum, const void* l, const void* do_, void* dq, void* dk,
+                        void* dv, void* db, float* dg, float* dl, int B, int T, int H, int K,
+                        int V, int L, int dtype_qkv, int dtype_beta, int dtype_l, int dtype_do,
+                        int level_base, int htype, int chunk_size, int l2norm_qk,
+                        float qk_scale, void* workspace, size_t workspace_bytes,
+                        const void* fwd_ws, size_t fwd_ws_bytes, bool kept, void* stream) {
   // chunkwise_hgdn.py:818-858
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
@@ -560,18 +618,72 @@ int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const v
                 dtype_do);
   if (!q || !k || !v || !beta || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !db || !dg || !dl)
     return fail(HATTN_ERR_VALUE, "null tensor pointer");
-  const size_t need = hattn_gdn_bwd_ws_bytes(B, T, H, K, V, nlev);
+  if (kept) {
+    const size_t fneed = hattn_gdn_fwd_keep_ws_bytes(B, T, H, K, V, nlev);
+    if (fwd_ws == nullptr || fwd_ws_bytes < fneed)
+      return fail(HATTN_ERR_VALUE,
+                  "forward workspace of %zu bytes is smaller than the %zu of the keeping forward",
+                  fwd_ws_bytes, fneed);
+  }
+  const size_t need = kept ? hattn_gdn_bwd_kept_ws_bytes(B, T, H, K, V, nlev)
+                           : hattn_gdn_bwd_ws_bytes(B, T, H, K, V, nlev);
   if (workspace_bytes < need || workspace == nullptr)
     return fail(HATTN_ERR_VALUE, "workspace of %zu bytes is smaller than the %zu required",
                 workspace_bytes, need);
   int unsupported = 0;
-  hipError_t e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl,
-                                      workspace, B, T, H, K, V, L, nlev, dtype_beta, dtype_l,
-                                      l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
-                                      &unsupported);
+  hipError_t e;
+  if (kept) {
+    const __bf16 *qn, *wn, *kn, *un, *hs;
+    hattn_gdn_fwd_keep_buffers(fwd_ws, B, T, H, K, V, nlev, &qn, &wn, &kn, &un, &hs);
+    e = hattn_gdn_bwd_kept_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, qn, wn,
+                                  kn, un, hs, workspace, B, T, H, K, V, L, nlev, dtype_beta,
+                                  dtype_l, l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
+                                  &unsupported);
+  } else {
+    e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, workspace,
+                             B, T, H, K, V, L, nlev, dtype_beta, dtype_l, l2norm_qk ? 1 : 0,
+                             qk_scale, (hipStream_t)stream, &unsupported);
+  }
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);
-  return check_hip(e, "hattn_gdn_chunkwise_bwd launch");
+  return check_hip(e, kept ? "hattn_gdn_chunkwise_bwd_fwd_ws launch" : "hattn_gdn_chunkwise_bwd launch");
+}
+
+int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,
+                            const float* g_cumsum, const void* l, const void* Aw, const void* Au,
+                            const void* do_, void* dq, void* dk, void* dv, void* db, float* dg,
+                            float* dl, int B, int T, int H, int K, int V, int L, int dtype_qkv,
+                            int dtype_beta, int dtype_l, int dtype_do, int level_base, int htype,
+                            int chunk_size, int l2norm_qk, float qk_scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  (void)Aw;
+  (void)Au;
+  return gdn_bwd_impl(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, B, T, H, K, V, L,
+                      dtype_qkv, dtype_beta, dtype_l, dtype_do, level_base, htype, chunk_size,
+                      l2norm_qk, qk_scale, workspace, workspace_bytes, nullptr, 0, false, stream);
+}
+
+size_t hattn_gdn_chunkwise_bwd_fwd_ws_workspace(int B, int T, int H, int K, int V, int L) {
+  (void)L;
+  if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+  return hattn_gdn_bwd_kept_ws_bytes(B, T, H, K, V, ceil_log2(T / 64));
+}
+
+int hattn_gdn_chunkwise_bwd_fwd_ws(const void* q, const void* k, const void* v, const void* beta,
+                                   const float* g_cumsum, const void* l, const void* Aw,
+                                   const void* Au, const void* do_, void* dq, void* dk, void* dv,
+                                   void* db, float* dg, float* dl, int B, int T, int H, int K,
+                                   int V, int L, int dtype_qkv, int dtype_beta, int dtype_l,
+                                   int dtype_do, int level_base, int htype, int chunk_size,
+                                   int l2norm_qk, float qk_scale, void* workspace,
+                                   size_t workspace_bytes, const void* fwd_workspace,
+                                   size_t fwd_workspace_bytes, void* stream) {
+  (void)Aw;
+  (void)Au;
+  return gdn_bwd_impl(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, B, T, H, K, V, L,
+                      dtype_qkv, dtype_beta, dtype_l, dtype_do, level_base, htype, chunk_size,
+                      l2norm_qk, qk_scale, workspace, workspace_bytes, fwd_workspace,
+                      fwd_workspace_bytes, true, stream);
 }
 
 int hattn_hstate_step(float* states, int* counts, const void* q, const void* k, const void* v,

@@ -44,6 +44,14 @@ SIGNATURES = [
      [_P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4
      + [_I] * 3 + [_I, ctypes.c_float] + [_P, _S, _P]),
     ("hattn_gdn_chunkwise_bwd_workspace", _S, [_I] * 6),
+    ("hattn_gdn_chunkwise_fwd_keep", _I,
+     [_P, _P, _P, _P, _F, _P, _P, _F, _P, _P, _F] + [_I] * 6 + [_I] * 4 + [_I] * 3
+     + [_I, ctypes.c_float] + [_P, _S, _P]),
+    ("hattn_gdn_chunkwise_fwd_keep_workspace", _S, [_I] * 6),
+    ("hattn_gdn_chunkwise_bwd_fwd_ws", _I,
+     [_P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F] + [_I] * 6 + [_I] * 4
+     + [_I] * 3 + [_I, ctypes.c_float] + [_P, _S, _P, _S, _P]),
+    ("hattn_gdn_chunkwise_bwd_fwd_ws_workspace", _S, [_I] * 6),
     ("hattn_hstate_step", _I,
      [_P] * 9 + [_I] * 12 + [ctypes.c_float] + [_I] * 4 + [_P]),
     ("hattn_mamba2_prefill_levels", _I, [_P] * 4 + [_I] * 10 + [_P]),

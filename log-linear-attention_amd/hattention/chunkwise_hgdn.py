@@ -96,6 +96,34 @@ def chunkwise_fwd(
     behaviour): the kernels take raw q, k and use q * scale / ||q|| and
     k / ||k||, what HAttentionFunction computes before the reference's call
     (kernel.py:110-111), without a separate pass over q and k."""
+    return chunkwise_fwd_keep(q, k, v, b, g, l, head_first, level_base, htype, chunk_size,
+                              output_final_state, qk_l2norm_scale=qk_l2norm_scale,
+                              keep=False)[:5]
+
+
+def chunkwise_fwd_keep(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    b: torch.Tensor,
+    g: torch.Tensor,
+    l: torch.Tensor,
+    head_first: bool,
+    level_base: int,
+    htype: HType,
+    chunk_size: int,
+    output_final_state: bool,
+    *,
+    qk_l2norm_scale: Optional[float] = None,
+    keep: bool = True,
+):
+    """:func:`chunkwise_fwd` that also returns the forward's workspace, holding
+    what the backward would recompute (q_new, W_new, K_new, U and every level's
+    state at every chunk start, bit for bit), when the backward can take it
+    (V in {64, 128}; else None): pass it to :func:`chunkwise_bwd` as ``fwd_ws``
+    with the same inputs, and the backward skips its recompute
+    (HAttentionFunction keeps it between its forward and backward).  Returns
+    (g_cumsum, o, Aw, Au, ht, fwd_ws)."""
     B, T, G, H, K, V, L = _validate(q, k, v, l, head_first, level_base, htype, chunk_size,
                                     b=b, g=g)
     if g.dtype != torch.float32:
@@ -112,9 +140,11 @@ def chunkwise_fwd(
     Au = torch.empty(B, T, H, CHUNK, dtype=k.dtype, device=dev)
     ht = torch.zeros(B, H, K, V, L, dtype=torch.float32, device=dev) if output_final_state else None
     lib = _lib.load()
+    keep = keep and V in (64, VB)
     ws, ws_ptr, ws_bytes = _lib.workspace(
-        lib.hattn_gdn_chunkwise_fwd_workspace(B, T, H, K, V, L), dev)
-    st = lib.hattn_gdn_chunkwise_fwd(
+        (lib.hattn_gdn_chunkwise_fwd_keep_workspace if keep
+         else lib.hattn_gdn_chunkwise_fwd_workspace)(B, T, H, K, V, L), dev)
+    st = (lib.hattn_gdn_chunkwise_fwd_keep if keep else lib.hattn_gdn_chunkwise_fwd)(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
         _lib.ptr(o), _lib.ptr(g_cumsum), _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(ht),
         B, T, H, K, V, L, _lib.dtype_code(q), _lib.dtype_code(b), _lib.dtype_code(l),
@@ -125,7 +155,7 @@ def chunkwise_fwd(
     _lib.check(st)
     if o_dtype != o.dtype:
         o, Aw, Au = o.to(o_dtype), Aw.to(k_dtype), Au.to(k_dtype)
-    return g_cumsum, o, Aw, Au, ht
+    return g_cumsum, o, Aw, Au, ht, (ws if keep else None)
 
 
 def chunkwise_bwd(
@@ -144,8 +174,14 @@ def chunkwise_bwd(
     chunk_size: int,
     *,
     qk_l2norm_scale: Optional[float] = None,
+    fwd_ws: Optional[torch.Tensor] = None,
 ):
     """Log-linear GDN backward (chunkwise_hgdn.py:791-1222).
+
+    ``fwd_ws`` (not in the reference): the workspace :func:`chunkwise_fwd_keep`
+    returned for the same inputs; the backward then takes q_new, W_new, K_new,
+    U and the level states from it instead of recomputing them (the same
+    gradients, bit for bit).
 
     With ``qk_l2norm_scale`` (as in :func:`chunkwise_fwd`) q and k are the raw
     inputs and dq, dk come back w.r.t. them: the kernels apply the l2norm
@@ -187,16 +223,22 @@ def chunkwise_bwd(
         db_b = torch.empty_like(b)
         dg_b = torch.empty(B, T, H, dtype=torch.float32, device=dev)
         dl_b = torch.empty(B, T, H, L, dtype=torch.float32, device=dev)
+        kept = fwd_ws is not None and len(blocks) == 1
         ws, ws_ptr, ws_bytes = _lib.workspace(
-            lib.hattn_gdn_chunkwise_bwd_workspace(B, T, H, K, Vb, L), dev)
-        st = lib.hattn_gdn_chunkwise_bwd(
+            (lib.hattn_gdn_chunkwise_bwd_fwd_ws_workspace if kept
+             else lib.hattn_gdn_chunkwise_bwd_workspace)(B, T, H, K, Vb, L), dev)
+        args = (
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(vb), _lib.ptr(b), _lib.ptr(g), _lib.ptr(l),
             _lib.ptr(Aw), _lib.ptr(Au), _lib.ptr(dob), _lib.ptr(dq_b), _lib.ptr(dk_b),
             _lib.ptr(dv_b), _lib.ptr(db_b), _lib.ptr(dg_b), _lib.ptr(dl_b), B, T, H, K, Vb, L,
             _lib.dtype_code(q), _lib.dtype_code(b), _lib.dtype_code(l), _lib.dtype_code(dob),
             level_base, htype.value, chunk_size, 1 if qk_l2norm_scale is not None else 0,
-            float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes,
-            _lib.stream_handle(dev))
+            float(qk_l2norm_scale) if qk_l2norm_scale is not None else 1.0, ws_ptr, ws_bytes)
+        if kept:
+            st = lib.hattn_gdn_chunkwise_bwd_fwd_ws(*args, _lib.ptr(fwd_ws), fwd_ws.numel(),
+                                                    _lib.stream_handle(dev))
+        else:
+            st = lib.hattn_gdn_chunkwise_bwd(*args, _lib.stream_handle(dev))
         _lib.check(st)
         del ws
         if len(blocks) == 1:

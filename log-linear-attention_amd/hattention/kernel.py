@@ -78,8 +78,9 @@ class HAttentionFunction(torch.autograd.Function):
             if scale is None:
                 raise NotImplementedError
             from hattention import chunkwise_hgdn as _hg
-            # q * scale / ||q|| and k / ||k|| are formed inside the kernels
-            g, o, Aw, Au, _ = _hg.chunkwise_fwd(
+            # q * scale / ||q|| and k / ||k|| are formed inside the kernels; the
+            # forward's workspace (what the backward would recompute) is kept
+            g, o, Aw, Au, _, ctx.fwd_ws = _hg.chunkwise_fwd_keep(
                 q=q, k=k, v=v, b=b, g=g, l=l, head_first=head_first, level_base=level_base,
                 htype=htype, chunk_size=chunk_sizes[0], output_final_state=False,
                 qk_l2norm_scale=scale)
@@ -126,7 +127,7 @@ class HAttentionFunction(torch.autograd.Function):
             dq, dk, dv, db, dg, dl = _hg.chunkwise_bwd(
                 q=q, k=k, v=v, b=b, g=g, l=l, Aw=Aw, Au=Au, do=do, head_first=ctx.head_first,
                 level_base=ctx.level_base, htype=ctx.htype, chunk_size=ctx.chunk_sizes[0],
-                qk_l2norm_scale=ctx.scale)
+                qk_l2norm_scale=ctx.scale, fwd_ws=ctx.fwd_ws)
         else:
             raise NotImplementedError
         return (dq.to(q), dk.to(k), dv.to(v), db.to(b) if b is not None else None,

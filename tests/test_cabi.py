@@ -230,6 +230,53 @@ def test_gdn_bwd_workspace_query():
     assert 0 < small < big
 
 
+def test_gdn_keep_workspace_queries():
+    lib = _lib.load()
+    args = (2, 2048, 4, 128, 128, 12)
+    fwd = lib.hattn_gdn_chunkwise_fwd_workspace(*args)
+    keep = lib.hattn_gdn_chunkwise_fwd_keep_workspace(*args)
+    bwd = lib.hattn_gdn_chunkwise_bwd_workspace(*args)
+    kept = lib.hattn_gdn_chunkwise_bwd_fwd_ws_workspace(*args)
+    # the keeping forward holds at least every level's state per chunk (bf16)
+    B, T, H, K, V, L = args
+    assert keep >= fwd + B * H * (T // 64) * 5 * V * K * 2
+    assert 0 < kept < bwd
+    assert lib.hattn_gdn_chunkwise_fwd_keep_workspace(1, 100, 1, 64, 64, 8) == 0
+    assert lib.hattn_gdn_chunkwise_bwd_fwd_ws_workspace(1, 100, 1, 64, 64, 8) == 0
+
+
+def test_gdn_keep_forward_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(None)
+
+    def call(V, ws=1 << 30):
+        return lib.hattn_gdn_chunkwise_fwd_keep(p, p, p, p, p, p, p, p, p, p, p, 1, 256, 2, 64,
+                                                V, 9, 0, 0, 0, 0, 2, 0, 64, 0, 1.0, p, ws, None)
+    # the kept buffers serve a backward in one V block
+    assert call(192) == _lib.HATTN_ERR_NOT_IMPLEMENTED
+    assert "V=192" in lib.hattn_last_error().decode()
+    assert call(128) == _lib.HATTN_ERR_VALUE   # valid shape: fails on the null pointers
+
+
+def test_gdn_kept_backward_argument_checks():
+    """Placeholder (never dereferenced) tensor pointers: the forward-workspace
+    checks come after the tensor checks and before any HIP call."""
+    lib = _lib.load()
+    x = ctypes.c_void_p(0x1000)
+    B, T, H, K, V, L = 1, 256, 2, 64, 64, 9
+    big = 1 << 40
+
+    def call(fwd, fwd_bytes, V=V):
+        return lib.hattn_gdn_chunkwise_bwd_fwd_ws(
+            x, x, x, x, x, x, None, None, x, x, x, x, x, x, x, B, T, H, K, V, L, 0, 0, 0, 0, 2,
+            0, 64, 0, 1.0, x, big, fwd, fwd_bytes, None)
+    assert call(None, big) == _lib.HATTN_ERR_VALUE
+    assert "forward workspace" in lib.hattn_last_error().decode()
+    need = lib.hattn_gdn_chunkwise_fwd_keep_workspace(B, T, H, K, V, L)
+    assert call(x, need - 1) == _lib.HATTN_ERR_VALUE
+    assert call(x, big, V=192) == _lib.HATTN_ERR_NOT_IMPLEMENTED
+
+
 def _fwd_noalloc(ptr=None, **kw):
     """hattn_mamba2_chunkwise_fwd_noalloc with NULL tensor pointers (or
     placeholders when ptr is given): the cases below fail in the host-side

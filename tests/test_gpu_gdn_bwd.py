@@ -170,3 +170,52 @@ def test_head_dim_256_bwd(T, V):
     64-column block at a time; V = 256 runs as two 128-column blocks."""
     L = 7 + math.ceil(math.log2(T // 64)) + 1
     _run(1, T, 2, 256, V, L, seed=T + V + 256)
+
+
+# ---------------------------------------------------------------------------
+# the forward that keeps what the backward recomputes
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,T,H,K,V,norm,fp32", [
+    (1, 1024, 2, 64, 64, False, False),
+    (2, 640, 2, 128, 128, True, False),
+    (1, 1024, 2, 192, 128, True, True),
+    (1, 640, 2, 256, 64, True, False),
+    (4, 8192, 16, 128, 128, True, False),   # BASELINE config 3
+])
+def test_kept_forward_buffers_give_the_same_gradients(B, T, H, K, V, norm, fp32):
+    """chunkwise_fwd_keep + chunkwise_bwd(fwd_ws=...) against chunkwise_fwd +
+    chunkwise_bwd (the recompute): the kept q_new, W_new, K_new, U and level
+    states are the recompute's values, so every output and gradient is equal
+    bit for bit; the forward's own outputs are unchanged by keeping."""
+    from hattention.chunkwise_hgdn import chunkwise_fwd, chunkwise_fwd_keep, chunkwise_bwd
+    from hattention.base import HType
+    L = 7 + math.ceil(math.log2(T // 64))
+    q, k, v, beta, g, l = make_gdn_inputs(B, T, H, K, V, L, seed=T + K)
+    if fp32:
+        beta, l = beta.float(), l.float()
+    dev = torch.device("cuda:0")
+    xs = [x.to(dev) for x in (q, k, v, beta, g, l)]
+    do = torch.randn(B, T, H, V, generator=torch.Generator().manual_seed(5)).bfloat16().to(dev)
+    sc = 0.125 if norm else None
+    print(f"[gdn keep] B={B} T={T} H={H} K={K} V={V} norm={norm} fp32={fp32}", flush=True)
+    ref_fwd = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, False, qk_l2norm_scale=sc)
+    ref = chunkwise_bwd(xs[0], xs[1], xs[2], xs[3], ref_fwd[0], xs[5], ref_fwd[2], ref_fwd[3],
+                        do, False, 2, HType.WEAK, 64, qk_l2norm_scale=sc)
+    kept = chunkwise_fwd_keep(*xs, False, 2, HType.WEAK, 64, False, qk_l2norm_scale=sc)
+    assert kept[5] is not None
+    got = chunkwise_bwd(xs[0], xs[1], xs[2], xs[3], kept[0], xs[5], kept[2], kept[3], do, False,
+                        2, HType.WEAK, 64, qk_l2norm_scale=sc, fwd_ws=kept[5])
+    torch.cuda.synchronize()
+    for i in range(4):
+        assert torch.equal(kept[i], ref_fwd[i]), ("fwd", i)
+    for name, a, r in zip(NAMES, got, ref):
+        assert torch.equal(a, r), (name, (a.float() - r.float()).abs().max().item())
+
+
+def test_kept_forward_not_offered_for_wide_v():
+    # V = 192 runs the backward in V blocks with their own recompute: no keep
+    from hattention.chunkwise_hgdn import chunkwise_fwd_keep
+    from hattention.base import HType
+    B, T, H, K, V, L = 1, 256, 2, 64, 192, 9
+    xs = [x.to("cuda:0") for x in make_gdn_inputs(B, T, H, K, V, L, seed=1)]
+    assert chunkwise_fwd_keep(*xs, False, 2, HType.WEAK, 64, False)[5] is None

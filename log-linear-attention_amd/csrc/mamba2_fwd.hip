@@ -505,6 +505,10 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
 constexpr int kLamCols = 25;
 static_assert(kMaxLU + 1 < kLamCols, "lambda pieces cover every level");
 
+// LT: element type of the staged lambda values: fp32, or for bf16 lambda
+// inputs bf16 (exact; half the LDS of the double-buffered staging), used where
+// that lets two workgroups share a CU (five top levels, T >= 32768).
+template <typename LT>
 struct Bf16Smem {
   __bf16 q[kBT * 64];         // Q[t][k]
   __bf16 k[kBT * 64];         // K[s][k]
@@ -519,14 +523,25 @@ struct Bf16Smem {
   // shifts them by one), to rows 0 .. kLamCols - 1: a value's row is a
   // compile-time offset from a per-lane base, and the rows outside 1 .. lu hold
   // values nobody reads (the neighbouring head's lambda or zeros)
-  float lam[2][kLamCols * kBT];
+  LT lam[2][kLamCols * kBT];
   float eg[2][kBT];
   float lpar[32];             // layer mode: L[h, 0 .. L - 1] (lambda parameters of the head)
   __bf16 top[1];              // [ntop][v][64] top-level states, transposed, swizzled
 };
 
+template <typename LT>
 inline int bf16_smem_bytes(int ntop) {
-  return (int)offsetof(Bf16Smem, top) + ntop * kKD * 64 * 2;
+  return (int)offsetof(Bf16Smem<LT>, top) + ntop * kKD * 64 * 2;
+}
+
+// LDS of one CU (two workgroups of the bf16 kernel per CU need at most half each)
+constexpr int kLdsPerCu = 160 * 1024;
+
+// four consecutive staged lambda values as fp32
+__device__ __forceinline__ floatx4 lam4(const float* p) { return *(const floatx4*)p; }
+__device__ __forceinline__ floatx4 lam4(const __bf16* p) {
+  const bf16x4 x = *(const bf16x4*)p;
+  return floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
 }
 
 // Top-level state element (v, k) in a 64 x 64 bf16 tile without padding: the
@@ -636,8 +651,8 @@ template <> struct P1T<3> { static constexpr int mt[3] = {2, 3, 2}, jt[3] = {1, 
 //   A tile (mt, jt): S^T[s = 16jt + 4lq + i][t = 16mt + ln] o exp(Gc_t - Gc_s)
 //                    o lambda[t, level(t, s)] (causal) -> bf16 A[t][s] in LDS.
 //   kv[2c + h]: D rows k = 32c + 8lq + 4h + i, column v = 16w + ln.
-template <int W>
-__device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const float* li,
+template <int W, typename LT>
+__device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, const LT* li,
                                         const bf16x8 (&qa)[4][2], const bf16x8& vt0,
                                         const bf16x8& vt1, floatx4 (&kv)[4], int lq, int ln) {
   using S = P1T<W>;
@@ -657,10 +672,10 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem& sm, const LdsBase& lb, const f
     gs[n] = *(const floatx4*)(sm.gc + 16 * jt + 4 * lq);
     if (jt < mt) {
       const int lev = 4 + (32 - __builtin_clz(mt ^ jt));
-      lam[n][0] = li[lev * kBT + 4 * ln + mt];
+      lam[n][0] = (float)li[lev * kBT + 4 * ln + mt];
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lam[n][i] = li[intra_level(ln, 4 * lq + i) * kBT + 4 * ln + mt];
+      for (int i = 0; i < 4; ++i) lam[n][i] = (float)li[intra_level(ln, 4 * lq + i) * kBT + 4 * ln + mt];
     }
   }
   bf16x8 kt[2][2];   // [h][s-half], first for k-half c = 0
@@ -781,7 +796,7 @@ __global__ void mamba2_fwd_sync_init_kernel(unsigned int* __restrict__ sync, int
 // (v = x dt' as it is staged), l is dl (lambda = compute_lambda(L[h], dl) as it
 // is staged), g comes from dt (g = A dt'), and the output is bf16(o) + x D[h]
 // (see layer_math.h); bf16 x only.
-template <typename TV, typename TL, typename TO, bool FUSED, bool LAYER = false>
+template <typename TV, typename TL, typename TO, bool FUSED, bool LAYER = false, bool LAM16 = false>
 __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
@@ -793,7 +808,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   constexpr int kPl = kKD * 64;                           // one top-level state tile
   constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-  Bf16Smem& sm = *(Bf16Smem*)smem_raw;
+  static_assert(!LAM16 || (sizeof(TL) == 2 && !LAYER), "bf16 staging of bf16 lambda inputs");
+  using LT = typename std::conditional<LAM16, __bf16, float>::type;
+  Bf16Smem<LT>& sm = *(Bf16Smem<LT>*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq0 = lane >> 4, ln0 = lane & 15;
   int h, p, b, vblk;
@@ -1006,16 +1023,20 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     } else {
       // every value of the lane's pieces is stored, at a compile-time offset
       // from one per-lane base (no compares, no divergent branches)
-      float* lamw = sm.lam[par] + lam_lane;
+      LT* lamw = sm.lam[par] + lam_lane;
 #pragma unroll
       for (int r = 0; r < kLP; ++r) {
         const unsigned int* u = (const unsigned int*)&lamr[r];
 #pragma unroll
         for (int i = 0; i < kPE; ++i) {
-          float val;
-          if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
-          else val = __builtin_bit_cast(float, u[i]);
-          lamw[(3 * kPE * r + i) * kBT] = val;
+          if constexpr (sizeof(LT) == 2) {
+            lamw[(3 * kPE * r + i) * kBT] = __builtin_bit_cast(bf16x8, lamr[r])[i];
+          } else {
+            float val;
+            if constexpr (kL16) val = __builtin_bit_cast(float, (i & 1) ? (u[i >> 1] & 0xffff0000u) : (u[i >> 1] << 16));
+            else val = __builtin_bit_cast(float, u[i]);
+            lamw[(3 * kPE * r + i) * kBT] = val;
+          }
         }
       }
     }
@@ -1265,7 +1286,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     store(min(j + 1, nch - 1), (j + 1) & 1);
     const int jn = min(j + 2, nch - 1);
     load(jn, 0);
-    const float* lpr = sm.lam[j & 1] + 8 * kBT;   // level 7 (row 8)
+    const LT* lpr = sm.lam[j & 1] + 8 * kBT;   // level 7 (row 8)
     const floatx4 egr = *(const floatx4*)(sm.eg[j & 1] + 4 * ln);   // exp(Gc_t), t = 16nt + ln
 
     // ---- phase 2: o^T[v = 16w + 4lq + i][t = 16nt + ln] ------------------------------
@@ -1287,7 +1308,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
 #pragma unroll
     for (int e = 0; e < kMaxLoc; ++e) {
       if (e < nloc && ((ic >> e) & 1)) {
-        const floatx4 lam = *(const floatx4*)(lpr + e * kBT + 4 * ln);
+        const floatx4 lam = lam4(lpr + e * kBT + 4 * ln);
         const bf16x8 h0 = cat8(st[e][0], st[e][1]);
         const bf16x8 h1 = cat8(st[e][2], st[e][3]);
         floatx4 tmp[4];
@@ -1317,7 +1338,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       const int u0 = ((lq ^ vrow) & 7) << 3, u1 = (((4 + lq) ^ vrow) & 7) << 3;
       bf16x8 h0 = *(const bf16x8*)(tb + e2 * kPl + u0);
       bf16x8 h1 = *(const bf16x8*)(tb + e2 * kPl + u1);
-      floatx4 lam = *(const floatx4*)(lpr + (nloc + e2) * kBT + 4 * ln);
+      floatx4 lam = lam4(lpr + (nloc + e2) * kBT + 4 * ln);
       while (true) {
         m &= m - 1;
         bf16x8 n0 = h0, n1 = h1;
@@ -1326,7 +1347,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
           const int e2n = __builtin_ctz(m);
           n0 = *(const bf16x8*)(tb + e2n * kPl + u0);
           n1 = *(const bf16x8*)(tb + e2n * kPl + u1);
-          nl = *(const floatx4*)(lpr + (nloc + e2n) * kBT + 4 * ln);
+          nl = lam4(lpr + (nloc + e2n) * kBT + 4 * ln);
         }
         floatx4 tmp[4];
 #pragma unroll
@@ -1567,13 +1588,18 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
   if constexpr (NP == 1) {
     // bf16: one fused single-pass launch (plus the flag reset) when there is
     // more than one segment, else the plain walk
-    const int smem = bf16_smem_bytes(ntop);
+    // bf16 lambda staged as bf16 where only that fits two workgroups per CU
+    const bool lam16 = sizeof(TL) == 2 && 2 * bf16_smem_bytes<float>(ntop) > kLdsPerCu &&
+                       2 * bf16_smem_bytes<__bf16>(ntop) <= kLdsPerCu;
+    const int smem = lam16 ? bf16_smem_bytes<__bf16>(ntop) : bf16_smem_bytes<float>(ntop);
     hipError_t e;
     if (NSEG > 1) {
       hipLaunchKernelGGL(mamba2_fwd_sync_init_kernel, dim3((w.nsync + 255) / 256), dim3(256), 0,
                          stream, w.sync, w.nsync);
       if ((e = hipGetLastError()) != hipSuccess) return e;
       auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true>;
+      if constexpr (sizeof(TL) == 2)
+        if (lam16) kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true, false, true>;
       e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
@@ -1632,7 +1658,7 @@ static hipError_t layer_launch_t(const void* q, const void* k, const void* x, co
   const int nvb64 = V / 64;
   const FwdWs w = fwd_ws_layout(ws, B, T, H, V, 0);
   const int ntop = nlev - min(slog, nlev);
-  const int smem = bf16_smem_bytes(ntop);
+  const int smem = bf16_smem_bytes<float>(ntop);
   hipError_t e;
   if (NSEG > 1) {
     hipLaunchKernelGGL(mamba2_fwd_sync_init_kernel, dim3((w.nsync + 255) / 256), dim3(256), 0,

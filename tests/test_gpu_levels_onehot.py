@@ -19,7 +19,7 @@ References:
   matrices of oracle.levels (the reference's weak / strong recursions,
   base.py:41-62), and ``oracle.mamba2.materialized_fwd`` (the explicit H
   matrix of base.py:75-98) on one level per run as a cross-check;
-* for the inter-chunk levels at T = 16384 (where the T x T matrix does not
+* for the inter-chunk levels at T = 16384 and 32768 (where the T x T matrix does not
   fit), the Fenwick block form: chunk n reads level 7 + e iff bit e of n is
   set, and then holds the chunks m < n that agree with n above bit e, i.e.
   the 2^e chunks starting at (n >> (e + 1)) << (e + 1).  This form is pinned
@@ -175,11 +175,14 @@ def test_weak_every_level_t4096(qdtype):
 
 
 @pytest.mark.gpu
-def test_weak_top_levels_north_star_length():
+@pytest.mark.parametrize("T", [16384, 32768])
+def test_weak_top_levels_north_star_length(T):
     # T = 16384 (the north star's length): 16 segments, local levels 7..10,
-    # top levels 11..14 built by the look-back from the segment summaries
-    T, H, K, V = 16384, 2, 64, 64
-    nlev = 8
+    # top levels 11..14 built by the look-back from the segment summaries;
+    # T = 32768: 32 segments, five top levels (the kernel then stages bf16
+    # lambda as bf16, so that two workgroups share a CU)
+    H, K, V = 2, 64, 64
+    nlev = int(math.log2(T // 64))
     L = 7 + nlev
     q, k, v = _inputs(T, H, K, V, seed=13)
     assert _max_state(k, v, T) < 256

@@ -637,12 +637,15 @@ __device__ __forceinline__ bf16x8 vtr_frag(const __bf16* X, const LdsBase& b, in
 
 // Phase-1 schedule: the 10 causal tiles plus the two zero tiles the 32-wide s
 // steps of A V read above the diagonal ((0,1), (2,3)), three per wave; tile n
-// of wave W is (P1T<W>::mt[n], P1T<W>::jt[n]).
+// of wave W is (P1T<W>::mt[n], P1T<W>::jt[n]).  A diagonal tile (a lambda
+// column per element) costs about twice an off-diagonal one (one lambda per
+// row), so every wave takes one diagonal tile: waves 0, 1 two off-diagonal
+// tiles, waves 2, 3 one (and a zero tile, skipped).
 template <int W> struct P1T;
-template <> struct P1T<0> { static constexpr int mt[3] = {0, 2, 3}, jt[3] = {0, 2, 2}; };
-template <> struct P1T<1> { static constexpr int mt[3] = {1, 3, 0}, jt[3] = {1, 0, 1}; };
-template <> struct P1T<2> { static constexpr int mt[3] = {1, 2, 3}, jt[3] = {0, 0, 3}; };
-template <> struct P1T<3> { static constexpr int mt[3] = {2, 3, 2}, jt[3] = {1, 1, 3}; };
+template <> struct P1T<0> { static constexpr int mt[3] = {0, 1, 2}, jt[3] = {0, 0, 0}; };
+template <> struct P1T<1> { static constexpr int mt[3] = {1, 2, 3}, jt[3] = {1, 1, 0}; };
+template <> struct P1T<2> { static constexpr int mt[3] = {2, 3, 0}, jt[3] = {2, 1, 1}; };
+template <> struct P1T<3> { static constexpr int mt[3] = {3, 3, 2}, jt[3] = {3, 2, 3}; };
 
 // Phase 1 of one wave plus the chunk's K^T diag(w) V for its V columns (which
 // needs no level state, so it is computed here, where its LDS reads and MFMAs

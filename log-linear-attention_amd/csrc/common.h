@@ -256,6 +256,20 @@ __device__ __forceinline__ float sum_lq(float x) {
   return x;
 }
 
+// Four sum_lq at once, transposed: lane (lq, ln) holds x[m] for m = 0..3 and
+// receives sum_lq of x[lq], i.e. the sum over the four 16-lane rows of x[lq],
+// in sum_lq's order ((row 0 + row 1) + (row 2 + row 3), each pair added in
+// either order).  Three lane exchanges instead of eight.
+__device__ __forceinline__ float sum_lq_t(const float (&x)[4], int lq) {
+  const bool odd = lq & 1;
+  // rows lq and lq ^ 1: keep m = lq & 1 and 2 + (lq & 1), send the other two
+  const float a0 = (odd ? x[1] : x[0]) + __shfl_xor(odd ? x[0] : x[1], 16, 64);
+  const float a1 = (odd ? x[3] : x[2]) + __shfl_xor(odd ? x[2] : x[3], 16, 64);
+  // rows lq and lq ^ 2: keep m = lq, send the other
+  const bool hi = lq & 2;
+  return (hi ? a1 : a0) + __shfl_xor(hi ? a0 : a1, 32, 64);
+}
+
 }  // namespace hattn
 
 namespace hattn {

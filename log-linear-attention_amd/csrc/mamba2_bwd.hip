@@ -646,22 +646,36 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int c = 0; c < 2; ++c) row_pairs<NP>(s.d, 16 * mt + ln, 32 * c, da[mt][c]);
+      // Y^T[k][t] = sum_v h[k][v] dO[t][v] for two t-tiles at a time (their LDS
+      // reads, then their MFMAs, then the dq and q . Y terms), then one
+      // transposed cross-row sum of the four tiles' q . Y: lane (lq, ln) stores
+      // the dlambda partial of token 16 lq + ln
       auto level = [&](const bf16x8* a0, const bf16x8* a1, int e, int col, float scale) {
+        float r[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          floatx4 y = mma<NP>(a0, da[mt][0], zero4());
-          y = mma<NP>(a1, da[mt][1], y);     // Y^T[k][t] = sum_v h[k][v] dO[t][v]
-          const int t = 16 * mt + ln;
-          const float sg = s.lam[col * kBT + t] * scale;
-          float r = 0.f;
+        for (int hf = 0; hf < 2; ++hf) {
+          float sg[2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dqT[mt][i] += y[i] * sg;
-            r += qk[mt][i] * y[i];
+          for (int u = 0; u < 2; ++u) sg[u] = s.lam[col * kBT + 16 * (2 * hf + u) + ln] * scale;
+          floatx4 y[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            y[u] = mma<NP>(a0, da[2 * hf + u][0], zero4());
+            y[u] = mma<NP>(a1, da[2 * hf + u][1], y[u]);
           }
-          r = sum_lq(r);
-          if (lq == 0) sm.dl_int[t][e][w] = r * scale;   // dlambda / exp(Gc_t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int mt = 2 * hf + u;
+            float rr = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              dqT[mt][i] += y[u][i] * sg[u];
+              rr += qk[mt][i] * y[u][i];
+            }
+            r[mt] = rr;
+          }
         }
+        sm.dl_int[16 * lq + ln][e][w] = sum_lq_t(r, lq) * scale;   // dlambda / exp(Gc_t)
       };
       if (nloc > 0) {
         // only the levels the chunk reads (bit e of the chunk index, uniform) are
@@ -674,9 +688,8 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
               cat8s<NP>(hT[e][0], hT[e][1], h0);
               cat8s<NP>(hT[e][2], hT[e][3], h1);
               level(h0, h1, e, 7 + e, 1.f);
-            } else if (lq == 0) {
-#pragma unroll
-              for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][e][w] = 0.f;
+            } else {
+              sm.dl_int[16 * lq + ln][e][w] = 0.f;
             }
           }
         }
@@ -712,11 +725,8 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           }
         }
       }
-      if (lq == 0)
-        for (int e2 = 0; e2 < ntop; ++e2)
-          if (!((p >> e2) & 1))
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) sm.dl_int[16 * mt + ln][nloc + e2][w] = 0.f;
+      for (int e2 = 0; e2 < ntop; ++e2)
+        if (!((p >> e2) & 1)) sm.dl_int[16 * lq + ln][nloc + e2][w] = 0.f;
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -995,32 +1005,46 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
       bf16x8 a0[NP], a1[NP];
       cat8s<NP>(dsum[0], dsum[1], a0);
       cat8s<NP>(dsum[2], dsum[3], a1);
+      // two s-tiles at a time: their LDS reads, then their MFMAs, then the FMAs;
+      // k_s . dk_s (inter-chunk part) by one transposed cross-row sum at the end
+      float r[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        bf16x8 rp[NP];
-        row_pairs<NP>(xs, 16 * mt + ln, 0, rp);
-        floatx4 y = mma<NP>(a0, rp, zero4());
-        row_pairs<NP>(xs, 16 * mt + ln, 32, rp);
-        y = mma<NP>(a1, rp, y);
-        const float ws = s.wt[16 * mt + ln];
+      for (int hf = 0; hf < 2; ++hf) {
+        bf16x8 rp[2][2][NP];
+        float ws[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[mt][i] += y[i] * ws;
-        if (role == 0) {
-          // k_s . dk_s, inter-chunk part
-          const int koff = (16 * mt + ln) * kLd + 16 * wr + 4 * lq;
-          const bf16x4 kx = *(const bf16x4*)(s.k[0] + koff);
-          float r = 0.f;
+        for (int u = 0; u < 2; ++u) {
+          row_pairs<NP>(xs, 16 * (2 * hf + u) + ln, 0, rp[u][0]);
+          row_pairs<NP>(xs, 16 * (2 * hf + u) + ln, 32, rp[u][1]);
+          ws[u] = s.wt[16 * (2 * hf + u) + ln];
+        }
+        floatx4 y[2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) r += (float)kx[i] * y[i];
-          if constexpr (NP == 2) {
-            const bf16x4 kl = *(const bf16x4*)(s.k[1] + koff);
+        for (int u = 0; u < 2; ++u) {
+          y[u] = mma<NP>(a0, rp[u][0], zero4());
+          y[u] = mma<NP>(a1, rp[u][1], y[u]);
+        }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r += (float)kl[i] * y[i];
+        for (int u = 0; u < 2; ++u) {
+          const int mt = 2 * hf + u;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[mt][i] += y[u][i] * ws[u];
+          if (role == 0) {
+            const int koff = (16 * mt + ln) * kLd + 16 * wr + 4 * lq;
+            const bf16x4 kx = *(const bf16x4*)(s.k[0] + koff);
+            float rr = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rr += (float)kx[i] * y[u][i];
+            if constexpr (NP == 2) {
+              const bf16x4 kl = *(const bf16x4*)(s.k[1] + koff);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) rr += (float)kl[i] * y[u][i];
+            }
+            r[mt] = rr;
           }
-          r = sum_lq(r) * ws;
-          if (lq == 0) sm.dgk[16 * mt + ln][wr] = r;
         }
       }
+      if (role == 0) sm.dgk[16 * lq + ln][wr] = sum_lq_t(r, lq) * s.wt[16 * lq + ln];
     }
     if (role == 0) {
 #pragma unroll

@@ -204,13 +204,18 @@ struct BwdLoader {
 // Phase-1 tiles (t-tile mt, s-tile jt) of the 64 x 64 intra-chunk matrices:
 // the 10 causal tiles plus the zero tiles (0,1) and (2,3) that the 32-wide
 // contraction steps read.  code = mt * 4 + jt, +16 marks a zero tile, -1 none.
-__device__ __forceinline__ int p1_tile4(int w, int n) {   // 4 waves, 3 each
-  constexpr int tab[4][3] = {{0, 10, 14}, {5, 12, 16 + 1}, {4, 8, 15}, {9, 13, 16 + 11}};
+// 4 waves, 3 each: one diagonal tile per wave, the six sub-diagonal tiles two
+// on each of waves 0, 1 and one on each of 2, 3 (with a zero tile)
+__device__ __forceinline__ int p1_tile4(int w, int n) {
+  constexpr int tab[4][3] = {{0, 4, 8}, {5, 9, 12}, {10, 13, 16 + 1}, {15, 14, 16 + 11}};
   return tab[w][n];
 }
-__device__ __forceinline__ int p1_tile8(int w, int n) {   // 8 waves, 2 each
-  constexpr int tab[8][2] = {{0, 15}, {5, 14}, {10, 13}, {4, 12}, {8, 9}, {16 + 1, -1},
-                             {16 + 11, -1}, {-1, -1}};
+// 8 waves, 2 each: every diagonal tile on a wave of its own, the six
+// sub-diagonal tiles two on each of waves 4, 5 and one on each of 6, 7 (with a
+// zero tile)
+__device__ __forceinline__ int p1_tile8(int w, int n) {
+  constexpr int tab[8][2] = {{0, -1}, {5, -1}, {10, -1}, {15, -1}, {4, 8}, {9, 12},
+                             {13, 16 + 1}, {14, 16 + 11}};
   return tab[w][n];
 }
 
@@ -266,6 +271,32 @@ __device__ __forceinline__ void store_planes4(__bf16 (*X)[kBT * kLd], int off, c
   if constexpr (NP == 2) *(bf16x4*)(X[NP - 1] + off) = lo;
 }
 
+// S^T and dP^T of two tiles (as st_dpt_tile): every LDS read of a 32-wide
+// contraction step is issued before its four MFMAs.
+__device__ __forceinline__ void st_dpt_tiles2(const BwdStage<1>& s, const int (&mt)[2],
+                                              const int (&jt)[2], floatx4 (&S)[2],
+                                              floatx4 (&P)[2]) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    bf16x8 ka[2], qb[2], va[2], db[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int ra = (16 * jt[n] + ln) * kLd + 32 * c + 8 * lq;
+      const int rb = (16 * mt[n] + ln) * kLd + 32 * c + 8 * lq;
+      ka[n] = *(const bf16x8*)(s.k[0] + ra);
+      qb[n] = *(const bf16x8*)(s.q[0] + rb);
+      va[n] = *(const bf16x8*)(s.v[0] + ra);
+      db[n] = *(const bf16x8*)(s.d[0] + rb);
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      S[n] = mfma16x16x32(ka[n], qb[n], c ? S[n] : zero4());
+      P[n] = mfma16x16x32(va[n], db[n], c ? P[n] : zero4());
+    }
+  }
+}
+
 // exp(Gc_t - Gc_s) * [s <= t] and the level of each element of a phase-1 tile.
 struct TileMask {
   float dec[4];
@@ -288,6 +319,27 @@ __device__ __forceinline__ TileMask tile_mask(const BwdStage<NP>& s, int mt, int
       m.lev[i] = intra_level(ln, sl);
       m.dec[i] = sl <= ln ? fexp(gct - gs[i]) : 0.f;
     }
+  }
+  return m;
+}
+
+// tile_mask without branches on the tile (mt, jt are wave-uniform but not
+// compile-time): dec is zero for every element when the tile is not causal
+template <int NP>
+__device__ __forceinline__ TileMask tile_mask_sel(const BwdStage<NP>& s, int mt, int jt,
+                                                  bool causal) {
+  const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
+  TileMask m;
+  const float gct = s.gc[16 * mt + ln];
+  const floatx4 gs = *(const floatx4*)(s.gc + 16 * jt + 4 * lq);
+  const bool off = jt < mt;
+  const int lev_off = 4 + intra_level(mt, jt);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sl = 4 * lq + i;
+    m.lev[i] = off ? lev_off : intra_level(ln, sl);
+    const float d = fexp(gct - gs[i]);
+    m.dec[i] = causal && (off || sl <= ln) ? d : 0.f;
   }
   return m;
 }
@@ -938,6 +990,53 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     __syncthreads();
 
     // ---- phase 1: (M o S) and (M o dP) tiles ---------------------------------------
+    if constexpr (NP == 1) {
+      // the wave's two tiles together (LDS reads, MFMAs, masks, then the eight
+      // independent row sums); a missing second tile computes tile (0, 0) and
+      // stores nothing, a zero tile stores zeros
+      int tmt[2], tjt[2];
+      bool live[2], causal[2];
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        const int code = p1_tile8(w, n);
+        live[n] = code >= 0;
+        causal[n] = code >= 0 && code < 16;
+        const int cc = code >= 0 ? code : 0;
+        tmt[n] = (cc & 15) >> 2;
+        tjt[n] = cc & 3;
+      }
+      floatx4 S[2], P[2];
+      st_dpt_tiles2(s, tmt, tjt, S, P);
+      float os[2][4], op[2][4], c[2][4];
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        const TileMask mk = tile_mask_sel(s, tmt[n], tjt[n], causal[n]);
+        const int t = 16 * tmt[n] + ln;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float m = mk.dec[i] * s.lam[mk.lev[i] * kBT + t];
+          os[n][i] = m * S[n][i];
+          op[n][i] = m * P[n][i];
+          c[n][i] = m * S[n][i] * P[n][i];
+        }
+      }
+      // k_s . dk_s (intra part) = column sum over t of (M o S o dP), in fp32
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c[n][i] = row_sum16(c[n][i]);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        if (causal[n] && ln == 0)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sm.kdk[16 * tjt[n] + 4 * lq + i][tmt[n]] = c[n][i];
+        if (live[n]) {
+          const int off = (16 * tmt[n] + ln) * kLd + 16 * tjt[n] + 4 * lq;
+          store_planes4<NP>(sm.as, off, os[n]);
+          store_planes4<NP>(sm.ap, off, op[n]);
+        }
+      }
+    } else
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const int code = p1_tile8(w, n);

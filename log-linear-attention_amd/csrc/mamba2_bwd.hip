@@ -1161,6 +1161,22 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     if (nloc > 0) {
       Planes ya = role == 0 ? s.d : s.q;   // A: dO^T / Q^T (rows of the state)
       Planes yb = role == 0 ? s.q : s.d;   // B: sigma o Q / sigma o dO
+      // bf16 inputs: the A fragments and the unscaled B fragments are the same for
+      // every level the chunk reads (only the lambda scaling of B differs), so they
+      // are loaded once per chunk, before the level loop, when any level reads
+      constexpr int NA = NP == 1 ? 4 : 1;
+      bf16x8 af[NA][2][NP], yt0[NP], yt1[NP];
+      if constexpr (NP == 1) {
+        if (ic & ((1 << nloc) - 1)) {
+          trfrag<NP>(yb, 0, 16 * wr, yt0);
+          trfrag<NP>(yb, 32, 16 * wr, yt1);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            trfrag<NP>(ya, 0, 16 * m, af[m][0]);
+            trfrag<NP>(ya, 32, 16 * m, af[m][1]);
+          }
+        }
+      }
 #pragma unroll
       for (int e = 0; e < kMaxLoc; ++e) {
         if (e < nloc) {
@@ -1175,20 +1191,32 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             for (int m = 0; m < 4; ++m) dh[e][m] *= gl;
             if (rd) {
               const float* sg = s.lam + (7 + e) * kBT;
-              bf16x8 yt[NP], b0[NP], b1[NP];
-              trfrag<NP>(yb, 0, 16 * wr, yt);
-              scale8s<NP>(yt, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
-                          b0);
-              trfrag<NP>(yb, 32, 16 * wr, yt);
-              scale8s<NP>(yt, *(const floatx4*)(sg + 32 + 8 * lq),
-                          *(const floatx4*)(sg + 36 + 8 * lq), b1);
+              bf16x8 b0[NP], b1[NP];
+              if constexpr (NP == 1) {
+                scale8s<NP>(yt0, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
+                            b0);
+                scale8s<NP>(yt1, *(const floatx4*)(sg + 32 + 8 * lq),
+                            *(const floatx4*)(sg + 36 + 8 * lq), b1);
 #pragma unroll
-              for (int m = 0; m < 4; ++m) {
-                bf16x8 af[NP];
-                trfrag<NP>(ya, 0, 16 * m, af);
-                dh[e][m] = mma<NP>(af, b0, dh[e][m]);
-                trfrag<NP>(ya, 32, 16 * m, af);
-                dh[e][m] = mma<NP>(af, b1, dh[e][m]);
+                for (int m = 0; m < 4; ++m) {
+                  dh[e][m] = mma<NP>(af[m][0], b0, dh[e][m]);
+                  dh[e][m] = mma<NP>(af[m][1], b1, dh[e][m]);
+                }
+              } else {
+                bf16x8 yt[NP];
+                trfrag<NP>(yb, 0, 16 * wr, yt);
+                scale8s<NP>(yt, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
+                            b0);
+                trfrag<NP>(yb, 32, 16 * wr, yt);
+                scale8s<NP>(yt, *(const floatx4*)(sg + 32 + 8 * lq),
+                            *(const floatx4*)(sg + 36 + 8 * lq), b1);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                  trfrag<NP>(ya, 0, 16 * m, af[0][0]);
+                  dh[e][m] = mma<NP>(af[0][0], b0, dh[e][m]);
+                  trfrag<NP>(ya, 32, 16 * m, af[0][1]);
+                  dh[e][m] = mma<NP>(af[0][1], b1, dh[e][m]);
+                }
               }
             }
           }

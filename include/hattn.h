@@ -78,9 +78,12 @@ const char* hattn_last_error(void);
  *   dtype_l / dtype_o in {BF16, FP32}                -> HATTN_ERR_NOT_IMPLEMENTED
  * htype HATTN_HTYPE_STRONG (the reference's USE_A2 / USE_H2 forward,
  * chunkwise.py:1118-1275 with the strong level function, base.py:49-62): BF16
- * q, k, v, L <= 32, T <= 64 * 2^9 and ht NULL (the reference keeps one of
- * four phase states per level, chunkwise.py:275-279, which is no HState; the
- * decode step builds strong states itself); else HATTN_ERR_NOT_IMPLEMENTED.
+ * q, k, v, L <= 32, T <= 64 * 2^9; else HATTN_ERR_NOT_IMPLEMENTED.  Its ht
+ * holds what the reference stores for the strong hierarchy: at level 7 + ell,
+ * ell = 1 .. ceil(log2(T / 64)) - 1, the raw phase-0 state of the strong state
+ * loop after the last chunk (chunkwise.py:179-279); level 7 and the intra-chunk
+ * levels are left untouched (zero in the reference).  It is no HState (the
+ * decode step builds strong states itself).
  */
 int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, const float* g,
                                const void* l, void* o, float* g_cumsum, float* ht, int B, int T,

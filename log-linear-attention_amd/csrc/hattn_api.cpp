@@ -24,6 +24,9 @@ size_t hattn_mamba2_fwd_static_scratch_bytes();
 hipError_t hattn_mamba2_fwd_static_scratch(void** ptr);
 int hattn_mamba2_fwd_max_levels(int x3);
 int hattn_mamba2_strong_max_levels();
+hipError_t hattn_mamba2_strong_ht_launch(const void* k, const void* v, const float* g, float* ht,
+                                         int B, int T, int G, int H, int V, int L,
+                                         hipStream_t stream);
 hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const void* v,
                                           const float* g, const void* l, void* o, float* gcum,
                                           int B, int T, int G, int H, int V, int L, int dt_l,
@@ -243,10 +246,6 @@ static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const fl
     if (dtype_qk != HATTN_BF16 || dtype_v != HATTN_BF16)
       return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: q/k/v dtype codes %d/%d (bf16 required)",
                   dtype_qk, dtype_v);
-    if (ht != nullptr)
-      return fail(HATTN_ERR_NOT_IMPLEMENTED,
-                  "HType.STRONG: output_final_state (the reference stores one of four phase states "
-                  "per level, chunkwise.py:275-279; use the recurrent HState for decoding)");
     if (int st = check_span(T, max_of({(size_t)G * K * 2, (size_t)H * V * elem_bytes(dtype_o),
                                         (size_t)H * L * elem_bytes(dtype_l), (size_t)H * 4})))
       return st;
@@ -259,6 +258,9 @@ static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const fl
     if (unsupported)
       return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: dtype combination l=%d o=%d", dtype_l,
                   dtype_o);
+    if (e == hipSuccess && ht != nullptr)
+      // the raw phase-0 state of each strong level (chunkwise.py:179-279)
+      e = hattn_mamba2_strong_ht_launch(k, v, g, ht, B, T, G, H, V, L, (hipStream_t)stream);
     return check_hip(e, "hattn_mamba2_chunkwise_fwd (strong) launch");
   }
   if (dtype_qk != HATTN_BF16 && dtype_qk != HATTN_FP32)

@@ -111,14 +111,16 @@ constexpr int kCohStore = 16;  // sc1
 // columns) and returns D_p (on every thread).  COH: the stores carry kCohStore.
 // LAYER: v is the layer's x and g comes from dt (v = x dt', g = A dt', see
 // layer_math.h); bf16 x only.  NSLOT: chunks held in registers ahead of the
-// one being multiplied (the loads in flight per workgroup).
+// one being multiplied (the loads in flight per workgroup).  Element (k, v) of
+// the summary goes to out[(k V + v) ostride], multiplied by oscale.
 template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false, int NSLOT = 2>
 __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restrict__ k,
                                               const TV* __restrict__ v,
                                               const float* __restrict__ g, float* __restrict__ out,
                                               int b, int h, int p, int vblk, int T, int G, int H,
                                               int V, int NT, int S,
-                                              const LayerArgs& la = LayerArgs{}) {
+                                              const LayerArgs& la = LayerArgs{},
+                                              int ostride = 1, float oscale = 1.f) {
   static_assert(!LAYER || (sizeof(TV) == 2 && NP == 1 && !GCUM), "layer mode: bf16 x");
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
@@ -276,13 +278,15 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
     for (int n = 0; n < 4; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        __hip_atomic_store(out + (size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln, acc[n][i],
+        __hip_atomic_store(out + ((size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln) * ostride,
+                           acc[n][i] * oscale,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) out[(size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln] = acc[n][i];
+      for (int i = 0; i < 4; ++i)
+        out[((size_t)(16 * w + 4 * lq + i) * V + 16 * n + ln) * ostride] = acc[n][i] * oscale;
   }
   return dsum;
 }

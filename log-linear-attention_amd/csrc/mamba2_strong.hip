@@ -292,6 +292,51 @@ static hipError_t strong_launch_t(const void* q, const void* k, const void* v, c
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Final states (output_final_state) of the strong hierarchy
+// ---------------------------------------------------------------------------
+// The reference stores, for each inter-chunk level ell = 1 .. nlev - 1 of the
+// strong loop (ell_init = 1, chunkwise.py:1215-1219), the raw phase-0 state b_h
+// of chunk_fwd_kernel_h with USE_H2 after its last chunk (chunkwise.py:179-279):
+// per chunk i, b_h is reset when i % 2^(ell+1) == 2^(ell+1) - 1 (skip_g, except
+// at the last chunk, which decays) or else decayed by exp(Gc_last(i)), then
+// gains the chunk's e^{Gc_last - Gc}-weighted k^T v when get_phase_index(i, ell)
+// is 0, i.e. i % 2^(ell+1) < 2^(ell-1).  After the last reset (the chunk before
+// base = 2^(ell+1) floor((NT - 1) / 2^(ell+1))) those chunks are
+// base .. base + 2^(ell-1) - 1, so
+//   ht[.., 7 + ell] = exp(G_T - G_end) Sum(base .. end),  end = min(base + 2^(ell-1), NT),
+// the range's summary (mamba2_common.h) decayed over the tokens after it.
+// Levels 0 .. 7 stay as the caller initialised them (zero, like the reference).
+// One workgroup per (row, ell, 64-column block of V).
+__global__ __launch_bounds__(256) void mamba2_strong_ht_kernel(
+    const __bf16* __restrict__ k, const __bf16* __restrict__ v, const float* __restrict__ g,
+    float* __restrict__ ht, int B, int T, int G, int H, int V, int L, int nlev) {
+  __shared__ __attribute__((aligned(16))) SumSmem<1> sm;
+  __shared__ float red[16];
+  const int nvb = V / 64;
+  const int vblk = blockIdx.x % nvb, ell = 1 + (blockIdx.x / nvb) % (nlev - 1);
+  const int row = blockIdx.x / (nvb * (nlev - 1));
+  if (row >= B * H) return;
+  const int b = row / H, h = row % H;
+  const int NT = T / kBT;
+  const int P = 2 << ell, S = 1 << (ell - 1);
+  const int base = (NT - 1) / P * P;
+  const int tend = min(base + S, NT) * kBT;   // first token after the range
+  // log-decay of the tokens after the range: sum of g over t >= tend
+  const float* gr = g + (size_t)b * T * H + h;
+  float x = 0.f;
+  for (int t = tend + (int)threadIdx.x; t < T; t += 256) x += gr[(size_t)t * H];
+  x = row_sum16(x);   // every lane of a 16-lane row holds the row's sum
+  if ((threadIdx.x & 15) == 0) red[threadIdx.x >> 4] = x;
+  __syncthreads();
+  float tail = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tail += red[i];
+  float* out = ht + (size_t)row * kKD * V * L + 7 + ell + (size_t)vblk * 64 * L;
+  seg_sum_body<__bf16, __bf16, false, 1, false>(sm, k, v, g, out, b, h, base / S, vblk, T, G, H,
+                                                 V, NT, S, LayerArgs{}, L, fexp(tail));
+}
+
 }  // namespace hattn
 
 int hattn_mamba2_strong_max_levels() { return hattn::kSMaxLev - 1; }
@@ -314,4 +359,20 @@ hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const vo
     return strong_launch_t<float, float>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
   *unsupported = 1;
   return hipSuccess;
+}
+
+// Final states of the strong hierarchy (levels 8 .. 6 + nlev of ht, the
+// others left as the caller initialised them); after the strong forward on the
+// same stream.  bf16 k, v; fp32 g (per-step log-decay).
+hipError_t hattn_mamba2_strong_ht_launch(const void* k, const void* v, const float* g, float* ht,
+                                         int B, int T, int G, int H, int V, int L,
+                                         hipStream_t stream) {
+  using namespace hattn;
+  int nlev = 0;
+  while ((1 << nlev) < T / kBT) ++nlev;
+  if (nlev < 2) return hipSuccess;   // only level 7 exists, and the reference leaves it zero
+  const int grid = B * H * (nlev - 1) * (V / 64);
+  hipLaunchKernelGGL(mamba2_strong_ht_kernel, dim3(grid), dim3(256), 0, stream, (const __bf16*)k,
+                     (const __bf16*)v, g, ht, B, T, G, H, V, L, nlev);
+  return hipGetLastError();
 }

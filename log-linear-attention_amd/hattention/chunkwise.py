@@ -119,9 +119,13 @@ def chunkwise_fwd(
     the inter-chunk level states at levels 7 .. 6 + ceil(log2(T/64)) (other
     levels zero), like the reference.
 
-    HType.STRONG (bf16 q / k / v, no final state) runs the strong kernel:
-    diagonal and sub-diagonal blocks from the strong level tables, farther
-    chunks from a chunk-level strong cascade (chunkwise.py:199-276, 587-641).
+    HType.STRONG (bf16 q / k / v) runs the strong kernel: diagonal and
+    sub-diagonal blocks from the strong level tables, farther chunks from a
+    chunk-level strong cascade (chunkwise.py:199-276, 587-641).  Its final
+    states are what the reference stores for the strong hierarchy: at level
+    7 + ell, ell = 1 .. ceil(log2(T/64)) - 1, the raw phase-0 state of its
+    strong state loop after the last chunk (chunkwise.py:179-279); level 7 and
+    the intra-chunk levels stay zero.
 
     The kernels contract over 64 key dimensions.  A larger K (a multiple of 64)
     runs one launch per 64-wide block of q and k: the output is linear in that

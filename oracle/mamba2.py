@@ -36,6 +36,11 @@ Restatements (reference file:line):
   Mamba-2 SSD recurrence h_t = exp(g_t) h_{t-1} + k_t v_t^T, o_t = q_t h_t:
   the textbook form that log-linear Mamba-2 reduces to when lambda == 1
   (the intent of the reference's check, hattention/mamba_apis.py:569-729).
+* ``strong_final_state`` -- the final states ``ht`` the reference's chunkwise
+  forward stores for HType.STRONG: the strong state loop of chunk_fwd_kernel_h
+  (USE_H2, chunkwise.py:94-280) with its raw phase-0 state b_h kept per level;
+  pinned against a closed form (a range of chunk summaries decayed to the end
+  of the sequence) in tests/test_oracle_mamba2.py.
 * ``autograd_bwd``      -- gradients (dq, dk, dv, dg, dl) of any of the above
   through torch.autograd; dg is w.r.t. the raw per-step g, which is what the
   reference returns after its reverse chunk-local cumsum (chunkwise.py:1596).
@@ -546,6 +551,42 @@ def chunked_scan_fwd(q, k, v, g, l, chunk_size: int = 64,
         y = torch.stack(ys, dim=1)
     g_cumsum = Gc.reshape(B0, T0, H)
     return y.reshape(B, T, H, V), g_cumsum, ht
+
+
+def strong_final_state(q, k, v, g, l, chunk_size: int = 64) -> torch.Tensor:
+    """``ht`` of chunkwise_fwd with HType.STRONG and output_final_state: the
+    loop of chunk_fwd_kernel_h with USE_H2, MODE_H2=1 and STORE_FINAL_STATE
+    (chunkwise.py:94-280) for the strong levels ell = 1 .. nlev - 1
+    (ell_init = 1, chunkwise.py:1215-1219), keeping its raw phase-0 state b_h.
+    Per chunk i: b_h is reset when skip_g(i, ell) (i % 2^(ell+1) == 2^(ell+1) - 1,
+    chunkwise.py:44-69; the last chunk decays instead, :227-233) or else
+    multiplied by exp(Gc_last(i)) (:250-257); then, when get_phase_index(i, ell)
+    (chunkwise.py:72-91, OFFSET=False) is 0, the chunk's decayed k^T v is added
+    (:258-275).  b_h is stored at level ell_h0 + ell (:277-279); the other
+    levels of the zero-initialised ht (chunkwise.py:1179) stay zero.
+    Returns [B, H, K, V, L]."""
+    C = chunk_size
+    q, k, v, g, l, (B, T, H, K, V, L, NT) = _chunk_views(q, k, v, g, l, C)
+    ell_h0 = get_num_levels(C, 2)
+    nlev = math.ceil(math.log2(NT)) if NT > 1 else 0
+    Gc = torch.cumsum(g, dim=2)
+    kv = _chunk_states(k, v, Gc)                                     # [B,NT,H,K,V]
+    last = torch.exp(Gc[:, :, -1, :])                                # [B,NT,H]
+    ht = torch.zeros(B, H, K, V, L, dtype=k.dtype)
+    for ell in range(1, nlev):
+        period = 1 << (ell + 1)
+        p0, p1 = 1 << ell, 1 << (ell - 1)
+        b_h = torch.zeros(B, H, K, V, dtype=k.dtype)
+        for i in range(NT):
+            if i % period == period - 1 and i != NT - 1:
+                b_h = torch.zeros_like(b_h)
+            else:
+                b_h = b_h * last[:, i][:, :, None, None]
+            phase = (int(i % period >= p0) << 1) | int(i % p0 >= p1)
+            if phase == 0:
+                b_h = b_h + kv[:, i]
+        ht[..., ell_h0 + ell] = b_h
+    return ht
 
 
 # --------------------------------------------------------------------------

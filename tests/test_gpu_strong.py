@@ -89,6 +89,44 @@ def test_strong_fwd_nine_chunk_levels():
     _run_fwd(1, 32768, 2, 2, 64, 64, 16, seed=327)
 
 
+@pytest.mark.parametrize("B,T,G,H,K,V", [
+    (1, 1024, 2, 2, 64, 64),      # 16 chunks: the last chunk ends every block
+    (1, 5184, 2, 2, 64, 64),      # 81 chunks: ragged blocks, one-chunk ranges at the end
+    (2, 2112, 1, 2, 128, 128),    # 33 chunks, grouped q / k, K and V of two 64-blocks
+    (1, 16384, 2, 2, 64, 64),     # the north star's length: levels 8 .. 14
+    (1, 32768, 1, 1, 64, 64),     # nine chunk levels
+])
+def test_strong_final_state(B, T, G, H, K, V):
+    """output_final_state with HType.STRONG: ht against the oracle's restatement
+    of the reference's USE_H2 state loop (oracle.mamba2.strong_final_state,
+    pinned against its closed form on the CPU), every row; 1e-2 relative to each
+    level's largest state, as the weak final states (a level decayed below
+    1e-12 of the largest state, which fp64 keeps and fp32 flushes to zero, is
+    checked against that floor); levels 0 .. 7 exactly zero.  o and g_cumsum
+    are the ones of the call without final states."""
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_fwd
+    L = _levels(T)
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=90 + T)
+    print(f"[strong ht] B={B} T={T} G={G} H={H} K={K} V={V} L={L}", flush=True)
+    ins = [x.to(DEV) for x in (q, k, v, g, l)]
+    o, gc, ht = chunkwise_fwd(*ins, False, 2, HType.STRONG, 64, True)
+    o0, gc0, _ = chunkwise_fwd(*ins, False, 2, HType.STRONG, 64, False)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o0) and torch.equal(gc, gc0)
+    assert ht.shape == (B, H, K, V, L) and ht.dtype == torch.float32
+    ref = M.strong_final_state(*(x.double() for x in (q, k, v, g, l)), chunk_size=64)
+    ht = ht.double().cpu()
+    assert ht[..., :8].abs().max() == 0
+    nlev = math.ceil(math.log2(T // 64))
+    scale = ref.abs().max().item()
+    for e in range(1, nlev):
+        r = ref[..., 7 + e]
+        err = ((ht[..., 7 + e] - r).abs().max() / max(r.abs().max().item(), 1e-12 * scale)).item()
+        print(f"  level {7 + e}: max-rel {err:.2e}", flush=True)
+        assert err < 1e-2, (e, err)
+
+
 def test_strong_differs_from_weak():
     """The strong path is taken: its output differs from the weak one's on the
     same inputs by far more than the tolerance."""

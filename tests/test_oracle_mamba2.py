@@ -276,3 +276,40 @@ def test_strong_backward_decomposition_matches_autograd(T, C, G):
     for name, a, r in zip(("dq", "dk", "dv", "dg", "dl"), got, ref):
         assert a.shape == r.shape, name
         assert rel(a, r) < 1e-11, (name, rel(a, r))
+
+
+@pytest.mark.parametrize("NT", [2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 31, 32, 33])
+def test_strong_final_state_closed_form(NT):
+    """strong_final_state (the reference's USE_H2 state loop with its phases and
+    resets) against the closed form the HIP kernel computes: level 7 + ell,
+    ell >= 1, holds the chunks base .. base + 2^(ell-1) - 1 (base: the start of
+    the aligned 2^(ell+1)-chunk block that holds the last chunk), each chunk's
+    decayed k^T v further decayed to the end of the sequence; every other level
+    zero.  A wrong phase test, reset position or final-chunk rule changes which
+    chunks a level holds."""
+    C = 4
+    B, H, K, V = 1, 2, 3, 2
+    T = C * NT
+    nlev = math.ceil(math.log2(NT))
+    L = 3 + nlev
+    gen = torch.Generator().manual_seed(1234 + NT)
+    q = torch.randn(B, T, H, K, generator=gen, dtype=torch.float64)
+    k = torch.randn(B, T, H, K, generator=gen, dtype=torch.float64)
+    v = torch.randn(B, T, H, V, generator=gen, dtype=torch.float64)
+    g = -0.2 * torch.rand(B, T, H, generator=gen, dtype=torch.float64)
+    l = torch.rand(B, T, H, L, generator=gen, dtype=torch.float64)
+    ht = M.strong_final_state(q, k, v, g, l, chunk_size=C)
+    ell_h0 = 3   # get_num_levels(4, 2)
+    G = torch.cumsum(g, dim=1)                                  # [B, T, H]
+    ref = torch.zeros_like(ht)
+    for ell in range(1, nlev):
+        P, S = 2 << ell, 1 << (ell - 1)
+        base = (NT - 1) // P * P
+        for c in range(base, min(base + S, NT)):
+            for t in range(C * c, C * c + C):
+                w = torch.exp(G[:, T - 1] - G[:, t])               # decay of token t to the end
+                ref[..., ell_h0 + ell] += torch.einsum("bh,bhk,bhv->bhkv", w, k[:, t], v[:, t])
+    assert torch.allclose(ht, ref, rtol=1e-12, atol=1e-12)
+    assert ht[..., ell_h0].abs().max() == 0          # ell = 0: not part of the strong loop
+    for ell in range(1, nlev):
+        assert ht[..., ell_h0 + ell].abs().max() > 0

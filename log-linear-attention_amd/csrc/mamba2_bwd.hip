@@ -625,8 +625,43 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(ln0));
 
     // ---- phase 1: (M o dP) tiles and the intra-chunk dlambda partials ----------
+    // bf16 (bf16 v: with fp32 v the staging registers leave no room): the
+    // wave's diagonal tile (its first) and its first sub-diagonal tile together
+    // (LDS reads, MFMAs, masks, then the partials), the third tile (a
+    // sub-diagonal one on waves 0 and 1, a zero tile on 2 and 3) after them
+    constexpr bool kP1Pair = NP == 1 && sizeof(TV) == 2;
+    if constexpr (kP1Pair) {
+      const int c1 = p1_tile4(w, 1);
+      int tmt[2] = {w, (c1 & 15) >> 2}, tjt[2] = {w, c1 & 3};
+      floatx4 S[2], P[2];
+      st_dpt_tiles2(s, tmt, tjt, S, P);
+      float out[2][4], x[2][4];
 #pragma unroll
-    for (int n = 0; n < 3; ++n) {
+      for (int n = 0; n < 2; ++n) {
+        const TileMask mk = tile_mask_sel(s, tmt[n], tjt[n], true);
+        const int t = 16 * tmt[n] + ln;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pd = mk.dec[i] * P[n][i];
+          out[n][i] = pd * s.lam[mk.lev[i] * kBT + t];
+          x[n][i] = pd * S[n][i];
+        }
+        if (n == 0) {
+#pragma unroll
+          for (int lv = 0; lv < 5; ++lv) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a += mk.lev[i] == lv ? x[0][i] : 0.f;
+            sm.dl_diag[t][lv][lq] = a;
+          }
+        } else {
+          sm.dl_off[t][tjt[1]][lq] = x[1][0] + x[1][1] + x[1][2] + x[1][3];
+        }
+        store_planes4<NP>(sm.a, t * kLd + 16 * tjt[n] + 4 * lq, out[n]);
+      }
+    }
+#pragma unroll
+    for (int n = kP1Pair ? 2 : 0; n < 3; ++n) {
       const int code = p1_tile4(w, n);
       const int mt = (code & 15) >> 2, jt = code & 3;
       const int t = 16 * mt + ln;

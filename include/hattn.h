@@ -232,6 +232,14 @@ size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, i
  *          given, as the reference's chunkwise_fwd does
  *   workspace >= hattn_gdn_chunkwise_fwd_workspace(...) bytes
  *
+ * htype HATTN_HTYPE_WEAK, or HATTN_HTYPE_STRONG: what the reference's chunkwise
+ * GDN path computes with the strong level table (chunkwise_hgdn.py:630,
+ * 724-728, 782): lambda of an intra-chunk pair at its strong level, the
+ * inter-chunk levels from 1 with the same (weak) delta-rule states, and every
+ * chunk reading every level >= 1; ht then holds levels 8 .. 6 + nlev (level 7
+ * is left as the caller set it, zero in the reference).  Any other htype ->
+ * HATTN_ERR_VALUE.
+ *
  * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64,
  * T * H * max(K, V) < 2^31 -> HATTN_ERR_VALUE; K in {64, 128, 192, 256} (the
  * reference's limit is K <= 256, chunkwise_hgdn.py:600-601), any V multiple of
@@ -296,6 +304,13 @@ size_t hattn_gdn_chunkwise_fwd_keep_workspace(int B, int T, int H, int K, int V,
  *   raw inputs and dq, dk are w.r.t. them (the l2norm chain rule of
  *   kernel.py:24-29, 224-225 applied inside the kernel)
  *   workspace >= hattn_gdn_chunkwise_bwd_workspace(...) bytes
+ *
+ * htype STRONG: the gradient of the strong forward above (the level reads at
+ * every chunk for levels >= 1 enter dq, dlambda and the dh scan).  The
+ * reference's backward for that mode masks the level reads with the weak
+ * skip_q (chunkwise_hgdn.py:1034, 1066-1067) and adds du on chunks whose u the
+ * forward masked (chunkwise.py:1008-1012), so it is not the derivative of its
+ * own forward; this one is.
  *
  * Constraints as hattn_gdn_chunkwise_fwd, except K in {64, 128, 192, 256} and V in
  * {64, 128} -> HATTN_ERR_NOT_IMPLEMENTED (the gradients are sums over independent column

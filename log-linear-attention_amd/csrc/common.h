@@ -49,6 +49,26 @@ __device__ __forceinline__ int intra_level(int t, int s) {
   return x == 0 ? 0 : 32 - __clz(x);
 }
 
+// The strong level function for t > s (base.py:49-62 with base 2), for the
+// compile-time level tables of the HType.STRONG kernels.
+constexpr int strong_level_ce(int t, int s) {
+  for (;;) {
+    int ell = 0;
+    while ((2 << ell) <= t) ++ell;          // floor(log2 t)
+    const int v = 1 << (ell > 0 ? ell - 1 : 0);
+    const int r = t - (1 << ell);
+    if (s < v) return ell + 1;
+    if (s < 2 * v && r >= v) return ell + 1;
+    if (s < 2 * v) {
+      t -= v;
+      s -= v;
+    } else {
+      t -= 2 * v;
+      s -= 2 * v;
+    }
+  }
+}
+
 // Workgroup -> (row, slice) map that keeps the slices of one (batch, head)
 // row on one XCD (workgroups are dispatched round-robin over the 8 XCDs), so
 // the rows they share (q, k, g, lambda) are fetched into that XCD's L2 once.

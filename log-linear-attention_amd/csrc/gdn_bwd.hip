@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
     const TL* __restrict__ l, const __bf16* __restrict__ hsave, __bf16* __restrict__ dq_p,
     __bf16* __restrict__ dw_p, __bf16* __restrict__ dk_p, float* __restrict__ du,
     float* __restrict__ dl_p, float* __restrict__ del_p, int B, int T, int H, int V, int L,
-    int nlev) {
+    int nlev, int strong) {
   using Sm = GdnBscanSmem<KD>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   Sm& s = *(Sm*)smem_raw;
@@ -204,9 +204,12 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
       for (int j = 0; j < TPW; ++j) cur[j] = dh[0][j];
       if (e < nlev) {
         const int per = 2 << e;
-        const bool rd = (ic >> e) & 1;
+        const bool bit = (ic >> e) & 1;
+        // the forward's level read: bit e set; strong: every chunk reads every
+        // level >= 1 and none reads level 0 (the writes keep the weak masks)
+        const bool rd = strong ? e >= 1 : bit;
         const bool nr = (ic & (per - 1)) != per - 1;
-        const float frd = rd ? 1.f : 0.f, fwr = 1.f - frd, fnr = nr ? 1.f : 0.f;
+        const float frd = rd ? 1.f : 0.f, fwr = bit ? 0.f : 1.f, fnr = nr ? 1.f : 0.f;
 #pragma unroll
         for (int i = 0; i < HU; ++i) {
           const int u = tid + NTH * i;
@@ -561,7 +564,8 @@ __device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], YAt yat,
   }
 }
 
-template <int KD, int VD, typename TB, typename TL>
+// STRONG: lambda of an intra-chunk pair at its strong level (the forward's P).
+template <int KD, int VD, typename TB, typename TL, bool STRONG = false>
 __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ gcum, const TL* __restrict__ l,
@@ -725,7 +729,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
         if (sc <= t) {
           const float gam = fexp(s.gc[t] - s.gc[sc]);
           zp = z[i] * S3[t * kLM + sc] * gam;
-          dp = z[i] * gam * s.lam[intra_level(t, sc)][t] * s.beta[sc];
+          dp = z[i] * gam * s.lam[gdn_intra_level<STRONG>(t, sc)][t] * s.beta[sc];
         }
         S0[t * kLM + sc] = zp;
         S4[t * kLM + sc] = dp;
@@ -745,7 +749,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     for (int x = 0; x < 16; ++x) {
       const int sc = c0 + x;
       if (sc <= r) {
-        const int lv = intra_level(r, sc);
+        const int lv = gdn_intra_level<STRONG>(r, sc);
         const float val = S0[r * kLM + sc] * s.beta[sc];
 #pragma unroll
         for (int l = 0; l < 7; ++l) dlv[l] += l == lv ? val : 0.f;
@@ -756,7 +760,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int t = c0 + x;
-      if (t >= r) cs += S0[t * kLM + r] * s.lam[intra_level(t, r)][t];
+      if (t >= r) cs += S0[t * kLM + r] * s.lam[gdn_intra_level<STRONG>(t, r)][t];
     }
 #pragma unroll
     for (int l = 0; l < 7; ++l) {
@@ -1107,7 +1111,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
         const int t = 32 * c + 8 * lq + j, sc = t16 + ln;
         const float gam = t >= sc ? fexp(s.gc[t] - s.gc[sc]) : 0.f;
         au[c][j] *= gam;
-        ar[c][j] *= gam * s.lam[intra_level(t, sc)][t];
+        ar[c][j] *= gam * s.lam[gdn_intra_level<STRONG>(t, sc)][t];
       }
     }
     float rbv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1238,7 +1242,7 @@ inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V,
   return w;
 }
 
-template <int KD, int VD, typename TB, typename TL>
+template <int KD, int VD, typename TB, typename TL, bool STRONG>
 static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const void* beta,
                             const float* gcum, const void* l, const void* dO, void* dq, void* dk,
                             void* dv, void* db, float* dg, float* dl, const GdnBwdWs& w, int B,
@@ -1255,11 +1259,11 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
     hipLaunchKernelGGL(ks, dim3(B * H * (VD / kBVs)), dim3(64 * gdn_bscan_waves<KD>()), smem,
                        stream, w.qn, w.wn, w.kn,
                        w.un, (const __bf16*)dO, gcum, (const TL*)l, w.hs, w.dq_p, w.dw_p, w.dk_p,
-                       w.du, w.dl_p, w.del_p, B, T, H, VD, L, nlev);
+                       w.du, w.dl_p, w.del_p, B, T, H, VD, L, nlev, STRONG ? 1 : 0);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kc = gdn_bwd_chunk_kernel<KD, VD, TB, TL>;
+    auto kc = gdn_bwd_chunk_kernel<KD, VD, TB, TL, STRONG>;
     const int smem = (int)sizeof(GdnBchunkSmem<KD, VD>);
     if ((e = hipFuncSetAttribute((const void*)kc, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  smem)) != hipSuccess)
@@ -1288,22 +1292,22 @@ hipError_t gdn_bwd_dispatch(const void* q, const void* k, const void* v, const v
                             const float* gcum, const void* l, const void* dO, void* dq, void* dk,
                             void* dv, void* db, float* dg, float* dl, const hattn::GdnBwdWs& w,
                             int B, int T, int H, int K, int V, int L, int nlev, int dt_b, int dt_l,
-                            int norm_qk, float scale, hipStream_t stream, int* unsupported) {
+                            int norm_qk, float scale, int strong, hipStream_t stream,
+                            int* unsupported) {
   using namespace hattn;
+#define HATTN_GDN_BT(KD_, VD_, TB_, TL_)                                                        \
+  return strong ? gdn_bwd_t<KD_, VD_, TB_, TL_, true>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db,  \
+                                                      dg, dl, w, B, T, H, L, nlev, norm_qk, scale, \
+                                                      stream)                                      \
+                : gdn_bwd_t<KD_, VD_, TB_, TL_, false>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, \
+                                                       dg, dl, w, B, T, H, L, nlev, norm_qk,       \
+                                                       scale, stream);
 #define HATTN_GDN_B(KD_, VD_)                                                                   \
   if (K == KD_ && V == VD_) {                                                                   \
-    if (dt_b == 0 && dt_l == 0)                                                                 \
-      return gdn_bwd_t<KD_, VD_, __bf16, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, \
-                                                 dl, w, B, T, H, L, nlev, norm_qk, scale, stream);              \
-    if (dt_b == 2 && dt_l == 2)                                                                 \
-      return gdn_bwd_t<KD_, VD_, float, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,   \
-                                               dl, w, B, T, H, L, nlev, norm_qk, scale, stream);                \
-    if (dt_b == 0 && dt_l == 2)                                                                 \
-      return gdn_bwd_t<KD_, VD_, __bf16, float>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
-                                                dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
-    if (dt_b == 2 && dt_l == 0)                                                                 \
-      return gdn_bwd_t<KD_, VD_, float, __bf16>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg,  \
-                                                dl, w, B, T, H, L, nlev, norm_qk, scale, stream);               \
+    if (dt_b == 0 && dt_l == 0) HATTN_GDN_BT(KD_, VD_, __bf16, __bf16)                          \
+    if (dt_b == 2 && dt_l == 2) HATTN_GDN_BT(KD_, VD_, float, float)                            \
+    if (dt_b == 0 && dt_l == 2) HATTN_GDN_BT(KD_, VD_, __bf16, float)                           \
+    if (dt_b == 2 && dt_l == 0) HATTN_GDN_BT(KD_, VD_, float, __bf16)                           \
   }
   HATTN_GDN_B(256, 128)
   HATTN_GDN_B(256, 64)
@@ -1314,6 +1318,7 @@ hipError_t gdn_bwd_dispatch(const void* q, const void* k, const void* v, const v
   HATTN_GDN_B(64, 128)
   HATTN_GDN_B(64, 64)
 #undef HATTN_GDN_B
+#undef HATTN_GDN_BT
   *unsupported = 1;
   return hipSuccess;
 }
@@ -1323,8 +1328,8 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, int norm_qk, float scale, hipStream_t stream,
-                                int* unsupported) {
+                                int dt_l, int norm_qk, float scale, int strong,
+                                hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
@@ -1333,7 +1338,7 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
                                             stream, unsupported);
   if (e != hipSuccess || *unsupported) return e;
   return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
-                          L, nlev, dt_b, dt_l, norm_qk, scale, stream, unsupported);
+                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, stream, unsupported);
 }
 
 size_t hattn_gdn_bwd_kept_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
@@ -1348,7 +1353,7 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
                                      float* dg, float* dl, const __bf16* qn, const __bf16* wn,
                                      const __bf16* kn, const __bf16* un, const __bf16* hs,
                                      void* ws, int B, int T, int H, int K, int V, int L, int nlev,
-                                     int dt_b, int dt_l, int norm_qk, float scale,
+                                     int dt_b, int dt_l, int norm_qk, float scale, int strong,
                                      hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
@@ -1359,5 +1364,5 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
   w.un = const_cast<__bf16*>(un);
   w.hs = const_cast<__bf16*>(hs);
   return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
-                          L, nlev, dt_b, dt_l, norm_qk, scale, stream, unsupported);
+                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, stream, unsupported);
 }

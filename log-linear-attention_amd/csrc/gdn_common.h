@@ -11,6 +11,31 @@ constexpr int kGBwdMaxLev = 8;   // inter-chunk levels of the backward scan (T <
 constexpr int kBVs = 32;      // V columns per backward-scan workgroup
 constexpr int kLM = 65;       // row stride of 64 x 64 fp32 LDS matrices
 
+// HType.STRONG intra-chunk levels: the reference's chunkwise GDN path takes
+// lambda of a pair inside a chunk at its strong level (make_levels_matrix with
+// htype STRONG, chunkwise_hgdn.py:630), which on an aligned 64-token chunk is
+// the strong function of the chunk-local positions; [t][s], 0 on and above
+// the diagonal.
+struct alignas(16) GdnStrongIntra {
+  unsigned char lv[kGC * kGC];
+  constexpr GdnStrongIntra() : lv() {
+    for (int a = 0; a < kGC; ++a)
+      for (int b = 0; b < kGC; ++b) lv[a * kGC + b] = (unsigned char)(b < a ? strong_level_ce(a, b) : 0);
+  }
+};
+__device__ constexpr GdnStrongIntra kGdnStrongIntra{};
+
+// Level of the pair (t, s) of one chunk (chunk-local, s <= t): the weak closed
+// form, or the strong table (a cached global byte read; only the STRONG
+// instantiations read it).
+template <bool STRONG>
+__device__ __forceinline__ int gdn_intra_level(int t, int s) {
+  if constexpr (STRONG)
+    return kGdnStrongIntra.lv[t * kGC + s];
+  else
+    return intra_level(t, s);
+}
+
 // 16-byte units of a row-major [NR][N] bf16 tile, 256 threads (threads
 // T0 .. T0 + 255 of the workgroup).  The unit loop has a compile-time trip
 // count and every load is issued before the first LDS store, so the tile costs

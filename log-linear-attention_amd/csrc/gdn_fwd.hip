@@ -73,7 +73,9 @@ constexpr int kPrepThreads = 512;
 // transposed) and U.
 enum { kPrepFwd = 0, kPrepRecompute = 1, kPrepFwdKeep = 2 };
 
-template <int KD, typename TB, typename TL, int MODE>
+// STRONG: the P tile takes lambda at the strong level of each pair (the
+// reference's HType.STRONG, chunkwise_hgdn.py:630); only P depends on it.
+template <int KD, typename TB, typename TL, int MODE, bool STRONG = false>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
           const int sc = 16 * st + 4 * lq + i;
           float x = 0.f;
           if (sc <= t)
-            x = d[i] * fexp(s.gc[t] - s.gc[sc]) * s.beta[sc] * s.lam[intra_level(t, sc)][t];
+            x = d[i] * fexp(s.gc[t] - s.gc[sc]) * s.beta[sc] * s.lam[gdn_intra_level<STRONG>(t, sc)][t];
           pb4[i] = (__bf16)x;
         }
         *(bf16x4*)(pm + (((size_t)row * NT + ic) * kGC + t) * kGC + 16 * st + 4 * lq) = pb4;
@@ -438,7 +440,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const __bf16* __restrict__ un, const __bf16* __restrict__ pm, const __bf16* __restrict__ vin,
     const float* __restrict__ gcum, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ ht, __bf16* __restrict__ hsave, int nrows, int T, int H, int V, int L,
-    int nlev, int final_state) {
+    int nlev, int final_state, int strong) {
   using C = GdnScanCfg<KD, BV>;
   using Sm = GdnScanSmem<KD, BV>;
   constexpr bool kSave = SMODE != kScanOut, kOut = SMODE != kScanSave;
@@ -565,10 +567,13 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const bool last = ic == NT - 1;
 
     const int per = 2 << e, pos = ic & (per - 1);
-    const bool rd = act && ((ic >> e) & 1);
+    const bool bit = (ic >> e) & 1;
+    // the level read: chunks with bit e set; with strong every chunk reads every
+    // level >= 1 (and level 0 is read by none), the states are the same
+    const bool rd = act && (strong ? e >= 1 : bit);
     const bool first = act && pos == 0;
     const bool reset = act && pos == per - 1 && !(last && final_state);
-    const bool wr = act && !rd;
+    const bool wr = act && !bit;
     const bool needy = act && !first && !reset;
 
     if constexpr (kSave) {
@@ -698,17 +703,19 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
 
     stage_store();     // chunk ic + 1
     if constexpr (kOut) {
-      // o = o_intra + the reads of the levels with bit e of ic set
+      // o = o_intra + the reads of the levels with bit e of ic set (strong: of
+      // every level >= 1)
       const int po = (ot & (kGC - 1)) * LP + ov;
       floatx4 x = *(const floatx4*)(&s.part[kGMaxLev][po]);
       for (int le = 0; le < nlev; ++le)
-        if ((ic >> le) & 1) x += *(const floatx4*)(&s.part[le][po]);
+        if (strong ? le >= 1 : ((ic >> le) & 1)) x += *(const floatx4*)(&s.part[le][po]);
       buf_store4<TO>(x, ro, o_voff, (unsigned)((size_t)ic * kGC * HV * sizeof(TO)));
     }
     __syncthreads();   // chunk ic + 1 staged; the level reads are summed
   }
-  if (final_state && ht != nullptr && act) {
-    // ht[b, h, k, v, 7 + e] (chunkwise_hgdn.py:786-787)
+  if (final_state && ht != nullptr && act && !(strong && e == 0)) {
+    // ht[b, h, k, v, 7 + e] (chunkwise_hgdn.py:786-787; strong: levels >= 1,
+    // level 7 stays as the caller zeroed it, :724-728)
     float* hb = ht + (size_t)row * KD * V * L + (size_t)v0 * L + 7 + e;
     const size_t VL = (size_t)V * L;
 #pragma unroll
@@ -783,13 +790,13 @@ inline int device_cus() {
   return cus[dev];
 }
 
-template <int KD, typename TB, typename TL, int MODE>
+template <int KD, typename TB, typename TL, int MODE, bool STRONG = false>
 static hipError_t gdn_prep_launch_t(const void* q, const void* k, const void* v, const void* beta,
                                     const float* g, const void* l, float* gcum, void* aw, void* au,
                                     __bf16* qn, __bf16* wn, __bf16* kn, __bf16* knT, __bf16* un,
                                     __bf16* pm, int B, int T, int H, int V, int L, int norm_qk,
                                     float scale, hipStream_t stream) {
-  auto kp = gdn_prep_kernel<KD, TB, TL, MODE>;
+  auto kp = gdn_prep_kernel<KD, TB, TL, MODE, STRONG>;
   const int smem = (int)sizeof(GdnPrepSmem<KD>);
   hipError_t e;
   if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -809,7 +816,7 @@ template <int KD, typename TL, typename TO>
 static hipError_t gdn_scan_launch_t(const GdnWs& w, const void* v, const float* gcum,
                                     const void* l, void* o, float* ht, __bf16* hsave, int B,
                                     int T, int H, int V, int L, int nlev, int final_state,
-                                    hipStream_t stream) {
+                                    int strong, hipStream_t stream) {
   constexpr int BV = ScanBV<KD>::value;
   // hsave without o: the recompute; both: a forward that keeps the states
   auto ks = !hsave ? gdn_scan_kernel<KD, BV, TL, TO, kScanOut>
@@ -824,36 +831,36 @@ static hipError_t gdn_scan_launch_t(const GdnWs& w, const void* v, const float* 
   const int grid = (rows + 7) / 8 * 8 * (V / BV);
   hipLaunchKernelGGL(ks, dim3(grid), dim3(512), smem, stream, w.qn, w.wn, w.knT, w.un, w.pm,
                      (const __bf16*)v, gcum, (const TL*)l, (TO*)o, ht, hsave, rows, T, H, V, L,
-                     nlev, final_state);
+                     nlev, final_state, strong);
   return hipGetLastError();
 }
 
-template <int KD, typename TB, typename TL, typename TO>
+template <int KD, typename TB, typename TL, typename TO, bool STRONG>
 static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, const void* beta,
                                const float* g, const void* l, void* o, float* gcum, void* aw,
                                void* au, float* ht, void* ws, int B, int T, int H, int V, int L,
                                int nlev, int norm_qk, float scale, hipStream_t stream) {
   const GdnWs w = gdn_ws_layout(ws, B, T, H, KD, V);
-  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwd>(
+  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwd, STRONG>(
       q, k, v, beta, g, l, gcum, aw, au, w.qn, w.wn, nullptr, w.knT, w.un, w.pm, B, T, H, V, L,
       norm_qk, scale, stream);
   if (e != hipSuccess) return e;
   return gdn_scan_launch_t<KD, TL, TO>(w, v, gcum, l, o, ht, nullptr, B, T, H, V, L, nlev,
-                                       ht != nullptr ? 1 : 0, stream);
+                                       ht != nullptr ? 1 : 0, STRONG ? 1 : 0, stream);
 }
 
-template <int KD, typename TB, typename TL, typename TO>
+template <int KD, typename TB, typename TL, typename TO, bool STRONG>
 static hipError_t gdn_launch_keep_t(const void* q, const void* k, const void* v, const void* beta,
                                     const float* g, const void* l, void* o, float* gcum, void* aw,
                                     void* au, float* ht, void* ws, int B, int T, int H, int V,
                                     int L, int nlev, int norm_qk, float scale, hipStream_t stream) {
   const GdnKeepWs w = gdn_keep_ws_layout(ws, B, T, H, KD, V, nlev);
-  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwdKeep>(
+  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwdKeep, STRONG>(
       q, k, v, beta, g, l, gcum, aw, au, w.f.qn, w.f.wn, w.kn, w.f.knT, w.f.un, w.f.pm, B, T, H,
       V, L, norm_qk, scale, stream);
   if (e != hipSuccess) return e;
   return gdn_scan_launch_t<KD, TL, TO>(w.f, v, gcum, l, o, ht, w.hs, B, T, H, V, L, nlev,
-                                       ht != nullptr ? 1 : 0, stream);
+                                       ht != nullptr ? 1 : 0, STRONG ? 1 : 0, stream);
 }
 
 }  // namespace hattn
@@ -879,13 +886,17 @@ hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v
                                      const void* beta, const float* g, const void* l, void* o,
                                      float* gcum, void* aw, void* au, float* ht, void* ws, int B,
                                      int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                     int dt_l, int dt_o, int norm_qk, float scale,
+                                     int dt_l, int dt_o, int norm_qk, float scale, int strong,
                                      hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
 #define HATTN_GDN_KDT(KD_, TB_, TL_)                                                            \
-  return gdn_launch_keep_t<KD_, TB_, TL_, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, \
-                                                  T, H, V, L, nlev, norm_qk, scale, stream);
+  return strong ? gdn_launch_keep_t<KD_, TB_, TL_, __bf16, true>(                                 \
+                      q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, H, V, L, nlev, norm_qk,  \
+                      scale, stream)                                                              \
+                : gdn_launch_keep_t<KD_, TB_, TL_, __bf16, false>(                                \
+                      q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, H, V, L, nlev, norm_qk,  \
+                      scale, stream);
 #define HATTN_GDN_K(KD_)                                                                        \
   if (K == KD_ && dt_o == 0) {                                                                  \
     if (dt_b == 0 && dt_l == 0) HATTN_GDN_KDT(KD_, __bf16, __bf16)                              \
@@ -916,12 +927,16 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
-                                float scale, hipStream_t stream, int* unsupported) {
+                                float scale, int strong, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
 #define HATTN_GDN_DT(KD_, TB_, TL_)                                                             \
-  return gdn_launch_t<KD_, TB_, TL_, __bf16>(q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, \
-                                             H, V, L, nlev, norm_qk, scale, stream);
+  return strong ? gdn_launch_t<KD_, TB_, TL_, __bf16, true>(q, k, v, beta, g, l, o, gcum, aw, au, \
+                                                            ht, ws, B, T, H, V, L, nlev, norm_qk,  \
+                                                            scale, stream)                        \
+                : gdn_launch_t<KD_, TB_, TL_, __bf16, false>(q, k, v, beta, g, l, o, gcum, aw,    \
+                                                             au, ht, ws, B, T, H, V, L, nlev,     \
+                                                             norm_qk, scale, stream);
 #define HATTN_GDN(KD_)                                                                          \
   if (K == KD_ && dt_o == 0) {                                                                  \
     if (dt_b == 0 && dt_l == 0) HATTN_GDN_DT(KD_, __bf16, __bf16)                               \
@@ -949,6 +964,8 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
                                       int nlev, int dt_b, int dt_l, int norm_qk, float scale,
                                       hipStream_t stream, int* unsupported) {
+  // the recompute writes the level states only, which do not depend on the
+  // hierarchy type (strong changes the reads), so it has no strong flag
   using namespace hattn;
   *unsupported = 0;
   GdnWs w;
@@ -964,7 +981,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
         V, L, norm_qk, scale, stream);                                                            \
     if (e != hipSuccess) return e;                                                                \
     return gdn_scan_launch_t<KD_, TL_, __bf16>(w, v, gcum, l, nullptr, nullptr, hsave, B, T, H, V, \
-                                               L, nlev, 0, stream);                               \
+                                               L, nlev, 0, 0, stream);                            \
   }
 #define HATTN_GDN_RC_D(KD_)                                                                      \
   if (K == KD_) {                                                                                \

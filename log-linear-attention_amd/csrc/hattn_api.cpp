@@ -52,13 +52,13 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
-                                float scale, hipStream_t stream, int* unsupported);
+                                float scale, int strong, hipStream_t stream, int* unsupported);
 size_t hattn_gdn_fwd_keep_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v,
                                      const void* beta, const float* g, const void* l, void* o,
                                      float* gcum, void* aw, void* au, float* ht, void* ws, int B,
                                      int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                     int dt_l, int dt_o, int norm_qk, float scale,
+                                     int dt_l, int dt_o, int norm_qk, float scale, int strong,
                                      hipStream_t stream, int* unsupported);
 void hattn_gdn_fwd_keep_buffers(const void* ws, int B, int T, int H, int K, int V, int nlev,
                                 const __bf16** qn, const __bf16** wn, const __bf16** kn,
@@ -70,15 +70,15 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
                                      float* dg, float* dl, const __bf16* qn, const __bf16* wn,
                                      const __bf16* kn, const __bf16* un, const __bf16* hs,
                                      void* ws, int B, int T, int H, int K, int V, int L, int nlev,
-                                     int dt_b, int dt_l, int norm_qk, float scale,
+                                     int dt_b, int dt_l, int norm_qk, float scale, int strong,
                                      hipStream_t stream, int* unsupported);
 size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, int norm_qk, float scale, hipStream_t stream,
-                                int* unsupported);
+                                int dt_l, int norm_qk, float scale, int strong,
+                                hipStream_t stream, int* unsupported);
 size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
                                    const void* l, const void* dO, void* dq, void* dk, void* dv,
@@ -503,8 +503,11 @@ static int gdn_fwd_impl(const void* q, const void* k, const void* v, const void*
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
-  if (htype != HATTN_HTYPE_WEAK)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  // HType.STRONG: the reference's strong chunkwise GDN path (strong intra-chunk
+  // levels, levels >= 1, every chunk reading every level; chunkwise_hgdn.py:630,
+  // 724-728, 782)
+  if (htype != HATTN_HTYPE_WEAK && htype != HATTN_HTYPE_STRONG)
+    return fail(HATTN_ERR_VALUE, "htype=%d", htype);
   if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
     return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
@@ -540,8 +543,8 @@ static int gdn_fwd_impl(const void* q, const void* k, const void* v, const void*
   hipError_t e =
       (keep ? hattn_gdn_fwd_keep_launch : hattn_gdn_fwd_launch)(
           q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, workspace, B, T, H, K, V, L, nlev,
-          dtype_beta, dtype_l, dtype_o, l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
-          &unsupported);
+          dtype_beta, dtype_l, dtype_o, l2norm_qk ? 1 : 0, qk_scale,
+          htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream, &unsupported);
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d o=%d", dtype_beta,
                 dtype_l, dtype_o);
@@ -593,13 +596,14 @@ static int gdn_bwd_impl(const void* q, const void* k, const void* v, const void*
                         int level_base, int htype, int chunk_size, int l2norm_qk,
                         float qk_scale, void* workspace, size_t workspace_bytes,
                         const void* fwd_ws, size_t fwd_ws_bytes, bool kept, void* stream) {
-  // chunkwise_hgdn.py:818-858
+  // chunkwise_hgdn.py:818-858; HType.STRONG: the gradient of the strong forward
+  // (level reads at every chunk for levels >= 1)
   if (chunk_size != 64)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "chunk_size=%d (only 64 is supported)", chunk_size);
   if (level_base != 2)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "level_base=%d (only 2 is supported)", level_base);
-  if (htype != HATTN_HTYPE_WEAK)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "only HType.WEAK is supported");
+  if (htype != HATTN_HTYPE_WEAK && htype != HATTN_HTYPE_STRONG)
+    return fail(HATTN_ERR_VALUE, "htype=%d", htype);
   if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || L <= 0)
     return fail(HATTN_ERR_VALUE, "non-positive dimension");
   if (T < 64 || T % 64 != 0) return fail(HATTN_ERR_VALUE, "T=%d and BT=64", T);
@@ -639,12 +643,14 @@ static int gdn_bwd_impl(const void* q, const void* k, const void* v, const void*
     hattn_gdn_fwd_keep_buffers(fwd_ws, B, T, H, K, V, nlev, &qn, &wn, &kn, &un, &hs);
     e = hattn_gdn_bwd_kept_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, qn, wn,
                                   kn, un, hs, workspace, B, T, H, K, V, L, nlev, dtype_beta,
-                                  dtype_l, l2norm_qk ? 1 : 0, qk_scale, (hipStream_t)stream,
+                                  dtype_l, l2norm_qk ? 1 : 0, qk_scale,
+                                  htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream,
                                   &unsupported);
   } else {
     e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, workspace,
                              B, T, H, K, V, L, nlev, dtype_beta, dtype_l, l2norm_qk ? 1 : 0,
-                             qk_scale, (hipStream_t)stream, &unsupported);
+                             qk_scale, htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream,
+                             &unsupported);
   }
   if (unsupported)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);

@@ -12,25 +12,6 @@ constexpr int kSC = 64;           // chunk
 constexpr int kSMaxLev = 10;      // chunk-level levels 0 .. 9 (T <= 64 * 2^9)
 constexpr int kSLocLev = 8;       // levels of the diagonal / sub-diagonal blocks (0 .. 7)
 
-// The strong level function for t > s (base.py:49-62 with base 2).
-constexpr int strong_level_ce(int t, int s) {
-  for (;;) {
-    int ell = 0;
-    while ((2 << ell) <= t) ++ell;          // floor(log2 t)
-    const int v = 1 << (ell > 0 ? ell - 1 : 0);
-    const int r = t - (1 << ell);
-    if (s < v) return ell + 1;
-    if (s < 2 * v && r >= v) return ell + 1;
-    if (s < 2 * v) {
-      t -= v;
-      s -= v;
-    } else {
-      t -= 2 * v;
-      s -= 2 * v;
-    }
-  }
-}
-
 struct alignas(16) StrongTables {
   unsigned char intra[kSC * kSC];   // [a][b], a >= b: level of (a, b) inside a chunk
   unsigned char sub[kSC * kSC];     // [a][b]: level of (64 + a, b)

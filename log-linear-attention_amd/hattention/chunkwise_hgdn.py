@@ -7,8 +7,17 @@ Same names, arguments and return tuples as hattention/chunkwise_hgdn.py:
   chunk_size) -> (dq, dk, dv, db, dg, dl)``            -- chunkwise_hgdn.py:791-1222
 
 Validation follows the reference (``ValueError`` for T % 64 and K / V not
-multiples of the block options, ``NotImplementedError`` for K > 256 and modes
-outside the weak base-2 hierarchy).  The backward kernels take K in {64, 128,
+multiples of the block options, ``NotImplementedError`` for K > 256 and level
+bases other than 2).  ``HType.STRONG`` runs what the reference's chunkwise path
+computes with the strong level table (chunkwise_hgdn.py:630, 724-728, 782):
+lambda of an intra-chunk pair at its strong level, the inter-chunk levels
+from 1 with the weak delta-rule states, and every chunk reading every level
+>= 1; ``ht`` holds those states (level 7 stays zero).  Its backward returns
+the gradient of that forward: the reference's own backward masks the level
+reads as the weak hierarchy does (skip_q on dO, chunkwise_hgdn.py:1034,
+1066-1067) and accumulates du on chunks whose u the forward masked
+(chunk_bwd_kernel_dv without the skip_kv exit, chunkwise.py:1008-1012), so it
+is not the derivative of its forward.  The backward kernels take K in {64, 128,
 192, 256} (``NotImplementedError`` from the C-ABI otherwise) and V in blocks of
 128.  Grouped q / k are expanded per head
 before the kernels like the reference (chunkwise_hgdn.py:614-623) and their
@@ -43,8 +52,10 @@ def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
         raise ValueError(f"H={H} is not a multiple of G={G}")
     if chunk_size != CHUNK:
         raise NotImplementedError(f"chunk_size={chunk_size} (only {CHUNK})")
-    if level_base != 2 or htype != HType.WEAK:
-        raise NotImplementedError("only the weak base-2 hierarchy is supported")
+    if level_base != 2:
+        raise NotImplementedError("only level base 2 is supported")
+    if htype not in (HType.WEAK, HType.STRONG):
+        raise ValueError(f"htype={htype}")
     if K > 256:
         raise NotImplementedError("current kernel does not support head dimension larger than 256.")
     if T % CHUNK != 0 or T < CHUNK:

@@ -39,13 +39,36 @@ Pinning (tests/test_oracle_gdn.py): recurrent == materialised == chunked (three
 structurally different algorithms); lambda == 1 equals the textbook gated delta
 rule; (I + A) Aw = I; beta = 0 gives o = 0; lambda one-hot on a level selects
 exactly that level's pairs; gradcheck of the chunked form.
+
+HType.STRONG: what the reference's chunkwise GDN path computes with the strong
+level table (chunkwise_hgdn.py:630, 724-728, 782), which is not the recurrent
+strong cascade (recurrent.py:56-74): the intra-chunk tile takes lambda at the
+strong level of the pair (make_levels_matrix with htype STRONG), the
+inter-chunk level loop starts at 1, every level keeps the weak delta-rule
+state (the same skip_kv / skip_g masks as HType.WEAK, chunk_delta_h.py:16-186),
+and every chunk reads every level >= 1 (chunk_fwd_kernel_o with USE_H2, which
+lifts the skip_q exit, chunkwise.py:521-527).  A level-e state read at chunk i
+holds the chunks j in [i & ~(2^(e+1) - 1), i) whose bit e is clear, so a pair
+of chunks can be counted at several levels and a chunk's immediate predecessor
+can be counted at none (with four chunks, chunk 2 for chunk 3: bit 1 of 2
+is set and level 0 is skipped).
+* ``chunked_fwd(..., htype=STRONG)`` restates that chunk loop;
+* ``strong_chunkwise_weights`` / ``materialized_fwd(..., weights=...)`` give the
+  same function as a pair sum whose weight is built from the chunk indices
+  directly (and the intra-chunk levels from the T x T strong table of
+  oracle.levels, so the chunk translation invariance of the table is checked
+  too).  The two agree to 1e-12 in float64; autograd through the chunked form
+  is pinned by gradcheck.
 """
 import math
 from typing import Optional
 
 import torch
 
-from oracle.levels import get_num_levels, levels_matrix
+from oracle.levels import (get_num_levels, levels_matrix, levels_matrix_strong,
+                           strong_intra_table)
+
+WEAK, STRONG = 0, 1   # HType values (hattention/base.py:12-14)
 
 
 def _check(q, k, v, beta, g, l):
@@ -92,8 +115,11 @@ def recurrent_fwd(q, k, v, beta, g, l, return_state: bool = False):
 # --------------------------------------------------------------------------
 # 2. materialised pair sum (tiny T)
 # --------------------------------------------------------------------------
-def materialized_fwd(q, k, v, beta, g, l):
-    """o_t = sum_{s<=t} lambda[t, lev(t,s)] q_t^T (G_t ... G_{s+1}) beta_s k_s v_s^T."""
+def materialized_fwd(q, k, v, beta, g, l, weights=None):
+    """o_t = sum_{s<=t} lambda[t, lev(t,s)] q_t^T (G_t ... G_{s+1}) beta_s k_s v_s^T.
+
+    ``weights`` [B, T, H, T] replaces lambda[t, lev(t, s)] by an explicit pair
+    weight w[b, t, h, s] (used for the strong chunkwise form)."""
     B, T, H, K, V, L = _check(q, k, v, beta, g, l)
     lev = torch.from_numpy(levels_matrix(T, default=0, clamp_min=0))
     I = torch.eye(K, dtype=q.dtype)
@@ -105,9 +131,40 @@ def materialized_fwd(q, k, v, beta, g, l):
         for t in range(s, T):
             if t > s:
                 x = torch.einsum("bhmn,bhn->bhm", G[:, t], x)
-            w = l[:, t, :, lev[t, s]] * (q[:, t] * x).sum(-1)                 # [B,H]
+            lw = l[:, t, :, lev[t, s]] if weights is None else weights[:, t, :, s]
+            w = lw * (q[:, t] * x).sum(-1)                                    # [B,H]
             o[:, t] = o[:, t] + w[..., None] * v[:, s]
     return o
+
+
+def strong_chunkwise_weights(l, chunk_size: int = 64):
+    """Pair weights [B, T, H, T] of the reference's chunkwise GDN path with
+    HType.STRONG (chunkwise_hgdn.py:630, 724-783), from the chunk indices:
+
+    * s in t's chunk: lambda[t, strong(t, s)], the strong level from the T x T
+      table (make_levels_matrix with htype STRONG, diagonal blocks only);
+    * s in an earlier chunk j of t's chunk i: the sum of lambda[t, h0 + e] over
+      the levels e in 1 .. nlev - 1 whose state at chunk i holds chunk j, i.e.
+      j >= i & ~(2^(e+1) - 1) and bit e of j clear (weak state, read at every
+      chunk); h0 = log2(chunk) + 1."""
+    B, T, H, L = l.shape
+    C = chunk_size
+    NT = T // C
+    h0 = get_num_levels(C, 2)
+    nlev = math.ceil(math.log2(NT)) if NT > 1 else 0
+    lev = torch.from_numpy(levels_matrix_strong(T, default=0, clamp_min=0))
+    w = torch.zeros(B, T, H, T, dtype=l.dtype)
+    for t in range(T):
+        i = t // C
+        for s in range(t + 1):
+            j = s // C
+            if j == i:
+                w[:, t, :, s] = l[:, t, :, lev[t, s]]
+                continue
+            for e in range(1, nlev):
+                if j >= (i & ~((2 << e) - 1)) and not (j >> e) & 1:
+                    w[:, t, :, s] = w[:, t, :, s] + l[:, t, :, h0 + e]
+    return w
 
 
 # --------------------------------------------------------------------------
@@ -160,8 +217,13 @@ def ut_transform(kc, bc, Gc):
     return A, Aw, Au, W
 
 
-def chunked_fwd(q, k, v, beta, g, l, chunk_size: int = 64, output_final_state: bool = False):
-    """chunkwise_hgdn.chunkwise_fwd (chunkwise_hgdn.py:566-788): (g_cumsum, o, Aw, Au, ht)."""
+def chunked_fwd(q, k, v, beta, g, l, chunk_size: int = 64, output_final_state: bool = False,
+                htype: int = WEAK):
+    """chunkwise_hgdn.chunkwise_fwd (chunkwise_hgdn.py:566-788): (g_cumsum, o, Aw, Au, ht).
+
+    htype STRONG: the strong intra-chunk levels, the level loop from 1 and every
+    chunk reading every level (chunkwise_hgdn.py:630, 724-728, 782; see the
+    module docstring); the states are the weak ones."""
     B, T, H, K, V, L = _check(q, k, v, beta, g, l)
     C = chunk_size
     if T % C:
@@ -179,7 +241,10 @@ def chunked_fwd(q, k, v, beta, g, l, chunk_size: int = 64, output_final_state: b
     U = Au @ (bc[..., None] * vc)
     gamma = _segsum_exp(Gc)
     # intra-chunk (chunk_fwd_kernel_o_intra, chunkwise_hgdn.py:41-126)
-    lev = torch.from_numpy(levels_matrix(C, default=0, clamp_min=0))
+    if htype == STRONG:
+        lev = torch.from_numpy(strong_intra_table(C))
+    else:
+        lev = torch.from_numpy(levels_matrix(C, default=0, clamp_min=0))
     tt = torch.arange(C)[:, None].expand(C, C)
     lam = lc[..., tt, lev]                                           # [B,H,NT,t,s]
     Cm = torch.tril(qc @ kc.transpose(-1, -2)) @ Aw                  # tril(QK^T) Aw
@@ -191,11 +256,13 @@ def chunked_fwd(q, k, v, beta, g, l, chunk_size: int = 64, output_final_state: b
     Qnew = eG[..., None] * (qc - torch.tril(qc @ kc.transpose(-1, -2)) @ W)
     glast = torch.exp(Gc[..., -1])                                   # [B,H,NT]
     ht = torch.zeros(B, H, K, V, L, dtype=q.dtype) if output_final_state else None
-    for ell in range(nlev):
+    # STRONG starts at level 1 (chunkwise_hgdn.py:724-728)
+    for ell in range(1 if htype == STRONG else 0, nlev):
         S = torch.zeros(B, H, K, V, dtype=q.dtype)
         period = 1 << (ell + 1)
         for i in range(NT):
-            if (i >> ell) & 1:                                       # reading chunk
+            # reading chunk; STRONG reads every chunk (USE_H2, chunkwise.py:521-527)
+            if htype == STRONG or (i >> ell) & 1:
                 o[:, :, i] = o[:, :, i] + lc[:, :, i, :, h0 + ell, None] * (Qnew[:, :, i] @ S)
             reset = (i % period == period - 1)
             if output_final_state and i == NT - 1:

@@ -212,7 +212,8 @@ def _gdn_bwd(**kw):
     (dict(K=256, V=64), _lib.HATTN_ERR_VALUE),      # K = 256 valid: fails on the null pointers
     (dict(K=64, V=192), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # V blocks of 64 / 128
     (dict(chunk=32), _lib.HATTN_ERR_NOT_IMPLEMENTED),
-    (dict(htype=1), _lib.HATTN_ERR_NOT_IMPLEMENTED),
+    (dict(htype=1), _lib.HATTN_ERR_VALUE),          # STRONG valid: fails on the null pointers
+    (dict(htype=2), _lib.HATTN_ERR_VALUE),          # neither WEAK nor STRONG
     (dict(do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # do must be bf16
     (dict(T=64 << 9, L=17), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > 8 inter-chunk levels
     (dict(ws=16), _lib.HATTN_ERR_VALUE),            # workspace too small

@@ -134,3 +134,51 @@ def test_scale_cancels_in_gdn_api():
     o1 = D.hattention_gdn_fwd(q, k, v, beta, g, l / scale, scale=scale, chunk_size=4)
     o2 = D.chunked_fwd(D.l2norm(q), D.l2norm(k), v, beta, g, l, chunk_size=4)[1]
     assert rel(o1, o2) < 1e-12
+
+
+# --------------------------------------------------------------------------
+# HType.STRONG: the reference's chunkwise GDN path with the strong level table
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("T,C", [(64, 8), (96, 8), (128, 16), (64, 16)])
+def test_strong_chunked_equals_pair_sum(T, C):
+    """The strong chunk loop (level loop from 1, every chunk reading every level,
+    strong intra-chunk levels) == the pair sum whose weights come from the chunk
+    indices and the T x T strong table."""
+    NT = T // C
+    L = int(math.log2(C)) + 1 + math.ceil(math.log2(NT)) + 1
+    q, k, v, beta, g, l = make(2, T, 2, 5, 3, L, seed=T + C)
+    o_chk = D.chunked_fwd(q, k, v, beta, g, l, chunk_size=C, htype=D.STRONG)[1]
+    o_mat = D.materialized_fwd(q, k, v, beta, g, l, weights=D.strong_chunkwise_weights(l, C))
+    assert rel(o_chk, o_mat) < 1e-12
+
+
+def test_strong_chunk_weights_by_hand():
+    """Known weights of the strong chunkwise path, read off the reference's masks
+    by hand for four chunks of 4 tokens (h0 = 3, nlev = 2: level 1 only): chunk
+    1 sees chunk 0 at level 1, chunks 2 and 3 see chunks 0 and 1 at level 1,
+    chunk 3 does not see chunk 2 (bit 1 of 2 is set, level 0 is skipped)."""
+    T, C = 16, 4
+    l = torch.arange(1, 1 + T * 6, dtype=torch.float64).reshape(1, T, 1, 6)
+    w = D.strong_chunkwise_weights(l, C)
+    for t in range(T):
+        i = t // C
+        for s in range(t + 1):
+            j = s // C
+            if j == i:
+                continue
+            want = l[0, t, 0, 4].item() if (i, j) in {(1, 0), (2, 0), (2, 1), (3, 0), (3, 1)} else 0.0
+            assert w[0, t, 0, s].item() == want, (t, s)
+
+
+def test_strong_differs_from_weak():
+    q, k, v, beta, g, l = make(1, 64, 1, 4, 3, 7, seed=5)
+    o_w = D.chunked_fwd(q, k, v, beta, g, l, chunk_size=8)[1]
+    o_s = D.chunked_fwd(q, k, v, beta, g, l, chunk_size=8, htype=D.STRONG)[1]
+    assert rel(o_s, o_w) > 1e-3
+
+
+def test_gradcheck_chunked_strong():
+    q, k, v, beta, g, l = make(1, 16, 1, 3, 2, 6, seed=19)
+    args = [x.clone().requires_grad_(True) for x in (q, k, v, beta, g, l)]
+    fn = lambda *a: D.chunked_fwd(*a, chunk_size=2, htype=D.STRONG)[1]
+    assert torch.autograd.gradcheck(fn, args, eps=1e-6, atol=1e-7)

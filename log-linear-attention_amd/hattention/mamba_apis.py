@@ -1,8 +1,10 @@
 """Mamba-2 style API of the log-linear Mamba-2 chunkwise path (MI355X).
 
 Mirrors hattention/mamba_apis.py:
+* ``LambdaLevelMLP``             -- :32-67  (non-fixed lambda: per-level rotary
+  embedding of L and dl, then one linear map each)
 * ``compute_lambda``             -- :70-85  (lambda modes positive / bounded / None)
-* ``compute_lambda_maybe_fixed`` -- :88-113 (fixed per-level lambdas only)
+* ``compute_lambda_maybe_fixed`` -- :88-113
 * ``hmamba_chunk_scan_combined`` -- :263-404 (dt / A / lambda pre-processing,
   then ``hattention_kernel`` with q=C, k=B, v=x*dt, g=A*dt, plus the D residual;
   with ``return_final_states`` the prefill ``hattention_prefill`` and its HState)
@@ -37,16 +39,92 @@ def compute_lambda(L: torch.Tensor, dl: torch.Tensor, lambda_mode: Optional[str]
     raise ValueError
 
 
+class RotaryPositionalEmbeddings(torch.nn.Module):
+    """The rotary position embedding the reference imports from torchtune
+    (``torchtune.modules.RotaryPositionalEmbeddings``, mamba_apis.py:27-30; not
+    installed here, version unpinned by the reference's requirements.txt):
+    RoFormer's rotation (Su et al. 2021) with torchtune's conventions.  The
+    feature pairs (2i, 2i + 1) of the last dim are rotated by the angle
+    pos * theta_i, theta_i = base^(-2i / dim) (base 10000), computed in fp32
+    (angle = float(pos) * theta_i, one rounding, as torchtune's cache); the
+    result takes x's dtype.  x is [b, s, n_h, dim]; input_pos [s] (or None
+    for 0 .. s - 1).  No parameters and no persistent buffers, like
+    torchtune's module, so a state dict carries nothing for it."""
+
+    def __init__(self, dim: int, max_seq_len: int = 4096, base: int = 10_000) -> None:
+        super().__init__()
+        if dim % 2:
+            raise ValueError("dim must be even")
+        self.dim = dim
+        self.max_seq_len = max_seq_len
+        self.base = base
+        theta = 1.0 / (base ** (torch.arange(0, dim, 2)[: dim // 2].float() / dim))
+        self.register_buffer("theta", theta, persistent=False)
+
+    def forward(self, x: torch.Tensor, *, input_pos: Optional[torch.Tensor] = None) -> torch.Tensor:
+        s = x.shape[1]
+        pos = torch.arange(s, device=x.device) if input_pos is None else input_pos
+        if pos.numel() and int(pos.max()) >= self.max_seq_len:
+            raise IndexError("position beyond max_seq_len")
+        ang = pos.to(device=x.device, dtype=torch.float32)[:, None] * self.theta.to(x.device)
+        c = torch.cos(ang)[None, :, None, :]          # [1, s, 1, dim / 2]
+        sn = torch.sin(ang)[None, :, None, :]
+        xf = x.float().unflatten(-1, (-1, 2))
+        x0, x1 = xf[..., 0], xf[..., 1]
+        out = torch.stack((x0 * c - x1 * sn, x1 * c + x0 * sn), dim=-1).flatten(-2)
+        return out.type_as(x)
+
+
+class LambdaLevelMLP(torch.nn.Module):
+    """mamba_apis.py:32-67: per-level lambda inputs from a ``dim``-wide L and
+    dl.  For level index i, x is rotated by the rotary embedding at position i
+    and mapped to one value by a linear layer (mlp0 for L, mlp1 for dl):
+    returns (y0, y1), each [..., num_levels].  Same submodules and parameter
+    names as the reference (mlp0, mlp1, rope), so its state dicts load."""
+
+    def __init__(self, dim: int, max_num_levels: int, **kwargs) -> None:
+        super().__init__()
+        self.dim = dim
+        self.max_num_levels = max_num_levels
+        self.mlp0 = torch.nn.Linear(in_features=dim, out_features=1)
+        self.mlp1 = torch.nn.Linear(in_features=dim, out_features=1)
+        self.rope = RotaryPositionalEmbeddings(dim=dim, max_seq_len=max_num_levels)
+
+    def forward(self, x0: torch.Tensor, x1: torch.Tensor,
+                num_levels: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        if x0.ndim != 4 or x1.ndim != 4:
+            raise ValueError
+        if num_levels > self.max_num_levels:
+            raise ValueError
+        y0s, y1s = [], []
+        for i in range(num_levels):
+            p0 = torch.full((x0.shape[1],), i, dtype=torch.int32, device=x0.device)
+            p1 = torch.full((x1.shape[1],), i, dtype=torch.int32, device=x1.device)
+            y0s.append(self.mlp0(self.rope(x0, input_pos=p0)))
+            y1s.append(self.mlp1(self.rope(x1, input_pos=p1)))
+        return torch.cat(y0s, dim=-1), torch.cat(y1s, dim=-1)
+
+
 def compute_lambda_maybe_fixed(L, dl, lambda_mode, lambda_level_max, lambda_level_fixed,
                                lambda_level_module=None) -> torch.Tensor:
-    """mamba_apis.py:88-113 (the LambdaLevelMLP branch needs torchtune's RoPE and
-    is not part of this build)."""
+    """mamba_apis.py:88-113."""
     if lambda_level_fixed:
         if not all([L.ndim in [3, 4], dl.ndim in [3, 4], L.shape[-1] == lambda_level_max,
                     dl.shape[-1] == lambda_level_max]):
             raise ValueError
         return compute_lambda(L=L, dl=dl, lambda_mode=lambda_mode)
-    raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+    L_new, dl_new = _level_inputs(L, dl, lambda_level_max, lambda_level_module)
+    return compute_lambda(L=L_new, dl=dl_new, lambda_mode=lambda_mode)
+
+
+def _level_inputs(L, dl, lambda_level_max, lambda_level_module):
+    """The non-fixed branch of mamba_apis.py:104-112: (L, dl) of width
+    ``lambda_level_module.dim`` -> per-level (L_new, dl_new) of width
+    ``lambda_level_max`` through the LambdaLevelMLP (torch ops, autograd)."""
+    if not all([L.ndim in [3, 4], dl.ndim in [3, 4], L.shape[-1] == lambda_level_module.dim,
+                dl.shape[-1] == lambda_level_module.dim]):
+        raise ValueError
+    return lambda_level_module(L, dl, num_levels=lambda_level_max)
 
 
 def hmamba_split_conv1d_scan_combined(
@@ -196,7 +274,10 @@ def hmamba_chunk_scan_combined(
         raise ValueError
     # compute_lambda_maybe_fixed's checks (mamba_apis.py:96-102) on L [1, 1, H, Lv]
     if not lambda_level_fixed:
-        raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+        # mamba_apis.py:104-112: the LambdaLevelMLP maps L [H, dim] and dl [B, T, H,
+        # dim] to per-level inputs; the fused scan then runs as for fixed levels
+        L4, dl = _level_inputs(L[None, None], dl, lambda_level_max, lambda_level_module)
+        L = L4[0, 0]
     if not all([L.dim() + 2 in (3, 4), dl.dim() in (3, 4), L.shape[-1] == lambda_level_max,
                 dl.shape[-1] == lambda_level_max]):
         raise ValueError
@@ -284,7 +365,11 @@ def hselective_state_update(
             raise ValueError
 
     if not lambda_level_fixed:
-        raise NotImplementedError("non-fixed lambda (LambdaLevelMLP) is not supported")
+        # mamba_apis.py:530-536 hands the LambdaLevelMLP 3-D [1, H, dim] / [B, H, dim]
+        # inputs, which its forward rejects (:42-43): the reference's decode step
+        # raises ValueError with non-fixed lambda, and so does this one
+        L4, dl = _level_inputs(L[None], dl, lambda_level_max, lambda_level_module)
+        L = L4[0]
     if not all([L.dim() + 1 in (3, 4), dl.dim() in (3, 4), L.shape[-1] == lambda_level_max,
                 dl.shape[-1] == lambda_level_max]):
         raise ValueError

@@ -380,3 +380,45 @@ def test_causal_conv1d_silu_matches_oracle(dtype, W, S):
     # columns outside the conv window get no gradient from this op
     assert torch.count_nonzero(dz.grad[..., :col0]) == 0
     assert torch.count_nonzero(dz.grad[..., col0 + Dc:]) == 0
+
+
+@pytest.mark.parametrize("mode", ["positive", "bounded"])
+def test_layer_non_fixed_lambda(mode):
+    """lambda_level_fixed=False (mamba_apis.py:104-112): the LambdaLevelMLP maps L
+    [H, 16] and dl [B, T, H, 16] to per-level inputs, then the fused scan runs.
+    Output and the MLP's parameter gradients equal, bit for bit, the fixed-level
+    call on the MLP's outputs; the output matches the fp64 oracle layer on them."""
+    from hattention.base import HType, HStruct
+    from hattention.mamba_apis import LambdaLevelMLP, hmamba_chunk_scan_combined
+    B, T, H, P, N, Lv, Dl = 2, 1024, 4, 64, 64, 11, 16
+    torch.manual_seed(5)
+    mlp = LambdaLevelMLP(dim=Dl, max_num_levels=15).to(DEV)
+    x, dt, A, Bm, Cm, _, _, D, bias = _inputs(B, T, H, 1, P, N, Lv, 81, torch.bfloat16)
+    gen = torch.Generator("cpu").manual_seed(82)
+    dl = torch.randn(B, T, H, Dl, generator=gen)
+    L = torch.randn(H, Dl, generator=gen) * 0.5
+    args = [t.to(DEV) for t in (x, dt, A, Bm, Cm)]
+    kw = dict(lambda_mode=mode, lambda_level_max=Lv, lambda_level_base=2,
+              lambda_htype=HType.WEAK, lambda_hstruct=HStruct.MAMBA2)
+    dy = torch.randn(B, T, H, P, generator=gen).to(DEV)
+    print(f"[layer non-fixed lambda] mode={mode}", flush=True)
+    y, _ = hmamba_chunk_scan_combined(*args, dl.to(DEV), L.to(DEV), 64, D=D.to(DEV),
+                                      dt_bias=bias.to(DEV), dt_softplus=True,
+                                      lambda_level_fixed=False, lambda_level_module=mlp, **kw)
+    (y.float() * dy).sum().backward()
+    g1 = [p.grad.clone() for p in mlp.parameters()]
+    mlp.zero_grad()
+    L4, dl2 = mlp(L.to(DEV)[None, None], dl.to(DEV), num_levels=Lv)
+    y2, _ = hmamba_chunk_scan_combined(*args, dl2, L4[0, 0], 64, D=D.to(DEV),
+                                       dt_bias=bias.to(DEV), dt_softplus=True,
+                                       lambda_level_fixed=True, **kw)
+    (y2.float() * dy).sum().backward()
+    assert torch.equal(y, y2)
+    for a, b in zip(g1, (p.grad for p in mlp.parameters())):
+        assert torch.equal(a, b)
+    ref = M.layer_fwd(x.double(), dt.double(), A.double(), Bm.double(), Cm.double(),
+                      dl2.detach().double().cpu(), L4[0, 0].detach().double().cpu(), D.double(),
+                      bias.double(), lambda_mode=mode)
+    mx, fro = _errs(y, ref)
+    print(f"  y max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+    assert mx < 2e-2 and fro < 1e-2

@@ -546,6 +546,8 @@ ONLY_CASES = {
         "north star fwd+bwd", NS_SHAPE, torch.bfloat16, dev, st, ev, n, w, backward=True),
     "c2_fwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
         "C2", (1, 32768, 32, 64, 128, 16), torch.bfloat16, dev, st, ev, n, w),
+    "c2_x3_fwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
+        "C2 bf16x3", (1, 32768, 32, 64, 128, 16), torch.float32, dev, st, ev, n, w),
     "c4_fwd_bwd": lambda dev, st, ev, n, w: mamba2_fwd_record(
         "C4 fwd+bwd", (8, 8192, 24, 64, 64, 14), torch.bfloat16, dev, st, ev, n, w,
         backward=True),

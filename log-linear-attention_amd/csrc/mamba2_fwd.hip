@@ -344,24 +344,23 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_fwd_main_kernel(
             qa[mt][c][pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           }
       const float* lamt = s.lam + 4 * lq;
-      // local levels without branches (a level the chunk does not read gets a
-      // zero B operand), so the MFMA chains of all levels interleave
+      // only the local levels the chunk reads (bit e of the chunk index; a
+      // uniform branch): with three MFMAs per product the skipped half of the
+      // level products is the larger cost, not the lost interleaving
 #pragma unroll
       for (int e = 0; e < MAXLOC; ++e) {
-        const bool rd = any_loc && e < nloc && ((ic >> e) & 1);
-        const float z = rd ? 1.f : 0.f;
-        bf16x8 b0[NP], b1[NP];
-        cat8s<NP>(st[e][0] * z, st[e][1] * z, b0);
-        cat8s<NP>(st[e][2] * z, st[e][3] * z, b1);
+        if (any_loc && e < nloc && ((ic >> e) & 1)) {
+          bf16x8 b0[NP], b1[NP];
+          cat8s<NP>(st[e][0], st[e][1], b0);
+          cat8s<NP>(st[e][2], st[e][3], b1);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          floatx4 tmp = mma<NP>(qa[mt][0], b0, zero4());
-          tmp = mma<NP>(qa[mt][1], b1, tmp);
-          // a level past nloc has no staged lambda column (stale LDS, possibly
-          // NaN bits): select, never multiply, its weight away
-          const floatx4 lam = *(const floatx4*)(lamt + (7 + e) * kBT + 16 * mt);
+          for (int mt = 0; mt < 4; ++mt) {
+            floatx4 tmp = mma<NP>(qa[mt][0], b0, zero4());
+            tmp = mma<NP>(qa[mt][1], b1, tmp);
+            const floatx4 lam = *(const floatx4*)(lamt + (7 + e) * kBT + 16 * mt);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * (rd ? lam[i] : 0.f);
+            for (int i = 0; i < 4; ++i) acc[mt][i] += tmp[i] * lam[i];
+          }
         }
       }
       if (any_top) {
@@ -1619,7 +1618,8 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
                        gcum, ht, w.sums, w.segd, w.sync, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
                        ht != nullptr ? 1 : 0, LayerArgs{}, lookback_ctl());
     return hipGetLastError();
-  }
+  } else {
+  // bf16x3 (NP = 2): segment summaries, staged top-level states, then the walk
   if (NSEG > 1) {
     auto sk = mamba2_seg_sum_kernel<TK, TV, false, NP>;
     hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), 0, stream,
@@ -1645,6 +1645,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
                      (const __bf16*)w.htop, B, T, G, H, V, L, nlev, nvb64, slog, NSEG,
                      ht != nullptr ? 1 : 0);
   return hipGetLastError();
+  }
 }
 
 // The layer scan of hmamba_chunk_scan_combined with its pre- and

@@ -74,8 +74,10 @@ const char* hattn_last_error(void);
  *   htype not HATTN_HTYPE_WEAK / HATTN_HTYPE_STRONG  -> HATTN_ERR_VALUE
  *   chunk_size == 64, level_base == 2, K == 64 (the Python host layer runs a
  *   larger K as one call per 64-wide block of q and k and sums the outputs),
- *   dtype_qk BF16 (bf16 MFMA) or FP32 (bf16x3, fp32-accurate), dtype_v /
- *   dtype_l / dtype_o in {BF16, FP32}                -> HATTN_ERR_NOT_IMPLEMENTED
+ *   dtype_qk BF16 (bf16 MFMA; dtype_v / dtype_l / dtype_o in {BF16, FP32}),
+ *   FP16 (fp16 MFMA, HType.WEAK: dtype_v / dtype_o in {FP16, FP32}, dtype_l
+ *   FP32) or FP32 (bf16x3, fp32-accurate; v, l, o FP32)
+ *                                                    -> HATTN_ERR_NOT_IMPLEMENTED
  * htype HATTN_HTYPE_STRONG (the reference's USE_A2 / USE_H2 forward,
  * chunkwise.py:1118-1275 with the strong level function, base.py:49-62): BF16
  * q, k, v, L <= 32, T <= 64 * 2^9; else HATTN_ERR_NOT_IMPLEMENTED.  Its ht

@@ -147,6 +147,57 @@ __device__ __forceinline__ bf16x8 cat8(floatx4 a, floatx4 b) {
                 (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
 }
 
+// 16-bit MFMA operand formats.  The kernels move q, k, v, A and states as
+// 16-bit patterns held in bf16x8 / bf16x4 registers and LDS tiles whatever
+// their format; E (__bf16 or _Float16) selects the conversions to and from
+// fp32 and the MFMA opcode (v_mfma_f32_16x16x32_bf16 / _f16), so fp16 inputs
+// multiply natively, as the reference's fp16 dots do.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <typename E>
+__device__ __forceinline__ floatx4 mfma16(bf16x8 a, bf16x8 b, floatx4 c) {
+  if constexpr (sizeof(E) == 2 && __is_same(E, _Float16))
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return mfma16x16x32(a, b, c);
+}
+
+// fp32 -> format E, as a 16-bit pattern in a __bf16 slot
+template <typename E>
+__device__ __forceinline__ __bf16 to16(float x) {
+  if constexpr (__is_same(E, _Float16))
+    return __builtin_bit_cast(__bf16, (_Float16)x);
+  else
+    return (__bf16)x;
+}
+
+// a 16-bit pattern of format E -> fp32
+template <typename E>
+__device__ __forceinline__ float from16(__bf16 x) {
+  if constexpr (__is_same(E, _Float16))
+    return (float)__builtin_bit_cast(_Float16, x);
+  else
+    return (float)x;
+}
+
+template <typename E>
+__device__ __forceinline__ bf16x4 cvt4e(floatx4 x) {
+  if constexpr (__is_same(E, _Float16))
+    return bf16x4{to16<E>(x[0]), to16<E>(x[1]), to16<E>(x[2]), to16<E>(x[3])};
+  else
+    return cvt4(x);
+}
+
+template <typename E>
+__device__ __forceinline__ bf16x8 cat8e(floatx4 a, floatx4 b) {
+  if constexpr (__is_same(E, _Float16))
+    return bf16x8{to16<E>(a[0]), to16<E>(a[1]), to16<E>(a[2]), to16<E>(a[3]),
+                  to16<E>(b[0]), to16<E>(b[1]), to16<E>(b[2]), to16<E>(b[3])};
+  else
+    return cat8(a, b);
+}
+
 }  // namespace hattn
 
 namespace hattn {
@@ -183,6 +234,9 @@ template <> __device__ __forceinline__ void buf_store<float>(float x, rsrc_t r, 
 template <> __device__ __forceinline__ void buf_store<__bf16>(__bf16 x, rsrc_t r, unsigned int voff, unsigned int soff) {
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, x), r, voff, soff, 0);
 }
+template <> __device__ __forceinline__ void buf_store<_Float16>(_Float16 x, rsrc_t r, unsigned int voff, unsigned int soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, x), r, voff, soff, 0);
+}
 
 }  // namespace hattn
 
@@ -207,7 +261,7 @@ __device__ __forceinline__ void buf_store16(uint4 x, rsrc_t r, unsigned int voff
 template <typename T>
 __device__ __forceinline__ void buf_store4(floatx4 x, rsrc_t r, unsigned int voff, unsigned int soff) {
   if constexpr (sizeof(T) == 2) {
-    const bf16x4 b = cvt4(x);
+    const bf16x4 b = cvt4e<T>(x);
     buf_store8(__builtin_bit_cast(uint2, b), r, voff, soff);
   } else {
     buf_store16(__builtin_bit_cast(uint4, x), r, voff, soff);
@@ -303,21 +357,22 @@ __device__ __forceinline__ __bf16 bf16_lo(float x, __bf16 hi) { return (__bf16)(
 
 // Product of fragment planes: NP = 1 (plain bf16) or 2 (hi, lo); the small
 // terms are accumulated first.
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ floatx4 mma(const bf16x8* a, const bf16x8* b, floatx4 c) {
+  static_assert(NP == 1 || __is_same(E, __bf16), "bf16x3 splits into bf16 planes");
   if constexpr (NP == 2) {
     c = mfma16x16x32(a[1], b[0], c);
     c = mfma16x16x32(a[0], b[1], c);
   }
-  return mfma16x16x32(a[0], b[0], c);
+  return mfma16<E>(a[0], b[0], c);
 }
 
 // fp32 fragment (8 values) -> hi / lo planes.
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ void split8(const float* x, bf16x8* out) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const __bf16 h = (__bf16)x[j];
+    const __bf16 h = to16<E>(x[j]);
     out[0][j] = h;
     if constexpr (NP == 2) out[1][j] = bf16_lo(x[j], h);
   }

@@ -263,10 +263,13 @@ static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const fl
       e = hattn_mamba2_strong_ht_launch(k, v, g, ht, B, T, G, H, V, L, (hipStream_t)stream);
     return check_hip(e, "hattn_mamba2_chunkwise_fwd (strong) launch");
   }
-  if (dtype_qk != HATTN_BF16 && dtype_qk != HATTN_FP32)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16 or fp32 required)", dtype_qk);
-  // fp32 q / k select the bf16x3 kernels (fp32-accurate products)
+  if (dtype_qk != HATTN_BF16 && dtype_qk != HATTN_FP16 && dtype_qk != HATTN_FP32)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k dtype code %d (bf16, fp16 or fp32 required)",
+                dtype_qk);
+  // fp32 q / k select the bf16x3 kernels (fp32-accurate products); fp16 q / k the
+  // fused kernel on fp16 MFMA (fp16 or fp32 v and o, fp32 lambda)
   const int x3 = dtype_qk == HATTN_FP32;
+  const int h16 = dtype_qk == HATTN_FP16;
   if (nlev > hattn_mamba2_fwd_max_levels(x3))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d%s", T,
                 hattn_mamba2_fwd_max_levels(x3), x3 ? " in fp32" : "");
@@ -274,9 +277,14 @@ static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const fl
   const bool bf_or_f32 = (dtype_v == HATTN_BF16 || dtype_v == HATTN_FP32) &&
                          (dtype_l == HATTN_BF16 || dtype_l == HATTN_FP32) &&
                          (dtype_o == HATTN_BF16 || dtype_o == HATTN_FP32);
-  if (x3 ? !(dtype_v == HATTN_FP32 && dtype_l == HATTN_FP32 && dtype_o == HATTN_FP32) : !bf_or_f32)
+  const bool h_or_f32 = (dtype_v == HATTN_FP16 || dtype_v == HATTN_FP32) &&
+                        dtype_l == HATTN_FP32 && (dtype_o == HATTN_FP16 || dtype_o == HATTN_FP32);
+  if (x3 ? !(dtype_v == HATTN_FP32 && dtype_l == HATTN_FP32 && dtype_o == HATTN_FP32)
+         : h16 ? !h_or_f32 : !bf_or_f32)
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k=%d v=%d l=%d o=%d%s", dtype_qk,
-                dtype_v, dtype_l, dtype_o, x3 ? " (fp32 q/k need fp32 v, lambda and o)" : "");
+                dtype_v, dtype_l, dtype_o,
+                x3 ? " (fp32 q/k need fp32 v, lambda and o)"
+                   : h16 ? " (fp16 q/k need fp16 or fp32 v and o, fp32 lambda)" : "");
   if (int st = check_span(T, max_of({(size_t)G * K * elem_bytes(dtype_qk),
                                       (size_t)H * V * elem_bytes(dtype_v),
                                       (size_t)H * V * elem_bytes(dtype_o),

@@ -54,7 +54,7 @@ __device__ __forceinline__ void load_tile64(Tile64<T>& t, rsrc_t rs, unsigned in
 }
 
 // Store a staged tile as NP bf16 planes (plane 1: the bf16x3 low part of fp32 data).
-template <int NP, typename T>
+template <int NP, typename T, typename E = __bf16>
 __device__ __forceinline__ void store_tile64(const Tile64<T>& t, __bf16* p0, __bf16* p1) {
   const int tid = threadIdx.x;
 #pragma unroll
@@ -68,8 +68,8 @@ __device__ __forceinline__ void store_tile64(const Tile64<T>& t, __bf16* p0, __b
       bf16x4 hi, lo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        hi[j] = (__bf16)e[j];
-        lo[j] = bf16_lo(e[j], hi[j]);
+        hi[j] = to16<E>(e[j]);
+        if constexpr (NP == 2) lo[j] = bf16_lo(e[j], hi[j]);
       }
       *(bf16x4*)(p0 + off) = hi;
       if constexpr (NP == 2) *(bf16x4*)(p1 + off) = lo;
@@ -113,7 +113,9 @@ constexpr int kCohStore = 16;  // sc1
 // layer_math.h); bf16 x only.  NSLOT: chunks held in registers ahead of the
 // one being multiplied (the loads in flight per workgroup).  Element (k, v) of
 // the summary goes to out[(k V + v) ostride], multiplied by oscale.
-template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false, int NSLOT = 2>
+// E: the 16-bit MFMA format of K and V (bf16, or fp16 for fp16 inputs; NP = 1).
+template <typename TK, typename TV, bool GCUM, int NP, bool COH, bool LAYER = false, int NSLOT = 2,
+          typename E = __bf16>
 __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restrict__ k,
                                               const TV* __restrict__ v,
                                               const float* __restrict__ g, float* __restrict__ out,
@@ -184,7 +186,7 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
 #pragma unroll
     for (int s = 0; s < NSLOT; ++s)
       if (s == slot) {
-        store_tile64<NP>(kr[s], sm.k[buf][0], sm.k[buf][NP - 1]);
+        store_tile64<NP, TK, E>(kr[s], sm.k[buf][0], sm.k[buf][NP - 1]);
         if constexpr (LAYER) {
           // v = x dt' on the thread's two rows (tid >> 3 and + 32), rounded to bf16
           Tile64<TV> vs = vr[s];
@@ -199,7 +201,7 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
           }
           store_tile64<NP>(vs, sm.v[buf][0], sm.v[buf][NP - 1]);
         } else {
-          store_tile64<NP>(vr[s], sm.v[buf][0], sm.v[buf][NP - 1]);
+          store_tile64<NP, TV, E>(vr[s], sm.v[buf][0], sm.v[buf][NP - 1]);
         }
         if (w == 0) {
           float gv = gr[s];
@@ -241,18 +243,18 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
           if constexpr (NP == 2) kl = tr_frag(sm.k[buf][1], kLd, 32 * c, 16 * w);
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
-            const float x = NP == 2 ? (float)kh[jj] + (float)kl[jj] : (float)kh[jj];
+            const float x = NP == 2 ? (float)kh[jj] + (float)kl[jj] : from16<E>(kh[jj]);
             ka[jj] = x * (jj < 4 ? w0[jj] : w1[jj - 4]);
           }
         }
         bf16x8 a[NP];
-        split8<NP>(ka, a);
+        split8<NP, E>(ka, a);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           bf16x8 bv[NP];   // V[s][v = 16n + ln]
 #pragma unroll
           for (int pl = 0; pl < NP; ++pl) bv[pl] = tr_frag(sm.v[buf][pl], kLd, 32 * c, 16 * n);
-          acc[n] = mma<NP>(a, bv, acc[n]);
+          acc[n] = mma<NP, E>(a, bv, acc[n]);
         }
       }
     }

@@ -563,7 +563,7 @@ __device__ __forceinline__ int sidx(int r, int c) {
 
 // Stage a 64 x 64 tile held in registers (Tile64 layout) into a swizzled
 // bf16 tile: bf16 data as 16-byte units, fp32 data converted to 8-byte halves.
-template <int (*F)(int), typename T>
+template <int (*F)(int), typename T, typename E = __bf16>
 __device__ __forceinline__ void store_tile_swz(const Tile64<T>& t, __bf16* dst) {
   const int tid = threadIdx.x;
 #pragma unroll
@@ -575,7 +575,7 @@ __device__ __forceinline__ void store_tile_swz(const Tile64<T>& t, __bf16* dst) 
       const int r = (tid >> 4) + 16 * rr;
       const float* e = (const float*)&t.r[rr];
       *(bf16x4*)(dst + sidx<F>(r, 4 * (tid & 15))) =
-          bf16x4{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3]};
+          cvt4e<E>(floatx4{e[0], e[1], e[2], e[3]});
     }
   }
 }
@@ -653,7 +653,7 @@ template <> struct P1T<3> { static constexpr int mt[3] = {3, 3, 2}, jt[3] = {3, 
 //   A tile (mt, jt): S^T[s = 16jt + 4lq + i][t = 16mt + ln] o exp(Gc_t - Gc_s)
 //                    o lambda[t, level(t, s)] (causal) -> bf16 A[t][s] in LDS.
 //   kv[2c + h]: D rows k = 32c + 8lq + 4h + i, column v = 16w + ln.
-template <int W, typename LT>
+template <int W, typename LT, typename E = __bf16>
 __device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, const LT* li,
                                         const bf16x8 (&qa)[4][2], const bf16x8& vt0,
                                         const bf16x8& vt1, floatx4 (&kv)[4], int lq, int ln) {
@@ -697,21 +697,21 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, con
   for (int n = 0; n < 3; ++n) {
     const int mt = S::mt[n], jt = S::jt[n];
     if (jt > mt) continue;
-    acc[n] = mfma16x16x32(kf[n][0], qa[mt][0], zero4());
-    acc[n] = mfma16x16x32(kf[n][1], qa[mt][1], acc[n]);
+    acc[n] = mfma16<E>(kf[n][0], qa[mt][0], zero4());
+    acc[n] = mfma16<E>(kf[n][1], qa[mt][1], acc[n]);
   }
   bf16x8 wv0, wv1;   // (w o V)[s][v = 16w + ln], s = 8lq + j / 32 + 8lq + j
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    wv0[i] = (__bf16)((float)vt0[i] * w0a[i]);
-    wv0[4 + i] = (__bf16)((float)vt0[4 + i] * w0b[i]);
-    wv1[i] = (__bf16)((float)vt1[i] * w1a[i]);
-    wv1[4 + i] = (__bf16)((float)vt1[4 + i] * w1b[i]);
+    wv0[i] = to16<E>(from16<E>(vt0[i]) * w0a[i]);
+    wv0[4 + i] = to16<E>(from16<E>(vt0[4 + i]) * w0b[i]);
+    wv1[i] = to16<E>(from16<E>(vt1[i]) * w1a[i]);
+    wv1[4 + i] = to16<E>(from16<E>(vt1[4 + i]) * w1b[i]);
   }
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    kv[hh] = mfma16x16x32(kt[hh][0], wv0, zero4());
-    kv[hh] = mfma16x16x32(kt[hh][1], wv1, kv[hh]);
+    kv[hh] = mfma16<E>(kt[hh][0], wv0, zero4());
+    kv[hh] = mfma16<E>(kt[hh][1], wv1, kv[hh]);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -722,8 +722,8 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, con
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    kv[2 + hh] = mfma16x16x32(kt[hh][0], wv0, zero4());
-    kv[2 + hh] = mfma16x16x32(kt[hh][1], wv1, kv[2 + hh]);
+    kv[2 + hh] = mfma16<E>(kt[hh][0], wv0, zero4());
+    kv[2 + hh] = mfma16<E>(kt[hh][1], wv1, kv[2 + hh]);
   }
   // ---- scaling, A tiles -> LDS ----
 #pragma unroll
@@ -736,7 +736,7 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, con
       float val[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) val[i] = acc[n][i] * fexp2(gt[n] - gs[n][i]) * lam[n][0];
-      out = bf16x4{(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
+      out = cvt4e<E>(floatx4{val[0], val[1], val[2], val[3]});
     } else {
       float val[4];
 #pragma unroll
@@ -744,7 +744,7 @@ __device__ __forceinline__ void bf16_p1(Bf16Smem<LT>& sm, const LdsBase& lb, con
         const float x = acc[n][i] * fexp2(gt[n] - gs[n][i]) * lam[n][i];
         val[i] = 4 * lq + i <= ln ? x : 0.f;
       }
-      out = bf16x4{(__bf16)val[0], (__bf16)val[1], (__bf16)val[2], (__bf16)val[3]};
+      out = cvt4e<E>(floatx4{val[0], val[1], val[2], val[3]});
     }
     *(bf16x4*)(sm.a + lb.aw + 1024 * mt + ((lb.awu ^ (2 * jt)) << 3)) = out;
   }
@@ -798,7 +798,8 @@ __global__ void mamba2_fwd_sync_init_kernel(unsigned int* __restrict__ sync, int
 // (v = x dt' as it is staged), l is dl (lambda = compute_lambda(L[h], dl) as it
 // is staged), g comes from dt (g = A dt'), and the output is bf16(o) + x D[h]
 // (see layer_math.h); bf16 x only.
-template <typename TV, typename TL, typename TO, bool FUSED, bool LAYER = false, bool LAM16 = false>
+template <typename TV, typename TL, typename TO, bool FUSED, bool LAYER = false, bool LAM16 = false,
+          typename E = __bf16>
 __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const TV* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
@@ -806,7 +807,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     float* __restrict__ segd, unsigned int* __restrict__ sync, int B, int T, int G, int H,
     int V, int L, int nlev, int nvb64, int slog, int NSEG, int final_state, LayerArgs la,
     LookbackCtl lbc) {
-  static_assert(!LAYER || sizeof(TV) == 2, "layer mode: bf16 x");
+  static_assert(!LAYER || (sizeof(TV) == 2 && __is_same(E, __bf16)), "layer mode: bf16 x");
   constexpr int kPl = kKD * 64;                           // one top-level state tile
   constexpr int kLPS = (kMaxLoc + kMaxTop) * kBT;          // one lambda' buffer
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     if (p < NSEG - 1 || is_final_seg) {
       SumSmem<1>& ss = *(SumSmem<1>*)smem_raw;
       float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vcol0;
-      const float dsum = seg_sum_body<__bf16, TV, false, 1, true, LAYER, 4>(
+      const float dsum = seg_sum_body<__bf16, TV, false, 1, true, LAYER, 4, E>(
           ss, k, v, g, out, b, h, p, vblk, T, G, H, V, NT, 1 << slog, la);
       if (tid == 0)
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, dsum), rsd,
@@ -997,8 +998,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
   // chunk j's registers -> LDS; par: the lambda / exp(Gc) buffer it goes to
   auto store = [&](int j, int par) {
     float gx = 0.f;
-    store_tile_swz<swz_qk>(rg.q, sm.q);
-    store_tile_swz<swz_qk>(rg.k, sm.k);
+    store_tile_swz<swz_qk, __bf16, E>(rg.q, sm.q);
+    store_tile_swz<swz_qk, __bf16, E>(rg.k, sm.k);
     if constexpr (LAYER) {
       // v = x dt' on the thread's two rows (dwv holds their dt', see dt_xform),
       // rounded to bf16 as the layer's v
@@ -1013,7 +1014,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       }
       store_tile_swz<swz_v>(xs, sm.v);
     } else {
-      store_tile_swz<swz_v>(rg.v, sm.v);
+      store_tile_swz<swz_v, TV, E>(rg.v, sm.v);
     }
     if (w == 0) {
       const float x = chunk_cumsum(rg.g);   // lane t holds Gc_t (layer mode: g from dt_xform)
@@ -1190,7 +1191,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + top_idx(v4 + c, kr + 16 * i)] = (__bf16)hacc[i][c];
+        for (int i = 0; i < 4; ++i) sm.top[e2 * kPl + top_idx(v4 + c, kr + 16 * i)] = to16<E>(hacc[i][c]);
     }
     if (is_final_seg) {
       // final states of the top levels (chunkwise.py:229-279): a level the last
@@ -1278,10 +1279,10 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     // ---- phase 1: A = S o M, and the chunk's K^T diag(w) V -------------------------
     floatx4 kv[4];
     switch (w) {
-      case 0: bf16_p1<0>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
-      case 1: bf16_p1<1>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
-      case 2: bf16_p1<2>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
-      default: bf16_p1<3>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      case 0: bf16_p1<0, LT, E>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      case 1: bf16_p1<1, LT, E>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      case 2: bf16_p1<2, LT, E>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
+      default: bf16_p1<3, LT, E>(sm, lb, sm.lam[j & 1] + kBT, qa, vt0, vt1, kv, lq, ln); break;
     }
     const float glr = sm.gc[kBT - 1];   // chunk log2-decay
     __syncthreads();   // A visible; chunk j's stage (but lambda') no longer read
@@ -1300,9 +1301,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
       af[4] = *(const bf16x8*)(sm.a + lb.ra1 + 1024 * 2);
       af[5] = *(const bf16x8*)(sm.a + lb.ra1 + 1024 * 3);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16x16x32(vt0, af[nt], zero4());
-      acc[2] = mfma16x16x32(vt1, af[4], acc[2]);
-      acc[3] = mfma16x16x32(vt1, af[5], acc[3]);
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16<E>(vt0, af[nt], zero4());
+      acc[2] = mfma16<E>(vt1, af[4], acc[2]);
+      acc[3] = mfma16<E>(vt1, af[5], acc[3]);
     }
     load(jn, 1);
     // local levels the chunk reads (bit e of the chunk index): all eight MFMAs of
@@ -1311,13 +1312,13 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
     for (int e = 0; e < kMaxLoc; ++e) {
       if (e < nloc && ((ic >> e) & 1)) {
         const floatx4 lam = lam4(lpr + e * kBT + 4 * ln);
-        const bf16x8 h0 = cat8(st[e][0], st[e][1]);
-        const bf16x8 h1 = cat8(st[e][2], st[e][3]);
+        const bf16x8 h0 = cat8e<E>(st[e][0], st[e][1]);
+        const bf16x8 h1 = cat8e<E>(st[e][2], st[e][3]);
         floatx4 tmp[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h0, qa[nt][0], zero4());
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16<E>(h0, qa[nt][0], zero4());
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h1, qa[nt][1], tmp[nt]);
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16<E>(h1, qa[nt][1], tmp[nt]);
         const float sc = fexp2(dl[e]);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
@@ -1353,9 +1354,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_fwd_bf16_kernel(
         }
         floatx4 tmp[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h0, qa[nt][0], zero4());
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16<E>(h0, qa[nt][0], zero4());
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16x16x32(h1, qa[nt][1], tmp[nt]);
+        for (int nt = 0; nt < 4; ++nt) tmp[nt] = mfma16<E>(h1, qa[nt][1], tmp[nt]);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
           const float cf = lam[nt] * egr[nt] * ee;
@@ -1575,7 +1576,10 @@ namespace hattn {
 
 inline LookbackCtl lookback_ctl() { return LookbackCtl{g_spin_limit.load(), g_publish.load()}; }
 
-template <typename TK, typename TV, typename TL, typename TO, int NP, int MAXLOC>
+// E: the 16-bit MFMA format of the fused single pass (NP = 1): bf16, or fp16
+// for fp16 q / k / v.
+template <typename TK, typename TV, typename TL, typename TO, int NP, int MAXLOC,
+          typename E = __bf16>
 static hipError_t launch_t(const void* q, const void* k, const void* v, const float* g,
                            const void* l, void* o, float* gcum, float* ht, void* ws, int B,
                            int T, int G, int H, int V, int L, int nlev, hipStream_t stream) {
@@ -1599,9 +1603,9 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
       hipLaunchKernelGGL(mamba2_fwd_sync_init_kernel, dim3((w.nsync + 255) / 256), dim3(256), 0,
                          stream, w.sync, w.nsync);
       if ((e = hipGetLastError()) != hipSuccess) return e;
-      auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true>;
+      auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true, false, false, E>;
       if constexpr (sizeof(TL) == 2)
-        if (lam16) kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true, false, true>;
+        if (lam16) kern = mamba2_fwd_bf16_kernel<TV, TL, TO, true, false, true, E>;
       e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
@@ -1610,7 +1614,7 @@ static hipError_t launch_t(const void* q, const void* k, const void* v, const fl
                          NSEG, ht != nullptr ? 1 : 0, LayerArgs{}, lookback_ctl());
       return hipGetLastError();
     }
-    auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, false>;
+    auto kern = mamba2_fwd_bf16_kernel<TV, TL, TO, false, false, false, E>;
     e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(xcd_head_grid(B * NSEG, H, nvb64)), dim3(256), smem, stream,
@@ -1702,6 +1706,21 @@ hipError_t hattn_mamba2_fwd_launch(const void* q, const void* k, const void* v, 
     if (dt_v == DT_FP32 && dt_l == DT_FP32 && dt_o == DT_FP32)
       return launch_t<float, float, float, float, 2, kMaxLocX3>(q, k, v, g, l, o, gcum, ht, ws,
                                                                 B, T, G, H, V, L, nlev, stream);
+    *unsupported = 1;
+    return hipSuccess;
+  }
+  if (dt_qk == DT_FP16) {
+    // fp16 q / k / v on fp16 MFMA (fp32 lambda; v and o fp16 or fp32)
+#define HATTN_DISPATCH_H(TV_, TO_)                                                               \
+  return launch_t<_Float16, TV_, float, TO_, 1, kMaxLoc, _Float16>(q, k, v, g, l, o, gcum, ht, ws, \
+                                                                  B, T, G, H, V, L, nlev, stream);
+    if (dt_l == DT_FP32) {
+      if (dt_v == DT_FP16 && dt_o == DT_FP16) { HATTN_DISPATCH_H(_Float16, _Float16) }
+      if (dt_v == DT_FP16 && dt_o == DT_FP32) { HATTN_DISPATCH_H(_Float16, float) }
+      if (dt_v == DT_FP32 && dt_o == DT_FP16) { HATTN_DISPATCH_H(float, _Float16) }
+      if (dt_v == DT_FP32 && dt_o == DT_FP32) { HATTN_DISPATCH_H(float, float) }
+    }
+#undef HATTN_DISPATCH_H
     *unsupported = 1;
     return hipSuccess;
   }

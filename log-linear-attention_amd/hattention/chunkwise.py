@@ -64,11 +64,22 @@ def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
         raise ValueError(f"L={L} levels are too few for T={T}")
 
 
+def _native_half(q, k, v, l):
+    """The forward's fp16 path (HType.WEAK): fp16 q / k multiply natively on
+    fp16 MFMA, as the reference's fp16 dots do.  v stays fp16 (a bf16 v is read
+    as fp32, exact), lambda is read as fp32 (exact for fp16 and bf16)."""
+    if v.dtype == torch.bfloat16:
+        v = v.float().contiguous()
+    if l.dtype != torch.float32:
+        l = l.float().contiguous()
+    return q, k, v, l
+
+
 def _widen_half(q, k, v, l):
-    """fp16 inputs have no kernels of their own.  fp16 values are exact in
-    fp32, so fp16 q / k run the fp32-accurate (bf16x3) kernels, and fp16 v or
-    lambda next to bf16 q / k are read as fp32; the caller returns o and the
-    gradients in the inputs' dtypes."""
+    """Where there is no fp16 kernel (the backward, HType.STRONG): fp16 values
+    are exact in fp32, so fp16 q / k run the fp32-accurate (bf16x3) kernels,
+    and fp16 v or lambda next to bf16 q / k are read as fp32; the caller
+    returns o and the gradients in the inputs' dtypes."""
     half = torch.float16
     if q.dtype == half:
         q, k = q.float().contiguous(), k.float().contiguous()
@@ -110,9 +121,10 @@ def chunkwise_fwd(
 ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """Log-linear Mamba-2 forward (chunkwise.py:1118-1275).
 
-    bf16 q / k multiply on bf16 MFMA; fp32 q / k select the bf16x3 kernels
-    (each product as three bf16 MFMAs over hi / lo splits, fp32-accurate), the
-    counterpart of the reference's fp32 dots.
+    bf16 q / k multiply on bf16 MFMA, fp16 q / k on fp16 MFMA (HType.WEAK; the
+    reference's fp16 dots); fp32 q / k select the bf16x3 kernels (each product
+    as three bf16 MFMAs over hi / lo splits, fp32-accurate), the counterpart of
+    the reference's fp32 dots.
 
     Returns ``o`` [B,T,H,V] in v.dtype, the chunk-local inclusive cumsum of g
     [B,T,H] fp32 and, if ``output_final_state``, ``ht`` [B,H,K,V,L] fp32 holding
@@ -153,7 +165,10 @@ def chunkwise_fwd_keep(q, k, v, g, l, head_first, level_base, htype, chunk_size,
     if q.dtype != k.dtype:
         raise ValueError("q and k must share a dtype")
     out_dtype = v.dtype
-    q, k, v, l = _widen_half(q, k, v, l)
+    if q.dtype == torch.float16 and htype == HType.WEAK:
+        q, k, v, l = _native_half(q, k, v, l)
+    else:
+        q, k, v, l = _widen_half(q, k, v, l)
     if q.dtype == torch.float32:
         # fp32 q / k run the bf16x3 (fp32-accurate) kernels, which read fp32 v
         # and lambda and write fp32 o

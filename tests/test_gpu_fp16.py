@@ -1,17 +1,26 @@
 """fp16 inputs (the reference's kernels take fp16 q / k / v / lambda).
 
-The library has no fp16 kernels.  The host layer widens fp16 exactly: fp16
-Mamba-2 q / k run the fp32-accurate (bf16x3) kernels, fp16 v / lambda next to
-bf16 q / k are read as fp32, and the output and gradients come back in the
-inputs' dtypes.  GDN rounds fp16 q / k / v to bf16 (its kernels read bf16) and
-reads fp16 beta / lambda as fp32.
+The Mamba-2 forward (HType.WEAK) multiplies fp16 q / k / v natively on fp16
+MFMA (the fused single pass with fp16 operands; lambda read as fp32), as the
+reference's fp16 dots do.  Elsewhere the host layer widens fp16 exactly: the
+Mamba-2 backward runs the fp32-accurate (bf16x3) kernels on the widened
+inputs, and the output and gradients come back in the inputs' dtypes.  GDN
+rounds fp16 q / k / v to bf16 (its kernels read bf16) and reads fp16 beta /
+lambda as fp32.
 
 Checks:
-* Mamba-2 forward and backward with fp16 inputs against the fp64 oracle fed
-  the same fp16 values: the bf16x3 kernels are fp32-accurate, so the error is
-  the final fp16 rounding of o and the gradients (2^-11 relative): max-abs/rel
-  below 2e-3, relative Frobenius below 1e-3 (dg, a reverse cumsum with heavy
-  cancellation, below 1e-2);
+* Mamba-2 forward with fp16 inputs against the fp64 oracle fed the same fp16
+  values: the kernel rounds the A tiles and the level states to fp16 for the
+  MFMAs (as the reference's fp16 path keeps them in fp16), 2^-11 relative per
+  operand (three more mantissa bits than bf16; measured 3e-4 .. 7e-4):
+  max-abs/rel below 2e-3, relative Frobenius below 1e-3; and it takes the
+  fp16 kernel, not the widening: the C-ABI accepts the fp16 dtype code and
+  the result is farther from the oracle than the fp32-accurate run on the
+  widened inputs (about 1e-5);
+* Mamba-2 backward with fp16 inputs: the bf16x3 kernels are fp32-accurate, so
+  the error is the final fp16 rounding of the gradients (2^-11 relative):
+  max-abs/rel below 2e-3, relative Frobenius below 1e-3 (dg, a reverse cumsum
+  with heavy cancellation, below 1e-2);
 * GDN forward with fp16 inputs against the fp64 oracle on the same fp16
   values, to the bf16 tolerances of the GDN tests (2e-2 / 1e-2);
 * GDN backward with fp16 inputs equals the backward on the bf16-rounded
@@ -116,3 +125,47 @@ def test_gdn_backward_fp16_matches_bf16_rounded_inputs():
         mx, fro = _errs(a, r.float())
         print(f"  {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
         assert mx < 2e-3 and fro < 1e-3, (name, mx, fro)
+
+
+@pytest.mark.parametrize("T,final_state", [(4096, False), (2048, True)])
+def test_mamba2_forward_fp16_native(T, final_state):
+    """The fp16 forward over several segments (the look-back and top levels) and
+    its final states, against the fp64 oracle on the same fp16 values; the
+    fp16 dtype code reaches the kernels (no widening to the fp32-accurate
+    path, whose result is closer to the oracle)."""
+    from hattention import _lib
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_fwd
+    B, H, K, V = 2, 2, 64, 64
+    L = 7 + math.ceil(math.log2(T // 64))
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, seed=T + 3, dtype=HALF)
+    dev = torch.device("cuda:0")
+    print(f"[fp16 mamba2 native] T={T} final_state={final_state}", flush=True)
+    xs = [x.to(dev) for x in (q, k, v, g, l)]
+    o, gc, ht = chunkwise_fwd(*xs, False, 2, HType.WEAK, 64, final_state)
+    o32, _, _ = chunkwise_fwd(*(x.float() for x in xs), False, 2, HType.WEAK, 64, False)
+    torch.cuda.synchronize()
+    assert o.dtype == HALF
+    # the C-ABI takes fp16 q / k (the kernels' own dtype code, not NOT_IMPLEMENTED)
+    lib = _lib.load()
+    p = None
+    st = lib.hattn_mamba2_chunkwise_fwd(p, p, p, p, p, p, p, p, B, T, H, H, K, V, L,
+                                        _lib.DTYPE_CODES[HALF], _lib.DTYPE_CODES[HALF], 2,
+                                        _lib.DTYPE_CODES[HALF], 2, 0, 64, p, 0, p)
+    assert st == _lib.HATTN_ERR_VALUE   # past the dtype rules: fails on the null pointers
+    for b in range(B):
+        for h in range(H):
+            sl = lambda x: x[b:b + 1, :, h:h + 1].double().cpu()
+            o_ref, _, ht_ref = chunked_scan_fwd(sl(q), sl(k), sl(v), sl(g), sl(l), chunk_size=64,
+                                                output_final_state=final_state)
+            mx, fro = _errs(o[b:b + 1, :, h:h + 1], o_ref)
+            mx32, _ = _errs(o32[b:b + 1, :, h:h + 1], o_ref)
+            print(f"  row ({b},{h}) o: max-rel {mx:.2e} fro {fro:.2e} (fp32 path {mx32:.2e})",
+                  flush=True)
+            assert mx < 2e-3 and fro < 1e-3, (b, h, mx, fro)
+            assert mx32 < mx
+            if final_state:
+                a = ht[b, h].double().cpu()
+                r = ht_ref[0, 0]
+                mxh = ((a - r).abs().max() / r.abs().max()).item()
+                assert mxh < 2e-3, (b, h, mxh)

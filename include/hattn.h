@@ -165,8 +165,9 @@ void hattn_debug_lookback(int spin_limit, int publish);
  * Constraints: as the forward (T % 64, L >= 7 + ceil(log2(T/64)), K and V
  * multiples of 64 -> HATTN_ERR_VALUE); K == V == 64 (the Python host layer
  * runs larger K and V as one call per 64-wide block), q/k/do either all BF16
- * (bf16 MFMA; v and l in {BF16, FP32}) or all FP32 (bf16x3 kernels,
- * fp32-accurate; v and l FP32, dq / dk / dv written in fp32)
+ * (bf16 MFMA; v and l in {BF16, FP32}), all FP16 (fp16 MFMA; v FP16 or FP32,
+ * l FP32) or all FP32 (bf16x3 kernels, fp32-accurate; v and l FP32, dq / dk /
+ * dv written in fp32)
  *                                                  -> HATTN_ERR_NOT_IMPLEMENTED.
  * htype HATTN_HTYPE_STRONG (the reference's USE_A2 / USE_H2 backward,
  * chunkwise.py:1377-1580): BF16 q, k, v and do (l BF16 or FP32), T <= 64 *

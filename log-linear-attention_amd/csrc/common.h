@@ -379,10 +379,10 @@ __device__ __forceinline__ void split8(const float* x, bf16x8* out) {
 }
 
 // Two D-layout quads -> one B fragment (as cat8), split into NP planes.
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ void cat8s(floatx4 a, floatx4 b, bf16x8* out) {
   const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  split8<NP>(x, out);
+  split8<NP, E>(x, out);
 }
 
 }  // namespace hattn

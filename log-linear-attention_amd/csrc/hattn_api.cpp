@@ -426,14 +426,20 @@ static int mamba2_bwd_impl(const void* q, const void* k, const void* v, const fl
   if (nlev > hattn_mamba2_fwd_max_levels(0))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T,
                 hattn_mamba2_fwd_max_levels(0));
-  // bf16 q / k / dO: bf16 kernels; fp32 q / k / dO: bf16x3 kernels (fp32 v and lambda)
+  // bf16 q / k / dO: bf16 kernels; fp16: the same kernels on fp16 MFMA (fp16 or
+  // fp32 v, fp32 lambda); fp32 q / k / dO: bf16x3 kernels (fp32 v and lambda)
   if (!((dtype_qk == HATTN_BF16 && dtype_do == HATTN_BF16) ||
+        (dtype_qk == HATTN_FP16 && dtype_do == HATTN_FP16) ||
         (dtype_qk == HATTN_FP32 && dtype_do == HATTN_FP32)))
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/do dtype codes %d/%d (bf16 or fp32, both alike)",
-                dtype_qk, dtype_do);
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "q/k/do dtype codes %d/%d (bf16, fp16 or fp32, both alike)", dtype_qk, dtype_do);
   if (dtype_qk == HATTN_FP32 && !(dtype_v == HATTN_FP32 && dtype_l == HATTN_FP32))
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "fp32 q/k need fp32 v and lambda (v=%d l=%d)", dtype_v,
                 dtype_l);
+  if (dtype_qk == HATTN_FP16 &&
+      !((dtype_v == HATTN_FP16 || dtype_v == HATTN_FP32) && dtype_l == HATTN_FP32))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "fp16 q/k need fp16 or fp32 v and fp32 lambda (v=%d l=%d)", dtype_v, dtype_l);
   if (int st = check_span(T, max_of({(size_t)H * K * elem_bytes(dtype_qk),
                                       (size_t)H * V * elem_bytes(dtype_v),
                                       (size_t)H * V * elem_bytes(dtype_do),

@@ -68,7 +68,7 @@ struct BwdRegs {
 
 // One 16-byte unit of a staged tile: bf16 data as is, fp32 data as NP bf16
 // planes of four elements (row r, column c of a kLd-strided tile).
-template <int NP, typename T>
+template <int NP, typename T, typename E = __bf16>
 __device__ __forceinline__ void stage_unit(const uint4& u, __bf16 (*dst)[kBT * kLd], int off) {
   if constexpr (sizeof(T) == 2) {
     *(uint4*)(dst[0] + off) = u;
@@ -77,8 +77,8 @@ __device__ __forceinline__ void stage_unit(const uint4& u, __bf16 (*dst)[kBT * k
     bf16x4 hi, lo;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      hi[j] = (__bf16)e[j];
-      lo[j] = bf16_lo(e[j], hi[j]);
+      hi[j] = to16<E>(e[j]);
+      if constexpr (NP == 2) lo[j] = bf16_lo(e[j], hi[j]);
     }
     *(bf16x4*)(dst[0] + off) = hi;
     if constexpr (NP == 2) *(bf16x4*)(dst[NP - 1] + off) = lo;
@@ -162,7 +162,7 @@ struct BwdLoader {
   }
 
   // Returns exp(Gc) of this thread's lambda row (token lrow of the chunk).
-  template <int NP>
+  template <int NP, typename E = __bf16>
   __device__ float store(const BwdRegs<NTHR, TK, TV, TL>& r, BwdStage<NP>& s) const {
     using R = BwdRegs<NTHR, TK, TV, TL>;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -170,15 +170,15 @@ struct BwdLoader {
     for (int u = 0; u < R::NK; ++u) {
       const int off = sizeof(TK) == 2 ? ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)
                                       : ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15);
-      stage_unit<NP, TK>(r.q[u], s.q, off);
-      stage_unit<NP, TK>(r.k[u], s.k, off);
-      stage_unit<NP, TK>(r.d[u], s.d, off);
+      stage_unit<NP, TK, E>(r.q[u], s.q, off);
+      stage_unit<NP, TK, E>(r.k[u], s.k, off);
+      stage_unit<NP, TK, E>(r.d[u], s.d, off);
     }
 #pragma unroll
     for (int u = 0; u < R::NV; ++u) {
       const int off = sizeof(TV) == 2 ? ((tid >> 3) + u * (NTHR / 8)) * kLd + 8 * (tid & 7)
                                       : ((tid >> 4) + u * (NTHR / 16)) * kLd + 4 * (tid & 15);
-      stage_unit<NP, TV>(r.v[u], s.v, off);
+      stage_unit<NP, TV, E>(r.v[u], s.v, off);
     }
     const float x = r.g;                       // already the chunk-local cumsum
     const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
@@ -232,7 +232,7 @@ __device__ __forceinline__ void trfrag(const __bf16 (*X)[kBT * kLd], int r0, int
 }
 
 // S^T and dP^T tile (s rows 16jt.., t columns 16mt..): D[m = s][n = t].
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ void st_dpt_tile(const BwdStage<NP>& s, int mt, int jt, floatx4& S,
                                             floatx4& P) {
   const int lane = threadIdx.x & 63, lq = lane >> 4, ln = lane & 15;
@@ -245,27 +245,27 @@ __device__ __forceinline__ void st_dpt_tile(const BwdStage<NP>& s, int mt, int j
     bf16x8 a[NP], bq[NP];
     frag8<NP>(s.k, ra, a);
     frag8<NP>(s.q, rb, bq);
-    S = mma<NP>(a, bq, S);
+    S = mma<NP, E>(a, bq, S);
     frag8<NP>(s.v, ra, a);
     frag8<NP>(s.d, rb, bq);
-    P = mma<NP>(a, bq, P);
+    P = mma<NP, E>(a, bq, P);
   }
 }
 
 // fp32 value of staged element planes
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ float plane_val(const __bf16 (*X)[kBT * kLd], int off) {
-  return NP == 2 ? (float)X[0][off] + (float)X[NP - 1][off] : (float)X[0][off];
+  return NP == 2 ? (float)X[0][off] + (float)X[NP - 1][off] : from16<E>(X[0][off]);
 }
 
 // Four fp32 values stored as NP bf16 planes of an intermediate tile.
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ void store_planes4(__bf16 (*X)[kBT * kLd], int off, const float* x) {
   bf16x4 hi, lo;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    hi[i] = (__bf16)x[i];
-    lo[i] = bf16_lo(x[i], hi[i]);
+    hi[i] = to16<E>(x[i]);
+    if constexpr (NP == 2) lo[i] = bf16_lo(x[i], hi[i]);
   }
   *(bf16x4*)(X[0] + off) = hi;
   if constexpr (NP == 2) *(bf16x4*)(X[NP - 1] + off) = lo;
@@ -273,6 +273,7 @@ __device__ __forceinline__ void store_planes4(__bf16 (*X)[kBT * kLd], int off, c
 
 // S^T and dP^T of two tiles (as st_dpt_tile): every LDS read of a 32-wide
 // contraction step is issued before its four MFMAs.
+template <typename E = __bf16>
 __device__ __forceinline__ void st_dpt_tiles2(const BwdStage<1>& s, const int (&mt)[2],
                                               const int (&jt)[2], floatx4 (&S)[2],
                                               floatx4 (&P)[2]) {
@@ -291,8 +292,8 @@ __device__ __forceinline__ void st_dpt_tiles2(const BwdStage<1>& s, const int (&
     }
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-      S[n] = mfma16x16x32(ka[n], qb[n], c ? S[n] : zero4());
-      P[n] = mfma16x16x32(va[n], db[n], c ? P[n] : zero4());
+      S[n] = mfma16<E>(ka[n], qb[n], c ? S[n] : zero4());
+      P[n] = mfma16<E>(va[n], db[n], c ? P[n] : zero4());
     }
   }
 }
@@ -360,20 +361,21 @@ __device__ __forceinline__ void row_pairs(const __bf16 (*X)[kBT * kLd], int row,
   for (int pl = 0; pl < NP; ++pl) f[pl] = row_pair(X[pl], row, c0);
 }
 
+template <typename E = __bf16>
 __device__ __forceinline__ bf16x8 scale8(bf16x8 x, floatx4 a, floatx4 b) {
   bf16x8 y;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    y[i] = (__bf16)((float)x[i] * a[i]);
-    y[4 + i] = (__bf16)((float)x[4 + i] * b[i]);
+    y[i] = to16<E>(from16<E>(x[i]) * a[i]);
+    y[4 + i] = to16<E>(from16<E>(x[4 + i]) * b[i]);
   }
   return y;
 }
 // planes x (value hi + lo) scaled elementwise by (a, b), re-split into planes
-template <int NP>
+template <int NP, typename E = __bf16>
 __device__ __forceinline__ void scale8s(const bf16x8* x, floatx4 a, floatx4 b, bf16x8* y) {
   if constexpr (NP == 1) {
-    y[0] = scale8(x[0], a, b);
+    y[0] = scale8<E>(x[0], a, b);
   } else {
     float f[8];
 #pragma unroll
@@ -397,7 +399,7 @@ struct RsumSmem {
   float sig[4][kBT];
 };
 
-template <int NP, typename TK, typename TL>
+template <int NP, typename TK, typename TL, typename E = __bf16>
 __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
     const TK* __restrict__ q, const TK* __restrict__ dO, const float* __restrict__ gcin,
     const TL* __restrict__ l, float* __restrict__ rsum, int B, int T, int H, int L, int NT,
@@ -461,7 +463,7 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
         rr[sl].lv = to_f32<TL>(buf_load<TL>(rl, (lt * H * L + lcol) * sizeof(TL), t0 * lrowb));
       }
   };
-  float E = 0.f;
+  float Ecum = 0.f;
   auto step = [&](int ic, int slot) {
     __syncthreads();   // previous chunk's reads of sm are done
     float glast = 0.f;
@@ -470,10 +472,10 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
       if (sl == slot) {
 #pragma unroll
         for (int u = 0; u < NK; ++u) {
-          stage_unit<NP, TK>(rr[sl].q[u], sm.q, soff + RK * u * kLd);
-          stage_unit<NP, TK>(rr[sl].d[u], sm.d, soff + RK * u * kLd);
+          stage_unit<NP, TK, E>(rr[sl].q[u], sm.q, soff + RK * u * kLd);
+          stage_unit<NP, TK, E>(rr[sl].d[u], sm.d, soff + RK * u * kLd);
         }
-        sm.sig[le][lt] = le < ne ? rr[sl].lv * fexp(E + rr[sl].gct) : 0.f;
+        sm.sig[le][lt] = le < ne ? rr[sl].lv * fexp(Ecum + rr[sl].gct) : 0.f;
         glast = rr[sl].glast;
       }
     load(ic + 2, slot);
@@ -490,13 +492,13 @@ __global__ __launch_bounds__(256) void mamba2_bwd_rsum_kernel(
         if (a < ne) {
           const float* sg = sm.sig[a] + 32 * c + 8 * lq;
           bf16x8 qs[NP];
-          scale8s<NP>(qa, *(const floatx4*)sg, *(const floatx4*)(sg + 4), qs);
+          scale8s<NP, E>(qa, *(const floatx4*)sg, *(const floatx4*)(sg + 4), qs);
 #pragma unroll
-          for (int n = 0; n < 4; ++n) acc[a][n] = mma<NP>(qs, db[n], acc[a][n]);
+          for (int n = 0; n < 4; ++n) acc[a][n] = mma<NP, E>(qs, db[n], acc[a][n]);
         }
       }
     }
-    E += glast;
+    Ecum += glast;
   };
   load(c0, 0);
   load(c0 + 1, 1);
@@ -537,7 +539,7 @@ struct DqSmem {
 // after the first chunk their MFMA fragments come from L2; the fragments of
 // the segment's first top level are loaded once, before the walk, the others
 // one level ahead of their use.
-template <int NP, typename TK, typename TV, typename TL>
+template <int NP, typename TK, typename TV, typename TL, typename E = __bf16>
 __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     const TK* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
@@ -616,7 +618,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     // the thread's own slot: the dlambda section reads it after the chunk's last
     // barrier, and the next chunk's staging rewrites the shared stage before its
     // first barrier
-    sm.eg_own[tid] = ld.store(rg, s);
+    sm.eg_own[tid] = ld.template store<NP, E>(rg, s);
     __syncthreads();
     // lane indices made opaque per chunk, so the LDS addresses of the phases are
     // recomputed (a few VALU ops) instead of held in VGPRs across the walk
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       const int c1 = p1_tile4(w, 1);
       int tmt[2] = {w, (c1 & 15) >> 2}, tjt[2] = {w, c1 & 3};
       floatx4 S[2], P[2];
-      st_dpt_tiles2(s, tmt, tjt, S, P);
+      st_dpt_tiles2<E>(s, tmt, tjt, S, P);
       float out[2][4], x[2][4];
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
         } else {
           sm.dl_off[t][tjt[1]][lq] = x[1][0] + x[1][1] + x[1][2] + x[1][3];
         }
-        store_planes4<NP>(sm.a, t * kLd + 16 * tjt[n] + 4 * lq, out[n]);
+        store_planes4<NP, E>(sm.a, t * kLd + 16 * tjt[n] + 4 * lq, out[n]);
       }
     }
 #pragma unroll
@@ -668,7 +670,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       float out[4] = {0.f, 0.f, 0.f, 0.f};
       if (code < 16) {
         floatx4 S, P;
-        st_dpt_tile(s, mt, jt, S, P);
+        st_dpt_tile<NP, E>(s, mt, jt, S, P);
         const TileMask mk = tile_mask(s, mt, jt);
         float x[4];
 #pragma unroll
@@ -689,7 +691,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           }
         }
       }
-      store_planes4<NP>(sm.a, t * kLd + 16 * jt + 4 * lq, out);
+      store_planes4<NP, E>(sm.a, t * kLd + 16 * jt + 4 * lq, out);
     }
     __syncthreads();
     // the next chunk's loads, issued after phase 1 rather than at the chunk start,
@@ -708,10 +710,10 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
         const int ar = (16 * mt + ln) * kLd + 8 * lq;
         bf16x8 af[NP];
         frag8<NP>(sm.a, ar, af);
-        dqT[mt] = mma<NP>(kt0, af, zero4());
+        dqT[mt] = mma<NP, E>(kt0, af, zero4());
         if (mt >= 2) {
           frag8<NP>(sm.a, ar + 32, af);
-          dqT[mt] = mma<NP>(kt1, af, dqT[mt]);
+          dqT[mt] = mma<NP, E>(kt1, af, dqT[mt]);
         }
       }
     }
@@ -721,7 +723,7 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
     for (int mt = 0; mt < 4; ++mt) {
       const int off = (16 * mt + ln) * kLd + 16 * w + 4 * lq;
       const bf16x4 x = *(const bf16x4*)(s.q[0] + off);
-      qk[mt] = floatx4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+      qk[mt] = floatx4{from16<E>(x[0]), from16<E>(x[1]), from16<E>(x[2]), from16<E>(x[3])};
       if constexpr (NP == 2) {
         const bf16x4 y = *(const bf16x4*)(s.q[1] + off);
         qk[mt] += floatx4{(float)y[0], (float)y[1], (float)y[2], (float)y[3]};
@@ -747,8 +749,8 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           floatx4 y[2];
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            y[u] = mma<NP>(a0, da[2 * hf + u][0], zero4());
-            y[u] = mma<NP>(a1, da[2 * hf + u][1], y[u]);
+            y[u] = mma<NP, E>(a0, da[2 * hf + u][0], zero4());
+            y[u] = mma<NP, E>(a1, da[2 * hf + u][1], y[u]);
           }
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
@@ -772,8 +774,8 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
           if (e < nloc) {
             if (ic > c0 && ((ic >> e) & 1)) {
               bf16x8 h0[NP], h1[NP];
-              cat8s<NP>(hT[e][0], hT[e][1], h0);
-              cat8s<NP>(hT[e][2], hT[e][3], h1);
+              cat8s<NP, E>(hT[e][0], hT[e][1], h0);
+              cat8s<NP, E>(hT[e][2], hT[e][3], h1);
               level(h0, h1, e, 7 + e, 1.f);
             } else {
               sm.dl_int[16 * lq + ln][e][w] = 0.f;
@@ -826,18 +828,18 @@ __global__ __launch_bounds__(256, NP == 1 ? 2 : 1) void mamba2_bwd_dq_kernel(
       {
         bf16x8 kt[NP], kb0[NP], kb1[NP];
         trfrag<NP>(s.k, 0, 16 * w, kt);
-        scale8s<NP>(kt, *(const floatx4*)(s.wt + 8 * lq), *(const floatx4*)(s.wt + 8 * lq + 4),
+        scale8s<NP, E>(kt, *(const floatx4*)(s.wt + 8 * lq), *(const floatx4*)(s.wt + 8 * lq + 4),
                     kb0);
         trfrag<NP>(s.k, 32, 16 * w, kt);
-        scale8s<NP>(kt, *(const floatx4*)(s.wt + 32 + 8 * lq),
+        scale8s<NP, E>(kt, *(const floatx4*)(s.wt + 32 + 8 * lq),
                     *(const floatx4*)(s.wt + 36 + 8 * lq), kb1);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           bf16x8 vf[NP];
           trfrag<NP>(s.v, 0, 16 * m, vf);
-          kv[m] = mma<NP>(vf, kb0, zero4());
+          kv[m] = mma<NP, E>(vf, kb0, zero4());
           trfrag<NP>(s.v, 32, 16 * m, vf);
-          kv[m] = mma<NP>(vf, kb1, kv[m]);
+          kv[m] = mma<NP, E>(vf, kb1, kv[m]);
         }
       }
       const float gl = fexp(glr);
@@ -913,7 +915,7 @@ struct DkvSmem {
   float kdk[kBT][4];        // k . dk intra-chunk column sums [s][t-tile]
 };
 
-template <int NP, typename TK, typename TV, typename TL>
+template <int NP, typename TK, typename TV, typename TL, typename E = __bf16>
 __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
     const TK* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     const TK* __restrict__ dO, const float* __restrict__ gcin, const TL* __restrict__ l,
@@ -1017,7 +1019,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
   // previous chunk's loads are unconditional (the first chunk reloaded at the end)
   int ic = cend - 1;
   do {
-    ld.store(rg, s);
+    ld.template store<NP, E>(rg, s);
     // q . dq of this chunk's tokens (written by the dq kernel), needed by wave 0 at
     // the end of the chunk: loaded now so the load has the whole chunk to land
     const unsigned int vo_g = (unsigned int)lane * H * 4, so_g = (unsigned int)ic * kBT * H * 4;
@@ -1041,7 +1043,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         tjt[n] = cc & 3;
       }
       floatx4 S[2], P[2];
-      st_dpt_tiles2(s, tmt, tjt, S, P);
+      st_dpt_tiles2<E>(s, tmt, tjt, S, P);
       float os[2][4], op[2][4], c[2][4];
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
@@ -1067,8 +1069,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
           for (int i = 0; i < 4; ++i) sm.kdk[16 * tjt[n] + 4 * lq + i][tmt[n]] = c[n][i];
         if (live[n]) {
           const int off = (16 * tmt[n] + ln) * kLd + 16 * tjt[n] + 4 * lq;
-          store_planes4<NP>(sm.as, off, os[n]);
-          store_planes4<NP>(sm.ap, off, op[n]);
+          store_planes4<NP, E>(sm.as, off, os[n]);
+          store_planes4<NP, E>(sm.ap, off, op[n]);
         }
       }
     } else
@@ -1081,7 +1083,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         float os[4] = {0.f, 0.f, 0.f, 0.f}, op[4] = {0.f, 0.f, 0.f, 0.f};
         if (code < 16) {
           floatx4 S, P;
-          st_dpt_tile(s, mt, jt, S, P);
+          st_dpt_tile<NP, E>(s, mt, jt, S, P);
           const TileMask mk = tile_mask(s, mt, jt);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -1093,8 +1095,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             if (ln == 0) sm.kdk[16 * jt + 4 * lq + i][mt] = c;
           }
         }
-        store_planes4<NP>(sm.as, t * kLd + 16 * jt + 4 * lq, os);
-        store_planes4<NP>(sm.ap, t * kLd + 16 * jt + 4 * lq, op);
+        store_planes4<NP, E>(sm.as, t * kLd + 16 * jt + 4 * lq, os);
+        store_planes4<NP, E>(sm.ap, t * kLd + 16 * jt + 4 * lq, op);
       }
     }
     __syncthreads();
@@ -1117,10 +1119,10 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         // t-steps covering t >= s: both for s-tiles 0, 1; the second for 2, 3
         bf16x8 bx[NP];
         trfrag<NP>(xb, 32, 16 * mt, bx);
-        out[mt] = mma<NP>(a1, bx, zero4());
+        out[mt] = mma<NP, E>(a1, bx, zero4());
         if (mt < 2) {
           trfrag<NP>(xb, 0, 16 * mt, bx);
-          out[mt] = mma<NP>(a0, bx, out[mt]);
+          out[mt] = mma<NP, E>(a0, bx, out[mt]);
         }
       }
     }
@@ -1137,8 +1139,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         }
       }
       bf16x8 a0[NP], a1[NP];
-      cat8s<NP>(dsum[0], dsum[1], a0);
-      cat8s<NP>(dsum[2], dsum[3], a1);
+      cat8s<NP, E>(dsum[0], dsum[1], a0);
+      cat8s<NP, E>(dsum[2], dsum[3], a1);
       // two s-tiles at a time: their LDS reads, then their MFMAs, then the FMAs;
       // k_s . dk_s (inter-chunk part) by one transposed cross-row sum at the end
       float r[4];
@@ -1155,8 +1157,8 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
         floatx4 y[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          y[u] = mma<NP>(a0, rp[u][0], zero4());
-          y[u] = mma<NP>(a1, rp[u][1], y[u]);
+          y[u] = mma<NP, E>(a0, rp[u][0], zero4());
+          y[u] = mma<NP, E>(a1, rp[u][1], y[u]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -1168,7 +1170,7 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
             const bf16x4 kx = *(const bf16x4*)(s.k[0] + koff);
             float rr = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rr += (float)kx[i] * y[u][i];
+            for (int i = 0; i < 4; ++i) rr += from16<E>(kx[i]) * y[u][i];
             if constexpr (NP == 2) {
               const bf16x4 kl = *(const bf16x4*)(s.k[1] + koff);
 #pragma unroll
@@ -1228,29 +1230,29 @@ __global__ __launch_bounds__(512, 1) void mamba2_bwd_dkv_kernel(
               const float* sg = s.lam + (7 + e) * kBT;
               bf16x8 b0[NP], b1[NP];
               if constexpr (NP == 1) {
-                scale8s<NP>(yt0, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
+                scale8s<NP, E>(yt0, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
                             b0);
-                scale8s<NP>(yt1, *(const floatx4*)(sg + 32 + 8 * lq),
+                scale8s<NP, E>(yt1, *(const floatx4*)(sg + 32 + 8 * lq),
                             *(const floatx4*)(sg + 36 + 8 * lq), b1);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                  dh[e][m] = mma<NP>(af[m][0], b0, dh[e][m]);
-                  dh[e][m] = mma<NP>(af[m][1], b1, dh[e][m]);
+                  dh[e][m] = mma<NP, E>(af[m][0], b0, dh[e][m]);
+                  dh[e][m] = mma<NP, E>(af[m][1], b1, dh[e][m]);
                 }
               } else {
                 bf16x8 yt[NP];
                 trfrag<NP>(yb, 0, 16 * wr, yt);
-                scale8s<NP>(yt, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
+                scale8s<NP, E>(yt, *(const floatx4*)(sg + 8 * lq), *(const floatx4*)(sg + 8 * lq + 4),
                             b0);
                 trfrag<NP>(yb, 32, 16 * wr, yt);
-                scale8s<NP>(yt, *(const floatx4*)(sg + 32 + 8 * lq),
+                scale8s<NP, E>(yt, *(const floatx4*)(sg + 32 + 8 * lq),
                             *(const floatx4*)(sg + 36 + 8 * lq), b1);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                   trfrag<NP>(ya, 0, 16 * m, af[0][0]);
-                  dh[e][m] = mma<NP>(af[0][0], b0, dh[e][m]);
+                  dh[e][m] = mma<NP, E>(af[0][0], b0, dh[e][m]);
                   trfrag<NP>(ya, 32, 16 * m, af[0][1]);
-                  dh[e][m] = mma<NP>(af[0][1], b1, dh[e][m]);
+                  dh[e][m] = mma<NP, E>(af[0][1], b1, dh[e][m]);
                 }
               }
             }
@@ -1326,7 +1328,8 @@ inline BwdWs bwd_ws_layout(void* base, int B, int T, int H, int V, int nlev) {
 // fsums / fsegd (or null): the forward's segment summaries and log-decays of
 // these inputs (its workspace, same segmentation and layout), which then
 // replace the summary pass.
-template <int NP, typename TK, typename TV, typename TL>
+// E: the 16-bit MFMA format (NP = 1): bf16, or fp16 for fp16 q / k / v / dO.
+template <int NP, typename TK, typename TV, typename TL, typename E = __bf16>
 static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, const float* gc,
                                const void* l, const void* dO, void* dq, void* dk, void* dv,
                                float* dg, float* dl, void* ws, const float* fsums,
@@ -1343,7 +1346,7 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   const float* segd = reuse ? fsegd : w.segd;
   hipError_t e;
   if (NSEG > 1 && !reuse) {
-    auto sk = mamba2_seg_sum_kernel<TK, TV, true, NP>;
+    auto sk = mamba2_seg_sum_kernel<TK, TV, true, NP, E>;
     hipLaunchKernelGGL(sk, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
                        (const TK*)k, (const TV*)v, gc, w.sums, w.segd, B, T, H, H, V, NT,
                        1 << slog, NSEG, 1);
@@ -1351,18 +1354,19 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
   }
   if (ntop > 0) {
     // top-level states of every segment for the dq kernel
-    hipLaunchKernelGGL(mamba2_htop_kernel<NP>, dim3(rows * 4), dim3(256), 0, stream, sums,
-                       segd, w.htop, V, NSEG, ntop, 1);
+    auto hk = mamba2_htop_kernel<NP, E>;
+    hipLaunchKernelGGL(hk, dim3(rows * 4), dim3(256), 0, stream, sums, segd, w.htop, V, NSEG,
+                       ntop, 1);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int ngrp = (ntop + 3) / 4;
-    auto rk = mamba2_bwd_rsum_kernel<NP, TK, TL>;
+    auto rk = mamba2_bwd_rsum_kernel<NP, TK, TL, E>;
     hipLaunchKernelGGL(rk, dim3(xcd_head_grid(B * NSEG, H, ngrp)), dim3(256), 0, stream,
                        (const TK*)q, (const TK*)dO, gc, (const TL*)l, w.rsum, B, T, H, L, NT,
                        slog, NSEG, nloc, ntop, ngrp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kq = mamba2_bwd_dq_kernel<NP, TK, TV, TL>;
+    auto kq = mamba2_bwd_dq_kernel<NP, TK, TV, TL, E>;
     hipLaunchKernelGGL(kq, dim3(xcd_head_grid(B * NSEG, H, 1)), dim3(256), 0, stream,
                        (const TK*)q, (const TK*)k, (const TV*)v, (const TK*)dO, gc,
                        (const TL*)l, w.htop, (TK*)dq, dl, w.dgq, B, T, H, V, L, nlev, slog,
@@ -1370,7 +1374,7 @@ static hipError_t bwd_launch_t(const void* q, const void* k, const void* v, cons
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kk = mamba2_bwd_dkv_kernel<NP, TK, TV, TL>;
+    auto kk = mamba2_bwd_dkv_kernel<NP, TK, TV, TL, E>;
     hipLaunchKernelGGL(kk, dim3(rows * NSEG), dim3(512), 0, stream, (const TK*)q,
                        (const TK*)k, (const TV*)v, (const TK*)dO, gc, (const TL*)l,
                        w.rsum, segd, w.dgq, (TK*)dk, (TV*)dv, dg, w.segtot, B, T, H, V, L,
@@ -1406,6 +1410,17 @@ hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, 
     if (dt_v == 2 && dt_l == 2)
       return bwd_launch_t<2, float, float, float>(q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums,
                                                   fsegd, B, T, H, V, L, nlev, stream);
+    *unsupported = 1;
+    return hipSuccess;
+  }
+  if (dt_qk == 1) {
+    // fp16 q / k / dO on fp16 MFMA (fp32 lambda; v fp16 or fp32)
+    if (dt_l == 2 && dt_v == 1)
+      return bwd_launch_t<1, _Float16, _Float16, float, _Float16>(
+          q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
+    if (dt_l == 2 && dt_v == 2)
+      return bwd_launch_t<1, _Float16, float, float, _Float16>(
+          q, k, v, gc, l, dO, dq, dk, dv, dg, dl, ws, fsums, fsegd, B, T, H, V, L, nlev, stream);
     *unsupported = 1;
     return hipSuccess;
   }

@@ -293,7 +293,7 @@ __device__ __forceinline__ float seg_sum_body(SumSmem<NP>& sm, const TK* __restr
   return dsum;
 }
 
-template <typename TK, typename TV, bool GCUM, int NP>
+template <typename TK, typename TV, bool GCUM, int NP, typename E = __bf16>
 __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
     const TK* __restrict__ k, const TV* __restrict__ v, const float* __restrict__ g,
     float* __restrict__ sums, float* __restrict__ segd, int B, int T, int G, int H, int V,
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
   const int vblk = xm.slice, h = xm.h, p = xm.grp % NSEG, b = xm.grp / NSEG;
   const int row = b * H + h;
   float* out = sums + ((size_t)row * NSEG + p) * kKD * V + vblk * 64;
-  const float dsum = seg_sum_body<TK, TV, GCUM, NP, false>(sm, k, v, g, out, b, h, p, vblk, T, G,
+  const float dsum = seg_sum_body<TK, TV, GCUM, NP, false, false, 2, E>(sm, k, v, g, out, b, h, p, vblk, T, G,
                                                           H, V, NT, S);
   if (threadIdx.x == 0 && vblk == 0) segd[(size_t)row * NSEG + p] = dsum;
 }
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void mamba2_seg_sum_kernel(
 // 64 x 64 tile); each thread owns 4 consecutive elements and streams the
 // row's summaries.  Output: NP bf16 planes [row][p][e2][vblk][plane][64][64],
 // written only where segment p reads level e2.
-template <int NP>
+template <int NP, typename E = __bf16>
 __global__ __launch_bounds__(256) void mamba2_htop_kernel(const float* __restrict__ sums,
                                                           const float* __restrict__ segd,
                                                           __bf16* __restrict__ htop, int V,
@@ -363,8 +363,8 @@ __global__ __launch_bounds__(256) void mamba2_htop_kernel(const float* __restric
           bf16x4 hi, lo;
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            hi[jj] = (__bf16)h[e2][jj];
-            lo[jj] = bf16_lo(h[e2][jj], hi[jj]);
+            hi[jj] = to16<E>(h[e2][jj]);
+            if constexpr (NP == 2) lo[jj] = bf16_lo(h[e2][jj], hi[jj]);
           }
           __bf16* o = dst + (size_t)p * pstride + (size_t)e2 * estride;
           *(bf16x4*)o = hi;

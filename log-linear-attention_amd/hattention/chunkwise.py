@@ -65,9 +65,10 @@ def _validate(B, T, G, H, K, V, L, level_base, htype, chunk_size):
 
 
 def _native_half(q, k, v, l):
-    """The forward's fp16 path (HType.WEAK): fp16 q / k multiply natively on
-    fp16 MFMA, as the reference's fp16 dots do.  v stays fp16 (a bf16 v is read
-    as fp32, exact), lambda is read as fp32 (exact for fp16 and bf16)."""
+    """The fp16 path (HType.WEAK, forward and backward): fp16 q / k (and dO)
+    multiply natively on fp16 MFMA, as the reference's fp16 dots do.  v stays
+    fp16 (a bf16 v is read as fp32, exact), lambda is read as fp32 (exact for
+    fp16 and bf16)."""
     if v.dtype == torch.bfloat16:
         v = v.float().contiguous()
     if l.dtype != torch.float32:
@@ -76,7 +77,7 @@ def _native_half(q, k, v, l):
 
 
 def _widen_half(q, k, v, l):
-    """Where there is no fp16 kernel (the backward, HType.STRONG): fp16 values
+    """Where there is no fp16 kernel (HType.STRONG): fp16 values
     are exact in fp32, so fp16 q / k run the fp32-accurate (bf16x3) kernels,
     and fp16 v or lambda next to bf16 q / k are read as fp32; the caller
     returns o and the gradients in the inputs' dtypes."""
@@ -236,7 +237,8 @@ def chunkwise_bwd(
 ):
     """Log-linear Mamba-2 backward (chunkwise.py:1286-1597).
 
-    bf16 q / k run the bf16 MFMA kernels; fp32 q / k the bf16x3 kernels (every
+    bf16 q / k run the bf16 MFMA kernels, fp16 q / k the same kernels on fp16
+    MFMA (HType.WEAK); fp32 q / k the bf16x3 kernels (every
     product and every intermediate that feeds one as hi / lo bf16 planes,
     fp32-accurate), the counterpart of the reference's fp32 backward.
 
@@ -273,7 +275,10 @@ def chunkwise_bwd(
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
     q_dtype, k_dtype, v_dtype = q.dtype, k.dtype, v.dtype
-    q, k, v, l = _widen_half(q, k, v, l)
+    if q.dtype == torch.float16 and htype == HType.WEAK:
+        q, k, v, l = _native_half(q, k, v, l)
+    else:
+        q, k, v, l = _widen_half(q, k, v, l)
     do = do.to(q.dtype).contiguous()
     if q.dtype == torch.float32:
         # fp32 q / k run the bf16x3 (fp32-accurate) backward, which reads fp32 v,

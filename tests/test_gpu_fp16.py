@@ -1,12 +1,10 @@
 """fp16 inputs (the reference's kernels take fp16 q / k / v / lambda).
 
-The Mamba-2 forward (HType.WEAK) multiplies fp16 q / k / v natively on fp16
-MFMA (the fused single pass with fp16 operands; lambda read as fp32), as the
-reference's fp16 dots do.  Elsewhere the host layer widens fp16 exactly: the
-Mamba-2 backward runs the fp32-accurate (bf16x3) kernels on the widened
-inputs, and the output and gradients come back in the inputs' dtypes.  GDN
-rounds fp16 q / k / v to bf16 (its kernels read bf16) and reads fp16 beta /
-lambda as fp32.
+The Mamba-2 forward and backward (HType.WEAK) multiply fp16 q / k / v / dO
+natively on fp16 MFMA (the bf16 kernels with fp16 operands; lambda read as
+fp32), as the reference's fp16 dots do; the output and gradients come back in
+the inputs' dtypes.  GDN rounds fp16 q / k / v to bf16 (its kernels read bf16)
+and reads fp16 beta / lambda as fp32.
 
 Checks:
 * Mamba-2 forward with fp16 inputs against the fp64 oracle fed the same fp16
@@ -17,10 +15,11 @@ Checks:
   fp16 kernel, not the widening: the C-ABI accepts the fp16 dtype code and
   the result is farther from the oracle than the fp32-accurate run on the
   widened inputs (about 1e-5);
-* Mamba-2 backward with fp16 inputs: the bf16x3 kernels are fp32-accurate, so
-  the error is the final fp16 rounding of the gradients (2^-11 relative):
-  max-abs/rel below 2e-3, relative Frobenius below 1e-3 (dg, a reverse cumsum
-  with heavy cancellation, below 1e-2);
+* Mamba-2 backward with fp16 inputs against autograd through the fp64 oracle:
+  the kernels round their MFMA operands (staged tiles, the intra-chunk
+  matrices, the level states) to fp16, 2^-11 relative (measured 1.5e-4 ..
+  7e-4): max-abs/rel below 2e-3, relative Frobenius below 1e-3 (dg, a reverse
+  cumsum with heavy cancellation, below 1e-2);
 * GDN forward with fp16 inputs against the fp64 oracle on the same fp16
   values, to the bf16 tolerances of the GDN tests (2e-2 / 1e-2);
 * GDN backward with fp16 inputs equals the backward on the bf16-rounded
@@ -169,3 +168,19 @@ def test_mamba2_forward_fp16_native(T, final_state):
                 r = ht_ref[0, 0]
                 mxh = ((a - r).abs().max() / r.abs().max()).item()
                 assert mxh < 2e-3, (b, h, mxh)
+
+
+def test_mamba2_backward_fp16_takes_fp16_kernels():
+    """The C-ABI backward takes fp16 q / k / dO (past its dtype rules: a call with
+    null pointers fails as ValueError, not NotImplementedError), and fp16 needs
+    fp32 lambda."""
+    from hattention import _lib
+    lib = _lib.load()
+    p = None
+    H16 = _lib.DTYPE_CODES[HALF]
+
+    def call(dl):
+        return lib.hattn_mamba2_chunkwise_bwd(p, p, p, p, p, p, p, p, p, p, p, 1, 1024, 2, 64, 64,
+                                              11, H16, H16, dl, H16, 2, 0, 64, p, 1 << 30, p)
+    assert call(2) == _lib.HATTN_ERR_VALUE
+    assert call(H16) == _lib.HATTN_ERR_NOT_IMPLEMENTED

@@ -246,8 +246,10 @@ size_t hattn_mamba2_chunkwise_bwd_workspace(int B, int T, int H, int K, int V, i
  * Constraints: T % 64, L >= 7 + ceil(log2(T/64)), K and V multiples of 64,
  * T * H * max(K, V) < 2^31 -> HATTN_ERR_VALUE; K in {64, 128, 192, 256} (the
  * reference's limit is K <= 256, chunkwise_hgdn.py:600-601), any V multiple of
- * 64, T <= 64 * 2^8 (16384), q/k/v bf16, beta / l in {BF16, FP32}, o bf16 ->
- * HATTN_ERR_NOT_IMPLEMENTED.
+ * 64, T <= 64 * 2^8 (16384) -> HATTN_ERR_NOT_IMPLEMENTED.  dtype_qkv BF16: beta / l in
+ * {BF16, FP32}, o BF16 (bf16 MFMA); dtype_qkv FP16 (fp16 MFMA; q, k, v, o, Aw, Au
+ * and the saved states in fp16, as the reference's fp16 dots): HType.WEAK, beta
+ * and l FP32, o FP16; any other combination -> HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_gdn_chunkwise_fwd(const void* q, const void* k, const void* v, const void* beta,
                             const float* g, const void* l, void* o, float* g_cumsum, void* Aw,
@@ -318,7 +320,8 @@ size_t hattn_gdn_chunkwise_fwd_keep_workspace(int B, int T, int H, int K, int V,
  * Constraints as hattn_gdn_chunkwise_fwd, except K in {64, 128, 192, 256} and V in
  * {64, 128} -> HATTN_ERR_NOT_IMPLEMENTED (the gradients are sums over independent column
  * blocks of V, so a caller splits a larger V into blocks of 128 / 64 and sums
- * dq, dk, db, dg, dl; hattention.chunkwise_hgdn.chunkwise_bwd does); do bf16 ->
+ * dq, dk, db, dg, dl; hattention.chunkwise_hgdn.chunkwise_bwd does); dtype_do equal to
+ * dtype_qkv; FP16 (dq, dk, dv in fp16) with HType.WEAK and FP32 beta / l only;
  * else HATTN_ERR_NOT_IMPLEMENTED.
  */
 int hattn_gdn_chunkwise_bwd(const void* q, const void* k, const void* v, const void* beta,

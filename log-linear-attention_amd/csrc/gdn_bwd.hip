@@ -47,7 +47,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
                                       __bf16* qn, __bf16* kn, __bf16* knT, __bf16* wn, __bf16* un,
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
                                       int nlev, int dt_b, int dt_l, int norm_qk, float scale,
-                                      hipStream_t stream, int* unsupported);
+                                      int h16, hipStream_t stream, int* unsupported);
 
 namespace hattn {
 
@@ -82,7 +82,10 @@ struct GdnBscanSmem {
 template <int KD>
 constexpr int gdn_bscan_waves() { return 8; }
 
-template <int KD, typename TL>
+// E: the 16-bit format of q_new, W_new, K_new, U, dO and the saved states (bf16,
+// or fp16 for fp16 inputs; fp16 MFMA).  The per-V-slice partial gradients are
+// bf16 either way (summed in fp32 by the chunk kernel).
+template <int KD, typename TL, typename E = __bf16>
 __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ kn,
     const __bf16* __restrict__ un, const __bf16* __restrict__ dO, const float* __restrict__ gcum,
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
           const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
-          *(bf16x4*)(s.dhs + (16 * vv + ln) * LK + 16 * kt + 4 * lq) = cvt4(cur[j]);
+          *(bf16x4*)(s.dhs + (16 * vv + ln) * LK + 16 * kt + 4 * lq) = cvt4e<E>(cur[j]);
         }
         __syncthreads();
         {
@@ -234,8 +237,8 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
           const float la = s.lam[e][t];
           const bf16x4 x = *(const bf16x4*)(s.dO + t * LVS + c);
           *(bf16x4*)(s.ldo + t * LVS + c) =
-              bf16x4{(__bf16)((float)x[0] * la), (__bf16)((float)x[1] * la),
-                     (__bf16)((float)x[2] * la), (__bf16)((float)x[3] * la)};
+              bf16x4{to16<E>(from16<E>(x[0]) * la), to16<E>(from16<E>(x[1]) * la),
+                     to16<E>(from16<E>(x[2]) * la), to16<E>(from16<E>(x[3]) * la)};
         }
 
         // (i) dV_new = K_new dh, V_new = wr U - nr W_new h, q_new h (for dlambda)
@@ -249,19 +252,19 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
             if (KD > 128) __builtin_amdgcn_sched_barrier(0);
             const bf16x8 bd = *(const bf16x8*)(s.dhs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
             const bf16x8 bh = *(const bf16x8*)(s.hs + (16 * vt + ln) * LK + 32 * c + 8 * lq);
-            dv = mfma16x16x32(*(const bf16x8*)(s.kn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bd, dv);
-            y = mfma16x16x32(*(const bf16x8*)(s.wn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, y);
-            z = mfma16x16x32(*(const bf16x8*)(s.qn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, z);
+            dv = mfma16<E>(*(const bf16x8*)(s.kn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bd, dv);
+            y = mfma16<E>(*(const bf16x8*)(s.wn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, y);
+            z = mfma16<E>(*(const bf16x8*)(s.qn + (16 * tt + ln) * LK + 32 * c + 8 * lq), bh, z);
           }
           bf16x4 dvb, vnb;
           float dlr[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int t = 16 * tt + 4 * lq + i;
-            vnb[i] = (__bf16)(fwr * (float)s.u[t * LVS + 16 * vt + ln] - fnr * y[i]);
-            dvb[i] = (__bf16)dv[i];
+            vnb[i] = to16<E>(fwr * from16<E>(s.u[t * LVS + 16 * vt + ln]) - fnr * y[i]);
+            dvb[i] = to16<E>(dv[i]);
             adu[x][i] += fwr * dv[i];
-            dlr[i] = frd * (float)s.dO[t * LVS + 16 * vt + ln] * z[i];
+            dlr[i] = frd * from16<E>(s.dO[t * LVS + 16 * vt + ln]) * z[i];
           }
           *(bf16x4*)(s.dvn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = dvb;
           *(bf16x4*)(s.vn + (16 * vt + ln) * kLd64 + 16 * tt + 4 * lq) = vnb;
@@ -294,9 +297,9 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
             const int kt = vt0 * APW + j;
             const bf16x8 bh = tr_frag(s.hs, LK, 0, 16 * kt);    // h^T[v][k]
             const bf16x8 bd = tr_frag(s.dhs, LK, 0, 16 * kt);   // dh^T[v][k]
-            adq[j] = mfma16x16x32(adO, bh, adq[j]);
-            adw[j] = mfma16x16x32(advn, bh, adw[j]);
-            adk[j] = mfma16x16x32(avn, bd, adk[j]);
+            adq[j] = mfma16<E>(adO, bh, adq[j]);
+            adw[j] = mfma16<E>(advn, bh, adw[j]);
+            adk[j] = mfma16<E>(avn, bd, adk[j]);
           }
           float dd = 0.f;
 #pragma unroll
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
             const int kt = (w * TPW + j) >> 1, vv = (w * TPW + j) & 1;
             const bf16x4 hv4 = *(const bf16x4*)(s.hs + (16 * vv + ln) * LK + 16 * kt + 4 * lq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dd += (float)hv4[i] * cur[j][i];
+            for (int i = 0; i < 4; ++i) dd += from16<E>(hv4[i]) * cur[j][i];
           }
           del += fnr * dd;
         }
@@ -318,9 +321,9 @@ __global__ __launch_bounds__(64 * gdn_bscan_waves<KD>(), 1) void gdn_bwd_scan_ke
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             const bf16x8 bdv = *(const bf16x8*)(s.dvn + (16 * vv + ln) * kLd64 + 32 * c + 8 * lq);
-            tw = mfma16x16x32(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
+            tw = mfma16<E>(tr_frag(s.wn, LK, 32 * c, 16 * kt), bdv, tw);
             const bf16x8 x = tr_frag(s.ldo, LVS, 32 * c, 16 * vv);   // (lambda_e o dO)[t][v]
-            tq = mfma16x16x32(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
+            tq = mfma16<E>(tr_frag(s.qn, LK, 32 * c, 16 * kt), x, tq);
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) cur[j][i] = fnr * (eL * cur[j][i] - tw[i]) + frd * tq[i];
@@ -467,11 +470,23 @@ __device__ __forceinline__ floatx4 mma_ff(const float* a, const float* b, floatx
   split8<2>(b, Bf);
   return mma<2>(A, Bf, c);
 }
+// E = fp16: the fp16 operand is exact as bf16 hi + lo (8 + 8 bits of mantissa,
+// a wider exponent range), so the product is the bf16x3 one (three MFMAs).
+template <typename E = __bf16>
 __device__ __forceinline__ floatx4 mma_fb(const float* a, bf16x8 b, floatx4 c) {
   bf16x8 A[2];
   split8<2>(a, A);
-  c = mfma16x16x32(A[1], b, c);
-  return mfma16x16x32(A[0], b, c);
+  if constexpr (__is_same(E, _Float16)) {
+    float bf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bf[j] = from16<E>(b[j]);
+    bf16x8 Bp[2];
+    split8<2>(bf, Bp);
+    return mma<2>(A, Bp, c);
+  } else {
+    c = mfma16x16x32(A[1], b, c);
+    return mfma16x16x32(A[0], b, c);
+  }
 }
 // ST[t][c] = (scale ? scale[t] : 1) * sum over NP partials of X[t][c], 64 rows of N.
 // Two units per step with all their partial loads issued together.
@@ -541,7 +556,7 @@ __device__ __forceinline__ void rows_store(float* ST, const RowsPf<NP>& pf, cons
 // the rows are the gradient w.r.t. y = x r s (r = 1 / ||x||, staged y in Y)
 // and the stored gradient is w.r.t. x: r s (x - y' (y' . x)), y' = y / s.
 // yat(t, c): the staged (normalised, scaled) value of row t, column c.
-template <int NKT, typename YAt>
+template <int NKT, typename E, typename YAt>
 __device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], YAt yat,
                                                   const float* rinv, float inv_s, float s,
                                                   int norm, __bf16* out, size_t ld, int t16) {
@@ -559,13 +574,14 @@ __device__ __forceinline__ void store_l2norm_grad(float (&x)[NKT][4], YAt yat,
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt) {
       const float y = norm ? yat(t, 16 * nt + ln) * inv_s : 0.f;
-      out[t * ld + 16 * nt + ln] = (__bf16)(f * (x[nt][i] - y * dot));
+      out[t * ld + 16 * nt + ln] = to16<E>(f * (x[nt][i] - y * dot));
     }
   }
 }
 
 // STRONG: lambda of an intra-chunk pair at its strong level (the forward's P).
-template <int KD, int VD, typename TB, typename TL, bool STRONG = false>
+// E: the 16-bit format of q, k, v, dO, dq, dk, dv (bf16, or fp16 for fp16 inputs).
+template <int KD, int VD, typename TB, typename TL, bool STRONG = false, typename E = __bf16>
 __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ gcum, const TL* __restrict__ l,
@@ -604,18 +620,18 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   if (norm_qk) {
     // use_qk_l2norm_in_kernel: the gradients below are w.r.t. q scale / ||q|| and
     // k / ||k||; the chain rule back to q and k is applied where dq, dk are stored
-    if constexpr (QG) l2norm_rinv_global<KD>(q + rowk, hk, s.rq);
+    if constexpr (QG) l2norm_rinv_global<KD, E>(q + rowk, hk, s.rq);
     __syncthreads();
-    if constexpr (!QG) l2norm_rows<KD, LK>(s.q, qk_scale, s.rq);
-    l2norm_rows<KD, LK>(s.k, 1.f, s.rk);
+    if constexpr (!QG) l2norm_rows<KD, LK, 0, E>(s.q, qk_scale, s.rq);
+    l2norm_rows<KD, LK, 0, E>(s.k, 1.f, s.rk);
   }
   // the staged value of q[t][c] (QG: from global memory, normalised as staged)
   auto q_at = [&](int t, int c) -> float {
     if constexpr (QG) {
-      const float x = (float)q[rowk + (size_t)t * hk + c];
-      return norm_qk ? (float)(__bf16)((float)(__bf16)(x * s.rq[t]) * qk_scale) : x;
+      const float x = from16<E>(q[rowk + (size_t)t * hk + c]);
+      return norm_qk ? from16<E>(to16<E>(from16<E>(to16<E>(x * s.rq[t])) * qk_scale)) : x;
     } else {
-      return (float)s.q[t * LK + c];
+      return from16<E>(s.q[t * LK + c]);
     }
   };
   if (w == 0) {
@@ -660,15 +676,15 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       bf16x8 aq;
       if constexpr (QG) {
         aq = *(const bf16x8*)(q + rowk + (size_t)(t16 + ln) * hk + 32 * c + 8 * lq);
-        if (norm_qk) aq = l2norm_scale8(aq, s.rq[t16 + ln], qk_scale);
+        if (norm_qk) aq = l2norm_scale8<E>(aq, s.rq[t16 + ln], qk_scale);
       } else {
         aq = *(const bf16x8*)(s.q + (t16 + ln) * LK + 32 * c + 8 * lq);
       }
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
-        kk[nt] = mfma16x16x32(ak, bk, kk[nt]);
-        qk[nt] = mfma16x16x32(aq, bk, qk[nt]);
+        kk[nt] = mfma16<E>(ak, bk, kk[nt]);
+        qk[nt] = mfma16<E>(aq, bk, qk[nt]);
       }
     }
 #pragma unroll
@@ -720,7 +736,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       if (nt <= w) {
 #pragma unroll
         for (int c = 0; c < VD / 32; ++c)
-          z = mfma16x16x32(ad[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), z);
+          z = mfma16<E>(ad[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), z);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -790,7 +806,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       floatx4 f = zero4();
 #pragma unroll
       for (int c = 0; c < KD / 32; ++c)
-        f = mma_fb(ax[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f);
+        f = mma_fb<E>(ax[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = t16 + 4 * lq + i, sc = 16 * nt + ln;
@@ -863,10 +879,10 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       floatx4 f2 = zero4(), f3 = zero4();
 #pragma unroll
       for (int c = 0; c < KD / 32; ++c)
-        f2 = mma_fb(a2[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f2);
+        f2 = mma_fb<E>(a2[c], *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq), f2);
 #pragma unroll
       for (int c = 0; c < VD / 32; ++c)
-        f3 = mma_fb(a3[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), f3);
+        f3 = mma_fb<E>(a3[c], *(const bf16x8*)(v + rowv + (size_t)(16 * nt + ln) * hv + 32 * c + 8 * lq), f3);
       float cs = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -974,7 +990,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       for (int rr = 0; rr < 2; ++rr) {
         const int u = tid + 256 * rr, t = u >> 3, c = 8 * (u & 7);
         bf16x8 x = *(const bf16x8*)(q + rowk + (size_t)t * hk + k0 + c);
-        if (norm_qk) x = l2norm_scale8(x, s.rq[t], qk_scale);
+        if (norm_qk) x = l2norm_scale8<E>(x, s.rq[t], qk_scale);
         *(bf16x8*)(SQ + t * LDB + c) = x;
       }
     }
@@ -995,7 +1011,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       for (int c = 0; c < 2; ++c) {
         float am[8], ap[8], bx[8];
         frn<kLM>(S0, t16, 32 * c, am);
-        acc = mma_fb(am, tr_frag(s.k, LK, 32 * c, k0 + 16 * nt), acc);
+        acc = mma_fb<E>(am, tr_frag(s.k, LK, 32 * c, k0 + 16 * nt), acc);
         frt<kLM>(S3, t16, 32 * c, ap);
         frt<LS>(ST, 16 * nt, 32 * c, bx);
         a2 = mma_ff(ap, bx, a2);
@@ -1008,7 +1024,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
       const int t = tid >> 2, part = tid & 3;
 #pragma unroll
       for (int kk = 16 * part; kk < 16 * part + 16; ++kk)
-        qx += ST[t * LS + kk] * (float)QB[t * LQB + kq + kk];
+        qx += ST[t * LS + kk] * from16<E>(QB[t * LQB + kq + kk]);
     }
     __syncthreads();
 
@@ -1042,13 +1058,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
         const bf16x8 bq = tr_frag(QB, LQB, 32 * c, kq + 16 * nt);
         float ad[8], am[8], at[8];
         frn<kLM>(S1, t16, 32 * c, ad);
-        u2[nt] = mma_fb(ad, bk, u2[nt]);
+        u2[nt] = mma_fb<E>(ad, bk, u2[nt]);
         frt<kLM>(S0, t16, 32 * c, am);
-        a1 = mma_fb(am, bq, a1);
+        a1 = mma_fb<E>(am, bq, a1);
         frt<kLM>(S1, t16, 32 * c, at);
 #pragma unroll
         for (int j = 0; j < 8; ++j) at[j] *= s.beta[32 * c + 8 * lq + j];
-        a1 = mma_fb(at, bk, a1);
+        a1 = mma_fb<E>(at, bk, a1);
       }
       u1[nt] = a1;
     }
@@ -1066,7 +1082,7 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int sr = t16 + 4 * lq + i, kk = 16 * nt + ln;
-        const float kv = (float)s.k[sr * LK + k0 + kk], dkn = ST[sr * LS + kk];
+        const float kv = from16<E>(s.k[sr * LK + k0 + kk]), dkn = ST[sr * LS + kk];
         dkh[4 * kb + nt][i] = u1[nt][i] + s.beta[sr] * u2[nt][i] + s.r[sr] * dkn;
         rb[i] += kv * u2[nt][i];
         kd[i] += dkn * kv;
@@ -1075,9 +1091,9 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
   }
   // dq = dq_hat, or with the in-kernel normalisation x -> y = x r (r = 1 / ||x||)
   // scaled by s: dq = r s (dq_hat - y (y . dq_hat)) (fla l2norm_bwd, kernel.py:24-29)
-  store_l2norm_grad<NKT>(dqh, q_at, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
+  store_l2norm_grad<NKT, E>(dqh, q_at, s.rq, norm_qk ? 1.f / qk_scale : 1.f, qk_scale, norm_qk,
                          dq + rowk, hk, t16);
-  store_l2norm_grad<NKT>(dkh, [&](int t, int c) { return (float)s.k[t * LK + c]; }, s.rk, 1.f,
+  store_l2norm_grad<NKT, E>(dkh, [&](int t, int c) { return from16<E>(s.k[t * LK + c]); }, s.rk, 1.f,
                          1.f, norm_qk, dk + rowk, hk, t16);
   {
     qx += __shfl_xor(qx, 1, 64);
@@ -1129,13 +1145,13 @@ __global__ __launch_bounds__(256, 1) void gdn_bwd_chunk_kernel(
           float bu[8];
           frt<LS>(ST, 16 * nt, 32 * c, bu);
           acc = mma_ff(au[c], bu, acc);
-          acc = mma_fb(ar[c], tr_frag(SD, LDB, 32 * c, 16 * nt), acc);
+          acc = mma_fb<E>(ar[c], tr_frag(SD, LDB, 32 * c, 16 * nt), acc);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int sr = t16 + 4 * lq + i, vv = v0 + 16 * nt + ln;
-          dv[rowv + sr * hv + vv] = (__bf16)(s.beta[sr] * acc[i]);
-          rbv[i] += (float)v[rowv + sr * hv + vv] * acc[i];
+          dv[rowv + sr * hv + vv] = to16<E>(s.beta[sr] * acc[i]);
+          rbv[i] += from16<E>(v[rowv + sr * hv + vv]) * acc[i];
         }
       }
       __syncthreads();
@@ -1242,7 +1258,7 @@ inline GdnBwdWs gdn_bwd_ws_layout(void* base, int B, int T, int H, int K, int V,
   return w;
 }
 
-template <int KD, int VD, typename TB, typename TL, bool STRONG>
+template <int KD, int VD, typename TB, typename TL, bool STRONG, typename E = __bf16>
 static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const void* beta,
                             const float* gcum, const void* l, const void* dO, void* dq, void* dk,
                             void* dv, void* db, float* dg, float* dl, const GdnBwdWs& w, int B,
@@ -1251,7 +1267,7 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
   const int NT = T / kGC;
   hipError_t e;
   {
-    auto ks = gdn_bwd_scan_kernel<KD, TL>;
+    auto ks = gdn_bwd_scan_kernel<KD, TL, E>;
     const int smem = (int)sizeof(GdnBscanSmem<KD>);
     if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  smem)) != hipSuccess)
@@ -1263,7 +1279,7 @@ static hipError_t gdn_bwd_t(const void* q, const void* k, const void* v, const v
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   {
-    auto kc = gdn_bwd_chunk_kernel<KD, VD, TB, TL, STRONG>;
+    auto kc = gdn_bwd_chunk_kernel<KD, VD, TB, TL, STRONG, E>;
     const int smem = (int)sizeof(GdnBchunkSmem<KD, VD>);
     if ((e = hipFuncSetAttribute((const void*)kc, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  smem)) != hipSuccess)
@@ -1292,7 +1308,7 @@ hipError_t gdn_bwd_dispatch(const void* q, const void* k, const void* v, const v
                             const float* gcum, const void* l, const void* dO, void* dq, void* dk,
                             void* dv, void* db, float* dg, float* dl, const hattn::GdnBwdWs& w,
                             int B, int T, int H, int K, int V, int L, int nlev, int dt_b, int dt_l,
-                            int norm_qk, float scale, int strong, hipStream_t stream,
+                            int norm_qk, float scale, int strong, int h16, hipStream_t stream,
                             int* unsupported) {
   using namespace hattn;
 #define HATTN_GDN_BT(KD_, VD_, TB_, TL_)                                                        \
@@ -1302,8 +1318,17 @@ hipError_t gdn_bwd_dispatch(const void* q, const void* k, const void* v, const v
                 : gdn_bwd_t<KD_, VD_, TB_, TL_, false>(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, \
                                                        dg, dl, w, B, T, H, L, nlev, norm_qk,       \
                                                        scale, stream);
+// fp16 q/k/v: the weak hierarchy with fp32 beta / lambda only.
 #define HATTN_GDN_B(KD_, VD_)                                                                   \
   if (K == KD_ && V == VD_) {                                                                   \
+    if (h16) {                                                                                  \
+      if (!strong && dt_b == 2 && dt_l == 2)                                                    \
+        return gdn_bwd_t<KD_, VD_, float, float, false, _Float16>(                              \
+            q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, L, nlev, norm_qk,   \
+            scale, stream);                                                                     \
+      *unsupported = 1;                                                                         \
+      return hipSuccess;                                                                        \
+    }                                                                                           \
     if (dt_b == 0 && dt_l == 0) HATTN_GDN_BT(KD_, VD_, __bf16, __bf16)                          \
     if (dt_b == 2 && dt_l == 2) HATTN_GDN_BT(KD_, VD_, float, float)                            \
     if (dt_b == 0 && dt_l == 2) HATTN_GDN_BT(KD_, VD_, __bf16, float)                           \
@@ -1328,17 +1353,17 @@ hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, con
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, int norm_qk, float scale, int strong,
+                                int dt_l, int norm_qk, float scale, int strong, int h16,
                                 hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   const GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev);
   hipError_t e = hattn_gdn_recompute_launch(q, k, v, beta, gcum, l, w.qn, w.kn, w.knT, w.wn, w.un, w.hs,
                                             B, T, H, K, V, L, nlev, dt_b, dt_l, norm_qk, scale,
-                                            stream, unsupported);
+                                            h16, stream, unsupported);
   if (e != hipSuccess || *unsupported) return e;
   return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
-                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, stream, unsupported);
+                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, h16, stream, unsupported);
 }
 
 size_t hattn_gdn_bwd_kept_ws_bytes(int B, int T, int H, int K, int V, int nlev) {
@@ -1354,7 +1379,7 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
                                      const __bf16* kn, const __bf16* un, const __bf16* hs,
                                      void* ws, int B, int T, int H, int K, int V, int L, int nlev,
                                      int dt_b, int dt_l, int norm_qk, float scale, int strong,
-                                     hipStream_t stream, int* unsupported) {
+                                     int h16, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   GdnBwdWs w = gdn_bwd_ws_layout(ws, B, T, H, K, V, nlev, false);
@@ -1364,5 +1389,5 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
   w.un = const_cast<__bf16*>(un);
   w.hs = const_cast<__bf16*>(hs);
   return gdn_bwd_dispatch(q, k, v, beta, gcum, l, dO, dq, dk, dv, db, dg, dl, w, B, T, H, K, V,
-                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, stream, unsupported);
+                          L, nlev, dt_b, dt_l, norm_qk, scale, strong, h16, stream, unsupported);
 }

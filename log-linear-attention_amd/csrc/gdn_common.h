@@ -242,14 +242,16 @@ __device__ __forceinline__ void tri_inv64_mfma(const float* A, float* X, float* 
 // (consecutive lanes); rinv (if not null) receives 1 / sqrt(||x||^2 + eps) of
 // each row, for the backward's chain rule.
 // bf16(bf16(x * ri) * scale) of eight values (the stored l2norm output).
+// E: the 16-bit format of the stored values (bf16, or fp16 for fp16 inputs).
+template <typename E = __bf16>
 __device__ __forceinline__ bf16x8 l2norm_scale8(bf16x8 x, float ri, float scale) {
   bf16x8 y;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) y[i] = (__bf16)((float)(__bf16)((float)x[i] * ri) * scale);
+  for (int i = 0; i < 8; ++i) y[i] = to16<E>(from16<E>(to16<E>(from16<E>(x[i]) * ri)) * scale);
   return y;
 }
 
-template <int N, int LD, int T0 = 0>
+template <int N, int LD, int T0 = 0, typename E = __bf16>
 __device__ __forceinline__ void l2norm_rows(__bf16* X, float scale, float* rinv) {
   constexpr int PER = N / 4, NU = PER / 8;   // columns per thread, 16-byte units
   const int t = (int)threadIdx.x - T0, r = t >> 2, part = t & 3;
@@ -260,20 +262,20 @@ __device__ __forceinline__ void l2norm_rows(__bf16* X, float scale, float* rinv)
   for (int j = 0; j < NU; ++j) {
     u[j] = *(const bf16x8*)(row + 8 * j);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += (float)u[j][i] * (float)u[j][i];
+    for (int i = 0; i < 8; ++i) ss += from16<E>(u[j][i]) * from16<E>(u[j][i]);
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   const float ri = __builtin_amdgcn_rsqf(ss + 1e-6f);
 #pragma unroll
-  for (int j = 0; j < NU; ++j) *(bf16x8*)(row + 8 * j) = l2norm_scale8(u[j], ri, scale);
+  for (int j = 0; j < NU; ++j) *(bf16x8*)(row + 8 * j) = l2norm_scale8<E>(u[j], ri, scale);
   if (rinv != nullptr && part == 0) rinv[r] = ri;
 }
 
 // 1 / sqrt(||x||^2 + eps) of the 64 rows of a global bf16 tile (row stride
 // ld elements, N columns), with the arithmetic of l2norm_rows (same column
 // split and sum order, so the same value): four threads per row, rinv[r].
-template <int N>
+template <int N, typename E = __bf16>
 __device__ __forceinline__ void l2norm_rinv_global(const __bf16* X, size_t ld, float* rinv) {
   constexpr int PER = N / 4, NU = PER / 8;
   const int t = (int)threadIdx.x, r = t >> 2, part = t & 3;
@@ -285,7 +287,7 @@ __device__ __forceinline__ void l2norm_rinv_global(const __bf16* X, size_t ld, f
 #pragma unroll
   for (int j = 0; j < NU; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += (float)u[j][i] * (float)u[j][i];
+    for (int i = 0; i < 8; ++i) ss += from16<E>(u[j][i]) * from16<E>(u[j][i]);
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   if (part == 0) rinv[r] = __builtin_amdgcn_rsqf(ss + 1e-6f);

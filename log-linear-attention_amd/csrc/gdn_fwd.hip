@@ -75,7 +75,9 @@ enum { kPrepFwd = 0, kPrepRecompute = 1, kPrepFwdKeep = 2 };
 
 // STRONG: the P tile takes lambda at the strong level of each pair (the
 // reference's HType.STRONG, chunkwise_hgdn.py:630); only P depends on it.
-template <int KD, typename TB, typename TL, int MODE, bool STRONG = false>
+// E: the 16-bit format of q, k, v and of every stored intermediate (bf16, or
+// fp16 for fp16 inputs: fp16 MFMA, as the reference's fp16 dots).
+template <int KD, typename TB, typename TL, int MODE, bool STRONG = false, typename E = __bf16>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const TB* __restrict__ beta, const float* __restrict__ g, const TL* __restrict__ l,
@@ -166,8 +168,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     __syncthreads();
     if (norm_qk) {
       // use_qk_l2norm_in_kernel (kernel.py:110-111): k / ||k|| and q scale / ||q||
-      if (tid < 256) l2norm_rows<KD, LK>(s.k, 1.f, nullptr);
-      else l2norm_rows<KD, LK, 256>(s.q, qk_scale, nullptr);
+      if (tid < 256) l2norm_rows<KD, LK, 0, E>(s.k, 1.f, nullptr);
+      else l2norm_rows<KD, LK, 256, E>(s.q, qk_scale, nullptr);
       __syncthreads();
     }
   };
@@ -193,8 +195,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         for (int n = 0; n < 2; ++n) {
           const int nt = 2 * wh + n;
           const bf16x8 bk = *(const bf16x8*)(s.k + (16 * nt + ln) * LK + 32 * c + 8 * lq);
-          kk[n] = mfma16x16x32(ak, bk, kk[n]);
-          qk[n] = mfma16x16x32(aq, bk, qk[n]);
+          kk[n] = mfma16<E>(ak, bk, kk[n]);
+          qk[n] = mfma16<E>(aq, bk, qk[n]);
         }
       }
 #pragma unroll
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * tt + 4 * lq + i, sc = 16 * (2 * wh + n) + ln;
           A[t * kLM + sc] = sc < t ? s.beta[t] * kk[n][i] : 0.f;
-          s.mq[t * kLd64 + sc] = (__bf16)(sc <= t ? qk[n][i] : 0.f);
+          s.mq[t * kLd64 + sc] = to16<E>(sc <= t ? qk[n][i] : 0.f);
         }
     }
     __syncthreads();
@@ -220,8 +222,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
       for (int j = 0; j < 8; ++j) {
         const int sc = s0 + j;
         const float x = sc <= t ? X[t * kLM + sc] : 0.f;
-        a[j] = (__bf16)x;
-        au[j] = (__bf16)(sc <= t ? x * fexp(s.gc[t] - s.gc[sc]) : 0.f);
+        a[j] = to16<E>(x);
+        au[j] = to16<E>(sc <= t ? x * fexp(s.gc[t] - s.gc[sc]) : 0.f);
       }
       *(bf16x8*)(s.aw + t * kLd64 + s0) = a;
       *(bf16x8*)(s.au + t * kLd64 + s0) = au;
@@ -248,8 +250,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int st = 2 * wh + j;
-        floatx4 d = mfma16x16x32(tr_frag(s.aw, kLd64, 0, 16 * st), bm0, zero4());
-        d = mfma16x16x32(tr_frag(s.aw, kLd64, 32, 16 * st), bm1, d);
+        floatx4 d = mfma16<E>(tr_frag(s.aw, kLd64, 0, 16 * st), bm0, zero4());
+        d = mfma16<E>(tr_frag(s.aw, kLd64, 32, 16 * st), bm1, d);
         bf16x4 pb4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
           float x = 0.f;
           if (sc <= t)
             x = d[i] * fexp(s.gc[t] - s.gc[sc]) * s.beta[sc] * s.lam[gdn_intra_level<STRONG>(t, sc)][t];
-          pb4[i] = (__bf16)x;
+          pb4[i] = to16<E>(x);
         }
         *(bf16x4*)(pm + (((size_t)row * NT + ic) * kGC + t) * kGC + 16 * st + 4 * lq) = pb4;
       }
@@ -281,17 +283,17 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
           const floatx4 b1 = *(const floatx4*)(s.beta + 32 * c + 8 * lq + 4);
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            a[jj] = (__bf16)((float)a[jj] * b0[jj]);
-            a[4 + jj] = (__bf16)((float)a[4 + jj] * b1[jj]);
+            a[jj] = to16<E>(from16<E>(a[jj]) * b0[jj]);
+            a[4 + jj] = to16<E>(from16<E>(a[4 + jj]) * b1[jj]);
           }
-          d = mfma16x16x32(a, c ? ba1 : ba0, d);
+          d = mfma16<E>(a, c ? ba1 : ba0, d);
         }
         const int col = 16 * ct + 4 * lq;
-        *(bf16x4*)(s.wt.w + t * kLd64 + col) = cvt4(d);
+        *(bf16x4*)(s.wt.w + t * kLd64 + col) = cvt4e<E>(d);
         floatx4 dw = d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dw[i] *= egt;
-        *(bf16x4*)(wn + ((tok0 + t) * H + h) * KD + 64 * cb + col) = cvt4(dw);
+        *(bf16x4*)(wn + ((tok0 + t) * H + h) * KD + 64 * cb + col) = cvt4e<E>(dw);
       }
       // K_new = exp(Gc_last - Gc_t) K: transposed per chunk (thread: column tid >> 3,
       // tokens 8 (tid & 7) .. +7), and token-major for the backward
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
         bf16x8 x;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          x[j] = (__bf16)((float)s.k[(t8 + j) * LK + 64 * cb + col] * fexp(egl - s.gc[t8 + j]));
+          x[j] = to16<E>(from16<E>(s.k[(t8 + j) * LK + 64 * cb + col]) * fexp(egl - s.gc[t8 + j]));
         *(bf16x8*)(knT + (((size_t)row * NT + ic) * KD + 64 * cb + col) * kGC + t8) = x;
         if constexpr (MODE != kPrepFwd) {
           const int tr = tid >> 3, c8 = 8 * (tid & 7);
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
           const bf16x8 kx = *(const bf16x8*)(s.k + tr * LK + 64 * cb + c8);
           bf16x8 kb;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) kb[j] = (__bf16)((float)kx[j] * ek);
+          for (int j = 0; j < 8; ++j) kb[j] = to16<E>(from16<E>(kx[j]) * ek);
           *(bf16x8*)(kn + ((tok0 + tr) * H + h) * KD + 64 * cb + c8) = kb;
         }
       }
@@ -317,14 +319,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int ct = 2 * wh + j;
-        floatx4 d = mfma16x16x32(tr_frag(s.wt.w, kLd64, 0, 16 * ct), bq0, zero4());
-        d = mfma16x16x32(tr_frag(s.wt.w, kLd64, 32, 16 * ct), bq1, d);
+        floatx4 d = mfma16<E>(tr_frag(s.wt.w, kLd64, 0, 16 * ct), bq0, zero4());
+        d = mfma16<E>(tr_frag(s.wt.w, kLd64, 32, 16 * ct), bq1, d);
         const int col = 16 * ct + 4 * lq;
         const bf16x4 qx = *(const bf16x4*)(s.q + t * LK + 64 * cb + col);
         floatx4 r;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = egt * ((float)qx[i] - d[i]);
-        *(bf16x4*)(qn + ((tok0 + t) * H + h) * KD + 64 * cb + col) = cvt4(r);
+        for (int i = 0; i < 4; ++i) r[i] = egt * (from16<E>(qx[i]) - d[i]);
+        *(bf16x4*)(qn + ((tok0 + t) * H + h) * KD + 64 * cb + col) = cvt4e<E>(r);
       }
       __syncthreads();
     }
@@ -348,12 +350,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
           const floatx4 b1 = *(const floatx4*)(s.beta + 32 * c + 8 * lq + 4);
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            a[jj] = (__bf16)((float)a[jj] * b0[jj]);
-            a[4 + jj] = (__bf16)((float)a[4 + jj] * b1[jj]);
+            a[jj] = to16<E>(from16<E>(a[jj]) * b0[jj]);
+            a[4 + jj] = to16<E>(from16<E>(a[4 + jj]) * b1[jj]);
           }
-          d = mfma16x16x32(a, c ? bu1 : bu0, d);
+          d = mfma16<E>(a, c ? bu1 : bu0, d);
         }
-        *(bf16x4*)(un + ((tok0 + t) * H + h) * V + 64 * vb + 16 * ct + 4 * lq) = cvt4(d);
+        *(bf16x4*)(un + ((tok0 + t) * H + h) * V + 64 * vb + 16 * ct + 4 * lq) = cvt4e<E>(d);
       }
       __syncthreads();
     };
@@ -434,7 +436,7 @@ __device__ __forceinline__ bf16x8 frag_k2(const __bf16* X, int ld, int r, int c)
 // from it.  Separate instantiations, so the plain forward carries no
 // registers for the states' stores.
 enum { kScanOut = 0, kScanSave = 1, kScanOutSave = 2 };
-template <int KD, int BV, typename TL, typename TO, int SMODE>
+template <int KD, int BV, typename TL, typename TO, int SMODE, typename E = __bf16>
 __global__ __launch_bounds__(512) void gdn_scan_kernel(
     const __bf16* __restrict__ qn, const __bf16* __restrict__ wn, const __bf16* __restrict__ knT,
     const __bf16* __restrict__ un, const __bf16* __restrict__ pm, const __bf16* __restrict__ vin,
@@ -582,7 +584,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int nt = 0; nt < NVT; ++nt)
-          buf_store8(__builtin_bit_cast(uint2, cvt4(st[kt][nt])), rh,
+          buf_store8(__builtin_bit_cast(uint2, cvt4e<E>(st[kt][nt])), rh,
                      (unsigned)(((16 * nt + ln) * KD + 16 * kt + 4 * lq) * 2),
                      (unsigned)((size_t)ic * nlev * V * KD * 2));
     }
@@ -598,12 +600,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
         for (int c = 0; c < NC; ++c) {
           bf16x8 bh[NVT];
 #pragma unroll
-          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8(st[2 * c][nt], st[2 * c + 1][nt]);
+          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8e<E>(st[2 * c][nt], st[2 * c + 1][nt]);
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt) {
             const bf16x8 a = frag_k2(s.wq[1], LK, 16 * tt + ln, 32 * c + 4 * lq);
 #pragma unroll
-            for (int nt = 0; nt < NVT; ++nt) racc[tt][nt] = mfma16x16x32(a, bh[nt], racc[tt][nt]);
+            for (int nt = 0; nt < NVT; ++nt) racc[tt][nt] = mfma16<E>(a, bh[nt], racc[tt][nt]);
           }
         }
 #pragma unroll
@@ -628,7 +630,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
             const bf16x8 a = *(const bf16x8*)(s.pm + (16 * tt + ln) * LT + 32 * c + 8 * lq);
 #pragma unroll
             for (int nt = 0; nt < NVT; ++nt)
-              x[nt] = mfma16x16x32(a, tr_frag(s.vs, LVS, 32 * c, 16 * nt), x[nt]);
+              x[nt] = mfma16<E>(a, tr_frag(s.vs, LVS, 32 * c, 16 * nt), x[nt]);
           }
 #pragma unroll
           for (int nt = 0; nt < NVT; ++nt)
@@ -657,12 +659,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
         for (int c = 0; c < NC; ++c) {
           bf16x8 bh[NVT];
 #pragma unroll
-          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8(st[2 * c][nt], st[2 * c + 1][nt]);
+          for (int nt = 0; nt < NVT; ++nt) bh[nt] = cat8e<E>(st[2 * c][nt], st[2 * c + 1][nt]);
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt) {
             const bf16x8 a = frag_k2(s.wq[0], LK, 16 * tt + ln, 32 * c + 4 * lq);
 #pragma unroll
-            for (int nt = 0; nt < NVT; ++nt) vn[tt][nt] = mfma16x16x32(a, bh[nt], vn[tt][nt]);
+            for (int nt = 0; nt < NVT; ++nt) vn[tt][nt] = mfma16<E>(a, bh[nt], vn[tt][nt]);
           }
         }
       }
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
           for (int nt = 0; nt < NVT; ++nt) {
             const bf16x4 u4 = *(const bf16x4*)(s.ut + (16 * nt + ln) * LT + 16 * tt + 4 * lq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vn[tt][nt][i] = (float)u4[i] - vn[tt][nt][i];
+            for (int i = 0; i < 4; ++i) vn[tt][nt][i] = from16<E>(u4[i]) - vn[tt][nt][i];
           }
       } else {
 #pragma unroll
@@ -690,12 +692,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(
       for (int c = 0; c < 2; ++c) {
         bf16x8 bv[NVT];
 #pragma unroll
-        for (int nt = 0; nt < NVT; ++nt) bv[nt] = cat8(vn[2 * c][nt], vn[2 * c + 1][nt]);
+        for (int nt = 0; nt < NVT; ++nt) bv[nt] = cat8e<E>(vn[2 * c][nt], vn[2 * c + 1][nt]);
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
           const bf16x8 a = frag_k2(s.kt, LT, 16 * kt + ln, 32 * c + 4 * lq);
 #pragma unroll
-          for (int nt = 0; nt < NVT; ++nt) st[kt][nt] = mfma16x16x32(a, bv[nt], st[kt][nt]);
+          for (int nt = 0; nt < NVT; ++nt) st[kt][nt] = mfma16<E>(a, bv[nt], st[kt][nt]);
         }
       }
     }
@@ -790,13 +792,13 @@ inline int device_cus() {
   return cus[dev];
 }
 
-template <int KD, typename TB, typename TL, int MODE, bool STRONG = false>
+template <int KD, typename TB, typename TL, int MODE, bool STRONG = false, typename E = __bf16>
 static hipError_t gdn_prep_launch_t(const void* q, const void* k, const void* v, const void* beta,
                                     const float* g, const void* l, float* gcum, void* aw, void* au,
                                     __bf16* qn, __bf16* wn, __bf16* kn, __bf16* knT, __bf16* un,
                                     __bf16* pm, int B, int T, int H, int V, int L, int norm_qk,
                                     float scale, hipStream_t stream) {
-  auto kp = gdn_prep_kernel<KD, TB, TL, MODE, STRONG>;
+  auto kp = gdn_prep_kernel<KD, TB, TL, MODE, STRONG, E>;
   const int smem = (int)sizeof(GdnPrepSmem<KD>);
   hipError_t e;
   if ((e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -812,16 +814,16 @@ static hipError_t gdn_prep_launch_t(const void* q, const void* k, const void* v,
   return hipGetLastError();
 }
 
-template <int KD, typename TL, typename TO>
+template <int KD, typename TL, typename TO, typename E = __bf16>
 static hipError_t gdn_scan_launch_t(const GdnWs& w, const void* v, const float* gcum,
                                     const void* l, void* o, float* ht, __bf16* hsave, int B,
                                     int T, int H, int V, int L, int nlev, int final_state,
                                     int strong, hipStream_t stream) {
   constexpr int BV = ScanBV<KD>::value;
   // hsave without o: the recompute; both: a forward that keeps the states
-  auto ks = !hsave ? gdn_scan_kernel<KD, BV, TL, TO, kScanOut>
-            : o ? gdn_scan_kernel<KD, BV, TL, TO, kScanOutSave>
-                : gdn_scan_kernel<KD, BV, TL, TO, kScanSave>;
+  auto ks = !hsave ? gdn_scan_kernel<KD, BV, TL, TO, kScanOut, E>
+            : o ? gdn_scan_kernel<KD, BV, TL, TO, kScanOutSave, E>
+                : gdn_scan_kernel<KD, BV, TL, TO, kScanSave, E>;
   const int smem = (int)sizeof(GdnScanSmem<KD, BV>);
   hipError_t e;
   if ((e = hipFuncSetAttribute((const void*)ks, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -835,31 +837,31 @@ static hipError_t gdn_scan_launch_t(const GdnWs& w, const void* v, const float* 
   return hipGetLastError();
 }
 
-template <int KD, typename TB, typename TL, typename TO, bool STRONG>
+template <int KD, typename TB, typename TL, typename TO, bool STRONG, typename E = __bf16>
 static hipError_t gdn_launch_t(const void* q, const void* k, const void* v, const void* beta,
                                const float* g, const void* l, void* o, float* gcum, void* aw,
                                void* au, float* ht, void* ws, int B, int T, int H, int V, int L,
                                int nlev, int norm_qk, float scale, hipStream_t stream) {
   const GdnWs w = gdn_ws_layout(ws, B, T, H, KD, V);
-  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwd, STRONG>(
+  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwd, STRONG, E>(
       q, k, v, beta, g, l, gcum, aw, au, w.qn, w.wn, nullptr, w.knT, w.un, w.pm, B, T, H, V, L,
       norm_qk, scale, stream);
   if (e != hipSuccess) return e;
-  return gdn_scan_launch_t<KD, TL, TO>(w, v, gcum, l, o, ht, nullptr, B, T, H, V, L, nlev,
+  return gdn_scan_launch_t<KD, TL, TO, E>(w, v, gcum, l, o, ht, nullptr, B, T, H, V, L, nlev,
                                        ht != nullptr ? 1 : 0, STRONG ? 1 : 0, stream);
 }
 
-template <int KD, typename TB, typename TL, typename TO, bool STRONG>
+template <int KD, typename TB, typename TL, typename TO, bool STRONG, typename E = __bf16>
 static hipError_t gdn_launch_keep_t(const void* q, const void* k, const void* v, const void* beta,
                                     const float* g, const void* l, void* o, float* gcum, void* aw,
                                     void* au, float* ht, void* ws, int B, int T, int H, int V,
                                     int L, int nlev, int norm_qk, float scale, hipStream_t stream) {
   const GdnKeepWs w = gdn_keep_ws_layout(ws, B, T, H, KD, V, nlev);
-  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwdKeep, STRONG>(
+  hipError_t e = gdn_prep_launch_t<KD, TB, TL, kPrepFwdKeep, STRONG, E>(
       q, k, v, beta, g, l, gcum, aw, au, w.f.qn, w.f.wn, w.kn, w.f.knT, w.f.un, w.f.pm, B, T, H,
       V, L, norm_qk, scale, stream);
   if (e != hipSuccess) return e;
-  return gdn_scan_launch_t<KD, TL, TO>(w.f, v, gcum, l, o, ht, w.hs, B, T, H, V, L, nlev,
+  return gdn_scan_launch_t<KD, TL, TO, E>(w.f, v, gcum, l, o, ht, w.hs, B, T, H, V, L, nlev,
                                        ht != nullptr ? 1 : 0, STRONG ? 1 : 0, stream);
 }
 
@@ -887,9 +889,25 @@ hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v
                                      float* gcum, void* aw, void* au, float* ht, void* ws, int B,
                                      int T, int H, int K, int V, int L, int nlev, int dt_b,
                                      int dt_l, int dt_o, int norm_qk, float scale, int strong,
-                                     hipStream_t stream, int* unsupported) {
+                                     int h16, hipStream_t stream, int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
+  if (h16) {
+    // fp16 q / k / v and o on fp16 MFMA (HType.WEAK, fp32 beta and lambda)
+#define HATTN_GDN_KH(KD_)                                                                       \
+  if (K == KD_)                                                                                 \
+    return gdn_launch_keep_t<KD_, float, float, _Float16, false, _Float16>(                     \
+        q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, H, V, L, nlev, norm_qk, scale, stream);
+    if (!strong && dt_b == 2 && dt_l == 2 && dt_o == 1) {
+      HATTN_GDN_KH(64)
+      HATTN_GDN_KH(128)
+      HATTN_GDN_KH(192)
+      HATTN_GDN_KH(256)
+    }
+#undef HATTN_GDN_KH
+    *unsupported = 1;
+    return hipSuccess;
+  }
 #define HATTN_GDN_KDT(KD_, TB_, TL_)                                                            \
   return strong ? gdn_launch_keep_t<KD_, TB_, TL_, __bf16, true>(                                 \
                       q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, H, V, L, nlev, norm_qk,  \
@@ -927,9 +945,26 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
-                                float scale, int strong, hipStream_t stream, int* unsupported) {
+                                float scale, int strong, int h16, hipStream_t stream,
+                                int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
+  if (h16) {
+    // fp16 q / k / v and o on fp16 MFMA (HType.WEAK, fp32 beta and lambda)
+#define HATTN_GDN_H(KD_)                                                                        \
+  if (K == KD_)                                                                                 \
+    return gdn_launch_t<KD_, float, float, _Float16, false, _Float16>(                          \
+        q, k, v, beta, g, l, o, gcum, aw, au, ht, ws, B, T, H, V, L, nlev, norm_qk, scale, stream);
+    if (!strong && dt_b == 2 && dt_l == 2 && dt_o == 1) {
+      HATTN_GDN_H(64)
+      HATTN_GDN_H(128)
+      HATTN_GDN_H(192)
+      HATTN_GDN_H(256)
+    }
+#undef HATTN_GDN_H
+    *unsupported = 1;
+    return hipSuccess;
+  }
 #define HATTN_GDN_DT(KD_, TB_, TL_)                                                             \
   return strong ? gdn_launch_t<KD_, TB_, TL_, __bf16, true>(q, k, v, beta, g, l, o, gcum, aw, au, \
                                                             ht, ws, B, T, H, V, L, nlev, norm_qk,  \
@@ -963,7 +998,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
                                       __bf16* qn, __bf16* kn, __bf16* knT, __bf16* wn, __bf16* un,
                                       __bf16* hsave, int B, int T, int H, int K, int V, int L,
                                       int nlev, int dt_b, int dt_l, int norm_qk, float scale,
-                                      hipStream_t stream, int* unsupported) {
+                                      int h16, hipStream_t stream, int* unsupported) {
   // the recompute writes the level states only, which do not depend on the
   // hierarchy type (strong changes the reads), so it has no strong flag
   using namespace hattn;
@@ -974,14 +1009,25 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
   w.knT = knT;
   w.un = un;
   w.pm = qn;   // read but unused without an output
-#define HATTN_GDN_RC(KD_, TB_, TL_)                                                               \
+#define HATTN_GDN_RCE(KD_, TB_, TL_, E_)                                                          \
   {                                                                                               \
-    hipError_t e = gdn_prep_launch_t<KD_, TB_, TL_, kPrepRecompute>(                              \
+    hipError_t e = gdn_prep_launch_t<KD_, TB_, TL_, kPrepRecompute, false, E_>(                   \
         q, k, v, beta, gcum, l, nullptr, nullptr, nullptr, qn, wn, kn, knT, un, nullptr, B, T, H, \
         V, L, norm_qk, scale, stream);                                                            \
     if (e != hipSuccess) return e;                                                                \
-    return gdn_scan_launch_t<KD_, TL_, __bf16>(w, v, gcum, l, nullptr, nullptr, hsave, B, T, H, V, \
-                                               L, nlev, 0, 0, stream);                            \
+    return gdn_scan_launch_t<KD_, TL_, __bf16, E_>(w, v, gcum, l, nullptr, nullptr, hsave, B, T, \
+                                                   H, V, L, nlev, 0, 0, stream);                  \
+  }
+#define HATTN_GDN_RC(KD_, TB_, TL_) HATTN_GDN_RCE(KD_, TB_, TL_, __bf16)
+  if (h16) {
+    if (dt_b == 2 && dt_l == 2) {
+      if (K == 64) HATTN_GDN_RCE(64, float, float, _Float16)
+      if (K == 128) HATTN_GDN_RCE(128, float, float, _Float16)
+      if (K == 192) HATTN_GDN_RCE(192, float, float, _Float16)
+      if (K == 256) HATTN_GDN_RCE(256, float, float, _Float16)
+    }
+    *unsupported = 1;
+    return hipSuccess;
   }
 #define HATTN_GDN_RC_D(KD_)                                                                      \
   if (K == KD_) {                                                                                \
@@ -996,6 +1042,7 @@ hipError_t hattn_gdn_recompute_launch(const void* q, const void* k, const void* 
   HATTN_GDN_RC_D(256)
 #undef HATTN_GDN_RC_D
 #undef HATTN_GDN_RC
+#undef HATTN_GDN_RCE
   *unsupported = 1;
   return hipSuccess;
 }

@@ -52,14 +52,15 @@ hipError_t hattn_gdn_fwd_launch(const void* q, const void* k, const void* v, con
                                 const float* g, const void* l, void* o, float* gcum, void* aw,
                                 void* au, float* ht, void* ws, int B, int T, int H, int K, int V,
                                 int L, int nlev, int dt_b, int dt_l, int dt_o, int norm_qk,
-                                float scale, int strong, hipStream_t stream, int* unsupported);
+                                float scale, int strong, int h16, hipStream_t stream,
+                                int* unsupported);
 size_t hattn_gdn_fwd_keep_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_fwd_keep_launch(const void* q, const void* k, const void* v,
                                      const void* beta, const float* g, const void* l, void* o,
                                      float* gcum, void* aw, void* au, float* ht, void* ws, int B,
                                      int T, int H, int K, int V, int L, int nlev, int dt_b,
                                      int dt_l, int dt_o, int norm_qk, float scale, int strong,
-                                     hipStream_t stream, int* unsupported);
+                                     int h16, hipStream_t stream, int* unsupported);
 void hattn_gdn_fwd_keep_buffers(const void* ws, int B, int T, int H, int K, int V, int nlev,
                                 const __bf16** qn, const __bf16** wn, const __bf16** kn,
                                 const __bf16** un, const __bf16** hs);
@@ -71,13 +72,13 @@ hipError_t hattn_gdn_bwd_kept_launch(const void* q, const void* k, const void* v
                                      const __bf16* kn, const __bf16* un, const __bf16* hs,
                                      void* ws, int B, int T, int H, int K, int V, int L, int nlev,
                                      int dt_b, int dt_l, int norm_qk, float scale, int strong,
-                                     hipStream_t stream, int* unsupported);
+                                     int h16, hipStream_t stream, int* unsupported);
 size_t hattn_gdn_bwd_ws_bytes(int B, int T, int H, int K, int V, int nlev);
 hipError_t hattn_gdn_bwd_launch(const void* q, const void* k, const void* v, const void* beta,
                                 const float* gcum, const void* l, const void* dO, void* dq,
                                 void* dk, void* dv, void* db, float* dg, float* dl, void* ws,
                                 int B, int T, int H, int K, int V, int L, int nlev, int dt_b,
-                                int dt_l, int norm_qk, float scale, int strong,
+                                int dt_l, int norm_qk, float scale, int strong, int h16,
                                 hipStream_t stream, int* unsupported);
 size_t hattn_mamba2_bwd_ws_bytes(int B, int T, int H, int V, int nlev);
 hipError_t hattn_mamba2_bwd_launch(const void* q, const void* k, const void* v, const float* gc,
@@ -538,8 +539,9 @@ static int gdn_fwd_impl(const void* q, const void* k, const void* v, const void*
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_fwd_max_levels());
   if ((size_t)T * H * (K > V ? K : V) >= ((size_t)1 << 31))
     return fail(HATTN_ERR_VALUE, "T * H * max(K, V) = %zu exceeds 2^31", (size_t)T * H * (K > V ? K : V));
-  if (dtype_qkv != HATTN_BF16)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v dtype code %d (bf16 required)", dtype_qkv);
+  // fp16 q/k/v (fp16 MFMA): HType.WEAK with fp32 beta / lambda and an fp16 o
+  if (dtype_qkv != HATTN_BF16 && dtype_qkv != HATTN_FP16)
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v dtype code %d (bf16 or fp16 required)", dtype_qkv);
   if (keep && !(V == 64 || V == 128))
     return fail(HATTN_ERR_NOT_IMPLEMENTED,
                 "V=%d: the kept buffers serve a backward in one V block (V in {64, 128})", V);
@@ -558,10 +560,14 @@ static int gdn_fwd_impl(const void* q, const void* k, const void* v, const void*
       (keep ? hattn_gdn_fwd_keep_launch : hattn_gdn_fwd_launch)(
           q, k, v, beta, g, l, o, g_cumsum, Aw, Au, ht, workspace, B, T, H, K, V, L, nlev,
           dtype_beta, dtype_l, dtype_o, l2norm_qk ? 1 : 0, qk_scale,
-          htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream, &unsupported);
+          htype == HATTN_HTYPE_STRONG ? 1 : 0, dtype_qkv == HATTN_FP16 ? 1 : 0,
+          (hipStream_t)stream, &unsupported);
   if (unsupported)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d o=%d", dtype_beta,
-                dtype_l, dtype_o);
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k/v=%d beta=%d l=%d o=%d%s",
+                dtype_qkv, dtype_beta, dtype_l, dtype_o,
+                dtype_qkv == HATTN_FP16 ? " (fp16 q/k/v need fp32 beta and lambda, an fp16 o and "
+                                          "HType.WEAK)"
+                                        : "");
   return check_hip(e, keep ? "hattn_gdn_chunkwise_fwd_keep launch" : "hattn_gdn_chunkwise_fwd launch");
 }
 
@@ -633,8 +639,9 @@ static int gdn_bwd_impl(const void* q, const void* k, const void* v, const void*
     return fail(HATTN_ERR_VALUE, "L=%d levels < 7 + ceil(log2(T/64))=%d", L, 7 + nlev);
   if (nlev > hattn_gdn_bwd_max_levels())
     return fail(HATTN_ERR_NOT_IMPLEMENTED, "T=%d exceeds 64 * 2^%d", T, hattn_gdn_bwd_max_levels());
-  if (dtype_qkv != HATTN_BF16 || dtype_do != HATTN_BF16)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "q/k/v/do dtype codes %d/%d (bf16 required)", dtype_qkv,
+  if (!((dtype_qkv == HATTN_BF16 || dtype_qkv == HATTN_FP16) && dtype_do == dtype_qkv))
+    return fail(HATTN_ERR_NOT_IMPLEMENTED,
+                "q/k/v/do dtype codes %d/%d (bf16 or fp16, the same for all four)", dtype_qkv,
                 dtype_do);
   if (!q || !k || !v || !beta || !g_cumsum || !l || !do_ || !dq || !dk || !dv || !db || !dg || !dl)
     return fail(HATTN_ERR_VALUE, "null tensor pointer");
@@ -658,16 +665,20 @@ static int gdn_bwd_impl(const void* q, const void* k, const void* v, const void*
     e = hattn_gdn_bwd_kept_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, qn, wn,
                                   kn, un, hs, workspace, B, T, H, K, V, L, nlev, dtype_beta,
                                   dtype_l, l2norm_qk ? 1 : 0, qk_scale,
-                                  htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream,
+                                  htype == HATTN_HTYPE_STRONG ? 1 : 0,
+                                  dtype_qkv == HATTN_FP16 ? 1 : 0, (hipStream_t)stream,
                                   &unsupported);
   } else {
     e = hattn_gdn_bwd_launch(q, k, v, beta, g_cumsum, l, do_, dq, dk, dv, db, dg, dl, workspace,
                              B, T, H, K, V, L, nlev, dtype_beta, dtype_l, l2norm_qk ? 1 : 0,
-                             qk_scale, htype == HATTN_HTYPE_STRONG ? 1 : 0, (hipStream_t)stream,
-                             &unsupported);
+                             qk_scale, htype == HATTN_HTYPE_STRONG ? 1 : 0,
+                             dtype_qkv == HATTN_FP16 ? 1 : 0, (hipStream_t)stream, &unsupported);
   }
   if (unsupported)
-    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination beta=%d l=%d", dtype_beta, dtype_l);
+    return fail(HATTN_ERR_NOT_IMPLEMENTED, "dtype combination q/k/v=%d beta=%d l=%d%s", dtype_qkv,
+                dtype_beta, dtype_l,
+                dtype_qkv == HATTN_FP16 ? " (fp16 q/k/v need fp32 beta and lambda and HType.WEAK)"
+                                        : "");
   return check_hip(e, kept ? "hattn_gdn_chunkwise_bwd_fwd_ws launch" : "hattn_gdn_chunkwise_bwd launch");
 }
 

@@ -70,13 +70,17 @@ def _validate(q, k, v, l, head_first, level_base, htype, chunk_size, **tensors):
     return B, T, G, H, K, V, L
 
 
-def _narrow_half(q, k, v, b, l):
-    """fp16 inputs have no kernels of their own: fp16 q / k / v are rounded to
-    bf16 on the device (the GDN kernels read bf16; the reference's fp16 dots
-    keep three more mantissa bits of the inputs), fp16 beta and lambda are
-    read as fp32 (exact).  The caller returns the outputs and gradients in the
-    inputs' dtypes."""
+def _narrow_half(q, k, v, b, l, htype):
+    """fp16 q / k / v with HType.WEAK run on kernels of their own (fp16 MFMA
+    operands, fp16 o, gradients and saved states, as the reference's fp16 dots
+    take them); those kernels read beta and lambda as fp32, so any 16-bit beta
+    or lambda is widened (exact).  HType.STRONG has no fp16 kernels: fp16
+    q / k / v are rounded to bf16 on the device (the reference's fp16 dots keep
+    three more mantissa bits of the inputs), fp16 beta and lambda read as fp32.
+    The caller returns the outputs and gradients in the inputs' dtypes."""
     half = torch.float16
+    if q.dtype == half and htype == HType.WEAK:
+        return q, k, v, b.float().contiguous(), l.float().contiguous()
     if q.dtype == half:
         q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
     if b.dtype == half:
@@ -141,7 +145,7 @@ def chunkwise_fwd_keep(
         raise ValueError("g (log-decay) must be float32")
     dev = _lib.require_device(q, k, v, b, g, l)
     o_dtype, k_dtype = v.dtype, k.dtype
-    q, k, v, b, l = _narrow_half(q, k, v, b, l)
+    q, k, v, b, l = _narrow_half(q, k, v, b, l, htype)
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()
         k = k.repeat_interleave(H // G, dim=2).contiguous()
@@ -211,7 +215,7 @@ def chunkwise_bwd(
         raise ValueError("do must have the shape of v")
     dev = _lib.require_device(q, k, v, b, g, l, do)
     dtypes = (q.dtype, k.dtype, v.dtype, b.dtype)
-    q, k, v, b, l = _narrow_half(q, k, v, b, l)
+    q, k, v, b, l = _narrow_half(q, k, v, b, l, htype)
     Aw, Au = Aw.to(k.dtype), Au.to(k.dtype)
     if G != H:
         q = q.repeat_interleave(H // G, dim=2).contiguous()

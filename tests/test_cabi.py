@@ -215,6 +215,9 @@ def _gdn_bwd(**kw):
     (dict(htype=1), _lib.HATTN_ERR_VALUE),          # STRONG valid: fails on the null pointers
     (dict(htype=2), _lib.HATTN_ERR_VALUE),          # neither WEAK nor STRONG
     (dict(do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),   # do must be bf16
+    (dict(dq=1, do=0), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # fp16 q/k/v need an fp16 do
+    (dict(dq=1, do=1), _lib.HATTN_ERR_VALUE),       # fp16 valid: fails on the null pointers
+    (dict(dq=2, do=2), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # no fp32 q/k/v kernels
     (dict(T=64 << 9, L=17), _lib.HATTN_ERR_NOT_IMPLEMENTED),  # > 8 inter-chunk levels
     (dict(ws=16), _lib.HATTN_ERR_VALUE),            # workspace too small
 ])
@@ -257,6 +260,23 @@ def test_gdn_keep_forward_argument_checks():
     assert call(192) == _lib.HATTN_ERR_NOT_IMPLEMENTED
     assert "V=192" in lib.hattn_last_error().decode()
     assert call(128) == _lib.HATTN_ERR_VALUE   # valid shape: fails on the null pointers
+
+
+def test_gdn_forward_dtype_codes():
+    """q/k/v dtype codes the GDN forward takes: bf16 and fp16 (fp16 with fp32
+    beta / lambda, fp16 o and HType.WEAK is checked at dispatch, after the null
+    pointer check); fp32 has no kernels."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(None)
+
+    def call(dt_qkv):
+        return lib.hattn_gdn_chunkwise_fwd(p, p, p, p, p, p, p, p, p, p, p, 1, 256, 2, 64, 64, 9,
+                                           dt_qkv, 2, 2, dt_qkv, 2, 0, 64, 0, 1.0, p, 1 << 30,
+                                           None)
+    assert call(0) == _lib.HATTN_ERR_VALUE
+    assert call(1) == _lib.HATTN_ERR_VALUE
+    assert call(2) == _lib.HATTN_ERR_NOT_IMPLEMENTED
+    assert "bf16 or fp16" in lib.hattn_last_error().decode()
 
 
 def test_gdn_kept_backward_argument_checks():

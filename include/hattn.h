@@ -66,7 +66,10 @@ const char* hattn_last_error(void);
  *             reference zero-initialises ht, chunkwise.py:1179).
  *   workspace device scratch of at least
  *             hattn_mamba2_chunkwise_fwd_workspace(...) bytes (may be NULL
- *             when that is 0); contents on entry are ignored.
+ *             when that is 0); contents on entry are ignored.  HType.STRONG
+ *             takes any size: with the full size its chunk walks run per
+ *             16-chunk segment in parallel (per-segment block sums in the
+ *             workspace), with less one serial walk per row.
  *
  * Constraints (status on violation):
  *   T % 64 == 0, T >= 64, H % G == 0, L >= 7 + ceil(log2(T / 64)),
@@ -94,8 +97,9 @@ int hattn_mamba2_chunkwise_fwd(const void* q, const void* k, const void* v, cons
                                int chunk_size, void* workspace, size_t workspace_bytes,
                                void* stream);
 
-/* Workspace bytes hattn_mamba2_chunkwise_fwd needs for these sizes (the
- * per-segment K x V summaries of the segment-parallel scan).  No counterpart
+/* Workspace bytes hattn_mamba2_chunkwise_fwd needs for these sizes, for
+ * either htype and any dtype (the per-segment K x V summaries of the
+ * segment-parallel scan; HType.STRONG: six block sums per segment).  No counterpart
  * in the reference, which allocates its intermediates with torch inside
  * chunkwise_fwd (chunkwise.py:1176-1179). */
 size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, int V, int L);
@@ -107,8 +111,9 @@ size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, i
  * harnesses that forbid hipMalloc).  Same arguments, results and status codes
  * as hattn_mamba2_chunkwise_fwd without the workspace pair; its scratch is a
  * file-scope static device array of 64 MiB per GPU (held until the process
- * ends), so sizes whose hattn_mamba2_chunkwise_fwd_workspace(...) exceeds
- * 64 MiB return HATTN_ERR_VALUE.  Every call on one GPU shares that array:
+ * ends), so HType.WEAK sizes whose segment summaries exceed 64 MiB return
+ * HATTN_ERR_VALUE; HType.STRONG sizes whose per-segment block sums exceed it
+ * run one serial walk per row instead (same results, slower).  Every call on one GPU shares that array:
  * calls that overlap on one GPU (concurrent streams or threads) race.
  */
 int hattn_mamba2_chunkwise_fwd_noalloc(const void* q, const void* k, const void* v,

@@ -29,8 +29,10 @@ hipError_t hattn_mamba2_strong_ht_launch(const void* k, const void* v, const flo
                                          hipStream_t stream);
 hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const void* v,
                                           const float* g, const void* l, void* o, float* gcum,
-                                          int B, int T, int G, int H, int V, int L, int dt_l,
-                                          int dt_o, hipStream_t stream, int* unsupported);
+                                          void* ws, size_t ws_bytes, int B, int T, int G, int H,
+                                          int V, int L, int dt_l, int dt_o, hipStream_t stream,
+                                          int* unsupported);
+size_t hattn_mamba2_strong_fwd_ws_bytes(int B, int T, int H, int V);
 size_t hattn_mamba2_strong_bwd_ws_bytes(int B, int T, int H, int nlev);
 hipError_t hattn_mamba2_layer_fwd_launch(const void* q, const void* k, const void* x,
                                          const void* dl, void* o, float* gcum, void* ws,
@@ -205,10 +207,12 @@ size_t hattn_mamba2_chunkwise_fwd_workspace(int B, int T, int G, int H, int K, i
   (void)L;
   if (B <= 0 || T < 64 || T % 64 != 0 || H <= 0 || V <= 0) return 0;
   // the bf16 kernels cut the sequence into the most segments: their workspace
-  // also covers the fp32 (bf16x3) kernels
+  // also covers the fp32 (bf16x3) kernels; HType.STRONG's segment-parallel walks
+  // take the per-segment block sums
   const size_t a = hattn_mamba2_fwd_ws_bytes(B, T, H, V, 0);
   const size_t b = hattn_mamba2_fwd_ws_bytes(B, T, H, V, 1);
-  return a > b ? a : b;
+  const size_t c = hattn_mamba2_strong_fwd_ws_bytes(B, T, H, V);
+  return max_of({a, b, c});
 }
 
 }  // extern "C"
@@ -252,10 +256,23 @@ static int mamba2_fwd_impl(const void* q, const void* k, const void* v, const fl
       return st;
     if (!q || !k || !v || !g || !l || !o || !g_cumsum)
       return fail(HATTN_ERR_VALUE, "null tensor pointer");
+    // segment-parallel walks when the workspace (or the static scratch) holds the
+    // per-segment block sums, else one serial walk per row
+    if (noalloc) {
+      const size_t cap = hattn_mamba2_fwd_static_scratch_bytes();
+      if (hattn_mamba2_strong_fwd_ws_bytes(B, T, H, V) <= cap) {
+        const hipError_t e = hattn_mamba2_fwd_static_scratch(&workspace);
+        if (e != hipSuccess) return check_hip(e, "static scratch address (hipGetSymbolAddress)");
+        workspace_bytes = cap;
+      } else {
+        workspace = nullptr;
+        workspace_bytes = 0;
+      }
+    }
     int unsupported = 0;
-    hipError_t e = hattn_mamba2_strong_fwd_launch(q, k, v, g, l, o, g_cumsum, B, T, G, H, V, L,
-                                                  dtype_l, dtype_o, (hipStream_t)stream,
-                                                  &unsupported);
+    hipError_t e = hattn_mamba2_strong_fwd_launch(q, k, v, g, l, o, g_cumsum, workspace,
+                                                  workspace_bytes, B, T, G, H, V, L, dtype_l,
+                                                  dtype_o, (hipStream_t)stream, &unsupported);
     if (unsupported)
       return fail(HATTN_ERR_NOT_IMPLEMENTED, "HType.STRONG: dtype combination l=%d o=%d", dtype_l,
                   dtype_o);

@@ -20,11 +20,11 @@
 // (value sum_s e^{Gc_last - Gc_s} k_s v_s^T, gate e^{Gc_last}), read after
 // the cascade and before the chunk's own decay and insertion.
 //
-// One workgroup (eight waves) per (batch, head, 16 columns of V) walks the
+// One workgroup (eight waves) per (batch, head, 32 columns of V) walks the
 // chunks in order; the walk is a chain of dependent steps, so the chunk's
 // work is split over two sets of waves that run side by side.  Near wave w
-// (0-3) owns the state rows k = 16 w .. +15 of every chunk-level level (one
-// 16 x 16 fp32 tile per level in registers); wave w and far wave w + 4 both
+// (0-3) owns the state rows k = 16 w .. +15 of every chunk-level level (two
+// 16 x 16 fp32 tiles per level in registers); wave w and far wave w + 4 both
 // own the output rows t = 16 w .. +15.  Per chunk: the cascade (near, uniform
 // selects over the levels), the levels >= 2 staged in LDS as bf16, then with
 // transposed products (lane: one token t, four consecutive v)
@@ -34,11 +34,29 @@
 //   far:  o^T += sum_j S_j^T (lam_j e^{Gc} Q)^T, and the store of o
 // and, after the hand-over, S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay
 // (near).
+//
+// Segment-parallel walks.  The chunks are cut into segments of 16.  Right after
+// the cascade at the first chunk c0 = 16 p of a segment p >= 1 the state holds
+//   level 1: chunk c0 - 1,  level 2: c0 - 2,  level 3: c0 - 4 .. c0 - 3,
+//   level 4: c0 - 8 .. c0 - 5,  level 5: c0 - 16 .. c0 - 9,
+// i.e. the previous segment's chunks 15, 14, 12-13, 8-11 and 0-7, and at a level
+// j >= 6 the whole segments q <= p - 2 with 4 + strong(p, q) = j (the strong
+// function of the segment indices: strong(16 p + i, 16 q + x) = 4 + strong(p, q)
+// for every i, x), each level the sum of its chunks' insertions decayed to c0,
+// with its chunk count.  So the walk of segment p starts there: a first kernel
+// writes, per segment, those five block sums and the whole segment's
+// (fp32 [K][V], decayed to the segment end) and the segment's total log-decay;
+// the walk of segment p loads the previous segment's five blocks, adds the
+// earlier segments at their levels, decayed over the segments between, and
+// walks its 16 chunks.  Without a workspace for the block sums one walk per
+// row covers every chunk.
 #include "mamba2_strong.h"
 
 namespace hattn {
 
-constexpr int kSBV = 16;          // V columns per workgroup
+constexpr int kSBV = 32;          // V columns per workgroup
+constexpr int kSNV = kSBV / 16;   // 16-column tiles per workgroup
+constexpr int kSVU = kSBV / 8;    // 16-byte units per row of a v tile
 constexpr int kSLK = 64 + 8;      // row stride of the bf16 q / k tiles
 constexpr int kSLV = kSBV + 8;    // row stride of the bf16 v tiles
 // Row strides of the per-token LDS rows that each lane of a 16-lane group reads
@@ -61,12 +79,120 @@ struct StrongSmem {
 };
 
 constexpr int kSThreads = 512;
+constexpr int kSSeg = 16;   // chunks per segment of the segment-parallel walks
+constexpr int kSBlk = 6;    // block sums per segment: chunks 0-7, 8-11, 12-13, 14, 15, 0-15
+
+// ---------------------------------------------------------------------------
+// Block sums of a segment (the starting state of the next segments' walks)
+// ---------------------------------------------------------------------------
+// One workgroup (four waves) per (row, segment p <= NSEG - 2, 64 columns of V):
+// per chunk X = K^T diag(e^{Gc_last - Gc}) V on MFMA (wave w: rows k = 16 w ..
+// +15), and six running sums, every one decayed by the chunk's total decay
+// before the chunk's X joins its block and the whole segment.
+//   blk [row][p][6][K = 64][V] fp32,  segd [row][NSEG] (p <= NSEG - 2 written)
+struct SegBlkSmem {
+  __bf16 k[kSC * kSLK];   // [t][k]
+  __bf16 v[kSC * kSLK];   // [t][v], 64 columns
+  float gc[kSC];          // chunk-local inclusive cumsum of g
+};
+
+__global__ __launch_bounds__(256) void mamba2_strong_segblk_kernel(
+    const __bf16* __restrict__ k, const __bf16* __restrict__ v, const float* __restrict__ g,
+    float* __restrict__ blk, float* __restrict__ segd, int nrows, int T, int G, int H, int V,
+    int NSEG) {
+  __shared__ __attribute__((aligned(16))) SegBlkSmem s;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, ln = lane & 15;
+  const int nvb = V / 64;
+  const XcdMap mp = xcd_map(blockIdx.x, (NSEG - 1) * nvb);
+  if (mp.row >= nrows) return;
+  const int row = mp.row, p = mp.slice / nvb, v0 = (mp.slice % nvb) * 64;
+  const int b = row / H, h = row % H, gq = h / (H / G);
+  const size_t hk = (size_t)G * 64, hv = (size_t)H * V;
+  // two 16-byte units of k and of v per thread: rows r_ld and r_ld + 32
+  const int r_ld = tid >> 3, c_ld = 8 * (tid & 7);
+  u32x4 pk[2], pv[2];
+  float pg;
+  auto prefetch = [&](int jc) __attribute__((always_inline)) {
+    const size_t t0 = (size_t)b * T + (size_t)jc * kSC;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const size_t tr = t0 + r_ld + 32 * u;
+      pk[u] = *(const u32x4*)(k + tr * hk + (size_t)gq * 64 + c_ld);
+      pv[u] = *(const u32x4*)(v + tr * hv + (size_t)h * V + v0 + c_ld);
+    }
+    pg = g[(t0 + lane) * H + h];
+  };
+  floatx4 acc[kSBlk][4];
+#pragma unroll
+  for (int m = 0; m < kSBlk; ++m)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[m][nt] = zero4();
+  float dseg = 0.f;
+  const int c0 = p * kSSeg;
+  prefetch(c0);
+  for (int i = 0; i < kSSeg; ++i) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      *(u32x4*)(s.k + (r_ld + 32 * u) * kSLK + c_ld) = pk[u];
+      *(u32x4*)(s.v + (r_ld + 32 * u) * kSLK + c_ld) = pv[u];
+    }
+    if (w == 0) {
+      float x = pg;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      s.gc[lane] = x;
+    }
+    __syncthreads();
+    if (i + 1 < kSSeg) prefetch(c0 + i + 1);
+    const float glast = s.gc[kSC - 1];
+    const float gd = fexp(glast);
+    dseg += glast;
+    // x[nt][e] = X[k = 16 w + 4 lq + e][v = 16 nt + ln]
+    floatx4 x[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) x[nt] = zero4();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      bf16x8 a = tr_frag(s.k, kSLK, 32 * c, 16 * w);   // K[s][k = 16 w + ln]
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        a[jj] = (__bf16)((float)a[jj] * fexp(glast - s.gc[32 * c + 8 * lq + jj]));
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        x[nt] = mfma16x16x32(a, tr_frag(s.v, kSLK, 32 * c, 16 * nt), x[nt]);
+    }
+    const int bi = i < 8 ? 0 : i < 12 ? 1 : i < 14 ? 2 : i < 15 ? 3 : 4;
+#pragma unroll
+    for (int m = 0; m < kSBlk; ++m) {
+      const float on = (m == bi || m == kSBlk - 1) ? 1.f : 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[m][nt][e] = acc[m][nt][e] * gd + on * x[nt][e];
+    }
+    __syncthreads();   // the next chunk's staging overwrites k, v, gc
+  }
+  float* out = blk + (size_t)(row * (NSEG - 1) + p) * kSBlk * 64 * V + v0 + ln;
+#pragma unroll
+  for (int m = 0; m < kSBlk; ++m)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        out[((size_t)m * 64 + 16 * w + 4 * lq + e) * V + 16 * nt] = acc[m][nt][e];
+  if (v0 == 0 && tid == 0) segd[row * NSEG + p] = dseg;
+}
 
 template <typename TL, typename TO>
 __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
-    float* __restrict__ gcum, int nrows, int T, int G, int H, int V, int L) {
+    float* __restrict__ gcum, const float* __restrict__ blk, const float* __restrict__ segd,
+    int nrows, int T, int G, int H, int V, int L, int NSEG) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   StrongSmem& s = *(StrongSmem*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -77,11 +203,15 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
   const bool near = w < 4;
   const int wq = w & 3;
   const int nvb = V / kSBV;
-  const XcdMap mp = xcd_map(blockIdx.x, nvb);
+  // NSEG > 1: segment seg's chunks c0 .. cend - 1 from the state at c0 (the
+  // block sums blk, segd); NSEG == 1: every chunk from the empty state
+  const XcdMap mp = xcd_map(blockIdx.x, nvb * NSEG);
   if (mp.row >= nrows) return;
-  const int row = mp.row, v0 = mp.slice * kSBV;
+  const int row = mp.row, seg = mp.slice / nvb, v0 = (mp.slice % nvb) * kSBV;
   const int b = row / H, h = row % H, gq = h / (H / G);
   const int NT = T / kSC;
+  const int c0 = seg * kSSeg;
+  const int cend = NSEG > 1 ? min(c0 + kSSeg, NT) : NT;
   const size_t hk = (size_t)G * 64, hv = (size_t)H * V;
   const int t_me = 16 * wq + ln;   // this lane's token in the transposed products
 
@@ -92,9 +222,11 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
 
   // Level-j state (near waves): one 16 x 16 fp32 tile, rows k = 16 w + 4 lq + i,
   // column v = ln (the MFMA D layout), and the number of chunks it holds.
-  floatx4 st[kSMaxLev];
+  floatx4 st[kSMaxLev][kSNV];
 #pragma unroll
-  for (int j = 0; j < kSMaxLev; ++j) st[j] = zero4();
+  for (int j = 0; j < kSMaxLev; ++j)
+#pragma unroll
+    for (int nt = 0; nt < kSNV; ++nt) st[j][nt] = zero4();
   int cnt[kSMaxLev];
 #pragma unroll
   for (int j = 0; j < kSMaxLev; ++j) cnt[j] = 0;
@@ -104,7 +236,8 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
   // k per thread, a v unit (threads < 128), g (wave 0) and up to four lambda
   // entries per thread (64 x L <= 2048).
   const int r_ld = tid >> 3, c_ld = 8 * (tid & 7);
-  const int rv_ld = tid >> 1, cv_ld = 8 * (tid & 1);
+  const int rv_ld = tid / kSVU, cv_ld = 8 * (tid % kSVU);
+  const bool v_ld = tid < kSC * kSVU;
   int lrel[4], llds[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -120,31 +253,95 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
     const size_t rq = (t0 + r_ld) * hk + (size_t)gq * 64 + c_ld;
     pq = *(const u32x4*)(q + rq);
     pk = *(const u32x4*)(k + rq);
-    pv = *(const u32x4*)(v + (t0 + (tid < 128 ? rv_ld : 0)) * hv + (size_t)h * V + v0 + cv_ld);
+    pv = *(const u32x4*)(v + (t0 + (v_ld ? rv_ld : 0)) * hv + (size_t)h * V + v0 + cv_ld);
     pg = g[(t0 + lane) * H + h];
     const TL* lb = l + (t0 * H + h) * L;
 #pragma unroll
     for (int u = 0; u < 4; ++u) pl[u] = lb[lrel[u]];
   };
-  prefetch(0);
 
-  for (int ic = 0; ic < NT; ++ic) {
+  if (c0 > 0) {
+    if (near) {
+      // the previous segment's blocks 0-7, 8-11, 12-13, 14, 15 -> levels 5, 4, 3, 2, 1
+      const int kr = 16 * w + 4 * lq;
+      const float* pb = blk + (size_t)(row * (NSEG - 1) + seg - 1) * kSBlk * 64 * V + v0 + ln;
+#pragma unroll
+      for (int m = 0; m < 5; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int nt = 0; nt < kSNV; ++nt)
+            st[5 - m][nt][i] = pb[((size_t)m * 64 + kr + i) * V + 16 * nt];
+      cnt[1] = 1;
+      cnt[2] = 1;
+      cnt[3] = 2;
+      cnt[4] = 4;
+      cnt[5] = 8;
+      // the whole segments q <= seg - 2 at level 4 + strong(seg, q), decayed over
+      // the segments q + 1 .. seg - 1
+      float dec = 0.f;
+      for (int q = seg - 2; q >= 0; --q) {
+        dec += segd[row * NSEG + q + 1];
+        const float f = fexp(dec);
+        const int lev = 4 + strong_level_ce(seg, q);
+        const float* ps = blk + ((size_t)(row * (NSEG - 1) + q) * kSBlk + kSBlk - 1) * 64 * V + v0 + ln;
+        float y[kSNV][4];
+#pragma unroll
+        for (int nt = 0; nt < kSNV; ++nt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[nt][i] = f * ps[(size_t)(kr + i) * V + 16 * nt];
+#pragma unroll
+        for (int j = 6; j < kSMaxLev; ++j)
+          if (lev == j) {
+#pragma unroll
+            for (int nt = 0; nt < kSNV; ++nt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) st[j][nt][i] += y[nt][i];
+            cnt[j] += kSSeg;
+          }
+      }
+    }
+    // chunk c0 - 1 (k, v, g cumsum) for the first sub-diagonal block; the
+    // loop's first barrier orders these writes before their reads
+    prefetch(c0 - 1);
+    const int pp = (c0 - 1) & 1;
+    *(u32x4*)(s.k[pp] + r_ld * kSLK + c_ld) = pk;
+    if (v_ld) *(u32x4*)(s.v[pp] + rv_ld * kSLV + cv_ld) = pv;
+    if (w == 0) {
+      float x = pg;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      s.gc[pp][lane] = x;
+    }
+  }
+  prefetch(c0);
+
+  for (int ic = c0; ic < cend; ++ic) {
     const int par = ic & 1;
     const size_t tok0 = (size_t)b * T + (size_t)ic * kSC;
     // ---- cascade (recurrent.py:56-74) over the chunk-level states ------------------
-    if (near) {
-      floatx4 carry = zero4();
+    // (a segment's walk starts from the state after the cascade at c0)
+    if (near && (ic > c0 || c0 == 0)) {
+      floatx4 carry[kSNV];
+#pragma unroll
+      for (int nt = 0; nt < kSNV; ++nt) carry[nt] = zero4();
       int cc = 0;
 #pragma unroll
       for (int j = 0; j < kSMaxLev; ++j) {
         const int cap = 1 << (j > 0 ? j - 1 : 0);
         const bool swap = j == 0 || cnt[j] + cc > cap;
-        const floatx4 old = st[j];
         const int oc = cnt[j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          st[j][i] = swap ? carry[i] : old[i] + carry[i];
-          carry[i] = swap ? old[i] : 0.f;
+        for (int nt = 0; nt < kSNV; ++nt) {
+          const floatx4 old = st[j][nt];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            st[j][nt][i] = swap ? carry[nt][i] : old[i] + carry[nt][i];
+            carry[nt][i] = swap ? old[i] : 0.f;
+          }
         }
         cnt[j] = swap ? cc : oc + cc;
         cc = swap ? oc : 0;
@@ -154,7 +351,7 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
     {
       *(u32x4*)(s.q + r_ld * kSLK + c_ld) = pq;
       *(u32x4*)(s.k[par] + r_ld * kSLK + c_ld) = pk;
-      if (tid < 128) *(u32x4*)(s.v[par] + rv_ld * kSLV + cv_ld) = pv;
+      if (v_ld) *(u32x4*)(s.v[par] + rv_ld * kSLV + cv_ld) = pv;
       if (w == 0) {
         float x = pg;
 #pragma unroll
@@ -171,13 +368,17 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
       if (near) {
 #pragma unroll
         for (int j = 2; j < kSMaxLev; ++j)
-          *(bf16x4*)(s.hs[j] + ln * kSLK + 16 * w + 4 * lq) = cvt4(st[j]);
+#pragma unroll
+          for (int nt = 0; nt < kSNV; ++nt)
+            *(bf16x4*)(s.hs[j] + (16 * nt + ln) * kSLK + 16 * w + 4 * lq) = cvt4(st[j][nt]);
       }
     }
     __syncthreads();
-    if (ic + 1 < NT) prefetch(ic + 1);
+    if (ic + 1 < cend) prefetch(ic + 1);
 
-    floatx4 acc = zero4();   // o^T[v = 4 lq + i][t = t_me]
+    floatx4 acc[kSNV];   // o^T[v = 16 nt + 4 lq + i][t = t_me]
+#pragma unroll
+    for (int nt = 0; nt < kSNV; ++nt) acc[nt] = zero4();
     const float gct = s.gc[par][t_me];
     // B operand of the q . k products: Q[t_me][32 c + 8 lq ..]
     const bf16x8 bq0 = *(const bf16x8*)(s.q + t_me * kSLK + 8 * lq);
@@ -215,10 +416,13 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
             }
           }
           // o^T[v][t] += V[s][v] P^T[s][t] over the 32 sources of the pair
-          acc = mfma16x16x32(tr_frag_d(s.v[pk2], kSLV, 32 * pp, 0), pb, acc);
+#pragma unroll
+          for (int nt = 0; nt < kSNV; ++nt)
+            acc[nt] = mfma16x16x32(tr_frag_d(s.v[pk2], kSLV, 32 * pp, 16 * nt), pb, acc[nt]);
         }
       }
-      s.onear[t_me][lq] = acc;
+#pragma unroll
+      for (int nt = 0; nt < kSNV; ++nt) s.onear[t_me][4 * nt + lq] = acc[nt];
     } else {
       // ---- far levels: o^T[v][t] += S_j^T[v][k] (lam[t, 6 + j] e^{Gc_t} q_t[k]) ----------
       // a lane's four values share its token t_me: the level weight is one
@@ -228,10 +432,14 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
       for (int j = 2; j < kSMaxLev; ++j) {
         if (6 + j < L) {
           const float f = s.lam[t_me][6 + j] * eg;
-          floatx4 y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 8 * lq), bq0, zero4());
-          y = mfma16x16x32(*(const bf16x8*)(s.hs[j] + ln * kSLK + 32 + 8 * lq), bq1, y);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += f * y[i];
+          for (int nt = 0; nt < kSNV; ++nt) {
+            const __bf16* hr = s.hs[j] + (16 * nt + ln) * kSLK + 8 * lq;
+            floatx4 y = mfma16x16x32(*(const bf16x8*)hr, bq0, zero4());
+            y = mfma16x16x32(*(const bf16x8*)(hr + 32), bq1, y);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nt][i] += f * y[i];
+          }
         }
       }
     }
@@ -244,28 +452,38 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
 #pragma unroll
       for (int j = 1; j < kSMaxLev; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[j][i] *= gd;
-      floatx4 sum = zero4();
+        for (int nt = 0; nt < kSNV; ++nt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[j][nt][i] *= gd;
+      floatx4 sum[kSNV];
+#pragma unroll
+      for (int nt = 0; nt < kSNV; ++nt) sum[nt] = zero4();
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bf16x8 a = tr_frag(s.k[par], kSLK, 32 * c, 16 * w);   // K[s][k = 16 w + ln]
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
           a[jj] = (__bf16)((float)a[jj] * fexp(glast - s.gc[par][32 * c + 8 * lq + jj]));
-        sum = mfma16x16x32(a, tr_frag(s.v[par], kSLV, 32 * c, 0), sum);
+#pragma unroll
+        for (int nt = 0; nt < kSNV; ++nt)
+          sum[nt] = mfma16x16x32(a, tr_frag(s.v[par], kSLV, 32 * c, 16 * nt), sum[nt]);
       }
-      st[0] = sum;
+#pragma unroll
+      for (int nt = 0; nt < kSNV; ++nt) st[0][nt] = sum[nt];
       cnt[0] += 1;
     } else {
-      // ---- o[t_me][v0 + 4 lq .. +3] = far + near ------------------------------------
-      const floatx4 an = s.onear[t_me][lq];
+      // ---- o[t_me][v0 + 16 nt + 4 lq .. +3] = far + near ----------------------------
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += an[i];
-      TO* op = o + (tok0 + t_me) * hv + (size_t)h * V + v0 + 4 * lq;
-      if constexpr (sizeof(TO) == 2) {
-        *(bf16x4*)op = cvt4(acc);
-      } else {
-        *(floatx4*)op = acc;
+      for (int nt = 0; nt < kSNV; ++nt) {
+        const floatx4 an = s.onear[t_me][4 * nt + lq];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][i] += an[i];
+        TO* op = o + (tok0 + t_me) * hv + (size_t)h * V + v0 + 16 * nt + 4 * lq;
+        if constexpr (sizeof(TO) == 2) {
+          *(bf16x4*)op = cvt4(acc[nt]);
+        } else {
+          *(floatx4*)op = acc[nt];
+        }
       }
     }
     // No barrier here: the next chunk's staging writes q, lambda, the level
@@ -275,10 +493,33 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
   }
 }
 
+// Workspace of the segment-parallel walks (0: one segment, no workspace).
+struct StrongFwdWs {
+  float* blk;
+  float* segd;
+  int nseg;
+  size_t bytes;
+};
+inline StrongFwdWs strong_fwd_ws_layout(void* ws, int B, int T, int H, int V) {
+  StrongFwdWs w{nullptr, nullptr, 1, 0};
+  const int NT = T / kSC;
+  if (NT <= kSSeg) return w;
+  w.nseg = (NT + kSSeg - 1) / kSSeg;
+  const size_t rows = (size_t)B * H;
+  const size_t nb = (rows * (w.nseg - 1) * kSBlk * 64 * V * 4 + 255) / 256 * 256;
+  w.bytes = nb + rows * w.nseg * 4;
+  unsigned char* p = (unsigned char*)ws;
+  if (p != nullptr) {
+    w.blk = (float*)p;
+    w.segd = (float*)(p + nb);
+  }
+  return w;
+}
+
 template <typename TL, typename TO>
 static hipError_t strong_launch_t(const void* q, const void* k, const void* v, const float* g,
-                                  const void* l, void* o, float* gcum, int B, int T, int G,
-                                  int H, int V, int L, hipStream_t stream) {
+                                  const void* l, void* o, float* gcum, void* ws, size_t ws_bytes,
+                                  int B, int T, int G, int H, int V, int L, hipStream_t stream) {
   auto kf = mamba2_strong_fwd_kernel<TL, TO>;
   const int smem = (int)sizeof(StrongSmem);
   hipError_t e;
@@ -286,9 +527,19 @@ static hipError_t strong_launch_t(const void* q, const void* k, const void* v, c
                                smem)) != hipSuccess)
     return e;
   const int rows = B * H;
-  const int grid = (rows + 7) / 8 * 8 * (V / kSBV);
+  StrongFwdWs w = strong_fwd_ws_layout(ws, B, T, H, V);
+  if (ws == nullptr || ws_bytes < w.bytes) w = StrongFwdWs{nullptr, nullptr, 1, 0};
+  if (w.nseg > 1) {
+    const int gridb = (rows + 7) / 8 * 8 * (w.nseg - 1) * (V / 64);
+    hipLaunchKernelGGL(mamba2_strong_segblk_kernel, dim3(gridb), dim3(256), 0, stream,
+                       (const __bf16*)k, (const __bf16*)v, g, w.blk, w.segd, rows, T, G, H, V,
+                       w.nseg);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const int grid = (rows + 7) / 8 * 8 * (V / kSBV) * w.nseg;
   hipLaunchKernelGGL(kf, dim3(grid), dim3(kSThreads), smem, stream, (const __bf16*)q, (const __bf16*)k,
-                     (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum, rows, T, G, H, V, L);
+                     (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum, (const float*)w.blk,
+                     (const float*)w.segd, rows, T, G, H, V, L, w.nseg);
   return hipGetLastError();
 }
 
@@ -341,22 +592,33 @@ __global__ __launch_bounds__(256) void mamba2_strong_ht_kernel(
 
 int hattn_mamba2_strong_max_levels() { return hattn::kSMaxLev - 1; }
 
+// Workspace bytes for the segment-parallel strong forward (0: the sizes have one
+// segment); with less, the forward walks every row serially.
+size_t hattn_mamba2_strong_fwd_ws_bytes(int B, int T, int H, int V) {
+  return hattn::strong_fwd_ws_layout(nullptr, B, T, H, V).bytes;
+}
+
 // bf16 q / k / v; lambda bf16 or fp32; o bf16 or fp32; K = 64; V a multiple of 16;
 // L <= 32.
 hipError_t hattn_mamba2_strong_fwd_launch(const void* q, const void* k, const void* v,
                                           const float* g, const void* l, void* o, float* gcum,
-                                          int B, int T, int G, int H, int V, int L, int dt_l,
-                                          int dt_o, hipStream_t stream, int* unsupported) {
+                                          void* ws, size_t ws_bytes, int B, int T, int G, int H,
+                                          int V, int L, int dt_l, int dt_o, hipStream_t stream,
+                                          int* unsupported) {
   using namespace hattn;
   *unsupported = 0;
   if (dt_l == 0 && dt_o == 0)
-    return strong_launch_t<__bf16, __bf16>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+    return strong_launch_t<__bf16, __bf16>(q, k, v, g, l, o, gcum, ws, ws_bytes, B, T, G, H, V, L,
+                                         stream);
   if (dt_l == 2 && dt_o == 0)
-    return strong_launch_t<float, __bf16>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+    return strong_launch_t<float, __bf16>(q, k, v, g, l, o, gcum, ws, ws_bytes, B, T, G, H, V, L,
+                                         stream);
   if (dt_l == 0 && dt_o == 2)
-    return strong_launch_t<__bf16, float>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+    return strong_launch_t<__bf16, float>(q, k, v, g, l, o, gcum, ws, ws_bytes, B, T, G, H, V, L,
+                                         stream);
   if (dt_l == 2 && dt_o == 2)
-    return strong_launch_t<float, float>(q, k, v, g, l, o, gcum, B, T, G, H, V, L, stream);
+    return strong_launch_t<float, float>(q, k, v, g, l, o, gcum, ws, ws_bytes, B, T, G, H, V, L,
+                                         stream);
   *unsupported = 1;
   return hipSuccess;
 }

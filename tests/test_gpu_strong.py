@@ -89,6 +89,88 @@ def test_strong_fwd_nine_chunk_levels():
     _run_fwd(1, 32768, 2, 2, 64, 64, 16, seed=327)
 
 
+@pytest.mark.parametrize("T", [1088, 2048, 3136, 8192])
+def test_strong_fwd_segment_parallel(T):
+    """More than 16 chunks: one walk per 16-chunk segment, started from the
+    block sums of the earlier segments (17 chunks: a one-chunk last segment;
+    49: a ragged one), every row."""
+    _run_fwd(2, T, 2, 2, 64, 128, _levels(T), seed=T + 1)
+
+
+@pytest.mark.parametrize("T", [4096, 16384])
+def test_strong_fwd_levels_onehot_slow_decay(T):
+    """Every chunk-level strong level on its own: lambda one-hot at column 6 + j
+    and a slow decay (|g| <= 2e-4 per token, so the blocks of whole earlier
+    segments that start each segment's walk keep their weight), o against the
+    oracle's cascade form level by level."""
+    from hattention.base import HType
+    from hattention.chunkwise import chunkwise_fwd
+    B, G, H, K, V = 1, 1, 1, 64, 64
+    L = _levels(T)
+    gen = torch.Generator().manual_seed(T + 3)
+    q = (torch.randn(B, T, G, K, generator=gen) / 8).bfloat16()
+    k = (torch.randn(B, T, G, K, generator=gen) / 8).bfloat16()
+    v = torch.randn(B, T, H, V, generator=gen).bfloat16()
+    g = -2e-4 * torch.rand(B, T, H, generator=gen)
+    seen = 0
+    for col in range(8, L):
+        l = torch.zeros(B, T, H, L)
+        l[..., col] = 1.0
+        l = l.bfloat16()
+        ref = M.chunked_strong_fwd(*(x.double() for x in (q, k, v, g, l)), chunk_size=64)
+        if ref.abs().max().item() == 0.0:
+            continue
+        seen += 1
+        o, _, _ = chunkwise_fwd(*(x.to(DEV) for x in (q, k, v, g, l)), False, 2, HType.STRONG, 64,
+                                False)
+        torch.cuda.synchronize()
+        mx, fro = _errs(o, ref)
+        print(f"  [strong onehot] T={T} level column {col}: |ref| {ref.abs().max().item():.2e} "
+              f"max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+        assert mx < TOL_MAX and fro < TOL_FRO, (col, mx, fro)
+    assert seen == L - 8
+
+
+@pytest.mark.parametrize("T", [2112, 16384])
+def test_strong_fwd_serial_walk_without_workspace(T):
+    """Without a workspace for the block sums the forward walks each row
+    serially; both walks against the oracle, and against each other (they
+    differ by fp32 association and the bf16 rounding of the staged states)."""
+    import ctypes
+    from hattention import _lib
+    B, G, H, K, V = 1, 2, 2, 64, 64
+    L = _levels(T)
+    q, k, v, g, l = make_mamba2_inputs(B, T, H, K, V, L, G=G, seed=T + 2)
+    print(f"[strong fwd serial] T={T}", flush=True)
+    lib = _lib.load()
+    xs = [x.to(DEV) for x in (q, k, v, g, l)]
+    need = lib.hattn_mamba2_chunkwise_fwd_workspace(B, T, G, H, K, V, L)
+    outs = []
+    for with_ws in (True, False):
+        o = torch.empty(v.shape, dtype=v.dtype, device=DEV)
+        gc = torch.empty(g.shape, dtype=torch.float32, device=DEV)
+        ws = torch.empty(need if with_ws else 1, dtype=torch.uint8, device=DEV)
+        st = lib.hattn_mamba2_chunkwise_fwd(
+            *(_lib.ptr(x) for x in xs), _lib.ptr(o), _lib.ptr(gc), None, B, T, G, H, K, V, L,
+            0, 0, 0, 0, 2, 1, 64, _lib.ptr(ws) if with_ws else None, need if with_ws else 0,
+            _lib.stream_handle(DEV))
+        _lib.check(st)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for h in range(H):
+        gi = h // (H // G)
+        qs, ks = (x[:, :, gi:gi + 1].double() for x in (q, k))
+        vs, gs, ls = (x[:, :, h:h + 1].double() for x in (v, g, l))
+        ref = M.chunked_strong_fwd(qs, ks, vs, gs, ls, chunk_size=64)
+        for name, o in zip(("parallel", "serial"), outs):
+            mx, fro = _errs(o[:, :, h:h + 1], ref)
+            print(f"  head {h} {name}: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+            assert mx < TOL_MAX and fro < TOL_FRO, (name, h, mx, fro)
+    mx, fro = _errs(outs[0], outs[1].float())
+    print(f"  parallel vs serial: max-rel {mx:.2e} fro {fro:.2e}", flush=True)
+    assert mx < 1e-2 and fro < 2e-3
+
+
 @pytest.mark.parametrize("B,T,G,H,K,V", [
     (1, 1024, 2, 2, 64, 64),      # 16 chunks: the last chunk ends every block
     (1, 5184, 2, 2, 64, 64),      # 81 chunks: ragged blocks, one-chunk ranges at the end

@@ -20,11 +20,12 @@
 // (value sum_s e^{Gc_last - Gc_s} k_s v_s^T, gate e^{Gc_last}), read after
 // the cascade and before the chunk's own decay and insertion.
 //
-// One workgroup (eight waves) per (batch, head, 32 columns of V) walks the
-// chunks in order; the walk is a chain of dependent steps, so the chunk's
-// work is split over two sets of waves that run side by side.  Near wave w
-// (0-3) owns the state rows k = 16 w .. +15 of every chunk-level level (two
-// 16 x 16 fp32 tiles per level in registers); wave w and far wave w + 4 both
+// One workgroup (eight waves) per (batch, head, 32 columns of V; 16 for the
+// serial walks below) walks the chunks in order; the walk is a chain of
+// dependent steps, so the chunk's work is split over two sets of waves that
+// run side by side.  Near wave w (0-3) owns the state rows k = 16 w .. +15 of
+// every chunk-level level (one 16 x 16 fp32 tile per 16 columns and level in
+// registers); wave w and far wave w + 4 both
 // own the output rows t = 16 w .. +15.  Per chunk: the cascade (near, uniform
 // selects over the levels), the levels >= 2 staged in LDS as bf16, then with
 // transposed products (lane: one token t, four consecutive v)
@@ -54,11 +55,9 @@
 
 namespace hattn {
 
-constexpr int kSBV = 32;          // V columns per workgroup
-constexpr int kSNV = kSBV / 16;   // 16-column tiles per workgroup
-constexpr int kSVU = kSBV / 8;    // 16-byte units per row of a v tile
+// NV 16-column tiles of V per workgroup: 2 for the segment-parallel walks,
+// 1 for the serial walks (twice the workgroups where every row is one chain).
 constexpr int kSLK = 64 + 8;      // row stride of the bf16 q / k tiles
-constexpr int kSLV = kSBV + 8;    // row stride of the bf16 v tiles
 // Row strides of the per-token LDS rows that each lane of a 16-lane group reads
 // for a different token: 33 words (lambda) and 17 words (level tables) put
 // the 16 rows on 16 different banks.
@@ -67,15 +66,17 @@ constexpr int kSTab = 17;
 
 __device__ constexpr StrongTables kStrong{};
 
+template <int NV>
 struct StrongSmem {
+  static constexpr int kSLV = 16 * NV + 8;   // row stride of the bf16 v tiles
   __bf16 q[kSC * kSLK];
   __bf16 k[2][kSC * kSLK];           // this chunk and the previous one (by parity)
   __bf16 v[2][kSC * kSLV];
-  __bf16 hs[kSMaxLev][kSBV * kSLK];  // chunk-level states, bf16 [v][k]
+  __bf16 hs[kSMaxLev][16 * NV * kSLK];  // chunk-level states, bf16 [v][k]
   float gc[2][kSC];                  // chunk-local inclusive cumsum of g
   float lam[kSC][kSLam];             // lambda[t, 0 .. L-1] of this chunk (L <= 32)
   unsigned tab[2][kSC * kSTab];      // intra / sub level tables, four levels a word
-  floatx4 onear[kSC][kSBV / 4];      // o^T of the near blocks, [t][v / 4]
+  floatx4 onear[kSC][4 * NV];      // o^T of the near blocks, [t][v / 4]
 };
 
 constexpr int kSThreads = 512;
@@ -187,14 +188,15 @@ __global__ __launch_bounds__(256) void mamba2_strong_segblk_kernel(
   if (v0 == 0 && tid == 0) segd[row * NSEG + p] = dseg;
 }
 
-template <typename TL, typename TO>
+template <typename TL, typename TO, int NV>
 __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const float* __restrict__ g, const TL* __restrict__ l, TO* __restrict__ o,
     float* __restrict__ gcum, const float* __restrict__ blk, const float* __restrict__ segd,
     int nrows, int T, int G, int H, int V, int L, int NSEG) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-  StrongSmem& s = *(StrongSmem*)smem_raw;
+  StrongSmem<NV>& s = *(StrongSmem<NV>*)smem_raw;
+  constexpr int kSBV = 16 * NV, kSNV = NV, kSVU = 2 * NV, kSLV = StrongSmem<NV>::kSLV;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, ln = lane & 15;
   // waves 0-3 (near): the cascade and the chunk-level states (rows k = 16 w ..),
@@ -520,15 +522,10 @@ template <typename TL, typename TO>
 static hipError_t strong_launch_t(const void* q, const void* k, const void* v, const float* g,
                                   const void* l, void* o, float* gcum, void* ws, size_t ws_bytes,
                                   int B, int T, int G, int H, int V, int L, hipStream_t stream) {
-  auto kf = mamba2_strong_fwd_kernel<TL, TO>;
-  const int smem = (int)sizeof(StrongSmem);
-  hipError_t e;
-  if ((e = hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               smem)) != hipSuccess)
-    return e;
   const int rows = B * H;
   StrongFwdWs w = strong_fwd_ws_layout(ws, B, T, H, V);
   if (ws == nullptr || ws_bytes < w.bytes) w = StrongFwdWs{nullptr, nullptr, 1, 0};
+  hipError_t e;
   if (w.nseg > 1) {
     const int gridb = (rows + 7) / 8 * 8 * (w.nseg - 1) * (V / 64);
     hipLaunchKernelGGL(mamba2_strong_segblk_kernel, dim3(gridb), dim3(256), 0, stream,
@@ -536,11 +533,19 @@ static hipError_t strong_launch_t(const void* q, const void* k, const void* v, c
                        w.nseg);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  const int grid = (rows + 7) / 8 * 8 * (V / kSBV) * w.nseg;
-  hipLaunchKernelGGL(kf, dim3(grid), dim3(kSThreads), smem, stream, (const __bf16*)q, (const __bf16*)k,
-                     (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum, (const float*)w.blk,
-                     (const float*)w.segd, rows, T, G, H, V, L, w.nseg);
-  return hipGetLastError();
+  auto walk = [&](auto kf, int smem, int bv) {
+    hipError_t r = hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       smem);
+    if (r != hipSuccess) return r;
+    const int grid = (rows + 7) / 8 * 8 * (V / bv) * w.nseg;
+    hipLaunchKernelGGL(kf, dim3(grid), dim3(kSThreads), smem, stream, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, g, (const TL*)l, (TO*)o, gcum,
+                       (const float*)w.blk, (const float*)w.segd, rows, T, G, H, V, L, w.nseg);
+    return hipGetLastError();
+  };
+  if (w.nseg > 1)
+    return walk(mamba2_strong_fwd_kernel<TL, TO, 2>, (int)sizeof(StrongSmem<2>), 32);
+  return walk(mamba2_strong_fwd_kernel<TL, TO, 1>, (int)sizeof(StrongSmem<1>), 16);
 }
 
 // ---------------------------------------------------------------------------

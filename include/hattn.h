@@ -68,7 +68,7 @@ const char* hattn_last_error(void);
  *             hattn_mamba2_chunkwise_fwd_workspace(...) bytes (may be NULL
  *             when that is 0); contents on entry are ignored.  HType.STRONG
  *             takes any size: with the full size its chunk walks run per
- *             16-chunk segment in parallel (per-segment block sums in the
+ *             32-chunk segment in parallel (per-segment block sums in the
  *             workspace), with less one serial walk per row.
  *
  * Constraints (status on violation):

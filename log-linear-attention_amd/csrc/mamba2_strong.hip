@@ -36,20 +36,21 @@
 // and, after the hand-over, S_0 = K^T diag(e^{Gc_last - Gc}) V after the decay
 // (near).
 //
-// Segment-parallel walks.  The chunks are cut into segments of 16.  Right after
-// the cascade at the first chunk c0 = 16 p of a segment p >= 1 the state holds
-//   level 1: chunk c0 - 1,  level 2: c0 - 2,  level 3: c0 - 4 .. c0 - 3,
-//   level 4: c0 - 8 .. c0 - 5,  level 5: c0 - 16 .. c0 - 9,
-// i.e. the previous segment's chunks 15, 14, 12-13, 8-11 and 0-7, and at a level
-// j >= 6 the whole segments q <= p - 2 with 4 + strong(p, q) = j (the strong
-// function of the segment indices: strong(16 p + i, 16 q + x) = 4 + strong(p, q)
-// for every i, x), each level the sum of its chunks' insertions decayed to c0,
-// with its chunk count.  So the walk of segment p starts there: a first kernel
-// writes, per segment, those five block sums and the whole segment's
+// Segment-parallel walks.  The chunks are cut into segments of S = 2^s chunks
+// (s = kSLog).  Right after the cascade at the first chunk c0 = S p of a
+// segment p >= 1 the state holds, at level s + 1 - m (m = 0 .. s), the previous
+// segment's chunks [S - S / 2^m, S - S / 2^(m+1)) (for S = 16: chunks 0-7 at
+// level 5, 8-11 at 4, 12-13 at 3, 14 at 2, 15 at 1), and at a level j >= s + 2
+// the whole segments q <= p - 2 with s + strong(p, q) = j (the strong function
+// of the segment indices: strong(S p + i, S q + x) = s + strong(p, q) for every
+// i, x), each level the sum of its chunks' insertions decayed to c0, with its
+// chunk count; within the segment the cascade never carries into a level
+// >= s + 2.  So the walk of segment p starts there: a first kernel writes, per
+// segment, those s + 1 block sums and the whole segment's
 // (fp32 [K][V], decayed to the segment end) and the segment's total log-decay;
-// the walk of segment p loads the previous segment's five blocks, adds the
+// the walk of segment p loads the previous segment's s + 1 blocks, adds the
 // earlier segments at their levels, decayed over the segments between, and
-// walks its 16 chunks.  Without a workspace for the block sums one walk per
+// walks its S chunks.  Without a workspace for the block sums one walk per
 // row covers every chunk.
 #include "mamba2_strong.h"
 
@@ -80,17 +81,18 @@ struct StrongSmem {
 };
 
 constexpr int kSThreads = 512;
-constexpr int kSSeg = 16;   // chunks per segment of the segment-parallel walks
-constexpr int kSBlk = 6;    // block sums per segment: chunks 0-7, 8-11, 12-13, 14, 15, 0-15
+constexpr int kSLog = 5;              // segments of 2^kSLog chunks
+constexpr int kSSeg = 1 << kSLog;     // chunks per segment of the segment-parallel walks
+constexpr int kSBlk = kSLog + 2;      // block sums per segment: kSLog + 1 blocks, the whole
 
 // ---------------------------------------------------------------------------
 // Block sums of a segment (the starting state of the next segments' walks)
 // ---------------------------------------------------------------------------
 // One workgroup (four waves) per (row, segment p <= NSEG - 2, 64 columns of V):
 // per chunk X = K^T diag(e^{Gc_last - Gc}) V on MFMA (wave w: rows k = 16 w ..
-// +15), and six running sums, every one decayed by the chunk's total decay
+// +15), and kSBlk running sums, every one decayed by the chunk's total decay
 // before the chunk's X joins its block and the whole segment.
-//   blk [row][p][6][K = 64][V] fp32,  segd [row][NSEG] (p <= NSEG - 2 written)
+//   blk [row][p][kSBlk][K = 64][V] fp32,  segd [row][NSEG] (p <= NSEG - 2 written)
 struct SegBlkSmem {
   __bf16 k[kSC * kSLK];   // [t][k]
   __bf16 v[kSC * kSLK];   // [t][v], 64 columns
@@ -166,7 +168,11 @@ __global__ __launch_bounds__(256) void mamba2_strong_segblk_kernel(
       for (int nt = 0; nt < 4; ++nt)
         x[nt] = mfma16x16x32(a, tr_frag(s.v, kSLK, 32 * c, 16 * nt), x[nt]);
     }
-    const int bi = i < 8 ? 0 : i < 12 ? 1 : i < 14 ? 2 : i < 15 ? 3 : 4;
+    // block m = 0 .. kSLog: chunks [S - S / 2^m, S - S / 2^(m+1)) (the last: chunk S - 1)
+    int bi = 0;
+#pragma unroll
+    for (int m = 1; m <= kSLog; ++m)
+      if (i >= kSSeg - (kSSeg >> m)) bi = m;
 #pragma unroll
     for (int m = 0; m < kSBlk; ++m) {
       const float on = (m == bi || m == kSBlk - 1) ? 1.f : 0.f;
@@ -264,28 +270,26 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
 
   if (c0 > 0) {
     if (near) {
-      // the previous segment's blocks 0-7, 8-11, 12-13, 14, 15 -> levels 5, 4, 3, 2, 1
+      // the previous segment's blocks m = 0 .. kSLog -> levels kSLog + 1 - m
+      // (S / 2, S / 4, .., 1, 1 chunks)
       const int kr = 16 * w + 4 * lq;
       const float* pb = blk + (size_t)(row * (NSEG - 1) + seg - 1) * kSBlk * 64 * V + v0 + ln;
 #pragma unroll
-      for (int m = 0; m < 5; ++m)
+      for (int m = 0; m <= kSLog; ++m) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int nt = 0; nt < kSNV; ++nt)
-            st[5 - m][nt][i] = pb[((size_t)m * 64 + kr + i) * V + 16 * nt];
-      cnt[1] = 1;
-      cnt[2] = 1;
-      cnt[3] = 2;
-      cnt[4] = 4;
-      cnt[5] = 8;
-      // the whole segments q <= seg - 2 at level 4 + strong(seg, q), decayed over
-      // the segments q + 1 .. seg - 1
+            st[kSLog + 1 - m][nt][i] = pb[((size_t)m * 64 + kr + i) * V + 16 * nt];
+        cnt[kSLog + 1 - m] = m < kSLog ? kSSeg >> (m + 1) : 1;
+      }
+      // the whole segments q <= seg - 2 at level kSLog + strong(seg, q), decayed
+      // over the segments q + 1 .. seg - 1
       float dec = 0.f;
       for (int q = seg - 2; q >= 0; --q) {
         dec += segd[row * NSEG + q + 1];
         const float f = fexp(dec);
-        const int lev = 4 + strong_level_ce(seg, q);
+        const int lev = kSLog + strong_level_ce(seg, q);
         const float* ps = blk + ((size_t)(row * (NSEG - 1) + q) * kSBlk + kSBlk - 1) * 64 * V + v0 + ln;
         float y[kSNV][4];
 #pragma unroll
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(kSThreads) void mamba2_strong_fwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) y[nt][i] = f * ps[(size_t)(kr + i) * V + 16 * nt];
 #pragma unroll
-        for (int j = 6; j < kSMaxLev; ++j)
+        for (int j = kSLog + 2; j < kSMaxLev; ++j)
           if (lev == j) {
 #pragma unroll
             for (int nt = 0; nt < kSNV; ++nt)

@@ -89,11 +89,11 @@ def test_strong_fwd_nine_chunk_levels():
     _run_fwd(1, 32768, 2, 2, 64, 64, 16, seed=327)
 
 
-@pytest.mark.parametrize("T", [1088, 2048, 3136, 8192])
+@pytest.mark.parametrize("T", [2112, 4096, 5184, 8192])
 def test_strong_fwd_segment_parallel(T):
-    """More than 16 chunks: one walk per 16-chunk segment, started from the
-    block sums of the earlier segments (17 chunks: a one-chunk last segment;
-    49: a ragged one), every row."""
+    """More than 32 chunks: one walk per 32-chunk segment, started from the
+    block sums of the earlier segments (33 chunks: a one-chunk last segment;
+    81: a ragged one), every row."""
     _run_fwd(2, T, 2, 2, 64, 128, _levels(T), seed=T + 1)
 
 

@@ -180,6 +180,20 @@ def test_bwd_argument_checks(kw, code):
     assert _lib.load().hattn_last_error().decode()
 
 
+def test_fwd_workspace_query_covers_strong_block_sums():
+    """The forward's workspace query covers HType.STRONG's segment-parallel
+    walks: per row, per 32-chunk segment but the last, seven fp32 64 x V block
+    sums (six blocks and the whole segment), plus a log-decay per segment;
+    none when the sequence is one segment."""
+    lib = _lib.load()
+    for B, T, H, V in ((4, 16384, 16, 64), (1, 4096, 2, 128), (2, 32768, 3, 64)):
+        nseg = (T // 64 + 31) // 32
+        need = B * H * (nseg - 1) * 7 * 64 * V * 4
+        assert lib.hattn_mamba2_chunkwise_fwd_workspace(B, T, H, H, 64, V, 20) >= need
+    # the north star's block sums fit the no-allocation entry point's 64 MiB
+    assert 4 * 16 * 7 * 7 * 64 * 64 * 4 < (64 << 20)
+
+
 def test_bwd_workspace_query_per_htype():
     lib = _lib.load()
     assert lib.hattn_mamba2_chunkwise_bwd_workspace(1, 100, 1, 64, 64, 8, 0) == 0
